@@ -1,0 +1,165 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X Q8_0 product (one GPU).
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W]
+
+Workload: the single Q8_0 GEMV shape (1024 x 1024, int8 U[-127,127], f16
+scales |N(0,0.02)|/127, x ~ N(0,1) rounded to Q8_0 on the fly) over a ring of
+512 distinct matrices (570 MB, more than the 256 MB Infinity Cache), so each
+step streams every weight from HBM: one step = round x to Q8_0 + one GEMV
+launch over all 512 matrices.  Inputs are resident in HBM before timing.
+
+Prints one JSON line.  `value` is the whole-ring GEMV throughput in GB/s of
+algorithmic bytes (34 B per 32 weights, plus x and y per matrix); `roofline`
+is the GEMV kernel alone against 8 TB/s; `cpu_baseline` is the CPU oracle
+(a scalar C restatement of the reference's int8 route) on a bounded sample.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import platform
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = "Q8_0 GEMV GB/s (% HBM peak); decoder tokens/s at Whisper base.en shape"
+HBM_PEAK_GBS = 8000.0
+N, K, RING = 1024, 1024, 512
+BYTES_PER_GEMV = N * K // 32 * 34 + K * 4 + N * 4   # 1,122,304 B per matrix
+
+
+def parse():
+    p = argparse.ArgumentParser()
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=200)
+    p.add_argument("--warmup", type=int, default=20)
+    p.add_argument("--cpu-seconds", type=float, default=10.0, help="bound on the CPU baseline's work")
+    p.add_argument("--no-cpu", action="store_true")
+    return p.parse_args()
+
+
+def ring_weights(seed: int = 1) -> tuple[np.ndarray, np.ndarray]:
+    """512 distinct 1024x1024 Q8_0 matrices stacked row-wise (one weight of
+    524288 rows: each output row is that matrix's row, so one launch is 512
+    GEMVs), and one activation vector."""
+    from gorelaxor_amd.synth import q8_weight
+
+    rng = np.random.default_rng(seed)
+    w = q8_weight(rng, N * RING, K)
+    x = rng.standard_normal(K).astype(np.float32)
+    return w, x
+
+
+def cpu_baseline(w8: np.ndarray, x: np.ndarray, seconds: float) -> dict:
+    """The oracle's int8 route (scalar C, one thread) over the first matrices
+    of the same ring until `seconds` of work; GB/s of the same algorithmic
+    bytes."""
+    import oracle
+
+    oracle.build()
+    per = N * K // 32 * 34
+    done, t0 = 0, time.perf_counter()
+    while True:
+        i = done % RING
+        oracle.matmul_q8_int(x, w8[i * per:(i + 1) * per], N, K)
+        done += 1
+        el = time.perf_counter() - t0
+        if el >= seconds:
+            break
+    return {"value": round(done * BYTES_PER_GEMV / el / 1e9, 3), "unit": "GB/s", "cores": 1, "kind": "port",
+            "sample": f"{done} GEMVs of 1024x1024 (the first {min(done, RING)} ring matrices), "
+                      f"{el:.1f} s, oracle/grx_oracle.c orc_matmul_q8_int, 1 thread, {platform.processor() or platform.machine()}"}
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build measures one GPU; --gpus must be 1",
+                          "detail": "the path shards data-parallel by stream/utterance with no exchange; see DESIGN.md"}))
+        sys.exit(2)
+
+    import torch
+    from gorelaxor_amd import kern
+
+    ctx = kern.default_context(0)
+    stream = torch.cuda.ExternalStream(ctx.stream)
+    w8, x = ring_weights()
+    w = kern.NewQ8(N * RING, K, w8, ctx)
+    dx = torch.from_numpy(x).cuda()
+    dq = torch.zeros(K, dtype=torch.int8, device="cuda")
+    ds = torch.zeros(K // 32, dtype=torch.float32, device="cuda")
+    dy = torch.zeros(N * RING, dtype=torch.float32, device="cuda")
+    torch.cuda.synchronize()
+
+    def step(evs=None, i=0):
+        kern.quant_act_dev(dq, ds, dx, 1, K, ctx=ctx)
+        if evs is not None:
+            evs[0][i].record(stream)
+        kern.matmul_prequant_dev(dy, dq, ds, 1, w, ctx=ctx)
+        if evs is not None:
+            evs[1][i].record(stream)
+
+    for _ in range(args.warmup):
+        step()
+    ctx.sync()
+    torch.cuda.synchronize()
+
+    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(args.steps)] for _ in range(2)]
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record(stream)
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        step(ev, i)
+    end.record(stream)
+    ctx.sync()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    total_ms = start.elapsed_time(end)
+    gemv_ms = [ev[0][i].elapsed_time(ev[1][i]) for i in range(args.steps)]
+    ms_step = total_ms / args.steps
+    gemv_avg = float(np.mean(gemv_ms))
+    launch_bytes = BYTES_PER_GEMV * RING
+    value = launch_bytes / (ms_step * 1e-3) / 1e9
+    achieved = launch_bytes / (gemv_avg * 1e-3) / 1e9
+
+    # parity spot check of this very run against the oracle (first matrix)
+    import oracle
+    oracle.build()
+    want = oracle.matmul_q8_int(x, w8[:N * K // 32 * 34], N, K)[0]
+    got = dy[:N].cpu().numpy()
+    parity = bool(np.array_equal(got.view(np.uint32), want.view(np.uint32)))
+
+    out = {
+        "metric": METRIC,
+        "value": round(value, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8",
+        "data": "synthetic",
+        "config": {"workload": "q8_0 GEMV 1024x1024 over a ring of 512 distinct matrices (570 MB) per step, "
+                               "x rounded to Q8_0 on the fly", "n": N, "k": K, "ring": RING,
+                   "bytes_per_step": launch_bytes, "hbm_fraction": round(value / HBM_PEAK_GBS, 4),
+                   "parity_bit_exact": parity, "wall_s": round(wall, 3)},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "gemv_q8_kernel<1,1,PREQ,STORE>", "kernel_avg_us": round(gemv_avg * 1e3, 3)},
+    }
+    if not args.no_cpu:
+        out["cpu_baseline"] = cpu_baseline(w8, x, args.cpu_seconds)
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

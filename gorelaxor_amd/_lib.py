@@ -1,0 +1,89 @@
+"""ctypes binding of libgrx.so (include/grx.h).
+
+The library is built in-tree (python -m gorelaxor_amd.build); loading it
+never falls back to anything else: a missing or unloadable library raises.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+import re
+
+PKG = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(PKG, "libgrx.so")
+HEADER = os.path.join(os.path.dirname(PKG), "include", "grx.h")
+
+GRX_OK = 0
+STATUS = {0: "GRX_OK", -1: "GRX_EINVAL", -2: "GRX_ESIZE", -3: "GRX_EDEVICE", -4: "GRX_ENOMEM",
+          -5: "GRX_ESTATE", -6: "GRX_ENODEV"}
+
+
+class GrxError(RuntimeError):
+    """A non-zero grx_status, with grx_last_error()'s message."""
+
+    def __init__(self, status: int, message: str):
+        super().__init__(f"{STATUS.get(status, status)}: {message}")
+        self.status = status
+
+
+_lib = None
+
+vp = C.c_void_p
+i32 = C.c_int
+sz = C.c_size_t
+
+# name -> (restype, argtypes); every grx_* entry point of include/grx.h
+SIGNATURES = {
+    "grx_version": (i32, []),
+    "grx_last_error": (C.c_char_p, []),
+    "grx_device_count": (i32, []),
+    "grx_ctx_create": (i32, [i32, C.POINTER(vp)]),
+    "grx_ctx_destroy": (i32, [vp]),
+    "grx_ctx_sync": (i32, [vp]),
+    "grx_ctx_stream": (vp, [vp]),
+    "grx_weight_q8_create": (i32, [vp, i32, i32, vp, sz, C.POINTER(vp)]),
+    "grx_weight_destroy": (i32, [vp]),
+    "grx_weight_rows": (i32, [vp]),
+    "grx_weight_cols": (i32, [vp]),
+    "grx_weight_bytes": (sz, [vp]),
+    "grx_weight_row": (i32, [vp, vp, i32, vp]),
+    "grx_weight_float32": (i32, [vp, vp, vp]),
+    "grx_to_q8": (i32, [vp, i32, i32, vp, vp]),
+    "grx_matmul_q8": (i32, [vp, vp, i32, vp, i32, i32, vp, vp]),
+    "grx_linear_q8": (i32, [vp, vp, vp, i32, vp, vp]),
+    "grx_matmul_q8_dev": (i32, [vp, vp, i32, vp, i32, i32, vp, vp]),
+    "grx_quant_act_dev": (i32, [vp, vp, vp, vp, i32, i32, i32]),
+    "grx_matmul_q8_prequant_dev": (i32, [vp, vp, i32, vp, vp, i32, vp, vp]),
+    "grx_block_dots_dev": (i32, [vp, vp, vp, i32, vp]),
+}
+
+
+def header_symbols() -> list[str]:
+    """Every function include/grx.h declares."""
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(grx_[a-z0-9_]+)\s*\(", text)))
+
+
+def lib() -> C.CDLL:
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(f"{LIB_PATH} is not built: run python -m gorelaxor_amd.build")
+        L = C.CDLL(LIB_PATH)
+        for name, (res, args) in SIGNATURES.items():
+            f = getattr(L, name)
+            f.restype = res
+            f.argtypes = args
+        _lib = L
+    return _lib
+
+
+def check(status: int) -> None:
+    if status != GRX_OK:
+        msg = lib().grx_last_error()
+        raise GrxError(status, msg.decode() if msg else "")
+
+
+def call(name: str, *args) -> None:
+    check(getattr(lib(), name)(*args))

@@ -1,0 +1,78 @@
+"""Build libgrx.so (gfx950) in-tree with hipcc.
+
+    python -m gorelaxor_amd.build
+
+The library lands next to this file (gorelaxor_amd/libgrx.so) so that it
+travels with the source tree; nothing is installed.
+"""
+from __future__ import annotations
+
+import glob
+import os
+import shutil
+import subprocess
+import sys
+import time
+
+PKG = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(PKG)
+CSRC = os.path.join(PKG, "csrc")
+LIB = os.path.join(PKG, "libgrx.so")
+BUILD_DIR = os.path.join(PKG, "_build")
+
+HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
+ARCH = "gfx950"
+
+# -ffp-contract=off: a product followed by a sum is never fused unless the
+# source asks for it (__fmaf_rn), which parity with the reference needs.
+# -packed-fp32-ops off: no v_pk_{add,mul,fma}_f32 are generated.
+FLAGS = [
+    f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC", "-ffp-contract=off",
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-Wall", "-Wno-unused-function", "-Wno-unused-command-line-argument",
+    "-I" + os.path.join(ROOT, "include"),
+]
+
+
+def sources():
+    return sorted(glob.glob(os.path.join(CSRC, "*.hip")))
+
+
+def _compile_one(src: str) -> tuple[str, subprocess.Popen]:
+    obj = os.path.join(BUILD_DIR, os.path.basename(src) + ".o")
+    cmd = [HIPCC, *FLAGS, "-c", src, "-o", obj]
+    p = subprocess.Popen(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
+    return obj, p
+
+
+def build(verbose: bool = True) -> str:
+    """Compile every csrc/*.hip for gfx950 and link gorelaxor_amd/libgrx.so."""
+    if not os.path.exists(HIPCC):
+        raise RuntimeError(f"hipcc not found at {HIPCC}")
+    os.makedirs(BUILD_DIR, exist_ok=True)
+    t0 = time.time()
+    jobs = [_compile_one(s) for s in sources()]
+    objs, failed = [], []
+    for obj, p in jobs:
+        out, _ = p.communicate()
+        lines = [l for l in out.splitlines() if "packed-fp32-ops" not in l]
+        if p.returncode != 0:
+            failed.append((obj, "\n".join(lines)))
+        elif verbose and lines:
+            print("\n".join(lines), file=sys.stderr)
+        objs.append(obj)
+    if failed:
+        raise RuntimeError("hipcc failed:\n" + "\n\n".join(f"{o}:\n{t}" for o, t in failed))
+    tmp = LIB + ".tmp"
+    cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError("link failed:\n" + r.stdout + r.stderr)
+    shutil.move(tmp, LIB)
+    if verbose:
+        print(f"built {LIB} in {time.time() - t0:.1f}s", file=sys.stderr)
+    return LIB
+
+
+if __name__ == "__main__":
+    build()

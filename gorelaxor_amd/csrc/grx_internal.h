@@ -1,0 +1,239 @@
+// grx_internal.h - shared declarations of libgrx.so (gfx950 only).
+//
+// Device helpers here restate, lane by lane, the arithmetic of the
+// reference's kernels (github.com/xattribution/gorelaxor, cited file:line);
+// they are written with explicit __fmul_rn/__fadd_rn/__fmaf_rn so that the
+// compiler can neither fuse nor reorder them, and the library is built with
+// -ffp-contract=off on top.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#include "../../include/grx.h"
+
+// ---------------------------------------------------------------- host side
+
+struct grx_ctx {
+    int device;
+    hipStream_t stream;
+    void *scratch;        // device scratch for host-pointer calls, grown on demand
+    size_t scratch_bytes;
+};
+
+// Q8_0 weight in HBM, packed once (grx_weight_q8_create).  Layout, for
+// tiles of 64 rows (row r = 64*tile + lane):
+//   qs: int8  [tiles][nb][2][64][16]  the 16 values 16h..16h+15 of block b
+//   ds: f16   [tiles][nb][64]         the scale of block b
+// Exactly 34 bytes per 32 weights (plus zero rows to a whole last tile).
+// A wave owns a tile: lane l reads row 64*tile+l, each of its 16-byte value
+// loads is one 1 KiB coalesced transaction for the wave and its scale load
+// one 128-byte transaction.
+struct grx_weight {
+    int rows, cols, nb, tiles, device;
+    int8_t *qs;
+    uint16_t *ds;
+    size_t bytes;
+};
+
+grx_status grx_fail(grx_status s, const char *fmt, ...);
+grx_status grx_hip_fail(hipError_t e, const char *what);
+grx_status grx_ctx_scratch(grx_ctx *ctx, size_t bytes, void **out);
+
+#define GRX_HIP(expr)                                                       \
+    do {                                                                    \
+        hipError_t e_ = (expr);                                             \
+        if (e_ != hipSuccess) return grx_hip_fail(e_, #expr);               \
+    } while (0)
+
+#define GRX_LAUNCHED(what)                                                  \
+    do {                                                                    \
+        hipError_t e_ = hipGetLastError();                                  \
+        if (e_ != hipSuccess) return grx_hip_fail(e_, what);                \
+    } while (0)
+
+static inline int grx_ceil_div(int a, int b) { return (a + b - 1) / b; }
+
+// ------------------------------------------------------------ device side
+
+#define GRX_QK 32
+
+__device__ __forceinline__ float grx_bits_f32(uint32_t u) { return __uint_as_float(u); }
+
+// f16 -> f32, exact incl. subnormals (internal/kern/f16.go:14-33); the
+// kernels run with f16 denormals kept (denorm mode 3), so the hardware
+// conversion is exact.
+__device__ __forceinline__ float grx_f16_to_f32(uint16_t h) {
+    _Float16 v;
+    __builtin_memcpy(&v, &h, 2);
+    return (float)v;
+}
+
+// f32 -> f16 round to nearest even with the reference's NaN and overflow
+// results (internal/kern/f16.go:36-71), in integer arithmetic.
+__device__ __forceinline__ uint16_t grx_f32_to_f16(float f) {
+    uint32_t b = __float_as_uint(f);
+    uint16_t sign = (uint16_t)(b >> 16) & 0x8000;
+    int32_t exp = (int32_t)(b >> 23) & 0xff;
+    uint32_t man = b & 0x7fffff;
+    if (exp == 0xff) return man != 0 ? (sign | 0x7e00) : (sign | 0x7c00);
+    int32_t e = exp - 127 + 15;
+    if (e >= 0x1f) return sign | 0x7c00;
+    if (e <= 0) {
+        if (e < -10) return sign;
+        man |= 0x800000;
+        uint32_t shift = (uint32_t)(14 - e);
+        uint32_t h = man >> shift;
+        uint32_t rem = man & ((1u << shift) - 1);
+        uint32_t half = 1u << (shift - 1);
+        if (rem > half || (rem == half && (h & 1) == 1)) h++;
+        return sign | (uint16_t)h;
+    }
+    uint32_t h = (uint32_t)e << 10 | man >> 13;
+    uint32_t rem = man & 0x1fff;
+    if (rem > 0x1000 || (rem == 0x1000 && (h & 1) == 1)) h++;
+    return sign | (uint16_t)h;
+}
+
+// quantU8 for one block of 32 values (internal/kern/q8int.go:88-105,
+// vnni_amd64.s:194-256): sc = amax*f32(1/127), id = 127/amax (0 for an
+// all-zero block), q = clamp(rne(x*id), -128, 127), kept signed.
+__device__ __forceinline__ float grx_quant_block(const float *x, int8_t *q) {
+    float amax = 0.0f;
+#pragma unroll
+    for (int i = 0; i < GRX_QK; ++i) {
+        float a = fabsf(x[i]);
+        amax = a > amax ? a : amax;
+    }
+    const float sc = __fmul_rn(amax, grx_bits_f32(0x3c010204u));
+    const float id = amax != 0.0f ? __fdiv_rn(127.0f, amax) : 0.0f;
+#pragma unroll
+    for (int i = 0; i < GRX_QK; ++i) {
+        float r = rintf(__fmul_rn(x[i], id));
+        r = fminf(fmaxf(r, -128.0f), 127.0f);
+        q[i] = (int8_t)(int)r;
+    }
+    return sc;
+}
+
+// EXP8 of internal/kern/kernels_amd64.s:236-258, one lane.
+__device__ __forceinline__ float grx_exp8(float x) {
+    x = x > -87.0f ? x : -87.0f;
+    x = x < 88.0f ? x : 88.0f;
+    const float n = rintf(__fmul_rn(x, grx_bits_f32(0x3fb8aa3bu)));
+    float r = __fmaf_rn(-n, grx_bits_f32(0x3f317200u), x);
+    r = __fmaf_rn(-n, grx_bits_f32(0x35bfbe8eu), r);
+    float p = grx_bits_f32(0x3ab60b61u);
+    p = __fmaf_rn(p, r, grx_bits_f32(0x3c088889u));
+    p = __fmaf_rn(p, r, grx_bits_f32(0x3d2aaaabu));
+    p = __fmaf_rn(p, r, grx_bits_f32(0x3e2aaaabu));
+    p = __fmaf_rn(p, r, 0.5f);
+    p = __fmaf_rn(p, r, 1.0f);
+    p = __fmaf_rn(p, r, 1.0f);
+    const int ni = (int)n;
+    return __fmul_rn(p, grx_bits_f32((uint32_t)(ni + 127) << 23));
+}
+
+// expf of internal/kern/mathx.go:7-33 (the scalar form), unfused.
+__device__ __forceinline__ float grx_expf_go(float x) {
+    if (x < -87.0f) return 0.0f;
+    if (x > 88.0f) return __builtin_inff();
+    float t = __fmul_rn(x, grx_bits_f32(0x3fb8aa3bu));
+    t = __fadd_rn(t, 0.5f);
+    int ni = (int)t;
+    if ((float)ni > t) ni--;
+    const float n = (float)ni;
+    float r = __fsub_rn(x, __fmul_rn(n, grx_bits_f32(0x3f317200u)));
+    r = __fsub_rn(r, __fmul_rn(n, grx_bits_f32(0x35bfbe8eu)));
+    float p = __fmul_rn(grx_bits_f32(0x3ab60b61u), r);
+    p = __fadd_rn(p, grx_bits_f32(0x3c088889u));
+    p = __fadd_rn(__fmul_rn(p, r), grx_bits_f32(0x3d2aaaabu));
+    p = __fadd_rn(__fmul_rn(p, r), grx_bits_f32(0x3e2aaaabu));
+    p = __fadd_rn(__fmul_rn(p, r), 0.5f);
+    p = __fadd_rn(__fmul_rn(p, r), 1.0f);
+    p = __fadd_rn(__fmul_rn(p, r), 1.0f);
+    if (ni < -126) {
+        const float v = __fmul_rn(p, grx_bits_f32((uint32_t)(ni + 127 + 64) << 23));
+        return __fmul_rn(v, grx_bits_f32(0x1f800000u));
+    }
+    return __fmul_rn(p, grx_bits_f32((uint32_t)(ni + 127) << 23));
+}
+
+// geluAVX of internal/kern/kernels_amd64.s:299-338, one lane.
+__device__ __forceinline__ float grx_gelu_avx(float v) {
+    float u = __fmul_rn(v, v);
+    u = __fmaf_rn(grx_bits_f32(0x3d372713u), u, 1.0f);
+    u = __fmul_rn(u, v);
+    u = __fmul_rn(u, grx_bits_f32(0x3f4c422au));
+    u = u < 9.0f ? u : 9.0f;
+    u = u > -9.0f ? u : -9.0f;
+    float e = grx_exp8(__fadd_rn(u, u));
+    e = __fadd_rn(e, 1.0f);
+    float t = __fdiv_rn(2.0f, e);
+    t = __fsub_rn(1.0f, t);
+    t = __fadd_rn(1.0f, t);
+    t = __fmul_rn(t, v);
+    return __fmul_rn(t, 0.5f);
+}
+
+// gelu of internal/kern/mathx.go:36-52 (the scalar form, used past the last
+// whole group of eight).
+__device__ __forceinline__ float grx_gelu_go(float v) {
+    float u = __fmul_rn(grx_bits_f32(0x3f4c422au), v);
+    float w = __fmul_rn(grx_bits_f32(0x3d372713u), v);
+    w = __fadd_rn(1.0f, __fmul_rn(w, v));
+    u = __fmul_rn(u, w);
+    float t;
+    if (u > 9.0f)
+        t = 1.0f;
+    else if (u < -9.0f)
+        t = -1.0f;
+    else
+        t = __fsub_rn(1.0f, __fdiv_rn(2.0f, __fadd_rn(grx_expf_go(__fmul_rn(2.0f, u)), 1.0f)));
+    return __fmul_rn(__fmul_rn(0.5f, v), __fadd_rn(1.0f, t));
+}
+
+// geluVec over an array of n values (kernels_amd64.go:119-129): element i
+// takes the assembly form below n &^ 7, the scalar form past it.
+__device__ __forceinline__ float grx_gelu_at(float v, int i, int n) {
+    return i < (n & ~7) ? grx_gelu_avx(v) : grx_gelu_go(v);
+}
+
+// Launch helpers of the product kernels (q8_gemv.hip).
+enum { GRX_PRO_PREQ = 0, GRX_PRO_QUANT = 1, GRX_PRO_LN = 2 };
+enum {
+    GRX_EPI_STORE = 0,   // y = c
+    GRX_EPI_RESID = 1,   // y = resid + c
+    GRX_EPI_GELU = 2,    // y = geluVec(c) over the flat output
+    GRX_EPI_QKV = 3,     // rows split in three: q, then K and V caches at *pos
+    GRX_EPI_ARGMAX = 4   // y = c (optional) and the first index of the maximum
+};
+
+struct GemvArgs {
+    const int8_t *qs;
+    const uint16_t *ds;
+    int rows, nb;
+    // activations: PREQ reads xq/xs; QUANT and LN read x (lda apart)
+    const int8_t *xq;
+    const float *xs;
+    const float *x;
+    int lda;
+    const float *ln_w, *ln_b;
+    // output
+    float *y;
+    int ldc;
+    const float *bias;
+    const float *resid;
+    int ldr;
+    // QKV: rows [0,seg) -> y, [seg,2seg) -> kc[(pos+m)*seg], [2seg,3seg) -> vc
+    int seg;
+    float *kc, *vc;
+    const int *pos;
+    // ARGMAX: one 64-bit key per activation row
+    unsigned long long *amax;
+};
+
+grx_status grx_gemv_launch(hipStream_t st, int m, int pro, int epi, const GemvArgs &a,
+                           int waves_hint);
+int grx_gemv_pick_waves(int tiles, int nb, int m);

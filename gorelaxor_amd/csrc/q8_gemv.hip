@@ -1,0 +1,509 @@
+// q8_gemv.hip - the Q8_0 int8 product for few activation rows (m <= 8 per
+// launch): the decode-time GEMV and the skinny GEMM of batched streams.
+//
+// Restates the int8 route of kern.MatMul (internal/kern/kern.go:185-196 ->
+// matmulQ8Int, q8int.go:148-223 of github.com/xattribution/gorelaxor) with
+// the per-output arithmetic of the VNNI tile kernel (vnni_amd64.s:58-69):
+//     c = bias (or 0);  for b in 0..nb-1:  c = fma(f32(s_b) * dw_b, da_b, c)
+// where s_b is the int32 dot of block b's rounded activations and weights.
+//
+// MI355X design: a workgroup owns one tile of 64 weight rows; lane l of
+// every wave owns row 64*tile+l.  The tile's blocks are split among W waves
+// (W = 1 for tall matrices, more for short ones so that a 512-row matrix
+// still spreads over many CUs).  Per block a lane issues two 16-byte loads
+// (one 1 KiB coalesced transaction per wave each) plus one 2-byte scale load,
+// eight v_dot4_i32_i8 against the activation block, one convert and one
+// multiply.  With W = 1 the lane also runs the ordered fma chain as it goes;
+// with W > 1 the products f32(s_b)*dw_b go to LDS and wave 0 runs the chain
+// in block order afterwards, so the result is the same bit for bit.
+#include <stdlib.h>
+
+#include <type_traits>
+
+#include "grx_internal.h"
+
+namespace {
+
+constexpr int BU = 4;  // blocks whose loads are issued before any is used
+
+// ---------------------------------------------------------------- helpers
+
+__device__ __forceinline__ int sdot8(const int4 &w0, const int4 &w1, const int4 &a0, const int4 &a1) {
+    int s = 0;
+    s = __builtin_amdgcn_sdot4(w0.x, a0.x, s, false);
+    s = __builtin_amdgcn_sdot4(w0.y, a0.y, s, false);
+    s = __builtin_amdgcn_sdot4(w0.z, a0.z, s, false);
+    s = __builtin_amdgcn_sdot4(w0.w, a0.w, s, false);
+    s = __builtin_amdgcn_sdot4(w1.x, a1.x, s, false);
+    s = __builtin_amdgcn_sdot4(w1.y, a1.y, s, false);
+    s = __builtin_amdgcn_sdot4(w1.z, a1.z, s, false);
+    s = __builtin_amdgcn_sdot4(w1.w, a1.w, s, false);
+    return s;
+}
+
+// Sum over the workgroup in float64, the same order in every thread.
+__device__ __forceinline__ double block_sum_f64(double v, double *red, int lane, int wave, int nwaves) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+    __syncthreads();
+    if (lane == 0) red[wave] = v;
+    __syncthreads();
+    double t = 0.0;
+    for (int w = 0; w < nwaves; ++w) t += red[w];
+    return t;
+}
+
+// Round (M rows x nb blocks) of float32 activations in LDS or global memory
+// into LDS: one thread per block.
+template <int M>
+__device__ __forceinline__ void quant_into_lds(const float *src, int ld, int nb, int8_t *lxq,
+                                               float *lxs, int tid, int nthreads) {
+    const int K = nb * GRX_QK;
+    for (int i = tid; i < M * nb; i += nthreads) {
+        const int m = i / nb, b = i - m * nb;
+        const float4 *p = reinterpret_cast<const float4 *>(src + (size_t)m * ld + b * GRX_QK);
+        float v[GRX_QK];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const float4 f = p[j];
+            v[4 * j] = f.x;
+            v[4 * j + 1] = f.y;
+            v[4 * j + 2] = f.z;
+            v[4 * j + 3] = f.w;
+        }
+        int8_t q[GRX_QK];
+        lxs[m * nb + b] = grx_quant_block(v, q);
+        int4 *d = reinterpret_cast<int4 *>(lxq + (size_t)m * K + b * GRX_QK);
+        int4 q0, q1;
+        __builtin_memcpy(&q0, q, 16);
+        __builtin_memcpy(&q1, q + 16, 16);
+        d[0] = q0;
+        d[1] = q1;
+    }
+}
+
+// ---------------------------------------------------------------- kernel
+
+template <int M, int W, int PRO, int EPI>
+__global__ __launch_bounds__(64 * W) void gemv_q8_kernel(const GemvArgs a) {
+    extern __shared__ __align__(16) unsigned char smem[];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: loops stay scalar
+    const int tile = blockIdx.x;
+    const int nb = a.nb, K = nb * GRX_QK;
+    const int row = tile * 64 + lane;
+
+    // LDS, each region 16-byte aligned (gemv_smem):
+    //   [lxq M*K int8][lxs M*nb f32][lp M*nb*64 f32 if W>1][lf M*K f32 if LN][red]
+    const size_t o_xs = (PRO != GRX_PRO_PREQ) ? (size_t)M * K : 0;
+    const size_t o_p = o_xs + ((PRO != GRX_PRO_PREQ) ? (((size_t)M * nb * 4 + 15) & ~(size_t)15) : 0);
+    const size_t o_f = o_p + (W > 1 ? (size_t)M * nb * 64 * 4 : 0);
+    const size_t o_r = o_f + (PRO == GRX_PRO_LN ? (size_t)M * K * 4 : 0);
+    int8_t *lxq = reinterpret_cast<int8_t *>(smem);
+    float *lxs = reinterpret_cast<float *>(smem + o_xs);
+    float *lp = reinterpret_cast<float *>(smem + o_p);
+    float *lf = reinterpret_cast<float *>(smem + o_f);
+    double *red = reinterpret_cast<double *>(smem + o_r);
+
+    // ---- prologue: the activation rows, rounded, in LDS (or left in HBM)
+    if constexpr (PRO == GRX_PRO_QUANT) {
+        quant_into_lds<M>(a.x, a.lda, nb, lxq, lxs, tid, 64 * W);
+        __syncthreads();
+    } else if constexpr (PRO == GRX_PRO_LN) {
+        // layerNorm (internal/kern/mathx.go:55-75) of each row, then quantU8.
+        for (int m = 0; m < M; ++m) {
+            const float *xr = a.x + (size_t)m * a.lda;
+            float *fr = lf + (size_t)m * K;
+            double ps = 0.0;
+            for (int i = tid; i < K; i += 64 * W) {
+                const float v = xr[i];
+                fr[i] = v;
+                ps += (double)v;
+            }
+            const double sum = block_sum_f64(ps, red, lane, wave, W);
+            const float mean = (float)(sum / (double)K);
+            double pv = 0.0;
+            for (int i = tid; i < K; i += 64 * W) {
+                const double d = (double)__fsub_rn(fr[i], mean);
+                pv += d * d;
+            }
+            const double vs = block_sum_f64(pv, red + W, lane, wave, W);
+            const float inv = (float)(1.0 / sqrt(vs / (double)K + 1e-5));
+            for (int i = tid; i < K; i += 64 * W) {
+                float t = __fsub_rn(fr[i], mean);
+                t = __fmul_rn(t, inv);
+                t = __fmul_rn(t, a.ln_w[i]);
+                fr[i] = __fadd_rn(t, a.ln_b[i]);
+            }
+        }
+        __syncthreads();
+        quant_into_lds<M>(lf, K, nb, lxq, lxs, tid, 64 * W);
+        __syncthreads();
+    }
+
+    auto act = [&](int m, int b, int4 &a0, int4 &a1) {
+        const int4 *p;
+        if constexpr (PRO == GRX_PRO_PREQ)
+            p = reinterpret_cast<const int4 *>(a.xq + (size_t)m * K + b * GRX_QK);
+        else
+            p = reinterpret_cast<const int4 *>(lxq + (size_t)m * K + b * GRX_QK);
+        a0 = p[0];
+        a1 = p[1];
+    };
+    auto act_scale = [&](int m, int b) -> float {
+        if constexpr (PRO == GRX_PRO_PREQ)
+            return a.xs[(size_t)m * nb + b];
+        else
+            return lxs[m * nb + b];
+    };
+
+    // ---- main loop: this wave's run of blocks
+    const int b0 = (wave * nb) / W, b1 = ((wave + 1) * nb) / W;
+    const int4 *__restrict__ wq = reinterpret_cast<const int4 *>(a.qs) + (size_t)tile * nb * 128;
+    const uint16_t *__restrict__ wd = a.ds + (size_t)tile * nb * 64;
+
+    float acc[M];
+    if constexpr (W == 1) {
+        const float bv = (a.bias != nullptr && row < a.rows) ? a.bias[row] : 0.0f;
+#pragma unroll
+        for (int m = 0; m < M; ++m) acc[m] = bv;
+    }
+
+    // U blocks: all loads issued first, then the dots in block order.
+    auto run = [&](auto u_tag, int bb) {
+        constexpr int U = decltype(u_tag)::value;
+        int4 w[2 * U];
+        uint32_t dh[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            w[2 * u] = wq[(size_t)(bb + u) * 128 + lane];
+            w[2 * u + 1] = wq[(size_t)(bb + u) * 128 + 64 + lane];
+            dh[u] = wd[(size_t)(bb + u) * 64 + lane];
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int b = bb + u;
+            const float dw = grx_f16_to_f32((uint16_t)dh[u]);
+#pragma unroll
+            for (int m = 0; m < M; ++m) {
+                int4 a0, a1;
+                act(m, b, a0, a1);
+                const int s = sdot8(w[2 * u], w[2 * u + 1], a0, a1);
+                const float pv = __fmul_rn((float)s, dw);
+                if constexpr (W == 1)
+                    acc[m] = __fmaf_rn(pv, act_scale(m, b), acc[m]);
+                else
+                    lp[((size_t)m * nb + b) * 64 + lane] = pv;
+            }
+        }
+    };
+    int bb = b0;
+    for (; bb + BU <= b1; bb += BU) run(std::integral_constant<int, BU>{}, bb);
+    for (; bb < b1; ++bb) run(std::integral_constant<int, 1>{}, bb);
+
+    if constexpr (W > 1) {
+        __syncthreads();
+        if (wave != 0) return;
+        const float bv = (a.bias != nullptr && row < a.rows) ? a.bias[row] : 0.0f;
+#pragma unroll
+        for (int m = 0; m < M; ++m) {
+            float c = bv;
+            for (int b = 0; b < nb; ++b) c = __fmaf_rn(lp[((size_t)m * nb + b) * 64 + lane], act_scale(m, b), c);
+            acc[m] = c;
+        }
+    }
+
+    // ---- epilogue
+    if constexpr (EPI == GRX_EPI_ARGMAX) {
+#pragma unroll
+        for (int m = 0; m < M; ++m) {
+            const float c = acc[m];
+            if (a.y != nullptr && row < a.rows) a.y[(size_t)m * a.ldc + row] = c;
+            // key: orderable float bits, then the complement of the index, so
+            // the maximum key is the largest value at its first index
+            // (whisper/transcribe.go:459-464); -0 counts as +0 and NaN never wins.
+            unsigned long long key = 0;
+            if (row < a.rows && !(c != c)) {
+                const float cc = c == 0.0f ? 0.0f : c;
+                const uint32_t u = __float_as_uint(cc);
+                const uint32_t ord = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+                key = ((unsigned long long)ord << 32) | (uint32_t)(0xffffffffu - (uint32_t)row);
+            }
+#pragma unroll
+            for (int o = 32; o > 0; o >>= 1) {
+                const unsigned long long k2 = __shfl_xor(key, o);
+                key = k2 > key ? k2 : key;
+            }
+            if (lane == 0) atomicMax(a.amax + m, key);
+        }
+        return;
+    }
+    if (row >= a.rows) return;
+#pragma unroll
+    for (int m = 0; m < M; ++m) {
+        const float c = acc[m];
+        if constexpr (EPI == GRX_EPI_STORE) {
+            a.y[(size_t)m * a.ldc + row] = c;
+        } else if constexpr (EPI == GRX_EPI_RESID) {
+            a.y[(size_t)m * a.ldc + row] = __fadd_rn(a.resid[(size_t)m * a.ldr + row], c);
+        } else if constexpr (EPI == GRX_EPI_GELU) {
+            // parGelu (whisper/encoder.go:147-151): geluVec over chunks of
+            // 1<<14 values of the flat [M][rows] output.
+            const int flat = m * a.rows + row, total = M * a.rows;
+            const int start = flat & ~((1 << 14) - 1);
+            const int len = min(1 << 14, total - start);
+            a.y[(size_t)m * a.ldc + row] = grx_gelu_at(c, flat - start, len);
+        } else if constexpr (EPI == GRX_EPI_QKV) {
+            const int pos = *a.pos + m;
+            if (row < a.seg)
+                a.y[(size_t)m * a.ldc + row] = c;
+            else if (row < 2 * a.seg)
+                a.kc[(size_t)pos * a.seg + row - a.seg] = c;
+            else
+                a.vc[(size_t)pos * a.seg + row - 2 * a.seg] = c;
+        }
+    }
+}
+
+// One thread per block: quantU8 of m rows (q8int.go:88-105), signed.
+__global__ void quant_act_kernel(const float *__restrict__ x, int lda, int m, int nb,
+                                 int8_t *__restrict__ q, float *__restrict__ sc) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= m * nb) return;
+    const int r = i / nb, b = i - r * nb;
+    const float *src = x + (size_t)r * lda + b * GRX_QK;
+    float v[GRX_QK];
+#pragma unroll
+    for (int j = 0; j < GRX_QK; ++j) v[j] = src[j];
+    int8_t qq[GRX_QK];
+    sc[i] = grx_quant_block(v, qq);
+    int8_t *d = q + (size_t)r * nb * GRX_QK + b * GRX_QK;
+#pragma unroll
+    for (int j = 0; j < GRX_QK; ++j) d[j] = qq[j];
+}
+
+// s[m][rows][nb]: one thread per (activation row, weight row, block).
+__global__ void block_dots_kernel(const int8_t *__restrict__ qs, int rows, int nb,
+                                  const int8_t *__restrict__ q, int m, int32_t *__restrict__ s) {
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= (size_t)m * rows * nb) return;
+    const int b = (int)(i % nb);
+    const int row = (int)((i / nb) % rows);
+    const int r = (int)(i / ((size_t)nb * rows));
+    const int tile = row >> 6, lane = row & 63;
+    const int4 *wq = reinterpret_cast<const int4 *>(qs) + ((size_t)tile * nb + b) * 128;
+    const int4 w0 = wq[lane], w1 = wq[64 + lane];
+    const int4 *ap = reinterpret_cast<const int4 *>(q + (size_t)r * nb * GRX_QK + b * GRX_QK);
+    s[i] = sdot8(w0, w1, ap[0], ap[1]);
+}
+
+size_t gemv_smem(int M, int W, int pro, int nb) {
+    const size_t K = (size_t)nb * GRX_QK;
+    size_t n = 0;
+    if (pro != GRX_PRO_PREQ) n += M * K + (((size_t)M * nb * 4 + 15) & ~(size_t)15);
+    if (W > 1) n += (size_t)M * nb * 64 * 4;
+    if (pro == GRX_PRO_LN) n += (size_t)M * K * 4 + 2 * 16 * sizeof(double);
+    return n;
+}
+
+template <int M, int W, int PRO, int EPI>
+hipError_t launch_one(hipStream_t st, const GemvArgs &a, int tiles) {
+    const size_t smem = gemv_smem(M, W, PRO, a.nb);
+    if (smem > 64 * 1024) {
+        static bool raised = false;
+        if (!raised) {
+            raised = true;
+            (void)hipFuncSetAttribute((const void *)gemv_q8_kernel<M, W, PRO, EPI>,
+                                      hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+        }
+    }
+    gemv_q8_kernel<M, W, PRO, EPI><<<tiles, 64 * W, smem, st>>>(a);
+    return hipGetLastError();
+}
+
+template <int M, int PRO, int EPI>
+hipError_t launch_w(hipStream_t st, const GemvArgs &a, int tiles, int W) {
+    switch (W) {
+        case 1: return launch_one<M, 1, PRO, EPI>(st, a, tiles);
+        case 2: return launch_one<M, 2, PRO, EPI>(st, a, tiles);
+        case 4: return launch_one<M, 4, PRO, EPI>(st, a, tiles);
+        case 8: return launch_one<M, 8, PRO, EPI>(st, a, tiles);
+        default: return launch_one<M, 16, PRO, EPI>(st, a, tiles);
+    }
+}
+
+template <int PRO, int EPI>
+hipError_t launch_m(hipStream_t st, int m, const GemvArgs &a, int tiles, int W) {
+    switch (m) {
+        case 1: return launch_w<1, PRO, EPI>(st, a, tiles, W);
+        case 2: return launch_w<2, PRO, EPI>(st, a, tiles, W);
+        case 4: return launch_w<4, PRO, EPI>(st, a, tiles, W);
+        default: return launch_w<8, PRO, EPI>(st, a, tiles, W);
+    }
+}
+
+}  // namespace
+
+// Waves per tile: enough tiles x waves to cover the CUs, never more waves
+// than blocks, and the LDS of the ordered chain within 64 KiB.
+// GRX_GEMV_WAVES (1, 2, 4, 8 or 16) forces the choice, for tests.
+int grx_gemv_pick_waves(int tiles, int nb, int m) {
+    if (const char *f = getenv("GRX_GEMV_WAVES")) {
+        const int w = atoi(f);
+        if (w == 1 || w == 2 || w == 4 || w == 8 || w == 16) return w;
+    }
+    int W = 1;
+    while (W < 16 && tiles * W < 2048 && 2 * W <= nb && (size_t)m * nb * 64 * 4 <= 80 * 1024) W *= 2;
+    return W;
+}
+
+// m must be 1, 2, 4 or 8; pro/epi one of the supported pairs below.
+grx_status grx_gemv_launch(hipStream_t st, int m, int pro, int epi, const GemvArgs &a, int waves) {
+    const int tiles = grx_ceil_div(a.rows, 64);
+    if (tiles == 0 || m == 0) return GRX_OK;
+    const int W = waves > 0 ? waves : grx_gemv_pick_waves(tiles, a.nb, m);
+    hipError_t e = hipErrorInvalidValue;
+    if (pro == GRX_PRO_PREQ && epi == GRX_EPI_STORE) e = launch_m<GRX_PRO_PREQ, GRX_EPI_STORE>(st, m, a, tiles, W);
+    else if (pro == GRX_PRO_QUANT && epi == GRX_EPI_STORE) e = launch_m<GRX_PRO_QUANT, GRX_EPI_STORE>(st, m, a, tiles, W);
+    else if (pro == GRX_PRO_QUANT && epi == GRX_EPI_RESID) e = launch_m<GRX_PRO_QUANT, GRX_EPI_RESID>(st, m, a, tiles, W);
+    else if (pro == GRX_PRO_LN && epi == GRX_EPI_STORE) e = launch_m<GRX_PRO_LN, GRX_EPI_STORE>(st, m, a, tiles, W);
+    else if (pro == GRX_PRO_LN && epi == GRX_EPI_GELU) e = launch_m<GRX_PRO_LN, GRX_EPI_GELU>(st, m, a, tiles, W);
+    else if (pro == GRX_PRO_LN && epi == GRX_EPI_QKV) e = launch_m<GRX_PRO_LN, GRX_EPI_QKV>(st, m, a, tiles, W);
+    else if (pro == GRX_PRO_LN && epi == GRX_EPI_ARGMAX) e = launch_m<GRX_PRO_LN, GRX_EPI_ARGMAX>(st, m, a, tiles, W);
+    else return grx_fail(GRX_EINVAL, "grx: no GEMV variant for prologue %d epilogue %d", pro, epi);
+    if (e != hipSuccess) return grx_hip_fail(e, "gemv_q8_kernel");
+    return GRX_OK;
+}
+
+// ---------------------------------------------------------------- C ABI
+
+static grx_status check_mm(const char *fn, grx_ctx *ctx, const void *dst, int ldc, const void *x,
+                           int lda, int m, const grx_weight *w) {
+    if (!ctx || !w) return grx_fail(GRX_EINVAL, "%s: NULL context or weight", fn);
+    if (m < 0) return grx_fail(GRX_EINVAL, "%s: m = %d", fn, m);
+    if (m > 0 && w->rows > 0 && (!dst || !x)) return grx_fail(GRX_EINVAL, "%s: NULL buffer", fn);
+    if (m > 0 && w->rows > 0 && (ldc < w->rows || lda < w->cols))
+        return grx_fail(GRX_EINVAL, "%s: ldc %d < %d or lda %d < %d", fn, ldc, w->rows, lda, w->cols);
+    if (ctx->device != w->device) return grx_fail(GRX_EINVAL, "%s: weight lives on device %d, context on %d", fn, w->device, ctx->device);
+    return GRX_OK;
+}
+
+// Rows of activations in launches of 8, 4, 2 and 1.
+static grx_status gemv_rows_preq(hipStream_t st, float *dst, int ldc, const int8_t *q, const float *sc,
+                                 int m, const grx_weight *w, const float *bias) {
+    const int K = w->cols, nb = w->nb;
+    int i = 0;
+    while (i < m) {
+        const int left = m - i;
+        const int mm = left >= 8 ? 8 : left >= 4 ? 4 : left >= 2 ? 2 : 1;
+        GemvArgs a = {};
+        a.qs = w->qs;
+        a.ds = w->ds;
+        a.rows = w->rows;
+        a.nb = nb;
+        a.xq = q + (size_t)i * K;
+        a.xs = sc + (size_t)i * nb;
+        a.y = dst + (size_t)i * ldc;
+        a.ldc = ldc;
+        a.bias = bias;
+        grx_status s = grx_gemv_launch(st, mm, GRX_PRO_PREQ, GRX_EPI_STORE, a, 0);
+        if (s != GRX_OK) return s;
+        i += mm;
+    }
+    return GRX_OK;
+}
+
+extern "C" grx_status grx_quant_act_dev(grx_ctx *ctx, int8_t *q, float *sc, const float *x, int lda,
+                                        int m, int k) {
+    if (!ctx) return grx_fail(GRX_EINVAL, "grx_quant_act_dev: NULL context");
+    if (m < 0 || k < 0 || lda < k) return grx_fail(GRX_EINVAL, "grx_quant_act_dev: bad shape");
+    if (k % GRX_QK != 0) return grx_fail(GRX_ESIZE, "grx_quant_act_dev: k %d is not a multiple of 32", k);
+    const int nb = k / GRX_QK;
+    if (m * nb == 0) return GRX_OK;
+    if (!q || !sc || !x) return grx_fail(GRX_EINVAL, "grx_quant_act_dev: NULL buffer");
+    GRX_HIP(hipSetDevice(ctx->device));
+    quant_act_kernel<<<grx_ceil_div(m * nb, 256), 256, 0, ctx->stream>>>(x, lda, m, nb, q, sc);
+    GRX_LAUNCHED("quant_act_kernel");
+    return GRX_OK;
+}
+
+extern "C" grx_status grx_matmul_q8_prequant_dev(grx_ctx *ctx, float *dst, int ldc, const int8_t *q,
+                                                 const float *sc, int m, const grx_weight *w,
+                                                 const float *bias) {
+    grx_status s = check_mm("grx_matmul_q8_prequant_dev", ctx, dst, ldc, q, w ? w->cols : 0, m, w);
+    if (s != GRX_OK) return s;
+    if (m == 0 || w->rows == 0) return GRX_OK;
+    if (!sc && w->cols > 0) return grx_fail(GRX_EINVAL, "grx_matmul_q8_prequant_dev: NULL scales");
+    GRX_HIP(hipSetDevice(ctx->device));
+    return gemv_rows_preq(ctx->stream, dst, ldc, q, sc, m, w, bias);
+}
+
+extern "C" grx_status grx_matmul_q8_dev(grx_ctx *ctx, float *dst, int ldc, const float *x, int lda, int m,
+                                        const grx_weight *w, const float *bias) {
+    grx_status s = check_mm("grx_matmul_q8_dev", ctx, dst, ldc, x, lda, m, w);
+    if (s != GRX_OK) return s;
+    if (m == 0 || w->rows == 0) return GRX_OK;
+    GRX_HIP(hipSetDevice(ctx->device));
+    const int K = w->cols, nb = w->nb;
+    void *buf;
+    const size_t qbytes = ((size_t)m * K + 255) & ~(size_t)255;
+    s = grx_ctx_scratch(ctx, qbytes + (size_t)m * nb * 4 + 16, &buf);
+    if (s != GRX_OK) return s;
+    int8_t *q = (int8_t *)buf;
+    float *sc = (float *)((char *)buf + qbytes);
+    s = grx_quant_act_dev(ctx, q, sc, x, lda, m, K);
+    if (s != GRX_OK) return s;
+    return grx_matmul_q8_prequant_dev(ctx, dst, ldc, q, sc, m, w, bias);
+}
+
+extern "C" grx_status grx_matmul_q8(grx_ctx *ctx, float *dst, int ldc, const float *x, int lda, int m,
+                                    const grx_weight *w, const float *bias) {
+    grx_status s = check_mm("grx_matmul_q8", ctx, dst, ldc, x, lda, m, w);
+    if (s != GRX_OK) return s;
+    if (m == 0 || w->rows == 0) return GRX_OK;
+    GRX_HIP(hipSetDevice(ctx->device));
+    const int K = w->cols, N = w->rows, nb = w->nb;
+    // device staging: [x m*K][y m*N][bias N][q m*K][sc m*nb]
+    auto al = [](size_t n) { return (n + 255) & ~(size_t)255; };
+    const size_t xb = al((size_t)m * K * 4), yb = al((size_t)m * N * 4), bb = al((size_t)N * 4);
+    const size_t qb = al((size_t)m * K), sb = al((size_t)m * nb * 4 + 4);
+    void *buf;
+    s = grx_ctx_scratch(ctx, xb + yb + bb + qb + sb, &buf);
+    if (s != GRX_OK) return s;
+    char *p = (char *)buf;
+    float *dx = (float *)p, *dy = (float *)(p + xb), *db = (float *)(p + xb + yb);
+    int8_t *dq = (int8_t *)(p + xb + yb + bb);
+    float *dsc = (float *)(p + xb + yb + bb + qb);
+    if (K > 0)
+        GRX_HIP(hipMemcpy2DAsync(dx, (size_t)K * 4, x, (size_t)lda * 4, (size_t)K * 4, m, hipMemcpyHostToDevice,
+                                 ctx->stream));
+    if (bias) GRX_HIP(hipMemcpyAsync(db, bias, (size_t)N * 4, hipMemcpyHostToDevice, ctx->stream));
+    if (K > 0) {
+        s = grx_quant_act_dev(ctx, dq, dsc, dx, K, m, K);
+        if (s != GRX_OK) return s;
+    }
+    s = grx_matmul_q8_prequant_dev(ctx, dy, N, dq, dsc, m, w, bias ? db : nullptr);
+    if (s != GRX_OK) return s;
+    GRX_HIP(hipMemcpy2DAsync(dst, (size_t)ldc * 4, dy, (size_t)N * 4, (size_t)N * 4, m, hipMemcpyDeviceToHost,
+                             ctx->stream));
+    GRX_HIP(hipStreamSynchronize(ctx->stream));
+    return GRX_OK;
+}
+
+extern "C" grx_status grx_linear_q8(grx_ctx *ctx, float *dst, const float *x, int m, const grx_weight *w,
+                                    const float *bias) {
+    if (!w) return grx_fail(GRX_EINVAL, "grx_linear_q8: NULL weight");
+    return grx_matmul_q8(ctx, dst, w->rows, x, w->cols, m, w, bias);
+}
+
+extern "C" grx_status grx_block_dots_dev(grx_ctx *ctx, int32_t *s, const int8_t *q, int m, const grx_weight *w) {
+    if (!ctx || !w) return grx_fail(GRX_EINVAL, "grx_block_dots_dev: NULL context or weight");
+    if (m < 0) return grx_fail(GRX_EINVAL, "grx_block_dots_dev: m = %d", m);
+    const size_t n = (size_t)m * w->rows * w->nb;
+    if (n == 0) return GRX_OK;
+    if (!s || !q) return grx_fail(GRX_EINVAL, "grx_block_dots_dev: NULL buffer");
+    GRX_HIP(hipSetDevice(ctx->device));
+    block_dots_kernel<<<(int)((n + 255) / 256), 256, 0, ctx->stream>>>(w->qs, w->rows, w->nb, q, m, s);
+    GRX_LAUNCHED("block_dots_kernel");
+    return GRX_OK;
+}

@@ -1,0 +1,128 @@
+/*
+ * grx.h - C ABI of the MI355X (gfx950) Q8_0 product library, libgrx.so.
+ *
+ * It replaces the Q8_0 branch of gorelaxor's operator seam, package
+ * internal/kern (github.com/xattribution/gorelaxor), for callers that hold a
+ * GPU.  Each entry point names the reference function it stands in for as
+ * file:line of that module.  Plain C types only: no HIP or torch types cross
+ * this boundary, so a cgo, ctypes or FFI binding needs nothing but this file.
+ *
+ * Conventions
+ *  - Every call returns a grx_status; 0 is success.  On failure,
+ *    grx_last_error() returns a message for the calling thread.  Nothing
+ *    throws across the boundary.
+ *  - Matrices are row-major.  A weight is `rows` outputs by `cols` inputs
+ *    (kern.Weight, internal/kern/kern.go:38-50); `cols` is a multiple of 32.
+ *  - Entry points without the _dev suffix take host pointers and return
+ *    when the result is in host memory.  _dev entry points take device
+ *    pointers (HBM) and only enqueue work on the context's stream; call
+ *    grx_ctx_sync() before reading the results.
+ *  - Threading: a grx_weight is immutable after creation and may be used
+ *    from any number of contexts and threads at once.  A grx_ctx owns one
+ *    HIP stream and its scratch buffers: use one context per thread.
+ */
+#ifndef GRX_H
+#define GRX_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef enum {
+    GRX_OK = 0,
+    GRX_EINVAL = -1,   /* a null pointer, negative size or stride too small */
+    GRX_ESIZE = -2,    /* a buffer too short for the shape, or cols % 32 != 0 */
+    GRX_EDEVICE = -3,  /* a HIP runtime error (message has the HIP text) */
+    GRX_ENOMEM = -4,   /* device memory exhausted */
+    GRX_ESTATE = -5,   /* call out of order (e.g. decoding past the context) */
+    GRX_ENODEV = -6    /* no gfx950 device visible */
+} grx_status;
+
+typedef struct grx_ctx grx_ctx;
+typedef struct grx_weight grx_weight;
+
+/* Library */
+int grx_version(void);
+const char *grx_last_error(void);
+/* Number of visible devices; 0 when there is no GPU (never an error). */
+int grx_device_count(void);
+
+/* Context: a device and one stream.  No reference counterpart: the
+ * reference runs on the calling goroutine (internal/kern/gemm.go:52-108). */
+grx_status grx_ctx_create(int device, grx_ctx **out);
+grx_status grx_ctx_destroy(grx_ctx *ctx);
+grx_status grx_ctx_sync(grx_ctx *ctx);
+/* The context's hipStream_t, as an opaque pointer, for callers that order
+ * their own device work with it. */
+void *grx_ctx_stream(grx_ctx *ctx);
+
+/* ---- Q8_0 weights ---- */
+
+/* kern.NewQ8 + Weight.Pack + Weight.DropRows (internal/kern/kern.go:76-103,
+ * q8int.go:35-64): check the shape, copy `rows` ggml Q8_0 rows (cols/32
+ * blocks of 34 bytes: a little-endian float16 scale, then 32 int8 values)
+ * to the device and repack them once into the HBM tile layout the GEMV
+ * streams.  The host buffer may be freed on return.  Errors as NewQ8:
+ * GRX_ESIZE when cols % 32 != 0 or nbytes < rows*cols/32*34. */
+grx_status grx_weight_q8_create(grx_ctx *ctx, int rows, int cols, const uint8_t *q8,
+                                size_t nbytes, grx_weight **out);
+grx_status grx_weight_destroy(grx_weight *w);
+/* Weight.Rows / Weight.Cols (kern.go:42). */
+int grx_weight_rows(const grx_weight *w);
+int grx_weight_cols(const grx_weight *w);
+/* Weight.Bytes (kern.go:172-179): device bytes the weight holds. */
+size_t grx_weight_bytes(const grx_weight *w);
+/* Weight.Row (kern.go:115-122, q8int.go:66-78): widen row j to float32,
+ * exactly. */
+grx_status grx_weight_row(grx_ctx *ctx, const grx_weight *w, int j, float *dst);
+/* Weight.Float32 (kern.go:124-134): the whole matrix widened, rows*cols. */
+grx_status grx_weight_float32(grx_ctx *ctx, const grx_weight *w, float *dst);
+
+/* Weight.ToQ8 (kern.go:136-170) on the device: round rows*cols float32
+ * values (cols % 32 == 0) to ggml Q8_0 bytes, rows*cols/32*34 of them,
+ * each block's scale amax/127 and each value rounded half away from zero. */
+grx_status grx_to_q8(grx_ctx *ctx, int rows, int cols, const float *v, uint8_t *q8_out);
+
+/* ---- products ---- */
+
+/* kern.MatMul (internal/kern/kern.go:183-196) on the int8 route of
+ * matmulQ8Int (q8int.go:148-223): dst[m][ldc] = x[m][lda] . W^T + bias.
+ * Each row of x is rounded to Q8_0 per 32 values (quantU8,
+ * q8int.go:88-105); each output starts from the bias (or 0) and takes
+ * c = fma(f32(s_b)*dw_b, da_b, c) block by block in order, as the VNNI
+ * kernel does (vnni_amd64.s:58-69), so results are bit-identical to it.
+ * bias may be NULL.  m == 0 is a no-op (kern.go:186-188). */
+grx_status grx_matmul_q8(grx_ctx *ctx, float *dst, int ldc, const float *x, int lda, int m,
+                         const grx_weight *w, const float *bias);
+/* kern.Linear (kern.go:198-201): MatMul with ldc = rows, lda = cols. */
+grx_status grx_linear_q8(grx_ctx *ctx, float *dst, const float *x, int m, const grx_weight *w,
+                         const float *bias);
+/* grx_matmul_q8 on device pointers, enqueued on the context's stream. */
+grx_status grx_matmul_q8_dev(grx_ctx *ctx, float *dst, int ldc, const float *x, int lda, int m,
+                             const grx_weight *w, const float *bias);
+
+/* quantU8 (internal/kern/q8int.go:86-105, vnni_amd64.s:194-256) on device
+ * pointers: round m rows of k float32 values (k % 32 == 0, rows lda apart)
+ * to signed int8 q[m][k] (the reference's unsigned byte minus 128) and one
+ * float32 scale per 32 values, sc[m][k/32]. */
+grx_status grx_quant_act_dev(grx_ctx *ctx, int8_t *q, float *sc, const float *x, int lda, int m,
+                             int k);
+/* The int8 product from activations rounded already (grx_quant_act_dev's
+ * output), device pointers.  The per-block int32 dots and the finalize are
+ * those of grx_matmul_q8. */
+grx_status grx_matmul_q8_prequant_dev(grx_ctx *ctx, float *dst, int ldc, const int8_t *q,
+                                      const float *sc, int m, const grx_weight *w,
+                                      const float *bias);
+/* The per-block int32 dot products s[m][rows][cols/32] of rounded
+ * activations with the weight (q8tile's int32 sums, vnni_amd64.s:34-54
+ * minus the 128*sum(w) offset), device pointers.  For parity checks. */
+grx_status grx_block_dots_dev(grx_ctx *ctx, int32_t *s, const int8_t *q, int m,
+                              const grx_weight *w);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,103 @@
+/*
+ * grx_oracle.h - CPU restatement of gorelaxor's Q8_0 hot path.
+ *
+ * TEST INFRASTRUCTURE ONLY.  This library is the checker that the HIP
+ * product is compared against; it is linked or loaded only by tests/,
+ * __graft_entry__.smoke() and the cpu_baseline leg of bench.py.  The
+ * product (gorelaxor_amd/libgrx.so) never calls into it.
+ *
+ * Every function restates one reference function, in the same arithmetic
+ * order, and cites it as file:line of the reference Go module
+ * github.com/xattribution/gorelaxor.  Where the reference has both a Go
+ * twin and an AVX2/VNNI assembly kernel, the restatement follows the
+ * kernel a VNNI host actually runs (the assembly), and says so.
+ *
+ * Floating point: the library is built with -ffp-contract=off; every fused
+ * multiply-add below is an explicit fmaf() matching a VFMADD in the
+ * reference assembly, and every other product is rounded on its own, as
+ * Go (GOAMD64=v1, no fusion) and the non-FMA instructions round it.
+ */
+#ifndef GRX_ORACLE_H
+#define GRX_ORACLE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define ORC_QK 32
+#define ORC_Q8_BYTES 34
+
+/* ---- half precision (internal/kern/f16.go) ---- */
+float orc_f16_to_f32(uint16_t h);
+uint16_t orc_f32_to_f16(float f);
+
+/* ---- weight rounding (kern.go ToQ8, kern_test.go quantQ8) ---- */
+void orc_quant_q8(const float *v, size_t nvals, uint8_t *out);
+void orc_dequant_q8(float *dst, const uint8_t *q, int nb);
+
+/* ---- activation rounding (q8int.go quantU8Go / vnni_amd64.s quantU8avx) ---- */
+void orc_quant_u8(uint8_t *dst, float *sc, const float *x, int nb);
+void orc_quant_act_i8(int8_t *dst, float *sc, const float *x, int nb);
+
+/* ---- int8 products ---- */
+void orc_block_dots(int32_t *s, const int8_t *qa, int m, const uint8_t *wq, int n, int k);
+void orc_matmul_q8_int(float *c, int ldc, const float *a, int lda, int m,
+                       const uint8_t *wq, int n, int k, const float *bias, int evex);
+void orc_matmul_q8_int_prequant(float *c, int ldc, const int8_t *qa, const float *sa, int m,
+                                const uint8_t *wq, int n, int k, const float *bias);
+void orc_matmul_q8_float(float *c, int ldc, const float *a, int lda, int m,
+                         const uint8_t *wq, int n, int k, const float *bias);
+
+/* ---- float kernels (mathx.go, kernels_amd64.s) ---- */
+float orc_expf(float x);
+float orc_exp8(float x);
+float orc_expsub(float *x, int n, float mx);
+void orc_softmax(float *x, int n);
+void orc_gelu_vec(float *x, int n);
+void orc_silu_vec(float *x, int n);
+void orc_axpy(float *dst, const float *src, int n, float s);
+void orc_layernorm(float *dst, const float *src, int rows, int n, const float *w, const float *b);
+void orc_layernorm_f64(float *dst, const float *src, int rows, int n, const float *w,
+                       const float *b, double eps);
+float orc_dot_f32_go(const float *x, const float *y, int n);
+void orc_dot_f32_x4(const float *x, const float *w, int ld, int k, float out[4]);
+int orc_argmax(const float *x, int n);
+
+/* ---- whisper-shaped decoder with Q8_0 weights (whisper/decoder.go) ---- */
+typedef struct {
+    const float *attn_ln_w, *attn_ln_b;
+    const uint8_t *q, *k, *v, *o;
+    const float *q_b, *v_b, *o_b;
+    const float *x_ln_w, *x_ln_b;
+    const uint8_t *xq, *xk, *xv, *xo;
+    const float *xq_b, *xv_b, *xo_b;
+    const float *mlp_ln_w, *mlp_ln_b;
+    const uint8_t *fc1, *fc2;
+    const float *fc1_b, *fc2_b;
+    float *cross_k; /* [head][audio_ctx][head_dim], keys pre-scaled */
+    float *cross_v; /* [head][head_dim][audio_ctx] */
+    float *self_k;  /* [text_ctx][state] */
+    float *self_v;  /* [text_ctx][state] */
+} orc_whisper_layer;
+
+typedef struct {
+    int n_vocab, n_text_ctx, n_state, n_head, n_layer, n_audio_ctx;
+    const uint8_t *tok_emb; /* Q8_0 [n_vocab][n_state] */
+    const float *dec_pos;   /* [n_text_ctx][n_state] */
+    const float *dec_ln_w, *dec_ln_b;
+    orc_whisper_layer *layers;
+    int n; /* positions filled in the self-attention caches */
+} orc_whisper;
+
+void orc_whisper_cross_kv(orc_whisper *m, const float *enc);
+int orc_whisper_decode(orc_whisper *m, const int *tokens, int nt, float *logits);
+void orc_whisper_greedy(orc_whisper *m, const int *prompt, int n_prompt, int n_steps,
+                        int *out_tokens);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,370 @@
+"""numpy front end of the C oracle (oracle/grx_oracle.c).
+
+TEST INFRASTRUCTURE ONLY: loaded by tests/, __graft_entry__.smoke() and
+bench.py's cpu_baseline leg as the checker of the HIP product.
+
+Each wrapper names the reference function (file:line in the Go module
+github.com/xattribution/gorelaxor) the C restatement follows.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+import subprocess
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "_build", "liboracle.so")
+
+QK = 32
+Q8_BYTES = 34
+
+
+def build(force: bool = False) -> str:
+    """Compile the oracle with its Makefile (gcc, no GPU needed)."""
+    if force or not os.path.exists(LIB_PATH):
+        subprocess.run(["make", "-s", "-C", HERE, "-B" if force else "all"], check=True)
+    return LIB_PATH
+
+
+_lib = None
+
+
+def lib() -> C.CDLL:
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            build()
+        _lib = C.CDLL(LIB_PATH)
+        _declare(_lib)
+    return _lib
+
+
+_f32p = np.ctypeslib.ndpointer(np.float32, flags="C_CONTIGUOUS")
+_u8p = np.ctypeslib.ndpointer(np.uint8, flags="C_CONTIGUOUS")
+_i8p = np.ctypeslib.ndpointer(np.int8, flags="C_CONTIGUOUS")
+_i32p = np.ctypeslib.ndpointer(np.int32, flags="C_CONTIGUOUS")
+
+
+def _declare(L):
+    L.orc_f16_to_f32.argtypes = [C.c_uint16]
+    L.orc_f16_to_f32.restype = C.c_float
+    L.orc_f32_to_f16.argtypes = [C.c_float]
+    L.orc_f32_to_f16.restype = C.c_uint16
+    L.orc_quant_q8.argtypes = [_f32p, C.c_size_t, _u8p]
+    L.orc_dequant_q8.argtypes = [_f32p, _u8p, C.c_int]
+    L.orc_quant_u8.argtypes = [_u8p, _f32p, _f32p, C.c_int]
+    L.orc_quant_act_i8.argtypes = [_i8p, _f32p, _f32p, C.c_int]
+    L.orc_block_dots.argtypes = [_i32p, _i8p, C.c_int, _u8p, C.c_int, C.c_int]
+    L.orc_matmul_q8_int.argtypes = [_f32p, C.c_int, _f32p, C.c_int, C.c_int, _u8p, C.c_int,
+                                    C.c_int, C.c_void_p, C.c_int]
+    L.orc_matmul_q8_int_prequant.argtypes = [_f32p, C.c_int, _i8p, _f32p, C.c_int, _u8p,
+                                             C.c_int, C.c_int, C.c_void_p]
+    L.orc_matmul_q8_float.argtypes = [_f32p, C.c_int, _f32p, C.c_int, C.c_int, _u8p, C.c_int,
+                                      C.c_int, C.c_void_p]
+    L.orc_expf.argtypes = [C.c_float]
+    L.orc_expf.restype = C.c_float
+    L.orc_exp8.argtypes = [C.c_float]
+    L.orc_exp8.restype = C.c_float
+    L.orc_expsub.argtypes = [_f32p, C.c_int, C.c_float]
+    L.orc_expsub.restype = C.c_float
+    L.orc_softmax.argtypes = [_f32p, C.c_int]
+    L.orc_gelu_vec.argtypes = [_f32p, C.c_int]
+    L.orc_silu_vec.argtypes = [_f32p, C.c_int]
+    L.orc_axpy.argtypes = [_f32p, _f32p, C.c_int, C.c_float]
+    L.orc_layernorm.argtypes = [_f32p, _f32p, C.c_int, C.c_int, _f32p, _f32p]
+    L.orc_layernorm_f64.argtypes = [_f32p, _f32p, C.c_int, C.c_int, C.c_void_p, C.c_void_p,
+                                    C.c_double]
+    L.orc_dot_f32_go.argtypes = [_f32p, _f32p, C.c_int]
+    L.orc_dot_f32_go.restype = C.c_float
+    L.orc_dot_f32_x4.argtypes = [_f32p, _f32p, C.c_int, C.c_int, _f32p]
+    L.orc_argmax.argtypes = [_f32p, C.c_int]
+    L.orc_argmax.restype = C.c_int
+    L.orc_whisper_cross_kv.argtypes = [C.c_void_p, _f32p]
+    L.orc_whisper_decode.argtypes = [C.c_void_p, _i32p, C.c_int, C.c_void_p]
+    L.orc_whisper_decode.restype = C.c_int
+    L.orc_whisper_greedy.argtypes = [C.c_void_p, _i32p, C.c_int, C.c_int, _i32p]
+
+
+def _f32(a):
+    return np.ascontiguousarray(a, dtype=np.float32)
+
+
+def _ptr(a):
+    return None if a is None else a.ctypes.data_as(C.c_void_p)
+
+
+# ---- half precision (internal/kern/f16.go:14-71) ----
+
+def f16_to_f32(h: int) -> float:
+    return lib().orc_f16_to_f32(h)
+
+
+def f32_to_f16(f: float) -> int:
+    return lib().orc_f32_to_f16(f)
+
+
+# ---- Q8_0 weights (kern.go:139-170, kern_test.go:10-28) ----
+
+def quant_q8(v: np.ndarray) -> np.ndarray:
+    """Round float32 values (a multiple of 32) to ggml Q8_0 bytes."""
+    v = _f32(v).ravel()
+    assert v.size % QK == 0
+    out = np.zeros(v.size // QK * Q8_BYTES, np.uint8)
+    lib().orc_quant_q8(v, v.size, out)
+    return out
+
+
+def dequant_q8(q: np.ndarray, nvals: int) -> np.ndarray:
+    q = np.ascontiguousarray(q, np.uint8)
+    out = np.zeros(nvals, np.float32)
+    lib().orc_dequant_q8(out, q, nvals // QK)
+    return out
+
+
+# ---- activations (q8int.go:88-105) ----
+
+def quant_u8(x: np.ndarray):
+    x = _f32(x).ravel()
+    nb = x.size // QK
+    q = np.zeros(nb * QK, np.uint8)
+    sc = np.zeros(nb, np.float32)
+    lib().orc_quant_u8(q, sc, x, nb)
+    return q, sc
+
+
+def quant_act_i8(x: np.ndarray):
+    """Activation rounding with the signed value kept (u8 - 128), per row."""
+    x = _f32(x)
+    rows = x.reshape(-1, x.shape[-1]) if x.ndim > 1 else x.reshape(1, -1)
+    k = rows.shape[1]
+    nb = k // QK
+    q = np.zeros((rows.shape[0], k), np.int8)
+    sc = np.zeros((rows.shape[0], nb), np.float32)
+    for i in range(rows.shape[0]):
+        qi = np.zeros(k, np.int8)
+        si = np.zeros(nb, np.float32)
+        lib().orc_quant_act_i8(qi, si, np.ascontiguousarray(rows[i]), nb)
+        q[i], sc[i] = qi, si
+    return q, sc
+
+
+# ---- int8 products (q8int.go:148-223, vnni_amd64.s:58-69) ----
+
+def block_dots(qa: np.ndarray, wq: np.ndarray, n: int, k: int) -> np.ndarray:
+    qa = np.ascontiguousarray(qa, np.int8).reshape(-1, k)
+    m = qa.shape[0]
+    s = np.zeros((m, n, k // QK), np.int32)
+    lib().orc_block_dots(s, qa, m, np.ascontiguousarray(wq, np.uint8), n, k)
+    return s
+
+
+def matmul_q8_int(x: np.ndarray, wq: np.ndarray, n: int, k: int, bias=None,
+                  evex: bool = True) -> np.ndarray:
+    """kern.MatMul on the int8 route: x [m][k] float32, wq Q8_0 rows [n]."""
+    x = _f32(x).reshape(-1, k)
+    m = x.shape[0]
+    c = np.zeros((m, n), np.float32)
+    b = None if bias is None else _f32(bias)
+    lib().orc_matmul_q8_int(c, n, x, k, m, np.ascontiguousarray(wq, np.uint8), n, k, _ptr(b),
+                            1 if evex else 0)
+    return c
+
+
+def matmul_q8_int_prequant(qa, sa, wq, n: int, k: int, bias=None) -> np.ndarray:
+    qa = np.ascontiguousarray(qa, np.int8).reshape(-1, k)
+    sa = _f32(sa).reshape(qa.shape[0], k // QK)
+    m = qa.shape[0]
+    c = np.zeros((m, n), np.float32)
+    b = None if bias is None else _f32(bias)
+    lib().orc_matmul_q8_int_prequant(c, n, qa, sa, m, np.ascontiguousarray(wq, np.uint8), n, k,
+                                     _ptr(b))
+    return c
+
+
+def matmul_q8_float(x: np.ndarray, wq: np.ndarray, n: int, k: int, bias=None) -> np.ndarray:
+    """kern.MatMul on the float route (gemvRows, m <= 16)."""
+    x = _f32(x).reshape(-1, k)
+    m = x.shape[0]
+    assert m <= 16
+    c = np.zeros((m, n), np.float32)
+    b = None if bias is None else _f32(bias)
+    lib().orc_matmul_q8_float(c, n, x, k, m, np.ascontiguousarray(wq, np.uint8), n, k, _ptr(b))
+    return c
+
+
+# ---- float kernels (mathx.go, kernels_amd64.s) ----
+
+def expf(x: float) -> float:
+    return lib().orc_expf(x)
+
+
+def exp8(x: float) -> float:
+    return lib().orc_exp8(x)
+
+
+def expsub(x: np.ndarray, mx: float):
+    x = _f32(x).copy()
+    s = lib().orc_expsub(x, x.size, mx)
+    return x, s
+
+
+def softmax(x: np.ndarray) -> np.ndarray:
+    x = _f32(x).copy()
+    lib().orc_softmax(x, x.size)
+    return x
+
+
+def gelu(x: np.ndarray) -> np.ndarray:
+    x = _f32(x).copy()
+    lib().orc_gelu_vec(x, x.size)
+    return x
+
+
+def silu(x: np.ndarray) -> np.ndarray:
+    x = _f32(x).copy()
+    lib().orc_silu_vec(x, x.size)
+    return x
+
+
+def axpy(dst: np.ndarray, src: np.ndarray, s: float) -> np.ndarray:
+    dst = _f32(dst).copy()
+    lib().orc_axpy(dst, _f32(src), dst.size, s)
+    return dst
+
+
+def layernorm(x: np.ndarray, w: np.ndarray, b: np.ndarray) -> np.ndarray:
+    x = _f32(x)
+    n = x.shape[-1]
+    rows = x.size // n
+    y = np.zeros_like(x)
+    lib().orc_layernorm(y, x, rows, n, _f32(w), _f32(b))
+    return y
+
+
+def layernorm_f64(x: np.ndarray, w=None, b=None, eps: float = 1e-5) -> np.ndarray:
+    x = _f32(x)
+    n = x.shape[-1]
+    rows = x.size // n
+    y = np.zeros_like(x)
+    wf = None if w is None else _f32(w)
+    bf = None if b is None else _f32(b)
+    lib().orc_layernorm_f64(y, x, rows, n, _ptr(wf), _ptr(bf), eps)
+    return y
+
+
+def dot_f32_go(x, y) -> float:
+    x, y = _f32(x), _f32(y)
+    return lib().orc_dot_f32_go(x, y, x.size)
+
+
+def dot_f32_x4(x, w, ld: int, k: int) -> np.ndarray:
+    out = np.zeros(4, np.float32)
+    lib().orc_dot_f32_x4(_f32(x), _f32(w), ld, k, out)
+    return out
+
+
+def argmax(x) -> int:
+    x = _f32(x)
+    return lib().orc_argmax(x, x.size)
+
+
+# ---- whisper-shaped decoder (whisper/decoder.go:33-140) ----
+
+class _Layer(C.Structure):
+    _fields_ = [(n, C.c_void_p) for n in (
+        "attn_ln_w", "attn_ln_b", "q", "k", "v", "o", "q_b", "v_b", "o_b",
+        "x_ln_w", "x_ln_b", "xq", "xk", "xv", "xo", "xq_b", "xv_b", "xo_b",
+        "mlp_ln_w", "mlp_ln_b", "fc1", "fc2", "fc1_b", "fc2_b",
+        "cross_k", "cross_v", "self_k", "self_v")]
+
+
+class _Model(C.Structure):
+    _fields_ = [("n_vocab", C.c_int), ("n_text_ctx", C.c_int), ("n_state", C.c_int),
+                ("n_head", C.c_int), ("n_layer", C.c_int), ("n_audio_ctx", C.c_int),
+                ("tok_emb", C.c_void_p), ("dec_pos", C.c_void_p), ("dec_ln_w", C.c_void_p),
+                ("dec_ln_b", C.c_void_p), ("layers", C.c_void_p), ("n", C.c_int)]
+
+
+class WhisperOracle:
+    """Oracle decoder over a tensor dict named as whisper/model.go:376-401 binds
+    them ("decoder.blocks.{i}.attn.query.weight", ...); Q8_0 matrices as uint8
+    rows, vectors as float32."""
+
+    _LAYER_MAP = {
+        "attn_ln_w": "attn_ln.weight", "attn_ln_b": "attn_ln.bias",
+        "q": "attn.query.weight", "k": "attn.key.weight", "v": "attn.value.weight",
+        "o": "attn.out.weight", "q_b": "attn.query.bias", "v_b": "attn.value.bias",
+        "o_b": "attn.out.bias", "x_ln_w": "cross_attn_ln.weight", "x_ln_b": "cross_attn_ln.bias",
+        "xq": "cross_attn.query.weight", "xk": "cross_attn.key.weight",
+        "xv": "cross_attn.value.weight", "xo": "cross_attn.out.weight",
+        "xq_b": "cross_attn.query.bias", "xv_b": "cross_attn.value.bias",
+        "xo_b": "cross_attn.out.bias", "mlp_ln_w": "mlp_ln.weight", "mlp_ln_b": "mlp_ln.bias",
+        "fc1": "mlp.0.weight", "fc2": "mlp.2.weight", "fc1_b": "mlp.0.bias", "fc2_b": "mlp.2.bias",
+    }
+
+    def __init__(self, hp: dict, tensors: dict):
+        self.hp = hp
+        st, nh, nl = hp["n_state"], hp["n_head"], hp["n_layer"]
+        nctx, tctx = hp["n_audio_ctx"], hp["n_text_ctx"]
+        self._keep = []
+
+        def keep(a):
+            a = np.ascontiguousarray(a)
+            self._keep.append(a)
+            return a.ctypes.data
+
+        layers = (_Layer * nl)()
+        self.cross_k, self.cross_v, self.self_k, self.self_v = [], [], [], []
+        for i in range(nl):
+            p = f"decoder.blocks.{i}."
+            for field, name in self._LAYER_MAP.items():
+                setattr(layers[i], field, keep(tensors[p + name]))
+            ck = np.zeros(nctx * st, np.float32)
+            cv = np.zeros(nctx * st, np.float32)
+            sk = np.zeros(tctx * st, np.float32)
+            sv = np.zeros(tctx * st, np.float32)
+            self.cross_k.append(ck)
+            self.cross_v.append(cv)
+            self.self_k.append(sk)
+            self.self_v.append(sv)
+            layers[i].cross_k = keep(ck)
+            layers[i].cross_v = keep(cv)
+            layers[i].self_k = keep(sk)
+            layers[i].self_v = keep(sv)
+        self._layers = layers
+        m = _Model()
+        m.n_vocab, m.n_text_ctx, m.n_state = hp["n_vocab"], tctx, st
+        m.n_head, m.n_layer, m.n_audio_ctx = nh, nl, nctx
+        m.tok_emb = keep(tensors["decoder.token_embedding.weight"])
+        m.dec_pos = keep(tensors["decoder.positional_embedding"])
+        m.dec_ln_w = keep(tensors["decoder.ln.weight"])
+        m.dec_ln_b = keep(tensors["decoder.ln.bias"])
+        m.layers = C.cast(layers, C.c_void_p)
+        m.n = 0
+        self._m = m
+
+    @property
+    def n(self) -> int:
+        return self._m.n
+
+    def reset(self):
+        self._m.n = 0
+
+    def set_encoder_output(self, enc: np.ndarray):
+        lib().orc_whisper_cross_kv(C.byref(self._m), _f32(enc))
+
+    def decode(self, tokens) -> np.ndarray:
+        toks = np.ascontiguousarray(tokens, np.int32)
+        lg = np.zeros(self.hp["n_vocab"], np.float32)
+        rc = lib().orc_whisper_decode(C.byref(self._m), toks, toks.size, _ptr(lg))
+        if rc != 0:
+            raise ValueError("tokens do not fit the text context")
+        return lg
+
+    def greedy(self, prompt, n_steps: int) -> np.ndarray:
+        p = np.ascontiguousarray(prompt, np.int32)
+        out = np.zeros(n_steps + 1, np.int32)
+        lib().orc_whisper_greedy(C.byref(self._m), p, p.size, n_steps, out)
+        return out

@@ -1,0 +1,239 @@
+"""Parity of the HIP Q8_0 product (libgrx.so through its C ABI) with the CPU
+oracle: bit-exact for the int8 work and for the float32 outputs, since the
+kernels keep the VNNI kernel's per-output order (vnni_amd64.s:58-69).
+
+Structure follows the reference tests (internal/kern/q8int_test.go,
+odd_test.go, kern_test.go of github.com/xattribution/gorelaxor).
+"""
+import os
+
+import numpy as np
+import pytest
+
+from gorelaxor_amd.synth import gemv_inputs, q8_weight
+
+pytestmark = pytest.mark.gpu
+
+QK = 32
+
+
+def _bits_equal(a, b):
+    a = np.ascontiguousarray(a, np.float32)
+    b = np.ascontiguousarray(b, np.float32)
+    return a.shape == b.shape and np.array_equal(a.view(np.uint32), b.view(np.uint32))
+
+
+def _report(got, want):
+    d = np.abs(got.astype(np.float64) - want)
+    i = int(np.argmax(d))
+    return f"max |diff| {d.max():.3g} at {i}: got {got.ravel()[i]!r} want {want.ravel()[i]!r}"
+
+
+@pytest.fixture
+def torch_dev():
+    import torch
+
+    assert torch.cuda.is_available()
+    return torch
+
+
+# ---------------------------------------------------------------- weights
+
+def test_row_and_float32_exact(kern, orc):
+    """Weight.Row / Float32 (kern.go:115-134) exactly d*q, a negative
+    subnormal scale (0x8001, odd_test.go:86-88) included."""
+    rng = np.random.default_rng(8)
+    n, k = 37, 96
+    wv = (rng.random(n * k) * 2 - 1).astype(np.float32)
+    q8 = orc.quant_q8(wv)
+    q8[0], q8[1] = 0x01, 0x80
+    w = kern.NewQ8(n, k, q8)
+    ref = orc.dequant_q8(q8, n * k)
+    assert _bits_equal(w.Float32(), ref)
+    row = np.zeros(k, np.float32)
+    for j in (0, 1, 36):
+        w.Row(row, j)
+        assert _bits_equal(row, ref[j * k:(j + 1) * k])
+    assert w.Bytes() >= n * k
+
+
+def test_newq8_errors(kern):
+    """NewQ8's checks (kern.go:76-84): cols % 32 and a short buffer."""
+    with pytest.raises(kern.GrxError, match="multiple of 32"):
+        kern.NewQ8(2, 40, np.zeros(200, np.uint8))
+    with pytest.raises(kern.GrxError, match="bytes for a"):
+        kern.NewQ8(2, 64, np.zeros(2 * 2 * 34 - 1, np.uint8))
+
+
+def test_to_q8_matches_oracle(kern, orc):
+    """Weight.ToQ8 (kern.go:136-170) on the GPU: bytes identical to the
+    oracle's, zero blocks and exact halves included."""
+    rng = np.random.default_rng(7)
+    n, k = 9, 96
+    v = rng.standard_normal(n * k).astype(np.float32)
+    v[:32] = 0
+    v[32] = 127.0
+    v[33:38] = [2.5, -2.5, 0.5, 1.5, -0.5]
+    v[96:128] *= 1e-6
+    got = kern.ToQ8(v, n, k)
+    assert np.array_equal(got, orc.quant_q8(v))
+
+
+# ---------------------------------------------------------------- activations and dots
+
+def test_quant_act_exact(kern, orc, torch_dev):
+    """quantU8 (q8int.go:88-105) on the GPU: bytes and scales bit-exact;
+    TestQuantU8AsmMatchesGo's cases (zero block, extreme -40) included."""
+    torch = torch_dev
+    rng = np.random.default_rng(3)
+    m, k = 3, 9 * QK
+    x = (rng.standard_normal((m, k)) * (1 + np.arange(k) // QK)).astype(np.float32)
+    x[0, 2 * QK:3 * QK] = 0
+    x[0, 5 * QK] = -40
+    x[1, :QK] = 127.0
+    x[1, 1:5] = [2.5, 3.5, -2.5, -0.5]
+    x[2, QK:2 * QK] *= 1e-30  # subnormal-range products
+    dx = torch.from_numpy(x).cuda()
+    dq = torch.zeros((m, k), dtype=torch.int8, device="cuda")
+    ds = torch.zeros((m, k // QK), dtype=torch.float32, device="cuda")
+    torch.cuda.synchronize()
+    kern.quant_act_dev(dq, ds, dx, m, k)
+    kern.default_context().sync()
+    q, sc = orc.quant_act_i8(x)
+    assert np.array_equal(dq.cpu().numpy(), q)
+    assert _bits_equal(ds.cpu().numpy(), sc)
+
+
+def test_block_dots_exact(kern, orc, torch_dev):
+    """Per-block int32 dots bit-exact with the oracle (and so with the int64
+    brute force the oracle is pinned to)."""
+    torch = torch_dev
+    rng = np.random.default_rng(11)
+    m, n, k = 3, 130, 320
+    qa = rng.integers(-128, 128, size=(m, k)).astype(np.int8)
+    qa[0, :QK] = -128
+    w8 = q8_weight(rng, n, k)
+    w = kern.NewQ8(n, k, w8)
+    ds = torch.zeros((m, n, k // QK), dtype=torch.int32, device="cuda")
+    dqa = torch.from_numpy(qa).cuda()
+    torch.cuda.synchronize()
+    kern.block_dots_dev(ds, dqa, m, w)
+    kern.default_context().sync()
+    assert np.array_equal(ds.cpu().numpy(), orc.block_dots(qa, w8, n, k))
+
+
+# ---------------------------------------------------------------- products
+
+def _check_matmul(kern, orc, rng, m, n, k, bias=True, lda_pad=3, ldc_pad=2):
+    x = rng.standard_normal((m, k + lda_pad)).astype(np.float32)
+    w8 = q8_weight(rng, n, k)
+    b = rng.standard_normal(n).astype(np.float32) if bias else None
+    w = kern.NewQ8(n, k, w8)
+    got = np.full((m, n + ldc_pad), 7.0, np.float32)
+    kern.MatMul(got, n + ldc_pad, x, k + lda_pad, m, w, b)
+    want = orc.matmul_q8_int(np.ascontiguousarray(x[:, :k]), w8, n, k, b)
+    assert _bits_equal(got[:, :n], want), f"{m}x{n}x{k}: " + _report(got[:, :n], want)
+    assert (got[:, n:] == 7.0).all(), "wrote past ldc's row"
+
+
+@pytest.mark.parametrize("m", [1, 2, 3, 5, 6, 7, 8, 9, 16, 17])
+def test_matmul_odd_sizes_bit_exact(kern, orc, m):
+    """TestOddSizesBothPaths / TestInt8MatMul shapes (odd_test.go:33-35,
+    q8int_test.go:87): every output bit-identical to the oracle's EVEX order,
+    strided rows (lda = k+3, ldc = n+2), with and without bias."""
+    rng = np.random.default_rng(100 + m)
+    for n in (1, 3, 4, 5, 15, 16, 17, 33, 64, 65, 129):
+        for k in (32, 64, 96, 544):
+            _check_matmul(kern, orc, rng, m, n, k, bias=(n % 2 == 1))
+
+
+@pytest.mark.parametrize("waves", ["1", "2", "4", "8", "16"])
+def test_matmul_every_wave_split(kern, orc, waves):
+    """Splitting a tile's blocks over 1..16 waves (ordered chain in LDS)
+    changes no bit."""
+    rng = np.random.default_rng(31)
+    os.environ["GRX_GEMV_WAVES"] = waves
+    try:
+        for m, n, k in ((1, 200, 1024), (2, 64, 512), (4, 70, 2048), (8, 130, 1280), (1, 64, 5120)):
+            _check_matmul(kern, orc, rng, m, n, k)
+    finally:
+        del os.environ["GRX_GEMV_WAVES"]
+
+
+def test_gemv_single_1024(kern, orc):
+    """The single Q8_0 GEMV workload: N = K = 1024, int8 U[-127,127], f16
+    scales |N(0,0.02)|/127 (~30% subnormal), x ~ N(0,1): bit-exact."""
+    w8, x = gemv_inputs(seed=1)
+    w = kern.NewQ8(1024, 1024, w8)
+    got = np.zeros(1024, np.float32)
+    kern.Linear(got, x, 1, w)
+    want = orc.matmul_q8_int(x, w8, 1024, 1024)[0]
+    assert _bits_equal(got, want), _report(got, want)
+
+
+def test_gemv_golden_fixture(kern):
+    """The committed fixture (tests/golden/q8_gemv_64x1024.npz) reproduced."""
+    path = os.path.join(os.path.dirname(__file__), "golden", "q8_gemv_64x1024.npz")
+    f = np.load(path)
+    n, k = int(f["n"]), int(f["k"])
+    w = kern.NewQ8(n, k, f["w"])
+    got = np.zeros((f["x"].shape[0], n), np.float32)
+    kern.MatMul(got, n, f["x"], k, f["x"].shape[0], w, f["bias"])
+    assert _bits_equal(got, f["y"])
+
+
+def test_gemv_logits_shape(kern, orc):
+    """A vocabulary-sized product (51864 x 512, whisper base.en logits)."""
+    rng = np.random.default_rng(5)
+    n, k = 51864, 512
+    w8 = q8_weight(rng, n, k, sigma=0.5)
+    x = rng.standard_normal(k).astype(np.float32)
+    w = kern.NewQ8(n, k, w8)
+    got = np.zeros(n, np.float32)
+    kern.Linear(got, x, 1, w)
+    want = orc.matmul_q8_int(x, w8, n, k)[0]
+    assert _bits_equal(got, want), _report(got, want)
+
+
+def test_matmul_zero_rows_is_noop(kern):
+    rng = np.random.default_rng(1)
+    w = kern.NewQ8(4, 32, q8_weight(rng, 4, 32))
+    dst = np.full(4, 3.0, np.float32)
+    kern.MatMul(dst, 4, np.zeros(32, np.float32), 32, 0, w)
+    assert (dst == 3.0).all()
+
+
+def test_matmul_short_buffer_raises(kern):
+    """The reference panics on a short slice (kernels_amd64.go:206-211);
+    the mirror raises IndexError before any launch."""
+    rng = np.random.default_rng(1)
+    w = kern.NewQ8(4, 64, q8_weight(rng, 4, 64))
+    with pytest.raises(IndexError):
+        kern.MatMul(np.zeros(4, np.float32), 4, np.zeros(63, np.float32), 64, 1, w)
+
+
+def test_device_pointer_forms(kern, orc, torch_dev):
+    """grx_matmul_q8_dev and the pre-rounded form on torch device tensors."""
+    torch = torch_dev
+    rng = np.random.default_rng(17)
+    m, n, k = 4, 300, 768
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    w8 = q8_weight(rng, n, k)
+    b = rng.standard_normal(n).astype(np.float32)
+    w = kern.NewQ8(n, k, w8)
+    want = orc.matmul_q8_int(x, w8, n, k, b)
+    dx, db = torch.from_numpy(x).cuda(), torch.from_numpy(b).cuda()
+    dy = torch.zeros((m, n), device="cuda")
+    torch.cuda.synchronize()
+    kern.matmul_dev(dy, dx, m, w, db)
+    kern.default_context().sync()
+    assert _bits_equal(dy.cpu().numpy(), want)
+    dq = torch.zeros((m, k), dtype=torch.int8, device="cuda")
+    ds = torch.zeros((m, k // QK), device="cuda")
+    kern.quant_act_dev(dq, ds, dx, m, k)
+    dy2 = torch.zeros((m, n), device="cuda")
+    kern.default_context().sync()
+    torch.cuda.synchronize()
+    kern.matmul_prequant_dev(dy2, dq, ds, m, w, db)
+    kern.default_context().sync()
+    assert _bits_equal(dy2.cpu().numpy(), want)
