@@ -84,18 +84,17 @@ def main():
                           "detail": "the path shards data-parallel by stream/utterance with no exchange; see DESIGN.md"}))
         sys.exit(2)
 
-    import torch
-    from gorelaxor_amd import kern
+    from gorelaxor_amd import hiprt, kern
 
     ctx = kern.default_context(0)
-    stream = torch.cuda.ExternalStream(ctx.stream)
+    stream = ctx.stream
     w8, x = ring_weights()
     w = kern.NewQ8(N * RING, K, w8, ctx)
-    dx = torch.from_numpy(x).cuda()
-    dq = torch.zeros(K, dtype=torch.int8, device="cuda")
-    ds = torch.zeros(K // 32, dtype=torch.float32, device="cuda")
-    dy = torch.zeros(N * RING, dtype=torch.float32, device="cuda")
-    torch.cuda.synchronize()
+    dx = hiprt.DeviceBuffer.from_array(x)
+    dq = hiprt.DeviceBuffer(K)
+    ds = hiprt.DeviceBuffer(K // 32 * 4)
+    dy = hiprt.DeviceBuffer(N * RING * 4)
+    hiprt.synchronize()
 
     def step(evs=None, i=0):
         kern.quant_act_dev(dq, ds, dx, 1, K, ctx=ctx)
@@ -108,20 +107,18 @@ def main():
     for _ in range(args.warmup):
         step()
     ctx.sync()
-    torch.cuda.synchronize()
 
-    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(args.steps)] for _ in range(2)]
-    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    ev = [[hiprt.Event() for _ in range(args.steps)] for _ in range(2)]
+    start, end = hiprt.Event(), hiprt.Event()
     start.record(stream)
     t0 = time.perf_counter()
     for i in range(args.steps):
         step(ev, i)
     end.record(stream)
     ctx.sync()
-    torch.cuda.synchronize()
     wall = time.perf_counter() - t0
-    total_ms = start.elapsed_time(end)
-    gemv_ms = [ev[0][i].elapsed_time(ev[1][i]) for i in range(args.steps)]
+    total_ms = start.elapsed_ms(end)
+    gemv_ms = [ev[0][i].elapsed_ms(ev[1][i]) for i in range(args.steps)]
     ms_step = total_ms / args.steps
     gemv_avg = float(np.mean(gemv_ms))
     launch_bytes = BYTES_PER_GEMV * RING
@@ -132,7 +129,7 @@ def main():
     import oracle
     oracle.build()
     want = oracle.matmul_q8_int(x, w8[:N * K // 32 * 34], N, K)[0]
-    got = dy[:N].cpu().numpy()
+    got = dy.download(np.float32, (N,))
     parity = bool(np.array_equal(got.view(np.uint32), want.view(np.uint32)))
 
     out = {

@@ -30,11 +30,11 @@ def _report(got, want):
 
 
 @pytest.fixture
-def torch_dev():
-    import torch
+def dev(kern):
+    """Device buffers on the library's own HIP runtime (gorelaxor_amd.hiprt)."""
+    from gorelaxor_amd import hiprt
 
-    assert torch.cuda.is_available()
-    return torch
+    return hiprt
 
 
 # ---------------------------------------------------------------- weights
@@ -81,10 +81,9 @@ def test_to_q8_matches_oracle(kern, orc):
 
 # ---------------------------------------------------------------- activations and dots
 
-def test_quant_act_exact(kern, orc, torch_dev):
+def test_quant_act_exact(kern, orc, dev):
     """quantU8 (q8int.go:88-105) on the GPU: bytes and scales bit-exact;
     TestQuantU8AsmMatchesGo's cases (zero block, extreme -40) included."""
-    torch = torch_dev
     rng = np.random.default_rng(3)
     m, k = 3, 9 * QK
     x = (rng.standard_normal((m, k)) * (1 + np.arange(k) // QK)).astype(np.float32)
@@ -93,33 +92,30 @@ def test_quant_act_exact(kern, orc, torch_dev):
     x[1, :QK] = 127.0
     x[1, 1:5] = [2.5, 3.5, -2.5, -0.5]
     x[2, QK:2 * QK] *= 1e-30  # subnormal-range products
-    dx = torch.from_numpy(x).cuda()
-    dq = torch.zeros((m, k), dtype=torch.int8, device="cuda")
-    ds = torch.zeros((m, k // QK), dtype=torch.float32, device="cuda")
-    torch.cuda.synchronize()
+    dx = dev.DeviceBuffer.from_array(x)
+    dq = dev.DeviceBuffer(m * k)
+    ds = dev.DeviceBuffer(m * (k // QK) * 4)
     kern.quant_act_dev(dq, ds, dx, m, k)
     kern.default_context().sync()
     q, sc = orc.quant_act_i8(x)
-    assert np.array_equal(dq.cpu().numpy(), q)
-    assert _bits_equal(ds.cpu().numpy(), sc)
+    assert np.array_equal(dq.download(np.int8, (m, k)), q)
+    assert _bits_equal(ds.download(np.float32, (m, k // QK)), sc)
 
 
-def test_block_dots_exact(kern, orc, torch_dev):
+def test_block_dots_exact(kern, orc, dev):
     """Per-block int32 dots bit-exact with the oracle (and so with the int64
     brute force the oracle is pinned to)."""
-    torch = torch_dev
     rng = np.random.default_rng(11)
     m, n, k = 3, 130, 320
     qa = rng.integers(-128, 128, size=(m, k)).astype(np.int8)
     qa[0, :QK] = -128
     w8 = q8_weight(rng, n, k)
     w = kern.NewQ8(n, k, w8)
-    ds = torch.zeros((m, n, k // QK), dtype=torch.int32, device="cuda")
-    dqa = torch.from_numpy(qa).cuda()
-    torch.cuda.synchronize()
+    ds = dev.DeviceBuffer(m * n * (k // QK) * 4)
+    dqa = dev.DeviceBuffer.from_array(qa)
     kern.block_dots_dev(ds, dqa, m, w)
     kern.default_context().sync()
-    assert np.array_equal(ds.cpu().numpy(), orc.block_dots(qa, w8, n, k))
+    assert np.array_equal(ds.download(np.int32, (m, n, k // QK)), orc.block_dots(qa, w8, n, k))
 
 
 # ---------------------------------------------------------------- products
@@ -212,9 +208,8 @@ def test_matmul_short_buffer_raises(kern):
         kern.MatMul(np.zeros(4, np.float32), 4, np.zeros(63, np.float32), 64, 1, w)
 
 
-def test_device_pointer_forms(kern, orc, torch_dev):
-    """grx_matmul_q8_dev and the pre-rounded form on torch device tensors."""
-    torch = torch_dev
+def test_device_pointer_forms(kern, orc, dev):
+    """grx_matmul_q8_dev and the pre-rounded form on device buffers."""
     rng = np.random.default_rng(17)
     m, n, k = 4, 300, 768
     x = rng.standard_normal((m, k)).astype(np.float32)
@@ -222,18 +217,15 @@ def test_device_pointer_forms(kern, orc, torch_dev):
     b = rng.standard_normal(n).astype(np.float32)
     w = kern.NewQ8(n, k, w8)
     want = orc.matmul_q8_int(x, w8, n, k, b)
-    dx, db = torch.from_numpy(x).cuda(), torch.from_numpy(b).cuda()
-    dy = torch.zeros((m, n), device="cuda")
-    torch.cuda.synchronize()
+    dx, db = dev.DeviceBuffer.from_array(x), dev.DeviceBuffer.from_array(b)
+    dy = dev.DeviceBuffer(m * n * 4)
     kern.matmul_dev(dy, dx, m, w, db)
     kern.default_context().sync()
-    assert _bits_equal(dy.cpu().numpy(), want)
-    dq = torch.zeros((m, k), dtype=torch.int8, device="cuda")
-    ds = torch.zeros((m, k // QK), device="cuda")
+    assert _bits_equal(dy.download(np.float32, (m, n)), want)
+    dq = dev.DeviceBuffer(m * k)
+    ds = dev.DeviceBuffer(m * (k // QK) * 4)
     kern.quant_act_dev(dq, ds, dx, m, k)
-    dy2 = torch.zeros((m, n), device="cuda")
-    kern.default_context().sync()
-    torch.cuda.synchronize()
+    dy2 = dev.DeviceBuffer(m * n * 4)
     kern.matmul_prequant_dev(dy2, dq, ds, m, w, db)
     kern.default_context().sync()
-    assert _bits_equal(dy2.cpu().numpy(), want)
+    assert _bits_equal(dy2.download(np.float32, (m, n)), want)
