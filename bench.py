@@ -41,6 +41,8 @@ def parse():
     p.add_argument("--warmup", type=int, default=20)
     p.add_argument("--cpu-seconds", type=float, default=10.0, help="bound on the CPU baseline's work")
     p.add_argument("--no-cpu", action="store_true")
+    p.add_argument("--copy-calibration", action="store_true",
+                   help="only copy the ring's bytes device to device 3 times (reference reading for HBM counters)")
     return p.parse_args()
 
 
@@ -85,6 +87,16 @@ def main():
         sys.exit(2)
 
     from gorelaxor_amd import hiprt, kern
+
+    if args.copy_calibration:
+        nbytes = N * RING * K // 32 * 34
+        a, b = hiprt.DeviceBuffer(nbytes), hiprt.DeviceBuffer(nbytes)
+        a.zero()
+        for _ in range(3):
+            b.copy_from(a)
+        hiprt.synchronize()
+        print(json.dumps({"copy_calibration_bytes": nbytes, "copies": 3}), flush=True)
+        return
 
     ctx = kern.default_context(0)
     stream = ctx.stream

@@ -10,7 +10,8 @@ import os
 import re
 
 PKG = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(PKG, "libgrx.so")
+# GRX_LIB names another build of the library (an experiment); default in-tree
+LIB_PATH = os.environ.get("GRX_LIB") or os.path.join(PKG, "libgrx.so")
 HEADER = os.path.join(os.path.dirname(PKG), "include", "grx.h")
 
 GRX_OK = 0
@@ -55,7 +56,20 @@ SIGNATURES = {
     "grx_quant_act_dev": (i32, [vp, vp, vp, vp, i32, i32, i32]),
     "grx_matmul_q8_prequant_dev": (i32, [vp, vp, i32, vp, vp, i32, vp, vp]),
     "grx_block_dots_dev": (i32, [vp, vp, vp, i32, vp]),
+    "grx_whisper_create": (i32, [vp, vp, C.POINTER(vp)]),
+    "grx_whisper_destroy": (i32, [vp]),
+    "grx_whisper_set_tensor": (i32, [vp, C.c_char_p, vp, sz]),
+    "grx_whisper_set_encoder_output": (i32, [vp, vp, i32]),
+    "grx_whisper_reset": (i32, [vp]),
+    "grx_whisper_pos": (i32, [vp]),
+    "grx_whisper_decode": (i32, [vp, vp, i32, vp, vp]),
+    "grx_whisper_greedy": (i32, [vp, vp, i32, i32, vp]),
 }
+
+
+class WhisperHParams(C.Structure):
+    """grx_whisper_hparams (whisper/model.go:16-21)."""
+    _fields_ = [(n, C.c_int) for n in ("n_vocab", "n_text_ctx", "n_state", "n_head", "n_layer", "n_audio_ctx")]
 
 
 def header_symbols() -> list[str]:

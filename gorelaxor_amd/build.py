@@ -38,24 +38,27 @@ def sources():
     return sorted(glob.glob(os.path.join(CSRC, "*.hip")))
 
 
-def _compile_one(src: str) -> tuple[str, subprocess.Popen]:
-    obj = os.path.join(BUILD_DIR, os.path.basename(src) + ".o")
-    cmd = [HIPCC, *FLAGS, "-c", src, "-o", obj]
+def _compile_one(src: str, build_dir: str, extra: list[str]) -> tuple[str, subprocess.Popen]:
+    obj = os.path.join(build_dir, os.path.basename(src) + ".o")
+    cmd = [HIPCC, *FLAGS, *extra, "-c", src, "-o", obj]
     p = subprocess.Popen(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
     return obj, p
 
 
-def build(verbose: bool = True) -> str:
-    """Compile every csrc/*.hip for gfx950 and link gorelaxor_amd/libgrx.so."""
+def build(verbose: bool = True, out: str = LIB, defines: list[str] | None = None) -> str:
+    """Compile every csrc/*.hip for gfx950 and link gorelaxor_amd/libgrx.so
+    (or `out`, with extra -D `defines`, for a variant build)."""
     if not os.path.exists(HIPCC):
         raise RuntimeError(f"hipcc not found at {HIPCC}")
-    os.makedirs(BUILD_DIR, exist_ok=True)
+    build_dir = BUILD_DIR if out == LIB else os.path.join(os.path.dirname(os.path.abspath(out)), "_build")
+    os.makedirs(build_dir, exist_ok=True)
+    extra = [f"-D{d}" for d in (defines or [])]
     t0 = time.time()
-    jobs = [_compile_one(s) for s in sources()]
+    jobs = [_compile_one(s, build_dir, extra) for s in sources()]
     objs, failed = [], []
     for obj, p in jobs:
-        out, _ = p.communicate()
-        lines = [l for l in out.splitlines() if "packed-fp32-ops" not in l]
+        text, _ = p.communicate()
+        lines = [l for l in text.splitlines() if "packed-fp32-ops" not in l]
         if p.returncode != 0:
             failed.append((obj, "\n".join(lines)))
         elif verbose and lines:
@@ -63,15 +66,15 @@ def build(verbose: bool = True) -> str:
         objs.append(obj)
     if failed:
         raise RuntimeError("hipcc failed:\n" + "\n\n".join(f"{o}:\n{t}" for o, t in failed))
-    tmp = LIB + ".tmp"
+    tmp = out + ".tmp"
     cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError("link failed:\n" + r.stdout + r.stderr)
-    shutil.move(tmp, LIB)
+    shutil.move(tmp, out)
     if verbose:
-        print(f"built {LIB} in {time.time() - t0:.1f}s", file=sys.stderr)
-    return LIB
+        print(f"built {out} in {time.time() - t0:.1f}s", file=sys.stderr)
+    return out
 
 
 if __name__ == "__main__":

@@ -24,7 +24,33 @@
 
 namespace {
 
-constexpr int BU = 4;  // blocks whose loads are issued before any is used
+#ifndef GRX_GEMV_BU
+#define GRX_GEMV_BU 8
+#endif
+#ifndef GRX_GEMV_NT
+#define GRX_GEMV_NT 1
+#endif
+constexpr int BU = GRX_GEMV_BU;  // blocks whose loads are issued before any is used
+
+// Weight loads are non-temporal: each weight byte is read once per product,
+// and streaming it past the caches measured 6.7-6.8 TB/s on a 570 MB ring
+// against 5.7-5.9 TB/s for ordinary loads (MI355X).
+typedef int grx_v4i __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ int4 wload(const int4 *p) {
+#if GRX_GEMV_NT
+    const grx_v4i v = __builtin_nontemporal_load(reinterpret_cast<const grx_v4i *>(p));
+    return make_int4(v.x, v.y, v.z, v.w);
+#else
+    return *p;
+#endif
+}
+__device__ __forceinline__ uint16_t wload(const uint16_t *p) {
+#if GRX_GEMV_NT
+    return __builtin_nontemporal_load(p);
+#else
+    return *p;
+#endif
+}
 
 // ---------------------------------------------------------------- helpers
 
@@ -176,9 +202,9 @@ __global__ __launch_bounds__(64 * W) void gemv_q8_kernel(const GemvArgs a) {
         uint32_t dh[U];
 #pragma unroll
         for (int u = 0; u < U; ++u) {
-            w[2 * u] = wq[(size_t)(bb + u) * 128 + lane];
-            w[2 * u + 1] = wq[(size_t)(bb + u) * 128 + 64 + lane];
-            dh[u] = wd[(size_t)(bb + u) * 64 + lane];
+            w[2 * u] = wload(wq + (size_t)(bb + u) * 128 + lane);
+            w[2 * u + 1] = wload(wq + (size_t)(bb + u) * 128 + 64 + lane);
+            dh[u] = wload(wd + (size_t)(bb + u) * 64 + lane);
         }
 #pragma unroll
         for (int u = 0; u < U; ++u) {

@@ -1,0 +1,697 @@
+// whisper_step.hip - a whisper-shaped text decoder step on one GPU.
+//
+// The graph is Model.decode of whisper/decoder.go:33-140 (github.com/
+// xattribution/gorelaxor) with every matrix a Q8_0 weight on the int8 route
+// of q8_gemv.hip; the vector kernels below restate the reference's float
+// arithmetic in its own order, so a step's logits are bit-identical to the
+// CPU oracle's and the greedy tokens are the same.
+//
+// One step is: embed, then per layer
+//   [LN -> q|k|v GEMV, k and v written into the cache at pos]  (one launch)
+//   [self-attention over pos+1 cached keys, one workgroup per head]
+//   [att -> Q8_0 -> out GEMV + residual]
+//   [LN -> cross query GEMV] [cross scores] [softmax] [cross values]
+//   [att -> Q8_0 -> cross out GEMV + residual]
+//   [LN -> fc1 GEMV -> GELU] [ff -> Q8_0 -> fc2 GEMV + residual]
+// and [LN -> logits GEMV -> argmax] [finish: token, pos+1].  Token and
+// position live in device memory, so the step is captured once into a HIP
+// graph and replayed; greedy decoding never returns to the host.
+#include <math.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include <map>
+#include <string>
+#include <vector>
+
+#include "grx_internal.h"
+
+namespace {
+
+constexpr int kAttnThreads = 256;
+
+// ---------------------------------------------------------------- kernels
+
+// x = widen(tokEmb.row(tok)) + decPos[pos] (decoder.go:42-46); clears the
+// argmax key of the step.
+__global__ void embed_kernel(const int8_t *__restrict__ qs, const uint16_t *__restrict__ ds, int nb,
+                             const float *__restrict__ dec_pos, const int *__restrict__ tok,
+                             const int *__restrict__ pos, int st, float *__restrict__ x,
+                             unsigned long long *__restrict__ amax) {
+    const int t = *tok, p = *pos;
+    const int tile = t >> 6, lane = t & 63;
+    for (int i = threadIdx.x; i < st; i += blockDim.x) {
+        const int b = i >> 5, h = (i >> 4) & 1, e = i & 15;
+        const int8_t q = qs[(((size_t)tile * nb + b) * 2 + h) * 1024 + lane * 16 + e];
+        const float d = grx_f16_to_f32(ds[((size_t)tile * nb + b) * 64 + lane]);
+        x[i] = __fadd_rn(__fmul_rn((float)q, d), dec_pos[(size_t)p * st + i]);
+    }
+    if (threadIdx.x == 0) *amax = 0ull;
+}
+
+// dotF32Go (internal/kern/gemm.go:294-308): four running sums, unfused.
+__device__ __forceinline__ float dot_go(const float *x, const float *y, int n) {
+    float s0 = 0.f, s1 = 0.f, s2 = 0.f, s3 = 0.f;
+    int i = 0;
+    for (; i + 4 <= n; i += 4) {
+        s0 = __fadd_rn(s0, __fmul_rn(x[i], y[i]));
+        s1 = __fadd_rn(s1, __fmul_rn(x[i + 1], y[i + 1]));
+        s2 = __fadd_rn(s2, __fmul_rn(x[i + 2], y[i + 2]));
+        s3 = __fadd_rn(s3, __fmul_rn(x[i + 3], y[i + 3]));
+    }
+    for (; i < n; i++) s0 = __fadd_rn(s0, __fmul_rn(x[i], y[i]));
+    return __fadd_rn(__fadd_rn(__fadd_rn(s0, s1), s2), s3);
+}
+
+// HSUM of kernels_amd64.s:90-95 over eight lane values.
+__device__ __forceinline__ float hsum8(const float *a) {
+    const float h0 = __fadd_rn(a[0], a[4]), h1 = __fadd_rn(a[1], a[5]);
+    const float h2 = __fadd_rn(a[2], a[6]), h3 = __fadd_rn(a[3], a[7]);
+    return __fadd_rn(__fadd_rn(h0, h1), __fadd_rn(h2, h3));
+}
+
+// One row of dot4f32avx (kernels_amd64.s:156-204), kk % 16 == 0.
+__device__ __forceinline__ float dot_avx(const float *x, const float *w, int kk) {
+    float A[8], B[8];
+#pragma unroll
+    for (int l = 0; l < 8; ++l) A[l] = B[l] = 0.f;
+    for (int c = 0; c < kk; c += 16) {
+#pragma unroll
+        for (int l = 0; l < 8; ++l) {
+            A[l] = __fmaf_rn(x[c + l], w[c + l], A[l]);
+            B[l] = __fmaf_rn(x[c + 8 + l], w[c + 8 + l], B[l]);
+        }
+    }
+    float S[8];
+#pragma unroll
+    for (int l = 0; l < 8; ++l) S[l] = __fadd_rn(A[l], B[l]);
+    return hsum8(S);
+}
+
+// dotF32x4 (kernels_amd64.go:75-95) for one row: assembly over k &^ 15,
+// dotF32Go over the rest added on.
+__device__ __forceinline__ float dot_x4(const float *x, const float *w, int k) {
+    const int kk = k & ~15;
+    float o = kk > 0 ? dot_avx(x, w, kk) : 0.f;
+    if (kk < k) o = __fadd_rn(o, dot_go(x + kk, w + kk, k - kk));
+    return o;
+}
+
+// softmax (internal/kern/mathx.go:78-90) of s[0..n) in LDS by one block:
+// max, e = EXP8(v-max) below n &^ 7 and expf past it, the eight lane sums
+// of expSubAVX + HSUM, plus the tail's own sum, then v *= 1/sum.
+__device__ void block_softmax(float *s, int n, float *part) {
+    const int tid = threadIdx.x, nt = blockDim.x;
+    float mx = -__builtin_inff();
+    for (int j = tid; j < n; j += nt) mx = s[j] > mx ? s[j] : mx;
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        const float v = __shfl_xor(mx, o);
+        mx = v > mx ? v : mx;
+    }
+    if ((tid & 63) == 0) part[16 + (tid >> 6)] = mx;
+    __syncthreads();
+    mx = -__builtin_inff();
+    for (int w = 0; w < (nt + 63) / 64; ++w) mx = part[16 + w] > mx ? part[16 + w] : mx;
+    const int n8 = n & ~7;
+    for (int j = tid; j < n; j += nt) {
+        const float d = __fsub_rn(s[j], mx);
+        s[j] = j < n8 ? grx_exp8(d) : grx_expf_go(d);
+    }
+    __syncthreads();
+    if (tid < 8) {
+        float acc = 0.f;
+        for (int j = tid; j < n8; j += 8) acc = __fadd_rn(acc, s[j]);
+        part[tid] = acc;
+    } else if (tid == 8) {
+        float t = 0.f;
+        for (int j = n8; j < n; ++j) t = __fadd_rn(t, s[j]);
+        part[8] = t;
+    }
+    __syncthreads();
+    const float sa = n8 > 0 ? hsum8(part) : 0.f;
+    const float inv = __fdiv_rn(1.0f, __fadd_rn(sa, part[8]));
+    for (int j = tid; j < n; j += nt) s[j] = __fmul_rn(s[j], inv);
+    __syncthreads();
+}
+
+// Causal self-attention of one head over the pos+1 cached positions
+// (decoder.go:70-87): scores dotF32Go(q, k_j)*sc, softmax, and
+// out[d] += p_j * v_j[d] in position order, unfused.
+__global__ __launch_bounds__(kAttnThreads) void self_attn_kernel(
+    const float *__restrict__ q, const float *__restrict__ kc, const float *__restrict__ vc,
+    const int *__restrict__ pos, int st, int hd, float sc, float *__restrict__ att) {
+    extern __shared__ float sm[];
+    float *part = sm;        // 32 floats
+    float *s = sm + 32;      // n_text_ctx floats
+    const int h = blockIdx.x, n = *pos + 1, tid = threadIdx.x;
+    const float *qh = q + h * hd;
+    for (int j = tid; j < n; j += blockDim.x) s[j] = __fmul_rn(dot_go(qh, kc + (size_t)j * st + h * hd, hd), sc);
+    __syncthreads();
+    block_softmax(s, n, part);
+    for (int d = tid; d < hd; d += blockDim.x) {
+        float o = 0.f;
+        const float *vd = vc + h * hd + d;
+        for (int j = 0; j < n; ++j) o = __fadd_rn(o, __fmul_rn(s[j], vd[(size_t)j * st]));
+        att[h * hd + d] = o;
+    }
+}
+
+// Cross-attention scores of one head for a run of keys (decoder.go:94-108):
+// dotF32x4 for the keys in whole groups of four, dotF32Go for the rest.
+__global__ __launch_bounds__(kAttnThreads) void cross_scores_kernel(
+    const float *__restrict__ q, const float *__restrict__ ck, int nctx, int hd, float *__restrict__ scores) {
+    const int h = blockIdx.x, j = blockIdx.y * blockDim.x + threadIdx.x;
+    if (j >= nctx) return;
+    const float *qh = q + h * hd;
+    const float *kj = ck + ((size_t)h * nctx + j) * hd;
+    scores[(size_t)h * nctx + j] = j < (nctx & ~3) ? dot_x4(qh, kj, hd) : dot_go(qh, kj, hd);
+}
+
+// softmax of each head's row of scores (decoder.go:109).
+__global__ __launch_bounds__(kAttnThreads) void softmax_rows_kernel(float *__restrict__ scores, int n) {
+    extern __shared__ float sm[];
+    float *part = sm, *s = sm + 32;
+    float *row = scores + (size_t)blockIdx.x * n;
+    for (int j = threadIdx.x; j < n; j += blockDim.x) s[j] = row[j];
+    __syncthreads();
+    block_softmax(s, n, part);
+    for (int j = threadIdx.x; j < n; j += blockDim.x) row[j] = s[j];
+}
+
+// Weighted values of one head (decoder.go:110-118): out[d] = dotF32x4(p,
+// Vt[d]) for d in groups of four (dotF32Go for a last partial group).
+// A wave serves four values of d: 16 lanes per d, lane l (l < 8) runs the
+// lane-l chain of the first accumulator and lane 8+l that of the second,
+// so the 16 chains of the assembly run side by side; the tail past
+// n &^ 15 is one lane's dotF32Go.
+__global__ __launch_bounds__(64) void cross_values_kernel(const float *__restrict__ p, const float *__restrict__ cv,
+                                                         int nctx, int hd, float *__restrict__ att) {
+    const int h = blockIdx.x, lane = threadIdx.x;
+    const int d = blockIdx.y * 4 + (lane >> 4);
+    const int c = lane & 15;
+    if (d >= hd) return;
+    const float *ph = p + (size_t)h * nctx;
+    const float *vd = cv + ((size_t)h * hd + d) * nctx;
+    if (d >= (hd & ~3)) {  // a last partial group of d: dotF32Go
+        if (c == 0) att[h * hd + d] = dot_go(ph, vd, nctx);
+        return;
+    }
+    const int kk = nctx & ~15;
+    float acc = 0.f;
+    for (int i = c; i < kk; i += 16) acc = __fmaf_rn(ph[i], vd[i], acc);
+    // S_l = A_l + B_l, then HSUM
+    const float other = __shfl_xor(acc, 8, 16);
+    const float S = __fadd_rn(c < 8 ? acc : other, c < 8 ? other : acc);
+    const float h4 = __fadd_rn(S, __shfl_xor(S, 4, 16));  // lanes l: S_l + S_{l^4}
+    const float h01 = __fadd_rn(h4, __shfl_xor(h4, 1, 16));
+    const float h23 = __shfl_xor(h01, 2, 16);
+    if (c == 0) {
+        float o = kk > 0 ? __fadd_rn(h01, h23) : 0.f;
+        if (kk < nctx) o = __fadd_rn(o, dot_go(ph + kk, vd + kk, nctx - kk));
+        att[h * hd + d] = o;
+    }
+}
+
+// End of a step: the argmax token, its record, the next position.
+__global__ void finish_kernel(const unsigned long long *__restrict__ amax, int *__restrict__ tok,
+                              int *__restrict__ pos, int *__restrict__ hist) {
+    const unsigned long long key = *amax;
+    const int t = (int)(0xffffffffu - (uint32_t)(key & 0xffffffffull));
+    const int p = *pos;
+    *tok = t;
+    hist[p] = t;
+    *pos = p + 1;
+}
+
+// cross K (scaled) [h][t][d] and V [h][d][t] from K, V [t][h*hd+d]
+// (whisper/encoder.go:131-142).
+__global__ void cross_layout_kernel(const float *__restrict__ k, const float *__restrict__ v, int nctx, int st,
+                                    int hd, float tsc, float *__restrict__ ck, float *__restrict__ cv) {
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= (size_t)nctx * st) return;
+    const int t = (int)(i / st), c = (int)(i % st);
+    const int h = c / hd, d = c % hd;
+    ck[((size_t)h * nctx + t) * hd + d] = __fmul_rn(k[i], tsc);
+    cv[((size_t)h * hd + d) * nctx + t] = v[i];
+}
+
+}  // namespace
+
+// ---------------------------------------------------------------- host side
+
+struct WLayer {
+    grx_weight *qkv = nullptr, *o = nullptr, *xq = nullptr, *xk = nullptr, *xv = nullptr, *xo = nullptr;
+    grx_weight *fc1 = nullptr, *fc2 = nullptr;
+    float *attn_ln_w, *attn_ln_b, *x_ln_w, *x_ln_b, *mlp_ln_w, *mlp_ln_b;
+    float *qkv_b, *o_b, *xq_b, *xv_b, *xo_b, *fc1_b, *fc2_b;
+    float *cross_k, *cross_v, *self_k, *self_v;
+};
+
+struct grx_whisper {
+    grx_ctx *ctx = nullptr;
+    grx_whisper_hparams hp{};
+    std::map<std::string, std::vector<uint8_t>> host;  // set_tensor copies, until finalize
+    bool ready = false, have_cross = false;
+    std::vector<WLayer> L;
+    grx_weight *tok_emb = nullptr;
+    std::vector<void *> allocs;  // every device buffer below
+    float *dec_pos = nullptr, *dec_ln_w = nullptr, *dec_ln_b = nullptr;
+    float *x = nullptr, *q = nullptr, *att = nullptr, *ff = nullptr, *logits = nullptr, *scores = nullptr;
+    unsigned long long *amax = nullptr;
+    int *tok = nullptr, *pos = nullptr, *hist = nullptr;
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t exec = nullptr;
+    int pos_host = 0;
+};
+
+namespace {
+
+struct Expect {
+    std::string name;
+    size_t bytes;
+};
+
+// Every decoder tensor Model.bind reads (whisper/model.go:376-401), with its size.
+std::vector<Expect> expected(const grx_whisper_hparams &hp) {
+    const size_t st = hp.n_state;
+    auto q8 = [](size_t rows, size_t cols) { return rows * (cols / 32) * 34; };
+    std::vector<Expect> e;
+    e.push_back({"decoder.positional_embedding", (size_t)hp.n_text_ctx * st * 4});
+    e.push_back({"decoder.token_embedding.weight", q8(hp.n_vocab, st)});
+    e.push_back({"decoder.ln.weight", st * 4});
+    e.push_back({"decoder.ln.bias", st * 4});
+    for (int i = 0; i < hp.n_layer; ++i) {
+        const std::string p = "decoder.blocks." + std::to_string(i) + ".";
+        for (const char *ln : {"attn_ln", "cross_attn_ln", "mlp_ln"}) {
+            e.push_back({p + ln + ".weight", st * 4});
+            e.push_back({p + ln + ".bias", st * 4});
+        }
+        for (const char *a : {"attn", "cross_attn"}) {
+            for (const char *w : {"query", "key", "value", "out"}) e.push_back({p + a + "." + w + ".weight", q8(st, st)});
+            for (const char *b : {"query", "value", "out"}) e.push_back({p + a + "." + b + ".bias", st * 4});
+        }
+        e.push_back({p + "mlp.0.weight", q8(4 * st, st)});
+        e.push_back({p + "mlp.0.bias", 4 * st * 4});
+        e.push_back({p + "mlp.2.weight", q8(st, 4 * st)});
+        e.push_back({p + "mlp.2.bias", st * 4});
+    }
+    return e;
+}
+
+grx_status dev_alloc(grx_whisper *m, size_t bytes, void **out) {
+    void *p = nullptr;
+    GRX_HIP(hipMalloc(&p, bytes > 0 ? bytes : 16));
+    m->allocs.push_back(p);
+    *out = p;
+    return GRX_OK;
+}
+
+template <typename T>
+grx_status dev_alloc_t(grx_whisper *m, size_t count, T **out) {
+    return dev_alloc(m, count * sizeof(T), reinterpret_cast<void **>(out));
+}
+
+grx_status upload_vec(grx_whisper *m, const std::string &name, float **out) {
+    const auto &h = m->host.at(name);
+    grx_status s = dev_alloc(m, h.size(), reinterpret_cast<void **>(out));
+    if (s != GRX_OK) return s;
+    GRX_HIP(hipMemcpy(*out, h.data(), h.size(), hipMemcpyHostToDevice));
+    return GRX_OK;
+}
+
+grx_status finalize(grx_whisper *m) {
+    if (m->ready) return GRX_OK;
+    const grx_whisper_hparams &hp = m->hp;
+    for (const Expect &e : expected(hp))
+        if (!m->host.count(e.name)) return grx_fail(GRX_ESTATE, "the model file has no tensor %s", e.name.c_str());
+    grx_status s;
+    const int st = hp.n_state, hd = st / hp.n_head;
+    GRX_HIP(hipSetDevice(m->ctx->device));
+    {
+        const auto &t = m->host.at("decoder.token_embedding.weight");
+        if ((s = grx_weight_q8_create(m->ctx, hp.n_vocab, st, t.data(), t.size(), &m->tok_emb)) != GRX_OK) return s;
+    }
+    if ((s = upload_vec(m, "decoder.positional_embedding", &m->dec_pos)) != GRX_OK) return s;
+    if ((s = upload_vec(m, "decoder.ln.weight", &m->dec_ln_w)) != GRX_OK) return s;
+    if ((s = upload_vec(m, "decoder.ln.bias", &m->dec_ln_b)) != GRX_OK) return s;
+    m->L.resize(hp.n_layer);
+    for (int i = 0; i < hp.n_layer; ++i) {
+        WLayer &L = m->L[i];
+        const std::string p = "decoder.blocks." + std::to_string(i) + ".";
+        auto mat = [&](const std::string &n, int rows, int cols, grx_weight **w) {
+            const auto &t = m->host.at(p + n);
+            return grx_weight_q8_create(m->ctx, rows, cols, t.data(), t.size(), w);
+        };
+        // q, k and v share their input: one weight of 3*st rows, one launch.
+        {
+            std::vector<uint8_t> cat;
+            for (const char *w : {"attn.query.weight", "attn.key.weight", "attn.value.weight"}) {
+                const auto &t = m->host.at(p + w);
+                cat.insert(cat.end(), t.begin(), t.end());
+            }
+            if ((s = grx_weight_q8_create(m->ctx, 3 * st, st, cat.data(), cat.size(), &L.qkv)) != GRX_OK) return s;
+            std::vector<float> b(3 * st, 0.0f);  // the key has no bias (decoder.go:65)
+            memcpy(b.data(), m->host.at(p + "attn.query.bias").data(), st * 4);
+            memcpy(b.data() + 2 * st, m->host.at(p + "attn.value.bias").data(), st * 4);
+            if ((s = dev_alloc_t(m, 3 * st, &L.qkv_b)) != GRX_OK) return s;
+            GRX_HIP(hipMemcpy(L.qkv_b, b.data(), b.size() * 4, hipMemcpyHostToDevice));
+        }
+        if ((s = mat("attn.out.weight", st, st, &L.o)) != GRX_OK) return s;
+        if ((s = mat("cross_attn.query.weight", st, st, &L.xq)) != GRX_OK) return s;
+        if ((s = mat("cross_attn.key.weight", st, st, &L.xk)) != GRX_OK) return s;
+        if ((s = mat("cross_attn.value.weight", st, st, &L.xv)) != GRX_OK) return s;
+        if ((s = mat("cross_attn.out.weight", st, st, &L.xo)) != GRX_OK) return s;
+        if ((s = mat("mlp.0.weight", 4 * st, st, &L.fc1)) != GRX_OK) return s;
+        if ((s = mat("mlp.2.weight", st, 4 * st, &L.fc2)) != GRX_OK) return s;
+        struct {
+            const char *n;
+            float **d;
+        } vecs[] = {{"attn_ln.weight", &L.attn_ln_w},       {"attn_ln.bias", &L.attn_ln_b},
+                    {"cross_attn_ln.weight", &L.x_ln_w},    {"cross_attn_ln.bias", &L.x_ln_b},
+                    {"mlp_ln.weight", &L.mlp_ln_w},         {"mlp_ln.bias", &L.mlp_ln_b},
+                    {"attn.out.bias", &L.o_b},              {"cross_attn.query.bias", &L.xq_b},
+                    {"cross_attn.value.bias", &L.xv_b},     {"cross_attn.out.bias", &L.xo_b},
+                    {"mlp.0.bias", &L.fc1_b},               {"mlp.2.bias", &L.fc2_b}};
+        for (auto &v : vecs)
+            if ((s = upload_vec(m, p + v.n, v.d)) != GRX_OK) return s;
+        const size_t cross = (size_t)hp.n_audio_ctx * st, self = (size_t)hp.n_text_ctx * st;
+        if ((s = dev_alloc_t(m, cross, &L.cross_k)) != GRX_OK) return s;
+        if ((s = dev_alloc_t(m, cross, &L.cross_v)) != GRX_OK) return s;
+        if ((s = dev_alloc_t(m, self, &L.self_k)) != GRX_OK) return s;
+        if ((s = dev_alloc_t(m, self, &L.self_v)) != GRX_OK) return s;
+        GRX_HIP(hipMemset(L.self_k, 0, self * 4));
+        GRX_HIP(hipMemset(L.self_v, 0, self * 4));
+    }
+    if ((s = dev_alloc_t(m, st, &m->x)) != GRX_OK) return s;
+    if ((s = dev_alloc_t(m, st, &m->q)) != GRX_OK) return s;
+    if ((s = dev_alloc_t(m, st, &m->att)) != GRX_OK) return s;
+    if ((s = dev_alloc_t(m, 4 * (size_t)st, &m->ff)) != GRX_OK) return s;
+    if ((s = dev_alloc_t(m, hp.n_vocab, &m->logits)) != GRX_OK) return s;
+    if ((s = dev_alloc_t(m, (size_t)hp.n_head * hp.n_audio_ctx, &m->scores)) != GRX_OK) return s;
+    if ((s = dev_alloc_t(m, 1, &m->amax)) != GRX_OK) return s;
+    if ((s = dev_alloc_t(m, 1, &m->tok)) != GRX_OK) return s;
+    if ((s = dev_alloc_t(m, 1, &m->pos)) != GRX_OK) return s;
+    if ((s = dev_alloc_t(m, hp.n_text_ctx, &m->hist)) != GRX_OK) return s;
+    GRX_HIP(hipMemset(m->pos, 0, 4));
+    GRX_HIP(hipMemset(m->tok, 0, 4));
+    m->host.clear();
+    m->ready = true;
+    (void)hd;
+    return GRX_OK;
+}
+
+GemvArgs gemv_args(const grx_weight *w) {
+    GemvArgs a = {};
+    a.qs = w->qs;
+    a.ds = w->ds;
+    a.rows = w->rows;
+    a.nb = w->nb;
+    return a;
+}
+
+// The launches of one decode step on stream st.
+grx_status enqueue_step(grx_whisper *m, hipStream_t stream) {
+    const grx_whisper_hparams &hp = m->hp;
+    const int st = hp.n_state, nh = hp.n_head, hd = st / nh, nctx = hp.n_audio_ctx;
+    const float sc = (float)(1.0 / sqrt((double)hd));
+    grx_status s;
+    embed_kernel<<<1, 256, 0, stream>>>(m->tok_emb->qs, m->tok_emb->ds, m->tok_emb->nb, m->dec_pos, m->tok, m->pos,
+                                        st, m->x, m->amax);
+    GRX_LAUNCHED("embed_kernel");
+    const size_t attn_smem = (32 + (size_t)hp.n_text_ctx) * 4, soft_smem = (32 + (size_t)nctx) * 4;
+    for (int li = 0; li < hp.n_layer; ++li) {
+        WLayer &L = m->L[li];
+        {  // LN -> q | k | v, k and v into the cache at pos
+            GemvArgs a = gemv_args(L.qkv);
+            a.x = m->x;
+            a.lda = st;
+            a.ln_w = L.attn_ln_w;
+            a.ln_b = L.attn_ln_b;
+            a.y = m->q;
+            a.ldc = st;
+            a.bias = L.qkv_b;
+            a.seg = st;
+            a.kc = L.self_k;
+            a.vc = L.self_v;
+            a.pos = m->pos;
+            if ((s = grx_gemv_launch(stream, 1, GRX_PRO_LN, GRX_EPI_QKV, a, 0)) != GRX_OK) return s;
+        }
+        self_attn_kernel<<<nh, kAttnThreads, attn_smem, stream>>>(m->q, L.self_k, L.self_v, m->pos, st, hd, sc, m->att);
+        GRX_LAUNCHED("self_attn_kernel");
+        {  // x += att . Wo^T + b
+            GemvArgs a = gemv_args(L.o);
+            a.x = m->att;
+            a.lda = st;
+            a.y = m->x;
+            a.ldc = st;
+            a.bias = L.o_b;
+            a.resid = m->x;
+            a.ldr = st;
+            if ((s = grx_gemv_launch(stream, 1, GRX_PRO_QUANT, GRX_EPI_RESID, a, 0)) != GRX_OK) return s;
+        }
+        {  // LN -> cross query
+            GemvArgs a = gemv_args(L.xq);
+            a.x = m->x;
+            a.lda = st;
+            a.ln_w = L.x_ln_w;
+            a.ln_b = L.x_ln_b;
+            a.y = m->q;
+            a.ldc = st;
+            a.bias = L.xq_b;
+            if ((s = grx_gemv_launch(stream, 1, GRX_PRO_LN, GRX_EPI_STORE, a, 0)) != GRX_OK) return s;
+        }
+        cross_scores_kernel<<<dim3(nh, grx_ceil_div(nctx, kAttnThreads)), kAttnThreads, 0, stream>>>(
+            m->q, L.cross_k, nctx, hd, m->scores);
+        GRX_LAUNCHED("cross_scores_kernel");
+        softmax_rows_kernel<<<nh, kAttnThreads, soft_smem, stream>>>(m->scores, nctx);
+        GRX_LAUNCHED("softmax_rows_kernel");
+        cross_values_kernel<<<dim3(nh, grx_ceil_div(hd, 4)), 64, 0, stream>>>(m->scores, L.cross_v, nctx, hd, m->att);
+        GRX_LAUNCHED("cross_values_kernel");
+        {  // x += att . Wxo^T + b
+            GemvArgs a = gemv_args(L.xo);
+            a.x = m->att;
+            a.lda = st;
+            a.y = m->x;
+            a.ldc = st;
+            a.bias = L.xo_b;
+            a.resid = m->x;
+            a.ldr = st;
+            if ((s = grx_gemv_launch(stream, 1, GRX_PRO_QUANT, GRX_EPI_RESID, a, 0)) != GRX_OK) return s;
+        }
+        {  // LN -> fc1 -> GELU
+            GemvArgs a = gemv_args(L.fc1);
+            a.x = m->x;
+            a.lda = st;
+            a.ln_w = L.mlp_ln_w;
+            a.ln_b = L.mlp_ln_b;
+            a.y = m->ff;
+            a.ldc = 4 * st;
+            a.bias = L.fc1_b;
+            if ((s = grx_gemv_launch(stream, 1, GRX_PRO_LN, GRX_EPI_GELU, a, 0)) != GRX_OK) return s;
+        }
+        {  // x += ff . Wfc2^T + b
+            GemvArgs a = gemv_args(L.fc2);
+            a.x = m->ff;
+            a.lda = 4 * st;
+            a.y = m->x;
+            a.ldc = st;
+            a.bias = L.fc2_b;
+            a.resid = m->x;
+            a.ldr = st;
+            if ((s = grx_gemv_launch(stream, 1, GRX_PRO_QUANT, GRX_EPI_RESID, a, 0)) != GRX_OK) return s;
+        }
+    }
+    {  // LN -> logits = tokEmb . h -> argmax
+        GemvArgs a = gemv_args(m->tok_emb);
+        a.x = m->x;
+        a.lda = st;
+        a.ln_w = m->dec_ln_w;
+        a.ln_b = m->dec_ln_b;
+        a.y = m->logits;
+        a.ldc = hp.n_vocab;
+        a.amax = m->amax;
+        if ((s = grx_gemv_launch(stream, 1, GRX_PRO_LN, GRX_EPI_ARGMAX, a, 0)) != GRX_OK) return s;
+    }
+    finish_kernel<<<1, 1, 0, stream>>>(m->amax, m->tok, m->pos, m->hist);
+    GRX_LAUNCHED("finish_kernel");
+    return GRX_OK;
+}
+
+// One step: the captured graph, or (GRX_NO_GRAPH=1, or capture refused)
+// the same launches directly.
+grx_status run_step(grx_whisper *m) {
+    hipStream_t stream = m->ctx->stream;
+    const char *ng = getenv("GRX_NO_GRAPH");
+    if (ng && ng[0] == '1') return enqueue_step(m, stream);
+    if (!m->exec) {
+        // an eager step first sets every kernel's attributes outside capture;
+        // its effect is undone by the caller's bookkeeping (it runs the step
+        // it was asked to run)
+        grx_status s = enqueue_step(m, stream);
+        if (s != GRX_OK) return s;
+        GRX_HIP(hipStreamSynchronize(stream));
+        hipError_t e = hipStreamBeginCapture(stream, hipStreamCaptureModeThreadLocal);
+        if (e == hipSuccess) {
+            s = enqueue_step(m, stream);
+            hipGraph_t g = nullptr;
+            e = hipStreamEndCapture(stream, &g);
+            if (s == GRX_OK && e == hipSuccess) e = hipGraphInstantiate(&m->exec, g, nullptr, nullptr, 0);
+            if (g) {
+                if (e == hipSuccess) m->graph = g;
+                else (void)hipGraphDestroy(g);
+            }
+        }
+        if (e != hipSuccess || s != GRX_OK) {
+            (void)hipGetLastError();
+            m->exec = nullptr;
+        }
+        return GRX_OK;
+    }
+    GRX_HIP(hipGraphLaunch(m->exec, stream));
+    return GRX_OK;
+}
+
+}  // namespace
+
+extern "C" grx_status grx_whisper_create(grx_ctx *ctx, const grx_whisper_hparams *hp, grx_whisper **out) {
+    if (!ctx || !hp || !out) return grx_fail(GRX_EINVAL, "grx_whisper_create: NULL argument");
+    *out = nullptr;
+    if (hp->n_vocab <= 0 || hp->n_text_ctx <= 0 || hp->n_state <= 0 || hp->n_head <= 0 || hp->n_layer <= 0 ||
+        hp->n_audio_ctx <= 0)
+        return grx_fail(GRX_EINVAL, "grx_whisper_create: every size must be positive");
+    if (hp->n_state % 32 != 0 || hp->n_state % hp->n_head != 0)
+        return grx_fail(GRX_ESIZE, "grx_whisper_create: n_state %d must be a multiple of 32 and of n_head %d",
+                        hp->n_state, hp->n_head);
+    grx_whisper *m = new grx_whisper();
+    m->ctx = ctx;
+    m->hp = *hp;
+    *out = m;
+    return GRX_OK;
+}
+
+extern "C" grx_status grx_whisper_destroy(grx_whisper *m) {
+    if (!m) return GRX_OK;
+    GRX_HIP(hipSetDevice(m->ctx->device));
+    GRX_HIP(hipStreamSynchronize(m->ctx->stream));
+    if (m->exec) (void)hipGraphExecDestroy(m->exec);
+    if (m->graph) (void)hipGraphDestroy(m->graph);
+    for (WLayer &L : m->L)
+        for (grx_weight *w : {L.qkv, L.o, L.xq, L.xk, L.xv, L.xo, L.fc1, L.fc2}) grx_weight_destroy(w);
+    grx_weight_destroy(m->tok_emb);
+    for (void *p : m->allocs) (void)hipFree(p);
+    delete m;
+    return GRX_OK;
+}
+
+extern "C" grx_status grx_whisper_set_tensor(grx_whisper *m, const char *name, const void *data, size_t nbytes) {
+    if (!m || !name || (!data && nbytes)) return grx_fail(GRX_EINVAL, "grx_whisper_set_tensor: NULL argument");
+    if (m->ready) return grx_fail(GRX_ESTATE, "grx_whisper_set_tensor: the model is in use already");
+    for (const Expect &e : expected(m->hp)) {
+        if (e.name != name) continue;
+        if (nbytes != e.bytes)
+            return grx_fail(GRX_ESIZE, "tensor %s has the wrong shape (%zu bytes, want %zu)", name, nbytes, e.bytes);
+        const uint8_t *p = static_cast<const uint8_t *>(data);
+        m->host[name].assign(p, p + nbytes);
+        return GRX_OK;
+    }
+    return grx_fail(GRX_EINVAL, "the model file has a tensor this program doesn't know: %s", name);
+}
+
+extern "C" grx_status grx_whisper_set_encoder_output(grx_whisper *m, const float *enc, int n_audio_ctx) {
+    if (!m || !enc) return grx_fail(GRX_EINVAL, "grx_whisper_set_encoder_output: NULL argument");
+    if (n_audio_ctx != m->hp.n_audio_ctx)
+        return grx_fail(GRX_ESIZE, "grx_whisper_set_encoder_output: %d positions, the model has %d", n_audio_ctx,
+                        m->hp.n_audio_ctx);
+    grx_status s = finalize(m);
+    if (s != GRX_OK) return s;
+    const int st = m->hp.n_state, nctx = n_audio_ctx, hd = st / m->hp.n_head;
+    const size_t n = (size_t)nctx * st;
+    float *denc = nullptr, *dk = nullptr, *dv = nullptr;
+    GRX_HIP(hipMalloc(&denc, n * 4));
+    GRX_HIP(hipMalloc(&dk, n * 4));
+    GRX_HIP(hipMalloc(&dv, n * 4));
+    hipStream_t stream = m->ctx->stream;
+    GRX_HIP(hipMemcpyAsync(denc, enc, n * 4, hipMemcpyHostToDevice, stream));
+    const float tsc = (float)(1.0 / sqrt((double)hd));
+    for (int li = 0; li < m->hp.n_layer && s == GRX_OK; ++li) {
+        WLayer &L = m->L[li];
+        s = grx_matmul_q8_dev(m->ctx, dk, st, denc, st, nctx, L.xk, nullptr);
+        if (s == GRX_OK) s = grx_matmul_q8_dev(m->ctx, dv, st, denc, st, nctx, L.xv, L.xv_b);
+        if (s == GRX_OK) {
+            cross_layout_kernel<<<(int)((n + 255) / 256), 256, 0, stream>>>(dk, dv, nctx, st, hd, tsc, L.cross_k,
+                                                                           L.cross_v);
+            hipError_t e = hipGetLastError();
+            if (e != hipSuccess) s = grx_hip_fail(e, "cross_layout_kernel");
+        }
+    }
+    hipError_t e = hipStreamSynchronize(stream);
+    (void)hipFree(denc);
+    (void)hipFree(dk);
+    (void)hipFree(dv);
+    if (s != GRX_OK) return s;
+    if (e != hipSuccess) return grx_hip_fail(e, "grx_whisper_set_encoder_output");
+    m->have_cross = true;
+    return GRX_OK;
+}
+
+extern "C" grx_status grx_whisper_reset(grx_whisper *m) {
+    if (!m) return grx_fail(GRX_EINVAL, "grx_whisper_reset: NULL model");
+    if (m->ready) GRX_HIP(hipMemsetAsync(m->pos, 0, 4, m->ctx->stream));
+    m->pos_host = 0;
+    return GRX_OK;
+}
+
+extern "C" int grx_whisper_pos(const grx_whisper *m) { return m ? m->pos_host : 0; }
+
+static grx_status check_ready(grx_whisper *m, const char *fn) {
+    if (!m) return grx_fail(GRX_EINVAL, "%s: NULL model", fn);
+    grx_status s = finalize(m);
+    if (s != GRX_OK) return s;
+    if (!m->have_cross) return grx_fail(GRX_ESTATE, "%s: no encoder output set", fn);
+    return GRX_OK;
+}
+
+extern "C" grx_status grx_whisper_decode(grx_whisper *m, const int32_t *tokens, int n, float *logits, int32_t *next) {
+    grx_status s = check_ready(m, "grx_whisper_decode");
+    if (s != GRX_OK) return s;
+    if (n < 0 || (n > 0 && !tokens)) return grx_fail(GRX_EINVAL, "grx_whisper_decode: bad tokens");
+    if (m->pos_host + n > m->hp.n_text_ctx)
+        return grx_fail(GRX_ESTATE, "grx_whisper_decode: %d tokens after %d positions exceed the context of %d", n,
+                        m->pos_host, m->hp.n_text_ctx);
+    for (int i = 0; i < n; ++i)
+        if (tokens[i] < 0 || tokens[i] >= m->hp.n_vocab)
+            return grx_fail(GRX_EINVAL, "grx_whisper_decode: token %d out of the vocabulary", tokens[i]);
+    hipStream_t stream = m->ctx->stream;
+    for (int i = 0; i < n; ++i) {
+        GRX_HIP(hipMemcpyAsync(m->tok, tokens + i, 4, hipMemcpyHostToDevice, stream));
+        if ((s = run_step(m)) != GRX_OK) return s;
+        m->pos_host++;
+    }
+    if (n > 0 && logits)
+        GRX_HIP(hipMemcpyAsync(logits, m->logits, (size_t)m->hp.n_vocab * 4, hipMemcpyDeviceToHost, stream));
+    if (n > 0 && next) GRX_HIP(hipMemcpyAsync(next, m->tok, 4, hipMemcpyDeviceToHost, stream));
+    GRX_HIP(hipStreamSynchronize(stream));
+    return GRX_OK;
+}
+
+extern "C" grx_status grx_whisper_greedy(grx_whisper *m, const int32_t *prompt, int n_prompt, int n_steps,
+                                         int32_t *out) {
+    grx_status s = check_ready(m, "grx_whisper_greedy");
+    if (s != GRX_OK) return s;
+    if (n_prompt <= 0 || n_steps < 0 || !prompt || !out)
+        return grx_fail(GRX_EINVAL, "grx_whisper_greedy: bad arguments");
+    if (n_prompt + n_steps > m->hp.n_text_ctx)
+        return grx_fail(GRX_ESTATE, "grx_whisper_greedy: %d prompt tokens and %d steps exceed the context of %d",
+                        n_prompt, n_steps, m->hp.n_text_ctx);
+    if ((s = grx_whisper_reset(m)) != GRX_OK) return s;
+    if ((s = grx_whisper_decode(m, prompt, n_prompt, nullptr, nullptr)) != GRX_OK) return s;
+    hipStream_t stream = m->ctx->stream;
+    for (int i = 0; i < n_steps; ++i) {
+        if ((s = run_step(m)) != GRX_OK) return s;
+        m->pos_host++;
+    }
+    GRX_HIP(hipMemcpyAsync(out, m->hist + (n_prompt - 1), (size_t)(n_steps + 1) * 4, hipMemcpyDeviceToHost, stream));
+    GRX_HIP(hipStreamSynchronize(stream));
+    return GRX_OK;
+}

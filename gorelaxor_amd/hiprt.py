@@ -75,6 +75,10 @@ class DeviceBuffer:
         _check(hip().hipMemcpy(out.ctypes.data, self.ptr, out.nbytes, D2H), "hipMemcpy D2H")
         return out
 
+    def copy_from(self, other: "DeviceBuffer", nbytes: int | None = None) -> None:
+        n = min(self.nbytes, other.nbytes) if nbytes is None else nbytes
+        _check(hip().hipMemcpy(self.ptr, other.ptr, n, D2D), "hipMemcpy D2D")
+
     def zero(self) -> None:
         _check(hip().hipMemset(self.ptr, 0, self.nbytes), "hipMemset")
 

@@ -122,6 +122,48 @@ grx_status grx_matmul_q8_prequant_dev(grx_ctx *ctx, float *dst, int ldc, const i
 grx_status grx_block_dots_dev(grx_ctx *ctx, int32_t *s, const int8_t *q, int m,
                               const grx_weight *w);
 
+/* ---- whisper-shaped text decoder with Q8_0 weights ---- */
+
+/* The decoder graph of whisper/decoder.go:33-140 with every matrix a Q8_0
+ * weight on the int8 route above, kept on one GPU: the self-attention KV
+ * cache, the cross-attention keys and values, the token and the position
+ * live in HBM, and one decode step is a fixed sequence of launches
+ * (replayed from a HIP graph) that ends in the argmax of the logits. */
+typedef struct {
+    int n_vocab, n_text_ctx, n_state, n_head, n_layer, n_audio_ctx; /* whisper/model.go:16-21 */
+} grx_whisper_hparams;
+
+typedef struct grx_whisper grx_whisper;
+
+grx_status grx_whisper_create(grx_ctx *ctx, const grx_whisper_hparams *hp, grx_whisper **out);
+grx_status grx_whisper_destroy(grx_whisper *m);
+/* Model.bind (whisper/model.go:300-404) for the decoder's tensors, by the
+ * ggml names ("decoder.token_embedding.weight", "decoder.blocks.0.attn.
+ * query.weight", ...): matrices as ggml Q8_0 rows, vectors as float32.
+ * Shapes are checked; all tensors must be set before the first decode. */
+grx_status grx_whisper_set_tensor(grx_whisper *m, const char *name, const void *data, size_t nbytes);
+/* The cross-attention keys and values of every layer from the encoder
+ * output, n_audio_ctx x n_state float32 on the host (whisper/encoder.go:
+ * 120-143): K scaled by 1/sqrt(head_dim) and kept [head][t][d], V kept
+ * transposed [head][d][t]. */
+grx_status grx_whisper_set_encoder_output(grx_whisper *m, const float *enc, int n_audio_ctx);
+/* Empty the self-attention cache (kvCache.n = 0, decoder.go:7-11). */
+grx_status grx_whisper_reset(grx_whisper *m);
+/* Positions filled in the self-attention cache. */
+int grx_whisper_pos(const grx_whisper *m);
+/* Model.decode (decoder.go:33-140) of n tokens after the cached positions;
+ * the logits of the last one go to `logits` (n_vocab floats, may be NULL)
+ * and their argmax - the first index of the largest value, as the greedy
+ * sampler takes it (whisper/transcribe.go:459-464) - to *next (may be
+ * NULL).  GRX_ESTATE when the tokens do not fit n_text_ctx. */
+grx_status grx_whisper_decode(grx_whisper *m, const int32_t *tokens, int n, float *logits, int32_t *next);
+/* Greedy decoding on the device (the loop of whisper/transcribe.go:207-260
+ * with plain argmax): the prompt, then n_steps single-token steps each fed
+ * the previous argmax, with no host round trip in between.  out receives
+ * n_steps+1 token ids: the argmax after the prompt, then one per step. */
+grx_status grx_whisper_greedy(grx_whisper *m, const int32_t *prompt, int n_prompt, int n_steps,
+                              int32_t *out);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,0 +1,103 @@
+"""The whisper-shaped Q8_0 decoder on the GPU against the CPU oracle: logits
+bit-identical at every step and greedy token sequences identical, at a small
+shape, at a shape with ragged attention lengths, and at the whisper base.en
+shape (d 512, 8 heads, 6 layers, FFN 2048, vocab 51864, 1500 audio
+positions)."""
+import os
+
+import numpy as np
+import pytest
+
+from gorelaxor_amd.synth import WHISPER_BASE_EN, WHISPER_TINY_TEST, encoder_output, whisper_model
+
+pytestmark = pytest.mark.gpu
+
+
+def _pair(orc, hp, seed=3):
+    from gorelaxor_amd.whisper import WhisperDecoder
+
+    t = whisper_model(hp, seed=seed)
+    enc = encoder_output(hp, seed=seed + 1)
+    ref = orc.WhisperOracle(hp, t)
+    ref.set_encoder_output(enc)
+    dec = WhisperDecoder(hp, t)
+    dec.set_encoder_output(enc)
+    return ref, dec
+
+
+def _same(a, b):
+    return np.array_equal(np.asarray(a, np.float32).view(np.uint32), np.asarray(b, np.float32).view(np.uint32))
+
+
+@pytest.mark.parametrize("shape", ["tiny", "ragged"])
+def test_decode_logits_bit_exact(kern, orc, shape):
+    hp = dict(WHISPER_TINY_TEST)
+    if shape == "ragged":  # audio length not a multiple of 16, odd head count
+        hp.update(n_audio_ctx=101, n_head=4, n_state=96, n_vocab=333)
+    ref, dec = _pair(orc, hp)
+    toks = [5, 17, 3, 99]
+    lr = ref.decode(toks)
+    lg, nxt = dec.decode(toks)
+    assert _same(lg, lr), f"prompt: max |diff| {np.abs(lg - lr).max()}"
+    assert nxt == orc.argmax(lr)
+    for step in range(12):  # one token at a time, graph replays after the first
+        tok = nxt
+        lr = ref.decode([tok])
+        lg, nxt = dec.decode([tok])
+        assert _same(lg, lr), f"step {step}: max |diff| {np.abs(lg - lr).max()}"
+        assert nxt == orc.argmax(lr)
+    assert dec.pos == ref.n
+
+
+def test_greedy_tokens_identical_and_eager_equals_graph(kern, orc):
+    hp = dict(WHISPER_TINY_TEST)
+    ref, dec = _pair(orc, hp, seed=9)
+    want = ref.greedy([1, 2, 3, 4], 40)
+    got = dec.greedy([1, 2, 3, 4], 40)
+    assert list(got) == list(want)
+    os.environ["GRX_NO_GRAPH"] = "1"
+    try:
+        from gorelaxor_amd.whisper import WhisperDecoder
+
+        t = whisper_model(hp, seed=9)
+        eager = WhisperDecoder(hp, t)
+        eager.set_encoder_output(encoder_output(hp, seed=10))
+        assert list(eager.greedy([1, 2, 3, 4], 40)) == list(want)
+    finally:
+        del os.environ["GRX_NO_GRAPH"]
+    # replaying the greedy loop again from an empty cache repeats it
+    assert list(dec.greedy([1, 2, 3, 4], 40)) == list(want)
+
+
+def test_context_limit_and_errors(kern, orc):
+    from gorelaxor_amd import GrxError
+    from gorelaxor_amd.whisper import WhisperDecoder
+
+    hp = dict(WHISPER_TINY_TEST)
+    dec = WhisperDecoder(hp, whisper_model(hp, seed=1))
+    with pytest.raises(GrxError, match="no encoder output"):
+        dec.decode([1])
+    dec.set_encoder_output(encoder_output(hp))
+    with pytest.raises(GrxError, match="exceed the context"):
+        dec.decode(list(range(hp["n_text_ctx"] + 1)))
+    with pytest.raises(GrxError, match="vocabulary"):
+        dec.decode([hp["n_vocab"]])
+    bad = WhisperDecoder(hp)
+    with pytest.raises(GrxError, match="wrong shape"):
+        bad.set_tensor("decoder.ln.weight", np.zeros(3, np.float32))
+    with pytest.raises(GrxError, match="doesn't know"):
+        bad.set_tensor("decoder.nope", np.zeros(3, np.float32))
+
+
+def test_base_en_shape_greedy(kern, orc):
+    """whisper base.en shape: the prompt, then greedy steps; tokens identical
+    and the last logits bit-identical."""
+    hp = dict(WHISPER_BASE_EN)
+    ref, dec = _pair(orc, hp, seed=7)
+    n_steps = 16
+    want = ref.greedy([50257, 50362, 50363, 50258], n_steps)
+    got = dec.greedy([50257, 50362, 50363, 50258], n_steps)
+    assert list(got) == list(want)
+    lr = ref.decode([int(want[-1])])
+    lg, _ = dec.decode([int(got[-1])])
+    assert _same(lg, lr)
