@@ -41,6 +41,9 @@ def parse():
     p.add_argument("--warmup", type=int, default=20)
     p.add_argument("--cpu-seconds", type=float, default=10.0, help="bound on the CPU baseline's work")
     p.add_argument("--no-cpu", action="store_true")
+    p.add_argument("--decoder-steps", type=int, default=220,
+                   help="greedy steps after the 4-token prompt (KV 4 -> 224)")
+    p.add_argument("--no-decoder", action="store_true")
     p.add_argument("--copy-calibration", action="store_true",
                    help="only copy the ring's bytes device to device 3 times (reference reading for HBM counters)")
     return p.parse_args()
@@ -77,6 +80,53 @@ def cpu_baseline(w8: np.ndarray, x: np.ndarray, seconds: float) -> dict:
     return {"value": round(done * BYTES_PER_GEMV / el / 1e9, 3), "unit": "GB/s", "cores": 1, "kind": "port",
             "sample": f"{done} GEMVs of 1024x1024 (the first {min(done, RING)} ring matrices), "
                       f"{el:.1f} s, oracle/grx_oracle.c orc_matmul_q8_int, 1 thread, {platform.processor() or platform.machine()}"}
+
+
+PROMPT = [50257, 50362, 50363, 50258]
+
+
+def decoder_bench(args) -> dict:
+    """whisper base.en-shaped decoder with random-init Q8_0 weights: cross
+    attention over a 1500 x 512 N(0,1) encoder output, a 4-token prompt, then
+    `decoder_steps` greedy steps (KV 4 -> 224), all on the device.  Reports
+    decoder steps per second (one token through the decoder per step), and
+    checks the tokens against the oracle's."""
+    import oracle
+    from gorelaxor_amd.synth import WHISPER_BASE_EN, encoder_output, whisper_model
+    from gorelaxor_amd.whisper import WhisperDecoder
+
+    hp = dict(WHISPER_BASE_EN)
+    t = whisper_model(hp, seed=7)
+    enc = encoder_output(hp, seed=8)
+    dec = WhisperDecoder(hp, t)
+    t0 = time.perf_counter()
+    dec.set_encoder_output(enc)
+    cross_s = time.perf_counter() - t0
+    n = args.decoder_steps
+    dec.greedy(PROMPT, n)  # warm: graph captured, caches warm
+    reps = 3
+    times = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        toks = dec.greedy(PROMPT, n)
+        times.append(time.perf_counter() - t0)
+    best = min(times)
+    steps = len(PROMPT) + n
+    res = {"tokens_per_s": round(steps / best, 1), "ms_per_token": round(best / steps * 1e3, 4),
+           "steps_per_run": steps, "generated_tokens": n + 1, "runs": reps,
+           "cross_kv_setup_ms": round(cross_s * 1e3, 2),
+           "shape": "d_model 512, 8 heads, 6 layers, FFN 2048, vocab 51864, audio 1500, KV 4->%d" % (len(PROMPT) + n)}
+    oracle.build()
+    ref = oracle.WhisperOracle(hp, t)
+    ref.set_encoder_output(enc)
+    t0 = time.perf_counter()
+    want = ref.greedy(PROMPT, n)
+    cpu_s = time.perf_counter() - t0
+    res["parity_tokens_identical"] = bool(np.array_equal(want, toks))
+    res["cpu_baseline"] = {"value": round(steps / cpu_s, 2), "unit": "tokens/s", "cores": 1, "kind": "port",
+                           "sample": f"the same {steps} decoder steps on the oracle (scalar C, 1 thread), {cpu_s:.2f} s"}
+    dec.close()
+    return res
 
 
 def main():
@@ -167,6 +217,10 @@ def main():
     }
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline(w8, x, args.cpu_seconds)
+    del w, dy, dx
+    if not args.no_decoder:
+        out["decoder"] = decoder_bench(args)
+        out["config"]["workload"] += "; whisper base.en-shaped greedy decoder (decoder.tokens_per_s)"
     print(json.dumps(out), flush=True)
 
 
