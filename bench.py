@@ -34,6 +34,19 @@ N, K, RING = 1024, 1024, 512
 BYTES_PER_GEMV = N * K // 32 * 34 + K * 4 + N * 4   # 1,122,304 B per matrix
 
 
+def measured_traffic() -> int | None:
+    """HBM bytes per launch of the ring GEMV as rocprofv3's FETCH_SIZE and
+    WRITE_SIZE counters read them, scaled by a copy of known size
+    (profiles/gemv_q8_ring_traffic.txt, written from those runs)."""
+    path = os.path.join(ROOT, "profiles", "gemv_q8_ring_traffic.txt")
+    if not os.path.exists(path):
+        return None
+    for line in open(path):
+        if line.startswith("traffic_bytes="):
+            return int(line.split("=", 1)[1])
+    return None
+
+
 def parse():
     p = argparse.ArgumentParser()
     p.add_argument("--gpus", type=int, default=1)
@@ -212,7 +225,7 @@ def main():
                    "bytes_per_step": launch_bytes, "hbm_fraction": round(value / HBM_PEAK_GBS, 4),
                    "parity_bit_exact": parity, "wall_s": round(wall, 3)},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),
                      "kernel": "gemv_q8_kernel<1,1,PREQ,STORE>", "kernel_avg_us": round(gemv_avg * 1e3, 3)},
     }
     if not args.no_cpu:

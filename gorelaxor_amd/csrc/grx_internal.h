@@ -201,13 +201,14 @@ __device__ __forceinline__ float grx_gelu_at(float v, int i, int n) {
 }
 
 // Launch helpers of the product kernels (q8_gemv.hip).
-enum { GRX_PRO_PREQ = 0, GRX_PRO_QUANT = 1, GRX_PRO_LN = 2 };
+enum { GRX_PRO_PREQ = 0, GRX_PRO_QUANT = 1, GRX_PRO_LN = 2, GRX_PRO_EMBED_LN = 3 };
 enum {
     GRX_EPI_STORE = 0,   // y = c
     GRX_EPI_RESID = 1,   // y = resid + c
     GRX_EPI_GELU = 2,    // y = geluVec(c) over the flat output
     GRX_EPI_QKV = 3,     // rows split in three: q, then K and V caches at *pos
-    GRX_EPI_ARGMAX = 4   // y = c (optional) and the first index of the maximum
+    GRX_EPI_ARGMAX = 4,  // y = c (optional) and the first index of the maximum
+    GRX_EPI_GELU_Q = 5   // y = geluVec(c), and y rounded to Q8_0 into yq/ys
 };
 
 struct GemvArgs {
@@ -230,8 +231,23 @@ struct GemvArgs {
     int seg;
     float *kc, *vc;
     const int *pos;
-    // ARGMAX: one 64-bit key per activation row
+    // ARGMAX: one 64-bit key per activation row; with counter set, the last
+    // workgroup writes tok_w[m], hist[pos+m] and pos_w = pos+M
     unsigned long long *amax;
+    unsigned int *counter;
+    int *tok_w, *pos_w, *hist;
+    // EMBED_LN: x rows from token embeddings (the tile layout of a weight)
+    // plus positional rows, stored to x_out by tile 0
+    const int *tok;
+    const int8_t *emb_qs;
+    const uint16_t *emb_ds;
+    const float *pos_emb;
+    float *x_out;
+    // GELU_Q: the output rounded to Q8_0 (int8 [M][rows], f32 [M][rows/32])
+    int8_t *yq;
+    float *ys;
+    // ordinary (cache-retained) weight loads instead of non-temporal ones
+    int cacheable;
 };
 
 grx_status grx_gemv_launch(hipStream_t st, int m, int pro, int epi, const GemvArgs &a,

@@ -80,31 +80,29 @@ __device__ __forceinline__ double block_sum_f64(double v, double *red, int lane,
 }
 
 // Round (M rows x nb blocks) of float32 activations in LDS or global memory
-// into LDS: one thread per block.
+// into LDS, 32 lanes per block: lane e holds value e, the block's largest
+// magnitude comes from five xor-shuffles within the 32 lanes (the maximum
+// is order-free), and each lane rounds its own value as grx_quant_block does.
 template <int M>
 __device__ __forceinline__ void quant_into_lds(const float *src, int ld, int nb, int8_t *lxq,
                                                float *lxs, int tid, int nthreads) {
     const int K = nb * GRX_QK;
-    for (int i = tid; i < M * nb; i += nthreads) {
-        const int m = i / nb, b = i - m * nb;
-        const float4 *p = reinterpret_cast<const float4 *>(src + (size_t)m * ld + b * GRX_QK);
-        float v[GRX_QK];
+    const int e = tid & 31;
+    for (int g = tid >> 5; g < M * nb; g += nthreads >> 5) {
+        const int m = g / nb, b = g - m * nb;
+        const float v = src[(size_t)m * ld + b * GRX_QK + e];
+        const float av = fabsf(v);
+        float amax = av > 0.0f ? av : 0.0f;
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            const float4 f = p[j];
-            v[4 * j] = f.x;
-            v[4 * j + 1] = f.y;
-            v[4 * j + 2] = f.z;
-            v[4 * j + 3] = f.w;
+        for (int o = 16; o > 0; o >>= 1) {
+            const float t = __shfl_xor(amax, o, 32);
+            amax = t > amax ? t : amax;
         }
-        int8_t q[GRX_QK];
-        lxs[m * nb + b] = grx_quant_block(v, q);
-        int4 *d = reinterpret_cast<int4 *>(lxq + (size_t)m * K + b * GRX_QK);
-        int4 q0, q1;
-        __builtin_memcpy(&q0, q, 16);
-        __builtin_memcpy(&q1, q + 16, 16);
-        d[0] = q0;
-        d[1] = q1;
+        const float id = amax != 0.0f ? __fdiv_rn(127.0f, amax) : 0.0f;
+        float r = rintf(__fmul_rn(v, id));
+        r = fminf(fmaxf(r, -128.0f), 127.0f);
+        lxq[(size_t)m * K + b * GRX_QK + e] = (int8_t)(int)r;
+        if (e == 0) lxs[m * nb + b] = __fmul_rn(amax, grx_bits_f32(0x3c010204u));
     }
 }
 
@@ -124,7 +122,7 @@ __global__ __launch_bounds__(64 * W) void gemv_q8_kernel(const GemvArgs a) {
     const size_t o_xs = (PRO != GRX_PRO_PREQ) ? (size_t)M * K : 0;
     const size_t o_p = o_xs + ((PRO != GRX_PRO_PREQ) ? (((size_t)M * nb * 4 + 15) & ~(size_t)15) : 0);
     const size_t o_f = o_p + (W > 1 ? (size_t)M * nb * 64 * 4 : 0);
-    const size_t o_r = o_f + (PRO == GRX_PRO_LN ? (size_t)M * K * 4 : 0);
+    const size_t o_r = o_f + (PRO >= GRX_PRO_LN ? (size_t)M * K * 4 : 0);
     int8_t *lxq = reinterpret_cast<int8_t *>(smem);
     float *lxs = reinterpret_cast<float *>(smem + o_xs);
     float *lp = reinterpret_cast<float *>(smem + o_p);
@@ -135,16 +133,32 @@ __global__ __launch_bounds__(64 * W) void gemv_q8_kernel(const GemvArgs a) {
     if constexpr (PRO == GRX_PRO_QUANT) {
         quant_into_lds<M>(a.x, a.lda, nb, lxq, lxs, tid, 64 * W);
         __syncthreads();
-    } else if constexpr (PRO == GRX_PRO_LN) {
+    } else if constexpr (PRO == GRX_PRO_LN || PRO == GRX_PRO_EMBED_LN) {
         // layerNorm (internal/kern/mathx.go:55-75) of each row, then quantU8.
         for (int m = 0; m < M; ++m) {
             const float *xr = a.x + (size_t)m * a.lda;
             float *fr = lf + (size_t)m * K;
             double ps = 0.0;
-            for (int i = tid; i < K; i += 64 * W) {
-                const float v = xr[i];
-                fr[i] = v;
-                ps += (double)v;
+            if constexpr (PRO == GRX_PRO_EMBED_LN) {
+                // the row is tokEmb.row(tok) + decPos[pos] (whisper/decoder.go:42-46),
+                // built by every workgroup; tile 0 stores it for the residual
+                const int t = a.tok[m], p = *a.pos + m;
+                const int etile = t >> 6, elane = t & 63;
+                for (int i = tid; i < K; i += 64 * W) {
+                    const int b = i >> 5, h = (i >> 4) & 1, e = i & 15;
+                    const int8_t q = a.emb_qs[(((size_t)etile * nb + b) * 2 + h) * 1024 + elane * 16 + e];
+                    const float d = grx_f16_to_f32(a.emb_ds[((size_t)etile * nb + b) * 64 + elane]);
+                    const float v = __fadd_rn(__fmul_rn((float)q, d), a.pos_emb[(size_t)p * K + i]);
+                    fr[i] = v;
+                    ps += (double)v;
+                    if (tile == 0) a.x_out[(size_t)m * a.lda + i] = v;
+                }
+            } else {
+                for (int i = tid; i < K; i += 64 * W) {
+                    const float v = xr[i];
+                    fr[i] = v;
+                    ps += (double)v;
+                }
             }
             const double sum = block_sum_f64(ps, red, lane, wave, W);
             const float mean = (float)(sum / (double)K);
@@ -202,9 +216,15 @@ __global__ __launch_bounds__(64 * W) void gemv_q8_kernel(const GemvArgs a) {
         uint32_t dh[U];
 #pragma unroll
         for (int u = 0; u < U; ++u) {
-            w[2 * u] = wload(wq + (size_t)(bb + u) * 128 + lane);
-            w[2 * u + 1] = wload(wq + (size_t)(bb + u) * 128 + 64 + lane);
-            dh[u] = wload(wd + (size_t)(bb + u) * 64 + lane);
+            if (a.cacheable) {
+                w[2 * u] = wq[(size_t)(bb + u) * 128 + lane];
+                w[2 * u + 1] = wq[(size_t)(bb + u) * 128 + 64 + lane];
+                dh[u] = wd[(size_t)(bb + u) * 64 + lane];
+            } else {
+                w[2 * u] = wload(wq + (size_t)(bb + u) * 128 + lane);
+                w[2 * u + 1] = wload(wq + (size_t)(bb + u) * 128 + 64 + lane);
+                dh[u] = wload(wd + (size_t)(bb + u) * 64 + lane);
+            }
         }
 #pragma unroll
         for (int u = 0; u < U; ++u) {
@@ -260,7 +280,65 @@ __global__ __launch_bounds__(64 * W) void gemv_q8_kernel(const GemvArgs a) {
                 const unsigned long long k2 = __shfl_xor(key, o);
                 key = k2 > key ? k2 : key;
             }
-            if (lane == 0) atomicMax(a.amax + m, key);
+            if (lane == 0) {
+                // a returning atomic: its old value comes back only once the
+                // maximum has been taken at the coherence point
+                const unsigned long long old = atomicMax(a.amax + m, key);
+                asm volatile("; argmax done %0" ::"v"((uint32_t)old));
+            }
+        }
+        if (a.counter != nullptr) {
+            // The last workgroup to finish ends the decode step: the argmax
+            // token, its record, the next position; then clears the key and
+            // the counter for the next step.  Device-scope atomics are
+            // coherent across the XCDs, and each workgroup's atomicMax has
+            // returned before its count is added, so no cache writeback is
+            // needed.
+            unsigned int done = 0;
+            if (lane == 0) done = atomicAdd(a.counter, 1u);
+            done = __shfl(done, 0);
+            if (done == gridDim.x - 1) {
+                const int p0 = *a.pos;
+                if (lane < M) {
+                    const unsigned long long k = atomicMax(a.amax + lane, 0ull);
+                    const int t = (int)(0xffffffffu - (uint32_t)(k & 0xffffffffull));
+                    a.tok_w[lane] = t;
+                    a.hist[p0 + lane] = t;
+                    a.amax[lane] = 0ull;
+                }
+                if (lane == 0) {
+                    *a.pos_w = p0 + M;
+                    *a.counter = 0u;
+                }
+            }
+        }
+        return;
+    }
+    if constexpr (EPI == GRX_EPI_GELU_Q) {
+        // geluVec, then quantU8 of the output's 32-value blocks for the next
+        // product: rows 64*tile..+31 and +32..+63 are two whole blocks
+        // (rows % 32 == 0), held by the two halves of this wave.
+#pragma unroll
+        for (int m = 0; m < M; ++m) {
+            const int flat = m * a.rows + row, total = M * a.rows;
+            const int start = flat & ~((1 << 14) - 1);
+            const int len = min(1 << 14, total - start);
+            const float v = row < a.rows ? grx_gelu_at(acc[m], flat - start, len) : 0.0f;
+            const float av = fabsf(v);
+            float amax = av > 0.0f ? av : 0.0f;
+#pragma unroll
+            for (int o = 16; o > 0; o >>= 1) {
+                const float t = __shfl_xor(amax, o, 32);
+                amax = t > amax ? t : amax;
+            }
+            if (row < a.rows) {
+                const float id = amax != 0.0f ? __fdiv_rn(127.0f, amax) : 0.0f;
+                float r = rintf(__fmul_rn(v, id));
+                r = fminf(fmaxf(r, -128.0f), 127.0f);
+                a.y[(size_t)m * a.ldc + row] = v;
+                a.yq[(size_t)m * a.rows + row] = (int8_t)(int)r;
+                if ((lane & 31) == 0) a.ys[(size_t)m * (a.rows >> 5) + (row >> 5)] = __fmul_rn(amax, grx_bits_f32(0x3c010204u));
+            }
         }
         return;
     }
@@ -328,7 +406,7 @@ size_t gemv_smem(int M, int W, int pro, int nb) {
     size_t n = 0;
     if (pro != GRX_PRO_PREQ) n += M * K + (((size_t)M * nb * 4 + 15) & ~(size_t)15);
     if (W > 1) n += (size_t)M * nb * 64 * 4;
-    if (pro == GRX_PRO_LN) n += (size_t)M * K * 4 + 2 * 16 * sizeof(double);
+    if (pro >= GRX_PRO_LN) n += (size_t)M * K * 4 + 2 * 16 * sizeof(double);
     return n;
 }
 
@@ -396,6 +474,9 @@ grx_status grx_gemv_launch(hipStream_t st, int m, int pro, int epi, const GemvAr
     else if (pro == GRX_PRO_LN && epi == GRX_EPI_GELU) e = launch_m<GRX_PRO_LN, GRX_EPI_GELU>(st, m, a, tiles, W);
     else if (pro == GRX_PRO_LN && epi == GRX_EPI_QKV) e = launch_m<GRX_PRO_LN, GRX_EPI_QKV>(st, m, a, tiles, W);
     else if (pro == GRX_PRO_LN && epi == GRX_EPI_ARGMAX) e = launch_m<GRX_PRO_LN, GRX_EPI_ARGMAX>(st, m, a, tiles, W);
+    else if (pro == GRX_PRO_LN && epi == GRX_EPI_GELU_Q) e = launch_m<GRX_PRO_LN, GRX_EPI_GELU_Q>(st, m, a, tiles, W);
+    else if (pro == GRX_PRO_EMBED_LN && epi == GRX_EPI_QKV) e = launch_m<GRX_PRO_EMBED_LN, GRX_EPI_QKV>(st, m, a, tiles, W);
+    else if (pro == GRX_PRO_PREQ && epi == GRX_EPI_RESID) e = launch_m<GRX_PRO_PREQ, GRX_EPI_RESID>(st, m, a, tiles, W);
     else return grx_fail(GRX_EINVAL, "grx: no GEMV variant for prologue %d epilogue %d", pro, epi);
     if (e != hipSuccess) return grx_hip_fail(e, "gemv_q8_kernel");
     return GRX_OK;

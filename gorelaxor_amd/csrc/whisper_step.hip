@@ -6,16 +6,18 @@
 // arithmetic in its own order, so a step's logits are bit-identical to the
 // CPU oracle's and the greedy tokens are the same.
 //
-// One step is: embed, then per layer
-//   [LN -> q|k|v GEMV, k and v written into the cache at pos]  (one launch)
-//   [self-attention over pos+1 cached keys, one workgroup per head]
-//   [att -> Q8_0 -> out GEMV + residual]
-//   [LN -> cross query GEMV] [cross scores] [softmax] [cross values]
-//   [att -> Q8_0 -> cross out GEMV + residual]
-//   [LN -> fc1 GEMV -> GELU] [ff -> Q8_0 -> fc2 GEMV + residual]
-// and [LN -> logits GEMV -> argmax] [finish: token, pos+1].  Token and
-// position live in device memory, so the step is captured once into a HIP
-// graph and replayed; greedy decoding never returns to the host.
+// One step is, per layer:
+//   [LN -> q|k|v GEMV, k and v written into the cache at pos]  (one launch;
+//    layer 0 builds the embedding row in the same prologue)
+//   [self-attention over pos+1 cached keys, one workgroup per head, output
+//    rounded to Q8_0]  [out GEMV + residual]
+//   [LN -> cross query GEMV] [cross scores] [softmax + weighted values,
+//    rounded to Q8_0]  [cross out GEMV + residual]
+//   [LN -> fc1 GEMV -> GELU, rounded to Q8_0] [fc2 GEMV + residual]
+// then [LN -> logits GEMV -> argmax; the last workgroup writes the token and
+// moves the position on].  Token and position live in device memory, so the
+// step is captured once into a HIP graph and replayed; greedy decoding never
+// returns to the host.
 #include <math.h>
 #include <stdlib.h>
 #include <string.h>
@@ -31,23 +33,6 @@ namespace {
 constexpr int kAttnThreads = 256;
 
 // ---------------------------------------------------------------- kernels
-
-// x = widen(tokEmb.row(tok)) + decPos[pos] (decoder.go:42-46); clears the
-// argmax key of the step.
-__global__ void embed_kernel(const int8_t *__restrict__ qs, const uint16_t *__restrict__ ds, int nb,
-                             const float *__restrict__ dec_pos, const int *__restrict__ tok,
-                             const int *__restrict__ pos, int st, float *__restrict__ x,
-                             unsigned long long *__restrict__ amax) {
-    const int t = *tok, p = *pos;
-    const int tile = t >> 6, lane = t & 63;
-    for (int i = threadIdx.x; i < st; i += blockDim.x) {
-        const int b = i >> 5, h = (i >> 4) & 1, e = i & 15;
-        const int8_t q = qs[(((size_t)tile * nb + b) * 2 + h) * 1024 + lane * 16 + e];
-        const float d = grx_f16_to_f32(ds[((size_t)tile * nb + b) * 64 + lane]);
-        x[i] = __fadd_rn(__fmul_rn((float)q, d), dec_pos[(size_t)p * st + i]);
-    }
-    if (threadIdx.x == 0) *amax = 0ull;
-}
 
 // dotF32Go (internal/kern/gemm.go:294-308): four running sums, unfused.
 __device__ __forceinline__ float dot_go(const float *x, const float *y, int n) {
@@ -121,6 +106,7 @@ __device__ void block_softmax(float *s, int n, float *part) {
     __syncthreads();
     if (tid < 8) {
         float acc = 0.f;
+#pragma unroll 16
         for (int j = tid; j < n8; j += 8) acc = __fadd_rn(acc, s[j]);
         part[tid] = acc;
     } else if (tid == 8) {
@@ -135,12 +121,37 @@ __device__ void block_softmax(float *s, int n, float *part) {
     __syncthreads();
 }
 
+// Round the values held by 32 consecutive lanes (one Q8_0 block) for the
+// next product: quantU8 (internal/kern/q8int.go:88-105) with the block's
+// largest magnitude from xor-shuffles.  Every lane of the 32 must call it.
+__device__ __forceinline__ void quant32_store(float v, int8_t *q, float *sc, int lane32) {
+    const float av = fabsf(v);
+    float amax = av > 0.0f ? av : 0.0f;
+#pragma unroll
+    for (int o = 16; o > 0; o >>= 1) {
+        const float t = __shfl_xor(amax, o, 32);
+        amax = t > amax ? t : amax;
+    }
+    const float id = amax != 0.0f ? __fdiv_rn(127.0f, amax) : 0.0f;
+    float r = rintf(__fmul_rn(v, id));
+    r = fminf(fmaxf(r, -128.0f), 127.0f);
+    *q = (int8_t)(int)r;
+    if (lane32 == 0) *sc = __fmul_rn(amax, grx_bits_f32(0x3c010204u));
+}
+
+constexpr int kBatch = 32;  // loads issued before their values are used
+constexpr int kBatchV = 64;  // the same for the cross values' longer chains
+
 // Causal self-attention of one head over the pos+1 cached positions
 // (decoder.go:70-87): scores dotF32Go(q, k_j)*sc, softmax, and
-// out[d] += p_j * v_j[d] in position order, unfused.
+// out[d] += p_j * v_j[d] in position order, unfused.  With QOUT (head_dim a
+// multiple of 32) the head's outputs are also rounded to Q8_0 for the out
+// projection.
+template <bool QOUT>
 __global__ __launch_bounds__(kAttnThreads) void self_attn_kernel(
     const float *__restrict__ q, const float *__restrict__ kc, const float *__restrict__ vc,
-    const int *__restrict__ pos, int st, int hd, float sc, float *__restrict__ att) {
+    const int *__restrict__ pos, int st, int hd, float sc, float *__restrict__ att, int8_t *__restrict__ att_q,
+    float *__restrict__ att_s) {
     extern __shared__ float sm[];
     float *part = sm;        // 32 floats
     float *s = sm + 32;      // n_text_ctx floats
@@ -152,8 +163,16 @@ __global__ __launch_bounds__(kAttnThreads) void self_attn_kernel(
     for (int d = tid; d < hd; d += blockDim.x) {
         float o = 0.f;
         const float *vd = vc + h * hd + d;
-        for (int j = 0; j < n; ++j) o = __fadd_rn(o, __fmul_rn(s[j], vd[(size_t)j * st]));
+        for (int j0 = 0; j0 < n; j0 += kBatch) {
+            float vv[kBatch];
+#pragma unroll
+            for (int u = 0; u < kBatch; ++u) vv[u] = j0 + u < n ? vd[(size_t)(j0 + u) * st] : 0.f;
+#pragma unroll
+            for (int u = 0; u < kBatch; ++u)
+                if (j0 + u < n) o = __fadd_rn(o, __fmul_rn(s[j0 + u], vv[u]));
+        }
         att[h * hd + d] = o;
+        if constexpr (QOUT) quant32_store(o, att_q + h * hd + d, att_s + (h * hd + d) / 32, d & 31);
     }
 }
 
@@ -168,60 +187,65 @@ __global__ __launch_bounds__(kAttnThreads) void cross_scores_kernel(
     scores[(size_t)h * nctx + j] = j < (nctx & ~3) ? dot_x4(qh, kj, hd) : dot_go(qh, kj, hd);
 }
 
-// softmax of each head's row of scores (decoder.go:109).
-__global__ __launch_bounds__(kAttnThreads) void softmax_rows_kernel(float *__restrict__ scores, int n) {
+// softmax of one head's scores (decoder.go:109) and its weighted values
+// (decoder.go:110-118): out[d] = dotF32x4(p, Vt[d]) for d in groups of four
+// (dotF32Go for a last partial group).  Each workgroup serves DG values of
+// d of one head, 16 lanes per d: lane l (l < 8) runs the lane-l chain of the
+// assembly's first accumulator, lane 8+l that of the second, in step order,
+// the values fetched kBatch steps at a time; the tail past n &^ 15 is one
+// lane's dotF32Go.  Every workgroup of a head computes the same softmax into
+// its LDS.  With QOUT (DG == 32) the 32 outputs are rounded to Q8_0.
+template <bool QOUT>
+__global__ __launch_bounds__(512) void cross_values_kernel(const float *__restrict__ scores,
+                                                          const float *__restrict__ cv, int nctx, int hd, int dg,
+                                                          float *__restrict__ att, int8_t *__restrict__ att_q,
+                                                          float *__restrict__ att_s) {
     extern __shared__ float sm[];
-    float *part = sm, *s = sm + 32;
-    float *row = scores + (size_t)blockIdx.x * n;
-    for (int j = threadIdx.x; j < n; j += blockDim.x) s[j] = row[j];
+    float *part = sm, *outv = sm + 32, *s = sm + 64;
+    const int h = blockIdx.x, tid = threadIdx.x;
+    const float *row = scores + (size_t)h * nctx;
+    for (int j = tid; j < nctx; j += blockDim.x) s[j] = row[j];
     __syncthreads();
-    block_softmax(s, n, part);
-    for (int j = threadIdx.x; j < n; j += blockDim.x) row[j] = s[j];
-}
-
-// Weighted values of one head (decoder.go:110-118): out[d] = dotF32x4(p,
-// Vt[d]) for d in groups of four (dotF32Go for a last partial group).
-// A wave serves four values of d: 16 lanes per d, lane l (l < 8) runs the
-// lane-l chain of the first accumulator and lane 8+l that of the second,
-// so the 16 chains of the assembly run side by side; the tail past
-// n &^ 15 is one lane's dotF32Go.
-__global__ __launch_bounds__(64) void cross_values_kernel(const float *__restrict__ p, const float *__restrict__ cv,
-                                                         int nctx, int hd, float *__restrict__ att) {
-    const int h = blockIdx.x, lane = threadIdx.x;
-    const int d = blockIdx.y * 4 + (lane >> 4);
-    const int c = lane & 15;
-    if (d >= hd) return;
-    const float *ph = p + (size_t)h * nctx;
-    const float *vd = cv + ((size_t)h * hd + d) * nctx;
-    if (d >= (hd & ~3)) {  // a last partial group of d: dotF32Go
-        if (c == 0) att[h * hd + d] = dot_go(ph, vd, nctx);
-        return;
+    block_softmax(s, nctx, part);
+    const int dl = tid >> 4, c = tid & 15;
+    const int d = blockIdx.y * dg + dl;
+    if (d < hd) {
+        const float *vd = cv + ((size_t)h * hd + d) * nctx;
+        float o;
+        if (d >= (hd & ~3)) {  // a last partial group of d: dotF32Go
+            o = dot_go(s, vd, nctx);
+        } else {
+            const int kk = nctx & ~15, steps = kk >> 4;
+            float acc = 0.f;
+            for (int t0 = 0; t0 < steps; t0 += kBatchV) {
+                float vv[kBatchV];
+#pragma unroll
+                for (int u = 0; u < kBatchV; ++u) vv[u] = t0 + u < steps ? vd[16 * (t0 + u) + c] : 0.f;
+#pragma unroll
+                for (int u = 0; u < kBatchV; ++u)
+                    if (t0 + u < steps) acc = __fmaf_rn(s[16 * (t0 + u) + c], vv[u], acc);
+            }
+            // S_l = A_l + B_l, then HSUM (kernels_amd64.s:194-202)
+            const float other = __shfl_xor(acc, 8, 16);
+            const float S = __fadd_rn(c < 8 ? acc : other, c < 8 ? other : acc);
+            const float h4 = __fadd_rn(S, __shfl_xor(S, 4, 16));
+            const float h01 = __fadd_rn(h4, __shfl_xor(h4, 1, 16));
+            const float h23 = __shfl_xor(h01, 2, 16);
+            o = kk > 0 ? __fadd_rn(h01, h23) : 0.f;
+            if (c == 0 && kk < nctx) o = __fadd_rn(o, dot_go(s + kk, vd + kk, nctx - kk));
+        }
+        if (c == 0) {
+            att[h * hd + d] = o;
+            if (QOUT) outv[dl] = o;
+        }
     }
-    const int kk = nctx & ~15;
-    float acc = 0.f;
-    for (int i = c; i < kk; i += 16) acc = __fmaf_rn(ph[i], vd[i], acc);
-    // S_l = A_l + B_l, then HSUM
-    const float other = __shfl_xor(acc, 8, 16);
-    const float S = __fadd_rn(c < 8 ? acc : other, c < 8 ? other : acc);
-    const float h4 = __fadd_rn(S, __shfl_xor(S, 4, 16));  // lanes l: S_l + S_{l^4}
-    const float h01 = __fadd_rn(h4, __shfl_xor(h4, 1, 16));
-    const float h23 = __shfl_xor(h01, 2, 16);
-    if (c == 0) {
-        float o = kk > 0 ? __fadd_rn(h01, h23) : 0.f;
-        if (kk < nctx) o = __fadd_rn(o, dot_go(ph + kk, vd + kk, nctx - kk));
-        att[h * hd + d] = o;
+    if constexpr (QOUT) {
+        __syncthreads();
+        if (tid < 32) {
+            const int dd = blockIdx.y * 32 + tid;
+            quant32_store(outv[tid], att_q + h * hd + dd, att_s + (h * hd + dd) / 32, tid);
+        }
     }
-}
-
-// End of a step: the argmax token, its record, the next position.
-__global__ void finish_kernel(const unsigned long long *__restrict__ amax, int *__restrict__ tok,
-                              int *__restrict__ pos, int *__restrict__ hist) {
-    const unsigned long long key = *amax;
-    const int t = (int)(0xffffffffu - (uint32_t)(key & 0xffffffffull));
-    const int p = *pos;
-    *tok = t;
-    hist[p] = t;
-    *pos = p + 1;
 }
 
 // cross K (scaled) [h][t][d] and V [h][d][t] from K, V [t][h*hd+d]
@@ -258,7 +282,10 @@ struct grx_whisper {
     std::vector<void *> allocs;  // every device buffer below
     float *dec_pos = nullptr, *dec_ln_w = nullptr, *dec_ln_b = nullptr;
     float *x = nullptr, *q = nullptr, *att = nullptr, *ff = nullptr, *logits = nullptr, *scores = nullptr;
+    int8_t *att_q = nullptr, *ff_q = nullptr;  // Q8_0 copies for the next product
+    float *att_s = nullptr, *ff_s = nullptr;
     unsigned long long *amax = nullptr;
+    unsigned int *counter = nullptr;
     int *tok = nullptr, *pos = nullptr, *hist = nullptr;
     hipGraph_t graph = nullptr;
     hipGraphExec_t exec = nullptr;
@@ -389,7 +416,14 @@ grx_status finalize(grx_whisper *m) {
     if ((s = dev_alloc_t(m, 4 * (size_t)st, &m->ff)) != GRX_OK) return s;
     if ((s = dev_alloc_t(m, hp.n_vocab, &m->logits)) != GRX_OK) return s;
     if ((s = dev_alloc_t(m, (size_t)hp.n_head * hp.n_audio_ctx, &m->scores)) != GRX_OK) return s;
+    if ((s = dev_alloc_t(m, st, &m->att_q)) != GRX_OK) return s;
+    if ((s = dev_alloc_t(m, st / 32, &m->att_s)) != GRX_OK) return s;
+    if ((s = dev_alloc_t(m, 4 * (size_t)st, &m->ff_q)) != GRX_OK) return s;
+    if ((s = dev_alloc_t(m, 4 * (size_t)st / 32, &m->ff_s)) != GRX_OK) return s;
+    if ((s = dev_alloc_t(m, 1, &m->counter)) != GRX_OK) return s;
+    GRX_HIP(hipMemset(m->counter, 0, 4));
     if ((s = dev_alloc_t(m, 1, &m->amax)) != GRX_OK) return s;
+    GRX_HIP(hipMemset(m->amax, 0, 8));
     if ((s = dev_alloc_t(m, 1, &m->tok)) != GRX_OK) return s;
     if ((s = dev_alloc_t(m, 1, &m->pos)) != GRX_OK) return s;
     if ((s = dev_alloc_t(m, hp.n_text_ctx, &m->hist)) != GRX_OK) return s;
@@ -401,12 +435,15 @@ grx_status finalize(grx_whisper *m) {
     return GRX_OK;
 }
 
+// The decode step's products read their weights with ordinary loads: the
+// step's 52 MB of weights stay in the 256 MB Infinity Cache from token to token.
 GemvArgs gemv_args(const grx_weight *w) {
     GemvArgs a = {};
     a.qs = w->qs;
     a.ds = w->ds;
     a.rows = w->rows;
     a.nb = w->nb;
+    a.cacheable = 1;
     return a;
 }
 
@@ -415,14 +452,13 @@ grx_status enqueue_step(grx_whisper *m, hipStream_t stream) {
     const grx_whisper_hparams &hp = m->hp;
     const int st = hp.n_state, nh = hp.n_head, hd = st / nh, nctx = hp.n_audio_ctx;
     const float sc = (float)(1.0 / sqrt((double)hd));
+    const bool qatt = hd % 32 == 0;  // attention outputs are whole Q8_0 blocks per head
     grx_status s;
-    embed_kernel<<<1, 256, 0, stream>>>(m->tok_emb->qs, m->tok_emb->ds, m->tok_emb->nb, m->dec_pos, m->tok, m->pos,
-                                        st, m->x, m->amax);
-    GRX_LAUNCHED("embed_kernel");
-    const size_t attn_smem = (32 + (size_t)hp.n_text_ctx) * 4, soft_smem = (32 + (size_t)nctx) * 4;
+    const size_t attn_smem = (32 + (size_t)hp.n_text_ctx) * 4, val_smem = (64 + (size_t)nctx) * 4;
+    const int dg = qatt ? 32 : 4;
     for (int li = 0; li < hp.n_layer; ++li) {
         WLayer &L = m->L[li];
-        {  // LN -> q | k | v, k and v into the cache at pos
+        {  // LN -> q | k | v, k and v into the cache at pos; layer 0 embeds first
             GemvArgs a = gemv_args(L.qkv);
             a.x = m->x;
             a.lda = st;
@@ -435,21 +471,38 @@ grx_status enqueue_step(grx_whisper *m, hipStream_t stream) {
             a.kc = L.self_k;
             a.vc = L.self_v;
             a.pos = m->pos;
-            if ((s = grx_gemv_launch(stream, 1, GRX_PRO_LN, GRX_EPI_QKV, a, 0)) != GRX_OK) return s;
+            int pro = GRX_PRO_LN;
+            if (li == 0) {
+                pro = GRX_PRO_EMBED_LN;
+                a.tok = m->tok;
+                a.emb_qs = m->tok_emb->qs;
+                a.emb_ds = m->tok_emb->ds;
+                a.pos_emb = m->dec_pos;
+                a.x_out = m->x;
+            }
+            if ((s = grx_gemv_launch(stream, 1, pro, GRX_EPI_QKV, a, 0)) != GRX_OK) return s;
         }
-        self_attn_kernel<<<nh, kAttnThreads, attn_smem, stream>>>(m->q, L.self_k, L.self_v, m->pos, st, hd, sc, m->att);
+        if (qatt)
+            self_attn_kernel<true><<<nh, kAttnThreads, attn_smem, stream>>>(m->q, L.self_k, L.self_v, m->pos, st, hd,
+                                                                           sc, m->att, m->att_q, m->att_s);
+        else
+            self_attn_kernel<false><<<nh, kAttnThreads, attn_smem, stream>>>(m->q, L.self_k, L.self_v, m->pos, st, hd,
+                                                                            sc, m->att, nullptr, nullptr);
         GRX_LAUNCHED("self_attn_kernel");
-        {  // x += att . Wo^T + b
-            GemvArgs a = gemv_args(L.o);
+        auto out_proj = [&](grx_weight *w, const float *b) {  // x += att . W^T + b
+            GemvArgs a = gemv_args(w);
             a.x = m->att;
             a.lda = st;
+            a.xq = m->att_q;
+            a.xs = m->att_s;
             a.y = m->x;
             a.ldc = st;
-            a.bias = L.o_b;
+            a.bias = b;
             a.resid = m->x;
             a.ldr = st;
-            if ((s = grx_gemv_launch(stream, 1, GRX_PRO_QUANT, GRX_EPI_RESID, a, 0)) != GRX_OK) return s;
-        }
+            return grx_gemv_launch(stream, 1, qatt ? GRX_PRO_PREQ : GRX_PRO_QUANT, GRX_EPI_RESID, a, 0);
+        };
+        if ((s = out_proj(L.o, L.o_b)) != GRX_OK) return s;
         {  // LN -> cross query
             GemvArgs a = gemv_args(L.xq);
             a.x = m->x;
@@ -464,22 +517,15 @@ grx_status enqueue_step(grx_whisper *m, hipStream_t stream) {
         cross_scores_kernel<<<dim3(nh, grx_ceil_div(nctx, kAttnThreads)), kAttnThreads, 0, stream>>>(
             m->q, L.cross_k, nctx, hd, m->scores);
         GRX_LAUNCHED("cross_scores_kernel");
-        softmax_rows_kernel<<<nh, kAttnThreads, soft_smem, stream>>>(m->scores, nctx);
-        GRX_LAUNCHED("softmax_rows_kernel");
-        cross_values_kernel<<<dim3(nh, grx_ceil_div(hd, 4)), 64, 0, stream>>>(m->scores, L.cross_v, nctx, hd, m->att);
+        if (qatt)
+            cross_values_kernel<true><<<dim3(nh, grx_ceil_div(hd, dg)), dg * 16, val_smem, stream>>>(
+                m->scores, L.cross_v, nctx, hd, dg, m->att, m->att_q, m->att_s);
+        else
+            cross_values_kernel<false><<<dim3(nh, grx_ceil_div(hd, dg)), dg * 16, val_smem, stream>>>(
+                m->scores, L.cross_v, nctx, hd, dg, m->att, nullptr, nullptr);
         GRX_LAUNCHED("cross_values_kernel");
-        {  // x += att . Wxo^T + b
-            GemvArgs a = gemv_args(L.xo);
-            a.x = m->att;
-            a.lda = st;
-            a.y = m->x;
-            a.ldc = st;
-            a.bias = L.xo_b;
-            a.resid = m->x;
-            a.ldr = st;
-            if ((s = grx_gemv_launch(stream, 1, GRX_PRO_QUANT, GRX_EPI_RESID, a, 0)) != GRX_OK) return s;
-        }
-        {  // LN -> fc1 -> GELU
+        if ((s = out_proj(L.xo, L.xo_b)) != GRX_OK) return s;
+        {  // LN -> fc1 -> GELU, rounded to Q8_0 for fc2
             GemvArgs a = gemv_args(L.fc1);
             a.x = m->x;
             a.lda = st;
@@ -488,22 +534,25 @@ grx_status enqueue_step(grx_whisper *m, hipStream_t stream) {
             a.y = m->ff;
             a.ldc = 4 * st;
             a.bias = L.fc1_b;
-            if ((s = grx_gemv_launch(stream, 1, GRX_PRO_LN, GRX_EPI_GELU, a, 0)) != GRX_OK) return s;
+            a.yq = m->ff_q;
+            a.ys = m->ff_s;
+            if ((s = grx_gemv_launch(stream, 1, GRX_PRO_LN, GRX_EPI_GELU_Q, a, 0)) != GRX_OK) return s;
         }
         {  // x += ff . Wfc2^T + b
             GemvArgs a = gemv_args(L.fc2);
-            a.x = m->ff;
-            a.lda = 4 * st;
+            a.xq = m->ff_q;
+            a.xs = m->ff_s;
             a.y = m->x;
             a.ldc = st;
             a.bias = L.fc2_b;
             a.resid = m->x;
             a.ldr = st;
-            if ((s = grx_gemv_launch(stream, 1, GRX_PRO_QUANT, GRX_EPI_RESID, a, 0)) != GRX_OK) return s;
+            if ((s = grx_gemv_launch(stream, 1, GRX_PRO_PREQ, GRX_EPI_RESID, a, 0)) != GRX_OK) return s;
         }
     }
-    {  // LN -> logits = tokEmb . h -> argmax
+    {  // LN -> logits = tokEmb . h -> argmax; the last workgroup ends the step
         GemvArgs a = gemv_args(m->tok_emb);
+        a.cacheable = 0;  // 26.5 MB streamed once per step: non-temporal loads
         a.x = m->x;
         a.lda = st;
         a.ln_w = m->dec_ln_w;
@@ -511,10 +560,13 @@ grx_status enqueue_step(grx_whisper *m, hipStream_t stream) {
         a.y = m->logits;
         a.ldc = hp.n_vocab;
         a.amax = m->amax;
+        a.counter = m->counter;
+        a.tok_w = m->tok;
+        a.pos = m->pos;
+        a.pos_w = m->pos;
+        a.hist = m->hist;
         if ((s = grx_gemv_launch(stream, 1, GRX_PRO_LN, GRX_EPI_ARGMAX, a, 0)) != GRX_OK) return s;
     }
-    finish_kernel<<<1, 1, 0, stream>>>(m->amax, m->tok, m->pos, m->hist);
-    GRX_LAUNCHED("finish_kernel");
     return GRX_OK;
 }
 
