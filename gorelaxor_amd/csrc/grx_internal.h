@@ -252,4 +252,10 @@ struct GemvArgs {
 
 grx_status grx_gemv_launch(hipStream_t st, int m, int pro, int epi, const GemvArgs &a,
                            int waves_hint);
+// The many-row product on the matrix cores (q8_gemm.hip), same results.
+grx_status grx_gemm_q8_launch(hipStream_t st, const grx_weight *w, const int8_t *xq, const float *xs, int m,
+                              const float *bias, float *y, int ldc);
+// Fewest activation rows that take the matrix-core product (GRX_GEMM_MIN_M
+// overrides it, for tests).
+int grx_gemm_min_m(void);
 int grx_gemv_pick_waves(int tiles, int nb, int m);

@@ -495,10 +495,19 @@ static grx_status check_mm(const char *fn, grx_ctx *ctx, const void *dst, int ld
     return GRX_OK;
 }
 
-// Rows of activations in launches of 8, 4, 2 and 1.
+int grx_gemm_min_m(void) {
+    if (const char *f = getenv("GRX_GEMM_MIN_M")) {
+        const int v = atoi(f);
+        if (v > 0) return v;
+    }
+    return 16;
+}
+
+// Many rows on the matrix cores; few rows in GEMV launches of 8, 4, 2 and 1.
 static grx_status gemv_rows_preq(hipStream_t st, float *dst, int ldc, const int8_t *q, const float *sc,
                                  int m, const grx_weight *w, const float *bias) {
     const int K = w->cols, nb = w->nb;
+    if (m >= grx_gemm_min_m() && nb > 0) return grx_gemm_q8_launch(st, w, q, sc, m, bias, dst, ldc);
     int i = 0;
     while (i < m) {
         const int left = m - i;

@@ -156,6 +156,29 @@ def test_matmul_every_wave_split(kern, orc, waves):
         del os.environ["GRX_GEMV_WAVES"]
 
 
+def test_matmul_matrix_cores_all_small_sizes(kern, orc):
+    """The matrix-core product forced for every m (GRX_GEMM_MIN_M=1): the
+    odd sizes again, bit-identical to the oracle."""
+    rng = np.random.default_rng(41)
+    os.environ["GRX_GEMM_MIN_M"] = "1"
+    try:
+        for m in (1, 2, 7, 15, 16, 17, 63, 64, 65):
+            for n in (1, 17, 64, 65, 129):
+                for k in (32, 96, 544):
+                    _check_matmul(kern, orc, rng, m, n, k, bias=(n % 2 == 1))
+    finally:
+        del os.environ["GRX_GEMM_MIN_M"]
+
+
+@pytest.mark.parametrize("m,n,k", [(126, 4096, 1024), (300, 1024, 1024), (1500, 512, 512), (251, 1024, 1024),
+                                   (16, 4096, 1024)])
+def test_matmul_many_rows_bit_exact(kern, orc, m, n, k):
+    """Encoder, prefill and cross-attention shapes (M >= 16: matrix cores),
+    and the reference benchmark's 300 x 1024 x 1024 (bench_test.go:35-55)."""
+    rng = np.random.default_rng(m * 7 + n)
+    _check_matmul(kern, orc, rng, m, n, k, lda_pad=0, ldc_pad=0)
+
+
 def test_gemv_single_1024(kern, orc):
     """The single Q8_0 GEMV workload: N = K = 1024, int8 U[-127,127], f16
     scales |N(0,0.02)|/127 (~30% subnormal), x ~ N(0,1): bit-exact."""
