@@ -80,3 +80,44 @@ def encoder_output(hp: dict, seed: int = 11) -> np.ndarray:
     """Cross-attention input: n_audio_ctx x n_state float32 ~ N(0, 1)."""
     rng = np.random.default_rng(seed)
     return rng.standard_normal(hp["n_audio_ctx"] * hp["n_state"]).astype(np.float32)
+
+
+POCKET_TTS_LM = dict(d=1024, heads=16, ff=4096, n_layer=6, ldim=32, max_pos=320, period=1e4)
+POCKET_TTS_TINY = dict(d=128, heads=2, ff=512, n_layer=2, ldim=32, max_pos=96, period=1e4)
+
+
+def pocket_model(hp: dict, seed: int = 5) -> dict:
+    """Random-init flow-LM transformer tensors, named as pockettts/model.go
+    reads them: transformer matrices Q8_0, the rest float32."""
+    rng = np.random.default_rng(seed)
+    d, ff, ld = hp["d"], hp["ff"], hp["ldim"]
+    t = {}
+
+    def vec(n, scale=0.02, base=0.0):
+        return (base + scale * rng.standard_normal(n)).astype(np.float32)
+
+    for i in range(hp["n_layer"]):
+        p = f"lm.blk.{i}."
+        for n in ("norm1", "norm2"):
+            t[p + n + ".weight"] = vec(d, 0.1, 1.0)
+            t[p + n + ".bias"] = vec(d, 0.1)
+        t[p + "attn_qkv.weight"] = q8_weight(rng, 3 * d, d, sigma=0.1)
+        t[p + "attn_out.weight"] = q8_weight(rng, d, d, sigma=0.1)
+        t[p + "ff1.weight"] = q8_weight(rng, ff, d, sigma=0.1)
+        t[p + "ff2.weight"] = q8_weight(rng, d, ff, sigma=0.05)
+    t["lm.input.weight"] = vec(d * ld, 0.2)
+    t["lm.bos"] = vec(ld, 1.0)
+    t["lm.out_norm.weight"] = vec(d, 0.1, 1.0)
+    t["lm.out_norm.bias"] = vec(d, 0.1)
+    t["lm.eos.weight"] = vec(d, 0.05)
+    t["lm.eos.bias"] = vec(1, 0.1)
+    return t
+
+
+def pocket_inputs(hp: dict, frames: int, prefix: int = 64, seed: int = 6):
+    """The text prefix (prefix x d random embedding rows) and teacher-forced
+    latents (frames x ldim, N(0,1)), seeded."""
+    rng = np.random.default_rng(seed)
+    x = rng.standard_normal((prefix, hp["d"])).astype(np.float32)
+    lat = rng.standard_normal((frames, hp["ldim"])).astype(np.float32)
+    return x, lat

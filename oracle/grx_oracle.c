@@ -772,3 +772,199 @@ void orc_whisper_greedy(orc_whisper *m, const int *prompt, int n_prompt, int n_s
     }
     free(lg);
 }
+
+/* ------------------------------------------------------------------ */
+/* float route of ws.matmul (gemm.go:116-259) with float32 B           */
+/* ------------------------------------------------------------------ */
+
+/* k6x16avx (kernels_amd64.s:5-88) for one output: acc = fma(a_k, b_k, acc)
+ * over k in order, then added to C (VADDPS). */
+static float k6x16_one(const float *a, const float *b, int ldb_col_stride, int k) {
+    float acc = 0.0f;
+    for (int kk = 0; kk < k; kk++) acc = fmaf(a[kk], b[(size_t)kk * ldb_col_stride], acc);
+    return acc;
+}
+
+/* gemvRows (gemm.go:195-259) for one row of A against float32 rows of B:
+ * dotF32x4 for whole groups of four columns, dotF32Go for the rest, bias
+ * added afterwards. */
+static void gemv_f32_row(float *y, const float *x, const float *b, int ldb, int n, int k, const float *bias) {
+    for (int j = 0; j < n; j += 4) {
+        if (j + 4 <= n) {
+            float out[4];
+            orc_dot_f32_x4(x, b + (size_t)j * ldb, ldb, k, out);
+            for (int r = 0; r < 4; r++) y[j + r] = out[r];
+        } else {
+            for (int jj = j; jj < n; jj++) y[jj] = orc_dot_f32_go(x, b + (size_t)jj * ldb, k);
+        }
+        if (bias)
+            for (int jj = j; jj < j + 4 && jj < n; jj++) y[jj] = y[jj] + bias[jj];
+    }
+}
+
+/* ws.matmul with float32 B (MatMulF32, kern.go:205-212, and Linear of an F32
+ * weight): C[m][n] = A[m][k] . B[n][k]^T + bias.  m <= 16: gemvRows.  m > 16:
+ * the rows in whole groups of six take k6x16avx over k in chunks of 256 from
+ * C = bias (or 0) (gemm.go:121-180); the last m % 6 rows take gemv. */
+void orc_matmul_f32(float *c, int ldc, const float *a, int lda, const float *b, int ldb, int m, int n,
+                    int k, const float *bias) {
+    if (m == 0 || n == 0) return;
+    if (m <= 16) {
+        for (int i = 0; i < m; i++) gemv_f32_row(c + (size_t)i * ldc, a + (size_t)i * lda, b, ldb, n, k, bias);
+        return;
+    }
+    int mfull = m / 6 * 6;
+    /* the packed panel holds B's column j as [kk][j]; element (kk, j) is b[j*ldb + kk] */
+    for (int i = 0; i < mfull; i++) {
+        float *ci = c + (size_t)i * ldc;
+        for (int j = 0; j < n; j++) ci[j] = bias ? bias[j] : 0.0f;
+        for (int k0 = 0; k0 < k; k0 += 256) {
+            int kn = k - k0 < 256 ? k - k0 : 256;
+            for (int j = 0; j < n; j++) {
+                float acc = k6x16_one(a + (size_t)i * lda + k0, b + (size_t)j * ldb + k0, 1, kn);
+                ci[j] = acc + ci[j];
+            }
+        }
+    }
+    for (int i = mfull; i < m; i++) gemv_f32_row(c + (size_t)i * ldc, a + (size_t)i * lda, b, ldb, n, k, bias);
+}
+
+/* ------------------------------------------------------------------ */
+/* pocket-TTS flow-LM transformer                                      */
+/* ------------------------------------------------------------------ */
+
+/* pockettts/nn.go:69-76 (ropeFreqs): f_i = f32(exp(f32(i) * c)),
+ * c = f32(-ln(period) * 2 / head_dim). */
+void orc_rope_freqs(float *f, int head_dim, double period) {
+    float c = (float)(-log(period) * 2.0 / (double)head_dim);
+    for (int i = 0; i < head_dim / 2; i++) {
+        float t = (float)i * c;
+        f[i] = (float)exp((double)t);
+    }
+}
+
+/* pockettts/nn.go:80-93 (applyRope): pair i of every head rotated by the
+ * angle f64(f_i * pos) with f32(cos), f32(sin), unfused. */
+void orc_apply_rope(float *x, int heads, const float *freqs, int half, int pos) {
+    int hd = half * 2;
+    float p = (float)pos;
+    for (int i = 0; i < half; i++) {
+        float fp = freqs[i] * p;
+        double a = (double)fp;
+        float c = (float)cos(a), s = (float)sin(a);
+        for (int h = 0; h < heads; h++) {
+            int j = h * hd + 2 * i;
+            float r = x[j], im = x[j + 1];
+            float rc = r * c, is = im * s, rs = r * s, ic = im * c;
+            x[j] = rc - is;
+            x[j + 1] = rs + ic;
+        }
+    }
+}
+
+/* pockettts/nn.go:200-254 (attend) with no context limit: per head, the
+ * scores of the T queries against every cached key (MatMulF32), scaled,
+ * softmax over the causal range (ExpSub, Scale), the rest cleared; then for
+ * T < 4 the values summed by AddScaled in key order (zero weights skipped),
+ * else MatMulF32 against the transposed values. */
+static void ptts_attend(orc_ptts *m, float *out, const float *qkv, int T, const orc_ptts_layer *L, int pos0) {
+    int d = m->d, hd = d / m->heads;
+    float scale = (float)(1.0 / sqrt((double)hd));
+    int nk = pos0 + T;
+    float *sc = (float *)malloc((size_t)T * nk * sizeof(float));
+    float *vt = (float *)malloc((size_t)hd * nk * sizeof(float));
+    for (int h = 0; h < m->heads; h++) {
+        orc_matmul_f32(sc, nk, qkv + h * hd, 3 * d, L->k + h * hd, d, T, nk, hd, NULL);
+        for (int r = 0; r < T; r++) {
+            int p = pos0 + r;
+            float *row = sc + (size_t)r * nk;
+            float mx = -INFINITY;
+            for (int j = 0; j <= p; j++) {
+                row[j] = row[j] * scale;
+                mx = row[j] > mx ? row[j] : mx;
+            }
+            float sum = orc_expsub(row, p + 1, mx);
+            float inv = 1.0f / sum;
+            for (int j = 0; j <= p; j++) row[j] = row[j] * inv;
+            for (int j = p + 1; j < nk; j++) row[j] = 0;
+        }
+        if (T < 4) {
+            for (int r = 0; r < T; r++) {
+                float *o = out + (size_t)r * d + h * hd;
+                for (int e = 0; e < hd; e++) o[e] = 0;
+                const float *row = sc + (size_t)r * nk;
+                for (int j = 0; j < nk; j++)
+                    if (row[j] != 0) orc_axpy(o, L->v + (size_t)j * d + h * hd, hd, row[j]);
+            }
+            continue;
+        }
+        for (int j = 0; j < nk; j++)
+            for (int e = 0; e < hd; e++) vt[(size_t)e * nk + j] = L->v[(size_t)j * d + h * hd + e];
+        orc_matmul_f32(out + h * hd, d, sc, nk, vt, nk, T, hd, nk, NULL);
+    }
+    free(sc);
+    free(vt);
+}
+
+/* pockettts/nn.go:142-182 (transformer.forward), no context limit and no
+ * layer scales (the flow LM's): T rows of x in place after m->pos. */
+int orc_ptts_forward(orc_ptts *m, float *x, int T) {
+    int d = m->d, ff = m->ff, hd = d / m->heads;
+    if (m->pos + T > m->max_pos) return -1;
+    float *h = (float *)malloc((size_t)T * d * sizeof(float));
+    float *qkv = (float *)malloc((size_t)T * 3 * d * sizeof(float));
+    float *att = (float *)malloc((size_t)T * d * sizeof(float));
+    float *f = (float *)malloc((size_t)T * ff * sizeof(float));
+    for (int li = 0; li < m->n_layer; li++) {
+        orc_ptts_layer *L = &m->layers[li];
+        orc_layernorm_f64(h, x, T, d, L->norm1_w, L->norm1_b, 1e-5);
+        orc_matmul_q8_int(qkv, 3 * d, h, d, T, L->qkv, 3 * d, d, NULL, 1);
+        for (int r = 0; r < T; r++) {
+            float *row = qkv + (size_t)r * 3 * d;
+            orc_apply_rope(row, m->heads, m->freqs, hd / 2, m->pos + r);
+            orc_apply_rope(row + d, m->heads, m->freqs, hd / 2, m->pos + r);
+        }
+        for (int r = 0; r < T; r++) {
+            memcpy(L->k + (size_t)(m->pos + r) * d, qkv + (size_t)r * 3 * d + d, (size_t)d * sizeof(float));
+            memcpy(L->v + (size_t)(m->pos + r) * d, qkv + (size_t)r * 3 * d + 2 * d, (size_t)d * sizeof(float));
+        }
+        ptts_attend(m, att, qkv, T, L, m->pos);
+        orc_matmul_q8_int(h, d, att, d, T, L->out, d, d, NULL, 1);
+        add_to(x, h, T * d);
+        orc_layernorm_f64(h, x, T, d, L->norm2_w, L->norm2_b, 1e-5);
+        orc_matmul_q8_int(f, ff, h, d, T, L->ff1, ff, d, NULL, 1);
+        orc_gelu_vec(f, T * ff);
+        orc_matmul_q8_int(h, d, f, ff, T, L->ff2, d, ff, NULL, 1);
+        add_to(x, h, T * d);
+    }
+    m->pos += T;
+    free(h);
+    free(qkv);
+    free(att);
+    free(f);
+    return 0;
+}
+
+/* pockettts/lm.go:164-170 (flowLM.run): forward, then out_norm of the last
+ * row (float64 LayerNorm, eps 1e-5). */
+int orc_ptts_run(orc_ptts *m, float *x, int T, float *out) {
+    if (orc_ptts_forward(m, x, T) != 0) return -1;
+    orc_layernorm_f64(out, x + (size_t)(T - 1) * m->d, 1, m->d, m->out_w, m->out_b, 1e-5);
+    return 0;
+}
+
+/* pockettts/lm.go:185-195 (flowLM.step): x = input . latent (bos when
+ * latent is NULL; an F32 weight on the float route), run, and the
+ * end-of-speech logit eos . out + b (a one-row F32 product: dotF32Go). */
+int orc_ptts_step(orc_ptts *m, const float *latent, float *out, float *eos) {
+    float *x = (float *)malloc((size_t)m->d * sizeof(float));
+    orc_matmul_f32(x, m->d, latent ? latent : m->bos, m->ldim, m->input, m->ldim, 1, m->d, m->ldim, NULL);
+    int rc = orc_ptts_run(m, x, 1, out);
+    if (rc == 0) {
+        float e;
+        orc_matmul_f32(&e, 1, out, m->d, m->eos_w, m->d, 1, 1, m->d, NULL);
+        *eos = e + m->eos_b;
+    }
+    free(x);
+    return rc;
+}

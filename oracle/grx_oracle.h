@@ -97,6 +97,36 @@ int orc_whisper_decode(orc_whisper *m, const int *tokens, int nt, float *logits)
 void orc_whisper_greedy(orc_whisper *m, const int *prompt, int n_prompt, int n_steps,
                         int *out_tokens);
 
+/* ---- float products of the reference's float route (gemm.go) ---- */
+void orc_matmul_f32(float *c, int ldc, const float *a, int lda, const float *b, int ldb, int m, int n,
+                    int k, const float *bias);
+
+/* ---- pocket-TTS flow-LM transformer (pockettts/nn.go, lm.go) ---- */
+void orc_rope_freqs(float *f, int head_dim, double period);
+void orc_apply_rope(float *x, int heads, const float *freqs, int half, int pos);
+
+typedef struct {
+    const float *norm1_w, *norm1_b, *norm2_w, *norm2_b;
+    const uint8_t *qkv, *out, *ff1, *ff2; /* Q8_0 rows: [3d][d], [d][d], [ff][d], [d][ff] */
+    float *k, *v;                         /* caches [max_pos][d] */
+} orc_ptts_layer;
+
+typedef struct {
+    int d, heads, ff, n_layer, max_pos, ldim;
+    const float *freqs;   /* head_dim/2 rotary frequencies */
+    orc_ptts_layer *layers;
+    const float *input;   /* [d][ldim] float32 */
+    const float *bos;     /* [ldim] */
+    const float *out_w, *out_b;
+    const float *eos_w;   /* [d] float32 */
+    float eos_b;
+    int pos;
+} orc_ptts;
+
+int orc_ptts_forward(orc_ptts *m, float *x, int T);
+int orc_ptts_run(orc_ptts *m, float *x, int T, float *out);
+int orc_ptts_step(orc_ptts *m, const float *latent, float *out, float *eos);
+
 #ifdef __cplusplus
 }
 #endif

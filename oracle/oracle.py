@@ -85,6 +85,16 @@ def _declare(L):
     L.orc_whisper_decode.argtypes = [C.c_void_p, _i32p, C.c_int, C.c_void_p]
     L.orc_whisper_decode.restype = C.c_int
     L.orc_whisper_greedy.argtypes = [C.c_void_p, _i32p, C.c_int, C.c_int, _i32p]
+    L.orc_matmul_f32.argtypes = [_f32p, C.c_int, _f32p, C.c_int, _f32p, C.c_int, C.c_int, C.c_int, C.c_int,
+                                 C.c_void_p]
+    L.orc_rope_freqs.argtypes = [_f32p, C.c_int, C.c_double]
+    L.orc_apply_rope.argtypes = [_f32p, C.c_int, _f32p, C.c_int, C.c_int]
+    L.orc_ptts_forward.argtypes = [C.c_void_p, _f32p, C.c_int]
+    L.orc_ptts_forward.restype = C.c_int
+    L.orc_ptts_run.argtypes = [C.c_void_p, _f32p, C.c_int, _f32p]
+    L.orc_ptts_run.restype = C.c_int
+    L.orc_ptts_step.argtypes = [C.c_void_p, C.c_void_p, _f32p, _f32p]
+    L.orc_ptts_step.restype = C.c_int
 
 
 def _f32(a):
@@ -368,3 +378,112 @@ class WhisperOracle:
         out = np.zeros(n_steps + 1, np.int32)
         lib().orc_whisper_greedy(C.byref(self._m), p, p.size, n_steps, out)
         return out
+
+
+# ---- float route products (gemm.go:116-259) ----
+
+def matmul_f32(a: np.ndarray, b: np.ndarray, bias=None) -> np.ndarray:
+    """ws.matmul with float32 B: a [m][k] . b [n][k]^T (+ bias)."""
+    a = _f32(a)
+    b = _f32(b)
+    m, k = a.shape
+    n = b.shape[0]
+    c = np.zeros((m, n), np.float32)
+    bb = None if bias is None else _f32(bias)
+    lib().orc_matmul_f32(c, n, a, k, b, k, m, n, k, _ptr(bb))
+    return c
+
+
+# ---- pocket-TTS flow-LM transformer (pockettts/nn.go, lm.go) ----
+
+def rope_freqs(head_dim: int, period: float = 1e4) -> np.ndarray:
+    f = np.zeros(head_dim // 2, np.float32)
+    lib().orc_rope_freqs(f, head_dim, period)
+    return f
+
+
+def apply_rope(x: np.ndarray, heads: int, freqs: np.ndarray, pos: int) -> np.ndarray:
+    x = _f32(x).copy()
+    lib().orc_apply_rope(x, heads, _f32(freqs), freqs.size, pos)
+    return x
+
+
+class _PLayer(C.Structure):
+    _fields_ = [(n, C.c_void_p) for n in ("norm1_w", "norm1_b", "norm2_w", "norm2_b", "qkv", "out", "ff1", "ff2",
+                                          "k", "v")]
+
+
+class _PModel(C.Structure):
+    _fields_ = [("d", C.c_int), ("heads", C.c_int), ("ff", C.c_int), ("n_layer", C.c_int), ("max_pos", C.c_int),
+                ("ldim", C.c_int), ("freqs", C.c_void_p), ("layers", C.c_void_p), ("input", C.c_void_p),
+                ("bos", C.c_void_p), ("out_w", C.c_void_p), ("out_b", C.c_void_p), ("eos_w", C.c_void_p),
+                ("eos_b", C.c_float), ("pos", C.c_int)]
+
+
+class PocketOracle:
+    """Oracle flow-LM transformer over tensors named as pockettts/model.go
+    reads them ("lm.blk.{i}.attn_qkv.weight", "lm.input.weight", ...)."""
+
+    def __init__(self, hp: dict, tensors: dict):
+        self.hp = hp
+        d, nl, mp = hp["d"], hp["n_layer"], hp["max_pos"]
+        self._keep = []
+
+        def keep(a):
+            a = np.ascontiguousarray(a)
+            self._keep.append(a)
+            return a.ctypes.data
+
+        layers = (_PLayer * nl)()
+        self.k, self.v = [], []
+        for i in range(nl):
+            p = f"lm.blk.{i}."
+            for f, n in (("norm1_w", "norm1.weight"), ("norm1_b", "norm1.bias"), ("norm2_w", "norm2.weight"),
+                         ("norm2_b", "norm2.bias"), ("qkv", "attn_qkv.weight"), ("out", "attn_out.weight"),
+                         ("ff1", "ff1.weight"), ("ff2", "ff2.weight")):
+                setattr(layers[i], f, keep(tensors[p + n]))
+            kc = np.zeros(mp * d, np.float32)
+            vc = np.zeros(mp * d, np.float32)
+            self.k.append(kc)
+            self.v.append(vc)
+            layers[i].k = keep(kc)
+            layers[i].v = keep(vc)
+        self._layers = layers
+        self.freqs = rope_freqs(d // hp["heads"], hp.get("period", 1e4))
+        m = _PModel()
+        m.d, m.heads, m.ff, m.n_layer, m.max_pos, m.ldim = d, hp["heads"], hp["ff"], nl, mp, hp["ldim"]
+        m.freqs = keep(self.freqs)
+        m.layers = C.cast(layers, C.c_void_p)
+        m.input = keep(tensors["lm.input.weight"])
+        m.bos = keep(tensors["lm.bos"])
+        m.out_w = keep(tensors["lm.out_norm.weight"])
+        m.out_b = keep(tensors["lm.out_norm.bias"])
+        m.eos_w = keep(tensors["lm.eos.weight"])
+        m.eos_b = float(tensors["lm.eos.bias"][0])
+        m.pos = 0
+        self._m = m
+
+    @property
+    def pos(self) -> int:
+        return self._m.pos
+
+    def reset(self):
+        self._m.pos = 0
+
+    def run(self, x: np.ndarray) -> np.ndarray:
+        """flowLM.run of T rows (the text prefix): out_norm of the last row."""
+        x = _f32(x).copy()
+        T = x.size // self.hp["d"]
+        out = np.zeros(self.hp["d"], np.float32)
+        if lib().orc_ptts_run(C.byref(self._m), x, T, out) != 0:
+            raise ValueError("rows do not fit the context")
+        return out
+
+    def step(self, latent=None):
+        """flowLM.step: (out_norm output, end-of-speech logit)."""
+        out = np.zeros(self.hp["d"], np.float32)
+        eos = np.zeros(1, np.float32)
+        lat = None if latent is None else _f32(latent)
+        if lib().orc_ptts_step(C.byref(self._m), _ptr(lat), out, eos) != 0:
+            raise ValueError("the step does not fit the context")
+        return out, float(eos[0])
