@@ -64,7 +64,19 @@ SIGNATURES = {
     "grx_whisper_pos": (i32, [vp]),
     "grx_whisper_decode": (i32, [vp, vp, i32, vp, vp]),
     "grx_whisper_greedy": (i32, [vp, vp, i32, i32, vp]),
+    "grx_pocket_create": (i32, [vp, vp, C.POINTER(vp)]),
+    "grx_pocket_destroy": (i32, [vp]),
+    "grx_pocket_set_tensor": (i32, [vp, C.c_char_p, vp, sz]),
+    "grx_pocket_reset": (i32, [vp]),
+    "grx_pocket_pos": (i32, [vp]),
+    "grx_pocket_run": (i32, [vp, vp, i32, vp]),
+    "grx_pocket_frames": (i32, [vp, vp, i32, vp, vp]),
 }
+
+
+class PocketHParams(C.Structure):
+    """grx_pocket_hparams."""
+    _fields_ = [(n, C.c_int) for n in ("d", "heads", "ff", "n_layer", "max_pos", "ldim")] + [("period", C.c_double)]
 
 
 class WhisperHParams(C.Structure):

@@ -1,0 +1,137 @@
+// grx_float.h - the reference's float-kernel orders as device functions.
+//
+// Each function restates one float kernel of github.com/xattribution/gorelaxor
+// (cited file:line) in its exact order of operations, so that the decoder
+// kernels built from them give bit-identical results to the CPU oracle.
+#pragma once
+
+#include "grx_internal.h"
+
+// dotF32Go (internal/kern/gemm.go:294-308): four running sums, unfused.
+__device__ __forceinline__ float dot_go(const float *x, const float *y, int n) {
+    float s0 = 0.f, s1 = 0.f, s2 = 0.f, s3 = 0.f;
+    int i = 0;
+    for (; i + 4 <= n; i += 4) {
+        s0 = __fadd_rn(s0, __fmul_rn(x[i], y[i]));
+        s1 = __fadd_rn(s1, __fmul_rn(x[i + 1], y[i + 1]));
+        s2 = __fadd_rn(s2, __fmul_rn(x[i + 2], y[i + 2]));
+        s3 = __fadd_rn(s3, __fmul_rn(x[i + 3], y[i + 3]));
+    }
+    for (; i < n; i++) s0 = __fadd_rn(s0, __fmul_rn(x[i], y[i]));
+    return __fadd_rn(__fadd_rn(__fadd_rn(s0, s1), s2), s3);
+}
+
+// HSUM of kernels_amd64.s:90-95 over eight lane values.
+__device__ __forceinline__ float hsum8(const float *a) {
+    const float h0 = __fadd_rn(a[0], a[4]), h1 = __fadd_rn(a[1], a[5]);
+    const float h2 = __fadd_rn(a[2], a[6]), h3 = __fadd_rn(a[3], a[7]);
+    return __fadd_rn(__fadd_rn(h0, h1), __fadd_rn(h2, h3));
+}
+
+// One row of dot4f32avx (kernels_amd64.s:156-204), kk % 16 == 0.
+__device__ __forceinline__ float dot_avx(const float *x, const float *w, int kk) {
+    float A[8], B[8];
+#pragma unroll
+    for (int l = 0; l < 8; ++l) A[l] = B[l] = 0.f;
+    for (int c = 0; c < kk; c += 16) {
+#pragma unroll
+        for (int l = 0; l < 8; ++l) {
+            A[l] = __fmaf_rn(x[c + l], w[c + l], A[l]);
+            B[l] = __fmaf_rn(x[c + 8 + l], w[c + 8 + l], B[l]);
+        }
+    }
+    float S[8];
+#pragma unroll
+    for (int l = 0; l < 8; ++l) S[l] = __fadd_rn(A[l], B[l]);
+    return hsum8(S);
+}
+
+// dotF32x4 (kernels_amd64.go:75-95) for one row: assembly over k &^ 15,
+// dotF32Go over the rest added on.
+__device__ __forceinline__ float dot_x4(const float *x, const float *w, int k) {
+    const int kk = k & ~15;
+    float o = kk > 0 ? dot_avx(x, w, kk) : 0.f;
+    if (kk < k) o = __fadd_rn(o, dot_go(x + kk, w + kk, k - kk));
+    return o;
+}
+
+// softmax (internal/kern/mathx.go:78-90) of s[0..n) in LDS by one block:
+// max, e = EXP8(v-max) below n &^ 7 and expf past it, the eight lane sums
+// of expSubAVX + HSUM, plus the tail's own sum, then v *= 1/sum.
+__device__ inline void block_softmax(float *s, int n, float *part) {
+    const int tid = threadIdx.x, nt = blockDim.x;
+    float mx = -__builtin_inff();
+    for (int j = tid; j < n; j += nt) mx = s[j] > mx ? s[j] : mx;
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        const float v = __shfl_xor(mx, o);
+        mx = v > mx ? v : mx;
+    }
+    if ((tid & 63) == 0) part[16 + (tid >> 6)] = mx;
+    __syncthreads();
+    mx = -__builtin_inff();
+    for (int w = 0; w < (nt + 63) / 64; ++w) mx = part[16 + w] > mx ? part[16 + w] : mx;
+    const int n8 = n & ~7;
+    for (int j = tid; j < n; j += nt) {
+        const float d = __fsub_rn(s[j], mx);
+        s[j] = j < n8 ? grx_exp8(d) : grx_expf_go(d);
+    }
+    __syncthreads();
+    if (tid < 8) {
+        float acc = 0.f;
+#pragma unroll 16
+        for (int j = tid; j < n8; j += 8) acc = __fadd_rn(acc, s[j]);
+        part[tid] = acc;
+    } else if (tid == 8) {
+        float t = 0.f;
+        for (int j = n8; j < n; ++j) t = __fadd_rn(t, s[j]);
+        part[8] = t;
+    }
+    __syncthreads();
+    const float sa = n8 > 0 ? hsum8(part) : 0.f;
+    const float inv = __fdiv_rn(1.0f, __fadd_rn(sa, part[8]));
+    for (int j = tid; j < n; j += nt) s[j] = __fmul_rn(s[j], inv);
+    __syncthreads();
+}
+
+// Round the values held by 32 consecutive lanes (one Q8_0 block) for the
+// next product: quantU8 (internal/kern/q8int.go:88-105) with the block's
+// largest magnitude from xor-shuffles.  Every lane of the 32 must call it.
+__device__ __forceinline__ void quant32_store(float v, int8_t *q, float *sc, int lane32) {
+    const float av = fabsf(v);
+    float amax = av > 0.0f ? av : 0.0f;
+#pragma unroll
+    for (int o = 16; o > 0; o >>= 1) {
+        const float t = __shfl_xor(amax, o, 32);
+        amax = t > amax ? t : amax;
+    }
+    const float id = amax != 0.0f ? __fdiv_rn(127.0f, amax) : 0.0f;
+    float r = rintf(__fmul_rn(v, id));
+    r = fminf(fmaxf(r, -128.0f), 127.0f);
+    *q = (int8_t)(int)r;
+    if (lane32 == 0) *sc = __fmul_rn(amax, grx_bits_f32(0x3c010204u));
+}
+
+
+// softmax of s[0..n) by one thread (the same arithmetic as block_softmax):
+// expSub's eight lane sums over n &^ 7, HSUM, the tail's own sum.
+__device__ inline void seq_softmax(float *s, int n) {
+    float mx = -__builtin_inff();
+    for (int j = 0; j < n; ++j) mx = s[j] > mx ? s[j] : mx;
+    const int n8 = n & ~7;
+    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    for (int j = 0; j < n8; ++j) {
+        const float e = grx_exp8(__fsub_rn(s[j], mx));
+        s[j] = e;
+        acc[j & 7] = __fadd_rn(acc[j & 7], e);
+    }
+    float t = 0.f;
+    for (int j = n8; j < n; ++j) {
+        const float e = grx_expf_go(__fsub_rn(s[j], mx));
+        s[j] = e;
+        t = __fadd_rn(t, e);
+    }
+    const float sa = n8 > 0 ? hsum8(acc) : 0.f;
+    const float inv = __fdiv_rn(1.0f, __fadd_rn(sa, t));
+    for (int j = 0; j < n; ++j) s[j] = __fmul_rn(s[j], inv);
+}

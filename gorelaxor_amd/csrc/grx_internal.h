@@ -201,14 +201,15 @@ __device__ __forceinline__ float grx_gelu_at(float v, int i, int n) {
 }
 
 // Launch helpers of the product kernels (q8_gemv.hip).
-enum { GRX_PRO_PREQ = 0, GRX_PRO_QUANT = 1, GRX_PRO_LN = 2, GRX_PRO_EMBED_LN = 3 };
+enum { GRX_PRO_PREQ = 0, GRX_PRO_QUANT = 1, GRX_PRO_LN = 2, GRX_PRO_EMBED_LN = 3, GRX_PRO_LN64 = 4 };
 enum {
     GRX_EPI_STORE = 0,   // y = c
     GRX_EPI_RESID = 1,   // y = resid + c
     GRX_EPI_GELU = 2,    // y = geluVec(c) over the flat output
     GRX_EPI_QKV = 3,     // rows split in three: q, then K and V caches at *pos
     GRX_EPI_ARGMAX = 4,  // y = c (optional) and the first index of the maximum
-    GRX_EPI_GELU_Q = 5   // y = geluVec(c), and y rounded to Q8_0 into yq/ys
+    GRX_EPI_GELU_Q = 5,  // y = geluVec(c), and y rounded to Q8_0 into yq/ys
+    GRX_EPI_QKV_ROPE = 6 // as QKV, with q and k rotated by the cos/sin table at pos
 };
 
 struct GemvArgs {
@@ -248,6 +249,14 @@ struct GemvArgs {
     float *ys;
     // ordinary (cache-retained) weight loads instead of non-temporal ones
     int cacheable;
+    // QKV_ROPE: cos/sin of every position's pair angles, [max_pos][half],
+    // half = head_dim/2 (pairs are adjacent rows of a head)
+    const float *rope_cos, *rope_sin;
+    int rope_half;
+    // LN64: the normalization's epsilon
+    double ln_eps;
+    // added to *pos for the rows of this launch (QKV, QKV_ROPE, EMBED_LN)
+    int pos_add;
 };
 
 grx_status grx_gemv_launch(hipStream_t st, int m, int pro, int epi, const GemvArgs &a,
@@ -258,4 +267,4 @@ grx_status grx_gemm_q8_launch(hipStream_t st, const grx_weight *w, const int8_t 
 // Fewest activation rows that take the matrix-core product (GRX_GEMM_MIN_M
 // overrides it, for tests).
 int grx_gemm_min_m(void);
-int grx_gemv_pick_waves(int tiles, int nb, int m);
+int grx_gemv_pick_waves(int tiles, int nb, int m, int pro);

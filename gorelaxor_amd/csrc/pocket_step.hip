@@ -1,0 +1,643 @@
+// pocket_step.hip - the pocket-TTS flow-LM transformer (the "LM step") on
+// one GPU.
+//
+// The graph is flowLM.text/run/step of pockettts/lm.go:164-195 over
+// transformer.forward and attend (pockettts/nn.go:142-254) of
+// github.com/xattribution/gorelaxor: float64 LayerNorm, q|k|v (Q8_0, int8
+// route, as pockettts/model.go:331-366 packs and drops these weights),
+// rotary q and k, causal attention over the cache, out projection, GELU
+// feed-forward; no context limit, no layer scales.  Every float step keeps
+// the reference's order (the float route of MatMulF32 for the scores and
+// values, expSub for the softmax, AddScaled for T < 4), so the frame outputs
+// and end-of-speech logits are bit-identical to the CPU oracle's.
+//
+// A frame is 32 launches: the input projection of the latent, per layer
+// [LN -> q|k|v + RoPE + cache] [attention, one workgroup per head, output
+// rounded to Q8_0] [out + residual] [LN -> ff1 -> GELU, rounded] [ff2 +
+// residual], and [out_norm, end-of-speech logit, position and frame + 1].
+// Position and frame index live in device memory: a run of teacher-forced
+// frames is one captured graph replayed per frame.  The text prefix (T rows
+// at once) goes through the same products in launches of up to 8 rows and
+// its own attention kernel, which follows MatMulF32's route for T rows.
+#include <math.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include <map>
+#include <string>
+#include <vector>
+
+#include "grx_float.h"
+#include "grx_internal.h"
+
+namespace {
+
+constexpr int kThreads = 256;
+
+// x = input . latent (lm.go:188-190): an F32 [d][ldim] weight on the float
+// route with one row, gemvRows (gemm.go:195-259): dotF32x4 for whole groups
+// of four outputs, dotF32Go for the rest.
+__global__ void input_kernel(const float *__restrict__ w, const float *__restrict__ lat_base,
+                             const int *__restrict__ frame, int d, int ldim, float *__restrict__ x) {
+    const int j = blockIdx.x * blockDim.x + threadIdx.x;
+    if (j >= d) return;
+    const float *lat = lat_base + (frame != nullptr ? (size_t)(*frame) * ldim : 0);
+    const float *wr = w + (size_t)j * ldim;
+    x[j] = j < (d & ~3) ? dot_x4(lat, wr, ldim) : dot_go(lat, wr, ldim);
+}
+
+// attend for one query row (T = 1, nn.go:200-244), one workgroup per head:
+// scores of the pos+1 keys by MatMulF32's one-row route (dotF32x4 per group
+// of four keys, dotF32Go for the rest), times 1/sqrt(hd), softmax by expSub,
+// then out += w_j * v_j with AddScaled in key order, zero weights skipped
+// (axpyAVX's fma below hd &^ 7, axpyGo past it).  With QOUT the head's
+// outputs are also rounded to Q8_0.
+template <bool QOUT>
+__global__ __launch_bounds__(kThreads) void attn_step_kernel(const float *__restrict__ q, const float *__restrict__ kc,
+                                                            const float *__restrict__ vc, const int *__restrict__ pos,
+                                                            int d, int hd, float scale, float *__restrict__ att,
+                                                            int8_t *__restrict__ att_q, float *__restrict__ att_s) {
+    extern __shared__ float sm[];
+    float *part = sm, *s = sm + 32;
+    const int h = blockIdx.x, n = *pos + 1, tid = threadIdx.x;
+    const float *qh = q + h * hd;
+    const int n4 = n & ~3;
+    for (int j = tid; j < n; j += blockDim.x) {
+        const float *kj = kc + (size_t)j * d + h * hd;
+        s[j] = __fmul_rn(j < n4 ? dot_x4(qh, kj, hd) : dot_go(qh, kj, hd), scale);
+    }
+    __syncthreads();
+    block_softmax(s, n, part);
+    const int h8 = hd & ~7;
+    for (int e = tid; e < hd; e += blockDim.x) {
+        float o = 0.f;
+        const float *ve = vc + h * hd + e;
+        for (int j = 0; j < n; ++j) {
+            const float w = s[j];
+            if (w == 0.f) continue;
+            const float v = ve[(size_t)j * d];
+            o = e < h8 ? __fmaf_rn(w, v, o) : __fadd_rn(o, __fmul_rn(w, v));
+        }
+        att[h * hd + e] = o;
+        if constexpr (QOUT) quant32_store(o, att_q + h * hd + e, att_s + (h * hd + e) / 32, e & 31);
+    }
+}
+
+// One output of ws.matmul's float route for row r of m rows (gemm.go:116-
+// 184): rows in whole groups of six (m > 16) take k6x16avx's chain, fma over
+// k in chunks of 256 added to C from 0; other rows take gemvRows (dotF32x4
+// for whole groups of four columns, dotF32Go for the rest).  a_r and b_j are
+// k long with element strides sa and sb.
+__device__ float route_dot(const float *a, int sa, const float *b, int sb, int k, int r, int m, int j, int n) {
+    const bool packed = m > 16 && r < m / 6 * 6;
+    if (packed) {
+        float c = 0.f;
+        for (int k0 = 0; k0 < k; k0 += 256) {
+            const int kn = min(256, k - k0);
+            float acc = 0.f;
+            for (int kk = 0; kk < kn; ++kk) acc = __fmaf_rn(a[(size_t)(k0 + kk) * sa], b[(size_t)(k0 + kk) * sb], acc);
+            c = __fadd_rn(acc, c);
+        }
+        return c;
+    }
+    // gemvRows: the element strides are 1 on this route's operands
+    return j < (n & ~3) ? dot_x4(a, b, k) : dot_go(a, b, k);
+}
+
+// attend for T rows at once after pos0 cached positions (nn.go:200-254),
+// one workgroup per head: the scores by MatMulF32's route for T rows, each
+// row's causal softmax, then T < 4: AddScaled in key order; else the
+// product with the transposed values by the same route.  sc and vt are
+// scratch [heads][T][nk] and [heads][hd][nk] in HBM.
+__global__ __launch_bounds__(kThreads) void attn_prefix_kernel(const float *__restrict__ q, const float *__restrict__ kc,
+                                                              const float *__restrict__ vc, int pos0, int T, int d,
+                                                              int hd, float scale, float *__restrict__ sc,
+                                                              float *__restrict__ vt, float *__restrict__ att) {
+    const int h = blockIdx.x, tid = threadIdx.x, nk = pos0 + T;
+    float *S = sc + (size_t)h * T * nk;
+    float *Vt = vt + (size_t)h * hd * nk;
+    for (int i = tid; i < T * nk; i += blockDim.x) {
+        const int r = i / nk, j = i % nk;
+        S[i] = route_dot(q + (size_t)r * 3 * d + h * hd, 1, kc + (size_t)j * d + h * hd, 1, hd, r, T, j, nk);
+    }
+    for (int i = tid; i < hd * nk; i += blockDim.x) {
+        const int e = i / nk, j = i % nk;
+        Vt[i] = vc[(size_t)j * d + h * hd + e];
+    }
+    __syncthreads();
+    for (int r = tid; r < T; r += blockDim.x) {
+        float *row = S + (size_t)r * nk;
+        const int p = pos0 + r;
+        for (int j = 0; j <= p; ++j) row[j] = __fmul_rn(row[j], scale);
+        seq_softmax(row, p + 1);
+        for (int j = p + 1; j < nk; ++j) row[j] = 0.f;
+    }
+    __syncthreads();
+    const int h8 = hd & ~7;
+    for (int i = tid; i < T * hd; i += blockDim.x) {
+        const int r = i / hd, e = i % hd;
+        const float *row = S + (size_t)r * nk;
+        float o;
+        if (T < 4) {
+            o = 0.f;
+            for (int j = 0; j < nk; ++j) {
+                const float w = row[j];
+                if (w == 0.f) continue;
+                const float v = Vt[(size_t)e * nk + j];
+                o = e < h8 ? __fmaf_rn(w, v, o) : __fadd_rn(o, __fmul_rn(w, v));
+            }
+        } else {
+            o = route_dot(row, 1, Vt + (size_t)e * nk, 1, nk, r, T, e, hd);
+        }
+        att[(size_t)r * d + h * hd + e] = o;
+    }
+}
+
+// End of a frame (lm.go:168-169, 191-194): out_norm (float64 LayerNorm of
+// the last row), eos = dotF32Go(out, w) + b, recorded at the frame index;
+// then position and frame move on (advance 0: neither moves).
+__global__ __launch_bounds__(kThreads) void finish_kernel(const float *__restrict__ x, int d, const float *__restrict__ nw,
+                                                          const float *__restrict__ nb, const float *__restrict__ ew,
+                                                          float eb, int *__restrict__ pos, int *__restrict__ frame,
+                                                          int advance, float *__restrict__ out_hist,
+                                                          float *__restrict__ eos_hist) {
+    __shared__ double red[16];
+    __shared__ float ov[8192];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nw_ = blockDim.x >> 6;
+    double ps = 0.0;
+    for (int i = tid; i < d; i += blockDim.x) ps += (double)x[i];
+    for (int o = 32; o > 0; o >>= 1) ps += __shfl_xor(ps, o);
+    if (lane == 0) red[wave] = ps;
+    __syncthreads();
+    double sum = 0.0;
+    for (int w = 0; w < nw_; ++w) sum += red[w];
+    const double mean = sum / (double)d;
+    __syncthreads();
+    double pv = 0.0;
+    for (int i = tid; i < d; i += blockDim.x) {
+        const double t = (double)x[i] - mean;
+        pv += t * t;
+    }
+    for (int o = 32; o > 0; o >>= 1) pv += __shfl_xor(pv, o);
+    if (lane == 0) red[8 + wave] = pv;
+    __syncthreads();
+    double qs = 0.0;
+    for (int w = 0; w < nw_; ++w) qs += red[8 + w];
+    const double inv = 1.0 / sqrt(qs / (double)d + 1e-5);
+    const int f = frame != nullptr ? *frame : 0;
+    float *out = out_hist + (size_t)f * d;
+    for (int i = tid; i < d; i += blockDim.x) {
+        float o = (float)(((double)x[i] - mean) * inv);
+        o = __fadd_rn(__fmul_rn(o, nw[i]), nb[i]);
+        out[i] = o;
+        ov[i] = o;
+    }
+    __syncthreads();
+    if (tid == 0) {
+        eos_hist[f] = __fadd_rn(dot_go(ov, ew, d), eb);
+        if (advance) {
+            *pos = *pos + 1;
+            if (frame != nullptr) *frame = f + 1;
+        }
+    }
+}
+
+}  // namespace
+
+// ---------------------------------------------------------------- host side
+
+struct PLayer {
+    grx_weight *qkv = nullptr, *out = nullptr, *ff1 = nullptr, *ff2 = nullptr;
+    float *n1w, *n1b, *n2w, *n2b;
+    float *k, *v;
+};
+
+struct grx_pocket {
+    grx_ctx *ctx = nullptr;
+    grx_pocket_hparams hp{};
+    std::map<std::string, std::vector<uint8_t>> host;
+    bool ready = false;
+    std::vector<PLayer> L;
+    std::vector<void *> allocs;
+    float *input = nullptr, *bos = nullptr, *onw = nullptr, *onb = nullptr, *eosw = nullptr;
+    float eosb = 0.f;
+    float *rope_cos = nullptr, *rope_sin = nullptr;
+    // activations, room for max_pos rows
+    float *x = nullptr, *q = nullptr, *att = nullptr, *ff = nullptr;
+    int8_t *att_q = nullptr, *ff_q = nullptr;
+    float *att_s = nullptr, *ff_s = nullptr;
+    float *sc = nullptr, *vt = nullptr;       // prefix attention scratch
+    float *lat = nullptr;                     // latents of a run of frames
+    float *out_hist = nullptr, *eos_hist = nullptr;
+    int *pos = nullptr, *frame = nullptr;
+    int pos_host = 0;
+    int lat_cap = 0;
+    hipGraphExec_t exec = nullptr;
+    hipGraph_t graph = nullptr;
+};
+
+namespace {
+
+struct PExpect {
+    std::string name;
+    size_t bytes;
+};
+
+std::vector<PExpect> pexpected(const grx_pocket_hparams &hp) {
+    const size_t d = hp.d, ff = hp.ff;
+    auto q8 = [](size_t rows, size_t cols) { return rows * (cols / 32) * 34; };
+    std::vector<PExpect> e;
+    for (int i = 0; i < hp.n_layer; ++i) {
+        const std::string p = "lm.blk." + std::to_string(i) + ".";
+        for (const char *n : {"norm1.weight", "norm1.bias", "norm2.weight", "norm2.bias"}) e.push_back({p + n, d * 4});
+        e.push_back({p + "attn_qkv.weight", q8(3 * d, d)});
+        e.push_back({p + "attn_out.weight", q8(d, d)});
+        e.push_back({p + "ff1.weight", q8(ff, d)});
+        e.push_back({p + "ff2.weight", q8(d, ff)});
+    }
+    e.push_back({"lm.input.weight", d * hp.ldim * 4});
+    e.push_back({"lm.bos", (size_t)hp.ldim * 4});
+    e.push_back({"lm.out_norm.weight", d * 4});
+    e.push_back({"lm.out_norm.bias", d * 4});
+    e.push_back({"lm.eos.weight", d * 4});
+    e.push_back({"lm.eos.bias", 4});
+    return e;
+}
+
+grx_status palloc(grx_pocket *m, size_t bytes, void **out) {
+    void *p = nullptr;
+    GRX_HIP(hipMalloc(&p, bytes > 0 ? bytes : 16));
+    m->allocs.push_back(p);
+    *out = p;
+    return GRX_OK;
+}
+
+template <typename T>
+grx_status palloc_t(grx_pocket *m, size_t count, T **out) {
+    return palloc(m, count * sizeof(T), reinterpret_cast<void **>(out));
+}
+
+grx_status pupload(grx_pocket *m, const std::string &name, float **out) {
+    const auto &h = m->host.at(name);
+    grx_status s = palloc(m, h.size(), reinterpret_cast<void **>(out));
+    if (s != GRX_OK) return s;
+    GRX_HIP(hipMemcpy(*out, h.data(), h.size(), hipMemcpyHostToDevice));
+    return GRX_OK;
+}
+
+// cos/sin of every position's pair angles (nn.go:69-93): f_i =
+// f32(exp(f64(f32(i) * f32(-ln(period)*2/hd)))), angle f64(f_i * f32(pos)),
+// kept as f32.  Computed once on the host.
+void rope_table(const grx_pocket_hparams &hp, std::vector<float> &cs, std::vector<float> &sn) {
+    const int hd = hp.d / hp.heads, half = hd / 2;
+    const float c = (float)(-log(hp.period) * 2.0 / (double)hd);
+    std::vector<float> f(half);
+    for (int i = 0; i < half; ++i) {
+        const float t = (float)i * c;
+        f[i] = (float)exp((double)t);
+    }
+    cs.resize((size_t)hp.max_pos * half);
+    sn.resize((size_t)hp.max_pos * half);
+    for (int p = 0; p < hp.max_pos; ++p)
+        for (int i = 0; i < half; ++i) {
+            const float fp = f[i] * (float)p;
+            const double a = (double)fp;
+            cs[(size_t)p * half + i] = (float)cos(a);
+            sn[(size_t)p * half + i] = (float)sin(a);
+        }
+}
+
+grx_status pfinalize(grx_pocket *m) {
+    if (m->ready) return GRX_OK;
+    const grx_pocket_hparams &hp = m->hp;
+    for (const PExpect &e : pexpected(hp))
+        if (!m->host.count(e.name)) return grx_fail(GRX_ESTATE, "the model file has no tensor %s", e.name.c_str());
+    GRX_HIP(hipSetDevice(m->ctx->device));
+    grx_status s;
+    const size_t d = hp.d, ff = hp.ff, mp = hp.max_pos;
+    m->L.resize(hp.n_layer);
+    for (int i = 0; i < hp.n_layer; ++i) {
+        PLayer &L = m->L[i];
+        const std::string p = "lm.blk." + std::to_string(i) + ".";
+        auto mat = [&](const char *n, int rows, int cols, grx_weight **w) {
+            const auto &t = m->host.at(p + n);
+            return grx_weight_q8_create(m->ctx, rows, cols, t.data(), t.size(), w);
+        };
+        if ((s = mat("attn_qkv.weight", 3 * hp.d, hp.d, &L.qkv)) != GRX_OK) return s;
+        if ((s = mat("attn_out.weight", hp.d, hp.d, &L.out)) != GRX_OK) return s;
+        if ((s = mat("ff1.weight", hp.ff, hp.d, &L.ff1)) != GRX_OK) return s;
+        if ((s = mat("ff2.weight", hp.d, hp.ff, &L.ff2)) != GRX_OK) return s;
+        if ((s = pupload(m, p + "norm1.weight", &L.n1w)) != GRX_OK) return s;
+        if ((s = pupload(m, p + "norm1.bias", &L.n1b)) != GRX_OK) return s;
+        if ((s = pupload(m, p + "norm2.weight", &L.n2w)) != GRX_OK) return s;
+        if ((s = pupload(m, p + "norm2.bias", &L.n2b)) != GRX_OK) return s;
+        if ((s = palloc_t(m, mp * d, &L.k)) != GRX_OK) return s;
+        if ((s = palloc_t(m, mp * d, &L.v)) != GRX_OK) return s;
+        GRX_HIP(hipMemset(L.k, 0, mp * d * 4));
+        GRX_HIP(hipMemset(L.v, 0, mp * d * 4));
+    }
+    if ((s = pupload(m, "lm.input.weight", &m->input)) != GRX_OK) return s;
+    if ((s = pupload(m, "lm.bos", &m->bos)) != GRX_OK) return s;
+    if ((s = pupload(m, "lm.out_norm.weight", &m->onw)) != GRX_OK) return s;
+    if ((s = pupload(m, "lm.out_norm.bias", &m->onb)) != GRX_OK) return s;
+    if ((s = pupload(m, "lm.eos.weight", &m->eosw)) != GRX_OK) return s;
+    memcpy(&m->eosb, m->host.at("lm.eos.bias").data(), 4);
+    std::vector<float> cs, sn;
+    rope_table(hp, cs, sn);
+    if ((s = palloc_t(m, cs.size(), &m->rope_cos)) != GRX_OK) return s;
+    if ((s = palloc_t(m, sn.size(), &m->rope_sin)) != GRX_OK) return s;
+    GRX_HIP(hipMemcpy(m->rope_cos, cs.data(), cs.size() * 4, hipMemcpyHostToDevice));
+    GRX_HIP(hipMemcpy(m->rope_sin, sn.data(), sn.size() * 4, hipMemcpyHostToDevice));
+    const int hd = hp.d / hp.heads;
+    if ((s = palloc_t(m, mp * d, &m->x)) != GRX_OK) return s;
+    if ((s = palloc_t(m, mp * 3 * d, &m->q)) != GRX_OK) return s;  // q rows 3d apart
+    if ((s = palloc_t(m, mp * d, &m->att)) != GRX_OK) return s;
+    if ((s = palloc_t(m, mp * ff, &m->ff)) != GRX_OK) return s;
+    if ((s = palloc_t(m, mp * d, &m->att_q)) != GRX_OK) return s;
+    if ((s = palloc_t(m, mp * d / 32, &m->att_s)) != GRX_OK) return s;
+    if ((s = palloc_t(m, mp * ff, &m->ff_q)) != GRX_OK) return s;
+    if ((s = palloc_t(m, mp * ff / 32, &m->ff_s)) != GRX_OK) return s;
+    if ((s = palloc_t(m, (size_t)hp.heads * mp * mp, &m->sc)) != GRX_OK) return s;
+    if ((s = palloc_t(m, (size_t)hp.heads * hd * mp, &m->vt)) != GRX_OK) return s;
+    if ((s = palloc_t(m, mp * d, &m->out_hist)) != GRX_OK) return s;
+    if ((s = palloc_t(m, mp, &m->eos_hist)) != GRX_OK) return s;
+    if ((s = palloc_t(m, 1, &m->pos)) != GRX_OK) return s;
+    if ((s = palloc_t(m, 1, &m->frame)) != GRX_OK) return s;
+    GRX_HIP(hipMemset(m->pos, 0, 4));
+    GRX_HIP(hipMemset(m->frame, 0, 4));
+    m->host.clear();
+    m->ready = true;
+    return GRX_OK;
+}
+
+GemvArgs pargs(const grx_weight *w) {
+    GemvArgs a = {};
+    a.qs = w->qs;
+    a.ds = w->ds;
+    a.rows = w->rows;
+    a.nb = w->nb;
+    a.cacheable = 1;
+    a.ln_eps = 1e-5;
+    return a;
+}
+
+// transformer.forward of rows r0..r0+mm-1 of x (nn.go:151-179) for one
+// layer's products; attention is separate.  ph: 0 = LN -> q|k|v, 1 = out +
+// residual, 2 = LN -> ff1 -> GELU, 3 = ff2 + residual.
+grx_status layer_product(grx_pocket *m, hipStream_t st, PLayer &L, int ph, int r0, int mm, bool qatt) {
+    const int d = m->hp.d, ff = m->hp.ff;
+    GemvArgs a;
+    switch (ph) {
+        case 0:
+            a = pargs(L.qkv);
+            a.x = m->x + (size_t)r0 * d;
+            a.lda = d;
+            a.ln_w = L.n1w;
+            a.ln_b = L.n1b;
+            a.y = m->q + (size_t)r0 * 3 * d;  // q rows 3d apart, as the reference's qkv rows
+            a.ldc = 3 * d;
+            a.seg = d;
+            a.kc = L.k;
+            a.vc = L.v;
+            a.pos = m->pos;
+            a.pos_add = r0;
+            a.rope_cos = m->rope_cos;
+            a.rope_sin = m->rope_sin;
+            a.rope_half = d / m->hp.heads / 2;
+            return grx_gemv_launch(st, mm, GRX_PRO_LN64, GRX_EPI_QKV_ROPE, a, 0);
+        case 1:
+            a = pargs(L.out);
+            a.x = m->att + (size_t)r0 * d;
+            a.lda = d;
+            a.xq = m->att_q + (size_t)r0 * d;
+            a.xs = m->att_s + (size_t)r0 * d / 32;
+            a.y = m->x + (size_t)r0 * d;
+            a.ldc = d;
+            a.resid = m->x + (size_t)r0 * d;
+            a.ldr = d;
+            return grx_gemv_launch(st, mm, qatt ? GRX_PRO_PREQ : GRX_PRO_QUANT, GRX_EPI_RESID, a, 0);
+        case 2:
+            a = pargs(L.ff1);
+            a.x = m->x + (size_t)r0 * d;
+            a.lda = d;
+            a.ln_w = L.n2w;
+            a.ln_b = L.n2b;
+            a.y = m->ff + (size_t)r0 * ff;
+            a.ldc = ff;
+            a.yq = m->ff_q + (size_t)r0 * ff;
+            a.ys = m->ff_s + (size_t)r0 * ff / 32;
+            return grx_gemv_launch(st, mm, GRX_PRO_LN64, GRX_EPI_GELU_Q, a, 0);
+        default:
+            a = pargs(L.ff2);
+            a.xq = m->ff_q + (size_t)r0 * ff;
+            a.xs = m->ff_s + (size_t)r0 * ff / 32;
+            a.y = m->x + (size_t)r0 * d;
+            a.ldc = d;
+            a.resid = m->x + (size_t)r0 * d;
+            a.ldr = d;
+            return grx_gemv_launch(st, mm, GRX_PRO_PREQ, GRX_EPI_RESID, a, 0);
+    }
+}
+
+// One frame (T = 1) from the latent at lat_base[*frame] (frame may be null:
+// lat_base itself), on stream st.
+grx_status enqueue_frame(grx_pocket *m, hipStream_t st, const float *lat_base, const int *frame) {
+    const grx_pocket_hparams &hp = m->hp;
+    const int d = hp.d, hd = d / hp.heads;
+    const bool qatt = hd % 32 == 0;
+    const float scale = (float)(1.0 / sqrt((double)hd));
+    grx_status s;
+    input_kernel<<<grx_ceil_div(d, kThreads), kThreads, 0, st>>>(m->input, lat_base, frame, d, hp.ldim, m->x);
+    GRX_LAUNCHED("input_kernel");
+    const size_t smem = (32 + (size_t)hp.max_pos) * 4;
+    for (int li = 0; li < hp.n_layer; ++li) {
+        PLayer &L = m->L[li];
+        if ((s = layer_product(m, st, L, 0, 0, 1, qatt)) != GRX_OK) return s;
+        if (qatt)
+            attn_step_kernel<true><<<hp.heads, kThreads, smem, st>>>(m->q, L.k, L.v, m->pos, d, hd, scale, m->att,
+                                                                     m->att_q, m->att_s);
+        else
+            attn_step_kernel<false><<<hp.heads, kThreads, smem, st>>>(m->q, L.k, L.v, m->pos, d, hd, scale, m->att,
+                                                                      nullptr, nullptr);
+        GRX_LAUNCHED("attn_step_kernel");
+        for (int ph = 1; ph < 4; ++ph)
+            if ((s = layer_product(m, st, L, ph, 0, 1, qatt)) != GRX_OK) return s;
+    }
+    finish_kernel<<<1, kThreads, 0, st>>>(m->x, d, m->onw, m->onb, m->eosw, m->eosb, m->pos, m->frame, 1,
+                                          m->out_hist, m->eos_hist);
+    GRX_LAUNCHED("finish_kernel");
+    return GRX_OK;
+}
+
+}  // namespace
+
+extern "C" grx_status grx_pocket_create(grx_ctx *ctx, const grx_pocket_hparams *hp, grx_pocket **out) {
+    if (!ctx || !hp || !out) return grx_fail(GRX_EINVAL, "grx_pocket_create: NULL argument");
+    *out = nullptr;
+    if (hp->d <= 0 || hp->heads <= 0 || hp->ff <= 0 || hp->n_layer <= 0 || hp->max_pos <= 0 || hp->ldim <= 0 ||
+        !(hp->period > 0))
+        return grx_fail(GRX_EINVAL, "grx_pocket_create: every size must be positive");
+    if (hp->d % 32 != 0 || hp->ff % 32 != 0 || hp->d % hp->heads != 0 || (hp->d / hp->heads) % 2 != 0)
+        return grx_fail(GRX_ESIZE, "%d values don't split into %d heads", hp->d, hp->heads);
+    if (hp->d > 8192 || (size_t)hp->max_pos * hp->max_pos * 4 > 64 * 1024 * 1024)
+        return grx_fail(GRX_ESIZE, "grx_pocket_create: d %d or max_pos %d too large", hp->d, hp->max_pos);
+    grx_pocket *m = new grx_pocket();
+    m->ctx = ctx;
+    m->hp = *hp;
+    *out = m;
+    return GRX_OK;
+}
+
+extern "C" grx_status grx_pocket_destroy(grx_pocket *m) {
+    if (!m) return GRX_OK;
+    GRX_HIP(hipSetDevice(m->ctx->device));
+    GRX_HIP(hipStreamSynchronize(m->ctx->stream));
+    if (m->exec) (void)hipGraphExecDestroy(m->exec);
+    if (m->graph) (void)hipGraphDestroy(m->graph);
+    for (PLayer &L : m->L)
+        for (grx_weight *w : {L.qkv, L.out, L.ff1, L.ff2}) grx_weight_destroy(w);
+    for (void *p : m->allocs) (void)hipFree(p);
+    delete m;
+    return GRX_OK;
+}
+
+extern "C" grx_status grx_pocket_set_tensor(grx_pocket *m, const char *name, const void *data, size_t nbytes) {
+    if (!m || !name || (!data && nbytes)) return grx_fail(GRX_EINVAL, "grx_pocket_set_tensor: NULL argument");
+    if (m->ready) return grx_fail(GRX_ESTATE, "grx_pocket_set_tensor: the model is in use already");
+    for (const PExpect &e : pexpected(m->hp)) {
+        if (e.name != name) continue;
+        if (nbytes != e.bytes)
+            return grx_fail(GRX_ESIZE, "tensor %s has the wrong shape (%zu bytes, want %zu)", name, nbytes, e.bytes);
+        const uint8_t *p = static_cast<const uint8_t *>(data);
+        m->host[name].assign(p, p + nbytes);
+        return GRX_OK;
+    }
+    return grx_fail(GRX_EINVAL, "the model file has a tensor this program doesn't know: %s", name);
+}
+
+extern "C" grx_status grx_pocket_reset(grx_pocket *m) {
+    if (!m) return grx_fail(GRX_EINVAL, "grx_pocket_reset: NULL model");
+    if (m->ready) GRX_HIP(hipMemsetAsync(m->pos, 0, 4, m->ctx->stream));
+    m->pos_host = 0;
+    return GRX_OK;
+}
+
+extern "C" int grx_pocket_pos(const grx_pocket *m) { return m ? m->pos_host : 0; }
+
+extern "C" grx_status grx_pocket_run(grx_pocket *m, const float *x, int T, float *out) {
+    if (!m || (!x && T > 0)) return grx_fail(GRX_EINVAL, "grx_pocket_run: NULL argument");
+    grx_status s = pfinalize(m);
+    if (s != GRX_OK) return s;
+    if (T <= 0) return grx_fail(GRX_EINVAL, "grx_pocket_run: T = %d", T);
+    if (m->pos_host + T > m->hp.max_pos)
+        return grx_fail(GRX_ESTATE, "grx_pocket_run: %d rows after %d positions exceed %d", T, m->pos_host,
+                        m->hp.max_pos);
+    const grx_pocket_hparams &hp = m->hp;
+    const int d = hp.d, hd = d / hp.heads, pos0 = m->pos_host;
+    const bool qatt = hd % 32 == 0;
+    hipStream_t st = m->ctx->stream;
+    GRX_HIP(hipMemcpyAsync(m->x, x, (size_t)T * d * 4, hipMemcpyHostToDevice, st));
+    const float scale = (float)(1.0 / sqrt((double)hd));
+    // rows in launches of 8, 4, 2 and 1
+    auto rows_of = [&](int left) { return left >= 8 ? 8 : left >= 4 ? 4 : left >= 2 ? 2 : 1; };
+    for (int li = 0; li < hp.n_layer; ++li) {
+        PLayer &L = m->L[li];
+        for (int r0 = 0; r0 < T;) {
+            const int mm = rows_of(T - r0);
+            if ((s = layer_product(m, st, L, 0, r0, mm, qatt)) != GRX_OK) return s;
+            r0 += mm;
+        }
+        attn_prefix_kernel<<<hp.heads, kThreads, 0, st>>>(m->q, L.k, L.v, pos0, T, d, hd, scale, m->sc, m->vt, m->att);
+        GRX_LAUNCHED("attn_prefix_kernel");
+        // the prefix's attention rows are rounded in the out product's prologue
+        for (int ph = 1; ph < 4; ++ph)
+            for (int r0 = 0; r0 < T;) {
+                const int mm = rows_of(T - r0);
+                if ((s = layer_product(m, st, L, ph, r0, mm, ph == 1 ? false : qatt)) != GRX_OK) return s;
+                r0 += mm;
+            }
+    }
+    // out_norm of the last row into the history slot of frame 0 (not kept)
+    finish_kernel<<<1, kThreads, 0, st>>>(m->x + (size_t)(T - 1) * d, d, m->onw, m->onb, m->eosw, m->eosb, m->pos,
+                                          nullptr, 0, m->out_hist, m->eos_hist);
+    GRX_LAUNCHED("finish_kernel");
+    m->pos_host += T;
+    GRX_HIP(hipMemcpyAsync(m->pos, &m->pos_host, 4, hipMemcpyHostToDevice, st));
+    if (out) GRX_HIP(hipMemcpyAsync(out, m->out_hist, (size_t)d * 4, hipMemcpyDeviceToHost, st));
+    GRX_HIP(hipStreamSynchronize(st));
+    return GRX_OK;
+}
+
+extern "C" grx_status grx_pocket_frames(grx_pocket *m, const float *latents, int n, float *outs, float *eos) {
+    if (!m) return grx_fail(GRX_EINVAL, "grx_pocket_frames: NULL model");
+    grx_status s = pfinalize(m);
+    if (s != GRX_OK) return s;
+    if (n < 0) return grx_fail(GRX_EINVAL, "grx_pocket_frames: n = %d", n);
+    if (m->pos_host + n > m->hp.max_pos)
+        return grx_fail(GRX_ESTATE, "grx_pocket_frames: %d frames after %d positions exceed %d", n, m->pos_host,
+                        m->hp.max_pos);
+    if (n == 0) return GRX_OK;
+    const grx_pocket_hparams &hp = m->hp;
+    hipStream_t st = m->ctx->stream;
+    if (n > m->lat_cap) {
+        if (m->lat) {
+            GRX_HIP(hipStreamSynchronize(st));
+            GRX_HIP(hipFree(m->lat));
+            for (auto &p : m->allocs)
+                if (p == m->lat) p = nullptr;
+            if (m->exec) {
+                (void)hipGraphExecDestroy(m->exec);
+                (void)hipGraphDestroy(m->graph);
+                m->exec = nullptr;
+                m->graph = nullptr;
+            }
+        }
+        GRX_HIP(hipMalloc(&m->lat, (size_t)hp.max_pos * hp.ldim * 4));
+        m->allocs.push_back(m->lat);
+        m->lat_cap = hp.max_pos;
+    }
+    // frame k's latent at lat[k]; latents NULL: the bos input for every frame
+    if (latents)
+        GRX_HIP(hipMemcpyAsync(m->lat, latents, (size_t)n * hp.ldim * 4, hipMemcpyHostToDevice, st));
+    else
+        for (int k = 0; k < n; ++k)
+            GRX_HIP(hipMemcpyAsync(m->lat + (size_t)k * hp.ldim, m->bos, (size_t)hp.ldim * 4, hipMemcpyDeviceToDevice,
+                                   st));
+    GRX_HIP(hipMemsetAsync(m->frame, 0, 4, st));
+    const char *ng = getenv("GRX_NO_GRAPH");
+    const bool eager = ng && ng[0] == '1';
+    for (int k = 0; k < n; ++k) {
+        if (eager || (!m->exec && k == 0)) {
+            if ((s = enqueue_frame(m, st, m->lat, m->frame)) != GRX_OK) return s;
+            if (!eager && !m->exec) {
+                // capture the frame once the eager one has set every attribute
+                GRX_HIP(hipStreamSynchronize(st));
+                hipError_t e = hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal);
+                if (e == hipSuccess) {
+                    grx_status cs = enqueue_frame(m, st, m->lat, m->frame);
+                    hipGraph_t g = nullptr;
+                    e = hipStreamEndCapture(st, &g);
+                    if (cs == GRX_OK && e == hipSuccess) e = hipGraphInstantiate(&m->exec, g, nullptr, nullptr, 0);
+                    if (g) {
+                        if (e == hipSuccess && cs == GRX_OK) m->graph = g;
+                        else (void)hipGraphDestroy(g);
+                    }
+                    if (e != hipSuccess || cs != GRX_OK) {
+                        (void)hipGetLastError();
+                        m->exec = nullptr;
+                    }
+                }
+            }
+            continue;
+        }
+        if (m->exec)
+            GRX_HIP(hipGraphLaunch(m->exec, st));
+        else if ((s = enqueue_frame(m, st, m->lat, m->frame)) != GRX_OK)
+            return s;
+    }
+    m->pos_host += n;
+    if (outs) GRX_HIP(hipMemcpyAsync(outs, m->out_hist, (size_t)n * hp.d * 4, hipMemcpyDeviceToHost, st));
+    if (eos) GRX_HIP(hipMemcpyAsync(eos, m->eos_hist, (size_t)n * 4, hipMemcpyDeviceToHost, st));
+    GRX_HIP(hipStreamSynchronize(st));
+    return GRX_OK;
+}

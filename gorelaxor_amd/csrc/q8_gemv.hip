@@ -142,7 +142,7 @@ __global__ __launch_bounds__(64 * W) void gemv_q8_kernel(const GemvArgs a) {
             if constexpr (PRO == GRX_PRO_EMBED_LN) {
                 // the row is tokEmb.row(tok) + decPos[pos] (whisper/decoder.go:42-46),
                 // built by every workgroup; tile 0 stores it for the residual
-                const int t = a.tok[m], p = *a.pos + m;
+                const int t = a.tok[m], p = *a.pos + a.pos_add + m;
                 const int etile = t >> 6, elane = t & 63;
                 for (int i = tid; i < K; i += 64 * W) {
                     const int b = i >> 5, h = (i >> 4) & 1, e = i & 15;
@@ -174,6 +174,35 @@ __global__ __launch_bounds__(64 * W) void gemv_q8_kernel(const GemvArgs a) {
                 t = __fmul_rn(t, inv);
                 t = __fmul_rn(t, a.ln_w[i]);
                 fr[i] = __fadd_rn(t, a.ln_b[i]);
+            }
+        }
+        __syncthreads();
+        quant_into_lds<M>(lf, K, nb, lxq, lxs, tid, 64 * W);
+        __syncthreads();
+    } else if constexpr (PRO == GRX_PRO_LN64) {
+        // layerNorm of pockettts/nn.go:27-49: statistics and the normalized
+        // value in float64, the gain and bias (when given) in float32.
+        for (int m = 0; m < M; ++m) {
+            const float *xr = a.x + (size_t)m * a.lda;
+            float *fr = lf + (size_t)m * K;
+            double ps = 0.0;
+            for (int i = tid; i < K; i += 64 * W) {
+                const float v = xr[i];
+                fr[i] = v;
+                ps += (double)v;
+            }
+            const double mean = block_sum_f64(ps, red, lane, wave, W) / (double)K;
+            double pv = 0.0;
+            for (int i = tid; i < K; i += 64 * W) {
+                const double d = (double)fr[i] - mean;
+                pv += d * d;
+            }
+            const double q = block_sum_f64(pv, red + W, lane, wave, W);
+            const double inv = 1.0 / sqrt(q / (double)K + a.ln_eps);
+            for (int i = tid; i < K; i += 64 * W) {
+                float o = (float)(((double)fr[i] - mean) * inv);
+                if (a.ln_w != nullptr) o = __fadd_rn(__fmul_rn(o, a.ln_w[i]), a.ln_b[i]);
+                fr[i] = o;
             }
         }
         __syncthreads();
@@ -342,6 +371,35 @@ __global__ __launch_bounds__(64 * W) void gemv_q8_kernel(const GemvArgs a) {
         }
         return;
     }
+    if constexpr (EPI == GRX_EPI_QKV_ROPE) {
+        // applyRope (pockettts/nn.go:80-93) on the q and k rows: the pair
+        // (2i, 2i+1) of a head sits in adjacent lanes; x'[2i] = r*c - im*s,
+        // x'[2i+1] = r*s + im*c, unfused, with f32 cos/sin of the angle.
+#pragma unroll
+        for (int m = 0; m < M; ++m) {
+            const float c = acc[m];
+            const float other = __shfl_xor(c, 1);
+            if (row >= a.rows) continue;
+            const int pos = *a.pos + a.pos_add + m;
+            if (row < 2 * a.seg) {
+                const int j = row % a.seg, hd = 2 * a.rope_half;
+                const int i = (j % hd) >> 1;
+                const float cs = a.rope_cos[(size_t)pos * a.rope_half + i];
+                const float sn = a.rope_sin[(size_t)pos * a.rope_half + i];
+                const bool even = (j & 1) == 0;
+                const float r = even ? c : other, im = even ? other : c;
+                const float v = even ? __fsub_rn(__fmul_rn(r, cs), __fmul_rn(im, sn))
+                                     : __fadd_rn(__fmul_rn(r, sn), __fmul_rn(im, cs));
+                if (row < a.seg)
+                    a.y[(size_t)m * a.ldc + row] = v;
+                else
+                    a.kc[(size_t)pos * a.seg + row - a.seg] = v;
+            } else {
+                a.vc[(size_t)pos * a.seg + row - 2 * a.seg] = c;
+            }
+        }
+        return;
+    }
     if (row >= a.rows) return;
 #pragma unroll
     for (int m = 0; m < M; ++m) {
@@ -358,7 +416,7 @@ __global__ __launch_bounds__(64 * W) void gemv_q8_kernel(const GemvArgs a) {
             const int len = min(1 << 14, total - start);
             a.y[(size_t)m * a.ldc + row] = grx_gelu_at(c, flat - start, len);
         } else if constexpr (EPI == GRX_EPI_QKV) {
-            const int pos = *a.pos + m;
+            const int pos = *a.pos + a.pos_add + m;
             if (row < a.seg)
                 a.y[(size_t)m * a.ldc + row] = c;
             else if (row < 2 * a.seg)
@@ -449,15 +507,15 @@ hipError_t launch_m(hipStream_t st, int m, const GemvArgs &a, int tiles, int W) 
 }  // namespace
 
 // Waves per tile: enough tiles x waves to cover the CUs, never more waves
-// than blocks, and the LDS of the ordered chain within 64 KiB.
+// than blocks, and the workgroup's LDS within 64 KiB.
 // GRX_GEMV_WAVES (1, 2, 4, 8 or 16) forces the choice, for tests.
-int grx_gemv_pick_waves(int tiles, int nb, int m) {
+int grx_gemv_pick_waves(int tiles, int nb, int m, int pro) {
     if (const char *f = getenv("GRX_GEMV_WAVES")) {
         const int w = atoi(f);
         if (w == 1 || w == 2 || w == 4 || w == 8 || w == 16) return w;
     }
     int W = 1;
-    while (W < 16 && tiles * W < 2048 && 2 * W <= nb && (size_t)m * nb * 64 * 4 <= 80 * 1024) W *= 2;
+    while (W < 16 && tiles * W < 2048 && 2 * W <= nb && gemv_smem(m, 2 * W, pro, nb) <= 64 * 1024) W *= 2;
     return W;
 }
 
@@ -465,7 +523,7 @@ int grx_gemv_pick_waves(int tiles, int nb, int m) {
 grx_status grx_gemv_launch(hipStream_t st, int m, int pro, int epi, const GemvArgs &a, int waves) {
     const int tiles = grx_ceil_div(a.rows, 64);
     if (tiles == 0 || m == 0) return GRX_OK;
-    const int W = waves > 0 ? waves : grx_gemv_pick_waves(tiles, a.nb, m);
+    const int W = waves > 0 ? waves : grx_gemv_pick_waves(tiles, a.nb, m, pro);
     hipError_t e = hipErrorInvalidValue;
     if (pro == GRX_PRO_PREQ && epi == GRX_EPI_STORE) e = launch_m<GRX_PRO_PREQ, GRX_EPI_STORE>(st, m, a, tiles, W);
     else if (pro == GRX_PRO_QUANT && epi == GRX_EPI_STORE) e = launch_m<GRX_PRO_QUANT, GRX_EPI_STORE>(st, m, a, tiles, W);
@@ -477,6 +535,8 @@ grx_status grx_gemv_launch(hipStream_t st, int m, int pro, int epi, const GemvAr
     else if (pro == GRX_PRO_LN && epi == GRX_EPI_GELU_Q) e = launch_m<GRX_PRO_LN, GRX_EPI_GELU_Q>(st, m, a, tiles, W);
     else if (pro == GRX_PRO_EMBED_LN && epi == GRX_EPI_QKV) e = launch_m<GRX_PRO_EMBED_LN, GRX_EPI_QKV>(st, m, a, tiles, W);
     else if (pro == GRX_PRO_PREQ && epi == GRX_EPI_RESID) e = launch_m<GRX_PRO_PREQ, GRX_EPI_RESID>(st, m, a, tiles, W);
+    else if (pro == GRX_PRO_LN64 && epi == GRX_EPI_QKV_ROPE) e = launch_m<GRX_PRO_LN64, GRX_EPI_QKV_ROPE>(st, m, a, tiles, W);
+    else if (pro == GRX_PRO_LN64 && epi == GRX_EPI_GELU_Q) e = launch_m<GRX_PRO_LN64, GRX_EPI_GELU_Q>(st, m, a, tiles, W);
     else return grx_fail(GRX_EINVAL, "grx: no GEMV variant for prologue %d epilogue %d", pro, epi);
     if (e != hipSuccess) return grx_hip_fail(e, "gemv_q8_kernel");
     return GRX_OK;

@@ -1,0 +1,70 @@
+"""Host driver of the pocket-TTS flow-LM transformer on the GPU.
+
+Mirrors flowLM.text/run/step of gorelaxor's pockettts package (github.com/
+xattribution/gorelaxor, pockettts/lm.go:164-195): tensors bound by the names
+pockettts/model.go reads, the text prefix run at once, then frames that stay
+on the device (teacher-forced latents; the flow head is not part of this).
+"""
+from __future__ import annotations
+
+import ctypes as C
+
+import numpy as np
+
+from . import _lib
+from .kern import Context, default_context
+
+
+class PocketLM:
+    def __init__(self, hp: dict, tensors: dict | None = None, ctx: Context | None = None):
+        self.ctx = ctx or default_context()
+        self.hp = dict(hp)
+        h = _lib.PocketHParams(d=hp["d"], heads=hp["heads"], ff=hp["ff"], n_layer=hp["n_layer"],
+                               max_pos=hp["max_pos"], ldim=hp["ldim"], period=float(hp.get("period", 1e4)))
+        out = C.c_void_p()
+        _lib.call("grx_pocket_create", self.ctx.handle, C.byref(h), C.byref(out))
+        self.handle = out
+        if tensors:
+            for name, arr in tensors.items():
+                self.set_tensor(name, arr)
+
+    def set_tensor(self, name: str, arr: np.ndarray) -> None:
+        a = np.ascontiguousarray(arr)
+        _lib.call("grx_pocket_set_tensor", self.handle, name.encode(), a.ctypes.data_as(C.c_void_p), a.nbytes)
+
+    def reset(self) -> None:
+        _lib.call("grx_pocket_reset", self.handle)
+
+    @property
+    def pos(self) -> int:
+        return _lib.lib().grx_pocket_pos(self.handle)
+
+    def run(self, x: np.ndarray) -> np.ndarray:
+        x = np.ascontiguousarray(x, np.float32)
+        T = x.size // self.hp["d"]
+        out = np.zeros(self.hp["d"], np.float32)
+        _lib.call("grx_pocket_run", self.handle, x.ctypes.data_as(C.c_void_p), T, out.ctypes.data_as(C.c_void_p))
+        return out
+
+    def frames(self, latents: np.ndarray | None, n: int | None = None):
+        """n steps fed latents[k] (None: bos every frame): (outputs [n][d], eos [n])."""
+        if latents is not None:
+            latents = np.ascontiguousarray(latents, np.float32)
+            n = latents.size // self.hp["ldim"]
+        outs = np.zeros((n, self.hp["d"]), np.float32)
+        eos = np.zeros(n, np.float32)
+        _lib.call("grx_pocket_frames", self.handle,
+                  None if latents is None else latents.ctypes.data_as(C.c_void_p), n,
+                  outs.ctypes.data_as(C.c_void_p), eos.ctypes.data_as(C.c_void_p))
+        return outs, eos
+
+    def close(self):
+        if self.handle:
+            _lib.call("grx_pocket_destroy", self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass

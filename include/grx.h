@@ -164,6 +164,40 @@ grx_status grx_whisper_decode(grx_whisper *m, const int32_t *tokens, int n, floa
 grx_status grx_whisper_greedy(grx_whisper *m, const int32_t *prompt, int n_prompt, int n_steps,
                               int32_t *out);
 
+/* ---- pocket-TTS flow-LM transformer with Q8_0 weights ---- */
+
+/* flowLM of pockettts/lm.go:164-195 over transformer.forward and attend of
+ * pockettts/nn.go:142-254 (float64 LayerNorm, rotary q and k with period
+ * `period`, causal attention, tanh-GELU feed-forward, no context limit),
+ * its transformer matrices Q8_0 on the int8 route as pockettts/model.go:
+ * 331-366 packs them.  The KV caches, position and frame index stay in HBM. */
+typedef struct {
+    int d, heads, ff, n_layer, max_pos, ldim;
+    double period;
+} grx_pocket_hparams;
+
+typedef struct grx_pocket grx_pocket;
+
+grx_status grx_pocket_create(grx_ctx *ctx, const grx_pocket_hparams *hp, grx_pocket **out);
+grx_status grx_pocket_destroy(grx_pocket *m);
+/* The flow LM's tensors by the names pockettts/model.go reads ("lm.blk.0.
+ * attn_qkv.weight", "lm.input.weight", "lm.bos", "lm.out_norm.weight",
+ * "lm.eos.weight", ...): transformer matrices as ggml Q8_0 rows, the rest
+ * float32; shapes checked. */
+grx_status grx_pocket_set_tensor(grx_pocket *m, const char *name, const void *data, size_t nbytes);
+/* Empty the caches (position 0). */
+grx_status grx_pocket_reset(grx_pocket *m);
+int grx_pocket_pos(const grx_pocket *m);
+/* flowLM.run (lm.go:164-170) of T rows of transformer input (the text
+ * prefix's embeddings, host float32 [T][d]) after the cached positions;
+ * out (d floats, may be NULL) receives out_norm of the last row. */
+grx_status grx_pocket_run(grx_pocket *m, const float *x, int T, float *out);
+/* n flowLM.step calls (lm.go:185-195) on the device, frame k fed latents[k]
+ * (host float32 [n][ldim]; NULL: the bos input every frame), no host round
+ * trip in between: outs (n x d, may be NULL) receives each frame's out_norm
+ * output and eos (n, may be NULL) its end-of-speech logit. */
+grx_status grx_pocket_frames(grx_pocket *m, const float *latents, int n, float *outs, float *eos);
+
 #ifdef __cplusplus
 }
 #endif
