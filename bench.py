@@ -57,6 +57,8 @@ def parse():
     p.add_argument("--decoder-steps", type=int, default=220,
                    help="greedy steps after the 4-token prompt (KV 4 -> 224)")
     p.add_argument("--no-decoder", action="store_true")
+    p.add_argument("--lm-frames", type=int, default=250, help="pocket-TTS-style frames after the 64-row prefix")
+    p.add_argument("--no-lm", action="store_true")
     p.add_argument("--copy-calibration", action="store_true",
                    help="only copy the ring's bytes device to device 3 times (reference reading for HBM counters)")
     return p.parse_args()
@@ -139,6 +141,54 @@ def decoder_bench(args) -> dict:
     res["cpu_baseline"] = {"value": round(steps / cpu_s, 2), "unit": "tokens/s", "cores": 1, "kind": "port",
                            "sample": f"the same {steps} decoder steps on the oracle (scalar C, 1 thread), {cpu_s:.2f} s"}
     dec.close()
+    return res
+
+
+def lm_bench(args) -> dict:
+    """pocket-TTS-style flow-LM transformer with random-init Q8_0 weights (d
+    1024, 16 heads, 6 layers, FFN 4096): a 64-row random-embedding text
+    prefix, then `lm_frames` teacher-forced latent frames (KV 64 -> 314),
+    all on the device; frames per second, outputs checked against the
+    oracle's, which is also the CPU baseline."""
+    import oracle
+    from gorelaxor_amd.pocket import PocketLM
+    from gorelaxor_amd.synth import POCKET_TTS_LM, pocket_inputs, pocket_model
+
+    hp = dict(POCKET_TTS_LM)
+    n = args.lm_frames
+    t = pocket_model(hp, seed=5)
+    x, lat = pocket_inputs(hp, n, prefix=64, seed=6)
+    lm = PocketLM(hp, t)
+    lm.run(x)
+    lm.frames(lat)  # warm: graph captured, caches warm
+    reps, times = 3, []
+    for _ in range(reps):
+        lm.reset()
+        t0 = time.perf_counter()
+        lm.run(x)
+        t1 = time.perf_counter()
+        outs, eos = lm.frames(lat)
+        times.append((t1 - t0, time.perf_counter() - t1))
+    prefix_s = min(a for a, _ in times)
+    frames_s = min(b for _, b in times)
+    res = {"frames_per_s": round(n / frames_s, 1), "ms_per_frame": round(frames_s / n * 1e3, 4),
+           "prefix_ms": round(prefix_s * 1e3, 3), "frames": n, "prefix_rows": 64, "runs": reps,
+           "shape": "d_model 1024, 16 heads, 6 layers, FFN 4096, KV 64->%d" % (64 + n)}
+    oracle.build()
+    ref = oracle.PocketOracle(hp, t)
+    t0 = time.perf_counter()
+    ref.run(x)
+    t1 = time.perf_counter()
+    ok = True
+    for k in range(n):
+        wo, we = ref.step(lat[k])
+        ok &= bool(np.array_equal(wo.view(np.uint32), outs[k].view(np.uint32))) and np.float32(we) == eos[k]
+    cpu_s = time.perf_counter() - t1
+    res["parity_bit_exact"] = ok
+    res["cpu_baseline"] = {"value": round(n / cpu_s, 2), "unit": "frames/s", "cores": 1, "kind": "port",
+                           "sample": f"the same {n} frames on the oracle (scalar C, 1 thread), {cpu_s:.2f} s; "
+                                     f"prefix {1e3 * (t1 - t0):.0f} ms"}
+    lm.close()
     return res
 
 
@@ -234,6 +284,9 @@ def main():
     if not args.no_decoder:
         out["decoder"] = decoder_bench(args)
         out["config"]["workload"] += "; whisper base.en-shaped greedy decoder (decoder.tokens_per_s)"
+    if not args.no_lm:
+        out["lm"] = lm_bench(args)
+        out["config"]["workload"] += "; pocket-TTS-style flow-LM frame loop (lm.frames_per_s)"
     print(json.dumps(out), flush=True)
 
 
