@@ -182,7 +182,7 @@ def lm_bench(args) -> dict:
     ok = True
     for k in range(n):
         wo, we = ref.step(lat[k])
-        ok &= bool(np.array_equal(wo.view(np.uint32), outs[k].view(np.uint32))) and np.float32(we) == eos[k]
+        ok = ok and bool(np.array_equal(wo.view(np.uint32), outs[k].view(np.uint32))) and bool(np.float32(we) == eos[k])
     cpu_s = time.perf_counter() - t1
     res["parity_bit_exact"] = ok
     res["cpu_baseline"] = {"value": round(n / cpu_s, 2), "unit": "frames/s", "cores": 1, "kind": "port",
