@@ -135,3 +135,55 @@ __device__ inline void seq_softmax(float *s, int n) {
     const float inv = __fdiv_rn(1.0f, __fadd_rn(sa, t));
     for (int j = 0; j < n; ++j) s[j] = __fmul_rn(s[j], inv);
 }
+
+// dot4f32avx (kernels_amd64.s:156-204) of one row on 16 lanes of a wave
+// (c = lane & 15): lane l < 8 runs chain A_l over elements 16i + l, lane 8+l
+// chain B_l over 16i + 8 + l; then S_l = A_l + B_l and HSUM by shuffles
+// within the 16 lanes.  Every lane of the 16 must call it with the same
+// row; the sum is returned in lane c == 0.  kk % 16 == 0.
+__device__ __forceinline__ float dot_avx16(const float *x, const float *w, int kk, int c) {
+    float acc = 0.f;
+    for (int i = c; i < kk; i += 16) acc = __fmaf_rn(x[i], w[i], acc);
+    const float other = __shfl_xor(acc, 8, 16);
+    const float S = __fadd_rn(c < 8 ? acc : other, c < 8 ? other : acc);
+    const float h4 = __fadd_rn(S, __shfl_xor(S, 4, 16));
+    const float h01 = __fadd_rn(h4, __shfl_xor(h4, 1, 16));
+    const float h23 = __shfl_xor(h01, 2, 16);
+    return kk > 0 ? __fadd_rn(h01, h23) : 0.f;
+}
+
+// dotF32Go (gemm.go:294-308) of one row on 4 lanes (c = lane & 3): lane c
+// keeps running sum s_c over elements c, c+4, ... below n &^ 3, lane 0 also
+// the tail; then ((s0 + s1) + s2) + s3 by shuffles.  Every lane of the 4
+// must call it; the sum is returned in lane c == 0.
+__device__ __forceinline__ float dot_go4(const float *x, const float *y, int n, int c) {
+    const int n4 = n & ~3;
+    float acc = 0.f;
+    for (int i = c; i < n4; i += 4) acc = __fadd_rn(acc, __fmul_rn(x[i], y[i]));
+    if (c == 0)
+        for (int i = n4; i < n; ++i) acc = __fadd_rn(acc, __fmul_rn(x[i], y[i]));
+    const float s1 = __shfl_xor(acc, 1, 4);
+    const float s2 = __shfl_xor(acc, 2, 4);
+    const float s3 = __shfl_xor(acc, 3, 4);
+    return __fadd_rn(__fadd_rn(__fadd_rn(acc, s1), s2), s3);
+}
+
+// Rows [r0, r0+rows) of one head's cached values (rows `ld` floats apart,
+// the head's hd values at `base`) into LDS vl[rows][hd], every thread of the
+// block issuing its loads at once (float4 when hd % 4 == 0).
+__device__ __forceinline__ void stage_rows(float *vl, const float *base, size_t ld, int r0, int rows, int hd) {
+    const int nt = blockDim.x, tid = threadIdx.x;
+    if ((hd & 3) == 0 && (ld & 3) == 0) {
+        const int n4 = rows * hd / 4;
+        for (int i = tid; i < n4; i += nt) {
+            const int j = (4 * i) / hd, e = (4 * i) % hd;
+            *reinterpret_cast<float4 *>(vl + 4 * i) =
+                *reinterpret_cast<const float4 *>(base + (size_t)(r0 + j) * ld + e);
+        }
+    } else {
+        for (int i = tid; i < rows * hd; i += nt) {
+            const int j = i / hd, e = i % hd;
+            vl[i] = base[(size_t)(r0 + j) * ld + e];
+        }
+    }
+}

@@ -55,11 +55,11 @@ __global__ void input_kernel(const float *__restrict__ w, const float *__restric
 template <bool QOUT>
 __global__ __launch_bounds__(kThreads) void attn_step_kernel(const float *__restrict__ q, const float *__restrict__ kc,
                                                             const float *__restrict__ vc, const int *__restrict__ pos,
-                                                            int d, int hd, float scale, float *__restrict__ att,
+                                                            int d, int hd, float scale, int rc, float *__restrict__ att,
                                                             int8_t *__restrict__ att_q, float *__restrict__ att_s) {
     extern __shared__ float sm[];
-    float *part = sm, *s = sm + 32;
     const int h = blockIdx.x, n = *pos + 1, tid = threadIdx.x;
+    float *part = sm, *s = sm + 32, *vl = sm + 32 + ((n + 3) & ~3);
     const float *qh = q + h * hd;
     const int n4 = n & ~3;
     for (int j = tid; j < n; j += blockDim.x) {
@@ -68,18 +68,33 @@ __global__ __launch_bounds__(kThreads) void attn_step_kernel(const float *__rest
     }
     __syncthreads();
     block_softmax(s, n, part);
+    // the values, rc rows at a time through LDS, summed in key order
     const int h8 = hd & ~7;
-    for (int e = tid; e < hd; e += blockDim.x) {
-        float o = 0.f;
-        const float *ve = vc + h * hd + e;
-        for (int j = 0; j < n; ++j) {
-            const float w = s[j];
-            if (w == 0.f) continue;
-            const float v = ve[(size_t)j * d];
-            o = e < h8 ? __fmaf_rn(w, v, o) : __fadd_rn(o, __fmul_rn(w, v));
+    float o = 0.f;
+    for (int r0 = 0; r0 < n; r0 += rc) {
+        const int rows = min(rc, n - r0);
+        stage_rows(vl, vc + h * hd, d, r0, rows, hd);
+        __syncthreads();
+        // keys of weight 0 are skipped (a select, so the loads of the
+        // unrolled loop issue together ahead of the dependent chain)
+        if (tid < h8) {
+#pragma unroll 16
+            for (int j = 0; j < rows; ++j) {
+                const float w = s[r0 + j], t = __fmaf_rn(w, vl[j * hd + tid], o);
+                o = w == 0.f ? o : t;
+            }
+        } else if (tid < hd) {
+#pragma unroll 16
+            for (int j = 0; j < rows; ++j) {
+                const float w = s[r0 + j], t = __fadd_rn(o, __fmul_rn(w, vl[j * hd + tid]));
+                o = w == 0.f ? o : t;
+            }
         }
-        att[h * hd + e] = o;
-        if constexpr (QOUT) quant32_store(o, att_q + h * hd + e, att_s + (h * hd + e) / 32, e & 31);
+        __syncthreads();
+    }
+    if (tid < hd) {
+        att[h * hd + tid] = o;
+        if constexpr (QOUT) quant32_store(o, att_q + h * hd + tid, att_s + (h * hd + tid) / 32, tid & 31);
     }
 }
 
@@ -162,7 +177,7 @@ __global__ __launch_bounds__(kThreads) void finish_kernel(const float *__restric
                                                           int advance, float *__restrict__ out_hist,
                                                           float *__restrict__ eos_hist) {
     __shared__ double red[16];
-    __shared__ float ov[8192];
+    __shared__ float ov[8192], ewl[8192], part4[4];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nw_ = blockDim.x >> 6;
     double ps = 0.0;
     for (int i = tid; i < d; i += blockDim.x) ps += (double)x[i];
@@ -191,10 +206,24 @@ __global__ __launch_bounds__(kThreads) void finish_kernel(const float *__restric
         o = __fadd_rn(__fmul_rn(o, nw[i]), nb[i]);
         out[i] = o;
         ov[i] = o;
+        ewl[i] = ew[i];
+    }
+    __syncthreads();
+    // dotF32Go (gemm.go:294-308): running sum t over elements t, t+4, ...
+    // below d &^ 3 (the tail into sum 0), each on its own thread
+    if (tid < 4) {
+        const int d4 = d & ~3;
+        float acc = 0.f;
+#pragma unroll 16
+        for (int i = tid; i < d4; i += 4) acc = __fadd_rn(acc, __fmul_rn(ov[i], ewl[i]));
+        if (tid == 0)
+            for (int i = d4; i < d; ++i) acc = __fadd_rn(acc, __fmul_rn(ov[i], ewl[i]));
+        part4[tid] = acc;
     }
     __syncthreads();
     if (tid == 0) {
-        eos_hist[f] = __fadd_rn(dot_go(ov, ew, d), eb);
+        const float dg = __fadd_rn(__fadd_rn(__fadd_rn(part4[0], part4[1]), part4[2]), part4[3]);
+        eos_hist[f] = __fadd_rn(dg, eb);
         if (advance) {
             *pos = *pos + 1;
             if (frame != nullptr) *frame = f + 1;
@@ -449,15 +478,17 @@ grx_status enqueue_frame(grx_pocket *m, hipStream_t st, const float *lat_base, c
     grx_status s;
     input_kernel<<<grx_ceil_div(d, kThreads), kThreads, 0, st>>>(m->input, lat_base, frame, d, hp.ldim, m->x);
     GRX_LAUNCHED("input_kernel");
-    const size_t smem = (32 + (size_t)hp.max_pos) * 4;
+    // LDS: 32 + max_pos scores, then value rows in chunks within 48 KiB
+    const int rc = max(1, min(hp.max_pos, (48 * 1024) / (hd * 4)));
+    const size_t smem = (32 + (((size_t)hp.max_pos + 3) & ~(size_t)3) + (size_t)rc * hd) * 4;
     for (int li = 0; li < hp.n_layer; ++li) {
         PLayer &L = m->L[li];
         if ((s = layer_product(m, st, L, 0, 0, 1, qatt)) != GRX_OK) return s;
         if (qatt)
-            attn_step_kernel<true><<<hp.heads, kThreads, smem, st>>>(m->q, L.k, L.v, m->pos, d, hd, scale, m->att,
+            attn_step_kernel<true><<<hp.heads, kThreads, smem, st>>>(m->q, L.k, L.v, m->pos, d, hd, scale, rc, m->att,
                                                                      m->att_q, m->att_s);
         else
-            attn_step_kernel<false><<<hp.heads, kThreads, smem, st>>>(m->q, L.k, L.v, m->pos, d, hd, scale, m->att,
+            attn_step_kernel<false><<<hp.heads, kThreads, smem, st>>>(m->q, L.k, L.v, m->pos, d, hd, scale, rc, m->att,
                                                                       nullptr, nullptr);
         GRX_LAUNCHED("attn_step_kernel");
         for (int ph = 1; ph < 4; ++ph)

@@ -22,6 +22,7 @@
 #include <stdlib.h>
 #include <string.h>
 
+#include <algorithm>
 #include <map>
 #include <string>
 #include <vector>
@@ -36,7 +37,7 @@ constexpr int kAttnThreads = 256;
 // ---------------------------------------------------------------- kernels
 
 constexpr int kBatch = 32;  // loads issued before their values are used
-constexpr int kBatchV = 64;  // the same for the cross values' longer chains
+constexpr int kBatchV = 96;  // the same for the cross values' longer chains (one batch at 1500 keys)
 
 // Causal self-attention of one head over the pos+1 cached positions
 // (decoder.go:70-87): scores dotF32Go(q, k_j)*sc, softmax, and
@@ -46,29 +47,30 @@ constexpr int kBatchV = 64;  // the same for the cross values' longer chains
 template <bool QOUT>
 __global__ __launch_bounds__(kAttnThreads) void self_attn_kernel(
     const float *__restrict__ q, const float *__restrict__ kc, const float *__restrict__ vc,
-    const int *__restrict__ pos, int st, int hd, float sc, float *__restrict__ att, int8_t *__restrict__ att_q,
+    const int *__restrict__ pos, int st, int hd, float sc, int rc, float *__restrict__ att, int8_t *__restrict__ att_q,
     float *__restrict__ att_s) {
     extern __shared__ float sm[];
-    float *part = sm;        // 32 floats
-    float *s = sm + 32;      // n_text_ctx floats
     const int h = blockIdx.x, n = *pos + 1, tid = threadIdx.x;
+    float *part = sm, *s = sm + 32, *vl = sm + 32 + ((n + 3) & ~3);
     const float *qh = q + h * hd;
     for (int j = tid; j < n; j += blockDim.x) s[j] = __fmul_rn(dot_go(qh, kc + (size_t)j * st + h * hd, hd), sc);
     __syncthreads();
     block_softmax(s, n, part);
-    for (int d = tid; d < hd; d += blockDim.x) {
-        float o = 0.f;
-        const float *vd = vc + h * hd + d;
-        for (int j0 = 0; j0 < n; j0 += kBatch) {
-            float vv[kBatch];
-#pragma unroll
-            for (int u = 0; u < kBatch; ++u) vv[u] = j0 + u < n ? vd[(size_t)(j0 + u) * st] : 0.f;
-#pragma unroll
-            for (int u = 0; u < kBatch; ++u)
-                if (j0 + u < n) o = __fadd_rn(o, __fmul_rn(s[j0 + u], vv[u]));
+    // the values, rc rows at a time through LDS, summed in position order
+    float o = 0.f;
+    for (int r0 = 0; r0 < n; r0 += rc) {
+        const int rows = min(rc, n - r0);
+        stage_rows(vl, vc + h * hd, st, r0, rows, hd);
+        __syncthreads();
+        if (tid < hd) {
+#pragma unroll 16
+            for (int j = 0; j < rows; ++j) o = __fadd_rn(o, __fmul_rn(s[r0 + j], vl[j * hd + tid]));
         }
-        att[h * hd + d] = o;
-        if constexpr (QOUT) quant32_store(o, att_q + h * hd + d, att_s + (h * hd + d) / 32, d & 31);
+        __syncthreads();
+    }
+    if (tid < hd) {
+        att[h * hd + tid] = o;
+        if constexpr (QOUT) quant32_store(o, att_q + h * hd + tid, att_s + (h * hd + tid) / 32, tid & 31);
     }
 }
 
@@ -350,7 +352,9 @@ grx_status enqueue_step(grx_whisper *m, hipStream_t stream) {
     const float sc = (float)(1.0 / sqrt((double)hd));
     const bool qatt = hd % 32 == 0;  // attention outputs are whole Q8_0 blocks per head
     grx_status s;
-    const size_t attn_smem = (32 + (size_t)hp.n_text_ctx) * 4, val_smem = (64 + (size_t)nctx) * 4;
+    const int rc = std::max(1, std::min(hp.n_text_ctx, (48 * 1024) / (hd * 4)));
+    const size_t attn_smem = (32 + (((size_t)hp.n_text_ctx + 3) & ~(size_t)3) + (size_t)rc * hd) * 4;
+    const size_t val_smem = (64 + (size_t)nctx) * 4;
     const int dg = qatt ? 32 : 4;
     for (int li = 0; li < hp.n_layer; ++li) {
         WLayer &L = m->L[li];
@@ -380,10 +384,10 @@ grx_status enqueue_step(grx_whisper *m, hipStream_t stream) {
         }
         if (qatt)
             self_attn_kernel<true><<<nh, kAttnThreads, attn_smem, stream>>>(m->q, L.self_k, L.self_v, m->pos, st, hd,
-                                                                           sc, m->att, m->att_q, m->att_s);
+                                                                           sc, rc, m->att, m->att_q, m->att_s);
         else
             self_attn_kernel<false><<<nh, kAttnThreads, attn_smem, stream>>>(m->q, L.self_k, L.self_v, m->pos, st, hd,
-                                                                            sc, m->att, nullptr, nullptr);
+                                                                            sc, rc, m->att, nullptr, nullptr);
         GRX_LAUNCHED("self_attn_kernel");
         auto out_proj = [&](grx_weight *w, const float *b) {  // x += att . W^T + b
             GemvArgs a = gemv_args(w);
