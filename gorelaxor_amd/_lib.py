@@ -71,12 +71,24 @@ SIGNATURES = {
     "grx_pocket_pos": (i32, [vp]),
     "grx_pocket_run": (i32, [vp, vp, i32, vp]),
     "grx_pocket_frames": (i32, [vp, vp, i32, vp, vp]),
+    "grx_conformer_create": (i32, [vp, vp, C.POINTER(vp)]),
+    "grx_conformer_destroy": (i32, [vp]),
+    "grx_conformer_set_tensor": (i32, [vp, C.c_char_p, vp, sz]),
+    "grx_conformer_frames_out": (i32, [vp, i32]),
+    "grx_conformer_encode": (i32, [vp, vp, i32, i32, vp, vp, vp]),
+    "grx_conformer_encode_dev": (i32, [vp, vp, i32, i32, vp, vp]),
 }
 
 
 class PocketHParams(C.Structure):
     """grx_pocket_hparams."""
     _fields_ = [(n, C.c_int) for n in ("d", "heads", "ff", "n_layer", "max_pos", "ldim")] + [("period", C.c_double)]
+
+
+class ConformerHParams(C.Structure):
+    """grx_conformer_hparams."""
+    _fields_ = [(n, C.c_int) for n in ("d", "heads", "layers", "dff", "conv_kernel", "sub_channels", "n_mels",
+                                       "xscaling", "conv_ln")]
 
 
 class WhisperHParams(C.Structure):

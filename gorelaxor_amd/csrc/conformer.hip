@@ -1,0 +1,1021 @@
+// conformer.hip - the FastConformer encoder forward (conformer/encoder.go of
+// github.com/xattribution/gorelaxor) with Q8_0 weights on one GPU, for a
+// batch of utterances of the same frame count.
+//
+// Every Linear is the int8 route (conformer/model.go:348-356 packs and drops
+// the rows of every encoder weight) on the matrix cores (q8_gemm.hip), its
+// activations rounded to Q8_0 by the kernel that produces them: the
+// LayerNorms, the pre-encoder convolutions, the attention output and the
+// depthwise convolution round their rows as they write them, and the first
+// feed-forward product rounds its SiLU output in its epilogue.  Residual
+// updates happen in the product epilogues.  Everything else - the
+// relative-position attention in the float route of MatMulF32, the GLU, the
+// depthwise convolution with its folded batch norm - is one kernel each and
+// restates the reference's order of operations, so every utterance's output
+// is bit-identical to the CPU restatement of encoder.go.
+//
+// Rows are [utterance][frame][channel]; the whole encode is one HIP graph
+// per (batch, frames) shape.
+#include <cmath>
+#include <cstring>
+#include <map>
+#include <string>
+#include <vector>
+
+#include "grx_float.h"
+#include "grx_internal.h"
+
+namespace {
+
+constexpr int kRowThreads = 256;
+constexpr int kAttnQ = 32;        // queries per attention block (encoder.go:211)
+constexpr int kAttnThreads = 512;
+
+// encoder.go:33-38 (subOut) for the non-causal pre-encoder, and the valid
+// length after s halvings.
+__host__ __device__ inline int sub_out(int n) { return (n - 1) / 2 + 1; }
+__device__ inline int stage_len(int valid, int s) {
+    int L = valid;
+    for (int i = 0; i < s; ++i) L = sub_out(L);
+    return L;
+}
+// The encoder's valid length L (encoder.go:166): min(L3, T), at least 0.
+__device__ inline int enc_len(int valid, int T) {
+    const int L = stage_len(valid, 3);
+    return max(0, min(L, T));
+}
+
+// Go's builtin max for float32 (NaN wins, +0 over -0).
+__device__ inline float go_max(float a, float b) {
+    if (a != a) return a;
+    if (b != b) return b;
+    if (a == b) return signbit(a) ? b : a;
+    return a > b ? a : b;
+}
+
+// ---------------------------------------------------------------- pre-encoder
+
+// conv0 (encoder.go:41-77) on the log-mel planes of B utterances ([b][mel]
+// [frame], frames past valid[b] read as 0), then maskRows and ReLU
+// (encoder.go:145-147): out [b][T1][F1][c].  Each output starts from the bias
+// and takes AddScaled of the nonzero taps in order: fma for the channels of
+// whole groups of eight, unfused for the rest.
+__global__ void sub_conv0_kernel(const float *__restrict__ mel, int B, int frames, int nm,
+                                 const int *__restrict__ valid, const float *__restrict__ w,
+                                 const float *__restrict__ bias, int c, int T1, int F1, float *__restrict__ out) {
+    const size_t total = (size_t)B * T1 * F1 * c;
+    for (size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x; idx < total;
+         idx += (size_t)gridDim.x * blockDim.x) {
+        const int ch = (int)(idx % c);
+        const size_t pos = idx / c;
+        const int f = (int)(pos % F1);
+        const int t = (int)((pos / F1) % T1);
+        const int b = (int)(pos / ((size_t)F1 * T1));
+        const int vb = valid[b];
+        if (t >= stage_len(vb, 1)) {
+            out[idx] = 0.f;
+            continue;
+        }
+        const int tv = min(frames, vb);
+        const float *mb = mel + (size_t)b * nm * frames;
+        const bool fm = ch < (c & ~7);
+        float o = bias[ch];
+        for (int kt = 0; kt < 3; ++kt) {
+            const int ti = 2 * t + kt - 1;
+            for (int kf = 0; kf < 3; ++kf) {
+                const int fi = 2 * f + kf - 1;
+                const float v = (ti >= 0 && ti < tv && fi >= 0 && fi < nm) ? mb[(size_t)fi * frames + ti] : 0.f;
+                if (v == 0.f) continue;
+                const float wv = w[(kt * 3 + kf) * c + ch];
+                o = fm ? __fmaf_rn(v, wv, o) : __fadd_rn(o, __fmul_rn(v, wv));
+            }
+        }
+        out[idx] = o < 0.f ? 0.f : o;
+    }
+}
+
+// dwConv2 (encoder.go:80-110) at halving s (input [b][T][F][c], one
+// workgroup of c threads per output position), rows from the stage's valid
+// length on zeroed, rounded to Q8_0 for the pointwise Linear that follows
+// (row (b, t1, f1) of c values).  RELU_IN: the input is the previous
+// pointwise output, read through maskRows and ReLU (encoder.go:152-153).
+template <bool RELU_IN>
+__global__ void sub_dwconv_kernel(const float *__restrict__ in, int T, int F, int c, const int *__restrict__ valid,
+                                  int s, const float *__restrict__ w, const float *__restrict__ bias, int T1, int F1,
+                                  int8_t *__restrict__ xq, float *__restrict__ xs) {
+    const int p = blockIdx.x, ch = threadIdx.x;
+    const int f1 = p % F1, t1 = (p / F1) % T1, b = p / (F1 * T1);
+    const int vb = valid[b];
+    const int Lin = stage_len(vb, s - 1), Lout = stage_len(vb, s);
+    float o = 0.f;
+    if (t1 < Lout) {
+        o = bias[ch];
+        for (int kt = 0; kt < 3; ++kt) {
+            const int ti = 2 * t1 + kt - 1;
+            if (ti < 0 || ti >= T) continue;
+            for (int kf = 0; kf < 3; ++kf) {
+                const int fi = 2 * f1 + kf - 1;
+                if (fi < 0 || fi >= F) continue;
+                float x = in[(((size_t)b * T + ti) * F + fi) * c + ch];
+                if constexpr (RELU_IN) x = ti < Lin ? (x < 0.f ? 0.f : x) : 0.f;
+                o = __fadd_rn(o, __fmul_rn(w[(kt * 3 + kf) * c + ch], x));
+            }
+        }
+    }
+    quant32_store(o, xq + (size_t)p * c + ch, xs + (size_t)p * (c / 32) + ch / 32, ch & 31);
+}
+
+// The last pointwise output through maskRows and ReLU, flattened [t][c*F+f]
+// (encoder.go:158-166) and rounded to Q8_0 for the output Linear: one
+// workgroup per (utterance, frame).
+__global__ void sub_flatten_kernel(const float *__restrict__ y, int T, int F, int c, const int *__restrict__ valid,
+                                   int8_t *__restrict__ xq, float *__restrict__ xs) {
+    const int row = blockIdx.x, t = row % T, b = row / T;
+    const int L = stage_len(valid[b], 3);
+    const int K = c * F;
+    for (int i = threadIdx.x; i < K; i += blockDim.x) {
+        const int ch = i / F, f = i % F;
+        const float v = y[((size_t)row * F + f) * c + ch];
+        const float r = t < L ? (v < 0.f ? 0.f : v) : 0.f;
+        quant32_store(r, xq + (size_t)row * K + i, xs + (size_t)row * (K / 32) + i / 32, i & 31);
+    }
+}
+
+// ---------------------------------------------------------------- LayerNorm rows
+
+// kern.LayerNorm of one row (internal/kern/mathx.go:55-75) held in LDS: the
+// float64 sums (exact in practice, so their order does not show), mean and
+// inv rounded to float32, y = (v-mean)*inv*w + b rounded step by step.
+__device__ void ln_row(float *v, int n, const float *w, const float *bb, double *red) {
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nw = blockDim.x >> 6;
+    double ps = 0.0;
+    for (int i = tid; i < n; i += blockDim.x) ps += (double)v[i];
+    for (int o = 32; o > 0; o >>= 1) ps += __shfl_xor(ps, o);
+    if (lane == 0) red[wave] = ps;
+    __syncthreads();
+    double sum = 0.0;
+    for (int i = 0; i < nw; ++i) sum += red[i];
+    const float mean = (float)(sum / (double)n);
+    double pv = 0.0;
+    for (int i = tid; i < n; i += blockDim.x) {
+        const double d = (double)__fsub_rn(v[i], mean);
+        pv += d * d;
+    }
+    for (int o = 32; o > 0; o >>= 1) pv += __shfl_xor(pv, o);
+    __syncthreads();
+    if (lane == 0) red[wave] = pv;
+    __syncthreads();
+    double vs = 0.0;
+    for (int i = 0; i < nw; ++i) vs += red[i];
+    const float inv = (float)(1.0 / sqrt(vs / (double)n + 1e-5));
+    for (int i = tid; i < n; i += blockDim.x) {
+        float t = __fsub_rn(v[i], mean);
+        t = __fmul_rn(t, inv);
+        t = __fmul_rn(t, w[i]);
+        v[i] = __fadd_rn(t, bb[i]);
+    }
+    __syncthreads();
+}
+
+// One workgroup per row of x [rows][n].  OUT: x = LN(x; w1, b1) written
+// back first (a block's norm_out, encoder.go:426).  Q: the row (after OUT,
+// LN(x; w2, b2)) rounded to Q8_0 into xq [rows][n], xs [rows][n/32].
+template <bool OUT, bool Q>
+__global__ __launch_bounds__(kRowThreads) void ln_rows_kernel(float *__restrict__ x, int n,
+                                                              const float *__restrict__ w1,
+                                                              const float *__restrict__ b1,
+                                                              const float *__restrict__ w2,
+                                                              const float *__restrict__ b2,
+                                                              int8_t *__restrict__ xq, float *__restrict__ xs) {
+    extern __shared__ float row[];
+    __shared__ double red[16];
+    const int r = blockIdx.x, tid = threadIdx.x;
+    float *xr = x + (size_t)r * n;
+    for (int i = tid; i < n; i += blockDim.x) row[i] = xr[i];
+    __syncthreads();
+    ln_row(row, n, w1, b1, red);
+    if constexpr (OUT) {
+        for (int i = tid; i < n; i += blockDim.x) xr[i] = row[i];
+        if constexpr (Q) ln_row(row, n, w2, b2, red);
+    }
+    if constexpr (Q) {
+        // n % 32 == 0 and the stride is a multiple of 32: whole blocks per 32 lanes
+        for (int i = tid; i < n; i += blockDim.x)
+            quant32_store(row[i], xq + (size_t)r * n + i, xs + (size_t)r * (n / 32) + i / 32, i & 31);
+    }
+}
+
+// ---------------------------------------------------------------- attention
+
+// Relative-position multi-head self-attention (encoder.go:259-330) of one
+// (utterance, head, block of 32 queries), keys limited to the utterance's
+// valid length L (queries at or past L see none).  qkv holds the q|k|v
+// Linear outputs [row][3D]; pp the block's projected position table
+// [2T-1][ldp].  qu = q + pos_u and qv = q + pos_v in float32; scores =
+// MatMulF32(qu, k) and bd = MatMulF32(qv, pp rows jlo..), each in the route
+// MatMulF32 takes for nq rows; row i adds bd shifted by nq-1-i, scales,
+// softmax by ExpSub/Scale; the output MatMulF32(p, v^T) is rounded to Q8_0
+// per 32 values of the head's slice for the out Linear.
+__global__ __launch_bounds__(kAttnThreads) void conf_attn_kernel(
+    const float *__restrict__ qkv, const float *__restrict__ pp, int ldp, const float *__restrict__ pos_u,
+    const float *__restrict__ pos_v, const int *__restrict__ valid, int T, int D, int hd, float scale,
+    int8_t *__restrict__ xq, float *__restrict__ xs) {
+    extern __shared__ float sm[];
+    const int blk = blockIdx.x, h = blockIdx.y, b = blockIdx.z, tid = threadIdx.x, nt = blockDim.x;
+    const int L = enc_len(valid[b], T);
+    const int q0 = blk * kAttnQ, q1 = min(T, q0 + kAttnQ), nq = q1 - q0;
+    const int khi = min(T, L);
+    const int k0 = 0, k1 = q0 < L ? khi : 0, nk = k1 - k0;
+    const size_t ld = 3 * (size_t)D;
+    const float *base = qkv + (size_t)b * T * ld;
+    const int nqb = hd / 32;
+    if (nk <= 0) {  // encoder.go:290-293: the block's output rows are zero
+        for (int g = tid >> 5; g < nq * nqb; g += nt >> 5) {
+            const int i = g / nqb, bb = g % nqb;
+            const size_t row = (size_t)b * T + q0 + i;
+            quant32_store(0.f, xq + row * D + h * hd + bb * 32 + (tid & 31), xs + row * (D / 32) + (h * hd) / 32 + bb,
+                          tid & 31);
+        }
+        return;
+    }
+    const int np = nq + nk - 1, jlo = T - 1 - (q1 - 1) + k0;
+    const int sq = hd + 1, sS = nk | 1, sB = np | 1;
+    float *qu = sm, *qv = sm + kAttnQ * sq, *S = qv + kAttnQ * sq, *BD = S + kAttnQ * sS;
+    float *rmx = BD + kAttnQ * sB, *rinv = rmx + kAttnQ;
+    for (int e = tid; e < nq * hd; e += nt) {
+        const int i = e / hd, j = e % hd;
+        const float q = base[(size_t)(q0 + i) * ld + h * hd + j];
+        qu[i * sq + j] = __fadd_rn(q, pos_u[h * hd + j]);
+        qv[i * sq + j] = __fadd_rn(q, pos_v[h * hd + j]);
+    }
+    __syncthreads();
+    for (int e = tid; e < nq * nk; e += nt) {
+        const int i = e % nq, kk = e / nq;
+        S[i * sS + kk] = matmul_f32_one(qu + i * sq, base + (size_t)(k0 + kk) * ld + D + h * hd, 1, hd, i, nq, kk, nk);
+    }
+    for (int e = tid; e < nq * np; e += nt) {
+        const int i = e % nq, jj = e / nq;
+        BD[i * sB + jj] = matmul_f32_one(qv + i * sq, pp + (size_t)(jlo + jj) * ldp + h * hd, 1, hd, i, nq, jj, np);
+    }
+    __syncthreads();
+    // the scores of row i: (s + bd[i][nq-1-i+kk]) * scale inside [lo, hi),
+    // -inf outside; the row maximum by one wave per row
+    const int lane = tid & 63, wave = tid >> 6, nw = nt >> 6;
+    for (int i = wave; i < nq; i += nw) {
+        const int hi = q0 + i < L ? khi : 0;
+        float mx = -__builtin_inff();
+        for (int kk = lane; kk < nk; kk += 64) {
+            const int kx = k0 + kk;
+            float v;
+            if (kx < 0 || kx >= hi) {
+                v = -__builtin_inff();
+            } else {
+                v = __fmul_rn(__fadd_rn(S[i * sS + kk], BD[i * sB + nq - 1 - i + kk]), scale);
+                mx = go_max(mx, v);
+            }
+            S[i * sS + kk] = v;
+        }
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) mx = go_max(mx, __shfl_xor(mx, o));
+        if (lane == 0) rmx[i] = mx;
+    }
+    __syncthreads();
+    // ExpSub: EXP8 below nk &^ 7, the scalar expf past it; rows whose
+    // maximum is -inf are cleared instead (encoder.go:312-315)
+    const int n8 = nk & ~7;
+    for (int e = tid; e < nq * nk; e += nt) {
+        const int i = e / nk, kk = e % nk;
+        const float mx = rmx[i];
+        float &v = S[i * sS + kk];
+        if (mx == -__builtin_inff())
+            v = 0.f;
+        else {
+            const float d = __fsub_rn(v, mx);
+            v = kk < n8 ? grx_exp8(d) : grx_expf_go(d);
+        }
+    }
+    __syncthreads();
+    // the eight lane sums of expSubAVX, HSUM, plus the tail's own sum; one
+    // wave per row, lanes 0..7 a lane sum each, lane 8 the tail
+    for (int i = wave; i < nq; i += nw) {
+        float acc = 0.f;
+        if (lane < 8) {
+            for (int kk = lane; kk < n8; kk += 8) acc = __fadd_rn(acc, S[i * sS + kk]);
+        } else if (lane == 8) {
+            for (int kk = n8; kk < nk; ++kk) acc = __fadd_rn(acc, S[i * sS + kk]);
+        }
+        float a8[8];
+#pragma unroll
+        for (int l = 0; l < 8; ++l) a8[l] = __shfl(acc, l);
+        const float tail = __shfl(acc, 8);
+        if (lane == 0) {
+            const float sa = n8 > 0 ? hsum8(a8) : 0.f;
+            rinv[i] = __fdiv_rn(1.0f, __fadd_rn(sa, tail));
+        }
+    }
+    __syncthreads();
+    for (int e = tid; e < nq * nk; e += nt) {
+        const int i = e / nk, kk = e % nk;
+        if (rmx[i] != -__builtin_inff()) S[i * sS + kk] = __fmul_rn(S[i * sS + kk], rinv[i]);
+    }
+    __syncthreads();
+    // out = MatMulF32(p, v^T): m = nq, n = hd, k = nk; v^T's row e is the
+    // value column e (elements ld apart)
+    float *O = qu;  // [nq][sq], qu is no longer needed
+    for (int e = tid; e < nq * hd; e += nt) {
+        const int i = e % nq, ee = e / nq;
+        O[i * sq + ee] = matmul_f32_one(S + i * sS, base + (size_t)k0 * ld + 2 * D + h * hd + ee, ld, nk, i, nq, ee, hd);
+    }
+    __syncthreads();
+    for (int g = tid >> 5; g < nq * nqb; g += nt >> 5) {
+        const int i = g / nqb, bb = g % nqb, e = tid & 31;
+        const size_t row = (size_t)b * T + q0 + i;
+        quant32_store(O[i * sq + bb * 32 + e], xq + row * D + h * hd + bb * 32 + e,
+                      xs + row * (D / 32) + (h * hd) / 32 + bb, e);
+    }
+}
+
+size_t attn_smem_floats(int T, int hd) {
+    const int nk = T, np = kAttnQ + T - 1;
+    return (size_t)2 * kAttnQ * (hd + 1) + (size_t)kAttnQ * (nk | 1) + (size_t)kAttnQ * (np | 1) + 2 * kAttnQ;
+}
+
+// ---------------------------------------------------------------- convolution module
+
+// GLU of the pointwise output (encoder.go:350-361): g = a * sigmoid(b) with
+// sigmoid(v) = 1/(1 + expf(-v)) (the scalar expf), rows at or past the
+// utterance's valid length zeroed.
+__global__ void conf_glu_kernel(const float *__restrict__ a, int R, int T, int D, const int *__restrict__ valid,
+                                float *__restrict__ g) {
+    const size_t total = (size_t)R * D;
+    for (size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x; idx < total;
+         idx += (size_t)gridDim.x * blockDim.x) {
+        const int c = (int)(idx % D);
+        const int row = (int)(idx / D), t = row % T, b = row / T;
+        float v = 0.f;
+        if (t < enc_len(valid[b], T)) {
+            const float *ar = a + (size_t)row * 2 * D;
+            const float sg = __fdiv_rn(1.0f, __fadd_rn(1.0f, grx_expf_go(-ar[D + c])));
+            v = __fmul_rn(ar[c], sg);
+        }
+        g[idx] = v;
+    }
+}
+
+// The centred depthwise convolution (encoder.go:362-385: from the bias, w*x
+// unfused over the taps in range, in order), the folded batch norm r*s + b
+// (unfused) or the LayerNorm (LN), SiLU of the AVX route, rounded to Q8_0
+// for pointwise2.  One workgroup per row.
+template <bool LN>
+__global__ __launch_bounds__(kRowThreads) void conf_dwconv_kernel(const float *__restrict__ g, int T, int D, int K,
+                                                                  const float *__restrict__ w,
+                                                                  const float *__restrict__ dwb,
+                                                                  const float *__restrict__ cn_w,
+                                                                  const float *__restrict__ cn_b,
+                                                                  int8_t *__restrict__ xq, float *__restrict__ xs) {
+    extern __shared__ float row[];
+    __shared__ double red[16];
+    const int r = blockIdx.x, t = r % T, b = r / T, tid = threadIdx.x;
+    const int padL = (K - 1) / 2;
+    const float *gb = g + (size_t)b * T * D;
+    for (int c = tid; c < D; c += blockDim.x) {
+        float o = dwb != nullptr ? dwb[c] : 0.f;
+        for (int j = 0; j < K; ++j) {
+            const int ti = t + j - padL;
+            if (ti < 0 || ti >= T) continue;
+            o = __fadd_rn(o, __fmul_rn(w[(size_t)j * D + c], gb[(size_t)ti * D + c]));
+        }
+        if constexpr (!LN) o = __fadd_rn(__fmul_rn(o, cn_w[c]), cn_b[c]);
+        row[c] = o;
+    }
+    __syncthreads();
+    if constexpr (LN) ln_row(row, D, cn_w, cn_b, red);
+    for (int c = tid; c < D; c += blockDim.x) {
+        const float v = row[c];
+        const float s = __fdiv_rn(v, __fadd_rn(grx_exp8(__fsub_rn(0.0f, v)), 1.0f));
+        quant32_store(s, xq + (size_t)r * D + c, xs + (size_t)r * (D / 32) + c / 32, c & 31);
+    }
+}
+
+}  // namespace
+
+// ---------------------------------------------------------------- host side
+
+struct CFF {
+    float *norm_w = nullptr, *norm_b = nullptr, *b1 = nullptr, *b2 = nullptr;
+    grx_weight *w1 = nullptr, *w2 = nullptr;
+};
+
+struct CBlock {
+    CFF ff1, ff2;
+    float *norm_attn_w, *norm_attn_b, *qkv_b, *out_b, *pos_u, *pos_v;
+    float *norm_conv_w, *norm_conv_b, *pw1_b, *pw2_b, *dw, *dw_b, *cn_w, *cn_b, *norm_out_w, *norm_out_b;
+    grx_weight *qkv = nullptr, *out = nullptr, *pw1 = nullptr, *pw2 = nullptr;
+};
+
+struct grx_conformer {
+    grx_ctx *ctx = nullptr;
+    grx_conformer_hparams hp{};
+    std::map<std::string, std::vector<uint8_t>> host;
+    bool ready = false;
+    std::vector<void *> allocs;        // weights and constants
+    std::vector<void *> work;          // shape-dependent buffers
+    // pre-encoder
+    float *w0, *b0, *w2, *b2, *w5, *b5, *b3, *b6, *outb;
+    grx_weight *w3 = nullptr, *w6 = nullptr, *wout = nullptr;
+    std::vector<CBlock> blk;
+    grx_weight *pos_all = nullptr;  // every block's linear_pos, [layers*d][d]
+    // shape-dependent state
+    int B = 0, frames = 0, T = 0;
+    float *mel = nullptr, *sub0 = nullptr, *suby = nullptr, *x = nullptr, *qkv = nullptr, *pp = nullptr;
+    float *conv = nullptr, *glu = nullptr, *pos = nullptr;
+    int8_t *xq = nullptr, *fq = nullptr, *pos_q = nullptr;  // fq: the rounded SiLU output of W1
+    float *xs = nullptr, *fs = nullptr, *pos_s = nullptr;
+    int *valid = nullptr;
+    int *valid_host = nullptr;  // pinned
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t exec = nullptr;
+};
+
+namespace {
+
+struct CExpect {
+    std::string name;
+    size_t bytes;
+    bool optional;
+};
+
+size_t q8b(size_t rows, size_t cols) { return rows * (cols / 32) * 34; }
+
+int sub_F(const grx_conformer_hparams &hp) { return sub_out(sub_out(sub_out(hp.n_mels))); }
+
+// The tensors loadEncoder reads (conformer/model.go:370-422), with sizes.
+std::vector<CExpect> cexpected(const grx_conformer_hparams &hp) {
+    const size_t d = hp.d, c = hp.sub_channels, ff = hp.dff, K = hp.conv_kernel;
+    const size_t cF = c * sub_F(hp);
+    std::vector<CExpect> e;
+    const std::string pe = "enc.pre_encode.";
+    for (const char *n : {"conv.0", "conv.2", "conv.5"}) {
+        e.push_back({pe + n + ".weight", c * 9 * 4, false});
+        e.push_back({pe + n + ".bias", c * 4, false});
+    }
+    for (const char *n : {"conv.3", "conv.6"}) {
+        e.push_back({pe + n + ".weight", q8b(c, c), false});
+        e.push_back({pe + n + ".bias", c * 4, false});
+    }
+    e.push_back({pe + "out.weight", q8b(d, cF), false});
+    e.push_back({pe + "out.bias", d * 4, false});
+    for (int i = 0; i < hp.layers; ++i) {
+        const std::string p = "enc.blocks." + std::to_string(i) + ".";
+        for (const char *f : {"ff1", "ff2"}) {
+            e.push_back({p + "norm_" + f + ".weight", d * 4, false});
+            e.push_back({p + "norm_" + f + ".bias", d * 4, false});
+            e.push_back({p + f + ".linear1.weight", q8b(ff, d), false});
+            e.push_back({p + f + ".linear1.bias", ff * 4, true});
+            e.push_back({p + f + ".linear2.weight", q8b(d, ff), false});
+            e.push_back({p + f + ".linear2.bias", d * 4, true});
+        }
+        for (const char *n : {"norm_attn", "norm_conv", "norm_out"}) {
+            e.push_back({p + n + ".weight", d * 4, false});
+            e.push_back({p + n + ".bias", d * 4, false});
+        }
+        for (const char *n : {"linear_q", "linear_k", "linear_v", "linear_out"}) {
+            e.push_back({p + "attn." + n + ".weight", q8b(d, d), false});
+            e.push_back({p + "attn." + n + ".bias", d * 4, true});
+        }
+        e.push_back({p + "attn.linear_pos.weight", q8b(d, d), false});
+        e.push_back({p + "attn.pos_bias_u", d * 4, false});
+        e.push_back({p + "attn.pos_bias_v", d * 4, false});
+        // the pointwise convolutions: Q8_0, or float16 rounded at load
+        e.push_back({p + "conv.pointwise1.weight", 0, false});
+        e.push_back({p + "conv.pointwise1.bias", 2 * d * 4, true});
+        e.push_back({p + "conv.pointwise2.weight", 0, false});
+        e.push_back({p + "conv.pointwise2.bias", d * 4, true});
+        e.push_back({p + "conv.depthwise.weight", d * K * 4, false});
+        e.push_back({p + "conv.depthwise.bias", d * 4, true});
+        e.push_back({p + "conv.bn.weight", d * 4, false});
+        e.push_back({p + "conv.bn.bias", d * 4, false});
+        e.push_back({p + "conv.bn.running_mean", d * 4, hp.conv_ln != 0});
+        e.push_back({p + "conv.bn.running_var", d * 4, hp.conv_ln != 0});
+    }
+    return e;
+}
+
+grx_status calloc_dev(std::vector<void *> &list, size_t bytes, void **out) {
+    void *p = nullptr;
+    GRX_HIP(hipMalloc(&p, bytes > 0 ? bytes : 16));
+    list.push_back(p);
+    *out = p;
+    return GRX_OK;
+}
+
+template <typename T>
+grx_status calloc_t(std::vector<void *> &list, size_t count, T **out) {
+    return calloc_dev(list, count * sizeof(T), reinterpret_cast<void **>(out));
+}
+
+grx_status upload(grx_conformer *m, const void *data, size_t bytes, float **out) {
+    grx_status s = calloc_t(m->allocs, bytes / 4, out);
+    if (s != GRX_OK) return s;
+    GRX_HIP(hipMemcpy(*out, data, bytes, hipMemcpyHostToDevice));
+    return GRX_OK;
+}
+
+// A named float vector (nullptr when optional and absent).
+grx_status cvec(grx_conformer *m, const std::string &name, float **out) {
+    *out = nullptr;
+    auto it = m->host.find(name);
+    if (it == m->host.end()) return GRX_OK;
+    return upload(m, it->second.data(), it->second.size(), out);
+}
+
+// transposeTaps (conformer/model.go:147-159): [c][taps] to [taps][c].
+std::vector<float> transpose_taps(const std::vector<uint8_t> &raw, int c, int taps) {
+    const float *w = reinterpret_cast<const float *>(raw.data());
+    std::vector<float> out((size_t)c * taps);
+    for (int i = 0; i < c; ++i)
+        for (int j = 0; j < taps; ++j) out[(size_t)j * c + i] = w[(size_t)i * taps + j];
+    return out;
+}
+
+// IEEE half to float, exactly.
+float half_to_float(uint16_t h) {
+    const uint32_t sign = (uint32_t)(h >> 15) << 31;
+    int e = (h >> 10) & 0x1f;
+    uint32_t f = h & 0x3ff, bits;
+    if (e == 0x1f) {
+        bits = sign | 0x7f800000u | (f << 13);
+    } else if (e == 0) {
+        if (f == 0) {
+            bits = sign;
+        } else {
+            e = 1;
+            while (!(f & 0x400)) {
+                f <<= 1;
+                --e;
+            }
+            f &= 0x3ff;
+            bits = sign | ((uint32_t)(e + 112) << 23) | (f << 13);
+        }
+    } else {
+        bits = sign | ((uint32_t)(e + 112) << 23) | (f << 13);
+    }
+    float out;
+    memcpy(&out, &bits, 4);
+    return out;
+}
+
+// A pointwise-convolution weight: Q8_0 rows as they are, or float16
+// widened and rounded by Weight.ToQ8 (conformer/model.go:397-402).
+grx_status pointwise_weight(grx_conformer *m, const std::string &name, int rows, int cols, grx_weight **out) {
+    const auto &raw = m->host.at(name);
+    const size_t n = (size_t)rows * cols;
+    if (raw.size() == q8b(rows, cols)) return grx_weight_q8_create(m->ctx, rows, cols, raw.data(), raw.size(), out);
+    if (raw.size() != n * 2) return grx_fail(GRX_ESIZE, "tensor %s is neither Q8_0 nor float16 %dx%d", name.c_str(), rows, cols);
+    std::vector<float> v(n);
+    const uint16_t *h = reinterpret_cast<const uint16_t *>(raw.data());
+    for (size_t i = 0; i < n; ++i) v[i] = half_to_float(h[i]);
+    std::vector<uint8_t> q(q8b(rows, cols));
+    grx_status s = grx_to_q8(m->ctx, rows, cols, v.data(), q.data());
+    if (s != GRX_OK) return s;
+    return grx_weight_q8_create(m->ctx, rows, cols, q.data(), q.size(), out);
+}
+
+grx_status cfinalize(grx_conformer *m) {
+    if (m->ready) return GRX_OK;
+    const grx_conformer_hparams &hp = m->hp;
+    for (const CExpect &e : cexpected(hp))
+        if (!e.optional && !m->host.count(e.name)) return grx_fail(GRX_ESTATE, "the model has no tensor %s", e.name.c_str());
+    GRX_HIP(hipSetDevice(m->ctx->device));
+    grx_status s;
+    const int d = hp.d, c = hp.sub_channels, cF = c * sub_F(hp), K = hp.conv_kernel;
+    const std::string pe = "enc.pre_encode.";
+    {
+        struct {
+            const char *n;
+            float **w, **b;
+        } taps[] = {{"conv.0", &m->w0, &m->b0}, {"conv.2", &m->w2, &m->b2}, {"conv.5", &m->w5, &m->b5}};
+        for (auto &t : taps) {
+            std::vector<float> tw = transpose_taps(m->host.at(pe + t.n + ".weight"), c, 9);
+            if ((s = upload(m, tw.data(), tw.size() * 4, t.w)) != GRX_OK) return s;
+            if ((s = cvec(m, pe + t.n + ".bias", t.b)) != GRX_OK) return s;
+        }
+    }
+    auto mat = [&](const std::string &n, int rows, int cols, grx_weight **w) {
+        const auto &t = m->host.at(n);
+        return grx_weight_q8_create(m->ctx, rows, cols, t.data(), t.size(), w);
+    };
+    if ((s = mat(pe + "conv.3.weight", c, c, &m->w3)) != GRX_OK) return s;
+    if ((s = mat(pe + "conv.6.weight", c, c, &m->w6)) != GRX_OK) return s;
+    if ((s = mat(pe + "out.weight", d, cF, &m->wout)) != GRX_OK) return s;
+    if ((s = cvec(m, pe + "conv.3.bias", &m->b3)) != GRX_OK) return s;
+    if ((s = cvec(m, pe + "conv.6.bias", &m->b6)) != GRX_OK) return s;
+    if ((s = cvec(m, pe + "out.bias", &m->outb)) != GRX_OK) return s;
+    m->blk.resize(hp.layers);
+    std::vector<uint8_t> pos_cat;
+    for (int i = 0; i < hp.layers; ++i) {
+        CBlock &B = m->blk[i];
+        const std::string p = "enc.blocks." + std::to_string(i) + ".";
+        for (int f = 0; f < 2; ++f) {
+            CFF &F = f == 0 ? B.ff1 : B.ff2;
+            const std::string n = f == 0 ? "ff1" : "ff2";
+            if ((s = cvec(m, p + "norm_" + n + ".weight", &F.norm_w)) != GRX_OK) return s;
+            if ((s = cvec(m, p + "norm_" + n + ".bias", &F.norm_b)) != GRX_OK) return s;
+            if ((s = mat(p + n + ".linear1.weight", hp.dff, d, &F.w1)) != GRX_OK) return s;
+            if ((s = mat(p + n + ".linear2.weight", d, hp.dff, &F.w2)) != GRX_OK) return s;
+            if ((s = cvec(m, p + n + ".linear1.bias", &F.b1)) != GRX_OK) return s;
+            if ((s = cvec(m, p + n + ".linear2.bias", &F.b2)) != GRX_OK) return s;
+        }
+        {  // q, k and v share their input: one weight of 3d rows, missing biases 0
+            std::vector<uint8_t> cat;
+            std::vector<float> bias(3 * (size_t)d, 0.0f);
+            int j = 0;
+            for (const char *n : {"linear_q", "linear_k", "linear_v"}) {
+                const auto &t = m->host.at(p + "attn." + n + ".weight");
+                cat.insert(cat.end(), t.begin(), t.end());
+                auto it = m->host.find(p + "attn." + n + ".bias");
+                if (it != m->host.end()) memcpy(bias.data() + (size_t)j * d, it->second.data(), (size_t)d * 4);
+                ++j;
+            }
+            if ((s = grx_weight_q8_create(m->ctx, 3 * d, d, cat.data(), cat.size(), &B.qkv)) != GRX_OK) return s;
+            if ((s = upload(m, bias.data(), bias.size() * 4, &B.qkv_b)) != GRX_OK) return s;
+        }
+        {
+            const auto &t = m->host.at(p + "attn.linear_pos.weight");
+            pos_cat.insert(pos_cat.end(), t.begin(), t.end());
+        }
+        if ((s = mat(p + "attn.linear_out.weight", d, d, &B.out)) != GRX_OK) return s;
+        if ((s = pointwise_weight(m, p + "conv.pointwise1.weight", 2 * d, d, &B.pw1)) != GRX_OK) return s;
+        if ((s = pointwise_weight(m, p + "conv.pointwise2.weight", d, d, &B.pw2)) != GRX_OK) return s;
+        struct {
+            const char *n;
+            float **v;
+        } vecs[] = {{"norm_attn.weight", &B.norm_attn_w}, {"norm_attn.bias", &B.norm_attn_b},
+                    {"attn.linear_out.bias", &B.out_b},   {"attn.pos_bias_u", &B.pos_u},
+                    {"attn.pos_bias_v", &B.pos_v},        {"norm_conv.weight", &B.norm_conv_w},
+                    {"norm_conv.bias", &B.norm_conv_b},   {"conv.pointwise1.bias", &B.pw1_b},
+                    {"conv.pointwise2.bias", &B.pw2_b},   {"conv.depthwise.bias", &B.dw_b},
+                    {"norm_out.weight", &B.norm_out_w},   {"norm_out.bias", &B.norm_out_b}};
+        for (auto &v : vecs)
+            if ((s = cvec(m, p + v.n, v.v)) != GRX_OK) return s;
+        {
+            std::vector<float> tw = transpose_taps(m->host.at(p + "conv.depthwise.weight"), d, K);
+            if ((s = upload(m, tw.data(), tw.size() * 4, &B.dw)) != GRX_OK) return s;
+        }
+        const float *gw = reinterpret_cast<const float *>(m->host.at(p + "conv.bn.weight").data());
+        const float *gb = reinterpret_cast<const float *>(m->host.at(p + "conv.bn.bias").data());
+        if (hp.conv_ln) {
+            if ((s = upload(m, gw, (size_t)d * 4, &B.cn_w)) != GRX_OK) return s;
+            if ((s = upload(m, gb, (size_t)d * 4, &B.cn_b)) != GRX_OK) return s;
+        } else {  // conformer/model.go:408-418: the batch norm folded to scale and bias
+            const float *mean = reinterpret_cast<const float *>(m->host.at(p + "conv.bn.running_mean").data());
+            const float *vr = reinterpret_cast<const float *>(m->host.at(p + "conv.bn.running_var").data());
+            std::vector<float> sw(d), sb(d);
+            for (int j = 0; j < d; ++j) {
+                const float sj = (float)((double)gw[j] / std::sqrt((double)vr[j] + 1e-5));
+                sw[j] = sj;
+                const float ms = mean[j] * sj;
+                sb[j] = gb[j] - ms;
+            }
+            if ((s = upload(m, sw.data(), (size_t)d * 4, &B.cn_w)) != GRX_OK) return s;
+            if ((s = upload(m, sb.data(), (size_t)d * 4, &B.cn_b)) != GRX_OK) return s;
+        }
+    }
+    if ((s = grx_weight_q8_create(m->ctx, hp.layers * d, d, pos_cat.data(), pos_cat.size(), &m->pos_all)) != GRX_OK)
+        return s;
+    m->host.clear();
+    m->ready = true;
+    return GRX_OK;
+}
+
+void free_work(grx_conformer *m) {
+    if (m->exec) (void)hipGraphExecDestroy(m->exec);
+    if (m->graph) (void)hipGraphDestroy(m->graph);
+    m->exec = nullptr;
+    m->graph = nullptr;
+    for (void *p : m->work) (void)hipFree(p);
+    m->work.clear();
+    if (m->valid_host) (void)hipHostFree(m->valid_host);
+    m->valid_host = nullptr;
+    m->B = m->frames = m->T = 0;
+}
+
+// relPosEmb (encoder.go:171-191) of n positions: [2n-1][d].
+std::vector<float> rel_pos(int n, int d) {
+    std::vector<float> out((size_t)(2 * n - 1) * d);
+    for (int i = 0; i < 2 * n - 1; ++i) {
+        const double pos = (double)(n - 1 - i);
+        float *row = out.data() + (size_t)i * d;
+        for (int j = 0; j < d; j += 2) {
+            const float div = (float)std::exp((double)j * -(std::log(10000.0) / (double)d));
+            const double a = (double)((float)pos * div);
+            row[j] = (float)std::sin(a);
+            if (j + 1 < d) row[j + 1] = (float)std::cos(a);
+        }
+    }
+    return out;
+}
+
+// Buffers for B utterances of `frames` mel frames, the position table of
+// their T and its rounding.
+grx_status cshape(grx_conformer *m, int B, int frames) {
+    if (m->B == B && m->frames == frames) return GRX_OK;
+    free_work(m);
+    const grx_conformer_hparams &hp = m->hp;
+    const int d = hp.d, c = hp.sub_channels, nm = hp.n_mels;
+    const int T1 = sub_out(frames), F1 = sub_out(nm), T2 = sub_out(T1), F2 = sub_out(F1), T = sub_out(T2),
+              F3 = sub_out(F2);
+    const size_t R = (size_t)B * T;
+    {  // the attention block's LDS: past 64 KiB it has to be asked for
+        const size_t need = attn_smem_floats(T, d / hp.heads) * 4;
+        int lim = 0;
+        GRX_HIP(hipDeviceGetAttribute(&lim, hipDeviceAttributeMaxSharedMemoryPerBlock, m->ctx->device));
+        if (need > (size_t)std::max(lim, 160 * 1024) || need > 160 * 1024)
+            return grx_fail(GRX_ESIZE, "%d frames give %d encoder frames, more than the attention kernel holds",
+                            frames, T);
+        if (need > 64 * 1024 &&
+            hipFuncSetAttribute((const void *)conf_attn_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                (int)need) != hipSuccess)
+            return grx_fail(GRX_ESIZE, "%d encoder frames need %zu bytes of LDS per attention block", T, need);
+    }
+    grx_status s;
+    auto &w = m->work;
+    if ((s = calloc_t(w, (size_t)B * nm * frames, &m->mel)) != GRX_OK) return s;
+    if ((s = calloc_t(w, (size_t)B * T1 * F1 * c, &m->sub0)) != GRX_OK) return s;
+    if ((s = calloc_t(w, (size_t)B * T2 * F2 * c, &m->suby)) != GRX_OK) return s;
+    // rounded activations: the largest row set of any product
+    size_t qn = std::max({(size_t)B * T2 * F2 * c, R * (size_t)c * F3, R * (size_t)hp.dff, R * 2 * (size_t)d});
+    if ((s = calloc_t(w, qn, &m->xq)) != GRX_OK) return s;
+    if ((s = calloc_t(w, qn / 32, &m->xs)) != GRX_OK) return s;
+    if ((s = calloc_t(w, R * hp.dff, &m->fq)) != GRX_OK) return s;
+    if ((s = calloc_t(w, R * hp.dff / 32, &m->fs)) != GRX_OK) return s;
+    if ((s = calloc_t(w, R * d, &m->x)) != GRX_OK) return s;
+    if ((s = calloc_t(w, R * 3 * d, &m->qkv)) != GRX_OK) return s;
+    if ((s = calloc_t(w, (size_t)(2 * T - 1) * hp.layers * d, &m->pp)) != GRX_OK) return s;
+    if ((s = calloc_t(w, R * 2 * d, &m->conv)) != GRX_OK) return s;
+    if ((s = calloc_t(w, R * d, &m->glu)) != GRX_OK) return s;
+    if ((s = calloc_t(w, (size_t)(2 * T - 1) * d, &m->pos)) != GRX_OK) return s;
+    if ((s = calloc_t(w, (size_t)(2 * T - 1) * d, &m->pos_q)) != GRX_OK) return s;
+    if ((s = calloc_t(w, (size_t)(2 * T - 1) * d / 32, &m->pos_s)) != GRX_OK) return s;
+    if ((s = calloc_t(w, B, &m->valid)) != GRX_OK) return s;
+    GRX_HIP(hipHostMalloc((void **)&m->valid_host, (size_t)B * sizeof(int), hipHostMallocDefault));
+    std::vector<float> pos = rel_pos(T, d);
+    GRX_HIP(hipMemcpy(m->pos, pos.data(), pos.size() * 4, hipMemcpyHostToDevice));
+    if ((s = grx_quant_act_dev(m->ctx, m->pos_q, m->pos_s, m->pos, d, 2 * T - 1, d)) != GRX_OK) return s;
+    GRX_HIP(hipStreamSynchronize(m->ctx->stream));
+    m->B = B;
+    m->frames = frames;
+    m->T = T;
+    return GRX_OK;
+}
+
+unsigned grid_for(size_t n) { return (unsigned)std::min<size_t>((n + 255) / 256, 1u << 20); }
+
+// The whole encode (encoder.go:432-489) of m->B utterances from m->mel into
+// m->x, enqueued on the stream.
+grx_status enqueue_encode(grx_conformer *m, hipStream_t st) {
+    const grx_conformer_hparams &hp = m->hp;
+    const int B = m->B, frames = m->frames, d = hp.d, c = hp.sub_channels, nm = hp.n_mels, T = m->T;
+    const int T1 = sub_out(frames), F1 = sub_out(nm), T2 = sub_out(T1), F2 = sub_out(F1), F3 = sub_out(F2);
+    const int R = B * T, hd = d / hp.heads, cF = c * F3;
+    grx_status s;
+    // pre-encoder (encoder.go:123-167)
+    sub_conv0_kernel<<<grid_for((size_t)B * T1 * F1 * c), 256, 0, st>>>(m->mel, B, frames, nm, m->valid, m->w0, m->b0,
+                                                                       c, T1, F1, m->sub0);
+    GRX_LAUNCHED("sub_conv0_kernel");
+    sub_dwconv_kernel<false><<<B * T2 * F2, c, 0, st>>>(m->sub0, T1, F1, c, m->valid, 2, m->w2, m->b2, T2, F2, m->xq,
+                                                        m->xs);
+    GRX_LAUNCHED("sub_dwconv_kernel");
+    if ((s = grx_gemm_q8_launch(st, m->w3, m->xq, m->xs, B * T2 * F2, m->b3, m->suby, c)) != GRX_OK) return s;
+    sub_dwconv_kernel<true><<<B * T * F3, c, 0, st>>>(m->suby, T2, F2, c, m->valid, 3, m->w5, m->b5, T, F3, m->xq,
+                                                      m->xs);
+    GRX_LAUNCHED("sub_dwconv_kernel");
+    if ((s = grx_gemm_q8_launch(st, m->w6, m->xq, m->xs, B * T * F3, m->b6, m->sub0, c)) != GRX_OK) return s;
+    sub_flatten_kernel<<<R, 256, 0, st>>>(m->sub0, T, F3, c, m->valid, m->xq, m->xs);
+    GRX_LAUNCHED("sub_flatten_kernel");
+    {  // output Linear, then xscale (encoder.go:445-451)
+        GemmOut o;
+        o.y = m->x;
+        o.ldc = d;
+        if (hp.xscaling) {
+            o.epi = GRX_GEMM_SCALE;
+            o.scale = (float)std::sqrt((double)d);
+        }
+        if ((s = grx_gemm_q8_launch_ex(st, m->wout, m->xq, m->xs, R, m->outb, o)) != GRX_OK) return s;
+    }
+    // every block's position projection at once: pp [2T-1][layers*d]
+    if ((s = grx_gemm_q8_launch(st, m->pos_all, m->pos_q, m->pos_s, 2 * T - 1, nullptr, m->pp, hp.layers * d)) !=
+        GRX_OK)
+        return s;
+    const size_t row_smem = (size_t)d * 4;
+    // the first block's feed-forward LayerNorm
+    ln_rows_kernel<false, true><<<R, kRowThreads, row_smem, st>>>(m->x, d, m->blk[0].ff1.norm_w, m->blk[0].ff1.norm_b,
+                                                                  nullptr, nullptr, m->xq, m->xs);
+    GRX_LAUNCHED("ln_rows_kernel");
+    const size_t attn_smem = attn_smem_floats(T, hd) * 4;
+    const float scale = (float)(1.0 / std::sqrt((double)hd));
+    const int nblk = (T + kAttnQ - 1) / kAttnQ;
+    for (int i = 0; i < hp.layers; ++i) {
+        const CBlock &Bk = m->blk[i];
+        auto ff_pair = [&](const CFF &F) -> grx_status {
+            // x += 0.5 * W2 . SiLU(W1 . LN(x)) (encoder.go:244-251); LN(x) is in xq
+            GemmOut o1;
+            o1.epi = GRX_GEMM_SILU_Q;
+            o1.yq = m->fq;
+            o1.ys = m->fs;
+            grx_status r = grx_gemm_q8_launch_ex(st, F.w1, m->xq, m->xs, R, F.b1, o1);
+            if (r != GRX_OK) return r;
+            GemmOut o2;
+            o2.y = m->x;
+            o2.ldc = d;
+            o2.epi = GRX_GEMM_AXPY_HALF;
+            return grx_gemm_q8_launch_ex(st, F.w2, m->fq, m->fs, R, F.b2, o2);
+        };
+        if ((s = ff_pair(Bk.ff1)) != GRX_OK) return s;
+        // attention (encoder.go:259-330)
+        ln_rows_kernel<false, true><<<R, kRowThreads, row_smem, st>>>(m->x, d, Bk.norm_attn_w, Bk.norm_attn_b, nullptr,
+                                                                      nullptr, m->xq, m->xs);
+        GRX_LAUNCHED("ln_rows_kernel");
+        if ((s = grx_gemm_q8_launch(st, Bk.qkv, m->xq, m->xs, R, Bk.qkv_b, m->qkv, 3 * d)) != GRX_OK) return s;
+        conf_attn_kernel<<<dim3(nblk, hp.heads, B), kAttnThreads, attn_smem, st>>>(
+            m->qkv, m->pp + (size_t)i * d, hp.layers * d, Bk.pos_u, Bk.pos_v, m->valid, T, d, hd, scale, m->xq, m->xs);
+        GRX_LAUNCHED("conf_attn_kernel");
+        {
+            GemmOut o;
+            o.y = m->x;
+            o.ldc = d;
+            o.epi = GRX_GEMM_ADD;
+            if ((s = grx_gemm_q8_launch_ex(st, Bk.out, m->xq, m->xs, R, Bk.out_b, o)) != GRX_OK) return s;
+        }
+        // convolution module (encoder.go:343-397)
+        ln_rows_kernel<false, true><<<R, kRowThreads, row_smem, st>>>(m->x, d, Bk.norm_conv_w, Bk.norm_conv_b, nullptr,
+                                                                      nullptr, m->xq, m->xs);
+        GRX_LAUNCHED("ln_rows_kernel");
+        if ((s = grx_gemm_q8_launch(st, Bk.pw1, m->xq, m->xs, R, Bk.pw1_b, m->conv, 2 * d)) != GRX_OK) return s;
+        conf_glu_kernel<<<grid_for((size_t)R * d), 256, 0, st>>>(m->conv, R, T, d, m->valid, m->glu);
+        GRX_LAUNCHED("conf_glu_kernel");
+        if (hp.conv_ln)
+            conf_dwconv_kernel<true><<<R, kRowThreads, row_smem, st>>>(m->glu, T, d, hp.conv_kernel, Bk.dw, Bk.dw_b,
+                                                                       Bk.cn_w, Bk.cn_b, m->xq, m->xs);
+        else
+            conf_dwconv_kernel<false><<<R, kRowThreads, row_smem, st>>>(m->glu, T, d, hp.conv_kernel, Bk.dw, Bk.dw_b,
+                                                                        Bk.cn_w, Bk.cn_b, m->xq, m->xs);
+        GRX_LAUNCHED("conf_dwconv_kernel");
+        {
+            GemmOut o;
+            o.y = m->x;
+            o.ldc = d;
+            o.epi = GRX_GEMM_ADD;
+            if ((s = grx_gemm_q8_launch_ex(st, Bk.pw2, m->xq, m->xs, R, Bk.pw2_b, o)) != GRX_OK) return s;
+        }
+        // second feed-forward, then norm_out (and the next block's first LayerNorm)
+        ln_rows_kernel<false, true><<<R, kRowThreads, row_smem, st>>>(m->x, d, Bk.ff2.norm_w, Bk.ff2.norm_b, nullptr,
+                                                                      nullptr, m->xq, m->xs);
+        GRX_LAUNCHED("ln_rows_kernel");
+        if ((s = ff_pair(Bk.ff2)) != GRX_OK) return s;
+        if (i + 1 < hp.layers) {
+            const CFF &N = m->blk[i + 1].ff1;
+            ln_rows_kernel<true, true><<<R, kRowThreads, row_smem, st>>>(m->x, d, Bk.norm_out_w, Bk.norm_out_b,
+                                                                         N.norm_w, N.norm_b, m->xq, m->xs);
+        } else {
+            ln_rows_kernel<true, false><<<R, kRowThreads, row_smem, st>>>(m->x, d, Bk.norm_out_w, Bk.norm_out_b,
+                                                                          nullptr, nullptr, nullptr, nullptr);
+        }
+        GRX_LAUNCHED("ln_rows_kernel");
+    }
+    return GRX_OK;
+}
+
+grx_status run_encode(grx_conformer *m) {
+    hipStream_t st = m->ctx->stream;
+    static const bool no_graph = getenv("GRX_NO_GRAPH") != nullptr;
+    if (no_graph) return enqueue_encode(m, st);
+    if (!m->exec) {
+        GRX_HIP(hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal));
+        grx_status s = enqueue_encode(m, st);
+        hipGraph_t g = nullptr;
+        hipError_t e = hipStreamEndCapture(st, &g);
+        if (s != GRX_OK) {
+            if (g) (void)hipGraphDestroy(g);
+            return s;
+        }
+        if (e != hipSuccess) return grx_fail(GRX_EDEVICE, "graph capture: %s", hipGetErrorString(e));
+        m->graph = g;
+        GRX_HIP(hipGraphInstantiate(&m->exec, g, nullptr, nullptr, 0));
+    }
+    GRX_HIP(hipGraphLaunch(m->exec, st));
+    return GRX_OK;
+}
+
+grx_status check_valid(const grx_conformer *m, const int *valid, int batch, int frames) {
+    (void)m;
+    for (int b = 0; b < batch; ++b)
+        if (valid[b] < 1 || valid[b] > frames)
+            return grx_fail(GRX_EINVAL, "utterance %d: valid frames %d outside [1, %d]", b, valid[b], frames);
+    return GRX_OK;
+}
+
+}  // namespace
+
+extern "C" grx_status grx_conformer_create(grx_ctx *ctx, const grx_conformer_hparams *hp, grx_conformer **out) {
+    if (!ctx || !hp || !out) return grx_fail(GRX_EINVAL, "grx_conformer_create: NULL argument");
+    *out = nullptr;
+    if (hp->d <= 0 || hp->heads <= 0 || hp->layers <= 0 || hp->dff <= 0 || hp->conv_kernel <= 0 ||
+        hp->sub_channels <= 0 || hp->n_mels <= 0)
+        return grx_fail(GRX_EINVAL, "grx_conformer_create: every size must be positive");
+    if (hp->d % 32 != 0 || hp->dff % 32 != 0 || hp->d % hp->heads != 0 || (hp->d / hp->heads) % 32 != 0)
+        return grx_fail(GRX_ESIZE, "d %d, dff %d, heads %d: sizes must split into 32-value blocks per head", hp->d,
+                        hp->dff, hp->heads);
+    if (hp->sub_channels % 32 != 0 || hp->sub_channels > 1024 || hp->d > 8192 || hp->conv_kernel % 2 != 1)
+        return grx_fail(GRX_ESIZE, "sub_channels %d (a multiple of 32 up to 1024), d %d or kernel %d unsupported",
+                        hp->sub_channels, hp->d, hp->conv_kernel);
+    if ((hp->sub_channels * sub_F(*hp)) % 32 != 0)
+        return grx_fail(GRX_ESIZE, "the pre-encoder output (%d values) is not whole Q8_0 blocks",
+                        hp->sub_channels * sub_F(*hp));
+    grx_conformer *m = new grx_conformer();
+    m->ctx = ctx;
+    m->hp = *hp;
+    *out = m;
+    return GRX_OK;
+}
+
+extern "C" grx_status grx_conformer_destroy(grx_conformer *m) {
+    if (!m) return GRX_OK;
+    GRX_HIP(hipSetDevice(m->ctx->device));
+    free_work(m);
+    for (void *p : m->allocs) (void)hipFree(p);
+    grx_weight *ws[] = {m->w3, m->w6, m->wout, m->pos_all};
+    for (grx_weight *w : ws) grx_weight_destroy(w);
+    for (CBlock &B : m->blk) {
+        grx_weight *bw[] = {B.ff1.w1, B.ff1.w2, B.ff2.w1, B.ff2.w2, B.qkv, B.out, B.pw1, B.pw2};
+        for (grx_weight *w : bw) grx_weight_destroy(w);
+    }
+    delete m;
+    return GRX_OK;
+}
+
+extern "C" grx_status grx_conformer_set_tensor(grx_conformer *m, const char *name, const void *data, size_t nbytes) {
+    if (!m || !name || (!data && nbytes)) return grx_fail(GRX_EINVAL, "grx_conformer_set_tensor: NULL argument");
+    if (m->ready) return grx_fail(GRX_ESTATE, "grx_conformer_set_tensor: the model is in use already");
+    for (const CExpect &e : cexpected(m->hp)) {
+        if (e.name != name) continue;
+        if (e.bytes != 0 && nbytes != e.bytes)
+            return grx_fail(GRX_ESIZE, "tensor %s has the wrong shape (%zu bytes, want %zu)", name, nbytes, e.bytes);
+        const uint8_t *p = static_cast<const uint8_t *>(data);
+        m->host[name] = std::vector<uint8_t>(p, p + nbytes);
+        return GRX_OK;
+    }
+    return grx_fail(GRX_EINVAL, "the model has a tensor this program doesn't know: %s", name);
+}
+
+extern "C" int grx_conformer_frames_out(const grx_conformer *m, int frames) {
+    (void)m;
+    return frames < 1 ? 0 : sub_out(sub_out(sub_out(frames)));
+}
+
+extern "C" grx_status grx_conformer_encode_dev(grx_conformer *m, const float *mel, int batch, int frames,
+                                               const int *valid, float *out) {
+    if (!m || !mel || !valid || !out) return grx_fail(GRX_EINVAL, "grx_conformer_encode_dev: NULL argument");
+    if (batch < 1 || frames < 1) return grx_fail(GRX_EINVAL, "grx_conformer_encode_dev: batch %d, frames %d", batch, frames);
+    grx_status s;
+    if ((s = check_valid(m, valid, batch, frames)) != GRX_OK) return s;
+    GRX_HIP(hipSetDevice(m->ctx->device));
+    if ((s = cfinalize(m)) != GRX_OK) return s;
+    if ((s = cshape(m, batch, frames)) != GRX_OK) return s;
+    hipStream_t st = m->ctx->stream;
+    const size_t mel_n = (size_t)batch * m->hp.n_mels * frames;
+    memcpy(m->valid_host, valid, (size_t)batch * sizeof(int));
+    GRX_HIP(hipMemcpyAsync(m->valid, m->valid_host, (size_t)batch * sizeof(int), hipMemcpyHostToDevice, st));
+    GRX_HIP(hipMemcpyAsync(m->mel, mel, mel_n * 4, hipMemcpyDeviceToDevice, st));
+    if ((s = run_encode(m)) != GRX_OK) return s;
+    GRX_HIP(hipMemcpyAsync(out, m->x, (size_t)batch * m->T * m->hp.d * 4, hipMemcpyDeviceToDevice, st));
+    // the pinned valid lengths are read by the copy above: wait before reuse
+    GRX_HIP(hipStreamSynchronize(st));
+    return GRX_OK;
+}
+
+extern "C" grx_status grx_conformer_encode(grx_conformer *m, const float *mel, int batch, int frames, const int *valid,
+                                           float *out, int *lens) {
+    if (!m || !mel || !valid || !out) return grx_fail(GRX_EINVAL, "grx_conformer_encode: NULL argument");
+    if (batch < 1 || frames < 1) return grx_fail(GRX_EINVAL, "grx_conformer_encode: batch %d, frames %d", batch, frames);
+    grx_status s;
+    if ((s = check_valid(m, valid, batch, frames)) != GRX_OK) return s;
+    GRX_HIP(hipSetDevice(m->ctx->device));
+    if ((s = cfinalize(m)) != GRX_OK) return s;
+    if ((s = cshape(m, batch, frames)) != GRX_OK) return s;
+    hipStream_t st = m->ctx->stream;
+    const size_t mel_n = (size_t)batch * m->hp.n_mels * frames;
+    memcpy(m->valid_host, valid, (size_t)batch * sizeof(int));
+    GRX_HIP(hipMemcpyAsync(m->valid, m->valid_host, (size_t)batch * sizeof(int), hipMemcpyHostToDevice, st));
+    GRX_HIP(hipMemcpyAsync(m->mel, mel, mel_n * 4, hipMemcpyHostToDevice, st));
+    if ((s = run_encode(m)) != GRX_OK) return s;
+    GRX_HIP(hipMemcpyAsync(out, m->x, (size_t)batch * m->T * m->hp.d * 4, hipMemcpyDeviceToHost, st));
+    GRX_HIP(hipStreamSynchronize(st));
+    if (lens)
+        for (int b = 0; b < batch; ++b) {
+            int L = valid[b];
+            for (int k = 0; k < 3; ++k) L = sub_out(L);
+            lens[b] = std::max(0, std::min(L, m->T));
+        }
+    return GRX_OK;
+}

@@ -187,3 +187,63 @@ __device__ __forceinline__ void stage_rows(float *vl, const float *base, size_t 
         }
     }
 }
+
+// dotF32Go, dot4f32avx and dotF32x4 with the second operand's elements sb
+// apart (the first's contiguous): the same orders as dot_go, dot_avx, dot_x4.
+__device__ __forceinline__ float dot_go_s(const float *x, const float *y, size_t sb, int n) {
+    float s0 = 0.f, s1 = 0.f, s2 = 0.f, s3 = 0.f;
+    int i = 0;
+    for (; i + 4 <= n; i += 4) {
+        s0 = __fadd_rn(s0, __fmul_rn(x[i], y[i * sb]));
+        s1 = __fadd_rn(s1, __fmul_rn(x[i + 1], y[(i + 1) * sb]));
+        s2 = __fadd_rn(s2, __fmul_rn(x[i + 2], y[(i + 2) * sb]));
+        s3 = __fadd_rn(s3, __fmul_rn(x[i + 3], y[(i + 3) * sb]));
+    }
+    for (; i < n; i++) s0 = __fadd_rn(s0, __fmul_rn(x[i], y[i * sb]));
+    return __fadd_rn(__fadd_rn(__fadd_rn(s0, s1), s2), s3);
+}
+
+__device__ __forceinline__ float dot_avx_s(const float *x, const float *w, size_t sb, int kk) {
+    float A[8], B[8];
+#pragma unroll
+    for (int l = 0; l < 8; ++l) A[l] = B[l] = 0.f;
+    for (int c = 0; c < kk; c += 16) {
+#pragma unroll
+        for (int l = 0; l < 8; ++l) {
+            A[l] = __fmaf_rn(x[c + l], w[(c + l) * sb], A[l]);
+            B[l] = __fmaf_rn(x[c + 8 + l], w[(c + 8 + l) * sb], B[l]);
+        }
+    }
+    float S[8];
+#pragma unroll
+    for (int l = 0; l < 8; ++l) S[l] = __fadd_rn(A[l], B[l]);
+    return hsum8(S);
+}
+
+__device__ __forceinline__ float dot_x4_s(const float *x, const float *w, size_t sb, int k) {
+    const int kk = k & ~15;
+    float o = kk > 0 ? dot_avx_s(x, w, sb, kk) : 0.f;
+    if (kk < k) o = __fadd_rn(o, dot_go_s(x + kk, w + kk * sb, sb, k - kk));
+    return o;
+}
+
+// One output (row r of m, column j of n) of MatMulF32 (internal/kern/
+// kern.go:205-212 over gemm.go:116-259) with no bias: for m > 16 the rows in
+// whole groups of six take k6x16avx (kernels_amd64.s:5-88: acc = fma(a, b,
+// acc) over k in chunks of 256, each chunk's acc added to C from 0), the
+// other rows gemvRows (dotF32x4 for whole groups of four columns, dotF32Go
+// for the rest).  a is contiguous; b's elements are sb apart.
+__device__ __forceinline__ float matmul_f32_one(const float *a, const float *b, size_t sb, int k, int r, int m, int j,
+                                                int n) {
+    if (m > 16 && r < m / 6 * 6) {
+        float c = 0.f;
+        for (int k0 = 0; k0 < k; k0 += 256) {
+            const int kn = min(256, k - k0);
+            float acc = 0.f;
+            for (int kk = 0; kk < kn; ++kk) acc = __fmaf_rn(a[k0 + kk], b[(size_t)(k0 + kk) * sb], acc);
+            c = __fadd_rn(acc, c);
+        }
+        return c;
+    }
+    return j < (n & ~3) ? dot_x4_s(a, b, sb, k) : dot_go_s(a, b, sb, k);
+}

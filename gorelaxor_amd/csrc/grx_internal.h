@@ -264,6 +264,18 @@ grx_status grx_gemv_launch(hipStream_t st, int m, int pro, int epi, const GemvAr
 // The many-row product on the matrix cores (q8_gemm.hip), same results.
 grx_status grx_gemm_q8_launch(hipStream_t st, const grx_weight *w, const int8_t *xq, const float *xs, int m,
                               const float *bias, float *y, int ldc);
+// Epilogues of the matrix-core product (q8_gemm.hip).
+enum { GRX_GEMM_STORE = 0, GRX_GEMM_ADD = 1, GRX_GEMM_AXPY_HALF = 2, GRX_GEMM_SCALE = 3, GRX_GEMM_SILU_Q = 4 };
+struct GemmOut {
+    float *y = nullptr;  // [m][ldc] (STORE writes it, ADD/AXPY_HALF update it)
+    int ldc = 0;
+    int epi = GRX_GEMM_STORE;
+    float scale = 1.0f;     // SCALE
+    int8_t *yq = nullptr;   // SILU_Q: [m][rows] int8
+    float *ys = nullptr;    //         [m][rows/32] scales
+};
+grx_status grx_gemm_q8_launch_ex(hipStream_t st, const grx_weight *w, const int8_t *xq, const float *xs, int m,
+                                 const float *bias, const GemmOut &o);
 // Fewest activation rows that take the matrix-core product (GRX_GEMM_MIN_M
 // overrides it, for tests).
 int grx_gemm_min_m(void);

@@ -29,12 +29,21 @@ typedef int v4i __attribute__((ext_vector_type(4)));
 
 constexpr int kGemmBU = 2;  // blocks whose loads are issued before use
 
+// What the epilogue does with each finished output c (GemmOut::epi):
+//   STORE      y = c
+//   ADD        y = y + c                      (kern.Add of the product)
+//   AXPY_HALF  y = fma(0.5, c, y)             (AddScaled(y, c, 0.5), whole groups of 8)
+//   SCALE      y = c * scale
+//   SILU_Q     SiLU(c) of the AVX route (c / (EXP8(0 - c) + 1)), rounded to
+//              Q8_0 per 32 outputs into yq [m][rows], ys [m][rows/32]
+template <int EPI>
 __global__ __launch_bounds__(256) void gemm_q8_mfma_kernel(const int8_t *__restrict__ qs,
                                                            const uint16_t *__restrict__ ds, int rows, int nb,
                                                            const int8_t *__restrict__ xq,
                                                            const float *__restrict__ xs, int m,
                                                            const float *__restrict__ bias, float *__restrict__ y,
-                                                           int ldc) {
+                                                           int ldc, float scale, int8_t *__restrict__ yq,
+                                                           float *__restrict__ ys) {
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int tile = blockIdx.y;                     // weight rows 64*tile ..
@@ -103,25 +112,95 @@ __global__ __launch_bounds__(256) void gemm_q8_mfma_kernel(const int8_t *__restr
     for (; b + kGemmBU <= nb; b += kGemmBU) fold(std::integral_constant<int, kGemmBU>{}, b);
     for (; b < nb; ++b) fold(std::integral_constant<int, 1>{}, b);
 
+    if constexpr (EPI == GRX_GEMM_SILU_Q) {
+        // The 64 columns of the tile are two Q8_0 blocks: block j holds
+        // columns 16*(2j) + li and 16*(2j+1) + li of the 16 lanes sharing lk,
+        // so a row's block maximum is four xor-shuffles within those lanes.
+        const int nr = rows / GRX_QK;
 #pragma unroll
-    for (int s = 0; s < 4; ++s) {
-        const int n = tile * 64 + 16 * s + li;
-        if (n >= rows) continue;
+        for (int j = 0; j < 2; ++j) {
+            const int n0 = tile * 64 + 32 * j;
+            const bool col_ok = n0 < rows;  // rows % 32 == 0: whole blocks
 #pragma unroll
-        for (int r = 0; r < 4; ++r)
-            if (drow_ok[r]) y[(size_t)drow[r] * ldc + n] = c[s][r];
+            for (int r = 0; r < 4; ++r) {
+                float v[2];
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+                    const float x = c[2 * j + h][r];
+                    v[h] = __fdiv_rn(x, __fadd_rn(grx_exp8(__fsub_rn(0.0f, x)), 1.0f));
+                }
+                const float a0 = fabsf(v[0]), a1 = fabsf(v[1]);
+                float amax = a0 > 0.0f ? a0 : 0.0f;
+                amax = a1 > amax ? a1 : amax;
+#pragma unroll
+                for (int o = 8; o > 0; o >>= 1) {
+                    const float t = __shfl_xor(amax, o, 16);
+                    amax = t > amax ? t : amax;
+                }
+                const float id = amax != 0.0f ? __fdiv_rn(127.0f, amax) : 0.0f;
+                if (col_ok && drow_ok[r]) {
+                    int8_t *qrow = yq + (size_t)drow[r] * rows + n0;
+#pragma unroll
+                    for (int h = 0; h < 2; ++h) {
+                        float q = rintf(__fmul_rn(v[h], id));
+                        q = fminf(fmaxf(q, -128.0f), 127.0f);
+                        qrow[16 * h + li] = (int8_t)(int)q;
+                    }
+                    if (li == 0) ys[(size_t)drow[r] * nr + n0 / GRX_QK] = __fmul_rn(amax, grx_bits_f32(0x3c010204u));
+                }
+            }
+        }
+    } else {
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+            const int n = tile * 64 + 16 * s + li;
+            if (n >= rows) continue;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                if (!drow_ok[r]) continue;
+                float *yp = y + (size_t)drow[r] * ldc + n;
+                if constexpr (EPI == GRX_GEMM_STORE) *yp = c[s][r];
+                if constexpr (EPI == GRX_GEMM_ADD) *yp = __fadd_rn(*yp, c[s][r]);
+                if constexpr (EPI == GRX_GEMM_AXPY_HALF) *yp = __fmaf_rn(0.5f, c[s][r], *yp);
+                if constexpr (EPI == GRX_GEMM_SCALE) *yp = __fmul_rn(c[s][r], scale);
+            }
+        }
     }
 }
 
 }  // namespace
 
+grx_status grx_gemm_q8_launch_ex(hipStream_t st, const grx_weight *w, const int8_t *xq, const float *xs, int m,
+                                 const float *bias, const GemmOut &o) {
+    if (m <= 0 || w->rows == 0) return GRX_OK;
+    if (o.epi == GRX_GEMM_SILU_Q && w->rows % GRX_QK != 0)
+        return grx_fail(GRX_ESIZE, "rounded product output needs rows %% 32 == 0 (rows %d)", w->rows);
+    dim3 grid(grx_ceil_div(m, 64), w->tiles);
+#define GRX_GEMM_CASE(E)                                                                                    \
+    case E:                                                                                                 \
+        gemm_q8_mfma_kernel<E><<<grid, 256, 0, st>>>(w->qs, w->ds, w->rows, w->nb, xq, xs, m, bias, o.y, o.ldc, \
+                                                     o.scale, o.yq, o.ys);                                  \
+        break;
+    switch (o.epi) {
+        GRX_GEMM_CASE(GRX_GEMM_STORE)
+        GRX_GEMM_CASE(GRX_GEMM_ADD)
+        GRX_GEMM_CASE(GRX_GEMM_AXPY_HALF)
+        GRX_GEMM_CASE(GRX_GEMM_SCALE)
+        GRX_GEMM_CASE(GRX_GEMM_SILU_Q)
+        default:
+            return grx_fail(GRX_EINVAL, "unknown product epilogue %d", o.epi);
+    }
+#undef GRX_GEMM_CASE
+    GRX_LAUNCHED("gemm_q8_mfma_kernel");
+    return GRX_OK;
+}
+
 // m rows of pre-rounded activations (xq [m][K], xs [m][K/32]) times the
 // weight, into y (rows ldc apart), plus bias.
 grx_status grx_gemm_q8_launch(hipStream_t st, const grx_weight *w, const int8_t *xq, const float *xs, int m,
                               const float *bias, float *y, int ldc) {
-    if (m <= 0 || w->rows == 0) return GRX_OK;
-    dim3 grid(grx_ceil_div(m, 64), w->tiles);
-    gemm_q8_mfma_kernel<<<grid, 256, 0, st>>>(w->qs, w->ds, w->rows, w->nb, xq, xs, m, bias, y, ldc);
-    GRX_LAUNCHED("gemm_q8_mfma_kernel");
-    return GRX_OK;
+    GemmOut o;
+    o.y = y;
+    o.ldc = ldc;
+    return grx_gemm_q8_launch_ex(st, w, xq, xs, m, bias, o);
 }

@@ -121,3 +121,129 @@ def pocket_inputs(hp: dict, frames: int, prefix: int = 64, seed: int = 6):
     x = rng.standard_normal((prefix, hp["d"])).astype(np.float32)
     lat = rng.standard_normal((frames, hp["ldim"])).astype(np.float32)
     return x, lat
+
+
+# Parakeet-TDT-0.6B-shaped FastConformer encoder (24 layers of d 1024) and a
+# tiny one for the oracle's own checks.
+PARAKEET_TDT_06B = dict(d=1024, heads=8, layers=24, dff=4096, conv_kernel=31, sub_channels=256, n_mels=128,
+                        xscaling=True, conv_norm="batch_norm")
+CONFORMER_TINY = dict(d=64, heads=2, layers=2, dff=256, conv_kernel=9, sub_channels=32, n_mels=32,
+                      xscaling=True, conv_norm="batch_norm")
+
+
+def conformer_model(hp: dict, seed: int = 9, pointwise_f16: bool = True) -> dict:
+    """Random-init encoder tensors named as conformer/model.go:370-422 reads
+    them.  Linear weights Q8_0 (scales sized so activations stay O(1)); the
+    pointwise convolutions float16 when pointwise_f16 (as Q8_0 model files
+    keep them), else Q8_0; taps and vectors float32."""
+    rng = np.random.default_rng(seed)
+    d, c, ff, K = hp["d"], hp["sub_channels"], hp["dff"], hp["conv_kernel"]
+    F = hp["n_mels"]
+    for _ in range(3):
+        F = (F - 1) // 2 + 1
+    t = {}
+
+    def vec(n, scale=0.1, base=0.0):
+        return (base + scale * rng.standard_normal(n)).astype(np.float32)
+
+    def lin(rows, cols):
+        return q8_weight(rng, rows, cols, sigma=2.0 / np.sqrt(cols))
+
+    pe = "enc.pre_encode."
+    for n in ("conv.0", "conv.2", "conv.5"):
+        t[pe + n + ".weight"] = vec(c * 9, 0.3)
+        t[pe + n + ".bias"] = vec(c)
+    for n in ("conv.3", "conv.6"):
+        t[pe + n + ".weight"] = lin(c, c)
+        t[pe + n + ".bias"] = vec(c)
+    t[pe + "out.weight"] = lin(d, c * F)
+    t[pe + "out.bias"] = vec(d)
+    for i in range(hp["layers"]):
+        p = f"enc.blocks.{i}."
+        for f in ("ff1", "ff2"):
+            t[p + f"norm_{f}.weight"] = vec(d, 0.1, 1.0)
+            t[p + f"norm_{f}.bias"] = vec(d)
+            t[p + f"{f}.linear1.weight"] = lin(ff, d)
+            t[p + f"{f}.linear1.bias"] = vec(ff)
+            t[p + f"{f}.linear2.weight"] = lin(d, ff)
+            t[p + f"{f}.linear2.bias"] = vec(d)
+        for n in ("norm_attn", "norm_conv", "norm_out"):
+            t[p + n + ".weight"] = vec(d, 0.1, 1.0)
+            t[p + n + ".bias"] = vec(d)
+        for n in ("linear_q", "linear_k", "linear_v", "linear_out"):
+            t[p + f"attn.{n}.weight"] = lin(d, d)
+            t[p + f"attn.{n}.bias"] = vec(d)
+        t[p + "attn.linear_pos.weight"] = lin(d, d)
+        t[p + "attn.pos_bias_u"] = vec(d)
+        t[p + "attn.pos_bias_v"] = vec(d)
+        for n, rows in (("pointwise1", 2 * d), ("pointwise2", d)):
+            if pointwise_f16:
+                t[p + f"conv.{n}.weight"] = (rng.standard_normal(rows * d) / np.sqrt(d)).astype(np.float16)
+            else:
+                t[p + f"conv.{n}.weight"] = lin(rows, d)
+        t[p + "conv.pointwise1.bias"] = vec(2 * d)
+        t[p + "conv.pointwise2.bias"] = vec(d)
+        t[p + "conv.depthwise.weight"] = vec(d * K, 0.3)
+        t[p + "conv.depthwise.bias"] = vec(d)
+        t[p + "conv.bn.weight"] = vec(d, 0.1, 1.0)
+        t[p + "conv.bn.bias"] = vec(d)
+        t[p + "conv.bn.running_mean"] = vec(d)
+        t[p + "conv.bn.running_var"] = rng.uniform(0.5, 1.5, d).astype(np.float32)
+    return t
+
+
+def _slaney_mel(hz):
+    f_sp, min_log_hz = 200.0 / 3, 1000.0
+    return np.where(hz < min_log_hz, hz / f_sp, min_log_hz / f_sp + np.log(np.maximum(hz, 1e-12) / min_log_hz)
+                    / (np.log(6.4) / 27))
+
+
+def _slaney_hz(mel):
+    f_sp, min_log_hz = 200.0 / 3, 1000.0
+    min_log_mel = min_log_hz / f_sp
+    return np.where(mel < min_log_mel, mel * f_sp, min_log_hz * np.exp(np.log(6.4) / 27 * (mel - min_log_mel)))
+
+
+def log_mel(pcm: np.ndarray, n_mels: int, sr: int = 16000, n_fft: int = 512, win: int = 400, hop: int = 160):
+    """NeMo-style log-mel features as conformer/mel.go computes them
+    (pre-emphasis 0.97, n_fft/2 zero padding, centred symmetric Hann window,
+    power spectrum, Slaney filterbank to 8 kHz, log(x + 2^-24), per-feature
+    normalization), with numpy's FFT: (mel [n_mels][frames], frames, valid)."""
+    n = len(pcm)
+    frames, valid = n // hop + 1, n // hop
+    pad = n_fft // 2
+    padded = np.zeros(n + 2 * pad)
+    x = pcm.astype(np.float64)
+    padded[pad] = x[0]
+    padded[pad + 1:pad + n] = x[1:] - 0.97 * x[:-1]
+    window = np.zeros(n_fft)
+    wp = (n_fft - win) // 2
+    window[wp:wp + win] = 0.5 - 0.5 * np.cos(2 * np.pi * np.arange(win) / (win - 1))
+    idx = np.arange(frames)[:, None] * hop + np.arange(n_fft)[None, :]
+    seg = np.where(idx < len(padded), padded[np.minimum(idx, len(padded) - 1)], 0.0)
+    spec = np.fft.rfft(seg * window, axis=1)
+    power = (spec.real ** 2 + spec.imag ** 2).astype(np.float32).astype(np.float64)
+    nf = n_fft // 2 + 1
+    lo, hi = _slaney_mel(np.float64(0.0)), _slaney_mel(np.float64(8000.0))
+    hz = _slaney_hz(lo + (hi - lo) * np.arange(n_mels + 2) / (n_mels + 1))
+    f = sr * np.arange(nf) / n_fft
+    fb = np.zeros((n_mels, nf), np.float32)
+    for j in range(n_mels):
+        lower = (f - hz[j]) / (hz[j + 1] - hz[j])
+        upper = (hz[j + 2] - f) / (hz[j + 2] - hz[j + 1])
+        fb[j] = (np.maximum(0, np.minimum(lower, upper)) * (2 / (hz[j + 2] - hz[j]))).astype(np.float32)
+    mel = np.log(power @ fb.astype(np.float64).T + 1.0 / (1 << 24)).astype(np.float32).T.copy()
+    nn = frames - 1
+    rows = mel[:, :nn].astype(np.float64)
+    mean = rows.mean(1, keepdims=True)
+    std = np.sqrt(((rows - mean) ** 2).sum(1, keepdims=True) / max(nn - 1, 1))
+    mel[:, :nn] = ((rows - mean) / (std + 1e-5)).astype(np.float32)
+    mel[:, nn] = 0
+    return np.ascontiguousarray(mel), frames, valid
+
+
+def noise_mel(n_mels: int, seconds: float = 10.0, seed: int = 4, sr: int = 16000):
+    """White noise N(0, 0.1^2) of the given length through log_mel."""
+    rng = np.random.default_rng(seed)
+    pcm = (rng.standard_normal(int(seconds * sr)) * 0.1).astype(np.float32)
+    return log_mel(pcm, n_mels, sr)

@@ -198,6 +198,47 @@ grx_status grx_pocket_run(grx_pocket *m, const float *x, int T, float *out);
  * output and eos (n, may be NULL) its end-of-speech logit. */
 grx_status grx_pocket_frames(grx_pocket *m, const float *latents, int n, float *outs, float *eos);
 
+/* ---- FastConformer encoder with Q8_0 weights ---- */
+
+/* Model.encode (conformer/encoder.go:432-489) of a non-streaming
+ * FastConformer (HParams of conformer/model.go:15-44 with AttStyle
+ * "regular", no attention or convolution limits, non-causal pre-encoder,
+ * subsampling 8): the depthwise-striding pre-encoder (encoder.go:123-167),
+ * xscale, and `layers` Conformer blocks (encoder.go:411-429), every Linear
+ * a Q8_0 weight on the int8 route as conformer/model.go:348-356 packs them.
+ * A batch of utterances of the same frame count runs at once; each
+ * utterance's output is the one it gets alone. */
+typedef struct {
+    int d, heads, layers, dff, conv_kernel, sub_channels, n_mels;
+    int xscaling; /* nonzero: x *= sqrt(d) after the pre-encoder (HParams.XScaling) */
+    int conv_ln;  /* nonzero: conv_norm_type "layer_norm", else folded batch norm */
+} grx_conformer_hparams;
+
+typedef struct grx_conformer grx_conformer;
+
+grx_status grx_conformer_create(grx_ctx *ctx, const grx_conformer_hparams *hp, grx_conformer **out);
+grx_status grx_conformer_destroy(grx_conformer *m);
+/* loadEncoder (conformer/model.go:370-422) by the names it reads
+ * ("enc.pre_encode.conv.0.weight", "enc.blocks.0.ff1.linear1.weight",
+ * "enc.blocks.0.conv.bn.running_var", ...): Linear weights as ggml Q8_0 rows
+ * (the pointwise convolutions may be float16 instead and are rounded by
+ * Weight.ToQ8 at load, model.go:397-402), convolution taps [c][taps] and
+ * vectors as float32.  Optional biases may be left out.  Shapes checked. */
+grx_status grx_conformer_set_tensor(grx_conformer *m, const char *name, const void *data, size_t nbytes);
+/* Encoder frames T for `frames` mel frames (three halvings, encoder.go:33-38). */
+int grx_conformer_frames_out(const grx_conformer *m, int frames);
+/* Model.encode of `batch` utterances: mel is [batch][n_mels][frames] float32
+ * on the host (Mel.Compute's layout), valid[b] the real frames of each
+ * (Mel.Valid, 1..frames).  out receives [batch][T][d]: of utterance b the
+ * first lens[b] rows are the encoder output (encoder.go:488), the rest what
+ * the computation leaves there.  lens may be NULL. */
+grx_status grx_conformer_encode(grx_conformer *m, const float *mel, int batch, int frames, const int *valid,
+                                float *out, int *lens);
+/* The same with mel and out in device memory (valid on the host); returns
+ * when the output is written. */
+grx_status grx_conformer_encode_dev(grx_conformer *m, const float *mel, int batch, int frames, const int *valid,
+                                    float *out);
+
 #ifdef __cplusplus
 }
 #endif

@@ -127,6 +127,45 @@ int orc_ptts_forward(orc_ptts *m, float *x, int T);
 int orc_ptts_run(orc_ptts *m, float *x, int T, float *out);
 int orc_ptts_step(orc_ptts *m, const float *latent, float *out, float *eos);
 
+/* ---- FastConformer encoder with Q8_0 weights (conformer/encoder.go) ---- */
+typedef struct {
+    const float *norm_w, *norm_b;
+    const uint8_t *w1, *w2; /* Q8_0 rows: [dff][d], [d][dff] */
+    const float *b1, *b2;   /* may be NULL */
+} orc_conf_ff;
+
+typedef struct {
+    orc_conf_ff ff1, ff2;
+    const float *norm_attn_w, *norm_attn_b;
+    const uint8_t *q, *k, *v, *out, *pos; /* Q8_0 [d][d] */
+    const float *q_b, *k_b, *v_b, *out_b; /* may be NULL */
+    const float *pos_u, *pos_v;           /* [heads][head_dim] */
+    const float *norm_conv_w, *norm_conv_b;
+    const uint8_t *pw1, *pw2; /* Q8_0 [2d][d], [d][d] */
+    const float *pw1_b, *pw2_b;
+    const float *dw;   /* depthwise taps, [kernel][d] */
+    const float *dw_b; /* may be NULL */
+    const float *cn_w, *cn_b; /* folded batch norm, or the LayerNorm's gain and bias */
+    const float *norm_out_w, *norm_out_b;
+} orc_conf_block;
+
+typedef struct {
+    int d, heads, layers, dff, conv_kernel, sub_channels, n_mels, xscaling, conv_ln;
+    const float *w0, *b0, *w2, *b2, *w5, *b5; /* pre-encoder 3x3 taps, [9][c] */
+    const uint8_t *w3, *w6, *out;             /* Q8_0 [c][c], [c][c], [d][c*F] */
+    const float *b3, *b6, *out_b;
+    orc_conf_block *blocks;
+} orc_conformer;
+
+void orc_conf_rel_pos(float *out, int n, int d);
+void orc_conf_bn_fold(const float *gw, const float *gb, const float *mean, const float *var, int d, float *s,
+                      float *b);
+int orc_conf_subsample(const orc_conformer *m, const float *mel, int frames, int valid, float *out, int *T_out,
+                       int *L_out);
+int orc_conf_block_run(const orc_conformer *m, int i, float *x, int T, int L, const float *pos);
+int orc_conformer_encode(const orc_conformer *m, const float *mel, int frames, int valid, int n_layers, float *out,
+                         int *T_out, int *L_out);
+
 #ifdef __cplusplus
 }
 #endif

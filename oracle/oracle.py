@@ -487,3 +487,168 @@ class PocketOracle:
         if lib().orc_ptts_step(C.byref(self._m), _ptr(lat), out, eos) != 0:
             raise ValueError("the step does not fit the context")
         return out, float(eos[0])
+
+
+# ---- FastConformer encoder (conformer/encoder.go) ----
+
+class _CFF(C.Structure):
+    _fields_ = [(n, C.c_void_p) for n in ("norm_w", "norm_b", "w1", "w2", "b1", "b2")]
+
+
+class _CBlock(C.Structure):
+    _fields_ = ([("ff1", _CFF), ("ff2", _CFF)] +
+                [(n, C.c_void_p) for n in ("norm_attn_w", "norm_attn_b", "q", "k", "v", "out", "pos", "q_b", "k_b",
+                                           "v_b", "out_b", "pos_u", "pos_v", "norm_conv_w", "norm_conv_b", "pw1",
+                                           "pw2", "pw1_b", "pw2_b", "dw", "dw_b", "cn_w", "cn_b", "norm_out_w",
+                                           "norm_out_b")])
+
+
+class _CModel(C.Structure):
+    _fields_ = ([(n, C.c_int) for n in ("d", "heads", "layers", "dff", "conv_kernel", "sub_channels", "n_mels",
+                                        "xscaling", "conv_ln")] +
+                [(n, C.c_void_p) for n in ("w0", "b0", "w2", "b2", "w5", "b5", "w3", "w6", "out", "b3", "b6",
+                                           "out_b", "blocks")])
+
+
+def _declare_conformer(L):
+    L.orc_conf_rel_pos.argtypes = [_f32p, C.c_int, C.c_int]
+    L.orc_conf_bn_fold.argtypes = [_f32p, _f32p, _f32p, _f32p, C.c_int, _f32p, _f32p]
+    L.orc_conf_subsample.argtypes = [C.c_void_p, _f32p, C.c_int, C.c_int, _f32p, C.POINTER(C.c_int),
+                                     C.POINTER(C.c_int)]
+    L.orc_conf_block_run.argtypes = [C.c_void_p, C.c_int, _f32p, C.c_int, C.c_int, _f32p]
+    L.orc_conformer_encode.argtypes = [C.c_void_p, _f32p, C.c_int, C.c_int, C.c_int, _f32p, C.POINTER(C.c_int),
+                                       C.POINTER(C.c_int)]
+
+
+def conf_frames_out(frames: int) -> int:
+    for _ in range(3):
+        frames = (frames - 1) // 2 + 1
+    return frames
+
+
+def conf_rel_pos(n: int, d: int) -> np.ndarray:
+    """relPosEmb (conformer/encoder.go:171-191): [2n-1][d]."""
+    L = lib()
+    _declare_conformer(L)
+    out = np.zeros((2 * n - 1) * d, np.float32)
+    L.orc_conf_rel_pos(out, n, d)
+    return out.reshape(2 * n - 1, d)
+
+
+def conf_bn_fold(gw, gb, mean, var):
+    """conformer/model.go:408-418: batch norm folded to (scale, bias)."""
+    L = lib()
+    _declare_conformer(L)
+    d = len(gw)
+    s, b = np.zeros(d, np.float32), np.zeros(d, np.float32)
+    L.orc_conf_bn_fold(_f32(gw), _f32(gb), _f32(mean), _f32(var), d, s, b)
+    return s, b
+
+
+def _transpose_taps(w, c, taps):
+    """transposeTaps (conformer/model.go:147-159): [c][taps] to [taps][c]."""
+    return np.ascontiguousarray(np.asarray(w, np.float32).reshape(c, taps).T)
+
+
+class ConformerOracle:
+    """Oracle encoder over tensors named as conformer/model.go reads them."""
+
+    def __init__(self, hp: dict, tensors: dict):
+        self.hp = hp
+        L = lib()
+        _declare_conformer(L)
+        d, c, K, nl = hp["d"], hp["sub_channels"], hp["conv_kernel"], hp["layers"]
+        conv_ln = hp.get("conv_norm", "batch_norm") == "layer_norm"
+        self._keep = []
+
+        def keep(a):
+            if a is None:
+                return None
+            a = np.ascontiguousarray(a)
+            self._keep.append(a)
+            return a.ctypes.data
+
+        def pointwise(name, rows, cols):
+            w = tensors[name]
+            if w.nbytes == rows * cols // QK * Q8_BYTES:
+                return w
+            # Weight.ToQ8 of a float16 weight (conformer/model.go:397-402)
+            return quant_q8(np.frombuffer(np.ascontiguousarray(w).tobytes(), np.float16).astype(np.float32))
+
+        m = _CModel()
+        m.d, m.heads, m.layers, m.dff = d, hp["heads"], nl, hp["dff"]
+        m.conv_kernel, m.sub_channels, m.n_mels = K, c, hp["n_mels"]
+        m.xscaling, m.conv_ln = int(bool(hp.get("xscaling", True))), int(conv_ln)
+        pe = "enc.pre_encode."
+        m.w0 = keep(_transpose_taps(tensors[pe + "conv.0.weight"], c, 9))
+        m.w2 = keep(_transpose_taps(tensors[pe + "conv.2.weight"], c, 9))
+        m.w5 = keep(_transpose_taps(tensors[pe + "conv.5.weight"], c, 9))
+        for f, n in (("b0", "conv.0.bias"), ("b2", "conv.2.bias"), ("b5", "conv.5.bias"), ("w3", "conv.3.weight"),
+                     ("w6", "conv.6.weight"), ("b3", "conv.3.bias"), ("b6", "conv.6.bias"),
+                     ("out", "out.weight"), ("out_b", "out.bias")):
+            setattr(m, f, keep(tensors[pe + n]))
+        blocks = (_CBlock * nl)()
+        for i in range(nl):
+            p = f"enc.blocks.{i}."
+            B = blocks[i]
+            for ffn, F in (("ff1", B.ff1), ("ff2", B.ff2)):
+                F.norm_w = keep(tensors[p + f"norm_{ffn}.weight"])
+                F.norm_b = keep(tensors[p + f"norm_{ffn}.bias"])
+                F.w1 = keep(tensors[p + f"{ffn}.linear1.weight"])
+                F.w2 = keep(tensors[p + f"{ffn}.linear2.weight"])
+                F.b1 = keep(tensors.get(p + f"{ffn}.linear1.bias"))
+                F.b2 = keep(tensors.get(p + f"{ffn}.linear2.bias"))
+            for f, n in (("norm_attn_w", "norm_attn.weight"), ("norm_attn_b", "norm_attn.bias"),
+                         ("q", "attn.linear_q.weight"), ("k", "attn.linear_k.weight"),
+                         ("v", "attn.linear_v.weight"), ("out", "attn.linear_out.weight"),
+                         ("pos", "attn.linear_pos.weight"), ("pos_u", "attn.pos_bias_u"),
+                         ("pos_v", "attn.pos_bias_v"), ("norm_conv_w", "norm_conv.weight"),
+                         ("norm_conv_b", "norm_conv.bias"), ("norm_out_w", "norm_out.weight"),
+                         ("norm_out_b", "norm_out.bias")):
+                setattr(B, f, keep(tensors[p + n]))
+            for f, n in (("q_b", "attn.linear_q.bias"), ("k_b", "attn.linear_k.bias"),
+                         ("v_b", "attn.linear_v.bias"), ("out_b", "attn.linear_out.bias"),
+                         ("pw1_b", "conv.pointwise1.bias"), ("pw2_b", "conv.pointwise2.bias"),
+                         ("dw_b", "conv.depthwise.bias")):
+                setattr(B, f, keep(tensors.get(p + n)))
+            B.pw1 = keep(pointwise(p + "conv.pointwise1.weight", 2 * d, d))
+            B.pw2 = keep(pointwise(p + "conv.pointwise2.weight", d, d))
+            B.dw = keep(_transpose_taps(tensors[p + "conv.depthwise.weight"], d, K))
+            if conv_ln:
+                B.cn_w = keep(tensors[p + "conv.bn.weight"])
+                B.cn_b = keep(tensors[p + "conv.bn.bias"])
+            else:
+                s, b = conf_bn_fold(tensors[p + "conv.bn.weight"], tensors[p + "conv.bn.bias"],
+                                    tensors[p + "conv.bn.running_mean"], tensors[p + "conv.bn.running_var"])
+                B.cn_w, B.cn_b = keep(s), keep(b)
+        self._blocks = blocks
+        m.blocks = C.cast(blocks, C.c_void_p)
+        self._m = m
+
+    def subsample(self, mel: np.ndarray, valid: int):
+        """encoder.go:123-167: (pre-encoder output [T][d], T, L)."""
+        mel = _f32(mel)
+        frames = mel.size // self.hp["n_mels"]
+        T = conf_frames_out(frames)
+        out = np.zeros(T * self.hp["d"], np.float32)
+        t, l = C.c_int(), C.c_int()
+        lib().orc_conf_subsample(C.byref(self._m), mel, frames, valid, out, C.byref(t), C.byref(l))
+        return out.reshape(T, self.hp["d"]), t.value, l.value
+
+    def block(self, i: int, x: np.ndarray, L: int) -> np.ndarray:
+        """Block i (encoder.go:411-429, its position projection first) on x [T][d]."""
+        x = _f32(x).copy()
+        T = x.size // self.hp["d"]
+        lib().orc_conf_block_run(C.byref(self._m), i, x, T, L, conf_rel_pos(T, self.hp["d"]).reshape(-1))
+        return x.reshape(T, self.hp["d"])
+
+    def encode(self, mel: np.ndarray, valid: int, layers: int | None = None):
+        """Model.encode without the prompt: (out [T][d], L); the first L rows are the output."""
+        mel = _f32(mel)
+        frames = mel.size // self.hp["n_mels"]
+        T = conf_frames_out(frames)
+        out = np.zeros(T * self.hp["d"], np.float32)
+        t, l = C.c_int(), C.c_int()
+        nl = self.hp["layers"] if layers is None else layers
+        lib().orc_conformer_encode(C.byref(self._m), mel, frames, valid, nl, out, C.byref(t), C.byref(l))
+        return out.reshape(T, self.hp["d"]), l.value

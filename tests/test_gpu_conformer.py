@@ -1,0 +1,113 @@
+"""GPU parity of the FastConformer encoder (conformer/encoder.go:432-489)
+against the CPU oracle: bit-identical outputs for every utterance of a
+batch, at a tiny shape (both convolution norms, Q8_0 and float16 pointwise
+weights), at the full parakeet width with two layers, and at all 24
+layers for the 10 s input, with batching shown not to change an
+utterance's output."""
+import numpy as np
+import pytest
+
+from gorelaxor_amd.synth import CONFORMER_TINY, PARAKEET_TDT_06B, conformer_model, noise_mel
+
+pytestmark = pytest.mark.gpu
+
+
+def _enc(kern, hp, t):
+    from gorelaxor_amd.conformer import ConformerEncoder
+    return ConformerEncoder(hp, t)
+
+
+def _mels(hp, n, seconds, seed):
+    out = [noise_mel(hp["n_mels"], seconds=seconds, seed=seed + i) for i in range(n)]
+    return np.stack([m for m, _, _ in out]), out[0][1], out[0][2]
+
+
+@pytest.mark.parametrize("conv_norm,f16", [("batch_norm", True), ("batch_norm", False), ("layer_norm", True)])
+def test_tiny_encode_bit_exact(kern, orc, conv_norm, f16):
+    hp = dict(CONFORMER_TINY, conv_norm=conv_norm)
+    t = conformer_model(hp, seed=21, pointwise_f16=f16)
+    mel, frames, valid = _mels(hp, 3, 1.5, 30)
+    vals = [valid, valid - 9, valid - 40]
+    enc = _enc(kern, hp, t)
+    got, lens = enc.encode(mel, vals)
+    o = orc.ConformerOracle(hp, t)
+    for b in range(3):
+        want, L = o.encode(mel[b], vals[b])
+        assert lens[b] == L
+        assert np.array_equal(got[b].view(np.uint32), want.view(np.uint32)), (b, np.abs(got[b] - want).max())
+    enc.close()
+
+
+def test_tiny_shape_change_and_rerun(kern, orc):
+    """A second call with another batch and frame count re-plans the work;
+    repeating a call gives the same bits."""
+    hp = dict(CONFORMER_TINY)
+    t = conformer_model(hp, seed=22)
+    enc = _enc(kern, hp, t)
+    o = orc.ConformerOracle(hp, t)
+    for seconds, n in ((1.0, 2), (0.7, 1), (1.0, 2)):
+        mel, frames, valid = _mels(hp, n, seconds, 40)
+        got, lens = enc.encode(mel, valid)
+        for b in range(n):
+            want, L = o.encode(mel[b], valid)
+            assert np.array_equal(got[b].view(np.uint32), want.view(np.uint32)), (seconds, b)
+    enc.close()
+
+
+def test_bad_input_errors(kern):
+    from gorelaxor_amd._lib import GrxError
+    hp = dict(CONFORMER_TINY)
+    t = conformer_model(hp, seed=23)
+    enc = _enc(kern, hp, None)
+    with pytest.raises(GrxError, match="EINVAL"):
+        enc.set_tensor("enc.blocks.0.no_such.weight", np.zeros(4, np.float32))
+    with pytest.raises(GrxError, match="ESIZE"):
+        enc.set_tensor("enc.blocks.0.norm_out.weight", np.zeros(3, np.float32))
+    mel, frames, valid = _mels(hp, 1, 1.0, 50)
+    with pytest.raises(GrxError, match="ESTATE"):
+        enc.encode(mel, valid)  # no tensors yet
+    for k, v in t.items():
+        enc.set_tensor(k, v)
+    with pytest.raises(GrxError, match="EINVAL"):
+        enc.encode(mel, frames + 1)
+    enc.close()
+
+
+@pytest.fixture(scope="module")
+def parakeet2():
+    hp = dict(PARAKEET_TDT_06B, layers=2)
+    return hp, conformer_model(hp, seed=31)
+
+
+def test_parakeet_width_two_layers_bit_exact(kern, orc, parakeet2):
+    """10 s of noise, d 1024, 8 heads, FFN 4096, kernel 31, 128 mels: the
+    pre-encoder and two blocks bit-identical to the oracle."""
+    hp, t = parakeet2
+    mel, frames, valid = _mels(hp, 1, 10.0, 60)
+    enc = _enc(kern, hp, t)
+    got, lens = enc.encode(mel, valid)
+    want, L = orc.ConformerOracle(hp, t).encode(mel[0], valid)
+    assert (got.shape[1], lens[0], L) == (126, 125, 125)
+    assert np.array_equal(got[0].view(np.uint32), want.view(np.uint32)), np.abs(got[0] - want).max()
+    enc.close()
+
+
+def test_parakeet_24_layers_bit_exact_and_batched(kern, orc):
+    """All 24 layers at batch 4 (utterances of different valid lengths): the
+    first (the full 10 s) bit-identical to the oracle, and a shorter one
+    equal to its own batch-1 encode, bit for bit."""
+    hp = dict(PARAKEET_TDT_06B)
+    t = conformer_model(hp, seed=32)
+    mel, frames, valid = _mels(hp, 4, 10.0, 70)
+    vals = [valid, valid - 100, valid - 333, valid]
+    enc = _enc(kern, hp, t)
+    got, lens = enc.encode(mel, vals)
+    assert list(lens) == [125, 113, 84, 125]
+    one, l1 = enc.encode(mel[2:3], vals[2])
+    assert np.array_equal(one[0].view(np.uint32), got[2].view(np.uint32))
+    enc.close()
+    want, L = orc.ConformerOracle(hp, t).encode(mel[0], vals[0])
+    assert L == 125
+    assert np.array_equal(got[0].view(np.uint32), want.view(np.uint32)), np.abs(got[0] - want).max()
+    x = got[0, :125]
+    assert np.isfinite(x).all() and 0.3 < float(np.abs(x).mean()) < 3.0
