@@ -59,6 +59,8 @@ def parse():
     p.add_argument("--no-decoder", action="store_true")
     p.add_argument("--lm-frames", type=int, default=250, help="pocket-TTS-style frames after the 64-row prefix")
     p.add_argument("--no-lm", action="store_true")
+    p.add_argument("--conformer-reps", type=int, default=10, help="timed encodes per batch size")
+    p.add_argument("--no-conformer", action="store_true")
     p.add_argument("--copy-calibration", action="store_true",
                    help="only copy the ring's bytes device to device 3 times (reference reading for HBM counters)")
     return p.parse_args()
@@ -192,6 +194,94 @@ def lm_bench(args) -> dict:
     return res
 
 
+MFMA_INT8_PEAK_TOPS = 5000.0   # MI355X dense int8 matrix peak, 5.0 POP/s
+
+
+def conformer_ops(hp: dict, frames: int, batch: int) -> int:
+    """Algorithmic int8 operations (2 per multiply-add) of every Linear of
+    one encode of `batch` utterances of `frames` mel frames: the
+    pre-encoder's two pointwise products and its output product, each
+    block's feed-forward, q|k|v, out and pointwise products on batch*T rows,
+    and each block's position projection on 2T-1 rows (shared)."""
+    d, c, ff, nl = hp["d"], hp["sub_channels"], hp["dff"], hp["layers"]
+    so = lambda n: (n - 1) // 2 + 1  # noqa: E731
+    T1, T2, T = so(frames), so(so(frames)), so(so(so(frames)))
+    F2, F3 = so(so(hp["n_mels"])), so(so(so(hp["n_mels"])))
+    pre = T2 * F2 * c * c + T * F3 * c * c + T * d * c * F3
+    per_row = 4 * ff * d + 3 * d * d + d * d + 2 * d * d + d * d
+    return 2 * (batch * (pre + nl * T * per_row) + nl * (2 * T - 1) * d * d)
+
+
+def conformer_weight_bytes(hp: dict) -> int:
+    """Q8_0 bytes of every Linear weight of the encoder (34 per 32)."""
+    d, c, ff, nl = hp["d"], hp["sub_channels"], hp["dff"], hp["layers"]
+    so = lambda n: (n - 1) // 2 + 1  # noqa: E731
+    F3 = so(so(so(hp["n_mels"])))
+    vals = 2 * c * c + d * c * F3 + nl * (4 * ff * d + 5 * d * d + 2 * d * d + d * d)
+    return vals // 32 * 34
+
+
+def conformer_bench(args) -> dict:
+    """Parakeet-TDT-0.6B-shaped FastConformer encoder forward (d 1024, 24
+    layers, FFN 4096, 8 heads, kernel 31, 256 pre-encoder channels) with
+    random-init Q8_0 weights over 10 s of white noise (N(0, 0.1^2), 16 kHz)
+    as 128-bin log-mel (1001 frames -> 126 encoder frames, 125 valid), at
+    batch 1 and 16, mel and output resident in HBM.  Utterances/s, int8 TOPS
+    of the Linears against the 5 POP/s MFMA peak; batch 1 output checked
+    against the oracle, whose encode of the same utterance is the CPU
+    baseline."""
+    import oracle
+    from gorelaxor_amd import hiprt
+    from gorelaxor_amd.conformer import ConformerEncoder, frames_out
+    from gorelaxor_amd.synth import PARAKEET_TDT_06B, conformer_model, noise_mel
+
+    hp = dict(PARAKEET_TDT_06B)
+    t = conformer_model(hp, seed=32)
+    mels = [noise_mel(hp["n_mels"], 10.0, seed=70 + i) for i in range(16)]
+    frames, valid = mels[0][1], mels[0][2]
+    mel = np.stack([m for m, _, _ in mels])
+    T = frames_out(frames)
+    enc = ConformerEncoder(hp, t)
+    stream = enc.ctx.stream
+    res = {"shape": "d_model 1024, 24 layers, FFN 4096, 8 heads, conv kernel 31, 128 mels, 10 s -> T %d" % T}
+    d = hp["d"]
+    for batch in (1, 16):
+        dm = hiprt.DeviceBuffer.from_array(np.ascontiguousarray(mel[:batch]))
+        do = hiprt.DeviceBuffer(batch * T * d * 4)
+        enc.encode_dev(dm.ptr, batch, frames, valid, do.ptr)  # plan + capture
+        enc.encode_dev(dm.ptr, batch, frames, valid, do.ptr)
+        ms = []
+        for _ in range(args.conformer_reps):
+            a, b = hiprt.Event(), hiprt.Event()
+            a.record(stream)
+            enc.encode_dev(dm.ptr, batch, frames, valid, do.ptr)
+            b.record(stream)
+            b.synchronize()
+            ms.append(a.elapsed_ms(b))
+        best = float(np.median(ms))
+        ops = conformer_ops(hp, frames, batch)
+        r = {"utterances_per_s": round(batch / (best * 1e-3), 2), "ms_per_encode": round(best, 3),
+             "int8_tops": round(ops / (best * 1e-3) / 1e12, 2), "int8_ops_per_encode": ops,
+             "mfma_fraction": round(ops / (best * 1e-3) / 1e12 / MFMA_INT8_PEAK_TOPS, 4), "reps": args.conformer_reps}
+        if batch == 1:
+            wbytes = conformer_weight_bytes(hp)
+            r["weight_bytes"] = wbytes
+            r["weight_stream_gbs"] = round(wbytes / (best * 1e-3) / 1e9, 1)
+            out1 = do.download(np.float32, (T, d))
+        res[f"batch{batch}"] = r
+        del dm, do
+    enc.close()
+    oracle.build()
+    t0 = time.perf_counter()
+    want, L = oracle.ConformerOracle(hp, t).encode(mel[0], valid)
+    cpu_s = time.perf_counter() - t0
+    res["parity_bit_exact"] = bool(np.array_equal(out1.view(np.uint32), want.view(np.uint32)))
+    res["cpu_baseline"] = {"value": round(1.0 / cpu_s, 4), "unit": "utterances/s", "cores": 1, "kind": "port",
+                           "sample": f"one 10 s utterance, all 24 layers, on the oracle (scalar C, 1 thread), "
+                                     f"{cpu_s:.1f} s"}
+    return res
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -287,6 +377,9 @@ def main():
     if not args.no_lm:
         out["lm"] = lm_bench(args)
         out["config"]["workload"] += "; pocket-TTS-style flow-LM frame loop (lm.frames_per_s)"
+    if not args.no_conformer:
+        out["conformer"] = conformer_bench(args)
+        out["config"]["workload"] += "; parakeet-shaped conformer encoder at batch 1 and 16 (conformer.*)"
     print(json.dumps(out), flush=True)
 
 

@@ -79,17 +79,17 @@ __global__ void sub_conv0_kernel(const float *__restrict__ mel, int B, int frame
         const int tv = min(frames, vb);
         const float *mb = mel + (size_t)b * nm * frames;
         const bool fm = ch < (c & ~7);
-        float o = bias[ch];
-        for (int kt = 0; kt < 3; ++kt) {
-            const int ti = 2 * t + kt - 1;
-            for (int kf = 0; kf < 3; ++kf) {
-                const int fi = 2 * f + kf - 1;
-                const float v = (ti >= 0 && ti < tv && fi >= 0 && fi < nm) ? mb[(size_t)fi * frames + ti] : 0.f;
-                if (v == 0.f) continue;
-                const float wv = w[(kt * 3 + kf) * c + ch];
-                o = fm ? __fmaf_rn(v, wv, o) : __fadd_rn(o, __fmul_rn(v, wv));
-            }
+        float v[9], wv[9];
+#pragma unroll
+        for (int j = 0; j < 9; ++j) {
+            const int ti = 2 * t + j / 3 - 1, fi = 2 * f + j % 3 - 1;
+            v[j] = (ti >= 0 && ti < tv && fi >= 0 && fi < nm) ? mb[(size_t)fi * frames + ti] : 0.f;
+            wv[j] = w[j * c + ch];
         }
+        float o = bias[ch];
+#pragma unroll
+        for (int j = 0; j < 9; ++j)
+            if (v[j] != 0.f) o = fm ? __fmaf_rn(v[j], wv[j], o) : __fadd_rn(o, __fmul_rn(v[j], wv[j]));
         out[idx] = o < 0.f ? 0.f : o;
     }
 }
@@ -109,18 +109,21 @@ __global__ void sub_dwconv_kernel(const float *__restrict__ in, int T, int F, in
     const int Lin = stage_len(vb, s - 1), Lout = stage_len(vb, s);
     float o = 0.f;
     if (t1 < Lout) {
-        o = bias[ch];
-        for (int kt = 0; kt < 3; ++kt) {
-            const int ti = 2 * t1 + kt - 1;
-            if (ti < 0 || ti >= T) continue;
-            for (int kf = 0; kf < 3; ++kf) {
-                const int fi = 2 * f1 + kf - 1;
-                if (fi < 0 || fi >= F) continue;
-                float x = in[(((size_t)b * T + ti) * F + fi) * c + ch];
-                if constexpr (RELU_IN) x = ti < Lin ? (x < 0.f ? 0.f : x) : 0.f;
-                o = __fadd_rn(o, __fmul_rn(w[(kt * 3 + kf) * c + ch], x));
-            }
+        float xv[9], wv[9];
+        bool ok[9];
+#pragma unroll
+        for (int j = 0; j < 9; ++j) {
+            const int ti = 2 * t1 + j / 3 - 1, fi = 2 * f1 + j % 3 - 1;
+            ok[j] = ti >= 0 && ti < T && fi >= 0 && fi < F;  // taps outside the plane are skipped
+            float x = ok[j] ? in[(((size_t)b * T + ti) * F + fi) * c + ch] : 0.f;
+            if constexpr (RELU_IN) x = ti < Lin ? (x < 0.f ? 0.f : x) : 0.f;
+            xv[j] = x;
+            wv[j] = w[j * c + ch];
         }
+        o = bias[ch];
+#pragma unroll
+        for (int j = 0; j < 9; ++j)
+            if (ok[j]) o = __fadd_rn(o, __fmul_rn(wv[j], xv[j]));
     }
     quant32_store(o, xq + (size_t)p * c + ch, xs + (size_t)p * (c / 32) + ch / 32, ch & 31);
 }
@@ -335,6 +338,243 @@ __global__ __launch_bounds__(kAttnThreads) void conf_attn_kernel(
     }
 }
 
+// rows x cols floats (cols % 4 == 0, source rows 16-byte aligned) from
+// global memory (rows ssrc floats apart) into LDS (rows sdst apart), every
+// thread keeping four 16-byte loads in flight.
+__device__ __forceinline__ void stage_f4(float *dst, int sdst, const float *src, size_t ssrc, int rows, int cols) {
+    const int c4 = cols >> 2, n = rows * c4, nt = blockDim.x;
+    for (int e0 = threadIdx.x; e0 < n; e0 += 4 * nt) {
+        float4 v[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int e = e0 + u * nt;
+            if (e < n) v[u] = *reinterpret_cast<const float4 *>(src + (size_t)(e / c4) * ssrc + 4 * (e % c4));
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int e = e0 + u * nt;
+            if (e < n) {
+                float *d = dst + (e / c4) * sdst + 4 * (e % c4);
+                d[0] = v[u].x;
+                d[1] = v[u].y;
+                d[2] = v[u].z;
+                d[3] = v[u].w;
+            }
+        }
+    }
+}
+
+// Four outputs of MatMulF32's 6x16 panel route (kernels_amd64.s:5-88) at
+// once: out_j = sum over k chunks of 256 of (fma chain over the chunk),
+// each chunk's chain added to the running result; a(j, k) and b(j, k) give
+// output j's operands.  The four chains are independent, so their loads
+// and FMAs interleave.
+template <class FA, class FB>
+__device__ __forceinline__ void packed4(const FA &a, const FB &b, int k, float out[4]) {
+    float c[4] = {0.f, 0.f, 0.f, 0.f};
+    for (int k0 = 0; k0 < k; k0 += 256) {
+        const int kn = min(256, k - k0);
+        float acc[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll 8
+        for (int kk = 0; kk < kn; ++kk) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) acc[j] = __fmaf_rn(a(j, k0 + kk), b(j, k0 + kk), acc[j]);
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) c[j] = __fadd_rn(acc[j], c[j]);
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) out[j] = c[j];
+}
+
+// The same attention with the head's keys, the rows of the position table
+// the block uses and the values staged in LDS, for RQ of the block's query
+// rows per workgroup (rows r0.. of block blk; the route of each product is
+// still chosen by the row's index in its block of 32 and by the block's
+// full column counts).  Only the band of bd that the rows use is computed:
+// bd[i][nq-1-i+kk] for the nk keys.
+template <int RQ>
+__global__ __launch_bounds__(kAttnThreads) void conf_attn_lds_kernel(
+    const float *__restrict__ qkv, const float *__restrict__ pp, int ldp, const float *__restrict__ pos_u,
+    const float *__restrict__ pos_v, const int *__restrict__ valid, int T, int D, int hd, float scale,
+    int8_t *__restrict__ xq, float *__restrict__ xs) {
+    extern __shared__ float sm[];
+    constexpr int kChunks = kAttnQ / RQ;
+    const int blk = blockIdx.x / kChunks, r0 = (blockIdx.x % kChunks) * RQ;
+    const int h = blockIdx.y, b = blockIdx.z, tid = threadIdx.x, nt = blockDim.x;
+    const int L = enc_len(valid[b], T);
+    const int q0 = blk * kAttnQ, q1 = min(T, q0 + kAttnQ), nq = q1 - q0;
+    if (r0 >= nq) return;
+    const int nr = min(RQ, nq - r0);  // rows r0 .. r0+nr-1 of the block
+    const int khi = min(T, L);
+    const int k0 = 0, k1 = q0 < L ? khi : 0, nk = k1 - k0;
+    const size_t ld = 3 * (size_t)D;
+    const float *base = qkv + (size_t)b * T * ld;
+    const int nqb = hd / 32;
+    if (nk <= 0) {
+        for (int g = tid >> 5; g < nr * nqb; g += nt >> 5) {
+            const int i = g / nqb, bb = g % nqb;
+            const size_t row = (size_t)b * T + q0 + r0 + i;
+            quant32_store(0.f, xq + row * D + h * hd + bb * 32 + (tid & 31), xs + row * (D / 32) + (h * hd) / 32 + bb,
+                          tid & 31);
+        }
+        return;
+    }
+    const int np = nq + nk - 1, jlo = T - 1 - (q1 - 1) + k0;
+    const int sq = hd + 1, sS = nk | 1;
+    float *qu = sm, *qv = qu + RQ * sq, *S = qv + RQ * sq, *BD = S + RQ * sS, *rmx = BD + RQ * sS,
+          *rinv = rmx + RQ, *st = rinv + RQ;
+    stage_f4(qu, sq, base + (size_t)(q0 + r0) * ld + h * hd, ld, nr, hd);
+    // keys k0.. of the head, rows sq apart
+    stage_f4(st, sq, base + (size_t)k0 * ld + D + h * hd, ld, nk, hd);
+    __syncthreads();
+    for (int e = tid; e < nr * hd; e += nt) {
+        const int i = e / hd, j = e % hd;
+        const float q = qu[i * sq + j];
+        qu[i * sq + j] = __fadd_rn(q, pos_u[h * hd + j]);
+        qv[i * sq + j] = __fadd_rn(q, pos_v[h * hd + j]);
+    }
+    __syncthreads();
+    // rows below pf (index in the block) take the panel route: whole groups
+    // of four of them run four chains per thread; every other output (the
+    // gemvRows rows, a last partial group) is a task of its own
+    const int pf = nq > 16 ? nq / 6 * 6 : 0;
+    const int pr = r0 < pf ? min(nr, pf - r0) : 0, ng = pr / 4, r1 = 4 * ng;
+    for (int e = tid; e < ng * nk + (nr - r1) * nk; e += nt) {
+        if (e < ng * nk) {
+            const int i0 = 4 * (e / nk), kk = e % nk;
+            float o[4];
+            const float *bk = st + kk * sq;
+            packed4([&](int j, int k) { return qu[(i0 + j) * sq + k]; }, [&](int, int k) { return bk[k]; }, hd, o);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) S[(i0 + j) * sS + kk] = o[j];
+        } else {
+            const int e2 = e - ng * nk, i = r1 + e2 / nk, kk = e2 % nk;
+            S[i * sS + kk] = matmul_f32_one(qu + i * sq, st + kk * sq, 1, hd, r0 + i, nq, kk, nk);
+        }
+    }
+    __syncthreads();
+    // position rows jlo + nq-1-(r0+i) + kk: from pb = jlo + nq-1-(r0+nr-1) on, nk + nr - 1 of them
+    const int pb = jlo + nq - 1 - (r0 + nr - 1), npr = nk + nr - 1;
+    stage_f4(st, sq, pp + (size_t)pb * ldp + h * hd, ldp, npr, hd);
+    __syncthreads();
+    // bd[i][kk] uses position row (nr-1-i) + kk of the staged ones: rows
+    // i0+j with keys kd+j share row nr-1-i0+kd, so a thread takes such a
+    // diagonal of four (kd in [0, nk-4]); the three outputs per row each
+    // group's diagonals miss, and every output of the other rows, are tasks
+    // of their own
+    const int nd = nk >= 4 ? nk - 3 : 0, gd = nd > 0 ? ng : 0, rs = nd > 0 ? r1 : 0;
+    const int n_diag = gd * nd, n_left = gd * 12, n_rest = (nr - rs) * nk;
+    for (int e = tid; e < n_diag + n_left + n_rest; e += nt) {
+        int i, kj;
+        if (e < n_diag) {
+            const int i0 = 4 * (e / nd), kd = e % nd;
+            float o[4];
+            const float *bp = st + (nr - 1 - i0 + kd) * sq;
+            packed4([&](int j, int k) { return qv[(i0 + j) * sq + k]; }, [&](int, int k) { return bp[k]; }, hd, o);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) BD[(i0 + j) * sS + kd + j] = o[j];
+            continue;
+        } else if (e < n_diag + n_left) {
+            const int e2 = e - n_diag, q = e2 % 12, j = q / 3, t = q % 3;
+            i = 4 * (e2 / 12) + j;
+            kj = t < j ? t : nk - 3 + t;
+        } else {
+            const int e2 = e - n_diag - n_left;
+            i = rs + e2 / nk;
+            kj = e2 % nk;
+        }
+        const int jj = nq - 1 - (r0 + i) + kj;  // column of bd in the block's product
+        BD[i * sS + kj] = matmul_f32_one(qv + i * sq, st + (nr - 1 - i + kj) * sq, 1, hd, r0 + i, nq, jj, np);
+    }
+    __syncthreads();
+    // values of the head (rows hd apart) while the rows are scored
+    stage_f4(st, hd, base + (size_t)k0 * ld + 2 * D + h * hd, ld, nk, hd);
+    const int lane = tid & 63, wave = tid >> 6, nw = nt >> 6;
+    for (int i = wave; i < nr; i += nw) {
+        const int hi = q0 + r0 + i < L ? khi : 0;
+        float mx = -__builtin_inff();
+        for (int kk = lane; kk < nk; kk += 64) {
+            const int kx = k0 + kk;
+            float v;
+            if (kx < 0 || kx >= hi) {
+                v = -__builtin_inff();
+            } else {
+                v = __fmul_rn(__fadd_rn(S[i * sS + kk], BD[i * sS + kk]), scale);
+                mx = go_max(mx, v);
+            }
+            S[i * sS + kk] = v;
+        }
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) mx = go_max(mx, __shfl_xor(mx, o));
+        if (lane == 0) rmx[i] = mx;
+    }
+    __syncthreads();
+    const int n8 = nk & ~7;
+    for (int e = tid; e < nr * nk; e += nt) {
+        const int i = e / nk, kk = e % nk;
+        const float mx = rmx[i];
+        float &v = S[i * sS + kk];
+        if (mx == -__builtin_inff())
+            v = 0.f;
+        else {
+            const float d = __fsub_rn(v, mx);
+            v = kk < n8 ? grx_exp8(d) : grx_expf_go(d);
+        }
+    }
+    __syncthreads();
+    for (int i = wave; i < nr; i += nw) {
+        float acc = 0.f;
+        if (lane < 8) {
+            for (int kk = lane; kk < n8; kk += 8) acc = __fadd_rn(acc, S[i * sS + kk]);
+        } else if (lane == 8) {
+            for (int kk = n8; kk < nk; ++kk) acc = __fadd_rn(acc, S[i * sS + kk]);
+        }
+        float a8[8];
+#pragma unroll
+        for (int l = 0; l < 8; ++l) a8[l] = __shfl(acc, l);
+        const float tail = __shfl(acc, 8);
+        if (lane == 0) {
+            const float sa = n8 > 0 ? hsum8(a8) : 0.f;
+            rinv[i] = __fdiv_rn(1.0f, __fadd_rn(sa, tail));
+        }
+    }
+    __syncthreads();
+    for (int e = tid; e < nr * nk; e += nt) {
+        const int i = e / nk, kk = e % nk;
+        if (rmx[i] != -__builtin_inff()) S[i * sS + kk] = __fmul_rn(S[i * sS + kk], rinv[i]);
+    }
+    __syncthreads();
+    float *O = qu;  // [nr][sq]
+    for (int e = tid; e < ng * hd + (nr - r1) * hd; e += nt) {
+        if (e < ng * hd) {
+            const int i0 = 4 * (e / hd), ee = e % hd;
+            float o[4];
+            const float *bv = st + ee;
+            packed4([&](int j, int k) { return S[(i0 + j) * sS + k]; }, [&](int, int k) { return bv[k * hd]; }, nk,
+                    o);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) O[(i0 + j) * sq + ee] = o[j];
+        } else {
+            const int e2 = e - ng * hd, i = r1 + e2 / hd, ee = e2 % hd;
+            O[i * sq + ee] = matmul_f32_one(S + i * sS, st + ee, hd, nk, r0 + i, nq, ee, hd);
+        }
+    }
+    __syncthreads();
+    for (int g = tid >> 5; g < nr * nqb; g += nt >> 5) {
+        const int i = g / nqb, bb = g % nqb, e = tid & 31;
+        const size_t row = (size_t)b * T + q0 + r0 + i;
+        quant32_store(O[i * sq + bb * 32 + e], xq + row * D + h * hd + bb * 32 + e,
+                      xs + row * (D / 32) + (h * hd) / 32 + bb, e);
+    }
+}
+
+size_t attn_lds_smem_floats(int T, int hd, int rq) {
+    const int nk = T, sq = hd + 1;
+    const size_t stage = std::max((size_t)(nk + rq - 1) * sq, (size_t)nk * hd);
+    return (size_t)2 * rq * sq + (size_t)2 * rq * (nk | 1) + 2 * rq + stage;
+}
+
 size_t attn_smem_floats(int T, int hd) {
     const int nk = T, np = kAttnQ + T - 1;
     return (size_t)2 * kAttnQ * (hd + 1) + (size_t)kAttnQ * (nk | 1) + (size_t)kAttnQ * (np | 1) + 2 * kAttnQ;
@@ -380,10 +620,19 @@ __global__ __launch_bounds__(kRowThreads) void conf_dwconv_kernel(const float *_
     const float *gb = g + (size_t)b * T * D;
     for (int c = tid; c < D; c += blockDim.x) {
         float o = dwb != nullptr ? dwb[c] : 0.f;
-        for (int j = 0; j < K; ++j) {
-            const int ti = t + j - padL;
-            if (ti < 0 || ti >= T) continue;
-            o = __fadd_rn(o, __fmul_rn(w[(size_t)j * D + c], gb[(size_t)ti * D + c]));
+        for (int j0 = 0; j0 < K; j0 += 8) {
+            float xv[8], wv[8];
+            bool ok[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                const int j = j0 + u, ti = t + j - padL;
+                ok[u] = j < K && ti >= 0 && ti < T;  // taps outside the frames are skipped
+                xv[u] = ok[u] ? gb[(size_t)ti * D + c] : 0.f;
+                wv[u] = ok[u] ? w[(size_t)j * D + c] : 0.f;
+            }
+#pragma unroll
+            for (int u = 0; u < 8; ++u)
+                if (ok[u]) o = __fadd_rn(o, __fmul_rn(wv[u], xv[u]));
         }
         if constexpr (!LN) o = __fadd_rn(__fmul_rn(o, cn_w[c]), cn_b[c]);
         row[c] = o;
@@ -427,6 +676,8 @@ struct grx_conformer {
     grx_weight *pos_all = nullptr;  // every block's linear_pos, [layers*d][d]
     // shape-dependent state
     int B = 0, frames = 0, T = 0;
+    int attn_rq = 0;         // query rows per staged attention workgroup (0: unstaged kernel)
+    size_t attn_smem = 0;
     float *mel = nullptr, *sub0 = nullptr, *suby = nullptr, *x = nullptr, *qkv = nullptr, *pp = nullptr;
     float *conv = nullptr, *glu = nullptr, *pos = nullptr;
     int8_t *xq = nullptr, *fq = nullptr, *pos_q = nullptr;  // fq: the rounded SiLU output of W1
@@ -726,17 +977,31 @@ grx_status cshape(grx_conformer *m, int B, int frames) {
     const int T1 = sub_out(frames), F1 = sub_out(nm), T2 = sub_out(T1), F2 = sub_out(F1), T = sub_out(T2),
               F3 = sub_out(F2);
     const size_t R = (size_t)B * T;
-    {  // the attention block's LDS: past 64 KiB it has to be asked for
-        const size_t need = attn_smem_floats(T, d / hp.heads) * 4;
-        int lim = 0;
-        GRX_HIP(hipDeviceGetAttribute(&lim, hipDeviceAttributeMaxSharedMemoryPerBlock, m->ctx->device));
-        if (need > (size_t)std::max(lim, 160 * 1024) || need > 160 * 1024)
-            return grx_fail(GRX_ESIZE, "%d frames give %d encoder frames, more than the attention kernel holds",
-                            frames, T);
-        if (need > 64 * 1024 &&
-            hipFuncSetAttribute((const void *)conf_attn_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                (int)need) != hipSuccess)
-            return grx_fail(GRX_ESIZE, "%d encoder frames need %zu bytes of LDS per attention block", T, need);
+    {  // the attention's LDS: past 64 KiB it has to be asked for.  The staged
+       // kernel takes 8 query rows per workgroup for few utterances, 16 for
+       // many; past what LDS holds the unstaged kernel runs.
+        const int hd = d / hp.heads, nblk = (T + kAttnQ - 1) / kAttnQ;
+        m->attn_rq = B * hp.heads * nblk * (kAttnQ / 8) < 1024 ? 8 : 16;
+        if (const char *e = getenv("GRX_CONF_ATTN_RQ")) m->attn_rq = atoi(e);  // 0 (unstaged), 8 or 16, for tests
+        if (m->attn_rq != 0 && m->attn_rq != 8 && m->attn_rq != 16) m->attn_rq = 8;
+        const size_t staged = attn_lds_smem_floats(T, hd, m->attn_rq) * 4;
+        const void *fn = m->attn_rq == 8 ? (const void *)conf_attn_lds_kernel<8> : (const void *)conf_attn_lds_kernel<16>;
+        if (m->attn_rq != 0 && staged <= 160 * 1024 &&
+            (staged <= 64 * 1024 ||
+             hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)staged) == hipSuccess)) {
+            m->attn_smem = staged;
+        } else {
+            (void)hipGetLastError();
+            m->attn_rq = 0;
+            const size_t need = attn_smem_floats(T, hd) * 4;
+            if (need > 160 * 1024 ||
+                (need > 64 * 1024 && hipFuncSetAttribute((const void *)conf_attn_kernel,
+                                                         hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                         (int)need) != hipSuccess))
+                return grx_fail(GRX_ESIZE, "%d frames give %d encoder frames, more than the attention kernel holds",
+                                frames, T);
+            m->attn_smem = need;
+        }
     }
     grx_status s;
     auto &w = m->work;
@@ -812,7 +1077,7 @@ grx_status enqueue_encode(grx_conformer *m, hipStream_t st) {
     ln_rows_kernel<false, true><<<R, kRowThreads, row_smem, st>>>(m->x, d, m->blk[0].ff1.norm_w, m->blk[0].ff1.norm_b,
                                                                   nullptr, nullptr, m->xq, m->xs);
     GRX_LAUNCHED("ln_rows_kernel");
-    const size_t attn_smem = attn_smem_floats(T, hd) * 4;
+    const size_t attn_smem = m->attn_smem;
     const float scale = (float)(1.0 / std::sqrt((double)hd));
     const int nblk = (T + kAttnQ - 1) / kAttnQ;
     for (int i = 0; i < hp.layers; ++i) {
@@ -837,8 +1102,18 @@ grx_status enqueue_encode(grx_conformer *m, hipStream_t st) {
                                                                       nullptr, m->xq, m->xs);
         GRX_LAUNCHED("ln_rows_kernel");
         if ((s = grx_gemm_q8_launch(st, Bk.qkv, m->xq, m->xs, R, Bk.qkv_b, m->qkv, 3 * d)) != GRX_OK) return s;
-        conf_attn_kernel<<<dim3(nblk, hp.heads, B), kAttnThreads, attn_smem, st>>>(
-            m->qkv, m->pp + (size_t)i * d, hp.layers * d, Bk.pos_u, Bk.pos_v, m->valid, T, d, hd, scale, m->xq, m->xs);
+        if (m->attn_rq == 8)
+            conf_attn_lds_kernel<8><<<dim3(nblk * (kAttnQ / 8), hp.heads, B), kAttnThreads, attn_smem, st>>>(
+                m->qkv, m->pp + (size_t)i * d, hp.layers * d, Bk.pos_u, Bk.pos_v, m->valid, T, d, hd, scale, m->xq,
+                m->xs);
+        else if (m->attn_rq == 16)
+            conf_attn_lds_kernel<16><<<dim3(nblk * (kAttnQ / 16), hp.heads, B), kAttnThreads, attn_smem, st>>>(
+                m->qkv, m->pp + (size_t)i * d, hp.layers * d, Bk.pos_u, Bk.pos_v, m->valid, T, d, hd, scale, m->xq,
+                m->xs);
+        else
+            conf_attn_kernel<<<dim3(nblk, hp.heads, B), kAttnThreads, attn_smem, st>>>(
+                m->qkv, m->pp + (size_t)i * d, hp.layers * d, Bk.pos_u, Bk.pos_v, m->valid, T, d, hd, scale, m->xq,
+                m->xs);
         GRX_LAUNCHED("conf_attn_kernel");
         {
             GemmOut o;

@@ -193,6 +193,7 @@ __device__ __forceinline__ void stage_rows(float *vl, const float *base, size_t 
 __device__ __forceinline__ float dot_go_s(const float *x, const float *y, size_t sb, int n) {
     float s0 = 0.f, s1 = 0.f, s2 = 0.f, s3 = 0.f;
     int i = 0;
+#pragma unroll 4
     for (; i + 4 <= n; i += 4) {
         s0 = __fadd_rn(s0, __fmul_rn(x[i], y[i * sb]));
         s1 = __fadd_rn(s1, __fmul_rn(x[i + 1], y[(i + 1) * sb]));
@@ -240,6 +241,7 @@ __device__ __forceinline__ float matmul_f32_one(const float *a, const float *b, 
         for (int k0 = 0; k0 < k; k0 += 256) {
             const int kn = min(256, k - k0);
             float acc = 0.f;
+#pragma unroll 16
             for (int kk = 0; kk < kn; ++kk) acc = __fmaf_rn(a[k0 + kk], b[(size_t)(k0 + kk) * sb], acc);
             c = __fadd_rn(acc, c);
         }

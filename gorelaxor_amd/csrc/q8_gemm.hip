@@ -19,6 +19,7 @@
 // and four activation scales.  The per-output fold (convert, multiply, fma:
 // 3 VALU ops per output per block) is the bound, not the MFMA: exact
 // per-block scaling costs that much vector work per 32 multiply-adds.
+#include <cstdlib>
 #include <type_traits>
 
 #include "grx_internal.h"
@@ -27,8 +28,6 @@ namespace {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 
-constexpr int kGemmBU = 2;  // blocks whose loads are issued before use
-
 // What the epilogue does with each finished output c (GemmOut::epi):
 //   STORE      y = c
 //   ADD        y = y + c                      (kern.Add of the product)
@@ -36,7 +35,13 @@ constexpr int kGemmBU = 2;  // blocks whose loads are issued before use
 //   SCALE      y = c * scale
 //   SILU_Q     SiLU(c) of the AVX route (c / (EXP8(0 - c) + 1)), rounded to
 //              Q8_0 per 32 outputs into yq [m][rows], ys [m][rows/32]
-template <int EPI>
+//
+// A wave computes 16 activation rows x 16*NS weight rows (NS 16x16 MFMA
+// tiles sharing the A fragment; NS of 1 or 2 give small products more
+// waves); a workgroup stacks four waves along the activation rows.  The
+// blocks are walked U at a time with two register sets: the loads of the
+// next U blocks are in flight while the current ones fold.
+template <int EPI, int NS, int U>
 __global__ __launch_bounds__(256) void gemm_q8_mfma_kernel(const int8_t *__restrict__ qs,
                                                            const uint16_t *__restrict__ ds, int rows, int nb,
                                                            const int8_t *__restrict__ xq,
@@ -44,20 +49,23 @@ __global__ __launch_bounds__(256) void gemm_q8_mfma_kernel(const int8_t *__restr
                                                            const float *__restrict__ bias, float *__restrict__ y,
                                                            int ldc, float scale, int8_t *__restrict__ yq,
                                                            float *__restrict__ ys) {
+    static_assert(NS == 1 || NS == 2 || NS == 4, "a 64-row weight tile splits into 1, 2 or 4 column groups");
+    constexpr int kGroups = 4 / NS;
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int tile = blockIdx.y;                     // weight rows 64*tile ..
-    const int m0 = blockIdx.x * 64 + wave * 16;      // activation rows m0 .. m0+15
+    const int tile = blockIdx.y / kGroups;                // weight rows 64*tile ..
+    const int sg = (blockIdx.y % kGroups) * NS;           // first 16-row group of the tile
+    const int m0 = blockIdx.x * 64 + wave * 16;           // activation rows m0 .. m0+15
     const int K = nb * GRX_QK;
-    const int li = lane & 15, lk = lane >> 4;        // fragment row/column, k group of 8
+    const int li = lane & 15, lk = lane >> 4;             // fragment row/column, k group of 8
 
     // A fragment: row m0+li, bytes 8*lk..8*lk+7 of each block
     const int arow = m0 + li;
     const bool arow_ok = arow < m;
     const int8_t *ap = xq + (size_t)(arow_ok ? arow : 0) * K + 8 * lk;
-    // B fragments: weight row 16*s+li of the tile, bytes 8*lk..: half lk/2, offset 8*(lk&1)
-    const int8_t *bp = qs + (size_t)tile * nb * 2048 + (lk >> 1) * 1024 + li * 16 + 8 * (lk & 1);
-    const uint16_t *dp = ds + (size_t)tile * nb * 64 + li;
+    // B fragments: weight row 16*(sg+s)+li of the tile, bytes 8*lk..: half lk/2, offset 8*(lk&1)
+    const int8_t *bp = qs + (size_t)tile * nb * 2048 + (lk >> 1) * 1024 + (16 * sg + li) * 16 + 8 * (lk & 1);
+    const uint16_t *dp = ds + (size_t)tile * nb * 64 + 16 * sg + li;
     // D layout: lane holds column li, rows 4*lk + r
     int drow[4];
     bool drow_ok[4];
@@ -70,56 +78,94 @@ __global__ __launch_bounds__(256) void gemm_q8_mfma_kernel(const int8_t *__restr
 #pragma unroll
     for (int r = 0; r < 4; ++r) sp[r] = xs + (size_t)(drow_ok[r] ? drow[r] : 0) * nb;
 
-    float c[4][4];
+    float c[NS][4];
 #pragma unroll
-    for (int s = 0; s < 4; ++s) {
-        const int n = tile * 64 + 16 * s + li;
+    for (int s = 0; s < NS; ++s) {
+        const int n = tile * 64 + 16 * (sg + s) + li;
         const float bv = (bias != nullptr && n < rows) ? bias[n] : 0.0f;
 #pragma unroll
         for (int r = 0; r < 4; ++r) c[s][r] = bv;
     }
 
-    auto fold = [&](auto u_tag, int b0) {
-        constexpr int U = decltype(u_tag)::value;
-        long av[U], bv[U][4];
-        uint32_t dh[U][4];
+    struct Set {
+        long av[U], bv[U][NS];
+        uint32_t dh[U][NS];
         float da[U][4];
+    };
+    auto load = [&](Set &S, int b0, int cnt) {
 #pragma unroll
         for (int u = 0; u < U; ++u) {
+            if (u >= cnt) break;
             const int b = b0 + u;
-            av[u] = arow_ok ? *reinterpret_cast<const long *>(ap + (size_t)b * GRX_QK) : 0l;
+            S.av[u] = arow_ok ? *reinterpret_cast<const long *>(ap + (size_t)b * GRX_QK) : 0l;
 #pragma unroll
-            for (int s = 0; s < 4; ++s) {
-                bv[u][s] = *reinterpret_cast<const long *>(bp + (size_t)b * 2048 + s * 256);
-                dh[u][s] = dp[(size_t)b * 64 + 16 * s];
+            for (int s = 0; s < NS; ++s) {
+                S.bv[u][s] = *reinterpret_cast<const long *>(bp + (size_t)b * 2048 + s * 256);
+                S.dh[u][s] = dp[(size_t)b * 64 + 16 * s];
             }
 #pragma unroll
-            for (int r = 0; r < 4; ++r) da[u][r] = sp[r][b];
+            for (int r = 0; r < 4; ++r) S.da[u][r] = sp[r][b];
         }
+    };
+    // per block in order: s = the int32 dot (one MFMA per 16x16 tile, K 32 =
+    // one Q8_0 block), then c = fma(f32(s) * dw, da, c)
+    auto fold = [&](const Set &S, int cnt) {
 #pragma unroll
         for (int u = 0; u < U; ++u) {
+            if (u >= cnt) break;
 #pragma unroll
-            for (int s = 0; s < 4; ++s) {
+            for (int s = 0; s < NS; ++s) {
                 v4i d = {0, 0, 0, 0};
-                d = __builtin_amdgcn_mfma_i32_16x16x32_i8(av[u], bv[u][s], d, 0, 0, 0);
-                const float dw = grx_f16_to_f32((uint16_t)dh[u][s]);
+                d = __builtin_amdgcn_mfma_i32_16x16x32_i8(S.av[u], S.bv[u][s], d, 0, 0, 0);
+                const float dw = grx_f16_to_f32((uint16_t)S.dh[u][s]);
 #pragma unroll
-                for (int r = 0; r < 4; ++r) c[s][r] = __fmaf_rn(__fmul_rn((float)d[r], dw), da[u][r], c[s][r]);
+                for (int r = 0; r < 4; ++r) c[s][r] = __fmaf_rn(__fmul_rn((float)d[r], dw), S.da[u][r], c[s][r]);
             }
         }
     };
+    Set s0, s1;
     int b = 0;
-    for (; b + kGemmBU <= nb; b += kGemmBU) fold(std::integral_constant<int, kGemmBU>{}, b);
-    for (; b < nb; ++b) fold(std::integral_constant<int, 1>{}, b);
+    if (nb >= U) load(s0, 0, U);
+    // whole groups of U with the next group's loads in flight
+    while (b + 2 * U <= nb) {
+        load(s1, b + U, U);
+        fold(s0, U);
+        b += U;
+        if (b + 2 * U <= nb) {
+            load(s0, b + U, U);
+            fold(s1, U);
+            b += U;
+        } else {
+            fold(s1, U);
+            b += U;
+            if (b + U <= nb) {  // one more whole group
+                load(s0, b, U);
+                fold(s0, U);
+                b += U;
+            }
+            goto tail;
+        }
+    }
+    if (b + U <= nb) {  // a last whole group, loaded already
+        fold(s0, U);
+        b += U;
+    }
+tail:
+    for (; b < nb; ++b) {  // the remaining blocks one at a time
+        Set t;
+        load(t, b, 1);
+        fold(t, 1);
+    }
 
     if constexpr (EPI == GRX_GEMM_SILU_Q) {
-        // The 64 columns of the tile are two Q8_0 blocks: block j holds
+        // The wave's columns are whole Q8_0 blocks (NS even): block j holds
         // columns 16*(2j) + li and 16*(2j+1) + li of the 16 lanes sharing lk,
         // so a row's block maximum is four xor-shuffles within those lanes.
+        static_assert(NS % 2 == 0, "rounded output needs whole 32-column blocks per wave");
         const int nr = rows / GRX_QK;
 #pragma unroll
-        for (int j = 0; j < 2; ++j) {
-            const int n0 = tile * 64 + 32 * j;
+        for (int j = 0; j < NS / 2; ++j) {
+            const int n0 = tile * 64 + 16 * sg + 32 * j;
             const bool col_ok = n0 < rows;  // rows % 32 == 0: whole blocks
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
@@ -152,8 +198,8 @@ __global__ __launch_bounds__(256) void gemm_q8_mfma_kernel(const int8_t *__restr
         }
     } else {
 #pragma unroll
-        for (int s = 0; s < 4; ++s) {
-            const int n = tile * 64 + 16 * s + li;
+        for (int s = 0; s < NS; ++s) {
+            const int n = tile * 64 + 16 * (sg + s) + li;
             if (n >= rows) continue;
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
@@ -168,6 +214,238 @@ __global__ __launch_bounds__(256) void gemm_q8_mfma_kernel(const int8_t *__restr
     }
 }
 
+// The product for many activation rows: a workgroup of eight waves (2 x 4)
+// computes 64 activation rows x 128 weight rows, each wave 32 x 32 (2 x 2
+// MFMA tiles).  kLdsCB blocks at a time of the rounded activations, the two
+// weight tiles, their scales and the activation scales are copied to LDS
+// with 16-byte loads, double-buffered (the next blocks' loads are in flight
+// while the current ones fold), so each activation row and weight row is
+// read from L2 once per workgroup instead of once per wave.  Per output the
+// fold is the same: c = fma(f32(s_b) * dw_b, da_b, c), blocks in order.
+constexpr int kLdsCB = 4;
+constexpr int kLdsThreads = 512;
+
+template <int EPI>
+__global__ __launch_bounds__(kLdsThreads) void gemm_q8_lds_kernel(const int8_t *__restrict__ qs,
+                                                                  const uint16_t *__restrict__ ds, int rows, int nb,
+                                                                  int tiles, const int8_t *__restrict__ xq,
+                                                                  const float *__restrict__ xs, int m,
+                                                                  const float *__restrict__ bias,
+                                                                  float *__restrict__ y, int ldc, float scale,
+                                                                  int8_t *__restrict__ yq, float *__restrict__ ys) {
+    // LDS per buffer: A [CB][64][32] bytes, B [CB][2 tiles][2 halves][64][16],
+    // weight scales [CB][128] u16, activation scales [CB][64] f32
+    constexpr int kA = kLdsCB * 64 * 32, kB = kLdsCB * 2 * 2048, kD = kLdsCB * 128 * 2, kS = kLdsCB * 64 * 4;
+    constexpr int kBuf = kA + kB + kD + kS;
+    __shared__ __align__(16) uint8_t lds[2 * kBuf];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wave >> 2, wn = wave & 3;             // wave rows 32*wm.., columns 32*wn..
+    const int mb = blockIdx.x * 64, t0 = blockIdx.y * 2;  // activation rows mb.., weight tiles t0, t0+1
+    const int K = nb * GRX_QK;
+    const int li = lane & 15, lk = lane >> 4;
+
+    // ---- the copy of blocks [b0, b0+CB) into registers, then LDS
+    // A: 64 rows x CB*32 bytes = 64 x (2*CB) 16-byte pieces (one per thread for CB 4)
+    // B: 2 tiles x CB x 2048 bytes = 2*CB*128 pieces (two per thread)
+    // dw: 2 tiles x CB x 128 bytes = 2*CB*8 pieces; da: 64 rows x CB floats (one piece per row)
+    constexpr int kApc = 64 * 2 * kLdsCB, kBpc = 2 * kLdsCB * 128, kDpc = 2 * kLdsCB * 8;
+    static_assert(kApc == kLdsThreads && kBpc == 2 * kLdsThreads, "copy split assumes CB 4 and 512 threads");
+    uint4 ra, rb[2], rd;
+    float4 rs;
+    auto gload = [&](int b0) {
+        {
+            const int row = tid / (2 * kLdsCB), piece = tid % (2 * kLdsCB);
+            const int gr = mb + row, bb = b0 + piece / 2;
+            ra = (gr < m && bb < nb) ? *reinterpret_cast<const uint4 *>(xq + (size_t)gr * K + (size_t)bb * 32 + 16 * (piece & 1))
+                                     : make_uint4(0, 0, 0, 0);
+        }
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const int pc = tid + h * kLdsThreads;
+            const int t = pc / (kLdsCB * 128), rem = pc % (kLdsCB * 128), u = rem / 128, off = rem % 128;
+            const int tile = t0 + t, bb = b0 + u;
+            rb[h] = (tile < tiles && bb < nb)
+                        ? *reinterpret_cast<const uint4 *>(qs + ((size_t)tile * nb + bb) * 2048 + 16 * off)
+                        : make_uint4(0, 0, 0, 0);
+        }
+        if (tid < kDpc) {
+            const int t = tid / (kLdsCB * 8), rem = tid % (kLdsCB * 8), u = rem / 8, off = rem % 8;
+            const int tile = t0 + t, bb = b0 + u;
+            rd = (tile < tiles && bb < nb)
+                     ? *reinterpret_cast<const uint4 *>(ds + ((size_t)tile * nb + bb) * 64 + 8 * off)
+                     : make_uint4(0, 0, 0, 0);
+        }
+        if (tid >= kDpc && tid < kDpc + 64) {
+            const int row = tid - kDpc, gr = mb + row;
+#pragma unroll
+            for (int u = 0; u < kLdsCB; ++u) {
+                const float v = (gr < m && b0 + u < nb) ? xs[(size_t)gr * nb + b0 + u] : 0.0f;
+                if (u == 0) rs.x = v;
+                if (u == 1) rs.y = v;
+                if (u == 2) rs.z = v;
+                if (u == 3) rs.w = v;
+            }
+        }
+    };
+    auto lstore = [&](int buf) {
+        uint8_t *base = lds + buf * kBuf;
+        {
+            const int row = tid / (2 * kLdsCB), piece = tid % (2 * kLdsCB), u = piece / 2;
+            *reinterpret_cast<uint4 *>(base + u * 2048 + row * 32 + 16 * (piece & 1)) = ra;
+        }
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const int pc = tid + h * kLdsThreads;
+            const int t = pc / (kLdsCB * 128), rem = pc % (kLdsCB * 128), u = rem / 128, off = rem % 128;
+            *reinterpret_cast<uint4 *>(base + kA + (u * 2 + t) * 2048 + 16 * off) = rb[h];
+        }
+        if (tid < kDpc) {
+            const int t = tid / (kLdsCB * 8), rem = tid % (kLdsCB * 8), u = rem / 8, off = rem % 8;
+            *reinterpret_cast<uint4 *>(base + kA + kB + (u * 128 + t * 64) * 2 + 16 * off) = rd;
+        }
+        if (tid >= kDpc && tid < kDpc + 64) {
+            const int row = tid - kDpc;
+            float *sa = reinterpret_cast<float *>(base + kA + kB + kD);
+            sa[0 * 64 + row] = rs.x;
+            sa[1 * 64 + row] = rs.y;
+            sa[2 * 64 + row] = rs.z;
+            sa[3 * 64 + row] = rs.w;
+        }
+    };
+
+    float c[2][2][4];  // [row frag][column frag][r]
+#pragma unroll
+    for (int g = 0; g < 2; ++g) {
+        const int n = t0 * 64 + 32 * wn + 16 * g + li;
+        const float bv = (bias != nullptr && n < rows) ? bias[n] : 0.0f;
+#pragma unroll
+        for (int f = 0; f < 2; ++f)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) c[f][g][r] = bv;
+    }
+    const int nsteps = (nb + kLdsCB - 1) / kLdsCB;
+    gload(0);
+    lstore(0);
+    __syncthreads();
+    for (int st = 0; st < nsteps; ++st) {
+        const int cur = st & 1;
+        if (st + 1 < nsteps) gload((st + 1) * kLdsCB);
+        const uint8_t *base = lds + cur * kBuf;
+        const uint16_t *dwl = reinterpret_cast<const uint16_t *>(base + kA + kB);
+        const float *dal = reinterpret_cast<const float *>(base + kA + kB + kD);
+        const int ub = min(kLdsCB, nb - st * kLdsCB);
+#pragma unroll
+        for (int u = 0; u < kLdsCB; ++u) {
+            if (u >= ub) break;
+            long av[2], bv[2];
+            float da[2][4], dw[2];
+#pragma unroll
+            for (int f = 0; f < 2; ++f) {
+                const int row = 32 * wm + 16 * f + li;
+                av[f] = *reinterpret_cast<const long *>(base + u * 2048 + row * 32 + 8 * lk);
+#pragma unroll
+                for (int r = 0; r < 4; ++r) da[f][r] = dal[u * 64 + 32 * wm + 16 * f + 4 * lk + r];
+            }
+#pragma unroll
+            for (int g = 0; g < 2; ++g) {
+                const int col = 32 * wn + 16 * g + li;  // 0..127 across the two tiles
+                const int t = col >> 6, cr = col & 63;
+                bv[g] = *reinterpret_cast<const long *>(base + kA + (u * 2 + t) * 2048 + (lk >> 1) * 1024 + cr * 16 +
+                                                        8 * (lk & 1));
+                dw[g] = grx_f16_to_f32(dwl[u * 128 + col]);
+            }
+#pragma unroll
+            for (int f = 0; f < 2; ++f)
+#pragma unroll
+                for (int g = 0; g < 2; ++g) {
+                    v4i d = {0, 0, 0, 0};
+                    d = __builtin_amdgcn_mfma_i32_16x16x32_i8(av[f], bv[g], d, 0, 0, 0);
+#pragma unroll
+                    for (int r = 0; r < 4; ++r)
+                        c[f][g][r] = __fmaf_rn(__fmul_rn((float)d[r], dw[g]), da[f][r], c[f][g][r]);
+                }
+        }
+        if (st + 1 < nsteps) {
+            lstore(cur ^ 1);
+            __syncthreads();
+        }
+    }
+
+#pragma unroll
+    for (int f = 0; f < 2; ++f) {
+        int drow[4];
+        bool drow_ok[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            drow[r] = mb + 32 * wm + 16 * f + 4 * lk + r;
+            drow_ok[r] = drow[r] < m;
+        }
+        if constexpr (EPI == GRX_GEMM_SILU_Q) {
+            // the wave's 32 columns are one Q8_0 block (rows % 32 == 0)
+            const int nr = rows / GRX_QK;
+            const int n0 = t0 * 64 + 32 * wn;
+            const bool col_ok = n0 < rows;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                float v[2];
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+                    const float x = c[f][h][r];
+                    v[h] = __fdiv_rn(x, __fadd_rn(grx_exp8(__fsub_rn(0.0f, x)), 1.0f));
+                }
+                const float a0 = fabsf(v[0]), a1 = fabsf(v[1]);
+                float amax = a0 > 0.0f ? a0 : 0.0f;
+                amax = a1 > amax ? a1 : amax;
+#pragma unroll
+                for (int o = 8; o > 0; o >>= 1) {
+                    const float t = __shfl_xor(amax, o, 16);
+                    amax = t > amax ? t : amax;
+                }
+                const float id = amax != 0.0f ? __fdiv_rn(127.0f, amax) : 0.0f;
+                if (col_ok && drow_ok[r]) {
+                    int8_t *qrow = yq + (size_t)drow[r] * rows + n0;
+#pragma unroll
+                    for (int h = 0; h < 2; ++h) {
+                        float q = rintf(__fmul_rn(v[h], id));
+                        q = fminf(fmaxf(q, -128.0f), 127.0f);
+                        qrow[16 * h + li] = (int8_t)(int)q;
+                    }
+                    if (li == 0) ys[(size_t)drow[r] * nr + n0 / GRX_QK] = __fmul_rn(amax, grx_bits_f32(0x3c010204u));
+                }
+            }
+        } else {
+#pragma unroll
+            for (int g = 0; g < 2; ++g) {
+                const int n = t0 * 64 + 32 * wn + 16 * g + li;
+                if (n >= rows) continue;
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    if (!drow_ok[r]) continue;
+                    float *yp = y + (size_t)drow[r] * ldc + n;
+                    if constexpr (EPI == GRX_GEMM_STORE) *yp = c[f][g][r];
+                    if constexpr (EPI == GRX_GEMM_ADD) *yp = __fadd_rn(*yp, c[f][g][r]);
+                    if constexpr (EPI == GRX_GEMM_AXPY_HALF) *yp = __fmaf_rn(0.5f, c[f][g][r], *yp);
+                    if constexpr (EPI == GRX_GEMM_SCALE) *yp = __fmul_rn(c[f][g][r], scale);
+                }
+            }
+        }
+    }
+}
+
+// Column-group width for a product: enough waves to cover the device
+// (16*NS weight rows per wave), NS = 4 once there are plenty.
+int pick_ns(int m, int rows, int epi) {
+    if (const char *e = getenv("GRX_GEMM_NS")) {
+        const int v = atoi(e);
+        if (v == 1 || v == 2 || v == 4) return (epi == GRX_GEMM_SILU_Q && v == 1) ? 2 : v;
+    }
+    const long waves4 = (long)grx_ceil_div(m, 16) * grx_ceil_div(rows, 64);
+    int ns = waves4 >= 4096 ? 4 : (waves4 >= 1024 ? 2 : 1);
+    if (epi == GRX_GEMM_SILU_Q && ns == 1) ns = 2;
+    return ns;
+}
+
 }  // namespace
 
 grx_status grx_gemm_q8_launch_ex(hipStream_t st, const grx_weight *w, const int8_t *xq, const float *xs, int m,
@@ -175,22 +453,59 @@ grx_status grx_gemm_q8_launch_ex(hipStream_t st, const grx_weight *w, const int8
     if (m <= 0 || w->rows == 0) return GRX_OK;
     if (o.epi == GRX_GEMM_SILU_Q && w->rows % GRX_QK != 0)
         return grx_fail(GRX_ESIZE, "rounded product output needs rows %% 32 == 0 (rows %d)", w->rows);
-    dim3 grid(grx_ceil_div(m, 64), w->tiles);
-#define GRX_GEMM_CASE(E)                                                                                    \
-    case E:                                                                                                 \
-        gemm_q8_mfma_kernel<E><<<grid, 256, 0, st>>>(w->qs, w->ds, w->rows, w->nb, xq, xs, m, bias, o.y, o.ldc, \
-                                                     o.scale, o.yq, o.ys);                                  \
+    // GRX_GEMM_LDS_MIN_M overrides the row count from which the LDS-staged
+    // tiles run (tests force each kernel with it)
+    const char *lm = getenv("GRX_GEMM_LDS_MIN_M");
+    if (m >= (lm ? atoi(lm) : 256)) {  // many rows: the LDS-staged 64 x 128 tiles
+        dim3 g2(grx_ceil_div(m, 64), grx_ceil_div(w->tiles, 2));
+#define GRX_GEMM_LDS(E)                                                                                           \
+    case E:                                                                                                       \
+        gemm_q8_lds_kernel<E><<<g2, kLdsThreads, 0, st>>>(w->qs, w->ds, w->rows, w->nb, w->tiles, xq, xs, m, bias, \
+                                                          o.y, o.ldc, o.scale, o.yq, o.ys);                       \
+        break;
+        switch (o.epi) {
+            GRX_GEMM_LDS(GRX_GEMM_STORE)
+            GRX_GEMM_LDS(GRX_GEMM_ADD)
+            GRX_GEMM_LDS(GRX_GEMM_AXPY_HALF)
+            GRX_GEMM_LDS(GRX_GEMM_SCALE)
+            GRX_GEMM_LDS(GRX_GEMM_SILU_Q)
+            default:
+                return grx_fail(GRX_EINVAL, "unknown product epilogue %d", o.epi);
+        }
+#undef GRX_GEMM_LDS
+        GRX_LAUNCHED("gemm_q8_lds_kernel");
+        return GRX_OK;
+    }
+    const int ns = pick_ns(m, w->rows, o.epi);
+    dim3 grid(grx_ceil_div(m, 64), w->tiles * (4 / ns));
+#define GRX_GEMM_GO(E, NS, U)                                                                                    \
+    gemm_q8_mfma_kernel<E, NS, U><<<grid, 256, 0, st>>>(w->qs, w->ds, w->rows, w->nb, xq, xs, m, bias, o.y, o.ldc, \
+                                                        o.scale, o.yq, o.ys)
+#define GRX_GEMM_CASE(E)                \
+    case E:                             \
+        if (ns == 4)                    \
+            GRX_GEMM_GO(E, 4, 4);       \
+        else if (ns == 2)               \
+            GRX_GEMM_GO(E, 2, 6);       \
+        else                            \
+            GRX_GEMM_GO(E, 1, 8);       \
         break;
     switch (o.epi) {
         GRX_GEMM_CASE(GRX_GEMM_STORE)
         GRX_GEMM_CASE(GRX_GEMM_ADD)
         GRX_GEMM_CASE(GRX_GEMM_AXPY_HALF)
         GRX_GEMM_CASE(GRX_GEMM_SCALE)
-        GRX_GEMM_CASE(GRX_GEMM_SILU_Q)
+        case GRX_GEMM_SILU_Q:
+            if (ns == 4)
+                GRX_GEMM_GO(GRX_GEMM_SILU_Q, 4, 4);
+            else
+                GRX_GEMM_GO(GRX_GEMM_SILU_Q, 2, 6);
+            break;
         default:
             return grx_fail(GRX_EINVAL, "unknown product epilogue %d", o.epi);
     }
 #undef GRX_GEMM_CASE
+#undef GRX_GEMM_GO
     GRX_LAUNCHED("gemm_q8_mfma_kernel");
     return GRX_OK;
 }

@@ -38,6 +38,25 @@ def test_tiny_encode_bit_exact(kern, orc, conv_norm, f16):
     enc.close()
 
 
+@pytest.mark.parametrize("rq", ["0", "8", "16"])
+def test_tiny_attention_variants_bit_exact(kern, orc, monkeypatch, rq):
+    """The unstaged attention kernel and the LDS-staged one at 8 and 16 query
+    rows per workgroup give the same bits as the oracle (T = 19: one query
+    block, rows in the 6x16 panels and in gemvRows)."""
+    monkeypatch.setenv("GRX_CONF_ATTN_RQ", rq)
+    hp = dict(CONFORMER_TINY)
+    t = conformer_model(hp, seed=24)
+    mel, frames, valid = _mels(hp, 2, 1.5, 35)
+    vals = [valid, valid - 30]
+    enc = _enc(kern, hp, t)
+    got, lens = enc.encode(mel, vals)
+    o = orc.ConformerOracle(hp, t)
+    for b in range(2):
+        want, L = o.encode(mel[b], vals[b])
+        assert np.array_equal(got[b].view(np.uint32), want.view(np.uint32)), (rq, b)
+    enc.close()
+
+
 def test_tiny_shape_change_and_rerun(kern, orc):
     """A second call with another batch and frame count re-plans the work;
     repeating a call gives the same bits."""

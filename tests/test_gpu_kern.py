@@ -170,6 +170,40 @@ def test_matmul_matrix_cores_all_small_sizes(kern, orc):
         del os.environ["GRX_GEMM_MIN_M"]
 
 
+@pytest.mark.parametrize("ns", ["1", "2", "4"])
+def test_matmul_matrix_cores_each_tile_width(kern, orc, ns):
+    """Every wave-tile width of the matrix-core product (16, 32 or 64 weight
+    rows per wave, GRX_GEMM_NS) over block counts that hit each branch of
+    its two-register-set walk (nb = 1 .. 40 around multiples of 4, 6, 8)."""
+    rng = np.random.default_rng(43 + int(ns))
+    os.environ["GRX_GEMM_MIN_M"] = "1"
+    os.environ["GRX_GEMM_NS"] = ns
+    try:
+        for nb in (1, 3, 4, 5, 6, 7, 8, 9, 11, 12, 13, 16, 17, 18, 24, 25, 40):
+            for m, n in ((1, 64), (17, 100), (70, 130)):
+                _check_matmul(kern, orc, rng, m, n, 32 * nb, bias=(nb % 2 == 1))
+    finally:
+        del os.environ["GRX_GEMM_MIN_M"]
+        del os.environ["GRX_GEMM_NS"]
+
+
+@pytest.mark.parametrize("lds_min", ["1", "100000"])
+def test_matmul_lds_tiles_and_register_tiles(kern, orc, lds_min):
+    """The LDS-staged 64 x 128 product forced for every row count
+    (GRX_GEMM_LDS_MIN_M=1), and the register-tiled one for every row count,
+    over partial row, column and block groups: bit-identical to the oracle."""
+    rng = np.random.default_rng(47)
+    os.environ["GRX_GEMM_MIN_M"] = "1"
+    os.environ["GRX_GEMM_LDS_MIN_M"] = lds_min
+    try:
+        for nb in (1, 3, 4, 5, 8, 9, 13):
+            for m, n in ((1, 64), (20, 100), (64, 128), (65, 129), (200, 300)):
+                _check_matmul(kern, orc, rng, m, n, 32 * nb, bias=(m % 2 == 1))
+    finally:
+        del os.environ["GRX_GEMM_MIN_M"]
+        del os.environ["GRX_GEMM_LDS_MIN_M"]
+
+
 @pytest.mark.parametrize("m,n,k", [(126, 4096, 1024), (300, 1024, 1024), (1500, 512, 512), (251, 1024, 1024),
                                    (16, 4096, 1024)])
 def test_matmul_many_rows_bit_exact(kern, orc, m, n, k):
