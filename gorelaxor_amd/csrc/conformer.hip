@@ -30,6 +30,7 @@ namespace {
 constexpr int kRowThreads = 256;
 constexpr int kAttnQ = 32;        // queries per attention block (encoder.go:211)
 constexpr int kAttnThreads = 512;
+constexpr int kAttnLdsThreads = 1024;
 
 // encoder.go:33-38 (subOut) for the non-causal pre-encoder, and the valid
 // length after s halvings.
@@ -55,42 +56,73 @@ __device__ inline float go_max(float a, float b) {
 
 // ---------------------------------------------------------------- pre-encoder
 
-// conv0 (encoder.go:41-77) on the log-mel planes of B utterances ([b][mel]
-// [frame], frames past valid[b] read as 0), then maskRows and ReLU
-// (encoder.go:145-147): out [b][T1][F1][c].  Each output starts from the bias
-// and takes AddScaled of the nonzero taps in order: fma for the channels of
-// whole groups of eight, unfused for the rest.
-__global__ void sub_conv0_kernel(const float *__restrict__ mel, int B, int frames, int nm,
-                                 const int *__restrict__ valid, const float *__restrict__ w,
-                                 const float *__restrict__ bias, int c, int T1, int F1, float *__restrict__ out) {
-    const size_t total = (size_t)B * T1 * F1 * c;
-    for (size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x; idx < total;
-         idx += (size_t)gridDim.x * blockDim.x) {
-        const int ch = (int)(idx % c);
-        const size_t pos = idx / c;
-        const int f = (int)(pos % F1);
-        const int t = (int)((pos / F1) % T1);
-        const int b = (int)(pos / ((size_t)F1 * T1));
-        const int vb = valid[b];
-        if (t >= stage_len(vb, 1)) {
-            out[idx] = 0.f;
-            continue;
-        }
-        const int tv = min(frames, vb);
-        const float *mb = mel + (size_t)b * nm * frames;
-        const bool fm = ch < (c & ~7);
-        float v[9], wv[9];
+// conv0 then the first depthwise convolution (encoder.go:141-150) in one
+// pass: the conv0 outputs a depthwise output needs (3x3 positions, maskRows
+// and ReLU applied) are recomputed from the log-mel values instead of being
+// written out, which at 256 channels would be 64x the mel's size.  One
+// workgroup of c threads (a channel each) per output frame row (b, t2),
+// walking its F2 positions with the channel's taps in registers; the mel
+// rows 4*t2-3 .. 4*t2+3 (zero outside the plane and past the valid frames)
+// are staged in LDS.  Output rows past the stage's valid length are zeroed,
+// and each position's c values rounded to Q8_0 for the pointwise Linear.
+// conv0's arithmetic: from the bias, AddScaled of the nonzero taps in order
+// (fma for channels of whole groups of eight); the depthwise: from the bias,
+// w*x unfused over the taps in range.
+__global__ void sub_conv01_kernel(const float *__restrict__ mel, int frames, int nm, const int *__restrict__ valid,
+                                  const float *__restrict__ w0, const float *__restrict__ b0,
+                                  const float *__restrict__ w2, const float *__restrict__ b2, int c, int T1, int F1,
+                                  int T2, int F2, int8_t *__restrict__ xq, float *__restrict__ xs) {
+    extern __shared__ float patch[];  // [7][4*F2 + 3], column q = mel column q - 3
+    const int ch = threadIdx.x, t2 = blockIdx.x % T2, b = blockIdx.x / T2;
+    const int W = 4 * F2 + 3;
+    const int vb = valid[b], tv = min(frames, vb);
+    const int L1 = stage_len(vb, 1), L2 = stage_len(vb, 2);
+    for (int e = ch; e < 7 * W; e += blockDim.x) {
+        const int r = e / W, q = e % W, ti = 4 * t2 - 3 + r, fi = q - 3;
+        patch[e] = (ti >= 0 && ti < tv && fi >= 0 && fi < nm) ? mel[((size_t)b * nm + fi) * frames + ti] : 0.f;
+    }
+    __syncthreads();
+    float w0v[9], w2v[9];
 #pragma unroll
-        for (int j = 0; j < 9; ++j) {
-            const int ti = 2 * t + j / 3 - 1, fi = 2 * f + j % 3 - 1;
-            v[j] = (ti >= 0 && ti < tv && fi >= 0 && fi < nm) ? mb[(size_t)fi * frames + ti] : 0.f;
-            wv[j] = w[j * c + ch];
-        }
-        float o = bias[ch];
+    for (int j = 0; j < 9; ++j) {
+        w0v[j] = w0[j * c + ch];
+        w2v[j] = w2[j * c + ch];
+    }
+    const float bias0 = b0[ch], bias2 = b2[ch];
+    const bool fm = ch < (c & ~7);
+    for (int f2 = 0; f2 < F2; ++f2) {
+        float o = 0.f;
+        if (t2 < L2) {
+            // the 7x7 mel values of this position: patch columns 4f2 .. 4f2+6
+            float pv[7][7];
 #pragma unroll
-        for (int j = 0; j < 9; ++j)
-            if (v[j] != 0.f) o = fm ? __fmaf_rn(v[j], wv[j], o) : __fadd_rn(o, __fmul_rn(v[j], wv[j]));
-        out[idx] = o < 0.f ? 0.f : o;
+            for (int r = 0; r < 7; ++r)
+#pragma unroll
+                for (int q = 0; q < 7; ++q) pv[r][q] = patch[r * W + 4 * f2 + q];
+            o = bias2;
+#pragma unroll
+            for (int j2 = 0; j2 < 9; ++j2) {
+                const int kt = j2 / 3, kf = j2 % 3;
+                const int ti = 2 * t2 + kt - 1, fi = 2 * f2 + kf - 1;  // conv0 output position
+                if (ti < 0 || ti >= T1 || fi < 0 || fi >= F1) continue;
+                float x = 0.f;
+                if (ti < L1) {
+                    float a = bias0;
+#pragma unroll
+                    for (int j = 0; j < 9; ++j) {
+                        // mel (2ti + j/3 - 1, 2fi + j%3 - 1) = pv[2kt + j/3][2kf + j%3]; zero taps
+                        // are skipped (a select, not a branch)
+                        const float v = pv[2 * kt + j / 3][2 * kf + j % 3];
+                        const float t = fm ? __fmaf_rn(v, w0v[j], a) : __fadd_rn(a, __fmul_rn(v, w0v[j]));
+                        a = v != 0.f ? t : a;
+                    }
+                    x = a < 0.f ? 0.f : a;
+                }
+                o = __fadd_rn(o, __fmul_rn(w2v[j2], x));
+            }
+        }
+        const size_t p = ((size_t)b * T2 + t2) * F2 + f2;
+        quant32_store(o, xq + p * c + ch, xs + p * (c / 32) + ch / 32, ch & 31);
     }
 }
 
@@ -115,7 +147,11 @@ __global__ void sub_dwconv_kernel(const float *__restrict__ in, int T, int F, in
         for (int j = 0; j < 9; ++j) {
             const int ti = 2 * t1 + j / 3 - 1, fi = 2 * f1 + j % 3 - 1;
             ok[j] = ti >= 0 && ti < T && fi >= 0 && fi < F;  // taps outside the plane are skipped
-            float x = ok[j] ? in[(((size_t)b * T + ti) * F + fi) * c + ch] : 0.f;
+            // the load is issued at a clamped address and the value chosen
+            // afterwards, so the nine loads stay in flight together
+            const int tc = min(max(ti, 0), T - 1), fc = min(max(fi, 0), F - 1);
+            float x = in[(((size_t)b * T + tc) * F + fc) * c + ch];
+            x = ok[j] ? x : 0.f;
             if constexpr (RELU_IN) x = ti < Lin ? (x < 0.f ? 0.f : x) : 0.f;
             xv[j] = x;
             wv[j] = w[j * c + ch];
@@ -190,11 +226,12 @@ __global__ __launch_bounds__(kRowThreads) void ln_rows_kernel(float *__restrict_
                                                               const float *__restrict__ w2,
                                                               const float *__restrict__ b2,
                                                               int8_t *__restrict__ xq, float *__restrict__ xs) {
-    extern __shared__ float row[];
+    extern __shared__ __align__(16) float row[];
     __shared__ double red[16];
     const int r = blockIdx.x, tid = threadIdx.x;
     float *xr = x + (size_t)r * n;
-    for (int i = tid; i < n; i += blockDim.x) row[i] = xr[i];
+    for (int i = tid; i < n / 4; i += blockDim.x)  // n % 32 == 0
+        reinterpret_cast<float4 *>(row)[i] = reinterpret_cast<const float4 *>(xr)[i];
     __syncthreads();
     ln_row(row, n, w1, b1, red);
     if constexpr (OUT) {
@@ -346,9 +383,9 @@ __device__ __forceinline__ void stage_f4(float *dst, int sdst, const float *src,
     for (int e0 = threadIdx.x; e0 < n; e0 += 4 * nt) {
         float4 v[4];
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
-            const int e = e0 + u * nt;
-            if (e < n) v[u] = *reinterpret_cast<const float4 *>(src + (size_t)(e / c4) * ssrc + 4 * (e % c4));
+        for (int u = 0; u < 4; ++u) {  // clamped: the four loads stay in flight together
+            const int e = min(e0 + u * nt, n - 1);
+            v[u] = *reinterpret_cast<const float4 *>(src + (size_t)(e / c4) * ssrc + 4 * (e % c4));
         }
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
@@ -394,7 +431,7 @@ __device__ __forceinline__ void packed4(const FA &a, const FB &b, int k, float o
 // full column counts).  Only the band of bd that the rows use is computed:
 // bd[i][nq-1-i+kk] for the nk keys.
 template <int RQ>
-__global__ __launch_bounds__(kAttnThreads) void conf_attn_lds_kernel(
+__global__ __launch_bounds__(kAttnLdsThreads) void conf_attn_lds_kernel(
     const float *__restrict__ qkv, const float *__restrict__ pp, int ldp, const float *__restrict__ pos_u,
     const float *__restrict__ pos_v, const int *__restrict__ valid, int T, int D, int hd, float scale,
     int8_t *__restrict__ xq, float *__restrict__ xs) {
@@ -613,7 +650,7 @@ __global__ __launch_bounds__(kRowThreads) void conf_dwconv_kernel(const float *_
                                                                   const float *__restrict__ cn_w,
                                                                   const float *__restrict__ cn_b,
                                                                   int8_t *__restrict__ xq, float *__restrict__ xs) {
-    extern __shared__ float row[];
+    extern __shared__ __align__(16) float row[];
     __shared__ double red[16];
     const int r = blockIdx.x, t = r % T, b = r / T, tid = threadIdx.x;
     const int padL = (K - 1) / 2;
@@ -627,8 +664,9 @@ __global__ __launch_bounds__(kRowThreads) void conf_dwconv_kernel(const float *_
             for (int u = 0; u < 8; ++u) {
                 const int j = j0 + u, ti = t + j - padL;
                 ok[u] = j < K && ti >= 0 && ti < T;  // taps outside the frames are skipped
-                xv[u] = ok[u] ? gb[(size_t)ti * D + c] : 0.f;
-                wv[u] = ok[u] ? w[(size_t)j * D + c] : 0.f;
+                // clamped addresses keep the eight loads in flight together
+                xv[u] = gb[(size_t)min(max(ti, 0), T - 1) * D + c];
+                wv[u] = w[(size_t)min(j, K - 1) * D + c];
             }
 #pragma unroll
             for (int u = 0; u < 8; ++u)
@@ -643,6 +681,78 @@ __global__ __launch_bounds__(kRowThreads) void conf_dwconv_kernel(const float *_
         const float v = row[c];
         const float s = __fdiv_rn(v, __fadd_rn(grx_exp8(__fsub_rn(0.0f, v)), 1.0f));
         quant32_store(s, xq + (size_t)r * D + c, xs + (size_t)r * (D / 32) + c / 32, c & 31);
+    }
+}
+
+// The same depthwise convolution, folded batch norm, SiLU and rounding for
+// kDwRows consecutive frames x 64 channels per workgroup of four waves: the
+// channels' window of kDwRows + K - 1 gated frames and their K taps are
+// staged in LDS once (instead of K reads per output frame), then wave w
+// runs frames 4w .. 4w+3 side by side, lane = channel, taps in order for
+// each frame.  grid (ceil(T/kDwRows), D/64, B).
+constexpr int kDwRows = 16;
+__global__ __launch_bounds__(256) void conf_dwconv_win_kernel(const float *__restrict__ g, int T, int D, int K,
+                                                              const float *__restrict__ w,
+                                                              const float *__restrict__ dwb,
+                                                              const float *__restrict__ cn_w,
+                                                              const float *__restrict__ cn_b,
+                                                              int8_t *__restrict__ xq, float *__restrict__ xs) {
+    extern __shared__ float win[];  // [kDwRows + K - 1][64] frames, then [K][64] taps
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int t0 = blockIdx.x * kDwRows, c0 = blockIdx.y * 64, b = blockIdx.z, c = c0 + lane;
+    const int padL = (K - 1) / 2, nrow = min(kDwRows, T - t0), wr = nrow + K - 1;
+    float *wl = win + (kDwRows + K - 1) * 64;
+    const float *gb = g + (size_t)b * T * D + c0;
+    const int n = (wr + K) * 64;
+    for (int e0 = tid; e0 < n; e0 += 8 * 256) {
+        // every load issued at a clamped address, the value chosen after,
+        // so the eight stay in flight together
+        float v[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const int e = min(e0 + u * 256, n - 1), r = e >> 6, l = e & 63, ti = t0 - padL + r;
+            const float *src = r < wr ? gb + (size_t)min(max(ti, 0), T - 1) * D + l
+                                      : w + (size_t)min(r - wr, K - 1) * D + c0 + l;
+            v[u] = *src;
+        }
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const int e = e0 + u * 256, r = e >> 6, l = e & 63, ti = t0 - padL + r;
+            if (e < n) {
+                if (r < wr)
+                    win[e] = (ti >= 0 && ti < T) ? v[u] : 0.f;
+                else
+                    wl[(r - wr) * 64 + l] = v[u];
+            }
+        }
+    }
+    __syncthreads();
+    float o[4];
+    const float b0 = dwb != nullptr ? dwb[c] : 0.f;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) o[r] = b0;
+    const int r0 = 4 * wave;
+    for (int j = 0; j < K; ++j) {
+        const float wj = wl[j * 64 + lane];
+        float xv[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) xv[r] = win[(r0 + r + j) * 64 + lane];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int ti = t0 + r0 + r + j - padL;  // taps outside the frames are skipped
+            const float t = __fadd_rn(o[r], __fmul_rn(wj, xv[r]));
+            o[r] = (r0 + r < nrow && ti >= 0 && ti < T) ? t : o[r];
+        }
+    }
+    const float sw = cn_w[c], sb = cn_b[c];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        if (r0 + r < nrow) {  // uniform across the wave
+            const float a = __fadd_rn(__fmul_rn(o[r], sw), sb);
+            const float sl = __fdiv_rn(a, __fadd_rn(grx_exp8(__fsub_rn(0.0f, a)), 1.0f));
+            const size_t row = (size_t)b * T + t0 + r0 + r;
+            quant32_store(sl, xq + row * D + c, xs + row * (D / 32) + c / 32, c & 31);
+        }
     }
 }
 
@@ -677,6 +787,7 @@ struct grx_conformer {
     // shape-dependent state
     int B = 0, frames = 0, T = 0;
     int attn_rq = 0;         // query rows per staged attention workgroup (0: unstaged kernel)
+    bool dw_win = false;     // the windowed depthwise kernel runs (its LDS was granted)
     size_t attn_smem = 0;
     float *mel = nullptr, *sub0 = nullptr, *suby = nullptr, *x = nullptr, *qkv = nullptr, *pp = nullptr;
     float *conv = nullptr, *glu = nullptr, *pos = nullptr;
@@ -1003,10 +1114,18 @@ grx_status cshape(grx_conformer *m, int B, int frames) {
             m->attn_smem = need;
         }
     }
+    {  // the windowed depthwise convolution's LDS (frames and taps)
+        const size_t need = (size_t)(kDwRows + 2 * hp.conv_kernel - 1) * 64 * 4;
+        m->dw_win = d % 64 == 0 && !hp.conv_ln && need <= 160 * 1024 &&
+                    (need <= 64 * 1024 || hipFuncSetAttribute((const void *)conf_dwconv_win_kernel,
+                                                              hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                              (int)need) == hipSuccess);
+        (void)hipGetLastError();
+    }
     grx_status s;
     auto &w = m->work;
     if ((s = calloc_t(w, (size_t)B * nm * frames, &m->mel)) != GRX_OK) return s;
-    if ((s = calloc_t(w, (size_t)B * T1 * F1 * c, &m->sub0)) != GRX_OK) return s;
+    if ((s = calloc_t(w, (size_t)B * T * F3 * c, &m->sub0)) != GRX_OK) return s;
     if ((s = calloc_t(w, (size_t)B * T2 * F2 * c, &m->suby)) != GRX_OK) return s;
     // rounded activations: the largest row set of any product
     size_t qn = std::max({(size_t)B * T2 * F2 * c, R * (size_t)c * F3, R * (size_t)hp.dff, R * 2 * (size_t)d});
@@ -1045,12 +1164,9 @@ grx_status enqueue_encode(grx_conformer *m, hipStream_t st) {
     const int R = B * T, hd = d / hp.heads, cF = c * F3;
     grx_status s;
     // pre-encoder (encoder.go:123-167)
-    sub_conv0_kernel<<<grid_for((size_t)B * T1 * F1 * c), 256, 0, st>>>(m->mel, B, frames, nm, m->valid, m->w0, m->b0,
-                                                                       c, T1, F1, m->sub0);
-    GRX_LAUNCHED("sub_conv0_kernel");
-    sub_dwconv_kernel<false><<<B * T2 * F2, c, 0, st>>>(m->sub0, T1, F1, c, m->valid, 2, m->w2, m->b2, T2, F2, m->xq,
-                                                        m->xs);
-    GRX_LAUNCHED("sub_dwconv_kernel");
+    sub_conv01_kernel<<<B * T2, c, (size_t)7 * (4 * F2 + 3) * 4, st>>>(m->mel, frames, nm, m->valid, m->w0, m->b0,
+                                                                       m->w2, m->b2, c, T1, F1, T2, F2, m->xq, m->xs);
+    GRX_LAUNCHED("sub_conv01_kernel");
     if ((s = grx_gemm_q8_launch(st, m->w3, m->xq, m->xs, B * T2 * F2, m->b3, m->suby, c)) != GRX_OK) return s;
     sub_dwconv_kernel<true><<<B * T * F3, c, 0, st>>>(m->suby, T2, F2, c, m->valid, 3, m->w5, m->b5, T, F3, m->xq,
                                                       m->xs);
@@ -1103,11 +1219,11 @@ grx_status enqueue_encode(grx_conformer *m, hipStream_t st) {
         GRX_LAUNCHED("ln_rows_kernel");
         if ((s = grx_gemm_q8_launch(st, Bk.qkv, m->xq, m->xs, R, Bk.qkv_b, m->qkv, 3 * d)) != GRX_OK) return s;
         if (m->attn_rq == 8)
-            conf_attn_lds_kernel<8><<<dim3(nblk * (kAttnQ / 8), hp.heads, B), kAttnThreads, attn_smem, st>>>(
+            conf_attn_lds_kernel<8><<<dim3(nblk * (kAttnQ / 8), hp.heads, B), kAttnLdsThreads, attn_smem, st>>>(
                 m->qkv, m->pp + (size_t)i * d, hp.layers * d, Bk.pos_u, Bk.pos_v, m->valid, T, d, hd, scale, m->xq,
                 m->xs);
         else if (m->attn_rq == 16)
-            conf_attn_lds_kernel<16><<<dim3(nblk * (kAttnQ / 16), hp.heads, B), kAttnThreads, attn_smem, st>>>(
+            conf_attn_lds_kernel<16><<<dim3(nblk * (kAttnQ / 16), hp.heads, B), kAttnLdsThreads, attn_smem, st>>>(
                 m->qkv, m->pp + (size_t)i * d, hp.layers * d, Bk.pos_u, Bk.pos_v, m->valid, T, d, hd, scale, m->xq,
                 m->xs);
         else
@@ -1132,6 +1248,10 @@ grx_status enqueue_encode(grx_conformer *m, hipStream_t st) {
         if (hp.conv_ln)
             conf_dwconv_kernel<true><<<R, kRowThreads, row_smem, st>>>(m->glu, T, d, hp.conv_kernel, Bk.dw, Bk.dw_b,
                                                                        Bk.cn_w, Bk.cn_b, m->xq, m->xs);
+        else if (m->dw_win)
+            conf_dwconv_win_kernel<<<dim3((T + kDwRows - 1) / kDwRows, d / 64, B), 256,
+                                     (size_t)(kDwRows + 2 * hp.conv_kernel - 1) * 64 * 4, st>>>(
+                m->glu, T, d, hp.conv_kernel, Bk.dw, Bk.dw_b, Bk.cn_w, Bk.cn_b, m->xq, m->xs);
         else
             conf_dwconv_kernel<false><<<R, kRowThreads, row_smem, st>>>(m->glu, T, d, hp.conv_kernel, Bk.dw, Bk.dw_b,
                                                                         Bk.cn_w, Bk.cn_b, m->xq, m->xs);

@@ -169,21 +169,40 @@ __device__ __forceinline__ float dot_go4(const float *x, const float *y, int n, 
 }
 
 // Rows [r0, r0+rows) of one head's cached values (rows `ld` floats apart,
-// the head's hd values at `base`) into LDS vl[rows][hd], every thread of the
-// block issuing its loads at once (float4 when hd % 4 == 0).
+// the head's hd values at `base`) into LDS vl[rows][hd], every thread
+// keeping eight loads in flight (16-byte loads when hd % 4 == 0).
 __device__ __forceinline__ void stage_rows(float *vl, const float *base, size_t ld, int r0, int rows, int hd) {
     const int nt = blockDim.x, tid = threadIdx.x;
+    constexpr int kF = 8;
     if ((hd & 3) == 0 && (ld & 3) == 0) {
-        const int n4 = rows * hd / 4;
-        for (int i = tid; i < n4; i += nt) {
-            const int j = (4 * i) / hd, e = (4 * i) % hd;
-            *reinterpret_cast<float4 *>(vl + 4 * i) =
-                *reinterpret_cast<const float4 *>(base + (size_t)(r0 + j) * ld + e);
+        const int h4 = hd >> 2, n4 = rows * h4;
+        for (int i0 = tid; i0 < n4; i0 += kF * nt) {
+            float4 v[kF];
+#pragma unroll
+            for (int u = 0; u < kF; ++u) {  // clamped: the loads stay in flight together
+                const int i = min(i0 + u * nt, n4 - 1);
+                v[u] = *reinterpret_cast<const float4 *>(base + (size_t)(r0 + i / h4) * ld + 4 * (i % h4));
+            }
+#pragma unroll
+            for (int u = 0; u < kF; ++u) {
+                const int i = i0 + u * nt;
+                if (i < n4) *reinterpret_cast<float4 *>(vl + 4 * i) = v[u];
+            }
         }
     } else {
-        for (int i = tid; i < rows * hd; i += nt) {
-            const int j = i / hd, e = i % hd;
-            vl[i] = base[(size_t)(r0 + j) * ld + e];
+        const int n = rows * hd;
+        for (int i0 = tid; i0 < n; i0 += kF * nt) {
+            float v[kF];
+#pragma unroll
+            for (int u = 0; u < kF; ++u) {
+                const int i = min(i0 + u * nt, n - 1);
+                v[u] = base[(size_t)(r0 + i / hd) * ld + i % hd];
+            }
+#pragma unroll
+            for (int u = 0; u < kF; ++u) {
+                const int i = i0 + u * nt;
+                if (i < n) vl[i] = v[u];
+            }
         }
     }
 }

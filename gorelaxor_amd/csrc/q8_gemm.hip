@@ -92,6 +92,9 @@ __global__ __launch_bounds__(256) void gemm_q8_mfma_kernel(const int8_t *__restr
         uint32_t dh[U][NS];
         float da[U][4];
     };
+    // activation scales four blocks per 16-byte load when the rows allow it
+    // (nb % 4 == 0, whole groups of U): one load per four blocks per row
+    const bool da4 = (nb & 3) == 0;
     auto load = [&](Set &S, int b0, int cnt) {
 #pragma unroll
         for (int u = 0; u < U; ++u) {
@@ -103,8 +106,25 @@ __global__ __launch_bounds__(256) void gemm_q8_mfma_kernel(const int8_t *__restr
                 S.bv[u][s] = *reinterpret_cast<const long *>(bp + (size_t)b * 2048 + s * 256);
                 S.dh[u][s] = dp[(size_t)b * 64 + 16 * s];
             }
+        }
+        if (U % 4 == 0 && cnt == U && da4) {
 #pragma unroll
-            for (int r = 0; r < 4; ++r) S.da[u][r] = sp[r][b];
+            for (int r = 0; r < 4; ++r)
+#pragma unroll
+                for (int q = 0; q < U / 4; ++q) {
+                    const float4 v = *reinterpret_cast<const float4 *>(sp[r] + b0 + 4 * q);
+                    S.da[4 * q + 0][r] = v.x;
+                    S.da[4 * q + 1][r] = v.y;
+                    S.da[4 * q + 2][r] = v.z;
+                    S.da[4 * q + 3][r] = v.w;
+                }
+        } else {
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                if (u >= cnt) break;
+#pragma unroll
+                for (int r = 0; r < 4; ++r) S.da[u][r] = sp[r][b0 + u];
+            }
         }
     };
     // per block in order: s = the int32 dot (one MFMA per 16x16 tile, K 32 =
@@ -433,6 +453,17 @@ __global__ __launch_bounds__(kLdsThreads) void gemm_q8_lds_kernel(const int8_t *
     }
 }
 
+// Blocks per register set for each wave-tile width (swept on the device).
+#ifndef GRX_GEMM_U1
+#define GRX_GEMM_U1 8
+#endif
+#ifndef GRX_GEMM_U2
+#define GRX_GEMM_U2 8
+#endif
+#ifndef GRX_GEMM_U4
+#define GRX_GEMM_U4 4
+#endif
+
 // Column-group width for a product: enough waves to cover the device
 // (16*NS weight rows per wave), NS = 4 once there are plenty.
 int pick_ns(int m, int rows, int epi) {
@@ -484,11 +515,11 @@ grx_status grx_gemm_q8_launch_ex(hipStream_t st, const grx_weight *w, const int8
 #define GRX_GEMM_CASE(E)                \
     case E:                             \
         if (ns == 4)                    \
-            GRX_GEMM_GO(E, 4, 4);       \
+            GRX_GEMM_GO(E, 4, GRX_GEMM_U4); \
         else if (ns == 2)               \
-            GRX_GEMM_GO(E, 2, 6);       \
+            GRX_GEMM_GO(E, 2, GRX_GEMM_U2); \
         else                            \
-            GRX_GEMM_GO(E, 1, 8);       \
+            GRX_GEMM_GO(E, 1, GRX_GEMM_U1); \
         break;
     switch (o.epi) {
         GRX_GEMM_CASE(GRX_GEMM_STORE)
@@ -497,9 +528,9 @@ grx_status grx_gemm_q8_launch_ex(hipStream_t st, const grx_weight *w, const int8
         GRX_GEMM_CASE(GRX_GEMM_SCALE)
         case GRX_GEMM_SILU_Q:
             if (ns == 4)
-                GRX_GEMM_GO(GRX_GEMM_SILU_Q, 4, 4);
+                GRX_GEMM_GO(GRX_GEMM_SILU_Q, 4, GRX_GEMM_U4);
             else
-                GRX_GEMM_GO(GRX_GEMM_SILU_Q, 2, 6);
+                GRX_GEMM_GO(GRX_GEMM_SILU_Q, 2, GRX_GEMM_U2);
             break;
         default:
             return grx_fail(GRX_EINVAL, "unknown product epilogue %d", o.epi);
