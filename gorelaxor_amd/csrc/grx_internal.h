@@ -257,6 +257,13 @@ struct GemvArgs {
     double ln_eps;
     // added to *pos for the rows of this launch (QKV, QKV_ROPE, EMBED_LN)
     int pos_add;
+    // nonzero: the M rows are independent streams at one position (each
+    // with its own token, KV cache kv_stream floats after the previous
+    // stream's, and argmax record hist_stream ints apart) instead of
+    // consecutive positions of one stream
+    int streams;
+    size_t kv_stream;
+    int hist_stream;
 };
 
 grx_status grx_gemv_launch(hipStream_t st, int m, int pro, int epi, const GemvArgs &a,

@@ -31,6 +31,10 @@ namespace {
 #define GRX_GEMV_NT 1
 #endif
 constexpr int BU = GRX_GEMV_BU;  // blocks whose loads are issued before any is used
+// Several activation rows over several waves: the blocks go in rounds of
+// kRound, each round's partial products through LDS, and wave m folds row
+// m after every round (so LDS holds one round, not every block).
+constexpr int kRound = 32;
 
 // Weight loads are non-temporal: each weight byte is read once per product,
 // and streaming it past the caches measured 6.7-6.8 TB/s on a 570 MB ring
@@ -121,7 +125,8 @@ __global__ __launch_bounds__(64 * W) void gemv_q8_kernel(const GemvArgs a) {
     //   [lxq M*K int8][lxs M*nb f32][lp M*nb*64 f32 if W>1][lf M*K f32 if LN][red]
     const size_t o_xs = (PRO != GRX_PRO_PREQ) ? (size_t)M * K : 0;
     const size_t o_p = o_xs + ((PRO != GRX_PRO_PREQ) ? (((size_t)M * nb * 4 + 15) & ~(size_t)15) : 0);
-    const size_t o_f = o_p + (W > 1 ? (size_t)M * nb * 64 * 4 : 0);
+    constexpr bool RND = M > 1 && W > 1;
+    const size_t o_f = o_p + (W > 1 ? (size_t)M * (RND ? kRound : nb) * 64 * 4 : 0);
     const size_t o_r = o_f + (PRO >= GRX_PRO_LN ? (size_t)M * K * 4 : 0);
     int8_t *lxq = reinterpret_cast<int8_t *>(smem);
     float *lxs = reinterpret_cast<float *>(smem + o_xs);
@@ -142,7 +147,7 @@ __global__ __launch_bounds__(64 * W) void gemv_q8_kernel(const GemvArgs a) {
             if constexpr (PRO == GRX_PRO_EMBED_LN) {
                 // the row is tokEmb.row(tok) + decPos[pos] (whisper/decoder.go:42-46),
                 // built by every workgroup; tile 0 stores it for the residual
-                const int t = a.tok[m], p = *a.pos + a.pos_add + m;
+                const int t = a.tok[m], p = *a.pos + a.pos_add + (a.streams ? 0 : m);
                 const int etile = t >> 6, elane = t & 63;
                 for (int i = tid; i < K; i += 64 * W) {
                     const int b = i >> 5, h = (i >> 4) & 1, e = i & 15;
@@ -239,7 +244,8 @@ __global__ __launch_bounds__(64 * W) void gemv_q8_kernel(const GemvArgs a) {
     }
 
     // U blocks: all loads issued first, then the dots in block order.
-    auto run = [&](auto u_tag, int bb) {
+    // Partial products go to lp at block b - rb (rows ld apart).
+    auto run = [&](auto u_tag, int bb, int rb, int ldp) {
         constexpr int U = decltype(u_tag)::value;
         int4 w[2 * U];
         uint32_t dh[U];
@@ -268,15 +274,41 @@ __global__ __launch_bounds__(64 * W) void gemv_q8_kernel(const GemvArgs a) {
                 if constexpr (W == 1)
                     acc[m] = __fmaf_rn(pv, act_scale(m, b), acc[m]);
                 else
-                    lp[((size_t)m * nb + b) * 64 + lane] = pv;
+                    lp[((size_t)m * ldp + (b - rb)) * 64 + lane] = pv;
             }
         }
     };
-    int bb = b0;
-    for (; bb + BU <= b1; bb += BU) run(std::integral_constant<int, BU>{}, bb);
-    for (; bb < b1; ++bb) run(std::integral_constant<int, 1>{}, bb);
+    if constexpr (RND) {
+        // rounds of kRound blocks, kRound / W per wave; wave w folds the rows
+        // m = w, w + W, ... over the round in block order
+        constexpr int BR = kRound / W > 0 ? kRound / W : 1;
+        constexpr int R = BR * W;
+        const float bv = (a.bias != nullptr && row < a.rows) ? a.bias[row] : 0.0f;
+#pragma unroll
+        for (int m = 0; m < M; ++m) acc[m] = bv;
+        for (int r0 = 0; r0 < nb; r0 += R) {
+            const int bs = r0 + wave * BR, be = min(bs + BR, nb);
+            if (be - bs == BR)
+                run(std::integral_constant<int, BR>{}, bs, r0, R);
+            else
+                for (int b = bs; b < be; ++b) run(std::integral_constant<int, 1>{}, b, r0, R);
+            __syncthreads();
+            const int re = min(r0 + R, nb);
+#pragma unroll
+            for (int m = 0; m < M; ++m) {
+                if (m % W != wave) continue;  // uniform across the wave
+                for (int b = r0; b < re; ++b)
+                    acc[m] = __fmaf_rn(lp[((size_t)m * R + (b - r0)) * 64 + lane], act_scale(m, b), acc[m]);
+            }
+            __syncthreads();
+        }
+    } else {
+        int bb = b0;
+        for (; bb + BU <= b1; bb += BU) run(std::integral_constant<int, BU>{}, bb, 0, nb);
+        for (; bb < b1; ++bb) run(std::integral_constant<int, 1>{}, bb, 0, nb);
+    }
 
-    if constexpr (W > 1) {
+    if constexpr (W > 1 && !RND) {
         __syncthreads();
         if (wave != 0) return;
         const float bv = (a.bias != nullptr && row < a.rows) ? a.bias[row] : 0.0f;
@@ -288,10 +320,13 @@ __global__ __launch_bounds__(64 * W) void gemv_q8_kernel(const GemvArgs a) {
         }
     }
 
-    // ---- epilogue
+    // ---- epilogue: row m is ended by wave 0 (one wave, or after the fold
+    // above), or by wave m % W when rows were folded round by round
+    auto mine = [&](int m) { return !RND || m % W == wave; };
     if constexpr (EPI == GRX_EPI_ARGMAX) {
 #pragma unroll
         for (int m = 0; m < M; ++m) {
+            if (!mine(m)) continue;
             const float c = acc[m];
             if (a.y != nullptr && row < a.rows) a.y[(size_t)m * a.ldc + row] = c;
             // key: orderable float bits, then the complement of the index, so
@@ -322,7 +357,10 @@ __global__ __launch_bounds__(64 * W) void gemv_q8_kernel(const GemvArgs a) {
             // the counter for the next step.  Device-scope atomics are
             // coherent across the XCDs, and each workgroup's atomicMax has
             // returned before its count is added, so no cache writeback is
-            // needed.
+            // needed.  (Rows folded by several waves: every wave's atomicMax
+            // is in before wave 0 counts.)
+            if constexpr (RND) __syncthreads();
+            if (wave != 0) return;
             unsigned int done = 0;
             if (lane == 0) done = atomicAdd(a.counter, 1u);
             done = __shfl(done, 0);
@@ -332,11 +370,14 @@ __global__ __launch_bounds__(64 * W) void gemv_q8_kernel(const GemvArgs a) {
                     const unsigned long long k = atomicMax(a.amax + lane, 0ull);
                     const int t = (int)(0xffffffffu - (uint32_t)(k & 0xffffffffull));
                     a.tok_w[lane] = t;
-                    a.hist[p0 + lane] = t;
+                    if (a.streams)
+                        a.hist[(size_t)lane * a.hist_stream + p0] = t;
+                    else
+                        a.hist[p0 + lane] = t;
                     a.amax[lane] = 0ull;
                 }
                 if (lane == 0) {
-                    *a.pos_w = p0 + M;
+                    *a.pos_w = p0 + (a.streams ? 1 : M);
                     *a.counter = 0u;
                 }
             }
@@ -349,7 +390,9 @@ __global__ __launch_bounds__(64 * W) void gemv_q8_kernel(const GemvArgs a) {
         // (rows % 32 == 0), held by the two halves of this wave.
 #pragma unroll
         for (int m = 0; m < M; ++m) {
-            const int flat = m * a.rows + row, total = M * a.rows;
+            if (!mine(m)) continue;
+            // streams: each row is its own [1][rows] buffer
+            const int flat = a.streams ? row : m * a.rows + row, total = a.streams ? a.rows : M * a.rows;
             const int start = flat & ~((1 << 14) - 1);
             const int len = min(1 << 14, total - start);
             const float v = row < a.rows ? grx_gelu_at(acc[m], flat - start, len) : 0.0f;
@@ -377,6 +420,7 @@ __global__ __launch_bounds__(64 * W) void gemv_q8_kernel(const GemvArgs a) {
         // x'[2i+1] = r*s + im*c, unfused, with f32 cos/sin of the angle.
 #pragma unroll
         for (int m = 0; m < M; ++m) {
+            if (!mine(m)) continue;
             const float c = acc[m];
             const float other = __shfl_xor(c, 1);
             if (row >= a.rows) continue;
@@ -403,6 +447,7 @@ __global__ __launch_bounds__(64 * W) void gemv_q8_kernel(const GemvArgs a) {
     if (row >= a.rows) return;
 #pragma unroll
     for (int m = 0; m < M; ++m) {
+        if (!mine(m)) continue;
         const float c = acc[m];
         if constexpr (EPI == GRX_EPI_STORE) {
             a.y[(size_t)m * a.ldc + row] = c;
@@ -411,18 +456,21 @@ __global__ __launch_bounds__(64 * W) void gemv_q8_kernel(const GemvArgs a) {
         } else if constexpr (EPI == GRX_EPI_GELU) {
             // parGelu (whisper/encoder.go:147-151): geluVec over chunks of
             // 1<<14 values of the flat [M][rows] output.
-            const int flat = m * a.rows + row, total = M * a.rows;
+            const int flat = a.streams ? row : m * a.rows + row, total = a.streams ? a.rows : M * a.rows;
             const int start = flat & ~((1 << 14) - 1);
             const int len = min(1 << 14, total - start);
             a.y[(size_t)m * a.ldc + row] = grx_gelu_at(c, flat - start, len);
         } else if constexpr (EPI == GRX_EPI_QKV) {
-            const int pos = *a.pos + a.pos_add + m;
+            // one stream: rows are positions pos.., caches [pos][seg];
+            // streams: row m at pos in stream m's cache (kv_stream floats on)
+            const int pos = *a.pos + a.pos_add + (a.streams ? 0 : m);
+            const size_t so = a.streams ? (size_t)m * a.kv_stream : 0;
             if (row < a.seg)
                 a.y[(size_t)m * a.ldc + row] = c;
             else if (row < 2 * a.seg)
-                a.kc[(size_t)pos * a.seg + row - a.seg] = c;
+                a.kc[so + (size_t)pos * a.seg + row - a.seg] = c;
             else
-                a.vc[(size_t)pos * a.seg + row - 2 * a.seg] = c;
+                a.vc[so + (size_t)pos * a.seg + row - 2 * a.seg] = c;
         }
     }
 }
@@ -463,7 +511,7 @@ size_t gemv_smem(int M, int W, int pro, int nb) {
     const size_t K = (size_t)nb * GRX_QK;
     size_t n = 0;
     if (pro != GRX_PRO_PREQ) n += M * K + (((size_t)M * nb * 4 + 15) & ~(size_t)15);
-    if (W > 1) n += (size_t)M * nb * 64 * 4;
+    if (W > 1) n += (size_t)M * (M > 1 ? kRound : nb) * 64 * 4;
     if (pro >= GRX_PRO_LN) n += (size_t)M * K * 4 + 2 * 16 * sizeof(double);
     return n;
 }
@@ -516,6 +564,8 @@ int grx_gemv_pick_waves(int tiles, int nb, int m, int pro) {
     }
     int W = 1;
     while (W < 16 && tiles * W < 2048 && 2 * W <= nb && gemv_smem(m, 2 * W, pro, nb) <= 64 * 1024) W *= 2;
+    // several rows fold in rounds, one wave per row: at least m waves
+    if (m > 1 && W > 1 && W < m && gemv_smem(m, m, pro, nb) <= 64 * 1024) W = m;
     return W;
 }
 
