@@ -59,6 +59,9 @@ def parse():
     p.add_argument("--no-decoder", action="store_true")
     p.add_argument("--lm-frames", type=int, default=250, help="pocket-TTS-style frames after the 64-row prefix")
     p.add_argument("--no-lm", action="store_true")
+    p.add_argument("--streams-steps", type=int, default=220,
+                   help="greedy steps of the 8-stream large-v3-turbo decoder after its 4-token prompt")
+    p.add_argument("--no-streams", action="store_true")
     p.add_argument("--conformer-reps", type=int, default=10, help="timed encodes per batch size")
     p.add_argument("--no-conformer", action="store_true")
     p.add_argument("--copy-calibration", action="store_true",
@@ -143,6 +146,64 @@ def decoder_bench(args) -> dict:
     res["cpu_baseline"] = {"value": round(steps / cpu_s, 2), "unit": "tokens/s", "cores": 1, "kind": "port",
                            "sample": f"the same {steps} decoder steps on the oracle (scalar C, 1 thread), {cpu_s:.2f} s"}
     dec.close()
+    return res
+
+
+def streams_bench(args) -> dict:
+    """whisper large-v3-turbo-shaped decoder with random-init Q8_0 weights (d
+    1280, 20 heads, 4 layers, FFN 5120, vocab 51866), 8 independent streams
+    each with its own 1500 x 1280 N(0,1) encoder output, stepping together
+    (every product 8 rows): 4-token prompt + `streams_steps` greedy steps
+    per stream.  Aggregate tokens/s over the 8 streams; stream 0's tokens
+    checked against the oracle (whose rate on that stream is the CPU
+    baseline; the reference decodes one stream at a time) and stream 3's
+    against its own single-stream decode on the GPU."""
+    import oracle
+    from gorelaxor_amd.synth import WHISPER_LARGE_V3_TURBO, encoder_output, whisper_model
+    from gorelaxor_amd.whisper import WhisperDecoder
+
+    hp = dict(WHISPER_LARGE_V3_TURBO)
+    S, n = 8, args.streams_steps
+    t = whisper_model(hp, seed=23)
+    encs = [encoder_output(hp, seed=60 + k) for k in range(S)]
+    dec = WhisperDecoder(hp, t, streams=S)
+    t0 = time.perf_counter()
+    for k in range(S):
+        dec.set_encoder_output_stream(k, encs[k])
+    cross_s = time.perf_counter() - t0
+    prompt = [PROMPT] * S
+    dec.greedy_streams(prompt, n)  # warm: graph captured
+    times = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        toks = dec.greedy_streams(prompt, n)
+        times.append(time.perf_counter() - t0)
+    best = min(times)
+    steps = len(PROMPT) + n
+    d, ff, nv, nl, nctx = hp["n_state"], 4 * hp["n_state"], hp["n_vocab"], hp["n_layer"], hp["n_audio_ctx"]
+    wbytes = (nl * (8 * d * d + 2 * ff * d) + nv * d) // 32 * 34
+    cross = S * nl * 2 * nctx * d * 4
+    res = {"tokens_per_s": round(S * steps / best, 1), "ms_per_step": round(best / steps * 1e3, 4),
+           "streams": S, "steps_per_run": steps, "runs": 3, "cross_kv_setup_ms": round(cross_s * 1e3, 1),
+           "step_bytes_weights_and_cross_kv": wbytes + cross,
+           "hbm_gbs_weights_and_cross_kv": round((wbytes + cross) / (best / steps) / 1e9, 1),
+           "shape": "d_model 1280, 20 heads, 4 layers, FFN 5120, vocab 51866, audio 1500, 8 streams, KV 4->%d"
+                    % steps}
+    dec.close()
+    one = WhisperDecoder(hp, t)
+    one.set_encoder_output(encs[3])
+    same = bool(np.array_equal(one.greedy(PROMPT, n), toks[3]))
+    one.close()
+    oracle.build()
+    ref = oracle.WhisperOracle(hp, t)
+    ref.set_encoder_output(encs[0])
+    t0 = time.perf_counter()
+    want = ref.greedy(PROMPT, n)
+    cpu_s = time.perf_counter() - t0
+    res["parity_tokens_identical"] = bool(np.array_equal(want, toks[0])) and same
+    res["cpu_baseline"] = {"value": round(steps / cpu_s, 2), "unit": "tokens/s", "cores": 1, "kind": "port",
+                           "sample": f"stream 0's {steps} decoder steps on the oracle (scalar C, 1 thread), "
+                                     f"{cpu_s:.1f} s; the reference decodes streams one after another"}
     return res
 
 
@@ -374,6 +435,9 @@ def main():
     if not args.no_decoder:
         out["decoder"] = decoder_bench(args)
         out["config"]["workload"] += "; whisper base.en-shaped greedy decoder (decoder.tokens_per_s)"
+    if not args.no_streams:
+        out["streams"] = streams_bench(args)
+        out["config"]["workload"] += "; large-v3-turbo-shaped decoder, 8 streams batched (streams.tokens_per_s)"
     if not args.no_lm:
         out["lm"] = lm_bench(args)
         out["config"]["workload"] += "; pocket-TTS-style flow-LM frame loop (lm.frames_per_s)"

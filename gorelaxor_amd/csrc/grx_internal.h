@@ -264,6 +264,9 @@ struct GemvArgs {
     int streams;
     size_t kv_stream;
     int hist_stream;
+    // ARGMAX with key slots: each workgroup writes its rows' best keys to
+    // keys[tile][M] and a one-workgroup kernel ends the step (no counter)
+    unsigned long long *keys;
 };
 
 grx_status grx_gemv_launch(hipStream_t st, int m, int pro, int epi, const GemvArgs &a,
@@ -271,6 +274,16 @@ grx_status grx_gemv_launch(hipStream_t st, int m, int pro, int epi, const GemvAr
 // The many-row product on the matrix cores (q8_gemm.hip), same results.
 grx_status grx_gemm_q8_launch(hipStream_t st, const grx_weight *w, const int8_t *xq, const float *xs, int m,
                               const float *bias, float *y, int ldc);
+// Row kernels (rows.hip): LayerNorm + rounding to Q8_0 of `rows` rows of n
+// values (x rows ldx apart) into xq [rows][n], xs [rows][n/32]; and the
+// whisper decoder's embedding rows (token tok[r], position *pos) written to
+// x [rows][n] before the same.
+grx_status grx_ln_quant_rows(hipStream_t st, const float *x, int ldx, int rows, int n, const float *w,
+                             const float *b, int8_t *xq, float *xs);
+grx_status grx_embed_ln_quant_rows(hipStream_t st, const int *tok, const int *pos, const grx_weight *emb,
+                                   const float *pos_emb, float *x, int rows, const float *w, const float *b,
+                                   int8_t *xq, float *xs);
+
 // Epilogues of the matrix-core product (q8_gemm.hip).
 enum { GRX_GEMM_STORE = 0, GRX_GEMM_ADD = 1, GRX_GEMM_AXPY_HALF = 2, GRX_GEMM_SCALE = 3, GRX_GEMM_SILU_Q = 4 };
 struct GemmOut {

@@ -34,7 +34,11 @@ constexpr int BU = GRX_GEMV_BU;  // blocks whose loads are issued before any is 
 // Several activation rows over several waves: the blocks go in rounds of
 // kRound, each round's partial products through LDS, and wave m folds row
 // m after every round (so LDS holds one round, not every block).
-constexpr int kRound = 32;
+constexpr int kRound = 16;
+// Pre-rounded activations of several rows up to this many bytes are copied
+// to LDS; multi-row products may take up to kMultiLds bytes of LDS.
+constexpr size_t kStageMax = 40960;
+constexpr size_t kMultiLds = 128 * 1024;
 
 // Weight loads are non-temporal: each weight byte is read once per product,
 // and streaming it past the caches measured 6.7-6.8 TB/s on a 570 MB ring
@@ -122,12 +126,21 @@ __global__ __launch_bounds__(64 * W) void gemv_q8_kernel(const GemvArgs a) {
     const int row = tile * 64 + lane;
 
     // LDS, each region 16-byte aligned (gemv_smem):
-    //   [lxq M*K int8][lxs M*nb f32][lp M*nb*64 f32 if W>1][lf M*K f32 if LN][red]
-    const size_t o_xs = (PRO != GRX_PRO_PREQ) ? (size_t)M * K : 0;
-    const size_t o_p = o_xs + ((PRO != GRX_PRO_PREQ) ? (((size_t)M * nb * 4 + 15) & ~(size_t)15) : 0);
+    //   [lxq M*K int8][lxs M*nb f32][lp M*(nb or kRound)*64 f32 if W>1, and
+    //   in the same bytes lf M*K f32 if LN: lf is done with before lp is
+    //   written][red]
+    // activations in LDS: rounded here, or (several rows, up to kStageMax
+    // bytes of them) copied from HBM; several pre-rounded rows keep their
+    // scales in LDS either way
+    const bool LQ = PRO != GRX_PRO_PREQ || (M > 1 && (size_t)M * K <= kStageMax);
+    constexpr bool LS = PRO != GRX_PRO_PREQ || M > 1;
+    const size_t o_xs = LQ ? (size_t)M * K : 0;
+    const size_t o_p = o_xs + (LS ? (((size_t)M * nb * 4 + 15) & ~(size_t)15) : 0);
     constexpr bool RND = M > 1 && W > 1;
-    const size_t o_f = o_p + (W > 1 ? (size_t)M * (RND ? kRound : nb) * 64 * 4 : 0);
-    const size_t o_r = o_f + (PRO >= GRX_PRO_LN ? (size_t)M * K * 4 : 0);
+    const size_t n_p = W > 1 ? (size_t)M * (RND ? kRound : nb) * 64 * 4 : 0;
+    const size_t n_f = PRO >= GRX_PRO_LN ? (size_t)M * K * 4 : 0;
+    const size_t o_f = o_p;
+    const size_t o_r = o_p + (n_p > n_f ? n_p : n_f);
     int8_t *lxq = reinterpret_cast<int8_t *>(smem);
     float *lxs = reinterpret_cast<float *>(smem + o_xs);
     float *lp = reinterpret_cast<float *>(smem + o_p);
@@ -135,6 +148,17 @@ __global__ __launch_bounds__(64 * W) void gemv_q8_kernel(const GemvArgs a) {
     double *red = reinterpret_cast<double *>(smem + o_r);
 
     // ---- prologue: the activation rows, rounded, in LDS (or left in HBM)
+    if constexpr (PRO == GRX_PRO_PREQ && M > 1) {
+        // several pre-rounded rows: copied to LDS once (16-byte pieces), so
+        // the blocks' dots and the folds read LDS instead of HBM
+        if (LQ) {
+            const int n16 = M * K / 16;
+            for (int i = tid; i < n16; i += 64 * W)
+                reinterpret_cast<int4 *>(lxq)[i] = reinterpret_cast<const int4 *>(a.xq)[i];
+        }
+        for (int i = tid; i < M * nb; i += 64 * W) lxs[i] = a.xs[i];
+        __syncthreads();
+    }
     if constexpr (PRO == GRX_PRO_QUANT) {
         quant_into_lds<M>(a.x, a.lda, nb, lxq, lxs, tid, 64 * W);
         __syncthreads();
@@ -217,7 +241,7 @@ __global__ __launch_bounds__(64 * W) void gemv_q8_kernel(const GemvArgs a) {
 
     auto act = [&](int m, int b, int4 &a0, int4 &a1) {
         const int4 *p;
-        if constexpr (PRO == GRX_PRO_PREQ)
+        if (!LQ)
             p = reinterpret_cast<const int4 *>(a.xq + (size_t)m * K + b * GRX_QK);
         else
             p = reinterpret_cast<const int4 *>(lxq + (size_t)m * K + b * GRX_QK);
@@ -225,7 +249,7 @@ __global__ __launch_bounds__(64 * W) void gemv_q8_kernel(const GemvArgs a) {
         a1 = p[1];
     };
     auto act_scale = [&](int m, int b) -> float {
-        if constexpr (PRO == GRX_PRO_PREQ)
+        if constexpr (!LS)
             return a.xs[(size_t)m * nb + b];
         else
             return lxs[m * nb + b];
@@ -297,6 +321,7 @@ __global__ __launch_bounds__(64 * W) void gemv_q8_kernel(const GemvArgs a) {
 #pragma unroll
             for (int m = 0; m < M; ++m) {
                 if (m % W != wave) continue;  // uniform across the wave
+#pragma unroll 4
                 for (int b = r0; b < re; ++b)
                     acc[m] = __fmaf_rn(lp[((size_t)m * R + (b - r0)) * 64 + lane], act_scale(m, b), acc[m]);
             }
@@ -345,10 +370,16 @@ __global__ __launch_bounds__(64 * W) void gemv_q8_kernel(const GemvArgs a) {
                 key = k2 > key ? k2 : key;
             }
             if (lane == 0) {
-                // a returning atomic: its old value comes back only once the
-                // maximum has been taken at the coherence point
-                const unsigned long long old = atomicMax(a.amax + m, key);
-                asm volatile("; argmax done %0" ::"v"((uint32_t)old));
+                if (a.keys != nullptr) {
+                    // one slot per workgroup and row: no contended atomics;
+                    // argmax_finish_kernel takes the maximum afterwards
+                    a.keys[(size_t)blockIdx.x * M + m] = key;
+                } else {
+                    // a returning atomic: its old value comes back only once
+                    // the maximum has been taken at the coherence point
+                    const unsigned long long old = atomicMax(a.amax + m, key);
+                    asm volatile("; argmax done %0" ::"v"((uint32_t)old));
+                }
             }
         }
         if (a.counter != nullptr) {
@@ -475,6 +506,44 @@ __global__ __launch_bounds__(64 * W) void gemv_q8_kernel(const GemvArgs a) {
     }
 }
 
+// End of a decode step from per-workgroup argmax keys (keys [nslots][M]):
+// row m's token is the first index of its largest value (the maximum key),
+// recorded at the position (streams: in stream m's record), then the
+// position moves on (streams: by one; one stream's rows: by M).
+__global__ __launch_bounds__(256) void argmax_finish_kernel(const unsigned long long *__restrict__ keys, int nslots,
+                                                            int M, int *__restrict__ tok_w, int *__restrict__ hist,
+                                                            int *__restrict__ pos, int streams, int hist_stream) {
+    __shared__ unsigned long long best[4][8];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    for (int m = 0; m < M; ++m) {
+        unsigned long long k = 0;
+        for (int t = tid; t < nslots; t += blockDim.x) {
+            const unsigned long long v = keys[(size_t)t * M + m];
+            k = v > k ? v : k;
+        }
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) {
+            const unsigned long long v = __shfl_xor(k, o);
+            k = v > k ? v : k;
+        }
+        if (lane == 0) best[wave][m] = k;
+    }
+    __syncthreads();
+    if (tid < M) {
+        unsigned long long k = 0;
+        for (int w = 0; w < (int)(blockDim.x >> 6); ++w) k = best[w][tid] > k ? best[w][tid] : k;
+        const int p0 = *pos;
+        const int t = (int)(0xffffffffu - (uint32_t)(k & 0xffffffffull));
+        tok_w[tid] = t;
+        if (streams)
+            hist[(size_t)tid * hist_stream + p0] = t;
+        else
+            hist[p0 + tid] = t;
+    }
+    __syncthreads();
+    if (tid == 0) *pos = *pos + (streams ? 1 : M);
+}
+
 // One thread per block: quantU8 of m rows (q8int.go:88-105), signed.
 __global__ void quant_act_kernel(const float *__restrict__ x, int lda, int m, int nb,
                                  int8_t *__restrict__ q, float *__restrict__ sc) {
@@ -510,9 +579,12 @@ __global__ void block_dots_kernel(const int8_t *__restrict__ qs, int rows, int n
 size_t gemv_smem(int M, int W, int pro, int nb) {
     const size_t K = (size_t)nb * GRX_QK;
     size_t n = 0;
-    if (pro != GRX_PRO_PREQ) n += M * K + (((size_t)M * nb * 4 + 15) & ~(size_t)15);
-    if (W > 1) n += (size_t)M * (M > 1 ? kRound : nb) * 64 * 4;
-    if (pro >= GRX_PRO_LN) n += (size_t)M * K * 4 + 2 * 16 * sizeof(double);
+    if (pro != GRX_PRO_PREQ || (M > 1 && (size_t)M * K <= kStageMax)) n += M * K;
+    if (pro != GRX_PRO_PREQ || M > 1) n += ((size_t)M * nb * 4 + 15) & ~(size_t)15;
+    const size_t n_p = W > 1 ? (size_t)M * (M > 1 ? kRound : nb) * 64 * 4 : 0;
+    const size_t n_f = pro >= GRX_PRO_LN ? (size_t)M * K * 4 : 0;
+    n += n_p > n_f ? n_p : n_f;  // the two share their bytes
+    if (pro >= GRX_PRO_LN) n += 2 * 16 * sizeof(double);
     return n;
 }
 
@@ -562,10 +634,11 @@ int grx_gemv_pick_waves(int tiles, int nb, int m, int pro) {
         const int w = atoi(f);
         if (w == 1 || w == 2 || w == 4 || w == 8 || w == 16) return w;
     }
+    const size_t lim = m > 1 ? kMultiLds : 64 * 1024;
     int W = 1;
-    while (W < 16 && tiles * W < 2048 && 2 * W <= nb && gemv_smem(m, 2 * W, pro, nb) <= 64 * 1024) W *= 2;
+    while (W < 16 && tiles * W < 2048 && 2 * W <= nb && gemv_smem(m, 2 * W, pro, nb) <= lim) W *= 2;
     // several rows fold in rounds, one wave per row: at least m waves
-    if (m > 1 && W > 1 && W < m && gemv_smem(m, m, pro, nb) <= 64 * 1024) W = m;
+    if (m > 1 && W > 1 && W < m && gemv_smem(m, m, pro, nb) <= lim) W = m;
     return W;
 }
 
@@ -585,10 +658,18 @@ grx_status grx_gemv_launch(hipStream_t st, int m, int pro, int epi, const GemvAr
     else if (pro == GRX_PRO_LN && epi == GRX_EPI_GELU_Q) e = launch_m<GRX_PRO_LN, GRX_EPI_GELU_Q>(st, m, a, tiles, W);
     else if (pro == GRX_PRO_EMBED_LN && epi == GRX_EPI_QKV) e = launch_m<GRX_PRO_EMBED_LN, GRX_EPI_QKV>(st, m, a, tiles, W);
     else if (pro == GRX_PRO_PREQ && epi == GRX_EPI_RESID) e = launch_m<GRX_PRO_PREQ, GRX_EPI_RESID>(st, m, a, tiles, W);
+    else if (pro == GRX_PRO_PREQ && epi == GRX_EPI_QKV) e = launch_m<GRX_PRO_PREQ, GRX_EPI_QKV>(st, m, a, tiles, W);
+    else if (pro == GRX_PRO_PREQ && epi == GRX_EPI_GELU_Q) e = launch_m<GRX_PRO_PREQ, GRX_EPI_GELU_Q>(st, m, a, tiles, W);
+    else if (pro == GRX_PRO_PREQ && epi == GRX_EPI_ARGMAX) e = launch_m<GRX_PRO_PREQ, GRX_EPI_ARGMAX>(st, m, a, tiles, W);
     else if (pro == GRX_PRO_LN64 && epi == GRX_EPI_QKV_ROPE) e = launch_m<GRX_PRO_LN64, GRX_EPI_QKV_ROPE>(st, m, a, tiles, W);
     else if (pro == GRX_PRO_LN64 && epi == GRX_EPI_GELU_Q) e = launch_m<GRX_PRO_LN64, GRX_EPI_GELU_Q>(st, m, a, tiles, W);
     else return grx_fail(GRX_EINVAL, "grx: no GEMV variant for prologue %d epilogue %d", pro, epi);
     if (e != hipSuccess) return grx_hip_fail(e, "gemv_q8_kernel");
+    if (epi == GRX_EPI_ARGMAX && a.keys != nullptr) {
+        argmax_finish_kernel<<<1, 256, 0, st>>>(a.keys, tiles, m, a.tok_w, a.hist, a.pos_w, a.streams,
+                                                a.hist_stream);
+        GRX_LAUNCHED("argmax_finish_kernel");
+    }
     return GRX_OK;
 }
 

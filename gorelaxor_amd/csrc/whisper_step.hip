@@ -39,19 +39,28 @@ constexpr int kAttnThreads = 256;
 constexpr int kBatch = 32;  // loads issued before their values are used
 constexpr int kBatchV = 96;  // the same for the cross values' longer chains (one batch at 1500 keys)
 
-// Causal self-attention of one head over the pos+1 cached positions
-// (decoder.go:70-87): scores dotF32Go(q, k_j)*sc, softmax, and
+// Causal self-attention of one head (blockIdx.x) of one stream (blockIdx.y,
+// its cache kv_stream floats after the previous stream's) over the pos+1
+// cached positions (decoder.go:70-87): scores dotF32Go(q, k_j)*sc, softmax, and
 // out[d] += p_j * v_j[d] in position order, unfused.  With QOUT (head_dim a
 // multiple of 32) the head's outputs are also rounded to Q8_0 for the out
 // projection.
 template <bool QOUT>
 __global__ __launch_bounds__(kAttnThreads) void self_attn_kernel(
     const float *__restrict__ q, const float *__restrict__ kc, const float *__restrict__ vc,
-    const int *__restrict__ pos, int st, int hd, float sc, int rc, float *__restrict__ att, int8_t *__restrict__ att_q,
-    float *__restrict__ att_s) {
+    const int *__restrict__ pos, int st, int hd, float sc, int rc, size_t kv_stream, float *__restrict__ att,
+    int8_t *__restrict__ att_q, float *__restrict__ att_s) {
     extern __shared__ float sm[];
-    const int h = blockIdx.x, n = *pos + 1, tid = threadIdx.x;
+    const int h = blockIdx.x, n = *pos + 1, tid = threadIdx.x, sm_ = blockIdx.y;  // head, stream
     float *part = sm, *s = sm + 32, *vl = sm + 32 + ((n + 3) & ~3);
+    q += (size_t)sm_ * st;
+    kc += sm_ * kv_stream;
+    vc += sm_ * kv_stream;
+    att += (size_t)sm_ * st;
+    if constexpr (QOUT) {
+        att_q += (size_t)sm_ * st;
+        att_s += (size_t)sm_ * (st / 32);
+    }
     const float *qh = q + h * hd;
     for (int j = tid; j < n; j += blockDim.x) s[j] = __fmul_rn(dot_go(qh, kc + (size_t)j * st + h * hd, hd), sc);
     __syncthreads();
@@ -74,12 +83,17 @@ __global__ __launch_bounds__(kAttnThreads) void self_attn_kernel(
     }
 }
 
-// Cross-attention scores of one head for a run of keys (decoder.go:94-108):
+// Cross-attention scores of one head for a run of keys of stream blockIdx.z
+// (its cross keys x_stream floats after the previous stream's) (decoder.go:94-108):
 // dotF32x4 for the keys in whole groups of four, dotF32Go for the rest.
 __global__ __launch_bounds__(kAttnThreads) void cross_scores_kernel(
-    const float *__restrict__ q, const float *__restrict__ ck, int nctx, int hd, float *__restrict__ scores) {
-    const int h = blockIdx.x, j = blockIdx.y * blockDim.x + threadIdx.x;
+    const float *__restrict__ q, const float *__restrict__ ck, int nctx, int hd, int st, size_t x_stream,
+    float *__restrict__ scores) {
+    const int h = blockIdx.x, j = blockIdx.y * blockDim.x + threadIdx.x, sm_ = blockIdx.z;  // stream sm_
     if (j >= nctx) return;
+    q += (size_t)sm_ * st;
+    ck += sm_ * x_stream;
+    scores += (size_t)sm_ * (st / hd) * nctx;
     const float *qh = q + h * hd;
     const float *kj = ck + ((size_t)h * nctx + j) * hd;
     scores[(size_t)h * nctx + j] = j < (nctx & ~3) ? dot_x4(qh, kj, hd) : dot_go(qh, kj, hd);
@@ -93,14 +107,23 @@ __global__ __launch_bounds__(kAttnThreads) void cross_scores_kernel(
 // the values fetched kBatch steps at a time; the tail past n &^ 15 is one
 // lane's dotF32Go.  Every workgroup of a head computes the same softmax into
 // its LDS.  With QOUT (DG == 32) the 32 outputs are rounded to Q8_0.
+// blockIdx.z is the stream (its cross values x_stream floats after the
+// previous stream's).
 template <bool QOUT>
 __global__ __launch_bounds__(512) void cross_values_kernel(const float *__restrict__ scores,
                                                           const float *__restrict__ cv, int nctx, int hd, int dg,
-                                                          float *__restrict__ att, int8_t *__restrict__ att_q,
-                                                          float *__restrict__ att_s) {
+                                                          int st, size_t x_stream, float *__restrict__ att,
+                                                          int8_t *__restrict__ att_q, float *__restrict__ att_s) {
     extern __shared__ float sm[];
     float *part = sm, *outv = sm + 32, *s = sm + 64;
-    const int h = blockIdx.x, tid = threadIdx.x;
+    const int h = blockIdx.x, tid = threadIdx.x, sm_ = blockIdx.z;  // head, stream
+    scores += (size_t)sm_ * (st / hd) * nctx;
+    cv += sm_ * x_stream;
+    att += (size_t)sm_ * st;
+    if constexpr (QOUT) {
+        att_q += (size_t)sm_ * st;
+        att_s += (size_t)sm_ * (st / 32);
+    }
     const float *row = scores + (size_t)h * nctx;
     for (int j = tid; j < nctx; j += blockDim.x) s[j] = row[j];
     __syncthreads();
@@ -173,6 +196,8 @@ struct WLayer {
 struct grx_whisper {
     grx_ctx *ctx = nullptr;
     grx_whisper_hparams hp{};
+    int S = 1;  // streams decoded side by side (rows of every product)
+    std::vector<bool> have_xs;  // cross K/V set, per stream
     std::map<std::string, std::vector<uint8_t>> host;  // set_tensor copies, until finalize
     bool ready = false, have_cross = false;
     std::vector<WLayer> L;
@@ -181,8 +206,11 @@ struct grx_whisper {
     float *dec_pos = nullptr, *dec_ln_w = nullptr, *dec_ln_b = nullptr;
     float *x = nullptr, *q = nullptr, *att = nullptr, *ff = nullptr, *logits = nullptr, *scores = nullptr;
     int8_t *att_q = nullptr, *ff_q = nullptr;  // Q8_0 copies for the next product
+    int8_t *ln_q = nullptr;                    // several streams: LayerNorm rows rounded once per product
+    float *ln_s = nullptr;
     float *att_s = nullptr, *ff_s = nullptr;
     unsigned long long *amax = nullptr;
+    unsigned long long *keys = nullptr;  // argmax keys, [vocabulary tiles][streams]
     unsigned int *counter = nullptr;
     int *tok = nullptr, *pos = nullptr, *hist = nullptr;
     hipGraph_t graph = nullptr;
@@ -300,7 +328,7 @@ grx_status finalize(grx_whisper *m) {
                     {"mlp.0.bias", &L.fc1_b},               {"mlp.2.bias", &L.fc2_b}};
         for (auto &v : vecs)
             if ((s = upload_vec(m, p + v.n, v.d)) != GRX_OK) return s;
-        const size_t cross = (size_t)hp.n_audio_ctx * st, self = (size_t)hp.n_text_ctx * st;
+        const size_t cross = (size_t)m->S * hp.n_audio_ctx * st, self = (size_t)m->S * hp.n_text_ctx * st;
         if ((s = dev_alloc_t(m, cross, &L.cross_k)) != GRX_OK) return s;
         if ((s = dev_alloc_t(m, cross, &L.cross_v)) != GRX_OK) return s;
         if ((s = dev_alloc_t(m, self, &L.self_k)) != GRX_OK) return s;
@@ -308,25 +336,29 @@ grx_status finalize(grx_whisper *m) {
         GRX_HIP(hipMemset(L.self_k, 0, self * 4));
         GRX_HIP(hipMemset(L.self_v, 0, self * 4));
     }
-    if ((s = dev_alloc_t(m, st, &m->x)) != GRX_OK) return s;
-    if ((s = dev_alloc_t(m, st, &m->q)) != GRX_OK) return s;
-    if ((s = dev_alloc_t(m, st, &m->att)) != GRX_OK) return s;
-    if ((s = dev_alloc_t(m, 4 * (size_t)st, &m->ff)) != GRX_OK) return s;
-    if ((s = dev_alloc_t(m, hp.n_vocab, &m->logits)) != GRX_OK) return s;
-    if ((s = dev_alloc_t(m, (size_t)hp.n_head * hp.n_audio_ctx, &m->scores)) != GRX_OK) return s;
-    if ((s = dev_alloc_t(m, st, &m->att_q)) != GRX_OK) return s;
-    if ((s = dev_alloc_t(m, st / 32, &m->att_s)) != GRX_OK) return s;
-    if ((s = dev_alloc_t(m, 4 * (size_t)st, &m->ff_q)) != GRX_OK) return s;
-    if ((s = dev_alloc_t(m, 4 * (size_t)st / 32, &m->ff_s)) != GRX_OK) return s;
+    const size_t S = m->S;
+    if ((s = dev_alloc_t(m, S * st, &m->x)) != GRX_OK) return s;
+    if ((s = dev_alloc_t(m, S * st, &m->q)) != GRX_OK) return s;
+    if ((s = dev_alloc_t(m, S * st, &m->att)) != GRX_OK) return s;
+    if ((s = dev_alloc_t(m, S * 4 * (size_t)st, &m->ff)) != GRX_OK) return s;
+    if ((s = dev_alloc_t(m, S * hp.n_vocab, &m->logits)) != GRX_OK) return s;
+    if ((s = dev_alloc_t(m, S * hp.n_head * hp.n_audio_ctx, &m->scores)) != GRX_OK) return s;
+    if ((s = dev_alloc_t(m, S * st, &m->att_q)) != GRX_OK) return s;
+    if ((s = dev_alloc_t(m, S * st, &m->ln_q)) != GRX_OK) return s;
+    if ((s = dev_alloc_t(m, S * st / 32, &m->ln_s)) != GRX_OK) return s;
+    if ((s = dev_alloc_t(m, S * st / 32, &m->att_s)) != GRX_OK) return s;
+    if ((s = dev_alloc_t(m, S * 4 * (size_t)st, &m->ff_q)) != GRX_OK) return s;
+    if ((s = dev_alloc_t(m, S * 4 * (size_t)st / 32, &m->ff_s)) != GRX_OK) return s;
     if ((s = dev_alloc_t(m, 1, &m->counter)) != GRX_OK) return s;
     GRX_HIP(hipMemset(m->counter, 0, 4));
-    if ((s = dev_alloc_t(m, 1, &m->amax)) != GRX_OK) return s;
-    GRX_HIP(hipMemset(m->amax, 0, 8));
-    if ((s = dev_alloc_t(m, 1, &m->tok)) != GRX_OK) return s;
+    if ((s = dev_alloc_t(m, S, &m->amax)) != GRX_OK) return s;
+    if ((s = dev_alloc_t(m, (size_t)grx_ceil_div(hp.n_vocab, 64) * S, &m->keys)) != GRX_OK) return s;
+    GRX_HIP(hipMemset(m->amax, 0, 8 * S));
+    if ((s = dev_alloc_t(m, S, &m->tok)) != GRX_OK) return s;
     if ((s = dev_alloc_t(m, 1, &m->pos)) != GRX_OK) return s;
-    if ((s = dev_alloc_t(m, hp.n_text_ctx, &m->hist)) != GRX_OK) return s;
+    if ((s = dev_alloc_t(m, S * hp.n_text_ctx, &m->hist)) != GRX_OK) return s;
     GRX_HIP(hipMemset(m->pos, 0, 4));
-    GRX_HIP(hipMemset(m->tok, 0, 4));
+    GRX_HIP(hipMemset(m->tok, 0, 4 * S));
     m->host.clear();
     m->ready = true;
     (void)hd;
@@ -356,6 +388,25 @@ grx_status enqueue_step(grx_whisper *m, hipStream_t stream) {
     const size_t attn_smem = (32 + (((size_t)hp.n_text_ctx + 3) & ~(size_t)3) + (size_t)rc * hd) * 4;
     const size_t val_smem = (64 + (size_t)nctx) * 4;
     const int dg = qatt ? 32 : 4;
+    const int S = m->S;  // rows of every product: one per stream
+    const size_t kv_stream = (size_t)hp.n_text_ctx * st, x_stream = (size_t)nctx * st;
+    // streams at one position: each row its own token, cache and record
+    auto gemv_args = [&](const grx_weight *w) {
+        GemvArgs a = ::gemv_args(w);
+        a.streams = S > 1;
+        a.kv_stream = kv_stream;
+        a.hist_stream = hp.n_text_ctx;
+        return a;
+    };
+    // Several streams: each LayerNorm'd row is rounded once by its own
+    // workgroup and the product reads it pre-rounded (the fused prologue
+    // would redo the rows in every workgroup of the product).
+    const bool sep = S > 1;
+    auto ln_rows = [&](const float *w, const float *b, GemvArgs &a) {
+        a.xq = m->ln_q;
+        a.xs = m->ln_s;
+        return grx_ln_quant_rows(stream, m->x, st, S, st, w, b, m->ln_q, m->ln_s);
+    };
     for (int li = 0; li < hp.n_layer; ++li) {
         WLayer &L = m->L[li];
         {  // LN -> q | k | v, k and v into the cache at pos; layer 0 embeds first
@@ -380,14 +431,23 @@ grx_status enqueue_step(grx_whisper *m, hipStream_t stream) {
                 a.pos_emb = m->dec_pos;
                 a.x_out = m->x;
             }
-            if ((s = grx_gemv_launch(stream, 1, pro, GRX_EPI_QKV, a, 0)) != GRX_OK) return s;
+            if (sep) {
+                pro = GRX_PRO_PREQ;
+                a.xq = m->ln_q;
+                a.xs = m->ln_s;
+                s = li == 0 ? grx_embed_ln_quant_rows(stream, m->tok, m->pos, m->tok_emb, m->dec_pos, m->x, S,
+                                                      L.attn_ln_w, L.attn_ln_b, m->ln_q, m->ln_s)
+                            : grx_ln_quant_rows(stream, m->x, st, S, st, L.attn_ln_w, L.attn_ln_b, m->ln_q, m->ln_s);
+                if (s != GRX_OK) return s;
+            }
+            if ((s = grx_gemv_launch(stream, S, pro, GRX_EPI_QKV, a, 0)) != GRX_OK) return s;
         }
         if (qatt)
-            self_attn_kernel<true><<<nh, kAttnThreads, attn_smem, stream>>>(m->q, L.self_k, L.self_v, m->pos, st, hd,
-                                                                           sc, rc, m->att, m->att_q, m->att_s);
+            self_attn_kernel<true><<<dim3(nh, S), kAttnThreads, attn_smem, stream>>>(
+                m->q, L.self_k, L.self_v, m->pos, st, hd, sc, rc, kv_stream, m->att, m->att_q, m->att_s);
         else
-            self_attn_kernel<false><<<nh, kAttnThreads, attn_smem, stream>>>(m->q, L.self_k, L.self_v, m->pos, st, hd,
-                                                                            sc, rc, m->att, nullptr, nullptr);
+            self_attn_kernel<false><<<dim3(nh, S), kAttnThreads, attn_smem, stream>>>(
+                m->q, L.self_k, L.self_v, m->pos, st, hd, sc, rc, kv_stream, m->att, nullptr, nullptr);
         GRX_LAUNCHED("self_attn_kernel");
         auto out_proj = [&](grx_weight *w, const float *b) {  // x += att . W^T + b
             GemvArgs a = gemv_args(w);
@@ -400,7 +460,7 @@ grx_status enqueue_step(grx_whisper *m, hipStream_t stream) {
             a.bias = b;
             a.resid = m->x;
             a.ldr = st;
-            return grx_gemv_launch(stream, 1, qatt ? GRX_PRO_PREQ : GRX_PRO_QUANT, GRX_EPI_RESID, a, 0);
+            return grx_gemv_launch(stream, S, qatt ? GRX_PRO_PREQ : GRX_PRO_QUANT, GRX_EPI_RESID, a, 0);
         };
         if ((s = out_proj(L.o, L.o_b)) != GRX_OK) return s;
         {  // LN -> cross query
@@ -412,17 +472,19 @@ grx_status enqueue_step(grx_whisper *m, hipStream_t stream) {
             a.y = m->q;
             a.ldc = st;
             a.bias = L.xq_b;
-            if ((s = grx_gemv_launch(stream, 1, GRX_PRO_LN, GRX_EPI_STORE, a, 0)) != GRX_OK) return s;
+            if (sep && (s = ln_rows(L.x_ln_w, L.x_ln_b, a)) != GRX_OK) return s;
+            if ((s = grx_gemv_launch(stream, S, sep ? GRX_PRO_PREQ : GRX_PRO_LN, GRX_EPI_STORE, a, 0)) != GRX_OK)
+                return s;
         }
-        cross_scores_kernel<<<dim3(nh, grx_ceil_div(nctx, kAttnThreads)), kAttnThreads, 0, stream>>>(
-            m->q, L.cross_k, nctx, hd, m->scores);
+        cross_scores_kernel<<<dim3(nh, grx_ceil_div(nctx, kAttnThreads), S), kAttnThreads, 0, stream>>>(
+            m->q, L.cross_k, nctx, hd, st, x_stream, m->scores);
         GRX_LAUNCHED("cross_scores_kernel");
         if (qatt)
-            cross_values_kernel<true><<<dim3(nh, grx_ceil_div(hd, dg)), dg * 16, val_smem, stream>>>(
-                m->scores, L.cross_v, nctx, hd, dg, m->att, m->att_q, m->att_s);
+            cross_values_kernel<true><<<dim3(nh, grx_ceil_div(hd, dg), S), dg * 16, val_smem, stream>>>(
+                m->scores, L.cross_v, nctx, hd, dg, st, x_stream, m->att, m->att_q, m->att_s);
         else
-            cross_values_kernel<false><<<dim3(nh, grx_ceil_div(hd, dg)), dg * 16, val_smem, stream>>>(
-                m->scores, L.cross_v, nctx, hd, dg, m->att, nullptr, nullptr);
+            cross_values_kernel<false><<<dim3(nh, grx_ceil_div(hd, dg), S), dg * 16, val_smem, stream>>>(
+                m->scores, L.cross_v, nctx, hd, dg, st, x_stream, m->att, nullptr, nullptr);
         GRX_LAUNCHED("cross_values_kernel");
         if ((s = out_proj(L.xo, L.xo_b)) != GRX_OK) return s;
         {  // LN -> fc1 -> GELU, rounded to Q8_0 for fc2
@@ -436,7 +498,9 @@ grx_status enqueue_step(grx_whisper *m, hipStream_t stream) {
             a.bias = L.fc1_b;
             a.yq = m->ff_q;
             a.ys = m->ff_s;
-            if ((s = grx_gemv_launch(stream, 1, GRX_PRO_LN, GRX_EPI_GELU_Q, a, 0)) != GRX_OK) return s;
+            if (sep && (s = ln_rows(L.mlp_ln_w, L.mlp_ln_b, a)) != GRX_OK) return s;
+            if ((s = grx_gemv_launch(stream, S, sep ? GRX_PRO_PREQ : GRX_PRO_LN, GRX_EPI_GELU_Q, a, 0)) != GRX_OK)
+                return s;
         }
         {  // x += ff . Wfc2^T + b
             GemvArgs a = gemv_args(L.fc2);
@@ -447,7 +511,7 @@ grx_status enqueue_step(grx_whisper *m, hipStream_t stream) {
             a.bias = L.fc2_b;
             a.resid = m->x;
             a.ldr = st;
-            if ((s = grx_gemv_launch(stream, 1, GRX_PRO_PREQ, GRX_EPI_RESID, a, 0)) != GRX_OK) return s;
+            if ((s = grx_gemv_launch(stream, S, GRX_PRO_PREQ, GRX_EPI_RESID, a, 0)) != GRX_OK) return s;
         }
     }
     {  // LN -> logits = tokEmb . h -> argmax; the last workgroup ends the step
@@ -459,13 +523,21 @@ grx_status enqueue_step(grx_whisper *m, hipStream_t stream) {
         a.ln_b = m->dec_ln_b;
         a.y = m->logits;
         a.ldc = hp.n_vocab;
+        // per-workgroup argmax keys and a one-workgroup end of step (no
+        // contended atomics); GRX_ARGMAX_ATOMIC=1 takes the atomic form
+        static const bool atomic_form = getenv("GRX_ARGMAX_ATOMIC") && getenv("GRX_ARGMAX_ATOMIC")[0] == '1';
         a.amax = m->amax;
-        a.counter = m->counter;
+        if (atomic_form)
+            a.counter = m->counter;
+        else
+            a.keys = m->keys;
         a.tok_w = m->tok;
         a.pos = m->pos;
         a.pos_w = m->pos;
         a.hist = m->hist;
-        if ((s = grx_gemv_launch(stream, 1, GRX_PRO_LN, GRX_EPI_ARGMAX, a, 0)) != GRX_OK) return s;
+        if (sep && (s = ln_rows(m->dec_ln_w, m->dec_ln_b, a)) != GRX_OK) return s;
+        if ((s = grx_gemv_launch(stream, S, sep ? GRX_PRO_PREQ : GRX_PRO_LN, GRX_EPI_ARGMAX, a, 0)) != GRX_OK)
+            return s;
     }
     return GRX_OK;
 }
@@ -507,8 +579,15 @@ grx_status run_step(grx_whisper *m) {
 }  // namespace
 
 extern "C" grx_status grx_whisper_create(grx_ctx *ctx, const grx_whisper_hparams *hp, grx_whisper **out) {
+    return grx_whisper_create_streams(ctx, hp, 1, out);
+}
+
+extern "C" grx_status grx_whisper_create_streams(grx_ctx *ctx, const grx_whisper_hparams *hp, int n_streams,
+                                                 grx_whisper **out) {
     if (!ctx || !hp || !out) return grx_fail(GRX_EINVAL, "grx_whisper_create: NULL argument");
     *out = nullptr;
+    if (n_streams != 1 && n_streams != 2 && n_streams != 4 && n_streams != 8)
+        return grx_fail(GRX_EINVAL, "grx_whisper_create_streams: %d streams (1, 2, 4 or 8)", n_streams);
     if (hp->n_vocab <= 0 || hp->n_text_ctx <= 0 || hp->n_state <= 0 || hp->n_head <= 0 || hp->n_layer <= 0 ||
         hp->n_audio_ctx <= 0)
         return grx_fail(GRX_EINVAL, "grx_whisper_create: every size must be positive");
@@ -518,9 +597,13 @@ extern "C" grx_status grx_whisper_create(grx_ctx *ctx, const grx_whisper_hparams
     grx_whisper *m = new grx_whisper();
     m->ctx = ctx;
     m->hp = *hp;
+    m->S = n_streams;
+    m->have_xs.assign(n_streams, false);
     *out = m;
     return GRX_OK;
 }
+
+extern "C" int grx_whisper_streams(const grx_whisper *m) { return m ? m->S : 0; }
 
 extern "C" grx_status grx_whisper_destroy(grx_whisper *m) {
     if (!m) return GRX_OK;
@@ -551,7 +634,14 @@ extern "C" grx_status grx_whisper_set_tensor(grx_whisper *m, const char *name, c
 }
 
 extern "C" grx_status grx_whisper_set_encoder_output(grx_whisper *m, const float *enc, int n_audio_ctx) {
+    return grx_whisper_set_encoder_output_stream(m, 0, enc, n_audio_ctx);
+}
+
+extern "C" grx_status grx_whisper_set_encoder_output_stream(grx_whisper *m, int stream_ix, const float *enc,
+                                                            int n_audio_ctx) {
     if (!m || !enc) return grx_fail(GRX_EINVAL, "grx_whisper_set_encoder_output: NULL argument");
+    if (stream_ix < 0 || stream_ix >= m->S)
+        return grx_fail(GRX_EINVAL, "grx_whisper_set_encoder_output: stream %d of %d", stream_ix, m->S);
     if (n_audio_ctx != m->hp.n_audio_ctx)
         return grx_fail(GRX_ESIZE, "grx_whisper_set_encoder_output: %d positions, the model has %d", n_audio_ctx,
                         m->hp.n_audio_ctx);
@@ -571,8 +661,9 @@ extern "C" grx_status grx_whisper_set_encoder_output(grx_whisper *m, const float
         s = grx_matmul_q8_dev(m->ctx, dk, st, denc, st, nctx, L.xk, nullptr);
         if (s == GRX_OK) s = grx_matmul_q8_dev(m->ctx, dv, st, denc, st, nctx, L.xv, L.xv_b);
         if (s == GRX_OK) {
-            cross_layout_kernel<<<(int)((n + 255) / 256), 256, 0, stream>>>(dk, dv, nctx, st, hd, tsc, L.cross_k,
-                                                                           L.cross_v);
+            cross_layout_kernel<<<(int)((n + 255) / 256), 256, 0, stream>>>(dk, dv, nctx, st, hd, tsc,
+                                                                           L.cross_k + stream_ix * n,
+                                                                           L.cross_v + stream_ix * n);
             hipError_t e = hipGetLastError();
             if (e != hipSuccess) s = grx_hip_fail(e, "cross_layout_kernel");
         }
@@ -583,7 +674,8 @@ extern "C" grx_status grx_whisper_set_encoder_output(grx_whisper *m, const float
     (void)hipFree(dv);
     if (s != GRX_OK) return s;
     if (e != hipSuccess) return grx_hip_fail(e, "grx_whisper_set_encoder_output");
-    m->have_cross = true;
+    m->have_xs[stream_ix] = true;
+    m->have_cross = std::all_of(m->have_xs.begin(), m->have_xs.end(), [](bool b) { return b; });
     return GRX_OK;
 }
 
@@ -607,6 +699,7 @@ static grx_status check_ready(grx_whisper *m, const char *fn) {
 extern "C" grx_status grx_whisper_decode(grx_whisper *m, const int32_t *tokens, int n, float *logits, int32_t *next) {
     grx_status s = check_ready(m, "grx_whisper_decode");
     if (s != GRX_OK) return s;
+    if (m->S != 1) return grx_fail(GRX_ESTATE, "grx_whisper_decode: %d streams: use grx_whisper_greedy_streams", m->S);
     if (n < 0 || (n > 0 && !tokens)) return grx_fail(GRX_EINVAL, "grx_whisper_decode: bad tokens");
     if (m->pos_host + n > m->hp.n_text_ctx)
         return grx_fail(GRX_ESTATE, "grx_whisper_decode: %d tokens after %d positions exceed the context of %d", n,
@@ -631,6 +724,7 @@ extern "C" grx_status grx_whisper_greedy(grx_whisper *m, const int32_t *prompt, 
                                          int32_t *out) {
     grx_status s = check_ready(m, "grx_whisper_greedy");
     if (s != GRX_OK) return s;
+    if (m->S != 1) return grx_fail(GRX_ESTATE, "grx_whisper_greedy: %d streams: use grx_whisper_greedy_streams", m->S);
     if (n_prompt <= 0 || n_steps < 0 || !prompt || !out)
         return grx_fail(GRX_EINVAL, "grx_whisper_greedy: bad arguments");
     if (n_prompt + n_steps > m->hp.n_text_ctx)
@@ -644,6 +738,41 @@ extern "C" grx_status grx_whisper_greedy(grx_whisper *m, const int32_t *prompt, 
         m->pos_host++;
     }
     GRX_HIP(hipMemcpyAsync(out, m->hist + (n_prompt - 1), (size_t)(n_steps + 1) * 4, hipMemcpyDeviceToHost, stream));
+    GRX_HIP(hipStreamSynchronize(stream));
+    return GRX_OK;
+}
+
+extern "C" grx_status grx_whisper_greedy_streams(grx_whisper *m, const int32_t *prompts, int n_prompt, int n_steps,
+                                                 int32_t *out) {
+    grx_status s = check_ready(m, "grx_whisper_greedy_streams");
+    if (s != GRX_OK) return s;
+    const int S = m->S;
+    if (n_prompt <= 0 || n_steps < 0 || !prompts || !out)
+        return grx_fail(GRX_EINVAL, "grx_whisper_greedy_streams: bad arguments");
+    if (n_prompt + n_steps > m->hp.n_text_ctx)
+        return grx_fail(GRX_ESTATE, "grx_whisper_greedy_streams: %d prompt tokens and %d steps exceed the context of %d",
+                        n_prompt, n_steps, m->hp.n_text_ctx);
+    for (int i = 0; i < S * n_prompt; ++i)
+        if (prompts[i] < 0 || prompts[i] >= m->hp.n_vocab)
+            return grx_fail(GRX_EINVAL, "grx_whisper_greedy_streams: token %d out of the vocabulary", prompts[i]);
+    if ((s = grx_whisper_reset(m)) != GRX_OK) return s;
+    hipStream_t stream = m->ctx->stream;
+    // the prompt position by position, every stream's token uploaded first
+    std::vector<int32_t> col(S);
+    for (int i = 0; i < n_prompt; ++i) {
+        for (int k = 0; k < S; ++k) col[k] = prompts[(size_t)k * n_prompt + i];
+        GRX_HIP(hipMemcpyAsync(m->tok, col.data(), (size_t)S * 4, hipMemcpyHostToDevice, stream));
+        if ((s = run_step(m)) != GRX_OK) return s;
+        m->pos_host++;
+        GRX_HIP(hipStreamSynchronize(stream));  // col is reused
+    }
+    for (int i = 0; i < n_steps; ++i) {
+        if ((s = run_step(m)) != GRX_OK) return s;
+        m->pos_host++;
+    }
+    for (int k = 0; k < S; ++k)
+        GRX_HIP(hipMemcpyAsync(out + (size_t)k * (n_steps + 1), m->hist + (size_t)k * m->hp.n_text_ctx + (n_prompt - 1),
+                               (size_t)(n_steps + 1) * 4, hipMemcpyDeviceToHost, stream));
     GRX_HIP(hipStreamSynchronize(stream));
     return GRX_OK;
 }

@@ -42,6 +42,7 @@ def gemv_inputs(seed: int = 1, n: int = 1024, k: int = 1024):
 
 
 WHISPER_BASE_EN = dict(n_vocab=51864, n_text_ctx=448, n_state=512, n_head=8, n_layer=6, n_audio_ctx=1500)
+WHISPER_LARGE_V3_TURBO = dict(n_vocab=51866, n_text_ctx=448, n_state=1280, n_head=20, n_layer=4, n_audio_ctx=1500)
 WHISPER_TINY_TEST = dict(n_vocab=1000, n_text_ctx=64, n_state=128, n_head=2, n_layer=2, n_audio_ctx=96)
 
 

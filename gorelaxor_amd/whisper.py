@@ -18,13 +18,17 @@ from .kern import Context, default_context
 
 
 class WhisperDecoder:
-    def __init__(self, hp: dict, tensors: dict | None = None, ctx: Context | None = None):
+    """One decode session, or `streams` (2, 4 or 8) independent sessions
+    stepping together with shared weights (each its own encoder output)."""
+
+    def __init__(self, hp: dict, tensors: dict | None = None, ctx: Context | None = None, streams: int = 1):
         self.ctx = ctx or default_context()
         self.hp = dict(hp)
+        self.streams = streams
         h = _lib.WhisperHParams(**{k: int(hp[k]) for k in ("n_vocab", "n_text_ctx", "n_state", "n_head",
                                                           "n_layer", "n_audio_ctx")})
         out = C.c_void_p()
-        _lib.call("grx_whisper_create", self.ctx.handle, C.byref(h), C.byref(out))
+        _lib.call("grx_whisper_create_streams", self.ctx.handle, C.byref(h), streams, C.byref(out))
         self.handle = out
         if tensors:
             for name, arr in tensors.items():
@@ -38,6 +42,20 @@ class WhisperDecoder:
         e = np.ascontiguousarray(enc, np.float32)
         _lib.call("grx_whisper_set_encoder_output", self.handle, e.ctypes.data_as(C.c_void_p),
                   e.size // self.hp["n_state"])
+
+    def set_encoder_output_stream(self, stream: int, enc: np.ndarray) -> None:
+        e = np.ascontiguousarray(enc, np.float32)
+        _lib.call("grx_whisper_set_encoder_output_stream", self.handle, stream, e.ctypes.data_as(C.c_void_p),
+                  e.size // self.hp["n_state"])
+
+    def greedy_streams(self, prompts, n_steps: int) -> np.ndarray:
+        """Greedy decoding of every stream: prompts [streams][n_prompt] ->
+        tokens [streams][n_steps + 1]."""
+        p = np.ascontiguousarray(prompts, np.int32).reshape(self.streams, -1)
+        out = np.zeros((self.streams, n_steps + 1), np.int32)
+        _lib.call("grx_whisper_greedy_streams", self.handle, p.ctypes.data_as(C.c_void_p), p.shape[1], n_steps,
+                  out.ctypes.data_as(C.c_void_p))
+        return out
 
     def reset(self) -> None:
         _lib.call("grx_whisper_reset", self.handle)

@@ -164,6 +164,24 @@ grx_status grx_whisper_decode(grx_whisper *m, const int32_t *tokens, int n, floa
 grx_status grx_whisper_greedy(grx_whisper *m, const int32_t *prompt, int n_prompt, int n_steps,
                               int32_t *out);
 
+/* Several independent decodes side by side: n_streams (1, 2, 4 or 8)
+ * whisper sessions, each its own encoder output, KV cache and token loop
+ * (whisper/transcribe.go:207-260 run once per stream), sharing the weights
+ * and stepping together, so every product takes n_streams rows at once.
+ * Each stream's tokens are the ones its own decode gives.  No reference
+ * counterpart: the reference decodes one session at a time. */
+grx_status grx_whisper_create_streams(grx_ctx *ctx, const grx_whisper_hparams *hp, int n_streams,
+                                      grx_whisper **out);
+int grx_whisper_streams(const grx_whisper *m);
+/* grx_whisper_set_encoder_output for one stream (0 .. n_streams-1); every
+ * stream needs one before decoding. */
+grx_status grx_whisper_set_encoder_output_stream(grx_whisper *m, int stream, const float *enc, int n_audio_ctx);
+/* grx_whisper_greedy for every stream: prompts [n_streams][n_prompt],
+ * out [n_streams][n_steps+1].  (grx_whisper_decode and grx_whisper_greedy
+ * serve one stream and return GRX_ESTATE for more.) */
+grx_status grx_whisper_greedy_streams(grx_whisper *m, const int32_t *prompts, int n_prompt, int n_steps,
+                                      int32_t *out);
+
 /* ---- pocket-TTS flow-LM transformer with Q8_0 weights ---- */
 
 /* flowLM of pockettts/lm.go:164-195 over transformer.forward and attend of

@@ -101,3 +101,74 @@ def test_base_en_shape_greedy(kern, orc):
     lr = ref.decode([int(want[-1])])
     lg, _ = dec.decode([int(got[-1])])
     assert _same(lg, lr)
+
+
+def _streams(hp, t, n, seed):
+    from gorelaxor_amd.whisper import WhisperDecoder
+
+    dec = WhisperDecoder(hp, t, streams=n)
+    encs = [encoder_output(hp, seed=seed + k) for k in range(n)]
+    for k, e in enumerate(encs):
+        dec.set_encoder_output_stream(k, e)
+    return dec, encs
+
+
+@pytest.mark.parametrize("n", [2, 4, 8])
+def test_streams_tokens_identical_to_each_oracle_decode(kern, orc, n):
+    """Independent streams decoded side by side (every product n rows): each
+    stream's greedy tokens are those of its own oracle decode."""
+    hp = dict(WHISPER_TINY_TEST)
+    t = whisper_model(hp, seed=21)
+    dec, encs = _streams(hp, t, n, seed=40)
+    prompts = [[1 + k, 2, 3 + 2 * k, 4] for k in range(n)]
+    got = dec.greedy_streams(prompts, 30)
+    for k in range(n):
+        ref = orc.WhisperOracle(hp, t)
+        ref.set_encoder_output(encs[k])
+        assert list(got[k]) == list(ref.greedy(prompts[k], 30)), k
+    # the loop again from empty caches repeats itself (graph replays)
+    assert np.array_equal(dec.greedy_streams(prompts, 30), got)
+
+
+def test_streams_errors(kern):
+    from gorelaxor_amd import GrxError
+    from gorelaxor_amd.whisper import WhisperDecoder
+
+    hp = dict(WHISPER_TINY_TEST)
+    t = whisper_model(hp, seed=2)
+    with pytest.raises(GrxError, match="streams"):
+        WhisperDecoder(hp, t, streams=3)
+    dec = WhisperDecoder(hp, t, streams=2)
+    dec.set_encoder_output_stream(0, encoder_output(hp, seed=1))
+    with pytest.raises(GrxError, match="no encoder output"):
+        dec.greedy_streams([[1, 2], [3, 4]], 2)  # stream 1 has none
+    dec.set_encoder_output_stream(1, encoder_output(hp, seed=2))
+    with pytest.raises(GrxError, match="greedy_streams"):
+        dec.decode([1])
+    with pytest.raises(GrxError, match="stream 2"):
+        dec.set_encoder_output_stream(2, encoder_output(hp, seed=3))
+
+
+def test_large_v3_turbo_eight_streams(kern, orc):
+    """large-v3-turbo shape (d 1280, 20 heads, 4 layers, FFN 5120, vocab
+    51866, 1500 audio positions), 8 streams: two streams' tokens against the
+    oracle, the rest against their own single-stream GPU decode."""
+    from gorelaxor_amd.synth import WHISPER_LARGE_V3_TURBO
+    from gorelaxor_amd.whisper import WhisperDecoder
+
+    hp = dict(WHISPER_LARGE_V3_TURBO)
+    t = whisper_model(hp, seed=23)
+    dec, encs = _streams(hp, t, 8, seed=60)
+    prompt = [50258, 50259, 50360, 50364]
+    n = 12
+    got = dec.greedy_streams([prompt] * 8, n)
+    dec.close()
+    for k in (0, 5):
+        ref = orc.WhisperOracle(hp, t)
+        ref.set_encoder_output(encs[k])
+        assert list(got[k]) == list(ref.greedy(prompt, n)), k
+    one = WhisperDecoder(hp, t)
+    for k in (1, 2, 3, 4, 6, 7):
+        one.set_encoder_output(encs[k])
+        assert list(one.greedy(prompt, n)) == list(got[k]), k
+    assert len({tuple(g) for g in got}) > 1  # the streams differ
