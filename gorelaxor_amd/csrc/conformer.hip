@@ -1161,7 +1161,7 @@ grx_status enqueue_encode(grx_conformer *m, hipStream_t st) {
     const grx_conformer_hparams &hp = m->hp;
     const int B = m->B, frames = m->frames, d = hp.d, c = hp.sub_channels, nm = hp.n_mels, T = m->T;
     const int T1 = sub_out(frames), F1 = sub_out(nm), T2 = sub_out(T1), F2 = sub_out(F1), F3 = sub_out(F2);
-    const int R = B * T, hd = d / hp.heads, cF = c * F3;
+    const int R = B * T, hd = d / hp.heads;
     grx_status s;
     // pre-encoder (encoder.go:123-167)
     sub_conv01_kernel<<<B * T2, c, (size_t)7 * (4 * F2 + 3) * 4, st>>>(m->mel, frames, nm, m->valid, m->w0, m->b0,

@@ -39,19 +39,171 @@ constexpr int kAttnThreads = 256;
 constexpr int kBatch = 32;  // loads issued before their values are used
 constexpr int kBatchV = 96;  // the same for the cross values' longer chains (one batch at 1500 keys)
 
+// Self-attention workgroups are 256 threads; heads of 64 over at most
+// kSmallN positions take the branch-free body, others the general one.
+constexpr int kSmallHd = 64, kSmallN = 256, kSmallKld = kSmallHd + 4;
+// LDS floats of the branch-free body: K rows, V rows, p, chain-major exps,
+// reductions, a dummy slot
+constexpr size_t kSmallLds = (size_t)kSmallN * kSmallKld + (size_t)kSmallN * kSmallHd + 2 * kSmallN + 16 + 4;
+
+// The softmax sums of block_softmax (mathx.go:78-90) for wave 0, from the
+// exps below n8 stored chain-major (chain c = j % 8 at ch[c*cs + j/8],
+// cs % 4 == 0) and the tail's exps tl[0..n-n8): lane 0 gets
+// 1 / (HSUM(eight chains) + tail).  Branch-free: whole runs of 32 steps,
+// then a last run under selects.
+__device__ __forceinline__ float softmax_inv(const float *ch, int cs, const float *tl, int n) {
+    const int lane = threadIdx.x & 63, c = lane & 7, n8 = n & ~7, nt = n - n8, N = n8 >> 3;
+    const float4 *cr = reinterpret_cast<const float4 *>(ch + c * cs);
+    float acc = 0.f;
+    int g0 = 0;
+    for (; g0 + 32 <= N; g0 += 32) {
+        float4 t[8];
+#pragma unroll
+        for (int g = 0; g < 8; ++g) t[g] = cr[(g0 >> 2) + g];
+#pragma unroll
+        for (int g = 0; g < 8; ++g) {
+            acc = __fadd_rn(acc, t[g].x);
+            acc = __fadd_rn(acc, t[g].y);
+            acc = __fadd_rn(acc, t[g].z);
+            acc = __fadd_rn(acc, t[g].w);
+        }
+    }
+    if (g0 < N) {
+        float4 t[8];
+#pragma unroll
+        for (int g = 0; g < 8; ++g) t[g] = cr[min((g0 >> 2) + g, (N - 1) >> 2)];
+#pragma unroll
+        for (int g = 0; g < 8; ++g) {
+            const int m = g0 + 4 * g;
+            float f;
+            f = __fadd_rn(acc, t[g].x);
+            acc = m + 0 < N ? f : acc;
+            f = __fadd_rn(acc, t[g].y);
+            acc = m + 1 < N ? f : acc;
+            f = __fadd_rn(acc, t[g].z);
+            acc = m + 2 < N ? f : acc;
+            f = __fadd_rn(acc, t[g].w);
+            acc = m + 3 < N ? f : acc;
+        }
+    }
+    float tt = 0.f;
+#pragma unroll
+    for (int i = 0; i < 7; ++i) {
+        const float f = __fadd_rn(tt, tl[min(i, max(nt - 1, 0))]);
+        tt = i < nt ? f : tt;
+    }
+    const float p0 = __shfl(acc, 0), p1 = __shfl(acc, 1), p2 = __shfl(acc, 2), p3 = __shfl(acc, 3);
+    const float p4 = __shfl(acc, 4), p5 = __shfl(acc, 5), p6 = __shfl(acc, 6), p7 = __shfl(acc, 7);
+    const float sa = n8 > 0 ? __fadd_rn(__fadd_rn(__fadd_rn(p0, p4), __fadd_rn(p1, p5)),
+                                        __fadd_rn(__fadd_rn(p2, p6), __fadd_rn(p3, p7)))
+                            : 0.f;
+    return __fdiv_rn(1.0f, __fadd_rn(sa, tt));
+}
+
+// Causal self-attention of one head over n <= kSmallN positions, head_dim
+// 64, without divergent branches: every K and V row through LDS in one batch
+// (K rows 68 floats apart for conflict-free 16-byte reads; rows past n are
+// copies of row n-1 for K and zeros for V), thread j's score, the softmax,
+// then wave 0's lane d sums p_j * v_j[d] in position order (p_j = 0 past n,
+// so the loop runs whole groups of 32).
+template <bool QOUT>
+__device__ __forceinline__ void self_attn_small(float *sm, const float *q, const float *kc, const float *vc, int n,
+                                                int st, float sc, float *att, int8_t *att_q, float *att_s) {
+    constexpr int HD = kSmallHd, RC = kSmallN, KLD = kSmallKld;
+    float *kl = sm, *vl = kl + RC * KLD, *p = vl + RC * HD, *ch = p + RC, *red = ch + RC, *dummy = red + 16;
+    const int h = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const float *kb = kc + h * HD, *vb = vc + h * HD;
+    constexpr int PER = RC * HD / 4 / 256;  // 16-byte pieces per thread per row set
+    float4 kv[PER], vv[PER];
+#pragma unroll
+    for (int u = 0; u < PER; ++u) {
+        const int i = tid + u * 256;
+        const size_t g = (size_t)min(i >> 4, n - 1) * st + 4 * (i & 15);
+        kv[u] = *reinterpret_cast<const float4 *>(kb + g);
+        vv[u] = *reinterpret_cast<const float4 *>(vb + g);
+    }
+#pragma unroll
+    for (int u = 0; u < PER; ++u) {
+        const int i = tid + u * 256, r = i >> 4, c4 = i & 15;
+        *reinterpret_cast<float4 *>(kl + r * KLD + 4 * c4) = kv[u];
+        *reinterpret_cast<float4 *>(vl + r * HD + 4 * c4) = r < n ? vv[u] : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+    __syncthreads();
+    // dotF32Go (gemm.go:294-308): four running sums over the float4 pieces
+    const float *qh = q + h * HD, *kr = kl + tid * KLD;
+    float s0 = 0.f, s1 = 0.f, s2 = 0.f, s3 = 0.f;
+#pragma unroll
+    for (int i = 0; i < HD; i += 4) {
+        const float4 a = *reinterpret_cast<const float4 *>(qh + i);
+        const float4 b = *reinterpret_cast<const float4 *>(kr + i);
+        s0 = __fadd_rn(s0, __fmul_rn(a.x, b.x));
+        s1 = __fadd_rn(s1, __fmul_rn(a.y, b.y));
+        s2 = __fadd_rn(s2, __fmul_rn(a.z, b.z));
+        s3 = __fadd_rn(s3, __fmul_rn(a.w, b.w));
+    }
+    const float score = __fmul_rn(__fadd_rn(__fadd_rn(__fadd_rn(s0, s1), s2), s3), sc);
+    const bool live = tid < n;
+    float mx = live ? score : -__builtin_inff();
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        const float t = __shfl_xor(mx, o);
+        mx = t > mx ? t : mx;
+    }
+    if (lane == 0) red[wave] = mx;
+    __syncthreads();
+    mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    const int n8 = n & ~7;
+    const float d = __fsub_rn(score, mx);
+    const float e = tid < n8 ? grx_exp8(d) : grx_expf_go(d);
+    *(tid < n8 ? ch + (tid & 7) * (RC / 8) + (tid >> 3) : dummy) = e;
+    *(live ? p + tid : dummy + 1) = e;
+    __syncthreads();
+    if (wave == 0) {
+        const float inv = softmax_inv(ch, RC / 8, p + n8, n);
+        if (lane == 0) red[8] = inv;
+    }
+    __syncthreads();
+    p[tid] = live ? __fmul_rn(e, red[8]) : 0.f;
+    __syncthreads();
+    if (wave == 0) {
+        float o = 0.f;
+        const int n32 = (n + 31) & ~31;
+        for (int j0 = 0; j0 < n32; j0 += 32) {
+#pragma unroll
+            for (int g = 0; g < 8; ++g) {
+                const float4 pp = *reinterpret_cast<const float4 *>(p + j0 + 4 * g);
+                const float *vr = vl + (j0 + 4 * g) * HD + lane;
+                o = __fadd_rn(o, __fmul_rn(pp.x, vr[0]));
+                o = __fadd_rn(o, __fmul_rn(pp.y, vr[HD]));
+                o = __fadd_rn(o, __fmul_rn(pp.z, vr[2 * HD]));
+                o = __fadd_rn(o, __fmul_rn(pp.w, vr[3 * HD]));
+            }
+        }
+        att[h * HD + lane] = o;
+        if constexpr (QOUT) quant32_store(o, att_q + h * HD + lane, att_s + (h * HD + lane) / 32, lane & 31);
+    }
+}
+
 // Causal self-attention of one head (blockIdx.x) of one stream (blockIdx.y,
 // its cache kv_stream floats after the previous stream's) over the pos+1
 // cached positions (decoder.go:70-87): scores dotF32Go(q, k_j)*sc, softmax, and
 // out[d] += p_j * v_j[d] in position order, unfused.  With QOUT (head_dim a
 // multiple of 32) the head's outputs are also rounded to Q8_0 for the out
-// projection.
+// projection.  Heads of 64 over at most kSmallN positions take the
+// branch-free body above (the choice is uniform: n is read on the device).
 template <bool QOUT>
 __global__ __launch_bounds__(kAttnThreads) void self_attn_kernel(
     const float *__restrict__ q, const float *__restrict__ kc, const float *__restrict__ vc,
     const int *__restrict__ pos, int st, int hd, float sc, int rc, size_t kv_stream, float *__restrict__ att,
     int8_t *__restrict__ att_q, float *__restrict__ att_s) {
-    extern __shared__ float sm[];
+    extern __shared__ __align__(16) float sm[];
     const int h = blockIdx.x, n = *pos + 1, tid = threadIdx.x, sm_ = blockIdx.y;  // head, stream
+    if (hd == kSmallHd && n <= kSmallN) {
+        self_attn_small<QOUT>(sm, q + (size_t)sm_ * st, kc + sm_ * kv_stream, vc + sm_ * kv_stream, n, st, sc,
+                              att + (size_t)sm_ * st, QOUT ? att_q + (size_t)sm_ * st : nullptr,
+                              QOUT ? att_s + (size_t)sm_ * (st / 32) : nullptr);
+        return;
+    }
     float *part = sm, *s = sm + 32, *vl = sm + 32 + ((n + 3) & ~3);
     q += (size_t)sm_ * st;
     kc += sm_ * kv_stream;
@@ -86,7 +238,7 @@ __global__ __launch_bounds__(kAttnThreads) void self_attn_kernel(
 // Cross-attention scores of one head for a run of keys of stream blockIdx.z
 // (its cross keys x_stream floats after the previous stream's) (decoder.go:94-108):
 // dotF32x4 for the keys in whole groups of four, dotF32Go for the rest.
-__global__ __launch_bounds__(kAttnThreads) void cross_scores_kernel(
+__global__ __launch_bounds__(64) void cross_scores_kernel(
     const float *__restrict__ q, const float *__restrict__ ck, int nctx, int hd, int st, size_t x_stream,
     float *__restrict__ scores) {
     const int h = blockIdx.x, j = blockIdx.y * blockDim.x + threadIdx.x, sm_ = blockIdx.z;  // stream sm_
@@ -163,6 +315,127 @@ __global__ __launch_bounds__(512) void cross_values_kernel(const float *__restri
     if constexpr (QOUT) {
         __syncthreads();
         if (tid < 32) {
+            const int dd = blockIdx.y * 32 + tid;
+            quant32_store(outv[tid], att_q + h * hd + dd, att_s + (h * hd + dd) / 32, tid);
+        }
+    }
+}
+
+// dotF32Go (gemm.go:294-308) of at most 15 values, r of them, without
+// branches (clamped reads, selected sums).
+__device__ __forceinline__ float dot_go15(const float *x, const float *y, int r) {
+    float s0 = 0.f, s1 = 0.f, s2 = 0.f, s3 = 0.f;
+    const int last = max(r - 1, 0);
+#pragma unroll
+    for (int i = 0; i < 12; i += 4) {
+        const bool ok = i + 4 <= r;
+        const float f0 = __fadd_rn(s0, __fmul_rn(x[min(i, last)], y[min(i, last)]));
+        const float f1 = __fadd_rn(s1, __fmul_rn(x[min(i + 1, last)], y[min(i + 1, last)]));
+        const float f2 = __fadd_rn(s2, __fmul_rn(x[min(i + 2, last)], y[min(i + 2, last)]));
+        const float f3 = __fadd_rn(s3, __fmul_rn(x[min(i + 3, last)], y[min(i + 3, last)]));
+        s0 = ok ? f0 : s0;
+        s1 = ok ? f1 : s1;
+        s2 = ok ? f2 : s2;
+        s3 = ok ? f3 : s3;
+    }
+    const int r4 = r & ~3;
+#pragma unroll
+    for (int i = 0; i < 3; ++i) {
+        const float f = __fadd_rn(s0, __fmul_rn(x[min(r4 + i, last)], y[min(r4 + i, last)]));
+        s0 = i < (r & 3) ? f : s0;
+    }
+    return __fadd_rn(__fadd_rn(__fadd_rn(s0, s1), s2), s3);
+}
+
+// Cross values without divergent branches, for nctx <= kFastCtx and head_dim
+// a multiple of 4: the same softmax and dotF32x4 chains as
+// cross_values_kernel, 32 values of d per workgroup of 512 threads.  Each
+// lane's 96 values of V are loaded before the scores; each thread holds 3
+// scores, the exps below n8 go to a chain-major copy for the eight sums
+// (softmax_inv), and the probabilities to LDS for the chains.
+constexpr int kFastCtx = 3 * 512;
+template <bool QOUT>
+__global__ __launch_bounds__(512) void cross_values_fast_kernel(const float *__restrict__ scores,
+                                                                const float *__restrict__ cv, int nctx, int hd,
+                                                                int st, size_t x_stream, float *__restrict__ att,
+                                                                int8_t *__restrict__ att_q, float *__restrict__ att_s) {
+    constexpr int NT = 512, PER = kFastCtx / NT, CS = kFastCtx / 8 + 32, KB = 96;
+    __shared__ __align__(16) float ch[8 * CS + 8];
+    __shared__ __align__(16) float p[kFastCtx + 16];
+    __shared__ float red[32], outv[32];
+    const int h = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, sm_ = blockIdx.z;
+    scores += ((size_t)sm_ * (st / hd) + h) * nctx;
+    cv += sm_ * x_stream;
+    att += (size_t)sm_ * st;
+    const int dl = tid >> 4, c = tid & 15, d = blockIdx.y * 32 + dl;
+    const int kk = nctx & ~15, steps = kk >> 4;
+    const float *vd = cv + ((size_t)h * hd + min(d, hd - 1)) * nctx;
+    float vv[KB];
+#pragma unroll
+    for (int u = 0; u < KB; ++u) vv[u] = vd[min(16 * u + c, nctx - 1)];
+    float sv[PER];
+#pragma unroll
+    for (int u = 0; u < PER; ++u) sv[u] = scores[min(tid + u * NT, nctx - 1)];
+    float mx = sv[0];
+#pragma unroll
+    for (int u = 1; u < PER; ++u) mx = sv[u] > mx ? sv[u] : mx;
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        const float t = __shfl_xor(mx, o);
+        mx = t > mx ? t : mx;
+    }
+    if (lane == 0) red[wave] = mx;
+    __syncthreads();
+    mx = red[0];
+#pragma unroll
+    for (int w = 1; w < NT / 64; ++w) mx = red[w] > mx ? red[w] : mx;
+    const int n8 = nctx & ~7;
+    float e[PER];
+    float *dummy = ch + 8 * CS;
+#pragma unroll
+    for (int u = 0; u < PER; ++u) {
+        const int j = tid + u * NT;
+        const float dd = __fsub_rn(sv[u], mx);
+        e[u] = j < n8 ? grx_exp8(dd) : grx_expf_go(dd);
+        *(j < n8 ? ch + (j & 7) * CS + (j >> 3) : dummy) = e[u];
+        *(j < nctx ? p + j : dummy + 1) = e[u];
+    }
+    __syncthreads();
+    if (wave == 0) {
+        const float inv = softmax_inv(ch, CS, p + n8, nctx);
+        if (lane == 0) red[8] = inv;
+    }
+    __syncthreads();
+    const float inv = red[8];
+#pragma unroll
+    for (int u = 0; u < PER; ++u) {
+        const int j = tid + u * NT;
+        *(j < nctx ? p + j : dummy + 2) = __fmul_rn(e[u], inv);
+    }
+    __syncthreads();
+    // dot4f32avx's lane chains over whole steps of 16, then HSUM
+    float acc = 0.f;
+#pragma unroll
+    for (int u = 0; u < KB; ++u) {
+        const float f = __fmaf_rn(p[16 * u + c], vv[u], acc);
+        acc = u < steps ? f : acc;
+    }
+    const float other = __shfl_xor(acc, 8, 16);
+    const float S = __fadd_rn(c < 8 ? acc : other, c < 8 ? other : acc);
+    const float h4 = __fadd_rn(S, __shfl_xor(S, 4, 16));
+    const float h01 = __fadd_rn(h4, __shfl_xor(h4, 1, 16));
+    const float h23 = __shfl_xor(h01, 2, 16);
+    float o = kk > 0 ? __fadd_rn(h01, h23) : 0.f;
+    if (kk < nctx) o = __fadd_rn(o, dot_go15(p + kk, vd + kk, nctx - kk));
+    if (c == 0) {
+        if (d < hd) att[h * hd + d] = o;
+        outv[dl] = o;
+    }
+    if constexpr (QOUT) {
+        __syncthreads();
+        if (tid < 32) {
+            att_q += (size_t)sm_ * st;
+            att_s += (size_t)sm_ * (st / 32);
             const int dd = blockIdx.y * 32 + tid;
             quant32_store(outv[tid], att_q + h * hd + dd, att_s + (h * hd + dd) / 32, tid);
         }
@@ -385,7 +658,18 @@ grx_status enqueue_step(grx_whisper *m, hipStream_t stream) {
     const bool qatt = hd % 32 == 0;  // attention outputs are whole Q8_0 blocks per head
     grx_status s;
     const int rc = std::max(1, std::min(hp.n_text_ctx, (48 * 1024) / (hd * 4)));
-    const size_t attn_smem = (32 + (((size_t)hp.n_text_ctx + 3) & ~(size_t)3) + (size_t)rc * hd) * 4;
+    size_t attn_smem = (32 + (((size_t)hp.n_text_ctx + 3) & ~(size_t)3) + (size_t)rc * hd) * 4;
+    if (hd == kSmallHd) {
+        attn_smem = std::max(attn_smem, kSmallLds * 4);
+        static bool raised = false;  // set by the eager step that precedes any capture
+        if (!raised) {
+            raised = true;
+            GRX_HIP(hipFuncSetAttribute((const void *)self_attn_kernel<true>,
+                                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)(kSmallLds * 4)));
+            GRX_HIP(hipFuncSetAttribute((const void *)self_attn_kernel<false>,
+                                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)(kSmallLds * 4)));
+        }
+    }
     const size_t val_smem = (64 + (size_t)nctx) * 4;
     const int dg = qatt ? 32 : 4;
     const int S = m->S;  // rows of every product: one per stream
@@ -476,15 +760,23 @@ grx_status enqueue_step(grx_whisper *m, hipStream_t stream) {
             if ((s = grx_gemv_launch(stream, S, sep ? GRX_PRO_PREQ : GRX_PRO_LN, GRX_EPI_STORE, a, 0)) != GRX_OK)
                 return s;
         }
-        cross_scores_kernel<<<dim3(nh, grx_ceil_div(nctx, kAttnThreads), S), kAttnThreads, 0, stream>>>(
+        cross_scores_kernel<<<dim3(nh, grx_ceil_div(nctx, 64), S), 64, 0, stream>>>(
             m->q, L.cross_k, nctx, hd, st, x_stream, m->scores);
         GRX_LAUNCHED("cross_scores_kernel");
-        if (qatt)
+        if (nctx <= kFastCtx && hd % 4 == 0) {
+            if (qatt)
+                cross_values_fast_kernel<true><<<dim3(nh, grx_ceil_div(hd, 32), S), 512, 0, stream>>>(
+                    m->scores, L.cross_v, nctx, hd, st, x_stream, m->att, m->att_q, m->att_s);
+            else
+                cross_values_fast_kernel<false><<<dim3(nh, grx_ceil_div(hd, 32), S), 512, 0, stream>>>(
+                    m->scores, L.cross_v, nctx, hd, st, x_stream, m->att, nullptr, nullptr);
+        } else if (qatt) {
             cross_values_kernel<true><<<dim3(nh, grx_ceil_div(hd, dg), S), dg * 16, val_smem, stream>>>(
                 m->scores, L.cross_v, nctx, hd, dg, st, x_stream, m->att, m->att_q, m->att_s);
-        else
+        } else {
             cross_values_kernel<false><<<dim3(nh, grx_ceil_div(hd, dg), S), dg * 16, val_smem, stream>>>(
                 m->scores, L.cross_v, nctx, hd, dg, st, x_stream, m->att, nullptr, nullptr);
+        }
         GRX_LAUNCHED("cross_values_kernel");
         if ((s = out_proj(L.xo, L.xo_b)) != GRX_OK) return s;
         {  // LN -> fc1 -> GELU, rounded to Q8_0 for fc2

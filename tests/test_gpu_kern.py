@@ -256,6 +256,21 @@ def test_matmul_zero_rows_is_noop(kern):
     assert (dst == 3.0).all()
 
 
+@pytest.mark.parametrize("m", [1, 3, 40])
+def test_matmul_no_columns_gives_bias(kern, m):
+    """A product with K = 0 (no blocks): every output is its bias, or 0."""
+    rng = np.random.default_rng(2)
+    n = 70
+    w = kern.NewQ8(n, 0, np.zeros(0, np.uint8))
+    b = rng.standard_normal(n).astype(np.float32)
+    dst = np.full((m, n), 3.0, np.float32)
+    x = np.zeros((m, 1), np.float32)
+    kern.MatMul(dst, n, x, 0, m, w, bias=b)
+    assert _bits_equal(dst, np.tile(b, (m, 1)))
+    kern.MatMul(dst, n, x, 0, m, w)
+    assert (dst == 0.0).all()
+
+
 def test_matmul_short_buffer_raises(kern):
     """The reference panics on a short slice (kernels_amd64.go:206-211);
     the mirror raises IndexError before any launch."""
