@@ -114,6 +114,171 @@ __device__ __forceinline__ void quant_into_lds(const float *src, int ld, int nb,
     }
 }
 
+// The products' epilogues: row m of the tile's 64 outputs (acc[m] in lane
+// `lane`) is ended by wave 0, or by wave m % W when rows were folded round
+// by round (RND).
+template <int M, int W, bool RND, int EPI>
+__device__ __forceinline__ void gemv_epilogue(const GemvArgs &a, const float (&acc)[M], int row, int lane,
+                                              int wave) {
+    auto mine = [&](int m) { return !RND || m % W == wave; };
+    if constexpr (EPI == GRX_EPI_ARGMAX) {
+#pragma unroll
+        for (int m = 0; m < M; ++m) {
+            if (!mine(m)) continue;
+            const float c = acc[m];
+            if (a.y != nullptr && row < a.rows) a.y[(size_t)m * a.ldc + row] = c;
+            // key: orderable float bits, then the complement of the index, so
+            // the maximum key is the largest value at its first index
+            // (whisper/transcribe.go:459-464); -0 counts as +0 and NaN never wins.
+            unsigned long long key = 0;
+            if (row < a.rows && !(c != c)) {
+                const float cc = c == 0.0f ? 0.0f : c;
+                const uint32_t u = __float_as_uint(cc);
+                const uint32_t ord = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+                key = ((unsigned long long)ord << 32) | (uint32_t)(0xffffffffu - (uint32_t)row);
+            }
+#pragma unroll
+            for (int o = 32; o > 0; o >>= 1) {
+                const unsigned long long k2 = __shfl_xor(key, o);
+                key = k2 > key ? k2 : key;
+            }
+            if (lane == 0) {
+                if (a.keys != nullptr) {
+                    // one slot per workgroup and row: no contended atomics;
+                    // argmax_finish_kernel takes the maximum afterwards
+                    a.keys[(size_t)blockIdx.x * M + m] = key;
+                } else {
+                    // a returning atomic: its old value comes back only once
+                    // the maximum has been taken at the coherence point
+                    const unsigned long long old = atomicMax(a.amax + m, key);
+                    asm volatile("; argmax done %0" ::"v"((uint32_t)old));
+                }
+            }
+        }
+        if (a.counter != nullptr) {
+            // The last workgroup to finish ends the decode step: the argmax
+            // token, its record, the next position; then clears the key and
+            // the counter for the next step.  Device-scope atomics are
+            // coherent across the XCDs, and each workgroup's atomicMax has
+            // returned before its count is added, so no cache writeback is
+            // needed.  (Rows folded by several waves: every wave's atomicMax
+            // is in before wave 0 counts.)
+            if constexpr (RND) __syncthreads();
+            if (wave != 0) return;
+            unsigned int done = 0;
+            if (lane == 0) done = atomicAdd(a.counter, 1u);
+            done = __shfl(done, 0);
+            if (done == gridDim.x - 1) {
+                const int p0 = *a.pos;
+                if (lane < M) {
+                    const unsigned long long k = atomicMax(a.amax + lane, 0ull);
+                    const int t = (int)(0xffffffffu - (uint32_t)(k & 0xffffffffull));
+                    a.tok_w[lane] = t;
+                    if (a.streams)
+                        a.hist[(size_t)lane * a.hist_stream + p0] = t;
+                    else
+                        a.hist[p0 + lane] = t;
+                    a.amax[lane] = 0ull;
+                }
+                if (lane == 0) {
+                    *a.pos_w = p0 + (a.streams ? 1 : M);
+                    *a.counter = 0u;
+                }
+            }
+        }
+        return;
+    }
+    if constexpr (EPI == GRX_EPI_GELU_Q) {
+        // geluVec, then quantU8 of the output's 32-value blocks for the next
+        // product: rows 64*tile..+31 and +32..+63 are two whole blocks
+        // (rows % 32 == 0), held by the two halves of this wave.
+#pragma unroll
+        for (int m = 0; m < M; ++m) {
+            if (!mine(m)) continue;
+            // streams: each row is its own [1][rows] buffer
+            const int flat = a.streams ? row : m * a.rows + row, total = a.streams ? a.rows : M * a.rows;
+            const int start = flat & ~((1 << 14) - 1);
+            const int len = min(1 << 14, total - start);
+            const float v = row < a.rows ? grx_gelu_at(acc[m], flat - start, len) : 0.0f;
+            const float av = fabsf(v);
+            float amax = av > 0.0f ? av : 0.0f;
+#pragma unroll
+            for (int o = 16; o > 0; o >>= 1) {
+                const float t = __shfl_xor(amax, o, 32);
+                amax = t > amax ? t : amax;
+            }
+            if (row < a.rows) {
+                const float id = amax != 0.0f ? __fdiv_rn(127.0f, amax) : 0.0f;
+                float r = rintf(__fmul_rn(v, id));
+                r = fminf(fmaxf(r, -128.0f), 127.0f);
+                a.y[(size_t)m * a.ldc + row] = v;
+                a.yq[(size_t)m * a.rows + row] = (int8_t)(int)r;
+                if ((lane & 31) == 0) a.ys[(size_t)m * (a.rows >> 5) + (row >> 5)] = __fmul_rn(amax, grx_bits_f32(0x3c010204u));
+            }
+        }
+        return;
+    }
+    if constexpr (EPI == GRX_EPI_QKV_ROPE) {
+        // applyRope (pockettts/nn.go:80-93) on the q and k rows: the pair
+        // (2i, 2i+1) of a head sits in adjacent lanes; x'[2i] = r*c - im*s,
+        // x'[2i+1] = r*s + im*c, unfused, with f32 cos/sin of the angle.
+#pragma unroll
+        for (int m = 0; m < M; ++m) {
+            if (!mine(m)) continue;
+            const float c = acc[m];
+            const float other = __shfl_xor(c, 1);
+            if (row >= a.rows) continue;
+            const int pos = *a.pos + a.pos_add + m;
+            if (row < 2 * a.seg) {
+                const int j = row % a.seg, hd = 2 * a.rope_half;
+                const int i = (j % hd) >> 1;
+                const float cs = a.rope_cos[(size_t)pos * a.rope_half + i];
+                const float sn = a.rope_sin[(size_t)pos * a.rope_half + i];
+                const bool even = (j & 1) == 0;
+                const float r = even ? c : other, im = even ? other : c;
+                const float v = even ? __fsub_rn(__fmul_rn(r, cs), __fmul_rn(im, sn))
+                                     : __fadd_rn(__fmul_rn(r, sn), __fmul_rn(im, cs));
+                if (row < a.seg)
+                    a.y[(size_t)m * a.ldc + row] = v;
+                else
+                    a.kc[(size_t)pos * a.seg + row - a.seg] = v;
+            } else {
+                a.vc[(size_t)pos * a.seg + row - 2 * a.seg] = c;
+            }
+        }
+        return;
+    }
+    if (row >= a.rows) return;
+#pragma unroll
+    for (int m = 0; m < M; ++m) {
+        if (!mine(m)) continue;
+        const float c = acc[m];
+        if constexpr (EPI == GRX_EPI_STORE) {
+            a.y[(size_t)m * a.ldc + row] = c;
+        } else if constexpr (EPI == GRX_EPI_RESID) {
+            a.y[(size_t)m * a.ldc + row] = __fadd_rn(a.resid[(size_t)m * a.ldr + row], c);
+        } else if constexpr (EPI == GRX_EPI_GELU) {
+            // parGelu (whisper/encoder.go:147-151): geluVec over chunks of
+            // 1<<14 values of the flat [M][rows] output.
+            const int flat = a.streams ? row : m * a.rows + row, total = a.streams ? a.rows : M * a.rows;
+            const int start = flat & ~((1 << 14) - 1);
+            const int len = min(1 << 14, total - start);
+            a.y[(size_t)m * a.ldc + row] = grx_gelu_at(c, flat - start, len);
+        } else if constexpr (EPI == GRX_EPI_QKV) {
+            // one stream: rows are positions pos.., caches [pos][seg];
+            // streams: row m at pos in stream m's cache (kv_stream floats on)
+            const int pos = *a.pos + a.pos_add + (a.streams ? 0 : m);
+            const size_t so = a.streams ? (size_t)m * a.kv_stream : 0;
+            if (row < a.seg)
+                a.y[(size_t)m * a.ldc + row] = c;
+            else if (row < 2 * a.seg)
+                a.kc[so + (size_t)pos * a.seg + row - a.seg] = c;
+            else
+                a.vc[so + (size_t)pos * a.seg + row - 2 * a.seg] = c;
+        }
+    }
+}
+
 // ---------------------------------------------------------------- kernel
 
 template <int M, int W, int PRO, int EPI>
@@ -347,163 +512,381 @@ __global__ __launch_bounds__(64 * W) void gemv_q8_kernel(const GemvArgs a) {
 
     // ---- epilogue: row m is ended by wave 0 (one wave, or after the fold
     // above), or by wave m % W when rows were folded round by round
-    auto mine = [&](int m) { return !RND || m % W == wave; };
-    if constexpr (EPI == GRX_EPI_ARGMAX) {
+    gemv_epilogue<M, W, RND, EPI>(a, acc, row, lane, wave);
+}
+
+// ---------------------------------------------------------------- one row
+
+// Cross-lane moves within rows of 16 lanes (DPP; every lane active): the
+// quad permutations [1,0,3,2] and [2,3,0,1], the mirror of each 8 and of
+// each 16 lanes.  Sums and maxima built from them hold the same value in
+// every lane of the group (a + b == b + a).
+constexpr int kDppXor1 = 0xb1, kDppXor2 = 0x4e, kDppHalfMirror = 0x141, kDppMirror = 0x140;
+
+template <int CTRL>
+__device__ __forceinline__ float dpp_f32(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false));
+}
+template <int CTRL>
+__device__ __forceinline__ double dpp_f64(double v) {
+    const unsigned long long u = (unsigned long long)__double_as_longlong(v);
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)u, CTRL, 0xf, 0xf, false);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)(u >> 32), CTRL, 0xf, 0xf, false);
+    return __longlong_as_double((long long)(((unsigned long long)hi << 32) | lo));
+}
+__device__ __forceinline__ double readlane_f64(double v, int l) {
+    const unsigned long long u = (unsigned long long)__double_as_longlong(v);
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)u, l);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(u >> 32), l);
+    return __longlong_as_double((long long)(((unsigned long long)hi << 32) | lo));
+}
+// The wave's float64 sum, the same in every lane: rows of 16 by DPP, then
+// (row0 + row1) + (row2 + row3).
+__device__ __forceinline__ double wave_sum_f64(double v) {
+    v = __dadd_rn(v, dpp_f64<kDppXor1>(v));
+    v = __dadd_rn(v, dpp_f64<kDppXor2>(v));
+    v = __dadd_rn(v, dpp_f64<kDppHalfMirror>(v));
+    v = __dadd_rn(v, dpp_f64<kDppMirror>(v));
+    return __dadd_rn(__dadd_rn(readlane_f64(v, 0), readlane_f64(v, 16)),
+                     __dadd_rn(readlane_f64(v, 32), readlane_f64(v, 48)));
+}
+// The largest of each 8 lanes' values (a Q8_0 block held as 8 float4s).
+__device__ __forceinline__ float max8(float m) {
+    float t = dpp_f32<kDppXor1>(m);
+    m = t > m ? t : m;
+    t = dpp_f32<kDppXor2>(m);
+    m = t > m ? t : m;
+    t = dpp_f32<kDppHalfMirror>(m);
+    return t > m ? t : m;
+}
+__device__ __forceinline__ float amax4(const float4 &v) {
+    float m = fabsf(v.x);
+    m = m > 0.0f ? m : 0.0f;
+    float t = fabsf(v.y);
+    m = t > m ? t : m;
+    t = fabsf(v.z);
+    m = t > m ? t : m;
+    t = fabsf(v.w);
+    return t > m ? t : m;
+}
+__device__ __forceinline__ uint32_t quant4(const float4 &v, float id) {
+    auto q = [&](float x) {
+        float r = rintf(__fmul_rn(x, id));
+        r = fminf(fmaxf(r, -128.0f), 127.0f);
+        return (uint32_t)(uint8_t)(int8_t)(int)r;
+    };
+    return q(v.x) | q(v.y) << 8 | q(v.z) << 16 | q(v.w) << 24;
+}
+
+// Widest row a one-row product rounds in its prologue: pieces of 4 values
+// per lane held in registers (5 x 64 x 4 = 1280 values).
+constexpr int kRowPieces = 5;
+// Blocks whose weight loads a one-row product issues before its prologue.
+constexpr int kPrefetch = 4;
+
+// The product of ONE activation row (decode steps): q8_gemv's tile scheme
+// with the latency of a single row in mind.
+//  - every wave issues its first kPrefetch blocks' weight loads (and wave 0
+//    the bias and residual) before anything waits;
+//  - the activation row is built by wave 0 alone (LayerNorm and rounding
+//    with cross-lane DPP sums, the row as 5 float4 pieces per lane, piece
+//    P = 64 j + lane), so the prologue has no workgroup barrier; the other
+//    waves wait once, at the barrier that publishes the rounded row;
+//  - the remaining blocks go in batches of BU with every load in flight,
+//    a last partial batch included (indices clamped, duplicates discarded);
+//  - with several waves, wave 0 folds the tile's block products in block
+//    order, 8 LDS reads in flight at a time.
+// The arithmetic per output is the same as gemv_q8_kernel's (bit for bit).
+template <int W, int PRO, int EPI>
+__global__ __launch_bounds__(64 * W) void gemv1_kernel(const GemvArgs a) {
+    extern __shared__ __align__(16) unsigned char smem[];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int tile = blockIdx.x;
+    const int nb = a.nb, K = nb * GRX_QK;
+    const int row = tile * 64 + lane;
+    constexpr bool PQ = PRO == GRX_PRO_PREQ;
+    // LDS: [lxq K int8][lxs nb f32][lp nb*64 f32 if W > 1]
+    const size_t o_xs = PQ ? 0 : (size_t)K;
+    const size_t o_p = o_xs + (PQ ? 0 : (((size_t)nb * 4 + 15) & ~(size_t)15));
+    int8_t *lxq = reinterpret_cast<int8_t *>(smem);
+    float *lxs = reinterpret_cast<float *>(smem + o_xs);
+    float *lp = reinterpret_cast<float *>(smem + o_p);
+
+    const int b0 = (wave * nb) / W, b1 = ((wave + 1) * nb) / W;
+    const int4 *__restrict__ wq = reinterpret_cast<const int4 *>(a.qs) + (size_t)tile * nb * 128;
+    const uint16_t *__restrict__ wd = a.ds + (size_t)tile * nb * 64;
+    auto load_block = [&](int b, int4 &w0, int4 &w1, uint32_t &dh) {
+        if (a.cacheable) {
+            w0 = wq[(size_t)b * 128 + lane];
+            w1 = wq[(size_t)b * 128 + 64 + lane];
+            dh = wd[(size_t)b * 64 + lane];
+        } else {
+            w0 = wload(wq + (size_t)b * 128 + lane);
+            w1 = wload(wq + (size_t)b * 128 + 64 + lane);
+            dh = wload(wd + (size_t)b * 64 + lane);
+        }
+    };
+    auto act = [&](int b, int4 &a0, int4 &a1) {
+        const int4 *p = reinterpret_cast<const int4 *>((PQ ? a.xq : lxq) + (size_t)b * GRX_QK);
+        a0 = p[0];
+        a1 = p[1];
+    };
+    auto act_scale = [&](int b) -> float { return PQ ? a.xs[b] : lxs[b]; };
+
+    // ---- loads that wait for nothing: the first npf blocks (1, 2 or
+    // kPrefetch; up to kPrefetch - 1 repeats of the last)
+    constexpr int PF = PQ ? 0 : kPrefetch;
+    int4 pw[2 * (PF > 0 ? PF : 1)];
+    uint32_t pd[PF > 0 ? PF : 1];
+    const int npf = PF > 0 ? min(PF, b1 - b0) : 0;
+    if constexpr (PF > 0) {
+        const int nl = npf <= 2 ? npf : PF;
 #pragma unroll
-        for (int m = 0; m < M; ++m) {
-            if (!mine(m)) continue;
-            const float c = acc[m];
-            if (a.y != nullptr && row < a.rows) a.y[(size_t)m * a.ldc + row] = c;
-            // key: orderable float bits, then the complement of the index, so
-            // the maximum key is the largest value at its first index
-            // (whisper/transcribe.go:459-464); -0 counts as +0 and NaN never wins.
-            unsigned long long key = 0;
-            if (row < a.rows && !(c != c)) {
-                const float cc = c == 0.0f ? 0.0f : c;
-                const uint32_t u = __float_as_uint(cc);
-                const uint32_t ord = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
-                key = ((unsigned long long)ord << 32) | (uint32_t)(0xffffffffu - (uint32_t)row);
-            }
+        for (int u = 0; u < PF; ++u)
+            if (u < nl) load_block(b0 + min(u, npf - 1), pw[2 * u], pw[2 * u + 1], pd[u]);
+    }
+    float bias = 0.0f, resid = 0.0f;
+    if (wave == 0 && row < a.rows) {
+        if (a.bias != nullptr) bias = a.bias[row];
+        if constexpr (EPI == GRX_EPI_RESID) resid = a.resid[row];
+    }
+
+    // ---- prologue (wave 0): the activation row, rounded to Q8_0, into LDS
+    if constexpr (!PQ) {
+        if (wave == 0) {
+            const int npc = K / 4;  // float4 pieces
+            float4 xv[kRowPieces], wv[kRowPieces], bv[kRowPieces];
+            const float4 *x4 = reinterpret_cast<const float4 *>(a.x);
 #pragma unroll
-            for (int o = 32; o > 0; o >>= 1) {
-                const unsigned long long k2 = __shfl_xor(key, o);
-                key = k2 > key ? k2 : key;
-            }
-            if (lane == 0) {
-                if (a.keys != nullptr) {
-                    // one slot per workgroup and row: no contended atomics;
-                    // argmax_finish_kernel takes the maximum afterwards
-                    a.keys[(size_t)blockIdx.x * M + m] = key;
+            for (int j = 0; j < kRowPieces; ++j) {
+                const int P = min(j * 64 + lane, npc - 1);
+                if constexpr (PRO == GRX_PRO_EMBED_LN) {
+                    // tokEmb.row(tok) + decPos[pos] (whisper/decoder.go:42-46):
+                    // the embedding row from its tile layout, d*q then + pos
+                    const int t = a.tok[0], p = *a.pos + a.pos_add;
+                    const int etile = t >> 6, elane = t & 63, i = 4 * P;
+                    const int b = i >> 5, h = (i >> 4) & 1, e = i & 15;
+                    const uint32_t q4 = *reinterpret_cast<const uint32_t *>(
+                        a.emb_qs + (((size_t)etile * nb + b) * 2 + h) * 1024 + elane * 16 + e);
+                    const float d = grx_f16_to_f32(a.emb_ds[((size_t)etile * nb + b) * 64 + elane]);
+                    const float4 pe = reinterpret_cast<const float4 *>(a.pos_emb + (size_t)p * K)[P];
+                    xv[j].x = __fadd_rn(__fmul_rn((float)(int8_t)(q4 & 0xff), d), pe.x);
+                    xv[j].y = __fadd_rn(__fmul_rn((float)(int8_t)((q4 >> 8) & 0xff), d), pe.y);
+                    xv[j].z = __fadd_rn(__fmul_rn((float)(int8_t)((q4 >> 16) & 0xff), d), pe.z);
+                    xv[j].w = __fadd_rn(__fmul_rn((float)(int8_t)(q4 >> 24), d), pe.w);
                 } else {
-                    // a returning atomic: its old value comes back only once
-                    // the maximum has been taken at the coherence point
-                    const unsigned long long old = atomicMax(a.amax + m, key);
-                    asm volatile("; argmax done %0" ::"v"((uint32_t)old));
+                    xv[j] = x4[P];
+                }
+                if constexpr (PRO == GRX_PRO_LN || PRO == GRX_PRO_EMBED_LN || PRO == GRX_PRO_LN64) {
+                    if (PRO != GRX_PRO_LN64 || a.ln_w != nullptr) {
+                        wv[j] = reinterpret_cast<const float4 *>(a.ln_w)[P];
+                        bv[j] = reinterpret_cast<const float4 *>(a.ln_b)[P];
+                    }
                 }
             }
-        }
-        if (a.counter != nullptr) {
-            // The last workgroup to finish ends the decode step: the argmax
-            // token, its record, the next position; then clears the key and
-            // the counter for the next step.  Device-scope atomics are
-            // coherent across the XCDs, and each workgroup's atomicMax has
-            // returned before its count is added, so no cache writeback is
-            // needed.  (Rows folded by several waves: every wave's atomicMax
-            // is in before wave 0 counts.)
-            if constexpr (RND) __syncthreads();
-            if (wave != 0) return;
-            unsigned int done = 0;
-            if (lane == 0) done = atomicAdd(a.counter, 1u);
-            done = __shfl(done, 0);
-            if (done == gridDim.x - 1) {
-                const int p0 = *a.pos;
-                if (lane < M) {
-                    const unsigned long long k = atomicMax(a.amax + lane, 0ull);
-                    const int t = (int)(0xffffffffu - (uint32_t)(k & 0xffffffffull));
-                    a.tok_w[lane] = t;
-                    if (a.streams)
-                        a.hist[(size_t)lane * a.hist_stream + p0] = t;
-                    else
-                        a.hist[p0 + lane] = t;
-                    a.amax[lane] = 0ull;
-                }
-                if (lane == 0) {
-                    *a.pos_w = p0 + (a.streams ? 1 : M);
-                    *a.counter = 0u;
-                }
-            }
-        }
-        return;
-    }
-    if constexpr (EPI == GRX_EPI_GELU_Q) {
-        // geluVec, then quantU8 of the output's 32-value blocks for the next
-        // product: rows 64*tile..+31 and +32..+63 are two whole blocks
-        // (rows % 32 == 0), held by the two halves of this wave.
+            if constexpr (PRO == GRX_PRO_EMBED_LN) {
+                if (tile == 0) {
 #pragma unroll
-        for (int m = 0; m < M; ++m) {
-            if (!mine(m)) continue;
-            // streams: each row is its own [1][rows] buffer
-            const int flat = a.streams ? row : m * a.rows + row, total = a.streams ? a.rows : M * a.rows;
-            const int start = flat & ~((1 << 14) - 1);
-            const int len = min(1 << 14, total - start);
-            const float v = row < a.rows ? grx_gelu_at(acc[m], flat - start, len) : 0.0f;
-            const float av = fabsf(v);
-            float amax = av > 0.0f ? av : 0.0f;
-#pragma unroll
-            for (int o = 16; o > 0; o >>= 1) {
-                const float t = __shfl_xor(amax, o, 32);
-                amax = t > amax ? t : amax;
+                    for (int j = 0; j < kRowPieces; ++j)
+                        if (j * 64 + lane < npc) reinterpret_cast<float4 *>(a.x_out)[j * 64 + lane] = xv[j];
+                }
             }
-            if (row < a.rows) {
+            if constexpr (PRO == GRX_PRO_LN || PRO == GRX_PRO_EMBED_LN) {
+                // layerNorm (internal/kern/mathx.go:55-75): float64 sums,
+                // mean and inv rounded to float32, y = (v-mean)*inv*w + b
+                double ps = 0.0;
+#pragma unroll
+                for (int j = 0; j < kRowPieces; ++j) {
+                    if (j * 64 + lane < npc) {
+                        ps = __dadd_rn(ps, (double)xv[j].x);
+                        ps = __dadd_rn(ps, (double)xv[j].y);
+                        ps = __dadd_rn(ps, (double)xv[j].z);
+                        ps = __dadd_rn(ps, (double)xv[j].w);
+                    }
+                }
+                const float mean = (float)(wave_sum_f64(ps) / (double)K);
+                double pv = 0.0;
+                auto sq = [&](float v) {
+                    const double d = (double)__fsub_rn(v, mean);
+                    pv = __dadd_rn(pv, __dmul_rn(d, d));
+                };
+#pragma unroll
+                for (int j = 0; j < kRowPieces; ++j) {
+                    if (j * 64 + lane < npc) {
+                        sq(xv[j].x);
+                        sq(xv[j].y);
+                        sq(xv[j].z);
+                        sq(xv[j].w);
+                    }
+                }
+                const double vs = wave_sum_f64(pv);
+                const float inv = (float)(1.0 / sqrt(vs / (double)K + 1e-5));
+                auto nrm = [&](float v, float w, float b) {
+                    float t = __fsub_rn(v, mean);
+                    t = __fmul_rn(t, inv);
+                    t = __fmul_rn(t, w);
+                    return __fadd_rn(t, b);
+                };
+#pragma unroll
+                for (int j = 0; j < kRowPieces; ++j) {
+                    xv[j].x = nrm(xv[j].x, wv[j].x, bv[j].x);
+                    xv[j].y = nrm(xv[j].y, wv[j].y, bv[j].y);
+                    xv[j].z = nrm(xv[j].z, wv[j].z, bv[j].z);
+                    xv[j].w = nrm(xv[j].w, wv[j].w, bv[j].w);
+                }
+            } else if constexpr (PRO == GRX_PRO_LN64) {
+                // layerNorm of pockettts/nn.go:27-49: statistics and the
+                // normalized value in float64, gain and bias in float32
+                double ps = 0.0;
+#pragma unroll
+                for (int j = 0; j < kRowPieces; ++j) {
+                    if (j * 64 + lane < npc) {
+                        ps = __dadd_rn(ps, (double)xv[j].x);
+                        ps = __dadd_rn(ps, (double)xv[j].y);
+                        ps = __dadd_rn(ps, (double)xv[j].z);
+                        ps = __dadd_rn(ps, (double)xv[j].w);
+                    }
+                }
+                const double mean = wave_sum_f64(ps) / (double)K;
+                double pv = 0.0;
+                auto sq = [&](float v) {
+                    const double d = __dsub_rn((double)v, mean);
+                    pv = __dadd_rn(pv, __dmul_rn(d, d));
+                };
+#pragma unroll
+                for (int j = 0; j < kRowPieces; ++j) {
+                    if (j * 64 + lane < npc) {
+                        sq(xv[j].x);
+                        sq(xv[j].y);
+                        sq(xv[j].z);
+                        sq(xv[j].w);
+                    }
+                }
+                const double inv = 1.0 / sqrt(wave_sum_f64(pv) / (double)K + a.ln_eps);
+                const bool gb = a.ln_w != nullptr;
+                auto nrm = [&](float v, float w, float b) {
+                    float o = (float)__dmul_rn(__dsub_rn((double)v, mean), inv);
+                    return gb ? __fadd_rn(__fmul_rn(o, w), b) : o;
+                };
+#pragma unroll
+                for (int j = 0; j < kRowPieces; ++j) {
+                    xv[j].x = nrm(xv[j].x, wv[j].x, bv[j].x);
+                    xv[j].y = nrm(xv[j].y, wv[j].y, bv[j].y);
+                    xv[j].z = nrm(xv[j].z, wv[j].z, bv[j].z);
+                    xv[j].w = nrm(xv[j].w, wv[j].w, bv[j].w);
+                }
+            }
+            // quantU8 (q8int.go:88-105): a block is 8 pieces in 8 lanes
+#pragma unroll
+            for (int j = 0; j < kRowPieces; ++j) {
+                const int P = j * 64 + lane;
+                const float amax = max8(amax4(xv[j]));
                 const float id = amax != 0.0f ? __fdiv_rn(127.0f, amax) : 0.0f;
-                float r = rintf(__fmul_rn(v, id));
-                r = fminf(fmaxf(r, -128.0f), 127.0f);
-                a.y[(size_t)m * a.ldc + row] = v;
-                a.yq[(size_t)m * a.rows + row] = (int8_t)(int)r;
-                if ((lane & 31) == 0) a.ys[(size_t)m * (a.rows >> 5) + (row >> 5)] = __fmul_rn(amax, grx_bits_f32(0x3c010204u));
+                const uint32_t q = quant4(xv[j], id);
+                if (P < npc) {
+                    reinterpret_cast<uint32_t *>(lxq)[P] = q;
+                    if ((lane & 7) == 0) lxs[P >> 3] = __fmul_rn(amax, grx_bits_f32(0x3c010204u));
+                }
             }
         }
-        return;
+        __syncthreads();
     }
-    if constexpr (EPI == GRX_EPI_QKV_ROPE) {
-        // applyRope (pockettts/nn.go:80-93) on the q and k rows: the pair
-        // (2i, 2i+1) of a head sits in adjacent lanes; x'[2i] = r*c - im*s,
-        // x'[2i+1] = r*s + im*c, unfused, with f32 cos/sin of the angle.
+
+    // ---- this wave's blocks: the prefetched ones, then batches of BU
+    float acc = bias;
+    // U blocks from bb on, nv of them real (the rest repeat block bb+nv-1)
+    auto dots = [&](auto u_tag, const int4 *w, const uint32_t *dh, int bb, int nv) {
+        constexpr int U = decltype(u_tag)::value;
 #pragma unroll
-        for (int m = 0; m < M; ++m) {
-            if (!mine(m)) continue;
-            const float c = acc[m];
-            const float other = __shfl_xor(c, 1);
-            if (row >= a.rows) continue;
-            const int pos = *a.pos + a.pos_add + m;
-            if (row < 2 * a.seg) {
-                const int j = row % a.seg, hd = 2 * a.rope_half;
-                const int i = (j % hd) >> 1;
-                const float cs = a.rope_cos[(size_t)pos * a.rope_half + i];
-                const float sn = a.rope_sin[(size_t)pos * a.rope_half + i];
-                const bool even = (j & 1) == 0;
-                const float r = even ? c : other, im = even ? other : c;
-                const float v = even ? __fsub_rn(__fmul_rn(r, cs), __fmul_rn(im, sn))
-                                     : __fadd_rn(__fmul_rn(r, sn), __fmul_rn(im, cs));
-                if (row < a.seg)
-                    a.y[(size_t)m * a.ldc + row] = v;
-                else
-                    a.kc[(size_t)pos * a.seg + row - a.seg] = v;
+        for (int u = 0; u < U; ++u) {
+            const int b = bb + min(u, nv - 1);
+            int4 a0, a1;
+            act(b, a0, a1);
+            const int s = sdot8(w[2 * u], w[2 * u + 1], a0, a1);
+            const float pv = __fmul_rn((float)s, grx_f16_to_f32((uint16_t)dh[u]));
+            if constexpr (W == 1) {
+                const float f = __fmaf_rn(pv, act_scale(b), acc);
+                acc = u < nv ? f : acc;
             } else {
-                a.vc[(size_t)pos * a.seg + row - 2 * a.seg] = c;
+                lp[(size_t)b * 64 + lane] = pv;  // a repeated block writes its own value again
             }
         }
-        return;
-    }
-    if (row >= a.rows) return;
+    };
+    auto batch = [&](auto u_tag, int bb, int nv) {
+        constexpr int U = decltype(u_tag)::value;
+        int4 w[2 * U];
+        uint32_t dh[U];
 #pragma unroll
-    for (int m = 0; m < M; ++m) {
-        if (!mine(m)) continue;
-        const float c = acc[m];
-        if constexpr (EPI == GRX_EPI_STORE) {
-            a.y[(size_t)m * a.ldc + row] = c;
-        } else if constexpr (EPI == GRX_EPI_RESID) {
-            a.y[(size_t)m * a.ldc + row] = __fadd_rn(a.resid[(size_t)m * a.ldr + row], c);
-        } else if constexpr (EPI == GRX_EPI_GELU) {
-            // parGelu (whisper/encoder.go:147-151): geluVec over chunks of
-            // 1<<14 values of the flat [M][rows] output.
-            const int flat = a.streams ? row : m * a.rows + row, total = a.streams ? a.rows : M * a.rows;
-            const int start = flat & ~((1 << 14) - 1);
-            const int len = min(1 << 14, total - start);
-            a.y[(size_t)m * a.ldc + row] = grx_gelu_at(c, flat - start, len);
-        } else if constexpr (EPI == GRX_EPI_QKV) {
-            // one stream: rows are positions pos.., caches [pos][seg];
-            // streams: row m at pos in stream m's cache (kv_stream floats on)
-            const int pos = *a.pos + a.pos_add + (a.streams ? 0 : m);
-            const size_t so = a.streams ? (size_t)m * a.kv_stream : 0;
-            if (row < a.seg)
-                a.y[(size_t)m * a.ldc + row] = c;
-            else if (row < 2 * a.seg)
-                a.kc[so + (size_t)pos * a.seg + row - a.seg] = c;
-            else
-                a.vc[so + (size_t)pos * a.seg + row - 2 * a.seg] = c;
-        }
+        for (int u = 0; u < U; ++u) load_block(bb + min(u, nv - 1), w[2 * u], w[2 * u + 1], dh[u]);
+        dots(u_tag, w, dh, bb, nv);
+    };
+    // a last partial batch of nv blocks: the smallest of 1, 2, 4, BU that holds them
+    auto tail = [&](int bb, int nv) {
+        if (nv == 1)
+            batch(std::integral_constant<int, 1>{}, bb, 1);
+        else if (nv == 2)
+            batch(std::integral_constant<int, 2>{}, bb, 2);
+        else if (nv <= 4)
+            batch(std::integral_constant<int, 4>{}, bb, nv);
+        else
+            batch(std::integral_constant<int, BU>{}, bb, nv);
+    };
+    int bb = b0;
+    if constexpr (PF > 0) {
+        if (npf == 1)
+            dots(std::integral_constant<int, 1>{}, pw, pd, b0, 1);
+        else if (npf == 2)
+            dots(std::integral_constant<int, 2>{}, pw, pd, b0, 2);
+        else
+            dots(std::integral_constant<int, PF>{}, pw, pd, b0, npf);
+        bb += npf;
     }
+    for (; bb + BU <= b1; bb += BU) batch(std::integral_constant<int, BU>{}, bb, BU);
+    if (bb < b1) tail(bb, b1 - bb);
+
+    if constexpr (W > 1) {
+        __syncthreads();
+        if (wave != 0) return;
+        // the ordered chain c = fma(p_b, da_b, c) in block order
+        int b = 0;
+        for (; b + 8 <= nb; b += 8) {
+            float t[8], sc[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                t[u] = lp[(size_t)(b + u) * 64 + lane];
+                sc[u] = act_scale(b + u);
+            }
+#pragma unroll
+            for (int u = 0; u < 8; ++u) acc = __fmaf_rn(t[u], sc[u], acc);
+        }
+        for (; b < nb; ++b) acc = __fmaf_rn(lp[(size_t)b * 64 + lane], act_scale(b), acc);
+    }
+
+    // ---- epilogue (wave 0)
+    if constexpr (EPI == GRX_EPI_RESID) {
+        if (row < a.rows) a.y[row] = __fadd_rn(resid, acc);
+    } else if constexpr (EPI == GRX_EPI_STORE) {
+        if (row < a.rows) a.y[row] = acc;
+    } else {
+        const float accm[1] = {acc};
+        gemv_epilogue<1, W, false, EPI>(a, accm, row, lane, wave);
+    }
+}
+
+// One-row products take gemv1_kernel unless GRX_GEMV1=0 (the general
+// kernel, for comparisons) or the row is too wide for its prologue.
+bool gemv1_fits(int pro, int nb) {
+    const char *f = getenv("GRX_GEMV1");
+    if (f && f[0] == '0') return false;
+    return pro == GRX_PRO_PREQ || nb * GRX_QK <= kRowPieces * 256;
+}
+
+size_t gemv1_smem(int W, int pro, int nb) {
+    size_t n = 0;
+    if (pro != GRX_PRO_PREQ) n += (size_t)nb * GRX_QK + (((size_t)nb * 4 + 15) & ~(size_t)15);
+    if (W > 1) n += (size_t)nb * 64 * 4;
+    return n;
 }
 
 // End of a decode step from per-workgroup argmax keys (keys [nslots][M]):
@@ -614,8 +997,33 @@ hipError_t launch_w(hipStream_t st, const GemvArgs &a, int tiles, int W) {
     }
 }
 
+template <int W, int PRO, int EPI>
+hipError_t launch1_one(hipStream_t st, const GemvArgs &a, int tiles) {
+    const size_t smem = gemv1_smem(W, PRO, a.nb);
+    if (smem > 64 * 1024) {
+        static bool raised = false;
+        if (!raised) {
+            raised = true;
+            (void)hipFuncSetAttribute((const void *)gemv1_kernel<W, PRO, EPI>,
+                                      hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+        }
+    }
+    gemv1_kernel<W, PRO, EPI><<<tiles, 64 * W, smem, st>>>(a);
+    return hipGetLastError();
+}
+
 template <int PRO, int EPI>
 hipError_t launch_m(hipStream_t st, int m, const GemvArgs &a, int tiles, int W) {
+    if (m == 1 && gemv1_fits(PRO, a.nb)) {
+        while (W > 1 && W > a.nb) W >>= 1;  // every wave owns a block
+        switch (W) {
+            case 1: return launch1_one<1, PRO, EPI>(st, a, tiles);
+            case 2: return launch1_one<2, PRO, EPI>(st, a, tiles);
+            case 4: return launch1_one<4, PRO, EPI>(st, a, tiles);
+            case 8: return launch1_one<8, PRO, EPI>(st, a, tiles);
+            default: return launch1_one<16, PRO, EPI>(st, a, tiles);
+        }
+    }
     switch (m) {
         case 1: return launch_w<1, PRO, EPI>(st, a, tiles, W);
         case 2: return launch_w<2, PRO, EPI>(st, a, tiles, W);

@@ -156,6 +156,24 @@ def test_matmul_every_wave_split(kern, orc, waves):
         del os.environ["GRX_GEMV_WAVES"]
 
 
+@pytest.mark.parametrize("gemv1", ["0", "1"])
+def test_matmul_one_row_kernels(kern, orc, gemv1):
+    """One-row products through the decode kernel (GRX_GEMV1=1: loads issued
+    before the prologue, batched fold, partial last batch) and the general
+    kernel (GRX_GEMV1=0), every wave split, block counts that leave waves
+    with 1, 2, 3 and 10 blocks and a partial batch: every bit as the oracle."""
+    rng = np.random.default_rng(57)
+    os.environ["GRX_GEMV1"] = gemv1
+    try:
+        for waves in ("1", "2", "4", "8", "16"):
+            os.environ["GRX_GEMV_WAVES"] = waves
+            for n, k in ((64, 32), (65, 96), (130, 512), (64, 1024), (200, 1280), (70, 1312), (64, 5120)):
+                _check_matmul(kern, orc, rng, 1, n, k, bias=(n % 2 == 0))
+    finally:
+        os.environ.pop("GRX_GEMV_WAVES", None)
+        del os.environ["GRX_GEMV1"]
+
+
 def test_matmul_matrix_cores_all_small_sizes(kern, orc):
     """The matrix-core product forced for every m (GRX_GEMM_MIN_M=1): the
     odd sizes again, bit-identical to the oracle."""

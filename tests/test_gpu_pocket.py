@@ -3,6 +3,8 @@ the text prefix's out_norm output and every frame's output and
 end-of-speech logit bit-identical, at a small shape (prefix lengths that
 take each of MatMulF32's routes) and at the configured shape (d 1024, 16
 heads, 6 layers, FFN 4096, 64-row prefix)."""
+import os
+
 import numpy as np
 import pytest
 
@@ -26,6 +28,19 @@ def _pair(orc, hp, seed=5):
 def test_prefix_and_frames_bit_exact(kern, orc, prefix):
     """T < 4 (AddScaled), 4 <= T <= 16 (gemvRows), T > 16 (6x16 panels and
     gemv rows) for the prefix; then teacher-forced frames."""
+    _prefix_and_frames(orc, prefix)
+
+
+def test_frames_general_gemv_kernel(kern, orc):
+    """The same with one-row products on the general kernel (GRX_GEMV1=0)."""
+    os.environ["GRX_GEMV1"] = "0"
+    try:
+        _prefix_and_frames(orc, 3)
+    finally:
+        del os.environ["GRX_GEMV1"]
+
+
+def _prefix_and_frames(orc, prefix):
     hp = dict(POCKET_TTS_TINY)
     ref, lm = _pair(orc, hp)
     x, lat = pocket_inputs(hp, 8, prefix=prefix, seed=prefix)

@@ -29,11 +29,22 @@ def _same(a, b):
     return np.array_equal(np.asarray(a, np.float32).view(np.uint32), np.asarray(b, np.float32).view(np.uint32))
 
 
+@pytest.mark.parametrize("gemv1", ["1", "0"])
 @pytest.mark.parametrize("shape", ["tiny", "ragged"])
-def test_decode_logits_bit_exact(kern, orc, shape):
+def test_decode_logits_bit_exact(kern, orc, shape, gemv1):
+    """Every step's logits bit-identical, with the one-row decode kernel
+    (GRX_GEMV1=1, the default) and with the general product kernel."""
     hp = dict(WHISPER_TINY_TEST)
     if shape == "ragged":  # audio length not a multiple of 16, odd head count
         hp.update(n_audio_ctx=101, n_head=4, n_state=96, n_vocab=333)
+    os.environ["GRX_GEMV1"] = gemv1
+    try:
+        _decode_logits_bit_exact(orc, hp)
+    finally:
+        del os.environ["GRX_GEMV1"]
+
+
+def _decode_logits_bit_exact(orc, hp):
     ref, dec = _pair(orc, hp)
     toks = [5, 17, 3, 99]
     lr = ref.decode(toks)
