@@ -135,14 +135,18 @@ __device__ __forceinline__ float grx_exp8(float x) {
     return __fmul_rn(p, grx_bits_f32((uint32_t)(ni + 127) << 23));
 }
 
-// expf of internal/kern/mathx.go:7-33 (the scalar form), unfused.
+// expf of internal/kern/mathx.go:7-33 (the scalar form), unfused, without
+// branches: every case is computed and the reference's one selected (a
+// divergent branch costs more than the few extra operations).  t is kept
+// within +-256 before its conversion, which changes nothing for
+// -87 <= x <= 88 (t in [-125, 127.5]); outside that range the result is
+// the reference's 0 or +Inf.
 __device__ __forceinline__ float grx_expf_go(float x) {
-    if (x < -87.0f) return 0.0f;
-    if (x > 88.0f) return __builtin_inff();
     float t = __fmul_rn(x, grx_bits_f32(0x3fb8aa3bu));
     t = __fadd_rn(t, 0.5f);
-    int ni = (int)t;
-    if ((float)ni > t) ni--;
+    const float tc = fminf(fmaxf(t, -256.0f), 256.0f);
+    int ni = (int)tc;
+    ni -= (float)ni > tc ? 1 : 0;  // floor
     const float n = (float)ni;
     float r = __fsub_rn(x, __fmul_rn(n, grx_bits_f32(0x3f317200u)));
     r = __fsub_rn(r, __fmul_rn(n, grx_bits_f32(0x35bfbe8eu)));
@@ -153,11 +157,13 @@ __device__ __forceinline__ float grx_expf_go(float x) {
     p = __fadd_rn(__fmul_rn(p, r), 0.5f);
     p = __fadd_rn(__fmul_rn(p, r), 1.0f);
     p = __fadd_rn(__fmul_rn(p, r), 1.0f);
-    if (ni < -126) {
-        const float v = __fmul_rn(p, grx_bits_f32((uint32_t)(ni + 127 + 64) << 23));
-        return __fmul_rn(v, grx_bits_f32(0x1f800000u));
-    }
-    return __fmul_rn(p, grx_bits_f32((uint32_t)(ni + 127) << 23));
+    // ni < -126: p * 2^(ni+64) * 2^-64
+    const float small = __fmul_rn(__fmul_rn(p, grx_bits_f32((uint32_t)(ni + 127 + 64) << 23)),
+                                  grx_bits_f32(0x1f800000u));
+    const float big = __fmul_rn(p, grx_bits_f32((uint32_t)(ni + 127) << 23));
+    float e = ni < -126 ? small : big;
+    e = x < -87.0f ? 0.0f : e;
+    return x > 88.0f ? __builtin_inff() : e;
 }
 
 // geluAVX of internal/kern/kernels_amd64.s:299-338, one lane.
@@ -184,13 +190,10 @@ __device__ __forceinline__ float grx_gelu_go(float v) {
     float w = __fmul_rn(grx_bits_f32(0x3d372713u), v);
     w = __fadd_rn(1.0f, __fmul_rn(w, v));
     u = __fmul_rn(u, w);
-    float t;
-    if (u > 9.0f)
-        t = 1.0f;
-    else if (u < -9.0f)
-        t = -1.0f;
-    else
-        t = __fsub_rn(1.0f, __fdiv_rn(2.0f, __fadd_rn(grx_expf_go(__fmul_rn(2.0f, u)), 1.0f)));
+    // tanh(u) = 1 - 2/(e^{2u}+1), or +-1 past +-9; computed, then selected
+    float t = __fsub_rn(1.0f, __fdiv_rn(2.0f, __fadd_rn(grx_expf_go(__fmul_rn(2.0f, u)), 1.0f)));
+    t = u < -9.0f ? -1.0f : t;
+    t = u > 9.0f ? 1.0f : t;
     return __fmul_rn(__fmul_rn(0.5f, v), __fadd_rn(1.0f, t));
 }
 

@@ -578,8 +578,9 @@ __device__ __forceinline__ uint32_t quant4(const float4 &v, float id) {
     return q(v.x) | q(v.y) << 8 | q(v.z) << 16 | q(v.w) << 24;
 }
 
-// Widest row a one-row product rounds in its prologue: pieces of 4 values
-// per lane held in registers (5 x 64 x 4 = 1280 values).
+// Widest row a one-row product rounds in its prologue: NP pieces of 4
+// values per lane held in registers (NP = 2, 4 or 5: up to 512, 1024 or
+// 1280 values).
 constexpr int kRowPieces = 5;
 // Blocks whose weight loads a one-row product issues before its prologue.
 constexpr int kPrefetch = 4;
@@ -589,7 +590,7 @@ constexpr int kPrefetch = 4;
 //  - every wave issues its first kPrefetch blocks' weight loads (and wave 0
 //    the bias and residual) before anything waits;
 //  - the activation row is built by wave 0 alone (LayerNorm and rounding
-//    with cross-lane DPP sums, the row as 5 float4 pieces per lane, piece
+//    with cross-lane DPP sums, the row as NP float4 pieces per lane, piece
 //    P = 64 j + lane), so the prologue has no workgroup barrier; the other
 //    waves wait once, at the barrier that publishes the rounded row;
 //  - the remaining blocks go in batches of BU with every load in flight,
@@ -597,7 +598,7 @@ constexpr int kPrefetch = 4;
 //  - with several waves, wave 0 folds the tile's block products in block
 //    order, 8 LDS reads in flight at a time.
 // The arithmetic per output is the same as gemv_q8_kernel's (bit for bit).
-template <int W, int PRO, int EPI>
+template <int W, int NP, int PRO, int EPI>
 __global__ __launch_bounds__(64 * W) void gemv1_kernel(const GemvArgs a) {
     extern __shared__ __align__(16) unsigned char smem[];
     const int tid = threadIdx.x, lane = tid & 63;
@@ -606,9 +607,12 @@ __global__ __launch_bounds__(64 * W) void gemv1_kernel(const GemvArgs a) {
     const int nb = a.nb, K = nb * GRX_QK;
     const int row = tile * 64 + lane;
     constexpr bool PQ = PRO == GRX_PRO_PREQ;
+    // the rounded row in LDS when the prologue builds it; pre-rounded rows
+    // are read from HBM by each wave (a copy to LDS measured slower)
+    constexpr bool LQ = !PQ;
     // LDS: [lxq K int8][lxs nb f32][lp nb*64 f32 if W > 1]
-    const size_t o_xs = PQ ? 0 : (size_t)K;
-    const size_t o_p = o_xs + (PQ ? 0 : (((size_t)nb * 4 + 15) & ~(size_t)15));
+    const size_t o_xs = LQ ? (size_t)K : 0;
+    const size_t o_p = o_xs + (LQ ? (((size_t)nb * 4 + 15) & ~(size_t)15) : 0);
     int8_t *lxq = reinterpret_cast<int8_t *>(smem);
     float *lxs = reinterpret_cast<float *>(smem + o_xs);
     float *lp = reinterpret_cast<float *>(smem + o_p);
@@ -628,15 +632,15 @@ __global__ __launch_bounds__(64 * W) void gemv1_kernel(const GemvArgs a) {
         }
     };
     auto act = [&](int b, int4 &a0, int4 &a1) {
-        const int4 *p = reinterpret_cast<const int4 *>((PQ ? a.xq : lxq) + (size_t)b * GRX_QK);
+        const int4 *p = reinterpret_cast<const int4 *>((LQ ? lxq : a.xq) + (size_t)b * GRX_QK);
         a0 = p[0];
         a1 = p[1];
     };
-    auto act_scale = [&](int b) -> float { return PQ ? a.xs[b] : lxs[b]; };
+    auto act_scale = [&](int b) -> float { return LQ ? lxs[b] : a.xs[b]; };
 
     // ---- loads that wait for nothing: the first npf blocks (1, 2 or
     // kPrefetch; up to kPrefetch - 1 repeats of the last)
-    constexpr int PF = PQ ? 0 : kPrefetch;
+    constexpr int PF = LQ ? kPrefetch : 0;
     int4 pw[2 * (PF > 0 ? PF : 1)];
     uint32_t pd[PF > 0 ? PF : 1];
     const int npf = PF > 0 ? min(PF, b1 - b0) : 0;
@@ -656,10 +660,10 @@ __global__ __launch_bounds__(64 * W) void gemv1_kernel(const GemvArgs a) {
     if constexpr (!PQ) {
         if (wave == 0) {
             const int npc = K / 4;  // float4 pieces
-            float4 xv[kRowPieces], wv[kRowPieces], bv[kRowPieces];
+            float4 xv[NP], wv[NP], bv[NP];
             const float4 *x4 = reinterpret_cast<const float4 *>(a.x);
 #pragma unroll
-            for (int j = 0; j < kRowPieces; ++j) {
+            for (int j = 0; j < NP; ++j) {
                 const int P = min(j * 64 + lane, npc - 1);
                 if constexpr (PRO == GRX_PRO_EMBED_LN) {
                     // tokEmb.row(tok) + decPos[pos] (whisper/decoder.go:42-46):
@@ -688,7 +692,7 @@ __global__ __launch_bounds__(64 * W) void gemv1_kernel(const GemvArgs a) {
             if constexpr (PRO == GRX_PRO_EMBED_LN) {
                 if (tile == 0) {
 #pragma unroll
-                    for (int j = 0; j < kRowPieces; ++j)
+                    for (int j = 0; j < NP; ++j)
                         if (j * 64 + lane < npc) reinterpret_cast<float4 *>(a.x_out)[j * 64 + lane] = xv[j];
                 }
             }
@@ -697,7 +701,7 @@ __global__ __launch_bounds__(64 * W) void gemv1_kernel(const GemvArgs a) {
                 // mean and inv rounded to float32, y = (v-mean)*inv*w + b
                 double ps = 0.0;
 #pragma unroll
-                for (int j = 0; j < kRowPieces; ++j) {
+                for (int j = 0; j < NP; ++j) {
                     if (j * 64 + lane < npc) {
                         ps = __dadd_rn(ps, (double)xv[j].x);
                         ps = __dadd_rn(ps, (double)xv[j].y);
@@ -712,7 +716,7 @@ __global__ __launch_bounds__(64 * W) void gemv1_kernel(const GemvArgs a) {
                     pv = __dadd_rn(pv, __dmul_rn(d, d));
                 };
 #pragma unroll
-                for (int j = 0; j < kRowPieces; ++j) {
+                for (int j = 0; j < NP; ++j) {
                     if (j * 64 + lane < npc) {
                         sq(xv[j].x);
                         sq(xv[j].y);
@@ -729,7 +733,7 @@ __global__ __launch_bounds__(64 * W) void gemv1_kernel(const GemvArgs a) {
                     return __fadd_rn(t, b);
                 };
 #pragma unroll
-                for (int j = 0; j < kRowPieces; ++j) {
+                for (int j = 0; j < NP; ++j) {
                     xv[j].x = nrm(xv[j].x, wv[j].x, bv[j].x);
                     xv[j].y = nrm(xv[j].y, wv[j].y, bv[j].y);
                     xv[j].z = nrm(xv[j].z, wv[j].z, bv[j].z);
@@ -740,7 +744,7 @@ __global__ __launch_bounds__(64 * W) void gemv1_kernel(const GemvArgs a) {
                 // normalized value in float64, gain and bias in float32
                 double ps = 0.0;
 #pragma unroll
-                for (int j = 0; j < kRowPieces; ++j) {
+                for (int j = 0; j < NP; ++j) {
                     if (j * 64 + lane < npc) {
                         ps = __dadd_rn(ps, (double)xv[j].x);
                         ps = __dadd_rn(ps, (double)xv[j].y);
@@ -755,7 +759,7 @@ __global__ __launch_bounds__(64 * W) void gemv1_kernel(const GemvArgs a) {
                     pv = __dadd_rn(pv, __dmul_rn(d, d));
                 };
 #pragma unroll
-                for (int j = 0; j < kRowPieces; ++j) {
+                for (int j = 0; j < NP; ++j) {
                     if (j * 64 + lane < npc) {
                         sq(xv[j].x);
                         sq(xv[j].y);
@@ -770,7 +774,7 @@ __global__ __launch_bounds__(64 * W) void gemv1_kernel(const GemvArgs a) {
                     return gb ? __fadd_rn(__fmul_rn(o, w), b) : o;
                 };
 #pragma unroll
-                for (int j = 0; j < kRowPieces; ++j) {
+                for (int j = 0; j < NP; ++j) {
                     xv[j].x = nrm(xv[j].x, wv[j].x, bv[j].x);
                     xv[j].y = nrm(xv[j].y, wv[j].y, bv[j].y);
                     xv[j].z = nrm(xv[j].z, wv[j].z, bv[j].z);
@@ -779,7 +783,7 @@ __global__ __launch_bounds__(64 * W) void gemv1_kernel(const GemvArgs a) {
             }
             // quantU8 (q8int.go:88-105): a block is 8 pieces in 8 lanes
 #pragma unroll
-            for (int j = 0; j < kRowPieces; ++j) {
+            for (int j = 0; j < NP; ++j) {
                 const int P = j * 64 + lane;
                 const float amax = max8(amax4(xv[j]));
                 const float id = amax != 0.0f ? __fdiv_rn(127.0f, amax) : 0.0f;
@@ -997,33 +1001,53 @@ hipError_t launch_w(hipStream_t st, const GemvArgs &a, int tiles, int W) {
     }
 }
 
-template <int W, int PRO, int EPI>
+template <int W, int NP, int PRO, int EPI>
 hipError_t launch1_one(hipStream_t st, const GemvArgs &a, int tiles) {
     const size_t smem = gemv1_smem(W, PRO, a.nb);
     if (smem > 64 * 1024) {
         static bool raised = false;
         if (!raised) {
             raised = true;
-            (void)hipFuncSetAttribute((const void *)gemv1_kernel<W, PRO, EPI>,
+            (void)hipFuncSetAttribute((const void *)gemv1_kernel<W, NP, PRO, EPI>,
                                       hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
         }
     }
-    gemv1_kernel<W, PRO, EPI><<<tiles, 64 * W, smem, st>>>(a);
+    gemv1_kernel<W, NP, PRO, EPI><<<tiles, 64 * W, smem, st>>>(a);
     return hipGetLastError();
+}
+
+// One-row launches: pre-rounded rows on 1..16 waves; rows rounded in the
+// prologue on 1, 4 or 16 waves with 2, 4 or 5 pieces per lane.
+template <int PRO, int EPI>
+hipError_t launch1(hipStream_t st, const GemvArgs &a, int tiles, int W) {
+    while (W > 1 && W > a.nb) W >>= 1;  // every wave owns a block
+    if constexpr (PRO == GRX_PRO_PREQ) {
+        switch (W) {
+            case 1: return launch1_one<1, 1, PRO, EPI>(st, a, tiles);
+            case 2: return launch1_one<2, 1, PRO, EPI>(st, a, tiles);
+            case 4: return launch1_one<4, 1, PRO, EPI>(st, a, tiles);
+            case 8: return launch1_one<8, 1, PRO, EPI>(st, a, tiles);
+            default: return launch1_one<16, 1, PRO, EPI>(st, a, tiles);
+        }
+    } else {
+        const int pieces = a.nb * GRX_QK / 4;  // float4 pieces of the row
+        const int np = pieces <= 128 ? 2 : pieces <= 256 ? 4 : 5;
+        const int w = W >= 16 ? 16 : W >= 4 ? 4 : 1;
+        auto go = [&](auto np_tag) -> hipError_t {
+            constexpr int NP = decltype(np_tag)::value;
+            if (w == 1) return launch1_one<1, NP, PRO, EPI>(st, a, tiles);
+            if (w == 4) return launch1_one<4, NP, PRO, EPI>(st, a, tiles);
+            return launch1_one<16, NP, PRO, EPI>(st, a, tiles);
+        };
+        if (np == 2) return go(std::integral_constant<int, 2>{});
+        if (np == 4) return go(std::integral_constant<int, 4>{});
+        return go(std::integral_constant<int, 5>{});
+    }
 }
 
 template <int PRO, int EPI>
 hipError_t launch_m(hipStream_t st, int m, const GemvArgs &a, int tiles, int W) {
-    if (m == 1 && gemv1_fits(PRO, a.nb)) {
-        while (W > 1 && W > a.nb) W >>= 1;  // every wave owns a block
-        switch (W) {
-            case 1: return launch1_one<1, PRO, EPI>(st, a, tiles);
-            case 2: return launch1_one<2, PRO, EPI>(st, a, tiles);
-            case 4: return launch1_one<4, PRO, EPI>(st, a, tiles);
-            case 8: return launch1_one<8, PRO, EPI>(st, a, tiles);
-            default: return launch1_one<16, PRO, EPI>(st, a, tiles);
-        }
-    }
+    if (m == 1 && gemv1_fits(PRO, a.nb)) return launch1<PRO, EPI>(st, a, tiles, W);
     switch (m) {
         case 1: return launch_w<1, PRO, EPI>(st, a, tiles, W);
         case 2: return launch_w<2, PRO, EPI>(st, a, tiles, W);
@@ -1209,6 +1233,27 @@ extern "C" grx_status grx_linear_q8(grx_ctx *ctx, float *dst, const float *x, in
                                     const float *bias) {
     if (!w) return grx_fail(GRX_EINVAL, "grx_linear_q8: NULL weight");
     return grx_matmul_q8(ctx, dst, w->rows, x, w->cols, m, w, bias);
+}
+
+namespace {
+__global__ void vec_kernel(int fn, float *__restrict__ y, const float *__restrict__ x, int n) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    const float v = x[i];
+    y[i] = fn == GRX_VEC_EXPF ? grx_expf_go(v) : fn == GRX_VEC_EXP8 ? grx_exp8(v) : grx_gelu_at(v, i, n);
+}
+}  // namespace
+
+extern "C" grx_status grx_vec_dev(grx_ctx *ctx, int fn, float *y, const float *x, int n) {
+    if (!ctx) return grx_fail(GRX_EINVAL, "grx_vec_dev: NULL context");
+    if (fn < GRX_VEC_EXPF || fn > GRX_VEC_GELU) return grx_fail(GRX_EINVAL, "grx_vec_dev: function %d", fn);
+    if (n < 0) return grx_fail(GRX_EINVAL, "grx_vec_dev: n = %d", n);
+    if (n == 0) return GRX_OK;
+    if (!y || !x) return grx_fail(GRX_EINVAL, "grx_vec_dev: NULL buffer");
+    GRX_HIP(hipSetDevice(ctx->device));
+    vec_kernel<<<grx_ceil_div(n, 256), 256, 0, ctx->stream>>>(fn, y, x, n);
+    GRX_LAUNCHED("vec_kernel");
+    return GRX_OK;
 }
 
 extern "C" grx_status grx_block_dots_dev(grx_ctx *ctx, int32_t *s, const int8_t *q, int m, const grx_weight *w) {

@@ -41,10 +41,36 @@ constexpr int kBatchV = 96;  // the same for the cross values' longer chains (on
 
 // Self-attention workgroups are 256 threads; heads of 64 over at most
 // kSmallN positions take the branch-free body, others the general one.
-constexpr int kSmallHd = 64, kSmallN = 256, kSmallKld = kSmallHd + 4;
-// LDS floats of the branch-free body: K rows, V rows, p, chain-major exps,
-// reductions, a dummy slot
-constexpr size_t kSmallLds = (size_t)kSmallN * kSmallKld + (size_t)kSmallN * kSmallHd + 2 * kSmallN + 16 + 4;
+constexpr int kSmallHd = 64, kSmallN = 256, kSmallPld = kSmallHd + 4;
+// LDS floats of the branch-free body: products [kSmallN][kSmallPld] (rows 68
+// floats apart: 16-byte writes of 16 lanes fall in distinct banks), chain-
+// major exps, exps by position, reductions, a dummy slot
+constexpr size_t kSmallLds = (size_t)kSmallN * kSmallPld + 2 * kSmallN + 16 + 4;
+
+// A DPP move within rows of 16 lanes (every lane active).
+template <int CTRL>
+__device__ __forceinline__ float dpp_max_step(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false));
+}
+
+// The largest value of the wave, in every lane (DPP within rows of 16, then
+// the four rows).
+__device__ __forceinline__ float wave_max(float m) {
+    float t = dpp_max_step<0xb1>(m);
+    m = t > m ? t : m;
+    t = dpp_max_step<0x4e>(m);
+    m = t > m ? t : m;
+    t = dpp_max_step<0x141>(m);
+    m = t > m ? t : m;
+    t = dpp_max_step<0x140>(m);
+    m = t > m ? t : m;
+    const float a = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(m), 0));
+    const float b = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(m), 16));
+    const float c = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(m), 32));
+    const float d = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(m), 48));
+    const float ab = b > a ? b : a, cd = d > c ? d : c;
+    return cd > ab ? cd : ab;
+}
 
 // The softmax sums of block_softmax (mathx.go:78-90) for wave 0, from the
 // exps below n8 stored chain-major (chain c = j % 8 at ch[c*cs + j/8],
@@ -101,83 +127,69 @@ __device__ __forceinline__ float softmax_inv(const float *ch, int cs, const floa
 }
 
 // Causal self-attention of one head over n <= kSmallN positions, head_dim
-// 64, without divergent branches: every K and V row through LDS in one batch
-// (K rows 68 floats apart for conflict-free 16-byte reads; rows past n are
-// copies of row n-1 for K and zeros for V), thread j's score, the softmax,
-// then wave 0's lane d sums p_j * v_j[d] in position order (p_j = 0 past n,
-// so the loop runs whole groups of 32).
+// 64, with no divergent branches: thread j holds K and V row j in registers
+// (rows past n repeat row n-1), its score (dotF32Go), the maximum by DPP and
+// one barrier, its exp (chain-major and by position in LDS), every wave's own
+// 1 / sum (softmax_inv), then its products p_j * v_j[d] into LDS (zeros past
+// n); wave 0's lane d sums them in position order (whole groups of 32).
 template <bool QOUT>
 __device__ __forceinline__ void self_attn_small(float *sm, const float *q, const float *kc, const float *vc, int n,
                                                 int st, float sc, float *att, int8_t *att_q, float *att_s) {
-    constexpr int HD = kSmallHd, RC = kSmallN, KLD = kSmallKld;
-    float *kl = sm, *vl = kl + RC * KLD, *p = vl + RC * HD, *ch = p + RC, *red = ch + RC, *dummy = red + 16;
+    constexpr int HD = kSmallHd, RC = kSmallN, PLD = kSmallPld;
+    float *prod = sm, *ch = prod + RC * PLD, *pl = ch + RC, *red = pl + RC, *dummy = red + 16;
     const int h = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const float *kb = kc + h * HD, *vb = vc + h * HD;
-    constexpr int PER = RC * HD / 4 / 256;  // 16-byte pieces per thread per row set
-    float4 kv[PER], vv[PER];
+    const bool live = tid < n;
+    const int j = min(tid, n - 1);
+    const float4 *kr = reinterpret_cast<const float4 *>(kc + (size_t)j * st + h * HD);
+    const float4 *vr = reinterpret_cast<const float4 *>(vc + (size_t)j * st + h * HD);
+    float4 kv[HD / 4], vv[HD / 4];
 #pragma unroll
-    for (int u = 0; u < PER; ++u) {
-        const int i = tid + u * 256;
-        const size_t g = (size_t)min(i >> 4, n - 1) * st + 4 * (i & 15);
-        kv[u] = *reinterpret_cast<const float4 *>(kb + g);
-        vv[u] = *reinterpret_cast<const float4 *>(vb + g);
-    }
+    for (int i = 0; i < HD / 4; ++i) kv[i] = kr[i];
 #pragma unroll
-    for (int u = 0; u < PER; ++u) {
-        const int i = tid + u * 256, r = i >> 4, c4 = i & 15;
-        *reinterpret_cast<float4 *>(kl + r * KLD + 4 * c4) = kv[u];
-        *reinterpret_cast<float4 *>(vl + r * HD + 4 * c4) = r < n ? vv[u] : make_float4(0.f, 0.f, 0.f, 0.f);
-    }
-    __syncthreads();
+    for (int i = 0; i < HD / 4; ++i) vv[i] = vr[i];
     // dotF32Go (gemm.go:294-308): four running sums over the float4 pieces
-    const float *qh = q + h * HD, *kr = kl + tid * KLD;
+    const float4 *qh = reinterpret_cast<const float4 *>(q + h * HD);
     float s0 = 0.f, s1 = 0.f, s2 = 0.f, s3 = 0.f;
 #pragma unroll
-    for (int i = 0; i < HD; i += 4) {
-        const float4 a = *reinterpret_cast<const float4 *>(qh + i);
-        const float4 b = *reinterpret_cast<const float4 *>(kr + i);
+    for (int i = 0; i < HD / 4; ++i) {
+        const float4 a = qh[i], b = kv[i];
         s0 = __fadd_rn(s0, __fmul_rn(a.x, b.x));
         s1 = __fadd_rn(s1, __fmul_rn(a.y, b.y));
         s2 = __fadd_rn(s2, __fmul_rn(a.z, b.z));
         s3 = __fadd_rn(s3, __fmul_rn(a.w, b.w));
     }
     const float score = __fmul_rn(__fadd_rn(__fadd_rn(__fadd_rn(s0, s1), s2), s3), sc);
-    const bool live = tid < n;
-    float mx = live ? score : -__builtin_inff();
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {
-        const float t = __shfl_xor(mx, o);
-        mx = t > mx ? t : mx;
-    }
+    float mx = wave_max(live ? score : -__builtin_inff());
     if (lane == 0) red[wave] = mx;
     __syncthreads();
     mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
     const int n8 = n & ~7;
     const float d = __fsub_rn(score, mx);
-    const float e = tid < n8 ? grx_exp8(d) : grx_expf_go(d);
+    // both forms, then the reference's (EXP8 below n8, expf past it): no branch
+    const float e8 = grx_exp8(d), eg = grx_expf_go(d);
+    const float e = tid < n8 ? e8 : eg;
     *(tid < n8 ? ch + (tid & 7) * (RC / 8) + (tid >> 3) : dummy) = e;
-    *(live ? p + tid : dummy + 1) = e;
+    *(live ? pl + tid : dummy + 1) = e;
     __syncthreads();
-    if (wave == 0) {
-        const float inv = softmax_inv(ch, RC / 8, p + n8, n);
-        if (lane == 0) red[8] = inv;
+    const float inv = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(softmax_inv(ch, RC / 8, pl + n8, n)), 0));
+    const float pj = __fmul_rn(e, inv);
+    float4 *pr = reinterpret_cast<float4 *>(prod + tid * PLD);
+#pragma unroll
+    for (int i = 0; i < HD / 4; ++i) {
+        const float4 v = vv[i];
+        pr[i] = live ? make_float4(__fmul_rn(pj, v.x), __fmul_rn(pj, v.y), __fmul_rn(pj, v.z), __fmul_rn(pj, v.w))
+                     : make_float4(0.f, 0.f, 0.f, 0.f);
     }
-    __syncthreads();
-    p[tid] = live ? __fmul_rn(e, red[8]) : 0.f;
     __syncthreads();
     if (wave == 0) {
         float o = 0.f;
         const int n32 = (n + 31) & ~31;
         for (int j0 = 0; j0 < n32; j0 += 32) {
+            float t[32];
 #pragma unroll
-            for (int g = 0; g < 8; ++g) {
-                const float4 pp = *reinterpret_cast<const float4 *>(p + j0 + 4 * g);
-                const float *vr = vl + (j0 + 4 * g) * HD + lane;
-                o = __fadd_rn(o, __fmul_rn(pp.x, vr[0]));
-                o = __fadd_rn(o, __fmul_rn(pp.y, vr[HD]));
-                o = __fadd_rn(o, __fmul_rn(pp.z, vr[2 * HD]));
-                o = __fadd_rn(o, __fmul_rn(pp.w, vr[3 * HD]));
-            }
+            for (int i = 0; i < 32; ++i) t[i] = prod[(j0 + i) * PLD + lane];
+#pragma unroll
+            for (int i = 0; i < 32; ++i) o = __fadd_rn(o, t[i]);
         }
         att[h * HD + lane] = o;
         if constexpr (QOUT) quant32_store(o, att_q + h * HD + lane, att_s + (h * HD + lane) / 32, lane & 31);
@@ -440,6 +452,143 @@ __global__ __launch_bounds__(512) void cross_values_fast_kernel(const float *__r
             quant32_store(outv[tid], att_q + h * hd + dd, att_s + (h * hd + dd) / 32, tid);
         }
     }
+}
+
+// dotF32Go (gemm.go:294-308) of r < 16 values, x in LDS and y in registers,
+// static indices only: whole groups of four into four running sums, the
+// rest into the first, then ((s0 + s1) + s2) + s3.
+__device__ __forceinline__ float dot_go15_reg(const float *x, const float (&y)[16], int r) {
+    float s0 = 0.f, s1 = 0.f, s2 = 0.f, s3 = 0.f;
+    const int r4 = r & ~3;
+#pragma unroll
+    for (int i = 0; i < 12; i += 4) {
+        const bool ok = i + 4 <= r;
+        const float f0 = __fadd_rn(s0, __fmul_rn(x[i], y[i]));
+        const float f1 = __fadd_rn(s1, __fmul_rn(x[i + 1], y[i + 1]));
+        const float f2 = __fadd_rn(s2, __fmul_rn(x[i + 2], y[i + 2]));
+        const float f3 = __fadd_rn(s3, __fmul_rn(x[i + 3], y[i + 3]));
+        s0 = ok ? f0 : s0;
+        s1 = ok ? f1 : s1;
+        s2 = ok ? f2 : s2;
+        s3 = ok ? f3 : s3;
+    }
+#pragma unroll
+    for (int i = 0; i < 15; ++i) {
+        const float f = __fadd_rn(s0, __fmul_rn(x[i], y[i]));
+        s0 = i >= r4 && i < r ? f : s0;
+    }
+    return __fadd_rn(__fadd_rn(__fadd_rn(s0, s1), s2), s3);
+}
+
+// Cross values for kWaveOut outputs d of one head of one stream, four waves
+// (nctx <= kWaveCtx, head_dim % kWaveOut == 0): the head's softmax
+// (decoder.go:109, block_softmax's order: expSubAVX below nctx &^ 7 with
+// eight lane sums, expSubGo past it, 1 / sum, scale), then, as
+// cross_values_fast_kernel, out[d] = dotF32x4(p, Vt[d]) with 16 lanes per d
+// (lane c runs the chain of steps 16u + c), HSUM, dotF32Go for the tail.
+// Every workgroup of a head redoes its softmax (6 exps per thread; each
+// wave takes 1 / sum itself), so a head's values spread over
+// hd / kWaveOut CUs.  The outputs are left in float32 (the next product
+// rounds them).
+constexpr int kWaveCtx = 1536, kWaveOut = 16;
+
+__global__ __launch_bounds__(256) void cross_values_wave_kernel(const float *__restrict__ scores,
+                                                                const float *__restrict__ cv, int nctx, int hd,
+                                                                int st, size_t x_stream, float *__restrict__ att) {
+    constexpr int NT = 256, PER = kWaveCtx / NT, CS = kWaveCtx / 8 + 4, G = 16, KB = kWaveCtx / 16;
+    constexpr int R = KB + 4;  // row of pt: lane c's steps, 16-byte aligned
+    __shared__ __align__(16) float ch[8 * CS + 8];  // exps below n8, chain-major (+ dummy slots)
+    __shared__ __align__(16) float pt[16 * R];      // p[16u + c] at pt[c * R + u], u < steps
+    __shared__ float tl[16], p2[16], red[4];        // exps past n8; p past 16 * steps
+    const int h = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, sm_ = blockIdx.z;
+    scores += ((size_t)sm_ * (st / hd) + h) * nctx;
+    att += (size_t)sm_ * st;
+    const int dl = tid >> 4, c = tid & 15, d = blockIdx.y * kWaveOut + dl;
+    const int kk = nctx & ~15, steps = kk >> 4, nfull = steps / G, ng = (steps + G - 1) / G;
+    // values: one uniform base, 32-bit offsets
+    const float *__restrict__ vb = cv + sm_ * x_stream + ((size_t)h * hd + blockIdx.y * kWaveOut) * nctx;
+    // every value of this thread's chain in flight before the softmax
+    float vv[KB], vt[16];
+#pragma unroll
+    for (int u = 0; u < KB; ++u) vv[u] = vb[dl * nctx + min(16 * u + c, max(kk - 1, 0))];
+    // the values past 16 * steps (dotF32Go's tail), ahead of need
+#pragma unroll
+    for (int i = 0; i < 16; ++i) vt[i] = vb[dl * nctx + min(kk + i, nctx - 1)];
+    float sv[PER];
+#pragma unroll
+    for (int u = 0; u < PER; ++u) sv[u] = scores[min(tid + NT * u, nctx - 1)];
+    const int n8 = nctx & ~7, jt = n8 + tid;  // threads tid < nctx - n8 take the tail
+    const float st_ = scores[min(jt, nctx - 1)];
+    float mx = sv[0];
+#pragma unroll
+    for (int u = 1; u < PER; ++u) mx = sv[u] > mx ? sv[u] : mx;
+    mx = wave_max(mx);
+    if (lane == 0) red[wave] = mx;
+    __syncthreads();
+    mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    // EXP8 below n8 (branch-free), expf (scalar form) for the tail n8..nctx-1
+    float e[PER];
+    float *dummy = ch + 8 * CS;
+#pragma unroll
+    for (int u = 0; u < PER; ++u) {
+        const int jj = tid + NT * u;
+        e[u] = grx_exp8(__fsub_rn(sv[u], mx));
+        *(jj < n8 ? ch + (jj & 7) * CS + (jj >> 3) : dummy) = e[u];
+    }
+    const bool tail = jt < nctx;
+    const float et = grx_expf_go(__fsub_rn(st_, mx));
+    *(tail ? tl + tid : dummy + 1) = et;
+    __syncthreads();
+    const float inv = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(softmax_inv(ch, CS, tl, nctx)), 0));
+    // p = e * inv: below 16 * steps lane-major, past it in p2
+#pragma unroll
+    for (int u = 0; u < PER; ++u) {
+        const int jj = tid + NT * u;
+        const float pv = __fmul_rn(e[u], inv);
+        *(jj < kk ? pt + (jj & 15) * R + (jj >> 4) : jj < n8 ? p2 + (jj - kk) : dummy + 2) = pv;
+    }
+    *(tail ? p2 + (jt - kk) : dummy + 3) = __fmul_rn(et, inv);
+    __syncthreads();
+    // dot4f32avx's lane chains over whole steps of 16
+    const float4 *pr = reinterpret_cast<const float4 *>(pt + c * R);
+    float acc = 0.f;
+#pragma unroll
+    for (int g = 0; g < KB / G; ++g) {
+        if (g >= ng) break;  // uniform
+        float4 pp[G / 4];
+#pragma unroll
+        for (int i = 0; i < G / 4; ++i) pp[i] = pr[(G / 4) * g + i];
+        if (g < nfull) {
+#pragma unroll
+            for (int i = 0; i < G / 4; ++i) {
+                acc = __fmaf_rn(pp[i].x, vv[G * g + 4 * i], acc);
+                acc = __fmaf_rn(pp[i].y, vv[G * g + 4 * i + 1], acc);
+                acc = __fmaf_rn(pp[i].z, vv[G * g + 4 * i + 2], acc);
+                acc = __fmaf_rn(pp[i].w, vv[G * g + 4 * i + 3], acc);
+            }
+        } else {
+            const int left = steps - G * g;
+#pragma unroll
+            for (int i = 0; i < G / 4; ++i) {
+                float f = __fmaf_rn(pp[i].x, vv[G * g + 4 * i], acc);
+                acc = 4 * i < left ? f : acc;
+                f = __fmaf_rn(pp[i].y, vv[G * g + 4 * i + 1], acc);
+                acc = 4 * i + 1 < left ? f : acc;
+                f = __fmaf_rn(pp[i].z, vv[G * g + 4 * i + 2], acc);
+                acc = 4 * i + 2 < left ? f : acc;
+                f = __fmaf_rn(pp[i].w, vv[G * g + 4 * i + 3], acc);
+                acc = 4 * i + 3 < left ? f : acc;
+            }
+        }
+    }
+    const float other = __shfl_xor(acc, 8, 16);
+    const float S = __fadd_rn(c < 8 ? acc : other, c < 8 ? other : acc);
+    const float h4 = __fadd_rn(S, __shfl_xor(S, 4, 16));
+    const float h01 = __fadd_rn(h4, __shfl_xor(h4, 1, 16));
+    const float h23 = __shfl_xor(h01, 2, 16);
+    float o = kk > 0 ? __fadd_rn(h01, h23) : 0.f;
+    if (kk < nctx) o = __fadd_rn(o, dot_go15_reg(p2, vt, nctx - kk));
+    if (c == 0) att[h * hd + d] = o;
 }
 
 // cross K (scaled) [h][t][d] and V [h][d][t] from K, V [t][h*hd+d]
@@ -733,7 +882,7 @@ grx_status enqueue_step(grx_whisper *m, hipStream_t stream) {
             self_attn_kernel<false><<<dim3(nh, S), kAttnThreads, attn_smem, stream>>>(
                 m->q, L.self_k, L.self_v, m->pos, st, hd, sc, rc, kv_stream, m->att, nullptr, nullptr);
         GRX_LAUNCHED("self_attn_kernel");
-        auto out_proj = [&](grx_weight *w, const float *b) {  // x += att . W^T + b
+        auto out_proj = [&](grx_weight *w, const float *b, bool rounded) {  // x += att . W^T + b
             GemvArgs a = gemv_args(w);
             a.x = m->att;
             a.lda = st;
@@ -744,9 +893,9 @@ grx_status enqueue_step(grx_whisper *m, hipStream_t stream) {
             a.bias = b;
             a.resid = m->x;
             a.ldr = st;
-            return grx_gemv_launch(stream, S, qatt ? GRX_PRO_PREQ : GRX_PRO_QUANT, GRX_EPI_RESID, a, 0);
+            return grx_gemv_launch(stream, S, rounded ? GRX_PRO_PREQ : GRX_PRO_QUANT, GRX_EPI_RESID, a, 0);
         };
-        if ((s = out_proj(L.o, L.o_b)) != GRX_OK) return s;
+        if ((s = out_proj(L.o, L.o_b, qatt)) != GRX_OK) return s;
         {  // LN -> cross query
             GemvArgs a = gemv_args(L.xq);
             a.x = m->x;
@@ -763,7 +912,12 @@ grx_status enqueue_step(grx_whisper *m, hipStream_t stream) {
         cross_scores_kernel<<<dim3(nh, grx_ceil_div(nctx, 64), S), 64, 0, stream>>>(
             m->q, L.cross_k, nctx, hd, st, x_stream, m->scores);
         GRX_LAUNCHED("cross_scores_kernel");
-        if (nctx <= kFastCtx && hd % 4 == 0) {
+        // one stream: workgroups over 16 outputs each, float32 out
+        const bool wave_values = S == 1 && nctx <= kWaveCtx && hd % kWaveOut == 0;
+        if (wave_values) {
+            cross_values_wave_kernel<<<dim3(nh, hd / kWaveOut, S), 256, 0, stream>>>(m->scores, L.cross_v, nctx,
+                                                                                     hd, st, x_stream, m->att);
+        } else if (nctx <= kFastCtx && hd % 4 == 0) {
             if (qatt)
                 cross_values_fast_kernel<true><<<dim3(nh, grx_ceil_div(hd, 32), S), 512, 0, stream>>>(
                     m->scores, L.cross_v, nctx, hd, st, x_stream, m->att, m->att_q, m->att_s);
@@ -778,7 +932,7 @@ grx_status enqueue_step(grx_whisper *m, hipStream_t stream) {
                 m->scores, L.cross_v, nctx, hd, dg, st, x_stream, m->att, nullptr, nullptr);
         }
         GRX_LAUNCHED("cross_values_kernel");
-        if ((s = out_proj(L.xo, L.xo_b)) != GRX_OK) return s;
+        if ((s = out_proj(L.xo, L.xo_b, qatt && !wave_values)) != GRX_OK) return s;
         {  // LN -> fc1 -> GELU, rounded to Q8_0 for fc2
             GemvArgs a = gemv_args(L.fc1);
             a.x = m->x;

@@ -188,6 +188,15 @@ def block_dots_dev(s, q, m: int, w: Weight, ctx: Context | None = None) -> None:
     _lib.call("grx_block_dots_dev", ctx.handle, _ptr(s), _ptr(q), m, w.handle)
 
 
+# the elementwise float kernels of grx_vec_dev
+VEC_EXPF, VEC_EXP8, VEC_GELU = 0, 1, 2
+
+
+def vec_dev(fn: int, y, x, n: int, ctx: Context | None = None) -> None:
+    ctx = ctx or default_context()
+    _lib.call("grx_vec_dev", ctx.handle, fn, _ptr(y), _ptr(x), n)
+
+
 __all__ = ["QK", "Q8Bytes", "F32", "F16", "Q8_0", "Context", "default_context", "device_count", "Weight",
            "NewQ8", "ToQ8", "MatMul", "Linear", "matmul_dev", "quant_act_dev", "matmul_prequant_dev",
-           "block_dots_dev", "GrxError"]
+           "block_dots_dev", "vec_dev", "VEC_EXPF", "VEC_EXP8", "VEC_GELU", "GrxError"]

@@ -121,6 +121,15 @@ grx_status grx_matmul_q8_prequant_dev(grx_ctx *ctx, float *dst, int ldc, const i
  * minus the 128*sum(w) offset), device pointers.  For parity checks. */
 grx_status grx_block_dots_dev(grx_ctx *ctx, int32_t *s, const int8_t *q, int m,
                               const grx_weight *w);
+/* The elementwise float kernels of the path on n values, device pointers
+ * (y may equal x), exactly as the decode and encode kernels evaluate them.
+ * For parity checks:
+ *   GRX_VEC_EXPF  expf, the scalar form (whisper/mathx.go:7-33)
+ *   GRX_VEC_EXP8  EXP8, one lane of the vector form (kernels_amd64.s:236-258)
+ *   GRX_VEC_GELU  geluVec over the n values (kernels_amd64.go:119-129: the
+ *                 assembly form below n &^ 7, gelu (mathx.go:36-52) past it) */
+enum { GRX_VEC_EXPF = 0, GRX_VEC_EXP8 = 1, GRX_VEC_GELU = 2 };
+grx_status grx_vec_dev(grx_ctx *ctx, int fn, float *y, const float *x, int n);
 
 /* ---- whisper-shaped text decoder with Q8_0 weights ---- */
 

@@ -23,6 +23,15 @@ def _bits_equal(a, b):
     return a.shape == b.shape and np.array_equal(a.view(np.uint32), b.view(np.uint32))
 
 
+def _bits_equal_nan(a, b):
+    """Bit-equal, except that a NaN matches any NaN (the sign and payload of
+    a NaN made from non-NaN operands differ between x86 and gfx950)."""
+    a = np.ascontiguousarray(a, np.float32)
+    b = np.ascontiguousarray(b, np.float32)
+    na, nb = np.isnan(a), np.isnan(b)
+    return a.shape == b.shape and np.array_equal(na, nb) and np.array_equal(a[~na].view(np.uint32), b[~nb].view(np.uint32))
+
+
 def _report(got, want):
     d = np.abs(got.astype(np.float64) - want)
     i = int(np.argmax(d))
@@ -116,6 +125,41 @@ def test_block_dots_exact(kern, orc, dev):
     kern.block_dots_dev(ds, dqa, m, w)
     kern.default_context().sync()
     assert np.array_equal(ds.download(np.int32, (m, n, k // QK)), orc.block_dots(qa, w8, n, k))
+
+
+def test_float_kernels_bit_exact(kern, orc, dev):
+    """expf (scalar form), EXP8 and geluVec as the decode and encode kernels
+    evaluate them (branch-free), bit-identical to the oracle: a dense sweep
+    of the ranges the softmax and GELU reach, the cut-offs at -87 / 88 and
+    +-9 (GELU's tanh), NaN and infinities, and geluVec's scalar tail."""
+    rng = np.random.default_rng(5)
+    x = np.concatenate([
+        np.linspace(-100.0, 100.0, 20001, dtype=np.float32),
+        rng.standard_normal(4000).astype(np.float32) * 30,
+        np.array([-87.0, np.nextafter(np.float32(-87.0), np.float32(0)), np.nextafter(np.float32(-87.0), np.float32(-100)),
+                  88.0, np.nextafter(np.float32(88.0), np.float32(0)), np.nextafter(np.float32(88.0), np.float32(100)),
+                  0.0, -0.0, 1e-30, -1e-30, np.inf, -np.inf, np.nan], np.float32),
+    ]).astype(np.float32)
+    dx = dev.DeviceBuffer.from_array(x)
+    dy = dev.DeviceBuffer(x.size * 4)
+    for fn, want in ((kern.VEC_EXPF, np.array([orc.expf(float(v)) for v in x], np.float32)),
+                     (kern.VEC_EXP8, np.array([orc.exp8(float(v)) for v in x], np.float32))):
+        kern.vec_dev(fn, dy, dx, x.size)
+        kern.default_context().sync()
+        got = dy.download(np.float32, (x.size,))
+        assert _bits_equal_nan(got, want), f"function {fn}: " + _report(got, want)
+    # geluVec: |2u| crosses the +-9 cut-off near |v| = 3.3; lengths leave a
+    # scalar tail of 0..7 values
+    g = np.concatenate([np.linspace(-12.0, 12.0, 4801, dtype=np.float32),
+                        np.array([np.inf, -np.inf, np.nan, 0.0, -0.0], np.float32)])
+    for n in (g.size, g.size - 3, 7, 1):
+        gx = np.ascontiguousarray(g[:n])
+        dg = dev.DeviceBuffer.from_array(gx)
+        kern.vec_dev(kern.VEC_GELU, dg, dg, n)
+        kern.default_context().sync()
+        got = dg.download(np.float32, (n,))
+        want = orc.gelu(gx)
+        assert _bits_equal_nan(got, want), f"gelu n={n}: " + _report(got, want)
 
 
 # ---------------------------------------------------------------- products
