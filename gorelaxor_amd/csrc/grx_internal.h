@@ -212,7 +212,9 @@ enum {
     GRX_EPI_QKV = 3,     // rows split in three: q, then K and V caches at *pos
     GRX_EPI_ARGMAX = 4,  // y = c (optional) and the first index of the maximum
     GRX_EPI_GELU_Q = 5,  // y = geluVec(c), and y rounded to Q8_0 into yq/ys
-    GRX_EPI_QKV_ROPE = 6 // as QKV, with q and k rotated by the cos/sin table at pos
+    GRX_EPI_QKV_ROPE = 6, // as QKV, with q and k rotated by the cos/sin table at pos
+    GRX_EPI_XSCORES = 7   // one row, tile = one head of 64: the head's cross-attention
+                          // scores over a run of 64 keys (blockIdx.y) instead of y
 };
 
 struct GemvArgs {
@@ -270,6 +272,10 @@ struct GemvArgs {
     // ARGMAX with key slots: each workgroup writes its rows' best keys to
     // keys[tile][M] and a one-workgroup kernel ends the step (no counter)
     unsigned long long *keys;
+    // XSCORES: pre-scaled cross keys [heads][nctx][64], scores [heads][nctx]
+    const float *xk;
+    int nctx;
+    float *scores;
 };
 
 grx_status grx_gemv_launch(hipStream_t st, int m, int pro, int epi, const GemvArgs &a,

@@ -584,6 +584,9 @@ __device__ __forceinline__ uint32_t quant4(const float4 &v, float id) {
 constexpr int kRowPieces = 5;
 // Blocks whose weight loads a one-row product issues before its prologue.
 constexpr int kPrefetch = 4;
+// Row stride (floats) of the key rows staged for XSCORES: 16-byte reads of
+// a row per lane land in distinct banks.
+constexpr int kKeyLd = 68;
 
 // The product of ONE activation row (decode steps): q8_gemv's tile scheme
 // with the latency of a single row in mind.
@@ -610,12 +613,13 @@ __global__ __launch_bounds__(64 * W) void gemv1_kernel(const GemvArgs a) {
     // the rounded row in LDS when the prologue builds it; pre-rounded rows
     // are read from HBM by each wave (a copy to LDS measured slower)
     constexpr bool LQ = !PQ;
-    // LDS: [lxq K int8][lxs nb f32][lp nb*64 f32 if W > 1]
+    // LDS: [lxq K int8][lxs nb f32][lp nb*64 f32 if W > 1][lk 64*kKeyLd f32 if XSCORES]
     const size_t o_xs = LQ ? (size_t)K : 0;
     const size_t o_p = o_xs + (LQ ? (((size_t)nb * 4 + 15) & ~(size_t)15) : 0);
     int8_t *lxq = reinterpret_cast<int8_t *>(smem);
     float *lxs = reinterpret_cast<float *>(smem + o_xs);
     float *lp = reinterpret_cast<float *>(smem + o_p);
+    float *lk = reinterpret_cast<float *>(smem + o_p + (W > 1 ? (size_t)nb * 64 * 4 : 0));
 
     const int b0 = (wave * nb) / W, b1 = ((wave + 1) * nb) / W;
     const int4 *__restrict__ wq = reinterpret_cast<const int4 *>(a.qs) + (size_t)tile * nb * 128;
@@ -656,6 +660,21 @@ __global__ __launch_bounds__(64 * W) void gemv1_kernel(const GemvArgs a) {
         if constexpr (EPI == GRX_EPI_RESID) resid = a.resid[row];
     }
 
+    if constexpr (EPI == GRX_EPI_XSCORES) {
+        // waves 1..4 stage the 64 key rows of this run (rows past nctx
+        // repeat the last), kKeyLd floats apart, while wave 0 builds the row
+        static_assert(W >= 5, "XSCORES stages keys with waves 1..4");
+        if (wave >= 1 && wave <= 4) {
+            const float4 *kb = reinterpret_cast<const float4 *>(a.xk + (size_t)tile * a.nctx * 64);
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const int piece = (wave - 1) * 256 + u * 64 + lane;  // 16 pieces per key row
+                const int r = piece >> 4, c4 = piece & 15;
+                const int key = min((int)blockIdx.y * 64 + r, a.nctx - 1);
+                reinterpret_cast<float4 *>(lk + r * kKeyLd)[c4] = kb[(size_t)key * 16 + c4];
+            }
+        }
+    }
     // ---- prologue (wave 0): the activation row, rounded to Q8_0, into LDS
     if constexpr (!PQ) {
         if (wave == 0) {
@@ -868,7 +887,50 @@ __global__ __launch_bounds__(64 * W) void gemv1_kernel(const GemvArgs a) {
     }
 
     // ---- epilogue (wave 0)
-    if constexpr (EPI == GRX_EPI_RESID) {
+    if constexpr (EPI == GRX_EPI_XSCORES) {
+        // cross scores (whisper/decoder.go:94-108) of key j = 64*run + lane:
+        // dotF32x4 (dot4f32avx, kernels_amd64.s:156-204) for keys in whole
+        // groups of four, dotF32Go for the rest; q (this tile's 64 outputs)
+        // broadcast from the lanes
+        const int key = (int)blockIdx.y * 64 + lane;
+        const float4 *kr = reinterpret_cast<const float4 *>(lk + lane * kKeyLd);
+        float A[8], B[8], s0 = 0.f, s1 = 0.f, s2 = 0.f, s3 = 0.f;
+#pragma unroll
+        for (int l = 0; l < 8; ++l) A[l] = B[l] = 0.f;
+#pragma unroll
+        for (int c = 0; c < 64; c += 16) {
+            float kv[16];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const float4 t = kr[c / 4 + i];
+                kv[4 * i] = t.x;
+                kv[4 * i + 1] = t.y;
+                kv[4 * i + 2] = t.z;
+                kv[4 * i + 3] = t.w;
+            }
+#pragma unroll
+            for (int l = 0; l < 16; ++l) {
+                const float qd = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(acc), c + l));
+                if (l < 8)
+                    A[l] = __fmaf_rn(qd, kv[l], A[l]);
+                else
+                    B[l - 8] = __fmaf_rn(qd, kv[l], B[l - 8]);
+                const float pr = __fmul_rn(qd, kv[l]);
+                if ((l & 3) == 0) s0 = __fadd_rn(s0, pr);
+                if ((l & 3) == 1) s1 = __fadd_rn(s1, pr);
+                if ((l & 3) == 2) s2 = __fadd_rn(s2, pr);
+                if ((l & 3) == 3) s3 = __fadd_rn(s3, pr);
+            }
+        }
+        float S[8];
+#pragma unroll
+        for (int l = 0; l < 8; ++l) S[l] = __fadd_rn(A[l], B[l]);
+        const float h0 = __fadd_rn(S[0], S[4]), h1 = __fadd_rn(S[1], S[5]);
+        const float h2 = __fadd_rn(S[2], S[6]), h3 = __fadd_rn(S[3], S[7]);
+        const float x4 = __fadd_rn(__fadd_rn(h0, h1), __fadd_rn(h2, h3));
+        const float go = __fadd_rn(__fadd_rn(__fadd_rn(s0, s1), s2), s3);
+        if (key < a.nctx) a.scores[(size_t)tile * a.nctx + key] = key < (a.nctx & ~3) ? x4 : go;
+    } else if constexpr (EPI == GRX_EPI_RESID) {
         if (row < a.rows) a.y[row] = __fadd_rn(resid, acc);
     } else if constexpr (EPI == GRX_EPI_STORE) {
         if (row < a.rows) a.y[row] = acc;
@@ -886,10 +948,11 @@ bool gemv1_fits(int pro, int nb) {
     return pro == GRX_PRO_PREQ || nb * GRX_QK <= kRowPieces * 256;
 }
 
-size_t gemv1_smem(int W, int pro, int nb) {
+size_t gemv1_smem(int W, int pro, int nb, int epi = GRX_EPI_STORE) {
     size_t n = 0;
     if (pro != GRX_PRO_PREQ) n += (size_t)nb * GRX_QK + (((size_t)nb * 4 + 15) & ~(size_t)15);
     if (W > 1) n += (size_t)nb * 64 * 4;
+    if (epi == GRX_EPI_XSCORES) n += (size_t)64 * kKeyLd * 4;
     return n;
 }
 
@@ -1003,7 +1066,7 @@ hipError_t launch_w(hipStream_t st, const GemvArgs &a, int tiles, int W) {
 
 template <int W, int NP, int PRO, int EPI>
 hipError_t launch1_one(hipStream_t st, const GemvArgs &a, int tiles) {
-    const size_t smem = gemv1_smem(W, PRO, a.nb);
+    const size_t smem = gemv1_smem(W, PRO, a.nb, EPI);
     if (smem > 64 * 1024) {
         static bool raised = false;
         if (!raised) {
@@ -1012,7 +1075,8 @@ hipError_t launch1_one(hipStream_t st, const GemvArgs &a, int tiles) {
                                       hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
         }
     }
-    gemv1_kernel<W, NP, PRO, EPI><<<tiles, 64 * W, smem, st>>>(a);
+    const dim3 grid(tiles, EPI == GRX_EPI_XSCORES ? grx_ceil_div(a.nctx, 64) : 1);
+    gemv1_kernel<W, NP, PRO, EPI><<<grid, 64 * W, smem, st>>>(a);
     return hipGetLastError();
 }
 
@@ -1035,9 +1099,13 @@ hipError_t launch1(hipStream_t st, const GemvArgs &a, int tiles, int W) {
         const int w = W >= 16 ? 16 : W >= 4 ? 4 : 1;
         auto go = [&](auto np_tag) -> hipError_t {
             constexpr int NP = decltype(np_tag)::value;
-            if (w == 1) return launch1_one<1, NP, PRO, EPI>(st, a, tiles);
-            if (w == 4) return launch1_one<4, NP, PRO, EPI>(st, a, tiles);
-            return launch1_one<16, NP, PRO, EPI>(st, a, tiles);
+            if constexpr (EPI == GRX_EPI_XSCORES) {
+                return launch1_one<16, NP, PRO, EPI>(st, a, tiles);
+            } else {
+                if (w == 1) return launch1_one<1, NP, PRO, EPI>(st, a, tiles);
+                if (w == 4) return launch1_one<4, NP, PRO, EPI>(st, a, tiles);
+                return launch1_one<16, NP, PRO, EPI>(st, a, tiles);
+            }
         };
         if (np == 2) return go(std::integral_constant<int, 2>{});
         if (np == 4) return go(std::integral_constant<int, 4>{});
@@ -1088,6 +1156,12 @@ grx_status grx_gemv_launch(hipStream_t st, int m, int pro, int epi, const GemvAr
     else if (pro == GRX_PRO_LN && epi == GRX_EPI_QKV) e = launch_m<GRX_PRO_LN, GRX_EPI_QKV>(st, m, a, tiles, W);
     else if (pro == GRX_PRO_LN && epi == GRX_EPI_ARGMAX) e = launch_m<GRX_PRO_LN, GRX_EPI_ARGMAX>(st, m, a, tiles, W);
     else if (pro == GRX_PRO_LN && epi == GRX_EPI_GELU_Q) e = launch_m<GRX_PRO_LN, GRX_EPI_GELU_Q>(st, m, a, tiles, W);
+    else if (pro == GRX_PRO_LN && epi == GRX_EPI_XSCORES) {
+        // one row, 64-row tiles = heads of 64, 16 waves (keys staged by waves 1..4)
+        if (m != 1 || a.nb < 16 || !gemv1_fits(pro, a.nb))
+            return grx_fail(GRX_EINVAL, "grx: cross scores epilogue needs one row of 512..1280 values");
+        e = launch1<GRX_PRO_LN, GRX_EPI_XSCORES>(st, a, tiles, 16);
+    }
     else if (pro == GRX_PRO_EMBED_LN && epi == GRX_EPI_QKV) e = launch_m<GRX_PRO_EMBED_LN, GRX_EPI_QKV>(st, m, a, tiles, W);
     else if (pro == GRX_PRO_PREQ && epi == GRX_EPI_RESID) e = launch_m<GRX_PRO_PREQ, GRX_EPI_RESID>(st, m, a, tiles, W);
     else if (pro == GRX_PRO_PREQ && epi == GRX_EPI_QKV) e = launch_m<GRX_PRO_PREQ, GRX_EPI_QKV>(st, m, a, tiles, W);

@@ -799,6 +799,12 @@ GemvArgs gemv_args(const grx_weight *w) {
     return a;
 }
 
+// An environment switch set to "0" (for comparisons in tests).
+bool getenv_off(const char *name) {
+    const char *f = getenv(name);
+    return f && f[0] == '0';
+}
+
 // The launches of one decode step on stream st.
 grx_status enqueue_step(grx_whisper *m, hipStream_t stream) {
     const grx_whisper_hparams &hp = m->hp;
@@ -896,7 +902,21 @@ grx_status enqueue_step(grx_whisper *m, hipStream_t stream) {
             return grx_gemv_launch(stream, S, rounded ? GRX_PRO_PREQ : GRX_PRO_QUANT, GRX_EPI_RESID, a, 0);
         };
         if ((s = out_proj(L.o, L.o_b, qatt)) != GRX_OK) return s;
-        {  // LN -> cross query
+        // one stream, heads of 64: the cross query's tile of each head is
+        // computed inside the scores kernel (one launch instead of two)
+        const bool fused_scores = S == 1 && hd == 64 && st >= 512 && st <= 1280 && !getenv_off("GRX_FUSE_XSCORES");
+        if (fused_scores) {
+            GemvArgs a = gemv_args(L.xq);
+            a.x = m->x;
+            a.lda = st;
+            a.ln_w = L.x_ln_w;
+            a.ln_b = L.x_ln_b;
+            a.bias = L.xq_b;
+            a.xk = L.cross_k;
+            a.nctx = nctx;
+            a.scores = m->scores;
+            if ((s = grx_gemv_launch(stream, 1, GRX_PRO_LN, GRX_EPI_XSCORES, a, 16)) != GRX_OK) return s;
+        } else {  // LN -> cross query
             GemvArgs a = gemv_args(L.xq);
             a.x = m->x;
             a.lda = st;
@@ -908,10 +928,10 @@ grx_status enqueue_step(grx_whisper *m, hipStream_t stream) {
             if (sep && (s = ln_rows(L.x_ln_w, L.x_ln_b, a)) != GRX_OK) return s;
             if ((s = grx_gemv_launch(stream, S, sep ? GRX_PRO_PREQ : GRX_PRO_LN, GRX_EPI_STORE, a, 0)) != GRX_OK)
                 return s;
+            cross_scores_kernel<<<dim3(nh, grx_ceil_div(nctx, 64), S), 64, 0, stream>>>(
+                m->q, L.cross_k, nctx, hd, st, x_stream, m->scores);
+            GRX_LAUNCHED("cross_scores_kernel");
         }
-        cross_scores_kernel<<<dim3(nh, grx_ceil_div(nctx, 64), S), 64, 0, stream>>>(
-            m->q, L.cross_k, nctx, hd, st, x_stream, m->scores);
-        GRX_LAUNCHED("cross_scores_kernel");
         // one stream: workgroups over 16 outputs each, float32 out
         const bool wave_values = S == 1 && nctx <= kWaveCtx && hd % kWaveOut == 0;
         if (wave_values) {

@@ -30,18 +30,26 @@ def _same(a, b):
 
 
 @pytest.mark.parametrize("gemv1", ["1", "0"])
-@pytest.mark.parametrize("shape", ["tiny", "ragged"])
+@pytest.mark.parametrize("shape", ["tiny", "ragged", "wide"])
 def test_decode_logits_bit_exact(kern, orc, shape, gemv1):
     """Every step's logits bit-identical, with the one-row decode kernel
-    (GRX_GEMV1=1, the default) and with the general product kernel."""
+    (GRX_GEMV1=1, the default) and with the general product kernel.  The
+    wide shape (d 512, heads of 64) takes the cross query inside the scores
+    kernel (GRX_FUSE_XSCORES=0 turns that off with the general kernel); its
+    101 audio positions leave a partial last run of keys and three keys on
+    dotF32Go's route."""
     hp = dict(WHISPER_TINY_TEST)
     if shape == "ragged":  # audio length not a multiple of 16, odd head count
         hp.update(n_audio_ctx=101, n_head=4, n_state=96, n_vocab=333)
+    if shape == "wide":
+        hp.update(n_audio_ctx=101, n_head=8, n_state=512, n_vocab=333)
     os.environ["GRX_GEMV1"] = gemv1
+    os.environ["GRX_FUSE_XSCORES"] = gemv1
     try:
         _decode_logits_bit_exact(orc, hp)
     finally:
         del os.environ["GRX_GEMV1"]
+        del os.environ["GRX_FUSE_XSCORES"]
 
 
 def _decode_logits_bit_exact(orc, hp):
