@@ -35,9 +35,10 @@ constexpr int BU = GRX_GEMV_BU;  // blocks whose loads are issued before any is 
 // kRound, each round's partial products through LDS, and wave m folds row
 // m after every round (so LDS holds one round, not every block).
 constexpr int kRound = 16;
-// Pre-rounded activations of several rows up to this many bytes are copied
-// to LDS; multi-row products may take up to kMultiLds bytes of LDS.
-constexpr size_t kStageMax = 40960;
+// Pre-rounded activations of several rows (at most this many bytes: the
+// host splits larger products into fewer rows) are copied to LDS;
+// multi-row products may take up to kMultiLds bytes of LDS.
+constexpr size_t kStageMax = 65536;
 constexpr size_t kMultiLds = 128 * 1024;
 
 // Weight loads are non-temporal: each weight byte is read once per product,
@@ -114,12 +115,239 @@ __device__ __forceinline__ void quant_into_lds(const float *src, int ld, int nb,
     }
 }
 
+// ---------------------------------------------------------------- one row
+
+// Cross-lane moves within rows of 16 lanes (DPP; every lane active): the
+// quad permutations [1,0,3,2] and [2,3,0,1], the mirror of each 8 and of
+// each 16 lanes.  Sums and maxima built from them hold the same value in
+// every lane of the group (a + b == b + a).
+constexpr int kDppXor1 = 0xb1, kDppXor2 = 0x4e, kDppHalfMirror = 0x141, kDppMirror = 0x140;
+
+template <int CTRL>
+__device__ __forceinline__ float dpp_f32(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false));
+}
+template <int CTRL>
+__device__ __forceinline__ double dpp_f64(double v) {
+    const unsigned long long u = (unsigned long long)__double_as_longlong(v);
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)u, CTRL, 0xf, 0xf, false);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)(u >> 32), CTRL, 0xf, 0xf, false);
+    return __longlong_as_double((long long)(((unsigned long long)hi << 32) | lo));
+}
+__device__ __forceinline__ double readlane_f64(double v, int l) {
+    const unsigned long long u = (unsigned long long)__double_as_longlong(v);
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)u, l);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(u >> 32), l);
+    return __longlong_as_double((long long)(((unsigned long long)hi << 32) | lo));
+}
+// The wave's float64 sum, the same in every lane: rows of 16 by DPP, then
+// (row0 + row1) + (row2 + row3).
+__device__ __forceinline__ double wave_sum_f64(double v) {
+    v = __dadd_rn(v, dpp_f64<kDppXor1>(v));
+    v = __dadd_rn(v, dpp_f64<kDppXor2>(v));
+    v = __dadd_rn(v, dpp_f64<kDppHalfMirror>(v));
+    v = __dadd_rn(v, dpp_f64<kDppMirror>(v));
+    return __dadd_rn(__dadd_rn(readlane_f64(v, 0), readlane_f64(v, 16)),
+                     __dadd_rn(readlane_f64(v, 32), readlane_f64(v, 48)));
+}
+// The largest of each 8 lanes' values (a Q8_0 block held as 8 float4s).
+__device__ __forceinline__ float max8(float m) {
+    float t = dpp_f32<kDppXor1>(m);
+    m = t > m ? t : m;
+    t = dpp_f32<kDppXor2>(m);
+    m = t > m ? t : m;
+    t = dpp_f32<kDppHalfMirror>(m);
+    return t > m ? t : m;
+}
+__device__ __forceinline__ float amax4(const float4 &v) {
+    float m = fabsf(v.x);
+    m = m > 0.0f ? m : 0.0f;
+    float t = fabsf(v.y);
+    m = t > m ? t : m;
+    t = fabsf(v.z);
+    m = t > m ? t : m;
+    t = fabsf(v.w);
+    return t > m ? t : m;
+}
+__device__ __forceinline__ uint32_t quant4(const float4 &v, float id) {
+    auto q = [&](float x) {
+        float r = rintf(__fmul_rn(x, id));
+        r = fminf(fmaxf(r, -128.0f), 127.0f);
+        return (uint32_t)(uint8_t)(int8_t)(int)r;
+    };
+    return q(v.x) | q(v.y) << 8 | q(v.z) << 16 | q(v.w) << 24;
+}
+
+// Widest row a one-row product rounds in its prologue: NP pieces of 4
+// values per lane held in registers (NP = 2, 4 or 5: up to 512, 1024 or
+// 1280 values).
+constexpr int kRowPieces = 5;
+// Blocks whose weight loads a one-row product issues before its prologue.
+constexpr int kPrefetch = 4;
+// Row stride (floats) of the key rows staged for XSCORES: 16-byte reads of
+// a row per lane land in distinct banks.
+constexpr int kKeyLd = 68;
+
+// Activation row m of a product, built by ONE wave (every lane active) and
+// rounded to Q8_0 into LDS (lxq [.][K], lxs [.][nb]): the row as NP float4
+// pieces per lane (piece P = 64 j + lane, K <= 256 NP), then by PRO
+//   QUANT     quantU8 of x row m (q8int.go:88-105)
+//   LN        layerNorm (internal/kern/mathx.go:55-75), then quantU8
+//   EMBED_LN  the whisper embedding row (tok[m] at the position), stored to
+//             x_out row m by tile 0, then as LN
+//   LN64      layerNorm of pockettts/nn.go:27-49, then quantU8
+// with cross-lane DPP sums (float64) and maxima: no workgroup barrier.
+// after_loads() runs once the row's loads are issued (the caller's own
+// loads go there).
+template <int NP, int PRO, typename After>
+__device__ __forceinline__ void wave_row_prologue(const GemvArgs &a, int m, int8_t *lxq, float *lxs, int lane,
+                                                  int tile, After after_loads) {
+    const int nb = a.nb, K = nb * GRX_QK;
+    const int npc = K / 4;  // float4 pieces
+    float4 xv[NP], wv[NP], bv[NP];
+    const float4 *x4 = reinterpret_cast<const float4 *>(a.x + (size_t)m * a.lda);
+#pragma unroll
+    for (int j = 0; j < NP; ++j) {
+        const int P = min(j * 64 + lane, npc - 1);
+        if constexpr (PRO == GRX_PRO_EMBED_LN) {
+            // tokEmb.row(tok) + decPos[pos] (whisper/decoder.go:42-46):
+            // the embedding row from its tile layout, d*q then + pos
+            const int t = a.tok[m], p = *a.pos + a.pos_add + (a.streams ? 0 : m);
+            const int etile = t >> 6, elane = t & 63, i = 4 * P;
+            const int b = i >> 5, h = (i >> 4) & 1, e = i & 15;
+            const uint32_t q4 = *reinterpret_cast<const uint32_t *>(
+                a.emb_qs + (((size_t)etile * nb + b) * 2 + h) * 1024 + elane * 16 + e);
+            const float d = grx_f16_to_f32(a.emb_ds[((size_t)etile * nb + b) * 64 + elane]);
+            const float4 pe = reinterpret_cast<const float4 *>(a.pos_emb + (size_t)p * K)[P];
+            xv[j].x = __fadd_rn(__fmul_rn((float)(int8_t)(q4 & 0xff), d), pe.x);
+            xv[j].y = __fadd_rn(__fmul_rn((float)(int8_t)((q4 >> 8) & 0xff), d), pe.y);
+            xv[j].z = __fadd_rn(__fmul_rn((float)(int8_t)((q4 >> 16) & 0xff), d), pe.z);
+            xv[j].w = __fadd_rn(__fmul_rn((float)(int8_t)(q4 >> 24), d), pe.w);
+        } else {
+            xv[j] = x4[P];
+        }
+        if constexpr (PRO == GRX_PRO_LN || PRO == GRX_PRO_EMBED_LN || PRO == GRX_PRO_LN64) {
+            if (PRO != GRX_PRO_LN64 || a.ln_w != nullptr) {
+                wv[j] = reinterpret_cast<const float4 *>(a.ln_w)[P];
+                bv[j] = reinterpret_cast<const float4 *>(a.ln_b)[P];
+            }
+        }
+    }
+    // loads issued behind this row's (they complete in order): waiting for
+    // the row does not wait for them
+    after_loads();
+    if constexpr (PRO == GRX_PRO_EMBED_LN) {
+        if (tile == 0) {
+#pragma unroll
+            for (int j = 0; j < NP; ++j)
+                if (j * 64 + lane < npc) reinterpret_cast<float4 *>(a.x_out + (size_t)m * a.lda)[j * 64 + lane] = xv[j];
+        }
+    }
+    if constexpr (PRO == GRX_PRO_LN || PRO == GRX_PRO_EMBED_LN) {
+        // layerNorm (internal/kern/mathx.go:55-75): float64 sums,
+        // mean and inv rounded to float32, y = (v-mean)*inv*w + b
+        double ps = 0.0;
+#pragma unroll
+        for (int j = 0; j < NP; ++j) {
+            if (j * 64 + lane < npc) {
+                ps = __dadd_rn(ps, (double)xv[j].x);
+                ps = __dadd_rn(ps, (double)xv[j].y);
+                ps = __dadd_rn(ps, (double)xv[j].z);
+                ps = __dadd_rn(ps, (double)xv[j].w);
+            }
+        }
+        const float mean = (float)(wave_sum_f64(ps) / (double)K);
+        double pv = 0.0;
+        auto sq = [&](float v) {
+            const double d = (double)__fsub_rn(v, mean);
+            pv = __dadd_rn(pv, __dmul_rn(d, d));
+        };
+#pragma unroll
+        for (int j = 0; j < NP; ++j) {
+            if (j * 64 + lane < npc) {
+                sq(xv[j].x);
+                sq(xv[j].y);
+                sq(xv[j].z);
+                sq(xv[j].w);
+            }
+        }
+        const double vs = wave_sum_f64(pv);
+        const float inv = (float)(1.0 / sqrt(vs / (double)K + 1e-5));
+        auto nrm = [&](float v, float w, float b) {
+            float t = __fsub_rn(v, mean);
+            t = __fmul_rn(t, inv);
+            t = __fmul_rn(t, w);
+            return __fadd_rn(t, b);
+        };
+#pragma unroll
+        for (int j = 0; j < NP; ++j) {
+            xv[j].x = nrm(xv[j].x, wv[j].x, bv[j].x);
+            xv[j].y = nrm(xv[j].y, wv[j].y, bv[j].y);
+            xv[j].z = nrm(xv[j].z, wv[j].z, bv[j].z);
+            xv[j].w = nrm(xv[j].w, wv[j].w, bv[j].w);
+        }
+    } else if constexpr (PRO == GRX_PRO_LN64) {
+        // layerNorm of pockettts/nn.go:27-49: statistics and the
+        // normalized value in float64, gain and bias in float32
+        double ps = 0.0;
+#pragma unroll
+        for (int j = 0; j < NP; ++j) {
+            if (j * 64 + lane < npc) {
+                ps = __dadd_rn(ps, (double)xv[j].x);
+                ps = __dadd_rn(ps, (double)xv[j].y);
+                ps = __dadd_rn(ps, (double)xv[j].z);
+                ps = __dadd_rn(ps, (double)xv[j].w);
+            }
+        }
+        const double mean = wave_sum_f64(ps) / (double)K;
+        double pv = 0.0;
+        auto sq = [&](float v) {
+            const double d = __dsub_rn((double)v, mean);
+            pv = __dadd_rn(pv, __dmul_rn(d, d));
+        };
+#pragma unroll
+        for (int j = 0; j < NP; ++j) {
+            if (j * 64 + lane < npc) {
+                sq(xv[j].x);
+                sq(xv[j].y);
+                sq(xv[j].z);
+                sq(xv[j].w);
+            }
+        }
+        const double inv = 1.0 / sqrt(wave_sum_f64(pv) / (double)K + a.ln_eps);
+        const bool gb = a.ln_w != nullptr;
+        auto nrm = [&](float v, float w, float b) {
+            float o = (float)__dmul_rn(__dsub_rn((double)v, mean), inv);
+            return gb ? __fadd_rn(__fmul_rn(o, w), b) : o;
+        };
+#pragma unroll
+        for (int j = 0; j < NP; ++j) {
+            xv[j].x = nrm(xv[j].x, wv[j].x, bv[j].x);
+            xv[j].y = nrm(xv[j].y, wv[j].y, bv[j].y);
+            xv[j].z = nrm(xv[j].z, wv[j].z, bv[j].z);
+            xv[j].w = nrm(xv[j].w, wv[j].w, bv[j].w);
+        }
+    }
+    // quantU8 (q8int.go:88-105): a block is 8 pieces in 8 lanes
+#pragma unroll
+    for (int j = 0; j < NP; ++j) {
+        const int P = j * 64 + lane;
+        const float amax = max8(amax4(xv[j]));
+        const float id = amax != 0.0f ? __fdiv_rn(127.0f, amax) : 0.0f;
+        const uint32_t q = quant4(xv[j], id);
+        if (P < npc) {
+            reinterpret_cast<uint32_t *>(lxq + (size_t)m * K)[P] = q;
+            if ((lane & 7) == 0) lxs[m * nb + (P >> 3)] = __fmul_rn(amax, grx_bits_f32(0x3c010204u));
+        }
+    }
+}
+
 // The products' epilogues: row m of the tile's 64 outputs (acc[m] in lane
 // `lane`) is ended by wave 0, or by wave m % W when rows were folded round
 // by round (RND).
 template <int M, int W, bool RND, int EPI>
 __device__ __forceinline__ void gemv_epilogue(const GemvArgs &a, const float (&acc)[M], int row, int lane,
-                                              int wave) {
+                                              int wave, int pos0) {
     auto mine = [&](int m) { return !RND || m % W == wave; };
     if constexpr (EPI == GRX_EPI_ARGMAX) {
 #pragma unroll
@@ -228,7 +456,7 @@ __device__ __forceinline__ void gemv_epilogue(const GemvArgs &a, const float (&a
             const float c = acc[m];
             const float other = __shfl_xor(c, 1);
             if (row >= a.rows) continue;
-            const int pos = *a.pos + a.pos_add + m;
+            const int pos = pos0 + a.pos_add + m;
             if (row < 2 * a.seg) {
                 const int j = row % a.seg, hd = 2 * a.rope_half;
                 const int i = (j % hd) >> 1;
@@ -267,7 +495,7 @@ __device__ __forceinline__ void gemv_epilogue(const GemvArgs &a, const float (&a
         } else if constexpr (EPI == GRX_EPI_QKV) {
             // one stream: rows are positions pos.., caches [pos][seg];
             // streams: row m at pos in stream m's cache (kv_stream floats on)
-            const int pos = *a.pos + a.pos_add + (a.streams ? 0 : m);
+            const int pos = pos0 + a.pos_add + (a.streams ? 0 : m);
             const size_t so = a.streams ? (size_t)m * a.kv_stream : 0;
             if (row < a.seg)
                 a.y[(size_t)m * a.ldc + row] = c;
@@ -289,6 +517,7 @@ __global__ __launch_bounds__(64 * W) void gemv_q8_kernel(const GemvArgs a) {
     const int tile = blockIdx.x;
     const int nb = a.nb, K = nb * GRX_QK;
     const int row = tile * 64 + lane;
+    const int pos0 = (EPI == GRX_EPI_QKV || EPI == GRX_EPI_QKV_ROPE) ? *a.pos : 0;
 
     // LDS, each region 16-byte aligned (gemv_smem):
     //   [lxq M*K int8][lxs M*nb f32][lp M*(nb or kRound)*64 f32 if W>1, and
@@ -297,7 +526,9 @@ __global__ __launch_bounds__(64 * W) void gemv_q8_kernel(const GemvArgs a) {
     // activations in LDS: rounded here, or (several rows, up to kStageMax
     // bytes of them) copied from HBM; several pre-rounded rows keep their
     // scales in LDS either way
-    const bool LQ = PRO != GRX_PRO_PREQ || (M > 1 && (size_t)M * K <= kStageMax);
+    // compile-time, so the activation reads are LDS reads, not flat ones
+    // (the host keeps M * K within kStageMax for pre-rounded rows)
+    constexpr bool LQ = PRO != GRX_PRO_PREQ || M > 1;
     constexpr bool LS = PRO != GRX_PRO_PREQ || M > 1;
     const size_t o_xs = LQ ? (size_t)M * K : 0;
     const size_t o_p = o_xs + (LS ? (((size_t)M * nb * 4 + 15) & ~(size_t)15) : 0);
@@ -324,7 +555,16 @@ __global__ __launch_bounds__(64 * W) void gemv_q8_kernel(const GemvArgs a) {
         for (int i = tid; i < M * nb; i += 64 * W) lxs[i] = a.xs[i];
         __syncthreads();
     }
-    if constexpr (PRO == GRX_PRO_QUANT) {
+    // several rows of up to 1280 values and a wave for each: wave m builds
+    // row m with the one-wave prologue (no workgroup reductions)
+    constexpr bool WROW = PRO != GRX_PRO_PREQ && M > 1 && W >= M;
+    const bool wrow = WROW && K <= kRowPieces * 256;
+    if (wrow) {
+        if constexpr (WROW) {
+            if (wave < M) wave_row_prologue<kRowPieces, PRO>(a, wave, lxq, lxs, lane, tile, [] {});
+            __syncthreads();
+        }
+    } else if constexpr (PRO == GRX_PRO_QUANT) {
         quant_into_lds<M>(a.x, a.lda, nb, lxq, lxs, tid, 64 * W);
         __syncthreads();
     } else if constexpr (PRO == GRX_PRO_LN || PRO == GRX_PRO_EMBED_LN) {
@@ -469,28 +709,77 @@ __global__ __launch_bounds__(64 * W) void gemv_q8_kernel(const GemvArgs a) {
     };
     if constexpr (RND) {
         // rounds of kRound blocks, kRound / W per wave; wave w folds the rows
-        // m = w, w + W, ... over the round in block order
+        // m = w, w + W, ... over the round in block order.  The next round's
+        // weights are loaded before this round's products and fold.
         constexpr int BR = kRound / W > 0 ? kRound / W : 1;
         constexpr int R = BR * W;
         const float bv = (a.bias != nullptr && row < a.rows) ? a.bias[row] : 0.0f;
 #pragma unroll
         for (int m = 0; m < M; ++m) acc[m] = bv;
-        for (int r0 = 0; r0 < nb; r0 += R) {
-            const int bs = r0 + wave * BR, be = min(bs + BR, nb);
-            if (be - bs == BR)
-                run(std::integral_constant<int, BR>{}, bs, r0, R);
-            else
-                for (int b = bs; b < be; ++b) run(std::integral_constant<int, 1>{}, b, r0, R);
+        int4 wa[2 * BR], wb[2 * BR];
+        uint32_t da[BR], db[BR];
+        // this wave's blocks of the round at r0 (past nb: the last block again)
+        auto ld = [&](int4 *w, uint32_t *dh, int r0) {
+#pragma unroll
+            for (int u = 0; u < BR; ++u) {
+                const int b = min(r0 + wave * BR + u, nb - 1);
+                if (a.cacheable) {
+                    w[2 * u] = wq[(size_t)b * 128 + lane];
+                    w[2 * u + 1] = wq[(size_t)b * 128 + 64 + lane];
+                    dh[u] = wd[(size_t)b * 64 + lane];
+                } else {
+                    w[2 * u] = wload(wq + (size_t)b * 128 + lane);
+                    w[2 * u + 1] = wload(wq + (size_t)b * 128 + 64 + lane);
+                    dh[u] = wload(wd + (size_t)b * 64 + lane);
+                }
+            }
+        };
+        auto round = [&](const int4 *w, const uint32_t *dh, int r0) {
+#pragma unroll
+            for (int u = 0; u < BR; ++u) {
+                const int b = r0 + wave * BR + u;
+                if (b < nb) {  // uniform
+                    const float dw = grx_f16_to_f32((uint16_t)dh[u]);
+#pragma unroll
+                    for (int m = 0; m < M; ++m) {
+                        int4 a0, a1;
+                        act(m, b, a0, a1);
+                        const int sd = sdot8(w[2 * u], w[2 * u + 1], a0, a1);
+                        lp[((size_t)m * R + (b - r0)) * 64 + lane] = __fmul_rn((float)sd, dw);
+                    }
+                }
+            }
             __syncthreads();
             const int re = min(r0 + R, nb);
 #pragma unroll
             for (int m = 0; m < M; ++m) {
                 if (m % W != wave) continue;  // uniform across the wave
-#pragma unroll 4
-                for (int b = r0; b < re; ++b)
-                    acc[m] = __fmaf_rn(lp[((size_t)m * R + (b - r0)) * 64 + lane], act_scale(m, b), acc[m]);
+                if (re - r0 == R) {
+                    float t[R], sc[R];
+#pragma unroll
+                    for (int k = 0; k < R; ++k) {
+                        t[k] = lp[((size_t)m * R + k) * 64 + lane];
+                        sc[k] = act_scale(m, r0 + k);
+                    }
+#pragma unroll
+                    for (int k = 0; k < R; ++k) acc[m] = __fmaf_rn(t[k], sc[k], acc[m]);
+                } else {
+                    for (int b = r0; b < re; ++b)
+                        acc[m] = __fmaf_rn(lp[((size_t)m * R + (b - r0)) * 64 + lane], act_scale(m, b), acc[m]);
+                }
             }
             __syncthreads();
+        };
+        // loads are issued unconditionally (past nb they repeat the last
+        // block): the number in flight is then fixed, so waiting for one
+        // round's weights never waits for the next round's
+        ld(wa, da, 0);
+        for (int r0 = 0; r0 < nb; r0 += 2 * R) {
+            ld(wb, db, r0 + R);
+            round(wa, da, r0);
+            if (r0 + R >= nb) break;
+            ld(wa, da, r0 + 2 * R);
+            round(wb, db, r0 + R);
         }
     } else {
         int bb = b0;
@@ -512,81 +801,8 @@ __global__ __launch_bounds__(64 * W) void gemv_q8_kernel(const GemvArgs a) {
 
     // ---- epilogue: row m is ended by wave 0 (one wave, or after the fold
     // above), or by wave m % W when rows were folded round by round
-    gemv_epilogue<M, W, RND, EPI>(a, acc, row, lane, wave);
+    gemv_epilogue<M, W, RND, EPI>(a, acc, row, lane, wave, pos0);
 }
-
-// ---------------------------------------------------------------- one row
-
-// Cross-lane moves within rows of 16 lanes (DPP; every lane active): the
-// quad permutations [1,0,3,2] and [2,3,0,1], the mirror of each 8 and of
-// each 16 lanes.  Sums and maxima built from them hold the same value in
-// every lane of the group (a + b == b + a).
-constexpr int kDppXor1 = 0xb1, kDppXor2 = 0x4e, kDppHalfMirror = 0x141, kDppMirror = 0x140;
-
-template <int CTRL>
-__device__ __forceinline__ float dpp_f32(float v) {
-    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false));
-}
-template <int CTRL>
-__device__ __forceinline__ double dpp_f64(double v) {
-    const unsigned long long u = (unsigned long long)__double_as_longlong(v);
-    const uint32_t lo = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)u, CTRL, 0xf, 0xf, false);
-    const uint32_t hi = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)(u >> 32), CTRL, 0xf, 0xf, false);
-    return __longlong_as_double((long long)(((unsigned long long)hi << 32) | lo));
-}
-__device__ __forceinline__ double readlane_f64(double v, int l) {
-    const unsigned long long u = (unsigned long long)__double_as_longlong(v);
-    const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)u, l);
-    const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(u >> 32), l);
-    return __longlong_as_double((long long)(((unsigned long long)hi << 32) | lo));
-}
-// The wave's float64 sum, the same in every lane: rows of 16 by DPP, then
-// (row0 + row1) + (row2 + row3).
-__device__ __forceinline__ double wave_sum_f64(double v) {
-    v = __dadd_rn(v, dpp_f64<kDppXor1>(v));
-    v = __dadd_rn(v, dpp_f64<kDppXor2>(v));
-    v = __dadd_rn(v, dpp_f64<kDppHalfMirror>(v));
-    v = __dadd_rn(v, dpp_f64<kDppMirror>(v));
-    return __dadd_rn(__dadd_rn(readlane_f64(v, 0), readlane_f64(v, 16)),
-                     __dadd_rn(readlane_f64(v, 32), readlane_f64(v, 48)));
-}
-// The largest of each 8 lanes' values (a Q8_0 block held as 8 float4s).
-__device__ __forceinline__ float max8(float m) {
-    float t = dpp_f32<kDppXor1>(m);
-    m = t > m ? t : m;
-    t = dpp_f32<kDppXor2>(m);
-    m = t > m ? t : m;
-    t = dpp_f32<kDppHalfMirror>(m);
-    return t > m ? t : m;
-}
-__device__ __forceinline__ float amax4(const float4 &v) {
-    float m = fabsf(v.x);
-    m = m > 0.0f ? m : 0.0f;
-    float t = fabsf(v.y);
-    m = t > m ? t : m;
-    t = fabsf(v.z);
-    m = t > m ? t : m;
-    t = fabsf(v.w);
-    return t > m ? t : m;
-}
-__device__ __forceinline__ uint32_t quant4(const float4 &v, float id) {
-    auto q = [&](float x) {
-        float r = rintf(__fmul_rn(x, id));
-        r = fminf(fmaxf(r, -128.0f), 127.0f);
-        return (uint32_t)(uint8_t)(int8_t)(int)r;
-    };
-    return q(v.x) | q(v.y) << 8 | q(v.z) << 16 | q(v.w) << 24;
-}
-
-// Widest row a one-row product rounds in its prologue: NP pieces of 4
-// values per lane held in registers (NP = 2, 4 or 5: up to 512, 1024 or
-// 1280 values).
-constexpr int kRowPieces = 5;
-// Blocks whose weight loads a one-row product issues before its prologue.
-constexpr int kPrefetch = 4;
-// Row stride (floats) of the key rows staged for XSCORES: 16-byte reads of
-// a row per lane land in distinct banks.
-constexpr int kKeyLd = 68;
 
 // The product of ONE activation row (decode steps): q8_gemv's tile scheme
 // with the latency of a single row in mind.
@@ -648,17 +864,23 @@ __global__ __launch_bounds__(64 * W) void gemv1_kernel(const GemvArgs a) {
     int4 pw[2 * (PF > 0 ? PF : 1)];
     uint32_t pd[PF > 0 ? PF : 1];
     const int npf = PF > 0 ? min(PF, b1 - b0) : 0;
-    if constexpr (PF > 0) {
-        const int nl = npf <= 2 ? npf : PF;
+    auto prefetch = [&] {
+        if constexpr (PF > 0) {
+            const int nl = npf <= 2 ? npf : PF;
 #pragma unroll
-        for (int u = 0; u < PF; ++u)
-            if (u < nl) load_block(b0 + min(u, npf - 1), pw[2 * u], pw[2 * u + 1], pd[u]);
-    }
+            for (int u = 0; u < PF; ++u)
+                if (u < nl) load_block(b0 + min(u, npf - 1), pw[2 * u], pw[2 * u + 1], pd[u]);
+        }
+    };
+    // wave 0 issues them behind its prologue's loads (below)
+    if (PQ || wave != 0) prefetch();
     float bias = 0.0f, resid = 0.0f;
     if (wave == 0 && row < a.rows) {
         if (a.bias != nullptr) bias = a.bias[row];
         if constexpr (EPI == GRX_EPI_RESID) resid = a.resid[row];
     }
+    // the cache position of the QKV epilogues, read now rather than at the end
+    const int pos0 = (EPI == GRX_EPI_QKV || EPI == GRX_EPI_QKV_ROPE) ? *a.pos : 0;
 
     if constexpr (EPI == GRX_EPI_XSCORES) {
         // waves 1..4 stage the 64 key rows of this run (rows past nctx
@@ -677,142 +899,7 @@ __global__ __launch_bounds__(64 * W) void gemv1_kernel(const GemvArgs a) {
     }
     // ---- prologue (wave 0): the activation row, rounded to Q8_0, into LDS
     if constexpr (!PQ) {
-        if (wave == 0) {
-            const int npc = K / 4;  // float4 pieces
-            float4 xv[NP], wv[NP], bv[NP];
-            const float4 *x4 = reinterpret_cast<const float4 *>(a.x);
-#pragma unroll
-            for (int j = 0; j < NP; ++j) {
-                const int P = min(j * 64 + lane, npc - 1);
-                if constexpr (PRO == GRX_PRO_EMBED_LN) {
-                    // tokEmb.row(tok) + decPos[pos] (whisper/decoder.go:42-46):
-                    // the embedding row from its tile layout, d*q then + pos
-                    const int t = a.tok[0], p = *a.pos + a.pos_add;
-                    const int etile = t >> 6, elane = t & 63, i = 4 * P;
-                    const int b = i >> 5, h = (i >> 4) & 1, e = i & 15;
-                    const uint32_t q4 = *reinterpret_cast<const uint32_t *>(
-                        a.emb_qs + (((size_t)etile * nb + b) * 2 + h) * 1024 + elane * 16 + e);
-                    const float d = grx_f16_to_f32(a.emb_ds[((size_t)etile * nb + b) * 64 + elane]);
-                    const float4 pe = reinterpret_cast<const float4 *>(a.pos_emb + (size_t)p * K)[P];
-                    xv[j].x = __fadd_rn(__fmul_rn((float)(int8_t)(q4 & 0xff), d), pe.x);
-                    xv[j].y = __fadd_rn(__fmul_rn((float)(int8_t)((q4 >> 8) & 0xff), d), pe.y);
-                    xv[j].z = __fadd_rn(__fmul_rn((float)(int8_t)((q4 >> 16) & 0xff), d), pe.z);
-                    xv[j].w = __fadd_rn(__fmul_rn((float)(int8_t)(q4 >> 24), d), pe.w);
-                } else {
-                    xv[j] = x4[P];
-                }
-                if constexpr (PRO == GRX_PRO_LN || PRO == GRX_PRO_EMBED_LN || PRO == GRX_PRO_LN64) {
-                    if (PRO != GRX_PRO_LN64 || a.ln_w != nullptr) {
-                        wv[j] = reinterpret_cast<const float4 *>(a.ln_w)[P];
-                        bv[j] = reinterpret_cast<const float4 *>(a.ln_b)[P];
-                    }
-                }
-            }
-            if constexpr (PRO == GRX_PRO_EMBED_LN) {
-                if (tile == 0) {
-#pragma unroll
-                    for (int j = 0; j < NP; ++j)
-                        if (j * 64 + lane < npc) reinterpret_cast<float4 *>(a.x_out)[j * 64 + lane] = xv[j];
-                }
-            }
-            if constexpr (PRO == GRX_PRO_LN || PRO == GRX_PRO_EMBED_LN) {
-                // layerNorm (internal/kern/mathx.go:55-75): float64 sums,
-                // mean and inv rounded to float32, y = (v-mean)*inv*w + b
-                double ps = 0.0;
-#pragma unroll
-                for (int j = 0; j < NP; ++j) {
-                    if (j * 64 + lane < npc) {
-                        ps = __dadd_rn(ps, (double)xv[j].x);
-                        ps = __dadd_rn(ps, (double)xv[j].y);
-                        ps = __dadd_rn(ps, (double)xv[j].z);
-                        ps = __dadd_rn(ps, (double)xv[j].w);
-                    }
-                }
-                const float mean = (float)(wave_sum_f64(ps) / (double)K);
-                double pv = 0.0;
-                auto sq = [&](float v) {
-                    const double d = (double)__fsub_rn(v, mean);
-                    pv = __dadd_rn(pv, __dmul_rn(d, d));
-                };
-#pragma unroll
-                for (int j = 0; j < NP; ++j) {
-                    if (j * 64 + lane < npc) {
-                        sq(xv[j].x);
-                        sq(xv[j].y);
-                        sq(xv[j].z);
-                        sq(xv[j].w);
-                    }
-                }
-                const double vs = wave_sum_f64(pv);
-                const float inv = (float)(1.0 / sqrt(vs / (double)K + 1e-5));
-                auto nrm = [&](float v, float w, float b) {
-                    float t = __fsub_rn(v, mean);
-                    t = __fmul_rn(t, inv);
-                    t = __fmul_rn(t, w);
-                    return __fadd_rn(t, b);
-                };
-#pragma unroll
-                for (int j = 0; j < NP; ++j) {
-                    xv[j].x = nrm(xv[j].x, wv[j].x, bv[j].x);
-                    xv[j].y = nrm(xv[j].y, wv[j].y, bv[j].y);
-                    xv[j].z = nrm(xv[j].z, wv[j].z, bv[j].z);
-                    xv[j].w = nrm(xv[j].w, wv[j].w, bv[j].w);
-                }
-            } else if constexpr (PRO == GRX_PRO_LN64) {
-                // layerNorm of pockettts/nn.go:27-49: statistics and the
-                // normalized value in float64, gain and bias in float32
-                double ps = 0.0;
-#pragma unroll
-                for (int j = 0; j < NP; ++j) {
-                    if (j * 64 + lane < npc) {
-                        ps = __dadd_rn(ps, (double)xv[j].x);
-                        ps = __dadd_rn(ps, (double)xv[j].y);
-                        ps = __dadd_rn(ps, (double)xv[j].z);
-                        ps = __dadd_rn(ps, (double)xv[j].w);
-                    }
-                }
-                const double mean = wave_sum_f64(ps) / (double)K;
-                double pv = 0.0;
-                auto sq = [&](float v) {
-                    const double d = __dsub_rn((double)v, mean);
-                    pv = __dadd_rn(pv, __dmul_rn(d, d));
-                };
-#pragma unroll
-                for (int j = 0; j < NP; ++j) {
-                    if (j * 64 + lane < npc) {
-                        sq(xv[j].x);
-                        sq(xv[j].y);
-                        sq(xv[j].z);
-                        sq(xv[j].w);
-                    }
-                }
-                const double inv = 1.0 / sqrt(wave_sum_f64(pv) / (double)K + a.ln_eps);
-                const bool gb = a.ln_w != nullptr;
-                auto nrm = [&](float v, float w, float b) {
-                    float o = (float)__dmul_rn(__dsub_rn((double)v, mean), inv);
-                    return gb ? __fadd_rn(__fmul_rn(o, w), b) : o;
-                };
-#pragma unroll
-                for (int j = 0; j < NP; ++j) {
-                    xv[j].x = nrm(xv[j].x, wv[j].x, bv[j].x);
-                    xv[j].y = nrm(xv[j].y, wv[j].y, bv[j].y);
-                    xv[j].z = nrm(xv[j].z, wv[j].z, bv[j].z);
-                    xv[j].w = nrm(xv[j].w, wv[j].w, bv[j].w);
-                }
-            }
-            // quantU8 (q8int.go:88-105): a block is 8 pieces in 8 lanes
-#pragma unroll
-            for (int j = 0; j < NP; ++j) {
-                const int P = j * 64 + lane;
-                const float amax = max8(amax4(xv[j]));
-                const float id = amax != 0.0f ? __fdiv_rn(127.0f, amax) : 0.0f;
-                const uint32_t q = quant4(xv[j], id);
-                if (P < npc) {
-                    reinterpret_cast<uint32_t *>(lxq)[P] = q;
-                    if ((lane & 7) == 0) lxs[P >> 3] = __fmul_rn(amax, grx_bits_f32(0x3c010204u));
-                }
-            }
-        }
+        if (wave == 0) wave_row_prologue<NP, PRO>(a, 0, lxq, lxs, lane, tile, prefetch);
         __syncthreads();
     }
 
@@ -936,7 +1023,7 @@ __global__ __launch_bounds__(64 * W) void gemv1_kernel(const GemvArgs a) {
         if (row < a.rows) a.y[row] = acc;
     } else {
         const float accm[1] = {acc};
-        gemv_epilogue<1, W, false, EPI>(a, accm, row, lane, wave);
+        gemv_epilogue<1, W, false, EPI>(a, accm, row, lane, wave, pos0);
     }
 }
 
@@ -1029,7 +1116,7 @@ __global__ void block_dots_kernel(const int8_t *__restrict__ qs, int rows, int n
 size_t gemv_smem(int M, int W, int pro, int nb) {
     const size_t K = (size_t)nb * GRX_QK;
     size_t n = 0;
-    if (pro != GRX_PRO_PREQ || (M > 1 && (size_t)M * K <= kStageMax)) n += M * K;
+    if (pro != GRX_PRO_PREQ || M > 1) n += M * K;
     if (pro != GRX_PRO_PREQ || M > 1) n += ((size_t)M * nb * 4 + 15) & ~(size_t)15;
     const size_t n_p = W > 1 ? (size_t)M * (M > 1 ? kRound : nb) * 64 * 4 : 0;
     const size_t n_f = pro >= GRX_PRO_LN ? (size_t)M * K * 4 : 0;
@@ -1146,6 +1233,9 @@ int grx_gemv_pick_waves(int tiles, int nb, int m, int pro) {
 grx_status grx_gemv_launch(hipStream_t st, int m, int pro, int epi, const GemvArgs &a, int waves) {
     const int tiles = grx_ceil_div(a.rows, 64);
     if (tiles == 0 || m == 0) return GRX_OK;
+    if (m > 1 && pro == GRX_PRO_PREQ && (size_t)m * a.nb * GRX_QK > kStageMax)
+        return grx_fail(GRX_ESIZE, "grx: %d pre-rounded rows of %d values exceed %zu bytes of LDS", m,
+                        a.nb * GRX_QK, kStageMax);
     const int W = waves > 0 ? waves : grx_gemv_pick_waves(tiles, a.nb, m, pro);
     hipError_t e = hipErrorInvalidValue;
     if (pro == GRX_PRO_PREQ && epi == GRX_EPI_STORE) e = launch_m<GRX_PRO_PREQ, GRX_EPI_STORE>(st, m, a, tiles, W);
@@ -1208,7 +1298,8 @@ static grx_status gemv_rows_preq(hipStream_t st, float *dst, int ldc, const int8
     int i = 0;
     while (i < m) {
         const int left = m - i;
-        const int mm = left >= 8 ? 8 : left >= 4 ? 4 : left >= 2 ? 2 : 1;
+        int mm = left >= 8 ? 8 : left >= 4 ? 4 : left >= 2 ? 2 : 1;
+        while (mm > 1 && (size_t)mm * K > kStageMax) mm >>= 1;  // rows staged in LDS
         GemvArgs a = {};
         a.qs = w->qs;
         a.ds = w->ds;

@@ -128,25 +128,19 @@ __device__ __forceinline__ float softmax_inv(const float *ch, int cs, const floa
 
 // Causal self-attention of one head over n <= kSmallN positions, head_dim
 // 64, with no divergent branches: thread j holds K and V row j in registers
-// (rows past n repeat row n-1), its score (dotF32Go), the maximum by DPP and
+// (rows past n repeat row n-1 and are never used), its score (dotF32Go),
+// the maximum by DPP and
 // one barrier, its exp (chain-major and by position in LDS), every wave's own
 // 1 / sum (softmax_inv), then its products p_j * v_j[d] into LDS (zeros past
 // n); wave 0's lane d sums them in position order (whole groups of 32).
 template <bool QOUT>
-__device__ __forceinline__ void self_attn_small(float *sm, const float *q, const float *kc, const float *vc, int n,
-                                                int st, float sc, float *att, int8_t *att_q, float *att_s) {
+__device__ __forceinline__ void self_attn_small(float *sm, const float *q, const float4 (&kv)[kSmallHd / 4],
+                                                const float4 (&vv)[kSmallHd / 4], int n, float sc, float *att,
+                                                int8_t *att_q, float *att_s) {
     constexpr int HD = kSmallHd, RC = kSmallN, PLD = kSmallPld;
     float *prod = sm, *ch = prod + RC * PLD, *pl = ch + RC, *red = pl + RC, *dummy = red + 16;
     const int h = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const bool live = tid < n;
-    const int j = min(tid, n - 1);
-    const float4 *kr = reinterpret_cast<const float4 *>(kc + (size_t)j * st + h * HD);
-    const float4 *vr = reinterpret_cast<const float4 *>(vc + (size_t)j * st + h * HD);
-    float4 kv[HD / 4], vv[HD / 4];
-#pragma unroll
-    for (int i = 0; i < HD / 4; ++i) kv[i] = kr[i];
-#pragma unroll
-    for (int i = 0; i < HD / 4; ++i) vv[i] = vr[i];
     // dotF32Go (gemm.go:294-308): four running sums over the float4 pieces
     const float4 *qh = reinterpret_cast<const float4 *>(q + h * HD);
     float s0 = 0.f, s1 = 0.f, s2 = 0.f, s3 = 0.f;
@@ -207,12 +201,23 @@ template <bool QOUT>
 __global__ __launch_bounds__(kAttnThreads) void self_attn_kernel(
     const float *__restrict__ q, const float *__restrict__ kc, const float *__restrict__ vc,
     const int *__restrict__ pos, int st, int hd, float sc, int rc, size_t kv_stream, float *__restrict__ att,
-    int8_t *__restrict__ att_q, float *__restrict__ att_s) {
+    int8_t *__restrict__ att_q, float *__restrict__ att_s, int ctx_rows) {
     extern __shared__ __align__(16) float sm[];
-    const int h = blockIdx.x, n = *pos + 1, tid = threadIdx.x, sm_ = blockIdx.y;  // head, stream
+    const int h = blockIdx.x, tid = threadIdx.x, sm_ = blockIdx.y;  // head, stream
+    const int n = *pos + 1;
     if (hd == kSmallHd && n <= kSmallN) {
-        self_attn_small<QOUT>(sm, q + (size_t)sm_ * st, kc + sm_ * kv_stream, vc + sm_ * kv_stream, n, st, sc,
-                              att + (size_t)sm_ * st, QOUT ? att_q + (size_t)sm_ * st : nullptr,
+        // thread j's K and V row j (rows past n repeat row n-1: loading
+        // rows past the position measured slower than waiting for it)
+        const int j = min(min(tid, n - 1), ctx_rows - 1);
+        const float4 *kr = reinterpret_cast<const float4 *>(kc + sm_ * kv_stream + (size_t)j * st + h * kSmallHd);
+        const float4 *vr = reinterpret_cast<const float4 *>(vc + sm_ * kv_stream + (size_t)j * st + h * kSmallHd);
+        float4 kv[kSmallHd / 4], vv[kSmallHd / 4];
+#pragma unroll
+        for (int i = 0; i < kSmallHd / 4; ++i) kv[i] = kr[i];
+#pragma unroll
+        for (int i = 0; i < kSmallHd / 4; ++i) vv[i] = vr[i];
+        self_attn_small<QOUT>(sm, q + (size_t)sm_ * st, kv, vv, n, sc, att + (size_t)sm_ * st,
+                              QOUT ? att_q + (size_t)sm_ * st : nullptr,
                               QOUT ? att_s + (size_t)sm_ * (st / 32) : nullptr);
         return;
     }
@@ -837,10 +842,11 @@ grx_status enqueue_step(grx_whisper *m, hipStream_t stream) {
         a.hist_stream = hp.n_text_ctx;
         return a;
     };
-    // Several streams: each LayerNorm'd row is rounded once by its own
-    // workgroup and the product reads it pre-rounded (the fused prologue
-    // would redo the rows in every workgroup of the product).
-    const bool sep = S > 1;
+    // Several streams: the product's prologue builds each stream's row with
+    // one wave per row (rows up to 1280 values); wider rows are LayerNorm'd
+    // and rounded once by a row kernel and read pre-rounded
+    // (GRX_FUSE_LN=0 takes that route for every width).
+    const bool sep = S > 1 && (st > 1280 || getenv_off("GRX_FUSE_LN"));
     auto ln_rows = [&](const float *w, const float *b, GemvArgs &a) {
         a.xq = m->ln_q;
         a.xs = m->ln_s;
@@ -883,10 +889,10 @@ grx_status enqueue_step(grx_whisper *m, hipStream_t stream) {
         }
         if (qatt)
             self_attn_kernel<true><<<dim3(nh, S), kAttnThreads, attn_smem, stream>>>(
-                m->q, L.self_k, L.self_v, m->pos, st, hd, sc, rc, kv_stream, m->att, m->att_q, m->att_s);
+                m->q, L.self_k, L.self_v, m->pos, st, hd, sc, rc, kv_stream, m->att, m->att_q, m->att_s, hp.n_text_ctx);
         else
             self_attn_kernel<false><<<dim3(nh, S), kAttnThreads, attn_smem, stream>>>(
-                m->q, L.self_k, L.self_v, m->pos, st, hd, sc, rc, kv_stream, m->att, nullptr, nullptr);
+                m->q, L.self_k, L.self_v, m->pos, st, hd, sc, rc, kv_stream, m->att, nullptr, nullptr, hp.n_text_ctx);
         GRX_LAUNCHED("self_attn_kernel");
         auto out_proj = [&](grx_weight *w, const float *b, bool rounded) {  // x += att . W^T + b
             GemvArgs a = gemv_args(w);

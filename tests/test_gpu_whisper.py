@@ -132,10 +132,21 @@ def _streams(hp, t, n, seed):
     return dec, encs
 
 
+@pytest.mark.parametrize("fuse_ln", ["1", "0"])
 @pytest.mark.parametrize("n", [2, 4, 8])
-def test_streams_tokens_identical_to_each_oracle_decode(kern, orc, n):
+def test_streams_tokens_identical_to_each_oracle_decode(kern, orc, n, fuse_ln):
     """Independent streams decoded side by side (every product n rows): each
-    stream's greedy tokens are those of its own oracle decode."""
+    stream's greedy tokens are those of its own oracle decode, with each
+    stream's LayerNorm row built inside the product (one wave per row) or
+    by a row kernel beforehand (GRX_FUSE_LN=0)."""
+    os.environ["GRX_FUSE_LN"] = fuse_ln
+    try:
+        _streams_vs_oracle(orc, n)
+    finally:
+        del os.environ["GRX_FUSE_LN"]
+
+
+def _streams_vs_oracle(orc, n):
     hp = dict(WHISPER_TINY_TEST)
     t = whisper_model(hp, seed=21)
     dec, encs = _streams(hp, t, n, seed=40)
