@@ -94,6 +94,85 @@ __device__ inline void block_softmax(float *s, int n, float *part) {
     __syncthreads();
 }
 
+// A DPP move within rows of 16 lanes (every lane active).
+template <int CTRL>
+__device__ __forceinline__ float dpp_max_step(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false));
+}
+
+// The largest value of the wave, in every lane (DPP within rows of 16, then
+// the four rows).
+__device__ __forceinline__ float wave_max(float m) {
+    float t = dpp_max_step<0xb1>(m);
+    m = t > m ? t : m;
+    t = dpp_max_step<0x4e>(m);
+    m = t > m ? t : m;
+    t = dpp_max_step<0x141>(m);
+    m = t > m ? t : m;
+    t = dpp_max_step<0x140>(m);
+    m = t > m ? t : m;
+    const float a = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(m), 0));
+    const float b = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(m), 16));
+    const float c = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(m), 32));
+    const float d = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(m), 48));
+    const float ab = b > a ? b : a, cd = d > c ? d : c;
+    return cd > ab ? cd : ab;
+}
+
+// The softmax sums of block_softmax (mathx.go:78-90) for wave 0, from the
+// exps below n8 stored chain-major (chain c = j % 8 at ch[c*cs + j/8],
+// cs % 4 == 0) and the tail's exps tl[0..n-n8): lane 0 gets
+// 1 / (HSUM(eight chains) + tail).  Branch-free: whole runs of 32 steps,
+// then a last run under selects.
+__device__ __forceinline__ float softmax_inv(const float *ch, int cs, const float *tl, int n) {
+    const int lane = threadIdx.x & 63, c = lane & 7, n8 = n & ~7, nt = n - n8, N = n8 >> 3;
+    const float4 *cr = reinterpret_cast<const float4 *>(ch + c * cs);
+    float acc = 0.f;
+    int g0 = 0;
+    for (; g0 + 32 <= N; g0 += 32) {
+        float4 t[8];
+#pragma unroll
+        for (int g = 0; g < 8; ++g) t[g] = cr[(g0 >> 2) + g];
+#pragma unroll
+        for (int g = 0; g < 8; ++g) {
+            acc = __fadd_rn(acc, t[g].x);
+            acc = __fadd_rn(acc, t[g].y);
+            acc = __fadd_rn(acc, t[g].z);
+            acc = __fadd_rn(acc, t[g].w);
+        }
+    }
+    if (g0 < N) {
+        float4 t[8];
+#pragma unroll
+        for (int g = 0; g < 8; ++g) t[g] = cr[min((g0 >> 2) + g, (N - 1) >> 2)];
+#pragma unroll
+        for (int g = 0; g < 8; ++g) {
+            const int m = g0 + 4 * g;
+            float f;
+            f = __fadd_rn(acc, t[g].x);
+            acc = m + 0 < N ? f : acc;
+            f = __fadd_rn(acc, t[g].y);
+            acc = m + 1 < N ? f : acc;
+            f = __fadd_rn(acc, t[g].z);
+            acc = m + 2 < N ? f : acc;
+            f = __fadd_rn(acc, t[g].w);
+            acc = m + 3 < N ? f : acc;
+        }
+    }
+    float tt = 0.f;
+#pragma unroll
+    for (int i = 0; i < 7; ++i) {
+        const float f = __fadd_rn(tt, tl[min(i, max(nt - 1, 0))]);
+        tt = i < nt ? f : tt;
+    }
+    const float p0 = __shfl(acc, 0), p1 = __shfl(acc, 1), p2 = __shfl(acc, 2), p3 = __shfl(acc, 3);
+    const float p4 = __shfl(acc, 4), p5 = __shfl(acc, 5), p6 = __shfl(acc, 6), p7 = __shfl(acc, 7);
+    const float sa = n8 > 0 ? __fadd_rn(__fadd_rn(__fadd_rn(p0, p4), __fadd_rn(p1, p5)),
+                                        __fadd_rn(__fadd_rn(p2, p6), __fadd_rn(p3, p7)))
+                            : 0.f;
+    return __fdiv_rn(1.0f, __fadd_rn(sa, tt));
+}
+
 // Round the values held by 32 consecutive lanes (one Q8_0 block) for the
 // next product: quantU8 (internal/kern/q8int.go:88-105) with the block's
 // largest magnitude from xor-shuffles.  Every lane of the 32 must call it.

@@ -23,6 +23,7 @@
 #include <stdlib.h>
 #include <string.h>
 
+#include <algorithm>
 #include <map>
 #include <string>
 #include <vector>
@@ -46,6 +47,116 @@ __global__ void input_kernel(const float *__restrict__ w, const float *__restric
     x[j] = j < (d & ~3) ? dot_x4(lat, wr, ldim) : dot_go(lat, wr, ldim);
 }
 
+// Frame attention for heads of 64 over n <= kStepN keys, without divergent
+// branches (the arithmetic of attn_step_kernel's general body below): thread
+// j holds key row j (zeros past n, never used), its score (dotF32x4 below
+// n &^ 3, dotF32Go past it, times the scale), the maximum by DPP and one
+// barrier, EXP8 or expf, each wave's own 1 / sum (expSub's eight lane sums,
+// HSUM, the tail), then w_j and value row j into LDS (w = 0 past n); wave
+// 0's lane d runs AddScaled's chain o = fma(w_j, v_j[d], o) in key order,
+// zero weights skipped.
+constexpr int kStepHd = 64, kStepN = 512, kStepLd = kStepHd + 4, kStepThreads = kStepN;
+// chain-major exps kStepCs floats apart: the eight chains' 16-byte reads
+// fall in distinct banks
+constexpr int kStepCs = kStepN / 8 + 4;
+// LDS floats: value rows [kStepN][kStepLd], chain-major exps, exps by key,
+// weights, reductions, dummy slots
+constexpr size_t kStepLds = (size_t)kStepN * kStepLd + 8 * (size_t)kStepCs + 2 * (size_t)kStepN + 16 + 8;
+
+template <bool QOUT>
+__device__ __forceinline__ void attn_step_small(float *sm, const float *q, const float *kc, const float *vc, int n,
+                                                int d, float scale, float *att, int8_t *att_q, float *att_s) {
+    constexpr int HD = kStepHd, RC = kStepN, LD = kStepLd;
+    float *vl = sm, *ch = vl + RC * LD, *pl = ch + 8 * kStepCs, *pw = pl + RC, *red = pw + RC, *dummy = red + 16;
+    const int h = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const bool live = tid < n;
+    const int j = min(tid, n - 1);
+    const float4 *kr = reinterpret_cast<const float4 *>(kc + (size_t)j * d + h * HD);
+    const float4 *vr = reinterpret_cast<const float4 *>(vc + (size_t)j * d + h * HD);
+    float4 kv[HD / 4], vv[HD / 4];
+    if (live) {  // lanes past n load nothing (many lanes loading one repeated row measured far slower)
+#pragma unroll
+        for (int i = 0; i < HD / 4; ++i) kv[i] = kr[i];
+#pragma unroll
+        for (int i = 0; i < HD / 4; ++i) vv[i] = vr[i];
+    } else {
+#pragma unroll
+        for (int i = 0; i < HD / 4; ++i) kv[i] = vv[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+    const float4 *qh = reinterpret_cast<const float4 *>(q + h * HD);
+    // dot4f32avx's row (eight-lane accumulators A, B over steps of 16) and
+    // dotF32Go's four running sums, both from the same products' operands
+    float A[8], B[8], s0 = 0.f, s1 = 0.f, s2 = 0.f, s3 = 0.f;
+#pragma unroll
+    for (int l = 0; l < 8; ++l) A[l] = B[l] = 0.f;
+#pragma unroll
+    for (int i = 0; i < HD / 4; ++i) {
+        const float4 a = qh[i], b = kv[i];
+        const float av[4] = {a.x, a.y, a.z, a.w}, bv[4] = {b.x, b.y, b.z, b.w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const int c = 4 * i + e, l = c & 15;
+            if (l < 8)
+                A[l] = __fmaf_rn(av[e], bv[e], A[l]);
+            else
+                B[l - 8] = __fmaf_rn(av[e], bv[e], B[l - 8]);
+        }
+        s0 = __fadd_rn(s0, __fmul_rn(a.x, b.x));
+        s1 = __fadd_rn(s1, __fmul_rn(a.y, b.y));
+        s2 = __fadd_rn(s2, __fmul_rn(a.z, b.z));
+        s3 = __fadd_rn(s3, __fmul_rn(a.w, b.w));
+    }
+    float S[8];
+#pragma unroll
+    for (int l = 0; l < 8; ++l) S[l] = __fadd_rn(A[l], B[l]);
+    const float x4 = hsum8(S);
+    const float go = __fadd_rn(__fadd_rn(__fadd_rn(s0, s1), s2), s3);
+    const float score = __fmul_rn(tid < (n & ~3) ? x4 : go, scale);
+    float mx = wave_max(live ? score : -__builtin_inff());
+    if (lane == 0) red[wave] = mx;
+    __syncthreads();
+    mx = red[0];
+#pragma unroll
+    for (int w = 1; w < kStepThreads / 64; ++w) mx = red[w] > mx ? red[w] : mx;
+    const int n8 = n & ~7;
+    const float dd = __fsub_rn(score, mx);
+    const float e8 = grx_exp8(dd), eg = grx_expf_go(dd);
+    const float e = tid < n8 ? e8 : eg;
+    *(tid < n8 ? ch + (tid & 7) * kStepCs + (tid >> 3) : dummy) = e;
+    *(live ? pl + tid : dummy + 1) = e;
+    __syncthreads();
+    const float inv = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(softmax_inv(ch, kStepCs, pl + n8, n)), 0));
+    pw[tid] = live ? __fmul_rn(e, inv) : 0.f;
+    float4 *vw = reinterpret_cast<float4 *>(vl + tid * LD);
+#pragma unroll
+    for (int i = 0; i < HD / 4; ++i) vw[i] = vv[i];
+    __syncthreads();
+    if (wave == 0) {
+        float o = 0.f;
+        const int n32 = (n + 31) & ~31;
+        for (int j0 = 0; j0 < n32; j0 += 32) {
+            float w[32], v[32];
+#pragma unroll
+            for (int i = 0; i < 32; i += 4) {
+                const float4 t = *reinterpret_cast<const float4 *>(pw + j0 + i);
+                w[i] = t.x;
+                w[i + 1] = t.y;
+                w[i + 2] = t.z;
+                w[i + 3] = t.w;
+            }
+#pragma unroll
+            for (int i = 0; i < 32; ++i) v[i] = vl[(j0 + i) * LD + lane];
+            // a zero weight is skipped as fma(0, 0, o) == o (o starts at +0 and
+            // exact cancellation rounds to +0, so o is never -0): the select
+            // stays off the dependent chain
+#pragma unroll
+            for (int i = 0; i < 32; ++i) o = __fmaf_rn(w[i], w[i] == 0.f ? 0.f : v[i], o);
+        }
+        att[h * HD + lane] = o;
+        if constexpr (QOUT) quant32_store(o, att_q + h * HD + lane, att_s + (h * HD + lane) / 32, lane & 31);
+    }
+}
+
 // attend for one query row (T = 1, nn.go:200-244), one workgroup per head:
 // scores of the pos+1 keys by MatMulF32's one-row route (dotF32x4 per group
 // of four keys, dotF32Go for the rest), times 1/sqrt(hd), softmax by expSub,
@@ -53,12 +164,16 @@ __global__ void input_kernel(const float *__restrict__ w, const float *__restric
 // (axpyAVX's fma below hd &^ 7, axpyGo past it).  With QOUT the head's
 // outputs are also rounded to Q8_0.
 template <bool QOUT>
-__global__ __launch_bounds__(kThreads) void attn_step_kernel(const float *__restrict__ q, const float *__restrict__ kc,
+__global__ __launch_bounds__(kStepThreads) void attn_step_kernel(const float *__restrict__ q, const float *__restrict__ kc,
                                                             const float *__restrict__ vc, const int *__restrict__ pos,
                                                             int d, int hd, float scale, int rc, float *__restrict__ att,
                                                             int8_t *__restrict__ att_q, float *__restrict__ att_s) {
-    extern __shared__ float sm[];
+    extern __shared__ __align__(16) float sm[];
     const int h = blockIdx.x, n = *pos + 1, tid = threadIdx.x;
+    if (hd == kStepHd && n <= kStepN) {
+        attn_step_small<QOUT>(sm, q, kc, vc, n, d, scale, att, att_q, att_s);
+        return;
+    }
     float *part = sm, *s = sm + 32, *vl = sm + 32 + ((n + 3) & ~3);
     const float *qh = q + h * hd;
     const int n4 = n & ~3;
@@ -478,18 +593,30 @@ grx_status enqueue_frame(grx_pocket *m, hipStream_t st, const float *lat_base, c
     grx_status s;
     input_kernel<<<grx_ceil_div(d, kThreads), kThreads, 0, st>>>(m->input, lat_base, frame, d, hp.ldim, m->x);
     GRX_LAUNCHED("input_kernel");
-    // LDS: 32 + max_pos scores, then value rows in chunks within 48 KiB
+    // LDS: 32 + max_pos scores, then value rows in chunks within 48 KiB; or
+    // the branch-free body's (heads of 64, up to kStepN keys), 512 threads
     const int rc = max(1, min(hp.max_pos, (48 * 1024) / (hd * 4)));
-    const size_t smem = (32 + (((size_t)hp.max_pos + 3) & ~(size_t)3) + (size_t)rc * hd) * 4;
+    size_t smem = (32 + (((size_t)hp.max_pos + 3) & ~(size_t)3) + (size_t)rc * hd) * 4;
+    if (hd == kStepHd) {
+        smem = std::max(smem, kStepLds * 4);
+        static bool raised = false;  // set by the eager frame that precedes any capture
+        if (!raised) {
+            raised = true;
+            GRX_HIP(hipFuncSetAttribute((const void *)attn_step_kernel<true>,
+                                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)(kStepLds * 4)));
+            GRX_HIP(hipFuncSetAttribute((const void *)attn_step_kernel<false>,
+                                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)(kStepLds * 4)));
+        }
+    }
     for (int li = 0; li < hp.n_layer; ++li) {
         PLayer &L = m->L[li];
         if ((s = layer_product(m, st, L, 0, 0, 1, qatt)) != GRX_OK) return s;
         if (qatt)
-            attn_step_kernel<true><<<hp.heads, kThreads, smem, st>>>(m->q, L.k, L.v, m->pos, d, hd, scale, rc, m->att,
-                                                                     m->att_q, m->att_s);
+            attn_step_kernel<true><<<hp.heads, kStepThreads, smem, st>>>(m->q, L.k, L.v, m->pos, d, hd, scale, rc,
+                                                                         m->att, m->att_q, m->att_s);
         else
-            attn_step_kernel<false><<<hp.heads, kThreads, smem, st>>>(m->q, L.k, L.v, m->pos, d, hd, scale, rc, m->att,
-                                                                      nullptr, nullptr);
+            attn_step_kernel<false><<<hp.heads, kStepThreads, smem, st>>>(m->q, L.k, L.v, m->pos, d, hd, scale, rc,
+                                                                          m->att, nullptr, nullptr);
         GRX_LAUNCHED("attn_step_kernel");
         for (int ph = 1; ph < 4; ++ph)
             if ((s = layer_product(m, st, L, ph, 0, 1, qatt)) != GRX_OK) return s;

@@ -42,93 +42,16 @@ constexpr int kBatchV = 96;  // the same for the cross values' longer chains (on
 // Self-attention workgroups are 256 threads; heads of 64 over at most
 // kSmallN positions take the branch-free body, others the general one.
 constexpr int kSmallHd = 64, kSmallN = 256, kSmallPld = kSmallHd + 4;
+// chain-major exps kSmallCs floats apart (distinct banks for the eight chains)
+constexpr int kSmallCs = kSmallN / 8 + 4;
 // LDS floats of the branch-free body: products [kSmallN][kSmallPld] (rows 68
 // floats apart: 16-byte writes of 16 lanes fall in distinct banks), chain-
 // major exps, exps by position, reductions, a dummy slot
-constexpr size_t kSmallLds = (size_t)kSmallN * kSmallPld + 2 * kSmallN + 16 + 4;
-
-// A DPP move within rows of 16 lanes (every lane active).
-template <int CTRL>
-__device__ __forceinline__ float dpp_max_step(float v) {
-    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false));
-}
-
-// The largest value of the wave, in every lane (DPP within rows of 16, then
-// the four rows).
-__device__ __forceinline__ float wave_max(float m) {
-    float t = dpp_max_step<0xb1>(m);
-    m = t > m ? t : m;
-    t = dpp_max_step<0x4e>(m);
-    m = t > m ? t : m;
-    t = dpp_max_step<0x141>(m);
-    m = t > m ? t : m;
-    t = dpp_max_step<0x140>(m);
-    m = t > m ? t : m;
-    const float a = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(m), 0));
-    const float b = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(m), 16));
-    const float c = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(m), 32));
-    const float d = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(m), 48));
-    const float ab = b > a ? b : a, cd = d > c ? d : c;
-    return cd > ab ? cd : ab;
-}
-
-// The softmax sums of block_softmax (mathx.go:78-90) for wave 0, from the
-// exps below n8 stored chain-major (chain c = j % 8 at ch[c*cs + j/8],
-// cs % 4 == 0) and the tail's exps tl[0..n-n8): lane 0 gets
-// 1 / (HSUM(eight chains) + tail).  Branch-free: whole runs of 32 steps,
-// then a last run under selects.
-__device__ __forceinline__ float softmax_inv(const float *ch, int cs, const float *tl, int n) {
-    const int lane = threadIdx.x & 63, c = lane & 7, n8 = n & ~7, nt = n - n8, N = n8 >> 3;
-    const float4 *cr = reinterpret_cast<const float4 *>(ch + c * cs);
-    float acc = 0.f;
-    int g0 = 0;
-    for (; g0 + 32 <= N; g0 += 32) {
-        float4 t[8];
-#pragma unroll
-        for (int g = 0; g < 8; ++g) t[g] = cr[(g0 >> 2) + g];
-#pragma unroll
-        for (int g = 0; g < 8; ++g) {
-            acc = __fadd_rn(acc, t[g].x);
-            acc = __fadd_rn(acc, t[g].y);
-            acc = __fadd_rn(acc, t[g].z);
-            acc = __fadd_rn(acc, t[g].w);
-        }
-    }
-    if (g0 < N) {
-        float4 t[8];
-#pragma unroll
-        for (int g = 0; g < 8; ++g) t[g] = cr[min((g0 >> 2) + g, (N - 1) >> 2)];
-#pragma unroll
-        for (int g = 0; g < 8; ++g) {
-            const int m = g0 + 4 * g;
-            float f;
-            f = __fadd_rn(acc, t[g].x);
-            acc = m + 0 < N ? f : acc;
-            f = __fadd_rn(acc, t[g].y);
-            acc = m + 1 < N ? f : acc;
-            f = __fadd_rn(acc, t[g].z);
-            acc = m + 2 < N ? f : acc;
-            f = __fadd_rn(acc, t[g].w);
-            acc = m + 3 < N ? f : acc;
-        }
-    }
-    float tt = 0.f;
-#pragma unroll
-    for (int i = 0; i < 7; ++i) {
-        const float f = __fadd_rn(tt, tl[min(i, max(nt - 1, 0))]);
-        tt = i < nt ? f : tt;
-    }
-    const float p0 = __shfl(acc, 0), p1 = __shfl(acc, 1), p2 = __shfl(acc, 2), p3 = __shfl(acc, 3);
-    const float p4 = __shfl(acc, 4), p5 = __shfl(acc, 5), p6 = __shfl(acc, 6), p7 = __shfl(acc, 7);
-    const float sa = n8 > 0 ? __fadd_rn(__fadd_rn(__fadd_rn(p0, p4), __fadd_rn(p1, p5)),
-                                        __fadd_rn(__fadd_rn(p2, p6), __fadd_rn(p3, p7)))
-                            : 0.f;
-    return __fdiv_rn(1.0f, __fadd_rn(sa, tt));
-}
+constexpr size_t kSmallLds = (size_t)kSmallN * kSmallPld + 8 * kSmallCs + kSmallN + 16 + 4;
 
 // Causal self-attention of one head over n <= kSmallN positions, head_dim
 // 64, with no divergent branches: thread j holds K and V row j in registers
-// (rows past n repeat row n-1 and are never used), its score (dotF32Go),
+// (zeros past n, never used), its score (dotF32Go),
 // the maximum by DPP and
 // one barrier, its exp (chain-major and by position in LDS), every wave's own
 // 1 / sum (softmax_inv), then its products p_j * v_j[d] into LDS (zeros past
@@ -138,7 +61,7 @@ __device__ __forceinline__ void self_attn_small(float *sm, const float *q, const
                                                 const float4 (&vv)[kSmallHd / 4], int n, float sc, float *att,
                                                 int8_t *att_q, float *att_s) {
     constexpr int HD = kSmallHd, RC = kSmallN, PLD = kSmallPld;
-    float *prod = sm, *ch = prod + RC * PLD, *pl = ch + RC, *red = pl + RC, *dummy = red + 16;
+    float *prod = sm, *ch = prod + RC * PLD, *pl = ch + 8 * kSmallCs, *red = pl + RC, *dummy = red + 16;
     const int h = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const bool live = tid < n;
     // dotF32Go (gemm.go:294-308): four running sums over the float4 pieces
@@ -162,10 +85,10 @@ __device__ __forceinline__ void self_attn_small(float *sm, const float *q, const
     // both forms, then the reference's (EXP8 below n8, expf past it): no branch
     const float e8 = grx_exp8(d), eg = grx_expf_go(d);
     const float e = tid < n8 ? e8 : eg;
-    *(tid < n8 ? ch + (tid & 7) * (RC / 8) + (tid >> 3) : dummy) = e;
+    *(tid < n8 ? ch + (tid & 7) * kSmallCs + (tid >> 3) : dummy) = e;
     *(live ? pl + tid : dummy + 1) = e;
     __syncthreads();
-    const float inv = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(softmax_inv(ch, RC / 8, pl + n8, n)), 0));
+    const float inv = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(softmax_inv(ch, kSmallCs, pl + n8, n)), 0));
     const float pj = __fmul_rn(e, inv);
     float4 *pr = reinterpret_cast<float4 *>(prod + tid * PLD);
 #pragma unroll
@@ -206,16 +129,21 @@ __global__ __launch_bounds__(kAttnThreads) void self_attn_kernel(
     const int h = blockIdx.x, tid = threadIdx.x, sm_ = blockIdx.y;  // head, stream
     const int n = *pos + 1;
     if (hd == kSmallHd && n <= kSmallN) {
-        // thread j's K and V row j (rows past n repeat row n-1: loading
-        // rows past the position measured slower than waiting for it)
+        // thread j's K and V row j (many lanes loading one repeated row
+        // measured far slower than leaving them out)
         const int j = min(min(tid, n - 1), ctx_rows - 1);
         const float4 *kr = reinterpret_cast<const float4 *>(kc + sm_ * kv_stream + (size_t)j * st + h * kSmallHd);
         const float4 *vr = reinterpret_cast<const float4 *>(vc + sm_ * kv_stream + (size_t)j * st + h * kSmallHd);
         float4 kv[kSmallHd / 4], vv[kSmallHd / 4];
+        if (tid < n) {  // lanes past n load nothing
 #pragma unroll
-        for (int i = 0; i < kSmallHd / 4; ++i) kv[i] = kr[i];
+            for (int i = 0; i < kSmallHd / 4; ++i) kv[i] = kr[i];
 #pragma unroll
-        for (int i = 0; i < kSmallHd / 4; ++i) vv[i] = vr[i];
+            for (int i = 0; i < kSmallHd / 4; ++i) vv[i] = vr[i];
+        } else {
+#pragma unroll
+            for (int i = 0; i < kSmallHd / 4; ++i) kv[i] = vv[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+        }
         self_attn_small<QOUT>(sm, q + (size_t)sm_ * st, kv, vv, n, sc, att + (size_t)sm_ * st,
                               QOUT ? att_q + (size_t)sm_ * st : nullptr,
                               QOUT ? att_s + (size_t)sm_ * (st / 32) : nullptr);
