@@ -427,7 +427,7 @@ def main():
                    "parity_bit_exact": parity, "wall_s": round(wall, 3)},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),
-                     "kernel": "gemv_q8_kernel<1,1,PREQ,STORE>", "kernel_avg_us": round(gemv_avg * 1e3, 3)},
+                     "kernel": "gemv1_kernel<1,1,PREQ,STORE>", "kernel_avg_us": round(gemv_avg * 1e3, 3)},
     }
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline(w8, x, args.cpu_seconds)
