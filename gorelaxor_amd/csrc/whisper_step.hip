@@ -866,8 +866,10 @@ grx_status enqueue_step(grx_whisper *m, hipStream_t stream) {
                 m->q, L.cross_k, nctx, hd, st, x_stream, m->scores);
             GRX_LAUNCHED("cross_scores_kernel");
         }
-        // one stream: workgroups over 16 outputs each, float32 out
-        const bool wave_values = S == 1 && nctx <= kWaveCtx && hd % kWaveOut == 0;
+        // workgroups over 16 outputs each, float32 out (the cross-out product
+        // rounds its rows in its prologue; several streams: a wave per row)
+        const bool wave_values = nctx <= kWaveCtx && hd % kWaveOut == 0 && (S == 1 || st <= 1280) &&
+                                 !getenv_off("GRX_WAVE_VALUES");
         if (wave_values) {
             cross_values_wave_kernel<<<dim3(nh, hd / kWaveOut, S), 256, 0, stream>>>(m->scores, L.cross_v, nctx,
                                                                                      hd, st, x_stream, m->att);

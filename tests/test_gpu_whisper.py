@@ -137,13 +137,17 @@ def _streams(hp, t, n, seed):
 def test_streams_tokens_identical_to_each_oracle_decode(kern, orc, n, fuse_ln):
     """Independent streams decoded side by side (every product n rows): each
     stream's greedy tokens are those of its own oracle decode, with each
-    stream's LayerNorm row built inside the product (one wave per row) or
-    by a row kernel beforehand (GRX_FUSE_LN=0)."""
+    stream's LayerNorm row built inside the product (one wave per row) and
+    the cross values on 16-output workgroups, or (GRX_FUSE_LN=0,
+    GRX_WAVE_VALUES=0) a row kernel beforehand and the values kernel that
+    rounds its outputs."""
     os.environ["GRX_FUSE_LN"] = fuse_ln
+    os.environ["GRX_WAVE_VALUES"] = fuse_ln
     try:
         _streams_vs_oracle(orc, n)
     finally:
         del os.environ["GRX_FUSE_LN"]
+        del os.environ["GRX_WAVE_VALUES"]
 
 
 def _streams_vs_oracle(orc, n):
