@@ -69,6 +69,7 @@ SIGNATURES = {
     "grx_whisper_streams": (i32, [vp]),
     "grx_whisper_set_encoder_output_stream": (i32, [vp, i32, vp, i32]),
     "grx_whisper_greedy_streams": (i32, [vp, vp, i32, i32, vp]),
+    "grx_whisper_load_ggml": (i32, [vp, C.c_char_p, i32, vp, C.POINTER(vp)]),
     "grx_pocket_create": (i32, [vp, vp, C.POINTER(vp)]),
     "grx_pocket_destroy": (i32, [vp]),
     "grx_pocket_set_tensor": (i32, [vp, C.c_char_p, vp, sz]),

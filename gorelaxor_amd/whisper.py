@@ -34,6 +34,22 @@ class WhisperDecoder:
             for name, arr in tensors.items():
                 self.set_tensor(name, arr)
 
+    @classmethod
+    def from_ggml(cls, path: str, ctx: Context | None = None, streams: int = 1) -> "WhisperDecoder":
+        """A decoder from a whisper.cpp (ggml) model file (whisper.Load,
+        whisper/model.go:93-225): Q8_0 matrices go to the device as stored."""
+        self = cls.__new__(cls)
+        self.handle = None
+        self.ctx = ctx or default_context()
+        self.streams = streams
+        h = _lib.WhisperHParams()
+        out = C.c_void_p()
+        _lib.call("grx_whisper_load_ggml", self.ctx.handle, str(path).encode(), streams, C.byref(h), C.byref(out))
+        self.handle = out
+        self.hp = {k: int(getattr(h, k)) for k in ("n_vocab", "n_text_ctx", "n_state", "n_head", "n_layer",
+                                                   "n_audio_ctx")}
+        return self
+
     def set_tensor(self, name: str, arr: np.ndarray) -> None:
         a = np.ascontiguousarray(arr)
         _lib.call("grx_whisper_set_tensor", self.handle, name.encode(), a.ctypes.data_as(C.c_void_p), a.nbytes)

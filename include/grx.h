@@ -191,6 +191,19 @@ grx_status grx_whisper_set_encoder_output_stream(grx_whisper *m, int stream, con
 grx_status grx_whisper_greedy_streams(grx_whisper *m, const int32_t *prompts, int n_prompt, int n_steps,
                                       int32_t *out);
 
+/* A whisper.cpp (ggml) model file straight into a decoder of n_streams
+ * streams (1, 2, 4 or 8): replaces whisper.Load (whisper/model.go:93-225)
+ * and Model.bind (model.go:300-404) for the decoder.  The file is read and
+ * checked as the reference reads it (magic, dimensions, mel filters,
+ * vocabulary, tensors until the end; the same error texts, prefixed with
+ * the path), but a Q8_0 matrix goes to the device as stored instead of
+ * being widened to float16; other matrix types are widened as the
+ * reference widens them and rounded to Q8_0.  The encoder's tensors are
+ * checked and skipped.  *hp_out (may be NULL) receives the decoder's
+ * dimensions. */
+grx_status grx_whisper_load_ggml(grx_ctx *ctx, const char *path, int n_streams, grx_whisper_hparams *hp_out,
+                                 grx_whisper **out);
+
 /* ---- pocket-TTS flow-LM transformer with Q8_0 weights ---- */
 
 /* flowLM of pockettts/lm.go:164-195 over transformer.forward and attend of
