@@ -70,6 +70,28 @@ SIGNATURES = {
     "grx_whisper_set_encoder_output_stream": (i32, [vp, i32, vp, i32]),
     "grx_whisper_greedy_streams": (i32, [vp, vp, i32, i32, vp]),
     "grx_whisper_load_ggml": (i32, [vp, C.c_char_p, i32, vp, C.POINTER(vp)]),
+    "grx_gguf_open": (i32, [C.c_char_p, C.POINTER(vp)]),
+    "grx_gguf_parse": (i32, [vp, sz, C.POINTER(vp)]),
+    "grx_gguf_read_meta": (i32, [C.c_char_p, C.POINTER(vp)]),
+    "grx_gguf_close": (i32, [vp]),
+    "grx_gguf_version": (i32, [vp]),
+    "grx_gguf_n_tensors": (i32, [vp]),
+    "grx_gguf_tensor_name": (C.c_char_p, [vp, i32]),
+    "grx_gguf_n_keys": (i32, [vp]),
+    "grx_gguf_key": (C.c_char_p, [vp, i32]),
+    "grx_gguf_has": (i32, [vp, C.c_char_p]),
+    "grx_gguf_tensor_info": (i32, [vp, C.c_char_p, C.POINTER(i32), C.POINTER(i32), C.POINTER(C.c_int64)]),
+    "grx_gguf_int": (C.c_int64, [vp, C.c_char_p, C.c_int64]),
+    "grx_gguf_float": (C.c_double, [vp, C.c_char_p, C.c_double]),
+    "grx_gguf_bool": (i32, [vp, C.c_char_p, i32]),
+    "grx_gguf_string": (C.c_char_p, [vp, C.c_char_p, C.c_char_p]),
+    "grx_gguf_array_len": (C.c_int64, [vp, C.c_char_p]),
+    "grx_gguf_array_string": (C.c_char_p, [vp, C.c_char_p, C.c_int64]),
+    "grx_gguf_array_float": (C.c_double, [vp, C.c_char_p, C.c_int64]),
+    "grx_gguf_array_int": (C.c_int64, [vp, C.c_char_p, C.c_int64]),
+    "grx_gguf_float32": (i32, [vp, C.c_char_p, vp, sz]),
+    "grx_gguf_weight_shape": (i32, [vp, C.c_char_p, C.POINTER(C.c_int64), C.POINTER(C.c_int64)]),
+    "grx_gguf_weight_q8": (i32, [vp, vp, C.c_char_p, C.POINTER(vp)]),
     "grx_pocket_create": (i32, [vp, vp, C.POINTER(vp)]),
     "grx_pocket_destroy": (i32, [vp]),
     "grx_pocket_set_tensor": (i32, [vp, C.c_char_p, vp, sz]),

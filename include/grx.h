@@ -204,6 +204,53 @@ grx_status grx_whisper_greedy_streams(grx_whisper *m, const int32_t *prompts, in
 grx_status grx_whisper_load_ggml(grx_ctx *ctx, const char *path, int n_streams, grx_whisper_hparams *hp_out,
                                  grx_whisper **out);
 
+/* ---- GGUF model files (internal/gguf/gguf.go) ---- */
+
+/* A GGUF file (versions 2 and 3; tensors F32, F16, BF16, Q8_0) with the
+ * reference's checks against crafted files and its error texts.  Host
+ * only: these calls need no GPU, except grx_gguf_weight_q8. */
+typedef struct grx_gguf grx_gguf;
+/* gguf.Open (gguf.go:57-113): the header and tensor table; a tensor's bytes
+ * are read from the file when asked for.  Tensors whose sizes add up to
+ * more than the file are refused. */
+grx_status grx_gguf_open(const char *path, grx_gguf **out);
+/* gguf.Parse (gguf.go:277-289) of a file held in memory (copied). */
+grx_status grx_gguf_parse(const void *bytes, size_t n, grx_gguf **out);
+/* gguf.ReadMeta (gguf.go:219-234): the settings only, no tensor table. */
+grx_status grx_gguf_read_meta(const char *path, grx_gguf **out);
+grx_status grx_gguf_close(grx_gguf *g);
+int grx_gguf_version(const grx_gguf *g);
+/* File.Names (file order) and File.Keys (sorted). */
+int grx_gguf_n_tensors(const grx_gguf *g);
+const char *grx_gguf_tensor_name(const grx_gguf *g, int i);
+int grx_gguf_n_keys(const grx_gguf *g);
+const char *grx_gguf_key(const grx_gguf *g, int i);
+/* File.Has */
+int grx_gguf_has(const grx_gguf *g, const char *name);
+/* A tensor's type and dimensions (dims[0] the row length); unused dims 0. */
+grx_status grx_gguf_tensor_info(const grx_gguf *g, const char *name, int *type, int *n_dims, int64_t dims[4]);
+/* File.Int / Float / Bool / String (gguf.go:415-460): def when missing or
+ * of another kind.  Strings live as long as the file handle. */
+int64_t grx_gguf_int(const grx_gguf *g, const char *key, int64_t def);
+double grx_gguf_float(const grx_gguf *g, const char *key, double def);
+int grx_gguf_bool(const grx_gguf *g, const char *key, int def);
+const char *grx_gguf_string(const grx_gguf *g, const char *key, const char *def);
+/* File.Strings / Floats / Ints (gguf.go:462-510) element by element:
+ * grx_gguf_array_len is -1 when the key holds no array; an element of
+ * another kind reads as "" or 0, as there. */
+int64_t grx_gguf_array_len(const grx_gguf *g, const char *key);
+const char *grx_gguf_array_string(const grx_gguf *g, const char *key, int64_t i);
+double grx_gguf_array_float(const grx_gguf *g, const char *key, int64_t i);
+int64_t grx_gguf_array_int(const grx_gguf *g, const char *key, int64_t i);
+/* File.Float32 (gguf.go:518-542): n >= the tensor's values. */
+grx_status grx_gguf_float32(const grx_gguf *g, const char *name, float *out, size_t n);
+/* File.Weight's matrix shape (gguf.go:544-558): cols is the first
+ * dimension longer than one, the rest flattened into rows. */
+grx_status grx_gguf_weight_shape(const grx_gguf *g, const char *name, int64_t *rows, int64_t *cols);
+/* File.Weight + kern.NewQ8 + Pack (gguf.go:544-581, kern.go:41-93): a Q8_0
+ * tensor from the file to its device tiles, with no host copy kept. */
+grx_status grx_gguf_weight_q8(grx_ctx *ctx, const grx_gguf *g, const char *name, grx_weight **out);
+
 /* ---- pocket-TTS flow-LM transformer with Q8_0 weights ---- */
 
 /* flowLM of pockettts/lm.go:164-195 over transformer.forward and attend of
