@@ -188,7 +188,6 @@ struct grx_gguf {
     uint64_t base = 0, size = 0;
     std::string path;           // Open: tensors read from here
     std::vector<uint8_t> buf;   // Parse: the caller's bytes, copied
-    std::string scratch;        // the last string handed out
 
     const Val *get(const char *k) const {
         auto it = kv.find(k);
@@ -527,6 +526,14 @@ extern "C" grx_status grx_gguf_float32(const grx_gguf *g, const char *name, floa
         }
     }
     return GRX_OK;
+}
+
+// A tensor's stored bytes and type, for the model loaders in this library.
+grx_status grx_gguf_tensor_data(const grx_gguf *g, const char *name, int *type, std::vector<uint8_t> *out) {
+    const Tensor *t = find(g, name);
+    if (!t) return gfail(fmt("gguf: no tensor %s", name));
+    if (type) *type = (int)t->type;
+    return tensor_bytes(g, *t, out);
 }
 
 // File.Weight's shape (rows, cols) of any tensor

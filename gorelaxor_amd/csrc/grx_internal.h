@@ -38,6 +38,12 @@ struct grx_weight {
 };
 
 grx_status grx_fail(grx_status s, const char *fmt, ...);
+
+#ifdef __cplusplus
+#include <vector>
+// gguf.hip: a tensor's stored bytes and its ggml type code
+grx_status grx_gguf_tensor_data(const grx_gguf *g, const char *name, int *type, std::vector<uint8_t> *out);
+#endif
 grx_status grx_hip_fail(hipError_t e, const char *what);
 grx_status grx_ctx_scratch(grx_ctx *ctx, size_t bytes, void **out);
 

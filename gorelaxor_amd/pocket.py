@@ -28,6 +28,21 @@ class PocketLM:
             for name, arr in tensors.items():
                 self.set_tensor(name, arr)
 
+    @classmethod
+    def from_gguf(cls, path: str, max_pos: int, ctx: Context | None = None) -> "PocketLM":
+        """The flow LM of a Pocket TTS GGUF file (pockettts.Load, pockettts/
+        model.go:201-250): Q8_0 transformer matrices go to the device as
+        stored."""
+        self = cls.__new__(cls)
+        self.handle = None
+        self.ctx = ctx or default_context()
+        h = _lib.PocketHParams()
+        out = C.c_void_p()
+        _lib.call("grx_pocket_load_gguf", self.ctx.handle, str(path).encode(), max_pos, C.byref(h), C.byref(out))
+        self.handle = out
+        self.hp = {k: getattr(h, k) for k in ("d", "heads", "ff", "n_layer", "max_pos", "ldim", "period")}
+        return self
+
     def set_tensor(self, name: str, arr: np.ndarray) -> None:
         a = np.ascontiguousarray(arr)
         _lib.call("grx_pocket_set_tensor", self.handle, name.encode(), a.ctypes.data_as(C.c_void_p), a.nbytes)

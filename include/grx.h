@@ -272,6 +272,16 @@ grx_status grx_pocket_destroy(grx_pocket *m);
  * "lm.eos.weight", ...): transformer matrices as ggml Q8_0 rows, the rest
  * float32; shapes checked. */
 grx_status grx_pocket_set_tensor(grx_pocket *m, const char *name, const void *data, size_t nbytes);
+/* The flow LM of a Pocket TTS GGUF file (pockettts.Load, pockettts/model.go:
+ * 201-250, its loader model.go:49-125): the file's name and source checks,
+ * the LM settings (latent_dim, lm.d_model, lm.heads, lm.ff, lm.layers,
+ * lm.max_period) with the reference's range checks, layers counted as the
+ * reference counts them, every tensor's shape checked with the reference's
+ * texts; the transformer's Q8_0 matrices go from the file to the device as
+ * stored.  max_pos bounds the KV caches.  *hp_out (may be NULL) receives
+ * the dimensions.  The flow head, Mimi and the tokenizer are not read. */
+grx_status grx_pocket_load_gguf(grx_ctx *ctx, const char *path, int max_pos, grx_pocket_hparams *hp_out,
+                                grx_pocket **out);
 /* Empty the caches (position 0). */
 grx_status grx_pocket_reset(grx_pocket *m);
 int grx_pocket_pos(const grx_pocket *m);
