@@ -101,6 +101,7 @@ SIGNATURES = {
     "grx_pocket_run": (i32, [vp, vp, i32, vp]),
     "grx_pocket_frames": (i32, [vp, vp, i32, vp, vp]),
     "grx_conformer_create": (i32, [vp, vp, C.POINTER(vp)]),
+    "grx_conformer_load_gguf": (i32, [vp, C.c_char_p, vp, C.POINTER(vp)]),
     "grx_conformer_destroy": (i32, [vp]),
     "grx_conformer_set_tensor": (i32, [vp, C.c_char_p, vp, sz]),
     "grx_conformer_frames_out": (i32, [vp, i32]),

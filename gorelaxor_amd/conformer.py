@@ -37,6 +37,24 @@ class ConformerEncoder:
             for name, arr in tensors.items():
                 self.set_tensor(name, arr)
 
+    @classmethod
+    def from_gguf(cls, path: str, ctx: Context | None = None) -> "ConformerEncoder":
+        """The encoder of a FastConformer GGUF file (conformer.Load,
+        conformer/model.go:163-422): Q8_0 linear weights go to the device as
+        stored."""
+        self = cls.__new__(cls)
+        self.handle = None
+        self.ctx = ctx or default_context()
+        h = _lib.ConformerHParams()
+        out = C.c_void_p()
+        _lib.call("grx_conformer_load_gguf", self.ctx.handle, str(path).encode(), C.byref(h), C.byref(out))
+        self.handle = out
+        self.hp = {k: getattr(h, k) for k in ("d", "heads", "layers", "dff", "conv_kernel", "sub_channels",
+                                              "n_mels")}
+        self.hp["xscaling"] = bool(h.xscaling)
+        self.hp["conv_norm"] = "layer_norm" if h.conv_ln else "batch_norm"
+        return self
+
     def set_tensor(self, name: str, arr: np.ndarray) -> None:
         a = np.ascontiguousarray(arr)
         _lib.call("grx_conformer_set_tensor", self.handle, name.encode(), a.ctypes.data_as(C.c_void_p), a.nbytes)

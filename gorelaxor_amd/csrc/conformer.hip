@@ -64,14 +64,16 @@ __device__ inline float go_max(float a, float b) {
 // walking its F2 positions with the channel's taps in registers; the mel
 // rows 4*t2-3 .. 4*t2+3 (zero outside the plane and past the valid frames)
 // are staged in LDS.  Output rows past the stage's valid length are zeroed,
-// and each position's c values rounded to Q8_0 for the pointwise Linear.
+// and each position's c values rounded to Q8_0 for the pointwise Linear
+// (or, for a float32 pointwise weight, stored as they are in xf).
 // conv0's arithmetic: from the bias, AddScaled of the nonzero taps in order
 // (fma for channels of whole groups of eight); the depthwise: from the bias,
 // w*x unfused over the taps in range.
 __global__ void sub_conv01_kernel(const float *__restrict__ mel, int frames, int nm, const int *__restrict__ valid,
                                   const float *__restrict__ w0, const float *__restrict__ b0,
                                   const float *__restrict__ w2, const float *__restrict__ b2, int c, int T1, int F1,
-                                  int T2, int F2, int8_t *__restrict__ xq, float *__restrict__ xs) {
+                                  int T2, int F2, int8_t *__restrict__ xq, float *__restrict__ xs,
+                                  float *__restrict__ xf) {
     extern __shared__ float patch[];  // [7][4*F2 + 3], column q = mel column q - 3
     const int ch = threadIdx.x, t2 = blockIdx.x % T2, b = blockIdx.x / T2;
     const int W = 4 * F2 + 3;
@@ -122,19 +124,23 @@ __global__ void sub_conv01_kernel(const float *__restrict__ mel, int frames, int
             }
         }
         const size_t p = ((size_t)b * T2 + t2) * F2 + f2;
-        quant32_store(o, xq + p * c + ch, xs + p * (c / 32) + ch / 32, ch & 31);
+        if (xf)
+            xf[p * c + ch] = o;
+        else
+            quant32_store(o, xq + p * c + ch, xs + p * (c / 32) + ch / 32, ch & 31);
     }
 }
 
 // dwConv2 (encoder.go:80-110) at halving s (input [b][T][F][c], one
 // workgroup of c threads per output position), rows from the stage's valid
 // length on zeroed, rounded to Q8_0 for the pointwise Linear that follows
-// (row (b, t1, f1) of c values).  RELU_IN: the input is the previous
+// (row (b, t1, f1) of c values), or stored as they are in xf for a float32
+// pointwise weight.  RELU_IN: the input is the previous
 // pointwise output, read through maskRows and ReLU (encoder.go:152-153).
 template <bool RELU_IN>
 __global__ void sub_dwconv_kernel(const float *__restrict__ in, int T, int F, int c, const int *__restrict__ valid,
                                   int s, const float *__restrict__ w, const float *__restrict__ bias, int T1, int F1,
-                                  int8_t *__restrict__ xq, float *__restrict__ xs) {
+                                  int8_t *__restrict__ xq, float *__restrict__ xs, float *__restrict__ xf) {
     const int p = blockIdx.x, ch = threadIdx.x;
     const int f1 = p % F1, t1 = (p / F1) % T1, b = p / (F1 * T1);
     const int vb = valid[b];
@@ -161,7 +167,93 @@ __global__ void sub_dwconv_kernel(const float *__restrict__ in, int T, int F, in
         for (int j = 0; j < 9; ++j)
             if (ok[j]) o = __fadd_rn(o, __fmul_rn(wv[j], xv[j]));
     }
-    quant32_store(o, xq + (size_t)p * c + ch, xs + (size_t)p * (c / 32) + ch / 32, ch & 31);
+    if (xf)
+        xf[(size_t)p * c + ch] = o;
+    else
+        quant32_store(o, xq + (size_t)p * c + ch, xs + (size_t)p * (c / 32) + ch / 32, ch & 31);
+}
+
+// kern.Linear of a float32 weight (kern.go:185-201 -> ws.matmul,
+// gemm.go:116-185) applied to each utterance's `per` rows: with more than 16
+// rows, the rows in whole groups of six take k6x16 (kernels_amd64.s:5-88):
+// from the bias, each chunk of 256 k's fma chain (from zero) is added in.
+// This kernel computes that form for every row, 64 rows x 64 columns per
+// workgroup, 4 x 4 outputs per thread, 32 k's of x and w staged in LDS per
+// pass; the rows the reference sends to gemvRows are rewritten afterwards by
+// pw_f32_rows_kernel.  k is a multiple of 32.
+constexpr int kPwT = 64, kPwK = 32;
+__global__ __launch_bounds__(256) void pw_f32_kernel(const float *__restrict__ x, const float *__restrict__ w,
+                                                     const float *__restrict__ bias, float *__restrict__ y, int rows,
+                                                     int n, int k) {
+    __shared__ __align__(16) float as[kPwK][kPwT + 4];
+    __shared__ __align__(16) float ws[kPwK][kPwT + 4];
+    const int tid = threadIdx.x, tr = tid / 16, tc = tid % 16;
+    const int r0 = blockIdx.y * kPwT, c0 = blockIdx.x * kPwT;
+    float acc[4][4], out[4][4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int col = c0 + tc * 4 + j;
+        const float bj = col < n ? bias[col] : 0.f;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            out[i][j] = bj;
+            acc[i][j] = 0.f;
+        }
+    }
+    for (int k0 = 0; k0 < k; k0 += kPwK) {
+        for (int e = tid; e < kPwT * kPwK; e += 256) {
+            const int rr = e / kPwK, kk = e % kPwK, gr = r0 + rr, gc = c0 + rr;
+            as[kk][rr] = gr < rows ? x[(size_t)gr * k + k0 + kk] : 0.f;
+            ws[kk][rr] = gc < n ? w[(size_t)gc * k + k0 + kk] : 0.f;
+        }
+        __syncthreads();
+#pragma unroll 8
+        for (int kk = 0; kk < kPwK; ++kk) {
+            const float4 a = *reinterpret_cast<const float4 *>(&as[kk][tr * 4]);
+            const float4 b = *reinterpret_cast<const float4 *>(&ws[kk][tc * 4]);
+            const float av[4] = {a.x, a.y, a.z, a.w}, bv[4] = {b.x, b.y, b.z, b.w};
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) acc[i][j] = __fmaf_rn(av[i], bv[j], acc[i][j]);
+        }
+        __syncthreads();
+        if ((k0 + kPwK) % 256 == 0 || k0 + kPwK >= k) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    out[i][j] = __fadd_rn(acc[i][j], out[i][j]);
+                    acc[i][j] = 0.f;
+                }
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int row = r0 + tr * 4 + i;
+        if (row >= rows) continue;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int col = c0 + tc * 4 + j;
+            if (col < n) y[(size_t)row * n + col] = out[i][j];
+        }
+    }
+}
+
+// The rows of each utterance that ws.matmul sends to gemvRows (gemm.go:
+// 182-184, 195-259): rows lo..per-1 of every utterance (all of them when
+// per <= 16): dotF32x4 for whole groups of four columns, dotF32Go for the
+// rest, then the bias added.  One thread per output.
+__global__ void pw_f32_rows_kernel(const float *__restrict__ x, const float *__restrict__ w,
+                                   const float *__restrict__ bias, float *__restrict__ y, int B, int per, int lo,
+                                   int n, int k) {
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x, tail = (size_t)(per - lo);
+    if (i >= (size_t)B * tail * n) return;
+    const int j = (int)(i % n);
+    const size_t rr = i / n, row = rr / tail * per + lo + rr % tail;
+    const float *xr = x + row * k, *wj = w + (size_t)j * k;
+    const float o = j < (n & ~3) ? dot_x4_s(xr, wj, 1, k) : dot_go_s(xr, wj, 1, k);
+    y[row * n + j] = __fadd_rn(o, bias[j]);
 }
 
 // The last pointwise output through maskRows and ReLU, flattened [t][c*F+f]
@@ -782,6 +874,7 @@ struct grx_conformer {
     // pre-encoder
     float *w0, *b0, *w2, *b2, *w5, *b5, *b3, *b6, *outb;
     grx_weight *w3 = nullptr, *w6 = nullptr, *wout = nullptr;
+    float *w3f = nullptr, *w6f = nullptr;  // conv.3 / conv.6 stored float32: the float route
     std::vector<CBlock> blk;
     grx_weight *pos_all = nullptr;  // every block's linear_pos, [layers*d][d]
     // shape-dependent state
@@ -790,6 +883,7 @@ struct grx_conformer {
     bool dw_win = false;     // the windowed depthwise kernel runs (its LDS was granted)
     size_t attn_smem = 0;
     float *mel = nullptr, *sub0 = nullptr, *suby = nullptr, *x = nullptr, *qkv = nullptr, *pp = nullptr;
+    float *subx = nullptr;  // float input of a float32 pointwise Linear
     float *conv = nullptr, *glu = nullptr, *pos = nullptr;
     int8_t *xq = nullptr, *fq = nullptr, *pos_q = nullptr;  // fq: the rounded SiLU output of W1
     float *xs = nullptr, *fs = nullptr, *pos_s = nullptr;
@@ -822,7 +916,7 @@ std::vector<CExpect> cexpected(const grx_conformer_hparams &hp) {
         e.push_back({pe + n + ".bias", c * 4, false});
     }
     for (const char *n : {"conv.3", "conv.6"}) {
-        e.push_back({pe + n + ".weight", q8b(c, c), false});
+        e.push_back({pe + n + ".weight", 0, false});  // Q8_0, or float32: checked at finalize
         e.push_back({pe + n + ".bias", c * 4, false});
     }
     e.push_back({pe + "out.weight", q8b(d, cF), false});
@@ -967,8 +1061,20 @@ grx_status cfinalize(grx_conformer *m) {
         const auto &t = m->host.at(n);
         return grx_weight_q8_create(m->ctx, rows, cols, t.data(), t.size(), w);
     };
-    if ((s = mat(pe + "conv.3.weight", c, c, &m->w3)) != GRX_OK) return s;
-    if ((s = mat(pe + "conv.6.weight", c, c, &m->w6)) != GRX_OK) return s;
+    // conv.3 / conv.6: Q8_0 rows (the int8 route), or float32 values as the
+    // reference's converter stores them (the float route)
+    for (auto pw : {std::make_pair("conv.3.weight", &m->w3), std::make_pair("conv.6.weight", &m->w6)}) {
+        const std::string n = pe + pw.first;
+        const auto &t = m->host.at(n);
+        if (t.size() == (size_t)c * c * 4) {
+            float **dst = pw.second == &m->w3 ? &m->w3f : &m->w6f;
+            if ((s = upload(m, t.data(), t.size(), dst)) != GRX_OK) return s;
+        } else if (t.size() == q8b(c, c)) {
+            if ((s = mat(n, c, c, pw.second)) != GRX_OK) return s;
+        } else {
+            return grx_fail(GRX_ESIZE, "tensor %s is neither Q8_0 nor float32 %dx%d", n.c_str(), c, c);
+        }
+    }
     if ((s = mat(pe + "out.weight", d, cF, &m->wout)) != GRX_OK) return s;
     if ((s = cvec(m, pe + "conv.3.bias", &m->b3)) != GRX_OK) return s;
     if ((s = cvec(m, pe + "conv.6.bias", &m->b6)) != GRX_OK) return s;
@@ -1127,6 +1233,7 @@ grx_status cshape(grx_conformer *m, int B, int frames) {
     if ((s = calloc_t(w, (size_t)B * nm * frames, &m->mel)) != GRX_OK) return s;
     if ((s = calloc_t(w, (size_t)B * T * F3 * c, &m->sub0)) != GRX_OK) return s;
     if ((s = calloc_t(w, (size_t)B * T2 * F2 * c, &m->suby)) != GRX_OK) return s;
+    if ((m->w3f || m->w6f) && (s = calloc_t(w, (size_t)B * T2 * F2 * c, &m->subx)) != GRX_OK) return s;
     // rounded activations: the largest row set of any product
     size_t qn = std::max({(size_t)B * T2 * F2 * c, R * (size_t)c * F3, R * (size_t)hp.dff, R * 2 * (size_t)d});
     if ((s = calloc_t(w, qn, &m->xq)) != GRX_OK) return s;
@@ -1155,6 +1262,22 @@ grx_status cshape(grx_conformer *m, int B, int frames) {
 
 unsigned grid_for(size_t n) { return (unsigned)std::min<size_t>((n + 255) / 256, 1u << 20); }
 
+// A float32 pointwise Linear over B utterances of `per` rows of c values:
+// the k6x16 form for every row, then the gemvRows rows rewritten.
+grx_status pw_f32(hipStream_t st, const float *x, const float *w, const float *bias, float *y, int B, int per, int c) {
+    const int rows = B * per, lo = per > 16 ? per / 6 * 6 : 0;
+    if (lo > 0) {
+        pw_f32_kernel<<<dim3((c + kPwT - 1) / kPwT, (rows + kPwT - 1) / kPwT), 256, 0, st>>>(x, w, bias, y, rows, c, c);
+        GRX_LAUNCHED("pw_f32_kernel");
+    }
+    const size_t tail = (size_t)B * (per - lo) * c;
+    if (tail > 0) {
+        pw_f32_rows_kernel<<<(unsigned)((tail + 255) / 256), 256, 0, st>>>(x, w, bias, y, B, per, lo, c, c);
+        GRX_LAUNCHED("pw_f32_rows_kernel");
+    }
+    return GRX_OK;
+}
+
 // The whole encode (encoder.go:432-489) of m->B utterances from m->mel into
 // m->x, enqueued on the stream.
 grx_status enqueue_encode(grx_conformer *m, hipStream_t st) {
@@ -1164,14 +1287,22 @@ grx_status enqueue_encode(grx_conformer *m, hipStream_t st) {
     const int R = B * T, hd = d / hp.heads;
     grx_status s;
     // pre-encoder (encoder.go:123-167)
-    sub_conv01_kernel<<<B * T2, c, (size_t)7 * (4 * F2 + 3) * 4, st>>>(m->mel, frames, nm, m->valid, m->w0, m->b0,
-                                                                       m->w2, m->b2, c, T1, F1, T2, F2, m->xq, m->xs);
+    sub_conv01_kernel<<<B * T2, c, (size_t)7 * (4 * F2 + 3) * 4, st>>>(
+        m->mel, frames, nm, m->valid, m->w0, m->b0, m->w2, m->b2, c, T1, F1, T2, F2, m->xq, m->xs, m->w3f ? m->subx : nullptr);
     GRX_LAUNCHED("sub_conv01_kernel");
-    if ((s = grx_gemm_q8_launch(st, m->w3, m->xq, m->xs, B * T2 * F2, m->b3, m->suby, c)) != GRX_OK) return s;
+    if (m->w3f) {
+        if ((s = pw_f32(st, m->subx, m->w3f, m->b3, m->suby, B, T2 * F2, c)) != GRX_OK) return s;
+    } else if ((s = grx_gemm_q8_launch(st, m->w3, m->xq, m->xs, B * T2 * F2, m->b3, m->suby, c)) != GRX_OK) {
+        return s;
+    }
     sub_dwconv_kernel<true><<<B * T * F3, c, 0, st>>>(m->suby, T2, F2, c, m->valid, 3, m->w5, m->b5, T, F3, m->xq,
-                                                      m->xs);
+                                                      m->xs, m->w6f ? m->subx : nullptr);
     GRX_LAUNCHED("sub_dwconv_kernel");
-    if ((s = grx_gemm_q8_launch(st, m->w6, m->xq, m->xs, B * T * F3, m->b6, m->sub0, c)) != GRX_OK) return s;
+    if (m->w6f) {
+        if ((s = pw_f32(st, m->subx, m->w6f, m->b6, m->sub0, B, T * F3, c)) != GRX_OK) return s;
+    } else if ((s = grx_gemm_q8_launch(st, m->w6, m->xq, m->xs, B * T * F3, m->b6, m->sub0, c)) != GRX_OK) {
+        return s;
+    }
     sub_flatten_kernel<<<R, 256, 0, st>>>(m->sub0, T, F3, c, m->valid, m->xq, m->xs);
     GRX_LAUNCHED("sub_flatten_kernel");
     {  // output Linear, then xscale (encoder.go:445-451)

@@ -132,11 +132,13 @@ CONFORMER_TINY = dict(d=64, heads=2, layers=2, dff=256, conv_kernel=9, sub_chann
                       xscaling=True, conv_norm="batch_norm")
 
 
-def conformer_model(hp: dict, seed: int = 9, pointwise_f16: bool = True) -> dict:
+def conformer_model(hp: dict, seed: int = 9, pointwise_f16: bool = True, pre_f32: bool = False) -> dict:
     """Random-init encoder tensors named as conformer/model.go:370-422 reads
     them.  Linear weights Q8_0 (scales sized so activations stay O(1)); the
     pointwise convolutions float16 when pointwise_f16 (as Q8_0 model files
-    keep them), else Q8_0; taps and vectors float32."""
+    keep them), else Q8_0; the pre-encoder's conv.3 and conv.6 float32 when
+    pre_f32 (as the reference's converter writes them), else Q8_0; taps and
+    vectors float32."""
     rng = np.random.default_rng(seed)
     d, c, ff, K = hp["d"], hp["sub_channels"], hp["dff"], hp["conv_kernel"]
     F = hp["n_mels"]
@@ -155,7 +157,7 @@ def conformer_model(hp: dict, seed: int = 9, pointwise_f16: bool = True) -> dict
         t[pe + n + ".weight"] = vec(c * 9, 0.3)
         t[pe + n + ".bias"] = vec(c)
     for n in ("conv.3", "conv.6"):
-        t[pe + n + ".weight"] = lin(c, c)
+        t[pe + n + ".weight"] = vec(c * c, 2.0 / np.sqrt(c)) if pre_f32 else lin(c, c)
         t[pe + n + ".bias"] = vec(c)
     t[pe + "out.weight"] = lin(d, c * F)
     t[pe + "out.bias"] = vec(d)

@@ -319,9 +319,25 @@ grx_status grx_conformer_destroy(grx_conformer *m);
  * ("enc.pre_encode.conv.0.weight", "enc.blocks.0.ff1.linear1.weight",
  * "enc.blocks.0.conv.bn.running_var", ...): Linear weights as ggml Q8_0 rows
  * (the pointwise convolutions may be float16 instead and are rounded by
- * Weight.ToQ8 at load, model.go:397-402), convolution taps [c][taps] and
- * vectors as float32.  Optional biases may be left out.  Shapes checked. */
+ * Weight.ToQ8 at load, model.go:397-402; the pre-encoder's conv.3 and
+ * conv.6 may be float32 and then take kern's float route), convolution taps
+ * [c][taps] and vectors as float32.  Optional biases may be left out.
+ * Shapes checked. */
 grx_status grx_conformer_set_tensor(grx_conformer *m, const char *name, const void *data, size_t nbytes);
+/* The encoder of a FastConformer GGUF file (conformer.Load, conformer/
+ * model.go:163-422): the architecture check, the encoder and decoder
+ * settings with the reference's checks and texts, then loadEncoder's
+ * tensors in its order (the first missing one reported as there, optional
+ * biases may be absent).  Linear weights go from the file to the device as
+ * stored (Q8_0); pointwise convolutions may be float16 or float32 (rounded
+ * by Weight.ToQ8); the pre-encoder's conv.3 / conv.6 may be float32 (the
+ * float route, as converted files hold them).  Tensors that do not fit the
+ * settings fail here ("the model file doesn't fit its own settings").
+ * Streaming forms (chunked attention, limited contexts, causal
+ * subsampling) are refused.  *hp_out (may be NULL) receives the
+ * dimensions. */
+grx_status grx_conformer_load_gguf(grx_ctx *ctx, const char *path, grx_conformer_hparams *hp_out,
+                                   grx_conformer **out);
 /* Encoder frames T for `frames` mel frames (three halvings, encoder.go:33-38). */
 int grx_conformer_frames_out(const grx_conformer *m, int frames);
 /* Model.encode of `batch` utterances: mel is [batch][n_mels][frames] float32

@@ -155,6 +155,9 @@ typedef struct {
     const uint8_t *w3, *w6, *out;             /* Q8_0 [c][c], [c][c], [d][c*F] */
     const float *b3, *b6, *out_b;
     orc_conf_block *blocks;
+    /* conv.3 / conv.6 as float32 [c][c] (the reference's converter keeps
+     * them float32): when set, Linear takes the float route, not w3 / w6 */
+    const float *w3f, *w6f;
 } orc_conformer;
 
 void orc_conf_rel_pos(float *out, int n, int d);

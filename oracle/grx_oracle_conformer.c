@@ -63,6 +63,11 @@ static void linear(float *y, const float *x, int m, const uint8_t *w, int n, int
     if (m > 0) orc_matmul_q8_int(y, n, x, k, m, w, n, k, bias, 1);
 }
 
+/* kern.Linear of a float32 weight (kern.go:185-201): ws.matmul, gemm.go:116-185 */
+static void linear_f32(float *y, const float *x, int m, const float *w, int n, int k, const float *bias) {
+    if (m > 0) orc_matmul_f32(y, n, x, k, w, k, m, n, k, bias);
+}
+
 /* encoder.go:33-38 (subOut), non-causal: padding one on each side. */
 static inline int sub_out(int n) { return (n - 1) / 2 + 1; }
 
@@ -178,7 +183,10 @@ int orc_conf_subsample(const orc_conformer *m, const float *mel, int frames, int
     L = sub_out(L);
     mask_rows(x2, T, L, (size_t)F * c);
     float *y = (float *)malloc((size_t)T * F * c * sizeof(float));
-    linear(y, x2, T * F, m->w3, c, c, m->b3);
+    if (m->w3f)
+        linear_f32(y, x2, T * F, m->w3f, c, c, m->b3);
+    else
+        linear(y, x2, T * F, m->w3, c, c, m->b3);
     free(x2);
     mask_rows(y, T, L, (size_t)F * c);
     relu_vec(y, (size_t)T * F * c);
@@ -188,7 +196,10 @@ int orc_conf_subsample(const orc_conformer *m, const float *mel, int frames, int
     L = sub_out(L);
     mask_rows(x3, T, L, (size_t)F * c);
     y = (float *)malloc((size_t)T * F * c * sizeof(float));
-    linear(y, x3, T * F, m->w6, c, c, m->b6);
+    if (m->w6f)
+        linear_f32(y, x3, T * F, m->w6f, c, c, m->b6);
+    else
+        linear(y, x3, T * F, m->w6, c, c, m->b6);
     free(x3);
     mask_rows(y, T, L, (size_t)F * c);
     relu_vec(y, (size_t)T * F * c);

@@ -507,7 +507,7 @@ class _CModel(C.Structure):
     _fields_ = ([(n, C.c_int) for n in ("d", "heads", "layers", "dff", "conv_kernel", "sub_channels", "n_mels",
                                         "xscaling", "conv_ln")] +
                 [(n, C.c_void_p) for n in ("w0", "b0", "w2", "b2", "w5", "b5", "w3", "w6", "out", "b3", "b6",
-                                           "out_b", "blocks")])
+                                           "out_b", "blocks", "w3f", "w6f")])
 
 
 def _declare_conformer(L):
@@ -583,10 +583,13 @@ class ConformerOracle:
         m.w0 = keep(_transpose_taps(tensors[pe + "conv.0.weight"], c, 9))
         m.w2 = keep(_transpose_taps(tensors[pe + "conv.2.weight"], c, 9))
         m.w5 = keep(_transpose_taps(tensors[pe + "conv.5.weight"], c, 9))
-        for f, n in (("b0", "conv.0.bias"), ("b2", "conv.2.bias"), ("b5", "conv.5.bias"), ("w3", "conv.3.weight"),
-                     ("w6", "conv.6.weight"), ("b3", "conv.3.bias"), ("b6", "conv.6.bias"),
-                     ("out", "out.weight"), ("out_b", "out.bias")):
+        for f, n in (("b0", "conv.0.bias"), ("b2", "conv.2.bias"), ("b5", "conv.5.bias"), ("b3", "conv.3.bias"),
+                     ("b6", "conv.6.bias"), ("out", "out.weight"), ("out_b", "out.bias")):
             setattr(m, f, keep(tensors[pe + n]))
+        # conv.3 / conv.6: Q8_0 bytes, or float32 values (the float route)
+        for f, n in (("w3", "conv.3.weight"), ("w6", "conv.6.weight")):
+            w = tensors[pe + n]
+            setattr(m, f + "f" if w.dtype == np.float32 else f, keep(w))
         blocks = (_CBlock * nl)()
         for i in range(nl):
             p = f"enc.blocks.{i}."

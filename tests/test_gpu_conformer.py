@@ -38,6 +38,27 @@ def test_tiny_encode_bit_exact(kern, orc, conv_norm, f16):
     enc.close()
 
 
+@pytest.mark.parametrize("seconds", [1.5, 0.07])
+def test_tiny_float32_pre_encoder_pointwise(kern, orc, seconds):
+    """conv.3 and conv.6 stored float32, as the reference's converter writes
+    them: kern.Linear's float route (rows in whole groups of six by the
+    k6x16 chain, the rest by gemvRows; at 0.07 s every row takes gemvRows),
+    bit-identical to the oracle."""
+    hp = dict(CONFORMER_TINY)
+    t = conformer_model(hp, seed=25, pre_f32=True)
+    assert t["enc.pre_encode.conv.3.weight"].dtype == np.float32
+    mel, frames, valid = _mels(hp, 2, seconds, 36)
+    vals = [valid, max(1, valid - 3)]
+    enc = _enc(kern, hp, t)
+    got, lens = enc.encode(mel, vals)
+    o = orc.ConformerOracle(hp, t)
+    for b in range(2):
+        want, L = o.encode(mel[b], vals[b])
+        assert lens[b] == L
+        assert np.array_equal(got[b].view(np.uint32), want.view(np.uint32)), (b, np.abs(got[b] - want).max())
+    enc.close()
+
+
 @pytest.mark.parametrize("rq", ["0", "8", "16"])
 def test_tiny_attention_variants_bit_exact(kern, orc, monkeypatch, rq):
     """The unstaged attention kernel and the LDS-staged one at 8 and 16 query
@@ -92,15 +113,16 @@ def test_bad_input_errors(kern):
     enc.close()
 
 
-@pytest.fixture(scope="module")
-def parakeet2():
+@pytest.fixture(scope="module", params=[False, True], ids=["q8_pre", "f32_pre"])
+def parakeet2(request):
     hp = dict(PARAKEET_TDT_06B, layers=2)
-    return hp, conformer_model(hp, seed=31)
+    return hp, conformer_model(hp, seed=31, pre_f32=request.param)
 
 
 def test_parakeet_width_two_layers_bit_exact(kern, orc, parakeet2):
     """10 s of noise, d 1024, 8 heads, FFN 4096, kernel 31, 128 mels: the
-    pre-encoder and two blocks bit-identical to the oracle."""
+    pre-encoder (its conv.3 and conv.6 Q8_0, or float32 as converted files
+    hold them) and two blocks bit-identical to the oracle."""
     hp, t = parakeet2
     mel, frames, valid = _mels(hp, 1, 10.0, 60)
     enc = _enc(kern, hp, t)
