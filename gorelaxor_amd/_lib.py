@@ -70,6 +70,8 @@ SIGNATURES = {
     "grx_whisper_set_encoder_output_stream": (i32, [vp, i32, vp, i32]),
     "grx_whisper_greedy_streams": (i32, [vp, vp, i32, i32, vp]),
     "grx_whisper_load_ggml": (i32, [vp, C.c_char_p, i32, vp, C.POINTER(vp)]),
+    "grx_whisper_sample_logits": (i32, [vp, vp, i32, vp, vp, C.c_float, C.c_float, vp]),
+    "grx_whisper_sample": (i32, [vp, i32, vp, vp, C.c_float, C.c_float, vp]),
     "grx_gguf_open": (i32, [C.c_char_p, C.POINTER(vp)]),
     "grx_gguf_parse": (i32, [vp, sz, C.POINTER(vp)]),
     "grx_gguf_read_meta": (i32, [C.c_char_p, C.POINTER(vp)]),
@@ -119,6 +121,24 @@ class ConformerHParams(C.Structure):
     """grx_conformer_hparams."""
     _fields_ = [(n, C.c_int) for n in ("d", "heads", "layers", "dff", "conv_kernel", "sub_channels", "n_mels",
                                        "xscaling", "conv_ln")]
+
+
+class WhisperRules(C.Structure):
+    """grx_whisper_rules."""
+    _fields_ = [(n, C.c_int) for n in ("eot", "sot", "translate", "transcribe", "solm", "prev", "nosp",
+                                       "no_timestamps", "beg", "n_lang", "space")] + [
+        ("suppress", C.POINTER(C.c_int32)), ("n_suppress", C.c_int), ("n_audio_ctx", C.c_int),
+        ("max_initial_ts", C.c_double)]
+
+
+class WhisperSeq(C.Structure):
+    """grx_whisper_seq."""
+    _fields_ = [(n, C.c_int) for n in ("n_tokens", "last", "penult", "has_ts", "seek_delta")]
+
+
+class WhisperToken(C.Structure):
+    """grx_whisper_token."""
+    _fields_ = [("id", C.c_int), ("tid", C.c_int), ("p", C.c_float), ("plog", C.c_float), ("force_ts", C.c_int)]
 
 
 class WhisperHParams(C.Structure):

@@ -39,6 +39,32 @@ struct grx_weight {
 
 grx_status grx_fail(grx_status s, const char *fmt, ...);
 
+// whisper_sample.hip: one row of logits through whisper's token rules and
+// sampler (the public grx_whisper_rules / grx_whisper_seq, resolved)
+struct GrxSampleArgs {
+    int n, eot, sot, not_, nosp, solm, translate, transcribe, prev, beg, n_lang, space, tid0;
+    int initial, last, penult, has_ts, seek_delta, n_suppress;
+    float temp, r;
+};
+struct GrxSampleOut {
+    int id, tid;
+    float p, plog;
+    int force_ts, n_terms;
+};
+#ifdef __cplusplus
+// scratch: 2 x 65536 floats
+grx_status grx_sample_launch(hipStream_t st, const float *logits, const GrxSampleArgs &a, const int *suppress,
+                             float *scratch, GrxSampleOut *out);
+// the rules and sequence state in kernel form (checks the token ids)
+grx_status grx_sample_args(const grx_whisper_rules *rules, const grx_whisper_seq *seq, int n, float temp, float r,
+                           GrxSampleArgs *a);
+// runs the sampler on device logits (or host ones, copied first) and
+// returns the token (synchronous)
+grx_status grx_sample_run(grx_ctx *ctx, const float *dev_logits, const float *host_logits, int n,
+                          const grx_whisper_rules *rules, const grx_whisper_seq *seq, float temp, float r,
+                          grx_whisper_token *out);
+#endif
+
 #ifdef __cplusplus
 #include <vector>
 // gguf.hip: a tensor's stored bytes and its ggml type code

@@ -1098,6 +1098,15 @@ static grx_status check_ready(grx_whisper *m, const char *fn) {
     return GRX_OK;
 }
 
+extern "C" grx_status grx_whisper_sample(grx_whisper *m, int stream, const grx_whisper_rules *rules,
+                                         const grx_whisper_seq *seq, float temp, float r, grx_whisper_token *out) {
+    if (!m) return grx_fail(GRX_EINVAL, "grx_whisper_sample: NULL model");
+    if (stream < 0 || stream >= m->S) return grx_fail(GRX_EINVAL, "grx_whisper_sample: stream %d of %d", stream, m->S);
+    if (!m->logits) return grx_fail(GRX_ESTATE, "grx_whisper_sample: nothing decoded yet");
+    return grx_sample_run(m->ctx, m->logits + (size_t)stream * m->hp.n_vocab, nullptr, m->hp.n_vocab, rules, seq,
+                          temp, r, out);
+}
+
 extern "C" grx_status grx_whisper_decode(grx_whisper *m, const int32_t *tokens, int n, float *logits, int32_t *next) {
     grx_status s = check_ready(m, "grx_whisper_decode");
     if (s != GRX_OK) return s;

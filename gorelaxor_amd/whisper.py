@@ -17,6 +17,61 @@ from . import _lib
 from .kern import Context, default_context
 
 
+def special_tokens(n_vocab: int) -> dict:
+    """The special token ids of a vocabulary of n_vocab (newVocab, whisper/
+    vocab.go:20-45): English models from eot 50256; multilingual ones
+    (n_vocab >= 51865) one later, with n_vocab - 51766 languages after sot and
+    the task and timestamp tokens moved by the language count past 98."""
+    v = dict(eot=50256, sot=50257, translate=50357, transcribe=50358, solm=50359, prev=50360, nosp=50361,
+             no_timestamps=50362, beg=50363, n_lang=0)
+    if n_vocab >= 51865:
+        n_lang = n_vocab - 51765 - 1
+        dt = n_lang - 98
+        v["eot"] += 1
+        v["sot"] += 1
+        for k in ("translate", "transcribe", "solm", "prev", "nosp", "no_timestamps", "beg"):
+            v[k] += dt
+        v["n_lang"] = n_lang
+    return v
+
+
+class Rules:
+    """grx_whisper_rules from a dict of special tokens plus the suppress
+    list (vocab.suppressed()), the " " token (-1 if none) and the model's
+    audio context."""
+
+    def __init__(self, specials: dict, suppress=(), space: int = -1, n_audio_ctx: int = 1500,
+                 max_initial_ts: float = 1.0):
+        self.suppress = np.ascontiguousarray(suppress, np.int32)
+        self.c = _lib.WhisperRules(**{k: int(specials[k]) for k in (
+            "eot", "sot", "translate", "transcribe", "solm", "prev", "nosp", "no_timestamps", "beg", "n_lang")},
+            space=space, n_suppress=self.suppress.size, n_audio_ctx=n_audio_ctx, max_initial_ts=max_initial_ts)
+        self.c.suppress = self.suppress.ctypes.data_as(C.POINTER(C.c_int32))
+
+
+def _seq(tokens=(), has_ts: bool = False, seek_delta: int = 0):
+    t = list(tokens)
+    return _lib.WhisperSeq(n_tokens=len(t), last=t[-1] if t else 0, penult=t[-2] if len(t) > 1 else 0,
+                           has_ts=int(has_ts), seek_delta=seek_delta)
+
+
+def _tok(t) -> dict:
+    return dict(id=t.id, tid=t.tid, p=t.p, plog=t.plog, force_ts=bool(t.force_ts))
+
+
+def sample_logits(logits: np.ndarray, rules: Rules, tokens=(), has_ts: bool = False, seek_delta: int = 0,
+                  temp: float = 0.0, r: float = 0.0, ctx: Context | None = None) -> dict:
+    """session.process + session.sample (whisper/transcribe.go:370-494) on
+    the GPU over one row of logits: {id, tid, p, plog, force_ts}."""
+    ctx = ctx or default_context()
+    lg = np.ascontiguousarray(logits, np.float32)
+    out = _lib.WhisperToken()
+    seq = _seq(tokens, has_ts, seek_delta)
+    _lib.call("grx_whisper_sample_logits", ctx.handle, lg.ctypes.data_as(C.c_void_p), lg.size, C.byref(rules.c),
+              C.byref(seq), temp, r, C.byref(out))
+    return _tok(out)
+
+
 class WhisperDecoder:
     """One decode session, or `streams` (2, 4 or 8) independent sessions
     stepping together with shared weights (each its own encoder output)."""
@@ -72,6 +127,15 @@ class WhisperDecoder:
         _lib.call("grx_whisper_greedy_streams", self.handle, p.ctypes.data_as(C.c_void_p), p.shape[1], n_steps,
                   out.ctypes.data_as(C.c_void_p))
         return out
+
+    def sample(self, rules: Rules, tokens=(), has_ts: bool = False, seek_delta: int = 0, temp: float = 0.0,
+               r: float = 0.0, stream: int = 0) -> dict:
+        """The token rules and sampler over stream `stream`'s last logits,
+        which stay on the device."""
+        out = _lib.WhisperToken()
+        seq = _seq(tokens, has_ts, seek_delta)
+        _lib.call("grx_whisper_sample", self.handle, stream, C.byref(rules.c), C.byref(seq), temp, r, C.byref(out))
+        return _tok(out)
 
     def reset(self) -> None:
         _lib.call("grx_whisper_reset", self.handle)

@@ -204,6 +204,45 @@ grx_status grx_whisper_greedy_streams(grx_whisper *m, const int32_t *prompts, in
 grx_status grx_whisper_load_ggml(grx_ctx *ctx, const char *path, int n_streams, grx_whisper_hparams *hp_out,
                                  grx_whisper **out);
 
+/* ---- whisper's token rules and sampler (whisper/transcribe.go:370-494) ---- */
+
+/* The vocabulary's special tokens (whisper/vocab.go:18-45) and the rules'
+ * settings. */
+typedef struct {
+    int eot, sot, translate, transcribe, solm, prev, nosp, no_timestamps, beg;
+    int n_lang;               /* language tokens after sot */
+    int space;                /* the id of " ", or -1 when the vocabulary has none */
+    const int32_t *suppress;  /* vocab.suppressed(), host memory */
+    int n_suppress;
+    int n_audio_ctx;          /* the model's, for the initial timestamp limit */
+    double max_initial_ts;    /* seconds (maxInitialTS, 1.0) */
+} grx_whisper_rules;
+/* What the rules read of a sequence (seq of transcribe.go:100-115). */
+typedef struct {
+    int n_tokens;        /* len(q.tokens): tokens sampled in this window */
+    int last, penult;    /* the last two of them (read only when present) */
+    int has_ts;          /* q.hasTS */
+    int seek_delta;      /* q.seekDelta */
+} grx_whisper_seq;
+/* tok of transcribe.go (id, best timestamp, probability, log probability);
+ * force_ts: timestamps together outweighed every text token. */
+typedef struct {
+    int id, tid;
+    float p, plog;
+    int force_ts;
+} grx_whisper_token;
+/* session.process + session.sample over n logits in host memory: the
+ * temperature, the suppression and timestamp rules, logSoftmax, softmaxInf,
+ * then the argmax (temp 0) or the draw against r (s.rng.Float32(), drawn
+ * by the caller).  Bit-identical to the reference's float32 arithmetic,
+ * its left-to-right sums included. */
+grx_status grx_whisper_sample_logits(grx_ctx *ctx, const float *logits, int n, const grx_whisper_rules *rules,
+                                     const grx_whisper_seq *seq, float temp, float r, grx_whisper_token *out);
+/* The same over the logits of stream `stream`'s last decode, which stay on
+ * the device. */
+grx_status grx_whisper_sample(grx_whisper *m, int stream, const grx_whisper_rules *rules,
+                              const grx_whisper_seq *seq, float temp, float r, grx_whisper_token *out);
+
 /* ---- GGUF model files (internal/gguf/gguf.go) ---- */
 
 /* A GGUF file (versions 2 and 3; tensors F32, F16, BF16, Q8_0) with the

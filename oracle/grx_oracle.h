@@ -169,6 +169,26 @@ int orc_conf_block_run(const orc_conformer *m, int i, float *x, int T, int L, co
 int orc_conformer_encode(const orc_conformer *m, const float *mel, int frames, int valid, int n_layers, float *out,
                          int *T_out, int *L_out);
 
+/* ---- whisper's token rules and sampler (whisper/transcribe.go:370-536) ---- */
+typedef struct {
+    int eot, sot, translate, transcribe, solm, prev, nosp, no_timestamps, beg;
+    int n_lang, space;
+    const int *suppress;
+    int n_suppress;
+    int n_audio_ctx;
+    double max_initial_ts;
+} orc_whisper_rules;
+typedef struct {
+    int n_tokens, last, penult, has_ts, seek_delta;
+} orc_whisper_seq;
+typedef struct {
+    int id, tid;
+    float p, plog;
+    int force_ts;
+} orc_whisper_token;
+void orc_whisper_sample(const float *logits, int n, const orc_whisper_rules *v, const orc_whisper_seq *q,
+                        float temp, float r, orc_whisper_token *out);
+
 #ifdef __cplusplus
 }
 #endif

@@ -655,3 +655,45 @@ class ConformerOracle:
         nl = self.hp["layers"] if layers is None else layers
         lib().orc_conformer_encode(C.byref(self._m), mel, frames, valid, nl, out, C.byref(t), C.byref(l))
         return out.reshape(T, self.hp["d"]), l.value
+
+
+# ---- whisper's token rules and sampler (whisper/transcribe.go:370-536) ----
+
+class _ORules(C.Structure):
+    _fields_ = [(n, C.c_int) for n in ("eot", "sot", "translate", "transcribe", "solm", "prev", "nosp",
+                                       "no_timestamps", "beg", "n_lang", "space")] + [
+        ("suppress", C.POINTER(C.c_int)), ("n_suppress", C.c_int), ("n_audio_ctx", C.c_int),
+        ("max_initial_ts", C.c_double)]
+
+
+class _OSeq(C.Structure):
+    _fields_ = [(n, C.c_int) for n in ("n_tokens", "last", "penult", "has_ts", "seek_delta")]
+
+
+class _OTok(C.Structure):
+    _fields_ = [("id", C.c_int), ("tid", C.c_int), ("p", C.c_float), ("plog", C.c_float), ("force_ts", C.c_int)]
+
+
+def whisper_sample(logits, specials: dict, suppress=(), space: int = -1, tokens=(), has_ts: bool = False,
+                   seek_delta: int = 0, temp: float = 0.0, r: float = 0.0, n_audio_ctx: int = 1500,
+                   max_initial_ts: float = 1.0) -> dict:
+    """session.process + session.sample over one row of logits:
+    {id, tid, p, plog, force_ts}."""
+    L = lib()
+    if not hasattr(L.orc_whisper_sample, "_declared"):
+        L.orc_whisper_sample.argtypes = [_f32p, C.c_int, C.c_void_p, C.c_void_p, C.c_float, C.c_float, C.c_void_p]
+        L.orc_whisper_sample.restype = None
+        L.orc_whisper_sample._declared = True
+    lg = _f32(logits).ravel()
+    sup = np.ascontiguousarray(suppress, np.int32)
+    rules = _ORules(**{k: int(specials[k]) for k in ("eot", "sot", "translate", "transcribe", "solm", "prev",
+                                                      "nosp", "no_timestamps", "beg", "n_lang")},
+                    space=space, n_suppress=sup.size, n_audio_ctx=n_audio_ctx, max_initial_ts=max_initial_ts)
+    rules.suppress = sup.ctypes.data_as(C.POINTER(C.c_int))
+    t = list(tokens)
+    seq = _OSeq(n_tokens=len(t), last=t[-1] if t else 0, penult=t[-2] if len(t) > 1 else 0, has_ts=int(has_ts),
+                seek_delta=seek_delta)
+    out = _OTok()
+    L.orc_whisper_sample(lg, lg.size, C.byref(rules), C.byref(seq), temp, r, C.byref(out))
+    return dict(id=out.id, tid=out.tid, p=out.p, plog=out.plog, force_ts=bool(out.force_ts))
+
