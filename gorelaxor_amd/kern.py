@@ -131,6 +131,29 @@ def NewQ8(rows: int, cols: int, b, ctx: Context | None = None) -> Weight:
     return Weight(h, rows, cols, ctx)
 
 
+def LinearFloat(dst: np.ndarray, x: np.ndarray, w: Weight, bias=None) -> None:
+    """kern.Linear of one row on a weight that keeps its rows (the float
+    route, kern.go:185-196 -> gemvRows): dot4q8avx by groups of four rows,
+    dotQ8Go for the last partial group, then the bias."""
+    if x.dtype != np.float32 or x.size < w.Cols or dst.dtype != np.float32 or dst.size < w.Rows:
+        raise IndexError("kern: Linear buffers shorter than the weight")
+    if bias is not None and (bias.dtype != np.float32 or bias.size < w.Rows):
+        raise IndexError("kern: bias shorter than Rows")
+    _lib.call("grx_linear_q8_float", w.ctx.handle, _ptr(dst), _ptr(x), w.handle, _ptr(bias))
+
+
+def LinearF32(dst: np.ndarray, x: np.ndarray, w: np.ndarray, rows: int, cols: int, bias=None,
+              ctx: Context | None = None) -> None:
+    """kern.Linear of one row on a float32 weight (gemvRows: dotF32x4 by
+    groups of four rows, dotF32Go for the rest, then the bias)."""
+    ctx = ctx or default_context()
+    w = np.ascontiguousarray(w, np.float32)
+    if w.size < rows * cols or x.size < cols or dst.size < rows:
+        raise IndexError("kern: Linear buffers shorter than the weight")
+    _lib.call("grx_linear_f32", ctx.handle, _ptr(dst), _ptr(np.ascontiguousarray(x, np.float32)), _ptr(w), rows,
+              cols, _ptr(None if bias is None else np.ascontiguousarray(bias, np.float32)))
+
+
 def ToQ8(v: np.ndarray, rows: int, cols: int, ctx: Context | None = None) -> np.ndarray:
     """Weight.ToQ8 of an F32 matrix (kern.go:136-170) on the GPU: the Q8_0 bytes."""
     ctx = ctx or default_context()
@@ -198,5 +221,5 @@ def vec_dev(fn: int, y, x, n: int, ctx: Context | None = None) -> None:
 
 
 __all__ = ["QK", "Q8Bytes", "F32", "F16", "Q8_0", "Context", "default_context", "device_count", "Weight",
-           "NewQ8", "ToQ8", "MatMul", "Linear", "matmul_dev", "quant_act_dev", "matmul_prequant_dev",
+           "NewQ8", "ToQ8", "MatMul", "Linear", "LinearFloat", "LinearF32", "matmul_dev", "quant_act_dev", "matmul_prequant_dev",
            "block_dots_dev", "vec_dev", "VEC_EXPF", "VEC_EXP8", "VEC_GELU", "GrxError"]

@@ -131,6 +131,17 @@ grx_status grx_block_dots_dev(grx_ctx *ctx, int32_t *s, const int8_t *q, int m,
 enum { GRX_VEC_EXPF = 0, GRX_VEC_EXP8 = 1, GRX_VEC_GELU = 2 };
 grx_status grx_vec_dev(grx_ctx *ctx, int fn, float *y, const float *x, int n);
 
+/* kern.Linear of ONE row through the float route (kern.go:185-196 ->
+ * gemvRows, gemm.go:195-259): what the reference does for m = 1 when the
+ * weight keeps its rows (no DropRows) - dot4q8avx for rows in whole groups
+ * of four, dotQ8Go for the rest, then the bias - instead of the int8 route
+ * that grx_linear_q8 takes.  Host buffers. */
+grx_status grx_linear_q8_float(grx_ctx *ctx, float *dst, const float *x, const grx_weight *w, const float *bias);
+/* The same for a float32 weight (rows x cols, row-major, host memory):
+ * dotF32x4 for rows in whole groups of four, dotF32Go for the rest. */
+grx_status grx_linear_f32(grx_ctx *ctx, float *dst, const float *x, const float *w, int rows, int cols,
+                          const float *bias);
+
 /* ---- whisper-shaped text decoder with Q8_0 weights ---- */
 
 /* The decoder graph of whisper/decoder.go:33-140 with every matrix a Q8_0

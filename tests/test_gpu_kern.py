@@ -363,3 +363,37 @@ def test_device_pointer_forms(kern, orc, dev):
     kern.matmul_prequant_dev(dy2, dq, ds, m, w, db)
     kern.default_context().sync()
     assert _bits_equal(dy2.download(np.float32, (m, n)), want)
+
+
+@pytest.mark.parametrize("n", [1, 3, 4, 5, 63, 65, 130, 515, 2561])
+@pytest.mark.parametrize("k", [32, 96, 640, 1024])
+def test_linear_float_route_bit_exact(kern, orc, n, k):
+    """The float route of a Q8_0 weight that keeps its rows (m = 1):
+    dot4q8avx for rows in whole groups of four, dotQ8Go for the last partial
+    group (n % 4 rows), then the bias - bit for bit, with subnormal scales."""
+    rng = np.random.default_rng(n * 7 + k)
+    w8 = q8_weight(rng, n, k, sigma=0.05)
+    x = rng.standard_normal(k).astype(np.float32)
+    bias = rng.standard_normal(n).astype(np.float32)
+    w = kern.NewQ8(n, k, w8)
+    for b in (None, bias):
+        got = np.zeros(n, np.float32)
+        kern.LinearFloat(got, x, w, b)
+        want = orc.matmul_q8_float(x, w8, n, k, b)[0]
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), (n, k, b is None)
+
+
+@pytest.mark.parametrize("n,k", [(1, 16), (3, 17), (4, 32), (5, 47), (64, 256), (67, 100), (512, 32), (32, 512)])
+def test_linear_f32_bit_exact(kern, orc, n, k):
+    """A float32 weight's one-row product: dotF32x4 (the 16-wide kernel over
+    k &^ 15 and dotF32Go past it) for rows in groups of four, dotF32Go for
+    the rest, then the bias."""
+    rng = np.random.default_rng(n + 31 * k)
+    w = rng.standard_normal((n, k)).astype(np.float32)
+    x = rng.standard_normal(k).astype(np.float32)
+    bias = rng.standard_normal(n).astype(np.float32)
+    for b in (None, bias):
+        got = np.zeros(n, np.float32)
+        kern.LinearF32(got, x, w, n, k, b)
+        want = orc.matmul_f32(x[None], w, b)[0]
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), (n, k, b is None)
