@@ -98,6 +98,8 @@ SIGNATURES = {
     "grx_gguf_weight_q8": (i32, [vp, vp, C.c_char_p, C.POINTER(vp)]),
     "grx_pocket_create": (i32, [vp, vp, C.POINTER(vp)]),
     "grx_pocket_load_gguf": (i32, [vp, C.c_char_p, i32, vp, C.POINTER(vp)]),
+    "grx_pocket_flow_init": (i32, [vp, i32, i32, i32]),
+    "grx_pocket_speak": (i32, [vp, vp, vp, i32, vp, vp]),
     "grx_pocket_destroy": (i32, [vp]),
     "grx_pocket_set_tensor": (i32, [vp, C.c_char_p, vp, sz]),
     "grx_pocket_reset": (i32, [vp]),

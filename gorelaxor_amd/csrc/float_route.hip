@@ -23,11 +23,27 @@ namespace {
 
 constexpr int kFloatWaves = 4;  // tiles of 64 rows per workgroup
 
+// What happens to output row `row` of n after the bias (GrxFloatEpi):
+// stored, stored through kern.SiLU (siluAVX's x/(EXP8(0-x)+1) for the rows
+// below n &^ 7, siluGo's x/(1+expf(-x)) past them, kernels_amd64.go:241-250),
+// or added to h as h += gate*o (unfused).
+__device__ __forceinline__ void float_epilogue(const GrxFloatEpi &e, float o, int row, int n, float *y) {
+    if (e.kind == GRX_FEPI_SILU) {
+        const float a = __fdiv_rn(o, __fadd_rn(grx_exp8(__fsub_rn(0.f, o)), 1.f));
+        const float b = __fdiv_rn(o, __fadd_rn(1.f, grx_expf_go(-o)));
+        y[row] = row < (n & ~7) ? a : b;
+    } else if (e.kind == GRX_FEPI_GATE) {
+        y[row] = __fadd_rn(y[row], __fmul_rn(e.gate[row], o));
+    } else {
+        y[row] = o;
+    }
+}
+
 __global__ __launch_bounds__(64 * kFloatWaves) void q8_float_gemv_kernel(const float *__restrict__ x, int k,
                                                                           const int8_t *__restrict__ qs,
                                                                           const uint16_t *__restrict__ ds, int nb,
                                                                           int n, const float *__restrict__ bias,
-                                                                          float *__restrict__ y) {
+                                                                          float *__restrict__ y, GrxFloatEpi e) {
     extern __shared__ __align__(16) float xs[];
     for (int i = threadIdx.x; i < k; i += blockDim.x) xs[i] = x[i];
     __syncthreads();
@@ -70,12 +86,13 @@ __global__ __launch_bounds__(64 * kFloatWaves) void q8_float_gemv_kernel(const f
     }
     float o = avx ? hsum8(acc) : s;
     if (bias) o = __fadd_rn(o, bias[row]);
-    y[row] = o;
+    float_epilogue(e, o, row, n, y);
 }
 
 __global__ __launch_bounds__(256) void f32_gemv_kernel(const float *__restrict__ x, int k,
                                                        const float *__restrict__ w, int n,
-                                                       const float *__restrict__ bias, float *__restrict__ y) {
+                                                       const float *__restrict__ bias, float *__restrict__ y,
+                                                       GrxFloatEpi e) {
     extern __shared__ __align__(16) float xs[];
     for (int i = threadIdx.x; i < k; i += blockDim.x) xs[i] = x[i];
     __syncthreads();
@@ -84,28 +101,29 @@ __global__ __launch_bounds__(256) void f32_gemv_kernel(const float *__restrict__
     const float *wr = w + (size_t)row * k;
     float o = row < (n & ~3) ? dot_x4(xs, wr, k) : dot_go(xs, wr, k);
     if (bias) o = __fadd_rn(o, bias[row]);
-    y[row] = o;
+    float_epilogue(e, o, row, n, y);
 }
 
 constexpr int kMaxK = 32768;
 
 }  // namespace
 
-grx_status grx_float_gemv_q8(hipStream_t st, const grx_weight *w, const float *x, const float *bias, float *y) {
+grx_status grx_float_gemv_q8(hipStream_t st, const grx_weight *w, const float *x, const float *bias, float *y,
+                             GrxFloatEpi e) {
     if (w->cols > kMaxK) return grx_fail(GRX_ESIZE, "float route: %d columns (at most %d)", w->cols, kMaxK);
     if (w->rows == 0) return GRX_OK;
     const int blocks = grx_ceil_div(w->tiles, kFloatWaves);
     q8_float_gemv_kernel<<<blocks, 64 * kFloatWaves, (size_t)w->cols * 4, st>>>(x, w->cols, w->qs, w->ds, w->nb,
-                                                                                 w->rows, bias, y);
+                                                                                 w->rows, bias, y, e);
     GRX_LAUNCHED("q8_float_gemv_kernel");
     return GRX_OK;
 }
 
 grx_status grx_float_gemv_f32(hipStream_t st, const float *w, int n, int k, const float *x, const float *bias,
-                              float *y) {
+                              float *y, GrxFloatEpi e) {
     if (k > kMaxK) return grx_fail(GRX_ESIZE, "float route: %d columns (at most %d)", k, kMaxK);
     if (n == 0) return GRX_OK;
-    f32_gemv_kernel<<<grx_ceil_div(n, 256), 256, (size_t)k * 4, st>>>(x, k, w, n, bias, y);
+    f32_gemv_kernel<<<grx_ceil_div(n, 256), 256, (size_t)k * 4, st>>>(x, k, w, n, bias, y, e);
     GRX_LAUNCHED("f32_gemv_kernel");
     return GRX_OK;
 }

@@ -41,9 +41,15 @@ grx_status grx_fail(grx_status s, const char *fmt, ...);
 
 // float_route.hip: kern.MatMul's float route for one row of activations
 // (device buffers), for a Q8_0 weight that keeps its rows and for float32
-grx_status grx_float_gemv_q8(hipStream_t st, const grx_weight *w, const float *x, const float *bias, float *y);
+enum { GRX_FEPI_STORE = 0, GRX_FEPI_SILU = 1, GRX_FEPI_GATE = 2 };
+struct GrxFloatEpi {
+    int kind = GRX_FEPI_STORE;
+    const float *gate = nullptr;  // GATE: y[row] += gate[row] * (product + bias)
+};
+grx_status grx_float_gemv_q8(hipStream_t st, const grx_weight *w, const float *x, const float *bias, float *y,
+                             GrxFloatEpi e = GrxFloatEpi());
 grx_status grx_float_gemv_f32(hipStream_t st, const float *w, int n, int k, const float *x, const float *bias,
-                              float *y);
+                              float *y, GrxFloatEpi e = GrxFloatEpi());
 
 // whisper_sample.hip: one row of logits through whisper's token rules and
 // sampler (the public grx_whisper_rules / grx_whisper_seq, resolved)

@@ -30,6 +30,7 @@
 
 #include "grx_float.h"
 #include "grx_internal.h"
+#include "pocket_internal.h"
 
 namespace {
 
@@ -350,36 +351,6 @@ __global__ __launch_bounds__(kThreads) void finish_kernel(const float *__restric
 
 // ---------------------------------------------------------------- host side
 
-struct PLayer {
-    grx_weight *qkv = nullptr, *out = nullptr, *ff1 = nullptr, *ff2 = nullptr;
-    float *n1w, *n1b, *n2w, *n2b;
-    float *k, *v;
-};
-
-struct grx_pocket {
-    grx_ctx *ctx = nullptr;
-    grx_pocket_hparams hp{};
-    std::map<std::string, std::vector<uint8_t>> host;
-    bool ready = false;
-    std::vector<PLayer> L;
-    std::vector<void *> allocs;
-    float *input = nullptr, *bos = nullptr, *onw = nullptr, *onb = nullptr, *eosw = nullptr;
-    float eosb = 0.f;
-    float *rope_cos = nullptr, *rope_sin = nullptr;
-    // activations, room for max_pos rows
-    float *x = nullptr, *q = nullptr, *att = nullptr, *ff = nullptr;
-    int8_t *att_q = nullptr, *ff_q = nullptr;
-    float *att_s = nullptr, *ff_s = nullptr;
-    float *sc = nullptr, *vt = nullptr;       // prefix attention scratch
-    float *lat = nullptr;                     // latents of a run of frames
-    float *out_hist = nullptr, *eos_hist = nullptr;
-    int *pos = nullptr, *frame = nullptr;
-    int pos_host = 0;
-    int lat_cap = 0;
-    hipGraphExec_t exec = nullptr;
-    hipGraph_t graph = nullptr;
-};
-
 namespace {
 
 struct PExpect {
@@ -509,7 +480,8 @@ grx_status pfinalize(grx_pocket *m) {
     if ((s = palloc_t(m, 1, &m->frame)) != GRX_OK) return s;
     GRX_HIP(hipMemset(m->pos, 0, 4));
     GRX_HIP(hipMemset(m->frame, 0, 4));
-    m->host.clear();
+    // the transformer's host copies go; the flow head's stay until its own set-up
+    for (const PExpect &e : pexpected(hp)) m->host.erase(e.name);
     m->ready = true;
     return GRX_OK;
 }
@@ -629,6 +601,12 @@ grx_status enqueue_frame(grx_pocket *m, hipStream_t st, const float *lat_base, c
 
 }  // namespace
 
+grx_status pocket_finalize(grx_pocket *m) { return pfinalize(m); }
+grx_status pocket_enqueue_frame(grx_pocket *m, hipStream_t st, const float *lat_base, const int *frame) {
+    return enqueue_frame(m, st, lat_base, frame);
+}
+grx_status pocket_alloc(grx_pocket *m, size_t bytes, void **out) { return palloc(m, bytes, out); }
+
 extern "C" grx_status grx_pocket_create(grx_ctx *ctx, const grx_pocket_hparams *hp, grx_pocket **out) {
     if (!ctx || !hp || !out) return grx_fail(GRX_EINVAL, "grx_pocket_create: NULL argument");
     *out = nullptr;
@@ -652,6 +630,11 @@ extern "C" grx_status grx_pocket_destroy(grx_pocket *m) {
     GRX_HIP(hipStreamSynchronize(m->ctx->stream));
     if (m->exec) (void)hipGraphExecDestroy(m->exec);
     if (m->graph) (void)hipGraphDestroy(m->graph);
+    if (m->speak_exec) (void)hipGraphExecDestroy(m->speak_exec);
+    if (m->speak_graph) (void)hipGraphDestroy(m->speak_graph);
+    for (FlowMat *f : {&m->flow.cond, &m->flow.input, &m->flow.final_ada, &m->flow.out}) grx_weight_destroy(f->q8);
+    for (FlowRes &r : m->flow.res)
+        for (FlowMat *f : {&r.ada, &r.fc1, &r.fc2}) grx_weight_destroy(f->q8);
     for (PLayer &L : m->L)
         for (grx_weight *w : {L.qkv, L.out, L.ff1, L.ff2}) grx_weight_destroy(w);
     for (void *p : m->allocs) (void)hipFree(p);
@@ -661,12 +644,21 @@ extern "C" grx_status grx_pocket_destroy(grx_pocket *m) {
 
 extern "C" grx_status grx_pocket_set_tensor(grx_pocket *m, const char *name, const void *data, size_t nbytes) {
     if (!m || !name || (!data && nbytes)) return grx_fail(GRX_EINVAL, "grx_pocket_set_tensor: NULL argument");
-    if (m->ready) return grx_fail(GRX_ESTATE, "grx_pocket_set_tensor: the model is in use already");
+    const uint8_t *p = static_cast<const uint8_t *>(data);
+    size_t qa = 0, fb = 0;  // the flow head's tensors, once declared
+    if (pocket_flow_tensor(m, name, &qa, &fb)) {
+        if (nbytes != qa && nbytes != fb)
+            return grx_fail(GRX_ESIZE, "tensor %s has the wrong shape (%zu bytes, want %zu or %zu)", name, nbytes, qa,
+                            fb);
+        if (m->flow.ready) return grx_fail(GRX_ESTATE, "grx_pocket_set_tensor: the flow head is in use already");
+        m->host[name].assign(p, p + nbytes);
+        return GRX_OK;
+    }
     for (const PExpect &e : pexpected(m->hp)) {
         if (e.name != name) continue;
+        if (m->ready) return grx_fail(GRX_ESTATE, "grx_pocket_set_tensor: the model is in use already");
         if (nbytes != e.bytes)
             return grx_fail(GRX_ESIZE, "tensor %s has the wrong shape (%zu bytes, want %zu)", name, nbytes, e.bytes);
-        const uint8_t *p = static_cast<const uint8_t *>(data);
         m->host[name].assign(p, p + nbytes);
         return GRX_OK;
     }
@@ -750,7 +742,7 @@ extern "C" grx_status grx_pocket_frames(grx_pocket *m, const float *latents, int
                 m->graph = nullptr;
             }
         }
-        GRX_HIP(hipMalloc(&m->lat, (size_t)hp.max_pos * hp.ldim * 4));
+        GRX_HIP(hipMalloc(&m->lat, (size_t)(hp.max_pos + 1) * hp.ldim * 4));  // + the row a flow head writes last
         m->allocs.push_back(m->lat);
         m->lat_cap = hp.max_pos;
     }

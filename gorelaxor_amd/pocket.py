@@ -47,6 +47,26 @@ class PocketLM:
         a = np.ascontiguousarray(arr)
         _lib.call("grx_pocket_set_tensor", self.handle, name.encode(), a.ctypes.data_as(C.c_void_p), a.nbytes)
 
+    def flow_init(self, dim: int, depth: int, decode_steps: int) -> None:
+        """Declare the flow head (pockettts.flow.dim, flow.depth,
+        decode_steps); its flow.* tensors then bind by name."""
+        _lib.call("grx_pocket_flow_init", self.handle, dim, depth, decode_steps)
+
+    def speak(self, noise: np.ndarray, first_latent=None):
+        """speakChunk's frame loop on the device: one frame per noise row
+        (ldim values each), each fed the previous frame's sampled latent
+        (the first: first_latent, or bos).  Returns (latents [n][ldim], eos [n])."""
+        ld = self.hp["ldim"]
+        noise = np.ascontiguousarray(noise, np.float32).reshape(-1, ld)
+        n = noise.shape[0]
+        lat = np.zeros((n, ld), np.float32)
+        eos = np.zeros(n, np.float32)
+        fl = None if first_latent is None else np.ascontiguousarray(first_latent, np.float32)
+        _lib.call("grx_pocket_speak", self.handle, None if fl is None else fl.ctypes.data_as(C.c_void_p),
+                  noise.ctypes.data_as(C.c_void_p), n, lat.ctypes.data_as(C.c_void_p),
+                  eos.ctypes.data_as(C.c_void_p))
+        return lat, eos
+
     def reset(self) -> None:
         _lib.call("grx_pocket_reset", self.handle)
 

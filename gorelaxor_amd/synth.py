@@ -115,6 +115,46 @@ def pocket_model(hp: dict, seed: int = 5) -> dict:
     return t
 
 
+POCKET_FLOW = dict(dim=512, depth=6, steps=1)
+POCKET_FLOW_TINY = dict(dim=64, depth=2, steps=2)
+
+
+def pocket_flow_model(hp: dict, fhp: dict, seed: int = 12, q8: bool = True) -> dict:
+    """Random-init flow head (pockettts/model.go:230-247 names), typed as the
+    reference's converter types them: matrices of at least 64 x 64 whose rows
+    are whole Q8_0 blocks Q8_0 (when q8), the rest float32; the time
+    embedders' frequencies exp(-ln(10^4) i/128) as in the model."""
+    rng = np.random.default_rng(seed)
+    D, d, ld = fhp["dim"], hp["d"], hp["ldim"]
+    t = {}
+
+    def vec(n, scale=0.1, base=0.0):
+        return (base + scale * rng.standard_normal(n)).astype(np.float32)
+
+    def mat(rows, cols, gain=1.0):
+        if q8 and rows >= 64 and cols >= 64 and cols % QK == 0:
+            return q8_weight(rng, rows, cols, sigma=gain * 2.0 / np.sqrt(cols))
+        return (rng.standard_normal(rows * cols) * gain / np.sqrt(cols)).astype(np.float32)
+
+    t["flow.cond.weight"], t["flow.cond.bias"] = mat(D, d), vec(D)
+    t["flow.input.weight"], t["flow.input.bias"] = mat(D, ld), vec(D)
+    for i in range(2):
+        p = f"flow.time.{i}."
+        t[p + "freqs"] = np.exp(-np.log(1e4) * np.arange(128) / 128).astype(np.float32)
+        t[p + "fc1.weight"], t[p + "fc1.bias"] = mat(D, 256), vec(D)
+        t[p + "fc2.weight"], t[p + "fc2.bias"] = mat(D, D), vec(D)
+        t[p + "norm.alpha"] = vec(D, 0.1, 1.0)
+    for i in range(fhp["depth"]):
+        p = f"flow.res.{i}."
+        t[p + "norm.weight"], t[p + "norm.bias"] = vec(D, 0.1, 1.0), vec(D)
+        t[p + "fc1.weight"], t[p + "fc1.bias"] = mat(D, D), vec(D)
+        t[p + "fc2.weight"], t[p + "fc2.bias"] = mat(D, D, 0.5), vec(D)
+        t[p + "ada.weight"], t[p + "ada.bias"] = mat(3 * D, D, 0.5), vec(3 * D)
+    t["flow.final.ada.weight"], t["flow.final.ada.bias"] = mat(2 * D, D, 0.5), vec(2 * D)
+    t["flow.final.out.weight"], t["flow.final.out.bias"] = mat(ld, D), vec(ld)
+    return t
+
+
 def pocket_inputs(hp: dict, frames: int, prefix: int = 64, seed: int = 6):
     """The text prefix (prefix x d random embedding rows) and teacher-forced
     latents (frames x ldim, N(0,1)), seeded."""

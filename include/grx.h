@@ -332,6 +332,24 @@ grx_status grx_pocket_set_tensor(grx_pocket *m, const char *name, const void *da
  * the dimensions.  The flow head, Mimi and the tokenizer are not read. */
 grx_status grx_pocket_load_gguf(grx_ctx *ctx, const char *path, int max_pos, grx_pocket_hparams *hp_out,
                                 grx_pocket **out);
+/* Declare the flow head (SimpleMLPAdaLN, pockettts/lm.go:27-160): its width
+ * (pockettts.flow.dim), residual blocks (pockettts.flow.depth) and LSD steps
+ * per latent (pockettts.decode_steps).  Its tensors then bind by their
+ * names ("flow.cond.weight", "flow.res.0.ada.weight", "flow.time.1.freqs",
+ * "flow.final.out.weight", ...): matrices as ggml Q8_0 rows or float32
+ * (as the file stores them; each takes kern's float route, as the
+ * reference's unpacked weights do), vectors float32. */
+grx_status grx_pocket_flow_init(grx_pocket *m, int dim, int depth, int decode_steps);
+/* The frame loop of speakChunk (pockettts/speak.go:146-176) on the device:
+ * n frames, each a transformer step (flowLM.step, fed the previous frame's
+ * latent; the first frame is fed first_latent, or bos when NULL) and the
+ * flow head's sample from its output and noise[k] (ldim values per frame,
+ * drawn and scaled by the caller as speakChunk does), one captured graph a
+ * frame.  latents [n][ldim] receives each sampled latent (before the
+ * mean/std scaling), eos [n] the end-of-speech logits; either may be NULL.
+ * The caller applies the end-of-speech rule. */
+grx_status grx_pocket_speak(grx_pocket *m, const float *first_latent, const float *noise, int n, float *latents,
+                            float *eos);
 /* Empty the caches (position 0). */
 grx_status grx_pocket_reset(grx_pocket *m);
 int grx_pocket_pos(const grx_pocket *m);

@@ -9,6 +9,7 @@ github.com/xattribution/gorelaxor) the C restatement follows.
 from __future__ import annotations
 
 import ctypes as C
+import math
 import os
 import subprocess
 
@@ -697,3 +698,88 @@ def whisper_sample(logits, specials: dict, suppress=(), space: int = -1, tokens=
     L.orc_whisper_sample(lg, lg.size, C.byref(rules), C.byref(seq), temp, r, C.byref(out))
     return dict(id=out.id, tid=out.tid, p=out.p, plog=out.plog, force_ts=bool(out.force_ts))
 
+
+
+# ---- pocket-TTS flow head (pockettts/lm.go:27-160) ----
+
+class PocketFlowOracle:
+    """flowHead (SimpleMLPAdaLN) over tensors named as pockettts/model.go:
+    230-247 reads them; a matrix is Q8_0 bytes (the float route of a weight
+    that keeps its rows) or float32 [rows][cols]."""
+
+    def __init__(self, hp: dict, dim: int, depth: int, steps: int, tensors: dict):
+        self.hp, self.dim, self.depth, self.steps, self.t = hp, dim, depth, steps, tensors
+        self.tc = self.time_conds(steps)
+
+    def linear(self, name: str, x: np.ndarray, rows: int, cols: int) -> np.ndarray:
+        """linear1 (lm.go:55-57): kern.Linear of one row, float route."""
+        w = self.t[name + ".weight"]
+        bias = self.t.get(name + ".bias")
+        x = _f32(x)
+        if w.dtype == np.uint8:
+            return matmul_q8_float(x, w, rows, cols, bias)[0]
+        return matmul_f32(x[None], _f32(w).reshape(rows, cols), bias)[0]
+
+    def embed(self, e: int, t: float) -> np.ndarray:
+        """timeEmbed.embed (lm.go:59-87)."""
+        p = f"flow.time.{e}."
+        f = self.t[p + "freqs"]
+        half = f.size
+        x = np.zeros(2 * half, np.float32)
+        t32 = np.float32(t)
+        for i in range(half):
+            a = float(np.float32(t32 * f[i]))
+            x[i] = np.float32(math.cos(a))
+            x[half + i] = np.float32(math.sin(a))
+        h = silu(self.linear(p + "fc1", x, self.dim, 2 * half))
+        y = self.linear(p + "fc2", h, self.dim, self.dim)
+        s = 0.0
+        for v in y:
+            s += float(v)
+        mean = s / len(y)
+        q = 0.0
+        for v in y:
+            q += (float(v) - mean) * (float(v) - mean)
+        inv = np.float32(1 / math.sqrt(q / (len(y) - 1) + 1e-5))
+        alpha = self.t[p + "norm.alpha"]
+        return (y * (alpha * inv).astype(np.float32)).astype(np.float32)
+
+    def time_conds(self, steps: int):
+        """flowHead.timeConds (lm.go:89-104)."""
+        out = []
+        for i in range(steps):
+            s = self.embed(0, float(np.float32(i / steps)))
+            t = self.embed(1, float(np.float32((i + 1) / steps)))
+            out.append(((s + t) / np.float32(2)).astype(np.float32))
+        return out
+
+    def net(self, y: np.ndarray, x: np.ndarray) -> np.ndarray:
+        """flowHead.net (lm.go:124-160)."""
+        D = self.dim
+        h = self.linear("flow.input", x, D, self.hp["ldim"])
+        sy = silu(y)
+        for i in range(self.depth):
+            p = f"flow.res.{i}."
+            mod = self.linear(p + "ada", sy, 3 * D, D)
+            shift, scale, gate = mod[:D], mod[D:2 * D], mod[2 * D:]
+            n = layernorm_f64(h, self.t[p + "norm.weight"], self.t[p + "norm.bias"], 1e-6)
+            n = (n * (np.float32(1) + scale) + shift).astype(np.float32)
+            m = silu(self.linear(p + "fc1", n, D, D))
+            n = self.linear(p + "fc2", m, D, D)
+            h = (h + gate * n).astype(np.float32)
+        mod = self.linear("flow.final.ada", sy, 2 * D, D)
+        shift, scale = mod[:D], mod[D:2 * D]
+        n = layernorm_f64(h, None, None, 1e-6)
+        n = (n * (np.float32(1) + scale) + shift).astype(np.float32)
+        return self.linear("flow.final.out", n, self.hp["ldim"], D)
+
+    def sample(self, c: np.ndarray, x0: np.ndarray) -> np.ndarray:
+        """flowHead.sample (lm.go:107-122)."""
+        y = self.linear("flow.cond", c, self.dim, self.hp["d"])
+        cur = _f32(x0).copy()
+        n = np.float32(len(self.tc))
+        for t in self.tc:
+            yi = (y + t).astype(np.float32)
+            v = self.net(yi, cur)
+            cur = (cur + v / n).astype(np.float32)
+        return cur

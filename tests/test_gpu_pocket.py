@@ -97,3 +97,62 @@ def test_configured_shape(kern, orc):
     for k in range(24):
         wo, we = ref.step(lat[k])
         assert _same(outs[k], wo) and _same(eos[k], we), k
+
+
+def _speak_pair(orc, hp, fhp, seed, q8=True):
+    from gorelaxor_amd.pocket import PocketLM
+    from gorelaxor_amd.synth import pocket_flow_model
+
+    t = pocket_model(hp, seed=seed)
+    ft = pocket_flow_model(hp, fhp, seed=seed + 1, q8=q8)
+    lm = PocketLM(hp, t)
+    lm.flow_init(fhp["dim"], fhp["depth"], fhp["steps"])
+    for k, v in ft.items():
+        lm.set_tensor(k, v)
+    return lm, orc.PocketOracle(hp, t), orc.PocketFlowOracle(hp, fhp["dim"], fhp["depth"], fhp["steps"], ft)
+
+
+def _speak_check(lm, ref, flow, hp, prefix, frames, seed, chunks=1):
+    x, _ = pocket_inputs(hp, 1, prefix=prefix, seed=seed)
+    assert _same(lm.run(x), ref.run(x))
+    noise = np.random.default_rng(seed).standard_normal((frames, hp["ldim"])).astype(np.float32) * np.float32(0.7)
+    got_l, got_e = [], []
+    latent = None
+    for part in np.array_split(np.arange(frames), chunks):
+        lat, eos = lm.speak(noise[part], first_latent=latent)
+        got_l.append(lat)
+        got_e.append(eos)
+        latent = lat[-1]
+    got_l, got_e = np.concatenate(got_l), np.concatenate(got_e)
+    latent = None
+    for k in range(frames):
+        h, e = ref.step(latent)
+        nxt = flow.sample(h, noise[k])
+        assert _same(got_e[k], e), f"frame {k}: eos {got_e[k]} vs {e}"
+        assert _same(got_l[k], nxt), f"frame {k}: max |diff| {np.abs(got_l[k] - nxt).max()}"
+        latent = nxt
+
+
+@pytest.mark.parametrize("q8", [True, False])
+def test_speak_frames_with_flow_head_bit_exact(kern, orc, q8):
+    """speakChunk's loop on the device: each frame's transformer step fed the
+    previous frame's sampled latent, the flow head (two LSD steps, two
+    residual blocks) from its output and the frame's noise - latents and
+    end-of-speech logits bit-identical, over two calls that continue one
+    another; the flow matrices Q8_0 as converted files hold them, or all
+    float32."""
+    from gorelaxor_amd.synth import POCKET_FLOW_TINY
+
+    hp, fhp = dict(POCKET_TTS_TINY), dict(POCKET_FLOW_TINY)
+    lm, ref, flow = _speak_pair(orc, hp, fhp, seed=13, q8=q8)
+    _speak_check(lm, ref, flow, hp, prefix=5, frames=7, seed=14, chunks=2)
+
+
+def test_speak_configured_shape(kern, orc):
+    """d 1024 transformer with a 512-wide, 6-block flow head (one LSD step):
+    a 64-row prefix, then 12 frames, bit-identical."""
+    from gorelaxor_amd.synth import POCKET_FLOW
+
+    hp, fhp = dict(POCKET_TTS_LM), dict(POCKET_FLOW)
+    lm, ref, flow = _speak_pair(orc, hp, fhp, seed=15)
+    _speak_check(lm, ref, flow, hp, prefix=64, frames=12, seed=16)

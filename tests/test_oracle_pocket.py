@@ -145,3 +145,70 @@ def test_oracle_flow_lm_vs_float64(orc):
     assert m.pos == 26
     with pytest.raises(ValueError):
         m.run(np.zeros((hp["max_pos"], hp["d"]), np.float32))
+
+
+def _f64_flow(hp, fhp, t, c, x0):
+    """The flow head (pockettts/lm.go:59-160) in float64 from the dequantized
+    weights: the structure the oracle must follow, to float32 rounding."""
+    from gorelaxor_amd.synth import q8_dequant
+
+    D, d, ld = fhp["dim"], hp["d"], hp["ldim"]
+
+    def W(name, rows, cols):
+        w = t[name + ".weight"]
+        m = q8_dequant(w, rows, cols) if w.dtype == np.uint8 else w.reshape(rows, cols)
+        return m.astype(np.float64), t[name + ".bias"].astype(np.float64)
+
+    def lin(name, x, rows, cols):
+        w, b = W(name, rows, cols)
+        return w @ x + b
+
+    silu = lambda v: v / (1 + np.exp(-v))  # noqa: E731
+
+    def ln(h, w=None, b=None):
+        o = (h - h.mean()) / np.sqrt(h.var() + 1e-6)
+        return o * w + b if w is not None else o
+
+    def embed(e, tt):
+        p = f"flow.time.{e}."
+        f = t[p + "freqs"].astype(np.float64)
+        x = np.concatenate([np.cos(tt * f), np.sin(tt * f)])
+        y = lin(p + "fc2", silu(lin(p + "fc1", x, D, 256)), D, D)
+        return y * t[p + "norm.alpha"] / np.sqrt(y.var(ddof=1) + 1e-5)
+
+    steps = fhp["steps"]
+    tc = [(embed(0, i / steps) + embed(1, (i + 1) / steps)) / 2 for i in range(steps)]
+    y = lin("flow.cond", c.astype(np.float64), D, d)
+    cur = x0.astype(np.float64)
+    for tcs in tc:
+        sy = silu(y + tcs)
+        h = lin("flow.input", cur, D, ld)
+        for i in range(fhp["depth"]):
+            p = f"flow.res.{i}."
+            mod = lin(p + "ada", sy, 3 * D, D)
+            n = ln(h, t[p + "norm.weight"], t[p + "norm.bias"]) * (1 + mod[D:2 * D]) + mod[:D]
+            h = h + mod[2 * D:] * lin(p + "fc2", silu(lin(p + "fc1", n, D, D)), D, D)
+        mod = lin("flow.final.ada", sy, 2 * D, D)
+        n = ln(h) * (1 + mod[D:]) + mod[:D]
+        cur = cur + lin("flow.final.out", n, ld, D) / steps
+    return cur
+
+
+@pytest.mark.parametrize("q8", [True, False])
+def test_flow_head_structure_vs_float64(orc, q8):
+    """The oracle's flow head against the float64 restatement of lm.go's
+    SimpleMLPAdaLN (time conditions, adaLN shift/scale/gate, the residual
+    MLPs, the final modulation, the LSD update): equal to float32 rounding,
+    with the Q8_0/float32 typing of converted files and with all-float32."""
+    from gorelaxor_amd.synth import POCKET_FLOW_TINY, POCKET_TTS_TINY, pocket_flow_model
+
+    hp, fhp = dict(POCKET_TTS_TINY), dict(POCKET_FLOW_TINY)
+    t = pocket_flow_model(hp, fhp, seed=3, q8=q8)
+    o = orc.PocketFlowOracle(hp, fhp["dim"], fhp["depth"], fhp["steps"], t)
+    rng = np.random.default_rng(4)
+    for _ in range(3):
+        c = rng.standard_normal(hp["d"]).astype(np.float32)
+        x0 = rng.standard_normal(hp["ldim"]).astype(np.float32)
+        got = o.sample(c, x0)
+        want = _f64_flow(hp, fhp, t, c, x0)
+        assert np.allclose(got, want, rtol=2e-4, atol=2e-4), np.abs(got - want).max()
