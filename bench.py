@@ -252,6 +252,57 @@ def lm_bench(args) -> dict:
                            "sample": f"the same {n} frames on the oracle (scalar C, 1 thread), {cpu_s:.2f} s; "
                                      f"prefix {1e3 * (t1 - t0):.0f} ms"}
     lm.close()
+    res["speak"] = speak_bench(args, hp, t, x)
+    return res
+
+
+def speak_bench(args, hp, t, x) -> dict:
+    """speakChunk's frame loop on the device: per frame the transformer step
+    fed the previous sampled latent, then the flow head (512 wide, 6
+    residual blocks, 1 LSD step, random-init, typed as converted files:
+    Q8_0 matrices on kern's float route, float32 input/output projections)
+    from its output and seeded noise; frames per second, latents checked
+    against the oracle's."""
+    import oracle
+    from gorelaxor_amd.pocket import PocketLM
+    from gorelaxor_amd.synth import POCKET_FLOW, pocket_flow_model
+
+    fhp = dict(POCKET_FLOW)
+    n = args.lm_frames
+    ft = pocket_flow_model(hp, fhp, seed=7)
+    noise = np.random.default_rng(8).standard_normal((n, hp["ldim"])).astype(np.float32) * np.float32(0.3 ** 0.5)
+    lm = PocketLM(hp, t)
+    lm.flow_init(fhp["dim"], fhp["depth"], fhp["steps"])
+    for k, v in ft.items():
+        lm.set_tensor(k, v)
+    lm.run(x)
+    lm.speak(noise)  # warm: graph captured
+    times = []
+    for _ in range(3):
+        lm.reset()
+        lm.run(x)
+        t0 = time.perf_counter()
+        lats, eos = lm.speak(noise)
+        times.append(time.perf_counter() - t0)
+    lm.close()
+    best = min(times)
+    res = {"frames_per_s": round(n / best, 1), "ms_per_frame": round(best / n * 1e3, 4), "frames": n,
+           "flow_head": "dim %d, %d residual blocks, %d LSD step(s)" % (fhp["dim"], fhp["depth"], fhp["steps"])}
+    oracle.build()
+    ref = oracle.PocketOracle(hp, t)
+    flow = oracle.PocketFlowOracle(hp, fhp["dim"], fhp["depth"], fhp["steps"], ft)
+    ref.run(x)
+    ok, latent = True, None
+    t0 = time.perf_counter()
+    for k in range(n):
+        h, e = ref.step(latent)
+        latent = flow.sample(h, noise[k])
+        ok = ok and bool(np.array_equal(latent.view(np.uint32), lats[k].view(np.uint32))) and \
+            bool(np.float32(e) == eos[k])
+    res["parity_bit_exact"] = ok
+    res["cpu_baseline"] = {"value": round(n / (time.perf_counter() - t0), 2), "unit": "frames/s", "cores": 1,
+                           "kind": "port", "sample": f"the same {n} frames (transformer step and flow head) on the "
+                                                     "oracle (C kernels, 1 thread, Python glue)"}
     return res
 
 
