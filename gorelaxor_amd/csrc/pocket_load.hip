@@ -9,12 +9,15 @@
 // The transformer matrices go from the file to their device tiles as stored
 // (Q8_0, the form pack() gives the int8 kernels, model.go:322-366); the
 // input projection and the end-of-speech row are float32 (the converter
-// keeps matrices under 64 columns in float32).  The flow head, Mimi and the
-// tokenizer stay with the caller.  Host code only.
+// keeps matrices under 64 columns in float32).  When the file holds the flow
+// head, it is declared and bound too (settings pockettts.flow.dim,
+// flow.depth, decode_steps; matrices as stored).  Mimi and the tokenizer stay
+// with the caller.  Host code only.
 #include <stdarg.h>
 #include <stdio.h>
 
 #include <string>
+#include <tuple>
 #include <vector>
 
 #include "grx_internal.h"
@@ -173,6 +176,50 @@ extern "C" grx_status grx_pocket_load_gguf(grx_ctx *ctx, const char *path, int m
     if ((s = put_vec("lm.out_norm.bias", d)) != GRX_OK) return done(s);
     if ((s = put_f32mat("lm.eos.weight", 1, d)) != GRX_OK) return done(s);
     if ((s = put_vec("lm.eos.bias", 1)) != GRX_OK) return done(s);
+    // the flow head (model.go:230-247): its settings, then its tensors as
+    // stored (Q8_0 or float32 matrices, float32 vectors)
+    if (l.err.empty() && grx_gguf_has(f, "flow.cond.weight")) {
+        const int fd = l.num("pockettts.flow.dim"), depth = l.num("pockettts.flow.depth");
+        const int steps = l.num("pockettts.decode_steps");
+        if (l.err.empty() && (s = grx_pocket_flow_init(m, fd, depth, steps)) != GRX_OK) return done(s);
+        auto put_any = [&](const std::string &name, int64_t rows, int64_t cols) {
+            if (!l.mat_shape(name, rows, cols)) return GRX_OK;
+            int type = -1;
+            std::vector<uint8_t> d;
+            grx_status st = grx_gguf_tensor_data(f, name.c_str(), &type, &d);
+            if (st != GRX_OK) return st;
+            if (type == kQ8_0) return grx_pocket_set_tensor(m, name.c_str(), d.data(), d.size());
+            std::vector<float> v((size_t)(rows * cols));
+            if (grx_gguf_float32(f, name.c_str(), v.data(), v.size()) != GRX_OK) return (grx_status)GRX_EINVAL;
+            return grx_pocket_set_tensor(m, name.c_str(), v.data(), v.size() * 4);
+        };
+        const int64_t D = fd;
+        for (auto mt : {std::make_tuple("flow.cond", D, d), std::make_tuple("flow.input", D, ld),
+                        std::make_tuple("flow.final.ada", 2 * D, D), std::make_tuple("flow.final.out", ld, D)}) {
+            const std::string p = std::get<0>(mt);
+            if (l.err.empty() && (s = put_any(p + ".weight", std::get<1>(mt), std::get<2>(mt))) != GRX_OK)
+                return done(s);
+            if ((s = put_vec(p + ".bias", std::get<1>(mt))) != GRX_OK) return done(s);
+        }
+        for (int i = 0; i < 2; ++i) {
+            const std::string p = "flow.time." + std::to_string(i) + ".";
+            if ((s = put_vec(p + "freqs", 128)) != GRX_OK) return done(s);
+            if (l.err.empty() && (s = put_any(p + "fc1.weight", D, 256)) != GRX_OK) return done(s);
+            if ((s = put_vec(p + "fc1.bias", D)) != GRX_OK) return done(s);
+            if (l.err.empty() && (s = put_any(p + "fc2.weight", D, D)) != GRX_OK) return done(s);
+            if ((s = put_vec(p + "fc2.bias", D)) != GRX_OK) return done(s);
+            if ((s = put_vec(p + "norm.alpha", D)) != GRX_OK) return done(s);
+        }
+        for (int i = 0; i < depth && l.err.empty(); ++i) {
+            const std::string p = "flow.res." + std::to_string(i) + ".";
+            for (const char *v : {"norm.weight", "norm.bias", "fc1.bias", "fc2.bias"})
+                if ((s = put_vec(p + v, D)) != GRX_OK) return done(s);
+            if ((s = put_vec(p + "ada.bias", 3 * D)) != GRX_OK) return done(s);
+            if (l.err.empty() && (s = put_any(p + "fc1.weight", D, D)) != GRX_OK) return done(s);
+            if (l.err.empty() && (s = put_any(p + "fc2.weight", D, D)) != GRX_OK) return done(s);
+            if (l.err.empty() && (s = put_any(p + "ada.weight", 3 * D, D)) != GRX_OK) return done(s);
+        }
+    }
     if (!l.err.empty()) return done(grx_fail(l.code, "%s", l.err.c_str()));
     if (hp_out) *hp_out = hp;
     *out = m;

@@ -2,7 +2,7 @@
 GPU (pockettts.Load, pockettts/model.go:49-250).  The file is laid out as
 the reference's converter writes it (transformer matrices Q8_0, matrices
 under 64 columns float32, settings under pockettts.*), with tensors of the
-parts this build does not read (flow head) beside them; the loaded LM's
+parts this build does not read (Mimi) beside them; the loaded LM's
 prefix output, frame outputs and end-of-speech logits must be bit-identical
 to the oracle's over the same tensors, and bad files must fail with the
 reference's texts."""
@@ -45,8 +45,8 @@ def _tensors(hp, t):
             out.append((name, [d, 1], G.F32, a.tobytes()))
         else:
             out.append((name, [a.size], G.F32, a.tobytes()))
-    # a part of the model this build leaves to the caller
-    out.append(("flow.cond.weight", [d, 64], G.F32, np.zeros(64 * d, np.float32).tobytes()))
+    # a part of the model this build leaves to the caller (Mimi)
+    out.append(("mimi.quant", [ld, 64], G.F32, np.zeros(64 * ld, np.float32).tobytes()))
     return out
 
 
@@ -117,3 +117,44 @@ def test_load_errors(kern, orc, tmp_path, case, msg):
     with pytest.raises(GrxError, match=msg):
         PocketLM.from_gguf(p, max_pos=HP["max_pos"])
 
+
+
+def test_load_flow_head_and_speak_bit_exact(kern, orc, tmp_path):
+    """A file that also holds the flow head (settings pockettts.flow.dim,
+    flow.depth, decode_steps; Q8_0 matrices, float32 input/output
+    projections as the converter writes them): loaded, it speaks the
+    oracle's latents bit for bit."""
+    from gorelaxor_amd.pocket import PocketLM
+    from gorelaxor_amd.synth import POCKET_FLOW_TINY, pocket_flow_model
+
+    fhp = dict(POCKET_FLOW_TINY)
+    t = pocket_model(HP, seed=5)
+    ft = pocket_flow_model(HP, fhp, seed=6)
+    recs = _tensors(HP, t)
+    for name, a in ft.items():
+        if a.dtype == np.uint8:
+            cols = HP["d"] if name == "flow.cond.weight" else (256 if ".time." in name and "fc1" in name else fhp["dim"])
+            rows = a.size // 34 * 32 // cols
+            recs.append((name, [cols, rows], G.Q8_0, a.tobytes()))
+        elif name.endswith(".weight") and name in ("flow.input.weight", "flow.final.out.weight"):
+            cols = HP["ldim"] if name == "flow.input.weight" else fhp["dim"]
+            recs.append((name, [cols, a.size // cols], G.F32, a.tobytes()))
+        else:
+            recs.append((name, [a.size], G.F32, a.tobytes()))
+    sets = _settings(HP, **{"pockettts.flow.dim": (G.T_U32, fhp["dim"]),
+                            "pockettts.flow.depth": (G.T_U32, fhp["depth"]),
+                            "pockettts.decode_steps": (G.T_U32, fhp["steps"])})
+    p = _write(tmp_path / "f.gguf", HP, t, sets, recs)
+    lm = PocketLM.from_gguf(p, max_pos=HP["max_pos"])
+    ref = orc.PocketOracle(HP, t)
+    flow = orc.PocketFlowOracle(HP, fhp["dim"], fhp["depth"], fhp["steps"], ft)
+    x, _ = pocket_inputs(HP, 1, prefix=9, seed=3)
+    assert _same(lm.run(x), ref.run(x))
+    noise = np.random.default_rng(2).standard_normal((5, HP["ldim"])).astype(np.float32)
+    lats, eos = lm.speak(noise)
+    latent = None
+    for k in range(5):
+        h, e = ref.step(latent)
+        latent = flow.sample(h, noise[k])
+        assert _same(lats[k], latent) and _same(eos[k], e), k
+    lm.close()
