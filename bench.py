@@ -391,7 +391,47 @@ def conformer_bench(args) -> dict:
     res["cpu_baseline"] = {"value": round(1.0 / cpu_s, 4), "unit": "utterances/s", "cores": 1, "kind": "port",
                            "sample": f"one 10 s utterance, all 24 layers, on the oracle (scalar C, 1 thread), "
                                      f"{cpu_s:.1f} s"}
+    res["tdt_decode"] = tdt_bench(args, want[:L])
     return res
+
+
+def tdt_bench(args, enc: np.ndarray) -> dict:
+    """Model.Decode's greedy TDT loop (conformer/rnnt.go:111-173) over the
+    encoder output of the 10 s utterance, with a Parakeet-TDT-shaped head
+    (2 x 640 LSTM, joint 640, 1024 tokens + blank, durations 0..4,
+    random-init Q8_0): the whole loop on the device, encoder output resident
+    in HBM; decodes per second and tokens, checked against the oracle, whose
+    decode is the CPU baseline."""
+    import oracle
+    from gorelaxor_amd import hiprt
+    from gorelaxor_amd.rnnt import TransducerDecoder
+    from gorelaxor_amd.synth import RNNT_TDT, rnnt_model
+
+    hp = dict(RNNT_TDT)
+    t = rnnt_model(hp, seed=33)
+    T = enc.shape[0]
+    dec = TransducerDecoder(hp, t)
+    de = hiprt.DeviceBuffer.from_array(np.ascontiguousarray(enc, np.float32))
+    got = dec.decode_dev(de.ptr, T)  # graph captured
+    times = []
+    for _ in range(args.conformer_reps):
+        t0 = time.perf_counter()
+        dec.decode_dev(de.ptr, T)
+        times.append(time.perf_counter() - t0)
+    dec.close()
+    del de
+    best = float(np.median(times))
+    oracle.build()
+    t0 = time.perf_counter()
+    want, _ = oracle.RnntOracle(hp, t).decode(enc)
+    cpu_s = time.perf_counter() - t0
+    same = len(got) == len(want) and all(
+        (g.ID, g.Frame, g.Duration) == w[:3] and np.float32(g.P).tobytes() == np.float32(w[3]).tobytes()
+        for g, w in zip(got, want))
+    return {"frames": T, "tokens": len(got), "ms_per_decode": round(best * 1e3, 3),
+            "decodes_per_s": round(1.0 / best, 1), "parity_bit_exact": bool(same),
+            "cpu_baseline": {"value": round(1.0 / cpu_s, 2), "unit": "decodes/s", "cores": 1, "kind": "port",
+                             "sample": f"the same decode on the oracle (scalar C, 1 thread), {cpu_s * 1e3:.1f} ms"}}
 
 
 def main():

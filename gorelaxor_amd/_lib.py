@@ -113,6 +113,14 @@ SIGNATURES = {
     "grx_conformer_frames_out": (i32, [vp, i32]),
     "grx_conformer_encode": (i32, [vp, vp, i32, i32, vp, vp, vp]),
     "grx_conformer_encode_dev": (i32, [vp, vp, i32, i32, vp, vp]),
+    "grx_rnnt_create": (i32, [vp, vp, C.POINTER(vp)]),
+    "grx_rnnt_destroy": (i32, [vp]),
+    "grx_rnnt_set_tensor": (i32, [vp, C.c_char_p, vp, sz]),
+    "grx_rnnt_state_create": (i32, [vp, C.POINTER(vp)]),
+    "grx_rnnt_state_destroy": (i32, [vp]),
+    "grx_rnnt_state_read": (i32, [vp, vp, vp, C.POINTER(C.c_int)]),
+    "grx_rnnt_state_write": (i32, [vp, vp, vp, i32]),
+    "grx_rnnt_decode": (i32, [vp, vp, i32, i32, vp, i32, vp, i32, C.POINTER(C.c_int)]),
 }
 
 
@@ -125,6 +133,18 @@ class ConformerHParams(C.Structure):
     """grx_conformer_hparams."""
     _fields_ = [(n, C.c_int) for n in ("d", "heads", "layers", "dff", "conv_kernel", "sub_channels", "n_mels",
                                        "xscaling", "conv_ln")]
+
+
+class RnntHParams(C.Structure):
+    """grx_rnnt_hparams."""
+    _fields_ = [(n, C.c_int) for n in ("d", "pred_hidden", "pred_layers", "pred_vocab", "joint_hidden", "joint_act",
+                                       "tdt", "n_durations")] + [("durations", C.c_int * 16)] + [
+        (n, C.c_int) for n in ("max_symbols", "blank")]
+
+
+class RnntToken(C.Structure):
+    """grx_rnnt_token."""
+    _fields_ = [("id", C.c_int), ("frame", C.c_int), ("duration", C.c_int), ("p", C.c_float)]
 
 
 class WhisperRules(C.Structure):

@@ -55,6 +55,106 @@ __device__ __forceinline__ float dot_x4(const float *x, const float *w, int k) {
     return o;
 }
 
+// One Q8_0 weight row of the float route per four threads (256 threads = 64
+// rows of tile `tile`), x in LDS.  Thread j keeps the reference's lane chains j
+// and j+4 of dot4q8avx, so no chain changes order, and the HSUM is formed
+// across the four as (h0+h1)+(h2+h3), h_j = acc[j]+acc[j+4].  Rows of the last
+// partial group of four take dotQ8Go in their thread 0.  Blocks are read four
+// at a time.  Returns the product (no bias) with emit set in thread 0 of a
+// live row; every thread of the workgroup must call it (shuffles).
+__device__ __forceinline__ float q8_float_row(const float *xs, const int8_t *__restrict__ qs,
+                                              const uint16_t *__restrict__ ds, int nb, int n, int tile, int &row,
+                                              bool &emit) {
+    const int rl = threadIdx.x >> 2, j = threadIdx.x & 3;
+    row = tile * 64 + rl;
+    const bool live = row < n, avx = row < (n & ~3);
+    const int8_t *qt = qs + (size_t)tile * nb * 2 * 64 * 16 + (size_t)rl * 16;
+    const uint16_t *dt = ds + (size_t)tile * nb * 64 + rl;
+    auto ld = [&](int b, int4 &h0, int4 &h1, uint16_t &d) {
+        h0 = *reinterpret_cast<const int4 *>(qt + (size_t)(2 * b) * 64 * 16);
+        h1 = *reinterpret_cast<const int4 *>(qt + (size_t)(2 * b + 1) * 64 * 16);
+        d = dt[(size_t)b * 64];
+    };
+    float a0 = 0.f, a1 = 0.f, s = 0.f;
+    if (live && avx) {
+        // the reference's lane chains j and j+4 of one block
+        // value i of the block is byte i%4 of dword i/4; chain l = j + 4c
+        // reads values l, 8+l, 16+l, 24+l: byte j of dwords c, 2+c, 4+c, 6+c
+        const unsigned sh = 24u - 8u * (unsigned)j;
+        auto val = [&](int dw) { return (float)((int)((unsigned)dw << sh) >> 24); };
+        auto fold = [&](int b, const int4 &h0, const int4 &h1, uint16_t dh) {
+            const float d = grx_f16_to_f32(dh);
+            const float *xb = xs + b * 32;
+            const int dws[2][4] = {{h0.x, h0.z, h1.x, h1.z}, {h0.y, h0.w, h1.y, h1.w}};
+#pragma unroll
+            for (int c = 0; c < 2; ++c) {
+                const int l = j + 4 * c;
+                float t = __fmul_rn(val(dws[c][0]), xb[l]);
+                t = __fmaf_rn(val(dws[c][1]), xb[8 + l], t);
+                t = __fmaf_rn(val(dws[c][2]), xb[16 + l], t);
+                t = __fmaf_rn(val(dws[c][3]), xb[24 + l], t);
+                if (c == 0) a0 = __fmaf_rn(t, d, a0);
+                else a1 = __fmaf_rn(t, d, a1);
+            }
+        };
+        // groups of four blocks, the next group read (at a clamped index,
+        // unconditionally) while this one is folded
+        const int ng = nb / 4;
+        int4 c0[4], c1[4];
+        uint16_t cd[4];
+        if (ng > 0) {
+#pragma unroll
+            for (int u = 0; u < 4; ++u) ld(u, c0[u], c1[u], cd[u]);
+        }
+        for (int g = 0; g < ng; ++g) {
+            const int gn = min(g + 1, ng - 1);
+            int4 n0[4], n1[4];
+            uint16_t nd[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) ld(4 * gn + u, n0[u], n1[u], nd[u]);
+#pragma unroll
+            for (int u = 0; u < 4; ++u) fold(4 * g + u, c0[u], c1[u], cd[u]);
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                c0[u] = n0[u];
+                c1[u] = n1[u];
+                cd[u] = nd[u];
+            }
+        }
+        for (int b = 4 * ng; b < nb; ++b) {
+            int4 h0, h1;
+            uint16_t dh;
+            ld(b, h0, h1, dh);
+            fold(b, h0, h1, dh);
+        }
+    } else if (live && j == 0) {  // dotQ8Go (kern.go:248-266)
+        for (int b = 0; b < nb; ++b) {
+            int4 h0, h1;
+            uint16_t dh;
+            ld(b, h0, h1, dh);
+            int8_t w[32];
+            *reinterpret_cast<int4 *>(w) = h0;
+            *reinterpret_cast<int4 *>(w + 16) = h1;
+            const float d = grx_f16_to_f32(dh);
+            const float *xb = xs + b * 32;
+            float q0 = 0.f, q1 = 0.f, q2 = 0.f, q3 = 0.f;
+#pragma unroll
+            for (int i = 0; i < 32; i += 4) {
+                q0 = __fadd_rn(q0, __fmul_rn(xb[i], (float)w[i]));
+                q1 = __fadd_rn(q1, __fmul_rn(xb[i + 1], (float)w[i + 1]));
+                q2 = __fadd_rn(q2, __fmul_rn(xb[i + 2], (float)w[i + 2]));
+                q3 = __fadd_rn(q3, __fmul_rn(xb[i + 3], (float)w[i + 3]));
+            }
+            s = __fadd_rn(s, __fmul_rn(d, __fadd_rn(__fadd_rn(__fadd_rn(q0, q1), q2), q3)));
+        }
+    }
+    // HSUM over the row's four threads: h_j = acc[j] + acc[j+4], then (h0+h1)+(h2+h3)
+    const float h = __fadd_rn(a0, a1);
+    const float h1 = __shfl_down(h, 1, 4), h23 = __fadd_rn(__shfl_down(h, 2, 4), __shfl_down(h, 3, 4));
+    emit = live && j == 0;
+    return avx ? __fadd_rn(__fadd_rn(h, h1), h23) : s;
+}
+
 // softmax (internal/kern/mathx.go:78-90) of s[0..n) in LDS by one block:
 // max, e = EXP8(v-max) below n &^ 7 and expf past it, the eight lane sums
 // of expSubAVX + HSUM, plus the tail's own sum, then v *= 1/sum.

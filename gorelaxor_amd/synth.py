@@ -290,3 +290,44 @@ def noise_mel(n_mels: int, seconds: float = 10.0, seed: int = 4, sr: int = 16000
     rng = np.random.default_rng(seed)
     pcm = (rng.standard_normal(int(seconds * sr)) * 0.1).astype(np.float32)
     return log_mel(pcm, n_mels, sr)
+
+
+# A Parakeet-TDT-shaped transducer head (FastConformer d=1024, 2-layer LSTM
+# of 640, joint 640, 1024 tokens + blank, durations 0..4).
+RNNT_TDT = dict(d=1024, pred_hidden=640, pred_layers=2, pred_vocab=1025, joint_hidden=640, joint_act="relu",
+                head_kind="tdt", durations=[0, 1, 2, 3, 4], max_symbols=10, blank=-1)
+RNNT_TINY = dict(d=64, pred_hidden=64, pred_layers=2, pred_vocab=97, joint_hidden=64, joint_act="relu",
+                 head_kind="rnnt", blank=-1)
+
+
+def rnnt_model(hp: dict, seed: int = 21, blank_bias: float = 2.0, out_sigma: float = 2.0,
+               pred_sigma: float = 8.0) -> dict:
+    """Random-init decoder tensors named as conformer/model.go:306-315 reads
+    them: Q8_0 matrices sized so gates and logits stay O(1), float32
+    vectors, the embedding with NeMo's extra padding row, and blank's output
+    bias raised by blank_bias so that frames advance as well as emit."""
+    rng = np.random.default_rng(seed)
+    H, L, V, J, d = hp["pred_hidden"], hp["pred_layers"], hp["pred_vocab"], hp["joint_hidden"], hp["d"]
+    nd = len(hp.get("durations", [])) if hp.get("head_kind", "rnnt") == "tdt" else 0
+    blank = hp.get("blank", -1)
+    blank = blank if blank >= 0 else V - 1
+    t = {"pred.embed.weight": (rng.standard_normal((V, H)) * 0.5).astype(np.float32)}
+    for i in range(L):
+        p = f"pred.lstm.{i}."
+        t[p + "Wx"] = q8_weight(rng, 4 * H, H, sigma=2.0 / np.sqrt(H))
+        t[p + "Wh"] = q8_weight(rng, 4 * H, H, sigma=2.0 / np.sqrt(H))
+        t[p + "bias"] = (rng.standard_normal(4 * H) * 0.1).astype(np.float32)
+    t["joint.enc.weight"] = q8_weight(rng, J, d, sigma=2.0 / np.sqrt(d))
+    t["joint.enc.bias"] = (rng.standard_normal(J) * 0.1).astype(np.float32)
+    t["joint.pred.weight"] = q8_weight(rng, J, H, sigma=pred_sigma / np.sqrt(H))
+    t["joint.pred.bias"] = (rng.standard_normal(J) * 0.1).astype(np.float32)
+    t["joint.out.weight"] = q8_weight(rng, V + nd, J, sigma=out_sigma / np.sqrt(J))
+    ob = (rng.standard_normal(V + nd) * 0.1).astype(np.float32)
+    ob[blank] += np.float32(blank_bias)
+    t["joint.out.bias"] = ob
+    return t
+
+
+def rnnt_encoder_output(hp: dict, T: int, seed: int = 22) -> np.ndarray:
+    """Synthetic encoder output [T][d] (unit normal)."""
+    return np.random.default_rng(seed).standard_normal((T, hp["d"])).astype(np.float32)

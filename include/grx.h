@@ -420,6 +420,59 @@ grx_status grx_conformer_encode(grx_conformer *m, const float *mel, int batch, i
 grx_status grx_conformer_encode_dev(grx_conformer *m, const float *mel, int batch, int frames, const int *valid,
                                     float *out);
 
+/* ---- RNN-T / TDT greedy decoder (prediction network and joint) ---- */
+
+/* The transducer head of conformer/model.go:306-315 and the HParams it
+ * reads (model.go:191-235): pred_hidden, pred_layers, pred_vocab (tokens
+ * plus blank), joint_hidden, joint_act (0 "relu", 1 "sigmoid", 2 "tanh"),
+ * tdt (nonzero: "tdt", with n_durations durations and max_symbols; RNN-T
+ * takes no durations and 10 symbols a frame), blank (-1: pred_vocab - 1)
+ * and d, the encoder width.  Widths are multiples of 32. */
+typedef struct {
+    int d, pred_hidden, pred_layers, pred_vocab, joint_hidden, joint_act;
+    int tdt, n_durations, durations[16], max_symbols, blank;
+} grx_rnnt_hparams;
+
+/* Token (conformer/rnnt.go:10-15). */
+typedef struct {
+    int id, frame, duration;
+    float p;
+} grx_rnnt_token;
+
+typedef struct grx_rnnt grx_rnnt;
+/* DecoderState (rnnt.go:19-23): the LSTM's h and c per layer and the last
+ * emitted token, in device memory. */
+typedef struct grx_rnnt_state grx_rnnt_state;
+
+grx_status grx_rnnt_create(grx_ctx *ctx, const grx_rnnt_hparams *hp, grx_rnnt **out);
+grx_status grx_rnnt_destroy(grx_rnnt *m);
+/* fromGGUF's decoder tensors by name (model.go:306-315): "pred.embed.weight"
+ * (float32 [rows][pred_hidden], every id but blank has a row),
+ * "pred.lstm.<i>.Wx" / ".Wh" (Q8_0 [4H][H]), "pred.lstm.<i>.bias" (float32,
+ * the two NeMo biases summed), "joint.enc.weight" (Q8_0 [J][d]),
+ * "joint.pred.weight" (Q8_0 [J][H]), "joint.out.weight" (Q8_0 [pred_vocab +
+ * durations][J]) and their float32 biases.  The decoder is ready when all
+ * are set. */
+grx_status grx_rnnt_set_tensor(grx_rnnt *m, const char *name, const void *data, size_t nbytes);
+/* Model.NewDecoderState (rnnt.go:26-33): zeros, last = -1.  A state may
+ * outlive its decoder, not the decoder's context. */
+grx_status grx_rnnt_state_create(grx_rnnt *m, grx_rnnt_state **out);
+grx_status grx_rnnt_state_destroy(grx_rnnt_state *s);
+/* The state's h and c ([layers][pred_hidden] each, either may be NULL) and
+ * last token, to the host / from the host. */
+grx_status grx_rnnt_state_read(const grx_rnnt_state *s, float *h, float *c, int *last);
+grx_status grx_rnnt_state_write(grx_rnnt_state *s, const float *h, const float *c, int last);
+/* Model.Decode (rnnt.go:111-173): greedy RNN-T or TDT decoding of encoder
+ * output enc [T][d] (host memory, or device memory when enc_on_device),
+ * continuing from st and leaving the final state there (st NULL: start
+ * fresh, no state kept); token frames are offset by frame_offset.  The
+ * tokens go to out (room for cap; 16*T + 1024 always suffices) and their
+ * number to *n_out; more than cap is GRX_ESIZE, with the first cap
+ * written.  Each token's id, frame, duration and float32 probability are
+ * the reference's. */
+grx_status grx_rnnt_decode(grx_rnnt *m, const float *enc, int T, int enc_on_device, grx_rnnt_state *st,
+                           int frame_offset, grx_rnnt_token *out, int cap, int *n_out);
+
 #ifdef __cplusplus
 }
 #endif

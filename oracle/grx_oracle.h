@@ -189,6 +189,24 @@ typedef struct {
 void orc_whisper_sample(const float *logits, int n, const orc_whisper_rules *v, const orc_whisper_seq *q,
                         float temp, float r, orc_whisper_token *out);
 
+/* ---- RNN-T / TDT greedy decoding (conformer/rnnt.go) ---- */
+typedef struct {
+    int d, H, L, V, J, act, tdt, nd, dur[16], max_symbols, blank;
+    const float *embed;
+    const uint8_t *const *wx, *const *wh; /* Q8_0 [4H][H] per layer */
+    const float *const *b;                /* [4H] per layer */
+    const uint8_t *jenc, *jpred, *jout;
+    const float *jencb, *jpredb, *joutb;
+} orc_rnnt;
+typedef struct {
+    int id, frame, duration;
+    float p;
+} orc_rnnt_token;
+double orc_fd_exp(double x);
+float orc_tanh32(float x);
+int orc_rnnt_decode(const orc_rnnt *m, const float *enc, int T, float *h, float *c, int *last, int frame_offset,
+                    orc_rnnt_token *out, int cap);
+
 #ifdef __cplusplus
 }
 #endif

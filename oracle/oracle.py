@@ -783,3 +783,98 @@ class PocketFlowOracle:
             v = self.net(yi, cur)
             cur = (cur + v / n).astype(np.float32)
         return cur
+
+
+# ---------------------------------------------------------------- RNN-T / TDT
+
+class _RModel(C.Structure):
+    _fields_ = [("d", C.c_int), ("H", C.c_int), ("L", C.c_int), ("V", C.c_int), ("J", C.c_int), ("act", C.c_int),
+                ("tdt", C.c_int), ("nd", C.c_int), ("dur", C.c_int * 16), ("max_symbols", C.c_int),
+                ("blank", C.c_int), ("embed", C.c_void_p), ("wx", C.c_void_p), ("wh", C.c_void_p),
+                ("b", C.c_void_p), ("jenc", C.c_void_p), ("jpred", C.c_void_p), ("jout", C.c_void_p),
+                ("jencb", C.c_void_p), ("jpredb", C.c_void_p), ("joutb", C.c_void_p)]
+
+
+class _RToken(C.Structure):
+    _fields_ = [("id", C.c_int), ("frame", C.c_int), ("duration", C.c_int), ("p", C.c_float)]
+
+
+JOINT_ACTS = {"relu": 0, "sigmoid": 1, "tanh": 2}
+
+
+def fd_exp(x: float) -> float:
+    L = lib()
+    L.orc_fd_exp.argtypes = [C.c_double]
+    L.orc_fd_exp.restype = C.c_double
+    return L.orc_fd_exp(x)
+
+
+def tanh32(x: float) -> float:
+    L = lib()
+    L.orc_tanh32.argtypes = [C.c_float]
+    L.orc_tanh32.restype = C.c_float
+    return L.orc_tanh32(x)
+
+
+class RnntOracle:
+    """Oracle of Model.Decode (conformer/rnnt.go:111-173) over the decoder
+    tensors named as conformer/model.go:306-315 reads them.  hp: d,
+    pred_hidden, pred_layers, pred_vocab, joint_hidden, joint_act ("relu",
+    "sigmoid", "tanh"), head_kind ("rnnt" / "tdt"), durations, max_symbols,
+    blank (-1: pred_vocab - 1)."""
+
+    def __init__(self, hp: dict, tensors: dict):
+        self.hp = hp
+        tdt = hp.get("head_kind", "rnnt") == "tdt"
+        m = _RModel()
+        m.d, m.H, m.L = hp["d"], hp["pred_hidden"], hp["pred_layers"]
+        m.V, m.J = hp["pred_vocab"], hp["joint_hidden"]
+        m.act = JOINT_ACTS[hp.get("joint_act", "relu")]
+        m.tdt = int(tdt)
+        durs = list(hp.get("durations", [])) if tdt else []
+        m.nd = len(durs)
+        for i, v in enumerate(durs):
+            m.dur[i] = v
+        m.max_symbols = hp.get("max_symbols", 10) if tdt else 10
+        b = hp.get("blank", -1)
+        m.blank = b if b >= 0 else hp["pred_vocab"] - 1
+        self._keep = []
+
+        def keep(a):
+            a = np.ascontiguousarray(a)
+            self._keep.append(a)
+            return a.ctypes.data
+
+        Ln = m.L
+        self._wx = (C.c_void_p * Ln)(*[keep(tensors[f"pred.lstm.{i}.Wx"]) for i in range(Ln)])
+        self._wh = (C.c_void_p * Ln)(*[keep(tensors[f"pred.lstm.{i}.Wh"]) for i in range(Ln)])
+        self._b = (C.c_void_p * Ln)(*[keep(tensors[f"pred.lstm.{i}.bias"]) for i in range(Ln)])
+        m.wx, m.wh, m.b = C.cast(self._wx, C.c_void_p), C.cast(self._wh, C.c_void_p), C.cast(self._b, C.c_void_p)
+        m.embed = keep(tensors["pred.embed.weight"])
+        for f, n in (("jenc", "joint.enc.weight"), ("jpred", "joint.pred.weight"), ("jout", "joint.out.weight"),
+                     ("jencb", "joint.enc.bias"), ("jpredb", "joint.pred.bias"), ("joutb", "joint.out.bias")):
+            setattr(m, f, keep(tensors[n]))
+        self._m = m
+        L = lib()
+        L.orc_rnnt_decode.argtypes = [C.c_void_p, _f32p, C.c_int, _f32p, _f32p, C.POINTER(C.c_int), C.c_int,
+                                      C.c_void_p, C.c_int]
+        L.orc_rnnt_decode.restype = C.c_int
+
+    def new_state(self):
+        """NewDecoderState (rnnt.go:26-33): (h, c, last)."""
+        H, Ln = self.hp["pred_hidden"], self.hp["pred_layers"]
+        return np.zeros((Ln, H), np.float32), np.zeros((Ln, H), np.float32), -1
+
+    def decode(self, enc: np.ndarray, state=None, frame_offset: int = 0):
+        """(tokens as (id, frame, duration, p) tuples, final state)."""
+        enc = _f32(enc)
+        T = enc.size // self.hp["d"]
+        h, c, last = self.new_state() if state is None else (state[0].copy(), state[1].copy(), state[2])
+        h, c = np.ascontiguousarray(h, np.float32), np.ascontiguousarray(c, np.float32)
+        cap = 16 * T + 1024
+        out = (_RToken * cap)()
+        lv = C.c_int(last)
+        n = lib().orc_rnnt_decode(C.byref(self._m), enc, T, h.reshape(-1), c.reshape(-1), C.byref(lv),
+                                  frame_offset, C.cast(out, C.c_void_p), cap)
+        toks = [(out[i].id, out[i].frame, out[i].duration, float(np.float32(out[i].p))) for i in range(n)]
+        return toks, (h, c, lv.value)
