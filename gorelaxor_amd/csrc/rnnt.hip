@@ -14,8 +14,8 @@
 // the float route.  The loop is data-dependent (a blank advances the frame,
 // a token re-runs the prediction network), so it runs on the device: each
 // iteration is L gate launches, one prediction-projection launch (those
-// return at once unless the last iteration emitted a token) and one joint
-// launch whose last workgroup to finish applies the greedy decision to the
+// return at once unless the last iteration emitted a token), one joint
+// launch and a one-workgroup launch that applies the greedy decision to the
 // loop state in device memory.  A captured graph holds kIters iterations;
 // the host replays it until the loop reports done, so the host reads the
 // loop state once per kIters iterations.  The prediction projection is
@@ -36,7 +36,7 @@ constexpr int kExpChunk = 1024;
 
 // The loop state (rnnt.go:134-171) in device memory.
 struct RnntCtl {
-    int step, iter, newsym, dirty, done, cur, n_out, T, max_iters, frame_offset, counter;
+    int step, iter, newsym, dirty, done, cur, n_out, T, max_iters, frame_offset;
     int last[2];  // DecoderState.last of the two state slots
 };
 
@@ -213,19 +213,12 @@ __device__ __forceinline__ ArgBest better(ArgBest a, ArgBest b) {
 }
 
 // The joint (rnnt.go:90-106) of frame `step`: hidden = act(encProj[step] +
-// predProj) in LDS, logits = Wo hidden + b; then the workgroup that finishes
-// last takes the greedy step (rnnt.go:140-170): the first maximal token, the
-// TDT duration, the softmax probability of an emitted token (rnnt.go:78-85:
-// a float64 sum in order over the tokens), the state swap and the frame
-// advance.
-__global__ __launch_bounds__(256) void rnnt_joint_kernel(RnntCtl *ctl, RnntHp hp, const int8_t *wq,
+// predProj) in LDS, logits = Wo hidden + b.
+__global__ __launch_bounds__(256) void rnnt_joint_kernel(const RnntCtl *ctl, RnntHp hp, const int8_t *wq,
                                                          const uint16_t *wd, const float *__restrict__ bias,
                                                          const float *__restrict__ ep, const float *__restrict__ pp,
-                                                         float *logits, grx_rnnt_token *tokens) {
+                                                         float *logits) {
     extern __shared__ __align__(16) float xs[];
-    __shared__ double es[kExpChunk];
-    __shared__ ArgBest wbest[4];
-    __shared__ int is_last;
     if (ctl->done) return;
     const int J = hp.J, step = ctl->step;
     const float *e = ep + (size_t)step * J;
@@ -244,12 +237,16 @@ __global__ __launch_bounds__(256) void rnnt_joint_kernel(RnntCtl *ctl, RnntHp hp
     bool emit;
     const float o = q8_float_row(xs, wq, wd, J / 32, hp.R, blockIdx.x, row, emit);
     if (emit) logits[row] = __fadd_rn(o, bias[row]);
-    __threadfence();
-    __syncthreads();
-    if (threadIdx.x == 0) is_last = atomicAdd(&ctl->counter, 1) == (int)gridDim.x - 1;
-    __syncthreads();
-    if (!is_last) return;
-    __threadfence();
+}
+
+// The greedy step (rnnt.go:140-170) in one workgroup: the first maximal
+// token, the TDT duration, the softmax probability of an emitted token
+// (rnnt.go:78-85), the state swap and the frame advance.
+__global__ __launch_bounds__(256) void rnnt_decide_kernel(RnntCtl *ctl, RnntHp hp, const float *__restrict__ logits,
+                                                          grx_rnnt_token *tokens) {
+    __shared__ double es[kExpChunk];
+    __shared__ ArgBest wbest[4];
+    if (ctl->done) return;
     const int tid = threadIdx.x, V = hp.V;
     ArgBest b = {-__builtin_inff(), 0x7fffffff};
     for (int i = tid; i < V; i += blockDim.x) b = better(b, ArgBest{logits[i], i});
@@ -261,16 +258,41 @@ __global__ __launch_bounds__(256) void rnnt_joint_kernel(RnntCtl *ctl, RnntHp hp
     for (int w = 1; w < (int)blockDim.x / 64; ++w) b = better(b, wbest[w]);
     const int tok = b.i == 0x7fffffff ? 0 : b.i;
     const bool blank = tok == hp.blank;
-    double s = 0.0;
+    // softmaxAt's p = float32(e^0 / s), s the float64 sum in token order.  Any
+    // order of summing V non-negative terms lands within gamma = (V-1) 2^-53
+    // (relative) of the exact sum, so the in-order s lies within 2 gamma of a
+    // parallel sum t; if float32(1/s) is the same at both ends of that
+    // interval (1/s and its roundings are monotone), it is p.  Otherwise (a
+    // float32 rounding boundary inside an interval ~2^-41 wide) the sum is
+    // formed in order.
+    float p = 0.f;
     if (!blank) {
         const float mx = logits[tok];
-        for (int c0 = 0; c0 < V; c0 += kExpChunk) {
-            const int cn = min(kExpChunk, V - c0);
-            for (int i = tid; i < cn; i += blockDim.x) es[i] = fd_exp((double)__fsub_rn(logits[c0 + i], mx));
-            __syncthreads();
-            if (tid == 0)
-                for (int i = 0; i < cn; ++i) s = __dadd_rn(s, es[i]);
-            __syncthreads();
+        double part = 0.0;
+        for (int i = tid; i < V; i += blockDim.x) part = __dadd_rn(part, fd_exp((double)__fsub_rn(logits[i], mx)));
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) part = __dadd_rn(part, __shfl_xor(part, off));
+        if ((tid & 63) == 0) es[tid >> 6] = part;
+        __syncthreads();
+        double t = es[0];
+        for (int w = 1; w < (int)blockDim.x / 64; ++w) t = __dadd_rn(t, es[w]);
+        const double delta = (double)(V + 4) * 0x1p-52;
+        const float plo = (float)__ddiv_rn(1.0, __dmul_rn(t, 1.0 + delta));
+        const float phi = (float)__ddiv_rn(1.0, __dmul_rn(t, 1.0 - delta));
+        __syncthreads();
+        if (plo == phi) {
+            p = plo;
+        } else {
+            double sq = 0.0;
+            for (int c0 = 0; c0 < V; c0 += kExpChunk) {
+                const int cn = min(kExpChunk, V - c0);
+                for (int i = tid; i < cn; i += blockDim.x) es[i] = fd_exp((double)__fsub_rn(logits[c0 + i], mx));
+                __syncthreads();
+                if (tid == 0)
+                    for (int i = 0; i < cn; ++i) sq = __dadd_rn(sq, es[i]);
+                __syncthreads();
+            }
+            p = (float)__ddiv_rn(fd_exp((double)__fsub_rn(logits[tok], mx)), sq);
         }
     }
     if (tid != 0) return;
@@ -283,7 +305,6 @@ __global__ __launch_bounds__(256) void rnnt_joint_kernel(RnntCtl *ctl, RnntHp hp
     }
     int st = ctl->step, ns = ctl->newsym;
     if (!blank) {
-        const float p = (float)__ddiv_rn(fd_exp((double)__fsub_rn(logits[tok], logits[tok])), s);
         tokens[ctl->n_out] = grx_rnnt_token{tok, ctl->frame_offset + st, duration, p};
         ctl->n_out = ctl->n_out + 1;
         const int nx = 1 - ctl->cur;
@@ -314,7 +335,6 @@ __global__ __launch_bounds__(256) void rnnt_joint_kernel(RnntCtl *ctl, RnntHp hp
     ctl->newsym = ns;
     ctl->iter = it;
     ctl->done = (st < ctl->T && it < ctl->max_iters) ? 0 : 1;
-    ctl->counter = 0;
 }
 
 __global__ void rnnt_ctl_init_kernel(RnntCtl *ctl, int T, int max_iters, int frame_offset, int last) {
@@ -426,8 +446,10 @@ grx_status enqueue_iter(grx_rnnt *m, hipStream_t st) {
                                                                   m->gh + (size_t)(L - 1) * 4 * H, m->pp, m->S);
     GRX_LAUNCHED("rnnt_pred_kernel");
     rnnt_joint_kernel<<<m->jout->tiles, 256, (size_t)k.J * 4, st>>>(m->ctl, k, m->jout->qs, m->jout->ds, m->joutb,
-                                                                    m->ep, m->pp, m->logits, m->tokens);
+                                                                    m->ep, m->pp, m->logits);
     GRX_LAUNCHED("rnnt_joint_kernel");
+    rnnt_decide_kernel<<<1, 256, 0, st>>>(m->ctl, k, m->logits, m->tokens);
+    GRX_LAUNCHED("rnnt_decide_kernel");
     return GRX_OK;
 }
 

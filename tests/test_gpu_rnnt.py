@@ -98,6 +98,21 @@ def test_iteration_bound(kern, orc):
     dec.close()
 
 
+def test_probability_on_a_rounding_boundary(kern, orc):
+    """Logits whose probability sits by a float32 rounding boundary: the
+    decoder forms the in-order sum and returns the oracle's bits."""
+    import os
+    x = np.load(os.path.join(os.path.dirname(__file__), "golden", "rnnt_softmax_boundary.npy"))
+    t = synth.rnnt_model(TINY, seed=5)
+    t["joint.out.weight"] = np.zeros_like(t["joint.out.weight"])
+    t["joint.out.bias"] = x
+    enc = synth.rnnt_encoder_output(TINY, 3)
+    want, _ = orc.RnntOracle(TINY, t).decode(enc)
+    dec = _dec(TINY, t)
+    _same_tokens(dec.decode(enc), want)
+    dec.close()
+
+
 def test_device_encoder_output(kern, orc):
     from gorelaxor_amd import hiprt
 

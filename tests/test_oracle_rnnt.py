@@ -168,3 +168,22 @@ def test_synthetic_heads_emit_and_advance():
         toks, _ = O.RnntOracle(hp, synth.rnnt_model(hp)).decode(synth.rnnt_encoder_output(hp, 40))
         frames = {f for _, f, _, _ in toks}
         assert 5 < len(toks) and len(frames) < 40
+
+
+def test_boundary_fixture_needs_the_in_order_sum():
+    """tests/golden/rnnt_softmax_boundary.npy: 1/s lies within a quarter of
+    the decoder's error interval of a float32 rounding boundary."""
+    import os
+    x = np.load(os.path.join(os.path.dirname(__file__), "golden", "rnnt_softmax_boundary.npy"))
+    V = x.size
+    s = 0.0
+    for v in x:
+        s += O.fd_exp(float(np.float32(v - x.max())))
+    q = 1.0 / s
+    f = np.float32(q)
+    other = np.nextafter(f, np.float32(np.inf if q >= float(f) else -np.inf))
+    mid = (float(f) + float(other)) / 2
+    assert abs(mid - q) <= q * (V + 4) * 2.0 ** -52 / 4
+    o = O.RnntOracle(TINY, _fixed_joint(TINY, x))
+    toks, _ = o.decode(synth.rnnt_encoder_output(TINY, 1))
+    assert toks[0][0] == int(np.argmax(x)) and np.float32(toks[0][3]) == np.float32(q)
