@@ -115,6 +115,7 @@ SIGNATURES = {
     "grx_conformer_encode_dev": (i32, [vp, vp, i32, i32, vp, vp]),
     "grx_rnnt_create": (i32, [vp, vp, C.POINTER(vp)]),
     "grx_rnnt_destroy": (i32, [vp]),
+    "grx_rnnt_load_gguf": (i32, [vp, C.c_char_p, vp, C.POINTER(vp)]),
     "grx_rnnt_set_tensor": (i32, [vp, C.c_char_p, vp, sz]),
     "grx_rnnt_state_create": (i32, [vp, C.POINTER(vp)]),
     "grx_rnnt_state_destroy": (i32, [vp]),

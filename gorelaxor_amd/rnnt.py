@@ -93,6 +93,25 @@ class TransducerDecoder:
             for name, arr in tensors.items():
                 self.set_tensor(name, arr)
 
+    @classmethod
+    def from_gguf(cls, path: str, ctx: Context | None = None) -> "TransducerDecoder":
+        """The transducer head of a FastConformer GGUF file (conformer/
+        model.go:191-235, 306-315): Q8_0 matrices go to the device as
+        stored."""
+        self = cls.__new__(cls)
+        self.handle = None
+        self.ctx = ctx or default_context()
+        h = _lib.RnntHParams()
+        out = C.c_void_p()
+        _lib.call("grx_rnnt_load_gguf", self.ctx.handle, str(path).encode(), C.byref(h), C.byref(out))
+        self.handle = out
+        acts = {v: k for k, v in JOINT_ACTS.items()}
+        self.hp = dict(d=h.d, pred_hidden=h.pred_hidden, pred_layers=h.pred_layers, pred_vocab=h.pred_vocab,
+                       joint_hidden=h.joint_hidden, joint_act=acts[h.joint_act],
+                       head_kind="tdt" if h.tdt else "rnnt", blank=h.blank, max_symbols=h.max_symbols,
+                       durations=[h.durations[i] for i in range(h.n_durations)])
+        return self
+
     def set_tensor(self, name: str, arr: np.ndarray) -> None:
         a = np.ascontiguousarray(arr)
         _lib.call("grx_rnnt_set_tensor", self.handle, name.encode(), a.ctypes.data_as(C.c_void_p), a.nbytes)

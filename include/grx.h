@@ -454,6 +454,15 @@ grx_status grx_rnnt_destroy(grx_rnnt *m);
  * durations][J]) and their float32 biases.  The decoder is ready when all
  * are set. */
 grx_status grx_rnnt_set_tensor(grx_rnnt *m, const char *name, const void *data, size_t nbytes);
+/* The transducer head of a FastConformer GGUF file (conformer/model.go:
+ * 191-235, 306-315, 337-339): readHParams' decoder settings with its checks
+ * and texts, then the decoder tensors in fromGGUF's order (the first
+ * missing one reported as there); Q8_0 matrices go to the device as stored
+ * (other matrix types are refused), vectors are widened to float32.
+ * Tensors that do not fit the settings fail ("the model file doesn't fit
+ * its own settings").  *hp_out (may be NULL) receives the settings, blank
+ * resolved. */
+grx_status grx_rnnt_load_gguf(grx_ctx *ctx, const char *path, grx_rnnt_hparams *hp_out, grx_rnnt **out);
 /* Model.NewDecoderState (rnnt.go:26-33): zeros, last = -1.  A state may
  * outlive its decoder, not the decoder's context. */
 grx_status grx_rnnt_state_create(grx_rnnt *m, grx_rnnt_state **out);
