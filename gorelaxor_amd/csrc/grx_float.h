@@ -128,10 +128,7 @@ __device__ __forceinline__ float q8_float_row(const float *xs, const int8_t *__r
             fold(b, h0, h1, dh);
         }
     } else if (live && j == 0) {  // dotQ8Go (kern.go:248-266)
-        for (int b = 0; b < nb; ++b) {
-            int4 h0, h1;
-            uint16_t dh;
-            ld(b, h0, h1, dh);
+        auto go = [&](int b, const int4 &h0, const int4 &h1, uint16_t dh) {
             int8_t w[32];
             *reinterpret_cast<int4 *>(w) = h0;
             *reinterpret_cast<int4 *>(w + 16) = h1;
@@ -146,6 +143,22 @@ __device__ __forceinline__ float q8_float_row(const float *xs, const int8_t *__r
                 q3 = __fadd_rn(q3, __fmul_rn(xb[i + 3], (float)w[i + 3]));
             }
             s = __fadd_rn(s, __fmul_rn(d, __fadd_rn(__fadd_rn(__fadd_rn(q0, q1), q2), q3)));
+        };
+        // four blocks' reads issued before their sums
+        int b = 0;
+        for (; b + 4 <= nb; b += 4) {
+            int4 g0[4], g1[4];
+            uint16_t gd[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) ld(b + u, g0[u], g1[u], gd[u]);
+#pragma unroll
+            for (int u = 0; u < 4; ++u) go(b + u, g0[u], g1[u], gd[u]);
+        }
+        for (; b < nb; ++b) {
+            int4 h0, h1;
+            uint16_t dh;
+            ld(b, h0, h1, dh);
+            go(b, h0, h1, dh);
         }
     }
     // HSUM over the row's four threads: h_j = acc[j] + acc[j+4], then (h0+h1)+(h2+h3)

@@ -222,15 +222,27 @@ __global__ __launch_bounds__(256) void rnnt_joint_kernel(const RnntCtl *ctl, Rnn
     if (ctl->done) return;
     const int J = hp.J, step = ctl->step;
     const float *e = ep + (size_t)step * J;
-    for (int i = threadIdx.x; i < J; i += blockDim.x) {
-        float v = __fadd_rn(e[i], pp[i]);
-        if (hp.act == 1)
-            v = sigm(v);
-        else if (hp.act == 2)
-            v = tanh32(v);
-        else
-            v = v != v ? v : (v > 0.f ? v : 0.f);  // Go's max(v, 0): NaN stays, -0 gives +0
-        xs[i] = v;
+    for (int i0 = threadIdx.x; i0 < J; i0 += 8 * (int)blockDim.x) {  // every read in flight first
+        float a[8], c[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const int i = i0 + u * (int)blockDim.x;
+            a[u] = i < J ? e[i] : 0.f;
+            c[u] = i < J ? pp[i] : 0.f;
+        }
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const int i = i0 + u * (int)blockDim.x;
+            if (i >= J) break;
+            float v = __fadd_rn(a[u], c[u]);
+            if (hp.act == 1)
+                v = sigm(v);
+            else if (hp.act == 2)
+                v = tanh32(v);
+            else
+                v = v != v ? v : (v > 0.f ? v : 0.f);  // Go's max(v, 0): NaN stays, -0 gives +0
+            xs[i] = v;
+        }
     }
     __syncthreads();
     int row;
@@ -249,7 +261,19 @@ __global__ __launch_bounds__(256) void rnnt_decide_kernel(RnntCtl *ctl, RnntHp h
     if (ctl->done) return;
     const int tid = threadIdx.x, V = hp.V;
     ArgBest b = {-__builtin_inff(), 0x7fffffff};
-    for (int i = tid; i < V; i += blockDim.x) b = better(b, ArgBest{logits[i], i});
+    for (int i0 = tid; i0 < V; i0 += 8 * (int)blockDim.x) {  // eight reads in flight
+        float v[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const int i = i0 + u * (int)blockDim.x;
+            v[u] = i < V ? logits[i] : -__builtin_inff();
+        }
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const int i = i0 + u * (int)blockDim.x;
+            if (i < V) b = better(b, ArgBest{v[u], i});
+        }
+    }
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) b = better(b, ArgBest{__shfl_xor(b.v, off), __shfl_xor(b.i, off)});
     if ((tid & 63) == 0) wbest[tid >> 6] = b;
@@ -269,7 +293,17 @@ __global__ __launch_bounds__(256) void rnnt_decide_kernel(RnntCtl *ctl, RnntHp h
     if (!blank) {
         const float mx = logits[tok];
         double part = 0.0;
-        for (int i = tid; i < V; i += blockDim.x) part = __dadd_rn(part, fd_exp((double)__fsub_rn(logits[i], mx)));
+        for (int i0 = tid; i0 < V; i0 += 8 * (int)blockDim.x) {
+            float v[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                const int i = i0 + u * (int)blockDim.x;
+                v[u] = i < V ? logits[i] : 0.f;
+            }
+#pragma unroll
+            for (int u = 0; u < 8; ++u)
+                if (i0 + u * (int)blockDim.x < V) part = __dadd_rn(part, fd_exp((double)__fsub_rn(v[u], mx)));
+        }
 #pragma unroll
         for (int off = 32; off > 0; off >>= 1) part = __dadd_rn(part, __shfl_xor(part, off));
         if ((tid & 63) == 0) es[tid >> 6] = part;
