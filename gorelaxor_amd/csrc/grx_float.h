@@ -59,7 +59,8 @@ __device__ __forceinline__ float dot_x4(const float *x, const float *w, int k) {
 // rows of tile `tile`), x in LDS.  Thread j keeps the reference's lane chains j
 // and j+4 of dot4q8avx, so no chain changes order, and the HSUM is formed
 // across the four as (h0+h1)+(h2+h3), h_j = acc[j]+acc[j+4].  Rows of the last
-// partial group of four take dotQ8Go in their thread 0.  Blocks are read four
+// partial group of four take dotQ8Go, its block sums spread over the four
+// threads and chained in thread 0.  Blocks are read four
 // at a time.  Returns the product (no bias) with emit set in thread 0 of a
 // live row; every thread of the workgroup must call it (shuffles).
 __device__ __forceinline__ float q8_float_row(const float *xs, const int8_t *__restrict__ qs,
@@ -127,8 +128,12 @@ __device__ __forceinline__ float q8_float_row(const float *xs, const int8_t *__r
             ld(b, h0, h1, dh);
             fold(b, h0, h1, dh);
         }
-    } else if (live && j == 0) {  // dotQ8Go (kern.go:248-266)
-        auto go = [&](int b, const int4 &h0, const int4 &h1, uint16_t dh) {
+    } else if (live) {
+        // dotQ8Go (kern.go:248-266): per block four running sums and
+        // t = d*(((q0+q1)+q2)+q3), added to s in block order.  The blocks'
+        // t are independent: thread j forms those of blocks 4g+j, and
+        // thread 0 adds each group's four in order.
+        auto blk = [&](int b, const int4 &h0, const int4 &h1, uint16_t dh) {
             int8_t w[32];
             *reinterpret_cast<int4 *>(w) = h0;
             *reinterpret_cast<int4 *>(w + 16) = h1;
@@ -142,23 +147,28 @@ __device__ __forceinline__ float q8_float_row(const float *xs, const int8_t *__r
                 q2 = __fadd_rn(q2, __fmul_rn(xb[i + 2], (float)w[i + 2]));
                 q3 = __fadd_rn(q3, __fmul_rn(xb[i + 3], (float)w[i + 3]));
             }
-            s = __fadd_rn(s, __fmul_rn(d, __fadd_rn(__fadd_rn(__fadd_rn(q0, q1), q2), q3)));
+            return __fmul_rn(d, __fadd_rn(__fadd_rn(__fadd_rn(q0, q1), q2), q3));
         };
-        // four blocks' reads issued before their sums
-        int b = 0;
-        for (; b + 4 <= nb; b += 4) {
-            int4 g0[4], g1[4];
-            uint16_t gd[4];
+        const int ngrp = (nb + 3) / 4;
+        for (int g0 = 0; g0 < ngrp; g0 += 4) {  // four groups' reads in flight (indexes clamped into range)
+            int4 a0[4], a1[4];
+            uint16_t ad[4];
+            float t[4];
 #pragma unroll
-            for (int u = 0; u < 4; ++u) ld(b + u, g0[u], g1[u], gd[u]);
+            for (int u = 0; u < 4; ++u) ld(min((g0 + u) * 4 + j, nb - 1), a0[u], a1[u], ad[u]);
 #pragma unroll
-            for (int u = 0; u < 4; ++u) go(b + u, g0[u], g1[u], gd[u]);
-        }
-        for (; b < nb; ++b) {
-            int4 h0, h1;
-            uint16_t dh;
-            ld(b, h0, h1, dh);
-            go(b, h0, h1, dh);
+            for (int u = 0; u < 4; ++u) t[u] = blk(min((g0 + u) * 4 + j, nb - 1), a0[u], a1[u], ad[u]);
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const int gb = (g0 + u) * 4;
+                const float t1 = __shfl_down(t[u], 1, 4), t2 = __shfl_down(t[u], 2, 4), t3 = __shfl_down(t[u], 3, 4);
+                if (j == 0) {
+                    if (gb < nb) s = __fadd_rn(s, t[u]);
+                    if (gb + 1 < nb) s = __fadd_rn(s, t1);
+                    if (gb + 2 < nb) s = __fadd_rn(s, t2);
+                    if (gb + 3 < nb) s = __fadd_rn(s, t3);
+                }
+            }
         }
     }
     // HSUM over the row's four threads: h_j = acc[j] + acc[j+4], then (h0+h1)+(h2+h3)
