@@ -57,6 +57,7 @@ SIGNATURES = {
     "grx_matmul_q8_prequant_dev": (i32, [vp, vp, i32, vp, vp, i32, vp, vp]),
     "grx_block_dots_dev": (i32, [vp, vp, vp, i32, vp]),
     "grx_vec_dev": (i32, [vp, i32, vp, vp, i32]),
+    "grx_layernorm_dev": (i32, [vp, i32, i32, i32, vp, vp, i32, i32, vp, vp, C.c_double]),
     "grx_linear_q8_float": (i32, [vp, vp, vp, vp, vp]),
     "grx_linear_f32": (i32, [vp, vp, vp, vp, i32, i32, vp]),
     "grx_whisper_create": (i32, [vp, vp, C.POINTER(vp)]),

@@ -45,17 +45,30 @@ def _compile_one(src: str, build_dir: str, extra: list[str]) -> tuple[str, subpr
     return obj, p
 
 
-def build(verbose: bool = True, out: str = LIB, defines: list[str] | None = None) -> str:
+def _stale(src: str, build_dir: str, headers: list[str]) -> bool:
+    obj = os.path.join(build_dir, os.path.basename(src) + ".o")
+    if not os.path.exists(obj):
+        return True
+    t = os.path.getmtime(obj)
+    return any(os.path.getmtime(f) > t for f in [src, *headers])
+
+
+def build(verbose: bool = True, out: str = LIB, defines: list[str] | None = None, incremental: bool = False) -> str:
     """Compile every csrc/*.hip for gfx950 and link gorelaxor_amd/libgrx.so
-    (or `out`, with extra -D `defines`, for a variant build)."""
+    (or `out`, with extra -D `defines`, for a variant build).  incremental:
+    recompile only sources newer than their objects (or with a newer
+    header), for development; the default rebuilds everything."""
     if not os.path.exists(HIPCC):
         raise RuntimeError(f"hipcc not found at {HIPCC}")
     build_dir = BUILD_DIR if out == LIB else os.path.join(os.path.dirname(os.path.abspath(out)), "_build")
     os.makedirs(build_dir, exist_ok=True)
     extra = [f"-D{d}" for d in (defines or [])]
     t0 = time.time()
-    jobs = [_compile_one(s, build_dir, extra) for s in sources()]
-    objs, failed = [], []
+    headers = glob.glob(os.path.join(CSRC, "*.h")) + [os.path.join(ROOT, "include", "grx.h")]
+    todo = [s for s in sources() if not incremental or _stale(s, build_dir, headers)]
+    jobs = [_compile_one(s, build_dir, extra) for s in todo]
+    objs = [os.path.join(build_dir, os.path.basename(s) + ".o") for s in sources()]
+    failed = []
     for obj, p in jobs:
         text, _ = p.communicate()
         lines = [l for l in text.splitlines() if "packed-fp32-ops" not in l]
@@ -63,7 +76,6 @@ def build(verbose: bool = True, out: str = LIB, defines: list[str] | None = None
             failed.append((obj, "\n".join(lines)))
         elif verbose and lines:
             print("\n".join(lines), file=sys.stderr)
-        objs.append(obj)
     if failed:
         raise RuntimeError("hipcc failed:\n" + "\n\n".join(f"{o}:\n{t}" for o, t in failed))
     tmp = out + ".tmp"
@@ -78,4 +90,4 @@ def build(verbose: bool = True, out: str = LIB, defines: list[str] | None = None
 
 
 if __name__ == "__main__":
-    build()
+    build(incremental="--incremental" in sys.argv[1:])

@@ -24,6 +24,7 @@
 
 #include "grx_float.h"
 #include "grx_internal.h"
+#include "grx_ln.h"
 
 namespace {
 
@@ -274,31 +275,14 @@ __global__ void sub_flatten_kernel(const float *__restrict__ y, int T, int F, in
 
 // ---------------------------------------------------------------- LayerNorm rows
 
-// kern.LayerNorm of one row (internal/kern/mathx.go:55-75) held in LDS: the
-// float64 sums (exact in practice, so their order does not show), mean and
-// inv rounded to float32, y = (v-mean)*inv*w + b rounded step by step.
+// kern.LayerNorm of one row (internal/kern/mathx.go:55-75) held in LDS:
+// float64 sums with the reference's results (ln32_stats), mean and inv
+// rounded to float32, y = (v-mean)*inv*w + b rounded step by step.  The
+// caller has the whole row in LDS (a barrier after writing it).
 __device__ void ln_row(float *v, int n, const float *w, const float *bb, double *red) {
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nw = blockDim.x >> 6;
-    double ps = 0.0;
-    for (int i = tid; i < n; i += blockDim.x) ps += (double)v[i];
-    for (int o = 32; o > 0; o >>= 1) ps += __shfl_xor(ps, o);
-    if (lane == 0) red[wave] = ps;
-    __syncthreads();
-    double sum = 0.0;
-    for (int i = 0; i < nw; ++i) sum += red[i];
-    const float mean = (float)(sum / (double)n);
-    double pv = 0.0;
-    for (int i = tid; i < n; i += blockDim.x) {
-        const double d = (double)__fsub_rn(v[i], mean);
-        pv += d * d;
-    }
-    for (int o = 32; o > 0; o >>= 1) pv += __shfl_xor(pv, o);
-    __syncthreads();
-    if (lane == 0) red[wave] = pv;
-    __syncthreads();
-    double vs = 0.0;
-    for (int i = 0; i < nw; ++i) vs += red[i];
-    const float inv = (float)(1.0 / sqrt(vs / (double)n + 1e-5));
+    const int tid = threadIdx.x;
+    float mean, inv;
+    ln32_stats(v, n, red, mean, inv);
     for (int i = tid; i < n; i += blockDim.x) {
         float t = __fsub_rn(v[i], mean);
         t = __fmul_rn(t, inv);
@@ -319,7 +303,7 @@ __global__ __launch_bounds__(kRowThreads) void ln_rows_kernel(float *__restrict_
                                                               const float *__restrict__ b2,
                                                               int8_t *__restrict__ xq, float *__restrict__ xs) {
     extern __shared__ __align__(16) float row[];
-    __shared__ double red[16];
+    __shared__ double red[48];  // ln_block_reduce
     const int r = blockIdx.x, tid = threadIdx.x;
     float *xr = x + (size_t)r * n;
     for (int i = tid; i < n / 4; i += blockDim.x)  // n % 32 == 0
@@ -743,7 +727,7 @@ __global__ __launch_bounds__(kRowThreads) void conf_dwconv_kernel(const float *_
                                                                   const float *__restrict__ cn_b,
                                                                   int8_t *__restrict__ xq, float *__restrict__ xs) {
     extern __shared__ __align__(16) float row[];
-    __shared__ double red[16];
+    __shared__ double red[48];  // ln_block_reduce
     const int r = blockIdx.x, t = r % T, b = r / T, tid = threadIdx.x;
     const int padL = (K - 1) / 2;
     const float *gb = g + (size_t)b * T * D;

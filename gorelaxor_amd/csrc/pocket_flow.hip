@@ -21,6 +21,7 @@
 #include <algorithm>
 
 #include "grx_float.h"
+#include "grx_ln.h"
 #include "pocket_internal.h"
 
 namespace {
@@ -52,28 +53,10 @@ __global__ void flow_sy_kernel(const float *__restrict__ y, const float *__restr
 __global__ void flow_lnmod_kernel(const float *__restrict__ h, int dim, const float *__restrict__ w,
                                   const float *__restrict__ b, const float *__restrict__ shift,
                                   const float *__restrict__ scale, double eps, float *__restrict__ n) {
-    __shared__ double red[kFT / 64];
-    const int t = threadIdx.x, lane = t & 63, wv = t >> 6;
-    double ps = 0.0;
-    for (int j = t; j < dim; j += kFT) ps = __dadd_rn(ps, (double)h[j]);
-    for (int o = 32; o > 0; o >>= 1) ps = __dadd_rn(ps, __shfl_xor(ps, o));
-    if (lane == 0) red[wv] = ps;
-    __syncthreads();
-    double s = 0.0;
-    for (int i = 0; i < kFT / 64; ++i) s = __dadd_rn(s, red[i]);
-    const double mean = s / (double)dim;
-    __syncthreads();
-    double pq = 0.0;
-    for (int j = t; j < dim; j += kFT) {
-        const double dd = __dsub_rn((double)h[j], mean);
-        pq = __dadd_rn(pq, __dmul_rn(dd, dd));
-    }
-    for (int o = 32; o > 0; o >>= 1) pq = __dadd_rn(pq, __shfl_xor(pq, o));
-    if (lane == 0) red[wv] = pq;
-    __syncthreads();
-    double q = 0.0;
-    for (int i = 0; i < kFT / 64; ++i) q = __dadd_rn(q, red[i]);
-    const double inv = 1.0 / sqrt(q / (double)dim + eps);
+    __shared__ double red[48];  // ln_block_reduce
+    const int t = threadIdx.x;
+    double mean, inv;
+    ln64_stats(h, dim, eps, red, mean, inv);
     for (int j = t; j < dim; j += kFT) {
         float o = (float)__dmul_rn(__dsub_rn((double)h[j], mean), inv);
         if (w) o = __fadd_rn(__fmul_rn(o, w[j]), b[j]);

@@ -30,6 +30,7 @@
 
 #include "grx_float.h"
 #include "grx_internal.h"
+#include "grx_ln.h"
 #include "pocket_internal.h"
 
 namespace {
@@ -292,29 +293,11 @@ __global__ __launch_bounds__(kThreads) void finish_kernel(const float *__restric
                                                           float eb, int *__restrict__ pos, int *__restrict__ frame,
                                                           int advance, float *__restrict__ out_hist,
                                                           float *__restrict__ eos_hist) {
-    __shared__ double red[16];
+    __shared__ double red[48];  // ln_block_reduce
     __shared__ float ov[8192], ewl[8192], part4[4];
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nw_ = blockDim.x >> 6;
-    double ps = 0.0;
-    for (int i = tid; i < d; i += blockDim.x) ps += (double)x[i];
-    for (int o = 32; o > 0; o >>= 1) ps += __shfl_xor(ps, o);
-    if (lane == 0) red[wave] = ps;
-    __syncthreads();
-    double sum = 0.0;
-    for (int w = 0; w < nw_; ++w) sum += red[w];
-    const double mean = sum / (double)d;
-    __syncthreads();
-    double pv = 0.0;
-    for (int i = tid; i < d; i += blockDim.x) {
-        const double t = (double)x[i] - mean;
-        pv += t * t;
-    }
-    for (int o = 32; o > 0; o >>= 1) pv += __shfl_xor(pv, o);
-    if (lane == 0) red[8 + wave] = pv;
-    __syncthreads();
-    double qs = 0.0;
-    for (int w = 0; w < nw_; ++w) qs += red[8 + w];
-    const double inv = 1.0 / sqrt(qs / (double)d + 1e-5);
+    const int tid = threadIdx.x;
+    double mean, inv;
+    ln64_stats(x, d, 1e-5, red, mean, inv);
     const int f = frame != nullptr ? *frame : 0;
     float *out = out_hist + (size_t)f * d;
     for (int i = tid; i < d; i += blockDim.x) {

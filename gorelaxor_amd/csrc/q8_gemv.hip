@@ -21,6 +21,7 @@
 #include <type_traits>
 
 #include "grx_internal.h"
+#include "grx_ln.h"
 
 namespace {
 
@@ -76,18 +77,6 @@ __device__ __forceinline__ int sdot8(const int4 &w0, const int4 &w1, const int4 
     return s;
 }
 
-// Sum over the workgroup in float64, the same order in every thread.
-__device__ __forceinline__ double block_sum_f64(double v, double *red, int lane, int wave, int nwaves) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
-    __syncthreads();
-    if (lane == 0) red[wave] = v;
-    __syncthreads();
-    double t = 0.0;
-    for (int w = 0; w < nwaves; ++w) t += red[w];
-    return t;
-}
-
 // Round (M rows x nb blocks) of float32 activations in LDS or global memory
 // into LDS, 32 lanes per block: lane e holds value e, the block's largest
 // magnitude comes from five xor-shuffles within the 32 lanes (the maximum
@@ -117,39 +106,6 @@ __device__ __forceinline__ void quant_into_lds(const float *src, int ld, int nb,
 
 // ---------------------------------------------------------------- one row
 
-// Cross-lane moves within rows of 16 lanes (DPP; every lane active): the
-// quad permutations [1,0,3,2] and [2,3,0,1], the mirror of each 8 and of
-// each 16 lanes.  Sums and maxima built from them hold the same value in
-// every lane of the group (a + b == b + a).
-constexpr int kDppXor1 = 0xb1, kDppXor2 = 0x4e, kDppHalfMirror = 0x141, kDppMirror = 0x140;
-
-template <int CTRL>
-__device__ __forceinline__ float dpp_f32(float v) {
-    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false));
-}
-template <int CTRL>
-__device__ __forceinline__ double dpp_f64(double v) {
-    const unsigned long long u = (unsigned long long)__double_as_longlong(v);
-    const uint32_t lo = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)u, CTRL, 0xf, 0xf, false);
-    const uint32_t hi = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)(u >> 32), CTRL, 0xf, 0xf, false);
-    return __longlong_as_double((long long)(((unsigned long long)hi << 32) | lo));
-}
-__device__ __forceinline__ double readlane_f64(double v, int l) {
-    const unsigned long long u = (unsigned long long)__double_as_longlong(v);
-    const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)u, l);
-    const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(u >> 32), l);
-    return __longlong_as_double((long long)(((unsigned long long)hi << 32) | lo));
-}
-// The wave's float64 sum, the same in every lane: rows of 16 by DPP, then
-// (row0 + row1) + (row2 + row3).
-__device__ __forceinline__ double wave_sum_f64(double v) {
-    v = __dadd_rn(v, dpp_f64<kDppXor1>(v));
-    v = __dadd_rn(v, dpp_f64<kDppXor2>(v));
-    v = __dadd_rn(v, dpp_f64<kDppHalfMirror>(v));
-    v = __dadd_rn(v, dpp_f64<kDppMirror>(v));
-    return __dadd_rn(__dadd_rn(readlane_f64(v, 0), readlane_f64(v, 16)),
-                     __dadd_rn(readlane_f64(v, 32), readlane_f64(v, 48)));
-}
 // The largest of each 8 lanes' values (a Q8_0 block held as 8 float4s).
 __device__ __forceinline__ float max8(float m) {
     float t = dpp_f32<kDppXor1>(m);
@@ -244,89 +200,14 @@ __device__ __forceinline__ void wave_row_prologue(const GemvArgs &a, int m, int8
         }
     }
     if constexpr (PRO == GRX_PRO_LN || PRO == GRX_PRO_EMBED_LN) {
-        // layerNorm (internal/kern/mathx.go:55-75): float64 sums,
+        // layerNorm (internal/kern/mathx.go:55-75): float64 sums (in the
+        // reference's order where the tree's could round differently),
         // mean and inv rounded to float32, y = (v-mean)*inv*w + b
-        double ps = 0.0;
-#pragma unroll
-        for (int j = 0; j < NP; ++j) {
-            if (j * 64 + lane < npc) {
-                ps = __dadd_rn(ps, (double)xv[j].x);
-                ps = __dadd_rn(ps, (double)xv[j].y);
-                ps = __dadd_rn(ps, (double)xv[j].z);
-                ps = __dadd_rn(ps, (double)xv[j].w);
-            }
-        }
-        const float mean = (float)(wave_sum_f64(ps) / (double)K);
-        double pv = 0.0;
-        auto sq = [&](float v) {
-            const double d = (double)__fsub_rn(v, mean);
-            pv = __dadd_rn(pv, __dmul_rn(d, d));
-        };
-#pragma unroll
-        for (int j = 0; j < NP; ++j) {
-            if (j * 64 + lane < npc) {
-                sq(xv[j].x);
-                sq(xv[j].y);
-                sq(xv[j].z);
-                sq(xv[j].w);
-            }
-        }
-        const double vs = wave_sum_f64(pv);
-        const float inv = (float)(1.0 / sqrt(vs / (double)K + 1e-5));
-        auto nrm = [&](float v, float w, float b) {
-            float t = __fsub_rn(v, mean);
-            t = __fmul_rn(t, inv);
-            t = __fmul_rn(t, w);
-            return __fadd_rn(t, b);
-        };
-#pragma unroll
-        for (int j = 0; j < NP; ++j) {
-            xv[j].x = nrm(xv[j].x, wv[j].x, bv[j].x);
-            xv[j].y = nrm(xv[j].y, wv[j].y, bv[j].y);
-            xv[j].z = nrm(xv[j].z, wv[j].z, bv[j].z);
-            xv[j].w = nrm(xv[j].w, wv[j].w, bv[j].w);
-        }
+        wave_ln32<NP>(xv, wv, bv, npc, lane);
     } else if constexpr (PRO == GRX_PRO_LN64) {
         // layerNorm of pockettts/nn.go:27-49: statistics and the
         // normalized value in float64, gain and bias in float32
-        double ps = 0.0;
-#pragma unroll
-        for (int j = 0; j < NP; ++j) {
-            if (j * 64 + lane < npc) {
-                ps = __dadd_rn(ps, (double)xv[j].x);
-                ps = __dadd_rn(ps, (double)xv[j].y);
-                ps = __dadd_rn(ps, (double)xv[j].z);
-                ps = __dadd_rn(ps, (double)xv[j].w);
-            }
-        }
-        const double mean = wave_sum_f64(ps) / (double)K;
-        double pv = 0.0;
-        auto sq = [&](float v) {
-            const double d = __dsub_rn((double)v, mean);
-            pv = __dadd_rn(pv, __dmul_rn(d, d));
-        };
-#pragma unroll
-        for (int j = 0; j < NP; ++j) {
-            if (j * 64 + lane < npc) {
-                sq(xv[j].x);
-                sq(xv[j].y);
-                sq(xv[j].z);
-                sq(xv[j].w);
-            }
-        }
-        const double inv = 1.0 / sqrt(wave_sum_f64(pv) / (double)K + a.ln_eps);
-        const bool gb = a.ln_w != nullptr;
-        auto nrm = [&](float v, float w, float b) {
-            float o = (float)__dmul_rn(__dsub_rn((double)v, mean), inv);
-            return gb ? __fadd_rn(__fmul_rn(o, w), b) : o;
-        };
-#pragma unroll
-        for (int j = 0; j < NP; ++j) {
-            xv[j].x = nrm(xv[j].x, wv[j].x, bv[j].x);
-            xv[j].y = nrm(xv[j].y, wv[j].y, bv[j].y);
-            xv[j].z = nrm(xv[j].z, wv[j].z, bv[j].z);
-            xv[j].w = nrm(xv[j].w, wv[j].w, bv[j].w);
-        }
+        wave_ln64<NP>(xv, wv, bv, a.ln_w != nullptr, npc, lane, a.ln_eps);
     }
     // quantU8 (q8int.go:88-105): a block is 8 pieces in 8 lanes
 #pragma unroll
@@ -572,7 +453,6 @@ __global__ __launch_bounds__(64 * W) void gemv_q8_kernel(const GemvArgs a) {
         for (int m = 0; m < M; ++m) {
             const float *xr = a.x + (size_t)m * a.lda;
             float *fr = lf + (size_t)m * K;
-            double ps = 0.0;
             if constexpr (PRO == GRX_PRO_EMBED_LN) {
                 // the row is tokEmb.row(tok) + decPos[pos] (whisper/decoder.go:42-46),
                 // built by every workgroup; tile 0 stores it for the residual
@@ -584,25 +464,14 @@ __global__ __launch_bounds__(64 * W) void gemv_q8_kernel(const GemvArgs a) {
                     const float d = grx_f16_to_f32(a.emb_ds[((size_t)etile * nb + b) * 64 + elane]);
                     const float v = __fadd_rn(__fmul_rn((float)q, d), a.pos_emb[(size_t)p * K + i]);
                     fr[i] = v;
-                    ps += (double)v;
                     if (tile == 0) a.x_out[(size_t)m * a.lda + i] = v;
                 }
             } else {
-                for (int i = tid; i < K; i += 64 * W) {
-                    const float v = xr[i];
-                    fr[i] = v;
-                    ps += (double)v;
-                }
+                for (int i = tid; i < K; i += 64 * W) fr[i] = xr[i];
             }
-            const double sum = block_sum_f64(ps, red, lane, wave, W);
-            const float mean = (float)(sum / (double)K);
-            double pv = 0.0;
-            for (int i = tid; i < K; i += 64 * W) {
-                const double d = (double)__fsub_rn(fr[i], mean);
-                pv += d * d;
-            }
-            const double vs = block_sum_f64(pv, red + W, lane, wave, W);
-            const float inv = (float)(1.0 / sqrt(vs / (double)K + 1e-5));
+            __syncthreads();  // the row, built by every thread, is read by all of them
+            float mean, inv;
+            ln32_stats(fr, K, red, mean, inv);
             for (int i = tid; i < K; i += 64 * W) {
                 float t = __fsub_rn(fr[i], mean);
                 t = __fmul_rn(t, inv);
@@ -619,20 +488,10 @@ __global__ __launch_bounds__(64 * W) void gemv_q8_kernel(const GemvArgs a) {
         for (int m = 0; m < M; ++m) {
             const float *xr = a.x + (size_t)m * a.lda;
             float *fr = lf + (size_t)m * K;
-            double ps = 0.0;
-            for (int i = tid; i < K; i += 64 * W) {
-                const float v = xr[i];
-                fr[i] = v;
-                ps += (double)v;
-            }
-            const double mean = block_sum_f64(ps, red, lane, wave, W) / (double)K;
-            double pv = 0.0;
-            for (int i = tid; i < K; i += 64 * W) {
-                const double d = (double)fr[i] - mean;
-                pv += d * d;
-            }
-            const double q = block_sum_f64(pv, red + W, lane, wave, W);
-            const double inv = 1.0 / sqrt(q / (double)K + a.ln_eps);
+            for (int i = tid; i < K; i += 64 * W) fr[i] = xr[i];
+            __syncthreads();
+            double mean, inv;
+            ln64_stats(fr, K, a.ln_eps, red, mean, inv);
             for (int i = tid; i < K; i += 64 * W) {
                 float o = (float)(((double)fr[i] - mean) * inv);
                 if (a.ln_w != nullptr) o = __fadd_rn(__fmul_rn(o, a.ln_w[i]), a.ln_b[i]);
@@ -1121,7 +980,7 @@ size_t gemv_smem(int M, int W, int pro, int nb) {
     const size_t n_p = W > 1 ? (size_t)M * (M > 1 ? kRound : nb) * 64 * 4 : 0;
     const size_t n_f = pro >= GRX_PRO_LN ? (size_t)M * K * 4 : 0;
     n += n_p > n_f ? n_p : n_f;  // the two share their bytes
-    if (pro >= GRX_PRO_LN) n += 2 * 16 * sizeof(double);
+    if (pro >= GRX_PRO_LN) n += 3 * 16 * sizeof(double);  // ln_block_reduce
     return n;
 }
 

@@ -2,36 +2,20 @@
 // rows rounded to Q8_0 for the next product, and the whisper decoder's
 // token + position embedding in front of it.  One workgroup per row.
 #include "grx_internal.h"
+#include "grx_ln.h"
 
 namespace {
 
 constexpr int kThreads = 256;
 
-// kern.LayerNorm of one row held in LDS (internal/kern/mathx.go:55-75): the
-// float64 sums (exact in practice, so their order does not show), mean and
-// inv rounded to float32, y = (v-mean)*inv*w + b rounded step by step.
+// kern.LayerNorm of one row held in LDS (internal/kern/mathx.go:55-75):
+// float64 sums with the reference's results (ln32_stats), mean and inv
+// rounded to float32, y = (v-mean)*inv*w + b rounded step by step.  The
+// caller has the whole row in LDS (a barrier after writing it).
 __device__ void ln_lds_row(float *v, int n, const float *w, const float *bb, double *red) {
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nw = blockDim.x >> 6;
-    double ps = 0.0;
-    for (int i = tid; i < n; i += blockDim.x) ps += (double)v[i];
-    for (int o = 32; o > 0; o >>= 1) ps += __shfl_xor(ps, o);
-    if (lane == 0) red[wave] = ps;
-    __syncthreads();
-    double sum = 0.0;
-    for (int i = 0; i < nw; ++i) sum += red[i];
-    const float mean = (float)(sum / (double)n);
-    double pv = 0.0;
-    for (int i = tid; i < n; i += blockDim.x) {
-        const double d = (double)__fsub_rn(v[i], mean);
-        pv += d * d;
-    }
-    for (int o = 32; o > 0; o >>= 1) pv += __shfl_xor(pv, o);
-    __syncthreads();
-    if (lane == 0) red[wave] = pv;
-    __syncthreads();
-    double vs = 0.0;
-    for (int i = 0; i < nw; ++i) vs += red[i];
-    const float inv = (float)(1.0 / sqrt(vs / (double)n + 1e-5));
+    const int tid = threadIdx.x;
+    float mean, inv;
+    ln32_stats(v, n, red, mean, inv);
     for (int i = tid; i < n; i += blockDim.x) {
         float t = __fsub_rn(v[i], mean);
         t = __fmul_rn(t, inv);
@@ -68,7 +52,7 @@ __global__ __launch_bounds__(kThreads) void ln_quant_rows_kernel(const float *__
                                                                  const float *__restrict__ b, int8_t *__restrict__ xq,
                                                                  float *__restrict__ xs) {
     extern __shared__ __align__(16) float row[];
-    __shared__ double red[16];
+    __shared__ double red[48];  // ln_block_reduce
     const int r = blockIdx.x;
     const float *xr = x + (size_t)r * ldx;
     if ((n & 3) == 0 && (ldx & 3) == 0) {  // 16-byte loads, all in flight together
@@ -91,7 +75,7 @@ __global__ __launch_bounds__(kThreads) void embed_ln_quant_kernel(
     const uint16_t *__restrict__ emb_ds, int nb, const float *__restrict__ pos_emb, float *__restrict__ x,
     const float *__restrict__ w, const float *__restrict__ b, int8_t *__restrict__ xq, float *__restrict__ xs) {
     extern __shared__ __align__(16) float row[];
-    __shared__ double red[16];
+    __shared__ double red[48];  // ln_block_reduce
     const int r = blockIdx.x, n = nb * GRX_QK;
     const int t = tok[r], p = *pos;
     const int etile = t >> 6, elane = t & 63;

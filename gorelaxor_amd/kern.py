@@ -220,6 +220,23 @@ def vec_dev(fn: int, y, x, n: int, ctx: Context | None = None) -> None:
     _lib.call("grx_vec_dev", ctx.handle, fn, _ptr(y), _ptr(x), n)
 
 
+# grx_layernorm_dev: forms, kernel forms and flags
+LN_KERN, LN_F64 = 0, 1
+LN_BLOCK, LN_WAVE = 0, 1
+LN_TREE_ONLY = 1
+
+
+def layernorm_dev(form: int, impl: int, y, x, rows: int, n: int, w=None, b=None, eps: float = 1e-5,
+                  flags: int = 0, ctx: Context | None = None) -> None:
+    """The path's LayerNorms on device rows (kern's layerNorm, internal/
+    kern/mathx.go:55-75, or pockettts', nn.go:27-49) through the kernels'
+    own code, for parity checks."""
+    ctx = ctx or default_context()
+    _lib.call("grx_layernorm_dev", ctx.handle, form, impl, flags, _ptr(y), _ptr(x), rows, n,
+              _ptr(w) if w is not None else None, _ptr(b) if b is not None else None, float(eps))
+
+
 __all__ = ["QK", "Q8Bytes", "F32", "F16", "Q8_0", "Context", "default_context", "device_count", "Weight",
            "NewQ8", "ToQ8", "MatMul", "Linear", "LinearFloat", "LinearF32", "matmul_dev", "quant_act_dev", "matmul_prequant_dev",
-           "block_dots_dev", "vec_dev", "VEC_EXPF", "VEC_EXP8", "VEC_GELU", "GrxError"]
+           "block_dots_dev", "vec_dev", "VEC_EXPF", "VEC_EXP8", "VEC_GELU", "layernorm_dev", "LN_KERN", "LN_F64",
+           "LN_BLOCK", "LN_WAVE", "LN_TREE_ONLY", "GrxError"]

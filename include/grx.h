@@ -131,6 +131,30 @@ grx_status grx_block_dots_dev(grx_ctx *ctx, int32_t *s, const int8_t *q, int m,
 enum { GRX_VEC_EXPF = 0, GRX_VEC_EXP8 = 1, GRX_VEC_GELU = 2 };
 grx_status grx_vec_dev(grx_ctx *ctx, int fn, float *y, const float *x, int n);
 
+/* The path's two LayerNorms on `rows` rows of n float32 values, device
+ * pointers, exactly as the decode and encode kernels evaluate them.  For
+ * parity checks.
+ *   form GRX_LN_KERN  kern's layerNorm (internal/kern/mathx.go:55-75):
+ *                     float64 sums, mean and inv rounded to float32,
+ *                     eps 1e-5; w and b required
+ *   form GRX_LN_F64   pockettts' layerNorm (pockettts/nn.go:27-49): mean
+ *                     and inv in float64, each output rounded to float32,
+ *                     then * w + b when given (both or neither); eps given
+ *   impl GRX_LN_BLOCK a workgroup per row, the row in LDS (the encoder's
+ *                     rows, several-row products, the frame end, the flow
+ *                     head); n <= 8192
+ *   impl GRX_LN_WAVE  one wave per row, the row in registers (the one-row
+ *                     products' prologues); n % 4 == 0, n <= 1280
+ * The sums are formed in parallel, and again in the reference's order for
+ * the rows where the parallel sums could round to other float32 results.
+ * flags GRX_LN_TREE_ONLY skips that second pass (tests use it to show
+ * which rows need it); products never set it. */
+enum { GRX_LN_KERN = 0, GRX_LN_F64 = 1 };
+enum { GRX_LN_BLOCK = 0, GRX_LN_WAVE = 1 };
+enum { GRX_LN_TREE_ONLY = 1 };
+grx_status grx_layernorm_dev(grx_ctx *ctx, int form, int impl, int flags, float *y, const float *x, int rows, int n,
+                             const float *w, const float *b, double eps);
+
 /* kern.Linear of ONE row through the float route (kern.go:185-196 ->
  * gemvRows, gemm.go:195-259): what the reference does for m = 1 when the
  * weight keeps its rows (no DropRows) - dot4q8avx for rows in whole groups
