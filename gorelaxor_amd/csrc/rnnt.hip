@@ -32,6 +32,7 @@ namespace {
 
 constexpr int kIters = 16;     // loop iterations per graph replay
 constexpr int kMaxDur = 16;    // TDT durations held
+constexpr int kMaxDuration = 1 << 20;  // the largest duration (frames) a TDT head may name
 constexpr int kExpChunk = 1024;
 
 // The loop state (rnnt.go:134-171) in device memory.
@@ -355,7 +356,10 @@ __global__ __launch_bounds__(256) void rnnt_decide_kernel(RnntCtl *ctl, RnntHp h
             ns = 0;
         }
     } else {
-        st += duration;
+        // durations are at most kMaxDuration (checked at create) and st < T
+        // here, so the sum cannot overflow; past T the loop is over, so st
+        // is kept at T (no frame index past T is ever read)
+        st = min(st + duration, ctl->T);
         ++ns;
         if (duration != 0) {
             ns = 0;
@@ -556,7 +560,9 @@ extern "C" grx_status grx_rnnt_create(grx_ctx *ctx, const grx_rnnt_hparams *hp, 
         if (hp->max_symbols < 1 || hp->max_symbols > 100)
             return grx_fail(GRX_EINVAL, "conformer: tdt.max_symbols %d is out of range", hp->max_symbols);
         for (int i = 0; i < hp->n_durations; ++i)
-            if (hp->durations[i] < 0) return grx_fail(GRX_EINVAL, "grx_rnnt_create: negative duration");
+            if (hp->durations[i] < 0 || hp->durations[i] > kMaxDuration)
+                return grx_fail(GRX_EINVAL, "grx_rnnt_create: duration %d outside 0..%d", hp->durations[i],
+                                kMaxDuration);
     }
     grx_rnnt *m = new grx_rnnt;
     m->ctx = ctx;

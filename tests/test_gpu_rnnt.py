@@ -158,6 +158,11 @@ def test_errors(kern):
         TransducerDecoder(dict(TDT_TINY, max_symbols=0))
     with pytest.raises(ValueError, match="not supported"):
         TransducerDecoder(dict(TINY, head_kind="ctc"))
+    # a duration that could carry the frame index past int32 is refused at
+    # create (nothing is launched)
+    for bad in (-1, (1 << 20) + 1, (1 << 31) - 1):
+        with pytest.raises(GrxError, match="duration"):
+            TransducerDecoder(dict(TDT_TINY, durations=[0, 1, bad]))
     t = synth.rnnt_model(TINY)
     dec = TransducerDecoder(TINY)
     with pytest.raises(GrxError, match="unknown tensor"):
