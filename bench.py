@@ -341,7 +341,8 @@ def conformer_bench(args) -> dict:
     batch 1 and 16, mel and output resident in HBM.  Utterances/s, int8 TOPS
     of the Linears against the 5 POP/s MFMA peak; batch 1 output checked
     against the oracle, whose encode of the same utterance is the CPU
-    baseline."""
+    baseline, and each utterance of the batch of 16 against its own batch-1
+    encode."""
     import oracle
     from gorelaxor_amd import hiprt
     from gorelaxor_amd.conformer import ConformerEncoder, frames_out
@@ -380,14 +381,24 @@ def conformer_bench(args) -> dict:
             r["weight_bytes"] = wbytes
             r["weight_stream_gbs"] = round(wbytes / (best * 1e-3) / 1e9, 1)
             out1 = do.download(np.float32, (T, d))
+        else:
+            out16 = do.download(np.float32, (batch, T, d))
         res[f"batch{batch}"] = r
         del dm, do
+    # each utterance of the batch of 16 bit-identical to its own batch-1
+    # encode (utterance 0's batch-1 encode is checked against the oracle)
+    same16 = True
+    for i in range(16):
+        one, _ = enc.encode(mel[i:i + 1], valid)
+        same16 = same16 and bool(np.array_equal(one[0].view(np.uint32), out16[i].view(np.uint32)))
+    same16 = same16 and bool(np.array_equal(out1.view(np.uint32), out16[0].view(np.uint32)))
     enc.close()
     oracle.build()
     t0 = time.perf_counter()
     want, L = oracle.ConformerOracle(hp, t).encode(mel[0], valid)
     cpu_s = time.perf_counter() - t0
     res["parity_bit_exact"] = bool(np.array_equal(out1.view(np.uint32), want.view(np.uint32)))
+    res["batch16"]["parity_each_equals_its_batch1_encode"] = same16
     res["cpu_baseline"] = {"value": round(1.0 / cpu_s, 4), "unit": "utterances/s", "cores": 1, "kind": "port",
                            "sample": f"one 10 s utterance, all 24 layers, on the oracle (scalar C, 1 thread), "
                                      f"{cpu_s:.1f} s"}

@@ -152,3 +152,23 @@ def test_parakeet_24_layers_bit_exact_and_batched(kern, orc):
     assert np.array_equal(got[0].view(np.uint32), want.view(np.uint32)), np.abs(got[0] - want).max()
     x = got[0, :125]
     assert np.isfinite(x).all() and 0.3 < float(np.abs(x).mean()) < 3.0
+
+
+def test_parakeet_24_layers_batch16(kern, orc):
+    """The configuration's batch of 16: sixteen 10 s noise utterances through
+    all 24 layers at once (the batch whose attention takes the 16-query-row
+    LDS kernel at T = 126).  Each utterance's output is bit-identical to its
+    own batch-1 encode, and utterance 0 to the oracle."""
+    hp = dict(PARAKEET_TDT_06B)
+    t = conformer_model(hp, seed=32)
+    mel, frames, valid = _mels(hp, 16, 10.0, 70)
+    enc = _enc(kern, hp, t)
+    got, lens = enc.encode(mel, valid)
+    assert got.shape[:2] == (16, 126) and list(lens) == [125] * 16
+    for i in range(16):
+        one, _ = enc.encode(mel[i:i + 1], valid)
+        assert np.array_equal(one[0].view(np.uint32), got[i].view(np.uint32)), i
+    enc.close()
+    want, L = orc.ConformerOracle(hp, t).encode(mel[0], valid)
+    assert L == 125
+    assert np.array_equal(got[0].view(np.uint32), want.view(np.uint32)), np.abs(got[0] - want).max()

@@ -87,14 +87,16 @@ def test_context_limit(kern, orc):
 
 
 def test_configured_shape(kern, orc):
-    """d 1024, 16 heads, 6 layers, FFN 4096: a 64-row prefix, then 24
-    frames, bit-identical."""
+    """d 1024, 16 heads, 6 layers, FFN 4096: a 64-row prefix, then the
+    configuration's 250 frames (the cache grows from 64 to 314 positions),
+    every frame's output and eos logit bit-identical."""
     hp = dict(POCKET_TTS_LM)
     ref, lm = _pair(orc, hp, seed=5)
-    x, lat = pocket_inputs(hp, 24, prefix=64, seed=6)
+    x, lat = pocket_inputs(hp, 250, prefix=64, seed=6)
     assert _same(lm.run(x), ref.run(x))
     outs, eos = lm.frames(lat)
-    for k in range(24):
+    assert lm.pos == 314
+    for k in range(250):
         wo, we = ref.step(lat[k])
         assert _same(outs[k], wo) and _same(eos[k], we), k
 

@@ -109,17 +109,28 @@ def test_context_limit_and_errors(kern, orc):
 
 
 def test_base_en_shape_greedy(kern, orc):
-    """whisper base.en shape: the prompt, then greedy steps; tokens identical
-    and the last logits bit-identical."""
+    """whisper base.en shape over the configuration's whole decode: a
+    4-token prompt, then 220 greedy steps (the cache grows from 4 to 224
+    positions, whisper/transcribe.go:165).  The device's greedy loop gives
+    the oracle's tokens, and stepping both one token at a time, every
+    step's logits are bit-identical."""
     hp = dict(WHISPER_BASE_EN)
     ref, dec = _pair(orc, hp, seed=7)
-    n_steps = 16
-    want = ref.greedy([50257, 50362, 50363, 50258], n_steps)
-    got = dec.greedy([50257, 50362, 50363, 50258], n_steps)
+    prompt, n_steps = [50257, 50362, 50363, 50258], 220
+    want = ref.greedy(prompt, n_steps)
+    got = dec.greedy(prompt, n_steps)
     assert list(got) == list(want)
-    lr = ref.decode([int(want[-1])])
-    lg, _ = dec.decode([int(got[-1])])
-    assert _same(lg, lr)
+    ref.reset()
+    dec.reset()
+    lr = ref.decode(prompt)
+    lg, nxt = dec.decode(prompt)
+    assert _same(lg, lr) and nxt == int(want[0])
+    for s in range(n_steps):
+        lr = ref.decode([int(want[s])])
+        lg, nxt = dec.decode([int(want[s])])
+        assert _same(lg, lr), f"step {s}: max |diff| {np.abs(lg - lr).max()}"
+        assert nxt == int(want[s + 1]), s
+    assert dec.pos == len(prompt) + n_steps
 
 
 def _streams(hp, t, n, seed):
@@ -185,8 +196,9 @@ def test_streams_errors(kern):
 
 def test_large_v3_turbo_eight_streams(kern, orc):
     """large-v3-turbo shape (d 1280, 20 heads, 4 layers, FFN 5120, vocab
-    51866, 1500 audio positions), 8 streams: two streams' tokens against the
-    oracle, the rest against their own single-stream GPU decode."""
+    51866, 1500 audio positions), 8 streams over the configuration's 220
+    greedy steps each: two streams' tokens against the oracle, the rest
+    against their own single-stream GPU decode."""
     from gorelaxor_amd.synth import WHISPER_LARGE_V3_TURBO
     from gorelaxor_amd.whisper import WhisperDecoder
 
@@ -194,7 +206,7 @@ def test_large_v3_turbo_eight_streams(kern, orc):
     t = whisper_model(hp, seed=23)
     dec, encs = _streams(hp, t, 8, seed=60)
     prompt = [50258, 50259, 50360, 50364]
-    n = 12
+    n = 220
     got = dec.greedy_streams([prompt] * 8, n)
     dec.close()
     for k in (0, 5):
