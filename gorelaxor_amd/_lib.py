@@ -53,6 +53,7 @@ SIGNATURES = {
     "grx_matmul_q8": (i32, [vp, vp, i32, vp, i32, i32, vp, vp]),
     "grx_linear_q8": (i32, [vp, vp, vp, i32, vp, vp]),
     "grx_matmul_q8_dev": (i32, [vp, vp, i32, vp, i32, i32, vp, vp]),
+    "grx_matmul_q8_dev_noalloc": (i32, [vp, vp, i32, vp, i32, i32, vp, vp]),
     "grx_quant_act_dev": (i32, [vp, vp, vp, vp, i32, i32, i32]),
     "grx_matmul_q8_prequant_dev": (i32, [vp, vp, i32, vp, vp, i32, vp, vp]),
     "grx_block_dots_dev": (i32, [vp, vp, vp, i32, vp]),

@@ -65,6 +65,7 @@ extern "C" grx_status grx_ctx_create(int device, grx_ctx **out) {
         delete c;
         return grx_hip_fail(e, "hipStreamCreateWithFlags");
     }
+    grx_noalloc_setup(device);  // grx_matmul_q8_dev_noalloc's scratch address on this device
     *out = c;
     return GRX_OK;
 }

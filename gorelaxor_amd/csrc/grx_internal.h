@@ -83,6 +83,9 @@ grx_status grx_sample_run(grx_ctx *ctx, const float *dev_logits, const float *ho
 grx_status grx_gguf_tensor_data(const grx_gguf *g, const char *name, int *type, std::vector<uint8_t> *out);
 #endif
 grx_status grx_hip_fail(hipError_t e, const char *what);
+// q8_gemv.hip: looks up grx_matmul_q8_dev_noalloc's device scratch on the
+// current device, once (grx_ctx_create calls it)
+void grx_noalloc_setup(int device);
 grx_status grx_ctx_scratch(grx_ctx *ctx, size_t bytes, void **out);
 
 #define GRX_HIP(expr)                                                       \

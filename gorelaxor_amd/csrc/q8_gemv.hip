@@ -18,6 +18,7 @@
 // in block order afterwards, so the result is the same bit for bit.
 #include <stdlib.h>
 
+#include <mutex>
 #include <type_traits>
 
 #include "grx_internal.h"
@@ -1214,6 +1215,65 @@ extern "C" grx_status grx_matmul_q8_dev(grx_ctx *ctx, float *dst, int ldc, const
     if (s != GRX_OK) return s;
     int8_t *q = (int8_t *)buf;
     float *sc = (float *)((char *)buf + qbytes);
+    s = grx_quant_act_dev(ctx, q, sc, x, lda, m, K);
+    if (s != GRX_OK) return s;
+    return grx_matmul_q8_prequant_dev(ctx, dst, ldc, q, sc, m, w, bias);
+}
+
+// ---------------------------------------------------------------- allocation-free product
+
+// Device scratch of grx_matmul_q8_dev_noalloc: the last call's rounded
+// activations, int8 [m][K] (256-byte aligned), then float32 scales
+// [m][K/32].  Each GPU holds its own copy for the life of the process, and
+// every call on a GPU shares it: calls that overlap on one GPU (two
+// streams, or two threads) race for it.  Nothing in it needs to start at
+// zero: each call writes every byte it reads.
+constexpr size_t kNoAllocScratch = (size_t)4 << 20;
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratch];
+
+// The device address of `scratch` on each device (the array's name is a
+// host-side stand-in, not a device address), looked up once per device.
+constexpr int kMaxDevices = 64;
+static std::mutex g_scratch_mu;
+static void *g_scratch_ptr[kMaxDevices];
+static hipError_t g_scratch_err[kMaxDevices];
+
+// Called by grx_ctx_create with `device` current.
+void grx_noalloc_setup(int device) {
+    if (device < 0 || device >= kMaxDevices) return;
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    if (g_scratch_ptr[device] != nullptr) return;
+    void *p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    g_scratch_err[device] = e;
+    if (e == hipSuccess) g_scratch_ptr[device] = p;
+}
+
+extern "C" grx_status grx_matmul_q8_dev_noalloc(grx_ctx *ctx, float *dst, int ldc, const float *x, int lda, int m,
+                                                const grx_weight *w, const float *bias) {
+    grx_status s = check_mm("grx_matmul_q8_dev_noalloc", ctx, dst, ldc, x, lda, m, w);
+    if (s != GRX_OK) return s;
+    if (m == 0 || w->rows == 0) return GRX_OK;
+    const int K = w->cols, nb = w->nb;
+    const size_t qbytes = ((size_t)m * K + 255) & ~(size_t)255;
+    const size_t need = qbytes + (size_t)m * nb * 4;
+    if (need > kNoAllocScratch)
+        return grx_fail(GRX_ESIZE,
+                        "grx_matmul_q8_dev_noalloc: %d rows of %d values need %zu bytes of scratch, above its "
+                        "%zu (call grx_matmul_q8_dev, or split the rows)",
+                        m, K, need, kNoAllocScratch);
+    void *base;
+    {
+        std::lock_guard<std::mutex> lk(g_scratch_mu);
+        if (ctx->device >= kMaxDevices) return grx_fail(GRX_EINVAL, "grx_matmul_q8_dev_noalloc: device %d", ctx->device);
+        base = g_scratch_ptr[ctx->device];
+        if (base == nullptr)
+            return grx_hip_fail(g_scratch_err[ctx->device] != hipSuccess ? g_scratch_err[ctx->device] : hipErrorNotReady,
+                                "hipGetSymbolAddress(scratch)");
+    }
+    GRX_HIP(hipSetDevice(ctx->device));
+    int8_t *q = static_cast<int8_t *>(base);
+    float *sc = reinterpret_cast<float *>(static_cast<char *>(base) + qbytes);
     s = grx_quant_act_dev(ctx, q, sc, x, lda, m, K);
     if (s != GRX_OK) return s;
     return grx_matmul_q8_prequant_dev(ctx, dst, ldc, q, sc, m, w, bias);

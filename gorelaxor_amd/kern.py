@@ -194,6 +194,15 @@ def matmul_dev(dst, x, m: int, w: Weight, bias=None, ldc: int | None = None, lda
               w.handle, _ptr(bias))
 
 
+def matmul_dev_noalloc(dst, x, m: int, w: Weight, bias=None, ldc: int | None = None, lda: int | None = None,
+                       ctx: Context | None = None) -> None:
+    """matmul_dev with no allocation (grx_matmul_q8_dev_noalloc): the
+    library's fixed per-GPU scratch holds the rounded activations."""
+    ctx = ctx or w.ctx
+    _lib.call("grx_matmul_q8_dev_noalloc", ctx.handle, _ptr(dst), ldc or w.Rows, _ptr(x), lda or w.Cols, m,
+              w.handle, _ptr(bias))
+
+
 def quant_act_dev(q, sc, x, m: int, k: int, lda: int | None = None, ctx: Context | None = None) -> None:
     ctx = ctx or default_context()
     _lib.call("grx_quant_act_dev", ctx.handle, _ptr(q), _ptr(sc), _ptr(x), lda or k, m, k)
@@ -237,6 +246,7 @@ def layernorm_dev(form: int, impl: int, y, x, rows: int, n: int, w=None, b=None,
 
 
 __all__ = ["QK", "Q8Bytes", "F32", "F16", "Q8_0", "Context", "default_context", "device_count", "Weight",
-           "NewQ8", "ToQ8", "MatMul", "Linear", "LinearFloat", "LinearF32", "matmul_dev", "quant_act_dev", "matmul_prequant_dev",
+           "NewQ8", "ToQ8", "MatMul", "Linear", "LinearFloat", "LinearF32", "matmul_dev", "matmul_dev_noalloc",
+           "quant_act_dev", "matmul_prequant_dev",
            "block_dots_dev", "vec_dev", "VEC_EXPF", "VEC_EXP8", "VEC_GELU", "layernorm_dev", "LN_KERN", "LN_F64",
            "LN_BLOCK", "LN_WAVE", "LN_TREE_ONLY", "GrxError"]

@@ -104,6 +104,18 @@ grx_status grx_linear_q8(grx_ctx *ctx, float *dst, const float *x, int m, const 
 grx_status grx_matmul_q8_dev(grx_ctx *ctx, float *dst, int ldc, const float *x, int lda, int m,
                              const grx_weight *w, const float *bias);
 
+/* grx_matmul_q8_dev without any allocation.  No counterpart in the
+ * reference: it is for callers that cannot allocate device memory (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  The rounded activations go to a fixed device array of the
+ * library (4 MiB per GPU, held until the process ends) instead of the
+ * context's scratch: m * cols + m * cols/32 * 4 bytes (plus alignment to
+ * 256) must fit, else GRX_ESIZE.  Every call on a GPU shares that array:
+ * calls that overlap on one GPU (other streams or threads) race.  Results
+ * are those of grx_matmul_q8_dev, bit for bit. */
+grx_status grx_matmul_q8_dev_noalloc(grx_ctx *ctx, float *dst, int ldc, const float *x, int lda, int m,
+                                     const grx_weight *w, const float *bias);
+
 /* quantU8 (internal/kern/q8int.go:86-105, vnni_amd64.s:194-256) on device
  * pointers: round m rows of k float32 values (k % 32 == 0, rows lda apart)
  * to signed int8 q[m][k] (the reference's unsigned byte minus 128) and one
