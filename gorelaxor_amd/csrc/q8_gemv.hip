@@ -1202,6 +1202,35 @@ extern "C" grx_status grx_matmul_q8_prequant_dev(grx_ctx *ctx, float *dst, int l
     return gemv_rows_preq(ctx->stream, dst, ldc, q, sc, m, w, bias);
 }
 
+// Few rows (below the matrix cores' threshold) whose rounded values fit the
+// products' LDS: each GEMV launch rounds its rows in its own prologue
+// (quantU8, q8int.go:88-105, the same arithmetic as grx_quant_act_dev), so
+// a row costs one launch and no scratch.
+static grx_status gemv_rows_quant(hipStream_t st, float *dst, int ldc, const float *x, int lda, int m,
+                                  const grx_weight *w, const float *bias) {
+    const int K = w->cols;
+    int i = 0;
+    while (i < m) {
+        const int left = m - i;
+        int mm = left >= 8 ? 8 : left >= 4 ? 4 : left >= 2 ? 2 : 1;
+        while (mm > 1 && (size_t)mm * K > kStageMax) mm >>= 1;
+        GemvArgs a = {};
+        a.qs = w->qs;
+        a.ds = w->ds;
+        a.rows = w->rows;
+        a.nb = w->nb;
+        a.x = x + (size_t)i * lda;
+        a.lda = lda;
+        a.y = dst + (size_t)i * ldc;
+        a.ldc = ldc;
+        a.bias = bias;
+        grx_status s = grx_gemv_launch(st, mm, GRX_PRO_QUANT, GRX_EPI_STORE, a, 0);
+        if (s != GRX_OK) return s;
+        i += mm;
+    }
+    return GRX_OK;
+}
+
 extern "C" grx_status grx_matmul_q8_dev(grx_ctx *ctx, float *dst, int ldc, const float *x, int lda, int m,
                                         const grx_weight *w, const float *bias) {
     grx_status s = check_mm("grx_matmul_q8_dev", ctx, dst, ldc, x, lda, m, w);
@@ -1209,6 +1238,8 @@ extern "C" grx_status grx_matmul_q8_dev(grx_ctx *ctx, float *dst, int ldc, const
     if (m == 0 || w->rows == 0) return GRX_OK;
     GRX_HIP(hipSetDevice(ctx->device));
     const int K = w->cols, nb = w->nb;
+    if (nb > 0 && m < grx_gemm_min_m() && (size_t)K <= kStageMax)
+        return gemv_rows_quant(ctx->stream, dst, ldc, x, lda, m, w, bias);
     void *buf;
     const size_t qbytes = ((size_t)m * K + 255) & ~(size_t)255;
     s = grx_ctx_scratch(ctx, qbytes + (size_t)m * nb * 4 + 16, &buf);
