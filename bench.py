@@ -105,6 +105,28 @@ def cpu_baseline(w8: np.ndarray, x: np.ndarray, seconds: float) -> dict:
 PROMPT = [50257, 50362, 50363, 50258]
 
 
+def whisper_step_bytes(hp: dict, streams: int, positions) -> dict:
+    """Algorithmic HBM bytes of one decoder step, averaged over the steps'
+    positions: the Q8_0 matrices the step multiplies (per layer: self-
+    attention q|k|v and out, cross query and out, fc1, fc2; the token
+    embedding as the logits matrix; the cross keys and values were
+    projected once per window), every stream's cross keys and values
+    (float32), and the self-attention cache rows up to the position."""
+    d, nl, nv, na = hp["n_state"], hp["n_layer"], hp["n_vocab"], hp["n_audio_ctx"]
+    ff = 4 * d
+    weights = (nl * (6 * d * d + 2 * ff * d) + nv * d) // 32 * 34
+    cross = streams * nl * 2 * na * d * 4
+    self_kv = streams * nl * 2 * d * 4 * float(np.mean([p + 1 for p in positions]))
+    return {"weights": weights, "cross_kv": cross, "self_kv_avg": int(self_kv),
+            "total": int(weights + cross + self_kv)}
+
+
+def roofline(bytes_per_step: float, s_per_step: float) -> dict:
+    gbs = bytes_per_step / s_per_step / 1e9
+    return {"bound": "hbm", "bytes_per_step": int(bytes_per_step), "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS,
+            "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4)}
+
+
 def decoder_bench(args) -> dict:
     """whisper base.en-shaped decoder with random-init Q8_0 weights: cross
     attention over a 1500 x 512 N(0,1) encoder output, a 4-token prompt, then
@@ -120,7 +142,10 @@ def decoder_bench(args) -> dict:
     enc = encoder_output(hp, seed=8)
     dec = WhisperDecoder(hp, t)
     t0 = time.perf_counter()
-    dec.set_encoder_output(enc)
+    dec.set_encoder_output(enc)  # the first call also sends the weights to the device
+    first_s = time.perf_counter() - t0
+    t0 = time.perf_counter()
+    dec.set_encoder_output(enc)  # a later window: the cross keys and values alone
     cross_s = time.perf_counter() - t0
     n = args.decoder_steps
     dec.greedy(PROMPT, n)  # warm: graph captured, caches warm
@@ -132,9 +157,11 @@ def decoder_bench(args) -> dict:
         times.append(time.perf_counter() - t0)
     best = min(times)
     steps = len(PROMPT) + n
+    sb = whisper_step_bytes(hp, 1, range(steps))
     res = {"tokens_per_s": round(steps / best, 1), "ms_per_token": round(best / steps * 1e3, 4),
            "steps_per_run": steps, "generated_tokens": n + 1, "runs": reps,
-           "cross_kv_setup_ms": round(cross_s * 1e3, 2),
+           "roofline": roofline(sb["total"], best / steps), "step_bytes": sb,
+           "cross_kv_ms_per_window": round(cross_s * 1e3, 2), "first_window_ms_with_weight_upload": round(first_s * 1e3, 2),
            "shape": "d_model 512, 8 heads, 6 layers, FFN 2048, vocab 51864, audio 1500, KV 4->%d" % (len(PROMPT) + n)}
     oracle.build()
     ref = oracle.WhisperOracle(hp, t)
@@ -167,6 +194,7 @@ def streams_bench(args) -> dict:
     t = whisper_model(hp, seed=23)
     encs = [encoder_output(hp, seed=60 + k) for k in range(S)]
     dec = WhisperDecoder(hp, t, streams=S)
+    dec.set_encoder_output_stream(0, encs[0])  # the first call also sends the weights to the device
     t0 = time.perf_counter()
     for k in range(S):
         dec.set_encoder_output_stream(k, encs[k])
@@ -180,13 +208,11 @@ def streams_bench(args) -> dict:
         times.append(time.perf_counter() - t0)
     best = min(times)
     steps = len(PROMPT) + n
-    d, ff, nv, nl, nctx = hp["n_state"], 4 * hp["n_state"], hp["n_vocab"], hp["n_layer"], hp["n_audio_ctx"]
-    wbytes = (nl * (8 * d * d + 2 * ff * d) + nv * d) // 32 * 34
-    cross = S * nl * 2 * nctx * d * 4
+    sb = whisper_step_bytes(hp, S, range(steps))
     res = {"tokens_per_s": round(S * steps / best, 1), "ms_per_step": round(best / steps * 1e3, 4),
-           "streams": S, "steps_per_run": steps, "runs": 3, "cross_kv_setup_ms": round(cross_s * 1e3, 1),
-           "step_bytes_weights_and_cross_kv": wbytes + cross,
-           "hbm_gbs_weights_and_cross_kv": round((wbytes + cross) / (best / steps) / 1e9, 1),
+           "streams": S, "steps_per_run": steps, "runs": 3,
+           "roofline": roofline(sb["total"], best / steps), "step_bytes": sb,
+           "cross_kv_ms_all_streams": round(cross_s * 1e3, 1),
            "shape": "d_model 1280, 20 heads, 4 layers, FFN 5120, vocab 51866, audio 1500, 8 streams, KV 4->%d"
                     % steps}
     dec.close()
@@ -234,8 +260,20 @@ def lm_bench(args) -> dict:
         times.append((t1 - t0, time.perf_counter() - t1))
     prefix_s = min(a for a, _ in times)
     frames_s = min(b for _, b in times)
+    # per frame: the Q8_0 matrices (per layer q|k|v, out, ff1, ff2), the
+    # float32 input projection, out_norm and eos vectors, and the cache rows
+    # up to the frame's position (the 64-row prefix first)
+    d, ff, nl, ld = hp["d"], hp["ff"], hp["n_layer"], hp["ldim"]
+    wq8 = nl * (4 * d * d + 2 * ff * d) // 32 * 34
+    small = (ld * d + 5 * d) * 4
+    kv = nl * 2 * d * 4 * float(np.mean([64 + f + 1 for f in range(n)]))
+    frame_bytes = wq8 + small + kv
     res = {"frames_per_s": round(n / frames_s, 1), "ms_per_frame": round(frames_s / n * 1e3, 4),
-           "prefix_ms": round(prefix_s * 1e3, 3), "frames": n, "prefix_rows": 64, "runs": reps,
+           "roofline": roofline(frame_bytes, frames_s / n),
+           "frame_bytes": {"weights": wq8, "vectors": small, "kv_avg": int(kv), "total": int(frame_bytes)},
+           "prefix_ms": round(prefix_s * 1e3, 3), "prefix_int8_tops": round(
+               2 * 64 * nl * (4 * d * d + 2 * ff * d) / prefix_s / 1e12, 2),
+           "frames": n, "prefix_rows": 64, "runs": reps,
            "shape": "d_model 1024, 16 heads, 6 layers, FFN 4096, KV 64->%d" % (64 + n)}
     oracle.build()
     ref = oracle.PocketOracle(hp, t)

@@ -69,7 +69,10 @@ __global__ __launch_bounds__(64) void ln_wave_kernel(const float *__restrict__ x
     if constexpr (FORM == GRX_LN_KERN)
         wave_ln32<NP, CHECK>(xv, wv, bv, npc, lane);
     else
-        wave_ln64<NP, CHECK>(xv, wv, bv, w != nullptr, npc, lane, eps);
+        wave_ln64<NP, CHECK>(xv, wv, bv, w != nullptr, npc, lane, eps, [&](float4 (&v)[NP]) {
+#pragma unroll
+            for (int j = 0; j < NP; ++j) v[j] = x4[min(j * 64 + lane, npc - 1)];
+        });
 #pragma unroll
     for (int j = 0; j < NP; ++j)
         if (j * 64 + lane < npc) y4[j * 64 + lane] = xv[j];

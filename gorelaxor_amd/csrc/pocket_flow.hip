@@ -54,11 +54,14 @@ __global__ void flow_lnmod_kernel(const float *__restrict__ h, int dim, const fl
                                   const float *__restrict__ b, const float *__restrict__ shift,
                                   const float *__restrict__ scale, double eps, float *__restrict__ n) {
     __shared__ double red[48];  // ln_block_reduce
+    __shared__ float hl[8192];  // the row (dim <= 8192, checked at set-up)
     const int t = threadIdx.x;
+    for (int j = t; j < dim; j += kFT) hl[j] = h[j];
+    __syncthreads();
     double mean, inv;
-    ln64_stats(h, dim, eps, red, mean, inv);
+    ln64_stats(hl, dim, eps, red, mean, inv);
     for (int j = t; j < dim; j += kFT) {
-        float o = (float)__dmul_rn(__dsub_rn((double)h[j], mean), inv);
+        float o = (float)__dmul_rn(__dsub_rn((double)hl[j], mean), inv);
         if (w) o = __fadd_rn(__fmul_rn(o, w[j]), b[j]);
         n[j] = __fadd_rn(__fmul_rn(o, __fadd_rn(1.f, scale[j])), shift[j]);
     }

@@ -296,12 +296,15 @@ __global__ __launch_bounds__(kThreads) void finish_kernel(const float *__restric
     __shared__ double red[48];  // ln_block_reduce
     __shared__ float ov[8192], ewl[8192], part4[4];
     const int tid = threadIdx.x;
+    // the row in LDS (ewl, until the eos weights replace it below)
+    for (int i = tid; i < d; i += blockDim.x) ewl[i] = x[i];
+    __syncthreads();
     double mean, inv;
-    ln64_stats(x, d, 1e-5, red, mean, inv);
+    ln64_stats(ewl, d, 1e-5, red, mean, inv);
     const int f = frame != nullptr ? *frame : 0;
     float *out = out_hist + (size_t)f * d;
     for (int i = tid; i < d; i += blockDim.x) {
-        float o = (float)(((double)x[i] - mean) * inv);
+        float o = (float)(((double)ewl[i] - mean) * inv);
         o = __fadd_rn(__fmul_rn(o, nw[i]), nb[i]);
         out[i] = o;
         ov[i] = o;

@@ -208,7 +208,10 @@ __device__ __forceinline__ void wave_row_prologue(const GemvArgs &a, int m, int8
     } else if constexpr (PRO == GRX_PRO_LN64) {
         // layerNorm of pockettts/nn.go:27-49: statistics and the
         // normalized value in float64, gain and bias in float32
-        wave_ln64<NP>(xv, wv, bv, a.ln_w != nullptr, npc, lane, a.ln_eps);
+        wave_ln64<NP>(xv, wv, bv, a.ln_w != nullptr, npc, lane, a.ln_eps, [&](float4 (&v)[NP]) {
+#pragma unroll
+            for (int j = 0; j < NP; ++j) v[j] = x4[min(j * 64 + lane, npc - 1)];
+        });
     }
     // quantU8 (q8int.go:88-105): a block is 8 pieces in 8 lanes
 #pragma unroll
@@ -719,8 +722,10 @@ __global__ __launch_bounds__(64 * W) void gemv1_kernel(const GemvArgs a) {
     auto act_scale = [&](int b) -> float { return LQ ? lxs[b] : a.xs[b]; };
 
     // ---- loads that wait for nothing: the first npf blocks (1, 2 or
-    // kPrefetch; up to kPrefetch - 1 repeats of the last)
-    constexpr int PF = LQ ? kPrefetch : 0;
+    // PF; up to PF - 1 repeats of the last).  With 16 waves a wave owns at
+    // most 2 blocks of rows up to 1024 values; two more would only cost
+    // registers (a lane has 128 at 16 waves).
+    constexpr int PF = LQ ? (W >= 16 ? 2 : kPrefetch) : 0;
     int4 pw[2 * (PF > 0 ? PF : 1)];
     uint32_t pd[PF > 0 ? PF : 1];
     const int npf = PF > 0 ? min(PF, b1 - b0) : 0;
@@ -1028,7 +1033,7 @@ hipError_t launch1_one(hipStream_t st, const GemvArgs &a, int tiles) {
 }
 
 // One-row launches: pre-rounded rows on 1..16 waves; rows rounded in the
-// prologue on 1, 4 or 16 waves with 2, 4 or 5 pieces per lane.
+// prologue on 1, 4, 8 or 16 waves with 2, 4 or 5 pieces per lane.
 template <int PRO, int EPI>
 hipError_t launch1(hipStream_t st, const GemvArgs &a, int tiles, int W) {
     while (W > 1 && W > a.nb) W >>= 1;  // every wave owns a block
@@ -1043,7 +1048,7 @@ hipError_t launch1(hipStream_t st, const GemvArgs &a, int tiles, int W) {
     } else {
         const int pieces = a.nb * GRX_QK / 4;  // float4 pieces of the row
         const int np = pieces <= 128 ? 2 : pieces <= 256 ? 4 : 5;
-        const int w = W >= 16 ? 16 : W >= 4 ? 4 : 1;
+        const int w = W >= 16 ? 16 : W >= 8 ? 8 : W >= 4 ? 4 : 1;
         auto go = [&](auto np_tag) -> hipError_t {
             constexpr int NP = decltype(np_tag)::value;
             if constexpr (EPI == GRX_EPI_XSCORES) {
@@ -1051,6 +1056,7 @@ hipError_t launch1(hipStream_t st, const GemvArgs &a, int tiles, int W) {
             } else {
                 if (w == 1) return launch1_one<1, NP, PRO, EPI>(st, a, tiles);
                 if (w == 4) return launch1_one<4, NP, PRO, EPI>(st, a, tiles);
+                if (w == 8) return launch1_one<8, NP, PRO, EPI>(st, a, tiles);
                 return launch1_one<16, NP, PRO, EPI>(st, a, tiles);
             }
         };
@@ -1086,6 +1092,10 @@ int grx_gemv_pick_waves(int tiles, int nb, int m, int pro) {
     while (W < 16 && tiles * W < 2048 && 2 * W <= nb && gemv_smem(m, 2 * W, pro, nb) <= lim) W *= 2;
     // several rows fold in rounds, one wave per row: at least m waves
     if (m > 1 && W > 1 && W < m && gemv_smem(m, m, pro, nb) <= lim) W = m;
+    // the float64 LayerNorm prologue (its bound check included) needs more
+    // than the 128 registers a lane has at 16 waves; 8 waves measured the
+    // same as 16 for these products
+    if (pro == GRX_PRO_LN64 && W > 8) W = 8;
     return W;
 }
 

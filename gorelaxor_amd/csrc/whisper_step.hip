@@ -568,6 +568,7 @@ struct grx_whisper {
     unsigned long long *keys = nullptr;  // argmax keys, [vocabulary tiles][streams]
     unsigned int *counter = nullptr;
     int *tok = nullptr, *pos = nullptr, *hist = nullptr;
+    float *xenc = nullptr, *xk_tmp = nullptr, *xv_tmp = nullptr;  // cross K/V precompute staging
     hipGraph_t graph = nullptr;
     hipGraphExec_t exec = nullptr;
     int pos_host = 0;
@@ -1051,10 +1052,12 @@ extern "C" grx_status grx_whisper_set_encoder_output_stream(grx_whisper *m, int 
     if (s != GRX_OK) return s;
     const int st = m->hp.n_state, nctx = n_audio_ctx, hd = st / m->hp.n_head;
     const size_t n = (size_t)nctx * st;
-    float *denc = nullptr, *dk = nullptr, *dv = nullptr;
-    GRX_HIP(hipMalloc(&denc, n * 4));
-    GRX_HIP(hipMalloc(&dk, n * 4));
-    GRX_HIP(hipMalloc(&dv, n * 4));
+    if (m->xenc == nullptr) {  // staging for every later window too
+        if ((s = dev_alloc_t(m, n, &m->xenc)) != GRX_OK) return s;
+        if ((s = dev_alloc_t(m, n, &m->xk_tmp)) != GRX_OK) return s;
+        if ((s = dev_alloc_t(m, n, &m->xv_tmp)) != GRX_OK) return s;
+    }
+    float *denc = m->xenc, *dk = m->xk_tmp, *dv = m->xv_tmp;
     hipStream_t stream = m->ctx->stream;
     GRX_HIP(hipMemcpyAsync(denc, enc, n * 4, hipMemcpyHostToDevice, stream));
     const float tsc = (float)(1.0 / sqrt((double)hd));
@@ -1071,9 +1074,6 @@ extern "C" grx_status grx_whisper_set_encoder_output_stream(grx_whisper *m, int 
         }
     }
     hipError_t e = hipStreamSynchronize(stream);
-    (void)hipFree(denc);
-    (void)hipFree(dk);
-    (void)hipFree(dv);
     if (s != GRX_OK) return s;
     if (e != hipSuccess) return grx_hip_fail(e, "grx_whisper_set_encoder_output");
     m->have_xs[stream_ix] = true;

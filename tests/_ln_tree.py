@@ -7,9 +7,9 @@ tree and falls back to the in-order sums when a float32 result could
 differ.  This module restates the two trees the kernels use, in the same
 order of additions (numpy float64 and float32 arithmetic round like the
 device's), so that a test can show that a row needs the fallback:
-  - "block": ln_block_sum2 with 256 threads: thread t sums terms t, t+256,
-    ... in order; each wave's 64 partials by a butterfly (xor 32 .. 1);
-    the four waves' sums in order;
+  - "block": ln_block_reduce with 256 threads: thread t sums terms t, t+256,
+    ... in order; each wave's 64 partials as wave_sum_f64 below; the four
+    waves' sums in order;
   - "wave": wave_ln32/wave_ln64 with the row as float4 pieces per lane
     (piece P = 64 j + lane, j < 5): lane sums its pieces' values in order;
     DPP xor 1, xor 2, mirror of 8, mirror of 16; then (r0 + r16) + (r32 +
@@ -28,6 +28,17 @@ def serial(t: np.ndarray) -> np.ndarray:
     return np.add.accumulate(t, axis=1)[:, -1] if t.shape[1] else np.zeros(t.shape[0])
 
 
+HALF_MIRROR = (IDX & ~7) | (7 - (IDX & 7))
+MIRROR = (IDX & ~15) | (15 - (IDX & 15))
+
+
+def _dpp_wave(v: np.ndarray) -> np.ndarray:
+    """wave_sum_f64 over the last axis (64 lanes)."""
+    for perm in (IDX ^ 1, IDX ^ 2, HALF_MIRROR, MIRROR):
+        v = v + v[..., perm]
+    return (v[..., 0] + v[..., 16]) + (v[..., 32] + v[..., 48])
+
+
 def tree_block(t: np.ndarray, threads: int = 256) -> np.ndarray:
     rows, n = t.shape
     k = -(-n // threads)
@@ -36,17 +47,11 @@ def tree_block(t: np.ndarray, threads: int = 256) -> np.ndarray:
     p = np.zeros((rows, threads))
     for j in range(k):
         p = p + pad[:, j * threads:(j + 1) * threads]
-    w = p.reshape(rows, threads // 64, 64)
-    for o in (32, 16, 8, 4, 2, 1):
-        w = w + w[:, :, IDX ^ o]
+    w = _dpp_wave(p.reshape(rows, threads // 64, 64))
     s = np.zeros(rows)
     for i in range(threads // 64):
-        s = s + w[:, i, 0]
+        s = s + w[:, i]
     return s
-
-
-HALF_MIRROR = (IDX & ~7) | (7 - (IDX & 7))
-MIRROR = (IDX & ~15) | (15 - (IDX & 15))
 
 
 def tree_wave(t: np.ndarray, pieces: int = 5) -> np.ndarray:
@@ -59,10 +64,7 @@ def tree_wave(t: np.ndarray, pieces: int = 5) -> np.ndarray:
         Pc = np.minimum(P, npc - 1)
         for c in range(4):
             lanes = lanes + np.where(ok, t[:, 4 * Pc + c], 0.0)
-    v = lanes
-    for perm in (IDX ^ 1, IDX ^ 2, HALF_MIRROR, MIRROR):
-        v = v + v[:, perm]
-    return (v[:, 0] + v[:, 16]) + (v[:, 32] + v[:, 48])
+    return _dpp_wave(lanes)
 
 
 def tree(t: np.ndarray, impl: str) -> np.ndarray:
@@ -91,10 +93,12 @@ def ulp_exp(x: np.ndarray) -> np.ndarray:
     return np.where(b == 0, 127, e)
 
 
-def sum_exact(a, emin):
+def sum_exact(a, mn):
+    """ln_sum_exact: every partial sum of float32 values a float64, given
+    a = n max|v| and mn = the smallest nonzero |v| (inf if none)."""
     with np.errstate(over="ignore"):
-        lim = np.ldexp(1.0, np.minimum(53 + emin, 1023))
-    return np.where(emin < 127, a * (1.0 + 2.0 ** -30) < lim, True)
+        lim = np.ldexp(1.0, np.minimum(53 + ulp_exp(mn), 1023))
+    return ~(mn < np.inf) | (a < lim)
 
 
 def _mean32(s, n):
@@ -115,9 +119,18 @@ def mean32_sure(s, a, n, dep):
     return _same(_mean32(s - e, n), _mean32(s + e, n))
 
 
-def inv32_sure(vs, n, dep):
-    e = slack(n, dep, vs)
-    return _same(_inv32(vs - e, n), _inv32(vs + e, n))
+def inv_width(r):
+    """ln_inv_width: the relative half-width around 1/sqrt(x/n + eps)."""
+    r = np.asarray(r, np.float64)
+    with np.errstate(invalid="ignore"):
+        w = (0.5 * r) * (1.0 + 5.0 * r) + 10.5 * U
+    return np.where(r <= 0.5, w, np.inf)
+
+
+def inv32_sure(inv_d, n, dep):
+    w = inv_width(slack(n, dep, 1.0))
+    with np.errstate(invalid="ignore"):
+        return _same((inv_d * (1.0 - w)).astype(np.float32), (inv_d * (1.0 + w)).astype(np.float32))
 
 
 def _inv64(q, n, eps):
@@ -125,16 +138,17 @@ def _inv64(q, n, eps):
         return 1.0 / np.sqrt(q / float(n) + eps)
 
 
-def ln64_bound(mean, a, q, n, dep, exact, eps):
+def ln64_bound(mean, inv, a, q, n, dep, exact, eps):
     am, dn = np.abs(mean), float(n)
     es = np.where(exact, 0.0, slack(n, dep, a))
     em = np.where(exact, 0.0, (es / dn) * 1.001 + (3.0 * U) * am)
     shift = (2.0 * em) * (es + (dn * U * 1.001) * am) + dn * (em * em)
-    eq = (slack(n, dep, q) + shift) * 1.01
-    ilo = _inv64(q + eq, n, eps)
-    ihi = _inv64(np.maximum(q - eq, 0.0), n, eps)
+    with np.errstate(invalid="ignore", divide="ignore"):
+        r = np.where(exact, slack(n, dep, 1.0), slack(n, dep, 1.0) + shift / (q + dn * eps))
+    w = inv_width(r * 1.01)
+    ihi = inv * (1.0 + w)
     c1 = (em * ihi) * 1.0102
-    c2 = ((ihi - ilo) + (8.1 * U) * ihi) * 1.01
+    c2 = (w * inv + (8.1 * U) * ihi) * 1.01
     return c1, c2
 
 
@@ -144,10 +158,13 @@ def out64_sure(d, x, c1, c2):
 
 
 def values(x: np.ndarray, impl: str):
-    """The values' tree sum, their magnitudes' tree sum and whether the sum
-    is exact in every order (ln_block_values / ln_wave_values)."""
+    """The values' tree sum, n max|v| (>= their magnitudes' sum) and whether
+    the sum is exact in every order (ln_block_values / ln_wave_values)."""
     xd = x.astype(np.float64)
-    return tree(xd, impl), tree(np.abs(xd), impl), sum_exact(tree(np.abs(xd), impl), ulp_exp(x).min(axis=1))
+    ax = np.abs(x.astype(np.float32))
+    a = float(x.shape[1]) * ax.max(axis=1).astype(np.float64)
+    mn = np.where(ax > 0, ax, np.float32(np.inf)).min(axis=1)
+    return tree(xd, impl), a, sum_exact(a, mn)
 
 
 # ---- the two LayerNorms as the GPU forms them
@@ -169,7 +186,7 @@ def ln32(x, w, b, impl: str, check: bool = True):
     d = (x - mean[:, None]).astype(np.float64)
     vs = tree(d * d, impl)
     if check:
-        bad = ~inv32_sure(vs, n, dep)
+        bad = ~inv32_sure(1.0 / np.sqrt(vs / float(n) + 1e-5), n, dep)
         vs = np.where(bad, serial(d * d), vs)
         fell |= bad
     inv = _inv32(vs, n)
@@ -191,7 +208,7 @@ def ln64(x, w, b, eps: float, impl: str, check: bool = True):
     inv = _inv64(q, n, eps)
     fell = np.zeros(rows, bool)
     if check:
-        c1, c2 = ln64_bound(mean, a, q, n, dep, exact, eps)
+        c1, c2 = ln64_bound(mean, inv, a, q, n, dep, exact, eps)
         bad = ~np.all(out64_sure(d, d * inv[:, None], c1, c2), axis=1)
         ms = np.where(exact, mean, serial(xd) / float(n))
         ds = xd - ms[:, None]
