@@ -81,25 +81,89 @@ def ring_weights(seed: int = 1) -> tuple[np.ndarray, np.ndarray]:
     return w, x
 
 
+def cpu_info() -> dict:
+    """The host CPU: model name, logical CPUs, physical cores, the VNNI form
+    the baseline takes."""
+    model, phys = platform.processor() or platform.machine(), set()
+    try:
+        cur = {}
+        for line in open("/proc/cpuinfo"):
+            if ":" in line:
+                k, v = [t.strip() for t in line.split(":", 1)]
+                cur[k] = v
+                if k == "model name":
+                    model = v
+            elif cur:
+                phys.add((cur.get("physical id"), cur.get("core id")))
+                cur = {}
+        if cur:
+            phys.add((cur.get("physical id"), cur.get("core id")))
+    except OSError:
+        pass
+    import oracle
+
+    kind = {2: "AVX512-VNNI (EVEX)", 1: "AVX-VNNI (VEX)", 0: "none"}[oracle.vnni_kind()]
+    return {"cpu": model, "logical_cpus": os.cpu_count(), "physical_cores": len(phys) or None, "vnni": kind}
+
+
+def cpu_threads() -> int:
+    """The host threads a baseline may use: the box's CPU share when it says
+    (OMP_NUM_THREADS), else every logical CPU."""
+    try:
+        return max(1, int(os.environ.get("OMP_NUM_THREADS", "")))
+    except ValueError:
+        return os.cpu_count() or 1
+
+
 def cpu_baseline(w8: np.ndarray, x: np.ndarray, seconds: float) -> dict:
-    """The oracle's int8 route (scalar C, one thread) over the first matrices
-    of the same ring until `seconds` of work; GB/s of the same algorithmic
-    bytes."""
+    """The reference's CPU path for the same products: matmulQ8Int with the
+    VNNI tile kernel and its task split (internal/kern/q8int.go:148-223,
+    vnni_amd64.s), restated with intrinsics in oracle/grx_vnni.cc and
+    checked bit-equal to the oracle; one kern.MatMul per matrix of the same
+    512-matrix ring, at all of the box's threads (`value`) and at one, plus
+    one matrix over and over (cache-resident, as the reference's own kernel
+    benchmark runs it).  GB/s of the same algorithmic bytes."""
     import oracle
 
     oracle.build()
-    per = N * K // 32 * 34
-    done, t0 = 0, time.perf_counter()
-    while True:
-        i = done % RING
-        oracle.matmul_q8_int(x, w8[i * per:(i + 1) * per], N, K)
-        done += 1
+    info = cpu_info()
+    if oracle.vnni_kind() == 0:
+        return {"value": None, "unit": "GB/s", "cores": 0, "kind": "port", **info,
+                "sample": "this CPU has neither AVX512-VNNI nor AVX-VNNI: the reference's int8 kernel cannot run"}
+    panels, per = oracle.vnni_pack_many(w8, RING, N, K)
+    y = np.zeros(RING * N, np.float32)
+    want = oracle.matmul_q8_int(x, w8[:N * K // 32 * 34], N, K)[0]
+    oracle.vnni_ring(y, x, panels, per, 1, N, K, 1, 1)
+    same = bool(np.array_equal(y[:N].view(np.uint32), want.view(np.uint32)))
+    budget = seconds / 4
+
+    def rate(count: int, threads: int) -> tuple[float, int]:
+        # one pass to size the sample, then whole passes filling the budget
+        t0 = time.perf_counter()
+        oracle.vnni_ring(y, x, panels, per, count, N, K, threads, 1)
+        one = time.perf_counter() - t0
+        reps = max(1, int(budget / max(one, 1e-6)))
+        t0 = time.perf_counter()
+        oracle.vnni_ring(y, x, panels, per, count, N, K, threads, reps)
         el = time.perf_counter() - t0
-        if el >= seconds:
-            break
-    return {"value": round(done * BYTES_PER_GEMV / el / 1e9, 3), "unit": "GB/s", "cores": 1, "kind": "port",
-            "sample": f"{done} GEMVs of 1024x1024 (the first {min(done, RING)} ring matrices), "
-                      f"{el:.1f} s, oracle/grx_oracle.c orc_matmul_q8_int, 1 thread, {platform.processor() or platform.machine()}"}
+        return reps * count * BYTES_PER_GEMV / el / 1e9, reps * count
+
+    th = cpu_threads()
+    ring_all, n_all = rate(RING, th)
+    ring_one, n_one = rate(RING, 1)
+    single_all, _ = rate(1, th)
+    single_one, _ = rate(1, 1)
+    # `value` is the faster of the two thread counts: for one row of 1024 x
+    # 1024 the task split's per-call hand-off can cost more than it saves
+    best_th, best = (th, ring_all) if ring_all >= ring_one else (1, ring_one)
+    return {"value": round(best, 3), "unit": "GB/s", "cores": best_th, "kind": "port", **info,
+            "parity_bit_exact": same,
+            "ring": {"threads": th, "value": round(ring_all, 3), "one_thread": round(ring_one, 3), "unit": "GB/s"},
+            "cache_resident_single_matrix": {"threads": th, "value": round(single_all, 3),
+                                             "one_thread": round(single_one, 3), "unit": "GB/s"},
+            "sample": f"{n_all} GEMVs of 1024x1024 over the 512-matrix ring at {th} threads and {n_one} at one, "
+                      f"about {budget:.1f} s each, oracle/grx_vnni.cc (matmulQ8Int, quantU8avx, q8tile with "
+                      f"vpdpbusd, the reference's task split); value: the faster, {best_th} thread(s)"}
 
 
 PROMPT = [50257, 50362, 50363, 50258]
@@ -171,6 +235,7 @@ def decoder_bench(args) -> dict:
     cpu_s = time.perf_counter() - t0
     res["parity_tokens_identical"] = bool(np.array_equal(want, toks))
     res["cpu_baseline"] = {"value": round(steps / cpu_s, 2), "unit": "tokens/s", "cores": 1, "kind": "port",
+                           **cpu_info(),
                            "sample": f"the same {steps} decoder steps on the oracle (scalar C, 1 thread), {cpu_s:.2f} s"}
     dec.close()
     return res
@@ -228,6 +293,7 @@ def streams_bench(args) -> dict:
     cpu_s = time.perf_counter() - t0
     res["parity_tokens_identical"] = bool(np.array_equal(want, toks[0])) and same
     res["cpu_baseline"] = {"value": round(steps / cpu_s, 2), "unit": "tokens/s", "cores": 1, "kind": "port",
+                           **cpu_info(),
                            "sample": f"stream 0's {steps} decoder steps on the oracle (scalar C, 1 thread), "
                                      f"{cpu_s:.1f} s; the reference decodes streams one after another"}
     return res
@@ -287,6 +353,7 @@ def lm_bench(args) -> dict:
     cpu_s = time.perf_counter() - t1
     res["parity_bit_exact"] = ok
     res["cpu_baseline"] = {"value": round(n / cpu_s, 2), "unit": "frames/s", "cores": 1, "kind": "port",
+                           **cpu_info(),
                            "sample": f"the same {n} frames on the oracle (scalar C, 1 thread), {cpu_s:.2f} s; "
                                      f"prefix {1e3 * (t1 - t0):.0f} ms"}
     lm.close()
@@ -339,7 +406,8 @@ def speak_bench(args, hp, t, x) -> dict:
             bool(np.float32(e) == eos[k])
     res["parity_bit_exact"] = ok
     res["cpu_baseline"] = {"value": round(n / (time.perf_counter() - t0), 2), "unit": "frames/s", "cores": 1,
-                           "kind": "port", "sample": f"the same {n} frames (transformer step and flow head) on the "
+                           "kind": "port", **cpu_info(),
+                           "sample": f"the same {n} frames (transformer step and flow head) on the "
                                                      "oracle (C kernels, 1 thread, Python glue)"}
     return res
 
@@ -438,6 +506,7 @@ def conformer_bench(args) -> dict:
     res["parity_bit_exact"] = bool(np.array_equal(out1.view(np.uint32), want.view(np.uint32)))
     res["batch16"]["parity_each_equals_its_batch1_encode"] = same16
     res["cpu_baseline"] = {"value": round(1.0 / cpu_s, 4), "unit": "utterances/s", "cores": 1, "kind": "port",
+                           **cpu_info(),
                            "sample": f"one 10 s utterance, all 24 layers, on the oracle (scalar C, 1 thread), "
                                      f"{cpu_s:.1f} s"}
     res["tdt_decode"] = tdt_bench(args, want[:L])
@@ -480,6 +549,7 @@ def tdt_bench(args, enc: np.ndarray) -> dict:
     return {"frames": T, "tokens": len(got), "ms_per_decode": round(best * 1e3, 3),
             "decodes_per_s": round(1.0 / best, 1), "parity_bit_exact": bool(same),
             "cpu_baseline": {"value": round(1.0 / cpu_s, 2), "unit": "decodes/s", "cores": 1, "kind": "port",
+                             **cpu_info(),
                              "sample": f"the same decode on the oracle (scalar C, 1 thread), {cpu_s * 1e3:.1f} ms"}}
 
 
@@ -548,6 +618,27 @@ def main():
     value = launch_bytes / (ms_step * 1e-3) / 1e9
     achieved = launch_bytes / (gemv_avg * 1e-3) / 1e9
 
+    # one 1024 x 1024 matrix on its own (the reference's kernel-benchmark
+    # shape): launches back to back, and each launch waited for
+    w1 = kern.NewQ8(N, K, w8[:N * K // 32 * 34], ctx)
+    dy1 = hiprt.DeviceBuffer(N * 4)
+    for _ in range(20):
+        kern.matmul_dev(dy1, dx, 1, w1, ctx=ctx)
+    ctx.sync()
+    a1, b1 = hiprt.Event(), hiprt.Event()
+    a1.record(stream)
+    for _ in range(200):
+        kern.matmul_dev(dy1, dx, 1, w1, ctx=ctx)
+    b1.record(stream)
+    ctx.sync()
+    single_us = a1.elapsed_ms(b1) / 200 * 1e3
+    t0 = time.perf_counter()
+    for _ in range(200):
+        kern.matmul_dev(dy1, dx, 1, w1, ctx=ctx)
+        ctx.sync()
+    single_sync_us = (time.perf_counter() - t0) / 200 * 1e6
+    del w1, dy1
+
     # parity spot check of this very run against the oracle (first matrix)
     import oracle
     oracle.build()
@@ -571,7 +662,10 @@ def main():
         "config": {"workload": "q8_0 GEMV 1024x1024 over a ring of 512 distinct matrices (570 MB) per step, "
                                "x rounded to Q8_0 on the fly", "n": N, "k": K, "ring": RING,
                    "bytes_per_step": launch_bytes, "hbm_fraction": round(value / HBM_PEAK_GBS, 4),
-                   "parity_bit_exact": parity, "wall_s": round(wall, 3)},
+                   "parity_bit_exact": parity, "wall_s": round(wall, 3),
+                   "single_matrix": {"us_per_gemv_back_to_back": round(single_us, 2),
+                                     "us_per_gemv_synchronized": round(single_sync_us, 2),
+                                     "gbs_back_to_back": round(BYTES_PER_GEMV / (single_us * 1e-6) / 1e9, 1)}},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),
                      "kernel": "gemv1_kernel<1,4,QUANT,STORE>", "kernel_avg_us": round(gemv_avg * 1e3, 3)},

@@ -17,14 +17,16 @@ import numpy as np
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "_build", "liboracle.so")
+VNNI_PATH = os.path.join(HERE, "_build", "libgrx_vnni.so")
 
 QK = 32
 Q8_BYTES = 34
 
 
 def build(force: bool = False) -> str:
-    """Compile the oracle with its Makefile (gcc, no GPU needed)."""
-    if force or not os.path.exists(LIB_PATH):
+    """Compile the oracle (and the VNNI baseline) with its Makefile (gcc,
+    no GPU needed)."""
+    if force or not os.path.exists(LIB_PATH) or not os.path.exists(VNNI_PATH):
         subprocess.run(["make", "-s", "-C", HERE, "-B" if force else "all"], check=True)
     return LIB_PATH
 
@@ -878,3 +880,91 @@ class RnntOracle:
                                   frame_offset, C.cast(out, C.c_void_p), cap)
         toks = [(out[i].id, out[i].frame, out[i].duration, float(np.float32(out[i].p))) for i in range(n)]
         return toks, (h, c, lv.value)
+
+
+# ---- the reference's int8 CPU path with VNNI (grx_vnni.cc): the
+# benchmark's CPU baseline, and its parity with orc_matmul_q8_int
+
+_vnni = None
+
+
+def vnni_lib() -> C.CDLL:
+    global _vnni
+    if _vnni is None:
+        if not os.path.exists(VNNI_PATH):
+            build()
+        L = C.CDLL(VNNI_PATH)
+        L.vnni_kind.restype = C.c_int
+        L.vnni_panel_bytes.argtypes = [C.c_int, C.c_int]
+        L.vnni_panel_bytes.restype = C.c_size_t
+        L.vnni_pack.argtypes = [_u8p, C.c_int, C.c_int, C.c_void_p]
+        L.vnni_matmul.argtypes = [C.c_void_p, C.c_int, C.c_void_p, C.c_int, C.c_int, C.c_void_p, C.c_int, C.c_int,
+                                  C.c_void_p, C.c_int, C.c_void_p, C.c_void_p]
+        L.vnni_matmul.restype = C.c_int
+        L.vnni_ring.argtypes = [C.c_void_p, C.c_void_p, C.c_void_p, C.c_size_t, C.c_int, C.c_int, C.c_int, C.c_int,
+                                C.c_int, C.c_void_p, C.c_void_p]
+        L.vnni_ring.restype = C.c_int
+        _vnni = L
+    return _vnni
+
+
+def vnni_kind() -> int:
+    """2: AVX512-VNNI (the EVEX kernel), 1: AVX-VNNI (VEX), 0: neither."""
+    return vnni_lib().vnni_kind()
+
+
+class VnniWeight:
+    """A Q8_0 matrix packed as the reference's panels (packQ8Panels,
+    internal/kern/q8int.go:35-64), for vnni_matmul."""
+
+    def __init__(self, q8: np.ndarray, n: int, k: int):
+        self.n, self.k = n, k
+        self.panels = np.zeros(vnni_lib().vnni_panel_bytes(n, k), np.uint8)
+        vnni_lib().vnni_pack(np.ascontiguousarray(q8, np.uint8), n, k, self.panels.ctypes.data)
+
+
+class VnniScratch:
+    """matmulQ8Int's rounded activations for up to m rows of k values."""
+
+    def __init__(self, m: int, k: int):
+        mp = (m + 5) // 6 * 6
+        self.q = np.zeros(mp * k, np.uint8)
+        self.sc = np.zeros(mp * (k // 32), np.float32)
+
+
+def vnni_matmul(x: np.ndarray, w: VnniWeight, bias=None, threads: int = 1, out=None, scratch=None) -> np.ndarray:
+    """matmulQ8Int (internal/kern/q8int.go:148-223) with the VNNI tile
+    kernel: x [m][k] float32 -> [m][n]."""
+    x = np.ascontiguousarray(x, np.float32)
+    m = x.shape[0]
+    y = out if out is not None else np.zeros((m, w.n), np.float32)
+    s = scratch if scratch is not None else VnniScratch(m, w.k)
+    b = None if bias is None else np.ascontiguousarray(bias, np.float32)
+    rc = vnni_lib().vnni_matmul(y.ctypes.data, w.n, x.ctypes.data, w.k, m, w.panels.ctypes.data, w.n, w.k,
+                                None if b is None else b.ctypes.data, threads, s.q.ctypes.data, s.sc.ctypes.data)
+    if rc != 0:
+        raise RuntimeError("vnni_matmul: this processor has neither AVX512-VNNI nor AVX-VNNI")
+    return y
+
+
+def vnni_pack_many(q8: np.ndarray, count: int, n: int, k: int) -> tuple[np.ndarray, int]:
+    """count Q8_0 matrices of n x k, back to back in q8, packed as panels:
+    (the panels, bytes per matrix)."""
+    per = vnni_lib().vnni_panel_bytes(n, k)
+    q8 = np.ascontiguousarray(q8, np.uint8)
+    src = n * (k // 32) * 34
+    out = np.empty(per * count, np.uint8)
+    for i in range(count):
+        vnni_lib().vnni_pack(q8[i * src:(i + 1) * src], n, k, out[i * per:(i + 1) * per].ctypes.data)
+    return out, per
+
+
+def vnni_ring(y: np.ndarray, x: np.ndarray, panels: np.ndarray, per: int, count: int, n: int, k: int, threads: int,
+              reps: int) -> None:
+    """reps passes of one-row products over count packed matrices (C loop)."""
+    s = VnniScratch(1, k)
+    x = np.ascontiguousarray(x, np.float32)
+    rc = vnni_lib().vnni_ring(y.ctypes.data, x.ctypes.data, panels.ctypes.data, per, count, n, k, threads, reps,
+                              s.q.ctypes.data, s.sc.ctypes.data)
+    if rc != 0:
+        raise RuntimeError("vnni_ring: this processor has neither AVX512-VNNI nor AVX-VNNI")
