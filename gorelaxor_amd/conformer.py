@@ -15,11 +15,67 @@ from . import _lib
 from .kern import Context, default_context
 
 
-def frames_out(frames: int) -> int:
-    """Encoder frames for `frames` mel frames (three stride-2 halvings)."""
+def frames_out(frames: int, causal: bool = False) -> int:
+    """Encoder frames for `frames` mel frames (three stride-2 halvings,
+    subOut of conformer/encoder.go:33-38: a causal pre-encoder pads two
+    before and one after)."""
     for _ in range(3):
-        frames = (frames - 1) // 2 + 1
+        frames = frames // 2 + 1 if causal else (frames - 1) // 2 + 1
     return frames
+
+
+def stream_geom(hp: dict, right: int) -> dict:
+    """newGeom (conformer/stream.go:23-69): a cache-aware model's chunking
+    for right context `right`: chunks of 8*(right+1) mel frames (the first
+    1+8*right) led by the 9 frames before them, whose first 2 encoder rows
+    are dropped; attention over `left` earlier rows."""
+    if hp.get("att_style", "regular") != "chunked_limited":
+        raise ValueError("conformer: this model can't stream")
+    left = -1
+    choices = hp.get("context_choices") or []
+    for lc, rc in choices:
+        if rc == right:
+            left = lc
+    if not choices and right == hp.get("att_right", -1):
+        left = hp.get("att_left", -1)
+    if left < 0:
+        raise ValueError(f"conformer: the model wasn't trained for a right context of {right}")
+    sub = hp.get("subsampling", 8)
+    cache = hp.get("pre_encode_cache", -1)
+    cache = sub + 1 if cache < 0 else cache
+    drop = hp.get("drop_extra", -1)
+    drop = 1 + (cache - 1) // sub if drop < 0 else drop
+    first = hp.get("sampling_frames_first", -1)
+    first = 1 if first < 0 else first
+    chunk = right + 1
+    return dict(right=right, chunk=chunk, left=left, left_chunks=left // chunk, mel_first=first + sub * right,
+                mel_next=sub * chunk, mel_cache=cache, drop=drop, sample_first=first, sub=sub)
+
+
+def mel_chunks(mel: np.ndarray, g: dict, final: bool = True):
+    """The chunks melChunker.chunks (conformer/stream.go:187-226) cuts from
+    mel frames [n_mels][frames] that are all there: (frames [n_mels][nf]
+    (the cache frames, zero before the first, then the chunk), length,
+    first) for each, a last short chunk when final (a remainder shorter
+    than the sampling frames is dropped)."""
+    nm, avail = mel.shape
+    out, buf, n = [], 0, 0
+    while buf < avail:
+        size, need = (g["mel_next"], g["sub"]) if n else (g["mel_first"], g["sample_first"])
+        if not final and buf + size > avail:
+            break
+        k = min(size, avail - buf)
+        if k < need:
+            break
+        cache = g["mel_cache"] if n else 0
+        ch = np.zeros((nm, cache + k), np.float32)
+        lo = buf - cache
+        src = mel[:, max(lo, 0):buf + k]
+        ch[:, ch.shape[1] - src.shape[1]:] = src
+        out.append((ch, cache + k, n == 0))
+        buf += size
+        n += 1
+    return out
 
 
 class ConformerEncoder:

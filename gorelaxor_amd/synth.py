@@ -182,8 +182,9 @@ def conformer_model(hp: dict, seed: int = 9, pointwise_f16: bool = True, pre_f32
     rng = np.random.default_rng(seed)
     d, c, ff, K = hp["d"], hp["sub_channels"], hp["dff"], hp["conv_kernel"]
     F = hp["n_mels"]
+    causal = bool(hp.get("causal_sub", hp.get("att_style", "regular") == "chunked_limited"))
     for _ in range(3):
-        F = (F - 1) // 2 + 1
+        F = F // 2 + 1 if causal else (F - 1) // 2 + 1
     t = {}
 
     def vec(n, scale=0.1, base=0.0):

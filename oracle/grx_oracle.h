@@ -158,7 +158,46 @@ typedef struct {
     /* conv.3 / conv.6 as float32 [c][c] (the reference's converter keeps
      * them float32): when set, Linear takes the float route, not w3 / w6 */
     const float *w3f, *w6f;
+    /* HParams' attention and convolution forms (conformer/model.go:15-44):
+     * causal_sub pads the pre-encoder two before and one after; att_style 1
+     * is "chunked_limited" (cache-aware streaming), 0 "regular"; att_left,
+     * att_right, conv_left, conv_right as the file gives them (-1: none) */
+    int causal_sub, att_style, att_left, att_right, conv_left, conv_right;
 } orc_conformer;
+
+/* One query's keys [lo, hi) (keyRange, conformer/encoder.go:193-212, cut at
+ * the valid length as encodeEmbeddings does, :465-472; a streaming chunk's
+ * keys as streamEncode builds them, stream.go:273-287). */
+enum { ORC_KEYS_ALL = 0, ORC_KEYS_CHUNKED = 1, ORC_KEYS_WINDOW = 2, ORC_KEYS_STREAM = 3 };
+typedef struct {
+    int mode;
+    int T, L;               /* keys (offline: = queries) and the valid length */
+    int chunk, left_chunks; /* CHUNKED, STREAM */
+    int left, right;        /* WINDOW */
+    int c, slot0, Tc;       /* STREAM: cached keys, the cache slot of key 0, the chunk's rows */
+} orc_keys;
+void orc_conf_key_range(const orc_keys *k, int q, int *lo, int *hi);
+/* offlineKeys (encoder.go:196-212) for T frames of which L are valid: the
+ * key form and the query block length. */
+int orc_conf_offline_keys(const orc_conformer *m, int T, int L, orc_keys *k);
+int orc_conf_pad_left(const orc_conformer *m);
+
+/* Cache-aware streaming (conformer/stream.go:23-88, 241-307): the geometry
+ * for one right context and one stream's caches. */
+typedef struct {
+    int right, chunk, left, left_chunks, drop;
+    int kv_len;
+    float **kv;       /* per layer: up to left rows of normalized attention input */
+    float **conv;     /* per layer: the last pad_left gated frames */
+    float **pos_proj; /* per layer: positions left+chunk-1 down to -(chunk-1), projected */
+} orc_conf_stream;
+orc_conf_stream *orc_conf_stream_new(const orc_conformer *m, int right, int left, int drop);
+void orc_conf_stream_free(const orc_conformer *m, orc_conf_stream *s);
+/* streamStep: one chunk's log-mel [mels][nf] (cache frames first), length
+ * of them real; out receives the chunk's encoder rows (at most nf rows),
+ * *L_out how many.  -1 when the chunk has more rows than the geometry. */
+int orc_conf_stream_step(const orc_conformer *m, orc_conf_stream *s, const float *mel, int nf, int length, int first,
+                         float *out, int *L_out);
 
 void orc_conf_rel_pos(float *out, int n, int d);
 void orc_conf_bn_fold(const float *gw, const float *gb, const float *mean, const float *var, int d, float *s,

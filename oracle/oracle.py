@@ -510,7 +510,14 @@ class _CModel(C.Structure):
     _fields_ = ([(n, C.c_int) for n in ("d", "heads", "layers", "dff", "conv_kernel", "sub_channels", "n_mels",
                                         "xscaling", "conv_ln")] +
                 [(n, C.c_void_p) for n in ("w0", "b0", "w2", "b2", "w5", "b5", "w3", "w6", "out", "b3", "b6",
-                                           "out_b", "blocks", "w3f", "w6f")])
+                                           "out_b", "blocks", "w3f", "w6f")] +
+                [(n, C.c_int) for n in ("causal_sub", "att_style", "att_left", "att_right", "conv_left",
+                                        "conv_right")])
+
+
+class _CKeys(C.Structure):
+    _fields_ = [(n, C.c_int) for n in ("mode", "T", "L", "chunk", "left_chunks", "left", "right", "c", "slot0",
+                                       "Tc")]
 
 
 def _declare_conformer(L):
@@ -520,6 +527,15 @@ def _declare_conformer(L):
                                      C.POINTER(C.c_int)]
     L.orc_conf_block_run.argtypes = [C.c_void_p, C.c_int, _f32p, C.c_int, C.c_int, _f32p]
     L.orc_conformer_encode.argtypes = [C.c_void_p, _f32p, C.c_int, C.c_int, C.c_int, _f32p, C.POINTER(C.c_int),
+                                       C.POINTER(C.c_int)]
+    L.orc_conf_key_range.argtypes = [C.c_void_p, C.c_int, C.POINTER(C.c_int), C.POINTER(C.c_int)]
+    L.orc_conf_key_range.restype = None
+    L.orc_conf_offline_keys.argtypes = [C.c_void_p, C.c_int, C.c_int, C.c_void_p]
+    L.orc_conf_stream_new.argtypes = [C.c_void_p, C.c_int, C.c_int, C.c_int]
+    L.orc_conf_stream_new.restype = C.c_void_p
+    L.orc_conf_stream_free.argtypes = [C.c_void_p, C.c_void_p]
+    L.orc_conf_stream_free.restype = None
+    L.orc_conf_stream_step.argtypes = [C.c_void_p, C.c_void_p, _f32p, C.c_int, C.c_int, C.c_int, _f32p,
                                        C.POINTER(C.c_int)]
 
 
@@ -582,6 +598,11 @@ class ConformerOracle:
         m.d, m.heads, m.layers, m.dff = d, hp["heads"], nl, hp["dff"]
         m.conv_kernel, m.sub_channels, m.n_mels = K, c, hp["n_mels"]
         m.xscaling, m.conv_ln = int(bool(hp.get("xscaling", True))), int(conv_ln)
+        chunked = hp.get("att_style", "regular") == "chunked_limited"
+        m.att_style = int(chunked)
+        m.causal_sub = int(bool(hp.get("causal_sub", chunked)))
+        m.att_left, m.att_right = hp.get("att_left", -1), hp.get("att_right", -1)
+        m.conv_left, m.conv_right = hp.get("conv_left", -1), hp.get("conv_right", -1)
         pe = "enc.pre_encode."
         m.w0 = keep(_transpose_taps(tensors[pe + "conv.0.weight"], c, 9))
         m.w2 = keep(_transpose_taps(tensors[pe + "conv.2.weight"], c, 9))
@@ -635,7 +656,7 @@ class ConformerOracle:
         """encoder.go:123-167: (pre-encoder output [T][d], T, L)."""
         mel = _f32(mel)
         frames = mel.size // self.hp["n_mels"]
-        T = conf_frames_out(frames)
+        T = self.frames_out(frames)
         out = np.zeros(T * self.hp["d"], np.float32)
         t, l = C.c_int(), C.c_int()
         lib().orc_conf_subsample(C.byref(self._m), mel, frames, valid, out, C.byref(t), C.byref(l))
@@ -652,12 +673,76 @@ class ConformerOracle:
         """Model.encode without the prompt: (out [T][d], L); the first L rows are the output."""
         mel = _f32(mel)
         frames = mel.size // self.hp["n_mels"]
-        T = conf_frames_out(frames)
+        T = self.frames_out(frames)
         out = np.zeros(T * self.hp["d"], np.float32)
         t, l = C.c_int(), C.c_int()
         nl = self.hp["layers"] if layers is None else layers
         lib().orc_conformer_encode(C.byref(self._m), mel, frames, valid, nl, out, C.byref(t), C.byref(l))
         return out.reshape(T, self.hp["d"]), l.value
+
+    def frames_out(self, frames: int) -> int:
+        causal = bool(self._m.causal_sub)
+        for _ in range(3):
+            frames = frames // 2 + 1 if causal else (frames - 1) // 2 + 1
+        return frames
+
+    def offline_keys(self, T: int, L: int):
+        """offlineKeys (encoder.go:196-212): (the key form, block length)."""
+        k = _CKeys()
+        bl = lib().orc_conf_offline_keys(C.byref(self._m), T, L, C.byref(k))
+        return k, bl
+
+    def stream(self, right: int, left: int, drop: int) -> "ConformerOracleStream":
+        return ConformerOracleStream(self, right, left, drop)
+
+
+def conf_key_range(k, q: int):
+    """keyRange of query q under the key form k: (lo, hi)."""
+    lo, hi = C.c_int(), C.c_int()
+    lib().orc_conf_key_range(C.byref(k), q, C.byref(lo), C.byref(hi))
+    return lo.value, hi.value
+
+
+def conf_stream_keys(L: int, chunk: int, left_chunks: int, c: int, left: int, Tc: int):
+    """A streaming chunk's key form (stream.go:273-287)."""
+    return _CKeys(mode=3, L=L, chunk=chunk, left_chunks=left_chunks, c=c, slot0=left - c, Tc=Tc)
+
+
+class ConformerOracleStream:
+    """One stream's caches and its chunk steps (stream.go:72-88, 241-307)."""
+
+    def __init__(self, enc: ConformerOracle, right: int, left: int, drop: int):
+        self.enc = enc
+        self._p = lib().orc_conf_stream_new(C.byref(enc._m), right, left, drop)
+        self.first = True
+
+    def step(self, mel: np.ndarray, length: int):
+        """One chunk [n_mels][nf] (the cache frames first): its encoder rows [L][d]."""
+        mel = _f32(mel)
+        nf = mel.size // self.enc.hp["n_mels"]
+        out = np.zeros(max(nf, 1) * self.enc.hp["d"], np.float32)
+        n = C.c_int()
+        r = lib().orc_conf_stream_step(C.byref(self.enc._m), self._p, mel, nf, length, int(self.first), out,
+                                       C.byref(n))
+        if r != 0:
+            raise ValueError("the chunk has more encoder rows than the stream's geometry")
+        self.first = False
+        return out[:n.value * self.enc.hp["d"]].reshape(n.value, self.enc.hp["d"])
+
+    @property
+    def kv_len(self) -> int:
+        return C.cast(self._p, C.POINTER(C.c_int * 6)).contents[5]
+
+    def close(self):
+        if self._p:
+            lib().orc_conf_stream_free(C.byref(self.enc._m), self._p)
+            self._p = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
 
 
 # ---- whisper's token rules and sampler (whisper/transcribe.go:370-536) ----
