@@ -115,6 +115,11 @@ SIGNATURES = {
     "grx_conformer_frames_out": (i32, [vp, i32]),
     "grx_conformer_encode": (i32, [vp, vp, i32, i32, vp, vp, vp]),
     "grx_conformer_encode_dev": (i32, [vp, vp, i32, i32, vp, vp]),
+    "grx_conformer_stream_create": (i32, [vp, i32, i32, C.POINTER(vp)]),
+    "grx_conformer_stream_destroy": (i32, [vp]),
+    "grx_conformer_stream_geometry": (i32, [vp, vp]),
+    "grx_conformer_stream_step": (i32, [vp, vp, i32, vp, vp, vp]),
+    "grx_conformer_stream_step_dev": (i32, [vp, vp, i32, vp, vp, vp]),
     "grx_rnnt_create": (i32, [vp, vp, C.POINTER(vp)]),
     "grx_rnnt_destroy": (i32, [vp]),
     "grx_rnnt_load_gguf": (i32, [vp, C.c_char_p, vp, C.POINTER(vp)]),
@@ -135,7 +140,16 @@ class PocketHParams(C.Structure):
 class ConformerHParams(C.Structure):
     """grx_conformer_hparams."""
     _fields_ = [(n, C.c_int) for n in ("d", "heads", "layers", "dff", "conv_kernel", "sub_channels", "n_mels",
-                                       "xscaling", "conv_ln")]
+                                       "xscaling", "conv_ln", "att_chunked", "att_left", "att_right", "conv_left",
+                                       "conv_right", "causal_sub", "n_context_choices")] + [
+        ("context_choices", (C.c_int * 2) * 8)] + [
+        (n, C.c_int) for n in ("pre_encode_cache", "drop_extra", "sampling_frames_first")]
+
+
+class ConformerStreamGeom(C.Structure):
+    """grx_conformer_stream_geom."""
+    _fields_ = [(n, C.c_int) for n in ("right", "chunk", "left", "left_chunks", "mel_first", "mel_next", "mel_cache",
+                                       "drop", "sample_first")]
 
 
 class RnntHParams(C.Structure):

@@ -78,14 +78,35 @@ def mel_chunks(mel: np.ndarray, g: dict, final: bool = True):
     return out
 
 
+def _hparams(hp: dict) -> "_lib.ConformerHParams":
+    """grx_conformer_hparams from HParams-named settings (conformer/
+    model.go:15-44): att_style "regular" or "chunked_limited", the limits -1
+    where there are none, causal_sub as readEncoder defaults it."""
+    chunked = hp.get("att_style", "regular") == "chunked_limited"
+    h = _lib.ConformerHParams(d=hp["d"], heads=hp["heads"], layers=hp["layers"], dff=hp["dff"],
+                              conv_kernel=hp["conv_kernel"], sub_channels=hp["sub_channels"],
+                              n_mels=hp["n_mels"], xscaling=int(bool(hp.get("xscaling", True))),
+                              conv_ln=int(hp.get("conv_norm", "batch_norm") == "layer_norm"),
+                              att_chunked=int(chunked), att_left=hp.get("att_left", -1),
+                              att_right=hp.get("att_right", -1), conv_left=hp.get("conv_left", -1),
+                              conv_right=hp.get("conv_right", -1),
+                              causal_sub=int(bool(hp.get("causal_sub", chunked))),
+                              pre_encode_cache=hp.get("pre_encode_cache", -1), drop_extra=hp.get("drop_extra", -1),
+                              sampling_frames_first=hp.get("sampling_frames_first", -1))
+    choices = list(hp.get("context_choices") or [])
+    if len(choices) > 8:
+        raise ValueError("at most 8 attention context choices")
+    h.n_context_choices = len(choices)
+    for i, (lc, rc) in enumerate(choices):
+        h.context_choices[i][0], h.context_choices[i][1] = lc, rc
+    return h
+
+
 class ConformerEncoder:
     def __init__(self, hp: dict, tensors: dict | None = None, ctx: Context | None = None):
         self.ctx = ctx or default_context()
         self.hp = dict(hp)
-        h = _lib.ConformerHParams(d=hp["d"], heads=hp["heads"], layers=hp["layers"], dff=hp["dff"],
-                                  conv_kernel=hp["conv_kernel"], sub_channels=hp["sub_channels"],
-                                  n_mels=hp["n_mels"], xscaling=int(bool(hp.get("xscaling", True))),
-                                  conv_ln=int(hp.get("conv_norm", "batch_norm") == "layer_norm"))
+        h = _hparams(hp)
         out = C.c_void_p()
         _lib.call("grx_conformer_create", self.ctx.handle, C.byref(h), C.byref(out))
         self.handle = out
@@ -106,10 +127,19 @@ class ConformerEncoder:
         _lib.call("grx_conformer_load_gguf", self.ctx.handle, str(path).encode(), C.byref(h), C.byref(out))
         self.handle = out
         self.hp = {k: getattr(h, k) for k in ("d", "heads", "layers", "dff", "conv_kernel", "sub_channels",
-                                              "n_mels")}
+                                              "n_mels", "att_left", "att_right", "conv_left", "conv_right",
+                                              "pre_encode_cache", "drop_extra", "sampling_frames_first")}
         self.hp["xscaling"] = bool(h.xscaling)
         self.hp["conv_norm"] = "layer_norm" if h.conv_ln else "batch_norm"
+        self.hp["att_style"] = "chunked_limited" if h.att_chunked else "regular"
+        self.hp["causal_sub"] = bool(h.causal_sub)
+        self.hp["context_choices"] = [(h.context_choices[i][0], h.context_choices[i][1])
+                                      for i in range(h.n_context_choices)]
         return self
+
+    @property
+    def causal(self) -> bool:
+        return bool(self.hp.get("causal_sub", self.hp.get("att_style", "regular") == "chunked_limited"))
 
     def set_tensor(self, name: str, arr: np.ndarray) -> None:
         a = np.ascontiguousarray(arr)
@@ -124,7 +154,7 @@ class ConformerEncoder:
         batch, nm, frames = mel.shape
         assert nm == self.hp["n_mels"]
         v = np.ascontiguousarray(np.broadcast_to(np.asarray(valid, np.int32), (batch,)))
-        T = frames_out(frames)
+        T = frames_out(frames, self.causal)
         out = np.zeros((batch, T, self.hp["d"]), np.float32)
         lens = np.zeros(batch, np.int32)
         _lib.call("grx_conformer_encode", self.handle, mel.ctypes.data_as(C.c_void_p), batch, frames,
@@ -140,6 +170,61 @@ class ConformerEncoder:
     def close(self):
         if self.handle:
             _lib.call("grx_conformer_destroy", self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class ConformerStream:
+    """Cache-aware streaming (conformer/stream.go:23-88, 241-307) of `batch`
+    streams stepped together: each step takes one chunk per stream as the
+    reference's chunker cuts them (mel_chunks) and returns each stream's
+    encoder rows for it.  Right context `right` is one of the model's
+    trained choices."""
+
+    def __init__(self, enc: ConformerEncoder, right: int, batch: int = 1):
+        self.enc = enc
+        self.batch = batch
+        out = C.c_void_p()
+        _lib.call("grx_conformer_stream_create", enc.handle, right, batch, C.byref(out))
+        self.handle = out
+        g = _lib.ConformerStreamGeom()
+        _lib.call("grx_conformer_stream_geometry", self.handle, C.byref(g))
+        self.geom = {k: getattr(g, k) for k, _ in _lib.ConformerStreamGeom._fields_}
+        self.geom["sub"] = 8
+
+    def step(self, mel: np.ndarray, length) -> list[np.ndarray]:
+        """mel [batch][n_mels][nf] (or [n_mels][nf] for one stream), length
+        the real frames of each: each stream's rows [L][d]."""
+        mel = np.ascontiguousarray(mel, np.float32)
+        if mel.ndim == 2:
+            mel = mel[None]
+        batch, nm, nf = mel.shape
+        assert batch == self.batch and nm == self.enc.hp["n_mels"]
+        ln = np.ascontiguousarray(np.broadcast_to(np.asarray(length, np.int32), (batch,)))
+        d, chunk = self.enc.hp["d"], self.geom["chunk"]
+        out = np.zeros((batch, chunk, d), np.float32)
+        lens = np.zeros(batch, np.int32)
+        _lib.call("grx_conformer_stream_step", self.handle, mel.ctypes.data_as(C.c_void_p), nf,
+                  ln.ctypes.data_as(C.c_void_p), out.ctypes.data_as(C.c_void_p), lens.ctypes.data_as(C.c_void_p))
+        return [out[b, :lens[b]] for b in range(batch)]
+
+    def step_dev(self, mel_ptr: int, nf: int, length, out_ptr: int) -> np.ndarray:
+        """The step with mel [batch][n_mels][nf] and out [batch][chunk][d] in
+        device memory: the rows of each stream."""
+        ln = np.ascontiguousarray(np.broadcast_to(np.asarray(length, np.int32), (self.batch,)))
+        lens = np.zeros(self.batch, np.int32)
+        _lib.call("grx_conformer_stream_step_dev", self.handle, C.c_void_p(mel_ptr), nf,
+                  ln.ctypes.data_as(C.c_void_p), C.c_void_p(out_ptr), lens.ctypes.data_as(C.c_void_p))
+        return lens
+
+    def close(self):
+        if self.handle:
+            _lib.call("grx_conformer_stream_destroy", self.handle)
             self.handle = None
 
     def __del__(self):

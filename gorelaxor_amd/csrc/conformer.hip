@@ -18,6 +18,7 @@
 // per (batch, frames) shape.
 #include <cmath>
 #include <cstring>
+#include <functional>
 #include <map>
 #include <string>
 #include <vector>
@@ -33,19 +34,76 @@ constexpr int kAttnQ = 32;        // queries per attention block (encoder.go:211
 constexpr int kAttnThreads = 512;
 constexpr int kAttnLdsThreads = 1024;
 
-// encoder.go:33-38 (subOut) for the non-causal pre-encoder, and the valid
-// length after s halvings.
-__host__ __device__ inline int sub_out(int n) { return (n - 1) / 2 + 1; }
-__device__ inline int stage_len(int valid, int s) {
+// encoder.go:33-38 (subOut): a causal pre-encoder pads two before and one
+// after, the centred one one on each side; and the valid length after s
+// halvings.
+__host__ __device__ inline int sub_out(int n, int causal) { return causal ? n / 2 + 1 : (n - 1) / 2 + 1; }
+__host__ __device__ inline int stage_len(int valid, int s, int causal) {
     int L = valid;
-    for (int i = 0; i < s; ++i) L = sub_out(L);
+    for (int i = 0; i < s; ++i) L = sub_out(L, causal);
     return L;
 }
-// The encoder's valid length L (encoder.go:166): min(L3, T), at least 0.
-__device__ inline int enc_len(int valid, int T) {
-    const int L = stage_len(valid, 3);
-    return max(0, min(L, T));
+
+// A query's keys [lo, hi), per offlineKeys (encoder.go:196-212) cut at the
+// valid length L (encoder.go:465-472), or for a streaming chunk per
+// stream.go:273-287.  Queries go in blocks of bl rows, each block's keys
+// the union of its rows' ranges.
+enum { kKeysAll = 0, kKeysChunked = 1, kKeysWindow = 2, kKeysStream = 3 };
+struct AttnKeys {
+    int mode, bl;
+    int chunk, lchunks;  // chunked and streaming: rows per chunk, chunks of left context
+    int left, right;     // window limits; streaming: the left context (rows a stream keeps)
+};
+// q: the query's key index (a streaming chunk's queries follow its c
+// cached keys); T: the keys; L: the valid rows (queries past them see no
+// key).  The streaming form is the closed form of the reference's two
+// loops: the keys of whole chunks (NeMo's cache slots, key 0 in slot
+// left - c) from lchunks chunks before the query's through its own.
+__device__ inline void attn_keys(const AttnKeys &k, int q, int T, int L, int c, int &lo, int &hi) {
+    if (k.mode == kKeysStream) {
+        if (q - c >= L) {
+            lo = hi = 0;
+            return;
+        }
+        const int slot0 = k.left - c, qc = (slot0 + q) / k.chunk;
+        lo = max(0, (qc - k.lchunks) * k.chunk - slot0);
+        hi = min(c + L, (qc + 1) * k.chunk - slot0);
+        return;
+    }
+    if (q >= L) {
+        lo = hi = 0;
+        return;
+    }
+    int l = 0, h = T;
+    if (k.mode == kKeysChunked) {
+        const int cq = q / k.chunk;
+        l = max(0, (cq - k.lchunks) * k.chunk);
+        h = min(T, (cq + 1) * k.chunk);
+    } else if (k.mode == kKeysWindow) {
+        l = max(0, q - k.left);
+        h = min(T, q + k.right + 1);
+    }
+    lo = l;
+    hi = min(h, L);
 }
+
+// Where the attention finds its rows.  Queries of utterance b: q + (b*T +
+// t)*ldq.  Keys: K at kv + kvb*b + key*ldkv, V vo floats further; a stream's
+// keys start at its ring's head (ctl[1] rows in).  Position rows: pp, rows
+// ldp apart, row 0 for relative position Tk-1 (offline), or for maxfirst
+// in a streaming table (the rows for Tk-1 found from ctl[0]).
+struct AttnIO {
+    const float *q;
+    int ldq;
+    const float *kv;
+    int ldkv, vo;
+    size_t kvb;
+    const float *pp;
+    int ldp, maxfirst;
+    const int *lens;  // valid rows per utterance
+    const int *ctl;   // streaming: [0] cached keys c, [1] ring head; null offline
+    int T;            // queries per utterance
+};
 
 // Go's builtin max for float32 (NaN wins, +0 over -0).
 __device__ inline float go_max(float a, float b) {
@@ -71,17 +129,17 @@ __device__ inline float go_max(float a, float b) {
 // (fma for channels of whole groups of eight); the depthwise: from the bias,
 // w*x unfused over the taps in range.
 __global__ void sub_conv01_kernel(const float *__restrict__ mel, int frames, int nm, const int *__restrict__ valid,
-                                  const float *__restrict__ w0, const float *__restrict__ b0,
+                                  int causal, const float *__restrict__ w0, const float *__restrict__ b0,
                                   const float *__restrict__ w2, const float *__restrict__ b2, int c, int T1, int F1,
                                   int T2, int F2, int8_t *__restrict__ xq, float *__restrict__ xs,
                                   float *__restrict__ xf) {
-    extern __shared__ float patch[];  // [7][4*F2 + 3], column q = mel column q - 3
+    extern __shared__ float patch[];  // [7][4*F2 + 3], column q = mel column q - 3*pl
     const int ch = threadIdx.x, t2 = blockIdx.x % T2, b = blockIdx.x / T2;
-    const int W = 4 * F2 + 3;
+    const int W = 4 * F2 + 3, pl = causal ? 2 : 1;  // the padding before
     const int vb = valid[b], tv = min(frames, vb);
-    const int L1 = stage_len(vb, 1), L2 = stage_len(vb, 2);
+    const int L1 = stage_len(vb, 1, causal), L2 = stage_len(vb, 2, causal);
     for (int e = ch; e < 7 * W; e += blockDim.x) {
-        const int r = e / W, q = e % W, ti = 4 * t2 - 3 + r, fi = q - 3;
+        const int r = e / W, q = e % W, ti = 4 * t2 - 3 * pl + r, fi = q - 3 * pl;
         patch[e] = (ti >= 0 && ti < tv && fi >= 0 && fi < nm) ? mel[((size_t)b * nm + fi) * frames + ti] : 0.f;
     }
     __syncthreads();
@@ -96,7 +154,8 @@ __global__ void sub_conv01_kernel(const float *__restrict__ mel, int frames, int
     for (int f2 = 0; f2 < F2; ++f2) {
         float o = 0.f;
         if (t2 < L2) {
-            // the 7x7 mel values of this position: patch columns 4f2 .. 4f2+6
+            // the 7x7 mel values of this position: patch columns 4f2 .. 4f2+6,
+            // rows and columns 4t2-3pl.., 4f2-3pl.. of the plane
             float pv[7][7];
 #pragma unroll
             for (int r = 0; r < 7; ++r)
@@ -106,14 +165,14 @@ __global__ void sub_conv01_kernel(const float *__restrict__ mel, int frames, int
 #pragma unroll
             for (int j2 = 0; j2 < 9; ++j2) {
                 const int kt = j2 / 3, kf = j2 % 3;
-                const int ti = 2 * t2 + kt - 1, fi = 2 * f2 + kf - 1;  // conv0 output position
+                const int ti = 2 * t2 + kt - pl, fi = 2 * f2 + kf - pl;  // conv0 output position
                 if (ti < 0 || ti >= T1 || fi < 0 || fi >= F1) continue;
                 float x = 0.f;
                 if (ti < L1) {
                     float a = bias0;
 #pragma unroll
                     for (int j = 0; j < 9; ++j) {
-                        // mel (2ti + j/3 - 1, 2fi + j%3 - 1) = pv[2kt + j/3][2kf + j%3]; zero taps
+                        // mel (2ti + j/3 - pl, 2fi + j%3 - pl) = pv[2kt + j/3][2kf + j%3]; zero taps
                         // are skipped (a select, not a branch)
                         const float v = pv[2 * kt + j / 3][2 * kf + j % 3];
                         const float t = fm ? __fmaf_rn(v, w0v[j], a) : __fadd_rn(a, __fmul_rn(v, w0v[j]));
@@ -140,19 +199,20 @@ __global__ void sub_conv01_kernel(const float *__restrict__ mel, int frames, int
 // pointwise output, read through maskRows and ReLU (encoder.go:152-153).
 template <bool RELU_IN>
 __global__ void sub_dwconv_kernel(const float *__restrict__ in, int T, int F, int c, const int *__restrict__ valid,
-                                  int s, const float *__restrict__ w, const float *__restrict__ bias, int T1, int F1,
-                                  int8_t *__restrict__ xq, float *__restrict__ xs, float *__restrict__ xf) {
+                                  int causal, int s, const float *__restrict__ w, const float *__restrict__ bias,
+                                  int T1, int F1, int8_t *__restrict__ xq, float *__restrict__ xs,
+                                  float *__restrict__ xf) {
     const int p = blockIdx.x, ch = threadIdx.x;
     const int f1 = p % F1, t1 = (p / F1) % T1, b = p / (F1 * T1);
-    const int vb = valid[b];
-    const int Lin = stage_len(vb, s - 1), Lout = stage_len(vb, s);
+    const int vb = valid[b], pl = causal ? 2 : 1;
+    const int Lin = stage_len(vb, s - 1, causal), Lout = stage_len(vb, s, causal);
     float o = 0.f;
     if (t1 < Lout) {
         float xv[9], wv[9];
         bool ok[9];
 #pragma unroll
         for (int j = 0; j < 9; ++j) {
-            const int ti = 2 * t1 + j / 3 - 1, fi = 2 * f1 + j % 3 - 1;
+            const int ti = 2 * t1 + j / 3 - pl, fi = 2 * f1 + j % 3 - pl;
             ok[j] = ti >= 0 && ti < T && fi >= 0 && fi < F;  // taps outside the plane are skipped
             // the load is issued at a clamped address and the value chosen
             // afterwards, so the nine loads stay in flight together
@@ -259,15 +319,18 @@ __global__ void pw_f32_rows_kernel(const float *__restrict__ x, const float *__r
 
 // The last pointwise output through maskRows and ReLU, flattened [t][c*F+f]
 // (encoder.go:158-166) and rounded to Q8_0 for the output Linear: one
-// workgroup per (utterance, frame).
+// workgroup per kept (utterance, frame): frames drop.. of each utterance's
+// T (a streaming chunk's first rows are dropped, stream.go:255-258), Tp of
+// them, to rows b*Tp + t - drop.
 __global__ void sub_flatten_kernel(const float *__restrict__ y, int T, int F, int c, const int *__restrict__ valid,
-                                   int8_t *__restrict__ xq, float *__restrict__ xs) {
-    const int row = blockIdx.x, t = row % T, b = row / T;
-    const int L = stage_len(valid[b], 3);
+                                   int causal, int drop, int Tp, int8_t *__restrict__ xq, float *__restrict__ xs) {
+    const int row = blockIdx.x, b = row / Tp, t = row % Tp + drop;
+    const int L = stage_len(valid[b], 3, causal);
     const int K = c * F;
+    const size_t src = (size_t)b * T + t;
     for (int i = threadIdx.x; i < K; i += blockDim.x) {
         const int ch = i / F, f = i % F;
-        const float v = y[((size_t)row * F + f) * c + ch];
+        const float v = y[(src * F + f) * c + ch];
         const float r = t < L ? (v < 0.f ? 0.f : v) : 0.f;
         quant32_store(r, xq + (size_t)row * K + i, xs + (size_t)row * (K / 32) + i / 32, i & 31);
     }
@@ -323,27 +386,59 @@ __global__ __launch_bounds__(kRowThreads) void ln_rows_kernel(float *__restrict_
 
 // ---------------------------------------------------------------- attention
 
+// The keys [k0, k1) of a block of queries q0..q1-1 (key indices qoff+q):
+// the union of its rows' ranges (encoder.go:285-289).
+__device__ inline void block_keys(const AttnKeys &ak, int q0, int q1, int qoff, int Tk, int L, int c, int &k0,
+                                  int &k1) {
+    k0 = Tk;
+    k1 = 0;
+    for (int q = q0; q < q1; ++q) {
+        int lo, hi;
+        attn_keys(ak, qoff + q, Tk, L, c, lo, hi);
+        k0 = min(k0, lo);
+        k1 = max(k1, hi);
+    }
+}
+
+// A stream's cached keys and ring head (0 offline), the keys' first row
+// and the position rows for relative position Tk-1.
+struct AttnRows {
+    int c, Tk;
+    const float *kv, *pp;
+};
+__device__ inline AttnRows attn_rows(const AttnIO &io, int b) {
+    AttnRows r;
+    r.c = io.ctl ? io.ctl[0] : 0;
+    const int head = io.ctl ? io.ctl[1] : 0;
+    r.Tk = r.c + io.T;
+    r.kv = io.kv + io.kvb * b + (size_t)head * io.ldkv;
+    r.pp = io.ctl ? io.pp + (size_t)(io.maxfirst - (r.Tk - 1)) * io.ldp : io.pp;
+    return r;
+}
+
 // Relative-position multi-head self-attention (encoder.go:259-330) of one
-// (utterance, head, block of 32 queries), keys limited to the utterance's
-// valid length L (queries at or past L see none).  qkv holds the q|k|v
-// Linear outputs [row][3D]; pp the block's projected position table
-// [2T-1][ldp].  qu = q + pos_u and qv = q + pos_v in float32; scores =
-// MatMulF32(qu, k) and bd = MatMulF32(qv, pp rows jlo..), each in the route
-// MatMulF32 takes for nq rows; row i adds bd shifted by nq-1-i, scales,
-// softmax by ExpSub/Scale; the output MatMulF32(p, v^T) is rounded to Q8_0
-// per 32 values of the head's slice for the out Linear.
-__global__ __launch_bounds__(kAttnThreads) void conf_attn_kernel(
-    const float *__restrict__ qkv, const float *__restrict__ pp, int ldp, const float *__restrict__ pos_u,
-    const float *__restrict__ pos_v, const int *__restrict__ valid, int T, int D, int hd, float scale,
-    int8_t *__restrict__ xq, float *__restrict__ xs) {
+// (utterance, head, block of bl queries): the block's keys [k0, k1) (the
+// union of its rows' ranges), qu = q + pos_u and qv = q + pos_v in float32;
+// scores = MatMulF32(qu, k) and bd = MatMulF32(qv, pp rows jlo..), each in
+// the route MatMulF32 takes for nq rows; row i adds bd shifted by nq-1-i,
+// scales, keeps its own keys [lo, hi) (-inf outside), softmax by
+// ExpSub/Scale; the output MatMulF32(p, v^T) is rounded to Q8_0 per 32
+// values of the head's slice for the out Linear.
+__global__ __launch_bounds__(kAttnThreads) void conf_attn_kernel(const AttnIO io, const AttnKeys ak,
+                                                                 const float *__restrict__ pos_u,
+                                                                 const float *__restrict__ pos_v, int D, int hd,
+                                                                 float scale, int8_t *__restrict__ xq,
+                                                                 float *__restrict__ xs) {
     extern __shared__ float sm[];
     const int blk = blockIdx.x, h = blockIdx.y, b = blockIdx.z, tid = threadIdx.x, nt = blockDim.x;
-    const int L = enc_len(valid[b], T);
-    const int q0 = blk * kAttnQ, q1 = min(T, q0 + kAttnQ), nq = q1 - q0;
-    const int khi = min(T, L);
-    const int k0 = 0, k1 = q0 < L ? khi : 0, nk = k1 - k0;
-    const size_t ld = 3 * (size_t)D;
-    const float *base = qkv + (size_t)b * T * ld;
+    const int T = io.T, L = io.lens[b];
+    const AttnRows ar = attn_rows(io, b);
+    const int c = ar.c, Tk = ar.Tk, qoff = Tk - T;
+    const int q0 = blk * ak.bl, q1 = min(T, q0 + ak.bl), nq = q1 - q0;
+    int k0, k1;
+    block_keys(ak, q0, q1, qoff, Tk, L, c, k0, k1);
+    const int nk = k1 - k0;
+    const float *qb = io.q + (size_t)b * T * io.ldq;
     const int nqb = hd / 32;
     if (nk <= 0) {  // encoder.go:290-293: the block's output rows are zero
         for (int g = tid >> 5; g < nq * nqb; g += nt >> 5) {
@@ -354,36 +449,39 @@ __global__ __launch_bounds__(kAttnThreads) void conf_attn_kernel(
         }
         return;
     }
-    const int np = nq + nk - 1, jlo = T - 1 - (q1 - 1) + k0;
+    const int np = nq + nk - 1, jlo = Tk - 1 - (qoff + q1 - 1) + k0;
     const int sq = hd + 1, sS = nk | 1, sB = np | 1;
     float *qu = sm, *qv = sm + kAttnQ * sq, *S = qv + kAttnQ * sq, *BD = S + kAttnQ * sS;
     float *rmx = BD + kAttnQ * sB, *rinv = rmx + kAttnQ;
+    const float *kb = ar.kv + (size_t)k0 * io.ldkv;
     for (int e = tid; e < nq * hd; e += nt) {
         const int i = e / hd, j = e % hd;
-        const float q = base[(size_t)(q0 + i) * ld + h * hd + j];
+        const float q = qb[(size_t)(q0 + i) * io.ldq + h * hd + j];
         qu[i * sq + j] = __fadd_rn(q, pos_u[h * hd + j]);
         qv[i * sq + j] = __fadd_rn(q, pos_v[h * hd + j]);
     }
     __syncthreads();
     for (int e = tid; e < nq * nk; e += nt) {
         const int i = e % nq, kk = e / nq;
-        S[i * sS + kk] = matmul_f32_one(qu + i * sq, base + (size_t)(k0 + kk) * ld + D + h * hd, 1, hd, i, nq, kk, nk);
+        S[i * sS + kk] = matmul_f32_one(qu + i * sq, kb + (size_t)kk * io.ldkv + h * hd, 1, hd, i, nq, kk, nk);
     }
     for (int e = tid; e < nq * np; e += nt) {
         const int i = e % nq, jj = e / nq;
-        BD[i * sB + jj] = matmul_f32_one(qv + i * sq, pp + (size_t)(jlo + jj) * ldp + h * hd, 1, hd, i, nq, jj, np);
+        BD[i * sB + jj] =
+            matmul_f32_one(qv + i * sq, ar.pp + (size_t)(jlo + jj) * io.ldp + h * hd, 1, hd, i, nq, jj, np);
     }
     __syncthreads();
     // the scores of row i: (s + bd[i][nq-1-i+kk]) * scale inside [lo, hi),
     // -inf outside; the row maximum by one wave per row
     const int lane = tid & 63, wave = tid >> 6, nw = nt >> 6;
     for (int i = wave; i < nq; i += nw) {
-        const int hi = q0 + i < L ? khi : 0;
+        int lo, hi;
+        attn_keys(ak, qoff + q0 + i, Tk, L, c, lo, hi);
         float mx = -__builtin_inff();
         for (int kk = lane; kk < nk; kk += 64) {
             const int kx = k0 + kk;
             float v;
-            if (kx < 0 || kx >= hi) {
+            if (kx < lo || kx >= hi) {
                 v = -__builtin_inff();
             } else {
                 v = __fmul_rn(__fadd_rn(S[i * sS + kk], BD[i * sB + nq - 1 - i + kk]), scale);
@@ -436,11 +534,11 @@ __global__ __launch_bounds__(kAttnThreads) void conf_attn_kernel(
     }
     __syncthreads();
     // out = MatMulF32(p, v^T): m = nq, n = hd, k = nk; v^T's row e is the
-    // value column e (elements ld apart)
+    // value column e (elements ldkv apart)
     float *O = qu;  // [nq][sq], qu is no longer needed
     for (int e = tid; e < nq * hd; e += nt) {
         const int i = e % nq, ee = e / nq;
-        O[i * sq + ee] = matmul_f32_one(S + i * sS, base + (size_t)k0 * ld + 2 * D + h * hd + ee, ld, nk, i, nq, ee, hd);
+        O[i * sq + ee] = matmul_f32_one(S + i * sS, kb + io.vo + h * hd + ee, io.ldkv, nk, i, nq, ee, hd);
     }
     __syncthreads();
     for (int g = tid >> 5; g < nq * nqb; g += nt >> 5) {
@@ -503,26 +601,30 @@ __device__ __forceinline__ void packed4(const FA &a, const FB &b, int k, float o
 // The same attention with the head's keys, the rows of the position table
 // the block uses and the values staged in LDS, for RQ of the block's query
 // rows per workgroup (rows r0.. of block blk; the route of each product is
-// still chosen by the row's index in its block of 32 and by the block's
-// full column counts).  Only the band of bd that the rows use is computed:
+// still chosen by the row's index in its block and by the block's full
+// column counts).  Only the band of bd that the rows use is computed:
 // bd[i][nq-1-i+kk] for the nk keys.
 template <int RQ>
-__global__ __launch_bounds__(kAttnLdsThreads) void conf_attn_lds_kernel(
-    const float *__restrict__ qkv, const float *__restrict__ pp, int ldp, const float *__restrict__ pos_u,
-    const float *__restrict__ pos_v, const int *__restrict__ valid, int T, int D, int hd, float scale,
-    int8_t *__restrict__ xq, float *__restrict__ xs) {
+__global__ __launch_bounds__(kAttnLdsThreads) void conf_attn_lds_kernel(const AttnIO io, const AttnKeys ak,
+                                                                        const float *__restrict__ pos_u,
+                                                                        const float *__restrict__ pos_v, int D,
+                                                                        int hd, float scale,
+                                                                        int8_t *__restrict__ xq,
+                                                                        float *__restrict__ xs) {
     extern __shared__ float sm[];
-    constexpr int kChunks = kAttnQ / RQ;
-    const int blk = blockIdx.x / kChunks, r0 = (blockIdx.x % kChunks) * RQ;
+    const int pieces = (ak.bl + RQ - 1) / RQ;
+    const int blk = blockIdx.x / pieces, r0 = (blockIdx.x % pieces) * RQ;
     const int h = blockIdx.y, b = blockIdx.z, tid = threadIdx.x, nt = blockDim.x;
-    const int L = enc_len(valid[b], T);
-    const int q0 = blk * kAttnQ, q1 = min(T, q0 + kAttnQ), nq = q1 - q0;
+    const int T = io.T, L = io.lens[b];
+    const AttnRows ar = attn_rows(io, b);
+    const int c = ar.c, Tk = ar.Tk, qoff = Tk - T;
+    const int q0 = blk * ak.bl, q1 = min(T, q0 + ak.bl), nq = q1 - q0;
     if (r0 >= nq) return;
     const int nr = min(RQ, nq - r0);  // rows r0 .. r0+nr-1 of the block
-    const int khi = min(T, L);
-    const int k0 = 0, k1 = q0 < L ? khi : 0, nk = k1 - k0;
-    const size_t ld = 3 * (size_t)D;
-    const float *base = qkv + (size_t)b * T * ld;
+    int k0, k1;
+    block_keys(ak, q0, q1, qoff, Tk, L, c, k0, k1);
+    const int nk = k1 - k0;
+    const float *qb = io.q + (size_t)b * T * io.ldq;
     const int nqb = hd / 32;
     if (nk <= 0) {
         for (int g = tid >> 5; g < nr * nqb; g += nt >> 5) {
@@ -533,13 +635,14 @@ __global__ __launch_bounds__(kAttnLdsThreads) void conf_attn_lds_kernel(
         }
         return;
     }
-    const int np = nq + nk - 1, jlo = T - 1 - (q1 - 1) + k0;
+    const int np = nq + nk - 1, jlo = Tk - 1 - (qoff + q1 - 1) + k0;
     const int sq = hd + 1, sS = nk | 1;
     float *qu = sm, *qv = qu + RQ * sq, *S = qv + RQ * sq, *BD = S + RQ * sS, *rmx = BD + RQ * sS,
           *rinv = rmx + RQ, *st = rinv + RQ;
-    stage_f4(qu, sq, base + (size_t)(q0 + r0) * ld + h * hd, ld, nr, hd);
+    const float *kb = ar.kv + (size_t)k0 * io.ldkv;
+    stage_f4(qu, sq, qb + (size_t)(q0 + r0) * io.ldq + h * hd, io.ldq, nr, hd);
     // keys k0.. of the head, rows sq apart
-    stage_f4(st, sq, base + (size_t)k0 * ld + D + h * hd, ld, nk, hd);
+    stage_f4(st, sq, kb + h * hd, io.ldkv, nk, hd);
     __syncthreads();
     for (int e = tid; e < nr * hd; e += nt) {
         const int i = e / hd, j = e % hd;
@@ -569,7 +672,7 @@ __global__ __launch_bounds__(kAttnLdsThreads) void conf_attn_lds_kernel(
     __syncthreads();
     // position rows jlo + nq-1-(r0+i) + kk: from pb = jlo + nq-1-(r0+nr-1) on, nk + nr - 1 of them
     const int pb = jlo + nq - 1 - (r0 + nr - 1), npr = nk + nr - 1;
-    stage_f4(st, sq, pp + (size_t)pb * ldp + h * hd, ldp, npr, hd);
+    stage_f4(st, sq, ar.pp + (size_t)pb * io.ldp + h * hd, io.ldp, npr, hd);
     __syncthreads();
     // bd[i][kk] uses position row (nr-1-i) + kk of the staged ones: rows
     // i0+j with keys kd+j share row nr-1-i0+kd, so a thread takes such a
@@ -602,15 +705,16 @@ __global__ __launch_bounds__(kAttnLdsThreads) void conf_attn_lds_kernel(
     }
     __syncthreads();
     // values of the head (rows hd apart) while the rows are scored
-    stage_f4(st, hd, base + (size_t)k0 * ld + 2 * D + h * hd, ld, nk, hd);
+    stage_f4(st, hd, kb + io.vo + h * hd, io.ldkv, nk, hd);
     const int lane = tid & 63, wave = tid >> 6, nw = nt >> 6;
     for (int i = wave; i < nr; i += nw) {
-        const int hi = q0 + r0 + i < L ? khi : 0;
+        int lo, hi;
+        attn_keys(ak, qoff + q0 + r0 + i, Tk, L, c, lo, hi);
         float mx = -__builtin_inff();
         for (int kk = lane; kk < nk; kk += 64) {
             const int kx = k0 + kk;
             float v;
-            if (kx < 0 || kx >= hi) {
+            if (kx < lo || kx >= hi) {
                 v = -__builtin_inff();
             } else {
                 v = __fmul_rn(__fadd_rn(S[i * sS + kk], BD[i * sS + kk]), scale);
@@ -697,8 +801,8 @@ size_t attn_smem_floats(int T, int hd) {
 
 // GLU of the pointwise output (encoder.go:350-361): g = a * sigmoid(b) with
 // sigmoid(v) = 1/(1 + expf(-v)) (the scalar expf), rows at or past the
-// utterance's valid length zeroed.
-__global__ void conf_glu_kernel(const float *__restrict__ a, int R, int T, int D, const int *__restrict__ valid,
+// utterance's valid rows lens[b] zeroed.
+__global__ void conf_glu_kernel(const float *__restrict__ a, int R, int T, int D, const int *__restrict__ lens,
                                 float *__restrict__ g) {
     const size_t total = (size_t)R * D;
     for (size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x; idx < total;
@@ -706,7 +810,7 @@ __global__ void conf_glu_kernel(const float *__restrict__ a, int R, int T, int D
         const int c = (int)(idx % D);
         const int row = (int)(idx / D), t = row % T, b = row / T;
         float v = 0.f;
-        if (t < enc_len(valid[b], T)) {
+        if (t < lens[b]) {
             const float *ar = a + (size_t)row * 2 * D;
             const float sg = __fdiv_rn(1.0f, __fadd_rn(1.0f, grx_expf_go(-ar[D + c])));
             v = __fmul_rn(ar[c], sg);
@@ -715,12 +819,27 @@ __global__ void conf_glu_kernel(const float *__restrict__ a, int R, int T, int D
     }
 }
 
-// The centred depthwise convolution (encoder.go:362-385: from the bias, w*x
-// unfused over the taps in range, in order), the folded batch norm r*s + b
-// (unfused) or the LayerNorm (LN), SiLU of the AVX route, rounded to Q8_0
-// for pointwise2.  One workgroup per row.
+// The gated frames before a call's first one (encoder.go:372-377): a
+// stream's last padL frames in a ring of padL rows per stream (the oldest
+// at slot ctl[2]), or none (offline: those taps are skipped).
+struct ConvPrev {
+    const float *ring;  // [B][padL][D], or null
+    const int *ctl;
+};
+// Frame ti < 0 of utterance b, or null when there is none.
+__device__ inline const float *conv_prev_row(const ConvPrev &cp, int b, int ti, int padL, int D) {
+    if (cp.ring == nullptr || ti < -padL) return nullptr;
+    const int slot = (cp.ctl[2] + padL + ti) % padL;
+    return cp.ring + ((size_t)b * padL + slot) * D;
+}
+
+// The depthwise convolution (encoder.go:362-385: from the bias, w*x unfused
+// over the taps in range, tap j at frame t + j - padL, in order), the folded
+// batch norm r*s + b (unfused) or the LayerNorm (LN), SiLU of the AVX route,
+// rounded to Q8_0 for pointwise2.  One workgroup per row.
 template <bool LN>
 __global__ __launch_bounds__(kRowThreads) void conf_dwconv_kernel(const float *__restrict__ g, int T, int D, int K,
+                                                                  int padL, const ConvPrev cp,
                                                                   const float *__restrict__ w,
                                                                   const float *__restrict__ dwb,
                                                                   const float *__restrict__ cn_w,
@@ -729,7 +848,6 @@ __global__ __launch_bounds__(kRowThreads) void conf_dwconv_kernel(const float *_
     extern __shared__ __align__(16) float row[];
     __shared__ double red[48];  // ln_block_reduce
     const int r = blockIdx.x, t = r % T, b = r / T, tid = threadIdx.x;
-    const int padL = (K - 1) / 2;
     const float *gb = g + (size_t)b * T * D;
     for (int c = tid; c < D; c += blockDim.x) {
         float o = dwb != nullptr ? dwb[c] : 0.f;
@@ -739,9 +857,11 @@ __global__ __launch_bounds__(kRowThreads) void conf_dwconv_kernel(const float *_
 #pragma unroll
             for (int u = 0; u < 8; ++u) {
                 const int j = j0 + u, ti = t + j - padL;
-                ok[u] = j < K && ti >= 0 && ti < T;  // taps outside the frames are skipped
+                const float *pr = ti < 0 ? conv_prev_row(cp, b, ti, padL, D) : nullptr;
+                // taps outside the frames (and before a stream's cache) are skipped
+                ok[u] = j < K && ((ti >= 0 && ti < T) || pr != nullptr);
                 // clamped addresses keep the eight loads in flight together
-                xv[u] = gb[(size_t)min(max(ti, 0), T - 1) * D + c];
+                xv[u] = pr != nullptr ? pr[c] : gb[(size_t)min(max(ti, 0), T - 1) * D + c];
                 wv[u] = w[(size_t)min(j, K - 1) * D + c];
             }
 #pragma unroll
@@ -768,6 +888,7 @@ __global__ __launch_bounds__(kRowThreads) void conf_dwconv_kernel(const float *_
 // each frame.  grid (ceil(T/kDwRows), D/64, B).
 constexpr int kDwRows = 16;
 __global__ __launch_bounds__(256) void conf_dwconv_win_kernel(const float *__restrict__ g, int T, int D, int K,
+                                                              int padL, const ConvPrev cp,
                                                               const float *__restrict__ w,
                                                               const float *__restrict__ dwb,
                                                               const float *__restrict__ cn_w,
@@ -776,10 +897,11 @@ __global__ __launch_bounds__(256) void conf_dwconv_win_kernel(const float *__res
     extern __shared__ float win[];  // [kDwRows + K - 1][64] frames, then [K][64] taps
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int t0 = blockIdx.x * kDwRows, c0 = blockIdx.y * 64, b = blockIdx.z, c = c0 + lane;
-    const int padL = (K - 1) / 2, nrow = min(kDwRows, T - t0), wr = nrow + K - 1;
+    const int nrow = min(kDwRows, T - t0), wr = nrow + K - 1;
     float *wl = win + (kDwRows + K - 1) * 64;
     const float *gb = g + (size_t)b * T * D + c0;
     const int n = (wr + K) * 64;
+    const int lo_t = cp.ring != nullptr ? -padL : 0;  // the first frame a tap may read
     for (int e0 = tid; e0 < n; e0 += 8 * 256) {
         // every load issued at a clamped address, the value chosen after,
         // so the eight stay in flight together
@@ -787,7 +909,8 @@ __global__ __launch_bounds__(256) void conf_dwconv_win_kernel(const float *__res
 #pragma unroll
         for (int u = 0; u < 8; ++u) {
             const int e = min(e0 + u * 256, n - 1), r = e >> 6, l = e & 63, ti = t0 - padL + r;
-            const float *src = r < wr ? gb + (size_t)min(max(ti, 0), T - 1) * D + l
+            const float *pr = (r < wr && ti < 0) ? conv_prev_row(cp, b, ti, padL, D) : nullptr;
+            const float *src = r < wr ? (pr != nullptr ? pr + c0 + l : gb + (size_t)min(max(ti, 0), T - 1) * D + l)
                                       : w + (size_t)min(r - wr, K - 1) * D + c0 + l;
             v[u] = *src;
         }
@@ -796,7 +919,7 @@ __global__ __launch_bounds__(256) void conf_dwconv_win_kernel(const float *__res
             const int e = e0 + u * 256, r = e >> 6, l = e & 63, ti = t0 - padL + r;
             if (e < n) {
                 if (r < wr)
-                    win[e] = (ti >= 0 && ti < T) ? v[u] : 0.f;
+                    win[e] = (ti >= lo_t && ti < T) ? v[u] : 0.f;
                 else
                     wl[(r - wr) * 64 + l] = v[u];
             }
@@ -817,7 +940,7 @@ __global__ __launch_bounds__(256) void conf_dwconv_win_kernel(const float *__res
         for (int r = 0; r < 4; ++r) {
             const int ti = t0 + r0 + r + j - padL;  // taps outside the frames are skipped
             const float t = __fadd_rn(o[r], __fmul_rn(wj, xv[r]));
-            o[r] = (r0 + r < nrow && ti >= 0 && ti < T) ? t : o[r];
+            o[r] = (r0 + r < nrow && ti >= lo_t && ti < T) ? t : o[r];
         }
     }
     const float sw = cn_w[c], sb = cn_b[c];
@@ -829,6 +952,47 @@ __global__ __launch_bounds__(256) void conf_dwconv_win_kernel(const float *__res
             const size_t row = (size_t)b * T + t0 + r0 + r;
             quant32_store(sl, xq + row * D + c, xs + row * (D / 32) + c / 32, c & 31);
         }
+    }
+}
+
+// ---------------------------------------------------------------- stream caches
+
+// A chunk's key and value rows (the K and V thirds of the q|k|v product,
+// rows [B][T][3D]) into each stream's ring of cap rows: chunk row i to slot
+// (head + c + i) % cap, written twice (slot and slot + cap), so that any cap
+// consecutive slots from the head read as one run of rows.  ctl: [0] the
+// cached keys c, [1] the head.
+__global__ void kv_ring_append_kernel(const float *__restrict__ qkv, int B, int T, int D, float *__restrict__ ring,
+                                      int cap, const int *__restrict__ ctl) {
+    const int c = ctl[0], head = ctl[1];
+    const size_t total = (size_t)B * T * 2 * D;
+    for (size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x; idx < total;
+         idx += (size_t)gridDim.x * blockDim.x) {
+        const int col = (int)(idx % (2 * D));
+        const size_t rt = idx / (2 * D);
+        const int i = (int)(rt % T), b = (int)(rt / T);
+        const float v = qkv[rt * 3 * D + D + col];
+        const int slot = (head + c + i) % cap;
+        float *rb = ring + (size_t)b * 2 * cap * 2 * D;
+        rb[(size_t)slot * 2 * D + col] = v;
+        rb[(size_t)(slot + cap) * 2 * D + col] = v;
+    }
+}
+
+// The chunk's last min(T, padL) gated frames into each stream's
+// convolution ring (stream.go:302-305): frame i to slot (ctl[2] + i) % padL,
+// over the oldest ones.
+__global__ void conv_ring_append_kernel(const float *__restrict__ g, int B, int T, int D, float *__restrict__ ring,
+                                        int padL, const int *__restrict__ ctl) {
+    const int head = ctl[2], n = min(T, padL), i0 = T - n;
+    const size_t total = (size_t)B * n * D;
+    for (size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x; idx < total;
+         idx += (size_t)gridDim.x * blockDim.x) {
+        const int col = (int)(idx % D);
+        const size_t rt = idx / D;
+        const int i = i0 + (int)(rt % n), b = (int)(rt / n);
+        const int slot = (head + i) % padL;
+        ring[((size_t)b * padL + slot) * D + col] = g[((size_t)b * T + i) * D + col];
     }
 }
 
@@ -871,8 +1035,8 @@ struct grx_conformer {
     float *conv = nullptr, *glu = nullptr, *pos = nullptr;
     int8_t *xq = nullptr, *fq = nullptr, *pos_q = nullptr;  // fq: the rounded SiLU output of W1
     float *xs = nullptr, *fs = nullptr, *pos_s = nullptr;
-    int *valid = nullptr;
-    int *valid_host = nullptr;  // pinned
+    int *valid = nullptr;       // [B] mel frames, then [B] encoder rows of each utterance
+    int *valid_host = nullptr;  // pinned, the same 2B values
     hipGraph_t graph = nullptr;
     hipGraphExec_t exec = nullptr;
 };
@@ -887,7 +1051,7 @@ struct CExpect {
 
 size_t q8b(size_t rows, size_t cols) { return rows * (cols / 32) * 34; }
 
-int sub_F(const grx_conformer_hparams &hp) { return sub_out(sub_out(sub_out(hp.n_mels))); }
+int sub_F(const grx_conformer_hparams &hp) { return stage_len(hp.n_mels, 3, hp.causal_sub); }
 
 // The tensors loadEncoder reads (conformer/model.go:370-422), with sizes.
 std::vector<CExpect> cexpected(const grx_conformer_hparams &hp) {
@@ -1152,11 +1316,12 @@ void free_work(grx_conformer *m) {
     m->B = m->frames = m->T = 0;
 }
 
-// relPosEmb (encoder.go:171-191) of n positions: [2n-1][d].
-std::vector<float> rel_pos(int n, int d) {
-    std::vector<float> out((size_t)(2 * n - 1) * d);
-    for (int i = 0; i < 2 * n - 1; ++i) {
-        const double pos = (double)(n - 1 - i);
+// relPosRange (encoder.go:183-191): count rows for relative positions
+// first, first-1, ...; relPosEmb(n) is first = n-1, count = 2n-1.
+std::vector<float> rel_pos(int first, int count, int d) {
+    std::vector<float> out((size_t)count * d);
+    for (int i = 0; i < count; ++i) {
+        const double pos = (double)(first - i);
         float *row = out.data() + (size_t)i * d;
         for (int j = 0; j < d; j += 2) {
             const float div = (float)std::exp((double)j * -(std::log(10000.0) / (double)d));
@@ -1168,73 +1333,130 @@ std::vector<float> rel_pos(int n, int d) {
     return out;
 }
 
+// offlineKeys (encoder.go:196-212) for T encoder frames.
+AttnKeys offline_keys(const grx_conformer_hparams &hp, int T) {
+    AttnKeys k{};
+    const int al = hp.att_left, ar = hp.att_right;
+    if (hp.att_chunked && al >= 0 && ar >= 0) {
+        k.mode = kKeysChunked;
+        k.chunk = ar + 1;
+        k.lchunks = al / k.chunk;
+        k.bl = k.chunk;
+    } else if (al >= 0 && ar >= 0 && T - 1 > std::min(al, ar)) {
+        k.mode = kKeysWindow;
+        k.left = al;
+        k.right = ar;
+        k.bl = 16;
+    } else {
+        k.mode = kKeysAll;
+        k.bl = kAttnQ;
+    }
+    return k;
+}
+
+// convPadLeft (encoder.go:399-404).
+int pad_left(const grx_conformer_hparams &hp) {
+    return hp.conv_left >= 0 && hp.conv_right >= 0 ? hp.conv_left : (hp.conv_kernel - 1) / 2;
+}
+
+// Which attention kernel runs and its LDS: the staged kernel takes 8 query
+// rows per workgroup for few workgroups, 16 for many; past what LDS holds
+// the unstaged kernel runs.  nk: the most keys a block sees.
+grx_status attn_pick(int B, int heads, int nblk, int bl, int nk, int hd, int *rq, size_t *smem) {
+    *rq = B * heads * nblk * ((bl + 7) / 8) < 1024 ? 8 : 16;
+    if (const char *e = getenv("GRX_CONF_ATTN_RQ")) *rq = atoi(e);  // 0 (unstaged), 8 or 16, for tests
+    if (*rq != 0 && *rq != 8 && *rq != 16) *rq = 8;
+    const size_t sq = hd + 1;
+    const size_t stage = std::max((size_t)(nk + *rq - 1) * sq, (size_t)nk * hd);
+    const size_t staged = ((size_t)2 * *rq * sq + (size_t)2 * *rq * (nk | 1) + 2 * *rq + stage) * 4;
+    const void *fn = *rq == 8 ? (const void *)conf_attn_lds_kernel<8> : (const void *)conf_attn_lds_kernel<16>;
+    if (*rq != 0 && staged <= 160 * 1024 &&
+        (staged <= 64 * 1024 ||
+         hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)staged) == hipSuccess)) {
+        *smem = staged;
+        return GRX_OK;
+    }
+    (void)hipGetLastError();
+    *rq = 0;
+    const size_t np = kAttnQ + nk - 1;
+    const size_t need = ((size_t)2 * kAttnQ * sq + (size_t)kAttnQ * (nk | 1) + (size_t)kAttnQ * (np | 1) + 2 * kAttnQ) * 4;
+    if (need > 160 * 1024 ||
+        (need > 64 * 1024 && hipFuncSetAttribute((const void *)conf_attn_kernel,
+                                                 hipFuncAttributeMaxDynamicSharedMemorySize, (int)need) != hipSuccess))
+        return grx_fail(GRX_ESIZE, "%d keys per query block are more than the attention kernel holds", nk);
+    *smem = need;
+    return GRX_OK;
+}
+
+// Whether the windowed depthwise kernel runs (its LDS granted).
+bool dw_win_ok(const grx_conformer_hparams &hp) {
+    const size_t need = (size_t)(kDwRows + 2 * hp.conv_kernel - 1) * 64 * 4;
+    const bool ok = hp.d % 64 == 0 && !hp.conv_ln && need <= 160 * 1024 &&
+                    (need <= 64 * 1024 || hipFuncSetAttribute((const void *)conf_dwconv_win_kernel,
+                                                              hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                              (int)need) == hipSuccess);
+    (void)hipGetLastError();
+    return ok;
+}
+
+// The working buffers of B utterances of `frames` mel frames whose
+// pre-encoder gives T rows each, Tp kept (the blocks' rows).
+struct CBuf {
+    float *mel = nullptr, *sub0 = nullptr, *suby = nullptr, *subx = nullptr, *x = nullptr, *qkv = nullptr;
+    float *conv = nullptr, *glu = nullptr;
+    int8_t *xq = nullptr, *fq = nullptr;
+    float *xs = nullptr, *fs = nullptr;
+};
+grx_status cbuf_alloc(const grx_conformer *m, std::vector<void *> &w, int B, int frames, int Tp, CBuf *b) {
+    const grx_conformer_hparams &hp = m->hp;
+    const int d = hp.d, c = hp.sub_channels, nm = hp.n_mels, cs = hp.causal_sub;
+    const int T2 = stage_len(frames, 2, cs), F2 = stage_len(nm, 2, cs), T = stage_len(frames, 3, cs),
+              F3 = stage_len(nm, 3, cs);
+    const size_t R = (size_t)B * Tp;
+    grx_status s;
+    if ((s = calloc_t(w, (size_t)B * nm * frames, &b->mel)) != GRX_OK) return s;
+    if ((s = calloc_t(w, (size_t)B * T * F3 * c, &b->sub0)) != GRX_OK) return s;
+    if ((s = calloc_t(w, (size_t)B * T2 * F2 * c, &b->suby)) != GRX_OK) return s;
+    if ((m->w3f || m->w6f) && (s = calloc_t(w, (size_t)B * T2 * F2 * c, &b->subx)) != GRX_OK) return s;
+    // rounded activations: the largest row set of any product
+    const size_t qn = std::max({(size_t)B * T2 * F2 * c, R * (size_t)c * F3, R * (size_t)hp.dff, R * 2 * (size_t)d});
+    if ((s = calloc_t(w, qn, &b->xq)) != GRX_OK) return s;
+    if ((s = calloc_t(w, qn / 32, &b->xs)) != GRX_OK) return s;
+    if ((s = calloc_t(w, R * hp.dff, &b->fq)) != GRX_OK) return s;
+    if ((s = calloc_t(w, R * hp.dff / 32, &b->fs)) != GRX_OK) return s;
+    if ((s = calloc_t(w, R * d, &b->x)) != GRX_OK) return s;
+    if ((s = calloc_t(w, R * 3 * d, &b->qkv)) != GRX_OK) return s;
+    if ((s = calloc_t(w, R * 2 * d, &b->conv)) != GRX_OK) return s;
+    if ((s = calloc_t(w, R * d, &b->glu)) != GRX_OK) return s;
+    return GRX_OK;
+}
+
 // Buffers for B utterances of `frames` mel frames, the position table of
 // their T and its rounding.
 grx_status cshape(grx_conformer *m, int B, int frames) {
     if (m->B == B && m->frames == frames) return GRX_OK;
     free_work(m);
     const grx_conformer_hparams &hp = m->hp;
-    const int d = hp.d, c = hp.sub_channels, nm = hp.n_mels;
-    const int T1 = sub_out(frames), F1 = sub_out(nm), T2 = sub_out(T1), F2 = sub_out(F1), T = sub_out(T2),
-              F3 = sub_out(F2);
-    const size_t R = (size_t)B * T;
-    {  // the attention's LDS: past 64 KiB it has to be asked for.  The staged
-       // kernel takes 8 query rows per workgroup for few utterances, 16 for
-       // many; past what LDS holds the unstaged kernel runs.
-        const int hd = d / hp.heads, nblk = (T + kAttnQ - 1) / kAttnQ;
-        m->attn_rq = B * hp.heads * nblk * (kAttnQ / 8) < 1024 ? 8 : 16;
-        if (const char *e = getenv("GRX_CONF_ATTN_RQ")) m->attn_rq = atoi(e);  // 0 (unstaged), 8 or 16, for tests
-        if (m->attn_rq != 0 && m->attn_rq != 8 && m->attn_rq != 16) m->attn_rq = 8;
-        const size_t staged = attn_lds_smem_floats(T, hd, m->attn_rq) * 4;
-        const void *fn = m->attn_rq == 8 ? (const void *)conf_attn_lds_kernel<8> : (const void *)conf_attn_lds_kernel<16>;
-        if (m->attn_rq != 0 && staged <= 160 * 1024 &&
-            (staged <= 64 * 1024 ||
-             hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)staged) == hipSuccess)) {
-            m->attn_smem = staged;
-        } else {
-            (void)hipGetLastError();
-            m->attn_rq = 0;
-            const size_t need = attn_smem_floats(T, hd) * 4;
-            if (need > 160 * 1024 ||
-                (need > 64 * 1024 && hipFuncSetAttribute((const void *)conf_attn_kernel,
-                                                         hipFuncAttributeMaxDynamicSharedMemorySize,
-                                                         (int)need) != hipSuccess))
-                return grx_fail(GRX_ESIZE, "%d frames give %d encoder frames, more than the attention kernel holds",
-                                frames, T);
-            m->attn_smem = need;
-        }
+    const int d = hp.d, T = stage_len(frames, 3, hp.causal_sub);
+    {
+        const AttnKeys k = offline_keys(hp, T);
+        grx_status s = attn_pick(B, hp.heads, (T + k.bl - 1) / k.bl, k.bl, T, d / hp.heads, &m->attn_rq, &m->attn_smem);
+        if (s != GRX_OK) return s;
     }
-    {  // the windowed depthwise convolution's LDS (frames and taps)
-        const size_t need = (size_t)(kDwRows + 2 * hp.conv_kernel - 1) * 64 * 4;
-        m->dw_win = d % 64 == 0 && !hp.conv_ln && need <= 160 * 1024 &&
-                    (need <= 64 * 1024 || hipFuncSetAttribute((const void *)conf_dwconv_win_kernel,
-                                                              hipFuncAttributeMaxDynamicSharedMemorySize,
-                                                              (int)need) == hipSuccess);
-        (void)hipGetLastError();
-    }
+    m->dw_win = dw_win_ok(hp);
     grx_status s;
     auto &w = m->work;
-    if ((s = calloc_t(w, (size_t)B * nm * frames, &m->mel)) != GRX_OK) return s;
-    if ((s = calloc_t(w, (size_t)B * T * F3 * c, &m->sub0)) != GRX_OK) return s;
-    if ((s = calloc_t(w, (size_t)B * T2 * F2 * c, &m->suby)) != GRX_OK) return s;
-    if ((m->w3f || m->w6f) && (s = calloc_t(w, (size_t)B * T2 * F2 * c, &m->subx)) != GRX_OK) return s;
-    // rounded activations: the largest row set of any product
-    size_t qn = std::max({(size_t)B * T2 * F2 * c, R * (size_t)c * F3, R * (size_t)hp.dff, R * 2 * (size_t)d});
-    if ((s = calloc_t(w, qn, &m->xq)) != GRX_OK) return s;
-    if ((s = calloc_t(w, qn / 32, &m->xs)) != GRX_OK) return s;
-    if ((s = calloc_t(w, R * hp.dff, &m->fq)) != GRX_OK) return s;
-    if ((s = calloc_t(w, R * hp.dff / 32, &m->fs)) != GRX_OK) return s;
-    if ((s = calloc_t(w, R * d, &m->x)) != GRX_OK) return s;
-    if ((s = calloc_t(w, R * 3 * d, &m->qkv)) != GRX_OK) return s;
+    CBuf b;
+    if ((s = cbuf_alloc(m, w, B, frames, T, &b)) != GRX_OK) return s;
+    m->mel = b.mel, m->sub0 = b.sub0, m->suby = b.suby, m->subx = b.subx, m->x = b.x, m->qkv = b.qkv;
+    m->conv = b.conv, m->glu = b.glu, m->xq = b.xq, m->xs = b.xs, m->fq = b.fq, m->fs = b.fs;
     if ((s = calloc_t(w, (size_t)(2 * T - 1) * hp.layers * d, &m->pp)) != GRX_OK) return s;
-    if ((s = calloc_t(w, R * 2 * d, &m->conv)) != GRX_OK) return s;
-    if ((s = calloc_t(w, R * d, &m->glu)) != GRX_OK) return s;
     if ((s = calloc_t(w, (size_t)(2 * T - 1) * d, &m->pos)) != GRX_OK) return s;
     if ((s = calloc_t(w, (size_t)(2 * T - 1) * d, &m->pos_q)) != GRX_OK) return s;
     if ((s = calloc_t(w, (size_t)(2 * T - 1) * d / 32, &m->pos_s)) != GRX_OK) return s;
-    if ((s = calloc_t(w, B, &m->valid)) != GRX_OK) return s;
-    GRX_HIP(hipHostMalloc((void **)&m->valid_host, (size_t)B * sizeof(int), hipHostMallocDefault));
-    std::vector<float> pos = rel_pos(T, d);
+    if ((s = calloc_t(w, 2 * (size_t)B, &m->valid)) != GRX_OK) return s;
+    GRX_HIP(hipHostMalloc((void **)&m->valid_host, 2 * (size_t)B * sizeof(int), hipHostMallocDefault));
+    std::vector<float> pos = rel_pos(T - 1, 2 * T - 1, d);
     GRX_HIP(hipMemcpy(m->pos, pos.data(), pos.size() * 4, hipMemcpyHostToDevice));
     if ((s = grx_quant_act_dev(m->ctx, m->pos_q, m->pos_s, m->pos, d, 2 * T - 1, d)) != GRX_OK) return s;
     GRX_HIP(hipStreamSynchronize(m->ctx->stream));
@@ -1262,133 +1484,189 @@ grx_status pw_f32(hipStream_t st, const float *x, const float *w, const float *b
     return GRX_OK;
 }
 
-// The whole encode (encoder.go:432-489) of m->B utterances from m->mel into
-// m->x, enqueued on the stream.
-grx_status enqueue_encode(grx_conformer *m, hipStream_t st) {
+// One run of the encoder over B utterances (or streams' chunks): the
+// pre-encoder on `frames` mel frames (T rows each, the first `drop` cut,
+// Tp kept), xscale, then every block.
+struct CRun {
+    int B, frames, T, Tp, drop;
+    CBuf b;
+    const int *valid, *lens;  // device: mel frames and encoder rows per utterance
+    // the attention: key form, position rows, kernel
+    AttnKeys keys;
+    const float *pp;
+    int maxfirst;
+    const int *ctl;  // streaming: c, ring heads (device); null offline
+    int attn_rq;
+    size_t attn_smem;
+    bool dw_win;
+    // streaming caches per layer (null offline)
+    float *kv_ring;
+    size_t kv_ring_layer;
+    int cap;
+    float *conv_ring;
+    size_t conv_ring_layer;
+};
+
+grx_status enqueue_run(grx_conformer *m, const CRun &r, hipStream_t st) {
     const grx_conformer_hparams &hp = m->hp;
-    const int B = m->B, frames = m->frames, d = hp.d, c = hp.sub_channels, nm = hp.n_mels, T = m->T;
-    const int T1 = sub_out(frames), F1 = sub_out(nm), T2 = sub_out(T1), F2 = sub_out(F1), F3 = sub_out(F2);
-    const int R = B * T, hd = d / hp.heads;
+    const int B = r.B, frames = r.frames, d = hp.d, c = hp.sub_channels, nm = hp.n_mels, T = r.T, Tp = r.Tp;
+    const int cs = hp.causal_sub, padL = pad_left(hp);
+    const int T1 = stage_len(frames, 1, cs), F1 = stage_len(nm, 1, cs), T2 = stage_len(frames, 2, cs),
+              F2 = stage_len(nm, 2, cs), F3 = stage_len(nm, 3, cs);
+    const int R = B * Tp, hd = d / hp.heads;
+    const CBuf &bf = r.b;
     grx_status s;
     // pre-encoder (encoder.go:123-167)
-    sub_conv01_kernel<<<B * T2, c, (size_t)7 * (4 * F2 + 3) * 4, st>>>(
-        m->mel, frames, nm, m->valid, m->w0, m->b0, m->w2, m->b2, c, T1, F1, T2, F2, m->xq, m->xs, m->w3f ? m->subx : nullptr);
+    sub_conv01_kernel<<<B * T2, c, (size_t)7 * (4 * F2 + 3) * 4, st>>>(bf.mel, frames, nm, r.valid, cs, m->w0, m->b0,
+                                                                      m->w2, m->b2, c, T1, F1, T2, F2, bf.xq, bf.xs,
+                                                                      m->w3f ? bf.subx : nullptr);
     GRX_LAUNCHED("sub_conv01_kernel");
     if (m->w3f) {
-        if ((s = pw_f32(st, m->subx, m->w3f, m->b3, m->suby, B, T2 * F2, c)) != GRX_OK) return s;
-    } else if ((s = grx_gemm_q8_launch(st, m->w3, m->xq, m->xs, B * T2 * F2, m->b3, m->suby, c)) != GRX_OK) {
+        if ((s = pw_f32(st, bf.subx, m->w3f, m->b3, bf.suby, B, T2 * F2, c)) != GRX_OK) return s;
+    } else if ((s = grx_gemm_q8_launch(st, m->w3, bf.xq, bf.xs, B * T2 * F2, m->b3, bf.suby, c)) != GRX_OK) {
         return s;
     }
-    sub_dwconv_kernel<true><<<B * T * F3, c, 0, st>>>(m->suby, T2, F2, c, m->valid, 3, m->w5, m->b5, T, F3, m->xq,
-                                                      m->xs, m->w6f ? m->subx : nullptr);
+    sub_dwconv_kernel<true><<<B * T * F3, c, 0, st>>>(bf.suby, T2, F2, c, r.valid, cs, 3, m->w5, m->b5, T, F3, bf.xq,
+                                                      bf.xs, m->w6f ? bf.subx : nullptr);
     GRX_LAUNCHED("sub_dwconv_kernel");
     if (m->w6f) {
-        if ((s = pw_f32(st, m->subx, m->w6f, m->b6, m->sub0, B, T * F3, c)) != GRX_OK) return s;
-    } else if ((s = grx_gemm_q8_launch(st, m->w6, m->xq, m->xs, B * T * F3, m->b6, m->sub0, c)) != GRX_OK) {
+        if ((s = pw_f32(st, bf.subx, m->w6f, m->b6, bf.sub0, B, T * F3, c)) != GRX_OK) return s;
+    } else if ((s = grx_gemm_q8_launch(st, m->w6, bf.xq, bf.xs, B * T * F3, m->b6, bf.sub0, c)) != GRX_OK) {
         return s;
     }
-    sub_flatten_kernel<<<R, 256, 0, st>>>(m->sub0, T, F3, c, m->valid, m->xq, m->xs);
+    sub_flatten_kernel<<<R, 256, 0, st>>>(bf.sub0, T, F3, c, r.valid, cs, r.drop, Tp, bf.xq, bf.xs);
     GRX_LAUNCHED("sub_flatten_kernel");
-    {  // output Linear, then xscale (encoder.go:445-451)
+    {  // output Linear, then xscale (encoder.go:445-451; stream.go:259)
         GemmOut o;
-        o.y = m->x;
+        o.y = bf.x;
         o.ldc = d;
         if (hp.xscaling) {
             o.epi = GRX_GEMM_SCALE;
             o.scale = (float)std::sqrt((double)d);
         }
-        if ((s = grx_gemm_q8_launch_ex(st, m->wout, m->xq, m->xs, R, m->outb, o)) != GRX_OK) return s;
+        if ((s = grx_gemm_q8_launch_ex(st, m->wout, bf.xq, bf.xs, R, m->outb, o)) != GRX_OK) return s;
     }
-    // every block's position projection at once: pp [2T-1][layers*d]
-    if ((s = grx_gemm_q8_launch(st, m->pos_all, m->pos_q, m->pos_s, 2 * T - 1, nullptr, m->pp, hp.layers * d)) !=
-        GRX_OK)
-        return s;
     const size_t row_smem = (size_t)d * 4;
     // the first block's feed-forward LayerNorm
-    ln_rows_kernel<false, true><<<R, kRowThreads, row_smem, st>>>(m->x, d, m->blk[0].ff1.norm_w, m->blk[0].ff1.norm_b,
-                                                                  nullptr, nullptr, m->xq, m->xs);
+    ln_rows_kernel<false, true><<<R, kRowThreads, row_smem, st>>>(bf.x, d, m->blk[0].ff1.norm_w, m->blk[0].ff1.norm_b,
+                                                                  nullptr, nullptr, bf.xq, bf.xs);
     GRX_LAUNCHED("ln_rows_kernel");
-    const size_t attn_smem = m->attn_smem;
     const float scale = (float)(1.0 / std::sqrt((double)hd));
-    const int nblk = (T + kAttnQ - 1) / kAttnQ;
+    const int nblk = (Tp + r.keys.bl - 1) / r.keys.bl;
     for (int i = 0; i < hp.layers; ++i) {
         const CBlock &Bk = m->blk[i];
         auto ff_pair = [&](const CFF &F) -> grx_status {
             // x += 0.5 * W2 . SiLU(W1 . LN(x)) (encoder.go:244-251); LN(x) is in xq
             GemmOut o1;
             o1.epi = GRX_GEMM_SILU_Q;
-            o1.yq = m->fq;
-            o1.ys = m->fs;
-            grx_status r = grx_gemm_q8_launch_ex(st, F.w1, m->xq, m->xs, R, F.b1, o1);
-            if (r != GRX_OK) return r;
+            o1.yq = bf.fq;
+            o1.ys = bf.fs;
+            grx_status q = grx_gemm_q8_launch_ex(st, F.w1, bf.xq, bf.xs, R, F.b1, o1);
+            if (q != GRX_OK) return q;
             GemmOut o2;
-            o2.y = m->x;
+            o2.y = bf.x;
             o2.ldc = d;
             o2.epi = GRX_GEMM_AXPY_HALF;
-            return grx_gemm_q8_launch_ex(st, F.w2, m->fq, m->fs, R, F.b2, o2);
+            return grx_gemm_q8_launch_ex(st, F.w2, bf.fq, bf.fs, R, F.b2, o2);
         };
         if ((s = ff_pair(Bk.ff1)) != GRX_OK) return s;
         // attention (encoder.go:259-330)
-        ln_rows_kernel<false, true><<<R, kRowThreads, row_smem, st>>>(m->x, d, Bk.norm_attn_w, Bk.norm_attn_b, nullptr,
-                                                                      nullptr, m->xq, m->xs);
+        ln_rows_kernel<false, true><<<R, kRowThreads, row_smem, st>>>(bf.x, d, Bk.norm_attn_w, Bk.norm_attn_b, nullptr,
+                                                                      nullptr, bf.xq, bf.xs);
         GRX_LAUNCHED("ln_rows_kernel");
-        if ((s = grx_gemm_q8_launch(st, Bk.qkv, m->xq, m->xs, R, Bk.qkv_b, m->qkv, 3 * d)) != GRX_OK) return s;
-        if (m->attn_rq == 8)
-            conf_attn_lds_kernel<8><<<dim3(nblk * (kAttnQ / 8), hp.heads, B), kAttnLdsThreads, attn_smem, st>>>(
-                m->qkv, m->pp + (size_t)i * d, hp.layers * d, Bk.pos_u, Bk.pos_v, m->valid, T, d, hd, scale, m->xq,
-                m->xs);
-        else if (m->attn_rq == 16)
-            conf_attn_lds_kernel<16><<<dim3(nblk * (kAttnQ / 16), hp.heads, B), kAttnLdsThreads, attn_smem, st>>>(
-                m->qkv, m->pp + (size_t)i * d, hp.layers * d, Bk.pos_u, Bk.pos_v, m->valid, T, d, hd, scale, m->xq,
-                m->xs);
+        if ((s = grx_gemm_q8_launch(st, Bk.qkv, bf.xq, bf.xs, R, Bk.qkv_b, bf.qkv, 3 * d)) != GRX_OK) return s;
+        AttnIO io{};
+        io.q = bf.qkv;
+        io.ldq = 3 * d;
+        io.lens = r.lens;
+        io.T = Tp;
+        if (r.kv_ring) {
+            // the chunk's keys and values join the stream's ring, which then
+            // holds every key of the chunk's queries
+            float *ring = r.kv_ring + r.kv_ring_layer * i;
+            kv_ring_append_kernel<<<grid_for((size_t)R * 2 * d), 256, 0, st>>>(bf.qkv, B, Tp, d, ring, r.cap, r.ctl);
+            GRX_LAUNCHED("kv_ring_append_kernel");
+            io.kv = ring;
+            io.ldkv = 2 * d;
+            io.vo = d;
+            io.kvb = (size_t)2 * r.cap * 2 * d;
+            io.pp = r.pp + (size_t)i * d;
+            io.ldp = hp.layers * d;
+            io.maxfirst = r.maxfirst;
+            io.ctl = r.ctl;
+        } else {
+            io.kv = bf.qkv + d;
+            io.ldkv = 3 * d;
+            io.vo = d;
+            io.kvb = (size_t)Tp * 3 * d;
+            io.pp = r.pp + (size_t)i * d;
+            io.ldp = hp.layers * d;
+        }
+        if (r.attn_rq == 8)
+            conf_attn_lds_kernel<8><<<dim3(nblk * ((r.keys.bl + 7) / 8), hp.heads, B), kAttnLdsThreads, r.attn_smem,
+                                      st>>>(io, r.keys, Bk.pos_u, Bk.pos_v, d, hd, scale, bf.xq, bf.xs);
+        else if (r.attn_rq == 16)
+            conf_attn_lds_kernel<16><<<dim3(nblk * ((r.keys.bl + 15) / 16), hp.heads, B), kAttnLdsThreads,
+                                       r.attn_smem, st>>>(io, r.keys, Bk.pos_u, Bk.pos_v, d, hd, scale, bf.xq, bf.xs);
         else
-            conf_attn_kernel<<<dim3(nblk, hp.heads, B), kAttnThreads, attn_smem, st>>>(
-                m->qkv, m->pp + (size_t)i * d, hp.layers * d, Bk.pos_u, Bk.pos_v, m->valid, T, d, hd, scale, m->xq,
-                m->xs);
+            conf_attn_kernel<<<dim3(nblk, hp.heads, B), kAttnThreads, r.attn_smem, st>>>(io, r.keys, Bk.pos_u,
+                                                                                         Bk.pos_v, d, hd, scale,
+                                                                                         bf.xq, bf.xs);
         GRX_LAUNCHED("conf_attn_kernel");
         {
             GemmOut o;
-            o.y = m->x;
+            o.y = bf.x;
             o.ldc = d;
             o.epi = GRX_GEMM_ADD;
-            if ((s = grx_gemm_q8_launch_ex(st, Bk.out, m->xq, m->xs, R, Bk.out_b, o)) != GRX_OK) return s;
+            if ((s = grx_gemm_q8_launch_ex(st, Bk.out, bf.xq, bf.xs, R, Bk.out_b, o)) != GRX_OK) return s;
         }
         // convolution module (encoder.go:343-397)
-        ln_rows_kernel<false, true><<<R, kRowThreads, row_smem, st>>>(m->x, d, Bk.norm_conv_w, Bk.norm_conv_b, nullptr,
-                                                                      nullptr, m->xq, m->xs);
+        ln_rows_kernel<false, true><<<R, kRowThreads, row_smem, st>>>(bf.x, d, Bk.norm_conv_w, Bk.norm_conv_b, nullptr,
+                                                                      nullptr, bf.xq, bf.xs);
         GRX_LAUNCHED("ln_rows_kernel");
-        if ((s = grx_gemm_q8_launch(st, Bk.pw1, m->xq, m->xs, R, Bk.pw1_b, m->conv, 2 * d)) != GRX_OK) return s;
-        conf_glu_kernel<<<grid_for((size_t)R * d), 256, 0, st>>>(m->conv, R, T, d, m->valid, m->glu);
+        if ((s = grx_gemm_q8_launch(st, Bk.pw1, bf.xq, bf.xs, R, Bk.pw1_b, bf.conv, 2 * d)) != GRX_OK) return s;
+        conf_glu_kernel<<<grid_for((size_t)R * d), 256, 0, st>>>(bf.conv, R, Tp, d, r.lens, bf.glu);
         GRX_LAUNCHED("conf_glu_kernel");
+        ConvPrev cp{};
+        if (r.conv_ring && padL > 0) {
+            cp.ring = r.conv_ring + r.conv_ring_layer * i;
+            cp.ctl = r.ctl;
+        }
         if (hp.conv_ln)
-            conf_dwconv_kernel<true><<<R, kRowThreads, row_smem, st>>>(m->glu, T, d, hp.conv_kernel, Bk.dw, Bk.dw_b,
-                                                                       Bk.cn_w, Bk.cn_b, m->xq, m->xs);
-        else if (m->dw_win)
-            conf_dwconv_win_kernel<<<dim3((T + kDwRows - 1) / kDwRows, d / 64, B), 256,
+            conf_dwconv_kernel<true><<<R, kRowThreads, row_smem, st>>>(bf.glu, Tp, d, hp.conv_kernel, padL, cp, Bk.dw,
+                                                                       Bk.dw_b, Bk.cn_w, Bk.cn_b, bf.xq, bf.xs);
+        else if (r.dw_win)
+            conf_dwconv_win_kernel<<<dim3((Tp + kDwRows - 1) / kDwRows, d / 64, B), 256,
                                      (size_t)(kDwRows + 2 * hp.conv_kernel - 1) * 64 * 4, st>>>(
-                m->glu, T, d, hp.conv_kernel, Bk.dw, Bk.dw_b, Bk.cn_w, Bk.cn_b, m->xq, m->xs);
+                bf.glu, Tp, d, hp.conv_kernel, padL, cp, Bk.dw, Bk.dw_b, Bk.cn_w, Bk.cn_b, bf.xq, bf.xs);
         else
-            conf_dwconv_kernel<false><<<R, kRowThreads, row_smem, st>>>(m->glu, T, d, hp.conv_kernel, Bk.dw, Bk.dw_b,
-                                                                        Bk.cn_w, Bk.cn_b, m->xq, m->xs);
+            conf_dwconv_kernel<false><<<R, kRowThreads, row_smem, st>>>(bf.glu, Tp, d, hp.conv_kernel, padL, cp,
+                                                                        Bk.dw, Bk.dw_b, Bk.cn_w, Bk.cn_b, bf.xq,
+                                                                        bf.xs);
         GRX_LAUNCHED("conf_dwconv_kernel");
+        if (cp.ring) {  // after the convolution has read the frames they replace
+            conv_ring_append_kernel<<<grid_for((size_t)B * std::min(Tp, padL) * d), 256, 0, st>>>(
+                bf.glu, B, Tp, d, const_cast<float *>(cp.ring), padL, r.ctl);
+            GRX_LAUNCHED("conv_ring_append_kernel");
+        }
         {
             GemmOut o;
-            o.y = m->x;
+            o.y = bf.x;
             o.ldc = d;
             o.epi = GRX_GEMM_ADD;
-            if ((s = grx_gemm_q8_launch_ex(st, Bk.pw2, m->xq, m->xs, R, Bk.pw2_b, o)) != GRX_OK) return s;
+            if ((s = grx_gemm_q8_launch_ex(st, Bk.pw2, bf.xq, bf.xs, R, Bk.pw2_b, o)) != GRX_OK) return s;
         }
         // second feed-forward, then norm_out (and the next block's first LayerNorm)
-        ln_rows_kernel<false, true><<<R, kRowThreads, row_smem, st>>>(m->x, d, Bk.ff2.norm_w, Bk.ff2.norm_b, nullptr,
-                                                                      nullptr, m->xq, m->xs);
+        ln_rows_kernel<false, true><<<R, kRowThreads, row_smem, st>>>(bf.x, d, Bk.ff2.norm_w, Bk.ff2.norm_b, nullptr,
+                                                                      nullptr, bf.xq, bf.xs);
         GRX_LAUNCHED("ln_rows_kernel");
         if ((s = ff_pair(Bk.ff2)) != GRX_OK) return s;
         if (i + 1 < hp.layers) {
             const CFF &N = m->blk[i + 1].ff1;
-            ln_rows_kernel<true, true><<<R, kRowThreads, row_smem, st>>>(m->x, d, Bk.norm_out_w, Bk.norm_out_b,
-                                                                         N.norm_w, N.norm_b, m->xq, m->xs);
+            ln_rows_kernel<true, true><<<R, kRowThreads, row_smem, st>>>(bf.x, d, Bk.norm_out_w, Bk.norm_out_b,
+                                                                         N.norm_w, N.norm_b, bf.xq, bf.xs);
         } else {
-            ln_rows_kernel<true, false><<<R, kRowThreads, row_smem, st>>>(m->x, d, Bk.norm_out_w, Bk.norm_out_b,
+            ln_rows_kernel<true, false><<<R, kRowThreads, row_smem, st>>>(bf.x, d, Bk.norm_out_w, Bk.norm_out_b,
                                                                           nullptr, nullptr, nullptr, nullptr);
         }
         GRX_LAUNCHED("ln_rows_kernel");
@@ -1396,13 +1674,37 @@ grx_status enqueue_encode(grx_conformer *m, hipStream_t st) {
     return GRX_OK;
 }
 
-grx_status run_encode(grx_conformer *m) {
-    hipStream_t st = m->ctx->stream;
+// The whole offline encode (encoder.go:432-489) of m->B utterances from
+// m->mel into m->x, enqueued on the stream: every block's position
+// projection first (pp [2T-1][layers*d]), then the run.
+grx_status enqueue_encode(grx_conformer *m, hipStream_t st) {
+    const grx_conformer_hparams &hp = m->hp;
+    const int T = m->T;
+    grx_status s = grx_gemm_q8_launch(st, m->pos_all, m->pos_q, m->pos_s, 2 * T - 1, nullptr, m->pp, hp.layers * hp.d);
+    if (s != GRX_OK) return s;
+    CRun r{};
+    r.B = m->B;
+    r.frames = m->frames;
+    r.T = r.Tp = T;
+    r.b.mel = m->mel, r.b.sub0 = m->sub0, r.b.suby = m->suby, r.b.subx = m->subx, r.b.x = m->x, r.b.qkv = m->qkv;
+    r.b.conv = m->conv, r.b.glu = m->glu, r.b.xq = m->xq, r.b.xs = m->xs, r.b.fq = m->fq, r.b.fs = m->fs;
+    r.valid = m->valid;
+    r.lens = m->valid + m->B;
+    r.keys = offline_keys(hp, T);
+    r.pp = m->pp;
+    r.attn_rq = m->attn_rq;
+    r.attn_smem = m->attn_smem;
+    r.dw_win = m->dw_win;
+    return enqueue_run(m, r, st);
+}
+
+grx_status run_graph(hipStream_t st, hipGraph_t *graph, hipGraphExec_t *exec,
+                     const std::function<grx_status(hipStream_t)> &enqueue) {
     static const bool no_graph = getenv("GRX_NO_GRAPH") != nullptr;
-    if (no_graph) return enqueue_encode(m, st);
-    if (!m->exec) {
+    if (no_graph) return enqueue(st);
+    if (!*exec) {
         GRX_HIP(hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal));
-        grx_status s = enqueue_encode(m, st);
+        grx_status s = enqueue(st);
         hipGraph_t g = nullptr;
         hipError_t e = hipStreamEndCapture(st, &g);
         if (s != GRX_OK) {
@@ -1410,11 +1712,15 @@ grx_status run_encode(grx_conformer *m) {
             return s;
         }
         if (e != hipSuccess) return grx_fail(GRX_EDEVICE, "graph capture: %s", hipGetErrorString(e));
-        m->graph = g;
-        GRX_HIP(hipGraphInstantiate(&m->exec, g, nullptr, nullptr, 0));
+        *graph = g;
+        GRX_HIP(hipGraphInstantiate(exec, g, nullptr, nullptr, 0));
     }
-    GRX_HIP(hipGraphLaunch(m->exec, st));
+    GRX_HIP(hipGraphLaunch(*exec, st));
     return GRX_OK;
+}
+
+grx_status run_encode(grx_conformer *m) {
+    return run_graph(m->ctx->stream, &m->graph, &m->exec, [m](hipStream_t st) { return enqueue_encode(m, st); });
 }
 
 grx_status check_valid(const grx_conformer *m, const int *valid, int batch, int frames) {
@@ -1425,7 +1731,306 @@ grx_status check_valid(const grx_conformer *m, const int *valid, int batch, int 
     return GRX_OK;
 }
 
+// The encoder rows of an utterance of `valid` frames out of T (encoder.go:166).
+int enc_rows(const grx_conformer_hparams &hp, int valid, int T) {
+    return std::max(0, std::min(stage_len(valid, 3, hp.causal_sub), T));
+}
+
+grx_status encode_common(grx_conformer *m, const float *mel, int batch, int frames, const int *valid,
+                         hipMemcpyKind kind) {
+    grx_status s;
+    if ((s = check_valid(m, valid, batch, frames)) != GRX_OK) return s;
+    GRX_HIP(hipSetDevice(m->ctx->device));
+    if ((s = cfinalize(m)) != GRX_OK) return s;
+    if ((s = cshape(m, batch, frames)) != GRX_OK) return s;
+    hipStream_t st = m->ctx->stream;
+    const size_t mel_n = (size_t)batch * m->hp.n_mels * frames;
+    for (int b = 0; b < batch; ++b) {
+        m->valid_host[b] = valid[b];
+        m->valid_host[batch + b] = enc_rows(m->hp, valid[b], m->T);
+    }
+    GRX_HIP(hipMemcpyAsync(m->valid, m->valid_host, 2 * (size_t)batch * sizeof(int), hipMemcpyHostToDevice, st));
+    GRX_HIP(hipMemcpyAsync(m->mel, mel, mel_n * 4, kind, st));
+    return run_encode(m);
+}
+
 }  // namespace
+
+// ---------------------------------------------------------------- streams
+
+struct grx_conformer_stream {
+    grx_conformer *m = nullptr;
+    int B = 0;
+    grx_conformer_stream_geom g{};
+    int cap = 0, padL = 0, maxfirst = 0;
+    bool dw_win = false;
+    int steps = 0;                          // chunks done
+    int kv_len = 0, kv_head = 0, conv_head = 0;
+    std::vector<void *> allocs;
+    float *kv_ring = nullptr;    // [layers][B][2*cap][2d]: keys | values
+    float *conv_ring = nullptr;  // [layers][B][padL][d]
+    float *pp = nullptr;         // [left+2*chunk-1][layers*d]: positions maxfirst down, projected
+    int *ctl = nullptr;          // device [4 + 2B]: c, kv head, conv head, 0, mel frames[B], rows[B]
+    int *ctl_host = nullptr;     // pinned
+    // working buffers, for chunks of up to buf_frames mel frames
+    int buf_frames = 0;
+    std::vector<void *> work;
+    CBuf b;
+    struct Shape {
+        hipGraph_t graph = nullptr;
+        hipGraphExec_t exec = nullptr;
+        int attn_rq = 0;
+        size_t attn_smem = 0;
+    };
+    std::map<std::pair<int, int>, Shape> shapes;  // by (frames, first)
+};
+
+namespace {
+
+void stream_free_work(grx_conformer_stream *s) {
+    for (auto &kv : s->shapes) {
+        if (kv.second.exec) (void)hipGraphExecDestroy(kv.second.exec);
+        if (kv.second.graph) (void)hipGraphDestroy(kv.second.graph);
+    }
+    s->shapes.clear();
+    for (void *p : s->work) (void)hipFree(p);
+    s->work.clear();
+    s->b = CBuf();
+    s->buf_frames = 0;
+}
+
+// newGeom (stream.go:23-69).
+grx_status stream_geom(const grx_conformer_hparams &hp, int right, grx_conformer_stream_geom *g) {
+    if (!hp.att_chunked) return grx_fail(GRX_EINVAL, "conformer: this model can't stream");
+    int left = -1;
+    for (int i = 0; i < hp.n_context_choices; ++i)
+        if (hp.context_choices[i][1] == right) left = hp.context_choices[i][0];
+    if (hp.n_context_choices == 0 && right == hp.att_right) left = hp.att_left;
+    if (left < 0 || right < 0)
+        return grx_fail(GRX_EINVAL, "conformer: the model wasn't trained for a right context of %d", right);
+    const int sub = 8;
+    const int cache = hp.pre_encode_cache < 0 ? sub + 1 : hp.pre_encode_cache;
+    const int drop = hp.drop_extra < 0 ? 1 + (cache - 1) / sub : hp.drop_extra;
+    const int first = hp.sampling_frames_first < 0 ? 1 : hp.sampling_frames_first;
+    g->right = right;
+    g->chunk = right + 1;
+    g->left = left;
+    g->left_chunks = left / g->chunk;
+    g->mel_first = first + sub * right;
+    g->mel_next = sub * g->chunk;
+    g->mel_cache = cache;
+    g->drop = drop;
+    g->sample_first = first;
+    return GRX_OK;
+}
+
+grx_status stream_bufs(grx_conformer_stream *s, int frames) {
+    if (frames <= s->buf_frames) return GRX_OK;
+    stream_free_work(s);
+    const int T = stage_len(frames, 3, s->m->hp.causal_sub);
+    grx_status r = cbuf_alloc(s->m, s->work, s->B, frames, T, &s->b);
+    if (r != GRX_OK) return r;
+    s->buf_frames = frames;
+    return GRX_OK;
+}
+
+// One chunk: the pre-encoder over it, its first rows dropped unless it is
+// the stream's first, then the blocks with the caches (stream.go:249-307).
+grx_status stream_run(grx_conformer_stream *s, const float *mel, int nf, const int *length, hipMemcpyKind kind,
+                      int *Tp_out) {
+    grx_conformer *m = s->m;
+    const grx_conformer_hparams &hp = m->hp;
+    const int B = s->B, first = s->steps == 0;
+    const int T = stage_len(nf, 3, hp.causal_sub), drop = first ? 0 : std::min(s->g.drop, T);
+    const int Tp = T - drop;
+    *Tp_out = Tp;
+    if (Tp <= 0) return GRX_OK;  // stream.go:262-264: no rows, nothing changes
+    if (Tp > s->g.chunk)
+        return grx_fail(GRX_ESIZE, "a chunk of %d mel frames gives %d encoder rows, more than the stream's %d", nf, Tp,
+                        s->g.chunk);
+    grx_status r;
+    if ((r = stream_bufs(s, nf)) != GRX_OK) return r;
+    auto key = std::make_pair(nf, first);
+    auto it = s->shapes.find(key);
+    if (it == s->shapes.end()) {
+        grx_conformer_stream::Shape sh;
+        // LDS for the most keys a chunk's queries see: the full left
+        // context and the chunk's own rows
+        if ((r = attn_pick(B, hp.heads, 1, Tp, s->g.left + Tp, hp.d / hp.heads, &sh.attn_rq, &sh.attn_smem)) !=
+            GRX_OK)
+            return r;
+        it = s->shapes.emplace(key, sh).first;
+    }
+    hipStream_t st = m->ctx->stream;
+    s->ctl_host[0] = s->kv_len;
+    s->ctl_host[1] = s->kv_head;
+    s->ctl_host[2] = s->conv_head;
+    s->ctl_host[3] = 0;
+    for (int b = 0; b < B; ++b) {
+        int L = stage_len(length[b], 3, hp.causal_sub);  // subsample's L, then the drop (stream.go:253-260)
+        L = std::max(0, std::min(L, T));
+        L = std::max(0, L - drop);
+        s->ctl_host[4 + b] = length[b];
+        s->ctl_host[4 + B + b] = std::min(L, Tp);
+    }
+    GRX_HIP(hipMemcpyAsync(s->ctl, s->ctl_host, (size_t)(4 + 2 * B) * sizeof(int), hipMemcpyHostToDevice, st));
+    GRX_HIP(hipMemcpyAsync(s->b.mel, mel, (size_t)B * hp.n_mels * nf * 4, kind, st));
+    grx_conformer_stream::Shape &sh = it->second;
+    CRun run{};
+    run.B = B;
+    run.frames = nf;
+    run.T = T;
+    run.Tp = Tp;
+    run.drop = drop;
+    run.b = s->b;
+    run.valid = s->ctl + 4;
+    run.lens = s->ctl + 4 + B;
+    run.keys.mode = kKeysStream;
+    run.keys.bl = Tp;  // stream.go:272: one block of the chunk's rows
+    run.keys.chunk = s->g.chunk;
+    run.keys.lchunks = s->g.left_chunks;
+    run.keys.left = s->g.left;
+    run.pp = s->pp;
+    run.maxfirst = s->maxfirst;
+    run.ctl = s->ctl;
+    run.attn_rq = sh.attn_rq;
+    run.attn_smem = sh.attn_smem;
+    run.dw_win = s->dw_win;
+    run.kv_ring = s->kv_ring;
+    run.kv_ring_layer = (size_t)B * 2 * s->cap * 2 * hp.d;
+    run.cap = s->cap;
+    run.conv_ring = s->padL > 0 ? s->conv_ring : nullptr;
+    run.conv_ring_layer = (size_t)B * s->padL * hp.d;
+    if ((r = run_graph(st, &sh.graph, &sh.exec, [m, run](hipStream_t q) { return enqueue_run(m, run, q); })) != GRX_OK)
+        return r;
+    // the caches after the chunk (stream.go:296-306)
+    const int Tk = s->kv_len + Tp, keep = std::min(Tk, s->g.left);
+    s->kv_head = (s->kv_head + Tk - keep) % s->cap;
+    s->kv_len = keep;
+    if (s->padL > 0) s->conv_head = (s->conv_head + Tp) % s->padL;
+    s->steps++;
+    return GRX_OK;
+}
+
+grx_status stream_step(grx_conformer_stream *s, const float *mel, int nf, const int *length, float *out, int *lens,
+                       hipMemcpyKind in, hipMemcpyKind outk) {
+    if (!s || !mel || !length || !out) return grx_fail(GRX_EINVAL, "grx_conformer_stream_step: NULL argument");
+    if (nf < 1) return grx_fail(GRX_EINVAL, "grx_conformer_stream_step: %d frames", nf);
+    for (int b = 0; b < s->B; ++b)
+        if (length[b] < 1 || length[b] > nf)
+            return grx_fail(GRX_EINVAL, "stream %d: length %d outside [1, %d]", b, length[b], nf);
+    GRX_HIP(hipSetDevice(s->m->ctx->device));
+    int Tp = 0;
+    grx_status r = stream_run(s, mel, nf, length, in, &Tp);
+    if (r != GRX_OK) return r;
+    const int d = s->m->hp.d, B = s->B, chunk = s->g.chunk;
+    hipStream_t st = s->m->ctx->stream;
+    if (Tp > 0) {
+        GRX_HIP(hipMemcpy2DAsync(out, (size_t)chunk * d * 4, s->b.x, (size_t)Tp * d * 4, (size_t)Tp * d * 4, B, outk,
+                                 st));
+    }
+    // the pinned control values are read by the copy above: wait before reuse
+    GRX_HIP(hipStreamSynchronize(st));
+    if (lens)
+        for (int b = 0; b < B; ++b) lens[b] = Tp > 0 ? s->ctl_host[4 + B + b] : 0;
+    return GRX_OK;
+}
+
+}  // namespace
+
+extern "C" grx_status grx_conformer_stream_create(grx_conformer *m, int right, int batch, grx_conformer_stream **out) {
+    if (!m || !out) return grx_fail(GRX_EINVAL, "grx_conformer_stream_create: NULL argument");
+    *out = nullptr;
+    if (batch < 1 || batch > 4096) return grx_fail(GRX_EINVAL, "grx_conformer_stream_create: batch %d", batch);
+    grx_conformer_stream_geom g;
+    grx_status r;
+    if ((r = stream_geom(m->hp, right, &g)) != GRX_OK) return r;
+    if (g.chunk > kAttnQ)
+        return grx_fail(GRX_ESIZE, "a chunk of %d rows is more than the attention kernels take (%d)", g.chunk, kAttnQ);
+    GRX_HIP(hipSetDevice(m->ctx->device));
+    if ((r = cfinalize(m)) != GRX_OK) return r;
+    const grx_conformer_hparams &hp = m->hp;
+    grx_conformer_stream *s = new grx_conformer_stream();
+    s->m = m;
+    s->B = batch;
+    s->g = g;
+    s->cap = g.left + g.chunk;
+    s->padL = pad_left(hp);
+    s->maxfirst = g.left + g.chunk - 1;
+    s->dw_win = dw_win_ok(hp);
+    auto fail = [&](grx_status e) {
+        grx_conformer_stream_destroy(s);
+        return e;
+    };
+    const int d = hp.d, count = g.left + 2 * g.chunk - 1;
+    if ((r = calloc_t(s->allocs, (size_t)hp.layers * batch * 2 * s->cap * 2 * d, &s->kv_ring)) != GRX_OK) return fail(r);
+    if ((r = calloc_t(s->allocs, (size_t)hp.layers * batch * std::max(s->padL, 1) * d, &s->conv_ring)) != GRX_OK)
+        return fail(r);
+    if ((r = calloc_t(s->allocs, (size_t)count * hp.layers * d, &s->pp)) != GRX_OK) return fail(r);
+    if ((r = calloc_t(s->allocs, (size_t)4 + 2 * batch, &s->ctl)) != GRX_OK) return fail(r);
+    if (hipHostMalloc((void **)&s->ctl_host, (size_t)(4 + 2 * batch) * sizeof(int), hipHostMallocDefault) !=
+        hipSuccess) {
+        (void)hipGetLastError();
+        s->ctl_host = nullptr;
+        return fail(grx_fail(GRX_ENOMEM, "grx_conformer_stream_create: pinned memory"));
+    }
+    // newEncState: zero convolution caches (newEncState, stream.go:80-88),
+    // and the projected positions left+chunk-1 .. -(chunk-1) of every layer
+    if (hipMemset(s->conv_ring, 0, (size_t)hp.layers * batch * std::max(s->padL, 1) * d * 4) != hipSuccess)
+        return fail(grx_hip_fail(hipGetLastError(), "hipMemset"));
+    {
+        std::vector<float> pos = rel_pos(s->maxfirst, count, d);
+        float *dpos = nullptr, *dps = nullptr;
+        int8_t *dpq = nullptr;
+        std::vector<void *> tmp;
+        auto done = [&](grx_status e) {
+            for (void *p : tmp) (void)hipFree(p);
+            return e;
+        };
+        if ((r = calloc_t(tmp, pos.size(), &dpos)) != GRX_OK || (r = calloc_t(tmp, pos.size(), &dpq)) != GRX_OK ||
+            (r = calloc_t(tmp, pos.size() / 32, &dps)) != GRX_OK)
+            return fail(done(r));
+        if (hipMemcpy(dpos, pos.data(), pos.size() * 4, hipMemcpyHostToDevice) != hipSuccess)
+            return fail(done(grx_hip_fail(hipGetLastError(), "hipMemcpy")));
+        if ((r = grx_quant_act_dev(m->ctx, dpq, dps, dpos, d, count, d)) != GRX_OK ||
+            (r = grx_gemm_q8_launch(m->ctx->stream, m->pos_all, dpq, dps, count, nullptr, s->pp, hp.layers * d)) !=
+                GRX_OK)
+            return fail(done(r));
+        if (hipStreamSynchronize(m->ctx->stream) != hipSuccess)
+            return fail(done(grx_hip_fail(hipGetLastError(), "hipStreamSynchronize")));
+        done(GRX_OK);
+    }
+    *out = s;
+    return GRX_OK;
+}
+
+extern "C" grx_status grx_conformer_stream_destroy(grx_conformer_stream *s) {
+    if (!s) return GRX_OK;
+    GRX_HIP(hipSetDevice(s->m->ctx->device));
+    stream_free_work(s);
+    for (void *p : s->allocs) (void)hipFree(p);
+    if (s->ctl_host) (void)hipHostFree(s->ctl_host);
+    delete s;
+    return GRX_OK;
+}
+
+extern "C" grx_status grx_conformer_stream_geometry(const grx_conformer_stream *s, grx_conformer_stream_geom *g) {
+    if (!s || !g) return grx_fail(GRX_EINVAL, "grx_conformer_stream_geometry: NULL argument");
+    *g = s->g;
+    return GRX_OK;
+}
+
+extern "C" grx_status grx_conformer_stream_step(grx_conformer_stream *s, const float *mel, int nf, const int *length,
+                                                float *out, int *lens) {
+    return stream_step(s, mel, nf, length, out, lens, hipMemcpyHostToDevice, hipMemcpyDeviceToHost);
+}
+
+extern "C" grx_status grx_conformer_stream_step_dev(grx_conformer_stream *s, const float *mel, int nf,
+                                                    const int *length, float *out, int *lens) {
+    return stream_step(s, mel, nf, length, out, lens, hipMemcpyDeviceToDevice, hipMemcpyDeviceToDevice);
+}
+
+// ---------------------------------------------------------------- the model
 
 extern "C" grx_status grx_conformer_create(grx_ctx *ctx, const grx_conformer_hparams *hp, grx_conformer **out) {
     if (!ctx || !hp || !out) return grx_fail(GRX_EINVAL, "grx_conformer_create: NULL argument");
@@ -1436,9 +2041,25 @@ extern "C" grx_status grx_conformer_create(grx_ctx *ctx, const grx_conformer_hpa
     if (hp->d % 32 != 0 || hp->dff % 32 != 0 || hp->d % hp->heads != 0 || (hp->d / hp->heads) % 32 != 0)
         return grx_fail(GRX_ESIZE, "d %d, dff %d, heads %d: sizes must split into 32-value blocks per head", hp->d,
                         hp->dff, hp->heads);
-    if (hp->sub_channels % 32 != 0 || hp->sub_channels > 1024 || hp->d > 8192 || hp->conv_kernel % 2 != 1)
-        return grx_fail(GRX_ESIZE, "sub_channels %d (a multiple of 32 up to 1024), d %d or kernel %d unsupported",
-                        hp->sub_channels, hp->d, hp->conv_kernel);
+    if (hp->sub_channels % 32 != 0 || hp->sub_channels > 1024 || hp->d > 8192)
+        return grx_fail(GRX_ESIZE, "sub_channels %d (a multiple of 32 up to 1024) or d %d unsupported",
+                        hp->sub_channels, hp->d);
+    if (hp->att_left < -1 || hp->att_right < -1 || hp->conv_left < -1 || hp->conv_right < -1)
+        return grx_fail(GRX_EINVAL, "grx_conformer_create: a context limit below -1");
+    const bool conv_padded = hp->conv_left >= 0 && hp->conv_right >= 0;
+    if (conv_padded ? hp->conv_left + hp->conv_right + 1 != hp->conv_kernel : hp->conv_kernel % 2 != 1)
+        return grx_fail(GRX_ESIZE, "convolution padding %d + %d does not fit kernel %d", hp->conv_left,
+                        hp->conv_right, hp->conv_kernel);
+    if (hp->att_chunked && hp->att_left >= 0 && hp->att_right >= 0 && hp->att_right + 1 > kAttnQ)
+        return grx_fail(GRX_ESIZE, "chunks of %d rows are more than the attention kernels take (%d)",
+                        hp->att_right + 1, kAttnQ);
+    if (hp->n_context_choices < 0 || hp->n_context_choices > 8)
+        return grx_fail(GRX_EINVAL, "grx_conformer_create: %d context choices (at most 8)", hp->n_context_choices);
+    for (int i = 0; i < hp->n_context_choices; ++i)
+        if (hp->context_choices[i][0] < -1 || hp->context_choices[i][1] < -1 ||
+            hp->context_choices[i][1] + 1 > kAttnQ)
+            return grx_fail(GRX_EINVAL, "context choice [%d, %d] unsupported", hp->context_choices[i][0],
+                            hp->context_choices[i][1]);
     if ((hp->sub_channels * sub_F(*hp)) % 32 != 0)
         return grx_fail(GRX_ESIZE, "the pre-encoder output (%d values) is not whole Q8_0 blocks",
                         hp->sub_channels * sub_F(*hp));
@@ -1479,8 +2100,7 @@ extern "C" grx_status grx_conformer_set_tensor(grx_conformer *m, const char *nam
 }
 
 extern "C" int grx_conformer_frames_out(const grx_conformer *m, int frames) {
-    (void)m;
-    return frames < 1 ? 0 : sub_out(sub_out(sub_out(frames)));
+    return frames < 1 ? 0 : stage_len(frames, 3, m ? m->hp.causal_sub : 0);
 }
 
 extern "C" grx_status grx_conformer_encode_dev(grx_conformer *m, const float *mel, int batch, int frames,
@@ -1488,16 +2108,8 @@ extern "C" grx_status grx_conformer_encode_dev(grx_conformer *m, const float *me
     if (!m || !mel || !valid || !out) return grx_fail(GRX_EINVAL, "grx_conformer_encode_dev: NULL argument");
     if (batch < 1 || frames < 1) return grx_fail(GRX_EINVAL, "grx_conformer_encode_dev: batch %d, frames %d", batch, frames);
     grx_status s;
-    if ((s = check_valid(m, valid, batch, frames)) != GRX_OK) return s;
-    GRX_HIP(hipSetDevice(m->ctx->device));
-    if ((s = cfinalize(m)) != GRX_OK) return s;
-    if ((s = cshape(m, batch, frames)) != GRX_OK) return s;
+    if ((s = encode_common(m, mel, batch, frames, valid, hipMemcpyDeviceToDevice)) != GRX_OK) return s;
     hipStream_t st = m->ctx->stream;
-    const size_t mel_n = (size_t)batch * m->hp.n_mels * frames;
-    memcpy(m->valid_host, valid, (size_t)batch * sizeof(int));
-    GRX_HIP(hipMemcpyAsync(m->valid, m->valid_host, (size_t)batch * sizeof(int), hipMemcpyHostToDevice, st));
-    GRX_HIP(hipMemcpyAsync(m->mel, mel, mel_n * 4, hipMemcpyDeviceToDevice, st));
-    if ((s = run_encode(m)) != GRX_OK) return s;
     GRX_HIP(hipMemcpyAsync(out, m->x, (size_t)batch * m->T * m->hp.d * 4, hipMemcpyDeviceToDevice, st));
     // the pinned valid lengths are read by the copy above: wait before reuse
     GRX_HIP(hipStreamSynchronize(st));
@@ -1509,23 +2121,11 @@ extern "C" grx_status grx_conformer_encode(grx_conformer *m, const float *mel, i
     if (!m || !mel || !valid || !out) return grx_fail(GRX_EINVAL, "grx_conformer_encode: NULL argument");
     if (batch < 1 || frames < 1) return grx_fail(GRX_EINVAL, "grx_conformer_encode: batch %d, frames %d", batch, frames);
     grx_status s;
-    if ((s = check_valid(m, valid, batch, frames)) != GRX_OK) return s;
-    GRX_HIP(hipSetDevice(m->ctx->device));
-    if ((s = cfinalize(m)) != GRX_OK) return s;
-    if ((s = cshape(m, batch, frames)) != GRX_OK) return s;
+    if ((s = encode_common(m, mel, batch, frames, valid, hipMemcpyHostToDevice)) != GRX_OK) return s;
     hipStream_t st = m->ctx->stream;
-    const size_t mel_n = (size_t)batch * m->hp.n_mels * frames;
-    memcpy(m->valid_host, valid, (size_t)batch * sizeof(int));
-    GRX_HIP(hipMemcpyAsync(m->valid, m->valid_host, (size_t)batch * sizeof(int), hipMemcpyHostToDevice, st));
-    GRX_HIP(hipMemcpyAsync(m->mel, mel, mel_n * 4, hipMemcpyHostToDevice, st));
-    if ((s = run_encode(m)) != GRX_OK) return s;
     GRX_HIP(hipMemcpyAsync(out, m->x, (size_t)batch * m->T * m->hp.d * 4, hipMemcpyDeviceToHost, st));
     GRX_HIP(hipStreamSynchronize(st));
     if (lens)
-        for (int b = 0; b < batch; ++b) {
-            int L = valid[b];
-            for (int k = 0; k < 3; ++k) L = sub_out(L);
-            lens[b] = std::max(0, std::min(L, m->T));
-        }
+        for (int b = 0; b < batch; ++b) lens[b] = enc_rows(m->hp, valid[b], m->T);
     return GRX_OK;
 }

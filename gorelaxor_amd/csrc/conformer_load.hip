@@ -16,13 +16,13 @@
 // the reference would find a tensor that does not fit the settings only
 // when the first recording panics ("the model file doesn't fit its own
 // settings"), the shapes are checked here at load, with that text.  The
-// forms this build does not run (cache-aware streaming attention, limited
-// attention or convolution context, causal subsampling) are refused by
-// name.  The RNN-T/TDT decoder and the vocabulary stay with the caller.
-// Host code only.
+// attention and convolution forms and the streaming settings are read as
+// readEncoder and readHParams read them.  The RNN-T/TDT decoder and the
+// vocabulary stay with the caller.  Host code only.
 #include <stdarg.h>
 #include <stdio.h>
 
+#include <algorithm>
 #include <string>
 #include <vector>
 
@@ -188,12 +188,21 @@ extern "C" grx_status grx_conformer_load_gguf(grx_ctx *ctx, const char *path, gr
     if (grx_gguf_int(f, (q + "predictor.vocab").c_str(), 0) < 2 || grx_gguf_int(f, (q + "predictor.hidden").c_str(), 0) <= 0 ||
         grx_gguf_int(f, (q + "predictor.n_layers").c_str(), 0) <= 0 || grx_gguf_int(f, (q + "joint.hidden").c_str(), 0) <= 0)
         return grx_fail(GRX_EINVAL, "conformer: the model file is missing its decoder settings");
-    // what the device encoder runs: the offline form
-    if (style != "regular" || att_l != -1 || att_r != -1)
-        return grx_fail(GRX_EINVAL, "conformer: attention context \"%s\" [%lld, %lld]: this build runs the offline encoder",
-                        style.c_str(), (long long)att_l, (long long)att_r);
-    if (conv_l != -1 || conv_r != -1 || causal_sub)
-        return grx_fail(GRX_EINVAL, "conformer: causal convolution or subsampling: this build runs the offline encoder");
+    if (att_l < -1 || att_r < -1 || conv_l < -1 || conv_r < -1 || att_l > (1 << 20) || att_r > (1 << 20) ||
+        conv_l > (1 << 20) || conv_r > (1 << 20))
+        return grx_fail(GRX_EINVAL, "conformer: the model file is missing its encoder settings");
+    // att_context_size_choices: (left, right) pairs (readHParams, model.go:212-216)
+    std::vector<int64_t> choices;
+    {
+        const int64_t n = grx_gguf_array_len(f, (q + "encoder.att_context_size_choices").c_str());
+        if (n >= 2 && n <= 1024)
+            for (int64_t i = 0; i < n; ++i)
+                choices.push_back(grx_gguf_array_int(f, (q + "encoder.att_context_size_choices").c_str(), i));
+        else if (n > 1024)
+            return grx_fail(GRX_EINVAL, "conformer: %lld attention context choices", (long long)n / 2);
+    }
+    if (choices.size() / 2 > 8)
+        return grx_fail(GRX_EINVAL, "conformer: %zu attention context choices (this build takes 8)", choices.size() / 2);
     if (conv_norm != "batch_norm" && conv_norm != "layer_norm")
         return grx_fail(GRX_EINVAL, "conformer: conv_norm_type \"%s\" is not supported", conv_norm.c_str());
     const int64_t n_mels = grx_gguf_int(f, "stt.frontend.num_mels", 80);  // melConfig, model.go:237-251
@@ -210,10 +219,31 @@ extern "C" grx_status grx_conformer_load_gguf(grx_ctx *ctx, const char *path, gr
     hp.n_mels = (int)n_mels;
     hp.xscaling = xscaling;
     hp.conv_ln = conv_norm == "layer_norm";
+    hp.att_chunked = style == "chunked_limited";  // HParams.Causal (model.go:46)
+    hp.att_left = (int)att_l;
+    hp.att_right = (int)att_r;
+    hp.conv_left = (int)conv_l;
+    hp.conv_right = (int)conv_r;
+    hp.causal_sub = causal_sub;
+    hp.n_context_choices = (int)(choices.size() / 2);
+    for (size_t i = 0; i + 1 < choices.size(); i += 2) {
+        if (choices[i] < -1 || choices[i] > (1 << 20) || choices[i + 1] < -1 || choices[i + 1] > (1 << 20))
+            return grx_fail(GRX_EINVAL, "conformer: attention context choice [%lld, %lld] is out of range",
+                            (long long)choices[i], (long long)choices[i + 1]);
+        hp.context_choices[i / 2][0] = (int)choices[i];
+        hp.context_choices[i / 2][1] = (int)choices[i + 1];
+    }
+    // the streaming settings (readHParams, model.go:193-196)
+    const auto clampi = [](int64_t v) { return (int)std::max<int64_t>(-1, std::min<int64_t>(v, 1 << 20)); };
+    hp.pre_encode_cache = clampi(grx_gguf_int(f, (q + "encoder.streaming.pre_encode_cache_size").c_str(), -1));
+    hp.drop_extra = clampi(grx_gguf_int(f, (q + "encoder.streaming.drop_extra_pre_encoded").c_str(), -1));
+    hp.sampling_frames_first = clampi(grx_gguf_int(f, (q + "encoder.streaming.sampling_frames_first").c_str(), -1));
     CLoader l{ctx, f};
     if ((s = grx_conformer_create(ctx, &hp, &l.m)) != GRX_OK) return s;
     // loadEncoder (model.go:358-422), in its order
-    const int64_t c = subc, F = (((n_mels - 1) / 2 + 1 - 1) / 2 + 1 - 1) / 2 + 1;
+    int64_t F = n_mels;  // subOut three times (encoder.go:33-38)
+    for (int k = 0; k < 3; ++k) F = causal_sub ? F / 2 + 1 : (F - 1) / 2 + 1;
+    const int64_t c = subc;
     const std::string pe = "enc.pre_encode.";
     l.vec(pe + "conv.0.weight", c * 9);
     l.vec(pe + "conv.0.bias", c);

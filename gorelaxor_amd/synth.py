@@ -170,6 +170,14 @@ PARAKEET_TDT_06B = dict(d=1024, heads=8, layers=24, dff=4096, conv_kernel=31, su
                         xscaling=True, conv_norm="batch_norm")
 CONFORMER_TINY = dict(d=64, heads=2, layers=2, dff=256, conv_kernel=9, sub_channels=32, n_mels=32,
                       xscaling=True, conv_norm="batch_norm")
+# A cache-aware streaming FastConformer (Nemotron-Speech-Streaming-0.6B
+# shape): chunked limited attention with 70 rows of left context and the
+# four trained right contexts, a causal convolution of 9 taps with its
+# LayerNorm, the causal pre-encoder.
+NEMOTRON_STREAMING = dict(d=1024, heads=8, layers=24, dff=4096, conv_kernel=9, sub_channels=256, n_mels=128,
+                          xscaling=True, conv_norm="layer_norm", att_style="chunked_limited", att_left=70,
+                          att_right=13, context_choices=[(70, 13), (70, 6), (70, 1), (70, 0)], conv_left=8,
+                          conv_right=0)
 
 
 def conformer_model(hp: dict, seed: int = 9, pointwise_f16: bool = True, pre_f32: bool = False) -> dict:

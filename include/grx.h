@@ -401,18 +401,34 @@ grx_status grx_pocket_frames(grx_pocket *m, const float *latents, int n, float *
 
 /* ---- FastConformer encoder with Q8_0 weights ---- */
 
-/* Model.encode (conformer/encoder.go:432-489) of a non-streaming
- * FastConformer (HParams of conformer/model.go:15-44 with AttStyle
- * "regular", no attention or convolution limits, non-causal pre-encoder,
- * subsampling 8): the depthwise-striding pre-encoder (encoder.go:123-167),
- * xscale, and `layers` Conformer blocks (encoder.go:411-429), every Linear
- * a Q8_0 weight on the int8 route as conformer/model.go:348-356 packs them.
- * A batch of utterances of the same frame count runs at once; each
- * utterance's output is the one it gets alone. */
+/* Model.encode (conformer/encoder.go:432-489) of a FastConformer (HParams
+ * of conformer/model.go:15-44, subsampling 8): the depthwise-striding
+ * pre-encoder (encoder.go:123-167, causal or centred), xscale, and `layers`
+ * Conformer blocks (encoder.go:411-429) with the attention limits of
+ * offlineKeys (encoder.go:196-212) and the depthwise convolution's padding,
+ * every Linear a Q8_0 weight on the int8 route as conformer/model.go:
+ * 348-356 packs them.  A batch of utterances of the same frame count runs
+ * at once; each utterance's output is the one it gets alone.  A
+ * cache-aware ("chunked_limited") model also streams
+ * (grx_conformer_stream_*). */
 typedef struct {
     int d, heads, layers, dff, conv_kernel, sub_channels, n_mels;
     int xscaling; /* nonzero: x *= sqrt(d) after the pre-encoder (HParams.XScaling) */
     int conv_ln;  /* nonzero: conv_norm_type "layer_norm", else folded batch norm */
+    /* The attention and convolution forms.  att_chunked nonzero:
+     * AttStyle "chunked_limited", else "regular"; att_left, att_right:
+     * the attention context (-1: no limit); conv_left, conv_right: the
+     * depthwise convolution's padding (both -1: centred, else they add up
+     * to conv_kernel - 1); causal_sub nonzero: the causal pre-encoder.
+     * Every field is read: -1 where the model has no limit. */
+    int att_chunked, att_left, att_right, conv_left, conv_right, causal_sub;
+    /* Streaming settings (conformer/stream.go:23-69): the trained (left,
+     * right) context pairs (att_context_size_choices) and the pre-encoder
+     * cache, the rows it drops and the first chunk's sampling frames (-1:
+     * NeMo's 9, 2 and 1). */
+    int n_context_choices;
+    int context_choices[8][2];
+    int pre_encode_cache, drop_extra, sampling_frames_first;
 } grx_conformer_hparams;
 
 typedef struct grx_conformer grx_conformer;
@@ -437,12 +453,14 @@ grx_status grx_conformer_set_tensor(grx_conformer *m, const char *name, const vo
  * by Weight.ToQ8); the pre-encoder's conv.3 / conv.6 may be float32 (the
  * float route, as converted files hold them).  Tensors that do not fit the
  * settings fail here ("the model file doesn't fit its own settings").
- * Streaming forms (chunked attention, limited contexts, causal
- * subsampling) are refused.  *hp_out (may be NULL) receives the
- * dimensions. */
+ * The attention and convolution forms and the streaming settings are
+ * read as readEncoder and readHParams read them (att_context_size_choices
+ * beyond 8 pairs are refused).  *hp_out (may be NULL) receives the
+ * settings. */
 grx_status grx_conformer_load_gguf(grx_ctx *ctx, const char *path, grx_conformer_hparams *hp_out,
                                    grx_conformer **out);
-/* Encoder frames T for `frames` mel frames (three halvings, encoder.go:33-38). */
+/* Encoder frames T for `frames` mel frames (three halvings, encoder.go:33-38,
+ * causal ones for a causal pre-encoder). */
 int grx_conformer_frames_out(const grx_conformer *m, int frames);
 /* Model.encode of `batch` utterances: mel is [batch][n_mels][frames] float32
  * on the host (Mel.Compute's layout), valid[b] the real frames of each
@@ -455,6 +473,37 @@ grx_status grx_conformer_encode(grx_conformer *m, const float *mel, int batch, i
  * when the output is written. */
 grx_status grx_conformer_encode_dev(grx_conformer *m, const float *mel, int batch, int frames, const int *valid,
                                     float *out);
+
+/* ---- Cache-aware streaming of a FastConformer encoder ---- */
+
+/* newGeom and newEncState (conformer/stream.go:23-88): `batch` streams
+ * stepped together, with right context `right` (one of the model's
+ * trained choices; the left context is the one trained with it).  Each
+ * stream keeps, per layer, its last `left` attention key and value rows
+ * and its last conv_left gated frames in device memory. */
+typedef struct grx_conformer_stream grx_conformer_stream;
+typedef struct {
+    int right, chunk, left, left_chunks; /* encoder rows; chunk = right + 1 */
+    int mel_first, mel_next;             /* mel frames of the first chunk and of the later ones */
+    int mel_cache, drop;                 /* frames before each later chunk, and the encoder rows they give */
+    int sample_first;                    /* the fewest frames a first chunk may have */
+} grx_conformer_stream_geom;
+grx_status grx_conformer_stream_create(grx_conformer *m, int right, int batch, grx_conformer_stream **out);
+grx_status grx_conformer_stream_destroy(grx_conformer_stream *s);
+grx_status grx_conformer_stream_geometry(const grx_conformer_stream *s, grx_conformer_stream_geom *g);
+/* streamStep (stream.go:241-307) of one chunk per stream: mel is
+ * [batch][n_mels][nf] float32 on the host (the cache frames first, as the
+ * chunker cuts them), length[b] the real frames of each (1..nf).  The
+ * first call is each stream's first chunk.  out receives [batch][chunk][d]:
+ * stream b's first lens[b] rows are its encoder rows for the chunk (lens
+ * may be NULL).  A chunk whose rows after the drop exceed one chunk is an
+ * error; one that gives no rows leaves the streams unchanged. */
+grx_status grx_conformer_stream_step(grx_conformer_stream *s, const float *mel, int nf, const int *length, float *out,
+                                     int *lens);
+/* The same with mel and out in device memory (length and lens on the
+ * host); returns when the output is written. */
+grx_status grx_conformer_stream_step_dev(grx_conformer_stream *s, const float *mel, int nf, const int *length,
+                                         float *out, int *lens);
 
 /* ---- RNN-T / TDT greedy decoder (prediction network and joint) ---- */
 

@@ -73,12 +73,47 @@ def test_load_encode_bit_exact(kern, orc, tmp_path, conv_norm):
     t = conformer_model(hp, seed=41, pointwise_f16=True, pre_f32=True)
     p = _write(tmp_path / "c.gguf", hp, t)
     enc = ConformerEncoder.from_gguf(p)
-    assert enc.hp == hp
+    assert {k: enc.hp[k] for k in hp} == hp
+    assert enc.hp["att_style"] == "regular" and not enc.hp["causal_sub"]
+    assert (enc.hp["att_left"], enc.hp["att_right"], enc.hp["conv_left"], enc.hp["conv_right"]) == (-1, -1, -1, -1)
     mel, frames, valid = noise_mel(hp["n_mels"], seconds=1.5, seed=42)
     got, lens = enc.encode(mel[None], [valid])
     want, L = orc.ConformerOracle(hp, t).encode(mel, valid)
     assert lens[0] == L
     assert np.array_equal(got[0].view(np.uint32), want.view(np.uint32)), np.abs(got[0] - want).max()
+    enc.close()
+
+
+def test_load_streaming_model(kern, orc, tmp_path):
+    """A cache-aware model's file (readEncoder / readHParams settings:
+    chunked_limited attention 28 left, trained right contexts, the causal
+    convolution and pre-encoder, the streaming cache settings): the loaded
+    encoder streams bit-identically to the oracle."""
+    from gorelaxor_amd.conformer import ConformerEncoder, ConformerStream, mel_chunks, stream_geom
+
+    hp = dict(HP, conv_norm="layer_norm", att_style="chunked_limited", att_left=28, att_right=13,
+              context_choices=[(28, 13), (28, 1)], conv_left=8, conv_right=0)
+    t = conformer_model(hp, seed=43, pointwise_f16=True, pre_f32=True)
+    e = "stt.parakeet.encoder."
+    sets = _settings(hp, **{e + "att_context_style": (G.T_STR, "chunked_limited"),
+                            e + "att_context_left": (G.T_I32, 28), e + "att_context_right": (G.T_I32, 13),
+                            e + "conv_context_left": (G.T_I32, 8), e + "conv_context_right": (G.T_I32, 0),
+                            e + "streaming.pre_encode_cache_size": (G.T_I32, 9)})
+    sets.append(G.kv(e + "att_context_size_choices", G.T_ARR, [28, 13, 28, 1], G.T_I32))
+    p = _write(tmp_path / "s.gguf", hp, t, settings=sets)
+    enc = ConformerEncoder.from_gguf(p)
+    assert enc.hp["att_style"] == "chunked_limited" and enc.hp["causal_sub"]
+    assert (enc.hp["att_left"], enc.hp["att_right"], enc.hp["conv_left"], enc.hp["conv_right"]) == (28, 13, 8, 0)
+    assert enc.hp["context_choices"] == [(28, 13), (28, 1)] and enc.hp["pre_encode_cache"] == 9
+    mel, frames, valid = noise_mel(hp["n_mels"], seconds=3.0, seed=44)
+    for right in (1, 13):
+        g = stream_geom(hp, right)
+        s = ConformerStream(enc, right)
+        o = orc.ConformerOracle(hp, t).stream(right, g["left"], g["drop"])
+        for j, (ch, n, _) in enumerate(mel_chunks(mel, g)):
+            got, want = s.step(ch, n)[0], o.step(ch, n)
+            assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), (right, j)
+        s.close()
     enc.close()
 
 
@@ -97,8 +132,9 @@ def _case(case, hp, t):
         sets = _settings(hp, no_durations=True)
     elif case == "decoder":
         sets = _settings(hp, **{"stt.parakeet.joint.hidden": (None, None)})
-    elif case == "streaming":
-        sets = _settings(hp, **{e + "att_context_style": (G.T_STR, "chunked_limited")})
+    elif case == "choices":
+        sets = _settings(hp)
+        sets.append(G.kv(e + "att_context_size_choices", G.T_ARR, [70, 13] * 9, G.T_I32))
     elif case == "missing":
         tens = [r for r in tens if r[0] != "enc.blocks.1.norm_out.bias"]
     elif case == "misfit":  # a linear weight of the wrong size
@@ -115,7 +151,7 @@ def _case(case, hp, t):
     ("arch", 'architecture "pockettts" is not a FastConformer transducer'),
     ("settings", "missing its encoder settings"), ("subsampling", "subsampling 4 is not supported"),
     ("ctc", '"ctc" models are not supported'), ("durations", "a TDT model needs its durations"),
-    ("decoder", "missing its decoder settings"), ("streaming", "this build runs the offline encoder"),
+    ("decoder", "missing its decoder settings"), ("choices", "9 attention context choices"),
     ("missing", "the model has no enc.blocks.1.norm_out.bias"),
     ("misfit", r"doesn't fit its own settings \(enc.blocks.0.ff1.linear1.weight is 128x64, want 256x64\)"),
     ("type", "enc.blocks.1.attn.linear_q.weight is type 1"),
