@@ -64,6 +64,7 @@ def parse():
     p.add_argument("--no-streams", action="store_true")
     p.add_argument("--conformer-reps", type=int, default=10, help="timed encodes per batch size")
     p.add_argument("--no-conformer", action="store_true")
+    p.add_argument("--no-conformer-stream", action="store_true")
     p.add_argument("--copy-calibration", action="store_true",
                    help="only copy the ring's bytes device to device 3 times (reference reading for HBM counters)")
     return p.parse_args()
@@ -513,6 +514,96 @@ def conformer_bench(args) -> dict:
     return res
 
 
+def stream_step_bytes(hp: dict, weight_bytes: int, batch: int, keys: int, rows: int) -> int:
+    """HBM bytes of one chunk step: every Linear weight once (Q8_0), and per
+    stream and layer the keys and values its queries read (keys rows of 2d
+    float32), the chunk's own rows written into the rings, and the
+    convolution cache read and written (pad_left rows of d)."""
+    d, nl = hp["d"], hp["layers"]
+    pl = hp["conv_left"] if hp.get("conv_left", -1) >= 0 and hp.get("conv_right", -1) >= 0 else \
+        (hp["conv_kernel"] - 1) // 2
+    per = nl * (keys * 2 * d * 4 + rows * 2 * 2 * d * 4 + 2 * pl * d * 4)
+    return weight_bytes + batch * per
+
+
+def conformer_stream_bench(args) -> dict:
+    """Cache-aware streaming (conformer/stream.go:241-307) of a
+    Nemotron-Speech-Streaming-shaped encoder (d 1024, 24 layers, FFN 4096,
+    8 heads, causal convolution of 9 taps, 70 rows of left context) with
+    random-init Q8_0 weights over 10 s of white noise: every chunk step of
+    the recording at right context 13 (chunks of 14 rows, 1.12 s of audio)
+    and 0 (one row, 80 ms), for 1 and 16 streams stepped together, chunk
+    mels resident in HBM.  ms per chunk step (the API call, which waits for
+    its output), encoder rows/s, real-time factor, HBM bytes per step and
+    their roofline; the first chunks checked against the oracle, whose
+    chunk steps are the CPU baseline."""
+    import oracle
+    from gorelaxor_amd import hiprt
+    from gorelaxor_amd.conformer import ConformerEncoder, ConformerStream, mel_chunks, stream_geom
+    from gorelaxor_amd.synth import NEMOTRON_STREAMING, conformer_model, noise_mel
+
+    hp = dict(NEMOTRON_STREAMING)
+    t = conformer_model(hp, seed=35)
+    mels = [noise_mel(hp["n_mels"], 10.0, seed=90 + i)[0] for i in range(16)]
+    enc = ConformerEncoder(hp, t)
+    d = hp["d"]
+    c, F3 = hp["sub_channels"], hp["n_mels"]
+    for _ in range(3):
+        F3 = F3 // 2 + 1
+    wbytes = (2 * c * c + d * c * F3 + hp["layers"] * (4 * hp["dff"] * d + 5 * d * d + 2 * d * d + d * d)) // 32 * 34
+    res = {"shape": "d_model 1024, 24 layers, FFN 4096, 8 heads, causal conv kernel 9, 128 mels, left context 70",
+           "weight_bytes": wbytes}
+    oracle.build()
+    for right in (13, 0):
+        g = stream_geom(hp, right)
+        chunks = [mel_chunks(m, g) for m in mels]
+        n = len(chunks[0])
+        r = {"chunk_rows": g["chunk"], "chunk_audio_s": g["mel_next"] * 0.01, "chunks": n}
+        for batch in (1, 16):
+            s = ConformerStream(enc, right, batch=batch)
+            dms = [hiprt.DeviceBuffer.from_array(np.ascontiguousarray(np.stack([chunks[b][j][0] for b in range(batch)])))
+                   for j in range(n)]
+            do = hiprt.DeviceBuffer(batch * g["chunk"] * d * 4)
+            times, first_rows = [], None
+            for j in range(n):
+                nf = chunks[0][j][0].shape[1]
+                t0 = time.perf_counter()
+                s.step_dev(dms[j].ptr, nf, [chunks[b][j][1] for b in range(batch)], do.ptr)
+                times.append(time.perf_counter() - t0)
+                if j < 2 and batch == 1:
+                    first_rows = (first_rows or []) + [do.download(np.float32, (g["chunk"], d))]
+            s.close()
+            del dms, do
+            # the steady chunks: the left context full, every graph captured
+            steady = [x for j, x in enumerate(times) if j >= 2 and chunks[0][j][0].shape[1] == chunks[0][2][0].shape[1]]
+            ms = float(np.median(steady)) * 1e3
+            keys = g["left"] + g["chunk"]
+            sb = stream_step_bytes(hp, wbytes, batch, keys, g["chunk"])
+            r[f"batch{batch}"] = {"ms_per_chunk": round(ms, 3),
+                                  "rows_per_s": round(batch * g["chunk"] / (ms * 1e-3), 1),
+                                  "real_time_factor": round(batch * g["mel_next"] * 0.01 / (ms * 1e-3), 1),
+                                  "step_bytes": sb, "roofline": roofline(sb, ms * 1e-3),
+                                  "first_chunk_ms": round(times[0] * 1e3, 3)}
+            if batch == 1:
+                o = oracle.ConformerOracle(hp, t).stream(right, g["left"], g["drop"])
+                same, cpu = True, []
+                for j in range(2):
+                    ch, ln, _ = chunks[0][j]
+                    t0 = time.perf_counter()
+                    want = o.step(ch, ln)
+                    cpu.append(time.perf_counter() - t0)
+                    got = first_rows[j][:len(want)]
+                    same = same and bool(np.array_equal(got.view(np.uint32), want.view(np.uint32)))
+                r["parity_first_chunks_bit_exact"] = same
+                r["cpu_baseline"] = {"value": round(1.0 / cpu[1], 3), "unit": "chunk steps/s", "cores": 1,
+                                     "kind": "port", **cpu_info(),
+                                     "sample": f"the second chunk step of one stream on the oracle (scalar C, "
+                                               f"1 thread), {cpu[1] * 1e3:.1f} ms"}
+        res[f"right{right}"] = r
+    enc.close()
+    return res
+
+
 def tdt_bench(args, enc: np.ndarray) -> dict:
     """Model.Decode's greedy TDT loop (conformer/rnnt.go:111-173) over the
     encoder output of the 10 s utterance, with a Parakeet-TDT-shaped head
@@ -685,6 +776,10 @@ def main():
     if not args.no_conformer:
         out["conformer"] = conformer_bench(args)
         out["config"]["workload"] += "; parakeet-shaped conformer encoder at batch 1 and 16 (conformer.*)"
+    if not args.no_conformer_stream:
+        out["conformer_stream"] = conformer_stream_bench(args)
+        out["config"]["workload"] += ("; Nemotron-streaming-shaped chunk steps at right contexts 13 and 0, "
+                                      "1 and 16 streams (conformer_stream.*)")
     print(json.dumps(out), flush=True)
 
 

@@ -1962,6 +1962,14 @@ extern "C" grx_status grx_conformer_stream_create(grx_conformer *m, int right, i
         grx_conformer_stream_destroy(s);
         return e;
     };
+    // working buffers for the longest chunk that gives at most one chunk of
+    // rows after the drop, so that no step allocates (or recaptures a
+    // shape's graph for new buffers)
+    {
+        int nf = 1;
+        while (stage_len(nf + 1, 3, hp.causal_sub) - g.drop <= g.chunk) ++nf;
+        if ((r = stream_bufs(s, std::max(nf, g.mel_first))) != GRX_OK) return fail(r);
+    }
     const int d = hp.d, count = g.left + 2 * g.chunk - 1;
     if ((r = calloc_t(s->allocs, (size_t)hp.layers * batch * 2 * s->cap * 2 * d, &s->kv_ring)) != GRX_OK) return fail(r);
     if ((r = calloc_t(s->allocs, (size_t)hp.layers * batch * std::max(s->padL, 1) * d, &s->conv_ring)) != GRX_OK)
