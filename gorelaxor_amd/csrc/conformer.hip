@@ -1107,7 +1107,7 @@ std::vector<CExpect> cexpected(const grx_conformer_hparams &hp) {
 
 grx_status calloc_dev(std::vector<void *> &list, size_t bytes, void **out) {
     void *p = nullptr;
-    GRX_HIP(hipMalloc(&p, bytes > 0 ? bytes : 16));
+    GRX_HIP(grx_dev_malloc(&p, bytes > 0 ? bytes : 16));
     list.push_back(p);
     *out = p;
     return GRX_OK;
@@ -1185,8 +1185,32 @@ grx_status pointwise_weight(grx_conformer *m, const std::string &name, int rows,
     return grx_weight_q8_create(m->ctx, rows, cols, q.data(), q.size(), out);
 }
 
+// What cfinalize made (the device weights and constants), released: after a
+// failed finalize the model is as before it (its host tensors kept), and
+// grx_conformer_destroy releases a finished one.
+void crelease(grx_conformer *m) {
+    for (void *p : m->allocs) (void)hipFree(p);
+    m->allocs.clear();
+    for (grx_weight **w : {&m->w3, &m->w6, &m->wout, &m->pos_all}) {
+        grx_weight_destroy(*w);
+        *w = nullptr;
+    }
+    m->w3f = m->w6f = nullptr;
+    for (CBlock &B : m->blk)
+        for (grx_weight *w : {B.ff1.w1, B.ff1.w2, B.ff2.w1, B.ff2.w2, B.qkv, B.out, B.pw1, B.pw2}) grx_weight_destroy(w);
+    m->blk.clear();
+}
+
+grx_status cfinalize_tensors(grx_conformer *m);
+
 grx_status cfinalize(grx_conformer *m) {
     if (m->ready) return GRX_OK;
+    const grx_status s = cfinalize_tensors(m);
+    if (s != GRX_OK) crelease(m);
+    return s;
+}
+
+grx_status cfinalize_tensors(grx_conformer *m) {
     const grx_conformer_hparams &hp = m->hp;
     for (const CExpect &e : cexpected(hp))
         if (!e.optional && !m->host.count(e.name)) return grx_fail(GRX_ESTATE, "the model has no tensor %s", e.name.c_str());
@@ -1227,7 +1251,7 @@ grx_status cfinalize(grx_conformer *m) {
     if ((s = cvec(m, pe + "conv.3.bias", &m->b3)) != GRX_OK) return s;
     if ((s = cvec(m, pe + "conv.6.bias", &m->b6)) != GRX_OK) return s;
     if ((s = cvec(m, pe + "out.bias", &m->outb)) != GRX_OK) return s;
-    m->blk.resize(hp.layers);
+    m->blk.assign(hp.layers, CBlock());
     std::vector<uint8_t> pos_cat;
     for (int i = 0; i < hp.layers; ++i) {
         CBlock &B = m->blk[i];
@@ -1455,7 +1479,7 @@ grx_status cshape(grx_conformer *m, int B, int frames) {
     if ((s = calloc_t(w, (size_t)(2 * T - 1) * d, &m->pos_q)) != GRX_OK) return s;
     if ((s = calloc_t(w, (size_t)(2 * T - 1) * d / 32, &m->pos_s)) != GRX_OK) return s;
     if ((s = calloc_t(w, 2 * (size_t)B, &m->valid)) != GRX_OK) return s;
-    GRX_HIP(hipHostMalloc((void **)&m->valid_host, 2 * (size_t)B * sizeof(int), hipHostMallocDefault));
+    GRX_HIP(grx_pinned_malloc((void **)&m->valid_host, 2 * (size_t)B * sizeof(int)));
     std::vector<float> pos = rel_pos(T - 1, 2 * T - 1, d);
     GRX_HIP(hipMemcpy(m->pos, pos.data(), pos.size() * 4, hipMemcpyHostToDevice));
     if ((s = grx_quant_act_dev(m->ctx, m->pos_q, m->pos_s, m->pos, d, 2 * T - 1, d)) != GRX_OK) return s;
@@ -1976,8 +2000,7 @@ extern "C" grx_status grx_conformer_stream_create(grx_conformer *m, int right, i
         return fail(r);
     if ((r = calloc_t(s->allocs, (size_t)count * hp.layers * d, &s->pp)) != GRX_OK) return fail(r);
     if ((r = calloc_t(s->allocs, (size_t)4 + 2 * batch, &s->ctl)) != GRX_OK) return fail(r);
-    if (hipHostMalloc((void **)&s->ctl_host, (size_t)(4 + 2 * batch) * sizeof(int), hipHostMallocDefault) !=
-        hipSuccess) {
+    if (grx_pinned_malloc((void **)&s->ctl_host, (size_t)(4 + 2 * batch) * sizeof(int)) != hipSuccess) {
         (void)hipGetLastError();
         s->ctl_host = nullptr;
         return fail(grx_fail(GRX_ENOMEM, "grx_conformer_stream_create: pinned memory"));
@@ -2082,13 +2105,7 @@ extern "C" grx_status grx_conformer_destroy(grx_conformer *m) {
     if (!m) return GRX_OK;
     GRX_HIP(hipSetDevice(m->ctx->device));
     free_work(m);
-    for (void *p : m->allocs) (void)hipFree(p);
-    grx_weight *ws[] = {m->w3, m->w6, m->wout, m->pos_all};
-    for (grx_weight *w : ws) grx_weight_destroy(w);
-    for (CBlock &B : m->blk) {
-        grx_weight *bw[] = {B.ff1.w1, B.ff1.w2, B.ff2.w1, B.ff2.w2, B.qkv, B.out, B.pw1, B.pw2};
-        for (grx_weight *w : bw) grx_weight_destroy(w);
-    }
+    crelease(m);
     delete m;
     return GRX_OK;
 }

@@ -7,11 +7,40 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <atomic>
 #include <string>
 
 #include "grx_internal.h"
 
 static thread_local std::string g_last_error;
+
+// Allocations left before an injected out-of-memory failure (-1: none).
+static std::atomic<long long> g_alloc_countdown{-1};
+
+// Whether this allocation is the one grx_debug_fail_alloc_after named; the
+// countdown then stops, so later allocations (the cleanup's) succeed.
+static bool alloc_injected_failure() {
+    long long c = g_alloc_countdown.load();
+    while (c >= 0)
+        if (g_alloc_countdown.compare_exchange_weak(c, c - 1)) return c == 0;
+    return false;
+}
+
+hipError_t grx_dev_malloc(void **p, size_t bytes) {
+    *p = nullptr;
+    if (alloc_injected_failure()) return hipErrorOutOfMemory;
+    return hipMalloc(p, bytes);
+}
+
+hipError_t grx_pinned_malloc(void **p, size_t bytes) {
+    *p = nullptr;
+    if (alloc_injected_failure()) return hipErrorOutOfMemory;
+    return hipHostMalloc(p, bytes, hipHostMallocDefault);
+}
+
+extern "C" void grx_debug_fail_alloc_after(long long n) { g_alloc_countdown.store(n < 0 ? -1 : n); }
+
+extern "C" long long grx_debug_alloc_countdown(void) { return g_alloc_countdown.load(); }
 
 grx_status grx_fail(grx_status s, const char *fmt, ...) {
     char buf[512];
@@ -95,7 +124,7 @@ grx_status grx_ctx_scratch(grx_ctx *ctx, size_t bytes, void **out) {
         ctx->scratch = nullptr;
         ctx->scratch_bytes = 0;
         size_t want = bytes + bytes / 4 + 4096;
-        GRX_HIP(hipMalloc(&ctx->scratch, want));
+        GRX_HIP(grx_dev_malloc(&ctx->scratch, want));
         ctx->scratch_bytes = want;
     }
     *out = ctx->scratch;
@@ -155,9 +184,9 @@ extern "C" grx_status grx_weight_q8_create(grx_ctx *ctx, int rows, int cols, con
     hipError_t e = hipSuccess;
     void *raw = nullptr;
     if (w->bytes > 0) {
-        e = hipMalloc(&w->qs, qbytes > 0 ? qbytes : 16);
-        if (e == hipSuccess) e = hipMalloc(&w->ds, dbytes > 0 ? dbytes : 16);
-        if (e == hipSuccess && need > 0) e = hipMalloc(&raw, need);
+        e = grx_dev_malloc((void **)&w->qs, qbytes > 0 ? qbytes : 16);
+        if (e == hipSuccess) e = grx_dev_malloc((void **)&w->ds, dbytes > 0 ? dbytes : 16);
+        if (e == hipSuccess && need > 0) e = grx_dev_malloc(&raw, need);
         if (e == hipSuccess && need > 0)
             e = hipMemcpyAsync(raw, q8, need, hipMemcpyHostToDevice, ctx->stream);
         if (e == hipSuccess && w->tiles > 0 && w->nb > 0) {

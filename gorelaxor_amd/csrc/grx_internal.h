@@ -83,6 +83,11 @@ grx_status grx_sample_run(grx_ctx *ctx, const float *dev_logits, const float *ho
 grx_status grx_gguf_tensor_data(const grx_gguf *g, const char *name, int *type, std::vector<uint8_t> *out);
 #endif
 grx_status grx_hip_fail(hipError_t e, const char *what);
+// Every device and pinned allocation of the library: hipMalloc and
+// hipHostMalloc, or the out-of-memory failure grx_debug_fail_alloc_after
+// injects.
+hipError_t grx_dev_malloc(void **p, size_t bytes);
+hipError_t grx_pinned_malloc(void **p, size_t bytes);
 // q8_gemv.hip: looks up grx_matmul_q8_dev_noalloc's device scratch on the
 // current device, once (grx_ctx_create calls it)
 void grx_noalloc_setup(int device);

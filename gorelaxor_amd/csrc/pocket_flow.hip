@@ -196,9 +196,42 @@ bool pocket_flow_tensor(const grx_pocket *m, const std::string &name, size_t *qa
     return false;
 }
 
-grx_status pocket_flow_finalize(grx_pocket *m) {
+// The flow head's weights, and the device allocations from index `mark` of
+// the model's list on (those its finalize made), released; its settings
+// stay, so a failed finalize can be tried again.
+void pocket_flow_release(grx_pocket *m, size_t mark) {
     FlowHead &f = m->flow;
-    if (f.ready) return GRX_OK;
+    for (FlowMat *w : {&f.cond, &f.input, &f.final_ada, &f.out}) grx_weight_destroy(w->q8);
+    for (FlowRes &r : f.res)
+        for (FlowMat *w : {&r.ada, &r.fc1, &r.fc2}) grx_weight_destroy(w->q8);
+    for (size_t i = mark; i < m->allocs.size(); ++i) (void)hipFree(m->allocs[i]);
+    if (mark < m->allocs.size()) m->allocs.resize(mark);
+    FlowHead keep;
+    keep.on = f.on;
+    keep.dim = f.dim;
+    keep.depth = f.depth;
+    keep.steps = f.steps;
+    f = keep;
+}
+
+namespace {
+
+grx_status flow_finalize_tensors(grx_pocket *m);
+
+}  // namespace
+
+grx_status pocket_flow_finalize(grx_pocket *m) {
+    if (m->flow.ready) return GRX_OK;
+    const size_t mark = m->allocs.size();
+    const grx_status s = flow_finalize_tensors(m);
+    if (s != GRX_OK) pocket_flow_release(m, mark);
+    return s;
+}
+
+namespace {
+
+grx_status flow_finalize_tensors(grx_pocket *m) {
+    FlowHead &f = m->flow;
     if (!f.on) return grx_fail(GRX_ESTATE, "the flow head is not declared (grx_pocket_flow_init)");
     for (const Spec &x : flow_specs(m->hp, f))
         if (!m->host.count(x.name)) return grx_fail(GRX_ESTATE, "the model file has no tensor %s", x.name.c_str());
@@ -234,8 +267,19 @@ grx_status pocket_flow_finalize(grx_pocket *m) {
     if ((s = dev(m, 3 * (size_t)D, &f.mod)) != GRX_OK) return s;
     if ((s = dev(m, (size_t)ld, &f.cur)) != GRX_OK) return s;
     if ((s = dev(m, (size_t)ld, &f.v)) != GRX_OK) return s;
-    // timeConds (lm.go:89-104): the mean of the start and end times' embeddings
-    FlowMat t1[2], t2[2];
+    // timeConds (lm.go:89-104): the mean of the start and end times' embeddings,
+    // from embedders used only here (their weights released on every exit)
+    struct TimeMats {
+        FlowMat t1[2], t2[2];
+        ~TimeMats() {
+            for (int e = 0; e < 2; ++e) {
+                grx_weight_destroy(t1[e].q8);
+                grx_weight_destroy(t2[e].q8);
+            }
+        }
+    } tm;
+    FlowMat(&t1)[2] = tm.t1;
+    FlowMat(&t2)[2] = tm.t2;
     float *tb1[2], *tb2[2];
     for (int e = 0; e < 2; ++e) {
         const std::string p = "flow.time." + std::to_string(e) + ".";
@@ -252,16 +296,14 @@ grx_status pocket_flow_finalize(grx_pocket *m) {
                            b.data());
         for (int j = 0; j < D && s == GRX_OK; ++j) tc[(size_t)i * D + j] = (a[j] + b[j]) / 2;
     }
-    for (int e = 0; e < 2; ++e) {
-        grx_weight_destroy(t1[e].q8);
-        grx_weight_destroy(t2[e].q8);
-    }
     if (s != GRX_OK) return s;
     GRX_HIP(hipMemcpy(f.tc, tc.data(), tc.size() * 4, hipMemcpyHostToDevice));
     for (const Spec &x : flow_specs(m->hp, f)) m->host.erase(x.name);
     f.ready = true;
     return GRX_OK;
 }
+
+}  // namespace
 
 // flowHead.sample for the frame the transformer just finished; the latent
 // goes to m->lat[*frame]

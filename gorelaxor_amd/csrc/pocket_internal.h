@@ -74,5 +74,7 @@ grx_status pocket_alloc(grx_pocket *m, size_t bytes, void **out);
 // pocket_flow.hip
 bool pocket_flow_tensor(const grx_pocket *m, const std::string &name, size_t *bytes_a, size_t *bytes_b);
 grx_status pocket_flow_finalize(grx_pocket *m);
+// the flow head's weights and its allocations from index mark of m->allocs on
+void pocket_flow_release(grx_pocket *m, size_t mark);
 grx_status pocket_flow_enqueue(grx_pocket *m, hipStream_t st);
 

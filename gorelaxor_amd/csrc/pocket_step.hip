@@ -367,7 +367,7 @@ std::vector<PExpect> pexpected(const grx_pocket_hparams &hp) {
 
 grx_status palloc(grx_pocket *m, size_t bytes, void **out) {
     void *p = nullptr;
-    GRX_HIP(hipMalloc(&p, bytes > 0 ? bytes : 16));
+    GRX_HIP(grx_dev_malloc(&p, bytes > 0 ? bytes : 16));
     m->allocs.push_back(p);
     *out = p;
     return GRX_OK;
@@ -408,15 +408,36 @@ void rope_table(const grx_pocket_hparams &hp, std::vector<float> &cs, std::vecto
         }
 }
 
+// What pfinalize made (and, with it, anything allocated later: the flow
+// head's buffers, the latents), released; the flow head's weights are
+// released by pocket_flow_release.  After a failed finalize the model is
+// as before it (its host tensors kept).
+void prelease(grx_pocket *m) {
+    for (PLayer &L : m->L)
+        for (grx_weight *w : {L.qkv, L.out, L.ff1, L.ff2}) grx_weight_destroy(w);
+    m->L.clear();
+    for (void *p : m->allocs) (void)hipFree(p);
+    m->allocs.clear();
+    m->lat = nullptr;
+}
+
+grx_status pfinalize_tensors(grx_pocket *m);
+
 grx_status pfinalize(grx_pocket *m) {
     if (m->ready) return GRX_OK;
+    const grx_status s = pfinalize_tensors(m);
+    if (s != GRX_OK) prelease(m);
+    return s;
+}
+
+grx_status pfinalize_tensors(grx_pocket *m) {
     const grx_pocket_hparams &hp = m->hp;
     for (const PExpect &e : pexpected(hp))
         if (!m->host.count(e.name)) return grx_fail(GRX_ESTATE, "the model file has no tensor %s", e.name.c_str());
     GRX_HIP(hipSetDevice(m->ctx->device));
     grx_status s;
     const size_t d = hp.d, ff = hp.ff, mp = hp.max_pos;
-    m->L.resize(hp.n_layer);
+    m->L.assign(hp.n_layer, PLayer());
     for (int i = 0; i < hp.n_layer; ++i) {
         PLayer &L = m->L[i];
         const std::string p = "lm.blk." + std::to_string(i) + ".";
@@ -618,12 +639,8 @@ extern "C" grx_status grx_pocket_destroy(grx_pocket *m) {
     if (m->graph) (void)hipGraphDestroy(m->graph);
     if (m->speak_exec) (void)hipGraphExecDestroy(m->speak_exec);
     if (m->speak_graph) (void)hipGraphDestroy(m->speak_graph);
-    for (FlowMat *f : {&m->flow.cond, &m->flow.input, &m->flow.final_ada, &m->flow.out}) grx_weight_destroy(f->q8);
-    for (FlowRes &r : m->flow.res)
-        for (FlowMat *f : {&r.ada, &r.fc1, &r.fc2}) grx_weight_destroy(f->q8);
-    for (PLayer &L : m->L)
-        for (grx_weight *w : {L.qkv, L.out, L.ff1, L.ff2}) grx_weight_destroy(w);
-    for (void *p : m->allocs) (void)hipFree(p);
+    pocket_flow_release(m, m->allocs.size());
+    prelease(m);
     delete m;
     return GRX_OK;
 }
@@ -728,7 +745,7 @@ extern "C" grx_status grx_pocket_frames(grx_pocket *m, const float *latents, int
                 m->graph = nullptr;
             }
         }
-        GRX_HIP(hipMalloc(&m->lat, (size_t)(hp.max_pos + 1) * hp.ldim * 4));  // + the row a flow head writes last
+        GRX_HIP(grx_dev_malloc((void **)&m->lat, (size_t)(hp.max_pos + 1) * hp.ldim * 4));  // + the row a flow head writes last
         m->allocs.push_back(m->lat);
         m->lat_cap = hp.max_pos;
     }

@@ -454,7 +454,7 @@ std::vector<RExpect> rexpected(const grx_rnnt_hparams &hp, int embed_rows) {
 }
 
 grx_status ralloc(grx_rnnt *m, size_t bytes, void **p) {
-    GRX_HIP(hipMalloc(p, bytes < 4 ? 4 : bytes));
+    GRX_HIP(grx_dev_malloc(p, bytes < 4 ? 4 : bytes));
     (void)m;
     return GRX_OK;
 }
@@ -462,7 +462,12 @@ grx_status ralloc(grx_rnnt *m, size_t bytes, void **p) {
 grx_status upload_vec(grx_rnnt *m, const void *data, size_t bytes, float **out) {
     grx_status s = ralloc(m, bytes, reinterpret_cast<void **>(out));
     if (s != GRX_OK) return s;
-    GRX_HIP(hipMemcpy(*out, data, bytes, hipMemcpyHostToDevice));
+    const hipError_t e = hipMemcpy(*out, data, bytes, hipMemcpyHostToDevice);
+    if (e != hipSuccess) {
+        (void)hipFree(*out);
+        *out = nullptr;
+        return grx_hip_fail(e, "hipMemcpy");
+    }
     return GRX_OK;
 }
 
@@ -522,7 +527,28 @@ grx_status ensure_T(grx_rnnt *m, int T) {
     return GRX_OK;
 }
 
+// The loop's control and state buffers rfinalize makes, released (after a
+// failed finalize the decoder is as before it; grx_rnnt_destroy frees them
+// too).
+void rrelease(grx_rnnt *m) {
+    for (void **p : {(void **)&m->ctl, (void **)&m->S, (void **)&m->gx, (void **)&m->gh, (void **)&m->pp,
+                     (void **)&m->logits}) {
+        if (*p) (void)hipFree(*p);
+        *p = nullptr;
+    }
+    if (m->ctl_host) (void)hipHostFree(m->ctl_host);
+    m->ctl_host = nullptr;
+}
+
+grx_status rfinalize_buffers(grx_rnnt *m);
+
 grx_status rfinalize(grx_rnnt *m) {
+    const grx_status s = rfinalize_buffers(m);
+    if (s != GRX_OK) rrelease(m);
+    return s;
+}
+
+grx_status rfinalize_buffers(grx_rnnt *m) {
     const grx_rnnt_hparams &hp = m->hp;
     const auto ex = rexpected(hp, m->embed_rows);
     for (size_t i = 0; i < ex.size(); ++i)
@@ -530,7 +556,7 @@ grx_status rfinalize(grx_rnnt *m) {
     const int H = hp.pred_hidden, L = hp.pred_layers;
     grx_status s;
     if ((s = ralloc(m, sizeof(RnntCtl), reinterpret_cast<void **>(&m->ctl))) != GRX_OK) return s;
-    GRX_HIP(hipHostMalloc(reinterpret_cast<void **>(&m->ctl_host), sizeof(RnntCtl), 0));
+    GRX_HIP(grx_pinned_malloc(reinterpret_cast<void **>(&m->ctl_host), sizeof(RnntCtl)));
     if ((s = ralloc(m, (size_t)2 * 2 * L * H * 4, reinterpret_cast<void **>(&m->S))) != GRX_OK) return s;
     if ((s = ralloc(m, (size_t)L * 4 * H * 4, reinterpret_cast<void **>(&m->gx))) != GRX_OK) return s;
     if ((s = ralloc(m, (size_t)L * 4 * H * 4, reinterpret_cast<void **>(&m->gh))) != GRX_OK) return s;
@@ -605,10 +631,9 @@ extern "C" grx_status grx_rnnt_destroy(grx_rnnt *m) {
     grx_weight_destroy(m->jenc);
     grx_weight_destroy(m->jpred);
     grx_weight_destroy(m->jout);
-    for (void *p : {(void *)m->embed, (void *)m->jencb, (void *)m->jpredb, (void *)m->joutb, (void *)m->ctl,
-                    (void *)m->S, (void *)m->gx, (void *)m->gh, (void *)m->pp, (void *)m->logits})
+    for (void *p : {(void *)m->embed, (void *)m->jencb, (void *)m->jpredb, (void *)m->joutb})
         if (p) (void)hipFree(p);
-    if (m->ctl_host) (void)hipHostFree(m->ctl_host);
+    rrelease(m);
     delete m;
     return GRX_OK;
 }
@@ -673,7 +698,7 @@ extern "C" grx_status grx_rnnt_state_create(grx_rnnt *m, grx_rnnt_state **out) {
     GRX_HIP(hipSetDevice(m->ctx->device));
     const size_t bytes = (size_t)2 * m->k.L * m->k.H * 4;
     grx_rnnt_state *s = new grx_rnnt_state{m, m->ctx, m->k.L, m->k.H, m->k.V, m->k.blank, m->embed_rows, nullptr, -1};
-    hipError_t e = hipMalloc(reinterpret_cast<void **>(&s->hc), bytes);
+    hipError_t e = grx_dev_malloc(reinterpret_cast<void **>(&s->hc), bytes);
     if (e == hipSuccess) e = hipMemset(s->hc, 0, bytes);
     if (e != hipSuccess) {
         if (s->hc) (void)hipFree(s->hc);
@@ -721,7 +746,13 @@ extern "C" grx_status grx_rnnt_decode(grx_rnnt *m, const float *enc, int T, int 
                                       int frame_offset, grx_rnnt_token *out, int cap, int *n_out) {
     if (!m || (!enc && T > 0) || !n_out || (!out && cap > 0) || T < 0 || cap < 0)
         return grx_fail(GRX_EINVAL, "grx_rnnt_decode: NULL argument or negative size");
-    if (!m->ready) return grx_fail(GRX_ESTATE, "grx_rnnt_decode: the decoder's tensors are not all set");
+    if (!m->ready) {
+        // the last tensor's set-up may have failed (out of memory): try again
+        for (bool h : m->have)
+            if (!h) return grx_fail(GRX_ESTATE, "grx_rnnt_decode: the decoder's tensors are not all set");
+        grx_status fs = rfinalize(m);
+        if (fs != GRX_OK) return fs;
+    }
     if (st && (st->m != m || st->L != m->k.L || st->H != m->k.H))
         return grx_fail(GRX_EINVAL, "grx_rnnt_decode: the state belongs to another decoder");
     *n_out = 0;

@@ -610,7 +610,7 @@ std::vector<Expect> expected(const grx_whisper_hparams &hp) {
 
 grx_status dev_alloc(grx_whisper *m, size_t bytes, void **out) {
     void *p = nullptr;
-    GRX_HIP(hipMalloc(&p, bytes > 0 ? bytes : 16));
+    GRX_HIP(grx_dev_malloc(&p, bytes > 0 ? bytes : 16));
     m->allocs.push_back(p);
     *out = p;
     return GRX_OK;
@@ -629,8 +629,29 @@ grx_status upload_vec(grx_whisper *m, const std::string &name, float **out) {
     return GRX_OK;
 }
 
+// What finalize made (weights, constants and step buffers), released: after
+// a failed finalize the model is as before it (its host tensors kept), and
+// grx_whisper_destroy releases a finished one.
+void wrelease(grx_whisper *m) {
+    for (WLayer &L : m->L)
+        for (grx_weight *w : {L.qkv, L.o, L.xq, L.xk, L.xv, L.xo, L.fc1, L.fc2}) grx_weight_destroy(w);
+    m->L.clear();
+    grx_weight_destroy(m->tok_emb);
+    m->tok_emb = nullptr;
+    for (void *p : m->allocs) (void)hipFree(p);
+    m->allocs.clear();
+}
+
+grx_status finalize_tensors(grx_whisper *m);
+
 grx_status finalize(grx_whisper *m) {
     if (m->ready) return GRX_OK;
+    const grx_status s = finalize_tensors(m);
+    if (s != GRX_OK) wrelease(m);
+    return s;
+}
+
+grx_status finalize_tensors(grx_whisper *m) {
     const grx_whisper_hparams &hp = m->hp;
     for (const Expect &e : expected(hp))
         if (!m->host.count(e.name)) return grx_fail(GRX_ESTATE, "the model file has no tensor %s", e.name.c_str());
@@ -644,7 +665,7 @@ grx_status finalize(grx_whisper *m) {
     if ((s = upload_vec(m, "decoder.positional_embedding", &m->dec_pos)) != GRX_OK) return s;
     if ((s = upload_vec(m, "decoder.ln.weight", &m->dec_ln_w)) != GRX_OK) return s;
     if ((s = upload_vec(m, "decoder.ln.bias", &m->dec_ln_b)) != GRX_OK) return s;
-    m->L.resize(hp.n_layer);
+    m->L.assign(hp.n_layer, WLayer());
     for (int i = 0; i < hp.n_layer; ++i) {
         WLayer &L = m->L[i];
         const std::string p = "decoder.blocks." + std::to_string(i) + ".";
@@ -1014,10 +1035,7 @@ extern "C" grx_status grx_whisper_destroy(grx_whisper *m) {
     GRX_HIP(hipStreamSynchronize(m->ctx->stream));
     if (m->exec) (void)hipGraphExecDestroy(m->exec);
     if (m->graph) (void)hipGraphDestroy(m->graph);
-    for (WLayer &L : m->L)
-        for (grx_weight *w : {L.qkv, L.o, L.xq, L.xk, L.xv, L.xo, L.fc1, L.fc2}) grx_weight_destroy(w);
-    grx_weight_destroy(m->tok_emb);
-    for (void *p : m->allocs) (void)hipFree(p);
+    wrelease(m);
     delete m;
     return GRX_OK;
 }
@@ -1052,11 +1070,10 @@ extern "C" grx_status grx_whisper_set_encoder_output_stream(grx_whisper *m, int 
     if (s != GRX_OK) return s;
     const int st = m->hp.n_state, nctx = n_audio_ctx, hd = st / m->hp.n_head;
     const size_t n = (size_t)nctx * st;
-    if (m->xenc == nullptr) {  // staging for every later window too
-        if ((s = dev_alloc_t(m, n, &m->xenc)) != GRX_OK) return s;
-        if ((s = dev_alloc_t(m, n, &m->xk_tmp)) != GRX_OK) return s;
-        if ((s = dev_alloc_t(m, n, &m->xv_tmp)) != GRX_OK) return s;
-    }
+    // staging for every later window too; each buffer on its own, so that
+    // a call that failed half-way allocates only what is still missing
+    for (float **b : {&m->xenc, &m->xk_tmp, &m->xv_tmp})
+        if (*b == nullptr && (s = dev_alloc_t(m, n, b)) != GRX_OK) return s;
     float *denc = m->xenc, *dk = m->xk_tmp, *dv = m->xv_tmp;
     hipStream_t stream = m->ctx->stream;
     GRX_HIP(hipMemcpyAsync(denc, enc, n * 4, hipMemcpyHostToDevice, stream));

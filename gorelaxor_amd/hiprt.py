@@ -120,5 +120,12 @@ class Event:
             pass
 
 
+def mem_free() -> int:
+    """Free device memory in bytes (hipMemGetInfo)."""
+    free, total = C.c_size_t(), C.c_size_t()
+    _check(hip().hipMemGetInfo(C.byref(free), C.byref(total)), "hipMemGetInfo")
+    return free.value
+
+
 def synchronize() -> None:
     _check(hip().hipDeviceSynchronize(), "hipDeviceSynchronize")

@@ -567,6 +567,20 @@ grx_status grx_rnnt_state_write(grx_rnnt_state *s, const float *h, const float *
 grx_status grx_rnnt_decode(grx_rnnt *m, const float *enc, int T, int enc_on_device, grx_rnnt_state *st,
                            int frame_offset, grx_rnnt_token *out, int cap, int *n_out);
 
+/* ---- Fault injection, for tests of the cleanup paths ---- */
+
+/* No counterpart in the reference (its tests reach its error paths through
+ * panics turned into errors, conformer/robust_test.go:16-27, model.go:
+ * 282-289).  For callers that test how the library fails: the n-th device
+ * or pinned allocation from now on (n = 0: the next one) fails as out of
+ * memory, so the call that makes it returns GRX_ENOMEM; the allocations
+ * after it succeed again.  n < 0 disarms it.  Process-wide; not for use
+ * while other threads call the library. */
+void grx_debug_fail_alloc_after(long long n);
+/* Allocations left before the injected failure, -1 when none is armed (the
+ * failing one taken, or disarmed). */
+long long grx_debug_alloc_countdown(void);
+
 #ifdef __cplusplus
 }
 #endif
