@@ -65,6 +65,9 @@ def parse():
     p.add_argument("--conformer-reps", type=int, default=10, help="timed encodes per batch size")
     p.add_argument("--no-conformer", action="store_true")
     p.add_argument("--no-conformer-stream", action="store_true")
+    p.add_argument("--profile-leg", choices=["speak", "tdt", "sampler", "conformer-stream"],
+                   help="only this workload, for a profiler (no headline line): the pocket speak loop, the TDT "
+                        "decode, whisper's sampler, or the streaming chunk steps")
     p.add_argument("--copy-calibration", action="store_true",
                    help="only copy the ring's bytes device to device 3 times (reference reading for HBM counters)")
     return p.parse_args()
@@ -644,6 +647,66 @@ def tdt_bench(args, enc: np.ndarray) -> dict:
                              "sample": f"the same decode on the oracle (scalar C, 1 thread), {cpu_s * 1e3:.1f} ms"}}
 
 
+def profile_leg(args) -> dict:
+    """One workload alone, as the committed profiles run it."""
+    leg = args.profile_leg
+    if leg == "speak":
+        # the pocket flow LM (d 1024, 6 layers) with the flow head (512, 6
+        # residual blocks, 1 LSD step): a 64-row prefix, then 40 frames
+        from gorelaxor_amd.pocket import PocketLM
+        from gorelaxor_amd.synth import POCKET_FLOW, POCKET_TTS_LM, pocket_flow_model, pocket_inputs, pocket_model
+        hp, fhp = dict(POCKET_TTS_LM), dict(POCKET_FLOW)
+        t, ft = pocket_model(hp, seed=5), pocket_flow_model(hp, fhp, seed=7)
+        x, _ = pocket_inputs(hp, 1, prefix=64, seed=6)
+        noise = np.random.default_rng(8).standard_normal((40, hp["ldim"])).astype(np.float32)
+        lm = PocketLM(hp, t)
+        lm.flow_init(fhp["dim"], fhp["depth"], fhp["steps"])
+        for k, v in ft.items():
+            lm.set_tensor(k, v)
+        for _ in range(3):
+            lm.reset()
+            lm.run(x)
+            t0 = time.perf_counter()
+            lm.speak(noise)
+            ms = (time.perf_counter() - t0) * 1e3
+        lm.close()
+        return {"leg": leg, "frames": 40, "ms_last_speak": round(ms, 3)}
+    if leg == "tdt":
+        # the Parakeet-TDT-shaped head over 125 frames of N(0, 1), 6 decodes
+        from gorelaxor_amd.rnnt import TransducerDecoder
+        from gorelaxor_amd.synth import RNNT_TDT, rnnt_encoder_output, rnnt_model
+        hp = dict(RNNT_TDT)
+        dec = TransducerDecoder(hp, rnnt_model(hp, seed=30))
+        enc = rnnt_encoder_output(hp, 125, seed=31)
+        for _ in range(6):
+            toks = dec.decode(enc)
+        dec.close()
+        return {"leg": leg, "frames": 125, "tokens": len(toks)}
+    if leg == "sampler":
+        # whisper's rules and sampler over 51,864 logits (one text token,
+        # temperature 0): 21 calls for each of three logit kinds
+        from gorelaxor_amd.whisper import Rules, sample_logits, special_tokens
+        n = 51864
+        sp = special_tokens(n)
+        rules = Rules(sp, [1, 2, 7, 8, 9, 10, 220, 1906, 3556, 50254], space=220)
+        rng = np.random.default_rng(3)
+        beg = sp["beg"]
+        kinds = {"wide": (rng.standard_normal(n) * 6.0).astype(np.float32)}
+        lg = (rng.standard_normal(n) * 2.5).astype(np.float32)
+        lg[rng.integers(0, beg, 5)] += 18.0
+        lg[beg:] -= 6.0
+        kinds["spread"] = lg
+        kinds["flat"] = (rng.standard_normal(n) * 0.05).astype(np.float32)
+        out = {}
+        for name, lg in kinds.items():
+            for _ in range(21):
+                tok = sample_logits(lg, rules, tokens=[300])
+            out[name] = tok["id"]
+        return {"leg": leg, "ids": out}
+    # the streaming chunk steps alone
+    return {"leg": leg, "conformer_stream": conformer_stream_bench(args)}
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -653,6 +716,9 @@ def main():
 
     from gorelaxor_amd import hiprt, kern
 
+    if args.profile_leg:
+        print(json.dumps(profile_leg(args)), flush=True)
+        return
     if args.copy_calibration:
         nbytes = N * RING * K // 32 * 34
         a, b = hiprt.DeviceBuffer(nbytes), hiprt.DeviceBuffer(nbytes)
