@@ -117,6 +117,7 @@ SIGNATURES = {
     "grx_conformer_encode_dev": (i32, [vp, vp, i32, i32, vp, vp]),
     "grx_debug_fail_alloc_after": (None, [C.c_longlong]),
     "grx_debug_alloc_countdown": (C.c_longlong, []),
+    "grx_debug_tune": (i32, [C.c_char_p, i32]),
     "grx_conformer_stream_create": (i32, [vp, i32, i32, C.POINTER(vp)]),
     "grx_conformer_stream_destroy": (i32, [vp]),
     "grx_conformer_stream_geometry": (i32, [vp, vp]),

@@ -1388,7 +1388,7 @@ int pad_left(const grx_conformer_hparams &hp) {
 // the unstaged kernel runs.  nk: the most keys a block sees.
 grx_status attn_pick(int B, int heads, int nblk, int bl, int nk, int hd, int *rq, size_t *smem) {
     *rq = B * heads * nblk * ((bl + 7) / 8) < 1024 ? 8 : 16;
-    if (const char *e = getenv("GRX_CONF_ATTN_RQ")) *rq = atoi(e);  // 0 (unstaged), 8 or 16, for tests
+    if (grx_tune(GRX_TUNE_CONF_ATTN_RQ) >= 0) *rq = grx_tune(GRX_TUNE_CONF_ATTN_RQ);  // 0 (unstaged), 8 or 16, for tests
     if (*rq != 0 && *rq != 8 && *rq != 16) *rq = 8;
     const size_t sq = hd + 1;
     const size_t stage = std::max((size_t)(nk + *rq - 1) * sq, (size_t)nk * hd);
@@ -1724,8 +1724,7 @@ grx_status enqueue_encode(grx_conformer *m, hipStream_t st) {
 
 grx_status run_graph(hipStream_t st, hipGraph_t *graph, hipGraphExec_t *exec,
                      const std::function<grx_status(hipStream_t)> &enqueue) {
-    static const bool no_graph = getenv("GRX_NO_GRAPH") != nullptr;
-    if (no_graph) return enqueue(st);
+    if (grx_tune(GRX_TUNE_NO_GRAPH) == 1) return enqueue(st);
     if (!*exec) {
         GRX_HIP(hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal));
         grx_status s = enqueue(st);

@@ -7,7 +7,10 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <stdlib.h>
+
 #include <atomic>
+#include <mutex>
 #include <string>
 
 #include "grx_internal.h"
@@ -41,6 +44,38 @@ hipError_t grx_pinned_malloc(void **p, size_t bytes) {
 extern "C" void grx_debug_fail_alloc_after(long long n) { g_alloc_countdown.store(n < 0 ? -1 : n); }
 
 extern "C" long long grx_debug_alloc_countdown(void) { return g_alloc_countdown.load(); }
+
+// The kernel-choice table: names (the GRX_* environment variables without
+// their prefix) in the order of the GRX_TUNE_* ids.
+static const char *const kTuneNames[GRX_TUNE_COUNT] = {
+    "GEMM_MIN_M", "GEMM_KERNEL", "GEMM_NS",    "GEMM_KB",     "GEMV_WAVES",    "GEMV1",
+    "CONF_ATTN_RQ", "FUSE_LN",   "FUSE_XSCORES", "WAVE_VALUES", "ARGMAX_ATOMIC", "NO_GRAPH"};
+static std::atomic<int> g_tune[GRX_TUNE_COUNT];
+static std::once_flag g_tune_once;
+
+static void tune_init() {
+    for (int i = 0; i < GRX_TUNE_COUNT; ++i) {
+        const std::string env = std::string("GRX_") + kTuneNames[i];
+        const char *v = getenv(env.c_str());
+        g_tune[i].store(v && v[0] ? atoi(v) : -1);
+    }
+}
+
+int grx_tune(int id) {
+    std::call_once(g_tune_once, tune_init);
+    return (id >= 0 && id < GRX_TUNE_COUNT) ? g_tune[id].load(std::memory_order_relaxed) : -1;
+}
+
+extern "C" grx_status grx_debug_tune(const char *name, int value) {
+    std::call_once(g_tune_once, tune_init);
+    if (name != nullptr)
+        for (int i = 0; i < GRX_TUNE_COUNT; ++i)
+            if (strcmp(name, kTuneNames[i]) == 0) {
+                g_tune[i].store(value < 0 ? -1 : value);
+                return GRX_OK;
+            }
+    return grx_fail(GRX_EINVAL, "grx_debug_tune: no setting named %s", name ? name : "(null)");
+}
 
 grx_status grx_fail(grx_status s, const char *fmt, ...) {
     char buf[512];

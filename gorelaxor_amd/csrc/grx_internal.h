@@ -83,6 +83,26 @@ grx_status grx_sample_run(grx_ctx *ctx, const float *dev_logits, const float *ho
 grx_status grx_gguf_tensor_data(const grx_gguf *g, const char *name, int *type, std::vector<uint8_t> *out);
 #endif
 grx_status grx_hip_fail(hipError_t e, const char *what);
+
+// Kernel choices that tests and profiles override (grx_debug_tune; the
+// GRX_* environment variable of the same name, read once when the library
+// first asks, sets the starting value).  -1 means "the library's own choice".
+enum {
+    GRX_TUNE_GEMM_MIN_M,      // fewest rows that take the matrix-core product
+    GRX_TUNE_GEMM_KERNEL,     // 1 the whole-K register kernel, 2 the K-split one, 3 the LDS-staged one
+    GRX_TUNE_GEMM_NS,         // 16-column tiles per wave of the register kernels: 1, 2 or 4
+    GRX_TUNE_GEMM_KB,         // blocks per wave of the K-split kernel: 4, 8 or 16
+    GRX_TUNE_GEMV_WAVES,      // waves per tile of the GEMV: 1, 2, 4, 8 or 16
+    GRX_TUNE_GEMV1,           // 0: one-row products on the general GEMV kernel
+    GRX_TUNE_CONF_ATTN_RQ,    // conformer attention: 0 unstaged, 8 or 16 query rows per workgroup
+    GRX_TUNE_FUSE_LN,         // 0: batched decoder LayerNorm rows in their own launch
+    GRX_TUNE_FUSE_XSCORES,    // 0: whisper cross scores without the fused query product
+    GRX_TUNE_WAVE_VALUES,     // 0: whisper cross values on the wide-workgroup kernel
+    GRX_TUNE_ARGMAX_ATOMIC,   // 1: the decoders' argmax through a contended atomic
+    GRX_TUNE_NO_GRAPH,        // 1: model loops launch kernel by kernel (no HIP graphs)
+    GRX_TUNE_COUNT
+};
+int grx_tune(int id);
 // Every device and pinned allocation of the library: hipMalloc and
 // hipHostMalloc, or the out-of-memory failure grx_debug_fail_alloc_after
 // injects.

@@ -376,8 +376,7 @@ extern "C" grx_status grx_pocket_speak(grx_pocket *m, const float *first_latent,
                            first_latent ? hipMemcpyHostToDevice : hipMemcpyDeviceToDevice, st));
     GRX_HIP(hipMemcpyAsync(m->flow.noise, noise, (size_t)n * hp.ldim * 4, hipMemcpyHostToDevice, st));
     GRX_HIP(hipMemsetAsync(m->frame, 0, 4, st));
-    const char *ng = getenv("GRX_NO_GRAPH");
-    const bool eager = ng && ng[0] == '1';
+    const bool eager = grx_tune(GRX_TUNE_NO_GRAPH) == 1;
     auto one = [&]() {
         grx_status cs = pocket_enqueue_frame(m, st, m->lat, m->frame);
         return cs == GRX_OK ? pocket_flow_enqueue(m, st) : cs;

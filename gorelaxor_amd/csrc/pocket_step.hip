@@ -757,8 +757,7 @@ extern "C" grx_status grx_pocket_frames(grx_pocket *m, const float *latents, int
             GRX_HIP(hipMemcpyAsync(m->lat + (size_t)k * hp.ldim, m->bos, (size_t)hp.ldim * 4, hipMemcpyDeviceToDevice,
                                    st));
     GRX_HIP(hipMemsetAsync(m->frame, 0, 4, st));
-    const char *ng = getenv("GRX_NO_GRAPH");
-    const bool eager = ng && ng[0] == '1';
+    const bool eager = grx_tune(GRX_TUNE_NO_GRAPH) == 1;
     for (int k = 0; k < n; ++k) {
         if (eager || (!m->exec && k == 0)) {
             if ((s = enqueue_frame(m, st, m->lat, m->frame)) != GRX_OK) return s;

@@ -19,6 +19,7 @@
 // and four activation scales.  The per-output fold (convert, multiply, fma:
 // 3 VALU ops per output per block) is the bound, not the MFMA: exact
 // per-block scaling costs that much vector work per 32 multiply-adds.
+#include <cstdint>
 #include <cstdlib>
 #include <type_traits>
 
@@ -224,6 +225,196 @@ tail:
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 if (!drow_ok[r]) continue;
+                float *yp = y + (size_t)drow[r] * ldc + n;
+                if constexpr (EPI == GRX_GEMM_STORE) *yp = c[s][r];
+                if constexpr (EPI == GRX_GEMM_ADD) *yp = __fadd_rn(*yp, c[s][r]);
+                if constexpr (EPI == GRX_GEMM_AXPY_HALF) *yp = __fmaf_rn(0.5f, c[s][r], *yp);
+                if constexpr (EPI == GRX_GEMM_SCALE) *yp = __fmul_rn(c[s][r], scale);
+            }
+        }
+    }
+}
+
+// The product for fewer rows (m < 256: one utterance's encoder rows, a
+// streaming chunk): a workgroup owns one output tile of 16 activation rows x
+// 16*NS weight rows and splits the weight's blocks among its ks waves, KB
+// consecutive blocks each, so that even a 1024-row product puts thousands of
+// waves on the device and every wave issues all of its loads at once (the
+// whole-K register walk above waits out one memory latency per U blocks).
+// Each wave takes its blocks' int32 dots on the matrix cores and forms
+// t_b = f32(s_b) * dw_b for them (order-free); the ordered chain
+// c = fma(t_b, da_b, c) then runs wave after wave: wave 0 from the bias over
+// blocks 0..KB-1, and each next wave from the c the previous one left in
+// LDS, so every output sees the blocks in order, as in the other kernels.
+// The tiles are numbered so that the workgroups of one weight column group
+// (the row groups of the activations) land on one XCD and share its L2:
+// workgroup i runs on XCD i % 8.
+constexpr int kKsMaxWaves = 8;
+
+template <int EPI, int NS, int KB>
+__global__ __launch_bounds__(64 * kKsMaxWaves) void gemm_q8_ks_kernel(
+    const int8_t *__restrict__ qs, const uint16_t *__restrict__ ds, int rows, int nb, const int8_t *__restrict__ xq,
+    const float *__restrict__ xs, int m, const float *__restrict__ bias, float *__restrict__ y, int ldc, float scale,
+    int8_t *__restrict__ yq, float *__restrict__ ys, int ncg, int nrf, int da4) {
+    static_assert(NS == 1 || NS == 2, "16 or 32 weight rows per tile");
+    static_assert(KB % 4 == 0, "blocks per wave in whole groups of four");
+    __shared__ float cx[2][NS * 4][64];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int ks = __builtin_amdgcn_readfirstlane(blockDim.x >> 6);
+    const int gi = blockIdx.x, xcd = gi & 7, slot = gi >> 3;
+    const int rf = slot % nrf, cg = (slot / nrf) * 8 + xcd;
+    if (cg >= ncg) return;  // the whole workgroup: no barrier is skipped
+    const int K = nb * GRX_QK;
+    const int li = lane & 15, lk = lane >> 4;
+    const int n0 = cg * 16 * NS;                          // first weight row of the tile
+    const int tile = n0 >> 6, sub = n0 & 63;              // 64-row weight tile, row offset in it
+    const int b0 = wave * KB;
+    const int nbw = min(KB, nb - b0);                     // this wave's blocks (>= 1)
+
+    // A: activation row 16*rf+li (clamped: rows past m are computed, never
+    // stored), bytes 8*lk.. of each block
+    const int arow = min(16 * rf + li, m - 1);
+    const int8_t *ap = xq + (size_t)arow * K + 8 * lk;
+    const int8_t *bp = qs + (size_t)tile * nb * 2048 + (lk >> 1) * 1024 + (sub + li) * 16 + 8 * (lk & 1);
+    const uint16_t *dp = ds + (size_t)tile * nb * 64 + sub + li;
+    // D: lane holds weight row n0+16s+li, activation rows 16*rf+4*lk+r
+    int drow[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) drow[r] = 16 * rf + 4 * lk + r;
+    const float *sp[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) sp[r] = xs + (size_t)min(drow[r], m - 1) * nb;
+
+    // every load of the wave's blocks in flight at once (the last wave's
+    // block indices past nb are clamped and their results never used)
+    long av[KB], bv[KB][NS];
+    uint16_t dh[KB][NS];
+    float da[KB][4];
+#pragma unroll
+    for (int u = 0; u < KB; ++u) {
+        const int b = min(b0 + u, nb - 1);
+        av[u] = *reinterpret_cast<const long *>(ap + (size_t)b * GRX_QK);
+#pragma unroll
+        for (int s = 0; s < NS; ++s) {
+            bv[u][s] = *reinterpret_cast<const long *>(bp + (size_t)b * 2048 + s * 256);
+            dh[u][s] = dp[(size_t)b * 64 + 16 * s];
+        }
+    }
+    if (da4) {  // nb % 4 == 0 and xs 16-byte aligned: four blocks per load
+#pragma unroll
+        for (int q = 0; q < KB / 4; ++q) {
+            const int b = min(b0 + 4 * q, nb - 4);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const float4 v = *reinterpret_cast<const float4 *>(sp[r] + b);
+                da[4 * q + 0][r] = v.x;
+                da[4 * q + 1][r] = v.y;
+                da[4 * q + 2][r] = v.z;
+                da[4 * q + 3][r] = v.w;
+            }
+        }
+    } else {
+#pragma unroll
+        for (int u = 0; u < KB; ++u) {
+            const int b = min(b0 + u, nb - 1);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) da[u][r] = sp[r][b];
+        }
+    }
+    // the block dots and their scaled forms t = f32(s) * dw
+    float t[KB][NS][4];
+#pragma unroll
+    for (int u = 0; u < KB; ++u)
+#pragma unroll
+        for (int s = 0; s < NS; ++s) {
+            v4i d = {0, 0, 0, 0};
+            d = __builtin_amdgcn_mfma_i32_16x16x32_i8(av[u], bv[u][s], d, 0, 0, 0);
+            const float dw = grx_f16_to_f32(dh[u][s]);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) t[u][s][r] = __fmul_rn((float)d[r], dw);
+        }
+
+    // the ordered chain, one wave after another
+    float c[NS][4];
+    for (int p = 0; p < ks; ++p) {
+        if (wave == p) {
+            if (p == 0) {
+#pragma unroll
+                for (int s = 0; s < NS; ++s) {
+                    const int n = n0 + 16 * s + li;
+                    const float bv0 = (bias != nullptr && n < rows) ? bias[n] : 0.0f;
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) c[s][r] = bv0;
+                }
+            } else {
+#pragma unroll
+                for (int s = 0; s < NS; ++s)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) c[s][r] = cx[(p - 1) & 1][4 * s + r][lane];
+            }
+#pragma unroll
+            for (int u = 0; u < KB; ++u) {
+                if (u < nbw) {
+#pragma unroll
+                    for (int s = 0; s < NS; ++s)
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) c[s][r] = __fmaf_rn(t[u][s][r], da[u][r], c[s][r]);
+                }
+            }
+            if (p + 1 < ks) {
+#pragma unroll
+                for (int s = 0; s < NS; ++s)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) cx[p & 1][4 * s + r][lane] = c[s][r];
+            }
+        }
+        if (p + 1 < ks) __syncthreads();
+    }
+    if (wave != ks - 1) return;
+
+    if constexpr (EPI == GRX_GEMM_SILU_Q) {
+        // the tile's 32 columns are one Q8_0 block (rows % 32 == 0): a row's
+        // block maximum is four xor-shuffles among the 16 lanes sharing lk
+        static_assert(NS == 2, "rounded output needs whole 32-column blocks per tile");
+        const int nr = rows / GRX_QK;
+        const bool col_ok = n0 < rows;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            float v[2];
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const float x = c[h][r];
+                v[h] = __fdiv_rn(x, __fadd_rn(grx_exp8(__fsub_rn(0.0f, x)), 1.0f));
+            }
+            const float a0 = fabsf(v[0]), a1 = fabsf(v[1]);
+            float amax = a0 > 0.0f ? a0 : 0.0f;
+            amax = a1 > amax ? a1 : amax;
+#pragma unroll
+            for (int o = 8; o > 0; o >>= 1) {
+                const float tt = __shfl_xor(amax, o, 16);
+                amax = tt > amax ? tt : amax;
+            }
+            const float id = amax != 0.0f ? __fdiv_rn(127.0f, amax) : 0.0f;
+            if (col_ok && drow[r] < m) {
+                int8_t *qrow = yq + (size_t)drow[r] * rows + n0;
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+                    float q = rintf(__fmul_rn(v[h], id));
+                    q = fminf(fmaxf(q, -128.0f), 127.0f);
+                    qrow[16 * h + li] = (int8_t)(int)q;
+                }
+                if (li == 0) ys[(size_t)drow[r] * nr + n0 / GRX_QK] = __fmul_rn(amax, grx_bits_f32(0x3c010204u));
+            }
+        }
+    } else {
+#pragma unroll
+        for (int s = 0; s < NS; ++s) {
+            const int n = n0 + 16 * s + li;
+            if (n >= rows) continue;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                if (drow[r] >= m) continue;
                 float *yp = y + (size_t)drow[r] * ldc + n;
                 if constexpr (EPI == GRX_GEMM_STORE) *yp = c[s][r];
                 if constexpr (EPI == GRX_GEMM_ADD) *yp = __fadd_rn(*yp, c[s][r]);
@@ -467,10 +658,8 @@ __global__ __launch_bounds__(kLdsThreads) void gemm_q8_lds_kernel(const int8_t *
 // Column-group width for a product: enough waves to cover the device
 // (16*NS weight rows per wave), NS = 4 once there are plenty.
 int pick_ns(int m, int rows, int epi) {
-    if (const char *e = getenv("GRX_GEMM_NS")) {
-        const int v = atoi(e);
-        if (v == 1 || v == 2 || v == 4) return (epi == GRX_GEMM_SILU_Q && v == 1) ? 2 : v;
-    }
+    const int v = grx_tune(GRX_TUNE_GEMM_NS);
+    if (v == 1 || v == 2 || v == 4) return (epi == GRX_GEMM_SILU_Q && v == 1) ? 2 : v;
     // (measured at 64 and 126 rows: two 16-column tiles per wave win from
     // about 384 of these on, e.g. 126 x 4096 x 1024 14.0 -> 10.0 us)
     const long waves4 = (long)grx_ceil_div(m, 16) * grx_ceil_div(rows, 64);
@@ -479,17 +668,68 @@ int pick_ns(int m, int rows, int epi) {
     return ns;
 }
 
+// The K-split kernel's tile width and blocks per wave.  Measured on the
+// encoder's products at 14 and 126 rows (MI355X): 32-column tiles with 8
+// blocks per wave for K up to 2048 (126 x 1024 x 1024 7.7 -> 5.5 us,
+// 14 x 4096 x 1024 5.9 -> 4.8 us), 16-column tiles with 16 blocks per wave
+// past that (126 x 1024 x 4096 25 -> 19 us); the rounded SiLU output needs
+// the 32-column tiles (whole Q8_0 blocks).  False when a workgroup of
+// kKsMaxWaves waves cannot hold the weight's blocks.
+bool pick_ks(int nb, int epi, int *ns, int *kb) {
+    int n = (epi == GRX_GEMM_SILU_Q || nb <= 2 * kKsMaxWaves * 4) ? 2 : 1;
+    const int tn = grx_tune(GRX_TUNE_GEMM_NS);
+    if (tn == 1 || tn == 2) n = (epi == GRX_GEMM_SILU_Q) ? 2 : tn;
+    const int kbmax = n == 2 ? 8 : 16;
+    if (nb > kKsMaxWaves * kbmax) return false;
+    int k = n == 2 ? 8 : 16;
+    const int tk = grx_tune(GRX_TUNE_GEMM_KB);
+    if ((tk == 4 || tk == 8 || tk == 16) && tk <= kbmax && nb <= kKsMaxWaves * tk) k = tk;
+    *ns = n;
+    *kb = k;
+    return true;
+}
+
+template <int EPI, int NS, int KB>
+void launch_ks(hipStream_t st, const grx_weight *w, const int8_t *xq, const float *xs, int m, const float *bias,
+               const GemmOut &o, int da4) {
+    const int ncg = grx_ceil_div(w->rows, 16 * NS), nrf = grx_ceil_div(m, 16);
+    const int ks = grx_ceil_div(w->nb, KB);
+    const int groups = grx_ceil_div(ncg, 8) * 8 * nrf;
+    gemm_q8_ks_kernel<EPI, NS, KB><<<groups, 64 * ks, 0, st>>>(w->qs, w->ds, w->rows, w->nb, xq, xs, m, bias, o.y,
+                                                               o.ldc, o.scale, o.yq, o.ys, ncg, nrf, da4);
+}
+
+template <int EPI>
+void launch_ks_epi(hipStream_t st, const grx_weight *w, const int8_t *xq, const float *xs, int m, const float *bias,
+                   const GemmOut &o, int ns, int kb, int da4) {
+    if constexpr (EPI != GRX_GEMM_SILU_Q) {
+        if (ns == 1) {
+            if (kb == 4) return launch_ks<EPI, 1, 4>(st, w, xq, xs, m, bias, o, da4);
+            if (kb == 8) return launch_ks<EPI, 1, 8>(st, w, xq, xs, m, bias, o, da4);
+            return launch_ks<EPI, 1, 16>(st, w, xq, xs, m, bias, o, da4);
+        }
+    }
+    if (kb == 4) return launch_ks<EPI, 2, 4>(st, w, xq, xs, m, bias, o, da4);
+    return launch_ks<EPI, 2, 8>(st, w, xq, xs, m, bias, o, da4);
+}
+
 }  // namespace
 
 grx_status grx_gemm_q8_launch_ex(hipStream_t st, const grx_weight *w, const int8_t *xq, const float *xs, int m,
                                  const float *bias, const GemmOut &o) {
     if (m <= 0 || w->rows == 0) return GRX_OK;
+    if (o.epi < GRX_GEMM_STORE || o.epi > GRX_GEMM_SILU_Q)
+        return grx_fail(GRX_EINVAL, "unknown product epilogue %d", o.epi);
     if (o.epi == GRX_GEMM_SILU_Q && w->rows % GRX_QK != 0)
         return grx_fail(GRX_ESIZE, "rounded product output needs rows %% 32 == 0 (rows %d)", w->rows);
-    // GRX_GEMM_LDS_MIN_M overrides the row count from which the LDS-staged
-    // tiles run (tests force each kernel with it)
-    const char *lm = getenv("GRX_GEMM_LDS_MIN_M");
-    if (m >= (lm ? atoi(lm) : 256)) {  // many rows: the LDS-staged 64 x 128 tiles
+    // GEMM_KERNEL picks the kernel (tests force each one with it): the
+    // LDS-staged tiles from 256 rows on, the whole-K register walk from 129
+    // (e.g. 224 x 1024 x 4096: 26 us against 36 for the K-split tiles), the
+    // K-split tiles up to 128
+    const int kind = grx_tune(GRX_TUNE_GEMM_KERNEL);
+    int ks_ns = 1, ks_kb = 4;
+    const bool ks_ok = pick_ks(w->nb, o.epi, &ks_ns, &ks_kb) && (kind == 2 || m <= 128);
+    if (kind == 3 || (kind != 1 && kind != 2 && m >= 256)) {  // many rows: the LDS-staged 64 x 128 tiles
         dim3 g2(grx_ceil_div(m, 64), grx_ceil_div(w->tiles, 2));
 #define GRX_GEMM_LDS(E)                                                                                           \
     case E:                                                                                                       \
@@ -502,11 +742,23 @@ grx_status grx_gemm_q8_launch_ex(hipStream_t st, const grx_weight *w, const int8
             GRX_GEMM_LDS(GRX_GEMM_AXPY_HALF)
             GRX_GEMM_LDS(GRX_GEMM_SCALE)
             GRX_GEMM_LDS(GRX_GEMM_SILU_Q)
-            default:
-                return grx_fail(GRX_EINVAL, "unknown product epilogue %d", o.epi);
         }
 #undef GRX_GEMM_LDS
         GRX_LAUNCHED("gemm_q8_lds_kernel");
+        return GRX_OK;
+    }
+    if (kind != 1 && ks_ok) {  // fewer rows: the K-split tiles
+        const int da4 = (w->nb % 4 == 0 && ((uintptr_t)xs & 15) == 0) ? 1 : 0;
+        switch (o.epi) {
+            case GRX_GEMM_STORE: launch_ks_epi<GRX_GEMM_STORE>(st, w, xq, xs, m, bias, o, ks_ns, ks_kb, da4); break;
+            case GRX_GEMM_ADD: launch_ks_epi<GRX_GEMM_ADD>(st, w, xq, xs, m, bias, o, ks_ns, ks_kb, da4); break;
+            case GRX_GEMM_AXPY_HALF:
+                launch_ks_epi<GRX_GEMM_AXPY_HALF>(st, w, xq, xs, m, bias, o, ks_ns, ks_kb, da4);
+                break;
+            case GRX_GEMM_SCALE: launch_ks_epi<GRX_GEMM_SCALE>(st, w, xq, xs, m, bias, o, ks_ns, ks_kb, da4); break;
+            case GRX_GEMM_SILU_Q: launch_ks_epi<GRX_GEMM_SILU_Q>(st, w, xq, xs, m, bias, o, 2, ks_kb, da4); break;
+        }
+        GRX_LAUNCHED("gemm_q8_ks_kernel");
         return GRX_OK;
     }
     const int ns = pick_ns(m, w->rows, o.epi);
@@ -534,8 +786,6 @@ grx_status grx_gemm_q8_launch_ex(hipStream_t st, const grx_weight *w, const int8
             else
                 GRX_GEMM_GO(GRX_GEMM_SILU_Q, 2, GRX_GEMM_U2);
             break;
-        default:
-            return grx_fail(GRX_EINVAL, "unknown product epilogue %d", o.epi);
     }
 #undef GRX_GEMM_CASE
 #undef GRX_GEMM_GO

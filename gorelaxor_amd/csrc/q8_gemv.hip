@@ -892,11 +892,10 @@ __global__ __launch_bounds__(64 * W) void gemv1_kernel(const GemvArgs a) {
     }
 }
 
-// One-row products take gemv1_kernel unless GRX_GEMV1=0 (the general
-// kernel, for comparisons) or the row is too wide for its prologue.
+// One-row products take gemv1_kernel unless GEMV1 is tuned to 0 (the
+// general kernel, for comparisons) or the row is too wide for its prologue.
 bool gemv1_fits(int pro, int nb) {
-    const char *f = getenv("GRX_GEMV1");
-    if (f && f[0] == '0') return false;
+    if (grx_tune(GRX_TUNE_GEMV1) == 0) return false;
     return pro == GRX_PRO_PREQ || nb * GRX_QK <= kRowPieces * 256;
 }
 
@@ -1081,10 +1080,10 @@ hipError_t launch_m(hipStream_t st, int m, const GemvArgs &a, int tiles, int W) 
 
 // Waves per tile: enough tiles x waves to cover the CUs, never more waves
 // than blocks, and the workgroup's LDS within 64 KiB.
-// GRX_GEMV_WAVES (1, 2, 4, 8 or 16) forces the choice, for tests.
+// GEMV_WAVES (1, 2, 4, 8 or 16) forces the choice, for tests.
 int grx_gemv_pick_waves(int tiles, int nb, int m, int pro) {
-    if (const char *f = getenv("GRX_GEMV_WAVES")) {
-        const int w = atoi(f);
+    {
+        const int w = grx_tune(GRX_TUNE_GEMV_WAVES);
         if (w == 1 || w == 2 || w == 4 || w == 8 || w == 16) return w;
     }
     const size_t lim = m > 1 ? kMultiLds : 64 * 1024;
@@ -1153,11 +1152,8 @@ static grx_status check_mm(const char *fn, grx_ctx *ctx, const void *dst, int ld
 }
 
 int grx_gemm_min_m(void) {
-    if (const char *f = getenv("GRX_GEMM_MIN_M")) {
-        const int v = atoi(f);
-        if (v > 0) return v;
-    }
-    return 16;
+    const int v = grx_tune(GRX_TUNE_GEMM_MIN_M);
+    return v > 0 ? v : 16;
 }
 
 // Many rows on the matrix cores; few rows in GEMV launches of 8, 4, 2 and 1.

@@ -782,8 +782,7 @@ extern "C" grx_status grx_rnnt_decode(grx_rnnt *m, const float *enc, int T, int 
         GRX_HIP(hipMemsetAsync(m->S, 0, hcb, s0));
     rnnt_ctl_init_kernel<<<1, 64, 0, s0>>>(m->ctl, T, max_iters, frame_offset, st ? st->last : -1);
     GRX_LAUNCHED("rnnt_ctl_init_kernel");
-    const char *ng = getenv("GRX_NO_GRAPH");
-    const bool eager = ng && ng[0] == '1';
+    const bool eager = grx_tune(GRX_TUNE_NO_GRAPH) == 1;
     if (!eager && !m->exec) {
         GRX_HIP(hipStreamSynchronize(s0));
         hipError_t e = hipStreamBeginCapture(s0, hipStreamCaptureModeThreadLocal);

@@ -754,11 +754,8 @@ GemvArgs gemv_args(const grx_weight *w) {
     return a;
 }
 
-// An environment switch set to "0" (for comparisons in tests).
-bool getenv_off(const char *name) {
-    const char *f = getenv(name);
-    return f && f[0] == '0';
-}
+// A kernel choice tuned to 0 (for comparisons in tests).
+bool tuned_off(int id) { return grx_tune(id) == 0; }
 
 // The launches of one decode step on stream st.
 grx_status enqueue_step(grx_whisper *m, hipStream_t stream) {
@@ -796,7 +793,7 @@ grx_status enqueue_step(grx_whisper *m, hipStream_t stream) {
     // one wave per row (rows up to 1280 values); wider rows are LayerNorm'd
     // and rounded once by a row kernel and read pre-rounded
     // (GRX_FUSE_LN=0 takes that route for every width).
-    const bool sep = S > 1 && (st > 1280 || getenv_off("GRX_FUSE_LN"));
+    const bool sep = S > 1 && (st > 1280 || tuned_off(GRX_TUNE_FUSE_LN));
     auto ln_rows = [&](const float *w, const float *b, GemvArgs &a) {
         a.xq = m->ln_q;
         a.xs = m->ln_s;
@@ -860,7 +857,7 @@ grx_status enqueue_step(grx_whisper *m, hipStream_t stream) {
         if ((s = out_proj(L.o, L.o_b, qatt)) != GRX_OK) return s;
         // one stream, heads of 64: the cross query's tile of each head is
         // computed inside the scores kernel (one launch instead of two)
-        const bool fused_scores = S == 1 && hd == 64 && st >= 512 && st <= 1280 && !getenv_off("GRX_FUSE_XSCORES");
+        const bool fused_scores = S == 1 && hd == 64 && st >= 512 && st <= 1280 && !tuned_off(GRX_TUNE_FUSE_XSCORES);
         if (fused_scores) {
             GemvArgs a = gemv_args(L.xq);
             a.x = m->x;
@@ -891,7 +888,7 @@ grx_status enqueue_step(grx_whisper *m, hipStream_t stream) {
         // workgroups over 16 outputs each, float32 out (the cross-out product
         // rounds its rows in its prologue; several streams: a wave per row)
         const bool wave_values = nctx <= kWaveCtx && hd % kWaveOut == 0 && (S == 1 || st <= 1280) &&
-                                 !getenv_off("GRX_WAVE_VALUES");
+                                 !tuned_off(GRX_TUNE_WAVE_VALUES);
         if (wave_values) {
             cross_values_wave_kernel<<<dim3(nh, hd / kWaveOut, S), 256, 0, stream>>>(m->scores, L.cross_v, nctx,
                                                                                      hd, st, x_stream, m->att);
@@ -948,8 +945,8 @@ grx_status enqueue_step(grx_whisper *m, hipStream_t stream) {
         a.y = m->logits;
         a.ldc = hp.n_vocab;
         // per-workgroup argmax keys and a one-workgroup end of step (no
-        // contended atomics); GRX_ARGMAX_ATOMIC=1 takes the atomic form
-        static const bool atomic_form = getenv("GRX_ARGMAX_ATOMIC") && getenv("GRX_ARGMAX_ATOMIC")[0] == '1';
+        // contended atomics); ARGMAX_ATOMIC tuned to 1 takes the atomic form
+        const bool atomic_form = grx_tune(GRX_TUNE_ARGMAX_ATOMIC) == 1;
         a.amax = m->amax;
         if (atomic_form)
             a.counter = m->counter;
@@ -970,8 +967,7 @@ grx_status enqueue_step(grx_whisper *m, hipStream_t stream) {
 // the same launches directly.
 grx_status run_step(grx_whisper *m) {
     hipStream_t stream = m->ctx->stream;
-    const char *ng = getenv("GRX_NO_GRAPH");
-    if (ng && ng[0] == '1') return enqueue_step(m, stream);
+    if (grx_tune(GRX_TUNE_NO_GRAPH) == 1) return enqueue_step(m, stream);
     if (!m->exec) {
         // an eager step first sets every kernel's attributes outside capture;
         // its effect is undone by the caller's bookkeeping (it runs the step

@@ -245,8 +245,35 @@ def layernorm_dev(form: int, impl: int, y, x, rows: int, n: int, w=None, b=None,
               _ptr(w) if w is not None else None, _ptr(b) if b is not None else None, float(eps))
 
 
+def set_tune(name: str, value: int) -> None:
+    """Override one of the library's kernel choices (grx_debug_tune: GEMM_MIN_M,
+    GEMM_KERNEL, GEMM_NS, GEMM_KB, GEMV_WAVES, GEMV1, CONF_ATTN_RQ, FUSE_LN,
+    FUSE_XSCORES, WAVE_VALUES, ARGMAX_ATOMIC, NO_GRAPH); -1 hands it back.
+    The reference's tests switch kernels the same way (setInt, internal/kern/
+    kernels_amd64.go:190-200)."""
+    _lib.call("grx_debug_tune", name.encode(), int(value))
+
+
+class tuned:
+    """Context manager: the kernel choices given as keywords for the block,
+    handed back to the library afterwards."""
+
+    def __init__(self, **choices):
+        self.choices = {k: int(v) for k, v in choices.items()}
+
+    def __enter__(self):
+        for k, v in self.choices.items():
+            set_tune(k, v)
+        return self
+
+    def __exit__(self, *exc):
+        for k in self.choices:
+            set_tune(k, -1)
+        return False
+
+
 __all__ = ["QK", "Q8Bytes", "F32", "F16", "Q8_0", "Context", "default_context", "device_count", "Weight",
            "NewQ8", "ToQ8", "MatMul", "Linear", "LinearFloat", "LinearF32", "matmul_dev", "matmul_dev_noalloc",
            "quant_act_dev", "matmul_prequant_dev",
            "block_dots_dev", "vec_dev", "VEC_EXPF", "VEC_EXP8", "VEC_GELU", "layernorm_dev", "LN_KERN", "LN_F64",
-           "LN_BLOCK", "LN_WAVE", "LN_TREE_ONLY", "GrxError"]
+           "LN_BLOCK", "LN_WAVE", "LN_TREE_ONLY", "GrxError", "set_tune", "tuned"]

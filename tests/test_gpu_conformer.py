@@ -59,18 +59,18 @@ def test_tiny_float32_pre_encoder_pointwise(kern, orc, seconds):
     enc.close()
 
 
-@pytest.mark.parametrize("rq", ["0", "8", "16"])
-def test_tiny_attention_variants_bit_exact(kern, orc, monkeypatch, rq):
+@pytest.mark.parametrize("rq", [0, 8, 16])
+def test_tiny_attention_variants_bit_exact(kern, orc, rq):
     """The unstaged attention kernel and the LDS-staged one at 8 and 16 query
     rows per workgroup give the same bits as the oracle (T = 19: one query
     block, rows in the 6x16 panels and in gemvRows)."""
-    monkeypatch.setenv("GRX_CONF_ATTN_RQ", rq)
     hp = dict(CONFORMER_TINY)
     t = conformer_model(hp, seed=24)
     mel, frames, valid = _mels(hp, 2, 1.5, 35)
     vals = [valid, valid - 30]
-    enc = _enc(kern, hp, t)
-    got, lens = enc.encode(mel, vals)
+    with kern.tuned(CONF_ATTN_RQ=rq):
+        enc = _enc(kern, hp, t)
+        got, lens = enc.encode(mel, vals)
     o = orc.ConformerOracle(hp, t)
     for b in range(2):
         want, L = o.encode(mel[b], vals[b])

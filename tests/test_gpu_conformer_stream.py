@@ -92,13 +92,13 @@ def test_stream_long_left_context(kern, orc, right):
     assert _stream_case(kern, orc, STREAM_TINY, t, right, 8.0, 62) >= 99
 
 
-@pytest.mark.parametrize("rq", ["0", "8", "16"])
-def test_stream_attention_kernels(kern, orc, monkeypatch, rq):
+@pytest.mark.parametrize("rq", [0, 8, 16])
+def test_stream_attention_kernels(kern, orc, rq):
     """Each attention kernel form on the chunk steps: unstaged, and staged
     with 8 or 16 query rows per workgroup."""
-    monkeypatch.setenv("GRX_CONF_ATTN_RQ", rq)
     t = conformer_model(STREAM_TINY28, seed=39, pointwise_f16=True)
-    assert _stream_case(kern, orc, STREAM_TINY28, t, 6, 3.0, 63, f" rq {rq}") >= 35
+    with kern.tuned(CONF_ATTN_RQ=rq):
+        assert _stream_case(kern, orc, STREAM_TINY28, t, 6, 3.0, 63, f" rq {rq}") >= 35
 
 
 def test_streams_together_equal_alone(kern, orc):

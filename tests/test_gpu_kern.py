@@ -187,83 +187,78 @@ def test_matmul_odd_sizes_bit_exact(kern, orc, m):
             _check_matmul(kern, orc, rng, m, n, k, bias=(n % 2 == 1))
 
 
-@pytest.mark.parametrize("waves", ["1", "2", "4", "8", "16"])
+@pytest.mark.parametrize("waves", [1, 2, 4, 8, 16])
 def test_matmul_every_wave_split(kern, orc, waves):
     """Splitting a tile's blocks over 1..16 waves (ordered chain in LDS)
     changes no bit."""
     rng = np.random.default_rng(31)
-    os.environ["GRX_GEMV_WAVES"] = waves
-    try:
+    with kern.tuned(GEMV_WAVES=waves):
         for m, n, k in ((1, 200, 1024), (2, 64, 512), (4, 70, 2048), (8, 130, 1280), (1, 64, 5120)):
             _check_matmul(kern, orc, rng, m, n, k)
-    finally:
-        del os.environ["GRX_GEMV_WAVES"]
 
 
-@pytest.mark.parametrize("gemv1", ["0", "1"])
+@pytest.mark.parametrize("gemv1", [0, 1])
 def test_matmul_one_row_kernels(kern, orc, gemv1):
-    """One-row products through the decode kernel (GRX_GEMV1=1: loads issued
+    """One-row products through the decode kernel (GEMV1=1: loads issued
     before the prologue, batched fold, partial last batch) and the general
-    kernel (GRX_GEMV1=0), every wave split, block counts that leave waves
+    kernel (GEMV1=0), every wave split, block counts that leave waves
     with 1, 2, 3 and 10 blocks and a partial batch: every bit as the oracle."""
     rng = np.random.default_rng(57)
-    os.environ["GRX_GEMV1"] = gemv1
-    try:
-        for waves in ("1", "2", "4", "8", "16"):
-            os.environ["GRX_GEMV_WAVES"] = waves
-            for n, k in ((64, 32), (65, 96), (130, 512), (64, 1024), (200, 1280), (70, 1312), (64, 5120)):
-                _check_matmul(kern, orc, rng, 1, n, k, bias=(n % 2 == 0))
-    finally:
-        os.environ.pop("GRX_GEMV_WAVES", None)
-        del os.environ["GRX_GEMV1"]
+    with kern.tuned(GEMV1=gemv1):
+        for waves in (1, 2, 4, 8, 16):
+            with kern.tuned(GEMV_WAVES=waves):
+                for n, k in ((64, 32), (65, 96), (130, 512), (64, 1024), (200, 1280), (70, 1312), (64, 5120)):
+                    _check_matmul(kern, orc, rng, 1, n, k, bias=(n % 2 == 0))
 
 
-def test_matmul_matrix_cores_all_small_sizes(kern, orc):
-    """The matrix-core product forced for every m (GRX_GEMM_MIN_M=1): the
-    odd sizes again, bit-identical to the oracle."""
+@pytest.mark.parametrize("kernel", [1, 2])
+def test_matmul_matrix_cores_all_small_sizes(kern, orc, kernel):
+    """The matrix-core products forced for every m (GEMM_MIN_M=1), the
+    whole-K register kernel (1) and the K-split one (2): the odd sizes
+    again, bit-identical to the oracle."""
     rng = np.random.default_rng(41)
-    os.environ["GRX_GEMM_MIN_M"] = "1"
-    try:
+    with kern.tuned(GEMM_MIN_M=1, GEMM_KERNEL=kernel):
         for m in (1, 2, 7, 15, 16, 17, 63, 64, 65):
             for n in (1, 17, 64, 65, 129):
                 for k in (32, 96, 544):
                     _check_matmul(kern, orc, rng, m, n, k, bias=(n % 2 == 1))
-    finally:
-        del os.environ["GRX_GEMM_MIN_M"]
 
 
-@pytest.mark.parametrize("ns", ["1", "2", "4"])
+@pytest.mark.parametrize("ns", [1, 2, 4])
 def test_matmul_matrix_cores_each_tile_width(kern, orc, ns):
-    """Every wave-tile width of the matrix-core product (16, 32 or 64 weight
-    rows per wave, GRX_GEMM_NS) over block counts that hit each branch of
+    """Every wave-tile width of the register-walk product (16, 32 or 64
+    weight rows per wave, GEMM_NS) over block counts that hit each branch of
     its two-register-set walk (nb = 1 .. 40 around multiples of 4, 6, 8)."""
-    rng = np.random.default_rng(43 + int(ns))
-    os.environ["GRX_GEMM_MIN_M"] = "1"
-    os.environ["GRX_GEMM_NS"] = ns
-    try:
+    rng = np.random.default_rng(43 + ns)
+    with kern.tuned(GEMM_MIN_M=1, GEMM_KERNEL=1, GEMM_NS=ns):
         for nb in (1, 3, 4, 5, 6, 7, 8, 9, 11, 12, 13, 16, 17, 18, 24, 25, 40):
             for m, n in ((1, 64), (17, 100), (70, 130)):
                 _check_matmul(kern, orc, rng, m, n, 32 * nb, bias=(nb % 2 == 1))
-    finally:
-        del os.environ["GRX_GEMM_MIN_M"]
-        del os.environ["GRX_GEMM_NS"]
 
 
-@pytest.mark.parametrize("lds_min", ["1", "100000"])
-def test_matmul_lds_tiles_and_register_tiles(kern, orc, lds_min):
+@pytest.mark.parametrize("ns,kb", [(1, 4), (1, 8), (1, 16), (2, 4), (2, 8)])
+def test_matmul_k_split_each_shape(kern, orc, ns, kb):
+    """The K-split product at every tile width and blocks per wave (GEMM_NS,
+    GEMM_KB): block counts that give 1 to 8 waves per tile, a last wave with
+    1 to KB blocks, activation-scale rows not in whole groups of four, and
+    row counts with partial 16-row groups: bit-identical to the oracle."""
+    rng = np.random.default_rng(53 + 7 * ns + kb)
+    with kern.tuned(GEMM_MIN_M=1, GEMM_KERNEL=2, GEMM_NS=ns, GEMM_KB=kb):
+        for nb in sorted({1, 2, 3, 4, 5, 7, 8, 9, kb - 1, kb, kb + 1, 2 * kb + 3, 4 * kb, 8 * kb - 1, 8 * kb} - {0}):
+            for m, n in ((1, 64), (14, 100), (33, 130), (126, 48)):
+                _check_matmul(kern, orc, rng, m, n, 32 * nb, bias=(nb % 2 == 1))
+
+
+@pytest.mark.parametrize("kernel", [3, 1])
+def test_matmul_lds_tiles_and_register_tiles(kern, orc, kernel):
     """The LDS-staged 64 x 128 product forced for every row count
-    (GRX_GEMM_LDS_MIN_M=1), and the register-tiled one for every row count,
+    (GEMM_KERNEL=3), and the register-tiled one for every row count (1),
     over partial row, column and block groups: bit-identical to the oracle."""
     rng = np.random.default_rng(47)
-    os.environ["GRX_GEMM_MIN_M"] = "1"
-    os.environ["GRX_GEMM_LDS_MIN_M"] = lds_min
-    try:
+    with kern.tuned(GEMM_MIN_M=1, GEMM_KERNEL=kernel):
         for nb in (1, 3, 4, 5, 8, 9, 13):
             for m, n in ((1, 64), (20, 100), (64, 128), (65, 129), (200, 300)):
                 _check_matmul(kern, orc, rng, m, n, 32 * nb, bias=(m % 2 == 1))
-    finally:
-        del os.environ["GRX_GEMM_MIN_M"]
-        del os.environ["GRX_GEMM_LDS_MIN_M"]
 
 
 @pytest.mark.parametrize("m,n,k", [(126, 4096, 1024), (300, 1024, 1024), (1500, 512, 512), (251, 1024, 1024),

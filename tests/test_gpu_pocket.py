@@ -32,12 +32,9 @@ def test_prefix_and_frames_bit_exact(kern, orc, prefix):
 
 
 def test_frames_general_gemv_kernel(kern, orc):
-    """The same with one-row products on the general kernel (GRX_GEMV1=0)."""
-    os.environ["GRX_GEMV1"] = "0"
-    try:
+    """The same with one-row products on the general kernel (GEMV1=0)."""
+    with kern.tuned(GEMV1=0):
         _prefix_and_frames(orc, 3)
-    finally:
-        del os.environ["GRX_GEMV1"]
 
 
 def _prefix_and_frames(orc, prefix):

@@ -29,13 +29,13 @@ def _same(a, b):
     return np.array_equal(np.asarray(a, np.float32).view(np.uint32), np.asarray(b, np.float32).view(np.uint32))
 
 
-@pytest.mark.parametrize("gemv1", ["1", "0"])
+@pytest.mark.parametrize("gemv1", [1, 0])
 @pytest.mark.parametrize("shape", ["tiny", "ragged", "wide"])
 def test_decode_logits_bit_exact(kern, orc, shape, gemv1):
     """Every step's logits bit-identical, with the one-row decode kernel
-    (GRX_GEMV1=1, the default) and with the general product kernel.  The
+    (GEMV1=1, the default) and with the general product kernel.  The
     wide shape (d 512, heads of 64) takes the cross query inside the scores
-    kernel (GRX_FUSE_XSCORES=0 turns that off with the general kernel); its
+    kernel (FUSE_XSCORES=0 turns that off with the general kernel); its
     101 audio positions leave a partial last run of keys and three keys on
     dotF32Go's route."""
     hp = dict(WHISPER_TINY_TEST)
@@ -43,13 +43,8 @@ def test_decode_logits_bit_exact(kern, orc, shape, gemv1):
         hp.update(n_audio_ctx=101, n_head=4, n_state=96, n_vocab=333)
     if shape == "wide":
         hp.update(n_audio_ctx=101, n_head=8, n_state=512, n_vocab=333)
-    os.environ["GRX_GEMV1"] = gemv1
-    os.environ["GRX_FUSE_XSCORES"] = gemv1
-    try:
+    with kern.tuned(GEMV1=gemv1, FUSE_XSCORES=gemv1):
         _decode_logits_bit_exact(orc, hp)
-    finally:
-        del os.environ["GRX_GEMV1"]
-        del os.environ["GRX_FUSE_XSCORES"]
 
 
 def _decode_logits_bit_exact(orc, hp):
@@ -74,16 +69,13 @@ def test_greedy_tokens_identical_and_eager_equals_graph(kern, orc):
     want = ref.greedy([1, 2, 3, 4], 40)
     got = dec.greedy([1, 2, 3, 4], 40)
     assert list(got) == list(want)
-    os.environ["GRX_NO_GRAPH"] = "1"
-    try:
+    with kern.tuned(NO_GRAPH=1):
         from gorelaxor_amd.whisper import WhisperDecoder
 
         t = whisper_model(hp, seed=9)
         eager = WhisperDecoder(hp, t)
         eager.set_encoder_output(encoder_output(hp, seed=10))
         assert list(eager.greedy([1, 2, 3, 4], 40)) == list(want)
-    finally:
-        del os.environ["GRX_NO_GRAPH"]
     # replaying the greedy loop again from an empty cache repeats it
     assert list(dec.greedy([1, 2, 3, 4], 40)) == list(want)
 
@@ -143,22 +135,17 @@ def _streams(hp, t, n, seed):
     return dec, encs
 
 
-@pytest.mark.parametrize("fuse_ln", ["1", "0"])
+@pytest.mark.parametrize("fuse_ln", [1, 0])
 @pytest.mark.parametrize("n", [2, 4, 8])
 def test_streams_tokens_identical_to_each_oracle_decode(kern, orc, n, fuse_ln):
     """Independent streams decoded side by side (every product n rows): each
     stream's greedy tokens are those of its own oracle decode, with each
     stream's LayerNorm row built inside the product (one wave per row) and
-    the cross values on 16-output workgroups, or (GRX_FUSE_LN=0,
-    GRX_WAVE_VALUES=0) a row kernel beforehand and the values kernel that
+    the cross values on 16-output workgroups, or (FUSE_LN=0,
+    WAVE_VALUES=0) a row kernel beforehand and the values kernel that
     rounds its outputs."""
-    os.environ["GRX_FUSE_LN"] = fuse_ln
-    os.environ["GRX_WAVE_VALUES"] = fuse_ln
-    try:
+    with kern.tuned(FUSE_LN=fuse_ln, WAVE_VALUES=fuse_ln):
         _streams_vs_oracle(orc, n)
-    finally:
-        del os.environ["GRX_FUSE_LN"]
-        del os.environ["GRX_WAVE_VALUES"]
 
 
 def _streams_vs_oracle(orc, n):
