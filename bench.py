@@ -241,8 +241,33 @@ def decoder_bench(args) -> dict:
     res["cpu_baseline"] = {"value": round(steps / cpu_s, 2), "unit": "tokens/s", "cores": 1, "kind": "port",
                            **cpu_info(),
                            "sample": f"the same {steps} decoder steps on the oracle (scalar C, 1 thread), {cpu_s:.2f} s"}
+    if not args.no_cpu:
+        res["cpu_reference_f16"] = f16_decode_baseline(ref, t, n, steps)
     dec.close()
     return res
+
+
+def f16_decode_baseline(ref, t, n: int, steps: int) -> dict:
+    """The reference's own whisper decode on the host (float16 matrices, its
+    AVX2/F16C kernels and thread fan-out, oracle/grx_vnni.cc f16w_decode
+    restating whisper/decoder.go and gemm.go:223-256) over the same prompt
+    and steps, at one thread and at the host's threads: tokens/s.  Its
+    matrices are the Q8_0 ones widened to float16, so its tokens are its
+    own; this is the rate a user of the reference gets today."""
+    import oracle
+
+    f16 = oracle.WhisperF16(ref, t)
+    out = {"unit": "tokens/s", "kind": "port", **cpu_info()}
+    th = cpu_threads()
+    for label, threads in (("one_thread", 1), ("all_threads", th)):
+        f16.reset()
+        t0 = time.perf_counter()
+        f16.greedy(PROMPT, n, threads)
+        out[label] = round(steps / (time.perf_counter() - t0), 2)
+    out["threads"] = th
+    out["sample"] = (f"the same {steps} decoder steps (4-token prompt in one call, then one token a step) on "
+                     f"float16 matrices, at 1 and {th} threads")
+    return out
 
 
 def streams_bench(args) -> dict:

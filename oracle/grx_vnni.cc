@@ -20,7 +20,21 @@
 //                                                  task counter here)
 // The EVEX form needs AVX512-VNNI with AVX512-VL, the VEX form AVX-VNNI;
 // both give the same bits, which equal the oracle's orc_matmul_q8_int.
+//
+// Also the reference's own whisper decode on the CPU, for timing only (its
+// whisper package keeps every matrix as float16 and has no int8 route):
+//   decode          whisper/decoder.go:33-140     one step over the token(s),
+//                                                 self- and cross-attention
+//   gemv, parallel  whisper/gemm.go:223-256,52-108 four rows per task
+//   dot4f16avx      whisper/kernels_amd64.s:97-154 F16C widening, two
+//                                                 accumulator sets per row
+//   dot4f32avx      whisper/kernels_amd64.s:156-204 cross-attention rows
+//   expSubAVX       internal/kern/kernels_amd64.s:236-297 (EXP8 per 8 lanes)
+//   geluAVX         internal/kern/kernels_amd64.s:299-338
+// Its outputs are not compared with anything: the weights are float16, not
+// the Q8_0 the product path runs.
 #include <immintrin.h>
+#include <math.h>
 #include <stdint.h>
 #include <string.h>
 
@@ -216,9 +230,285 @@ Pool &pool(int threads) {
     return *g_pool;
 }
 
+// ---------------------------------------------------------------- whisper F16
+
+// dot4f16avx: out[r] = sum x[i] * w[r*ld+i], k a multiple of 16; per row two
+// accumulators (values 0-7 and 8-15 of each 16), added, then summed across.
+__attribute__((target("avx2,fma,f16c"))) void dot4_f16(const float *x, const uint16_t *w, size_t ld, int k,
+                                                       float out[4]) {
+    __m256 a[4], b[4];
+    for (int r = 0; r < 4; ++r) a[r] = b[r] = _mm256_setzero_ps();
+    for (int i = 0; i + 16 <= k; i += 16) {
+        const __m256 x0 = _mm256_loadu_ps(x + i), x1 = _mm256_loadu_ps(x + i + 8);
+        for (int r = 0; r < 4; ++r) {
+            const uint16_t *wr = w + r * ld + i;
+            a[r] = _mm256_fmadd_ps(x0, _mm256_cvtph_ps(_mm_loadu_si128(reinterpret_cast<const __m128i *>(wr))), a[r]);
+            b[r] = _mm256_fmadd_ps(x1, _mm256_cvtph_ps(_mm_loadu_si128(reinterpret_cast<const __m128i *>(wr + 8))),
+                                   b[r]);
+        }
+    }
+    for (int r = 0; r < 4; ++r) {
+        const __m256 v = _mm256_add_ps(a[r], b[r]);
+        __m128 h = _mm_add_ps(_mm256_castps256_ps128(v), _mm256_extractf128_ps(v, 1));
+        h = _mm_hadd_ps(h, h);
+        h = _mm_hadd_ps(h, h);
+        out[r] = _mm_cvtss_f32(h);
+    }
+}
+
+// dotF16Go for rows past the last whole group of four (and k past 16s).
+float dot_f16_go(const float *x, const uint16_t *w, int k) {
+    float s = 0.0f;
+    for (int i = 0; i < k; ++i) s += x[i] * f16_to_f32(w[i]);
+    return s;
+}
+
+// dot4f32avx: the same over float32 rows (k a multiple of 16 here).
+__attribute__((target("avx2,fma"))) void dot4_f32(const float *x, const float *w, size_t ld, int k, float out[4]) {
+    __m256 a[4], b[4];
+    for (int r = 0; r < 4; ++r) a[r] = b[r] = _mm256_setzero_ps();
+    int i = 0;
+    for (; i + 16 <= k; i += 16) {
+        const __m256 x0 = _mm256_loadu_ps(x + i), x1 = _mm256_loadu_ps(x + i + 8);
+        for (int r = 0; r < 4; ++r) {
+            a[r] = _mm256_fmadd_ps(x0, _mm256_loadu_ps(w + r * ld + i), a[r]);
+            b[r] = _mm256_fmadd_ps(x1, _mm256_loadu_ps(w + r * ld + i + 8), b[r]);
+        }
+    }
+    for (int r = 0; r < 4; ++r) {
+        const __m256 v = _mm256_add_ps(a[r], b[r]);
+        __m128 h = _mm_add_ps(_mm256_castps256_ps128(v), _mm256_extractf128_ps(v, 1));
+        h = _mm_hadd_ps(h, h);
+        h = _mm_hadd_ps(h, h);
+        float t = _mm_cvtss_f32(h);
+        for (int j = i; j < k; ++j) t += x[j] * w[r * ld + j];
+        out[r] = t;
+    }
+}
+
+float dot_f32_go(const float *x, const float *y, int n) {
+    float s = 0.0f;
+    for (int i = 0; i < n; ++i) s += x[i] * y[i];
+    return s;
+}
+
+// EXP8 on eight lanes (the same polynomial as the int8 path's SiLU).
+__attribute__((target("avx2,fma"))) __m256 exp8(__m256 x) {
+    x = _mm256_min_ps(_mm256_max_ps(x, _mm256_set1_ps(-87.0f)), _mm256_set1_ps(88.0f));
+    const __m256 n = _mm256_round_ps(_mm256_mul_ps(x, _mm256_set1_ps(1.44269504f)), _MM_FROUND_TO_NEAREST_INT);
+    __m256 r = _mm256_fnmadd_ps(n, _mm256_set1_ps(0.693359375f), x);
+    r = _mm256_fnmadd_ps(n, _mm256_set1_ps(-2.12194440e-4f), r);
+    __m256 p = _mm256_set1_ps(1.3888949e-3f);
+    p = _mm256_fmadd_ps(p, r, _mm256_set1_ps(8.3333338e-3f));
+    p = _mm256_fmadd_ps(p, r, _mm256_set1_ps(4.1666668e-2f));
+    p = _mm256_fmadd_ps(p, r, _mm256_set1_ps(1.6666667e-1f));
+    p = _mm256_fmadd_ps(p, r, _mm256_set1_ps(0.5f));
+    p = _mm256_fmadd_ps(p, r, _mm256_set1_ps(1.0f));
+    p = _mm256_fmadd_ps(p, r, _mm256_set1_ps(1.0f));
+    const __m256i e = _mm256_slli_epi32(_mm256_add_epi32(_mm256_cvtps_epi32(n), _mm256_set1_epi32(127)), 23);
+    return _mm256_mul_ps(p, _mm256_castsi256_ps(e));
+}
+
+// softmax: max, e^(x - max) with their sum (expSubAVX over groups of
+// eight, the scalar form past them), then times 1/sum.
+__attribute__((target("avx2,fma"))) void softmax(float *x, int n) {
+    float mx = -INFINITY;
+    for (int i = 0; i < n; ++i) mx = x[i] > mx ? x[i] : mx;
+    const int n8 = n & ~7;
+    __m256 acc = _mm256_setzero_ps();
+    const __m256 vm = _mm256_set1_ps(mx);
+    for (int i = 0; i < n8; i += 8) {
+        const __m256 e = exp8(_mm256_sub_ps(_mm256_loadu_ps(x + i), vm));
+        _mm256_storeu_ps(x + i, e);
+        acc = _mm256_add_ps(acc, e);
+    }
+    __m128 h = _mm_add_ps(_mm256_castps256_ps128(acc), _mm256_extractf128_ps(acc, 1));
+    h = _mm_hadd_ps(h, h);
+    h = _mm_hadd_ps(h, h);
+    float s = _mm_cvtss_f32(h);
+    for (int i = n8; i < n; ++i) {
+        x[i] = expf(x[i] - mx);
+        s += x[i];
+    }
+    const float inv = 1.0f / s;
+    for (int i = 0; i < n; ++i) x[i] *= inv;
+}
+
+// geluAVX over groups of eight, the scalar form past them.
+__attribute__((target("avx2,fma"))) void gelu(float *x, int n) {
+    const int n8 = n & ~7;
+    for (int i = 0; i < n8; i += 8) {
+        const __m256 v = _mm256_loadu_ps(x + i);
+        __m256 u = _mm256_fmadd_ps(_mm256_set1_ps(0.044715f), _mm256_mul_ps(v, v), _mm256_set1_ps(1.0f));
+        u = _mm256_mul_ps(_mm256_mul_ps(u, v), _mm256_set1_ps(0.7978845608f));
+        u = _mm256_min_ps(_mm256_max_ps(u, _mm256_set1_ps(-9.0f)), _mm256_set1_ps(9.0f));
+        const __m256 e = _mm256_add_ps(exp8(_mm256_add_ps(u, u)), _mm256_set1_ps(1.0f));
+        __m256 t = _mm256_sub_ps(_mm256_set1_ps(1.0f), _mm256_div_ps(_mm256_set1_ps(2.0f), e));
+        t = _mm256_mul_ps(_mm256_mul_ps(_mm256_add_ps(_mm256_set1_ps(1.0f), t), v), _mm256_set1_ps(0.5f));
+        _mm256_storeu_ps(x + i, t);
+    }
+    for (int i = n8; i < n; ++i) {
+        const float v = x[i], u = 0.7978845608f * v * (1.0f + 0.044715f * v * v);
+        const float t = u > 9.0f ? 1.0f : u < -9.0f ? -1.0f : 1.0f - 2.0f / (expf(2.0f * u) + 1.0f);
+        x[i] = 0.5f * v * (1.0f + t);
+    }
+}
+
+void layer_norm(float *y, const float *x, int n, const float *w, const float *b) {
+    double sum = 0;
+    for (int i = 0; i < n; ++i) sum += x[i];
+    const float mean = (float)(sum / n);
+    double vs = 0;
+    for (int i = 0; i < n; ++i) {
+        const double d = (double)(x[i] - mean);
+        vs += d * d;
+    }
+    const float inv = (float)(1.0 / sqrt(vs / n + 1e-5));
+    for (int i = 0; i < n; ++i) y[i] = (x[i] - mean) * inv * w[i] + b[i];
+}
+
+// gemv: y[n] = W[n][k] . x + bias, (n+3)/4 tasks of four rows over the
+// pool (one thread below 2^16 multiply-adds), contiguous task ranges.
+void gemv_f16(float *y, const float *x, const uint16_t *w, int n, int k, const float *bias, int threads) {
+    const int groups = (n + 3) / 4;
+    const int tt = (long)n * k < (1 << 16) ? 1 : threads;
+    auto part = [&](int lo, int hi) {
+        float out[4];
+        for (int g = lo; g < hi; ++g) {
+            const int j = 4 * g;
+            if (j + 4 <= n) {
+                const int kk = k & ~15;
+                if (kk > 0) dot4_f16(x, w + (size_t)j * k, k, kk, out);
+                else out[0] = out[1] = out[2] = out[3] = 0.0f;
+                for (int r = 0; r < 4; ++r) {
+                    if (kk < k) out[r] += dot_f16_go(x + kk, w + (size_t)(j + r) * k + kk, k - kk);
+                    y[j + r] = out[r];
+                }
+            } else {
+                for (int jj = j; jj < n; ++jj) y[jj] = dot_f16_go(x, w + (size_t)jj * k, k);
+            }
+            if (bias)
+                for (int jj = j; jj < std::min(j + 4, n); ++jj) y[jj] += bias[jj];
+        }
+    };
+    if (tt <= 1) {
+        part(0, groups);
+        return;
+    }
+    const int parts = std::min(tt, groups);
+    pool(tt).run(parts, [&](int t) { part(groups * t / parts, groups * (t + 1) / parts); });
+}
+
 }  // namespace
 
 extern "C" {
+
+// The reference's whisper decoder with float16 matrices (whisper/decoder.go).
+typedef struct {
+    const float *attn_ln_w, *attn_ln_b;
+    const uint16_t *q, *k, *v, *o;
+    const float *q_b, *v_b, *o_b;
+    const float *x_ln_w, *x_ln_b;
+    const uint16_t *xq, *xo;
+    const float *xq_b, *xo_b;
+    const float *mlp_ln_w, *mlp_ln_b;
+    const uint16_t *fc1, *fc2;
+    const float *fc1_b, *fc2_b;
+    const float *cross_k; /* [head][audio_ctx][head_dim] */
+    const float *cross_v; /* [head][head_dim][audio_ctx] */
+    float *self_k, *self_v; /* [text_ctx][state] */
+} f16w_layer;
+
+typedef struct {
+    int n_vocab, n_text_ctx, n_state, n_head, n_layer, n_audio_ctx;
+    const uint16_t *tok_emb; /* [n_vocab][n_state] */
+    const float *dec_pos, *dec_ln_w, *dec_ln_b;
+    f16w_layer *layers;
+    int n;
+} f16w_model;
+
+// One decode call over nt < 6 tokens (rows through gemv one at a time, as
+// matmul does below its 6-row tile); logits of the last token.
+int f16w_decode(f16w_model *m, const int *tokens, int nt, float *logits, int threads) {
+    const int st = m->n_state, nh = m->n_head, hd = st / nh, nctx = m->n_audio_ctx, pos0 = m->n;
+    if (nt < 1 || nt >= kTileRows || pos0 + nt > m->n_text_ctx) return -1;
+    if (threads < 1) threads = 1;
+    std::vector<float> x((size_t)nt * st), cur((size_t)nt * st), q((size_t)nt * st), att((size_t)nt * st),
+        ff((size_t)nt * 4 * st), sbuf((size_t)nt * nh * std::max(nctx, pos0 + nt));
+    const int sw = std::max(nctx, pos0 + nt);
+    const float sc = (float)(1.0 / sqrt((double)hd));
+    for (int i = 0; i < nt; ++i)
+        for (int j = 0; j < st; ++j)
+            x[(size_t)i * st + j] = f16_to_f32(m->tok_emb[(size_t)tokens[i] * st + j]) + m->dec_pos[(size_t)(pos0 + i) * st + j];
+    auto lin = [&](float *y, int ldy, const float *a, int lda, int n, int k, const uint16_t *w, const float *b) {
+        for (int i = 0; i < nt; ++i) gemv_f16(y + (size_t)i * ldy, a + (size_t)i * lda, w, n, k, b, threads);
+    };
+    auto jobs = [&](const std::function<void(int)> &fn) {
+        if (threads <= 1) {
+            for (int j = 0; j < nt * nh; ++j) fn(j);
+        } else {
+            pool(threads).run(nt * nh, fn);
+        }
+    };
+    for (int li = 0; li < m->n_layer; ++li) {
+        const f16w_layer &L = m->layers[li];
+        for (int i = 0; i < nt; ++i) layer_norm(&cur[(size_t)i * st], &x[(size_t)i * st], st, L.attn_ln_w, L.attn_ln_b);
+        lin(q.data(), st, cur.data(), st, st, st, L.q, L.q_b);
+        lin(L.self_k + (size_t)pos0 * st, st, cur.data(), st, st, st, L.k, nullptr);
+        lin(L.self_v + (size_t)pos0 * st, st, cur.data(), st, st, st, L.v, L.v_b);
+        jobs([&](int job) {
+            const int i = job / nh, h = job % nh, n = pos0 + i + 1;
+            float *s = &sbuf[(size_t)job * sw];
+            const float *qi = &q[(size_t)i * st + h * hd];
+            for (int j = 0; j < n; ++j) s[j] = dot_f32_go(qi, L.self_k + (size_t)j * st + h * hd, hd) * sc;
+            softmax(s, n);
+            float *out = &att[(size_t)i * st + h * hd];
+            for (int d = 0; d < hd; ++d) out[d] = 0.0f;
+            for (int j = 0; j < n; ++j) {
+                const float *vj = L.self_v + (size_t)j * st + h * hd;
+                for (int d = 0; d < hd; ++d) out[d] += s[j] * vj[d];
+            }
+        });
+        lin(cur.data(), st, att.data(), st, st, st, L.o, L.o_b);
+        for (size_t t = 0; t < x.size(); ++t) x[t] += cur[t];
+        for (int i = 0; i < nt; ++i) layer_norm(&cur[(size_t)i * st], &x[(size_t)i * st], st, L.x_ln_w, L.x_ln_b);
+        lin(q.data(), st, cur.data(), st, st, st, L.xq, L.xq_b);
+        jobs([&](int job) {
+            const int i = job / nh, h = job % nh;
+            const float *kd = L.cross_k + (size_t)h * nctx * hd, *vd = L.cross_v + (size_t)h * nctx * hd;
+            const float *qi = &q[(size_t)i * st + h * hd];
+            float *s = &sbuf[(size_t)job * sw];
+            float o4[4];
+            int j = 0;
+            for (; j + 4 <= nctx; j += 4) {
+                dot4_f32(qi, kd + (size_t)j * hd, hd, hd, o4);
+                for (int r = 0; r < 4; ++r) s[j + r] = o4[r];
+            }
+            for (; j < nctx; ++j) s[j] = dot_f32_go(qi, kd + (size_t)j * hd, hd);
+            softmax(s, nctx);
+            float *out = &att[(size_t)i * st + h * hd];
+            int d = 0;
+            for (; d + 4 <= hd; d += 4) {
+                dot4_f32(s, vd + (size_t)d * nctx, nctx, nctx, o4);
+                for (int r = 0; r < 4; ++r) out[d + r] = o4[r];
+            }
+            for (; d < hd; ++d) out[d] = dot_f32_go(s, vd + (size_t)d * nctx, nctx);
+        });
+        lin(cur.data(), st, att.data(), st, st, st, L.xo, L.xo_b);
+        for (size_t t = 0; t < x.size(); ++t) x[t] += cur[t];
+        for (int i = 0; i < nt; ++i) layer_norm(&cur[(size_t)i * st], &x[(size_t)i * st], st, L.mlp_ln_w, L.mlp_ln_b);
+        lin(ff.data(), 4 * st, cur.data(), st, 4 * st, st, L.fc1, L.fc1_b);
+        gelu(ff.data(), nt * 4 * st);
+        lin(cur.data(), st, ff.data(), 4 * st, st, 4 * st, L.fc2, L.fc2_b);
+        for (size_t t = 0; t < x.size(); ++t) x[t] += cur[t];
+    }
+    m->n = pos0 + nt;
+    std::vector<float> row(st);
+    layer_norm(row.data(), &x[(size_t)(nt - 1) * st], st, m->dec_ln_w, m->dec_ln_b);
+    gemv_f16(logits, row.data(), m->tok_emb, m->n_vocab, st, nullptr, threads);
+    return 0;
+}
+
 
 // 2: the EVEX form (AVX512-VNNI + AVX512-VL), 1: the VEX form (AVX-VNNI),
 // 0: neither (the baseline cannot run here).

@@ -1053,3 +1053,97 @@ def vnni_ring(y: np.ndarray, x: np.ndarray, panels: np.ndarray, per: int, count:
                               s.q.ctypes.data, s.sc.ctypes.data)
     if rc != 0:
         raise RuntimeError("vnni_ring: this processor has neither AVX512-VNNI nor AVX-VNNI")
+
+
+# ---- the reference's whisper decode with float16 matrices (grx_vnni.cc
+# f16w_decode, whisper/decoder.go:33-140): timing context only
+
+class _F16Layer(C.Structure):
+    _fields_ = [(f, C.c_void_p) for f in (
+        "attn_ln_w", "attn_ln_b", "q", "k", "v", "o", "q_b", "v_b", "o_b", "x_ln_w", "x_ln_b", "xq", "xo",
+        "xq_b", "xo_b", "mlp_ln_w", "mlp_ln_b", "fc1", "fc2", "fc1_b", "fc2_b", "cross_k", "cross_v",
+        "self_k", "self_v")]
+
+
+class _F16Model(C.Structure):
+    _fields_ = [("n_vocab", C.c_int), ("n_text_ctx", C.c_int), ("n_state", C.c_int), ("n_head", C.c_int),
+                ("n_layer", C.c_int), ("n_audio_ctx", C.c_int), ("tok_emb", C.c_void_p), ("dec_pos", C.c_void_p),
+                ("dec_ln_w", C.c_void_p), ("dec_ln_b", C.c_void_p), ("layers", C.c_void_p), ("n", C.c_int)]
+
+
+def q8_to_f16(q8: np.ndarray, rows: int, cols: int) -> np.ndarray:
+    """A Q8_0 matrix widened to float32 (scale times value) and rounded to
+    float16, as a float16 model file would hold it."""
+    b = np.ascontiguousarray(q8, np.uint8).reshape(rows, cols // 32, 34)
+    sc = b[:, :, :2].copy().view(np.float16).astype(np.float32)
+    v = b[:, :, 2:].view(np.int8).astype(np.float32)
+    return (v * sc).reshape(rows, cols).astype(np.float16)
+
+
+class WhisperF16:
+    """The reference's own CPU decoder (float16 matrices, AVX2/F16C kernels,
+    its thread fan-out) over a WhisperOracle's model: its matrices widened
+    from Q8_0 to float16, its vectors, positional rows and cross keys and
+    values (set the encoder output on the oracle first)."""
+
+    def __init__(self, orc: "WhisperOracle", tensors: dict):
+        hp = orc.hp
+        st, nl = hp["n_state"], hp["n_layer"]
+        self.hp = hp
+        self._keep = []
+
+        def keep(a):
+            a = np.ascontiguousarray(a)
+            self._keep.append(a)
+            return a.ctypes.data
+
+        def mat(name, rows, cols):
+            return keep(q8_to_f16(tensors[name], rows, cols))
+
+        L = vnni_lib()
+        L.f16w_decode.argtypes = [C.c_void_p, C.c_void_p, C.c_int, C.c_void_p, C.c_int]
+        L.f16w_decode.restype = C.c_int
+        layers = (_F16Layer * nl)()
+        for i in range(nl):
+            p = f"decoder.blocks.{i}."
+            ly = layers[i]
+            for f in ("attn_ln_w", "attn_ln_b", "q_b", "v_b", "o_b", "x_ln_w", "x_ln_b", "xq_b", "xo_b",
+                      "mlp_ln_w", "mlp_ln_b", "fc1_b", "fc2_b"):
+                setattr(ly, f, keep(np.asarray(tensors[p + WhisperOracle._LAYER_MAP[f]], np.float32)))
+            for f in ("q", "k", "v", "o", "xq", "xo"):
+                setattr(ly, f, mat(p + WhisperOracle._LAYER_MAP[f], st, st))
+            ly.fc1 = mat(p + WhisperOracle._LAYER_MAP["fc1"], 4 * st, st)
+            ly.fc2 = mat(p + WhisperOracle._LAYER_MAP["fc2"], st, 4 * st)
+            ly.cross_k = keep(orc.cross_k[i])
+            ly.cross_v = keep(orc.cross_v[i])
+            ly.self_k = keep(np.zeros(hp["n_text_ctx"] * st, np.float32))
+            ly.self_v = keep(np.zeros(hp["n_text_ctx"] * st, np.float32))
+        self._layers = layers
+        m = _F16Model()
+        m.n_vocab, m.n_text_ctx, m.n_state = hp["n_vocab"], hp["n_text_ctx"], st
+        m.n_head, m.n_layer, m.n_audio_ctx = hp["n_head"], nl, hp["n_audio_ctx"]
+        m.tok_emb = mat("decoder.token_embedding.weight", hp["n_vocab"], st)
+        m.dec_pos = keep(np.asarray(tensors["decoder.positional_embedding"], np.float32))
+        m.dec_ln_w = keep(np.asarray(tensors["decoder.ln.weight"], np.float32))
+        m.dec_ln_b = keep(np.asarray(tensors["decoder.ln.bias"], np.float32))
+        m.layers = C.cast(layers, C.c_void_p)
+        m.n = 0
+        self._m = m
+        self.logits = np.zeros(hp["n_vocab"], np.float32)
+
+    def reset(self):
+        self._m.n = 0
+
+    def decode(self, tokens, threads: int = 1) -> np.ndarray:
+        t = np.ascontiguousarray(tokens, np.int32)
+        if vnni_lib().f16w_decode(C.byref(self._m), t.ctypes.data, t.size, self.logits.ctypes.data, threads) != 0:
+            raise ValueError("tokens do not fit the text context (or 6 or more at once)")
+        return self.logits
+
+    def greedy(self, prompt, n_steps: int, threads: int = 1) -> list:
+        """The prompt in one call, then n_steps argmax tokens one at a time
+        (transcribe.go's greedy loop without its rules)."""
+        out = [int(np.argmax(self.decode(prompt, threads)))]
+        for _ in range(n_steps):
+            out.append(int(np.argmax(self.decode([out[-1]], threads))))
+        return out
