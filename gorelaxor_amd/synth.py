@@ -155,6 +155,88 @@ def pocket_flow_model(hp: dict, fhp: dict, seed: int = 12, q8: bool = True) -> d
     return t
 
 
+# Pocket TTS's Mimi decoder: the english_2026-09 settings the reference's
+# converter writes (tools/convert_pocket_tts.py:56-72, 336-360): d_model 512,
+# 8 heads, 2 layers, FFN 2048, 250 positions of context, 16x upsampling to
+# 200 Hz, SEANet ratios 6, 5, 4 (1920 samples per latent at 24 kHz).
+MIMI = dict(d=512, heads=8, ff=2048, n_layer=2, context=250, ldim=32, up_s=16, period=1e4, ratios=(6, 5, 4),
+            nf=64, k=7, res_k=3, last_k=3, dil_base=2, compress=2, n_res=1)
+MIMI_TINY = dict(d=64, heads=2, ff=128, n_layer=2, context=12, ldim=32, up_s=4, period=1e4, ratios=(3, 2),
+                 nf=16, k=5, res_k=3, last_k=3, dil_base=2, compress=2, n_res=2)
+
+
+def mimi_steps(hp: dict) -> list:
+    """SEANet's decoder steps as pockettts/model.go:163-181 builds them:
+    (kind, name, elu, cin, cout, k, stride, dilation) with kind "conv",
+    "convtr" or "res" (a residual block: name.1 of kernel res_k at the
+    dilation, then name.3 of kernel 1; cin = the block's channels)."""
+    mult = 1 << len(hp["ratios"])
+    nf, d = hp["nf"], hp["d"]
+    out = [("conv", "mimi.dec.0", False, d, mult * nf, hp["k"], 1, 1)]
+    idx = 1
+    for r in hp["ratios"]:
+        idx += 1
+        out.append(("convtr", f"mimi.dec.{idx}", True, mult * nf, mult * nf // 2, 2 * r, r, 1))
+        idx += 1
+        dim = mult * nf // 2
+        for j in range(hp["n_res"]):
+            out.append(("res", f"mimi.dec.{idx}", False, dim, dim // hp["compress"], hp["res_k"], 1,
+                        hp["dil_base"] ** j))
+            idx += 1
+        mult //= 2
+    idx += 1
+    out.append(("conv", f"mimi.dec.{idx}", True, nf, 1, hp["last_k"], 1, 1))
+    return out
+
+
+def mimi_model(hp: dict, seed: int = 15, q8: bool = True) -> dict:
+    """Random-init Mimi decoder tensors under the reference's names
+    (pockettts/model.go:105-181, 331-335), typed as its converter types them
+    (tools/convert_pocket_tts.py:150-156): matrices of at least 64 x 64 whose
+    rows are whole Q8_0 blocks Q8_0 (when q8), the rest float32.  Conv
+    weights [cout][k*cin], transposed-conv weights [k*cout][cin]."""
+    rng = np.random.default_rng(seed)
+    d, ff, ld = hp["d"], hp["ff"], hp["ldim"]
+    t = {}
+
+    def vec(n, scale=0.1, base=0.0):
+        return (base + scale * rng.standard_normal(n)).astype(np.float32)
+
+    def mat(rows, cols, gain=1.0):
+        if q8 and rows >= 64 and cols >= 64 and cols % QK == 0:
+            return q8_weight(rng, rows, cols, sigma=gain * 2.0 / np.sqrt(cols))
+        return (rng.standard_normal(rows * cols) * gain / np.sqrt(cols)).astype(np.float32)
+
+    t["mimi.quant"] = mat(d, ld)
+    t["mimi.up"] = vec(d * 2 * hp["up_s"], 0.3)
+    for i in range(hp["n_layer"]):
+        p = f"mimi.dec_tf.{i}."
+        for n in ("norm1", "norm2"):
+            t[p + n + ".weight"] = vec(d, 0.1, 1.0)
+            t[p + n + ".bias"] = vec(d, 0.1)
+        t[p + "attn_qkv.weight"] = mat(3 * d, d)
+        t[p + "attn_out.weight"] = mat(d, d)
+        t[p + "ff1.weight"] = mat(ff, d)
+        t[p + "ff2.weight"] = mat(d, ff, 0.5)
+        t[p + "ls1"] = vec(d, 0.05, 0.2)
+        t[p + "ls2"] = vec(d, 0.05, 0.2)
+    for kind, name, _, cin, cout, k, stride, _ in mimi_steps(hp):
+        if kind == "conv":
+            t[name + ".weight"], t[name + ".bias"] = mat(cout, k * cin), vec(cout)
+        elif kind == "convtr":
+            t[name + ".weight"], t[name + ".bias"] = mat(k * cout, cin), vec(cout)
+        else:
+            t[name + ".1.weight"], t[name + ".1.bias"] = mat(cout, k * cin), vec(cout)
+            t[name + ".3.weight"], t[name + ".3.bias"] = mat(cin, cout, 0.5), vec(cin)
+    return t
+
+
+def mimi_latents(hp: dict, n: int, seed: int = 16) -> np.ndarray:
+    """n latents as the speak loop hands them to the decoder (scaled back by
+    the flow LM's mean and std): [n][ldim] ~ N(0, 1)."""
+    return np.random.default_rng(seed).standard_normal((n, hp["ldim"])).astype(np.float32)
+
+
 def pocket_inputs(hp: dict, frames: int, prefix: int = 64, seed: int = 6):
     """The text prefix (prefix x d random embedding rows) and teacher-forced
     latents (frames x ldim, N(0,1)), seeded."""

@@ -127,6 +127,55 @@ int orc_ptts_forward(orc_ptts *m, float *x, int T);
 int orc_ptts_run(orc_ptts *m, float *x, int T, float *out);
 int orc_ptts_step(orc_ptts *m, const float *latent, float *out, float *eos);
 
+/* ---- pocket-TTS's Mimi decoder (pockettts/mimi.go, nn.go) ---- */
+typedef struct {
+    int n, k;            /* rows (outputs) and columns (inputs) */
+    const uint8_t *wq;   /* Q8_0 rows, or NULL */
+    const float *wf;     /* float32 rows when wq is NULL */
+    const float *b;      /* [n] or NULL */
+} orc_mlin;
+typedef struct {
+    int cin, cout, k, stride, dil;
+    orc_mlin w;          /* [cout][k*cin] */
+} orc_mconv;
+typedef struct {
+    int cin, cout, k, stride;
+    orc_mlin w;          /* [k*cout][cin]; w.b is the [cout] bias */
+} orc_mconvtr;
+typedef struct {
+    int kind;            /* 0 conv, 1 transposed conv, 2 residual block */
+    int elu;             /* ELU before the step */
+    orc_mconv c;         /* kind 0 */
+    orc_mconvtr t;       /* kind 1 */
+    orc_mconv a, b;      /* kind 2: a (kernel resK, dilation) then b (1x1) */
+} orc_sea_step;
+typedef struct {
+    const float *norm1_w, *norm1_b, *norm2_w, *norm2_b;
+    orc_mlin qkv, out, ff1, ff2;
+    const float *ls1, *ls2; /* layer scales [d], or NULL */
+} orc_mimi_layer;
+typedef struct {
+    int d, heads, ff, n_layer, context, ldim, up_s;
+    const float *freqs;     /* head_dim/2 rotary frequencies */
+    orc_mimi_layer *layers;
+    orc_mlin quant;         /* [d][ldim], no bias */
+    const float *up;        /* [d][2*up_s] depthwise taps */
+    int n_steps;
+    orc_sea_step *steps;
+} orc_mimi;
+typedef struct {
+    int pos, max_pos;
+    float **k, **v;         /* per layer [max_pos][d] */
+    float *up_part;         /* [up_s][d] */
+    int n_prev;
+    float **prev;           /* each conv's past rows, each convtr's partial */
+} orc_mimi_state;
+void orc_elu(float *x, size_t n);
+int orc_mconv_past(const orc_mconv *c);
+orc_mimi_state *orc_mimi_state_new(const orc_mimi *m, int max_pos);
+void orc_mimi_state_free(const orc_mimi *m, orc_mimi_state *s);
+int orc_mimi_decode(const orc_mimi *m, orc_mimi_state *st, const float *lat, int n, float *out, int *n_out);
+
 /* ---- FastConformer encoder with Q8_0 weights (conformer/encoder.go) ---- */
 typedef struct {
     const float *norm_w, *norm_b;

@@ -1147,3 +1147,148 @@ class WhisperF16:
         for _ in range(n_steps):
             out.append(int(np.argmax(self.decode([out[-1]], threads))))
         return out
+
+
+# ---- pocket-TTS's Mimi decoder (grx_oracle_mimi.c, pockettts/mimi.go) ----
+
+class _MLin(C.Structure):
+    _fields_ = [("n", C.c_int), ("k", C.c_int), ("wq", C.c_void_p), ("wf", C.c_void_p), ("b", C.c_void_p)]
+
+
+class _MConv(C.Structure):
+    _fields_ = [("cin", C.c_int), ("cout", C.c_int), ("k", C.c_int), ("stride", C.c_int), ("dil", C.c_int),
+                ("w", _MLin)]
+
+
+class _MConvTr(C.Structure):
+    _fields_ = [("cin", C.c_int), ("cout", C.c_int), ("k", C.c_int), ("stride", C.c_int), ("w", _MLin)]
+
+
+class _SeaStep(C.Structure):
+    _fields_ = [("kind", C.c_int), ("elu", C.c_int), ("c", _MConv), ("t", _MConvTr), ("a", _MConv), ("b", _MConv)]
+
+
+class _MimiLayer(C.Structure):
+    _fields_ = [("norm1_w", C.c_void_p), ("norm1_b", C.c_void_p), ("norm2_w", C.c_void_p), ("norm2_b", C.c_void_p),
+                ("qkv", _MLin), ("out", _MLin), ("ff1", _MLin), ("ff2", _MLin), ("ls1", C.c_void_p),
+                ("ls2", C.c_void_p)]
+
+
+class _Mimi(C.Structure):
+    _fields_ = [("d", C.c_int), ("heads", C.c_int), ("ff", C.c_int), ("n_layer", C.c_int), ("context", C.c_int),
+                ("ldim", C.c_int), ("up_s", C.c_int), ("freqs", C.c_void_p), ("layers", C.c_void_p),
+                ("quant", _MLin), ("up", C.c_void_p), ("n_steps", C.c_int), ("steps", C.c_void_p)]
+
+
+def _mimi_lib() -> C.CDLL:
+    L = lib()
+    if not getattr(L, "_mimi_ready", False):
+        L.orc_elu.argtypes = [_f32p, C.c_size_t]
+        L.orc_mimi_state_new.argtypes = [C.c_void_p, C.c_int]
+        L.orc_mimi_state_new.restype = C.c_void_p
+        L.orc_mimi_state_free.argtypes = [C.c_void_p, C.c_void_p]
+        L.orc_mimi_decode.argtypes = [C.c_void_p, C.c_void_p, _f32p, C.c_int, _f32p, C.POINTER(C.c_int)]
+        L.orc_mimi_decode.restype = C.c_int
+        L._mimi_ready = True
+    return L
+
+
+def elu(x: np.ndarray) -> np.ndarray:
+    """pockettts/nn.go:51-64 on a copy of x."""
+    y = np.array(x, np.float32).ravel()
+    _mimi_lib().orc_elu(y, y.size)
+    return y.reshape(np.shape(x))
+
+
+class MimiOracle:
+    """The Mimi decoder of pockettts/mimi.go over a tensor dict named as
+    pockettts/model.go reads them (Q8_0 matrices as uint8 rows, the rest
+    float32), with one streaming state (decState) of max_pos transformer
+    positions."""
+
+    def __init__(self, hp: dict, tensors: dict, max_pos: int = 4096):
+        from gorelaxor_amd.synth import mimi_steps
+
+        L = _mimi_lib()
+        self.hp = hp
+        d = hp["d"]
+        self._keep = []
+
+        def keep(a):
+            a = np.ascontiguousarray(a)
+            self._keep.append(a)
+            return a.ctypes.data
+
+        def lin(name, n, k, bias=None):
+            w = tensors[name]
+            ml = _MLin(n, k, None, None, keep(np.asarray(bias, np.float32)) if bias is not None else None)
+            if w.dtype == np.uint8:
+                ml.wq = keep(w)
+            else:
+                ml.wf = keep(np.asarray(w, np.float32))
+            return ml
+
+        self.hd = d // hp["heads"]
+        freqs = np.zeros(self.hd // 2, np.float32)
+        L.orc_rope_freqs(freqs, self.hd, float(hp["period"]))
+        layers = (_MimiLayer * hp["n_layer"])()
+        for i in range(hp["n_layer"]):
+            p = f"mimi.dec_tf.{i}."
+            ly = layers[i]
+            ly.norm1_w, ly.norm1_b = keep(tensors[p + "norm1.weight"]), keep(tensors[p + "norm1.bias"])
+            ly.norm2_w, ly.norm2_b = keep(tensors[p + "norm2.weight"]), keep(tensors[p + "norm2.bias"])
+            ly.qkv = lin(p + "attn_qkv.weight", 3 * d, d)
+            ly.out = lin(p + "attn_out.weight", d, d)
+            ly.ff1 = lin(p + "ff1.weight", hp["ff"], d)
+            ly.ff2 = lin(p + "ff2.weight", d, hp["ff"])
+            ly.ls1 = keep(tensors[p + "ls1"]) if p + "ls1" in tensors else None
+            ly.ls2 = keep(tensors[p + "ls2"]) if p + "ls2" in tensors else None
+        steps_desc = mimi_steps(hp)
+        steps = (_SeaStep * len(steps_desc))()
+        for s, (kind, name, el, cin, cout, k, stride, dil) in zip(steps, steps_desc):
+            s.elu = int(el)
+            if kind == "conv":
+                s.kind = 0
+                s.c = _MConv(cin, cout, k, stride, dil, lin(name + ".weight", cout, k * cin, tensors[name + ".bias"]))
+            elif kind == "convtr":
+                s.kind = 1
+                s.t = _MConvTr(cin, cout, k, stride, lin(name + ".weight", k * cout, cin, tensors[name + ".bias"]))
+            else:
+                s.kind = 2
+                s.a = _MConv(cin, cout, k, 1, dil, lin(name + ".1.weight", cout, k * cin, tensors[name + ".1.bias"]))
+                s.b = _MConv(cout, cin, 1, 1, 1, lin(name + ".3.weight", cin, cout, tensors[name + ".3.bias"]))
+        m = _Mimi()
+        m.d, m.heads, m.ff, m.n_layer = d, hp["heads"], hp["ff"], hp["n_layer"]
+        m.context, m.ldim, m.up_s = hp["context"], hp["ldim"], hp["up_s"]
+        m.freqs = keep(freqs)
+        m.layers = C.cast(layers, C.c_void_p)
+        m.quant = lin("mimi.quant", d, hp["ldim"])
+        m.up = keep(tensors["mimi.up"])
+        m.n_steps = len(steps_desc)
+        m.steps = C.cast(steps, C.c_void_p)
+        self._layers, self._steps, self._m = layers, steps, m
+        self.samples_per_latent = hp["up_s"] * int(np.prod(hp["ratios"]))
+        self.max_pos = max_pos
+        self._st = L.orc_mimi_state_new(C.byref(m), max_pos)
+
+    def reset(self):
+        lib().orc_mimi_state_free(C.byref(self._m), self._st)
+        self._st = lib().orc_mimi_state_new(C.byref(self._m), self.max_pos)
+
+    def decode(self, lat: np.ndarray) -> np.ndarray:
+        """n latents [n][ldim] -> n * samples_per_latent samples, continuing
+        the stream."""
+        lat = _f32(np.atleast_2d(lat))
+        n = lat.shape[0]
+        out = np.zeros(n * self.samples_per_latent, np.float32)
+        no = C.c_int(0)
+        if lib().orc_mimi_decode(C.byref(self._m), self._st, lat, n, out, C.byref(no)) != 0:
+            raise ValueError("past the transformer's positions")
+        assert no.value == out.size
+        return out
+
+    def __del__(self):
+        try:
+            lib().orc_mimi_state_free(C.byref(self._m), self._st)
+        except Exception:
+            pass
