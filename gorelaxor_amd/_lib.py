@@ -123,6 +123,13 @@ SIGNATURES = {
     "grx_conformer_stream_geometry": (i32, [vp, vp]),
     "grx_conformer_stream_step": (i32, [vp, vp, i32, vp, vp, vp]),
     "grx_conformer_stream_step_dev": (i32, [vp, vp, i32, vp, vp, vp]),
+    "grx_mimi_create": (i32, [vp, vp, C.POINTER(vp)]),
+    "grx_mimi_destroy": (i32, [vp]),
+    "grx_mimi_set_tensor": (i32, [vp, C.c_char_p, vp, sz]),
+    "grx_mimi_reset": (i32, [vp]),
+    "grx_mimi_decode": (i32, [vp, vp, i32, vp]),
+    "grx_mimi_decode_dev": (i32, [vp, vp, i32, vp]),
+    "grx_mimi_samples_per_latent": (i32, [vp]),
     "grx_rnnt_create": (i32, [vp, vp, C.POINTER(vp)]),
     "grx_rnnt_destroy": (i32, [vp]),
     "grx_rnnt_load_gguf": (i32, [vp, C.c_char_p, vp, C.POINTER(vp)]),
@@ -160,6 +167,14 @@ class RnntHParams(C.Structure):
     _fields_ = [(n, C.c_int) for n in ("d", "pred_hidden", "pred_layers", "pred_vocab", "joint_hidden", "joint_act",
                                        "tdt", "n_durations")] + [("durations", C.c_int * 16)] + [
         (n, C.c_int) for n in ("max_symbols", "blank")]
+
+
+class MimiHParams(C.Structure):
+    """grx_mimi_hparams."""
+    _fields_ = [(n, C.c_int) for n in ("d", "heads", "ff", "layers", "context", "ldim", "upsample")] + [
+        ("period", C.c_double), ("n_ratios", C.c_int), ("ratios", C.c_int * 8)] + [
+        (n, C.c_int) for n in ("n_filters", "kernel_size", "residual_kernel_size", "last_kernel_size",
+                               "dilation_base", "compress", "n_residual", "max_latents")]
 
 
 class RnntToken(C.Structure):

@@ -234,89 +234,6 @@ __global__ void sub_dwconv_kernel(const float *__restrict__ in, int T, int F, in
         quant32_store(o, xq + (size_t)p * c + ch, xs + (size_t)p * (c / 32) + ch / 32, ch & 31);
 }
 
-// kern.Linear of a float32 weight (kern.go:185-201 -> ws.matmul,
-// gemm.go:116-185) applied to each utterance's `per` rows: with more than 16
-// rows, the rows in whole groups of six take k6x16 (kernels_amd64.s:5-88):
-// from the bias, each chunk of 256 k's fma chain (from zero) is added in.
-// This kernel computes that form for every row, 64 rows x 64 columns per
-// workgroup, 4 x 4 outputs per thread, 32 k's of x and w staged in LDS per
-// pass; the rows the reference sends to gemvRows are rewritten afterwards by
-// pw_f32_rows_kernel.  k is a multiple of 32.
-constexpr int kPwT = 64, kPwK = 32;
-__global__ __launch_bounds__(256) void pw_f32_kernel(const float *__restrict__ x, const float *__restrict__ w,
-                                                     const float *__restrict__ bias, float *__restrict__ y, int rows,
-                                                     int n, int k) {
-    __shared__ __align__(16) float as[kPwK][kPwT + 4];
-    __shared__ __align__(16) float ws[kPwK][kPwT + 4];
-    const int tid = threadIdx.x, tr = tid / 16, tc = tid % 16;
-    const int r0 = blockIdx.y * kPwT, c0 = blockIdx.x * kPwT;
-    float acc[4][4], out[4][4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const int col = c0 + tc * 4 + j;
-        const float bj = col < n ? bias[col] : 0.f;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            out[i][j] = bj;
-            acc[i][j] = 0.f;
-        }
-    }
-    for (int k0 = 0; k0 < k; k0 += kPwK) {
-        for (int e = tid; e < kPwT * kPwK; e += 256) {
-            const int rr = e / kPwK, kk = e % kPwK, gr = r0 + rr, gc = c0 + rr;
-            as[kk][rr] = gr < rows ? x[(size_t)gr * k + k0 + kk] : 0.f;
-            ws[kk][rr] = gc < n ? w[(size_t)gc * k + k0 + kk] : 0.f;
-        }
-        __syncthreads();
-#pragma unroll 8
-        for (int kk = 0; kk < kPwK; ++kk) {
-            const float4 a = *reinterpret_cast<const float4 *>(&as[kk][tr * 4]);
-            const float4 b = *reinterpret_cast<const float4 *>(&ws[kk][tc * 4]);
-            const float av[4] = {a.x, a.y, a.z, a.w}, bv[4] = {b.x, b.y, b.z, b.w};
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-#pragma unroll
-                for (int j = 0; j < 4; ++j) acc[i][j] = __fmaf_rn(av[i], bv[j], acc[i][j]);
-        }
-        __syncthreads();
-        if ((k0 + kPwK) % 256 == 0 || k0 + kPwK >= k) {
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-#pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    out[i][j] = __fadd_rn(acc[i][j], out[i][j]);
-                    acc[i][j] = 0.f;
-                }
-        }
-    }
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int row = r0 + tr * 4 + i;
-        if (row >= rows) continue;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int col = c0 + tc * 4 + j;
-            if (col < n) y[(size_t)row * n + col] = out[i][j];
-        }
-    }
-}
-
-// The rows of each utterance that ws.matmul sends to gemvRows (gemm.go:
-// 182-184, 195-259): rows lo..per-1 of every utterance (all of them when
-// per <= 16): dotF32x4 for whole groups of four columns, dotF32Go for the
-// rest, then the bias added.  One thread per output.
-__global__ void pw_f32_rows_kernel(const float *__restrict__ x, const float *__restrict__ w,
-                                   const float *__restrict__ bias, float *__restrict__ y, int B, int per, int lo,
-                                   int n, int k) {
-    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x, tail = (size_t)(per - lo);
-    if (i >= (size_t)B * tail * n) return;
-    const int j = (int)(i % n);
-    const size_t rr = i / n, row = rr / tail * per + lo + rr % tail;
-    const float *xr = x + row * k, *wj = w + (size_t)j * k;
-    const float o = j < (n & ~3) ? dot_x4_s(xr, wj, 1, k) : dot_go_s(xr, wj, 1, k);
-    y[row * n + j] = __fadd_rn(o, bias[j]);
-}
-
 // The last pointwise output through maskRows and ReLU, flattened [t][c*F+f]
 // (encoder.go:158-166) and rounded to Q8_0 for the output Linear: one
 // workgroup per kept (utterance, frame): frames drop.. of each utterance's
@@ -1492,22 +1409,6 @@ grx_status cshape(grx_conformer *m, int B, int frames) {
 
 unsigned grid_for(size_t n) { return (unsigned)std::min<size_t>((n + 255) / 256, 1u << 20); }
 
-// A float32 pointwise Linear over B utterances of `per` rows of c values:
-// the k6x16 form for every row, then the gemvRows rows rewritten.
-grx_status pw_f32(hipStream_t st, const float *x, const float *w, const float *bias, float *y, int B, int per, int c) {
-    const int rows = B * per, lo = per > 16 ? per / 6 * 6 : 0;
-    if (lo > 0) {
-        pw_f32_kernel<<<dim3((c + kPwT - 1) / kPwT, (rows + kPwT - 1) / kPwT), 256, 0, st>>>(x, w, bias, y, rows, c, c);
-        GRX_LAUNCHED("pw_f32_kernel");
-    }
-    const size_t tail = (size_t)B * (per - lo) * c;
-    if (tail > 0) {
-        pw_f32_rows_kernel<<<(unsigned)((tail + 255) / 256), 256, 0, st>>>(x, w, bias, y, B, per, lo, c, c);
-        GRX_LAUNCHED("pw_f32_rows_kernel");
-    }
-    return GRX_OK;
-}
-
 // One run of the encoder over B utterances (or streams' chunks): the
 // pre-encoder on `frames` mel frames (T rows each, the first `drop` cut,
 // Tp kept), xscale, then every block.
@@ -1546,7 +1447,7 @@ grx_status enqueue_run(grx_conformer *m, const CRun &r, hipStream_t st) {
                                                                       m->w3f ? bf.subx : nullptr);
     GRX_LAUNCHED("sub_conv01_kernel");
     if (m->w3f) {
-        if ((s = pw_f32(st, bf.subx, m->w3f, m->b3, bf.suby, B, T2 * F2, c)) != GRX_OK) return s;
+        if ((s = grx_float_rows_f32(st, bf.subx, m->w3f, m->b3, bf.suby, B, T2 * F2, c, c)) != GRX_OK) return s;
     } else if ((s = grx_gemm_q8_launch(st, m->w3, bf.xq, bf.xs, B * T2 * F2, m->b3, bf.suby, c)) != GRX_OK) {
         return s;
     }
@@ -1554,7 +1455,7 @@ grx_status enqueue_run(grx_conformer *m, const CRun &r, hipStream_t st) {
                                                       bf.xs, m->w6f ? bf.subx : nullptr);
     GRX_LAUNCHED("sub_dwconv_kernel");
     if (m->w6f) {
-        if ((s = pw_f32(st, bf.subx, m->w6f, m->b6, bf.sub0, B, T * F3, c)) != GRX_OK) return s;
+        if ((s = grx_float_rows_f32(st, bf.subx, m->w6f, m->b6, bf.sub0, B, T * F3, c, c)) != GRX_OK) return s;
     } else if ((s = grx_gemm_q8_launch(st, m->w6, bf.xq, bf.xs, B * T * F3, m->b6, bf.sub0, c)) != GRX_OK) {
         return s;
     }

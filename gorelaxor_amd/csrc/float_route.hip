@@ -22,6 +22,92 @@
 
 namespace {
 
+// kern.Linear of a float32 weight (kern.go:185-201 -> ws.matmul,
+// gemm.go:116-185) applied to each of B groups of `per` rows: with more than
+// 16 rows, the rows in whole groups of six take k6x16 (kernels_amd64.s:5-88):
+// from the bias (0 without one), each chunk of 256 k's fma chain (from zero)
+// is added in.  This kernel computes that form for every row, 64 rows x 64
+// columns per workgroup, 4 x 4 outputs per thread, 32 k's of x and w staged
+// in LDS per pass (k's past the end staged as zeros: fma(0, 0, acc) leaves a
+// chain that started at +0 unchanged); the rows the reference sends to
+// gemvRows are rewritten afterwards by f32_rows_gemv_kernel.
+constexpr int kPwT = 64, kPwK = 32;
+__global__ __launch_bounds__(256) void f32_rows_k6x16_kernel(const float *__restrict__ x, const float *__restrict__ w,
+                                                             const float *__restrict__ bias, float *__restrict__ y,
+                                                             int rows, int n, int k) {
+    __shared__ __align__(16) float as[kPwK][kPwT + 4];
+    __shared__ __align__(16) float ws[kPwK][kPwT + 4];
+    const int tid = threadIdx.x, tr = tid / 16, tc = tid % 16;
+    const int r0 = blockIdx.y * kPwT, c0 = blockIdx.x * kPwT;
+    float acc[4][4], out[4][4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int col = c0 + tc * 4 + j;
+        const float bj = (bias != nullptr && col < n) ? bias[col] : 0.f;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            out[i][j] = bj;
+            acc[i][j] = 0.f;
+        }
+    }
+    for (int k0 = 0; k0 < k; k0 += kPwK) {
+        for (int e = tid; e < kPwT * kPwK; e += 256) {
+            const int rr = e / kPwK, kk = e % kPwK, gr = r0 + rr, gc = c0 + rr;
+            const bool kin = k0 + kk < k;
+            as[kk][rr] = (gr < rows && kin) ? x[(size_t)gr * k + k0 + kk] : 0.f;
+            ws[kk][rr] = (gc < n && kin) ? w[(size_t)gc * k + k0 + kk] : 0.f;
+        }
+        __syncthreads();
+#pragma unroll 8
+        for (int kk = 0; kk < kPwK; ++kk) {
+            const float4 a = *reinterpret_cast<const float4 *>(&as[kk][tr * 4]);
+            const float4 b = *reinterpret_cast<const float4 *>(&ws[kk][tc * 4]);
+            const float av[4] = {a.x, a.y, a.z, a.w}, bv[4] = {b.x, b.y, b.z, b.w};
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) acc[i][j] = __fmaf_rn(av[i], bv[j], acc[i][j]);
+        }
+        __syncthreads();
+        if ((k0 + kPwK) % 256 == 0 || k0 + kPwK >= k) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    out[i][j] = __fadd_rn(acc[i][j], out[i][j]);
+                    acc[i][j] = 0.f;
+                }
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int row = r0 + tr * 4 + i;
+        if (row >= rows) continue;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int col = c0 + tc * 4 + j;
+            if (col < n) y[(size_t)row * n + col] = out[i][j];
+        }
+    }
+}
+
+// The rows of each group that ws.matmul sends to gemvRows (gemm.go:
+// 182-184, 195-259): rows lo..per-1 of every group (all of them when
+// per <= 16): dotF32x4 for whole groups of four columns, dotF32Go for the
+// rest, then the bias added (none without one).  One thread per output.
+__global__ void f32_rows_gemv_kernel(const float *__restrict__ x, const float *__restrict__ w,
+                                     const float *__restrict__ bias, float *__restrict__ y, int B, int per, int lo,
+                                     int n, int k) {
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x, tail = (size_t)(per - lo);
+    if (i >= (size_t)B * tail * n) return;
+    const int j = (int)(i % n);
+    const size_t rr = i / n, row = rr / tail * per + lo + rr % tail;
+    const float *xr = x + row * k, *wj = w + (size_t)j * k;
+    const float o = j < (n & ~3) ? dot_x4_s(xr, wj, 1, k) : dot_go_s(xr, wj, 1, k);
+    y[row * n + j] = bias != nullptr ? __fadd_rn(o, bias[j]) : o;
+}
+
+
 // What happens to output row `row` of n after the bias (GrxFloatEpi):
 // stored, stored through kern.SiLU (siluAVX's x/(EXP8(0-x)+1) for the rows
 // below n &^ 7, siluGo's x/(1+expf(-x)) past them, kernels_amd64.go:241-250),
@@ -174,5 +260,25 @@ extern "C" grx_status grx_linear_f32(grx_ctx *ctx, float *dst, const float *x, c
     if ((s = grx_float_gemv_f32(ctx->stream, dw, rows, cols, dx, dbias, dy)) != GRX_OK) return s;
     GRX_HIP(hipMemcpyAsync(dst, dy, yb, hipMemcpyDeviceToHost, ctx->stream));
     GRX_HIP(hipStreamSynchronize(ctx->stream));
+    return GRX_OK;
+}
+
+// kern.Linear of a float32 weight w [n][k] over B groups of `per` rows of x
+// [B*per][k] into y [B*per][n] (bias nullable): the k6x16 form for every
+// row when a group has more than 16, then the gemvRows rows rewritten.
+grx_status grx_float_rows_f32(hipStream_t st, const float *x, const float *w, const float *bias, float *y, int B,
+                              int per, int n, int k) {
+    const int rows = B * per, lo = per > 16 ? per / 6 * 6 : 0;
+    if (rows == 0 || n == 0) return GRX_OK;
+    if (lo > 0) {
+        f32_rows_k6x16_kernel<<<dim3((n + kPwT - 1) / kPwT, (rows + kPwT - 1) / kPwT), 256, 0, st>>>(x, w, bias, y,
+                                                                                                     rows, n, k);
+        GRX_LAUNCHED("f32_rows_k6x16_kernel");
+    }
+    const size_t tail = (size_t)B * (per - lo) * n;
+    if (tail > 0) {
+        f32_rows_gemv_kernel<<<(unsigned)((tail + 255) / 256), 256, 0, st>>>(x, w, bias, y, B, per, lo, n, k);
+        GRX_LAUNCHED("f32_rows_gemv_kernel");
+    }
     return GRX_OK;
 }

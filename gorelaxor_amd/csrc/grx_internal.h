@@ -50,6 +50,14 @@ grx_status grx_float_gemv_q8(hipStream_t st, const grx_weight *w, const float *x
                              GrxFloatEpi e = GrxFloatEpi());
 grx_status grx_float_gemv_f32(hipStream_t st, const float *w, int n, int k, const float *x, const float *bias,
                               float *y, GrxFloatEpi e = GrxFloatEpi());
+// kern.Linear of a float32 weight [n][k] over B groups of `per` rows (the
+// k6x16 form for rows in whole groups of six when a group has more than 16,
+// gemvRows for the rest); bias nullable.
+grx_status grx_float_rows_f32(hipStream_t st, const float *x, const float *w, const float *bias, float *y, int B,
+                              int per, int n, int k);
+// quantU8 of m rows of k values (k % 32 == 0, rows lda apart) into q [m][k]
+// and sc [m][k/32]
+grx_status grx_quant_rows(hipStream_t st, const float *x, int lda, int m, int k, int8_t *q, float *sc);
 
 // whisper_sample.hip: one row of logits through whisper's token rules and
 // sampler (the public grx_whisper_rules / grx_whisper_seq, resolved)

@@ -1183,6 +1183,14 @@ static grx_status gemv_rows_preq(hipStream_t st, float *dst, int ldc, const int8
     return GRX_OK;
 }
 
+grx_status grx_quant_rows(hipStream_t st, const float *x, int lda, int m, int k, int8_t *q, float *sc) {
+    const int nb = k / GRX_QK;
+    if (m * nb == 0) return GRX_OK;
+    quant_act_kernel<<<grx_ceil_div(m * nb, 256), 256, 0, st>>>(x, lda, m, nb, q, sc);
+    GRX_LAUNCHED("quant_act_kernel");
+    return GRX_OK;
+}
+
 extern "C" grx_status grx_quant_act_dev(grx_ctx *ctx, int8_t *q, float *sc, const float *x, int lda,
                                         int m, int k) {
     if (!ctx) return grx_fail(GRX_EINVAL, "grx_quant_act_dev: NULL context");

@@ -399,6 +399,53 @@ grx_status grx_pocket_run(grx_pocket *m, const float *x, int T, float *out);
  * output and eos (n, may be NULL) its end-of-speech logit. */
 grx_status grx_pocket_frames(grx_pocket *m, const float *latents, int n, float *outs, float *eos);
 
+/* ---- pocket-TTS's Mimi decoder (latents to audio) ---- */
+
+/* mimiDecoder of pockettts/mimi.go:23-152 (its settings as pockettts.Load
+ * reads them, pockettts/model.go:280-308): a latent's 1x1 projection to
+ * d channels, the depthwise transposed upsampling by `upsample` with its
+ * overlap carried to the next call, the context-limited transformer with
+ * layer scales (pockettts/nn.go:142-254), then SEANet's decoder (a conv,
+ * per ratio ELU + transposed conv + residual blocks, ELU + a last conv to
+ * one channel; model.go:163-181).  Every Linear takes kern.MatMul's route
+ * for its weight: Q8_0 matrices the int8 route (model.go:331-366 packs
+ * them), float32 ones the float route.  max_latents bounds the latents one
+ * decode call takes. */
+typedef struct {
+    int d, heads, ff, layers, context, ldim, upsample;
+    double period;
+    int n_ratios;
+    int ratios[8];
+    int n_filters, kernel_size, residual_kernel_size, last_kernel_size, dilation_base, compress, n_residual;
+    int max_latents;
+} grx_mimi_hparams;
+
+typedef struct grx_mimi grx_mimi;
+
+grx_status grx_mimi_create(grx_ctx *ctx, const grx_mimi_hparams *hp, grx_mimi **out);
+grx_status grx_mimi_destroy(grx_mimi *m);
+/* The decoder's tensors by the names pockettts/model.go reads ("mimi.quant",
+ * "mimi.up", "mimi.dec_tf.0.attn_qkv.weight", "mimi.dec_tf.0.ls1",
+ * "mimi.dec.2.weight", "mimi.dec.3.1.bias", ...): a matrix as ggml Q8_0
+ * rows or float32 (told apart by nbytes, as a GGUF file types them),
+ * vectors float32; shapes checked.  The last one given completes the
+ * model. */
+grx_status grx_mimi_set_tensor(grx_mimi *m, const char *name, const void *data, size_t nbytes);
+/* A fresh decState (mimi.go:112-119): empty caches, position 0, no carried
+ * rows. */
+grx_status grx_mimi_reset(grx_mimi *m);
+/* mimiDecoder.decode (mimi.go:122-152): n latents (host float32 [n][ldim],
+ * already scaled back by the flow LM's mean and std) to
+ * n * samples_per_latent samples in out (host), continuing the stream.
+ * The speak loop's fade-in of the first frame (speak.go:180-184) is the
+ * caller's.  GRX_ESIZE past max_latents. */
+grx_status grx_mimi_decode(grx_mimi *m, const float *lat, int n, float *out);
+/* The same with device buffers, enqueued on the context's stream. */
+grx_status grx_mimi_decode_dev(grx_mimi *m, const float *lat, int n, float *out);
+/* upsample x the product of the ratios (1920 at the english_2026-09
+ * settings); 0 for NULL. */
+int grx_mimi_samples_per_latent(const grx_mimi *m);
+
 /* ---- FastConformer encoder with Q8_0 weights ---- */
 
 /* Model.encode (conformer/encoder.go:432-489) of a FastConformer (HParams
