@@ -65,9 +65,9 @@ def parse():
     p.add_argument("--conformer-reps", type=int, default=10, help="timed encodes per batch size")
     p.add_argument("--no-conformer", action="store_true")
     p.add_argument("--no-conformer-stream", action="store_true")
-    p.add_argument("--profile-leg", choices=["speak", "tdt", "sampler", "conformer-stream"],
+    p.add_argument("--profile-leg", choices=["speak", "tdt", "sampler", "conformer-stream", "mimi"],
                    help="only this workload, for a profiler (no headline line): the pocket speak loop, the TDT "
-                        "decode, whisper's sampler, or the streaming chunk steps")
+                        "decode, whisper's sampler, the streaming chunk steps, or the Mimi decoder")
     p.add_argument("--copy-calibration", action="store_true",
                    help="only copy the ring's bytes device to device 3 times (reference reading for HBM counters)")
     return p.parse_args()
@@ -387,6 +387,7 @@ def lm_bench(args) -> dict:
                                      f"prefix {1e3 * (t1 - t0):.0f} ms"}
     lm.close()
     res["speak"] = speak_bench(args, hp, t, x)
+    res["mimi"] = mimi_bench(args)
     return res
 
 
@@ -438,6 +439,50 @@ def speak_bench(args, hp, t, x) -> dict:
                            "kind": "port", **cpu_info(),
                            "sample": f"the same {n} frames (transformer step and flow head) on the "
                                                      "oracle (C kernels, 1 thread, Python glue)"}
+    return res
+
+
+def mimi_bench(args) -> dict:
+    """Pocket TTS's Mimi decoder at the english_2026-09 shape (d 512, 8
+    heads, 2 layers, context 250, 16x upsampling, SEANet 6/5/4: 1920
+    samples at 24 kHz per latent), random-init with the converter's typing,
+    decoding lm_frames latents one per call as the speak loop does (a host
+    round trip each): latents/s and the real-time factor; the first 8
+    latents checked bit for bit against the oracle, whose rate is the CPU
+    baseline."""
+    import oracle
+    from gorelaxor_amd.mimi import MimiDecoder
+    from gorelaxor_amd.synth import MIMI, mimi_latents, mimi_model
+
+    hp = dict(MIMI)
+    n = args.lm_frames
+    t = mimi_model(hp, seed=17)
+    lat = mimi_latents(hp, n, seed=18)
+    dec = MimiDecoder(hp, t, max_latents=1)
+    spl = dec.samples_per_latent
+    first = np.concatenate([dec.decode(lat[k:k + 1]) for k in range(8)])
+    times = []
+    for _ in range(3):
+        dec.reset()
+        t0 = time.perf_counter()
+        for k in range(n):
+            dec.decode(lat[k:k + 1])
+        times.append(time.perf_counter() - t0)
+    dec.close()
+    best = min(times)
+    audio_s = n * spl / 24000.0
+    res = {"latents_per_s": round(n / best, 1), "ms_per_latent": round(best / n * 1e3, 4), "latents": n,
+           "samples_per_latent": spl, "real_time_factor": round(audio_s / best, 1),
+           "shape": "d_model 512, 8 heads, 2 layers, FFN 2048, context 250, upsample 16, SEANet ratios 6/5/4, "
+                    "64 filters"}
+    oracle.build()
+    ref = oracle.MimiOracle(hp, t)
+    t0 = time.perf_counter()
+    want = np.concatenate([ref.decode(lat[k:k + 1]) for k in range(8)])
+    cpu_s = time.perf_counter() - t0
+    res["parity_first_8_bit_exact"] = bool(np.array_equal(want.view(np.uint32), first.view(np.uint32)))
+    res["cpu_baseline"] = {"value": round(8 / cpu_s, 2), "unit": "latents/s", "cores": 1, "kind": "port",
+                           **cpu_info(), "sample": f"the first 8 latents on the oracle (C, 1 thread), {cpu_s:.2f} s"}
     return res
 
 
@@ -728,6 +773,18 @@ def profile_leg(args) -> dict:
                 tok = sample_logits(lg, rules, tokens=[300])
             out[name] = tok["id"]
         return {"leg": leg, "ids": out}
+    if leg == "mimi":
+        # the Mimi decoder at the english_2026-09 shape, 40 latents one per
+        # call, after 8 to warm up
+        from gorelaxor_amd.mimi import MimiDecoder
+        from gorelaxor_amd.synth import MIMI, mimi_latents, mimi_model
+        hp = dict(MIMI)
+        dec = MimiDecoder(hp, mimi_model(hp, seed=17), max_latents=1)
+        lat = mimi_latents(hp, 48, seed=18)
+        for k in range(48):
+            dec.decode(lat[k:k + 1])
+        dec.close()
+        return {"leg": leg, "latents": 48}
     # the streaming chunk steps alone
     return {"leg": leg, "conformer_stream": conformer_stream_bench(args)}
 
@@ -736,7 +793,7 @@ def main():
     args = parse()
     if args.gpus != 1:
         print(json.dumps({"error": "this build measures one GPU; --gpus must be 1",
-                          "detail": "the path shards data-parallel by stream/utterance with no exchange; see DESIGN.md"}))
+                          "detail": "the path shards data-parallel by stream/utterance with no exchange"}))
         sys.exit(2)
 
     from gorelaxor_amd import hiprt, kern

@@ -91,6 +91,28 @@ __global__ __launch_bounds__(256) void f32_rows_k6x16_kernel(const float *__rest
     }
 }
 
+// The k6x16 form of the rows below lo of each group, one thread per output
+// (for narrow outputs, where the 64 x 64 tiles would idle): from the bias,
+// each chunk of 256 k's fma chain added in.
+__global__ void f32_rows_k6x16_one_kernel(const float *__restrict__ x, const float *__restrict__ w,
+                                          const float *__restrict__ bias, float *__restrict__ y, int B, int per,
+                                          int lo, int n, int k) {
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= (size_t)B * lo * n) return;
+    const int j = (int)(i % n);
+    const size_t rr = i / n, row = rr / lo * per + rr % lo;
+    const float *a = x + row * k, *b = w + (size_t)j * k;
+    float c = bias != nullptr ? bias[j] : 0.f;
+    for (int k0 = 0; k0 < k; k0 += 256) {
+        const int kn = min(256, k - k0);
+        float acc = 0.f;
+#pragma unroll 8
+        for (int kk = 0; kk < kn; ++kk) acc = __fmaf_rn(a[k0 + kk], b[k0 + kk], acc);
+        c = __fadd_rn(acc, c);
+    }
+    y[row * n + j] = c;
+}
+
 // The rows of each group that ws.matmul sends to gemvRows (gemm.go:
 // 182-184, 195-259): rows lo..per-1 of every group (all of them when
 // per <= 16): dotF32x4 for whole groups of four columns, dotF32Go for the
@@ -270,7 +292,11 @@ grx_status grx_float_rows_f32(hipStream_t st, const float *x, const float *w, co
                               int per, int n, int k) {
     const int rows = B * per, lo = per > 16 ? per / 6 * 6 : 0;
     if (rows == 0 || n == 0) return GRX_OK;
-    if (lo > 0) {
+    if (lo > 0 && n < kPwT) {  // narrow outputs: a thread per output
+        const size_t cnt = (size_t)B * lo * n;
+        f32_rows_k6x16_one_kernel<<<(unsigned)((cnt + 255) / 256), 256, 0, st>>>(x, w, bias, y, B, per, lo, n, k);
+        GRX_LAUNCHED("f32_rows_k6x16_one_kernel");
+    } else if (lo > 0) {
         f32_rows_k6x16_kernel<<<dim3((n + kPwT - 1) / kPwT, (rows + kPwT - 1) / kPwT), 256, 0, st>>>(x, w, bias, y,
                                                                                                      rows, n, k);
         GRX_LAUNCHED("f32_rows_k6x16_kernel");

@@ -31,6 +31,7 @@ namespace {
 
 constexpr int kThreads = 256;
 constexpr int kMaxPast = 64;  // carried rows of one convolution
+constexpr size_t kMaxAttnLds = 128 * 1024;  // a head's value rows and one query's scores
 
 // ---------------------------------------------------------------- kernels
 
@@ -127,60 +128,56 @@ __global__ void mimi_rope_ring_kernel(float *__restrict__ qkv, int T, int d, int
 }
 
 // attend (nn.go:200-254) for T rows after pos0 positions, one workgroup per
-// head: query p sees keys max(lo0, p - context + 1) .. p, lo0 = max(0,
-// pos0 - context + 1); the scores of the nk = pos0 + T - lo0 keys by
-// MatMulF32's route for T rows, each row's window scaled and softmaxed
-// (expSub), the rest 0; then T < 4: AddScaled in key order, zero weights
-// skipped; else the product with the transposed values by the same route.
-// Keys and values come from the ring; sc and vt are scratch [heads][T][nk]
-// and [heads][hd][nk].
+// (head, query row): query p sees keys max(lo0, p - context + 1) .. p, lo0 =
+// max(0, pos0 - context + 1); the row's scores over its window by
+// MatMulF32's route for T rows (outside the window they are 0 after the
+// softmax, as the reference clears them), scaled and softmaxed (expSub's
+// order, block_softmax); then T < 4: AddScaled over the nk = pos0 + T - lo0
+// keys in order, zero weights skipped; else the product of the row with the
+// values by the same route, over all nk keys.  The head's value rows are
+// staged in LDS ([nk][hd]), keys read from the ring.
 __global__ __launch_bounds__(kThreads) void mimi_attn_kernel(const float *__restrict__ qkv, const float *__restrict__ kr,
                                                              const float *__restrict__ vr, int cap, long long pos0,
                                                              int T, int d, int hd, int context, float scale,
-                                                             float *__restrict__ sc, float *__restrict__ vt,
                                                              float *__restrict__ att) {
-    const int h = blockIdx.x, tid = threadIdx.x;
+    extern __shared__ __align__(16) float sm[];
+    const int h = blockIdx.x, r = blockIdx.y, tid = threadIdx.x;
     const long long lo0 = pos0 - context + 1 > 0 ? pos0 - context + 1 : 0;
     const int nk = (int)(pos0 + T - lo0);
-    float *S = sc + (size_t)h * T * nk;
-    float *Vt = vt + (size_t)h * hd * nk;
-    for (int i = tid; i < T * nk; i += blockDim.x) {
-        const int r = i / nk, j = i % nk;
-        const float *kj = kr + (size_t)((lo0 + j) % cap) * d + h * hd;
-        S[i] = matmul_f32_one(qkv + (size_t)r * 3 * d + h * hd, kj, 1, hd, r, T, j, nk);
-    }
-    for (int i = tid; i < hd * nk; i += blockDim.x) {
-        const int e = i / nk, j = i % nk;
-        Vt[i] = vr[(size_t)((lo0 + j) % cap) * d + h * hd + e];
-    }
-    __syncthreads();
-    for (int r = tid; r < T; r += blockDim.x) {
-        float *row = S + (size_t)r * nk;
-        const long long p = pos0 + r;
-        const long long lo = p - context + 1 > lo0 ? p - context + 1 : lo0;
-        float *s = row + (lo - lo0);
-        const int ns = (int)(p + 1 - lo);
-        for (int j = 0; j < ns; ++j) s[j] = __fmul_rn(s[j], scale);
-        seq_softmax(s, ns);
-        for (int j = 0; j < lo - lo0; ++j) row[j] = 0.f;
-        for (int j = (int)(p + 1 - lo0); j < nk; ++j) row[j] = 0.f;
+    const long long p = pos0 + r;
+    const long long lo = p - context + 1 > lo0 ? p - context + 1 : lo0;
+    const int off = (int)(lo - lo0), ns = (int)(p + 1 - lo);
+    float *V = sm;            // [nk][hd]
+    float *s = V + nk * hd;   // [nk]
+    float *q = s + nk;        // [hd]
+    float *part = q + hd;     // block_softmax's 32
+    for (int i = tid; i < hd; i += blockDim.x) q[i] = qkv[(size_t)r * 3 * d + h * hd + i];
+    for (int i = tid; i < nk * hd; i += blockDim.x) {
+        const int j = i / hd, e = i % hd;
+        V[i] = vr[(size_t)((lo0 + j) % cap) * d + h * hd + e];
     }
     __syncthreads();
+    for (int j = tid; j < nk; j += blockDim.x) {
+        float v = 0.f;
+        if (j >= off && j < off + ns)
+            v = __fmul_rn(matmul_f32_one(q, kr + (size_t)((lo0 + j) % cap) * d + h * hd, 1, hd, r, T, j, nk), scale);
+        s[j] = v;
+    }
+    __syncthreads();
+    block_softmax(s + off, ns, part);
     const int h8 = hd & ~7;
-    for (int i = tid; i < T * hd; i += blockDim.x) {
-        const int r = i / hd, e = i % hd;
-        const float *row = S + (size_t)r * nk;
+    for (int e = tid; e < hd; e += blockDim.x) {
         float o;
         if (T < 4) {
             o = 0.f;
             for (int j = 0; j < nk; ++j) {
-                const float w = row[j];
+                const float w = s[j];
                 if (w == 0.f) continue;
-                const float v = Vt[(size_t)e * nk + j];
+                const float v = V[(size_t)j * hd + e];
                 o = e < h8 ? __fmaf_rn(w, v, o) : __fadd_rn(o, __fmul_rn(w, v));
             }
         } else {
-            o = matmul_f32_one(row, Vt + (size_t)e * nk, 1, nk, r, T, e, hd);
+            o = matmul_f32_one(s, V + e, hd, nk, r, T, e, hd);
         }
         att[(size_t)r * d + h * hd + e] = o;
     }
@@ -334,16 +331,23 @@ struct grx_mimi {
     float *up_part = nullptr;
     // work
     float *x = nullptr, *y = nullptr, *h = nullptr, *o = nullptr, *col = nullptr, *z = nullptr;
-    float *qkv = nullptr, *att = nullptr, *f = nullptr, *sc = nullptr, *vt = nullptr, *lat = nullptr, *out = nullptr;
+    float *qkv = nullptr, *att = nullptr, *f = nullptr, *lat = nullptr, *out = nullptr;
     int8_t *xq = nullptr;
     float *xs = nullptr;
     float *rope = nullptr;        // device cos [tmax][hd/2] then sin
     float *rope_host = nullptr;   // pinned
     std::vector<float> freqs;
-    size_t act_floats = 0, col_floats = 0, z_floats = 0, h_floats = 0, q_bytes = 0;
+    size_t act_floats = 0, col_floats = 0, z_floats = 0, h_floats = 0, q_bytes = 0, attn_lds = 0;
 };
 
 namespace {
+
+// LDS of the attention kernel: a head's value rows over the ring's
+// positions, one query's scores, the query, block_softmax's 32 floats
+size_t attn_lds(const grx_mimi_hparams &hp) {
+    const size_t cap = (size_t)hp.context + (size_t)hp.max_latents * hp.upsample - 1, hd = hp.d / hp.heads;
+    return (cap * hd + cap + hd + 32) * 4;
+}
 
 grx_status malloc_dev(grx_mimi *m, size_t bytes, void **out) {
     *out = nullptr;
@@ -451,8 +455,8 @@ grx_status enqueue_decode(grx_mimi *m, hipStream_t st, const float *lat, int n, 
         mimi_rope_ring_kernel<<<blocks, kThreads, 0, st>>>(m->qkv, T, d, hd, m->rope, m->rope + (size_t)m->tmax * half,
                                                            L.kr, L.vr, m->cap, m->pos);
         GRX_LAUNCHED("mimi_rope_ring_kernel");
-        mimi_attn_kernel<<<hp.heads, kThreads, 0, st>>>(m->qkv, L.kr, L.vr, m->cap, m->pos, T, d, hd, hp.context,
-                                                        scale, m->sc, m->vt, m->att);
+        mimi_attn_kernel<<<dim3(hp.heads, T), kThreads, m->attn_lds, st>>>(m->qkv, L.kr, L.vr, m->cap, m->pos, T, d, hd,
+                                                                          hp.context, scale, m->att);
         GRX_LAUNCHED("mimi_attn_kernel");
         if ((s = lin(m, st, L.out, m->att, T, m->h)) != GRX_OK) return s;
         gridn((size_t)T * d, &blocks);
@@ -642,6 +646,10 @@ grx_status alloc_state(grx_mimi *m) {
     const int d = hp.d, half = m->hd / 2;
     grx_status s;
     m->cap = hp.context + m->tmax - 1;
+    m->attn_lds = attn_lds(hp);
+    if (m->attn_lds > 64 * 1024)
+        GRX_HIP(hipFuncSetAttribute((const void *)mimi_attn_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                    (int)m->attn_lds));
     for (MLayer &L : m->layers) {
         if ((s = malloc_t(m, (size_t)m->cap * d, &L.kr)) != GRX_OK) return s;
         if ((s = malloc_t(m, (size_t)m->cap * d, &L.vr)) != GRX_OK) return s;
@@ -662,8 +670,6 @@ grx_status alloc_state(grx_mimi *m) {
     if ((s = malloc_t(m, (size_t)m->tmax * 3 * d, &m->qkv)) != GRX_OK) return s;
     if ((s = malloc_t(m, (size_t)m->tmax * d, &m->att)) != GRX_OK) return s;
     if ((s = malloc_t(m, (size_t)m->tmax * hp.ff, &m->f)) != GRX_OK) return s;
-    if ((s = malloc_t(m, (size_t)hp.heads * m->tmax * m->cap, &m->sc)) != GRX_OK) return s;
-    if ((s = malloc_t(m, (size_t)hp.heads * m->hd * m->cap, &m->vt)) != GRX_OK) return s;
     if ((s = malloc_t(m, m->q_bytes, &m->xq)) != GRX_OK) return s;
     if ((s = malloc_t(m, m->q_bytes / GRX_QK + 1, &m->xs)) != GRX_OK) return s;
     if ((s = malloc_t(m, (size_t)2 * m->tmax * half, &m->rope)) != GRX_OK) return s;
@@ -717,7 +723,7 @@ grx_status finalize(grx_mimi *m) {
             q.c.prev = q.a.prev = q.bb.prev = nullptr;
             q.t.partial = nullptr;
         }
-        m->up_part = m->x = m->y = m->h = m->o = m->col = m->z = m->qkv = m->att = m->f = m->sc = m->vt = nullptr;
+        m->up_part = m->x = m->y = m->h = m->o = m->col = m->z = m->qkv = m->att = m->f = nullptr;
         m->lat = m->out = m->rope = m->xs = nullptr;
         m->xq = nullptr;
         return s;
@@ -733,6 +739,9 @@ grx_status check_hp(const grx_mimi_hparams *hp) {
         return grx_fail(GRX_EINVAL, "grx_mimi_create: bad sizes (ff %d, layers %d, context %d, ldim %d, upsample %d, "
                                     "max_latents %d)", hp->ff, hp->layers, hp->context, hp->ldim, hp->upsample,
                         hp->max_latents);
+    if (attn_lds(*hp) > kMaxAttnLds)
+        return grx_fail(GRX_EINVAL, "grx_mimi_create: %d positions of context and %d latents a call need %zu bytes of "
+                                    "LDS (at most %zu)", hp->context, hp->max_latents, attn_lds(*hp), kMaxAttnLds);
     if (hp->n_ratios < 1 || hp->n_ratios > 8)
         return grx_fail(GRX_EINVAL, "grx_mimi_create: %d SEANet ratios", hp->n_ratios);
     for (int i = 0; i < hp->n_ratios; ++i)
