@@ -382,6 +382,10 @@ struct GemmOut {
     float scale = 1.0f;     // SCALE
     int8_t *yq = nullptr;   // SILU_Q: [m][rows] int8
     float *ys = nullptr;    //         [m][rows/32] scales
+    // [m][rows] floats the K-split product may use to carry each output's
+    // ordered chain from one run of blocks to the next when the weight has
+    // more blocks than one workgroup holds (few rows only); NULL: none
+    float *carry = nullptr;
 };
 grx_status grx_gemm_q8_launch_ex(hipStream_t st, const grx_weight *w, const int8_t *xq, const float *xs, int m,
                                  const float *bias, const GemmOut &o);

@@ -249,13 +249,17 @@ tail:
 // The tiles are numbered so that the workgroups of one weight column group
 // (the row groups of the activations) land on one XCD and share its L2:
 // workgroup i runs on XCD i % 8.
-constexpr int kKsMaxWaves = 8;
+// Waves a workgroup of the K-split kernel may have: 16 where a wave's
+// registers fit four waves a SIMD (16-column tiles of up to 8 blocks, 32-
+// column tiles of 4), else 8.
+constexpr int ks_max_waves(int ns, int kb) { return (ns == 1 && kb <= 8) || (ns == 2 && kb == 4) ? 16 : 8; }
 
 template <int EPI, int NS, int KB>
-__global__ __launch_bounds__(64 * kKsMaxWaves) void gemm_q8_ks_kernel(
+__global__ __launch_bounds__(64 * ks_max_waves(NS, KB)) void gemm_q8_ks_kernel(
     const int8_t *__restrict__ qs, const uint16_t *__restrict__ ds, int rows, int nb, const int8_t *__restrict__ xq,
     const float *__restrict__ xs, int m, const float *__restrict__ bias, float *__restrict__ y, int ldc, float scale,
-    int8_t *__restrict__ yq, float *__restrict__ ys, int ncg, int nrf, int da4) {
+    int8_t *__restrict__ yq, float *__restrict__ ys, int ncg, int nrf, int da4, int bbeg, int bend,
+    const float *init, int ldi) {
     static_assert(NS == 1 || NS == 2, "16 or 32 weight rows per tile");
     static_assert(KB % 4 == 0, "blocks per wave in whole groups of four");
     __shared__ float cx[2][NS * 4][64];
@@ -269,8 +273,11 @@ __global__ __launch_bounds__(64 * kKsMaxWaves) void gemm_q8_ks_kernel(
     const int li = lane & 15, lk = lane >> 4;
     const int n0 = cg * 16 * NS;                          // first weight row of the tile
     const int tile = n0 >> 6, sub = n0 & 63;              // 64-row weight tile, row offset in it
-    const int b0 = wave * KB;
-    const int nbw = min(KB, nb - b0);                     // this wave's blocks (>= 1)
+    // blocks bbeg..bend-1 of the nb (a run of them when the chain is carried
+    // through init); the chain starts from init[row][col] when given, else
+    // from the bias
+    const int b0 = bbeg + wave * KB;
+    const int nbw = min(KB, bend - b0);                   // this wave's blocks (>= 1)
 
     // A: activation row 16*rf+li (clamped: rows past m are computed, never
     // stored), bytes 8*lk.. of each block
@@ -293,7 +300,7 @@ __global__ __launch_bounds__(64 * kKsMaxWaves) void gemm_q8_ks_kernel(
     float da[KB][4];
 #pragma unroll
     for (int u = 0; u < KB; ++u) {
-        const int b = min(b0 + u, nb - 1);
+        const int b = min(b0 + u, bend - 1);
         av[u] = *reinterpret_cast<const long *>(ap + (size_t)b * GRX_QK);
 #pragma unroll
         for (int s = 0; s < NS; ++s) {
@@ -304,7 +311,7 @@ __global__ __launch_bounds__(64 * kKsMaxWaves) void gemm_q8_ks_kernel(
     if (da4) {  // nb % 4 == 0 and xs 16-byte aligned: four blocks per load
 #pragma unroll
         for (int q = 0; q < KB / 4; ++q) {
-            const int b = min(b0 + 4 * q, nb - 4);
+            const int b = min(b0 + 4 * q, bend - 4);
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const float4 v = *reinterpret_cast<const float4 *>(sp[r] + b);
@@ -317,7 +324,7 @@ __global__ __launch_bounds__(64 * kKsMaxWaves) void gemm_q8_ks_kernel(
     } else {
 #pragma unroll
         for (int u = 0; u < KB; ++u) {
-            const int b = min(b0 + u, nb - 1);
+            const int b = min(b0 + u, bend - 1);
 #pragma unroll
             for (int r = 0; r < 4; ++r) da[u][r] = sp[r][b];
         }
@@ -339,7 +346,14 @@ __global__ __launch_bounds__(64 * kKsMaxWaves) void gemm_q8_ks_kernel(
     float c[NS][4];
     for (int p = 0; p < ks; ++p) {
         if (wave == p) {
-            if (p == 0) {
+            if (p == 0 && init != nullptr) {
+#pragma unroll
+                for (int s = 0; s < NS; ++s) {
+                    const int n = min(n0 + 16 * s + li, rows - 1);
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) c[s][r] = init[(size_t)min(drow[r], m - 1) * ldi + n];
+                }
+            } else if (p == 0) {
 #pragma unroll
                 for (int s = 0; s < NS; ++s) {
                     const int n = n0 + 16 * s + li;
@@ -674,29 +688,68 @@ int pick_ns(int m, int rows, int epi) {
 // 14 x 4096 x 1024 5.9 -> 4.8 us), 16-column tiles with 16 blocks per wave
 // past that (126 x 1024 x 4096 25 -> 19 us); the rounded SiLU output needs
 // the 32-column tiles (whole Q8_0 blocks).  False when a workgroup of
-// kKsMaxWaves waves cannot hold the weight's blocks.
-bool pick_ks(int nb, int epi, int *ns, int *kb) {
-    int n = (epi == GRX_GEMM_SILU_Q || nb <= 2 * kKsMaxWaves * 4) ? 2 : 1;
+// ks_max_waves waves cannot hold the weight's blocks.
+// With one or two 16-row groups (decode-time rows: a few streams, a chunk
+// of one stream) the grid has few tiles, so the narrowest tiles and the
+// fewest blocks per wave that fit a workgroup win (8 x 1280 x 1280: 16
+// columns, 4 blocks a wave, 10 waves a workgroup).
+bool pick_ks(int m, int nb, int epi, bool carry, int *ns, int *kb) {
+    const bool few = grx_ceil_div(m, 16) <= 2 && epi != GRX_GEMM_SILU_Q;
+    int n = (epi == GRX_GEMM_SILU_Q || (!few && nb <= 2 * 8 * 4)) ? 2 : 1;
     const int tn = grx_tune(GRX_TUNE_GEMM_NS);
     if (tn == 1 || tn == 2) n = (epi == GRX_GEMM_SILU_Q) ? 2 : tn;
-    const int kbmax = n == 2 ? 8 : 16;
-    if (nb > kKsMaxWaves * kbmax) return false;
     int k = n == 2 ? 8 : 16;
+    if (few) {
+        k = 4;
+        while (k < 16 && nb > ks_max_waves(n, k) * k) k *= 2;
+        // a carried chain: runs of 16 waves x 8 blocks (8 x 1280 x 5120:
+        // 23.6 us on the GEMV, two runs here)
+        if (carry && k > 8) k = 8;
+    }
     const int tk = grx_tune(GRX_TUNE_GEMM_KB);
-    if ((tk == 4 || tk == 8 || tk == 16) && tk <= kbmax && nb <= kKsMaxWaves * tk) k = tk;
+    if ((tk == 4 || tk == 8 || tk == 16) && !(n == 2 && tk == 16)) k = tk;
+    if (n == 2 && k > 8) k = 8;
+    if (nb > ks_max_waves(n, k) * k && !(carry && few)) return false;
     *ns = n;
     *kb = k;
     return true;
 }
 
+// One K-split launch over blocks bbeg..bend-1, the chain from init (or the
+// bias when NULL); the runs of a carried chain store into o.carry.
+template <int EPI, int NS, int KB>
+void launch_ks_run(hipStream_t st, const grx_weight *w, const int8_t *xq, const float *xs, int m, const float *bias,
+                   float *y, int ldc, const GemmOut &o, int da4, int bbeg, int bend, const float *init) {
+    // init (a carried chain) rows are w->rows apart
+    const int ncg = grx_ceil_div(w->rows, 16 * NS), nrf = grx_ceil_div(m, 16);
+    const int ks = grx_ceil_div(bend - bbeg, KB);
+    const int groups = grx_ceil_div(ncg, 8) * 8 * nrf;
+    gemm_q8_ks_kernel<EPI, NS, KB><<<groups, 64 * ks, 0, st>>>(w->qs, w->ds, w->rows, w->nb, xq, xs, m, bias, y, ldc,
+                                                               o.scale, o.yq, o.ys, ncg, nrf, da4, bbeg, bend, init,
+                                                               w->rows);
+}
+
+// The whole product: one launch, or (a carry buffer given, more blocks than
+// a workgroup holds) runs of ks_max_waves * KB blocks, each continuing the
+// chain the last one stored, the epilogue in the last.
 template <int EPI, int NS, int KB>
 void launch_ks(hipStream_t st, const grx_weight *w, const int8_t *xq, const float *xs, int m, const float *bias,
                const GemmOut &o, int da4) {
-    const int ncg = grx_ceil_div(w->rows, 16 * NS), nrf = grx_ceil_div(m, 16);
-    const int ks = grx_ceil_div(w->nb, KB);
-    const int groups = grx_ceil_div(ncg, 8) * 8 * nrf;
-    gemm_q8_ks_kernel<EPI, NS, KB><<<groups, 64 * ks, 0, st>>>(w->qs, w->ds, w->rows, w->nb, xq, xs, m, bias, o.y,
-                                                               o.ldc, o.scale, o.yq, o.ys, ncg, nrf, da4);
+    const int run = ks_max_waves(NS, KB) * KB;
+    if (w->nb <= run || o.carry == nullptr) {
+        launch_ks_run<EPI, NS, KB>(st, w, xq, xs, m, bias, o.y, o.ldc, o, da4, 0, w->nb, nullptr);
+        return;
+    }
+    const float *init = nullptr;
+    for (int b = 0; b < w->nb; b += run) {
+        const int e = min(w->nb, b + run);
+        if (e < w->nb) {
+            launch_ks_run<GRX_GEMM_STORE, NS, KB>(st, w, xq, xs, m, bias, o.carry, w->rows, o, da4, b, e, init);
+            init = o.carry;
+        } else {
+            launch_ks_run<EPI, NS, KB>(st, w, xq, xs, m, bias, o.y, o.ldc, o, da4, b, e, init);
+        }
+    }
 }
 
 template <int EPI>
@@ -728,7 +781,7 @@ grx_status grx_gemm_q8_launch_ex(hipStream_t st, const grx_weight *w, const int8
     // K-split tiles up to 128
     const int kind = grx_tune(GRX_TUNE_GEMM_KERNEL);
     int ks_ns = 1, ks_kb = 4;
-    const bool ks_ok = pick_ks(w->nb, o.epi, &ks_ns, &ks_kb) && (kind == 2 || m <= 128);
+    const bool ks_ok = pick_ks(m, w->nb, o.epi, o.carry != nullptr, &ks_ns, &ks_kb) && (kind == 2 || m <= 128);
     if (kind == 3 || (kind != 1 && kind != 2 && m >= 256)) {  // many rows: the LDS-staged 64 x 128 tiles
         dim3 g2(grx_ceil_div(m, 64), grx_ceil_div(w->tiles, 2));
 #define GRX_GEMM_LDS(E)                                                                                           \

@@ -842,6 +842,18 @@ grx_status enqueue_step(grx_whisper *m, hipStream_t stream) {
                 m->q, L.self_k, L.self_v, m->pos, st, hd, sc, rc, kv_stream, m->att, nullptr, nullptr, hp.n_text_ctx);
         GRX_LAUNCHED("self_attn_kernel");
         auto out_proj = [&](grx_weight *w, const float *b, bool rounded) {  // x += att . W^T + b
+            if (S > 1 && w->nb <= 128) {
+                // several streams: the K-split matrix-core product, its
+                // blocks over ~10 waves per 16-column tile (the GEMV puts a
+                // 1280-row product on 20 workgroups)
+                if (!rounded && (s = grx_quant_rows(stream, m->att, st, S, st, m->att_q, m->att_s)) != GRX_OK)
+                    return s;
+                GemmOut o;
+                o.y = m->x;
+                o.ldc = st;
+                o.epi = GRX_GEMM_ADD;
+                return grx_gemm_q8_launch_ex(stream, w, m->att_q, m->att_s, S, b, o);
+            }
             GemvArgs a = gemv_args(w);
             a.x = m->att;
             a.lda = st;
@@ -923,7 +935,14 @@ grx_status enqueue_step(grx_whisper *m, hipStream_t stream) {
             if ((s = grx_gemv_launch(stream, S, sep ? GRX_PRO_PREQ : GRX_PRO_LN, GRX_EPI_GELU_Q, a, 0)) != GRX_OK)
                 return s;
         }
-        {  // x += ff . Wfc2^T + b
+        if (S > 1) {  // x += ff . Wfc2^T + b, several streams: the K-split product, the chain carried in q
+            GemmOut o;
+            o.y = m->x;
+            o.ldc = st;
+            o.epi = GRX_GEMM_ADD;
+            o.carry = m->q;
+            if ((s = grx_gemm_q8_launch_ex(stream, L.fc2, m->ff_q, m->ff_s, S, L.fc2_b, o)) != GRX_OK) return s;
+        } else {  // x += ff . Wfc2^T + b
             GemvArgs a = gemv_args(L.fc2);
             a.xq = m->ff_q;
             a.xs = m->ff_s;

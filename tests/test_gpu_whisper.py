@@ -148,18 +148,29 @@ def test_streams_tokens_identical_to_each_oracle_decode(kern, orc, n, fuse_ln):
         _streams_vs_oracle(orc, n)
 
 
-def _streams_vs_oracle(orc, n):
-    hp = dict(WHISPER_TINY_TEST)
+@pytest.mark.parametrize("n", [2, 8])
+def test_streams_wide_rows_carried_chain(kern, orc, n):
+    """Streams at d_model 1280 (the large-v3-turbo width): the out and
+    cross-out products on the K-split matrix-core kernel, and fc2 (5120
+    inputs, 160 blocks: more than one workgroup holds) in two runs with each
+    output's chain carried between them; greedy tokens equal each stream's
+    own oracle decode."""
+    hp = dict(WHISPER_TINY_TEST, n_state=1280, n_head=20, n_layer=2, n_audio_ctx=64, n_vocab=700)
+    _streams_vs_oracle(orc, n, hp, steps=8)
+
+
+def _streams_vs_oracle(orc, n, hp=None, steps=30):
+    hp = dict(hp or WHISPER_TINY_TEST)
     t = whisper_model(hp, seed=21)
     dec, encs = _streams(hp, t, n, seed=40)
     prompts = [[1 + k, 2, 3 + 2 * k, 4] for k in range(n)]
-    got = dec.greedy_streams(prompts, 30)
+    got = dec.greedy_streams(prompts, steps)
     for k in range(n):
         ref = orc.WhisperOracle(hp, t)
         ref.set_encoder_output(encs[k])
-        assert list(got[k]) == list(ref.greedy(prompts[k], 30)), k
+        assert list(got[k]) == list(ref.greedy(prompts[k], steps)), k
     # the loop again from empty caches repeats itself (graph replays)
-    assert np.array_equal(dec.greedy_streams(prompts, 30), got)
+    assert np.array_equal(dec.greedy_streams(prompts, steps), got)
 
 
 def test_streams_errors(kern):
