@@ -272,6 +272,67 @@ __device__ void ln_row(float *v, int n, const float *w, const float *bb, double 
     __syncthreads();
 }
 
+// ln_rows_kernel's work with one wave per row (no workgroup barrier): the
+// row as NP float4 pieces per lane (piece P = 64 j + lane, n <= 256 NP),
+// kern.LayerNorm by wave_ln32 (DPP sums with the in-order check), and the
+// rounding of each 32-value block (8 pieces in 8 consecutive lanes) by
+// xor-shuffle maxima.
+template <bool OUT, bool Q, int NP>
+__global__ __launch_bounds__(64) void ln_rows_wave_kernel(float *__restrict__ x, int n, const float *__restrict__ w1,
+                                                          const float *__restrict__ b1, const float *__restrict__ w2,
+                                                          const float *__restrict__ b2, int8_t *__restrict__ xq,
+                                                          float *__restrict__ xs) {
+    const int r = blockIdx.x, lane = threadIdx.x, npc = n / 4;
+    float4 *x4 = reinterpret_cast<float4 *>(x + (size_t)r * n);
+    float4 xv[NP], wv[NP], bv[NP];
+#pragma unroll
+    for (int j = 0; j < NP; ++j) {
+        const int P = min(j * 64 + lane, npc - 1);
+        xv[j] = x4[P];
+        wv[j] = reinterpret_cast<const float4 *>(w1)[P];
+        bv[j] = reinterpret_cast<const float4 *>(b1)[P];
+    }
+    wave_ln32<NP>(xv, wv, bv, npc, lane);
+    if constexpr (OUT) {
+#pragma unroll
+        for (int j = 0; j < NP; ++j)
+            if (j * 64 + lane < npc) x4[j * 64 + lane] = xv[j];
+        if constexpr (Q) {
+#pragma unroll
+            for (int j = 0; j < NP; ++j) {
+                const int P = min(j * 64 + lane, npc - 1);
+                wv[j] = reinterpret_cast<const float4 *>(w2)[P];
+                bv[j] = reinterpret_cast<const float4 *>(b2)[P];
+            }
+            wave_ln32<NP>(xv, wv, bv, npc, lane);
+        }
+    }
+    if constexpr (Q) {
+        // quantU8 of block b = pieces 8b..8b+7 (n % 32 == 0)
+#pragma unroll
+        for (int j = 0; j < NP; ++j) {
+            const float4 v = xv[j];
+            float amax = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
+#pragma unroll
+            for (int o = 4; o > 0; o >>= 1) {
+                const float t = __shfl_xor(amax, o, 8);
+                amax = t > amax ? t : amax;
+            }
+            const int P = j * 64 + lane;
+            if (P >= npc) continue;
+            const float id = amax != 0.0f ? __fdiv_rn(127.0f, amax) : 0.0f;
+            auto q1 = [&](float f) {
+                float t = rintf(__fmul_rn(f, id));
+                t = fminf(fmaxf(t, -128.0f), 127.0f);
+                return (uint32_t)(uint8_t)(int8_t)(int)t;
+            };
+            const uint32_t pk = q1(v.x) | q1(v.y) << 8 | q1(v.z) << 16 | q1(v.w) << 24;
+            *reinterpret_cast<uint32_t *>(xq + (size_t)r * n + 4 * P) = pk;
+            if ((P & 7) == 0) xs[(size_t)r * (n / 32) + P / 8] = __fmul_rn(amax, grx_bits_f32(0x3c010204u));
+        }
+    }
+}
+
 // One workgroup per row of x [rows][n].  OUT: x = LN(x; w1, b1) written
 // back first (a block's norm_out, encoder.go:426).  Q: the row (after OUT,
 // LN(x; w2, b2)) rounded to Q8_0 into xq [rows][n], xs [rows][n/32].
@@ -1409,6 +1470,26 @@ grx_status cshape(grx_conformer *m, int B, int frames) {
 
 unsigned grid_for(size_t n) { return (unsigned)std::min<size_t>((n + 255) / 256, 1u << 20); }
 
+// The rows' LayerNorm (and rounding) by ln_rows_wave_kernel where a wave
+// holds the row (n % 32 == 0, n <= 1280), else ln_rows_kernel.
+template <bool OUT, bool Q>
+grx_status ln_rows_launch(hipStream_t st, int R, float *x, int n, const float *w1, const float *b1, const float *w2,
+                          const float *b2, int8_t *xq, float *xs) {
+    if (n % 32 == 0 && n <= 1280) {
+        if (n <= 512)
+            ln_rows_wave_kernel<OUT, Q, 2><<<R, 64, 0, st>>>(x, n, w1, b1, w2, b2, xq, xs);
+        else if (n <= 1024)
+            ln_rows_wave_kernel<OUT, Q, 4><<<R, 64, 0, st>>>(x, n, w1, b1, w2, b2, xq, xs);
+        else
+            ln_rows_wave_kernel<OUT, Q, 5><<<R, 64, 0, st>>>(x, n, w1, b1, w2, b2, xq, xs);
+        GRX_LAUNCHED("ln_rows_wave_kernel");
+        return GRX_OK;
+    }
+    ln_rows_kernel<OUT, Q><<<R, kRowThreads, (size_t)n * 4, st>>>(x, n, w1, b1, w2, b2, xq, xs);
+    GRX_LAUNCHED("ln_rows_kernel");
+    return GRX_OK;
+}
+
 // One run of the encoder over B utterances (or streams' chunks): the
 // pre-encoder on `frames` mel frames (T rows each, the first `drop` cut,
 // Tp kept), xscale, then every block.
@@ -1473,9 +1554,8 @@ grx_status enqueue_run(grx_conformer *m, const CRun &r, hipStream_t st) {
     }
     const size_t row_smem = (size_t)d * 4;
     // the first block's feed-forward LayerNorm
-    ln_rows_kernel<false, true><<<R, kRowThreads, row_smem, st>>>(bf.x, d, m->blk[0].ff1.norm_w, m->blk[0].ff1.norm_b,
-                                                                  nullptr, nullptr, bf.xq, bf.xs);
-    GRX_LAUNCHED("ln_rows_kernel");
+    if ((s = ln_rows_launch<false, true>(st, R, bf.x, d, m->blk[0].ff1.norm_w, m->blk[0].ff1.norm_b,
+                                                                  nullptr, nullptr, bf.xq, bf.xs)) != GRX_OK) return s;
     const float scale = (float)(1.0 / std::sqrt((double)hd));
     const int nblk = (Tp + r.keys.bl - 1) / r.keys.bl;
     for (int i = 0; i < hp.layers; ++i) {
@@ -1496,9 +1576,8 @@ grx_status enqueue_run(grx_conformer *m, const CRun &r, hipStream_t st) {
         };
         if ((s = ff_pair(Bk.ff1)) != GRX_OK) return s;
         // attention (encoder.go:259-330)
-        ln_rows_kernel<false, true><<<R, kRowThreads, row_smem, st>>>(bf.x, d, Bk.norm_attn_w, Bk.norm_attn_b, nullptr,
-                                                                      nullptr, bf.xq, bf.xs);
-        GRX_LAUNCHED("ln_rows_kernel");
+        if ((s = ln_rows_launch<false, true>(st, R, bf.x, d, Bk.norm_attn_w, Bk.norm_attn_b, nullptr,
+                                                                      nullptr, bf.xq, bf.xs)) != GRX_OK) return s;
         if ((s = grx_gemm_q8_launch(st, Bk.qkv, bf.xq, bf.xs, R, Bk.qkv_b, bf.qkv, 3 * d)) != GRX_OK) return s;
         AttnIO io{};
         io.q = bf.qkv;
@@ -1546,9 +1625,8 @@ grx_status enqueue_run(grx_conformer *m, const CRun &r, hipStream_t st) {
             if ((s = grx_gemm_q8_launch_ex(st, Bk.out, bf.xq, bf.xs, R, Bk.out_b, o)) != GRX_OK) return s;
         }
         // convolution module (encoder.go:343-397)
-        ln_rows_kernel<false, true><<<R, kRowThreads, row_smem, st>>>(bf.x, d, Bk.norm_conv_w, Bk.norm_conv_b, nullptr,
-                                                                      nullptr, bf.xq, bf.xs);
-        GRX_LAUNCHED("ln_rows_kernel");
+        if ((s = ln_rows_launch<false, true>(st, R, bf.x, d, Bk.norm_conv_w, Bk.norm_conv_b, nullptr,
+                                                                      nullptr, bf.xq, bf.xs)) != GRX_OK) return s;
         if ((s = grx_gemm_q8_launch(st, Bk.pw1, bf.xq, bf.xs, R, Bk.pw1_b, bf.conv, 2 * d)) != GRX_OK) return s;
         conf_glu_kernel<<<grid_for((size_t)R * d), 256, 0, st>>>(bf.conv, R, Tp, d, r.lens, bf.glu);
         GRX_LAUNCHED("conf_glu_kernel");
@@ -1582,19 +1660,17 @@ grx_status enqueue_run(grx_conformer *m, const CRun &r, hipStream_t st) {
             if ((s = grx_gemm_q8_launch_ex(st, Bk.pw2, bf.xq, bf.xs, R, Bk.pw2_b, o)) != GRX_OK) return s;
         }
         // second feed-forward, then norm_out (and the next block's first LayerNorm)
-        ln_rows_kernel<false, true><<<R, kRowThreads, row_smem, st>>>(bf.x, d, Bk.ff2.norm_w, Bk.ff2.norm_b, nullptr,
-                                                                      nullptr, bf.xq, bf.xs);
-        GRX_LAUNCHED("ln_rows_kernel");
+        if ((s = ln_rows_launch<false, true>(st, R, bf.x, d, Bk.ff2.norm_w, Bk.ff2.norm_b, nullptr,
+                                                                      nullptr, bf.xq, bf.xs)) != GRX_OK) return s;
         if ((s = ff_pair(Bk.ff2)) != GRX_OK) return s;
         if (i + 1 < hp.layers) {
             const CFF &N = m->blk[i + 1].ff1;
-            ln_rows_kernel<true, true><<<R, kRowThreads, row_smem, st>>>(bf.x, d, Bk.norm_out_w, Bk.norm_out_b,
-                                                                         N.norm_w, N.norm_b, bf.xq, bf.xs);
+            if ((s = ln_rows_launch<true, true>(st, R, bf.x, d, Bk.norm_out_w, Bk.norm_out_b,
+                                                                         N.norm_w, N.norm_b, bf.xq, bf.xs)) != GRX_OK) return s;
         } else {
-            ln_rows_kernel<true, false><<<R, kRowThreads, row_smem, st>>>(bf.x, d, Bk.norm_out_w, Bk.norm_out_b,
-                                                                          nullptr, nullptr, nullptr, nullptr);
+            if ((s = ln_rows_launch<true, false>(st, R, bf.x, d, Bk.norm_out_w, Bk.norm_out_b,
+                                                                          nullptr, nullptr, nullptr, nullptr)) != GRX_OK) return s;
         }
-        GRX_LAUNCHED("ln_rows_kernel");
     }
     return GRX_OK;
 }

@@ -778,10 +778,14 @@ grx_status grx_gemm_q8_launch_ex(hipStream_t st, const grx_weight *w, const int8
     // GEMM_KERNEL picks the kernel (tests force each one with it): the
     // LDS-staged tiles from 256 rows on, the whole-K register walk from 129
     // (e.g. 224 x 1024 x 4096: 26 us against 36 for the K-split tiles), the
-    // K-split tiles up to 128
+    // K-split tiles up to 128 rows where the register walk has few tiles or
+    // a long K (at 126 rows: 4096 x 1024 10.4 us on the register walk
+    // against 11.9 K-split; 2048 x 1024 8.1 against 7.3; 1024 x 4096 25
+    // against 19)
     const int kind = grx_tune(GRX_TUNE_GEMM_KERNEL);
     int ks_ns = 1, ks_kb = 4;
-    const bool ks_ok = pick_ks(m, w->nb, o.epi, o.carry != nullptr, &ks_ns, &ks_kb) && (kind == 2 || m <= 128);
+    const bool ks_ok = pick_ks(m, w->nb, o.epi, o.carry != nullptr, &ks_ns, &ks_kb) &&
+                       (kind == 2 || (m <= 128 && (m <= 32 || w->rows <= 2048 || w->nb > 64)));
     if (kind == 3 || (kind != 1 && kind != 2 && m >= 256)) {  // many rows: the LDS-staged 64 x 128 tiles
         dim3 g2(grx_ceil_div(m, 64), grx_ceil_div(w->tiles, 2));
 #define GRX_GEMM_LDS(E)                                                                                           \
