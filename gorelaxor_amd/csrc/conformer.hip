@@ -1361,17 +1361,22 @@ int pad_left(const grx_conformer_hparams &hp) {
     return hp.conv_left >= 0 && hp.conv_right >= 0 ? hp.conv_left : (hp.conv_kernel - 1) / 2;
 }
 
-// Which attention kernel runs and its LDS: the staged kernel takes 8 query
-// rows per workgroup for few workgroups, 16 for many; past what LDS holds
+// Which attention kernel runs and its LDS: the staged kernel takes 4 query
+// rows per workgroup for few workgroups, 8 or 16 for more; past what LDS holds
 // the unstaged kernel runs.  nk: the most keys a block sees.
 grx_status attn_pick(int B, int heads, int nblk, int bl, int nk, int hd, int *rq, size_t *smem) {
-    *rq = B * heads * nblk * ((bl + 7) / 8) < 1024 ? 8 : 16;
-    if (grx_tune(GRX_TUNE_CONF_ATTN_RQ) >= 0) *rq = grx_tune(GRX_TUNE_CONF_ATTN_RQ);  // 0 (unstaged), 8 or 16, for tests
-    if (*rq != 0 && *rq != 8 && *rq != 16) *rq = 8;
+    // (batch 1 at T = 126: 128 workgroups of 8 rows; 4 rows each measured
+    // 4.32 -> 4.20 ms an encode, the streaming chunks 3.28 -> 3.20 ms)
+    const long n8 = (long)B * heads * nblk * ((bl + 7) / 8);
+    *rq = n8 < 256 ? 4 : n8 < 1024 ? 8 : 16;
+    if (grx_tune(GRX_TUNE_CONF_ATTN_RQ) >= 0) *rq = grx_tune(GRX_TUNE_CONF_ATTN_RQ);  // 0 (unstaged), 4, 8 or 16, for tests
+    if (*rq != 0 && *rq != 4 && *rq != 8 && *rq != 16) *rq = 8;
     const size_t sq = hd + 1;
     const size_t stage = std::max((size_t)(nk + *rq - 1) * sq, (size_t)nk * hd);
     const size_t staged = ((size_t)2 * *rq * sq + (size_t)2 * *rq * (nk | 1) + 2 * *rq + stage) * 4;
-    const void *fn = *rq == 8 ? (const void *)conf_attn_lds_kernel<8> : (const void *)conf_attn_lds_kernel<16>;
+    const void *fn = *rq == 4   ? (const void *)conf_attn_lds_kernel<4>
+                     : *rq == 8 ? (const void *)conf_attn_lds_kernel<8>
+                                : (const void *)conf_attn_lds_kernel<16>;
     if (*rq != 0 && staged <= 160 * 1024 &&
         (staged <= 64 * 1024 ||
          hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)staged) == hipSuccess)) {
@@ -1606,7 +1611,10 @@ grx_status enqueue_run(grx_conformer *m, const CRun &r, hipStream_t st) {
             io.pp = r.pp + (size_t)i * d;
             io.ldp = hp.layers * d;
         }
-        if (r.attn_rq == 8)
+        if (r.attn_rq == 4)
+            conf_attn_lds_kernel<4><<<dim3(nblk * ((r.keys.bl + 3) / 4), hp.heads, B), kAttnLdsThreads, r.attn_smem,
+                                      st>>>(io, r.keys, Bk.pos_u, Bk.pos_v, d, hd, scale, bf.xq, bf.xs);
+        else if (r.attn_rq == 8)
             conf_attn_lds_kernel<8><<<dim3(nblk * ((r.keys.bl + 7) / 8), hp.heads, B), kAttnLdsThreads, r.attn_smem,
                                       st>>>(io, r.keys, Bk.pos_u, Bk.pos_v, d, hd, scale, bf.xq, bf.xs);
         else if (r.attn_rq == 16)

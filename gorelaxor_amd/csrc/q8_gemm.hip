@@ -700,11 +700,12 @@ bool pick_ks(int m, int nb, int epi, bool carry, int *ns, int *kb) {
     if (tn == 1 || tn == 2) n = (epi == GRX_GEMM_SILU_Q) ? 2 : tn;
     int k = n == 2 ? 8 : 16;
     if (few) {
-        k = 4;
-        while (k < 16 && nb > ks_max_waves(n, k) * k) k *= 2;
-        // a carried chain: runs of 16 waves x 8 blocks (8 x 1280 x 5120:
-        // 23.6 us on the GEMV, two runs here)
-        if (carry && k > 8) k = 8;
+        // up to 64 blocks 16 waves of 4; past that 8 waves of 16 (14 x 1024
+        // x 4096: 9.2 us against 10.6 for 16 waves of 8); a carried chain
+        // in runs of 16 waves x 8 blocks (8 x 1280 x 5120: 23.6 us on the
+        // GEMV, two runs here)
+        k = nb <= ks_max_waves(n, 4) * 4 ? 4 : 16;
+        if (carry && nb > ks_max_waves(n, 16) * 16) k = 8;
     }
     const int tk = grx_tune(GRX_TUNE_GEMM_KB);
     if ((tk == 4 || tk == 8 || tk == 16) && !(n == 2 && tk == 16)) k = tk;

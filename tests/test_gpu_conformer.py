@@ -59,7 +59,7 @@ def test_tiny_float32_pre_encoder_pointwise(kern, orc, seconds):
     enc.close()
 
 
-@pytest.mark.parametrize("rq", [0, 8, 16])
+@pytest.mark.parametrize("rq", [0, 4, 8, 16])
 def test_tiny_attention_variants_bit_exact(kern, orc, rq):
     """The unstaged attention kernel and the LDS-staged one at 8 and 16 query
     rows per workgroup give the same bits as the oracle (T = 19: one query

@@ -92,7 +92,7 @@ def test_stream_long_left_context(kern, orc, right):
     assert _stream_case(kern, orc, STREAM_TINY, t, right, 8.0, 62) >= 99
 
 
-@pytest.mark.parametrize("rq", [0, 8, 16])
+@pytest.mark.parametrize("rq", [0, 4, 8, 16])
 def test_stream_attention_kernels(kern, orc, rq):
     """Each attention kernel form on the chunk steps: unstaged, and staged
     with 8 or 16 query rows per workgroup."""
