@@ -108,6 +108,7 @@ enum {
     GRX_TUNE_WAVE_VALUES,     // 0: whisper cross values on the wide-workgroup kernel
     GRX_TUNE_ARGMAX_ATOMIC,   // 1: the decoders' argmax through a contended atomic
     GRX_TUNE_NO_GRAPH,        // 1: model loops launch kernel by kernel (no HIP graphs)
+    GRX_TUNE_GEMM_STAGE_A,    // 0: the K-split kernel reads activations straight from memory, 1: through LDS
     GRX_TUNE_COUNT
 };
 int grx_tune(int id);

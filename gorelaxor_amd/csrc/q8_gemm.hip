@@ -254,7 +254,17 @@ tail:
 // column tiles of 4), else 8.
 constexpr int ks_max_waves(int ns, int kb) { return (ns == 1 && kb <= 8) || (ns == 2 && kb == 4) ? 16 : 8; }
 
-template <int EPI, int NS, int KB>
+// With SA the activations go through LDS: each wave copies its 16 rows x KB
+// blocks with 16-byte loads (a row's KB*32 bytes in whole cache lines, where
+// the MFMA fragment loads touch 16 rows' lines for 32 bytes each) and its
+// 16 x KB activation scales with one, then reads the fragments from LDS.
+// Bytes of LDS per wave for the staged activations: 16 rows of KB*32 bytes,
+// 16 apart beyond that (the fragment reads of 16 rows fall in different
+// banks), then the scales as [block][row].
+constexpr int ks_stage_row(int kb) { return kb * 32 + 16; }
+constexpr int ks_stage_bytes(int kb) { return 16 * ks_stage_row(kb) + 16 * kb * 4; }
+
+template <int EPI, int NS, int KB, bool SA>
 __global__ __launch_bounds__(64 * ks_max_waves(NS, KB)) void gemm_q8_ks_kernel(
     const int8_t *__restrict__ qs, const uint16_t *__restrict__ ds, int rows, int nb, const int8_t *__restrict__ xq,
     const float *__restrict__ xs, int m, const float *__restrict__ bias, float *__restrict__ y, int ldc, float scale,
@@ -263,6 +273,7 @@ __global__ __launch_bounds__(64 * ks_max_waves(NS, KB)) void gemm_q8_ks_kernel(
     static_assert(NS == 1 || NS == 2, "16 or 32 weight rows per tile");
     static_assert(KB % 4 == 0, "blocks per wave in whole groups of four");
     __shared__ float cx[2][NS * 4][64];
+    extern __shared__ __align__(16) int8_t ks_stage[];
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int ks = __builtin_amdgcn_readfirstlane(blockDim.x >> 6);
@@ -295,9 +306,53 @@ __global__ __launch_bounds__(64 * ks_max_waves(NS, KB)) void gemm_q8_ks_kernel(
 
     // every load of the wave's blocks in flight at once (the last wave's
     // block indices past nb are clamped and their results never used)
-    long av[KB], bv[KB][NS];
+    long av[SA ? 1 : KB], bv[KB][NS];
     uint16_t dh[KB][NS];
-    float da[KB][4];
+    float da[SA ? 1 : KB][4];  // SA: read from LDS as the chain needs them
+    constexpr int RS = ks_stage_row(KB);
+    int8_t *sa = ks_stage + wave * ks_stage_bytes(KB);
+    float *sd = reinterpret_cast<float *>(sa + 16 * RS);
+    if constexpr (SA) {
+        // (the launcher takes this route only with xq and xs 16-byte
+        // aligned and nb % 4 == 0)
+        constexpr int NA = KB / 2;  // 16-byte loads of the 16 rows x KB blocks
+        int4 ra[NA];
+#pragma unroll
+        for (int j = 0; j < NA; ++j) {
+            const int e = j * 64 + lane, i = e / (2 * KB), pc = e % (2 * KB);
+            const int row = min(16 * rf + i, m - 1), b = min(b0 + pc / 2, bend - 1);
+            ra[j] = *reinterpret_cast<const int4 *>(xq + (size_t)row * K + (size_t)b * GRX_QK + (pc & 1) * 16);
+        }
+        constexpr int DQ = KB / 4;  // float4s of scales per row
+        float4 rd = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (lane < 16 * DQ) {
+            const int i = lane / DQ, q = lane % DQ;
+            const int row = min(16 * rf + i, m - 1), b = min(b0 + 4 * q, bend - 4);
+            rd = *reinterpret_cast<const float4 *>(xs + (size_t)row * nb + b);
+        }
+#pragma unroll
+        for (int u = 0; u < KB; ++u) {
+            const int b = min(b0 + u, bend - 1);
+#pragma unroll
+            for (int s = 0; s < NS; ++s) {
+                bv[u][s] = *reinterpret_cast<const long *>(bp + (size_t)b * 2048 + s * 256);
+                dh[u][s] = dp[(size_t)b * 64 + 16 * s];
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < NA; ++j) {
+            const int e = j * 64 + lane, i = e / (2 * KB), pc = e % (2 * KB);
+            *reinterpret_cast<int4 *>(sa + i * RS + pc * 16) = ra[j];
+        }
+        if (lane < 16 * DQ) {
+            const int i = lane / DQ, q = lane % DQ;
+            sd[(4 * q + 0) * 16 + i] = rd.x;
+            sd[(4 * q + 1) * 16 + i] = rd.y;
+            sd[(4 * q + 2) * 16 + i] = rd.z;
+            sd[(4 * q + 3) * 16 + i] = rd.w;
+        }
+        __syncthreads();
+    } else {
 #pragma unroll
     for (int u = 0; u < KB; ++u) {
         const int b = min(b0 + u, bend - 1);
@@ -329,18 +384,25 @@ __global__ __launch_bounds__(64 * ks_max_waves(NS, KB)) void gemm_q8_ks_kernel(
             for (int r = 0; r < 4; ++r) da[u][r] = sp[r][b];
         }
     }
+    }
     // the block dots and their scaled forms t = f32(s) * dw
     float t[KB][NS][4];
 #pragma unroll
-    for (int u = 0; u < KB; ++u)
+    for (int u = 0; u < KB; ++u) {
+        long a;
+        if constexpr (SA)
+            a = *reinterpret_cast<const long *>(sa + li * RS + u * GRX_QK + 8 * lk);
+        else
+            a = av[u];
 #pragma unroll
         for (int s = 0; s < NS; ++s) {
             v4i d = {0, 0, 0, 0};
-            d = __builtin_amdgcn_mfma_i32_16x16x32_i8(av[u], bv[u][s], d, 0, 0, 0);
+            d = __builtin_amdgcn_mfma_i32_16x16x32_i8(a, bv[u][s], d, 0, 0, 0);
             const float dw = grx_f16_to_f32(dh[u][s]);
 #pragma unroll
             for (int r = 0; r < 4; ++r) t[u][s][r] = __fmul_rn((float)d[r], dw);
         }
+    }
 
     // the ordered chain, one wave after another
     float c[NS][4];
@@ -367,13 +429,36 @@ __global__ __launch_bounds__(64 * ks_max_waves(NS, KB)) void gemm_q8_ks_kernel(
 #pragma unroll
                     for (int r = 0; r < 4; ++r) c[s][r] = cx[(p - 1) & 1][4 * s + r][lane];
             }
+            // block u's activation scales of the lane's rows 4*lk .. 4*lk+3
+            auto scales = [&](int u) {
+                if constexpr (SA) {
+                    const float4 v = *reinterpret_cast<const float4 *>(sd + u * 16 + 4 * lk);
+                    return v;
+                } else {
+                    return make_float4(da[u][0], da[u][1], da[u][2], da[u][3]);
+                }
+            };
+            if (nbw == KB) {
 #pragma unroll
-            for (int u = 0; u < KB; ++u) {
-                if (u < nbw) {
+                for (int u = 0; u < KB; ++u) {
+                    const float4 a4 = scales(u);
+                    const float av4[4] = {a4.x, a4.y, a4.z, a4.w};
 #pragma unroll
                     for (int s = 0; s < NS; ++s)
 #pragma unroll
-                        for (int r = 0; r < 4; ++r) c[s][r] = __fmaf_rn(t[u][s][r], da[u][r], c[s][r]);
+                        for (int r = 0; r < 4; ++r) c[s][r] = __fmaf_rn(t[u][s][r], av4[r], c[s][r]);
+                }
+            } else {
+#pragma unroll
+                for (int u = 0; u < KB; ++u) {
+                    if (u < nbw) {
+                        const float4 a4 = scales(u);
+                        const float av4[4] = {a4.x, a4.y, a4.z, a4.w};
+#pragma unroll
+                        for (int s = 0; s < NS; ++s)
+#pragma unroll
+                            for (int r = 0; r < 4; ++r) c[s][r] = __fmaf_rn(t[u][s][r], av4[r], c[s][r]);
+                    }
                 }
             }
             if (p + 1 < ks) {
@@ -682,30 +767,40 @@ int pick_ns(int m, int rows, int epi) {
     return ns;
 }
 
-// The K-split kernel's tile width and blocks per wave.  Measured on the
-// encoder's products at 14 and 126 rows (MI355X): 32-column tiles with 8
-// blocks per wave for K up to 2048 (126 x 1024 x 1024 7.7 -> 5.5 us,
-// 14 x 4096 x 1024 5.9 -> 4.8 us), 16-column tiles with 16 blocks per wave
-// past that (126 x 1024 x 4096 25 -> 19 us); the rounded SiLU output needs
-// the 32-column tiles (whole Q8_0 blocks).  False when a workgroup of
-// ks_max_waves waves cannot hold the weight's blocks.
-// With one or two 16-row groups (decode-time rows: a few streams, a chunk
-// of one stream) the grid has few tiles, so the narrowest tiles and the
-// fewest blocks per wave that fit a workgroup win (8 x 1280 x 1280: 16
-// columns, 4 blocks a wave, 10 waves a workgroup).
-bool pick_ks(int m, int nb, int epi, bool carry, int *ns, int *kb) {
+// The K-split kernel's tile width and blocks per wave.  Activations staged
+// through LDS (sa; measured on MI355X at 126 rows): 32-column tiles of 8
+// blocks for the wide short-K products (126 x 4096 x 1024 8.2 us against
+// 8.9, 3072 x 1024 7.3 against 7.4), else 16-column tiles of 16 blocks
+// (1024 x 4096 9.7 us, 1024 x 1024 5.1, 2048 x 1024 6.2); with one or two
+// 16-row groups 8 blocks a wave up to 64 blocks (8 x 1280 x 1280 4.8 us
+// against 5.0 for 4), 16 past that (14 x 1024 x 4096 8.0 against 9.1).
+// Activations read straight from memory (16-byte alignment or whole
+// groups of four blocks missing): 32-column tiles with 8 blocks per wave
+// for K up to 2048 (126 x 1024 x 1024 7.7 -> 5.5 us, 14 x 4096 x 1024
+// 5.9 -> 4.8 us), 16-column tiles with 16 blocks per wave past that
+// (126 x 1024 x 4096 25 -> 19 us), and with one or two 16-row groups the
+// fewest blocks per wave that fit a workgroup (8 x 1280 x 1280: 16 columns,
+// 4 blocks a wave, 10 waves a workgroup).  The rounded SiLU output needs the
+// 32-column tiles (whole Q8_0 blocks).  A carried chain runs in 16 waves x
+// 8 blocks (8 x 1280 x 5120: 23.6 us on the GEMV, two runs here).  False
+// when a workgroup of ks_max_waves waves cannot hold the weight's blocks.
+bool pick_ks(int m, int nb, int rows, int epi, bool carry, bool sa, int *ns, int *kb) {
     const bool few = grx_ceil_div(m, 16) <= 2 && epi != GRX_GEMM_SILU_Q;
-    int n = (epi == GRX_GEMM_SILU_Q || (!few && nb <= 2 * 8 * 4)) ? 2 : 1;
+    int n, k;
+    if (sa) {
+        n = (epi == GRX_GEMM_SILU_Q || (!few && nb <= 2 * 8 * 4 && rows >= 3072)) ? 2 : 1;
+        k = n == 2 ? 8 : 16;
+        if (few) k = nb <= 64 ? 8 : 16;
+    } else {
+        n = (epi == GRX_GEMM_SILU_Q || (!few && nb <= 2 * 8 * 4)) ? 2 : 1;
+        k = n == 2 ? 8 : 16;
+        if (few) k = nb <= ks_max_waves(n, 4) * 4 ? 4 : 16;
+    }
+    if (few && carry && nb > ks_max_waves(n, 16) * 16) k = 8;
     const int tn = grx_tune(GRX_TUNE_GEMM_NS);
-    if (tn == 1 || tn == 2) n = (epi == GRX_GEMM_SILU_Q) ? 2 : tn;
-    int k = n == 2 ? 8 : 16;
-    if (few) {
-        // up to 64 blocks 16 waves of 4; past that 8 waves of 16 (14 x 1024
-        // x 4096: 9.2 us against 10.6 for 16 waves of 8); a carried chain
-        // in runs of 16 waves x 8 blocks (8 x 1280 x 5120: 23.6 us on the
-        // GEMV, two runs here)
-        k = nb <= ks_max_waves(n, 4) * 4 ? 4 : 16;
-        if (carry && nb > ks_max_waves(n, 16) * 16) k = 8;
+    if (tn == 1 || tn == 2) {
+        n = (epi == GRX_GEMM_SILU_Q) ? 2 : tn;
+        if (n == 2 && k > 8) k = 8;
     }
     const int tk = grx_tune(GRX_TUNE_GEMM_KB);
     if ((tk == 4 || tk == 8 || tk == 16) && !(n == 2 && tk == 16)) k = tk;
@@ -716,55 +811,80 @@ bool pick_ks(int m, int nb, int epi, bool carry, int *ns, int *kb) {
     return true;
 }
 
-// One K-split launch over blocks bbeg..bend-1, the chain from init (or the
-// bias when NULL); the runs of a carried chain store into o.carry.
+// Whether the staged-activation instantiation may take its LDS (asked once;
+// more than 64 KB needs the attribute).
 template <int EPI, int NS, int KB>
+bool ks_stage_ok() {
+    static const bool ok = [] {
+        const int need = ks_max_waves(NS, KB) * ks_stage_bytes(KB);
+        const bool r = need <= 64 * 1024 ||
+                       hipFuncSetAttribute((const void *)gemm_q8_ks_kernel<EPI, NS, KB, true>,
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, need) == hipSuccess;
+        (void)hipGetLastError();
+        return r;
+    }();
+    return ok;
+}
+
+template <int EPI, int NS, int KB, bool SA>
 void launch_ks_run(hipStream_t st, const grx_weight *w, const int8_t *xq, const float *xs, int m, const float *bias,
                    float *y, int ldc, const GemmOut &o, int da4, int bbeg, int bend, const float *init) {
     // init (a carried chain) rows are w->rows apart
     const int ncg = grx_ceil_div(w->rows, 16 * NS), nrf = grx_ceil_div(m, 16);
     const int ks = grx_ceil_div(bend - bbeg, KB);
     const int groups = grx_ceil_div(ncg, 8) * 8 * nrf;
-    gemm_q8_ks_kernel<EPI, NS, KB><<<groups, 64 * ks, 0, st>>>(w->qs, w->ds, w->rows, w->nb, xq, xs, m, bias, y, ldc,
-                                                               o.scale, o.yq, o.ys, ncg, nrf, da4, bbeg, bend, init,
-                                                               w->rows);
+    const size_t smem = SA ? (size_t)ks * ks_stage_bytes(KB) : 0;
+    gemm_q8_ks_kernel<EPI, NS, KB, SA><<<groups, 64 * ks, smem, st>>>(w->qs, w->ds, w->rows, w->nb, xq, xs, m, bias,
+                                                                      y, ldc, o.scale, o.yq, o.ys, ncg, nrf, da4,
+                                                                      bbeg, bend, init, w->rows);
 }
 
 // The whole product: one launch, or (a carry buffer given, more blocks than
 // a workgroup holds) runs of ks_max_waves * KB blocks, each continuing the
 // chain the last one stored, the epilogue in the last.
-template <int EPI, int NS, int KB>
+template <int EPI, int NS, int KB, bool SA>
 void launch_ks(hipStream_t st, const grx_weight *w, const int8_t *xq, const float *xs, int m, const float *bias,
                const GemmOut &o, int da4) {
     const int run = ks_max_waves(NS, KB) * KB;
     if (w->nb <= run || o.carry == nullptr) {
-        launch_ks_run<EPI, NS, KB>(st, w, xq, xs, m, bias, o.y, o.ldc, o, da4, 0, w->nb, nullptr);
+        launch_ks_run<EPI, NS, KB, SA>(st, w, xq, xs, m, bias, o.y, o.ldc, o, da4, 0, w->nb, nullptr);
         return;
     }
     const float *init = nullptr;
     for (int b = 0; b < w->nb; b += run) {
         const int e = min(w->nb, b + run);
         if (e < w->nb) {
-            launch_ks_run<GRX_GEMM_STORE, NS, KB>(st, w, xq, xs, m, bias, o.carry, w->rows, o, da4, b, e, init);
+            launch_ks_run<GRX_GEMM_STORE, NS, KB, SA>(st, w, xq, xs, m, bias, o.carry, w->rows, o, da4, b, e, init);
             init = o.carry;
         } else {
-            launch_ks_run<EPI, NS, KB>(st, w, xq, xs, m, bias, o.y, o.ldc, o, da4, b, e, init);
+            launch_ks_run<EPI, NS, KB, SA>(st, w, xq, xs, m, bias, o.y, o.ldc, o, da4, b, e, init);
         }
     }
 }
 
+// SA when asked and possible: 16-byte aligned activations and scales, whole
+// groups of four blocks, the LDS granted (for the carried runs' STORE
+// instantiation too)
+template <int EPI, int NS, int KB>
+void launch_ks_sa(hipStream_t st, const grx_weight *w, const int8_t *xq, const float *xs, int m, const float *bias,
+                  const GemmOut &o, int da4, bool sa) {
+    if (sa && ks_stage_ok<EPI, NS, KB>() && ks_stage_ok<GRX_GEMM_STORE, NS, KB>())
+        return launch_ks<EPI, NS, KB, true>(st, w, xq, xs, m, bias, o, da4);
+    return launch_ks<EPI, NS, KB, false>(st, w, xq, xs, m, bias, o, da4);
+}
+
 template <int EPI>
 void launch_ks_epi(hipStream_t st, const grx_weight *w, const int8_t *xq, const float *xs, int m, const float *bias,
-                   const GemmOut &o, int ns, int kb, int da4) {
+                   const GemmOut &o, int ns, int kb, int da4, bool sa) {
     if constexpr (EPI != GRX_GEMM_SILU_Q) {
         if (ns == 1) {
-            if (kb == 4) return launch_ks<EPI, 1, 4>(st, w, xq, xs, m, bias, o, da4);
-            if (kb == 8) return launch_ks<EPI, 1, 8>(st, w, xq, xs, m, bias, o, da4);
-            return launch_ks<EPI, 1, 16>(st, w, xq, xs, m, bias, o, da4);
+            if (kb == 4) return launch_ks_sa<EPI, 1, 4>(st, w, xq, xs, m, bias, o, da4, sa);
+            if (kb == 8) return launch_ks_sa<EPI, 1, 8>(st, w, xq, xs, m, bias, o, da4, sa);
+            return launch_ks_sa<EPI, 1, 16>(st, w, xq, xs, m, bias, o, da4, sa);
         }
     }
-    if (kb == 4) return launch_ks<EPI, 2, 4>(st, w, xq, xs, m, bias, o, da4);
-    return launch_ks<EPI, 2, 8>(st, w, xq, xs, m, bias, o, da4);
+    if (kb == 4) return launch_ks_sa<EPI, 2, 4>(st, w, xq, xs, m, bias, o, da4, sa);
+    return launch_ks_sa<EPI, 2, 8>(st, w, xq, xs, m, bias, o, da4, sa);
 }
 
 }  // namespace
@@ -777,16 +897,22 @@ grx_status grx_gemm_q8_launch_ex(hipStream_t st, const grx_weight *w, const int8
     if (o.epi == GRX_GEMM_SILU_Q && w->rows % GRX_QK != 0)
         return grx_fail(GRX_ESIZE, "rounded product output needs rows %% 32 == 0 (rows %d)", w->rows);
     // GEMM_KERNEL picks the kernel (tests force each one with it): the
-    // LDS-staged tiles from 256 rows on, the whole-K register walk from 129
-    // (e.g. 224 x 1024 x 4096: 26 us against 36 for the K-split tiles), the
-    // K-split tiles up to 128 rows where the register walk has few tiles or
-    // a long K (at 126 rows: 4096 x 1024 10.4 us on the register walk
-    // against 11.9 K-split; 2048 x 1024 8.1 against 7.3; 1024 x 4096 25
-    // against 19)
+    // LDS-staged tiles from 256 rows on; below that the K-split tiles with
+    // their activations staged through LDS (at 224 rows: 1024 x 4096 17 us
+    // against 26 on the whole-K register walk and 50 on the LDS tiles,
+    // 4096 x 1024 12 against 19 and 15); without the staging, the K-split
+    // tiles up to 128 rows where the register walk has few tiles or a long K
+    // (at 126 rows: 4096 x 1024 10.4 us on the register walk against 11.9
+    // K-split; 2048 x 1024 8.1 against 7.3; 1024 x 4096 25 against 19), the
+    // register walk otherwise
     const int kind = grx_tune(GRX_TUNE_GEMM_KERNEL);
+    // the K-split kernel stages the activations through LDS unless told not
+    // to or they are not in 16-byte aligned whole groups of four blocks
+    const int da4 = (w->nb % 4 == 0 && ((uintptr_t)xs & 15) == 0) ? 1 : 0;
+    const bool sa = grx_tune(GRX_TUNE_GEMM_STAGE_A) != 0 && da4 && ((uintptr_t)xq & 15) == 0;
     int ks_ns = 1, ks_kb = 4;
-    const bool ks_ok = pick_ks(m, w->nb, o.epi, o.carry != nullptr, &ks_ns, &ks_kb) &&
-                       (kind == 2 || (m <= 128 && (m <= 32 || w->rows <= 2048 || w->nb > 64)));
+    const bool ks_ok = pick_ks(m, w->nb, w->rows, o.epi, o.carry != nullptr, sa, &ks_ns, &ks_kb) &&
+                       (kind == 2 || (sa ? m < 256 : (m <= 128 && (m <= 32 || w->rows <= 2048 || w->nb > 64))));
     if (kind == 3 || (kind != 1 && kind != 2 && m >= 256)) {  // many rows: the LDS-staged 64 x 128 tiles
         dim3 g2(grx_ceil_div(m, 64), grx_ceil_div(w->tiles, 2));
 #define GRX_GEMM_LDS(E)                                                                                           \
@@ -806,15 +932,20 @@ grx_status grx_gemm_q8_launch_ex(hipStream_t st, const grx_weight *w, const int8
         return GRX_OK;
     }
     if (kind != 1 && ks_ok) {  // fewer rows: the K-split tiles
-        const int da4 = (w->nb % 4 == 0 && ((uintptr_t)xs & 15) == 0) ? 1 : 0;
         switch (o.epi) {
-            case GRX_GEMM_STORE: launch_ks_epi<GRX_GEMM_STORE>(st, w, xq, xs, m, bias, o, ks_ns, ks_kb, da4); break;
-            case GRX_GEMM_ADD: launch_ks_epi<GRX_GEMM_ADD>(st, w, xq, xs, m, bias, o, ks_ns, ks_kb, da4); break;
-            case GRX_GEMM_AXPY_HALF:
-                launch_ks_epi<GRX_GEMM_AXPY_HALF>(st, w, xq, xs, m, bias, o, ks_ns, ks_kb, da4);
+            case GRX_GEMM_STORE:
+                launch_ks_epi<GRX_GEMM_STORE>(st, w, xq, xs, m, bias, o, ks_ns, ks_kb, da4, sa);
                 break;
-            case GRX_GEMM_SCALE: launch_ks_epi<GRX_GEMM_SCALE>(st, w, xq, xs, m, bias, o, ks_ns, ks_kb, da4); break;
-            case GRX_GEMM_SILU_Q: launch_ks_epi<GRX_GEMM_SILU_Q>(st, w, xq, xs, m, bias, o, 2, ks_kb, da4); break;
+            case GRX_GEMM_ADD: launch_ks_epi<GRX_GEMM_ADD>(st, w, xq, xs, m, bias, o, ks_ns, ks_kb, da4, sa); break;
+            case GRX_GEMM_AXPY_HALF:
+                launch_ks_epi<GRX_GEMM_AXPY_HALF>(st, w, xq, xs, m, bias, o, ks_ns, ks_kb, da4, sa);
+                break;
+            case GRX_GEMM_SCALE:
+                launch_ks_epi<GRX_GEMM_SCALE>(st, w, xq, xs, m, bias, o, ks_ns, ks_kb, da4, sa);
+                break;
+            case GRX_GEMM_SILU_Q:
+                launch_ks_epi<GRX_GEMM_SILU_Q>(st, w, xq, xs, m, bias, o, 2, ks_kb, da4, sa);
+                break;
         }
         GRX_LAUNCHED("gemm_q8_ks_kernel");
         return GRX_OK;

@@ -236,16 +236,19 @@ def test_matmul_matrix_cores_each_tile_width(kern, orc, ns):
                 _check_matmul(kern, orc, rng, m, n, 32 * nb, bias=(nb % 2 == 1))
 
 
+@pytest.mark.parametrize("sa", [0, 1])
 @pytest.mark.parametrize("ns,kb", [(1, 4), (1, 8), (1, 16), (2, 4), (2, 8)])
-def test_matmul_k_split_each_shape(kern, orc, ns, kb):
+def test_matmul_k_split_each_shape(kern, orc, ns, kb, sa):
     """The K-split product at every tile width and blocks per wave (GEMM_NS,
-    GEMM_KB): block counts that give 1 to 8 waves per tile, a last wave with
+    GEMM_KB), with the activations read straight from memory or staged
+    through LDS (GEMM_STAGE_A; the staged route needs whole groups of four
+    blocks): block counts that give 1 to 8 waves per tile, a last wave with
     1 to KB blocks, activation-scale rows not in whole groups of four, and
     row counts with partial 16-row groups: bit-identical to the oracle."""
     rng = np.random.default_rng(53 + 7 * ns + kb)
-    with kern.tuned(GEMM_MIN_M=1, GEMM_KERNEL=2, GEMM_NS=ns, GEMM_KB=kb):
+    with kern.tuned(GEMM_MIN_M=1, GEMM_KERNEL=2, GEMM_NS=ns, GEMM_KB=kb, GEMM_STAGE_A=sa):
         for nb in sorted({1, 2, 3, 4, 5, 7, 8, 9, kb - 1, kb, kb + 1, 2 * kb + 3, 4 * kb, 8 * kb - 1, 8 * kb} - {0}):
-            for m, n in ((1, 64), (14, 100), (33, 130), (126, 48)):
+            for m, n in ((1, 64), (14, 100), (33, 130), (126, 48), (200, 40)):
                 _check_matmul(kern, orc, rng, m, n, 32 * nb, bias=(nb % 2 == 1))
 
 
