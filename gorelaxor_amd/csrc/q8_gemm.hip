@@ -254,17 +254,7 @@ tail:
 // column tiles of 4), else 8.
 constexpr int ks_max_waves(int ns, int kb) { return (ns == 1 && kb <= 8) || (ns == 2 && kb == 4) ? 16 : 8; }
 
-// With SA the activations go through LDS: each wave copies its 16 rows x KB
-// blocks with 16-byte loads (a row's KB*32 bytes in whole cache lines, where
-// the MFMA fragment loads touch 16 rows' lines for 32 bytes each) and its
-// 16 x KB activation scales with one, then reads the fragments from LDS.
-// Bytes of LDS per wave for the staged activations: 16 rows of KB*32 bytes,
-// 16 apart beyond that (the fragment reads of 16 rows fall in different
-// banks), then the scales as [block][row].
-constexpr int ks_stage_row(int kb) { return kb * 32 + 16; }
-constexpr int ks_stage_bytes(int kb) { return 16 * ks_stage_row(kb) + 16 * kb * 4; }
-
-template <int EPI, int NS, int KB, bool SA>
+template <int EPI, int NS, int KB>
 __global__ __launch_bounds__(64 * ks_max_waves(NS, KB)) void gemm_q8_ks_kernel(
     const int8_t *__restrict__ qs, const uint16_t *__restrict__ ds, int rows, int nb, const int8_t *__restrict__ xq,
     const float *__restrict__ xs, int m, const float *__restrict__ bias, float *__restrict__ y, int ldc, float scale,
@@ -273,7 +263,6 @@ __global__ __launch_bounds__(64 * ks_max_waves(NS, KB)) void gemm_q8_ks_kernel(
     static_assert(NS == 1 || NS == 2, "16 or 32 weight rows per tile");
     static_assert(KB % 4 == 0, "blocks per wave in whole groups of four");
     __shared__ float cx[2][NS * 4][64];
-    extern __shared__ __align__(16) int8_t ks_stage[];
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int ks = __builtin_amdgcn_readfirstlane(blockDim.x >> 6);
@@ -306,53 +295,9 @@ __global__ __launch_bounds__(64 * ks_max_waves(NS, KB)) void gemm_q8_ks_kernel(
 
     // every load of the wave's blocks in flight at once (the last wave's
     // block indices past nb are clamped and their results never used)
-    long av[SA ? 1 : KB], bv[KB][NS];
+    long av[KB], bv[KB][NS];
     uint16_t dh[KB][NS];
-    float da[SA ? 1 : KB][4];  // SA: read from LDS as the chain needs them
-    constexpr int RS = ks_stage_row(KB);
-    int8_t *sa = ks_stage + wave * ks_stage_bytes(KB);
-    float *sd = reinterpret_cast<float *>(sa + 16 * RS);
-    if constexpr (SA) {
-        // (the launcher takes this route only with xq and xs 16-byte
-        // aligned and nb % 4 == 0)
-        constexpr int NA = KB / 2;  // 16-byte loads of the 16 rows x KB blocks
-        int4 ra[NA];
-#pragma unroll
-        for (int j = 0; j < NA; ++j) {
-            const int e = j * 64 + lane, i = e / (2 * KB), pc = e % (2 * KB);
-            const int row = min(16 * rf + i, m - 1), b = min(b0 + pc / 2, bend - 1);
-            ra[j] = *reinterpret_cast<const int4 *>(xq + (size_t)row * K + (size_t)b * GRX_QK + (pc & 1) * 16);
-        }
-        constexpr int DQ = KB / 4;  // float4s of scales per row
-        float4 rd = make_float4(0.f, 0.f, 0.f, 0.f);
-        if (lane < 16 * DQ) {
-            const int i = lane / DQ, q = lane % DQ;
-            const int row = min(16 * rf + i, m - 1), b = min(b0 + 4 * q, bend - 4);
-            rd = *reinterpret_cast<const float4 *>(xs + (size_t)row * nb + b);
-        }
-#pragma unroll
-        for (int u = 0; u < KB; ++u) {
-            const int b = min(b0 + u, bend - 1);
-#pragma unroll
-            for (int s = 0; s < NS; ++s) {
-                bv[u][s] = *reinterpret_cast<const long *>(bp + (size_t)b * 2048 + s * 256);
-                dh[u][s] = dp[(size_t)b * 64 + 16 * s];
-            }
-        }
-#pragma unroll
-        for (int j = 0; j < NA; ++j) {
-            const int e = j * 64 + lane, i = e / (2 * KB), pc = e % (2 * KB);
-            *reinterpret_cast<int4 *>(sa + i * RS + pc * 16) = ra[j];
-        }
-        if (lane < 16 * DQ) {
-            const int i = lane / DQ, q = lane % DQ;
-            sd[(4 * q + 0) * 16 + i] = rd.x;
-            sd[(4 * q + 1) * 16 + i] = rd.y;
-            sd[(4 * q + 2) * 16 + i] = rd.z;
-            sd[(4 * q + 3) * 16 + i] = rd.w;
-        }
-        __syncthreads();
-    } else {
+    float da[KB][4];
 #pragma unroll
     for (int u = 0; u < KB; ++u) {
         const int b = min(b0 + u, bend - 1);
@@ -384,20 +329,14 @@ __global__ __launch_bounds__(64 * ks_max_waves(NS, KB)) void gemm_q8_ks_kernel(
             for (int r = 0; r < 4; ++r) da[u][r] = sp[r][b];
         }
     }
-    }
     // the block dots and their scaled forms t = f32(s) * dw
     float t[KB][NS][4];
 #pragma unroll
     for (int u = 0; u < KB; ++u) {
-        long a;
-        if constexpr (SA)
-            a = *reinterpret_cast<const long *>(sa + li * RS + u * GRX_QK + 8 * lk);
-        else
-            a = av[u];
 #pragma unroll
         for (int s = 0; s < NS; ++s) {
             v4i d = {0, 0, 0, 0};
-            d = __builtin_amdgcn_mfma_i32_16x16x32_i8(a, bv[u][s], d, 0, 0, 0);
+            d = __builtin_amdgcn_mfma_i32_16x16x32_i8(av[u], bv[u][s], d, 0, 0, 0);
             const float dw = grx_f16_to_f32(dh[u][s]);
 #pragma unroll
             for (int r = 0; r < 4; ++r) t[u][s][r] = __fmul_rn((float)d[r], dw);
@@ -429,35 +368,21 @@ __global__ __launch_bounds__(64 * ks_max_waves(NS, KB)) void gemm_q8_ks_kernel(
 #pragma unroll
                     for (int r = 0; r < 4; ++r) c[s][r] = cx[(p - 1) & 1][4 * s + r][lane];
             }
-            // block u's activation scales of the lane's rows 4*lk .. 4*lk+3
-            auto scales = [&](int u) {
-                if constexpr (SA) {
-                    const float4 v = *reinterpret_cast<const float4 *>(sd + u * 16 + 4 * lk);
-                    return v;
-                } else {
-                    return make_float4(da[u][0], da[u][1], da[u][2], da[u][3]);
-                }
-            };
             if (nbw == KB) {
 #pragma unroll
-                for (int u = 0; u < KB; ++u) {
-                    const float4 a4 = scales(u);
-                    const float av4[4] = {a4.x, a4.y, a4.z, a4.w};
+                for (int u = 0; u < KB; ++u)
 #pragma unroll
                     for (int s = 0; s < NS; ++s)
 #pragma unroll
-                        for (int r = 0; r < 4; ++r) c[s][r] = __fmaf_rn(t[u][s][r], av4[r], c[s][r]);
-                }
+                        for (int r = 0; r < 4; ++r) c[s][r] = __fmaf_rn(t[u][s][r], da[u][r], c[s][r]);
             } else {
 #pragma unroll
                 for (int u = 0; u < KB; ++u) {
                     if (u < nbw) {
-                        const float4 a4 = scales(u);
-                        const float av4[4] = {a4.x, a4.y, a4.z, a4.w};
 #pragma unroll
                         for (int s = 0; s < NS; ++s)
 #pragma unroll
-                            for (int r = 0; r < 4; ++r) c[s][r] = __fmaf_rn(t[u][s][r], av4[r], c[s][r]);
+                            for (int r = 0; r < 4; ++r) c[s][r] = __fmaf_rn(t[u][s][r], da[u][r], c[s][r]);
                     }
                 }
             }
@@ -519,6 +444,231 @@ __global__ __launch_bounds__(64 * ks_max_waves(NS, KB)) void gemm_q8_ks_kernel(
                 if constexpr (EPI == GRX_GEMM_ADD) *yp = __fadd_rn(*yp, c[s][r]);
                 if constexpr (EPI == GRX_GEMM_AXPY_HALF) *yp = __fmaf_rn(0.5f, c[s][r], *yp);
                 if constexpr (EPI == GRX_GEMM_SCALE) *yp = __fmul_rn(c[s][r], scale);
+            }
+        }
+    }
+}
+
+// The K-split product with its activations staged through LDS, for up to
+// 255 rows: the same tiles, waves and ordered chain as gemm_q8_ks_kernel,
+// but each wave copies its 16 activation rows x KB blocks into LDS with
+// 16-byte loads (a row's KB*32 bytes in whole cache lines, where a fragment
+// load touches 16 rows' lines for 32 bytes each) and the activation scales
+// with one more, and the matrix cores take the weights as the A operand and
+// the activations as B.  A lane then holds four consecutive weight rows of
+// one activation row: its chain needs one activation scale per block (a
+// 4-byte LDS read), its weight scales come as one 8-byte load per block,
+// and its outputs are four consecutive floats of one output row.  Offsets
+// from the (uniform) operand bases are 32-bit.
+// Bytes of LDS per wave: 16 rows of KB*32 bytes, 16 apart beyond that (the
+// fragment reads of 16 rows fall in different banks), then the scales as
+// [block][row].
+constexpr int kss_row(int kb) { return kb * 32 + 16; }
+constexpr int kss_bytes(int kb) { return 16 * kss_row(kb) + 16 * kb * 4; }
+
+template <int EPI, int NS, int KB>
+__global__ __launch_bounds__(64 * ks_max_waves(NS, KB)) void gemm_q8_kss_kernel(
+    const int8_t *__restrict__ qs, const uint16_t *__restrict__ ds, int rows, int nb, const int8_t *__restrict__ xq,
+    const float *__restrict__ xs, int m, const float *__restrict__ bias, float *__restrict__ y, int ldc, float scale,
+    int8_t *__restrict__ yq, float *__restrict__ ys, int ncg, int nrf, int bbeg, int bend, const float *init,
+    int ldi) {
+    static_assert(NS == 1 || NS == 2, "16 or 32 weight rows per tile");
+    static_assert(KB % 4 == 0, "blocks per wave in whole groups of four");
+    __shared__ float cx[2][NS * 4][64];
+    extern __shared__ __align__(16) int8_t kss_stage[];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int ks = __builtin_amdgcn_readfirstlane(blockDim.x >> 6);
+    const int gi = blockIdx.x, xcd = gi & 7, slot = gi >> 3;
+    const int rf = slot % nrf, cg = (slot / nrf) * 8 + xcd;
+    if (cg >= ncg) return;  // the whole workgroup: no barrier is skipped
+    const unsigned K = (unsigned)nb * GRX_QK;
+    const int li = lane & 15, lk = lane >> 4;
+    const int n0 = cg * 16 * NS;              // first weight row of the tile
+    const int tile = n0 >> 6, sub = n0 & 63;  // 64-row weight tile, row offset in it
+    const int b0 = bbeg + wave * KB;
+    const int nbw = min(KB, bend - b0);       // this wave's blocks (>= 1)
+    const int8_t *wq = qs + (size_t)tile * nb * 2048;
+    const uint16_t *wd = ds + (size_t)tile * nb * 64;
+    // A: weight row n0+16s+li, bytes 8*lk.. of each block; the lane's four
+    // weight scales (rows n0+16s+4*lk ..) are 8 contiguous bytes
+    const unsigned qoff = (unsigned)((lk >> 1) * 1024 + (sub + li) * 16 + 8 * (lk & 1));
+    const unsigned doff = (unsigned)(sub + 4 * lk);
+    const int arow = 16 * rf + li;            // the lane's activation row (B column)
+    constexpr int RS = kss_row(KB);
+    int8_t *sa = kss_stage + wave * kss_bytes(KB);
+    float *sd = reinterpret_cast<float *>(sa + 16 * RS);
+
+    // every load of the wave's blocks in flight at once (block indices past
+    // bend are clamped and their results never used; rows past m likewise)
+    constexpr int NA = KB / 2;  // 16-byte loads of the 16 rows x KB blocks
+    int4 ra[NA];
+#pragma unroll
+    for (int j = 0; j < NA; ++j) {
+        const int e = j * 64 + lane, i = e / (2 * KB), pc = e % (2 * KB);
+        const unsigned row = (unsigned)min(16 * rf + i, m - 1), b = (unsigned)min(b0 + pc / 2, bend - 1);
+        ra[j] = *reinterpret_cast<const int4 *>(xq + (row * K + b * GRX_QK + (pc & 1) * 16));
+    }
+    constexpr int DQ = KB / 4;  // float4s of scales per row
+    float4 rd = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (lane < 16 * DQ) {
+        const int i = lane / DQ, q = lane % DQ;
+        const unsigned row = (unsigned)min(16 * rf + i, m - 1), b = (unsigned)min(b0 + 4 * q, bend - 4);
+        rd = *reinterpret_cast<const float4 *>(xs + (row * (unsigned)nb + b));
+    }
+    long bv[KB][NS];
+    uint2 dq[KB][NS];
+#pragma unroll
+    for (int u = 0; u < KB; ++u) {
+        const unsigned b = (unsigned)min(b0 + u, bend - 1);
+#pragma unroll
+        for (int s = 0; s < NS; ++s) {
+            bv[u][s] = *reinterpret_cast<const long *>(wq + (qoff + b * 2048 + s * 256));
+            dq[u][s] = *reinterpret_cast<const uint2 *>(reinterpret_cast<const char *>(wd) +
+                                                          2 * (doff + b * 64 + 16 * s));
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < NA; ++j) {
+        const int e = j * 64 + lane, i = e / (2 * KB), pc = e % (2 * KB);
+        *reinterpret_cast<int4 *>(sa + i * RS + pc * 16) = ra[j];
+    }
+    if (lane < 16 * DQ) {
+        const int i = lane / DQ, q = lane % DQ;
+        sd[(4 * q + 0) * 16 + i] = rd.x;
+        sd[(4 * q + 1) * 16 + i] = rd.y;
+        sd[(4 * q + 2) * 16 + i] = rd.z;
+        sd[(4 * q + 3) * 16 + i] = rd.w;
+    }
+    __syncthreads();
+
+    // the block dots (weight rows 4*lk+r of the 16, activation row li) and
+    // their scaled forms t = f32(s) * dw
+    float t[KB][NS][4];
+#pragma unroll
+    for (int u = 0; u < KB; ++u) {
+        const long a = *reinterpret_cast<const long *>(sa + li * RS + u * GRX_QK + 8 * lk);
+#pragma unroll
+        for (int s = 0; s < NS; ++s) {
+            v4i d = {0, 0, 0, 0};
+            d = __builtin_amdgcn_mfma_i32_16x16x32_i8(bv[u][s], a, d, 0, 0, 0);
+            const uint32_t h[2] = {dq[u][s].x, dq[u][s].y};
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const float dw = grx_f16_to_f32((uint16_t)(h[r >> 1] >> (16 * (r & 1))));
+                t[u][s][r] = __fmul_rn((float)d[r], dw);
+            }
+        }
+    }
+
+    // the ordered chain, one wave after another
+    float c[NS][4];
+    for (int p = 0; p < ks; ++p) {
+        if (wave == p) {
+            if (p == 0 && init != nullptr) {
+                const int ar = min(arow, m - 1);
+#pragma unroll
+                for (int s = 0; s < NS; ++s)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r)
+                        c[s][r] = init[(size_t)ar * ldi + min(n0 + 16 * s + 4 * lk + r, rows - 1)];
+            } else if (p == 0) {
+#pragma unroll
+                for (int s = 0; s < NS; ++s)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        const int n = n0 + 16 * s + 4 * lk + r;
+                        c[s][r] = (bias != nullptr && n < rows) ? bias[n] : 0.0f;
+                    }
+            } else {
+#pragma unroll
+                for (int s = 0; s < NS; ++s)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) c[s][r] = cx[(p - 1) & 1][4 * s + r][lane];
+            }
+            if (nbw == KB) {
+#pragma unroll
+                for (int u = 0; u < KB; ++u) {
+                    const float da = sd[u * 16 + li];
+#pragma unroll
+                    for (int s = 0; s < NS; ++s)
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) c[s][r] = __fmaf_rn(t[u][s][r], da, c[s][r]);
+                }
+            } else {
+#pragma unroll
+                for (int u = 0; u < KB; ++u) {
+                    if (u < nbw) {
+                        const float da = sd[u * 16 + li];
+#pragma unroll
+                        for (int s = 0; s < NS; ++s)
+#pragma unroll
+                            for (int r = 0; r < 4; ++r) c[s][r] = __fmaf_rn(t[u][s][r], da, c[s][r]);
+                    }
+                }
+            }
+            if (p + 1 < ks) {
+#pragma unroll
+                for (int s = 0; s < NS; ++s)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) cx[p & 1][4 * s + r][lane] = c[s][r];
+            }
+        }
+        if (p + 1 < ks) __syncthreads();
+    }
+    if (wave != ks - 1) return;
+
+    if constexpr (EPI == GRX_GEMM_SILU_Q) {
+        // the tile's 32 columns are one Q8_0 block of the activation row
+        // (rows % 32 == 0), spread over the four lanes li, li+16, li+32,
+        // li+48: their block maximum is two xor-shuffles
+        static_assert(NS == 2, "rounded output needs whole 32-column blocks per tile");
+        const int nr = rows / GRX_QK;
+        float v[2][4];
+        float amax = 0.0f;
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const float x = c[h][r];
+                v[h][r] = __fdiv_rn(x, __fadd_rn(grx_exp8(__fsub_rn(0.0f, x)), 1.0f));
+                const float a = fabsf(v[h][r]);
+                amax = a > amax ? a : amax;
+            }
+#pragma unroll
+        for (int o = 16; o < 64; o <<= 1) {
+            const float tt = __shfl_xor(amax, o);
+            amax = tt > amax ? tt : amax;
+        }
+        const float id = amax != 0.0f ? __fdiv_rn(127.0f, amax) : 0.0f;
+        if (n0 < rows && arow < m) {
+            int8_t *qrow = yq + (size_t)arow * rows + n0;
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                uint32_t pk = 0;
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    float q = rintf(__fmul_rn(v[h][r], id));
+                    q = fminf(fmaxf(q, -128.0f), 127.0f);
+                    pk |= (uint32_t)(uint8_t)(int8_t)(int)q << (8 * r);
+                }
+                *reinterpret_cast<uint32_t *>(qrow + 16 * h + 4 * lk) = pk;
+            }
+            if (lk == 0) ys[(size_t)arow * nr + n0 / GRX_QK] = __fmul_rn(amax, grx_bits_f32(0x3c010204u));
+        }
+    } else {
+        if (arow >= m) return;
+#pragma unroll
+        for (int s = 0; s < NS; ++s) {
+            const int n = n0 + 16 * s + 4 * lk;
+            float *yp = y + (size_t)arow * ldc + n;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                if (n + r >= rows) continue;
+                if constexpr (EPI == GRX_GEMM_STORE) yp[r] = c[s][r];
+                if constexpr (EPI == GRX_GEMM_ADD) yp[r] = __fadd_rn(yp[r], c[s][r]);
+                if constexpr (EPI == GRX_GEMM_AXPY_HALF) yp[r] = __fmaf_rn(0.5f, c[s][r], yp[r]);
+                if constexpr (EPI == GRX_GEMM_SCALE) yp[r] = __fmul_rn(c[s][r], scale);
             }
         }
     }
@@ -816,9 +966,9 @@ bool pick_ks(int m, int nb, int rows, int epi, bool carry, bool sa, int *ns, int
 template <int EPI, int NS, int KB>
 bool ks_stage_ok() {
     static const bool ok = [] {
-        const int need = ks_max_waves(NS, KB) * ks_stage_bytes(KB);
+        const int need = ks_max_waves(NS, KB) * kss_bytes(KB);
         const bool r = need <= 64 * 1024 ||
-                       hipFuncSetAttribute((const void *)gemm_q8_ks_kernel<EPI, NS, KB, true>,
+                       hipFuncSetAttribute((const void *)gemm_q8_kss_kernel<EPI, NS, KB>,
                                            hipFuncAttributeMaxDynamicSharedMemorySize, need) == hipSuccess;
         (void)hipGetLastError();
         return r;
@@ -833,10 +983,14 @@ void launch_ks_run(hipStream_t st, const grx_weight *w, const int8_t *xq, const 
     const int ncg = grx_ceil_div(w->rows, 16 * NS), nrf = grx_ceil_div(m, 16);
     const int ks = grx_ceil_div(bend - bbeg, KB);
     const int groups = grx_ceil_div(ncg, 8) * 8 * nrf;
-    const size_t smem = SA ? (size_t)ks * ks_stage_bytes(KB) : 0;
-    gemm_q8_ks_kernel<EPI, NS, KB, SA><<<groups, 64 * ks, smem, st>>>(w->qs, w->ds, w->rows, w->nb, xq, xs, m, bias,
-                                                                      y, ldc, o.scale, o.yq, o.ys, ncg, nrf, da4,
-                                                                      bbeg, bend, init, w->rows);
+    if constexpr (SA)
+        gemm_q8_kss_kernel<EPI, NS, KB><<<groups, 64 * ks, (size_t)ks * kss_bytes(KB), st>>>(
+            w->qs, w->ds, w->rows, w->nb, xq, xs, m, bias, y, ldc, o.scale, o.yq, o.ys, ncg, nrf, bbeg, bend, init,
+            w->rows);
+    else
+        gemm_q8_ks_kernel<EPI, NS, KB><<<groups, 64 * ks, 0, st>>>(w->qs, w->ds, w->rows, w->nb, xq, xs, m, bias, y,
+                                                                   ldc, o.scale, o.yq, o.ys, ncg, nrf, da4, bbeg, bend,
+                                                                   init, w->rows);
 }
 
 // The whole product: one launch, or (a carry buffer given, more blocks than
