@@ -109,6 +109,7 @@ enum {
     GRX_TUNE_ARGMAX_ATOMIC,   // 1: the decoders' argmax through a contended atomic
     GRX_TUNE_NO_GRAPH,        // 1: model loops launch kernel by kernel (no HIP graphs)
     GRX_TUNE_GEMM_STAGE_A,    // 0: the K-split kernel reads activations straight from memory, 1: through LDS
+    GRX_TUNE_GEMV_MX,         // 0: several-row GEMVs on the dot-product kernel, not the matrix-core one
     GRX_TUNE_COUNT
 };
 int grx_tune(int id);

@@ -158,8 +158,9 @@ constexpr int kKeyLd = 68;
 // loads go there).
 template <int NP, int PRO, typename After>
 __device__ __forceinline__ void wave_row_prologue(const GemvArgs &a, int m, int8_t *lxq, float *lxs, int lane,
-                                                  int tile, After after_loads) {
+                                                  int tile, After after_loads, int ldq = 0) {
     const int nb = a.nb, K = nb * GRX_QK;
+    const size_t rq = ldq > 0 ? (size_t)ldq : (size_t)K;  // bytes between the rounded rows in lxq
     const int npc = K / 4;  // float4 pieces
     float4 xv[NP], wv[NP], bv[NP];
     const float4 *x4 = reinterpret_cast<const float4 *>(a.x + (size_t)m * a.lda);
@@ -221,7 +222,7 @@ __device__ __forceinline__ void wave_row_prologue(const GemvArgs &a, int m, int8
         const float id = amax != 0.0f ? __fdiv_rn(127.0f, amax) : 0.0f;
         const uint32_t q = quant4(xv[j], id);
         if (P < npc) {
-            reinterpret_cast<uint32_t *>(lxq + (size_t)m * K)[P] = q;
+            reinterpret_cast<uint32_t *>(lxq + (size_t)m * rq)[P] = q;
             if ((lane & 7) == 0) lxs[m * nb + (P >> 3)] = __fmul_rn(amax, grx_bits_f32(0x3c010204u));
         }
     }
@@ -667,6 +668,170 @@ __global__ __launch_bounds__(64 * W) void gemv_q8_kernel(const GemvArgs a) {
     gemv_epilogue<M, W, RND, EPI>(a, acc, row, lane, wave, pos0);
 }
 
+// Several activation rows (M = 2..8: a batch of streams, a short prompt) on
+// the matrix cores, with the multi-row GEMV's prologues and epilogues.  A
+// workgroup owns 16*NS weight rows (a quarter or half of a 64-row tile, so a
+// 1280-row product runs on 80 workgroups instead of 20) and its W waves
+// split the blocks, KB each: wave m builds activation row m with the
+// one-wave prologue, its weights' loads issued behind the row's (rounded
+// rows in LDS, 16 bytes apart beyond K so the fragment reads of 16 rows fall
+// in different banks), takes its blocks' int32 dots with
+// v_mfma_i32_16x16x32_i8
+// (weights as A, activation rows as B: a lane holds four consecutive weight
+// rows of one activation row) and forms t = f32(s) * dw; the ordered chain
+// c = fma(t, da, c) from the bias then runs wave after wave through LDS, so
+// every output sees the blocks in order, as in gemv_q8_kernel.  The last
+// wave hands its outputs, through LDS, to the lanes of their rows and ends
+// them with gemv_epilogue.
+template <int M, int PRO, int EPI, int NS, int KB>
+__global__ __launch_bounds__(512) void gemv_q8_mx_kernel(const GemvArgs a) {
+    static_assert(M >= 2 && M <= 8, "2 to 8 activation rows");
+    static_assert(KB % 4 == 0, "blocks per wave in whole groups of four");
+    extern __shared__ __align__(16) unsigned char smem[];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int nb = a.nb, K = nb * GRX_QK, ldq = K + 16;
+    const int WK = (nb + KB - 1) / KB;  // waves with blocks (the workgroup has max(WK, M))
+    // LDS: lxq [M][ldq] int8 | lxs [M][nb] f32 | cx [2][NS*4][64] f32 | ot [M][16*NS] f32
+    int8_t *lxq = reinterpret_cast<int8_t *>(smem);
+    float *lxs = reinterpret_cast<float *>(smem + (((size_t)M * ldq + 15) & ~(size_t)15));
+    float *cx = lxs + (((size_t)M * nb + 3) & ~(size_t)3);
+    float *ot = cx + 2 * NS * 4 * 64;
+    const int g = blockIdx.x;
+    const int n0 = g * 16 * NS, tile = n0 >> 6, sub = n0 & 63;
+    const int pos0 = (EPI == GRX_EPI_QKV || EPI == GRX_EPI_QKV_ROPE) ? *a.pos : 0;
+    const int li = lane & 15, lk = lane >> 4;
+
+    // the weights of the wave's blocks, issued behind its activation row's
+    // loads (they complete in order: the row does not wait for them)
+    const int b0 = wave * KB, nbw = min(KB, nb - b0);
+    const int8_t *wq = reinterpret_cast<const int8_t *>(a.qs) + (size_t)tile * nb * 2048;
+    const char *wd = reinterpret_cast<const char *>(a.ds + (size_t)tile * nb * 64);
+    const unsigned qoff = (unsigned)((lk >> 1) * 1024 + (sub + li) * 16 + 8 * (lk & 1));
+    const unsigned doff = (unsigned)(sub + 4 * lk);
+    long bv[KB][NS];
+    uint2 dq[KB][NS];
+    auto load_weights = [&] {
+        if (wave >= WK) return;
+#pragma unroll
+        for (int u = 0; u < KB; ++u) {
+            const unsigned b = (unsigned)min(b0 + u, nb - 1);
+#pragma unroll
+            for (int s = 0; s < NS; ++s) {
+                bv[u][s] = *reinterpret_cast<const long *>(wq + (qoff + b * 2048 + s * 256));
+                dq[u][s] = *reinterpret_cast<const uint2 *>(wd + 2 * (doff + b * 64 + 16 * s));
+            }
+        }
+    };
+
+    // ---- prologue: the M rounded rows in LDS, row m built by wave m
+    if constexpr (PRO == GRX_PRO_PREQ) {
+        load_weights();
+        const int n16 = K / 16;
+        for (int i = threadIdx.x; i < M * n16; i += blockDim.x) {
+            const int m = i / n16, j = i % n16;
+            reinterpret_cast<int4 *>(lxq + (size_t)m * ldq)[j] = reinterpret_cast<const int4 *>(a.xq + (size_t)m * K)[j];
+        }
+        for (int i = threadIdx.x; i < M * nb; i += blockDim.x) lxs[i] = a.xs[i];
+    } else {
+        if (wave < M)
+            wave_row_prologue<kRowPieces, PRO>(a, wave, lxq, lxs, lane, g, load_weights, ldq);
+        else
+            load_weights();
+    }
+    __syncthreads();
+    if (wave >= WK) {
+        // no blocks: through the chain's barriers only
+        for (int p = 0; p + 1 < WK; ++p) __syncthreads();
+        return;
+    }
+
+    // the block dots (weight rows 4*lk+r of each 16, activation row li) and
+    // their scaled forms t = f32(s) * dw; rows past M read row M-1 and are
+    // never stored
+    const int ar = min(li, M - 1);
+    float t[KB][NS][4];
+#pragma unroll
+    for (int u = 0; u < KB; ++u) {
+        const int b = min(b0 + u, nb - 1);
+        const long av = *reinterpret_cast<const long *>(lxq + (size_t)ar * ldq + b * GRX_QK + 8 * lk);
+#pragma unroll
+        for (int s = 0; s < NS; ++s) {
+            grx_v4i d = {0, 0, 0, 0};
+            d = __builtin_amdgcn_mfma_i32_16x16x32_i8(bv[u][s], av, d, 0, 0, 0);
+            const uint32_t h[2] = {dq[u][s].x, dq[u][s].y};
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const float dw = grx_f16_to_f32((uint16_t)(h[r >> 1] >> (16 * (r & 1))));
+                t[u][s][r] = __fmul_rn((float)d[r], dw);
+            }
+        }
+    }
+
+    // the ordered chain, one wave after another
+    float c[NS][4];
+    for (int p = 0; p < WK; ++p) {
+        if (wave == p) {
+            if (p == 0) {
+#pragma unroll
+                for (int s = 0; s < NS; ++s)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        const int n = n0 + 16 * s + 4 * lk + r;
+                        c[s][r] = (a.bias != nullptr && n < a.rows) ? a.bias[n] : 0.0f;
+                    }
+            } else {
+#pragma unroll
+                for (int s = 0; s < NS; ++s)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) c[s][r] = cx[(((p - 1) & 1) * NS * 4 + 4 * s + r) * 64 + lane];
+            }
+#pragma unroll
+            for (int u = 0; u < KB; ++u) {
+                if (u < nbw) {
+                    const float da = lxs[ar * nb + b0 + u];
+#pragma unroll
+                    for (int s = 0; s < NS; ++s)
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) c[s][r] = __fmaf_rn(t[u][s][r], da, c[s][r]);
+                }
+            }
+            if (p + 1 < WK) {
+#pragma unroll
+                for (int s = 0; s < NS; ++s)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) cx[((p & 1) * NS * 4 + 4 * s + r) * 64 + lane] = c[s][r];
+            }
+        }
+        if (p + 1 < WK) __syncthreads();
+    }
+    if (wave != WK - 1) return;
+
+    // ---- epilogue: output row n0+lane of activation row m in lane `lane`
+    constexpr int NR = 16 * NS;
+    if (li < M) {
+#pragma unroll
+        for (int s = 0; s < NS; ++s)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) ot[li * NR + 16 * s + 4 * lk + r] = c[s][r];
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    float acc[M];
+#pragma unroll
+    for (int m = 0; m < M; ++m) acc[m] = lane < NR ? ot[m * NR + lane] : 0.0f;
+    const int row = lane < NR ? n0 + lane : a.rows;
+    gemv_epilogue<M, 1, false, EPI>(a, acc, row, lane, 0, pos0);
+}
+
+// LDS of gemv_q8_mx_kernel.
+size_t gemv_mx_smem(int M, int NS, int nb) {
+    const size_t K = (size_t)nb * GRX_QK;
+    return ((M * (K + 16) + 15) & ~(size_t)15) + (((size_t)M * nb + 3) & ~(size_t)3) * 4 + 2 * NS * 4 * 64 * 4 +
+           (size_t)M * 16 * NS * 4;
+}
+
 // The product of ONE activation row (decode steps): q8_gemv's tile scheme
 // with the latency of a single row in mind.
 //  - every wave issues its first kPrefetch blocks' weight loads (and wave 0
@@ -1065,9 +1230,46 @@ hipError_t launch1(hipStream_t st, const GemvArgs &a, int tiles, int W) {
     }
 }
 
+template <int M, int PRO, int EPI, int NS, int KB>
+hipError_t launch_mx_one(hipStream_t st, const GemvArgs &a) {
+    const size_t smem = gemv_mx_smem(M, NS, a.nb);
+    const int groups = grx_ceil_div(a.rows, 16 * NS), WK = grx_ceil_div(a.nb, KB), W = WK > M ? WK : M;
+    gemv_q8_mx_kernel<M, PRO, EPI, NS, KB><<<groups, 64 * W, smem, st>>>(a);
+    return hipGetLastError();
+}
+
+// Whether gemv_q8_mx_kernel takes M rows of this product: 4 or 8 rows, at
+// most 8 waves of 8 blocks (16 with 16-row tiles), a one-wave prologue (rows
+// of at most 1280 values), its LDS within 64 KiB, an epilogue it ends (not
+// the argmax's per-tile slots nor the fused cross scores, not the float64
+// LayerNorm's registers), and not switched off (GEMV_MX = 0).  The rounded
+// GELU output stays on gemv_q8_kernel: 32-row tiles with the LayerNorm
+// prologue measured slower there (8 x 5120 x 1280: 14.6 us against 13.6).
+bool mx_takes(int m, int pro, int epi, int nb) {
+    if (grx_tune(GRX_TUNE_GEMV_MX) == 0) return false;
+    if (m != 4 && m != 8) return false;
+    if (nb < 1 || nb > 8 * 16) return false;
+    if (pro != GRX_PRO_PREQ && nb * GRX_QK > kRowPieces * 256) return false;
+    if (pro == GRX_PRO_LN64 || epi == GRX_EPI_ARGMAX || epi == GRX_EPI_XSCORES || epi == GRX_EPI_QKV_ROPE ||
+        epi == GRX_EPI_GELU_Q)
+        return false;
+    return gemv_mx_smem(m, 1, nb) <= 64 * 1024;
+}
+
+// 8 blocks a wave up to 64 blocks, 16 past that
+template <int M, int PRO, int EPI>
+hipError_t launch_mx(hipStream_t st, const GemvArgs &a) {
+    if (a.nb > 64) return launch_mx_one<M, PRO, EPI, 1, 16>(st, a);
+    return launch_mx_one<M, PRO, EPI, 1, 8>(st, a);
+}
+
 template <int PRO, int EPI>
 hipError_t launch_m(hipStream_t st, int m, const GemvArgs &a, int tiles, int W) {
     if (m == 1 && gemv1_fits(PRO, a.nb)) return launch1<PRO, EPI>(st, a, tiles, W);
+    if constexpr (PRO != GRX_PRO_LN64 && EPI != GRX_EPI_ARGMAX && EPI != GRX_EPI_XSCORES &&
+                  EPI != GRX_EPI_QKV_ROPE && EPI != GRX_EPI_GELU_Q) {
+        if (mx_takes(m, PRO, EPI, a.nb)) return m == 4 ? launch_mx<4, PRO, EPI>(st, a) : launch_mx<8, PRO, EPI>(st, a);
+    }
     switch (m) {
         case 1: return launch_w<1, PRO, EPI>(st, a, tiles, W);
         case 2: return launch_w<2, PRO, EPI>(st, a, tiles, W);

@@ -176,15 +176,20 @@ def _check_matmul(kern, orc, rng, m, n, k, bias=True, lda_pad=3, ldc_pad=2):
     assert (got[:, n:] == 7.0).all(), "wrote past ldc's row"
 
 
+@pytest.mark.parametrize("mx", [1, 0])
 @pytest.mark.parametrize("m", [1, 2, 3, 5, 6, 7, 8, 9, 16, 17])
-def test_matmul_odd_sizes_bit_exact(kern, orc, m):
+def test_matmul_odd_sizes_bit_exact(kern, orc, m, mx):
     """TestOddSizesBothPaths / TestInt8MatMul shapes (odd_test.go:33-35,
     q8int_test.go:87): every output bit-identical to the oracle's EVEX order,
-    strided rows (lda = k+3, ldc = n+2), with and without bias."""
+    strided rows (lda = k+3, ldc = n+2), with and without bias; groups of 4
+    and 8 rows on the matrix-core GEMV or (GEMV_MX=0) the dot-product one."""
     rng = np.random.default_rng(100 + m)
-    for n in (1, 3, 4, 5, 15, 16, 17, 33, 64, 65, 129):
-        for k in (32, 64, 96, 544):
-            _check_matmul(kern, orc, rng, m, n, k, bias=(n % 2 == 1))
+    with kern.tuned(GEMV_MX=mx):
+        for n in (1, 3, 4, 5, 15, 16, 17, 33, 64, 65, 129):
+            for k in (32, 64, 96, 544, 4096):
+                if k == 4096 and n > 65:
+                    continue
+                _check_matmul(kern, orc, rng, m, n, k, bias=(n % 2 == 1))
 
 
 @pytest.mark.parametrize("waves", [1, 2, 4, 8, 16])
