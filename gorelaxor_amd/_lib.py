@@ -130,6 +130,7 @@ SIGNATURES = {
     "grx_mimi_decode": (i32, [vp, vp, i32, vp]),
     "grx_mimi_decode_dev": (i32, [vp, vp, i32, vp]),
     "grx_mimi_samples_per_latent": (i32, [vp]),
+    "grx_mimi_load_gguf": (i32, [vp, C.c_char_p, i32, vp, C.POINTER(vp)]),
     "grx_rnnt_create": (i32, [vp, vp, C.POINTER(vp)]),
     "grx_rnnt_destroy": (i32, [vp]),
     "grx_rnnt_load_gguf": (i32, [vp, C.c_char_p, vp, C.POINTER(vp)]),

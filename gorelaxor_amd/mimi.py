@@ -42,6 +42,26 @@ class MimiDecoder:
             for name, arr in tensors.items():
                 self.set_tensor(name, arr)
 
+    @classmethod
+    def from_gguf(cls, path, max_latents: int = 4, ctx: Context | None = None) -> "MimiDecoder":
+        """The Mimi decoder of a Pocket TTS GGUF file (grx_mimi_load_gguf:
+        the Mimi part of pockettts.Load, pockettts/model.go:201-213,
+        280-308), its settings in .hp."""
+        self = cls.__new__(cls)
+        self.ctx = ctx or default_context()
+        self.handle = None
+        h = _lib.MimiHParams()
+        out = C.c_void_p()
+        _lib.call("grx_mimi_load_gguf", self.ctx.handle, str(path).encode(), max_latents, C.byref(h), C.byref(out))
+        self.handle = out
+        self.hp = dict(d=h.d, heads=h.heads, ff=h.ff, n_layer=h.layers, context=h.context, ldim=h.ldim,
+                       up_s=h.upsample, period=h.period, ratios=tuple(h.ratios[i] for i in range(h.n_ratios)),
+                       nf=h.n_filters, k=h.kernel_size, res_k=h.residual_kernel_size, last_k=h.last_kernel_size,
+                       dil_base=h.dilation_base, compress=h.compress, n_res=h.n_residual)
+        self.max_latents = max_latents
+        self.samples_per_latent = _lib.lib().grx_mimi_samples_per_latent(self.handle)
+        return self
+
     def set_tensor(self, name: str, arr: np.ndarray) -> None:
         """A matrix as ggml Q8_0 rows (uint8) or float32, a vector float32."""
         a = np.ascontiguousarray(arr)

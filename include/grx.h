@@ -445,6 +445,21 @@ grx_status grx_mimi_decode_dev(grx_mimi *m, const float *lat, int n, float *out)
 /* upsample x the product of the ratios (1920 at the english_2026-09
  * settings); 0 for NULL. */
 int grx_mimi_samples_per_latent(const grx_mimi *m);
+/* The Mimi decoder of a Pocket TTS GGUF file (the Mimi part of
+ * pockettts.Load, pockettts/model.go:201-213 and 280-308, with decoder()
+ * and resBlocks(), model.go:140-181): the file's name and source checks, the
+ * frame size from pockettts.sample_rate / frame_rate, the settings
+ * pockettts.mimi.{d_model, heads, ff, context, max_period, upsample} and
+ * pockettts.seanet.{ratios, n_filters, dimension, kernel_size,
+ * residual_kernel_size, last_kernel_size, dilation_base, compress,
+ * n_residual_layers} with the reference's range checks and texts ("a SEANet
+ * ratio of %d", "SEANet's ratios %v don't make %d-sample frames"), the
+ * transformer's layers counted by their norm1.weight, and every tensor's
+ * shape checked as mat()/vec() check it; matrices go to the device as
+ * stored (Q8_0 or float32).  max_latents bounds the latents one decode call
+ * takes; *hp_out (may be NULL) receives the settings. */
+grx_status grx_mimi_load_gguf(grx_ctx *ctx, const char *path, int max_latents, grx_mimi_hparams *hp_out,
+                              grx_mimi **out);
 
 /* ---- FastConformer encoder with Q8_0 weights ---- */
 
