@@ -1081,18 +1081,32 @@ __global__ __launch_bounds__(256) void argmax_finish_kernel(const unsigned long 
                                                             int *__restrict__ pos, int streams, int hist_stream) {
     __shared__ unsigned long long best[4][8];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    for (int m = 0; m < M; ++m) {
-        unsigned long long k = 0;
-        for (int t = tid; t < nslots; t += blockDim.x) {
-            const unsigned long long v = keys[(size_t)t * M + m];
-            k = v > k ? v : k;
-        }
+    // every row's keys of four slots a thread in flight at once
+    constexpr int U = 4;
+    unsigned long long k[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    for (int t0 = tid; t0 < nslots; t0 += U * 256) {
+        unsigned long long v[U][8];
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+#pragma unroll
+            for (int m = 0; m < 8; ++m) {
+                const int t = t0 + 256 * u;
+                v[u][m] = (m < M && t < nslots) ? keys[(size_t)t * M + m] : 0ull;
+            }
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+#pragma unroll
+            for (int m = 0; m < 8; ++m) k[m] = v[u][m] > k[m] ? v[u][m] : k[m];
+    }
+#pragma unroll
+    for (int m = 0; m < 8; ++m) {
+        if (m >= M) break;
 #pragma unroll
         for (int o = 32; o > 0; o >>= 1) {
-            const unsigned long long v = __shfl_xor(k, o);
-            k = v > k ? v : k;
+            const unsigned long long w = __shfl_xor(k[m], o);
+            k[m] = w > k[m] ? w : k[m];
         }
-        if (lane == 0) best[wave][m] = k;
+        if (lane == 0) best[wave][m] = k[m];
     }
     __syncthreads();
     if (tid < M) {
@@ -1241,10 +1255,12 @@ hipError_t launch_mx_one(hipStream_t st, const GemvArgs &a) {
 // Whether gemv_q8_mx_kernel takes M rows of this product: 4 or 8 rows, at
 // most 8 waves of 8 blocks (16 with 16-row tiles), a one-wave prologue (rows
 // of at most 1280 values), its LDS within 64 KiB, an epilogue it ends (not
-// the argmax's per-tile slots nor the fused cross scores, not the float64
-// LayerNorm's registers), and not switched off (GEMV_MX = 0).  The rounded
-// GELU output stays on gemv_q8_kernel: 32-row tiles with the LayerNorm
-// prologue measured slower there (8 x 5120 x 1280: 14.6 us against 13.6).
+// the fused cross scores, not the float64 LayerNorm's registers), and not
+// switched off (GEMV_MX = 0).  Measured slower and left on gemv_q8_kernel:
+// the rounded GELU output (its 32-row blocks on 32-row workgroups: 8 x 5120
+// x 1280 14.5 us against 13.5) and the argmax over the vocabulary (16-row
+// groups each staging the 8 rows: 8 x 51866 x 1280 30.4 us plus a row
+// kernel and 4x the key slots, against 34 us in all).
 bool mx_takes(int m, int pro, int epi, int nb) {
     if (grx_tune(GRX_TUNE_GEMV_MX) == 0) return false;
     if (m != 4 && m != 8) return false;

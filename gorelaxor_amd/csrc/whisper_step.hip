@@ -196,6 +196,38 @@ __global__ __launch_bounds__(64) void cross_scores_kernel(
     scores[(size_t)h * nctx + j] = j < (nctx & ~3) ? dot_x4(qh, kj, hd) : dot_go(qh, kj, hd);
 }
 
+// Row stride (floats) of the key rows staged by cross_scores64_kernel: a
+// lane's 16-byte reads of its own row land in distinct banks.
+constexpr int kXKeyLd = 68;
+
+// cross_scores_kernel for heads of 64 values: the run's 64 key rows are
+// staged through LDS with 16-byte loads, 16 lanes to a row (whole cache
+// lines per load, where a lane reading its own row touches 64 lines), and
+// lane j then takes key j's dotF32x4 / dotF32Go from LDS in the same order.
+// Keys past nctx repeat the last one and are not written.
+__global__ __launch_bounds__(64) void cross_scores64_kernel(const float *__restrict__ q,
+                                                            const float *__restrict__ ck, int nctx, int st,
+                                                            size_t x_stream, float *__restrict__ scores) {
+    constexpr int HD = 64;
+    __shared__ __align__(16) float lk[64 * kXKeyLd];
+    const int h = blockIdx.x, lane = threadIdx.x, sm_ = blockIdx.z, j0 = blockIdx.y * 64;
+    const float4 *kb = reinterpret_cast<const float4 *>(ck + sm_ * x_stream + (size_t)h * nctx * HD);
+    float4 kv[16];
+#pragma unroll
+    for (int u = 0; u < 16; ++u) {  // piece 64u + lane: row (64u + lane) / 16, float4 lane % 16
+        const int r = 4 * u + (lane >> 4), key = min(j0 + r, nctx - 1);
+        kv[u] = kb[(size_t)key * (HD / 4) + (lane & 15)];
+    }
+#pragma unroll
+    for (int u = 0; u < 16; ++u) reinterpret_cast<float4 *>(lk + (4 * u + (lane >> 4)) * kXKeyLd)[lane & 15] = kv[u];
+    __syncthreads();
+    const int j = j0 + lane;
+    if (j >= nctx) return;
+    const float *qh = q + (size_t)sm_ * st + h * HD;
+    const float *kr = lk + lane * kXKeyLd;
+    scores[((size_t)sm_ * (st / HD) + h) * nctx + j] = j < (nctx & ~3) ? dot_x4(qh, kr, HD) : dot_go(qh, kr, HD);
+}
+
 // softmax of one head's scores (decoder.go:109) and its weighted values
 // (decoder.go:110-118): out[d] = dotF32x4(p, Vt[d]) for d in groups of four
 // (dotF32Go for a last partial group).  Each workgroup serves DG values of
@@ -893,8 +925,13 @@ grx_status enqueue_step(grx_whisper *m, hipStream_t stream) {
             if (sep && (s = ln_rows(L.x_ln_w, L.x_ln_b, a)) != GRX_OK) return s;
             if ((s = grx_gemv_launch(stream, S, sep ? GRX_PRO_PREQ : GRX_PRO_LN, GRX_EPI_STORE, a, 0)) != GRX_OK)
                 return s;
-            cross_scores_kernel<<<dim3(nh, grx_ceil_div(nctx, 64), S), 64, 0, stream>>>(
-                m->q, L.cross_k, nctx, hd, st, x_stream, m->scores);
+            if (hd == 64) {
+                cross_scores64_kernel<<<dim3(nh, grx_ceil_div(nctx, 64), S), 64, 0, stream>>>(
+                    m->q, L.cross_k, nctx, st, x_stream, m->scores);
+            } else {
+                cross_scores_kernel<<<dim3(nh, grx_ceil_div(nctx, 64), S), 64, 0, stream>>>(
+                    m->q, L.cross_k, nctx, hd, st, x_stream, m->scores);
+            }
             GRX_LAUNCHED("cross_scores_kernel");
         }
         // workgroups over 16 outputs each, float32 out (the cross-out product
