@@ -54,7 +54,6 @@ struct grx_pocket {
     float *x = nullptr, *q = nullptr, *att = nullptr, *ff = nullptr;
     int8_t *att_q = nullptr, *ff_q = nullptr;
     float *att_s = nullptr, *ff_s = nullptr;
-    float *sc = nullptr, *vt = nullptr;       // prefix attention scratch
     float *lat = nullptr;                     // latents of a run of frames
     float *out_hist = nullptr, *eos_hist = nullptr;
     int *pos = nullptr, *frame = nullptr;

@@ -236,50 +236,47 @@ __device__ float route_dot(const float *a, int sa, const float *b, int sb, int k
     return j < (n & ~3) ? dot_x4(a, b, k) : dot_go(a, b, k);
 }
 
-// attend for T rows at once after pos0 cached positions (nn.go:200-254),
-// one workgroup per head: the scores by MatMulF32's route for T rows, each
-// row's causal softmax, then T < 4: AddScaled in key order; else the
-// product with the transposed values by the same route.  sc and vt are
-// scratch [heads][T][nk] and [heads][hd][nk] in HBM.
-__global__ __launch_bounds__(kThreads) void attn_prefix_kernel(const float *__restrict__ q, const float *__restrict__ kc,
-                                                              const float *__restrict__ vc, int pos0, int T, int d,
-                                                              int hd, float scale, float *__restrict__ sc,
-                                                              float *__restrict__ vt, float *__restrict__ att) {
-    const int h = blockIdx.x, tid = threadIdx.x, nk = pos0 + T;
-    float *S = sc + (size_t)h * T * nk;
-    float *Vt = vt + (size_t)h * hd * nk;
-    for (int i = tid; i < T * nk; i += blockDim.x) {
-        const int r = i / nk, j = i % nk;
-        S[i] = route_dot(q + (size_t)r * 3 * d + h * hd, 1, kc + (size_t)j * d + h * hd, 1, hd, r, T, j, nk);
-    }
-    for (int i = tid; i < hd * nk; i += blockDim.x) {
-        const int e = i / nk, j = i % nk;
-        Vt[i] = vc[(size_t)j * d + h * hd + e];
-    }
+// route_dot with the second operand's elements sb apart on both routes.
+__device__ float route_dot_s(const float *a, const float *b, size_t sb, int k, int r, int m, int j, int n) {
+    if (m > 16 && r < m / 6 * 6) return route_dot(a, 1, b, (int)sb, k, r, m, j, n);
+    return j < (n & ~3) ? dot_x4_s(a, b, sb, k) : dot_go_s(a, b, sb, k);
+}
+
+// attend for T rows after pos0 cached positions (nn.go:200-254), one
+// workgroup per (row r = blockIdx.x, head h = blockIdx.y): thread j takes
+// the scores of keys j, j + 64, ... by MatMulF32's route for T rows into
+// LDS, thread 0 the row's scale and causal softmax (seq_softmax, zeros past
+// the row's position), then thread e output e: T < 4 AddScaled in key
+// order, else the product with value column e (its elements d apart) by
+// the same route.  LDS: the row's pos0 + T scores.
+__global__ __launch_bounds__(64) void attn_prefix_kernel(const float *__restrict__ q, const float *__restrict__ kc,
+                                                         const float *__restrict__ vc, int pos0, int T, int d, int hd,
+                                                         float scale, float *__restrict__ att) {
+    extern __shared__ float row[];
+    const int r = blockIdx.x, h = blockIdx.y, tid = threadIdx.x, nk = pos0 + T, p = pos0 + r;
+    const float *qr = q + (size_t)r * 3 * d + h * hd;
+    for (int j = tid; j < nk; j += blockDim.x) row[j] = route_dot(qr, 1, kc + (size_t)j * d + h * hd, 1, hd, r, T, j, nk);
     __syncthreads();
-    for (int r = tid; r < T; r += blockDim.x) {
-        float *row = S + (size_t)r * nk;
-        const int p = pos0 + r;
+    if (tid == 0) {
         for (int j = 0; j <= p; ++j) row[j] = __fmul_rn(row[j], scale);
         seq_softmax(row, p + 1);
         for (int j = p + 1; j < nk; ++j) row[j] = 0.f;
     }
     __syncthreads();
     const int h8 = hd & ~7;
-    for (int i = tid; i < T * hd; i += blockDim.x) {
-        const int r = i / hd, e = i % hd;
-        const float *row = S + (size_t)r * nk;
+    for (int e = tid; e < hd; e += blockDim.x) {
+        const float *vcol = vc + h * hd + e;  // value j of column e at vcol[j * d]
         float o;
         if (T < 4) {
             o = 0.f;
             for (int j = 0; j < nk; ++j) {
                 const float w = row[j];
                 if (w == 0.f) continue;
-                const float v = Vt[(size_t)e * nk + j];
+                const float v = vcol[(size_t)j * d];
                 o = e < h8 ? __fmaf_rn(w, v, o) : __fadd_rn(o, __fmul_rn(w, v));
             }
         } else {
-            o = route_dot(row, 1, Vt + (size_t)e * nk, 1, nk, r, T, e, hd);
+            o = route_dot_s(row, vcol, (size_t)d, nk, r, T, e, hd);
         }
         att[(size_t)r * d + h * hd + e] = o;
     }
@@ -470,7 +467,6 @@ grx_status pfinalize_tensors(grx_pocket *m) {
     if ((s = palloc_t(m, sn.size(), &m->rope_sin)) != GRX_OK) return s;
     GRX_HIP(hipMemcpy(m->rope_cos, cs.data(), cs.size() * 4, hipMemcpyHostToDevice));
     GRX_HIP(hipMemcpy(m->rope_sin, sn.data(), sn.size() * 4, hipMemcpyHostToDevice));
-    const int hd = hp.d / hp.heads;
     if ((s = palloc_t(m, mp * d, &m->x)) != GRX_OK) return s;
     if ((s = palloc_t(m, mp * 3 * d, &m->q)) != GRX_OK) return s;  // q rows 3d apart
     if ((s = palloc_t(m, mp * d, &m->att)) != GRX_OK) return s;
@@ -479,8 +475,6 @@ grx_status pfinalize_tensors(grx_pocket *m) {
     if ((s = palloc_t(m, mp * d / 32, &m->att_s)) != GRX_OK) return s;
     if ((s = palloc_t(m, mp * ff, &m->ff_q)) != GRX_OK) return s;
     if ((s = palloc_t(m, mp * ff / 32, &m->ff_s)) != GRX_OK) return s;
-    if ((s = palloc_t(m, (size_t)hp.heads * mp * mp, &m->sc)) != GRX_OK) return s;
-    if ((s = palloc_t(m, (size_t)hp.heads * hd * mp, &m->vt)) != GRX_OK) return s;
     if ((s = palloc_t(m, mp * d, &m->out_hist)) != GRX_OK) return s;
     if ((s = palloc_t(m, mp, &m->eos_hist)) != GRX_OK) return s;
     if ((s = palloc_t(m, 1, &m->pos)) != GRX_OK) return s;
@@ -700,7 +694,8 @@ extern "C" grx_status grx_pocket_run(grx_pocket *m, const float *x, int T, float
             if ((s = layer_product(m, st, L, 0, r0, mm, qatt)) != GRX_OK) return s;
             r0 += mm;
         }
-        attn_prefix_kernel<<<hp.heads, kThreads, 0, st>>>(m->q, L.k, L.v, pos0, T, d, hd, scale, m->sc, m->vt, m->att);
+        attn_prefix_kernel<<<dim3(T, hp.heads), 64, (size_t)(pos0 + T) * 4, st>>>(m->q, L.k, L.v, pos0, T, d, hd,
+                                                                                 scale, m->att);
         GRX_LAUNCHED("attn_prefix_kernel");
         // the prefix's attention rows are rounded in the out product's prologue
         for (int ph = 1; ph < 4; ++ph)
