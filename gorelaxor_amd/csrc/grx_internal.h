@@ -358,6 +358,11 @@ struct GemvArgs {
     const float *xk;
     int nctx;
     float *scores;
+    // chunks > 1 (M of 2..8 rows, not ARGMAX, XSCORES nor streams): one
+    // launch runs that many consecutive groups of M rows, group g
+    // (blockIdx.z) with x, xq/xs, y, resid and yq/ys M*g rows on and
+    // pos_add M*g larger
+    int chunks;
 };
 
 grx_status grx_gemv_launch(hipStream_t st, int m, int pro, int epi, const GemvArgs &a,

@@ -501,9 +501,14 @@ GemvArgs pargs(const grx_weight *w) {
 // transformer.forward of rows r0..r0+mm-1 of x (nn.go:151-179) for one
 // layer's products; attention is separate.  ph: 0 = LN -> q|k|v, 1 = out +
 // residual, 2 = LN -> ff1 -> GELU, 3 = ff2 + residual.
-grx_status layer_product(grx_pocket *m, hipStream_t st, PLayer &L, int ph, int r0, int mm, bool qatt) {
+grx_status layer_product(grx_pocket *m, hipStream_t st, PLayer &L, int ph, int r0, int mm, bool qatt,
+                         int chunks = 1) {
     const int d = m->hp.d, ff = m->hp.ff;
     GemvArgs a;
+    auto launch = [&](int pro, int epi) {
+        a.chunks = chunks;
+        return grx_gemv_launch(st, mm, pro, epi, a, 0);
+    };
     switch (ph) {
         case 0:
             a = pargs(L.qkv);
@@ -521,7 +526,7 @@ grx_status layer_product(grx_pocket *m, hipStream_t st, PLayer &L, int ph, int r
             a.rope_cos = m->rope_cos;
             a.rope_sin = m->rope_sin;
             a.rope_half = d / m->hp.heads / 2;
-            return grx_gemv_launch(st, mm, GRX_PRO_LN64, GRX_EPI_QKV_ROPE, a, 0);
+            return launch(GRX_PRO_LN64, GRX_EPI_QKV_ROPE);
         case 1:
             a = pargs(L.out);
             a.x = m->att + (size_t)r0 * d;
@@ -532,7 +537,7 @@ grx_status layer_product(grx_pocket *m, hipStream_t st, PLayer &L, int ph, int r
             a.ldc = d;
             a.resid = m->x + (size_t)r0 * d;
             a.ldr = d;
-            return grx_gemv_launch(st, mm, qatt ? GRX_PRO_PREQ : GRX_PRO_QUANT, GRX_EPI_RESID, a, 0);
+            return launch(qatt ? GRX_PRO_PREQ : GRX_PRO_QUANT, GRX_EPI_RESID);
         case 2:
             a = pargs(L.ff1);
             a.x = m->x + (size_t)r0 * d;
@@ -543,7 +548,7 @@ grx_status layer_product(grx_pocket *m, hipStream_t st, PLayer &L, int ph, int r
             a.ldc = ff;
             a.yq = m->ff_q + (size_t)r0 * ff;
             a.ys = m->ff_s + (size_t)r0 * ff / 32;
-            return grx_gemv_launch(st, mm, GRX_PRO_LN64, GRX_EPI_GELU_Q, a, 0);
+            return launch(GRX_PRO_LN64, GRX_EPI_GELU_Q);
         default:
             a = pargs(L.ff2);
             a.xq = m->ff_q + (size_t)r0 * ff;
@@ -552,7 +557,7 @@ grx_status layer_product(grx_pocket *m, hipStream_t st, PLayer &L, int ph, int r
             a.ldc = d;
             a.resid = m->x + (size_t)r0 * d;
             a.ldr = d;
-            return grx_gemv_launch(st, mm, GRX_PRO_PREQ, GRX_EPI_RESID, a, 0);
+            return launch(GRX_PRO_PREQ, GRX_EPI_RESID);
     }
 }
 
@@ -685,14 +690,14 @@ extern "C" grx_status grx_pocket_run(grx_pocket *m, const float *x, int T, float
     hipStream_t st = m->ctx->stream;
     GRX_HIP(hipMemcpyAsync(m->x, x, (size_t)T * d * 4, hipMemcpyHostToDevice, st));
     const float scale = (float)(1.0 / sqrt((double)hd));
-    // rows in launches of 8, 4, 2 and 1
+    // rows in groups of 8 (every whole group in one launch), then 4, 2 and 1
     auto rows_of = [&](int left) { return left >= 8 ? 8 : left >= 4 ? 4 : left >= 2 ? 2 : 1; };
     for (int li = 0; li < hp.n_layer; ++li) {
         PLayer &L = m->L[li];
         for (int r0 = 0; r0 < T;) {
-            const int mm = rows_of(T - r0);
-            if ((s = layer_product(m, st, L, 0, r0, mm, qatt)) != GRX_OK) return s;
-            r0 += mm;
+            const int mm = rows_of(T - r0), nc = mm == 8 ? (T - r0) / 8 : 1;
+            if ((s = layer_product(m, st, L, 0, r0, mm, qatt, nc)) != GRX_OK) return s;
+            r0 += mm * nc;
         }
         attn_prefix_kernel<<<dim3(T, hp.heads), 64, (size_t)(pos0 + T) * 4, st>>>(m->q, L.k, L.v, pos0, T, d, hd,
                                                                                  scale, m->att);
@@ -700,9 +705,9 @@ extern "C" grx_status grx_pocket_run(grx_pocket *m, const float *x, int T, float
         // the prefix's attention rows are rounded in the out product's prologue
         for (int ph = 1; ph < 4; ++ph)
             for (int r0 = 0; r0 < T;) {
-                const int mm = rows_of(T - r0);
-                if ((s = layer_product(m, st, L, ph, r0, mm, ph == 1 ? false : qatt)) != GRX_OK) return s;
-                r0 += mm;
+                const int mm = rows_of(T - r0), nc = mm == 8 ? (T - r0) / 8 : 1;
+                if ((s = layer_product(m, st, L, ph, r0, mm, ph == 1 ? false : qatt, nc)) != GRX_OK) return s;
+                r0 += mm * nc;
             }
     }
     // out_norm of the last row into the history slot of frame 0 (not kept)

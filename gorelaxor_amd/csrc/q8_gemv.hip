@@ -395,8 +395,29 @@ __device__ __forceinline__ void gemv_epilogue(const GemvArgs &a, const float (&a
 
 // ---------------------------------------------------------------- kernel
 
+// The arguments of this workgroup's group of M rows (blockIdx.z) when one
+// launch runs several (GemvArgs::chunks).
+template <int M>
+__device__ __forceinline__ GemvArgs chunk_args(const GemvArgs &a0) {
+    GemvArgs a = a0;
+    const int g = blockIdx.z;
+    if (g > 0) {
+        const size_t r = (size_t)g * M, K = (size_t)a.nb * GRX_QK;
+        if (a.x) a.x += r * a.lda;
+        if (a.xq) a.xq += r * K;
+        if (a.xs) a.xs += r * a.nb;
+        if (a.y) a.y += r * a.ldc;
+        if (a.resid) a.resid += r * a.ldr;
+        if (a.yq) a.yq += r * a.rows;
+        if (a.ys) a.ys += r * (a.rows >> 5);
+        a.pos_add += (int)r;
+    }
+    return a;
+}
+
 template <int M, int W, int PRO, int EPI>
-__global__ __launch_bounds__(64 * W) void gemv_q8_kernel(const GemvArgs a) {
+__global__ __launch_bounds__(64 * W) void gemv_q8_kernel(const GemvArgs a0) {
+    const GemvArgs a = chunk_args<M>(a0);
     extern __shared__ __align__(16) unsigned char smem[];
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: loops stay scalar
@@ -684,7 +705,8 @@ __global__ __launch_bounds__(64 * W) void gemv_q8_kernel(const GemvArgs a) {
 // wave hands its outputs, through LDS, to the lanes of their rows and ends
 // them with gemv_epilogue.
 template <int M, int PRO, int EPI, int NS, int KB>
-__global__ __launch_bounds__(512) void gemv_q8_mx_kernel(const GemvArgs a) {
+__global__ __launch_bounds__(512) void gemv_q8_mx_kernel(const GemvArgs a0) {
+    const GemvArgs a = chunk_args<M>(a0);
     static_assert(M >= 2 && M <= 8, "2 to 8 activation rows");
     static_assert(KB % 4 == 0, "blocks per wave in whole groups of four");
     extern __shared__ __align__(16) unsigned char smem[];
@@ -1179,7 +1201,7 @@ hipError_t launch_one(hipStream_t st, const GemvArgs &a, int tiles) {
                                       hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
         }
     }
-    gemv_q8_kernel<M, W, PRO, EPI><<<tiles, 64 * W, smem, st>>>(a);
+    gemv_q8_kernel<M, W, PRO, EPI><<<dim3(tiles, 1, a.chunks > 1 ? a.chunks : 1), 64 * W, smem, st>>>(a);
     return hipGetLastError();
 }
 
@@ -1248,7 +1270,7 @@ template <int M, int PRO, int EPI, int NS, int KB>
 hipError_t launch_mx_one(hipStream_t st, const GemvArgs &a) {
     const size_t smem = gemv_mx_smem(M, NS, a.nb);
     const int groups = grx_ceil_div(a.rows, 16 * NS), WK = grx_ceil_div(a.nb, KB), W = WK > M ? WK : M;
-    gemv_q8_mx_kernel<M, PRO, EPI, NS, KB><<<groups, 64 * W, smem, st>>>(a);
+    gemv_q8_mx_kernel<M, PRO, EPI, NS, KB><<<dim3(groups, 1, a.chunks > 1 ? a.chunks : 1), 64 * W, smem, st>>>(a);
     return hipGetLastError();
 }
 
@@ -1323,6 +1345,9 @@ grx_status grx_gemv_launch(hipStream_t st, int m, int pro, int epi, const GemvAr
     if (m > 1 && pro == GRX_PRO_PREQ && (size_t)m * a.nb * GRX_QK > kStageMax)
         return grx_fail(GRX_ESIZE, "grx: %d pre-rounded rows of %d values exceed %zu bytes of LDS", m,
                         a.nb * GRX_QK, kStageMax);
+    if (a.chunks > 1 && (m < 2 || m > 8 || epi == GRX_EPI_ARGMAX || epi == GRX_EPI_XSCORES || a.streams ||
+                         a.chunks > 65535))
+        return grx_fail(GRX_EINVAL, "grx: %d groups of %d rows in one launch are not supported here", a.chunks, m);
     const int W = waves > 0 ? waves : grx_gemv_pick_waves(tiles, a.nb, m, pro);
     hipError_t e = hipErrorInvalidValue;
     if (pro == GRX_PRO_PREQ && epi == GRX_EPI_STORE) e = launch_m<GRX_PRO_PREQ, GRX_EPI_STORE>(st, m, a, tiles, W);

@@ -24,10 +24,12 @@ def _pair(orc, hp, seed=5):
     return orc.PocketOracle(hp, t), PocketLM(hp, t)
 
 
-@pytest.mark.parametrize("prefix", [1, 3, 4, 16, 17, 20])
+@pytest.mark.parametrize("prefix", [1, 3, 4, 16, 17, 20, 33])
 def test_prefix_and_frames_bit_exact(kern, orc, prefix):
     """T < 4 (AddScaled), 4 <= T <= 16 (gemvRows), T > 16 (6x16 panels and
-    gemv rows) for the prefix; then teacher-forced frames."""
+    gemv rows) for the prefix; every whole group of 8 rows of a product in
+    one launch (16: two groups, 33: four and a last row); then
+    teacher-forced frames."""
     _prefix_and_frames(orc, prefix)
 
 
