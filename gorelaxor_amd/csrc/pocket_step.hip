@@ -242,41 +242,118 @@ __device__ float route_dot_s(const float *a, const float *b, size_t sb, int k, i
     return j < (n & ~3) ? dot_x4_s(a, b, sb, k) : dot_go_s(a, b, sb, k);
 }
 
+// seq_softmax(s, n) with the 64 lanes of one wave (every lane calls it):
+// the maximum as its loop finds it (the first s[j] greater than the running
+// maximum from -inf: among equal values, +0 and -0 included, the lowest
+// index) by a reduction over (value, index), the exps in parallel, the
+// eight chains below n & ~7 summed in order by lanes 0-7 and the tail by
+// lane 8, then 1 / (HSUM + tail) and the scaled values in parallel.
+__device__ void wave_seq_softmax(float *s, int n) {
+    const int lane = threadIdx.x & 63;
+    float mx = -__builtin_inff();
+    int mi = 0x7fffffff;
+    for (int j = lane; j < n; j += 64)
+        if (s[j] > mx) {
+            mx = s[j];
+            mi = j;
+        }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        const float ov = __shfl_xor(mx, o);
+        const int oi = __shfl_xor(mi, o);
+        const bool take = ov > mx || (ov == mx && oi < mi);
+        mx = take ? ov : mx;
+        mi = take ? oi : mi;
+    }
+    const int n8 = n & ~7;
+    for (int j = lane; j < n; j += 64) {
+        const float dd = __fsub_rn(s[j], mx);
+        s[j] = j < n8 ? grx_exp8(dd) : grx_expf_go(dd);
+    }
+    __syncthreads();
+    float acc = 0.f;
+    if (lane < 8) {
+        for (int j = lane; j < n8; j += 8) acc = __fadd_rn(acc, s[j]);
+    } else if (lane == 8) {
+        for (int j = n8; j < n; ++j) acc = __fadd_rn(acc, s[j]);
+    }
+    float a8[8];
+#pragma unroll
+    for (int l = 0; l < 8; ++l) a8[l] = __shfl(acc, l);
+    const float t = __shfl(acc, 8);
+    const float sa = n8 > 0 ? hsum8(a8) : 0.f;
+    const float inv = __fdiv_rn(1.0f, __fadd_rn(sa, t));
+    for (int j = lane; j < n; j += 64) s[j] = __fmul_rn(s[j], inv);
+}
+
 // attend for T rows after pos0 cached positions (nn.go:200-254), one
-// workgroup per (row r = blockIdx.x, head h = blockIdx.y): thread j takes
-// the scores of keys j, j + 64, ... by MatMulF32's route for T rows into
-// LDS, thread 0 the row's scale and causal softmax (seq_softmax, zeros past
-// the row's position), then thread e output e: T < 4 AddScaled in key
-// order, else the product with value column e (its elements d apart) by
-// the same route.  LDS: the row's pos0 + T scores.
+// workgroup (a wave) per (row r = blockIdx.x, head h = blockIdx.y): thread
+// j takes the scores of keys j, j + 64, ... by MatMulF32's route for T
+// rows into LDS, the wave the row's scale and causal softmax
+// (wave_seq_softmax; zeros past the row's position), then thread e output
+// e: T < 4 AddScaled in key order, else the product with value column e by
+// the same route.  With `staged` (heads of 64) the head's key rows (65
+// floats apart) and value rows are first copied to LDS, 64 rows at a time
+// with every lane's 16-byte loads in flight at once, and read from there;
+// else they are read in place (value column e's elements d apart).  LDS:
+// the row's pos0 + T scores (rounded up to 4 floats), then if staged the
+// keys and the values.
 __global__ __launch_bounds__(64) void attn_prefix_kernel(const float *__restrict__ q, const float *__restrict__ kc,
                                                          const float *__restrict__ vc, int pos0, int T, int d, int hd,
-                                                         float scale, float *__restrict__ att) {
+                                                         float scale, float *__restrict__ att, int staged) {
     extern __shared__ float row[];
     const int r = blockIdx.x, h = blockIdx.y, tid = threadIdx.x, nk = pos0 + T, p = pos0 + r;
     const float *qr = q + (size_t)r * 3 * d + h * hd;
-    for (int j = tid; j < nk; j += blockDim.x) row[j] = route_dot(qr, 1, kc + (size_t)j * d + h * hd, 1, hd, r, T, j, nk);
-    __syncthreads();
-    if (tid == 0) {
-        for (int j = 0; j <= p; ++j) row[j] = __fmul_rn(row[j], scale);
-        seq_softmax(row, p + 1);
-        for (int j = p + 1; j < nk; ++j) row[j] = 0.f;
+    float *kl = row + ((nk + 3) & ~3), *vl = kl + (size_t)nk * 65;
+    if (staged) {
+        // rows c0 + 4u + tid / 16 of each run of 64, float4 tid % 16
+        for (int c0 = 0; c0 < nk; c0 += 64) {
+            float4 kr[16], vr[16];
+#pragma unroll
+            for (int u = 0; u < 16; ++u) {
+                const size_t j = (size_t)min(c0 + 4 * u + (tid >> 4), nk - 1);
+                kr[u] = reinterpret_cast<const float4 *>(kc + j * d + h * 64)[tid & 15];
+                vr[u] = reinterpret_cast<const float4 *>(vc + j * d + h * 64)[tid & 15];
+            }
+#pragma unroll
+            for (int u = 0; u < 16; ++u) {
+                const int j = c0 + 4 * u + (tid >> 4), e = 4 * (tid & 15);
+                if (j < nk) {
+                    float *kd = kl + j * 65 + e;
+                    kd[0] = kr[u].x;
+                    kd[1] = kr[u].y;
+                    kd[2] = kr[u].z;
+                    kd[3] = kr[u].w;
+                    reinterpret_cast<float4 *>(vl + j * 64)[tid & 15] = vr[u];
+                }
+            }
+        }
+        __syncthreads();
+    }
+    for (int j = tid; j < nk; j += 64) {
+        const float v = staged ? route_dot(qr, 1, kl + j * 65, 1, hd, r, T, j, nk)
+                               : route_dot(qr, 1, kc + (size_t)j * d + h * hd, 1, hd, r, T, j, nk);
+        row[j] = j <= p ? __fmul_rn(v, scale) : 0.f;
     }
     __syncthreads();
+    wave_seq_softmax(row, p + 1);
+    __syncthreads();
     const int h8 = hd & ~7;
-    for (int e = tid; e < hd; e += blockDim.x) {
-        const float *vcol = vc + h * hd + e;  // value j of column e at vcol[j * d]
+    for (int e = tid; e < hd; e += 64) {
+        // value j of column e at vcol[j * vs]
+        const float *vcol = staged ? vl + e : vc + h * hd + e;
+        const size_t vs = staged ? (size_t)64 : (size_t)d;
         float o;
         if (T < 4) {
             o = 0.f;
             for (int j = 0; j < nk; ++j) {
                 const float w = row[j];
                 if (w == 0.f) continue;
-                const float v = vcol[(size_t)j * d];
+                const float v = vcol[j * vs];
                 o = e < h8 ? __fmaf_rn(w, v, o) : __fadd_rn(o, __fmul_rn(w, v));
             }
         } else {
-            o = route_dot_s(row, vcol, (size_t)d, nk, r, T, e, hd);
+            o = route_dot_s(row, vcol, vs, nk, r, T, e, hd);
         }
         att[(size_t)r * d + h * hd + e] = o;
     }
@@ -699,8 +776,13 @@ extern "C" grx_status grx_pocket_run(grx_pocket *m, const float *x, int T, float
             if ((s = layer_product(m, st, L, 0, r0, mm, qatt, nc)) != GRX_OK) return s;
             r0 += mm * nc;
         }
-        attn_prefix_kernel<<<dim3(T, hp.heads), 64, (size_t)(pos0 + T) * 4, st>>>(m->q, L.k, L.v, pos0, T, d, hd,
-                                                                                 scale, m->att);
+        {
+            // heads of 64: keys and values through LDS while they fit in 64 KiB
+            const size_t nk = (size_t)pos0 + T, rowb = ((nk + 3) & ~(size_t)3) * 4, kvb = nk * 129 * 4;
+            const int staged = hd == 64 && rowb + kvb <= 64 * 1024;
+            attn_prefix_kernel<<<dim3(T, hp.heads), 64, rowb + (staged ? kvb : 0), st>>>(
+                m->q, L.k, L.v, pos0, T, d, hd, scale, m->att, staged);
+        }
         GRX_LAUNCHED("attn_prefix_kernel");
         // the prefix's attention rows are rounded in the out product's prologue
         for (int ph = 1; ph < 4; ++ph)

@@ -33,6 +33,20 @@ def test_prefix_and_frames_bit_exact(kern, orc, prefix):
     _prefix_and_frames(orc, prefix)
 
 
+def test_long_prefix(kern, orc):
+    """A prefix of 150 rows (keys past one wave's 64 lanes, softmax rows of
+    up to 150 scores): the output and the frames after it are the
+    oracle's."""
+    hp = dict(POCKET_TTS_TINY, max_pos=200)
+    ref, lm = _pair(orc, hp, seed=12)
+    x, lat = pocket_inputs(hp, 3, prefix=150, seed=13)
+    assert _same(lm.run(x), ref.run(x))
+    outs, eos = lm.frames(lat)
+    for k in range(lat.shape[0]):
+        wo, we = ref.step(lat[k])
+        assert _same(outs[k], wo) and _same(eos[k], we), k
+
+
 def test_frames_general_gemv_kernel(kern, orc):
     """The same with one-row products on the general kernel (GEMV1=0)."""
     with kern.tuned(GEMV1=0):
