@@ -814,7 +814,9 @@ __device__ inline const float *conv_prev_row(const ConvPrev &cp, int b, int ti, 
 // The depthwise convolution (encoder.go:362-385: from the bias, w*x unfused
 // over the taps in range, tap j at frame t + j - padL, in order), the folded
 // batch norm r*s + b (unfused) or the LayerNorm (LN), SiLU of the AVX route,
-// rounded to Q8_0 for pointwise2.  One workgroup per row.
+// rounded to Q8_0 for pointwise2.  One workgroup per row; a thread takes
+// four channels (blockDim apart) at a time with every tap's loads of the
+// four in flight together.
 template <bool LN>
 __global__ __launch_bounds__(kRowThreads) void conf_dwconv_kernel(const float *__restrict__ g, int T, int D, int K,
                                                                   int padL, const ConvPrev cp,
@@ -827,10 +829,17 @@ __global__ __launch_bounds__(kRowThreads) void conf_dwconv_kernel(const float *_
     __shared__ double red[48];  // ln_block_reduce
     const int r = blockIdx.x, t = r % T, b = r / T, tid = threadIdx.x;
     const float *gb = g + (size_t)b * T * D;
-    for (int c = tid; c < D; c += blockDim.x) {
-        float o = dwb != nullptr ? dwb[c] : 0.f;
+    const int nt = blockDim.x;
+    for (int c0 = tid; c0 < D; c0 += 4 * nt) {
+        float o[4];
+        int cc[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            cc[q] = min(c0 + q * nt, D - 1);  // clamped: loads stay in bounds, results unused
+            o[q] = dwb != nullptr ? dwb[cc[q]] : 0.f;
+        }
         for (int j0 = 0; j0 < K; j0 += 8) {
-            float xv[8], wv[8];
+            float xv[4][8], wv[4][8];
             bool ok[8];
 #pragma unroll
             for (int u = 0; u < 8; ++u) {
@@ -838,16 +847,29 @@ __global__ __launch_bounds__(kRowThreads) void conf_dwconv_kernel(const float *_
                 const float *pr = ti < 0 ? conv_prev_row(cp, b, ti, padL, D) : nullptr;
                 // taps outside the frames (and before a stream's cache) are skipped
                 ok[u] = j < K && ((ti >= 0 && ti < T) || pr != nullptr);
-                // clamped addresses keep the eight loads in flight together
-                xv[u] = pr != nullptr ? pr[c] : gb[(size_t)min(max(ti, 0), T - 1) * D + c];
-                wv[u] = w[(size_t)min(j, K - 1) * D + c];
+                // clamped addresses keep every load in flight together
+                const float *xr = pr != nullptr ? pr : gb + (size_t)min(max(ti, 0), T - 1) * D;
+                const float *wr = w + (size_t)min(j, K - 1) * D;
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    xv[q][u] = xr[cc[q]];
+                    wv[q][u] = wr[cc[q]];
+                }
             }
 #pragma unroll
-            for (int u = 0; u < 8; ++u)
-                if (ok[u]) o = __fadd_rn(o, __fmul_rn(wv[u], xv[u]));
+            for (int q = 0; q < 4; ++q)
+#pragma unroll
+                for (int u = 0; u < 8; ++u)
+                    if (ok[u]) o[q] = __fadd_rn(o[q], __fmul_rn(wv[q][u], xv[q][u]));
         }
-        if constexpr (!LN) o = __fadd_rn(__fmul_rn(o, cn_w[c]), cn_b[c]);
-        row[c] = o;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const int c = c0 + q * nt;
+            if (c >= D) break;
+            float v = o[q];
+            if constexpr (!LN) v = __fadd_rn(__fmul_rn(v, cn_w[c]), cn_b[c]);
+            row[c] = v;
+        }
     }
     __syncthreads();
     if constexpr (LN) ln_row(row, D, cn_w, cn_b, red);
