@@ -815,16 +815,23 @@ __global__ __launch_bounds__(kLdsThreads) void gemm_q8_lds_kernel(const int8_t *
                                                         8 * (lk & 1));
                 dw[g] = grx_f16_to_f32(dwl[u * 128 + col]);
             }
+            // the block's four products issued together, then their folds:
+            // no fold waits on a product issued just before it
+            v4i d[2][2];
 #pragma unroll
             for (int f = 0; f < 2; ++f)
 #pragma unroll
                 for (int g = 0; g < 2; ++g) {
-                    v4i d = {0, 0, 0, 0};
-                    d = __builtin_amdgcn_mfma_i32_16x16x32_i8(av[f], bv[g], d, 0, 0, 0);
+                    const v4i z = {0, 0, 0, 0};
+                    d[f][g] = __builtin_amdgcn_mfma_i32_16x16x32_i8(av[f], bv[g], z, 0, 0, 0);
+                }
+#pragma unroll
+            for (int f = 0; f < 2; ++f)
+#pragma unroll
+                for (int g = 0; g < 2; ++g)
 #pragma unroll
                     for (int r = 0; r < 4; ++r)
-                        c[f][g][r] = __fmaf_rn(__fmul_rn((float)d[r], dw[g]), da[f][r], c[f][g][r]);
-                }
+                        c[f][g][r] = __fmaf_rn(__fmul_rn((float)d[f][g][r], dw[g]), da[f][r], c[f][g][r]);
         }
         if (st + 1 < nsteps) {
             lstore(cur ^ 1);
