@@ -295,8 +295,10 @@ enum {
     GRX_EPI_ARGMAX = 4,  // y = c (optional) and the first index of the maximum
     GRX_EPI_GELU_Q = 5,  // y = geluVec(c), and y rounded to Q8_0 into yq/ys
     GRX_EPI_QKV_ROPE = 6, // as QKV, with q and k rotated by the cos/sin table at pos
-    GRX_EPI_XSCORES = 7   // one row, tile = one head of 64: the head's cross-attention
+    GRX_EPI_XSCORES = 7,  // one row, tile = one head of 64: the head's cross-attention
                           // scores over a run of 64 keys (blockIdx.y) instead of y
+    GRX_EPI_AXPY_HALF = 8,  // y = fma(0.5, c, resid) (a macaron feed-forward's residual)
+    GRX_EPI_SILU_Q = 9      // SiLU of c rounded to Q8_0 into yq/ys only (whole 32-row blocks)
 };
 
 struct GemvArgs {

@@ -1057,6 +1057,33 @@ grx_status grx_gemm_q8_launch_ex(hipStream_t st, const grx_weight *w, const int8
         return grx_fail(GRX_EINVAL, "unknown product epilogue %d", o.epi);
     if (o.epi == GRX_GEMM_SILU_Q && w->rows % GRX_QK != 0)
         return grx_fail(GRX_ESIZE, "rounded product output needs rows %% 32 == 0 (rows %d)", w->rows);
+    const int kind = grx_tune(GRX_TUNE_GEMM_KERNEL);
+    // one row (a conformer's one-row streaming chunk step, a single latent)
+    // on the one-row GEMV: the same blocks folded in the same order, its
+    // weights streamed once; a forced GEMM_KERNEL keeps the matrix cores
+    if (m == 1 && kind < 0 && o.carry == nullptr && o.epi != GRX_GEMM_SCALE && w->nb > 0 &&
+        grx_tune(GRX_TUNE_GEMV1) != 0) {
+        GemvArgs a = {};
+        a.qs = w->qs;
+        a.ds = w->ds;
+        a.rows = w->rows;
+        a.nb = w->nb;
+        a.xq = xq;
+        a.xs = xs;
+        a.bias = bias;
+        a.y = o.y;
+        a.ldc = o.ldc;
+        a.resid = o.y;
+        a.ldr = o.ldc;
+        a.yq = o.yq;
+        a.ys = o.ys;
+        a.cacheable = 0;  // weights streamed once a step
+        const int epi = o.epi == GRX_GEMM_STORE ? GRX_EPI_STORE
+                        : o.epi == GRX_GEMM_ADD ? GRX_EPI_RESID
+                        : o.epi == GRX_GEMM_AXPY_HALF ? GRX_EPI_AXPY_HALF
+                                                      : GRX_EPI_SILU_Q;
+        return grx_gemv_launch(st, 1, GRX_PRO_PREQ, epi, a, 0);
+    }
     // GEMM_KERNEL picks the kernel (tests force each one with it): the
     // LDS-staged tiles from 256 rows on; below that the K-split tiles with
     // their activations staged through LDS (at 224 rows: 1024 x 4096 17 us
@@ -1066,7 +1093,6 @@ grx_status grx_gemm_q8_launch_ex(hipStream_t st, const grx_weight *w, const int8
     // (at 126 rows: 4096 x 1024 10.4 us on the register walk against 11.9
     // K-split; 2048 x 1024 8.1 against 7.3; 1024 x 4096 25 against 19), the
     // register walk otherwise
-    const int kind = grx_tune(GRX_TUNE_GEMM_KERNEL);
     // the K-split kernel stages the activations through LDS unless told not
     // to or they are not in 16-byte aligned whole groups of four blocks
     const int da4 = (w->nb % 4 == 0 && ((uintptr_t)xs & 15) == 0) ? 1 : 0;

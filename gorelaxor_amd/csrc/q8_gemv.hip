@@ -302,6 +302,41 @@ __device__ __forceinline__ void gemv_epilogue(const GemvArgs &a, const float (&a
         }
         return;
     }
+    if constexpr (EPI == GRX_EPI_AXPY_HALF) {
+        // the matrix-core product's AXPY_HALF: y = fma(0.5, c, resid)
+#pragma unroll
+        for (int m = 0; m < M; ++m) {
+            if (!mine(m)) continue;
+            if (row < a.rows) a.y[(size_t)m * a.ldc + row] = __fmaf_rn(0.5f, acc[m], a.resid[(size_t)m * a.ldr + row]);
+        }
+        return;
+    }
+    if constexpr (EPI == GRX_EPI_SILU_Q) {
+        // the matrix-core product's SILU_Q: v = c / (EXP8(-c) + 1), then
+        // quantU8 of its 32-value blocks (rows 64*tile..+31 and +32..+63,
+        // rows % 32 == 0) into yq [M][rows], ys [M][rows/32]
+#pragma unroll
+        for (int m = 0; m < M; ++m) {
+            if (!mine(m)) continue;
+            const float x = acc[m];
+            const float v = row < a.rows ? __fdiv_rn(x, __fadd_rn(grx_exp8(__fsub_rn(0.0f, x)), 1.0f)) : 0.0f;
+            const float av = fabsf(v);
+            float amax = av > 0.0f ? av : 0.0f;
+#pragma unroll
+            for (int o = 16; o > 0; o >>= 1) {
+                const float t = __shfl_xor(amax, o, 32);
+                amax = t > amax ? t : amax;
+            }
+            if (row < a.rows) {
+                const float id = amax != 0.0f ? __fdiv_rn(127.0f, amax) : 0.0f;
+                float r = rintf(__fmul_rn(v, id));
+                r = fminf(fmaxf(r, -128.0f), 127.0f);
+                a.yq[(size_t)m * a.rows + row] = (int8_t)(int)r;
+                if ((lane & 31) == 0) a.ys[(size_t)m * (a.rows >> 5) + (row >> 5)] = __fmul_rn(amax, grx_bits_f32(0x3c010204u));
+            }
+        }
+        return;
+    }
     if constexpr (EPI == GRX_EPI_GELU_Q) {
         // geluVec, then quantU8 of the output's 32-value blocks for the next
         // product: rows 64*tile..+31 and +32..+63 are two whole blocks
@@ -1371,6 +1406,15 @@ grx_status grx_gemv_launch(hipStream_t st, int m, int pro, int epi, const GemvAr
     else if (pro == GRX_PRO_PREQ && epi == GRX_EPI_ARGMAX) e = launch_m<GRX_PRO_PREQ, GRX_EPI_ARGMAX>(st, m, a, tiles, W);
     else if (pro == GRX_PRO_LN64 && epi == GRX_EPI_QKV_ROPE) e = launch_m<GRX_PRO_LN64, GRX_EPI_QKV_ROPE>(st, m, a, tiles, W);
     else if (pro == GRX_PRO_LN64 && epi == GRX_EPI_GELU_Q) e = launch_m<GRX_PRO_LN64, GRX_EPI_GELU_Q>(st, m, a, tiles, W);
+    else if (pro == GRX_PRO_PREQ && (epi == GRX_EPI_AXPY_HALF || epi == GRX_EPI_SILU_Q)) {
+        // one pre-rounded row (the matrix-core product's one-row epilogues)
+        if (m != 1 || !gemv1_fits(pro, a.nb))
+            return grx_fail(GRX_EINVAL, "grx: epilogue %d takes one pre-rounded row on the one-row kernel", epi);
+        if (epi == GRX_EPI_SILU_Q && a.rows % GRX_QK != 0)
+            return grx_fail(GRX_ESIZE, "rounded product output needs rows %% 32 == 0 (rows %d)", a.rows);
+        e = epi == GRX_EPI_AXPY_HALF ? launch1<GRX_PRO_PREQ, GRX_EPI_AXPY_HALF>(st, a, tiles, W)
+                                     : launch1<GRX_PRO_PREQ, GRX_EPI_SILU_Q>(st, a, tiles, W);
+    }
     else return grx_fail(GRX_EINVAL, "grx: no GEMV variant for prologue %d epilogue %d", pro, epi);
     if (e != hipSuccess) return grx_hip_fail(e, "gemv_q8_kernel");
     if (epi == GRX_EPI_ARGMAX && a.keys != nullptr) {
