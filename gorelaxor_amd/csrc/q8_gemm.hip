@@ -1060,9 +1060,11 @@ grx_status grx_gemm_q8_launch_ex(hipStream_t st, const grx_weight *w, const int8
     const int kind = grx_tune(GRX_TUNE_GEMM_KERNEL);
     // one row (a conformer's one-row streaming chunk step, a single latent)
     // on the one-row GEMV: the same blocks folded in the same order, its
-    // weights streamed once; a forced GEMM_KERNEL keeps the matrix cores
+    // weights streamed once; a forced GEMM_KERNEL keeps the matrix cores,
+    // and so does a long K on few rows (1024 x 4096: 10.9 us on the GEMV's
+    // 16 workgroups against 9.1 K-split)
     if (m == 1 && kind < 0 && o.carry == nullptr && o.epi != GRX_GEMM_SCALE && w->nb > 0 &&
-        grx_tune(GRX_TUNE_GEMV1) != 0) {
+        (w->nb <= 64 || w->rows >= 2048) && grx_tune(GRX_TUNE_GEMV1) != 0) {
         GemvArgs a = {};
         a.qs = w->qs;
         a.ds = w->ds;
