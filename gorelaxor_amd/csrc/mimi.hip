@@ -393,6 +393,26 @@ void gridn(size_t n, unsigned *blocks) { *blocks = (unsigned)((n + kThreads - 1)
 // y += the product (kern.Add of it, the residual's sum).
 grx_status lin(grx_mimi *m, hipStream_t st, const MLin &w, const float *x, int rows, float *y, bool add = false) {
     if (rows == 0) return GRX_OK;
+    if (w.q && rows % 8 == 0 && rows <= 64 && w.k <= 1280) {
+        // a few groups of 8 rows in one several-row GEMV launch that rounds
+        // its rows in its own prologue (quantU8, the same arithmetic as the
+        // rounding launch it replaces)
+        GemvArgs a = {};
+        a.qs = w.q->qs;
+        a.ds = w.q->ds;
+        a.rows = w.q->rows;
+        a.nb = w.q->nb;
+        a.x = x;
+        a.lda = w.k;
+        a.bias = w.b;
+        a.y = y;
+        a.ldc = w.n;
+        a.resid = y;
+        a.ldr = w.n;
+        a.cacheable = 1;
+        a.chunks = rows / 8;
+        return grx_gemv_launch(st, 8, GRX_PRO_QUANT, add ? GRX_EPI_RESID : GRX_EPI_STORE, a, 0);
+    }
     if (w.q) {
         grx_status s = grx_quant_rows(st, x, w.k, rows, w.k, m->xq, m->xs);
         if (s != GRX_OK) return s;
