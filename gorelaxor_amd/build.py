@@ -9,6 +9,7 @@ from __future__ import annotations
 
 import glob
 import os
+import re
 import shutil
 import subprocess
 import sys
@@ -45,12 +46,29 @@ def _compile_one(src: str, build_dir: str, extra: list[str]) -> tuple[str, subpr
     return obj, p
 
 
-def _stale(src: str, build_dir: str, headers: list[str]) -> bool:
+def _local_includes(path: str, seen: set[str] | None = None) -> set[str]:
+    """The in-tree headers `path` includes with #include "...", transitively."""
+    seen = set() if seen is None else seen
+    try:
+        text = open(path).read()
+    except OSError:
+        return seen
+    for name in re.findall(r'^\s*#\s*include\s+"([^"]+)"', text, re.M):
+        for d in (os.path.dirname(path), CSRC, os.path.join(ROOT, "include")):
+            h = os.path.join(d, name)
+            if os.path.exists(h) and h not in seen:
+                seen.add(h)
+                _local_includes(h, seen)
+                break
+    return seen
+
+
+def _stale(src: str, build_dir: str) -> bool:
     obj = os.path.join(build_dir, os.path.basename(src) + ".o")
     if not os.path.exists(obj):
         return True
     t = os.path.getmtime(obj)
-    return any(os.path.getmtime(f) > t for f in [src, *headers])
+    return any(os.path.getmtime(f) > t for f in [src, *_local_includes(src)])
 
 
 def build(verbose: bool = True, out: str = LIB, defines: list[str] | None = None, incremental: bool = False) -> str:
@@ -64,8 +82,7 @@ def build(verbose: bool = True, out: str = LIB, defines: list[str] | None = None
     os.makedirs(build_dir, exist_ok=True)
     extra = [f"-D{d}" for d in (defines or [])]
     t0 = time.time()
-    headers = glob.glob(os.path.join(CSRC, "*.h")) + [os.path.join(ROOT, "include", "grx.h")]
-    todo = [s for s in sources() if not incremental or _stale(s, build_dir, headers)]
+    todo = [s for s in sources() if not incremental or _stale(s, build_dir)]
     jobs = [_compile_one(s, build_dir, extra) for s in todo]
     objs = [os.path.join(build_dir, os.path.basename(s) + ".o") for s in sources()]
     failed = []

@@ -110,6 +110,8 @@ enum {
     GRX_TUNE_NO_GRAPH,        // 1: model loops launch kernel by kernel (no HIP graphs)
     GRX_TUNE_GEMM_STAGE_A,    // 0: the K-split kernel reads activations straight from memory, 1: through LDS
     GRX_TUNE_GEMV_MX,         // 0: several-row GEMVs on the dot-product kernel, not the matrix-core one
+    GRX_TUNE_GEMV1_ROWS,      // rows per workgroup of one-row products: 8, 16, 32 (slices) or 64 (whole tiles)
+    GRX_TUNE_FUSE_SELF_ATTN,  // 0: whisper's q|k|v product and self-attention in launches of their own
     GRX_TUNE_COUNT
 };
 int grx_tune(int id);

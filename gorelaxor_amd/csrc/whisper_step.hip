@@ -29,6 +29,7 @@
 
 #include "grx_float.h"
 #include "grx_internal.h"
+#include "q8_gemv_impl.h"
 
 namespace {
 
@@ -472,18 +473,20 @@ __global__ __launch_bounds__(256) void cross_values_wave_kernel(const float *__r
     const int kk = nctx & ~15, steps = kk >> 4, nfull = steps / G, ng = (steps + G - 1) / G;
     // values: one uniform base, 32-bit offsets
     const float *__restrict__ vb = cv + sm_ * x_stream + ((size_t)h * hd + blockIdx.y * kWaveOut) * nctx;
-    // every value of this thread's chain in flight before the softmax
+    // the scores first (loads return in order: the softmax waits for
+    // nothing issued after them), then every value of this thread's chain,
+    // in flight during the softmax
+    float sv[PER];
+#pragma unroll
+    for (int u = 0; u < PER; ++u) sv[u] = scores[min(tid + NT * u, nctx - 1)];
+    const int n8 = nctx & ~7, jt = n8 + tid;  // threads tid < nctx - n8 take the tail
+    const float st_ = scores[min(jt, nctx - 1)];
     float vv[KB], vt[16];
 #pragma unroll
     for (int u = 0; u < KB; ++u) vv[u] = vb[dl * nctx + min(16 * u + c, max(kk - 1, 0))];
     // the values past 16 * steps (dotF32Go's tail), ahead of need
 #pragma unroll
     for (int i = 0; i < 16; ++i) vt[i] = vb[dl * nctx + min(kk + i, nctx - 1)];
-    float sv[PER];
-#pragma unroll
-    for (int u = 0; u < PER; ++u) sv[u] = scores[min(tid + NT * u, nctx - 1)];
-    const int n8 = nctx & ~7, jt = n8 + tid;  // threads tid < nctx - n8 take the tail
-    const float st_ = scores[min(jt, nctx - 1)];
     float mx = sv[0];
 #pragma unroll
     for (int u = 1; u < PER; ++u) mx = sv[u] > mx ? sv[u] : mx;
@@ -554,6 +557,286 @@ __global__ __launch_bounds__(256) void cross_values_wave_kernel(const float *__r
     float o = kk > 0 ? __fadd_rn(h01, h23) : 0.f;
     if (kk < nctx) o = __fadd_rn(o, dot_go15_reg(p2, vt, nctx - kk));
     if (c == 0) att[h * hd + d] = o;
+}
+
+// ---------------------------------------------------------------- q|k|v + self-attention
+
+// One stream's self-attention for head h (blockIdx.x), heads of 64, in one
+// launch (decoder.go:60-87): the head's q, k and v (three 64-row tiles of
+// the fused q|k|v weight on the int8 route: the LayerNorm'd row, or layer
+// 0's embedding row, built by wave 0 as the products' prologue builds it,
+// each output's fold in block order), k and v into the cache at pos, then
+// the causal attention over pos+1 positions with self_attn_kernel's
+// arithmetic (dotF32Go scores times sc, block_softmax's EXP8/expf split and
+// sums, out[d] += p_j * v_j[d] in position order, unfused), the output
+// rounded to Q8_0.  A decode step is a chain of dependent launches, each
+// with a fixed cost of several microseconds, so the head's product and its
+// attention share one; the cached keys and values of the first kQaChunk
+// positions are loaded before the product starts, their latency hidden
+// behind it.  Positions go to four threads each (a quarter of the head's 64
+// dims): dotF32Go's four running sums pass from lane to lane, quarter by
+// quarter in piece order, so every sum adds in the reference's order.
+constexpr int kQaPf = 3;        // (tile, block) pairs per wave whose loads precede the prologue
+constexpr int kQaChunk = 256;   // positions per pass (four threads each)
+constexpr int kQaMaxN = 1024;   // longest context the kernel takes
+constexpr int kQaPld = 68;      // floats between rows of products (16-byte writes in distinct banks)
+constexpr int kQaCs = kQaMaxN / 8 + 4;
+
+struct QaLds {
+    size_t xs, q, red, s, pj, ch, big, total;
+};
+__host__ __device__ inline QaLds qkv_attn_lds(int nb) {
+    QaLds o;
+    const size_t K = (size_t)nb * GRX_QK;
+    o.xs = (K + 15) & ~(size_t)15;
+    o.q = o.xs + (((size_t)nb * 4 + 15) & ~(size_t)15);
+    o.red = o.q + 3 * 64 * 4;
+    o.s = o.red + 32 * 4;
+    o.pj = o.s + (kQaMaxN + 8) * 4;
+    o.ch = o.pj + (kQaMaxN + 8) * 4;
+    o.big = o.ch + (8 * kQaCs + 16) * 4;
+    const size_t lp = (size_t)3 * nb * 64 * 4, prod = (size_t)kQaChunk * kQaPld * 4;
+    o.total = o.big + (lp > prod ? lp : prod);
+    return o;
+}
+
+// 16 bytes at byte offset off of a buffer resource; offsets past its size
+// read zeros and touch no memory (no branch, so the loads' wait counts stay
+// exact)
+typedef float grx_v4f __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ float4 rsrc_load4(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    const grx_v4f v = __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0);
+    return make_float4(v.x, v.y, v.z, v.w);
+}
+// A buffer resource over the first n bytes at p (raw: no stride, no swizzle)
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc_of(const float *p, uint32_t n) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(p), (short)0, (int)n, 0x00020000);
+}
+
+// row shift by one lane within rows of 16 (lane l receives lane l-1's value)
+__device__ __forceinline__ float shr1(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x111, 0xf, 0xf, false));
+}
+
+template <int NP, int PRO>
+__global__ __launch_bounds__(1024) void qkv_attn_kernel(const GemvArgs a, float sc, int ctx_rows,
+                                                        float *__restrict__ att, int8_t *__restrict__ att_q,
+                                                        float *__restrict__ att_s) {
+    extern __shared__ __align__(16) unsigned char smem[];
+    constexpr int W = 16;
+    const int h = blockIdx.x, tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int st = a.seg, nb = a.nb, tpm = st >> 6;  // tiles per q, k or v matrix
+    const int pos = *a.pos, n = pos + 1;
+    const QaLds L = qkv_attn_lds(nb);
+    int8_t *lxq = reinterpret_cast<int8_t *>(smem);
+    float *lxs = reinterpret_cast<float *>(smem + L.xs);
+    float *lq = reinterpret_cast<float *>(smem + L.q), *lk = lq + 64, *lv = lk + 64;
+    float *red = reinterpret_cast<float *>(smem + L.red);
+    float *sl = reinterpret_cast<float *>(smem + L.s), *pjl = reinterpret_cast<float *>(smem + L.pj);
+    float *ch = reinterpret_cast<float *>(smem + L.ch), *dummy = ch + 8 * kQaCs;
+    float *lp = reinterpret_cast<float *>(smem + L.big), *prod = lp;
+
+    // ---- loads that wait for nothing: this wave's first (tile, block)
+    // pairs.  The cached key and value quarters of positions 0..255
+    // (thread t: position t / 4, quarter t % 4) go out once the row is
+    // built (keys) and once the blocks' products are formed (values): issued
+    // with the weights they would hold up the row the prologue waits for.
+    // They read through buffer resources of pos rows: rows from pos on read
+    // zeros without a memory access (row pos comes from LDS).
+    const int p = tid >> 2, c = tid & 3;
+    const int np = 3 * nb, ne = wave < np ? (np - wave + W - 1) / W : 0;
+    const int4 *__restrict__ wq = reinterpret_cast<const int4 *>(a.qs);
+    auto load_pair = [&](int e, int4 &w0, int4 &w1, uint32_t &dh) {
+        const int u = e / nb, b = e - u * nb;
+        const size_t blk = (size_t)(u * tpm + h) * nb + b;
+        w0 = wq[blk * 128 + lane];
+        w1 = wq[blk * 128 + 64 + lane];
+        dh = a.ds[blk * 64 + lane];
+    };
+    int4 pw[2 * kQaPf];
+    uint32_t pd[kQaPf];
+    const int npf = min(kQaPf, ne);
+    float4 kq[4], vq[4];
+    const __amdgpu_buffer_rsrc_t krs = rsrc_of(a.kc, (uint32_t)pos * st * 4), vrs = rsrc_of(a.vc, (uint32_t)pos * st * 4);
+    const uint32_t qoff = (uint32_t)(h * 64 + 16 * c) * 4;  // this thread's quarter within a row
+    auto early = [&] {
+#pragma unroll
+        for (int u = 0; u < kQaPf; ++u)
+            if (u < npf) load_pair(wave + u * W, pw[2 * u], pw[2 * u + 1], pd[u]);
+    };
+    if (wave != 0) early();
+    float bias = 0.0f;
+    if (wave < 3 && a.bias != nullptr) bias = a.bias[wave * st + h * 64 + lane];
+
+    // ---- prologue (wave 0): the row, rounded to Q8_0, into LDS
+    if (wave == 0) wave_row_prologue<NP, PRO>(a, 0, lxq, lxs, lane, h, early);
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < 4; ++i) kq[i] = rsrc_load4(krs, (uint32_t)p * st * 4 + qoff + 16 * i);
+
+    // ---- block products of pair e = u * nb + b into lp [3 * nb][64]
+    auto dots = [&](int e, const int4 &w0, const int4 &w1, uint32_t dh) {
+        const int b = e - (e / nb) * nb;
+        const int4 *pa = reinterpret_cast<const int4 *>(lxq + (size_t)b * GRX_QK);
+        const int s = sdot8(w0, w1, pa[0], pa[1]);
+        lp[(size_t)e * 64 + lane] = __fmul_rn((float)s, grx_f16_to_f32((uint16_t)dh));
+    };
+#pragma unroll
+    for (int u = 0; u < kQaPf; ++u)
+        if (u < npf) dots(wave + u * W, pw[2 * u], pw[2 * u + 1], pd[u]);
+    for (int u0 = kQaPf; u0 < ne; u0 += kQaPf) {
+        int4 w[2 * kQaPf];
+        uint32_t dh[kQaPf];
+        const int nv = min(kQaPf, ne - u0);
+#pragma unroll
+        for (int u = 0; u < kQaPf; ++u)
+            if (u < nv) load_pair(wave + (u0 + u) * W, w[2 * u], w[2 * u + 1], dh[u]);
+#pragma unroll
+        for (int u = 0; u < kQaPf; ++u)
+            if (u < nv) dots(wave + (u0 + u) * W, w[2 * u], w[2 * u + 1], dh[u]);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) vq[i] = rsrc_load4(vrs, (uint32_t)p * st * 4 + qoff + 16 * i);
+    __syncthreads();
+
+    // ---- waves 0, 1, 2 fold q, k, v: c = fma(p_b, da_b, c) in block order
+    if (wave < 3) {
+        float acc = bias;
+        const float *lpu = lp + (size_t)wave * nb * 64;
+        int b = 0;
+        for (; b + 8 <= nb; b += 8) {
+            float t[8], s8[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                t[u] = lpu[(size_t)(b + u) * 64 + lane];
+                s8[u] = lxs[b + u];
+            }
+#pragma unroll
+            for (int u = 0; u < 8; ++u) acc = __fmaf_rn(t[u], s8[u], acc);
+        }
+        for (; b < nb; ++b) acc = __fmaf_rn(lpu[(size_t)b * 64 + lane], lxs[b], acc);
+        lq[wave * 64 + lane] = acc;  // lq, lk, lv
+        if (wave == 1) a.kc[(size_t)pos * st + h * 64 + lane] = acc;
+        if (wave == 2) a.vc[(size_t)pos * st + h * 64 + lane] = acc;
+    }
+    __syncthreads();
+
+    // ---- scores of positions 0..n-1 (dotF32Go, gemm.go:294-308, times sc)
+    float4 qv[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) qv[i] = reinterpret_cast<const float4 *>(lq + 16 * c)[i];
+    const int nch = (n + kQaChunk - 1) / kQaChunk;
+    for (int k = 0; k < nch; ++k) {
+        const int j = k * kQaChunk + p;
+        float4 kk[4];
+        if (k == 0) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) kk[i] = kq[i];
+        } else {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) kk[i] = rsrc_load4(krs, (uint32_t)j * st * 4 + qoff + 16 * i);
+        }
+        if (j == pos) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) kk[i] = reinterpret_cast<const float4 *>(lk + 16 * c)[i];
+        }
+        // quarter r extends the four sums quarter r-1 left (lane c's are
+        // right once lane c-1's have arrived, after round c)
+        float s0 = 0.f, s1 = 0.f, s2 = 0.f, s3 = 0.f;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            if (r > 0) {
+                s0 = shr1(s0);
+                s1 = shr1(s1);
+                s2 = shr1(s2);
+                s3 = shr1(s3);
+            }
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                s0 = __fadd_rn(s0, __fmul_rn(qv[i].x, kk[i].x));
+                s1 = __fadd_rn(s1, __fmul_rn(qv[i].y, kk[i].y));
+                s2 = __fadd_rn(s2, __fmul_rn(qv[i].z, kk[i].z));
+                s3 = __fadd_rn(s3, __fmul_rn(qv[i].w, kk[i].w));
+            }
+        }
+        if (c == 3 && j < n) sl[j] = __fmul_rn(__fadd_rn(__fadd_rn(__fadd_rn(s0, s1), s2), s3), sc);
+    }
+    __syncthreads();
+    // ---- softmax (mathx.go:78-90 as block_softmax forms it): thread t
+    // owns position t; waves with no position below n wait at the barriers
+    // (the serial sums run faster without them on the same SIMDs)
+    const bool live = tid < n, wlive = wave * 64 < n;
+    const float sv = live ? sl[tid] : -__builtin_inff();
+    float e = 0.0f;
+    if (wlive) {
+        const float m = wave_max(sv);
+        if (lane == 0) red[wave] = m;
+    }
+    __syncthreads();
+    if (wlive) {
+        const int nw = (n + 63) >> 6;
+        float mx = red[0];
+        for (int w = 1; w < nw; ++w) mx = red[w] > mx ? red[w] : mx;
+        const int n8 = n & ~7;
+        const float d = __fsub_rn(sv, mx);
+        const float e8 = grx_exp8(d), eg = grx_expf_go(d);
+        e = tid < n8 ? e8 : eg;
+        *(tid < n8 ? ch + (tid & 7) * kQaCs + (tid >> 3) : dummy) = e;
+        *(live ? sl + tid : dummy + 1) = e;
+    }
+    __syncthreads();
+    if (wave == 0) {
+        const float inv = softmax_inv(ch, kQaCs, sl + (n & ~7), n);
+        if (lane == 0) red[16] = inv;
+    }
+    __syncthreads();
+    if (live) pjl[tid] = __fmul_rn(e, red[16]);
+    __syncthreads();
+
+    // ---- out[d] += p_j * v_j[d] in position order: each pass's products
+    // into LDS (zeros past n), wave 0's lane d adds them in order
+    float o = 0.f;
+    for (int k = 0; k < nch; ++k) {
+        const int j = k * kQaChunk + p;
+        float4 vv[4];
+        if (k == 0) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) vv[i] = vq[i];
+        } else {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) vv[i] = rsrc_load4(vrs, (uint32_t)j * st * 4 + qoff + 16 * i);
+        }
+        if (j == pos) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) vv[i] = reinterpret_cast<const float4 *>(lv + 16 * c)[i];
+        }
+        const bool lj = j < n;
+        const float pj = pjl[lj ? j : 0];
+        float4 *pr = reinterpret_cast<float4 *>(prod + (size_t)p * kQaPld + 16 * c);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const float4 v = vv[i];
+            pr[i] = lj ? make_float4(__fmul_rn(pj, v.x), __fmul_rn(pj, v.y), __fmul_rn(pj, v.z), __fmul_rn(pj, v.w))
+                       : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+        __syncthreads();
+        if (wave == 0) {
+            const int rows = min(kQaChunk, n - k * kQaChunk), r32 = (rows + 31) & ~31;
+            for (int j0 = 0; j0 < r32; j0 += 32) {
+                float t[32];
+#pragma unroll
+                for (int i = 0; i < 32; ++i) t[i] = prod[(size_t)(j0 + i) * kQaPld + lane];
+#pragma unroll
+                for (int i = 0; i < 32; ++i) o = __fadd_rn(o, t[i]);
+            }
+        }
+        __syncthreads();
+    }
+    if (wave == 0) {
+        att[h * 64 + lane] = o;
+        quant32_store(o, att_q + h * 64 + lane, att_s + (h * 64 + lane) / 32, lane & 31);
+    }
 }
 
 // cross K (scaled) [h][t][d] and V [h][d][t] from K, V [t][h*hd+d]
@@ -789,6 +1072,21 @@ GemvArgs gemv_args(const grx_weight *w) {
 // A kernel choice tuned to 0 (for comparisons in tests).
 bool tuned_off(int id) { return grx_tune(id) == 0; }
 
+// One stream's fused q|k|v + self-attention of every head (qkv_attn_kernel).
+template <int NP, int PRO>
+grx_status launch_qkv_attn(hipStream_t stream, const GemvArgs &a, int nh, float sc, int ctx_rows, grx_whisper *m) {
+    static bool raised = false;  // set by the eager step that precedes any capture
+    if (!raised) {
+        raised = true;
+        GRX_HIP(hipFuncSetAttribute((const void *)qkv_attn_kernel<NP, PRO>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                    160 * 1024));
+    }
+    qkv_attn_kernel<NP, PRO><<<nh, 1024, qkv_attn_lds(a.nb).total, stream>>>(a, sc, ctx_rows, m->att, m->att_q,
+                                                                               m->att_s);
+    GRX_LAUNCHED("qkv_attn_kernel");
+    return GRX_OK;
+}
+
 // The launches of one decode step on stream st.
 grx_status enqueue_step(grx_whisper *m, hipStream_t stream) {
     const grx_whisper_hparams &hp = m->hp;
@@ -831,9 +1129,36 @@ grx_status enqueue_step(grx_whisper *m, hipStream_t stream) {
         a.xs = m->ln_s;
         return grx_ln_quant_rows(stream, m->x, st, S, st, w, b, m->ln_q, m->ln_s);
     };
+    // one stream, heads of 64: each head's q|k|v product and its attention
+    // in one launch (rows up to 512 values: wider rows' prologue registers
+    // do not fit beside the prefetched keys and values; contexts up to
+    // kQaMaxN)
+    const bool fused_attn = S == 1 && hd == 64 && st % 64 == 0 && st <= 512 && hp.n_text_ctx <= kQaMaxN &&
+                            !tuned_off(GRX_TUNE_FUSE_SELF_ATTN);
     for (int li = 0; li < hp.n_layer; ++li) {
         WLayer &L = m->L[li];
-        {  // LN -> q | k | v, k and v into the cache at pos; layer 0 embeds first
+        if (fused_attn) {
+            GemvArgs a = gemv_args(L.qkv);
+            a.x = m->x;
+            a.lda = st;
+            a.ln_w = L.attn_ln_w;
+            a.ln_b = L.attn_ln_b;
+            a.bias = L.qkv_b;
+            a.seg = st;
+            a.kc = L.self_k;
+            a.vc = L.self_v;
+            a.pos = m->pos;
+            if (li == 0) {
+                a.tok = m->tok;
+                a.emb_qs = m->tok_emb->qs;
+                a.emb_ds = m->tok_emb->ds;
+                a.pos_emb = m->dec_pos;
+                a.x_out = m->x;
+            }
+            s = li == 0 ? launch_qkv_attn<2, GRX_PRO_EMBED_LN>(stream, a, nh, sc, hp.n_text_ctx, m)
+                        : launch_qkv_attn<2, GRX_PRO_LN>(stream, a, nh, sc, hp.n_text_ctx, m);
+            if (s != GRX_OK) return s;
+        } else {  // LN -> q | k | v, k and v into the cache at pos; layer 0 embeds first
             GemvArgs a = gemv_args(L.qkv);
             a.x = m->x;
             a.lda = st;
@@ -865,14 +1190,16 @@ grx_status enqueue_step(grx_whisper *m, hipStream_t stream) {
                 if (s != GRX_OK) return s;
             }
             if ((s = grx_gemv_launch(stream, S, pro, GRX_EPI_QKV, a, 0)) != GRX_OK) return s;
+            if (qatt)
+                self_attn_kernel<true><<<dim3(nh, S), kAttnThreads, attn_smem, stream>>>(
+                    m->q, L.self_k, L.self_v, m->pos, st, hd, sc, rc, kv_stream, m->att, m->att_q, m->att_s,
+                    hp.n_text_ctx);
+            else
+                self_attn_kernel<false><<<dim3(nh, S), kAttnThreads, attn_smem, stream>>>(
+                    m->q, L.self_k, L.self_v, m->pos, st, hd, sc, rc, kv_stream, m->att, nullptr, nullptr,
+                    hp.n_text_ctx);
+            GRX_LAUNCHED("self_attn_kernel");
         }
-        if (qatt)
-            self_attn_kernel<true><<<dim3(nh, S), kAttnThreads, attn_smem, stream>>>(
-                m->q, L.self_k, L.self_v, m->pos, st, hd, sc, rc, kv_stream, m->att, m->att_q, m->att_s, hp.n_text_ctx);
-        else
-            self_attn_kernel<false><<<dim3(nh, S), kAttnThreads, attn_smem, stream>>>(
-                m->q, L.self_k, L.self_v, m->pos, st, hd, sc, rc, kv_stream, m->att, nullptr, nullptr, hp.n_text_ctx);
-        GRX_LAUNCHED("self_attn_kernel");
         auto out_proj = [&](grx_weight *w, const float *b, bool rounded) {  // x += att . W^T + b
             if (S > 1 && w->nb <= 128) {
                 // several streams: the K-split matrix-core product, its

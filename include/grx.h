@@ -650,11 +650,12 @@ long long grx_debug_alloc_countdown(void);
  * later products take.  Overrides one of the library's kernel choices
  * by name: GEMM_MIN_M, GEMM_KERNEL, GEMM_NS, GEMM_KB, GEMV_WAVES, GEMV1,
  * CONF_ATTN_RQ, FUSE_LN, FUSE_XSCORES, WAVE_VALUES, ARGMAX_ATOMIC,
- * NO_GRAPH; value -1 gives the choice back to the library.  The
- * environment variable GRX_<name>, read once, sets the starting value.
- * Every choice gives the same results bit for bit.  Process-wide; a model
- * whose HIP graph is already captured keeps the kernels it captured.
- * GRX_EINVAL for an unknown name. */
+ * NO_GRAPH, GEMM_STAGE_A, GEMV_MX, GEMV1_ROWS, FUSE_SELF_ATTN; value -1
+ * gives the choice back to the library.  The environment variable
+ * GRX_<name>, read once, sets the starting value.  Every choice gives the
+ * same results bit for bit.  Process-wide; a model whose HIP graph is
+ * already captured keeps the kernels it captured.  GRX_EINVAL for an
+ * unknown name. */
 grx_status grx_debug_tune(const char *name, int value);
 
 #ifdef __cplusplus

@@ -216,6 +216,23 @@ def test_matmul_one_row_kernels(kern, orc, gemv1):
                     _check_matmul(kern, orc, rng, 1, n, k, bias=(n % 2 == 0))
 
 
+@pytest.mark.parametrize("rows", [8, 16, 32, 64])
+def test_matmul_one_row_slices(kern, orc, rows):
+    """One-row products on slices of 8, 16 or 32 rows of the weight's
+    64-row tiles (GEMV1_ROWS; 64 = whole tiles), every wave count: block
+    counts that leave a partial last group of blocks and waves with no
+    block, row counts with partial tiles and slices past the last row,
+    tile counts that are not a multiple of the 8 XCDs: every bit as the
+    oracle."""
+    rng = np.random.default_rng(61 + rows)
+    with kern.tuned(GEMV1_ROWS=rows):
+        for waves in (-1, 1, 2, 4, 8, 16):
+            with kern.tuned(GEMV_WAVES=waves):
+                for n, k in ((8, 32), (65, 96), (130, 512), (64, 1024), (200, 1280), (70, 1312), (520, 2048),
+                             (64, 5120), (1000, 160)):
+                    _check_matmul(kern, orc, rng, 1, n, k, bias=(n % 2 == 0))
+
+
 @pytest.mark.parametrize("kernel", [1, 2])
 def test_matmul_matrix_cores_all_small_sizes(kern, orc, kernel):
     """The matrix-core products forced for every m (GEMM_MIN_M=1), the

@@ -53,6 +53,16 @@ def test_frames_general_gemv_kernel(kern, orc):
         _prefix_and_frames(orc, 3)
 
 
+@pytest.mark.parametrize("rows", [8, 16, 32, 64])
+def test_frames_each_row_slice(kern, orc, rows):
+    """The frames with one-row products on slices of 8, 16 or 32 rows of
+    each tile (GEMV1_ROWS; 64 = whole tiles): the rotary q|k|v epilogue
+    (pairs in adjacent lanes), the float64 LayerNorm prologue, the rounded
+    GELU: bit-identical."""
+    with kern.tuned(GEMV1_ROWS=rows):
+        _prefix_and_frames(orc, 3)
+
+
 def _prefix_and_frames(orc, prefix):
     hp = dict(POCKET_TTS_TINY)
     ref, lm = _pair(orc, hp)

@@ -33,18 +33,57 @@ def _same(a, b):
 @pytest.mark.parametrize("shape", ["tiny", "ragged", "wide"])
 def test_decode_logits_bit_exact(kern, orc, shape, gemv1):
     """Every step's logits bit-identical, with the one-row decode kernel
-    (GEMV1=1, the default) and with the general product kernel.  The
-    wide shape (d 512, heads of 64) takes the cross query inside the scores
-    kernel (FUSE_XSCORES=0 turns that off with the general kernel); its
-    101 audio positions leave a partial last run of keys and three keys on
-    dotF32Go's route."""
+    (GEMV1=1, the default) and with the general product kernel.  The tiny
+    and wide shapes (heads of 64) take each head's q|k|v product and its
+    self-attention in one launch and the wide one the cross query inside
+    the scores kernel (FUSE_SELF_ATTN=0 and FUSE_XSCORES=0 turn both off
+    with the general kernel); its 101 audio positions leave a partial last
+    run of keys and three keys on dotF32Go's route."""
     hp = dict(WHISPER_TINY_TEST)
     if shape == "ragged":  # audio length not a multiple of 16, odd head count
         hp.update(n_audio_ctx=101, n_head=4, n_state=96, n_vocab=333)
     if shape == "wide":
         hp.update(n_audio_ctx=101, n_head=8, n_state=512, n_vocab=333)
-    with kern.tuned(GEMV1=gemv1, FUSE_XSCORES=gemv1):
+    with kern.tuned(GEMV1=gemv1, FUSE_XSCORES=gemv1, FUSE_SELF_ATTN=gemv1):
         _decode_logits_bit_exact(orc, hp)
+
+
+@pytest.mark.parametrize("rows", [8, 16, 32, 64])
+@pytest.mark.parametrize("shape", ["ragged", "wide"])
+def test_decode_each_row_slice(kern, orc, shape, rows):
+    """The one-row products on slices of 8, 16 or 32 rows of each 64-row
+    tile (GEMV1_ROWS; 64 = whole tiles): the q|k|v cache epilogue, the
+    embedding prologue stored once, the residual and rounded GELU
+    epilogues; every step's logits bit-identical."""
+    hp = dict(WHISPER_TINY_TEST)
+    if shape == "ragged":
+        hp.update(n_audio_ctx=101, n_head=4, n_state=96, n_vocab=333)
+    if shape == "wide":
+        hp.update(n_audio_ctx=101, n_head=8, n_state=512, n_vocab=333)
+    with kern.tuned(GEMV1_ROWS=rows):
+        _decode_logits_bit_exact(orc, hp)
+
+
+@pytest.mark.parametrize("fuse", [1, 0])
+def test_decode_self_attention_past_one_pass(kern, orc, fuse):
+    """A context longer than one pass of the fused q|k|v + self-attention
+    kernel (256 positions, four threads each): heads of 64 over 300
+    positions, logits bit-identical at every step; and the same with the
+    product and the attention in launches of their own (FUSE_SELF_ATTN=0)."""
+    hp = dict(WHISPER_TINY_TEST, n_text_ctx=320)
+    with kern.tuned(FUSE_SELF_ATTN=fuse):
+        ref, dec = _pair(orc, hp, seed=21)
+        toks = [5, 17, 3, 99]
+        lr = ref.decode(toks)
+        lg, nxt = dec.decode(toks)
+        assert _same(lg, lr)
+        for step in range(296):
+            tok = nxt
+            lr = ref.decode([tok])
+            lg, nxt = dec.decode([tok])
+            assert _same(lg, lr), f"step {step}: max |diff| {np.abs(lg - lr).max()}"
+            assert nxt == orc.argmax(lr)
+        assert dec.pos == 300
 
 
 def _decode_logits_bit_exact(orc, hp):
