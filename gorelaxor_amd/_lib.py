@@ -73,6 +73,10 @@ SIGNATURES = {
     "grx_whisper_streams": (i32, [vp]),
     "grx_whisper_set_encoder_output_stream": (i32, [vp, i32, vp, i32]),
     "grx_whisper_greedy_streams": (i32, [vp, vp, i32, i32, vp]),
+    "grx_whisper_stream_copy": (i32, [vp, i32, i32]),
+    "grx_whisper_share_encoder_output": (i32, [vp, i32, i32]),
+    "grx_whisper_steps": (i32, [vp, i32, vp]),
+    "grx_whisper_logits": (i32, [vp, i32, vp]),
     "grx_whisper_load_ggml": (i32, [vp, C.c_char_p, i32, vp, C.POINTER(vp)]),
     "grx_whisper_sample_logits": (i32, [vp, vp, i32, vp, vp, C.c_float, C.c_float, vp]),
     "grx_whisper_sample": (i32, [vp, i32, vp, vp, C.c_float, C.c_float, vp]),
@@ -108,6 +112,13 @@ SIGNATURES = {
     "grx_pocket_pos": (i32, [vp]),
     "grx_pocket_run": (i32, [vp, vp, i32, vp]),
     "grx_pocket_frames": (i32, [vp, vp, i32, vp, vp]),
+    "grx_pocket_state_create": (i32, [vp, vp, vp, i32, C.POINTER(vp)]),
+    "grx_pocket_load_voice_gguf": (i32, [vp, C.c_char_p, C.POINTER(vp)]),
+    "grx_pocket_state_save": (i32, [vp, C.POINTER(vp)]),
+    "grx_pocket_set_state": (i32, [vp, vp]),
+    "grx_pocket_state_positions": (i32, [vp]),
+    "grx_pocket_state_read": (i32, [vp, vp, vp]),
+    "grx_pocket_state_destroy": (i32, [vp]),
     "grx_conformer_create": (i32, [vp, vp, C.POINTER(vp)]),
     "grx_conformer_load_gguf": (i32, [vp, C.c_char_p, vp, C.POINTER(vp)]),
     "grx_conformer_destroy": (i32, [vp]),

@@ -43,6 +43,7 @@ struct PLayer {
 struct grx_pocket {
     grx_ctx *ctx = nullptr;
     grx_pocket_hparams hp{};
+    std::string sha;  // general.source.sha256 of the model file it was loaded from ("" when built from tensors)
     std::map<std::string, std::vector<uint8_t>> host;
     bool ready = false;
     std::vector<PLayer> L;

@@ -23,6 +23,7 @@
 #include <vector>
 
 #include "grx_internal.h"
+#include "pocket_internal.h"
 
 namespace {
 
@@ -126,6 +127,7 @@ extern "C" grx_status grx_pocket_load_gguf(grx_ctx *ctx, const char *path, int m
     if (!l.err.empty()) return grx_fail(l.code, "%s", l.err.c_str());
     grx_pocket *m = nullptr;
     if ((s = grx_pocket_create(ctx, &hp, &m)) != GRX_OK) return s;
+    m->sha = grx_gguf_string(f, "general.source.sha256", "");
     auto done = [&](grx_status st) {
         if (st != GRX_OK) grx_pocket_destroy(m);
         return st;

@@ -37,7 +37,6 @@ constexpr int kAttnThreads = 256;
 
 // ---------------------------------------------------------------- kernels
 
-constexpr int kBatch = 32;  // loads issued before their values are used
 constexpr int kBatchV = 96;  // the same for the cross values' longer chains (one batch at 1500 keys)
 
 // Self-attention workgroups are 256 threads; heads of 64 over at most
@@ -234,7 +233,7 @@ __global__ __launch_bounds__(64) void cross_scores64_kernel(const float *__restr
 // (dotF32Go for a last partial group).  Each workgroup serves DG values of
 // d of one head, 16 lanes per d: lane l (l < 8) runs the lane-l chain of the
 // assembly's first accumulator, lane 8+l that of the second, in step order,
-// the values fetched kBatch steps at a time; the tail past n &^ 15 is one
+// the values fetched a batch of steps at a time; the tail past n &^ 15 is one
 // lane's dotF32Go.  Every workgroup of a head computes the same softmax into
 // its LDS.  With QOUT (DG == 32) the 32 outputs are rounded to Q8_0.
 // blockIdx.z is the stream (its cross values x_stream floats after the
@@ -1581,5 +1580,98 @@ extern "C" grx_status grx_whisper_greedy_streams(grx_whisper *m, const int32_t *
         GRX_HIP(hipMemcpyAsync(out + (size_t)k * (n_steps + 1), m->hist + (size_t)k * m->hp.n_text_ctx + (n_prompt - 1),
                                (size_t)(n_steps + 1) * 4, hipMemcpyDeviceToHost, stream));
     GRX_HIP(hipStreamSynchronize(stream));
+    return GRX_OK;
+}
+
+// kvCache.copyFrom (whisper/decoder.go:22-28) between the streams of one
+// decoder: stream dst's self-attention keys and values take stream src's
+// rows for the positions filled so far, its next token and its token record
+// src's.  Cross keys and values stay (grx_whisper_share_encoder_output).
+extern "C" grx_status grx_whisper_stream_copy(grx_whisper *m, int dst, int src) {
+    if (!m) return grx_fail(GRX_EINVAL, "grx_whisper_stream_copy: NULL model");
+    if (dst < 0 || dst >= m->S || src < 0 || src >= m->S)
+        return grx_fail(GRX_EINVAL, "grx_whisper_stream_copy: streams %d, %d of %d", dst, src, m->S);
+    grx_status s = finalize(m);
+    if (s != GRX_OK) return s;
+    if (dst == src) return GRX_OK;
+    const grx_whisper_hparams &hp = m->hp;
+    const size_t kv_stream = (size_t)hp.n_text_ctx * hp.n_state, rows = (size_t)m->pos_host * hp.n_state * 4;
+    hipStream_t stream = m->ctx->stream;
+    GRX_HIP(hipSetDevice(m->ctx->device));
+    for (int li = 0; li < hp.n_layer && rows > 0; ++li) {
+        WLayer &L = m->L[li];
+        GRX_HIP(hipMemcpyAsync(L.self_k + dst * kv_stream, L.self_k + src * kv_stream, rows, hipMemcpyDeviceToDevice,
+                               stream));
+        GRX_HIP(hipMemcpyAsync(L.self_v + dst * kv_stream, L.self_v + src * kv_stream, rows, hipMemcpyDeviceToDevice,
+                               stream));
+    }
+    GRX_HIP(hipMemcpyAsync(m->tok + dst, m->tok + src, 4, hipMemcpyDeviceToDevice, stream));
+    GRX_HIP(hipMemcpyAsync(m->hist + (size_t)dst * hp.n_text_ctx, m->hist + (size_t)src * hp.n_text_ctx,
+                           (size_t)hp.n_text_ctx * 4, hipMemcpyDeviceToDevice, stream));
+    GRX_HIP(hipStreamSynchronize(stream));
+    return GRX_OK;
+}
+
+// Stream dst takes stream src's cross-attention keys and values: streams
+// decoding one window (transcribe.go:170-204, bestOf sequences) share its
+// encoder output without a second projection (a device copy).
+extern "C" grx_status grx_whisper_share_encoder_output(grx_whisper *m, int dst, int src) {
+    if (!m) return grx_fail(GRX_EINVAL, "grx_whisper_share_encoder_output: NULL model");
+    if (dst < 0 || dst >= m->S || src < 0 || src >= m->S)
+        return grx_fail(GRX_EINVAL, "grx_whisper_share_encoder_output: streams %d, %d of %d", dst, src, m->S);
+    if (!m->ready || !m->have_xs[src])
+        return grx_fail(GRX_ESTATE, "grx_whisper_share_encoder_output: stream %d has no encoder output", src);
+    if (dst == src) return GRX_OK;
+    const grx_whisper_hparams &hp = m->hp;
+    const size_t n = (size_t)hp.n_audio_ctx * hp.n_state;
+    hipStream_t stream = m->ctx->stream;
+    GRX_HIP(hipSetDevice(m->ctx->device));
+    for (int li = 0; li < hp.n_layer; ++li) {
+        WLayer &L = m->L[li];
+        GRX_HIP(hipMemcpyAsync(L.cross_k + dst * n, L.cross_k + src * n, n * 4, hipMemcpyDeviceToDevice, stream));
+        GRX_HIP(hipMemcpyAsync(L.cross_v + dst * n, L.cross_v + src * n, n * 4, hipMemcpyDeviceToDevice, stream));
+    }
+    GRX_HIP(hipStreamSynchronize(stream));
+    m->have_xs[dst] = true;
+    m->have_cross = std::all_of(m->have_xs.begin(), m->have_xs.end(), [](bool b) { return b; });
+    return GRX_OK;
+}
+
+// n_steps greedy steps of every stream from the current position, each
+// stream fed the token its last step chose (the loop of transcribe.go:
+// 207-260 with plain argmax, continued); out [n_streams][n_steps] receives
+// the tokens chosen.
+extern "C" grx_status grx_whisper_steps(grx_whisper *m, int n_steps, int32_t *out) {
+    grx_status s = check_ready(m, "grx_whisper_steps");
+    if (s != GRX_OK) return s;
+    if (n_steps < 0 || (n_steps > 0 && !out)) return grx_fail(GRX_EINVAL, "grx_whisper_steps: bad arguments");
+    if (n_steps > 0 && m->pos_host == 0)
+        return grx_fail(GRX_ESTATE, "grx_whisper_steps: nothing decoded yet (no token to feed)");
+    if (m->pos_host + n_steps > m->hp.n_text_ctx)
+        return grx_fail(GRX_ESTATE, "grx_whisper_steps: %d steps after %d positions exceed the context of %d", n_steps,
+                        m->pos_host, m->hp.n_text_ctx);
+    const int p0 = m->pos_host;
+    for (int i = 0; i < n_steps; ++i) {
+        if ((s = run_step(m)) != GRX_OK) return s;
+        m->pos_host++;
+    }
+    hipStream_t stream = m->ctx->stream;
+    for (int k = 0; k < m->S && n_steps > 0; ++k)
+        GRX_HIP(hipMemcpyAsync(out + (size_t)k * n_steps, m->hist + (size_t)k * m->hp.n_text_ctx + p0,
+                               (size_t)n_steps * 4, hipMemcpyDeviceToHost, stream));
+    GRX_HIP(hipStreamSynchronize(stream));
+    return GRX_OK;
+}
+
+// The logits of stream `stream`'s last step (n_vocab floats) into host memory.
+extern "C" grx_status grx_whisper_logits(grx_whisper *m, int stream_ix, float *out) {
+    if (!m || !out) return grx_fail(GRX_EINVAL, "grx_whisper_logits: NULL argument");
+    if (stream_ix < 0 || stream_ix >= m->S)
+        return grx_fail(GRX_EINVAL, "grx_whisper_logits: stream %d of %d", stream_ix, m->S);
+    if (!m->logits || m->pos_host == 0) return grx_fail(GRX_ESTATE, "grx_whisper_logits: nothing decoded yet");
+    GRX_HIP(hipSetDevice(m->ctx->device));
+    GRX_HIP(hipMemcpyAsync(out, m->logits + (size_t)stream_ix * m->hp.n_vocab, (size_t)m->hp.n_vocab * 4,
+                           hipMemcpyDeviceToHost, m->ctx->stream));
+    GRX_HIP(hipStreamSynchronize(m->ctx->stream));
     return GRX_OK;
 }

@@ -15,6 +15,40 @@ from . import _lib
 from .kern import Context, default_context
 
 
+class PocketState:
+    """The flow LM's transformer state on the device (tstate, pockettts/
+    nn.go:113-126): each layer's rotated keys and values for `positions`
+    positions.  A Voice (pockettts/voice.go:13-24) is one; seeding an LM
+    with it (PocketLM.set_state) leaves it unchanged."""
+
+    def __init__(self, handle, n_layer: int, d: int):
+        self.handle = handle
+        self.n_layer, self.d = n_layer, d
+
+    @property
+    def positions(self) -> int:
+        return _lib.lib().grx_pocket_state_positions(self.handle)
+
+    def read(self):
+        """(k, v): host copies, [n_layer][positions][d] each."""
+        n = self.positions
+        k = np.zeros((self.n_layer, n, self.d), np.float32)
+        v = np.zeros((self.n_layer, n, self.d), np.float32)
+        _lib.call("grx_pocket_state_read", self.handle, k.ctypes.data_as(C.c_void_p), v.ctypes.data_as(C.c_void_p))
+        return k, v
+
+    def close(self):
+        if self.handle:
+            _lib.call("grx_pocket_state_destroy", self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
 class PocketLM:
     def __init__(self, hp: dict, tensors: dict | None = None, ctx: Context | None = None):
         self.ctx = ctx or default_context()
@@ -69,6 +103,37 @@ class PocketLM:
 
     def reset(self) -> None:
         _lib.call("grx_pocket_reset", self.handle)
+
+    def make_state(self, k: np.ndarray, v: np.ndarray) -> PocketState:
+        """A state from keys and values [n_layer][positions][d] (rotated keys,
+        as the caches hold them)."""
+        d, nl = self.hp["d"], self.hp["n_layer"]
+        k = np.ascontiguousarray(k, np.float32)
+        v = np.ascontiguousarray(v, np.float32)
+        if k.shape != v.shape or k.size % (d * nl) != 0:
+            raise ValueError(f"keys {k.shape} and values {v.shape} are not [{nl}][positions][{d}]")
+        out = C.c_void_p()
+        _lib.call("grx_pocket_state_create", self.handle, k.ctypes.data_as(C.c_void_p), v.ctypes.data_as(C.c_void_p),
+                  k.size // (d * nl), C.byref(out))
+        return PocketState(out, nl, d)
+
+    def load_voice(self, path: str) -> PocketState:
+        """Model.LoadVoice (pockettts/voice.go:26-64): a voice file made for
+        the model file this LM was loaded from."""
+        out = C.c_void_p()
+        _lib.call("grx_pocket_load_voice_gguf", self.handle, str(path).encode(), C.byref(out))
+        return PocketState(out, self.hp["n_layer"], self.hp["d"])
+
+    def state(self) -> PocketState:
+        """The LM's positions so far, copied into a new state."""
+        out = C.c_void_p()
+        _lib.call("grx_pocket_state_save", self.handle, C.byref(out))
+        return PocketState(out, self.hp["n_layer"], self.hp["d"])
+
+    def set_state(self, st: PocketState) -> None:
+        """tstate.clone into the LM (speakChunk, pockettts/speak.go:117): the
+        caches take the state's positions, the next position its count."""
+        _lib.call("grx_pocket_set_state", self.handle, st.handle)
 
     @property
     def pos(self) -> int:

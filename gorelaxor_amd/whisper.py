@@ -128,6 +128,28 @@ class WhisperDecoder:
                   out.ctypes.data_as(C.c_void_p))
         return out
 
+    def copy_stream(self, dst: int, src: int) -> None:
+        """kvCache.copyFrom (whisper/decoder.go:22-28): stream dst's cache,
+        next token and token record become stream src's."""
+        _lib.call("grx_whisper_stream_copy", self.handle, dst, src)
+
+    def share_encoder_output(self, dst: int, src: int) -> None:
+        """Stream dst takes stream src's cross keys and values."""
+        _lib.call("grx_whisper_share_encoder_output", self.handle, dst, src)
+
+    def steps(self, n_steps: int) -> np.ndarray:
+        """n_steps greedy steps of every stream from the current position,
+        each fed its last choice: tokens [streams][n_steps]."""
+        out = np.zeros((self.streams, n_steps), np.int32)
+        _lib.call("grx_whisper_steps", self.handle, n_steps, out.ctypes.data_as(C.c_void_p))
+        return out
+
+    def logits(self, stream: int = 0) -> np.ndarray:
+        """Stream `stream`'s logits of the last step."""
+        out = np.zeros(self.hp["n_vocab"], np.float32)
+        _lib.call("grx_whisper_logits", self.handle, stream, out.ctypes.data_as(C.c_void_p))
+        return out
+
     def sample(self, rules: Rules, tokens=(), has_ts: bool = False, seek_delta: int = 0, temp: float = 0.0,
                r: float = 0.0, stream: int = 0) -> dict:
         """The token rules and sampler over stream `stream`'s last logits,

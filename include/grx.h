@@ -238,6 +238,26 @@ grx_status grx_whisper_set_encoder_output_stream(grx_whisper *m, int stream, con
 grx_status grx_whisper_greedy_streams(grx_whisper *m, const int32_t *prompts, int n_prompt, int n_steps,
                                       int32_t *out);
 
+/* kvCache.copyFrom (whisper/decoder.go:22-28) between streams of one
+ * decoder: stream dst's self-attention cache takes stream src's rows for
+ * the positions filled so far, and dst's next token and token record
+ * become src's.  transcribe.go:196-204 decodes a window's prompt once and
+ * copies that cache to each bestOf sequence; here those sequences are the
+ * streams.  Cross keys and values are not copied. */
+grx_status grx_whisper_stream_copy(grx_whisper *m, int dst, int src);
+/* Stream dst takes stream src's cross-attention keys and values (streams
+ * decoding one window share its encoder output; a device copy, no second
+ * projection).  GRX_ESTATE when src has none. */
+grx_status grx_whisper_share_encoder_output(grx_whisper *m, int dst, int src);
+/* n_steps greedy steps of every stream from the current position, each
+ * stream fed the token its last step chose (the loop of
+ * whisper/transcribe.go:207-260 with plain argmax, continued after a
+ * decode, a greedy run or a stream copy); out [n_streams][n_steps]
+ * receives the tokens chosen. */
+grx_status grx_whisper_steps(grx_whisper *m, int n_steps, int32_t *out);
+/* The logits of stream `stream`'s last step (n_vocab floats, host). */
+grx_status grx_whisper_logits(grx_whisper *m, int stream, float *out);
+
 /* A whisper.cpp (ggml) model file straight into a decoder of n_streams
  * streams (1, 2, 4 or 8): replaces whisper.Load (whisper/model.go:93-225)
  * and Model.bind (model.go:300-404) for the decoder.  The file is read and
@@ -398,6 +418,40 @@ grx_status grx_pocket_run(grx_pocket *m, const float *x, int T, float *out);
  * trip in between: outs (n x d, may be NULL) receives each frame's out_norm
  * output and eos (n, may be NULL) its end-of-speech logit. */
 grx_status grx_pocket_frames(grx_pocket *m, const float *latents, int n, float *outs, float *eos);
+
+/* The flow LM's transformer state (tstate, pockettts/nn.go:113-126): each
+ * layer's rotated keys and values for `positions` positions, held in device
+ * memory on the LM's device.  A Voice (pockettts/voice.go:13-24) is such a
+ * state.  A state does not change when the LM runs on from it, so one
+ * voice seeds any number of chunks, as speakChunk's clone does. */
+typedef struct grx_pocket_state grx_pocket_state;
+/* A state from host keys and values k, v [n_layer][positions][d] (the LM's
+ * layer count and width), as a Voice holds them. */
+grx_status grx_pocket_state_create(grx_pocket *m, const float *k, const float *v, int positions,
+                                   grx_pocket_state **out);
+/* Model.LoadVoice (pockettts/voice.go:26-64): a voice GGUF file made for the
+ * model file the LM was loaded from (grx_pocket_load_gguf; its
+ * general.source.sha256), with the reference's checks in its order and its
+ * texts: architecture "pockettts-voice", the model's hash, the LM's layer
+ * count and 1..4096 positions, tensors voice.{i}.k and voice.{i}.v of
+ * [positions][d] (float32, float16 or bfloat16, widened to float32), every
+ * value a number. */
+grx_status grx_pocket_load_voice_gguf(grx_pocket *m, const char *path, grx_pocket_state **out);
+/* The LM's current state (its positions so far), copied into a new state
+ * on the device. */
+grx_status grx_pocket_state_save(grx_pocket *m, grx_pocket_state **out);
+/* tstate.clone (nn.go:128-140) into the LM, as speakChunk seeds a chunk
+ * from its voice (speak.go:117): the LM's caches take the state's
+ * positions and its next position becomes the state's count; the state
+ * is unchanged.  The LM's max_pos bounds the room left for the text and
+ * the frames (GRX_ESTATE when the state alone exceeds it; GRX_EINVAL for
+ * another layer count, width or device). */
+grx_status grx_pocket_set_state(grx_pocket *m, const grx_pocket_state *s);
+int grx_pocket_state_positions(const grx_pocket_state *s);
+/* Host copies of the state's keys and values, [n_layer][positions][d]
+ * floats each (either may be NULL). */
+grx_status grx_pocket_state_read(const grx_pocket_state *s, float *k, float *v);
+grx_status grx_pocket_state_destroy(grx_pocket_state *s);
 
 /* ---- pocket-TTS's Mimi decoder (latents to audio) ---- */
 

@@ -473,6 +473,27 @@ class PocketOracle:
     def reset(self):
         self._m.pos = 0
 
+    def set_state(self, k: np.ndarray, v: np.ndarray) -> None:
+        """Seed the caches with a state of n positions, k and v [n_layer][n][d]
+        (a Voice, pockettts/voice.go:26-64, cloned as speakChunk clones it,
+        speak.go:117): rows 0..n-1 of every layer, next position n."""
+        d, nl = self.hp["d"], self.hp["n_layer"]
+        k = _f32(k).reshape(nl, -1, d)
+        v = _f32(v).reshape(nl, -1, d)
+        n = k.shape[1]
+        if n > self.hp["max_pos"]:
+            raise ValueError("the state does not fit the context")
+        for i in range(nl):
+            self.k[i][: n * d] = k[i].ravel()
+            self.v[i][: n * d] = v[i].ravel()
+        self._m.pos = n
+
+    def state(self):
+        """(k, v) [n_layer][pos][d]: the caches' rows so far."""
+        d, n = self.hp["d"], self.pos
+        return (np.stack([c[: n * d].reshape(n, d) for c in self.k]),
+                np.stack([c[: n * d].reshape(n, d) for c in self.v]))
+
     def run(self, x: np.ndarray) -> np.ndarray:
         """flowLM.run of T rows (the text prefix): out_norm of the last row."""
         x = _f32(x).copy()

@@ -255,3 +255,59 @@ def test_large_v3_turbo_eight_streams(kern, orc):
         one.set_encoder_output(encs[k])
         assert list(one.greedy(prompt, n)) == list(got[k]), k
     assert len({tuple(g) for g in got}) > 1  # the streams differ
+
+
+@pytest.mark.parametrize("n", [2, 4])
+def test_forked_streams_equal_redecoding_the_prompt(kern, orc, n):
+    """transcribe.go:170-204 over streams: one window's encoder output set
+    on stream 0 and shared with the others (no second projection); the
+    prompt decoded on stream 0 while the other streams decode other
+    prompts; then kvCache.copyFrom (decoder.go:22-28) of stream 0 into
+    every other stream.  Every stream then continues exactly as
+    re-decoding the prompt does: the same greedy tokens as the oracle's
+    prompt decode, and at every step the oracle's logits bit for bit."""
+    from gorelaxor_amd.whisper import WhisperDecoder
+
+    hp = dict(WHISPER_TINY_TEST)
+    t = whisper_model(hp, seed=23)
+    enc = encoder_output(hp, seed=24)
+    dec = WhisperDecoder(hp, t, streams=n)
+    dec.set_encoder_output_stream(0, enc)
+    for k in range(1, n):
+        dec.share_encoder_output(k, 0)
+    prompt = [7, 3, 11, 5]
+    prompts = [prompt] + [[20 + k, 2, 9, 1 + k] for k in range(1, n)]
+    first = dec.greedy_streams(prompts, 0)
+    ref = orc.WhisperOracle(hp, t)
+    ref.set_encoder_output(enc)
+    want = ref.greedy(prompt, 12)
+    assert first[0, 0] == want[0]
+    for k in range(1, n):
+        dec.copy_stream(k, 0)
+    ref.reset()
+    lr = ref.decode(prompt)
+    for s in range(12):
+        got = dec.steps(1)
+        lr = ref.decode([int(want[s])])
+        for k in range(n):
+            assert got[k, 0] == want[s + 1], (s, k)
+            assert _same(dec.logits(k), lr), (s, k)
+    assert dec.pos == len(prompt) + 12
+
+
+def test_stream_copy_errors(kern):
+    from gorelaxor_amd import GrxError
+    from gorelaxor_amd.whisper import WhisperDecoder
+
+    hp = dict(WHISPER_TINY_TEST)
+    dec = WhisperDecoder(hp, whisper_model(hp, seed=1), streams=2)
+    with pytest.raises(GrxError, match="streams 2, 0 of 2"):
+        dec.copy_stream(2, 0)
+    with pytest.raises(GrxError, match="no encoder output"):
+        dec.share_encoder_output(1, 0)
+    dec.set_encoder_output_stream(0, encoder_output(hp))
+    dec.share_encoder_output(1, 0)
+    with pytest.raises(GrxError, match="nothing decoded"):
+        dec.steps(1)
+    with pytest.raises(GrxError, match="nothing decoded"):
+        dec.logits(0)

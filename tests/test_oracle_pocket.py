@@ -212,3 +212,34 @@ def test_flow_head_structure_vs_float64(orc, q8):
         got = o.sample(c, x0)
         want = _f64_flow(hp, fhp, t, c, x0)
         assert np.allclose(got, want, rtol=2e-4, atol=2e-4), np.abs(got - want).max()
+
+
+def _same(a, b):
+    return np.array_equal(np.asarray(a, np.float32).view(np.uint32), np.asarray(b, np.float32).view(np.uint32))
+
+
+def test_oracle_seeded_state_continues_its_run(orc):
+    """tstate.clone (nn.go:128-140): a fresh oracle seeded with the state a
+    run left (its caches' rows and position) runs on to the same bits as the
+    run that made it, for a text prefix and for frames; seeding a state of
+    other values gives other outputs (the seeded rows are what attend
+    reads)."""
+    hp = dict(POCKET_TTS_TINY)
+    t = pocket_model(hp, seed=3)
+    x, lat = pocket_inputs(hp, 5, prefix=9, seed=4)
+    a = orc.PocketOracle(hp, t)
+    a.run(x[:6])
+    k, v = a.state()
+    assert k.shape == (hp["n_layer"], 6, hp["d"])
+    want = a.run(x[6:])
+    wf = [a.step(lat[j]) for j in range(5)]
+    b = orc.PocketOracle(hp, t)
+    b.set_state(k, v)
+    assert b.pos == 6
+    assert _same(b.run(x[6:]), want)
+    for j in range(5):
+        o, e = b.step(lat[j])
+        assert _same(o, wf[j][0]) and _same(e, wf[j][1])
+    c = orc.PocketOracle(hp, t)
+    c.set_state(k * np.float32(0.5), v)
+    assert not _same(c.run(x[6:]), want)
