@@ -243,8 +243,52 @@ def decoder_bench(args) -> dict:
                            "sample": f"the same {steps} decoder steps on the oracle (scalar C, 1 thread), {cpu_s:.2f} s"}
     if not args.no_cpu:
         res["cpu_reference_f16"] = f16_decode_baseline(ref, t, n, steps)
+    res["rules_loop"] = rules_loop_bench(dec, ref, n)
     dec.close()
     return res
+
+
+def rules_loop_bench(dec, ref, n: int) -> dict:
+    """The window loop with whisper's token rules on the device
+    (grx_whisper_rules_loop: process + sample on each step's logits, the
+    loop's timestamp and end rules, the token fed back, no host round trip)
+    after the 4-token prompt, `n` iterations at temperature 0 with the
+    timestamp tokens in the suppress list (so the random-init model's loop
+    runs all n iterations), against the oracle's restatement of the same
+    loop: every token's id, best timestamp and the bits of p and plog."""
+    import oracle
+    from gorelaxor_amd.whisper import Rules, special_tokens
+
+    hp = dec.hp
+    sp = special_tokens(hp["n_vocab"])
+    sup = [1, 2, 7, 8, 9, 10, 220, 1906, 3556, 50254] + list(range(sp["beg"], hp["n_vocab"]))
+    rules = Rules(sp, sup, space=220)
+    times = []
+    for _ in range(3):
+        dec.reset()
+        t0 = time.perf_counter()
+        dec.decode(PROMPT, want_logits=False)
+        got, st = dec.rules_loop(rules, 0, 30000, n)
+        times.append(time.perf_counter() - t0)
+    best = min(times)
+    steps = len(PROMPT) + st["n_tokens"]
+    ref.reset()
+    lr = ref.decode(PROMPT)
+    t0 = time.perf_counter()
+    want, wst = oracle.whisper_window_loop(ref, lr, sp, suppress=sup, space=220, seek=0, seek_end=30000, n_max=n)
+    cpu_s = time.perf_counter() - t0
+
+    def same(g, w):
+        return (g["id"], g["tid"]) == (w["id"], w["tid"]) and all(
+            np.float32(g[k]).view(np.uint32) == np.float32(w[k]).view(np.uint32) for k in ("p", "plog"))
+
+    ok = st == wst and len(got) == len(want) and all(same(g, w) for g, w in zip(got, want))
+    return {"tokens_per_s": round(steps / best, 1), "ms_per_token": round(best / steps * 1e3, 4),
+            "iterations": st["n_tokens"], "parity_bit_exact": bool(ok),
+            "cpu_baseline": {"value": round(st["n_tokens"] / cpu_s, 2), "unit": "tokens/s", "cores": 1,
+                             "kind": "port", **cpu_info(),
+                             "sample": f"the same {st['n_tokens']} iterations of the oracle's loop (decode and "
+                                       f"sampler, scalar C, 1 thread), {cpu_s:.2f} s"}}
 
 
 def f16_decode_baseline(ref, t, n: int, steps: int) -> dict:

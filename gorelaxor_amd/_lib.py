@@ -77,6 +77,7 @@ SIGNATURES = {
     "grx_whisper_share_encoder_output": (i32, [vp, i32, i32]),
     "grx_whisper_steps": (i32, [vp, i32, vp]),
     "grx_whisper_logits": (i32, [vp, i32, vp]),
+    "grx_whisper_rules_loop": (i32, [vp, vp, vp, vp, vp]),
     "grx_whisper_load_ggml": (i32, [vp, C.c_char_p, i32, vp, C.POINTER(vp)]),
     "grx_whisper_sample_logits": (i32, [vp, vp, i32, vp, vp, C.c_float, C.c_float, vp]),
     "grx_whisper_sample": (i32, [vp, i32, vp, vp, C.c_float, C.c_float, vp]),
@@ -210,6 +211,17 @@ class WhisperSeq(C.Structure):
 class WhisperToken(C.Structure):
     """grx_whisper_token."""
     _fields_ = [("id", C.c_int), ("tid", C.c_int), ("p", C.c_float), ("plog", C.c_float), ("force_ts", C.c_int)]
+
+
+class WhisperLoop(C.Structure):
+    """grx_whisper_loop."""
+    _fields_ = [(n, C.c_int) for n in ("seek", "seek_end", "delta_min", "win_frames", "n_max")] + [
+        ("temp", C.c_float), ("r", C.POINTER(C.c_float))]
+
+
+class WhisperLoopResult(C.Structure):
+    """grx_whisper_loop_result."""
+    _fields_ = [(n, C.c_int) for n in ("n_tokens", "done", "failed", "result_len", "seek_delta", "has_ts")]
 
 
 class WhisperHParams(C.Structure):

@@ -71,10 +71,26 @@ struct GrxSampleOut {
     float p, plog;
     int force_ts, n_terms;
 };
+// The decode loop of one window (transcribe.go:207-237) on the device: the
+// sequence the rules read (seq of transcribe.go:100-115) and the loop's
+// counter, read by the sampler before it samples and updated after.
+struct GrxLoopDev {
+    int i;  // iterations done
+    int n_tokens, last, penult;
+    int has_ts, seek_delta, result_len;
+    int done, failed;
+};
+struct GrxLoopArgs {
+    GrxLoopDev *st;          // nullptr: one sample from the arguments as given
+    int *tok_w;              // the decoder's next token
+    grx_whisper_token *rec;  // [n_max] each iteration's token
+    const float *rs;         // [n_max] draws (temperature above 0), or nullptr
+    int seek, seek_end, delta_min, win_frames, n_max;
+};
 #ifdef __cplusplus
-// scratch: 2 x 65536 floats
+// scratch: 2 x 65536 floats; out may be NULL in loop form
 grx_status grx_sample_launch(hipStream_t st, const float *logits, const GrxSampleArgs &a, const int *suppress,
-                             float *scratch, GrxSampleOut *out);
+                             float *scratch, GrxSampleOut *out, const GrxLoopArgs &la = GrxLoopArgs{});
 // the rules and sequence state in kernel form (checks the token ids)
 grx_status grx_sample_args(const grx_whisper_rules *rules, const grx_whisper_seq *seq, int n, float temp, float r,
                            GrxSampleArgs *a);

@@ -234,16 +234,32 @@ __device__ __forceinline__ float log_plus(float s, float m) { return __fadd_rn((
 // thread t at j*1024 + t, so a wave's accesses are contiguous) that only the
 // owning thread reads and writes.  The logits themselves are read once,
 // coalesced, through LDS.
+// In loop form (la.st set) the sequence state comes from the device, the
+// draw from la.rs, and the chosen token goes to the loop's record and the
+// decoder's next token, the state moving on as transcribe.go:211-237 moves
+// it; a sequence done or failed is left alone.
 template <int CH>
 __global__ __launch_bounds__(kThreads) void sample_kernel(const float *__restrict__ logits, GrxSampleArgs a,
                                                           const int *__restrict__ suppress, float *__restrict__ vg,
-                                                          float *__restrict__ g, GrxSampleOut *__restrict__ out) {
+                                                          float *__restrict__ g, GrxSampleOut *__restrict__ out,
+                                                          const GrxLoopArgs la) {
     static_assert(CH % 4 == 0, "entries per thread in groups of four");
     constexpr int ch = CH;
     extern __shared__ __align__(16) unsigned char smem[];
     SampleShared &sh = *reinterpret_cast<SampleShared *>(smem);
     const int t = threadIdx.x, n = a.n, i0 = t * ch;
     const float ninf = -INFINITY;
+    GrxLoopDev lst{};
+    if (la.st != nullptr) {
+        lst = *la.st;  // the same for every thread: the return below is uniform
+        if (lst.done || lst.failed || lst.i >= la.n_max) return;
+        a.initial = lst.n_tokens == 0;
+        a.last = lst.n_tokens > 0 && lst.last >= a.beg;
+        a.penult = lst.n_tokens < 2 || lst.penult >= a.beg;
+        a.has_ts = lst.has_ts;
+        a.seek_delta = lst.seek_delta;
+        if (la.rs != nullptr) a.r = la.rs[lst.i];
+    }
     // the suppress list and the single special tokens into a bitmap
     for (int i = t; i < (n + 31) / 32; i += kThreads) sh.mask[i] = 0u;
     __syncthreads();
@@ -423,20 +439,69 @@ __global__ __launch_bounds__(kThreads) void sample_kernel(const float *__restric
     // the chosen token's probability and log probability, from its owner
     if (id >= i0 && id < i0 + ch) {
         const float x = vt[id - i0];
-        out->p = gt[id - i0];
-        out->plog = x > ninf ? __fsub_rn(x, ls) : ninf;
+        const float p = gt[id - i0], plog = x > ninf ? __fsub_rn(x, ls) : ninf;
+        if (out != nullptr) {
+            out->p = p;
+            out->plog = plog;
+        }
+        if (la.st != nullptr) {
+            la.rec[lst.i].p = p;
+            la.rec[lst.i].plog = plog;
+        }
     }
-    if (t == 0) {
+    if (t == 0 && out != nullptr) {
         out->id = id;
         out->tid = tid;
         out->force_ts = force_ts;
         out->n_terms = terms;
     }
+    if (t == 0 && la.st != nullptr) {
+        // the loop's bookkeeping for this token (transcribe.go:211-237)
+        const int i = lst.i;
+        la.rec[i].id = id;
+        la.rec[i].tid = tid;
+        la.rec[i].force_ts = force_ts;
+        lst.penult = lst.last;
+        lst.last = id;
+        ++lst.n_tokens;
+        bool go = true;
+        if (id > a.beg) {
+            const int nd = 2 * (id - a.beg);
+            if (lst.has_ts && lst.seek_delta > nd && lst.result_len < i) {
+                lst.failed = 1;
+                go = false;
+            } else {
+                lst.seek_delta = nd;
+                lst.result_len = i + 1;
+                lst.has_ts = 1;
+            }
+        }
+        const bool at_end = la.seek + lst.seek_delta + la.delta_min >= la.seek_end;
+        if (go && (id == a.eot || (lst.has_ts && at_end))) {
+            if (lst.result_len == 0) {
+                if (at_end) {
+                    lst.result_len = i + 1;
+                } else {
+                    lst.failed = 1;
+                    go = false;
+                }
+            }
+            if (go) {
+                lst.done = 1;
+                go = false;
+            }
+        }
+        if (go && i == la.n_max - 1 && (lst.result_len == 0 || lst.seek_delta < la.win_frames / 2))
+            lst.failed = 1;  // stuck repeating itself
+        lst.i = i + 1;
+        *la.st = lst;
+        *la.tok_w = id;
+    }
 }
 
 template <int CH>
 grx_status launch_ch(hipStream_t st, const float *logits, const GrxSampleArgs &a, const int *suppress, float *scratch,
-                     GrxSampleOut *out) {
+                     GrxSampleOut *out, const GrxLoopArgs &la) {
     const size_t smem = sizeof(SampleShared);
     static bool attr = false;
     if (!attr) {
@@ -446,7 +511,7 @@ grx_status launch_ch(hipStream_t st, const float *logits, const GrxSampleArgs &a
         attr = true;
     }
     float *vg = scratch, *g = scratch + (size_t)kThreads * CH;
-    sample_kernel<CH><<<1, kThreads, smem, st>>>(logits, a, suppress, vg, g, out);
+    sample_kernel<CH><<<1, kThreads, smem, st>>>(logits, a, suppress, vg, g, out, la);
     GRX_LAUNCHED("sample_kernel");
     return GRX_OK;
 }
@@ -454,13 +519,13 @@ grx_status launch_ch(hipStream_t st, const float *logits, const GrxSampleArgs &a
 }  // namespace
 
 grx_status grx_sample_launch(hipStream_t st, const float *logits, const GrxSampleArgs &a, const int *suppress,
-                             float *scratch, GrxSampleOut *out) {
+                             float *scratch, GrxSampleOut *out, const GrxLoopArgs &la) {
     if (a.n <= 0 || a.n > kMaxLogits) return grx_fail(GRX_ESIZE, "whisper sampler: %d logits (1 .. %d)", a.n, kMaxLogits);
     const int per = (a.n + kThreads - 1) / kThreads;
-    if (per <= 16) return launch_ch<16>(st, logits, a, suppress, scratch, out);
-    if (per <= 32) return launch_ch<32>(st, logits, a, suppress, scratch, out);
-    if (per <= 52) return launch_ch<52>(st, logits, a, suppress, scratch, out);
-    return launch_ch<64>(st, logits, a, suppress, scratch, out);
+    if (per <= 16) return launch_ch<16>(st, logits, a, suppress, scratch, out, la);
+    if (per <= 32) return launch_ch<32>(st, logits, a, suppress, scratch, out, la);
+    if (per <= 52) return launch_ch<52>(st, logits, a, suppress, scratch, out, la);
+    return launch_ch<64>(st, logits, a, suppress, scratch, out, la);
 }
 
 grx_status grx_sample_args(const grx_whisper_rules *rules, const grx_whisper_seq *seq, int n, float temp, float r,

@@ -886,6 +886,13 @@ struct grx_whisper {
     hipGraph_t graph = nullptr;
     hipGraphExec_t exec = nullptr;
     int pos_host = 0;
+    // the decode loop with the token rules (grx_whisper_rules_loop)
+    float *samp_g = nullptr;            // the sampler's terms, 2 x 64k floats
+    int *samp_sup = nullptr;            // the suppress list
+    int samp_sup_cap = 0;
+    GrxLoopDev *loop_st = nullptr;      // the sequence and the loop counter
+    grx_whisper_token *loop_rec = nullptr;  // [n_text_ctx] the tokens sampled
+    float *loop_rs = nullptr;           // [n_text_ctx] draws
 };
 
 namespace {
@@ -1673,5 +1680,85 @@ extern "C" grx_status grx_whisper_logits(grx_whisper *m, int stream_ix, float *o
     GRX_HIP(hipMemcpyAsync(out, m->logits + (size_t)stream_ix * m->hp.n_vocab, (size_t)m->hp.n_vocab * 4,
                            hipMemcpyDeviceToHost, m->ctx->stream));
     GRX_HIP(hipStreamSynchronize(m->ctx->stream));
+    return GRX_OK;
+}
+
+// The loop of one window (whisper/transcribe.go:207-260) for one sequence,
+// on the device: after the prompt (decoded by the caller: its logits are
+// the last step's), each iteration runs process + sample (transcribe.go:
+// 370-494) on the last logits with the sequence state held in device
+// memory, applies the loop's timestamp, end and stuck rules (transcribe.go:
+// 211-237), and feeds the token to the next decode step.  The host enqueues
+// sixteen iterations at a time and reads the state back between them, so
+// the only round trips are those checks; a sequence that is done or failed
+// makes the later samplers of its batch return at once (their decode steps
+// run on unused tokens, and the position moves past them).
+extern "C" grx_status grx_whisper_rules_loop(grx_whisper *m, const grx_whisper_rules *rules,
+                                             const grx_whisper_loop *lp, grx_whisper_token *out,
+                                             grx_whisper_loop_result *res) {
+    grx_status s = check_ready(m, "grx_whisper_rules_loop");
+    if (s != GRX_OK) return s;
+    if (!rules || !lp || !out || !res) return grx_fail(GRX_EINVAL, "grx_whisper_rules_loop: NULL argument");
+    if (m->S != 1) return grx_fail(GRX_ESTATE, "grx_whisper_rules_loop: %d streams (one sequence only)", m->S);
+    if (m->pos_host == 0) return grx_fail(GRX_ESTATE, "grx_whisper_rules_loop: no prompt decoded");
+    if (lp->n_max < 0 || m->pos_host + lp->n_max > m->hp.n_text_ctx)
+        return grx_fail(GRX_ESTATE, "grx_whisper_rules_loop: %d iterations after %d positions exceed the context of %d",
+                        lp->n_max, m->pos_host, m->hp.n_text_ctx);
+    if (lp->temp > 0.f && lp->n_max > 0 && !lp->r)
+        return grx_fail(GRX_EINVAL, "grx_whisper_rules_loop: a temperature above 0 needs n_max draws");
+    const grx_whisper_seq none{};
+    GrxSampleArgs a;
+    if ((s = grx_sample_args(rules, &none, m->hp.n_vocab, lp->temp, 0.f, &a)) != GRX_OK) return s;
+    const int ctxn = m->hp.n_text_ctx;
+    if (!m->samp_g && (s = dev_alloc_t(m, (size_t)2 * 65536, &m->samp_g)) != GRX_OK) return s;
+    if (!m->loop_st && (s = dev_alloc_t(m, 1, &m->loop_st)) != GRX_OK) return s;
+    if (!m->loop_rec && (s = dev_alloc_t(m, (size_t)ctxn, &m->loop_rec)) != GRX_OK) return s;
+    if (!m->loop_rs && (s = dev_alloc_t(m, (size_t)ctxn, &m->loop_rs)) != GRX_OK) return s;
+    if (rules->n_suppress > m->samp_sup_cap) {
+        if ((s = dev_alloc_t(m, (size_t)rules->n_suppress, &m->samp_sup)) != GRX_OK) return s;
+        m->samp_sup_cap = rules->n_suppress;
+    }
+    hipStream_t stream = m->ctx->stream;
+    GRX_HIP(hipSetDevice(m->ctx->device));
+    if (rules->n_suppress > 0)
+        GRX_HIP(hipMemcpyAsync(m->samp_sup, rules->suppress, (size_t)rules->n_suppress * 4, hipMemcpyHostToDevice,
+                               stream));
+    GrxLoopDev st0{};
+    st0.seek_delta = lp->win_frames;  // a fresh seq (transcribe.go:201)
+    GRX_HIP(hipMemcpyAsync(m->loop_st, &st0, sizeof st0, hipMemcpyHostToDevice, stream));
+    if (lp->temp > 0.f && lp->n_max > 0)
+        GRX_HIP(hipMemcpyAsync(m->loop_rs, lp->r, (size_t)lp->n_max * 4, hipMemcpyHostToDevice, stream));
+    GrxLoopArgs la;
+    la.st = m->loop_st;
+    la.tok_w = m->tok;
+    la.rec = m->loop_rec;
+    la.rs = lp->temp > 0.f ? m->loop_rs : nullptr;
+    la.seek = lp->seek;
+    la.seek_end = lp->seek_end;
+    la.delta_min = lp->delta_min;
+    la.win_frames = lp->win_frames;
+    la.n_max = lp->n_max;
+    GrxLoopDev st{};
+    GRX_HIP(hipStreamSynchronize(stream));  // st0 and the draws are read from host memory
+    for (int it = 0; it < lp->n_max;) {
+        const int chunk = std::min(16, lp->n_max - it);
+        for (int k = 0; k < chunk; ++k) {
+            if ((s = grx_sample_launch(stream, m->logits, a, m->samp_sup, m->samp_g, nullptr, la)) != GRX_OK) return s;
+            if ((s = run_step(m)) != GRX_OK) return s;
+            m->pos_host++;
+        }
+        it += chunk;
+        GRX_HIP(hipMemcpyAsync(&st, m->loop_st, sizeof st, hipMemcpyDeviceToHost, stream));
+        GRX_HIP(hipStreamSynchronize(stream));
+        if (st.done || st.failed) break;
+    }
+    if (lp->n_max == 0) st = st0;
+    if (st.i > 0) GRX_HIP(hipMemcpy(out, m->loop_rec, (size_t)st.i * sizeof(grx_whisper_token), hipMemcpyDeviceToHost));
+    res->n_tokens = st.i;
+    res->done = st.done;
+    res->failed = st.failed;
+    res->result_len = st.result_len;
+    res->seek_delta = st.seek_delta;
+    res->has_ts = st.has_ts;
     return GRX_OK;
 }

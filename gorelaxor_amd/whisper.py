@@ -128,6 +128,25 @@ class WhisperDecoder:
                   out.ctypes.data_as(C.c_void_p))
         return out
 
+    def rules_loop(self, rules: "Rules", seek: int, seek_end: int, n_max: int, temp: float = 0.0, r=None,
+                   delta_min: int = 10, win_frames: int = 3000):
+        """One window's decode loop on the device after a decoded prompt
+        (whisper/transcribe.go:207-260): tokens (dicts of id, tid, p, plog,
+        force_ts) and the sequence's state (n_tokens, done, failed,
+        result_len, seek_delta, has_ts)."""
+        draws = None
+        if temp > 0:
+            draws = np.ascontiguousarray(r, np.float32)
+            if draws.size < n_max:
+                raise ValueError(f"{n_max} draws needed, {draws.size} given")
+        lp = _lib.WhisperLoop(seek=seek, seek_end=seek_end, delta_min=delta_min, win_frames=win_frames, n_max=n_max,
+                              temp=temp, r=None if draws is None else draws.ctypes.data_as(C.POINTER(C.c_float)))
+        out = (_lib.WhisperToken * max(n_max, 1))()
+        res = _lib.WhisperLoopResult()
+        _lib.call("grx_whisper_rules_loop", self.handle, C.byref(rules.c), C.byref(lp), out, C.byref(res))
+        toks = [_tok(out[k]) for k in range(res.n_tokens)]
+        return toks, {k: getattr(res, k) for k in ("n_tokens", "done", "failed", "result_len", "seek_delta", "has_ts")}
+
     def copy_stream(self, dst: int, src: int) -> None:
         """kvCache.copyFrom (whisper/decoder.go:22-28): stream dst's cache,
         next token and token record become stream src's."""

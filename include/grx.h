@@ -310,6 +310,36 @@ grx_status grx_whisper_sample_logits(grx_ctx *ctx, const float *logits, int n, c
 grx_status grx_whisper_sample(grx_whisper *m, int stream, const grx_whisper_rules *rules,
                               const grx_whisper_seq *seq, float temp, float r, grx_whisper_token *out);
 
+/* One window's decode loop (whisper/transcribe.go:207-260) on the device
+ * for one sequence: the window's place in the audio (mel frames of 10 ms),
+ * the loop's limits, the temperature and its draws. */
+typedef struct {
+    int seek, seek_end;  /* the window's first frame; the audio's end */
+    int delta_min;       /* deltaMin (transcribe.go:38): frames left that count as the end */
+    int win_frames;      /* frames in a window (3000): a fresh seq's seekDelta */
+    int n_max;           /* iterations at most (nMax = n_text_ctx/2 - 4) */
+    float temp;          /* 0: the most likely token; above 0: draws */
+    const float *r;      /* temp > 0: n_max draws s.rng.Float32(), in order (host) */
+} grx_whisper_loop;
+/* What the loop left of the seq (transcribe.go:100-115). */
+typedef struct {
+    int n_tokens;    /* tokens sampled, in out */
+    int done, failed;
+    int result_len, seek_delta, has_ts;
+} grx_whisper_loop_result;
+/* The loop after a prompt decoded with grx_whisper_decode (its logits are
+ * where the step left them): each iteration applies process + sample
+ * (transcribe.go:370-494) with the sequence state kept on the device, then
+ * the loop's rules - a timestamp moves seekDelta and the result length or
+ * fails the sequence when it goes back; the end token, or a timestamp that
+ * reaches the audio's end, finishes it; the last iteration fails a
+ * sequence stuck repeating itself - and feeds the token to the next decode
+ * step, with no host round trip in between (the state is read back every
+ * sixteen iterations).  out receives each token (n_max of them at most);
+ * *res the sequence's state.  One stream. */
+grx_status grx_whisper_rules_loop(grx_whisper *m, const grx_whisper_rules *rules, const grx_whisper_loop *loop,
+                                  grx_whisper_token *out, grx_whisper_loop_result *res);
+
 /* ---- GGUF model files (internal/gguf/gguf.go) ---- */
 
 /* A GGUF file (versions 2 and 3; tensors F32, F16, BF16, Q8_0) with the

@@ -808,6 +808,52 @@ def whisper_sample(logits, specials: dict, suppress=(), space: int = -1, tokens=
 
 
 
+def whisper_window_loop(ref, logits, specials: dict, suppress=(), space: int = -1, n_audio_ctx: int = 1500,
+                        seek: int = 0, seek_end: int = 3000, n_max: int = 220, temp: float = 0.0, r=None,
+                        delta_min: int = 10, win_frames: int = 3000):
+    """The loop of whisper/transcribe.go:207-260 for one seq after its prompt:
+    `ref` (a WhisperOracle) has decoded the prompt and `logits` are its last.
+    Each iteration samples with the rules (whisper_sample: process + sample,
+    transcribe.go:370-494), then applies transcribe.go:211-237 - a timestamp
+    above beg sets seekDelta = 2 (id - beg) and the result length, or fails
+    the seq when it goes back; eot, or a timestamp reaching the audio's end,
+    finishes it (failing it when no result was kept); the last iteration
+    fails a seq stuck repeating itself - and decodes the token while the seq
+    is active.  Returns (tokens, state)."""
+    beg, eot = specials["beg"], specials["eot"]
+    toks, ids = [], []
+    st = dict(done=0, failed=0, result_len=0, seek_delta=win_frames, has_ts=0)
+    lg = logits
+    for i in range(n_max):
+        t = whisper_sample(lg, specials, suppress=suppress, space=space, tokens=ids, has_ts=bool(st["has_ts"]),
+                           seek_delta=st["seek_delta"], temp=temp, r=float(r[i]) if temp > 0 else 0.0,
+                           n_audio_ctx=n_audio_ctx)
+        toks.append(t)
+        ids.append(t["id"])
+        if t["id"] > beg:
+            nd = 2 * (t["id"] - beg)
+            if st["has_ts"] and st["seek_delta"] > nd and st["result_len"] < i:
+                st["failed"] = 1
+                break
+            st["seek_delta"], st["result_len"], st["has_ts"] = nd, i + 1, 1
+        at_end = seek + st["seek_delta"] + delta_min >= seek_end
+        if t["id"] == eot or (st["has_ts"] and at_end):
+            if st["result_len"] == 0:
+                if at_end:
+                    st["result_len"] = i + 1
+                else:
+                    st["failed"] = 1
+                    break
+            st["done"] = 1
+            break
+        if i == n_max - 1 and (st["result_len"] == 0 or st["seek_delta"] < win_frames // 2):
+            st["failed"] = 1
+            break
+        lg = ref.decode([t["id"]])
+    st["n_tokens"] = len(toks)
+    return toks, st
+
+
 # ---- pocket-TTS flow head (pockettts/lm.go:27-160) ----
 
 class PocketFlowOracle:
