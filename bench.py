@@ -11,8 +11,11 @@ launch over all 512 matrices.  Inputs are resident in HBM before timing.
 
 Prints one JSON line.  `value` is the whole-ring GEMV throughput in GB/s of
 algorithmic bytes (34 B per 32 weights, plus x and y per matrix); `roofline`
-is the GEMV kernel alone against 8 TB/s; `cpu_baseline` is the CPU oracle
-(a scalar C restatement of the reference's int8 route) on a bounded sample.
+is the GEMV kernel alone against 8 TB/s; `cpu_baseline` is the reference's
+int8 route restated with VNNI intrinsics (oracle/grx_vnni.cc, bit-equal to
+the oracle) on the same ring at one thread and at the host's threads.  Each
+model loop's nested `cpu_baseline` runs the oracle's graph with its int8
+products on that same kernel, at one thread and at the host's threads.
 """
 from __future__ import annotations
 
@@ -117,6 +120,31 @@ def cpu_threads() -> int:
         return max(1, int(os.environ.get("OMP_NUM_THREADS", "")))
     except ValueError:
         return os.cpu_count() or 1
+
+
+def vnni_baseline(run, units: float, unit: str, sample: str) -> dict:
+    """A model loop's CPU baseline: `run()` (a fresh oracle graph doing
+    `units` of work; it returns the seconds of its timed part) with every
+    int8 product on the reference's kernel restated with VNNI intrinsics
+    (oracle/grx_vnni.cc: matmulQ8Int, quantU8avx, the 6x16 vpdpbusd tile,
+    the reference's task split), at one thread and at the host's threads,
+    each after an untimed run that packs every weight's panels (the
+    reference's Pack on first use).  value: the all-thread rate.  The rest
+    of the graph (attention, LayerNorm, the float routes) is the oracle's
+    scalar C on one thread, where the reference would use its AVX2 kernels
+    and fan some of it out, so the rate is a floor of the reference's."""
+    import oracle
+
+    th = cpu_threads()
+    rates = {}
+    for label, threads in (("one_thread", 1), ("all_threads", th)):
+        with oracle.vnni_products(threads):
+            run()
+            rates[label] = units / run()
+    return {"value": round(rates["all_threads"], 4), "unit": unit, "cores": th, "kind": "port", **cpu_info(),
+            "one_thread": round(rates["one_thread"], 4), "threads": th,
+            "sample": f"{sample}; int8 products on oracle/grx_vnni.cc (the reference's matmulQ8Int with VNNI) at "
+                      f"1 and {th} threads, the rest scalar C on one thread"}
 
 
 def cpu_baseline(w8: np.ndarray, x: np.ndarray, seconds: float) -> dict:
@@ -238,9 +266,16 @@ def decoder_bench(args) -> dict:
     want = ref.greedy(PROMPT, n)
     cpu_s = time.perf_counter() - t0
     res["parity_tokens_identical"] = bool(np.array_equal(want, toks))
-    res["cpu_baseline"] = {"value": round(steps / cpu_s, 2), "unit": "tokens/s", "cores": 1, "kind": "port",
-                           **cpu_info(),
-                           "sample": f"the same {steps} decoder steps on the oracle (scalar C, 1 thread), {cpu_s:.2f} s"}
+
+    def run_dec():
+        r = oracle.WhisperOracle(hp, t)
+        r.set_encoder_output(enc)
+        t0 = time.perf_counter()
+        r.greedy(PROMPT, n)
+        return time.perf_counter() - t0
+
+    res["cpu_baseline"] = vnni_baseline(run_dec, steps, "tokens/s", f"the same {steps} decoder steps on the oracle")
+    res["cpu_baseline"]["scalar_one_thread"] = round(steps / cpu_s, 2)
     if not args.no_cpu:
         res["cpu_reference_f16"] = f16_decode_baseline(ref, t, n, steps)
     res["rules_loop"] = rules_loop_bench(dec, ref, n)
@@ -365,10 +400,19 @@ def streams_bench(args) -> dict:
     want = ref.greedy(PROMPT, n)
     cpu_s = time.perf_counter() - t0
     res["parity_tokens_identical"] = bool(np.array_equal(want, toks[0])) and same
-    res["cpu_baseline"] = {"value": round(steps / cpu_s, 2), "unit": "tokens/s", "cores": 1, "kind": "port",
-                           **cpu_info(),
-                           "sample": f"stream 0's {steps} decoder steps on the oracle (scalar C, 1 thread), "
-                                     f"{cpu_s:.1f} s; the reference decodes streams one after another"}
+    ns = 32  # decoder steps timed (bounded sample)
+
+    def run_streams():
+        r = oracle.WhisperOracle(hp, t)
+        r.set_encoder_output(encs[0])
+        t0 = time.perf_counter()
+        r.greedy(PROMPT, ns)
+        return time.perf_counter() - t0
+
+    res["cpu_baseline"] = vnni_baseline(run_streams, len(PROMPT) + ns, "tokens/s",
+                                        f"stream 0's first {len(PROMPT) + ns} decoder steps on the oracle (the "
+                                        f"reference decodes streams one after another)")
+    res["cpu_baseline"]["scalar_one_thread"] = round(steps / cpu_s, 2)
     return res
 
 
@@ -425,10 +469,18 @@ def lm_bench(args) -> dict:
         ok = ok and bool(np.array_equal(wo.view(np.uint32), outs[k].view(np.uint32))) and bool(np.float32(we) == eos[k])
     cpu_s = time.perf_counter() - t1
     res["parity_bit_exact"] = ok
-    res["cpu_baseline"] = {"value": round(n / cpu_s, 2), "unit": "frames/s", "cores": 1, "kind": "port",
-                           **cpu_info(),
-                           "sample": f"the same {n} frames on the oracle (scalar C, 1 thread), {cpu_s:.2f} s; "
-                                     f"prefix {1e3 * (t1 - t0):.0f} ms"}
+    nf = 40  # frames timed (bounded sample)
+
+    def run_lm():
+        r = oracle.PocketOracle(hp, t)
+        r.run(x)
+        t0 = time.perf_counter()
+        for k in range(nf):
+            r.step(lat[k])
+        return time.perf_counter() - t0
+
+    res["cpu_baseline"] = vnni_baseline(run_lm, nf, "frames/s", f"the first {nf} frames after the 64-row prefix on the oracle")
+    res["cpu_baseline"]["scalar_one_thread"] = round(n / cpu_s, 2)
     lm.close()
     res["speak"] = speak_bench(args, hp, t, x)
     res["mimi"] = mimi_bench(args)
@@ -478,11 +530,24 @@ def speak_bench(args, hp, t, x) -> dict:
         latent = flow.sample(h, noise[k])
         ok = ok and bool(np.array_equal(latent.view(np.uint32), lats[k].view(np.uint32))) and \
             bool(np.float32(e) == eos[k])
+    scalar = n / (time.perf_counter() - t0)
     res["parity_bit_exact"] = ok
-    res["cpu_baseline"] = {"value": round(n / (time.perf_counter() - t0), 2), "unit": "frames/s", "cores": 1,
-                           "kind": "port", **cpu_info(),
-                           "sample": f"the same {n} frames (transformer step and flow head) on the "
-                                                     "oracle (C kernels, 1 thread, Python glue)"}
+    nf = 30
+
+    def run_speak():
+        r = oracle.PocketOracle(hp, t)
+        r.run(x)
+        lt = None
+        t0 = time.perf_counter()
+        for k in range(nf):
+            h, _ = r.step(lt)
+            lt = flow.sample(h, noise[k])
+        return time.perf_counter() - t0
+
+    res["cpu_baseline"] = vnni_baseline(run_speak, nf, "frames/s",
+                                        f"the first {nf} frames (transformer step and flow head, Python glue) on "
+                                        f"the oracle")
+    res["cpu_baseline"]["scalar_one_thread"] = round(scalar, 2)
     return res
 
 
@@ -525,8 +590,16 @@ def mimi_bench(args) -> dict:
     want = np.concatenate([ref.decode(lat[k:k + 1]) for k in range(8)])
     cpu_s = time.perf_counter() - t0
     res["parity_first_8_bit_exact"] = bool(np.array_equal(want.view(np.uint32), first.view(np.uint32)))
-    res["cpu_baseline"] = {"value": round(8 / cpu_s, 2), "unit": "latents/s", "cores": 1, "kind": "port",
-                           **cpu_info(), "sample": f"the first 8 latents on the oracle (C, 1 thread), {cpu_s:.2f} s"}
+
+    def run_mimi():
+        r = oracle.MimiOracle(hp, t)
+        t0 = time.perf_counter()
+        for k in range(8):
+            r.decode(lat[k:k + 1])
+        return time.perf_counter() - t0
+
+    res["cpu_baseline"] = vnni_baseline(run_mimi, 8, "latents/s", "the first 8 latents on the oracle, one per call")
+    res["cpu_baseline"]["scalar_one_thread"] = round(8 / cpu_s, 2)
     return res
 
 
@@ -623,10 +696,15 @@ def conformer_bench(args) -> dict:
     cpu_s = time.perf_counter() - t0
     res["parity_bit_exact"] = bool(np.array_equal(out1.view(np.uint32), want.view(np.uint32)))
     res["batch16"]["parity_each_equals_its_batch1_encode"] = same16
-    res["cpu_baseline"] = {"value": round(1.0 / cpu_s, 4), "unit": "utterances/s", "cores": 1, "kind": "port",
-                           **cpu_info(),
-                           "sample": f"one 10 s utterance, all 24 layers, on the oracle (scalar C, 1 thread), "
-                                     f"{cpu_s:.1f} s"}
+    def run_conf():
+        o = oracle.ConformerOracle(hp, t)
+        t0 = time.perf_counter()
+        o.encode(mel[0], valid)
+        return time.perf_counter() - t0
+
+    res["cpu_baseline"] = vnni_baseline(run_conf, 1.0, "utterances/s",
+                                        "one 10 s utterance, all 24 layers, on the oracle")
+    res["cpu_baseline"]["scalar_one_thread"] = round(1.0 / cpu_s, 4)
     res["tdt_decode"] = tdt_bench(args, want[:L])
     return res
 
@@ -712,10 +790,19 @@ def conformer_stream_bench(args) -> dict:
                     got = first_rows[j][:len(want)]
                     same = same and bool(np.array_equal(got.view(np.uint32), want.view(np.uint32)))
                 r["parity_first_chunks_bit_exact"] = same
-                r["cpu_baseline"] = {"value": round(1.0 / cpu[1], 3), "unit": "chunk steps/s", "cores": 1,
-                                     "kind": "port", **cpu_info(),
-                                     "sample": f"the second chunk step of one stream on the oracle (scalar C, "
-                                               f"1 thread), {cpu[1] * 1e3:.1f} ms"}
+
+                def run_chunk(right=right, g=g):
+                    o2 = oracle.ConformerOracle(hp, t).stream(right, g["left"], g["drop"])
+                    ch0, ln0, _ = chunks[0][0]
+                    o2.step(ch0, ln0)
+                    ch1, ln1, _ = chunks[0][1]
+                    t0 = time.perf_counter()
+                    o2.step(ch1, ln1)
+                    return time.perf_counter() - t0
+
+                r["cpu_baseline"] = vnni_baseline(run_chunk, 1.0, "chunk steps/s",
+                                                  "the second chunk step of one stream on the oracle")
+                r["cpu_baseline"]["scalar_one_thread"] = round(1.0 / cpu[1], 3)
         res[f"right{right}"] = r
     enc.close()
     return res
@@ -754,11 +841,17 @@ def tdt_bench(args, enc: np.ndarray) -> dict:
     same = len(got) == len(want) and all(
         (g.ID, g.Frame, g.Duration) == w[:3] and np.float32(g.P).tobytes() == np.float32(w[3]).tobytes()
         for g, w in zip(got, want))
+
+    def run_tdt():
+        r = oracle.RnntOracle(hp, t)
+        t0 = time.perf_counter()
+        r.decode(enc)
+        return time.perf_counter() - t0
+
     return {"frames": T, "tokens": len(got), "ms_per_decode": round(best * 1e3, 3),
             "decodes_per_s": round(1.0 / best, 1), "parity_bit_exact": bool(same),
-            "cpu_baseline": {"value": round(1.0 / cpu_s, 2), "unit": "decodes/s", "cores": 1, "kind": "port",
-                             **cpu_info(),
-                             "sample": f"the same decode on the oracle (scalar C, 1 thread), {cpu_s * 1e3:.1f} ms"}}
+            "cpu_baseline": {**vnni_baseline(run_tdt, 1.0, "decodes/s", "the same decode on the oracle"),
+                             "scalar_one_thread": round(1.0 / cpu_s, 2)}}
 
 
 def profile_leg(args) -> dict:

@@ -224,12 +224,24 @@ static void matmul_q8_int_core(float *c, int ldc, const int8_t *qa, const float 
     }
 }
 
+/* Another implementation of the EVEX-order product for the graphs below
+ * (orc_set_q8_product): the benchmark's CPU baselines route every product
+ * of a graph through the VNNI restatement of the reference's kernel
+ * (oracle/grx_vnni.cc, bit-equal to this one) at many threads.  NULL: this
+ * file's scalar form. */
+static orc_q8_product_fn g_q8_product = NULL;
+void orc_set_q8_product(orc_q8_product_fn fn) { g_q8_product = fn; }
+
 /* q8int.go:148-223 (matmulQ8Int): quantize each row of a (quantU8), set C
  * to the bias (or zero), then accumulate block by block.  Every output is
  * owned by one task, so its value does not depend on the thread split. */
 void orc_matmul_q8_int(float *c, int ldc, const float *a, int lda, int m, const uint8_t *wq,
                        int n, int k, const float *bias, int evex) {
     if (m == 0 || n == 0) return; /* kern.go:186-188 */
+    if (g_q8_product != NULL && evex) {
+        g_q8_product(c, ldc, a, lda, m, wq, n, k, bias);
+        return;
+    }
     int nb = k / ORC_QK;
     int8_t *qa = (int8_t *)malloc((size_t)m * k + 1);
     float *sa = (float *)malloc(((size_t)m * nb + 1) * sizeof(float));

@@ -44,6 +44,9 @@ void orc_quant_act_i8(int8_t *dst, float *sc, const float *x, int nb);
 
 /* ---- int8 products ---- */
 void orc_block_dots(int32_t *s, const int8_t *qa, int m, const uint8_t *wq, int n, int k);
+typedef void (*orc_q8_product_fn)(float *c, int ldc, const float *a, int lda, int m, const uint8_t *wq, int n,
+                                  int k, const float *bias);
+void orc_set_q8_product(orc_q8_product_fn fn);
 void orc_matmul_q8_int(float *c, int ldc, const float *a, int lda, int m,
                        const uint8_t *wq, int n, int k, const float *bias, int evex);
 void orc_matmul_q8_int_prequant(float *c, int ldc, const int8_t *qa, const float *sa, int m,

@@ -154,7 +154,11 @@ GRX_Q8TILE(q8tile_vex, "avx2,fma,avxvnni", _mm256_dpbusd_avx_epi32)
 // ---------------------------------------------------------------- threads
 
 // A persistent pool: run(n, fn) calls fn(0..n-1), task indices taken from
-// an atomic counter by the calling thread and the pool's threads.
+// an atomic counter by the calling thread and the pool's threads.  Idle
+// threads spin a while (~50 us) before they sleep on the condition
+// variable, and the caller spins for the last tasks before it waits: a
+// woken sleeper costs several microseconds, while the reference's
+// goroutines are handed their tasks by spinning schedulers.
 struct Pool {
     std::vector<std::thread> th;
     std::mutex mu;
@@ -163,6 +167,10 @@ struct Pool {
     std::atomic<int> next{0};
     int n = 0, gen = 0, busy = 0;
     bool stop = false;
+    // copies of gen and busy read without the lock, only to end a spin
+    std::atomic<int> gen_a{0}, busy_a{0};
+    std::atomic<bool> stop_a{false};
+    static constexpr int kSpin = 20000;
 
     explicit Pool(int threads) {
         for (int i = 1; i < threads; ++i) th.emplace_back([this] { loop(); });
@@ -171,6 +179,7 @@ struct Pool {
         {
             std::lock_guard<std::mutex> lk(mu);
             stop = true;
+            stop_a.store(true);
         }
         cv.notify_all();
         for (auto &t : th) t.join();
@@ -185,17 +194,21 @@ struct Pool {
     void loop() {
         int seen = 0;
         for (;;) {
+            for (int i = 0; i < kSpin && gen_a.load(std::memory_order_acquire) == seen && !stop_a.load(); ++i)
+                _mm_pause();
             {
                 std::unique_lock<std::mutex> lk(mu);
                 cv.wait(lk, [&] { return stop || gen != seen; });
                 if (stop) return;
                 seen = gen;
                 ++busy;
+                busy_a.store(busy);
             }
             drain();
             {
                 std::lock_guard<std::mutex> lk(mu);
-                if (--busy == 0) done_cv.notify_all();
+                busy_a.store(--busy);
+                if (busy == 0) done_cv.notify_all();
             }
         }
     }
@@ -210,9 +223,11 @@ struct Pool {
             n = count;
             next.store(0);
             ++gen;
+            gen_a.store(gen, std::memory_order_release);
         }
         cv.notify_all();
         drain();
+        for (int i = 0; i < kSpin && busy_a.load() != 0; ++i) _mm_pause();
         std::unique_lock<std::mutex> lk(mu);
         done_cv.wait(lk, [&] { return busy == 0 && next.load() >= n; });
     }
@@ -621,6 +636,64 @@ int vnni_matmul(float *c, int ldc, const float *a, int lda, int m, const uint8_t
     else
         pool(tt).run(ntasks, task);
     return 0;
+}
+
+// kern.MatMul on the int8 route for the oracle's graphs (the hook
+// orc_set_q8_product installs): matmulQ8Int over panels packed once per
+// weight on first use, as Weight.Pack does lazily (q8int.go:81-84), at
+// vnni_set_threads threads.  A weight is known by its ggml bytes' address,
+// shape and a sample of its bytes (vnni_forget drops every packed weight).
+namespace {
+struct Packed {
+    int n = 0, k = 0;
+    uint64_t tag = 0;
+    std::vector<uint8_t> panels;
+};
+std::mutex g_pack_mu;
+std::vector<std::pair<const uint8_t *, Packed>> g_packed;
+std::atomic<int> g_product_threads{1};
+uint64_t bytes_tag(const uint8_t *q, size_t nbytes) {
+    uint64_t h = 1469598103934665603ull;
+    const size_t step = nbytes / 61 + 1;
+    for (size_t i = 0; i < nbytes; i += step) h = (h ^ q[i]) * 1099511628211ull;
+    return h ^ q[nbytes - 1];
+}
+}  // namespace
+
+void vnni_set_threads(int threads) { g_product_threads.store(threads < 1 ? 1 : threads); }
+
+void vnni_forget(void) {
+    std::lock_guard<std::mutex> lk(g_pack_mu);
+    g_packed.clear();
+}
+
+void vnni_q8_product(float *c, int ldc, const float *a, int lda, int m, const uint8_t *wq, int n, int k,
+                     const float *bias) {
+    if (m == 0 || n == 0) return;
+    const size_t nbytes = (size_t)n * (k / kQK) * kQ8Bytes;
+    const uint64_t tag = bytes_tag(wq, nbytes);
+    const uint8_t *panels = nullptr;
+    {
+        std::lock_guard<std::mutex> lk(g_pack_mu);
+        for (auto &e : g_packed)
+            if (e.first == wq && e.second.n == n && e.second.k == k && e.second.tag == tag) panels = e.second.panels.data();
+        if (panels == nullptr) {
+            Packed p;
+            p.n = n;
+            p.k = k;
+            p.tag = tag;
+            p.panels.resize(vnni_panel_bytes(n, k));
+            vnni_pack(wq, n, k, p.panels.data());
+            g_packed.emplace_back(wq, std::move(p));
+            panels = g_packed.back().second.panels.data();
+        }
+    }
+    const int mp = (m + kTileRows - 1) / kTileRows * kTileRows;
+    thread_local std::vector<uint8_t> qa;
+    thread_local std::vector<float> sc;
+    if (qa.size() < (size_t)mp * k) qa.resize((size_t)mp * k);
+    if (sc.size() < (size_t)mp * (k / kQK)) sc.resize((size_t)mp * (k / kQK));
+    vnni_matmul(c, ldc, a, lda, m, panels, n, k, bias, g_product_threads.load(), qa.data(), sc.data());
 }
 
 // The benchmark's CPU loop: reps passes over `count` matrices (panels

@@ -8,6 +8,7 @@ github.com/xattribution/gorelaxor) the C restatement follows.
 """
 from __future__ import annotations
 
+import contextlib
 import ctypes as C
 import math
 import os
@@ -51,6 +52,8 @@ _i32p = np.ctypeslib.ndpointer(np.int32, flags="C_CONTIGUOUS")
 
 
 def _declare(L):
+    L.orc_set_q8_product.argtypes = [C.c_void_p]
+    L.orc_set_q8_product.restype = None
     L.orc_f16_to_f32.argtypes = [C.c_uint16]
     L.orc_f16_to_f32.restype = C.c_float
     L.orc_f32_to_f16.argtypes = [C.c_float]
@@ -1056,8 +1059,34 @@ def vnni_lib() -> C.CDLL:
         L.vnni_ring.argtypes = [C.c_void_p, C.c_void_p, C.c_void_p, C.c_size_t, C.c_int, C.c_int, C.c_int, C.c_int,
                                 C.c_int, C.c_void_p, C.c_void_p]
         L.vnni_ring.restype = C.c_int
+        L.vnni_set_threads.argtypes = [C.c_int]
+        L.vnni_set_threads.restype = None
+        L.vnni_forget.argtypes = []
+        L.vnni_forget.restype = None
         _vnni = L
     return _vnni
+
+
+@contextlib.contextmanager
+def vnni_products(threads: int):
+    """Within the block, every int8 product of the oracle's graphs (whisper,
+    pocket, conformer, Mimi, RNN-T: orc_matmul_q8_int, EVEX order) runs on
+    the VNNI restatement of the reference's matmulQ8Int (grx_vnni.cc,
+    vnni_q8_product: panels packed once per weight, the reference's task
+    split over `threads` threads) - the same bits, the reference's CPU
+    speed for the products.  The rest of each graph stays scalar C on one
+    thread.  Timing only (the benchmark's CPU baselines)."""
+    V, L = vnni_lib(), lib()
+    if V.vnni_kind() == 0:
+        raise RuntimeError("this processor has neither AVX512-VNNI nor AVX-VNNI")
+    V.vnni_set_threads(int(threads))
+    V.vnni_forget()
+    L.orc_set_q8_product(C.cast(V.vnni_q8_product, C.c_void_p))
+    try:
+        yield
+    finally:
+        L.orc_set_q8_product(None)
+        V.vnni_forget()
 
 
 def vnni_kind() -> int:

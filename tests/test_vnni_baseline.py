@@ -58,3 +58,50 @@ def test_ring_loop(vnni):
     for i in range(count):
         want = vnni.matmul_q8_int(x, w8[i * src:(i + 1) * src], n, k)[0]
         assert np.array_equal(_bits(y[i * n:(i + 1) * n]), _bits(want)), i
+
+
+def test_graphs_on_vnni_products_give_the_same_bits(orc):
+    """The CPU baselines run the oracle's graphs with every int8 product on
+    the VNNI restatement (oracle.vnni_products, 1 and 4 threads): the
+    outputs are the scalar oracle's bit for bit (whisper steps, the pocket
+    prefix and frames, a conformer encode)."""
+    import pytest
+
+    if orc.vnni_kind() == 0:
+        pytest.skip("no VNNI on this processor")
+    from gorelaxor_amd.synth import (CONFORMER_TINY, POCKET_TTS_TINY, WHISPER_TINY_TEST, conformer_model,
+                                     encoder_output, pocket_inputs, pocket_model, whisper_model)
+
+    def same(a, b):
+        return np.array_equal(np.asarray(a, np.float32).view(np.uint32), np.asarray(b, np.float32).view(np.uint32))
+
+    hp = dict(WHISPER_TINY_TEST)
+    t = whisper_model(hp, seed=4)
+    enc = encoder_output(hp, seed=5)
+
+    def whisper_run():
+        ref = orc.WhisperOracle(hp, t)
+        ref.set_encoder_output(enc)
+        return [ref.decode([1, 2, 3])] + [ref.decode([k]) for k in (7, 8, 9)]
+
+    php = dict(POCKET_TTS_TINY)
+    pt = pocket_model(php, seed=6)
+    x, lat = pocket_inputs(php, 3, prefix=9, seed=7)
+
+    def pocket_run():
+        ref = orc.PocketOracle(php, pt)
+        return [ref.run(x)] + [ref.step(lat[k])[0] for k in range(3)]
+
+    chp = dict(CONFORMER_TINY)
+    ct = conformer_model(chp, seed=8)
+    mel = np.random.default_rng(9).standard_normal((1, 48, chp["n_mels"])).astype(np.float32)
+
+    def conformer_run():
+        return [orc.ConformerOracle(chp, ct).encode(mel, 48)[0]]
+
+    for run in (whisper_run, pocket_run, conformer_run):
+        want = run()
+        for threads in (1, 4):
+            with orc.vnni_products(threads):
+                got = run()
+            assert all(same(g, w) for g, w in zip(got, want)), (run.__name__, threads)
