@@ -1187,6 +1187,13 @@ extern "C" grx_status grx_matmul_q8_dev_noalloc(grx_ctx *ctx, float *dst, int ld
     if (s != GRX_OK) return s;
     if (m == 0 || w->rows == 0) return GRX_OK;
     const int K = w->cols, nb = w->nb;
+    // few rows: each GEMV launch rounds its rows in its own prologue, so
+    // the scratch is not touched (one launch per group of rows, as
+    // grx_matmul_q8_dev takes them)
+    if (nb > 0 && m < grx_gemm_min_m() && (size_t)K <= kStageMax) {
+        GRX_HIP(hipSetDevice(ctx->device));
+        return gemv_rows_quant(ctx->stream, dst, ldc, x, lda, m, w, bias);
+    }
     const size_t qbytes = ((size_t)m * K + 255) & ~(size_t)255;
     const size_t need = qbytes + (size_t)m * nb * 4;
     if (need > kNoAllocScratch)

@@ -107,7 +107,9 @@ grx_status grx_matmul_q8_dev(grx_ctx *ctx, float *dst, int ldc, const float *x, 
 /* grx_matmul_q8_dev without any allocation.  No counterpart in the
  * reference: it is for callers that cannot allocate device memory (code
  * under HIP graph capture, tight serving loops, harnesses that forbid
- * hipMalloc).  The rounded activations go to a fixed device array of the
+ * hipMalloc).  Fewer rows than the matrix-core threshold (16) are rounded
+ * inside the product's own launches and need no memory beyond x and dst;
+ * for more rows the rounded activations go to a fixed device array of the
  * library (4 MiB per GPU, held until the process ends) instead of the
  * context's scratch: m * cols + m * cols/32 * 4 bytes (plus alignment to
  * 256) must fit, else GRX_ESIZE.  Every call on a GPU shares that array:

@@ -155,7 +155,7 @@ GRX_Q8TILE(q8tile_vex, "avx2,fma,avxvnni", _mm256_dpbusd_avx_epi32)
 
 // A persistent pool: run(n, fn) calls fn(0..n-1), task indices taken from
 // an atomic counter by the calling thread and the pool's threads.  Idle
-// threads spin a while (~50 us) before they sleep on the condition
+// threads spin a few microseconds before they sleep on the condition
 // variable, and the caller spins for the last tasks before it waits: a
 // woken sleeper costs several microseconds, while the reference's
 // goroutines are handed their tasks by spinning schedulers.
@@ -170,7 +170,7 @@ struct Pool {
     // copies of gen and busy read without the lock, only to end a spin
     std::atomic<int> gen_a{0}, busy_a{0};
     std::atomic<bool> stop_a{false};
-    static constexpr int kSpin = 20000;
+    static constexpr int kSpin = 2000;
 
     explicit Pool(int threads) {
         for (int i = 1; i < threads; ++i) th.emplace_back([this] { loop(); });

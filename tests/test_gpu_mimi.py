@@ -38,10 +38,19 @@ def test_tiny_streamed_bit_exact(kern, orc, q8):
     dec.close()
 
 
+@pytest.mark.parametrize("mx", [-1, 0])
 @pytest.mark.parametrize("per_call", [2, 3, 4])
-def test_tiny_several_latents_per_call(kern, orc, per_call):
+def test_tiny_several_latents_per_call(kern, orc, per_call, mx):
     """n latents per call (T = 4n rows: the MatMulF32 routes past 16 rows)
-    and a reset in between: the oracle's bits."""
+    and a reset in between: the oracle's bits.  GEMV_MX=0 sends the groups
+    of 8 rows to the dot-product several-row kernel instead of the
+    matrix-core one (its rounding prologue, the in-place residual and the
+    groups' offsets in one launch)."""
+    with kern.tuned(GEMV_MX=mx):
+        _several_per_call(orc, per_call)
+
+
+def _several_per_call(orc, per_call):
     hp = dict(MIMI_TINY)
     t = mimi_model(hp, seed=19, q8=True)
     ref, dec = _pair(orc, hp, t)
@@ -56,9 +65,16 @@ def test_tiny_several_latents_per_call(kern, orc, per_call):
     dec.close()
 
 
-def test_real_shape_bit_exact(kern, orc):
+@pytest.mark.parametrize("mx", [-1, 0])
+def test_real_shape_bit_exact(kern, orc, mx):
     """The english_2026-09 shape (d 512, 8 heads, SEANet 6/5/4, Q8_0 and
-    float32 as the converter types them): 6 latents one per call."""
+    float32 as the converter types them): 6 latents one per call; also with
+    the several-row products on the dot-product kernel (GEMV_MX=0)."""
+    with kern.tuned(GEMV_MX=mx):
+        _real_shape(orc)
+
+
+def _real_shape(orc):
     hp = dict(MIMI)
     t = mimi_model(hp, seed=17)
     ref, dec = _pair(orc, hp, t, max_latents=1)

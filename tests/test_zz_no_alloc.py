@@ -2,11 +2,14 @@
 fixed per-GPU scratch holds the rounded activations) against
 grx_matmul_q8_dev, bit for bit, through the C ABI: two calls in a row, the
 second smaller (so the scratch keeps the first call's bytes past the
-second's), a call near the scratch's limit, and one past it."""
+second's), a call near the scratch's limit, and one past it.  Every
+noalloc call runs with the library's allocation hook armed to fail the
+next allocation (grx_debug_fail_alloc_after(0)): the call must succeed and
+leave the hook armed, i.e. allocate nothing."""
 import numpy as np
 import pytest
 
-from gorelaxor_amd import GrxError
+from gorelaxor_amd import GrxError, _lib
 from gorelaxor_amd.synth import q8_weight
 
 pytestmark = pytest.mark.gpu
@@ -22,8 +25,15 @@ def _both(kern, rng, m, n, k, bias, lda_pad=8, ldc_pad=3):
     d1 = hiprt.DeviceBuffer.from_array(np.full((m, n + ldc_pad), 7.0, np.float32))
     d2 = hiprt.DeviceBuffer.from_array(np.full((m, n + ldc_pad), 7.0, np.float32))
     kern.matmul_dev(d1, dx, m, w, b, ldc=n + ldc_pad, lda=k + lda_pad)
-    kern.matmul_dev_noalloc(d2, dx, m, w, b, ldc=n + ldc_pad, lda=k + lda_pad)
     kern.default_context().sync()
+    lib = _lib.lib()
+    lib.grx_debug_fail_alloc_after(0)  # the next allocation fails
+    try:
+        kern.matmul_dev_noalloc(d2, dx, m, w, b, ldc=n + ldc_pad, lda=k + lda_pad)
+        kern.default_context().sync()
+        assert lib.grx_debug_alloc_countdown() == 0, "the allocation-free product allocated"
+    finally:
+        lib.grx_debug_fail_alloc_after(-1)
     y1 = d1.download(np.float32, (m, n + ldc_pad))
     y2 = d2.download(np.float32, (m, n + ldc_pad))
     return y1, y2
