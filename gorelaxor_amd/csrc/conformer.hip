@@ -955,6 +955,58 @@ __global__ __launch_bounds__(256) void conf_dwconv_win_kernel(const float *__res
     }
 }
 
+// The same depthwise convolution, folded batch norm, SiLU and rounding with
+// one wave per frame and 64 channels (lane = channel): the K gated values
+// its taps read and the K taps are loaded at once through buffer resources
+// (rows clamped into the buffers; a clamped row's value is never used), then
+// one chain over the taps in range.  The range is the same for the whole
+// wave, so a skipped tap costs no vector work.  grid (T, D/64, B), one wave
+// per workgroup.
+constexpr int kDwLaneK = 32;  // the largest kernel the registers hold
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t dw_rsrc(const float *p, uint32_t n) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(p), (short)0, (int)n, 0x00020000);
+}
+template <bool RING>
+__global__ __launch_bounds__(64) void conf_dwconv_lane_kernel(const float *__restrict__ g, int T, int D, int K,
+                                                              int padL, const ConvPrev cp,
+                                                              const float *__restrict__ w,
+                                                              const float *__restrict__ dwb,
+                                                              const float *__restrict__ cn_w,
+                                                              const float *__restrict__ cn_b,
+                                                              int8_t *__restrict__ xq, float *__restrict__ xs) {
+    const int lane = threadIdx.x, t = blockIdx.x, c = blockIdx.y * 64 + lane, b = blockIdx.z;
+    const int lo_t = RING ? -padL : 0;                     // the first frame a tap may read
+    const int f0 = t - padL;                               // the frame tap 0 reads
+    const int jlo = max(0, lo_t - f0), jhi = min(K, T - f0);  // the taps in range
+    const __amdgpu_buffer_rsrc_t gr = dw_rsrc(g + (size_t)b * T * D, (uint32_t)T * D * 4);
+    const __amdgpu_buffer_rsrc_t wr = dw_rsrc(w, (uint32_t)K * D * 4);
+    // (no branches among the loads: every one is issued before any is used)
+    float xv[kDwLaneK], wv[kDwLaneK];
+    const int head = RING ? cp.ctl[2] : 0;                 // the ring's oldest slot
+#pragma unroll
+    for (int j = 0; j < kDwLaneK; ++j) {
+        const int ti = f0 + j;
+        const int tc = min(max(ti, 0), T - 1), jc = min(j, K - 1);
+        if constexpr (RING) {
+            // frames before the call from the stream's ring of padL rows
+            const int slot = (head + padL + max(ti, -padL)) % padL;
+            const float *row = ti < 0 ? cp.ring + ((size_t)b * padL + slot) * D : g + ((size_t)b * T + tc) * D;
+            xv[j] = row[c];
+        } else {
+            xv[j] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(gr, (tc * D + c) * 4, 0, 0));
+        }
+        wv[j] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(wr, (jc * D + c) * 4, 0, 0));
+    }
+    float o = dwb != nullptr ? dwb[c] : 0.f;
+#pragma unroll
+    for (int j = 0; j < kDwLaneK; ++j)
+        if (j >= jlo && j < jhi) o = __fadd_rn(o, __fmul_rn(wv[j], xv[j]));
+    const float a = __fadd_rn(__fmul_rn(o, cn_w[c]), cn_b[c]);
+    const float sl = __fdiv_rn(a, __fadd_rn(grx_exp8(__fsub_rn(0.0f, a)), 1.0f));
+    const size_t row = (size_t)b * T + t;
+    quant32_store(sl, xq + row * D + c, xs + row * (D / 32) + c / 32, c & 31);
+}
+
 // ---------------------------------------------------------------- stream caches
 
 // A chunk's key and value rows (the K and V thirds of the q|k|v product,
@@ -1658,17 +1710,30 @@ grx_status enqueue_run(grx_conformer *m, const CRun &r, hipStream_t st) {
         if ((s = ln_rows_launch<false, true>(st, R, bf.x, d, Bk.norm_conv_w, Bk.norm_conv_b, nullptr,
                                                                       nullptr, bf.xq, bf.xs)) != GRX_OK) return s;
         if ((s = grx_gemm_q8_launch(st, Bk.pw1, bf.xq, bf.xs, R, Bk.pw1_b, bf.conv, 2 * d)) != GRX_OK) return s;
-        conf_glu_kernel<<<grid_for((size_t)R * d), 256, 0, st>>>(bf.conv, R, Tp, d, r.lens, bf.glu);
-        GRX_LAUNCHED("conf_glu_kernel");
         ConvPrev cp{};
         if (r.conv_ring && padL > 0) {
             cp.ring = r.conv_ring + r.conv_ring_layer * i;
             cp.ctl = r.ctl;
         }
+        // the depthwise kernel: 0 a workgroup per row, 1 LDS windows, 2 a
+        // wave per frame
+        const bool dw_lane = d % 64 == 0 && hp.conv_kernel <= kDwLaneK && !hp.conv_ln;
+        int dw = grx_tune(GRX_TUNE_CONF_DW);
+        if (dw < 0 || dw > 2) dw = dw_lane ? 2 : 1;
+        if (dw == 2 && !dw_lane) dw = 1;
+        if (dw == 1 && !r.dw_win) dw = 0;
+        conf_glu_kernel<<<grid_for((size_t)R * d), 256, 0, st>>>(bf.conv, R, Tp, d, r.lens, bf.glu);
+        GRX_LAUNCHED("conf_glu_kernel");
         if (hp.conv_ln)
             conf_dwconv_kernel<true><<<R, kRowThreads, row_smem, st>>>(bf.glu, Tp, d, hp.conv_kernel, padL, cp, Bk.dw,
                                                                        Bk.dw_b, Bk.cn_w, Bk.cn_b, bf.xq, bf.xs);
-        else if (r.dw_win)
+        else if (dw == 2 && cp.ring != nullptr)
+            conf_dwconv_lane_kernel<true><<<dim3(Tp, d / 64, B), 64, 0, st>>>(
+                bf.glu, Tp, d, hp.conv_kernel, padL, cp, Bk.dw, Bk.dw_b, Bk.cn_w, Bk.cn_b, bf.xq, bf.xs);
+        else if (dw == 2)
+            conf_dwconv_lane_kernel<false><<<dim3(Tp, d / 64, B), 64, 0, st>>>(
+                bf.glu, Tp, d, hp.conv_kernel, padL, cp, Bk.dw, Bk.dw_b, Bk.cn_w, Bk.cn_b, bf.xq, bf.xs);
+        else if (dw == 1)
             conf_dwconv_win_kernel<<<dim3((Tp + kDwRows - 1) / kDwRows, d / 64, B), 256,
                                      (size_t)(kDwRows + 2 * hp.conv_kernel - 1) * 64 * 4, st>>>(
                 bf.glu, Tp, d, hp.conv_kernel, padL, cp, Bk.dw, Bk.dw_b, Bk.cn_w, Bk.cn_b, bf.xq, bf.xs);

@@ -128,6 +128,8 @@ enum {
     GRX_TUNE_GEMV_MX,         // 0: several-row GEMVs on the dot-product kernel, not the matrix-core one
     GRX_TUNE_GEMV1_ROWS,      // rows per workgroup of one-row products: 8, 16, 32 (slices) or 64 (whole tiles)
     GRX_TUNE_FUSE_SELF_ATTN,  // 0: whisper's q|k|v product and self-attention in launches of their own
+    GRX_TUNE_CONF_DW,         // conformer depthwise convolution: 0 a workgroup per row, 1 windows in LDS,
+                              // 2 a wave per frame
     GRX_TUNE_COUNT
 };
 int grx_tune(int id);

@@ -467,7 +467,7 @@ constexpr int kss_row(int kb) { return kb * 32 + 16; }
 constexpr int kss_bytes(int kb) { return 16 * kss_row(kb) + 16 * kb * 4; }
 
 template <int EPI, int NS, int KB>
-__global__ __launch_bounds__(64 * ks_max_waves(NS, KB)) void gemm_q8_kss_kernel(
+__global__ __launch_bounds__(64 * ks_max_waves(NS, KB), 4) void gemm_q8_kss_kernel(
     const int8_t *__restrict__ qs, const uint16_t *__restrict__ ds, int rows, int nb, const int8_t *__restrict__ xq,
     const float *__restrict__ xs, int m, const float *__restrict__ bias, float *__restrict__ y, int ldc, float scale,
     int8_t *__restrict__ yq, float *__restrict__ ys, int ncg, int nrf, int bbeg, int bend, const float *init,
@@ -490,14 +490,30 @@ __global__ __launch_bounds__(64 * ks_max_waves(NS, KB)) void gemm_q8_kss_kernel(
     const int nbw = min(KB, bend - b0);       // this wave's blocks (>= 1)
     const int8_t *wq = qs + (size_t)tile * nb * 2048;
     const uint16_t *wd = ds + (size_t)tile * nb * 64;
-    // A: weight row n0+16s+li, bytes 8*lk.. of each block; the lane's four
-    // weight scales (rows n0+16s+4*lk ..) are 8 contiguous bytes
+    // A: weight row n0+16s+li, bytes 8*lk.. of each block; the lane's D rows
+    // are n0+16s+4*lk .. +3, whose four weight scales are 8 contiguous bytes
     const unsigned qoff = (unsigned)((lk >> 1) * 1024 + (sub + li) * 16 + 8 * (lk & 1));
-    const unsigned doff = (unsigned)(sub + 4 * lk);
     const int arow = 16 * rf + li;            // the lane's activation row (B column)
+    constexpr bool kResid = (EPI == GRX_GEMM_ADD || EPI == GRX_GEMM_AXPY_HALF) && NS == 1;
     constexpr int RS = kss_row(KB);
     int8_t *sa = kss_stage + wave * kss_bytes(KB);
     float *sd = reinterpret_cast<float *>(sa + 16 * RS);
+
+    // the chain's start (wave 0: a carried chain's init, else the bias) is
+    // loaded first, ahead of the operands, so the first link of the chain
+    // does not wait on memory
+    float cz[NS][4];
+    if (wave == 0) {
+        const int ar = min(arow, m - 1);
+#pragma unroll
+        for (int s = 0; s < NS; ++s)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int n = n0 + 16 * s + 4 * lk + r;
+                cz[s][r] = init != nullptr ? init[(size_t)ar * ldi + min(n, rows - 1)]
+                                           : ((bias != nullptr && n < rows) ? bias[n] : 0.0f);
+            }
+    }
 
     // every load of the wave's blocks in flight at once (block indices past
     // bend are clamped and their results never used; rows past m likewise)
@@ -517,16 +533,33 @@ __global__ __launch_bounds__(64 * ks_max_waves(NS, KB)) void gemm_q8_kss_kernel(
         rd = *reinterpret_cast<const float4 *>(xs + (row * (unsigned)nb + b));
     }
     long bv[KB][NS];
-    uint2 dq[KB][NS];
 #pragma unroll
     for (int u = 0; u < KB; ++u) {
         const unsigned b = (unsigned)min(b0 + u, bend - 1);
 #pragma unroll
-        for (int s = 0; s < NS; ++s) {
-            bv[u][s] = *reinterpret_cast<const long *>(wq + (qoff + b * 2048 + s * 256));
-            dq[u][s] = *reinterpret_cast<const uint2 *>(reinterpret_cast<const char *>(wd) +
-                                                          2 * (doff + b * 64 + 16 * s));
-        }
+        for (int s = 0; s < NS; ++s) bv[u][s] = *reinterpret_cast<const long *>(wq + (qoff + b * 2048 + s * 256));
+    }
+    // the weight scales in one load: lane q (< KB*NS*4) takes the four rows
+    // n0+16s+4j.. of block u, q = (u*NS + s)*4 + j; the lanes that need them
+    // fetch them from lane q with a cross-lane permute
+    uint2 wsq;
+    {
+        const int q = min(lane, KB * NS * 4 - 1), u = q / (4 * NS), s = (q >> 2) % NS, j = q & 3;
+        const unsigned b = (unsigned)min(b0 + u, bend - 1);
+        wsq = *reinterpret_cast<const uint2 *>(reinterpret_cast<const char *>(wd) + 2 * (sub + 16 * s + 4 * j + b * 64));
+    }
+    // the epilogue's residual (the last wave; each element of y is read and
+    // written by one lane only), loaded last, long before it is used (16
+    // columns a wave: 32 would not leave the registers for four waves a SIMD)
+    float yr[NS][4];
+    if (kResid && wave == ks - 1 && arow < m) {
+#pragma unroll
+        for (int s = 0; s < NS; ++s)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int n = n0 + 16 * s + 4 * lk + r;
+                yr[s][r] = n < rows ? y[(size_t)arow * ldc + n] : 0.0f;
+            }
     }
 #pragma unroll
     for (int j = 0; j < NA; ++j) {
@@ -552,7 +585,9 @@ __global__ __launch_bounds__(64 * ks_max_waves(NS, KB)) void gemm_q8_kss_kernel(
         for (int s = 0; s < NS; ++s) {
             v4i d = {0, 0, 0, 0};
             d = __builtin_amdgcn_mfma_i32_16x16x32_i8(bv[u][s], a, d, 0, 0, 0);
-            const uint32_t h[2] = {dq[u][s].x, dq[u][s].y};
+            const int src = ((u * NS + s) * 4 + lk) * 4;
+            const uint32_t h[2] = {(uint32_t)__builtin_amdgcn_ds_bpermute(src, (int)wsq.x),
+                                   (uint32_t)__builtin_amdgcn_ds_bpermute(src, (int)wsq.y)};
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const float dw = grx_f16_to_f32((uint16_t)(h[r >> 1] >> (16 * (r & 1))));
@@ -561,25 +596,25 @@ __global__ __launch_bounds__(64 * ks_max_waves(NS, KB)) void gemm_q8_kss_kernel(
         }
     }
 
+    // the chain's activation scales, read before the wave's turn comes (16
+    // columns a wave; with 32 the registers go to the products, and each
+    // read is followed by eight links rather than four)
+    constexpr bool kHoist = NS == 1;
+    float dav[kHoist ? KB : 1];
+    if constexpr (kHoist) {
+#pragma unroll
+        for (int u = 0; u < KB; ++u) dav[u] = sd[u * 16 + li];
+    }
+
     // the ordered chain, one wave after another
     float c[NS][4];
     for (int p = 0; p < ks; ++p) {
         if (wave == p) {
-            if (p == 0 && init != nullptr) {
-                const int ar = min(arow, m - 1);
+            if (p == 0) {
 #pragma unroll
                 for (int s = 0; s < NS; ++s)
 #pragma unroll
-                    for (int r = 0; r < 4; ++r)
-                        c[s][r] = init[(size_t)ar * ldi + min(n0 + 16 * s + 4 * lk + r, rows - 1)];
-            } else if (p == 0) {
-#pragma unroll
-                for (int s = 0; s < NS; ++s)
-#pragma unroll
-                    for (int r = 0; r < 4; ++r) {
-                        const int n = n0 + 16 * s + 4 * lk + r;
-                        c[s][r] = (bias != nullptr && n < rows) ? bias[n] : 0.0f;
-                    }
+                    for (int r = 0; r < 4; ++r) c[s][r] = cz[s][r];
             } else {
 #pragma unroll
                 for (int s = 0; s < NS; ++s)
@@ -589,7 +624,7 @@ __global__ __launch_bounds__(64 * ks_max_waves(NS, KB)) void gemm_q8_kss_kernel(
             if (nbw == KB) {
 #pragma unroll
                 for (int u = 0; u < KB; ++u) {
-                    const float da = sd[u * 16 + li];
+                    const float da = kHoist ? dav[kHoist ? u : 0] : sd[u * 16 + li];
 #pragma unroll
                     for (int s = 0; s < NS; ++s)
 #pragma unroll
@@ -599,7 +634,7 @@ __global__ __launch_bounds__(64 * ks_max_waves(NS, KB)) void gemm_q8_kss_kernel(
 #pragma unroll
                 for (int u = 0; u < KB; ++u) {
                     if (u < nbw) {
-                        const float da = sd[u * 16 + li];
+                        const float da = kHoist ? dav[kHoist ? u : 0] : sd[u * 16 + li];
 #pragma unroll
                         for (int s = 0; s < NS; ++s)
 #pragma unroll
@@ -666,8 +701,8 @@ __global__ __launch_bounds__(64 * ks_max_waves(NS, KB)) void gemm_q8_kss_kernel(
             for (int r = 0; r < 4; ++r) {
                 if (n + r >= rows) continue;
                 if constexpr (EPI == GRX_GEMM_STORE) yp[r] = c[s][r];
-                if constexpr (EPI == GRX_GEMM_ADD) yp[r] = __fadd_rn(yp[r], c[s][r]);
-                if constexpr (EPI == GRX_GEMM_AXPY_HALF) yp[r] = __fmaf_rn(0.5f, c[s][r], yp[r]);
+                if constexpr (EPI == GRX_GEMM_ADD) yp[r] = __fadd_rn(kResid ? yr[s][r] : yp[r], c[s][r]);
+                if constexpr (EPI == GRX_GEMM_AXPY_HALF) yp[r] = __fmaf_rn(0.5f, c[s][r], kResid ? yr[s][r] : yp[r]);
                 if constexpr (EPI == GRX_GEMM_SCALE) yp[r] = __fmul_rn(c[s][r], scale);
             }
         }

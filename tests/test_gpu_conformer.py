@@ -78,6 +78,37 @@ def test_tiny_attention_variants_bit_exact(kern, orc, rq):
     enc.close()
 
 
+@pytest.mark.parametrize("dw", [0, 1, 2])
+def test_depthwise_variants_bit_exact(kern, orc, dw):
+    """Every depthwise kernel - a workgroup per row, LDS windows, a wave per
+    frame - gives the oracle's bits: the tiny shape (kernel 9) with
+    utterances whose padding rows the GLU zeroes, and the parakeet width
+    (kernel 31) with two layers."""
+    hp = dict(CONFORMER_TINY)
+    t = conformer_model(hp, seed=26)
+    mel, frames, valid = _mels(hp, 3, 1.5, 37)
+    vals = [valid, valid - 9, valid - 60]
+    with kern.tuned(CONF_DW=dw):
+        enc = _enc(kern, hp, t)
+        got, lens = enc.encode(mel, vals)
+        enc.close()
+    o = orc.ConformerOracle(hp, t)
+    for b in range(3):
+        want, L = o.encode(mel[b], vals[b])
+        assert np.array_equal(got[b].view(np.uint32), want.view(np.uint32)), (dw, b)
+    hp = dict(PARAKEET_TDT_06B, layers=2)
+    t = conformer_model(hp, seed=33)
+    mel, frames, valid = _mels(hp, 2, 10.0, 61)
+    with kern.tuned(CONF_DW=dw):
+        enc = _enc(kern, hp, t)
+        got, lens = enc.encode(mel, [valid, valid - 250])
+        enc.close()
+    o = orc.ConformerOracle(hp, t)
+    for b, v in enumerate([valid, valid - 250]):
+        want, L = o.encode(mel[b], v)
+        assert np.array_equal(got[b].view(np.uint32), want.view(np.uint32)), (dw, b)
+
+
 def test_tiny_shape_change_and_rerun(kern, orc):
     """A second call with another batch and frame count re-plans the work;
     repeating a call gives the same bits."""
