@@ -366,15 +366,27 @@ __global__ __launch_bounds__(kRowThreads) void ln_rows_kernel(float *__restrict_
 
 // The keys [k0, k1) of a block of queries q0..q1-1 (key indices qoff+q):
 // the union of its rows' ranges (encoder.go:285-289).
+// The union of the ranges of block rows q0..q1-1: the rows that see keys
+// are a prefix of the block (those before the valid length), whose ranges'
+// ends never decrease with the row, so the first gives the start and the
+// last the end; a row that sees none counts as [0, 0), as a loop over the
+// rows taking min(lo) and max(hi) from k0 = Tk, k1 = 0 would have it.
 __device__ inline void block_keys(const AttnKeys &ak, int q0, int q1, int qoff, int Tk, int L, int c, int &k0,
                                   int &k1) {
+    const int lim = (ak.mode == kKeysStream ? c + L : L) - qoff;  // rows q < lim see keys
+    const int qv = min(q1, max(q0, lim));
     k0 = Tk;
     k1 = 0;
-    for (int q = q0; q < q1; ++q) {
+    if (qv > q0) {
         int lo, hi;
-        attn_keys(ak, qoff + q, Tk, L, c, lo, hi);
-        k0 = min(k0, lo);
-        k1 = max(k1, hi);
+        attn_keys(ak, qoff + q0, Tk, L, c, lo, hi);
+        k0 = lo;
+        attn_keys(ak, qoff + qv - 1, Tk, L, c, lo, hi);
+        k1 = hi;
+    }
+    if (qv < q1) {
+        k0 = min(k0, 0);
+        k1 = max(k1, 0);
     }
 }
 
@@ -553,6 +565,43 @@ __device__ __forceinline__ void stage_f4(float *dst, int sdst, const float *src,
     }
 }
 
+// stage_f4 in two halves: the loads of the first U float4s a thread takes
+// (issued early, held in registers while other work runs), then their
+// stores and the rest of the rows.
+template <int U>
+__device__ __forceinline__ void stage_pre(float4 (&v)[U], const float *src, size_t ssrc, int rows, int cols) {
+    const int c4 = cols >> 2, n = rows * c4, nt = blockDim.x;
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+        const int e = min((int)threadIdx.x + u * nt, n - 1);
+        v[u] = *reinterpret_cast<const float4 *>(src + (size_t)(e / c4) * ssrc + 4 * (e % c4));
+    }
+}
+template <int U>
+__device__ __forceinline__ void stage_post(float *dst, int sdst, const float4 (&v)[U], const float *src, size_t ssrc,
+                                           int rows, int cols) {
+    const int c4 = cols >> 2, n = rows * c4, nt = blockDim.x;
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+        const int e = threadIdx.x + u * nt;
+        if (e < n) {
+            float *d = dst + (e / c4) * sdst + 4 * (e % c4);
+            d[0] = v[u].x;
+            d[1] = v[u].y;
+            d[2] = v[u].z;
+            d[3] = v[u].w;
+        }
+    }
+    for (int e = threadIdx.x + U * nt; e < n; e += nt) {
+        const float4 w = *reinterpret_cast<const float4 *>(src + (size_t)(e / c4) * ssrc + 4 * (e % c4));
+        float *d = dst + (e / c4) * sdst + 4 * (e % c4);
+        d[0] = w.x;
+        d[1] = w.y;
+        d[2] = w.z;
+        d[3] = w.w;
+    }
+}
+
 // Four outputs of MatMulF32's 6x16 panel route (kernels_amd64.s:5-88) at
 // once: out_j = sum over k chunks of 256 of (fma chain over the chunk),
 // each chunk's chain added to the running result; a(j, k) and b(j, k) give
@@ -582,6 +631,20 @@ __device__ __forceinline__ void packed4(const FA &a, const FB &b, int k, float o
 // still chosen by the row's index in its block and by the block's full
 // column counts).  Only the band of bd that the rows use is computed:
 // bd[i][nq-1-i+kk] for the nk keys.
+// The (piece, head, utterance) of a workgroup of a (pieces, heads, B)
+// launch such that one head's workgroups share an XCD: workgroup L of the
+// launch runs on XCD L % 8, so XCD x takes the x-th eighth of the list in
+// (utterance, head, piece) order, and a head's keys, position rows and
+// values come into that XCD's L2 once rather than into all eight.
+__device__ __forceinline__ void attn_wg_xcd(int &px, int &h, int &b) {
+    const int nx = gridDim.x, ny = gridDim.y, n = nx * ny * gridDim.z;
+    const int l = blockIdx.x + nx * (blockIdx.y + ny * blockIdx.z);
+    const int w = n % 8 == 0 ? (l % 8) * (n / 8) + l / 8 : l;
+    px = w % nx;
+    h = (w / nx) % ny;
+    b = w / (nx * ny);
+}
+
 template <int RQ>
 __global__ __launch_bounds__(kAttnLdsThreads) void conf_attn_lds_kernel(const AttnIO io, const AttnKeys ak,
                                                                         const float *__restrict__ pos_u,
@@ -591,8 +654,10 @@ __global__ __launch_bounds__(kAttnLdsThreads) void conf_attn_lds_kernel(const At
                                                                         float *__restrict__ xs) {
     extern __shared__ float sm[];
     const int pieces = (ak.bl + RQ - 1) / RQ;
-    const int blk = blockIdx.x / pieces, r0 = (blockIdx.x % pieces) * RQ;
-    const int h = blockIdx.y, b = blockIdx.z, tid = threadIdx.x, nt = blockDim.x;
+    int px, h, b;
+    attn_wg_xcd(px, h, b);
+    const int blk = px / pieces, r0 = (px % pieces) * RQ;
+    const int tid = threadIdx.x, nt = blockDim.x;
     const int T = io.T, L = io.lens[b];
     const AttnRows ar = attn_rows(io, b);
     const int c = ar.c, Tk = ar.Tk, qoff = Tk - T;
@@ -618,9 +683,19 @@ __global__ __launch_bounds__(kAttnLdsThreads) void conf_attn_lds_kernel(const At
     float *qu = sm, *qv = qu + RQ * sq, *S = qv + RQ * sq, *BD = S + RQ * sS, *rmx = BD + RQ * sS,
           *rinv = rmx + RQ, *st = rinv + RQ;
     const float *kb = ar.kv + (size_t)k0 * io.ldkv;
+    // position rows jlo + nq-1-(r0+i) + kk: from pb = jlo + nq-1-(r0+nr-1) on, nk + nr - 1 of them
+    const int pb = jlo + nq - 1 - (r0 + nr - 1), npr = nk + nr - 1;
+    const float *pp = ar.pp + (size_t)pb * io.ldp + h * hd, *vp = kb + io.vo + h * hd;
     stage_f4(qu, sq, qb + (size_t)(q0 + r0) * io.ldq + h * hd, io.ldq, nr, hd);
     // keys k0.. of the head, rows sq apart
     stage_f4(st, sq, kb + h * hd, io.ldkv, nk, hd);
+    // the position rows' and the values' loads in flight while the scores
+    // are formed (they go to LDS once the keys, then the position rows, are
+    // done with)
+    constexpr int kPre = 5;
+    float4 pv[kPre], vv[kPre];
+    stage_pre(pv, pp, io.ldp, npr, hd);
+    stage_pre(vv, vp, io.ldkv, nk, hd);
     __syncthreads();
     for (int e = tid; e < nr * hd; e += nt) {
         const int i = e / hd, j = e % hd;
@@ -632,8 +707,12 @@ __global__ __launch_bounds__(kAttnLdsThreads) void conf_attn_lds_kernel(const At
     // rows below pf (index in the block) take the panel route: whole groups
     // of four of them run four chains per thread; every other output (the
     // gemvRows rows, a last partial group) is a task of its own
+    // (a workgroup with fewer groups than it has threads for one chain
+    // each runs every output as a task of its own: four times the chains at
+    // once, the same bits)
     const int pf = nq > 16 ? nq / 6 * 6 : 0;
-    const int pr = r0 < pf ? min(nr, pf - r0) : 0, ng = pr / 4, r1 = 4 * ng;
+    const int pr = r0 < pf ? min(nr, pf - r0) : 0, ng0 = pr / 4;
+    const int ng = 4 * ng0 * nk > nt ? ng0 : 0, r1 = 4 * ng;
     for (int e = tid; e < ng * nk + (nr - r1) * nk; e += nt) {
         if (e < ng * nk) {
             const int i0 = 4 * (e / nk), kk = e % nk;
@@ -648,9 +727,7 @@ __global__ __launch_bounds__(kAttnLdsThreads) void conf_attn_lds_kernel(const At
         }
     }
     __syncthreads();
-    // position rows jlo + nq-1-(r0+i) + kk: from pb = jlo + nq-1-(r0+nr-1) on, nk + nr - 1 of them
-    const int pb = jlo + nq - 1 - (r0 + nr - 1), npr = nk + nr - 1;
-    stage_f4(st, sq, ar.pp + (size_t)pb * io.ldp + h * hd, io.ldp, npr, hd);
+    stage_post(st, sq, pv, pp, io.ldp, npr, hd);
     __syncthreads();
     // bd[i][kk] uses position row (nr-1-i) + kk of the staged ones: rows
     // i0+j with keys kd+j share row nr-1-i0+kd, so a thread takes such a
@@ -683,7 +760,7 @@ __global__ __launch_bounds__(kAttnLdsThreads) void conf_attn_lds_kernel(const At
     }
     __syncthreads();
     // values of the head (rows hd apart) while the rows are scored
-    stage_f4(st, hd, kb + io.vo + h * hd, io.ldkv, nk, hd);
+    stage_post(st, hd, vv, vp, io.ldkv, nk, hd);
     const int lane = tid & 63, wave = tid >> 6, nw = nt >> 6;
     for (int i = wave; i < nr; i += nw) {
         int lo, hi;
@@ -720,9 +797,11 @@ __global__ __launch_bounds__(kAttnLdsThreads) void conf_attn_lds_kernel(const At
     __syncthreads();
     for (int i = wave; i < nr; i += nw) {
         float acc = 0.f;
-        if (lane < 8) {
+        if (lane < 8) {  // (unrolled: the reads go out ahead of the sum's chain)
+#pragma unroll 8
             for (int kk = lane; kk < n8; kk += 8) acc = __fadd_rn(acc, S[i * sS + kk]);
         } else if (lane == 8) {
+#pragma unroll 8
             for (int kk = n8; kk < nk; ++kk) acc = __fadd_rn(acc, S[i * sS + kk]);
         }
         float a8[8];
