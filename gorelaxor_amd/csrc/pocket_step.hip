@@ -128,10 +128,18 @@ __device__ __forceinline__ void attn_step_small(float *sm, const float *q, const
     *(live ? pl + tid : dummy + 1) = e;
     __syncthreads();
     const float inv = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(softmax_inv(ch, kStepCs, pl + n8, n)), 0));
-    pw[tid] = live ? __fmul_rn(e, inv) : 0.f;
+    const float wj = live ? __fmul_rn(e, inv) : 0.f;
+    pw[tid] = wj;
+    // a key of weight zero is skipped: its value row goes in as zeros, so
+    // the chain's fma(0, 0, o) leaves o as it is (o starts at +0 and exact
+    // cancellation rounds to +0, so o is never -0) whatever the row held
     float4 *vw = reinterpret_cast<float4 *>(vl + tid * LD);
+    const bool zr = wj == 0.f;
 #pragma unroll
-    for (int i = 0; i < HD / 4; ++i) vw[i] = vv[i];
+    for (int i = 0; i < HD / 4; ++i) {  // (per component: the row stays in registers)
+        const float a = vv[i].x, b = vv[i].y, c = vv[i].z, e4 = vv[i].w;
+        vw[i] = make_float4(zr ? 0.f : a, zr ? 0.f : b, zr ? 0.f : c, zr ? 0.f : e4);
+    }
     __syncthreads();
     if (wave == 0) {
         float o = 0.f;
@@ -148,11 +156,8 @@ __device__ __forceinline__ void attn_step_small(float *sm, const float *q, const
             }
 #pragma unroll
             for (int i = 0; i < 32; ++i) v[i] = vl[(j0 + i) * LD + lane];
-            // a zero weight is skipped as fma(0, 0, o) == o (o starts at +0 and
-            // exact cancellation rounds to +0, so o is never -0): the select
-            // stays off the dependent chain
 #pragma unroll
-            for (int i = 0; i < 32; ++i) o = __fmaf_rn(w[i], w[i] == 0.f ? 0.f : v[i], o);
+            for (int i = 0; i < 32; ++i) o = __fmaf_rn(w[i], v[i], o);
         }
         att[h * HD + lane] = o;
         if constexpr (QOUT) quant32_store(o, att_q + h * HD + lane, att_s + (h * HD + lane) / 32, lane & 31);
