@@ -602,6 +602,76 @@ __device__ __forceinline__ void stage_post(float *dst, int sdst, const float4 (&
     }
 }
 
+// MatMulF32's 6x16 panel route (kernels_amd64.s:5-88) for R rows a_j
+// (16-byte aligned, rows sa floats apart) against one operand b, reading
+// four k at a time with 16-byte LDS reads: out_j = sum over k chunks of 256
+// of (fma chain over the chunk, in k order), each chunk's chain added to
+// the running result from 0.  BS: b is 16-byte aligned and contiguous (one
+// 16-byte read per four k), else its elements are sb apart (four reads).
+// A tail of k % 4 (a chunk's end) reads one element at a time.
+template <int R, bool BS>
+__device__ __forceinline__ void panel_v4(const float *a, int sa, const float *b, size_t sb, int k, float out[R]) {
+    float c[R];
+#pragma unroll
+    for (int j = 0; j < R; ++j) c[j] = 0.f;
+    for (int k0 = 0; k0 < k; k0 += 256) {
+        const int kn = min(256, k - k0), k4 = kn & ~3;
+        float acc[R];
+#pragma unroll
+        for (int j = 0; j < R; ++j) acc[j] = 0.f;
+        auto step = [&](int kk) {
+            float4 bv;
+            if constexpr (BS) {
+                bv = *reinterpret_cast<const float4 *>(b + k0 + kk);
+            } else {
+                bv.x = b[(size_t)(k0 + kk) * sb];
+                bv.y = b[(size_t)(k0 + kk + 1) * sb];
+                bv.z = b[(size_t)(k0 + kk + 2) * sb];
+                bv.w = b[(size_t)(k0 + kk + 3) * sb];
+            }
+#pragma unroll
+            for (int j = 0; j < R; ++j) {
+                const float4 av = *reinterpret_cast<const float4 *>(a + (size_t)j * sa + k0 + kk);
+                acc[j] = __fmaf_rn(av.x, bv.x, acc[j]);
+                acc[j] = __fmaf_rn(av.y, bv.y, acc[j]);
+                acc[j] = __fmaf_rn(av.z, bv.z, acc[j]);
+                acc[j] = __fmaf_rn(av.w, bv.w, acc[j]);
+            }
+        };
+        // (one chain: eight steps' reads in flight; four chains: two, for
+        // the registers)
+        if constexpr (R == 1) {
+#pragma unroll 8
+            for (int kk = 0; kk < k4; kk += 4) step(kk);
+        } else {
+#pragma unroll 2
+            for (int kk = 0; kk < k4; kk += 4) step(kk);
+        }
+        for (int kk = k4; kk < kn; ++kk) {
+            const float bx = BS ? b[k0 + kk] : b[(size_t)(k0 + kk) * sb];
+#pragma unroll
+            for (int j = 0; j < R; ++j) acc[j] = __fmaf_rn(a[(size_t)j * sa + k0 + kk], bx, acc[j]);
+        }
+#pragma unroll
+        for (int j = 0; j < R; ++j) c[j] = __fadd_rn(acc[j], c[j]);
+    }
+#pragma unroll
+    for (int j = 0; j < R; ++j) out[j] = c[j];
+}
+
+// One output of MatMulF32 (matmul_f32_one's routes) with a 16-byte aligned
+// a: the panel route through panel_v4, the gemvRows route as before.
+template <bool BS>
+__device__ __forceinline__ float matmul_f32_one_v4(const float *a, const float *b, size_t sb, int k, int r, int m, int j,
+                                                   int n) {
+    if (m > 16 && r < m / 6 * 6) {
+        float o[1];
+        panel_v4<1, BS>(a, 0, b, sb, k, o);
+        return o[0];
+    }
+    return matmul_f32_one(a, b, sb, k, r, m, j, n);
+}
+
 // Four outputs of MatMulF32's 6x16 panel route (kernels_amd64.s:5-88) at
 // once: out_j = sum over k chunks of 256 of (fma chain over the chunk),
 // each chunk's chain added to the running result; a(j, k) and b(j, k) give
@@ -679,7 +749,22 @@ __global__ __launch_bounds__(kAttnLdsThreads) void conf_attn_lds_kernel(const At
         return;
     }
     const int np = nq + nk - 1, jlo = Tk - 1 - (qoff + q1 - 1) + k0;
-    const int sq = hd + 1, sS = nk | 1;
+    // rows below pf (index in the block) take the panel route: whole groups
+    // of four of them run four chains per thread; every other output (the
+    // gemvRows rows, a last partial group) is a task of its own
+    // (a workgroup with fewer groups than it has threads for one chain
+    // each runs every output as a task of its own: four times the chains at
+    // once, the same bits)
+    const int pf = nq > 16 ? nq / 6 * 6 : 0;
+    const int pr = r0 < pf ? min(nr, pf - r0) : 0, ng0 = pr / 4;
+    const int ng = 4 * ng0 * nk > nt ? ng0 : 0, r1 = 4 * ng;
+    // on the panel route (blocks of more than 16 rows) with groups, or with
+    // more single-chain tasks than threads, rows 16-byte aligned: the chains
+    // read four floats at once, sq = hd + 4 spreading a row per lane's 16-byte
+    // reads over the banks; otherwise (the gemvRows route, or a task per
+    // thread, measured faster so) one float at a time, spread by an odd stride
+    const bool v4 = nq > 16 && (ng > 0 || nr * nk > nt);
+    const int sq = v4 ? hd + 4 : hd + 1, sS = v4 ? (nk + 3) & ~3 : nk | 1;
     float *qu = sm, *qv = qu + RQ * sq, *S = qv + RQ * sq, *BD = S + RQ * sS, *rmx = BD + RQ * sS,
           *rinv = rmx + RQ, *st = rinv + RQ;
     const float *kb = ar.kv + (size_t)k0 * io.ldkv;
@@ -704,26 +789,17 @@ __global__ __launch_bounds__(kAttnLdsThreads) void conf_attn_lds_kernel(const At
         qv[i * sq + j] = __fadd_rn(q, pos_v[h * hd + j]);
     }
     __syncthreads();
-    // rows below pf (index in the block) take the panel route: whole groups
-    // of four of them run four chains per thread; every other output (the
-    // gemvRows rows, a last partial group) is a task of its own
-    // (a workgroup with fewer groups than it has threads for one chain
-    // each runs every output as a task of its own: four times the chains at
-    // once, the same bits)
-    const int pf = nq > 16 ? nq / 6 * 6 : 0;
-    const int pr = r0 < pf ? min(nr, pf - r0) : 0, ng0 = pr / 4;
-    const int ng = 4 * ng0 * nk > nt ? ng0 : 0, r1 = 4 * ng;
     for (int e = tid; e < ng * nk + (nr - r1) * nk; e += nt) {
         if (e < ng * nk) {
             const int i0 = 4 * (e / nk), kk = e % nk;
             float o[4];
-            const float *bk = st + kk * sq;
-            packed4([&](int j, int k) { return qu[(i0 + j) * sq + k]; }, [&](int, int k) { return bk[k]; }, hd, o);
+            panel_v4<4, true>(qu + i0 * sq, sq, st + kk * sq, 1, hd, o);
 #pragma unroll
             for (int j = 0; j < 4; ++j) S[(i0 + j) * sS + kk] = o[j];
         } else {
             const int e2 = e - ng * nk, i = r1 + e2 / nk, kk = e2 % nk;
-            S[i * sS + kk] = matmul_f32_one(qu + i * sq, st + kk * sq, 1, hd, r0 + i, nq, kk, nk);
+            S[i * sS + kk] = v4 ? matmul_f32_one_v4<true>(qu + i * sq, st + kk * sq, 1, hd, r0 + i, nq, kk, nk)
+                                : matmul_f32_one(qu + i * sq, st + kk * sq, 1, hd, r0 + i, nq, kk, nk);
         }
     }
     __syncthreads();
@@ -741,8 +817,7 @@ __global__ __launch_bounds__(kAttnLdsThreads) void conf_attn_lds_kernel(const At
         if (e < n_diag) {
             const int i0 = 4 * (e / nd), kd = e % nd;
             float o[4];
-            const float *bp = st + (nr - 1 - i0 + kd) * sq;
-            packed4([&](int j, int k) { return qv[(i0 + j) * sq + k]; }, [&](int, int k) { return bp[k]; }, hd, o);
+            panel_v4<4, true>(qv + i0 * sq, sq, st + (nr - 1 - i0 + kd) * sq, 1, hd, o);
 #pragma unroll
             for (int j = 0; j < 4; ++j) BD[(i0 + j) * sS + kd + j] = o[j];
             continue;
@@ -756,7 +831,9 @@ __global__ __launch_bounds__(kAttnLdsThreads) void conf_attn_lds_kernel(const At
             kj = e2 % nk;
         }
         const int jj = nq - 1 - (r0 + i) + kj;  // column of bd in the block's product
-        BD[i * sS + kj] = matmul_f32_one(qv + i * sq, st + (nr - 1 - i + kj) * sq, 1, hd, r0 + i, nq, jj, np);
+        const float *bq = qv + i * sq, *bpr = st + (nr - 1 - i + kj) * sq;
+        BD[i * sS + kj] = v4 ? matmul_f32_one_v4<true>(bq, bpr, 1, hd, r0 + i, nq, jj, np)
+                             : matmul_f32_one(bq, bpr, 1, hd, r0 + i, nq, jj, np);
     }
     __syncthreads();
     // values of the head (rows hd apart) while the rows are scored
@@ -824,14 +901,13 @@ __global__ __launch_bounds__(kAttnLdsThreads) void conf_attn_lds_kernel(const At
         if (e < ng * hd) {
             const int i0 = 4 * (e / hd), ee = e % hd;
             float o[4];
-            const float *bv = st + ee;
-            packed4([&](int j, int k) { return S[(i0 + j) * sS + k]; }, [&](int, int k) { return bv[k * hd]; }, nk,
-                    o);
+            panel_v4<4, false>(S + i0 * sS, sS, st + ee, hd, nk, o);
 #pragma unroll
             for (int j = 0; j < 4; ++j) O[(i0 + j) * sq + ee] = o[j];
         } else {
             const int e2 = e - ng * hd, i = r1 + e2 / hd, ee = e2 % hd;
-            O[i * sq + ee] = matmul_f32_one(S + i * sS, st + ee, hd, nk, r0 + i, nq, ee, hd);
+            O[i * sq + ee] = v4 ? matmul_f32_one_v4<false>(S + i * sS, st + ee, hd, nk, r0 + i, nq, ee, hd)
+                                : matmul_f32_one(S + i * sS, st + ee, hd, nk, r0 + i, nq, ee, hd);
         }
     }
     __syncthreads();
@@ -844,9 +920,9 @@ __global__ __launch_bounds__(kAttnLdsThreads) void conf_attn_lds_kernel(const At
 }
 
 size_t attn_lds_smem_floats(int T, int hd, int rq) {
-    const int nk = T, sq = hd + 1;
+    const int nk = T, sq = hd + 4, sS = (nk + 3) & ~3;
     const size_t stage = std::max((size_t)(nk + rq - 1) * sq, (size_t)nk * hd);
-    return (size_t)2 * rq * sq + (size_t)2 * rq * (nk | 1) + 2 * rq + stage;
+    return (size_t)2 * rq * sq + (size_t)2 * rq * sS + 2 * rq + stage;
 }
 
 size_t attn_smem_floats(int T, int hd) {
@@ -1524,9 +1600,8 @@ grx_status attn_pick(int B, int heads, int nblk, int bl, int nk, int hd, int *rq
     *rq = n8 < 256 ? 4 : n8 < 1024 ? 8 : 16;
     if (grx_tune(GRX_TUNE_CONF_ATTN_RQ) >= 0) *rq = grx_tune(GRX_TUNE_CONF_ATTN_RQ);  // 0 (unstaged), 4, 8 or 16, for tests
     if (*rq != 0 && *rq != 4 && *rq != 8 && *rq != 16) *rq = 8;
+    const size_t staged = attn_lds_smem_floats(nk, hd, *rq) * 4;
     const size_t sq = hd + 1;
-    const size_t stage = std::max((size_t)(nk + *rq - 1) * sq, (size_t)nk * hd);
-    const size_t staged = ((size_t)2 * *rq * sq + (size_t)2 * *rq * (nk | 1) + 2 * *rq + stage) * 4;
     const void *fn = *rq == 4   ? (const void *)conf_attn_lds_kernel<4>
                      : *rq == 8 ? (const void *)conf_attn_lds_kernel<8>
                                 : (const void *)conf_attn_lds_kernel<16>;
