@@ -728,9 +728,12 @@ __global__ __launch_bounds__(kLdsThreads) void gemm_q8_lds_kernel(const int8_t *
                                                                   const float *__restrict__ bias,
                                                                   float *__restrict__ y, int ldc, float scale,
                                                                   int8_t *__restrict__ yq, float *__restrict__ ys) {
-    // LDS per buffer: A [CB][64][32] bytes, B [CB][2 tiles][2 halves][64][16],
+    // LDS per buffer: A [64 rows][CB][32] bytes, rows kAr apart (16 bytes of
+    // padding: a fragment's 8-byte reads of 16 rows and a row's 16-byte
+    // stores fall in distinct banks), B [CB][2 tiles][2 halves][64][16],
     // weight scales [CB][128] u16, activation scales [CB][64] f32
-    constexpr int kA = kLdsCB * 64 * 32, kB = kLdsCB * 2 * 2048, kD = kLdsCB * 128 * 2, kS = kLdsCB * 64 * 4;
+    constexpr int kAr = kLdsCB * 32 + 16;
+    constexpr int kA = 64 * kAr, kB = kLdsCB * 2 * 2048, kD = kLdsCB * 128 * 2, kS = kLdsCB * 64 * 4;
     constexpr int kBuf = kA + kB + kD + kS;
     __shared__ __align__(16) uint8_t lds[2 * kBuf];
     const int tid = threadIdx.x, lane = tid & 63;
@@ -786,8 +789,8 @@ __global__ __launch_bounds__(kLdsThreads) void gemm_q8_lds_kernel(const int8_t *
     auto lstore = [&](int buf) {
         uint8_t *base = lds + buf * kBuf;
         {
-            const int row = tid / (2 * kLdsCB), piece = tid % (2 * kLdsCB), u = piece / 2;
-            *reinterpret_cast<uint4 *>(base + u * 2048 + row * 32 + 16 * (piece & 1)) = ra;
+            const int row = tid / (2 * kLdsCB), piece = tid % (2 * kLdsCB);
+            *reinterpret_cast<uint4 *>(base + row * kAr + 16 * piece) = ra;
         }
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
@@ -838,7 +841,7 @@ __global__ __launch_bounds__(kLdsThreads) void gemm_q8_lds_kernel(const int8_t *
 #pragma unroll
             for (int f = 0; f < 2; ++f) {
                 const int row = 32 * wm + 16 * f + li;
-                av[f] = *reinterpret_cast<const long *>(base + u * 2048 + row * 32 + 8 * lk);
+                av[f] = *reinterpret_cast<const long *>(base + row * kAr + u * 32 + 8 * lk);
 #pragma unroll
                 for (int r = 0; r < 4; ++r) da[f][r] = dal[u * 64 + 32 * wm + 16 * f + 4 * lk + r];
             }
