@@ -542,8 +542,22 @@ __global__ __launch_bounds__(kAttnThreads) void conf_attn_kernel(const AttnIO io
 // rows x cols floats (cols % 4 == 0, source rows 16-byte aligned) from
 // global memory (rows ssrc floats apart) into LDS (rows sdst apart), every
 // thread keeping four 16-byte loads in flight.
+// One float4 into LDS at d: a 16-byte store when the rows are 16-byte
+// aligned (stride a multiple of four floats), else four 4-byte ones.
+__device__ __forceinline__ void put_f4(float *d, bool a16, const float4 &v) {
+    if (a16) {
+        *reinterpret_cast<float4 *>(d) = v;
+    } else {
+        d[0] = v.x;
+        d[1] = v.y;
+        d[2] = v.z;
+        d[3] = v.w;
+    }
+}
+
 __device__ __forceinline__ void stage_f4(float *dst, int sdst, const float *src, size_t ssrc, int rows, int cols) {
     const int c4 = cols >> 2, n = rows * c4, nt = blockDim.x;
+    const bool a16 = (sdst & 3) == 0;
     for (int e0 = threadIdx.x; e0 < n; e0 += 4 * nt) {
         float4 v[4];
 #pragma unroll
@@ -554,13 +568,7 @@ __device__ __forceinline__ void stage_f4(float *dst, int sdst, const float *src,
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
             const int e = e0 + u * nt;
-            if (e < n) {
-                float *d = dst + (e / c4) * sdst + 4 * (e % c4);
-                d[0] = v[u].x;
-                d[1] = v[u].y;
-                d[2] = v[u].z;
-                d[3] = v[u].w;
-            }
+            if (e < n) put_f4(dst + (e / c4) * sdst + 4 * (e % c4), a16, v[u]);
         }
     }
 }
@@ -581,25 +589,15 @@ template <int U>
 __device__ __forceinline__ void stage_post(float *dst, int sdst, const float4 (&v)[U], const float *src, size_t ssrc,
                                            int rows, int cols) {
     const int c4 = cols >> 2, n = rows * c4, nt = blockDim.x;
+    const bool a16 = (sdst & 3) == 0;
 #pragma unroll
     for (int u = 0; u < U; ++u) {
         const int e = threadIdx.x + u * nt;
-        if (e < n) {
-            float *d = dst + (e / c4) * sdst + 4 * (e % c4);
-            d[0] = v[u].x;
-            d[1] = v[u].y;
-            d[2] = v[u].z;
-            d[3] = v[u].w;
-        }
+        if (e < n) put_f4(dst + (e / c4) * sdst + 4 * (e % c4), a16, v[u]);
     }
-    for (int e = threadIdx.x + U * nt; e < n; e += nt) {
-        const float4 w = *reinterpret_cast<const float4 *>(src + (size_t)(e / c4) * ssrc + 4 * (e % c4));
-        float *d = dst + (e / c4) * sdst + 4 * (e % c4);
-        d[0] = w.x;
-        d[1] = w.y;
-        d[2] = w.z;
-        d[3] = w.w;
-    }
+    for (int e = threadIdx.x + U * nt; e < n; e += nt)
+        put_f4(dst + (e / c4) * sdst + 4 * (e % c4), a16,
+               *reinterpret_cast<const float4 *>(src + (size_t)(e / c4) * ssrc + 4 * (e % c4)));
 }
 
 // MatMulF32's 6x16 panel route (kernels_amd64.s:5-88) for R rows a_j
@@ -722,7 +720,7 @@ __global__ __launch_bounds__(kAttnLdsThreads) void conf_attn_lds_kernel(const At
                                                                         int hd, float scale,
                                                                         int8_t *__restrict__ xq,
                                                                         float *__restrict__ xs) {
-    extern __shared__ float sm[];
+    extern __shared__ __align__(16) float sm[];
     const int pieces = (ak.bl + RQ - 1) / RQ;
     int px, h, b;
     attn_wg_xcd(px, h, b);
