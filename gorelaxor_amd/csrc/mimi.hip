@@ -104,7 +104,8 @@ __global__ __launch_bounds__(kThreads) void ln64_rows_kernel(const float *__rest
 // (pos0 + r) % cap.
 __global__ void mimi_rope_ring_kernel(float *__restrict__ qkv, int T, int d, int hd, const float *__restrict__ cs,
                                       const float *__restrict__ sn, float *__restrict__ kr, float *__restrict__ vr,
-                                      int cap, long long pos0) {
+                                      int cap, const long long *__restrict__ posd) {
+    const long long pos0 = *posd;
     const size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
     const int half = hd / 2, pairs = d / 2;
     if (idx >= (size_t)T * pairs) return;
@@ -137,10 +138,11 @@ __global__ void mimi_rope_ring_kernel(float *__restrict__ qkv, int T, int d, int
 // values by the same route, over all nk keys.  The head's value rows are
 // staged in LDS ([nk][hd]), keys read from the ring.
 __global__ __launch_bounds__(kThreads) void mimi_attn_kernel(const float *__restrict__ qkv, const float *__restrict__ kr,
-                                                             const float *__restrict__ vr, int cap, long long pos0,
-                                                             int T, int d, int hd, int context, float scale,
-                                                             float *__restrict__ att) {
+                                                             const float *__restrict__ vr, int cap,
+                                                             const long long *__restrict__ posd, int T, int d, int hd,
+                                                             int context, float scale, float *__restrict__ att) {
     extern __shared__ __align__(16) float sm[];
+    const long long pos0 = *posd;
     const int h = blockIdx.x, r = blockIdx.y, tid = threadIdx.x;
     const long long lo0 = pos0 - context + 1 > 0 ? pos0 - context + 1 : 0;
     const int nk = (int)(pos0 + T - lo0);
@@ -326,9 +328,17 @@ struct grx_mimi {
     bool ready = false;     // and the state and work buffers made
     hipEvent_t rope_copied = nullptr;  // the last call's copy of rope_host
     std::vector<void *> allocs;
-    // state
+    // state: the position (the host's copy forms the rotary angles, the
+    // device's is what the kernels read, so a captured call replays)
     long long pos = 0;
+    long long *posd = nullptr;
     float *up_part = nullptr;
+    // the captured call: one graph for the last (latents, input, output)
+    hipGraphExec_t exec = nullptr;
+    int g_n = 0;
+    const float *g_lat = nullptr;
+    float *g_out = nullptr;
+    bool no_graph = false;  // capture refused once: launch kernel by kernel
     // work
     float *x = nullptr, *y = nullptr, *h = nullptr, *o = nullptr, *col = nullptr, *z = nullptr;
     float *qkv = nullptr, *att = nullptr, *f = nullptr, *lat = nullptr, *out = nullptr;
@@ -363,6 +373,8 @@ grx_status malloc_t(grx_mimi *m, size_t count, T **out) {
 }
 
 void release(grx_mimi *m) {
+    if (m->exec) (void)hipGraphExecDestroy(m->exec);
+    m->exec = nullptr;
     for (void *p : m->allocs) (void)hipFree(p);
     m->allocs.clear();
     if (m->rope_host) (void)hipHostFree(m->rope_host);
@@ -443,18 +455,11 @@ grx_status conv_run(grx_mimi *m, hipStream_t st, MConv &c, const float *x, int T
 }
 
 // decode (mimi.go:122-152) of n latents at lat (device) into out (device)
-grx_status enqueue_decode(grx_mimi *m, hipStream_t st, const float *lat, int n, float *out) {
-    const grx_mimi_hparams &hp = m->hp;
-    const int d = hp.d, S = hp.upsample, T = n * S, hd = m->hd, half = hd / 2;
-    unsigned blocks;
-    grx_status s;
-    // latent projection (kern.Linear, no bias), then the upsampling
-    if ((s = lin(m, st, m->quant, lat, n, m->z)) != GRX_OK) return s;
-    gridn((size_t)T * d, &blocks);
-    mimi_up_kernel<<<blocks, kThreads, 0, st>>>(m->z, m->up, n, S, d, m->up_part, m->x);
-    GRX_LAUNCHED("mimi_up_kernel");
-    // the call's rotary angles (nn.go:83-86), as the oracle forms them; the
-    // staging buffer is rewritten once the previous call's copy is done
+// The call's rotary angles (nn.go:83-86), as the oracle forms them, into
+// the pinned staging buffer (host work, before the call's kernels): it is
+// rewritten once the previous call's copy of it is done.
+grx_status rope_angles(grx_mimi *m, int T) {
+    const int half = m->hd / 2;
     GRX_HIP(hipEventSynchronize(m->rope_copied));
     for (int r = 0; r < T; ++r) {
         const float p = (float)(m->pos + r);
@@ -464,8 +469,25 @@ grx_status enqueue_decode(grx_mimi *m, hipStream_t st, const float *lat, int n, 
             m->rope_host[(size_t)(m->tmax + r) * half + i] = (float)sin(a);
         }
     }
+    return GRX_OK;
+}
+
+__global__ void mimi_pos_kernel(long long *posd, int T) { *posd += T; }
+
+// The call's device work, in stream order (captured into a graph, or
+// launched kernel by kernel): the angles' copy, the kernels, and the
+// device position moved on by the call's rows.
+grx_status enqueue_decode(grx_mimi *m, hipStream_t st, const float *lat, int n, float *out) {
+    const grx_mimi_hparams &hp = m->hp;
+    const int d = hp.d, S = hp.upsample, T = n * S, hd = m->hd, half = hd / 2;
+    unsigned blocks;
+    grx_status s;
     GRX_HIP(hipMemcpyAsync(m->rope, m->rope_host, (size_t)2 * m->tmax * half * 4, hipMemcpyHostToDevice, st));
-    GRX_HIP(hipEventRecord(m->rope_copied, st));
+    // latent projection (kern.Linear, no bias), then the upsampling
+    if ((s = lin(m, st, m->quant, lat, n, m->z)) != GRX_OK) return s;
+    gridn((size_t)T * d, &blocks);
+    mimi_up_kernel<<<blocks, kThreads, 0, st>>>(m->z, m->up, n, S, d, m->up_part, m->x);
+    GRX_LAUNCHED("mimi_up_kernel");
     const float scale = (float)(1.0 / sqrt((double)hd));
     for (MLayer &L : m->layers) {
         ln64_rows_kernel<<<T, kThreads, (size_t)d * 4, st>>>(m->x, d, L.n1w, L.n1b, m->h);
@@ -473,10 +495,10 @@ grx_status enqueue_decode(grx_mimi *m, hipStream_t st, const float *lat, int n, 
         if ((s = lin(m, st, L.qkv, m->h, T, m->qkv)) != GRX_OK) return s;
         gridn((size_t)T * d / 2, &blocks);
         mimi_rope_ring_kernel<<<blocks, kThreads, 0, st>>>(m->qkv, T, d, hd, m->rope, m->rope + (size_t)m->tmax * half,
-                                                           L.kr, L.vr, m->cap, m->pos);
+                                                           L.kr, L.vr, m->cap, m->posd);
         GRX_LAUNCHED("mimi_rope_ring_kernel");
-        mimi_attn_kernel<<<dim3(hp.heads, T), kThreads, m->attn_lds, st>>>(m->qkv, L.kr, L.vr, m->cap, m->pos, T, d, hd,
-                                                                          hp.context, scale, m->att);
+        mimi_attn_kernel<<<dim3(hp.heads, T), kThreads, m->attn_lds, st>>>(m->qkv, L.kr, L.vr, m->cap, m->posd, T, d,
+                                                                          hd, hp.context, scale, m->att);
         GRX_LAUNCHED("mimi_attn_kernel");
         if ((s = lin(m, st, L.out, m->att, T, m->h)) != GRX_OK) return s;
         gridn((size_t)T * d, &blocks);
@@ -493,7 +515,8 @@ grx_status enqueue_decode(grx_mimi *m, hipStream_t st, const float *lat, int n, 
         add_scaled_kernel<<<blocks, kThreads, 0, st>>>(m->x, m->h, L.ls2, d, (size_t)T * d);
         GRX_LAUNCHED("add_scaled_kernel");
     }
-    m->pos += T;
+    mimi_pos_kernel<<<1, 1, 0, st>>>(m->posd, T);
+    GRX_LAUNCHED("mimi_pos_kernel");
     // SEANet (runSea, mimi.go:62-108): x and y alternate as the rows
     float *cur = m->x, *nxt = m->y;
     int R = T;
@@ -675,6 +698,7 @@ grx_status alloc_state(grx_mimi *m) {
         if ((s = malloc_t(m, (size_t)m->cap * d, &L.vr)) != GRX_OK) return s;
     }
     if ((s = malloc_t(m, (size_t)hp.upsample * d, &m->up_part)) != GRX_OK) return s;
+    if ((s = malloc_t(m, 1, &m->posd)) != GRX_OK) return s;
     for (MStep &q : m->steps) {
         for (MConv *c : {&q.c, &q.a, &q.bb})
             if (c->k > 0 && c->past > 0 && (s = malloc_t(m, (size_t)c->past * c->cin, &c->prev)) != GRX_OK) return s;
@@ -706,6 +730,7 @@ grx_status zero_state(grx_mimi *m) {
     hipStream_t st = m->ctx->stream;
     const grx_mimi_hparams &hp = m->hp;
     m->pos = 0;
+    GRX_HIP(hipMemsetAsync(m->posd, 0, sizeof(long long), st));
     GRX_HIP(hipMemsetAsync(m->up_part, 0, (size_t)hp.upsample * hp.d * 4, st));
     for (MStep &q : m->steps) {
         for (MConv *c : {&q.c, &q.a, &q.bb})
@@ -882,10 +907,52 @@ static grx_status decode_check(grx_mimi *m, const float *lat, int n, float *out,
     return ensure_ready(m, fn);
 }
 
+// One decode call: the angles on the host, then the call's device work as
+// one captured graph (made again when the latent count or the buffers
+// change; kernel by kernel with GRX_NO_GRAPH=1 or if capture is refused),
+// then the host's position.
+static grx_status run_decode(grx_mimi *m, hipStream_t st, const float *lat, int n, float *out) {
+    grx_status s = rope_angles(m, n * m->hp.upsample);
+    if (s != GRX_OK) return s;
+    if (grx_tune(GRX_TUNE_NO_GRAPH) == 1 || m->no_graph) {
+        if ((s = enqueue_decode(m, st, lat, n, out)) != GRX_OK) return s;
+    } else {
+        if (!m->exec || m->g_n != n || m->g_lat != lat || m->g_out != out) {
+            if (m->exec) GRX_HIP(hipGraphExecDestroy(m->exec));
+            m->exec = nullptr;
+            hipGraph_t g = nullptr;
+            hipError_t e = hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal);
+            if (e == hipSuccess) {
+                const grx_status cs = enqueue_decode(m, st, lat, n, out);
+                e = hipStreamEndCapture(st, &g);
+                if (cs == GRX_OK && e == hipSuccess) e = hipGraphInstantiate(&m->exec, g, nullptr, nullptr, 0);
+                if (g) (void)hipGraphDestroy(g);
+                if (cs != GRX_OK) return cs;
+            }
+            if (e != hipSuccess || !m->exec) {  // capture refused: kernel by kernel from now on
+                (void)hipGetLastError();
+                m->exec = nullptr;
+                m->no_graph = true;
+                if ((s = enqueue_decode(m, st, lat, n, out)) != GRX_OK) return s;
+                GRX_HIP(hipEventRecord(m->rope_copied, st));
+                m->pos += (long long)n * m->hp.upsample;
+                return GRX_OK;
+            }
+            m->g_n = n;
+            m->g_lat = lat;
+            m->g_out = out;
+        }
+        GRX_HIP(hipGraphLaunch(m->exec, st));
+    }
+    GRX_HIP(hipEventRecord(m->rope_copied, st));
+    m->pos += (long long)n * m->hp.upsample;
+    return GRX_OK;
+}
+
 extern "C" grx_status grx_mimi_decode_dev(grx_mimi *m, const float *lat, int n, float *out) {
     grx_status s = decode_check(m, lat, n, out, "grx_mimi_decode_dev");
     if (s != GRX_OK || n == 0) return s;
-    return enqueue_decode(m, m->ctx->stream, lat, n, out);
+    return run_decode(m, m->ctx->stream, lat, n, out);
 }
 
 extern "C" grx_status grx_mimi_decode(grx_mimi *m, const float *lat, int n, float *out) {
@@ -893,7 +960,7 @@ extern "C" grx_status grx_mimi_decode(grx_mimi *m, const float *lat, int n, floa
     if (s != GRX_OK || n == 0) return s;
     hipStream_t st = m->ctx->stream;
     GRX_HIP(hipMemcpyAsync(m->lat, lat, (size_t)n * m->hp.ldim * 4, hipMemcpyHostToDevice, st));
-    if ((s = enqueue_decode(m, st, m->lat, n, m->out)) != GRX_OK) return s;
+    if ((s = run_decode(m, st, m->lat, n, m->out)) != GRX_OK) return s;
     GRX_HIP(hipMemcpyAsync(out, m->out, (size_t)n * m->spl * 4, hipMemcpyDeviceToHost, st));
     GRX_HIP(hipStreamSynchronize(st));
     return GRX_OK;
