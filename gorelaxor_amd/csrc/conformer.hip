@@ -726,16 +726,22 @@ __global__ __launch_bounds__(kAttnLdsThreads) void conf_attn_lds_kernel(const At
     attn_wg_xcd(px, h, b);
     const int blk = px / pieces, r0 = (px % pieces) * RQ;
     const int tid = threadIdx.x, nt = blockDim.x;
-    const int T = io.T, L = io.lens[b];
-    const AttnRows ar = attn_rows(io, b);
-    const int c = ar.c, Tk = ar.Tk, qoff = Tk - T;
+    const int T = io.T;
     const int q0 = blk * ak.bl, q1 = min(T, q0 + ak.bl), nq = q1 - q0;
     if (r0 >= nq) return;
     const int nr = min(RQ, nq - r0);  // rows r0 .. r0+nr-1 of the block
+    // the query rows' loads first: they wait for nothing (the keys' rows
+    // wait for the stream's ring head)
+    const float *qb = io.q + (size_t)b * T * io.ldq;
+    const float *qsrc = qb + (size_t)(q0 + r0) * io.ldq + h * hd;
+    float4 qv4[1];
+    stage_pre(qv4, qsrc, io.ldq, nr, hd);
+    const int L = io.lens[b];
+    const AttnRows ar = attn_rows(io, b);
+    const int c = ar.c, Tk = ar.Tk, qoff = Tk - T;
     int k0, k1;
     block_keys(ak, q0, q1, qoff, Tk, L, c, k0, k1);
     const int nk = k1 - k0;
-    const float *qb = io.q + (size_t)b * T * io.ldq;
     const int nqb = hd / 32;
     if (nk <= 0) {
         for (int g = tid >> 5; g < nr * nqb; g += nt >> 5) {
@@ -769,16 +775,17 @@ __global__ __launch_bounds__(kAttnLdsThreads) void conf_attn_lds_kernel(const At
     // position rows jlo + nq-1-(r0+i) + kk: from pb = jlo + nq-1-(r0+nr-1) on, nk + nr - 1 of them
     const int pb = jlo + nq - 1 - (r0 + nr - 1), npr = nk + nr - 1;
     const float *pp = ar.pp + (size_t)pb * io.ldp + h * hd, *vp = kb + io.vo + h * hd;
-    stage_f4(qu, sq, qb + (size_t)(q0 + r0) * io.ldq + h * hd, io.ldq, nr, hd);
-    // keys k0.. of the head, rows sq apart
-    stage_f4(st, sq, kb + h * hd, io.ldkv, nk, hd);
-    // the position rows' and the values' loads in flight while the scores
-    // are formed (they go to LDS once the keys, then the position rows, are
-    // done with)
+    // the keys k0.. of the head (rows sq apart in LDS), and the position
+    // rows' and the values' loads, all in flight with the query rows' (the
+    // position rows and values go to LDS once the keys, then the position
+    // rows, are done with)
     constexpr int kPre = 5;
-    float4 pv[kPre], vv[kPre];
+    float4 kv4[4], pv[kPre], vv[kPre];
+    stage_pre(kv4, kb + h * hd, io.ldkv, nk, hd);
     stage_pre(pv, pp, io.ldp, npr, hd);
     stage_pre(vv, vp, io.ldkv, nk, hd);
+    stage_post(qu, sq, qv4, qsrc, io.ldq, nr, hd);
+    stage_post(st, sq, kv4, kb + h * hd, io.ldkv, nk, hd);
     __syncthreads();
     for (int e = tid; e < nr * hd; e += nt) {
         const int i = e / hd, j = e % hd;
@@ -930,8 +937,13 @@ size_t attn_smem_floats(int T, int hd) {
 
 // ---------------------------------------------------------------- convolution module
 
-// GLU of the pointwise output (encoder.go:350-361): g = a * sigmoid(b) with
-// sigmoid(v) = 1/(1 + expf(-v)) (the scalar expf), rows at or past the
+// Products of this many rows or fewer (one or two 16-row groups) may take
+// the blocks' LayerNorms in their prologues (CONF_FUSE=3; by default only
+// one-row products do).
+constexpr int kFuseLnRows = 32;
+
+// GLU of the pointwise output (encoder.go:350-361) by grx_glu_pair, the
+// output's rows paired as grx_glu_row lays them out, rows at or past the
 // utterance's valid rows lens[b] zeroed.
 __global__ void conf_glu_kernel(const float *__restrict__ a, int R, int T, int D, const int *__restrict__ lens,
                                 float *__restrict__ g) {
@@ -943,25 +955,27 @@ __global__ void conf_glu_kernel(const float *__restrict__ a, int R, int T, int D
         float v = 0.f;
         if (t < lens[b]) {
             const float *ar = a + (size_t)row * 2 * D;
-            const float sg = __fdiv_rn(1.0f, __fadd_rn(1.0f, grx_expf_go(-ar[D + c])));
-            v = __fmul_rn(ar[c], sg);
+            v = grx_glu_pair(ar[grx_glu_row(c, false)], ar[grx_glu_row(c, true)]);
         }
         g[idx] = v;
     }
 }
 
 // The gated frames before a call's first one (encoder.go:372-377): a
-// stream's last padL frames in a ring of padL rows per stream (the oldest
-// at slot ctl[2]), or none (offline: those taps are skipped).
+// stream's frames in a ring of cap >= padL + chunk rows per stream, frame
+// ti of this call at slot (ctl[2] + ti) mod cap (so the call's own frames
+// never overwrite the padL before them), or none (offline: those taps are
+// skipped).
 struct ConvPrev {
-    const float *ring;  // [B][padL][D], or null
+    const float *ring;  // [B][cap][D], or null
+    int cap;
     const int *ctl;
 };
 // Frame ti < 0 of utterance b, or null when there is none.
 __device__ inline const float *conv_prev_row(const ConvPrev &cp, int b, int ti, int padL, int D) {
     if (cp.ring == nullptr || ti < -padL) return nullptr;
-    const int slot = (cp.ctl[2] + padL + ti) % padL;
-    return cp.ring + ((size_t)b * padL + slot) * D;
+    const int slot = (cp.ctl[2] + cp.cap + ti) % cp.cap;
+    return cp.ring + ((size_t)b * cp.cap + slot) * D;
 }
 
 // The depthwise convolution (encoder.go:362-385: from the bias, w*x unfused
@@ -1135,15 +1149,15 @@ __global__ __launch_bounds__(64) void conf_dwconv_lane_kernel(const float *__res
     const __amdgpu_buffer_rsrc_t wr = dw_rsrc(w, (uint32_t)K * D * 4);
     // (no branches among the loads: every one is issued before any is used)
     float xv[kDwLaneK], wv[kDwLaneK];
-    const int head = RING ? cp.ctl[2] : 0;                 // the ring's oldest slot
+    const int head = RING ? cp.ctl[2] : 0;                 // the call's first frame's slot
 #pragma unroll
     for (int j = 0; j < kDwLaneK; ++j) {
         const int ti = f0 + j;
         const int tc = min(max(ti, 0), T - 1), jc = min(j, K - 1);
         if constexpr (RING) {
-            // frames before the call from the stream's ring of padL rows
-            const int slot = (head + padL + max(ti, -padL)) % padL;
-            const float *row = ti < 0 ? cp.ring + ((size_t)b * padL + slot) * D : g + ((size_t)b * T + tc) * D;
+            // frames before the call from the stream's ring
+            const int slot = (head + cp.cap + max(ti, -padL)) % cp.cap;
+            const float *row = ti < 0 ? cp.ring + ((size_t)b * cp.cap + slot) * D : g + ((size_t)b * T + tc) * D;
             xv[j] = row[c];
         } else {
             xv[j] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(gr, (tc * D + c) * 4, 0, 0));
@@ -1158,6 +1172,90 @@ __global__ __launch_bounds__(64) void conf_dwconv_lane_kernel(const float *__res
     const float sl = __fdiv_rn(a, __fadd_rn(grx_exp8(__fsub_rn(0.0f, a)), 1.0f));
     const size_t row = (size_t)b * T + t;
     quant32_store(sl, xq + row * D + c, xs + row * (D / 32) + c / 32, c & 31);
+}
+
+// The depthwise convolution with its LayerNorm (a causal streaming model's
+// conv_ln), rows of at most 1024 channels (D % 32 == 0) and kernels of at
+// most 16 taps: one workgroup per row, thread = four channels (a float4
+// piece: a row's loads are a quarter of the instructions one channel a
+// thread takes, which bound a lone workgroup's load time), every tap's
+// loads issued at once (the call's earlier frames from the stream's ring)
+// and one chain per channel over the taps in range, as
+// conf_dwconv_lane_kernel; the row's values to LDS, then every wave takes
+// the row's mean and inv (wave_ln32_stats: kern.LayerNorm,
+// internal/kern/mathx.go:55-75) and ends its own pieces: the
+// normalization, SiLU and the rounding (8 pieces in 8 lanes a block).
+template <int KM>
+__global__ __launch_bounds__(256) void conf_dwconv_ln_kernel(const float *__restrict__ g, int T, int D, int K,
+                                                             int padL, const ConvPrev cp,
+                                                             const float *__restrict__ w,
+                                                             const float *__restrict__ dwb,
+                                                             const float *__restrict__ cn_w,
+                                                             const float *__restrict__ cn_b,
+                                                             int8_t *__restrict__ xq, float *__restrict__ xs) {
+    __shared__ __align__(16) float rowv[1024];
+    const int r = blockIdx.x, t = r % T, b = r / T, tid = threadIdx.x;
+    const int npc = D / 4, P = min(tid, npc - 1);           // this thread's piece (clamped: loads stay in bounds)
+    const bool ring = cp.ring != nullptr;
+    const int lo_t = ring ? -padL : 0;                      // the first frame a tap may read
+    const int f0 = t - padL;                                // the frame tap 0 reads
+    const int jlo = max(0, lo_t - f0), jhi = min(K, T - f0);  // the taps in range
+    const int head = ring ? cp.ctl[2] : 0;                  // the call's first frame's slot
+    float4 xv[KM], wv[KM];
+#pragma unroll
+    for (int j = 0; j < KM; ++j) {
+        const int ti = f0 + j;
+        const int tc = min(max(ti, 0), T - 1), jc = min(j, K - 1);
+        const float *src = (ring && ti < 0)
+                               ? cp.ring + ((size_t)b * cp.cap + (head + cp.cap + max(ti, -padL)) % cp.cap) * D
+                               : g + ((size_t)b * T + tc) * D;
+        xv[j] = reinterpret_cast<const float4 *>(src)[P];
+        wv[j] = reinterpret_cast<const float4 *>(w + (size_t)jc * D)[P];
+    }
+    const float4 gw = reinterpret_cast<const float4 *>(cn_w)[P], gb = reinterpret_cast<const float4 *>(cn_b)[P];
+    float4 o = dwb != nullptr ? reinterpret_cast<const float4 *>(dwb)[P] : make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+    for (int j = 0; j < KM; ++j) {
+        if (j >= jlo && j < jhi) {
+            o.x = __fadd_rn(o.x, __fmul_rn(wv[j].x, xv[j].x));
+            o.y = __fadd_rn(o.y, __fmul_rn(wv[j].y, xv[j].y));
+            o.z = __fadd_rn(o.z, __fmul_rn(wv[j].z, xv[j].z));
+            o.w = __fadd_rn(o.w, __fmul_rn(wv[j].w, xv[j].w));
+        }
+    }
+    if (tid < npc) reinterpret_cast<float4 *>(rowv)[tid] = o;
+    __syncthreads();
+    constexpr int NP = 4;
+    const int lane = tid & 63;
+    float4 v4[NP];
+#pragma unroll
+    for (int j = 0; j < NP; ++j) v4[j] = reinterpret_cast<const float4 *>(rowv)[min(j * 64 + lane, npc - 1)];
+    float mean, inv;
+    wave_ln32_stats<NP>(v4, npc, lane, mean, inv);
+    auto end = [&](float v, float wg, float bg) {
+        float a = __fsub_rn(v, mean);
+        a = __fmul_rn(a, inv);
+        a = __fmul_rn(a, wg);
+        a = __fadd_rn(a, bg);
+        return __fdiv_rn(a, __fadd_rn(grx_exp8(__fsub_rn(0.0f, a)), 1.0f));
+    };
+    const float4 v = make_float4(end(o.x, gw.x, gb.x), end(o.y, gw.y, gb.y), end(o.z, gw.z, gb.z),
+                                 end(o.w, gw.w, gb.w));
+    float amax = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
+#pragma unroll
+    for (int s = 4; s > 0; s >>= 1) {
+        const float tt = __shfl_xor(amax, s, 8);
+        amax = tt > amax ? tt : amax;
+    }
+    if (tid >= npc) return;
+    const float id = amax != 0.0f ? __fdiv_rn(127.0f, amax) : 0.0f;
+    auto q1 = [&](float x) {
+        float q = rintf(__fmul_rn(x, id));
+        q = fminf(fmaxf(q, -128.0f), 127.0f);
+        return (uint32_t)(uint8_t)(int8_t)(int)q;
+    };
+    *reinterpret_cast<uint32_t *>(xq + (size_t)r * D + 4 * tid) = q1(v.x) | q1(v.y) << 8 | q1(v.z) << 16 | q1(v.w) << 24;
+    if ((tid & 7) == 0) xs[(size_t)r * (D / 32) + tid / 8] = __fmul_rn(amax, grx_bits_f32(0x3c010204u));
 }
 
 // ---------------------------------------------------------------- stream caches
@@ -1184,20 +1282,20 @@ __global__ void kv_ring_append_kernel(const float *__restrict__ qkv, int B, int 
     }
 }
 
-// The chunk's last min(T, padL) gated frames into each stream's
-// convolution ring (stream.go:302-305): frame i to slot (ctl[2] + i) % padL,
-// over the oldest ones.
+// The chunk's gated frames into each stream's convolution ring
+// (stream.go:302-305 keeps the last padL of them): frame i to slot (ctl[2]
+// + i) % cap, over frames older than the padL before the chunk.
 __global__ void conv_ring_append_kernel(const float *__restrict__ g, int B, int T, int D, float *__restrict__ ring,
-                                        int padL, const int *__restrict__ ctl) {
-    const int head = ctl[2], n = min(T, padL), i0 = T - n;
-    const size_t total = (size_t)B * n * D;
+                                        int cap, const int *__restrict__ ctl) {
+    const int head = ctl[2];
+    const size_t total = (size_t)B * T * D;
     for (size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x; idx < total;
          idx += (size_t)gridDim.x * blockDim.x) {
         const int col = (int)(idx % D);
         const size_t rt = idx / D;
-        const int i = i0 + (int)(rt % n), b = (int)(rt / n);
-        const int slot = (head + i) % padL;
-        ring[((size_t)b * padL + slot) * D + col] = g[((size_t)b * T + i) * D + col];
+        const int i = (int)(rt % T), b = (int)(rt / T);
+        const int slot = (head + i) % cap;
+        ring[((size_t)b * cap + slot) * D + col] = g[rt * D + col];
     }
 }
 
@@ -1237,6 +1335,7 @@ struct grx_conformer {
     size_t attn_smem = 0;
     float *mel = nullptr, *sub0 = nullptr, *suby = nullptr, *x = nullptr, *qkv = nullptr, *pp = nullptr;
     float *subx = nullptr;  // float input of a float32 pointwise Linear
+    float *x2 = nullptr;  // the residual rows' second buffer (blocks with fused LayerNorms alternate)
     float *conv = nullptr, *glu = nullptr, *pos = nullptr;
     int8_t *xq = nullptr, *fq = nullptr, *pos_q = nullptr;  // fq: the rounded SiLU output of W1
     float *xs = nullptr, *fs = nullptr, *pos_s = nullptr;
@@ -1374,19 +1473,40 @@ float half_to_float(uint16_t h) {
     return out;
 }
 
+// Rows of a pointwise1 weight (2d rows of `bytes` each) or bias (4
+// bytes) reordered into the GLU's pairs: row grx_glu_row(c, false) is row
+// c (channel c's a-row), grx_glu_row(c, true) row d + c (its b-row).  The
+// products of each row are unchanged (the same blocks in the same order).
+std::vector<uint8_t> glu_pair_rows(const uint8_t *src, int d, size_t bytes) {
+    std::vector<uint8_t> out((size_t)2 * d * bytes);
+    for (int c = 0; c < d; ++c) {
+        memcpy(out.data() + (size_t)grx_glu_row(c, false) * bytes, src + (size_t)c * bytes, bytes);
+        memcpy(out.data() + (size_t)grx_glu_row(c, true) * bytes, src + (size_t)(d + c) * bytes, bytes);
+    }
+    return out;
+}
+
 // A pointwise-convolution weight: Q8_0 rows as they are, or float16
-// widened and rounded by Weight.ToQ8 (conformer/model.go:397-402).
-grx_status pointwise_weight(grx_conformer *m, const std::string &name, int rows, int cols, grx_weight **out) {
+// widened and rounded by Weight.ToQ8 (conformer/model.go:397-402); glu:
+// pointwise1's rows paired for the GLU (glu_pair_rows).
+grx_status pointwise_weight(grx_conformer *m, const std::string &name, int rows, int cols, bool glu,
+                            grx_weight **out) {
     const auto &raw = m->host.at(name);
     const size_t n = (size_t)rows * cols;
-    if (raw.size() == q8b(rows, cols)) return grx_weight_q8_create(m->ctx, rows, cols, raw.data(), raw.size(), out);
-    if (raw.size() != n * 2) return grx_fail(GRX_ESIZE, "tensor %s is neither Q8_0 nor float16 %dx%d", name.c_str(), rows, cols);
-    std::vector<float> v(n);
-    const uint16_t *h = reinterpret_cast<const uint16_t *>(raw.data());
-    for (size_t i = 0; i < n; ++i) v[i] = half_to_float(h[i]);
-    std::vector<uint8_t> q(q8b(rows, cols));
-    grx_status s = grx_to_q8(m->ctx, rows, cols, v.data(), q.data());
-    if (s != GRX_OK) return s;
+    std::vector<uint8_t> q;
+    if (raw.size() == q8b(rows, cols)) {
+        q.assign(raw.begin(), raw.end());
+    } else {
+        if (raw.size() != n * 2)
+            return grx_fail(GRX_ESIZE, "tensor %s is neither Q8_0 nor float16 %dx%d", name.c_str(), rows, cols);
+        std::vector<float> v(n);
+        const uint16_t *h = reinterpret_cast<const uint16_t *>(raw.data());
+        for (size_t i = 0; i < n; ++i) v[i] = half_to_float(h[i]);
+        q.resize(q8b(rows, cols));
+        grx_status s = grx_to_q8(m->ctx, rows, cols, v.data(), q.data());
+        if (s != GRX_OK) return s;
+    }
+    if (glu) q = glu_pair_rows(q.data(), rows / 2, q8b(1, cols));
     return grx_weight_q8_create(m->ctx, rows, cols, q.data(), q.size(), out);
 }
 
@@ -1490,16 +1610,21 @@ grx_status cfinalize_tensors(grx_conformer *m) {
             pos_cat.insert(pos_cat.end(), t.begin(), t.end());
         }
         if ((s = mat(p + "attn.linear_out.weight", d, d, &B.out)) != GRX_OK) return s;
-        if ((s = pointwise_weight(m, p + "conv.pointwise1.weight", 2 * d, d, &B.pw1)) != GRX_OK) return s;
-        if ((s = pointwise_weight(m, p + "conv.pointwise2.weight", d, d, &B.pw2)) != GRX_OK) return s;
+        if ((s = pointwise_weight(m, p + "conv.pointwise1.weight", 2 * d, d, true, &B.pw1)) != GRX_OK) return s;
+        if ((s = pointwise_weight(m, p + "conv.pointwise2.weight", d, d, false, &B.pw2)) != GRX_OK) return s;
+        B.pw1_b = nullptr;
+        if (auto it = m->host.find(p + "conv.pointwise1.bias"); it != m->host.end()) {  // optional
+            const std::vector<uint8_t> pb = glu_pair_rows(it->second.data(), d, sizeof(float));
+            if ((s = upload(m, pb.data(), pb.size(), &B.pw1_b)) != GRX_OK) return s;
+        }
         struct {
             const char *n;
             float **v;
         } vecs[] = {{"norm_attn.weight", &B.norm_attn_w}, {"norm_attn.bias", &B.norm_attn_b},
                     {"attn.linear_out.bias", &B.out_b},   {"attn.pos_bias_u", &B.pos_u},
                     {"attn.pos_bias_v", &B.pos_v},        {"norm_conv.weight", &B.norm_conv_w},
-                    {"norm_conv.bias", &B.norm_conv_b},   {"conv.pointwise1.bias", &B.pw1_b},
-                    {"conv.pointwise2.bias", &B.pw2_b},   {"conv.depthwise.bias", &B.dw_b},
+                    {"norm_conv.bias", &B.norm_conv_b},   {"conv.pointwise2.bias", &B.pw2_b},
+                    {"conv.depthwise.bias", &B.dw_b},
                     {"norm_out.weight", &B.norm_out_w},   {"norm_out.bias", &B.norm_out_b}};
         for (auto &v : vecs)
             if ((s = cvec(m, p + v.n, v.v)) != GRX_OK) return s;
@@ -1635,7 +1760,8 @@ bool dw_win_ok(const grx_conformer_hparams &hp) {
 // The working buffers of B utterances of `frames` mel frames whose
 // pre-encoder gives T rows each, Tp kept (the blocks' rows).
 struct CBuf {
-    float *mel = nullptr, *sub0 = nullptr, *suby = nullptr, *subx = nullptr, *x = nullptr, *qkv = nullptr;
+    float *mel = nullptr, *sub0 = nullptr, *suby = nullptr, *subx = nullptr, *x = nullptr, *x2 = nullptr;
+    float *qkv = nullptr;
     float *conv = nullptr, *glu = nullptr;
     int8_t *xq = nullptr, *fq = nullptr;
     float *xs = nullptr, *fs = nullptr;
@@ -1658,6 +1784,7 @@ grx_status cbuf_alloc(const grx_conformer *m, std::vector<void *> &w, int B, int
     if ((s = calloc_t(w, R * hp.dff, &b->fq)) != GRX_OK) return s;
     if ((s = calloc_t(w, R * hp.dff / 32, &b->fs)) != GRX_OK) return s;
     if ((s = calloc_t(w, R * d, &b->x)) != GRX_OK) return s;
+    if ((s = calloc_t(w, R * d, &b->x2)) != GRX_OK) return s;
     if ((s = calloc_t(w, R * 3 * d, &b->qkv)) != GRX_OK) return s;
     if ((s = calloc_t(w, R * 2 * d, &b->conv)) != GRX_OK) return s;
     if ((s = calloc_t(w, R * d, &b->glu)) != GRX_OK) return s;
@@ -1681,7 +1808,7 @@ grx_status cshape(grx_conformer *m, int B, int frames) {
     auto &w = m->work;
     CBuf b;
     if ((s = cbuf_alloc(m, w, B, frames, T, &b)) != GRX_OK) return s;
-    m->mel = b.mel, m->sub0 = b.sub0, m->suby = b.suby, m->subx = b.subx, m->x = b.x, m->qkv = b.qkv;
+    m->mel = b.mel, m->sub0 = b.sub0, m->suby = b.suby, m->subx = b.subx, m->x = b.x, m->x2 = b.x2, m->qkv = b.qkv;
     m->conv = b.conv, m->glu = b.glu, m->xq = b.xq, m->xs = b.xs, m->fq = b.fq, m->fs = b.fs;
     if ((s = calloc_t(w, (size_t)(2 * T - 1) * hp.layers * d, &m->pp)) != GRX_OK) return s;
     if ((s = calloc_t(w, (size_t)(2 * T - 1) * d, &m->pos)) != GRX_OK) return s;
@@ -1742,6 +1869,7 @@ struct CRun {
     int cap;
     float *conv_ring;
     size_t conv_ring_layer;
+    int conv_cap;
 };
 
 grx_status enqueue_run(grx_conformer *m, const CRun &r, hipStream_t st) {
@@ -1773,9 +1901,60 @@ grx_status enqueue_run(grx_conformer *m, const CRun &r, hipStream_t st) {
     }
     sub_flatten_kernel<<<R, 256, 0, st>>>(bf.sub0, T, F3, c, r.valid, cs, r.drop, Tp, bf.xq, bf.xs);
     GRX_LAUNCHED("sub_flatten_kernel");
+    const size_t row_smem = (size_t)d * 4;
+    const float scale = (float)(1.0 / std::sqrt((double)hd));
+    const int nblk = (Tp + r.keys.bl - 1) / r.keys.bl;
+    // Which products take their LayerNorm, the GLU and the caches' copies
+    // into their own launch (decided once: every block has the same shapes).
+    // The LayerNorms by default only for one row (the one-row GEMV's
+    // prologue: a streaming chunk step at right context 0, 2.31 -> 2.02 ms);
+    // on the K-split kernel each workgroup normalizes its 16-row group
+    // itself, which measured slower than the LayerNorm launches at 14 and
+    // 16 rows (2.61 -> 2.76 ms a chunk step at right context 13), so there
+    // only when CONF_FUSE=3 asks.
+    const CBlock &B0 = m->blk[0];
+    auto probe = [&](const grx_weight *w, int epi, bool ln, bool ln2, bool ring) {
+        GemmOut o;
+        o.epi = epi;
+        o.y = bf.qkv;
+        o.ldc = w->rows;
+        o.lens = r.lens;
+        o.T = Tp;
+        if (ln) {
+            o.x = bf.x;
+            o.lda = d;
+            o.ln_w = B0.norm_attn_w;
+            o.ln_b = B0.norm_attn_b;
+            if (ln2) {
+                o.ln_w2 = B0.norm_attn_w;
+                o.ln_b2 = B0.norm_attn_b;
+                o.x_out = bf.x2;
+            }
+        }
+        if (ring) {
+            o.ring.p = bf.glu;
+            o.ring.ctl = r.ctl;
+        }
+        return grx_gemm_q8_fuses(w, R, o);
+    };
+    const bool kv_ring = r.kv_ring != nullptr, cv_ring = r.conv_ring != nullptr && padL > 0;
+    const int fz = grx_tune(GRX_TUNE_CONF_FUSE);  // 0 none, 3 LayerNorm prologues on up to 32 rows
+    const bool fuse_ln = R <= kFuseLnRows && fz != 0 && (fz == 3 || R == 1) && bf.x2 != nullptr &&
+                         probe(B0.qkv, GRX_GEMM_STORE, true, false, kv_ring) &&
+                         probe(B0.pw1, GRX_GEMM_GLU, true, false, cv_ring) &&
+                         probe(B0.ff1.w1, GRX_GEMM_SILU_Q, true, true, false) &&
+                         probe(B0.ff2.w1, GRX_GEMM_SILU_Q, true, false, false);
+    const bool fuse_glu = fz != 0 && probe(B0.pw1, GRX_GEMM_GLU, fuse_ln, false, cv_ring);
+    const bool fuse_kv = kv_ring && fz != 0 &&
+                         probe(B0.qkv, GRX_GEMM_STORE, fuse_ln, false, true);
+    // the residual rows: with the LayerNorms fused, each block from the
+    // second on continues in the other buffer (its first product stores the
+    // previous norm_out there), chosen so that the last block ends in bf.x
+    float *x = fuse_ln && (hp.layers - 1) % 2 != 0 ? bf.x2 : bf.x;
+    auto other = [&](float *p) { return p == bf.x ? bf.x2 : bf.x; };
     {  // output Linear, then xscale (encoder.go:445-451; stream.go:259)
         GemmOut o;
-        o.y = bf.x;
+        o.y = x;
         o.ldc = d;
         if (hp.xscaling) {
             o.epi = GRX_GEMM_SCALE;
@@ -1783,44 +1962,89 @@ grx_status enqueue_run(grx_conformer *m, const CRun &r, hipStream_t st) {
         }
         if ((s = grx_gemm_q8_launch_ex(st, m->wout, bf.xq, bf.xs, R, m->outb, o)) != GRX_OK) return s;
     }
-    const size_t row_smem = (size_t)d * 4;
     // the first block's feed-forward LayerNorm
-    if ((s = ln_rows_launch<false, true>(st, R, bf.x, d, m->blk[0].ff1.norm_w, m->blk[0].ff1.norm_b,
-                                                                  nullptr, nullptr, bf.xq, bf.xs)) != GRX_OK) return s;
-    const float scale = (float)(1.0 / std::sqrt((double)hd));
-    const int nblk = (Tp + r.keys.bl - 1) / r.keys.bl;
+    if (!fuse_ln && (s = ln_rows_launch<false, true>(st, R, x, d, B0.ff1.norm_w, B0.ff1.norm_b, nullptr, nullptr,
+                                                     bf.xq, bf.xs)) != GRX_OK)
+        return s;
+    // a product's fused LayerNorm of the residual rows (ln2: the previous
+    // block's norm_out first, kept in the other buffer, which the block
+    // then continues in)
+    auto with_ln = [&](GemmOut &o, const float *w1, const float *b1, const float *w2, const float *b2) {
+        if (!fuse_ln) return;
+        o.x = x;
+        o.lda = d;
+        o.ln_w = w1;
+        o.ln_b = b1;
+        if (w2 != nullptr) {
+            o.ln_w2 = w2;
+            o.ln_b2 = b2;
+            o.x_out = other(x);
+        }
+    };
     for (int i = 0; i < hp.layers; ++i) {
         const CBlock &Bk = m->blk[i];
-        auto ff_pair = [&](const CFF &F) -> grx_status {
-            // x += 0.5 * W2 . SiLU(W1 . LN(x)) (encoder.go:244-251); LN(x) is in xq
+        // x += 0.5 * W2 . SiLU(W1 . LN(x)) (encoder.go:244-251); LN(x) is in
+        // xq, or made by W1's prologue (the first feed-forward of a block
+        // after the first: the previous block's norm_out, then its own LN)
+        auto ff_pair = [&](const CFF &F, const CBlock *prev) -> grx_status {
             GemmOut o1;
             o1.epi = GRX_GEMM_SILU_Q;
             o1.yq = bf.fq;
             o1.ys = bf.fs;
+            if (prev != nullptr)
+                with_ln(o1, prev->norm_out_w, prev->norm_out_b, F.norm_w, F.norm_b);
+            else
+                with_ln(o1, F.norm_w, F.norm_b, nullptr, nullptr);
             grx_status q = grx_gemm_q8_launch_ex(st, F.w1, bf.xq, bf.xs, R, F.b1, o1);
             if (q != GRX_OK) return q;
+            if (o1.x_out != nullptr) x = o1.x_out;
             GemmOut o2;
-            o2.y = bf.x;
+            o2.y = x;
             o2.ldc = d;
             o2.epi = GRX_GEMM_AXPY_HALF;
             return grx_gemm_q8_launch_ex(st, F.w2, bf.fq, bf.fs, R, F.b2, o2);
         };
-        if ((s = ff_pair(Bk.ff1)) != GRX_OK) return s;
+        if ((s = ff_pair(Bk.ff1, fuse_ln && i > 0 ? &m->blk[i - 1] : nullptr)) != GRX_OK) return s;
         // attention (encoder.go:259-330)
-        if ((s = ln_rows_launch<false, true>(st, R, bf.x, d, Bk.norm_attn_w, Bk.norm_attn_b, nullptr,
-                                                                      nullptr, bf.xq, bf.xs)) != GRX_OK) return s;
-        if ((s = grx_gemm_q8_launch(st, Bk.qkv, bf.xq, bf.xs, R, Bk.qkv_b, bf.qkv, 3 * d)) != GRX_OK) return s;
+        if (!fuse_ln && (s = ln_rows_launch<false, true>(st, R, x, d, Bk.norm_attn_w, Bk.norm_attn_b, nullptr, nullptr,
+                                                         bf.xq, bf.xs)) != GRX_OK)
+            return s;
+        float *ring = r.kv_ring ? r.kv_ring + r.kv_ring_layer * i : nullptr;
+        {
+            GemmOut o;
+            o.y = bf.qkv;
+            o.ldc = 3 * d;
+            with_ln(o, Bk.norm_attn_w, Bk.norm_attn_b, nullptr, nullptr);
+            if (fuse_kv) {
+                // the chunk's keys and values (columns d..3d) into the
+                // stream's ring as well: row i to slot (head + c + i) % cap
+                // and + cap (kv_ring_append_kernel's layout)
+                o.ring.p = ring;
+                o.ring.bstride = (size_t)2 * r.cap * 2 * d;
+                o.ring.width = 2 * d;
+                o.ring.col0 = d;
+                o.ring.cap = r.cap;
+                o.ring.twice = 1;
+                o.ring.T = Tp;
+                o.ring.ctl = r.ctl;
+                o.ring.c0 = 0;
+                o.ring.c1 = 1;
+            }
+            if ((s = grx_gemm_q8_launch_ex(st, Bk.qkv, bf.xq, bf.xs, R, Bk.qkv_b, o)) != GRX_OK) return s;
+        }
         AttnIO io{};
         io.q = bf.qkv;
         io.ldq = 3 * d;
         io.lens = r.lens;
         io.T = Tp;
-        if (r.kv_ring) {
+        if (ring) {
             // the chunk's keys and values join the stream's ring, which then
             // holds every key of the chunk's queries
-            float *ring = r.kv_ring + r.kv_ring_layer * i;
-            kv_ring_append_kernel<<<grid_for((size_t)R * 2 * d), 256, 0, st>>>(bf.qkv, B, Tp, d, ring, r.cap, r.ctl);
-            GRX_LAUNCHED("kv_ring_append_kernel");
+            if (!fuse_kv) {
+                kv_ring_append_kernel<<<grid_for((size_t)R * 2 * d), 256, 0, st>>>(bf.qkv, B, Tp, d, ring, r.cap,
+                                                                                   r.ctl);
+                GRX_LAUNCHED("kv_ring_append_kernel");
+            }
             io.kv = ring;
             io.ldkv = 2 * d;
             io.vo = d;
@@ -1853,19 +2077,52 @@ grx_status enqueue_run(grx_conformer *m, const CRun &r, hipStream_t st) {
         GRX_LAUNCHED("conf_attn_kernel");
         {
             GemmOut o;
-            o.y = bf.x;
+            o.y = x;
             o.ldc = d;
             o.epi = GRX_GEMM_ADD;
             if ((s = grx_gemm_q8_launch_ex(st, Bk.out, bf.xq, bf.xs, R, Bk.out_b, o)) != GRX_OK) return s;
         }
         // convolution module (encoder.go:343-397)
-        if ((s = ln_rows_launch<false, true>(st, R, bf.x, d, Bk.norm_conv_w, Bk.norm_conv_b, nullptr,
-                                                                      nullptr, bf.xq, bf.xs)) != GRX_OK) return s;
-        if ((s = grx_gemm_q8_launch(st, Bk.pw1, bf.xq, bf.xs, R, Bk.pw1_b, bf.conv, 2 * d)) != GRX_OK) return s;
+        if (!fuse_ln && (s = ln_rows_launch<false, true>(st, R, x, d, Bk.norm_conv_w, Bk.norm_conv_b, nullptr, nullptr,
+                                                         bf.xq, bf.xs)) != GRX_OK)
+            return s;
         ConvPrev cp{};
-        if (r.conv_ring && padL > 0) {
+        if (cv_ring) {
             cp.ring = r.conv_ring + r.conv_ring_layer * i;
+            cp.cap = r.conv_cap;
             cp.ctl = r.ctl;
+        }
+        // pointwise1 (its rows paired for the GLU), the GLU (rows past an
+        // utterance's valid rows zeroed), and the chunk's gated frames into
+        // the stream's convolution ring: frame i to slot (ctl[2] + i) % cap
+        if (fuse_glu) {
+            GemmOut o;
+            o.epi = GRX_GEMM_GLU;
+            o.y = bf.glu;
+            o.ldc = d;
+            o.lens = r.lens;
+            o.T = Tp;
+            with_ln(o, Bk.norm_conv_w, Bk.norm_conv_b, nullptr, nullptr);
+            if (cv_ring) {
+                o.ring.p = const_cast<float *>(cp.ring);
+                o.ring.bstride = (size_t)cp.cap * d;
+                o.ring.width = d;
+                o.ring.cap = cp.cap;
+                o.ring.T = Tp;
+                o.ring.ctl = r.ctl;
+                o.ring.c0 = 2;
+            }
+            if ((s = grx_gemm_q8_launch_ex(st, Bk.pw1, bf.xq, bf.xs, R, Bk.pw1_b, o)) != GRX_OK) return s;
+        } else {
+            if ((s = grx_gemm_q8_launch(st, Bk.pw1, bf.xq, bf.xs, R, Bk.pw1_b, bf.conv, 2 * d)) != GRX_OK) return s;
+            conf_glu_kernel<<<grid_for((size_t)R * d), 256, 0, st>>>(bf.conv, R, Tp, d, r.lens, bf.glu);
+            GRX_LAUNCHED("conf_glu_kernel");
+            if (cp.ring) {
+                conv_ring_append_kernel<<<grid_for((size_t)R * d), 256, 0, st>>>(bf.glu, B, Tp, d,
+                                                                                  const_cast<float *>(cp.ring),
+                                                                                  cp.cap, r.ctl);
+                GRX_LAUNCHED("conv_ring_append_kernel");
+            }
         }
         // the depthwise kernel: 0 a workgroup per row, 1 LDS windows, 2 a
         // wave per frame (measured at the parakeet shape: 5.2 us against 10.6
@@ -1876,9 +2133,20 @@ grx_status enqueue_run(grx_conformer *m, const CRun &r, hipStream_t st) {
         if (dw < 0 || dw > 2) dw = dw_lane && R <= 1024 ? 2 : 1;
         if (dw == 2 && !dw_lane) dw = 1;
         if (dw == 1 && !r.dw_win) dw = 0;
-        conf_glu_kernel<<<grid_for((size_t)R * d), 256, 0, st>>>(bf.conv, R, Tp, d, r.lens, bf.glu);
-        GRX_LAUNCHED("conf_glu_kernel");
-        if (hp.conv_ln)
+        // with the LayerNorm: a row per workgroup of float4 pieces where
+        // the row has at most 1024 channels and the kernel at most 16 taps
+        // (one row at d 1024: 9.2 -> 4.8 us from the workgroup's start to
+        // its last store, against a channel a thread), else a row per
+        // workgroup whose reductions span it
+        const bool dw_ln4 = d <= 1024 && hp.conv_kernel <= 16 && grx_tune(GRX_TUNE_CONF_DW) != 0;
+        const int dw_ln_threads = 64 * grx_ceil_div(d / 4, 64);
+        if (hp.conv_ln && dw_ln4 && hp.conv_kernel <= 12)
+            conf_dwconv_ln_kernel<12><<<R, dw_ln_threads, 0, st>>>(bf.glu, Tp, d, hp.conv_kernel, padL, cp, Bk.dw,
+                                                                   Bk.dw_b, Bk.cn_w, Bk.cn_b, bf.xq, bf.xs);
+        else if (hp.conv_ln && dw_ln4)
+            conf_dwconv_ln_kernel<16><<<R, dw_ln_threads, 0, st>>>(bf.glu, Tp, d, hp.conv_kernel, padL, cp, Bk.dw,
+                                                                   Bk.dw_b, Bk.cn_w, Bk.cn_b, bf.xq, bf.xs);
+        else if (hp.conv_ln)
             conf_dwconv_kernel<true><<<R, kRowThreads, row_smem, st>>>(bf.glu, Tp, d, hp.conv_kernel, padL, cp, Bk.dw,
                                                                        Bk.dw_b, Bk.cn_w, Bk.cn_b, bf.xq, bf.xs);
         else if (dw == 2 && cp.ring != nullptr)
@@ -1896,31 +2164,33 @@ grx_status enqueue_run(grx_conformer *m, const CRun &r, hipStream_t st) {
                                                                         Bk.dw, Bk.dw_b, Bk.cn_w, Bk.cn_b, bf.xq,
                                                                         bf.xs);
         GRX_LAUNCHED("conf_dwconv_kernel");
-        if (cp.ring) {  // after the convolution has read the frames they replace
-            conv_ring_append_kernel<<<grid_for((size_t)B * std::min(Tp, padL) * d), 256, 0, st>>>(
-                bf.glu, B, Tp, d, const_cast<float *>(cp.ring), padL, r.ctl);
-            GRX_LAUNCHED("conv_ring_append_kernel");
-        }
         {
             GemmOut o;
-            o.y = bf.x;
+            o.y = x;
             o.ldc = d;
             o.epi = GRX_GEMM_ADD;
             if ((s = grx_gemm_q8_launch_ex(st, Bk.pw2, bf.xq, bf.xs, R, Bk.pw2_b, o)) != GRX_OK) return s;
         }
-        // second feed-forward, then norm_out (and the next block's first LayerNorm)
-        if ((s = ln_rows_launch<false, true>(st, R, bf.x, d, Bk.ff2.norm_w, Bk.ff2.norm_b, nullptr,
-                                                                      nullptr, bf.xq, bf.xs)) != GRX_OK) return s;
-        if ((s = ff_pair(Bk.ff2)) != GRX_OK) return s;
+        // second feed-forward, then norm_out (and the next block's first
+        // LayerNorm; fused: the next block's first product does both)
+        if (!fuse_ln && (s = ln_rows_launch<false, true>(st, R, x, d, Bk.ff2.norm_w, Bk.ff2.norm_b, nullptr, nullptr,
+                                                         bf.xq, bf.xs)) != GRX_OK)
+            return s;
+        if ((s = ff_pair(Bk.ff2, nullptr)) != GRX_OK) return s;
         if (i + 1 < hp.layers) {
-            const CFF &N = m->blk[i + 1].ff1;
-            if ((s = ln_rows_launch<true, true>(st, R, bf.x, d, Bk.norm_out_w, Bk.norm_out_b,
-                                                                         N.norm_w, N.norm_b, bf.xq, bf.xs)) != GRX_OK) return s;
+            if (!fuse_ln) {
+                const CFF &N = m->blk[i + 1].ff1;
+                if ((s = ln_rows_launch<true, true>(st, R, x, d, Bk.norm_out_w, Bk.norm_out_b, N.norm_w, N.norm_b,
+                                                    bf.xq, bf.xs)) != GRX_OK)
+                    return s;
+            }
         } else {
-            if ((s = ln_rows_launch<true, false>(st, R, bf.x, d, Bk.norm_out_w, Bk.norm_out_b,
-                                                                          nullptr, nullptr, nullptr, nullptr)) != GRX_OK) return s;
+            if ((s = ln_rows_launch<true, false>(st, R, x, d, Bk.norm_out_w, Bk.norm_out_b, nullptr, nullptr, nullptr,
+                                                 nullptr)) != GRX_OK)
+                return s;
         }
     }
+    if (x != bf.x) return grx_fail(GRX_EINVAL, "conformer: the blocks ended in the wrong buffer");
     return GRX_OK;
 }
 
@@ -1936,7 +2206,8 @@ grx_status enqueue_encode(grx_conformer *m, hipStream_t st) {
     r.B = m->B;
     r.frames = m->frames;
     r.T = r.Tp = T;
-    r.b.mel = m->mel, r.b.sub0 = m->sub0, r.b.suby = m->suby, r.b.subx = m->subx, r.b.x = m->x, r.b.qkv = m->qkv;
+    r.b.mel = m->mel, r.b.sub0 = m->sub0, r.b.suby = m->suby, r.b.subx = m->subx, r.b.x = m->x, r.b.x2 = m->x2;
+    r.b.qkv = m->qkv;
     r.b.conv = m->conv, r.b.glu = m->glu, r.b.xq = m->xq, r.b.xs = m->xs, r.b.fq = m->fq, r.b.fs = m->fs;
     r.valid = m->valid;
     r.lens = m->valid + m->B;
@@ -2012,12 +2283,13 @@ struct grx_conformer_stream {
     int B = 0;
     grx_conformer_stream_geom g{};
     int cap = 0, padL = 0, maxfirst = 0;
+    int conv_cap = 0;  // rows of a stream's convolution ring: padL + chunk
     bool dw_win = false;
     int steps = 0;                          // chunks done
     int kv_len = 0, kv_head = 0, conv_head = 0;
     std::vector<void *> allocs;
     float *kv_ring = nullptr;    // [layers][B][2*cap][2d]: keys | values
-    float *conv_ring = nullptr;  // [layers][B][padL][d]
+    float *conv_ring = nullptr;  // [layers][B][conv_cap][d]
     float *pp = nullptr;         // [left+2*chunk-1][layers*d]: positions maxfirst down, projected
     int *ctl = nullptr;          // device [4 + 2B]: c, kv head, conv head, 0, mel frames[B], rows[B]
     int *ctl_host = nullptr;     // pinned
@@ -2149,14 +2421,15 @@ grx_status stream_run(grx_conformer_stream *s, const float *mel, int nf, const i
     run.kv_ring_layer = (size_t)B * 2 * s->cap * 2 * hp.d;
     run.cap = s->cap;
     run.conv_ring = s->padL > 0 ? s->conv_ring : nullptr;
-    run.conv_ring_layer = (size_t)B * s->padL * hp.d;
+    run.conv_ring_layer = (size_t)B * s->conv_cap * hp.d;
+    run.conv_cap = s->conv_cap;
     if ((r = run_graph(st, &sh.graph, &sh.exec, [m, run](hipStream_t q) { return enqueue_run(m, run, q); })) != GRX_OK)
         return r;
     // the caches after the chunk (stream.go:296-306)
     const int Tk = s->kv_len + Tp, keep = std::min(Tk, s->g.left);
     s->kv_head = (s->kv_head + Tk - keep) % s->cap;
     s->kv_len = keep;
-    if (s->padL > 0) s->conv_head = (s->conv_head + Tp) % s->padL;
+    if (s->padL > 0) s->conv_head = (s->conv_head + Tp) % s->conv_cap;
     s->steps++;
     return GRX_OK;
 }
@@ -2205,6 +2478,7 @@ extern "C" grx_status grx_conformer_stream_create(grx_conformer *m, int right, i
     s->g = g;
     s->cap = g.left + g.chunk;
     s->padL = pad_left(hp);
+    s->conv_cap = s->padL + g.chunk;
     s->maxfirst = g.left + g.chunk - 1;
     s->dw_win = dw_win_ok(hp);
     auto fail = [&](grx_status e) {
@@ -2221,7 +2495,7 @@ extern "C" grx_status grx_conformer_stream_create(grx_conformer *m, int right, i
     }
     const int d = hp.d, count = g.left + 2 * g.chunk - 1;
     if ((r = calloc_t(s->allocs, (size_t)hp.layers * batch * 2 * s->cap * 2 * d, &s->kv_ring)) != GRX_OK) return fail(r);
-    if ((r = calloc_t(s->allocs, (size_t)hp.layers * batch * std::max(s->padL, 1) * d, &s->conv_ring)) != GRX_OK)
+    if ((r = calloc_t(s->allocs, (size_t)hp.layers * batch * s->conv_cap * d, &s->conv_ring)) != GRX_OK)
         return fail(r);
     if ((r = calloc_t(s->allocs, (size_t)count * hp.layers * d, &s->pp)) != GRX_OK) return fail(r);
     if ((r = calloc_t(s->allocs, (size_t)4 + 2 * batch, &s->ctl)) != GRX_OK) return fail(r);
@@ -2232,7 +2506,7 @@ extern "C" grx_status grx_conformer_stream_create(grx_conformer *m, int right, i
     }
     // newEncState: zero convolution caches (newEncState, stream.go:80-88),
     // and the projected positions left+chunk-1 .. -(chunk-1) of every layer
-    if (hipMemset(s->conv_ring, 0, (size_t)hp.layers * batch * std::max(s->padL, 1) * d * 4) != hipSuccess)
+    if (hipMemset(s->conv_ring, 0, (size_t)hp.layers * batch * s->conv_cap * d * 4) != hipSuccess)
         return fail(grx_hip_fail(hipGetLastError(), "hipMemset"));
     {
         std::vector<float> pos = rel_pos(s->maxfirst, count, d);

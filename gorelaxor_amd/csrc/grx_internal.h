@@ -117,7 +117,8 @@ enum {
     GRX_TUNE_GEMM_NS,         // 16-column tiles per wave of the register kernels: 1, 2 or 4
     GRX_TUNE_GEMM_KB,         // blocks per wave of the K-split kernel: 4, 8 or 16
     GRX_TUNE_GEMV_WAVES,      // waves per tile of the GEMV: 1, 2, 4, 8 or 16
-    GRX_TUNE_GEMV1,           // 0: one-row products on the general GEMV kernel
+    GRX_TUNE_GEMV1,           // 0: one-row products on the general GEMV kernel, 2: every one-row
+                              // matrix-core product on the one-row GEMV
     GRX_TUNE_CONF_ATTN_RQ,    // conformer attention: 0 unstaged, 8 or 16 query rows per workgroup
     GRX_TUNE_FUSE_LN,         // 0: batched decoder LayerNorm rows in their own launch
     GRX_TUNE_FUSE_XSCORES,    // 0: whisper cross scores without the fused query product
@@ -130,6 +131,9 @@ enum {
     GRX_TUNE_FUSE_SELF_ATTN,  // 0: whisper's q|k|v product and self-attention in launches of their own
     GRX_TUNE_CONF_DW,         // conformer depthwise convolution: 0 a workgroup per row, 1 windows in LDS,
                               // 2 a wave per frame
+    GRX_TUNE_CONF_FUSE,       // 0: conformer LayerNorms, GLU and cache copies in launches of their own,
+                              // 3: LayerNorms in the prologues of products of up to 32 rows too
+                              // (default: of one-row products only)
     GRX_TUNE_COUNT
 };
 int grx_tune(int id);
@@ -306,7 +310,8 @@ __device__ __forceinline__ float grx_gelu_at(float v, int i, int n) {
 }
 
 // Launch helpers of the product kernels (q8_gemv.hip).
-enum { GRX_PRO_PREQ = 0, GRX_PRO_QUANT = 1, GRX_PRO_LN = 2, GRX_PRO_EMBED_LN = 3, GRX_PRO_LN64 = 4 };
+enum { GRX_PRO_PREQ = 0, GRX_PRO_QUANT = 1, GRX_PRO_LN = 2, GRX_PRO_EMBED_LN = 3, GRX_PRO_LN64 = 4,
+       GRX_PRO_LN2 = 5 };  // LN2: LayerNorm (ln_w, ln_b) stored to x_out, then LayerNorm (ln_w2, ln_b2)
 enum {
     GRX_EPI_STORE = 0,   // y = c
     GRX_EPI_RESID = 1,   // y = resid + c
@@ -318,8 +323,46 @@ enum {
     GRX_EPI_XSCORES = 7,  // one row, tile = one head of 64: the head's cross-attention
                           // scores over a run of 64 keys (blockIdx.y) instead of y
     GRX_EPI_AXPY_HALF = 8,  // y = fma(0.5, c, resid) (a macaron feed-forward's residual)
-    GRX_EPI_SILU_Q = 9      // SiLU of c rounded to Q8_0 into yq/ys only (whole 32-row blocks)
+    GRX_EPI_SILU_Q = 9,     // SiLU of c rounded to Q8_0 into yq/ys only (whole 32-row blocks)
+    GRX_EPI_GLU = 10        // rows paired as a GLU: y[ch] = a * sigmoid(b) (grx_glu_pair)
 };
+
+// A copy of a product's outputs into per-stream rings of rows (a streaming
+// encoder's caches): activation row r is row t = r % T of stream b = r / T,
+// and goes to slot (ctl[c0] + ctl[c1] + t) % cap (c1 < 0: no second term)
+// of stream b's ring (bstride floats apart, rows of width floats); output
+// column n >= col0 lands in column n - col0.  twice: also to slot + cap (a
+// ring read as one run of rows from any slot).
+struct RingCopy {
+    float *p = nullptr;
+    size_t bstride = 0;
+    int width = 0, col0 = 0, cap = 1, twice = 0, T = 1;
+    const int *ctl = nullptr;
+    int c0 = 0, c1 = -1;
+};
+__device__ __forceinline__ float *ring_row(const RingCopy &r, int head, int arow) {
+    const int b = arow / r.T, t = arow - b * r.T;
+    return r.p + (size_t)b * r.bstride + (size_t)((head + t) % r.cap) * r.width;
+}
+__device__ __forceinline__ int ring_head(const RingCopy &r) {
+    return r.ctl[r.c0] + (r.c1 >= 0 ? r.ctl[r.c1] : 0);
+}
+__device__ __forceinline__ void ring_put(const RingCopy &r, float *row, int col, float v) {
+    row[col] = v;
+    if (r.twice) row[(size_t)r.cap * r.width + col] = v;
+}
+
+// The convolution module's GLU (conformer/encoder.go:350-361) on a product
+// whose 2d output rows are stored paired: in each group of 32 rows, rows
+// 0..15 are a-rows of channels 16g..16g+15 and rows 16..31 their b-rows
+// (channel c's a-row is row c, its b-row row d + c, of the weight as
+// stored in the file).  g = a * sigmoid(b), sigmoid(v) = 1/(1 + expf(-v))
+// with the scalar expf; rows at or past the utterance's valid rows are 0.
+__host__ __device__ __forceinline__ int grx_glu_row(int ch, bool b) { return 32 * (ch >> 4) + (ch & 15) + (b ? 16 : 0); }
+__device__ __forceinline__ float grx_glu_pair(float a, float b) {
+    const float sg = __fdiv_rn(1.0f, __fadd_rn(1.0f, grx_expf_go(-b)));
+    return __fmul_rn(a, sg);
+}
 
 struct GemvArgs {
     const int8_t *qs;
@@ -385,6 +428,13 @@ struct GemvArgs {
     // (blockIdx.z) with x, xq/xs, y, resid and yq/ys M*g rows on and
     // pos_add M*g larger
     int chunks;
+    // LN2: the second LayerNorm's gain and bias
+    const float *ln_w2, *ln_b2;
+    // STORE and GLU: outputs also copied into rings (ring.p set)
+    RingCopy ring;
+    // GLU: valid rows per stream (rows of a stream T apart in the launch)
+    const int *lens;
+    int T;
 };
 
 grx_status grx_gemv_launch(hipStream_t st, int m, int pro, int epi, const GemvArgs &a,
@@ -403,7 +453,8 @@ grx_status grx_embed_ln_quant_rows(hipStream_t st, const int *tok, const int *po
                                    int8_t *xq, float *xs);
 
 // Epilogues of the matrix-core product (q8_gemm.hip).
-enum { GRX_GEMM_STORE = 0, GRX_GEMM_ADD = 1, GRX_GEMM_AXPY_HALF = 2, GRX_GEMM_SCALE = 3, GRX_GEMM_SILU_Q = 4 };
+enum { GRX_GEMM_STORE = 0, GRX_GEMM_ADD = 1, GRX_GEMM_AXPY_HALF = 2, GRX_GEMM_SCALE = 3, GRX_GEMM_SILU_Q = 4,
+       GRX_GEMM_GLU = 5 };
 struct GemmOut {
     float *y = nullptr;  // [m][ldc] (STORE writes it, ADD/AXPY_HALF update it)
     int ldc = 0;
@@ -415,7 +466,28 @@ struct GemmOut {
     // ordered chain from one run of blocks to the next when the weight has
     // more blocks than one workgroup holds (few rows only); NULL: none
     float *carry = nullptr;
+    // GLU (weight rows paired as grx_glu_row lays them out): y [m][ldc]
+    // holds rows/2 channels; rows of stream b = r / T at or past lens[b]
+    // are zeroed
+    const int *lens = nullptr;
+    int T = 1;
+    // STORE and GLU: outputs also copied into rings
+    RingCopy ring;
+    // A fused prologue instead of pre-rounded activations: x [m][lda]
+    // LayerNorm'd (ln_w, ln_b) and rounded in the product; with ln_w2 set,
+    // the first LayerNorm is stored to x_out [m][lda] and a second (ln_w2,
+    // ln_b2) is rounded.  x_out must not alias x.  Only where
+    // grx_gemm_q8_fuses says so (xq/xs then unused).
+    const float *x = nullptr;
+    int lda = 0;
+    const float *ln_w = nullptr, *ln_b = nullptr, *ln_w2 = nullptr, *ln_b2 = nullptr;
+    float *x_out = nullptr;
 };
+// Whether the product of m rows takes o's fused parts (prologue, GLU, ring
+// copy) on the kernel it would run: the one-row GEMV, or the K-split kernel
+// with staged activations in one run of blocks (a prologue: rows of at most
+// 1024 values, at most two 16-row groups).
+bool grx_gemm_q8_fuses(const grx_weight *w, int m, const GemmOut &o);
 grx_status grx_gemm_q8_launch_ex(hipStream_t st, const grx_weight *w, const int8_t *xq, const float *xs, int m,
                                  const float *bias, const GemmOut &o);
 // Fewest activation rows that take the matrix-core product (GRX_GEMM_MIN_M

@@ -397,11 +397,11 @@ __device__ __forceinline__ void ln_wave_values(const float4 (&xv)[NP], int npc, 
     exact = ln_sum_exact(a, mn);
 }
 
-// kern.LayerNorm (mathx.go:55-75) of the wave's row in place: xv[j] =
-// (v - mean) * inv * w + b, rounded step by step.
+// kern.LayerNorm's mean and inv (mathx.go:59-69) of the wave's row, the
+// same in every lane.
 template <int NP, bool CHECK = true>
-__device__ __forceinline__ void wave_ln32(float4 (&xv)[NP], const float4 (&wv)[NP], const float4 (&bv)[NP], int npc,
-                                         int lane) {
+__device__ __forceinline__ void wave_ln32_stats(const float4 (&xv)[NP], int npc, int lane, float &mean_out,
+                                               float &inv_out) {
     const int K = 4 * npc, depth = ln_wave_depth(npc);
     double s, a;
     bool exact;
@@ -417,7 +417,17 @@ __device__ __forceinline__ void wave_ln32(float4 (&xv)[NP], const float4 (&wv)[N
         vs = wave_serial_sum(xv, npc, [mean](float v) { return ln32_sq(v, mean); });
         inv_d = 1.0 / sqrt(vs / (double)K + 1e-5);
     }
-    const float inv = (float)inv_d;
+    mean_out = mean;
+    inv_out = (float)inv_d;
+}
+
+// kern.LayerNorm (mathx.go:55-75) of the wave's row in place: xv[j] =
+// (v - mean) * inv * w + b, rounded step by step.
+template <int NP, bool CHECK = true>
+__device__ __forceinline__ void wave_ln32(float4 (&xv)[NP], const float4 (&wv)[NP], const float4 (&bv)[NP], int npc,
+                                         int lane) {
+    float mean, inv;
+    wave_ln32_stats<NP, CHECK>(xv, npc, lane, mean, inv);
     auto nrm = [&](float v, float w, float b) {
         float t = __fsub_rn(v, mean);
         t = __fmul_rn(t, inv);

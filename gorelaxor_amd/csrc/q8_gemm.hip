@@ -24,6 +24,7 @@
 #include <type_traits>
 
 #include "grx_internal.h"
+#include "grx_ln.h"
 
 namespace {
 
@@ -36,6 +37,8 @@ typedef int v4i __attribute__((ext_vector_type(4)));
 //   SCALE      y = c * scale
 //   SILU_Q     SiLU(c) of the AVX route (c / (EXP8(0 - c) + 1)), rounded to
 //              Q8_0 per 32 outputs into yq [m][rows], ys [m][rows/32]
+//   GLU        rows paired (grx_glu_row): y [m][rows/2] = a * sigmoid(b)
+//              (the K-split kernel and the one-row GEMV only)
 //
 // A wave computes 16 activation rows x 16*NS weight rows (NS 16x16 MFMA
 // tiles sharing the A fragment; NS of 1 or 2 give small products more
@@ -466,14 +469,35 @@ __global__ __launch_bounds__(64 * ks_max_waves(NS, KB)) void gemm_q8_ks_kernel(
 constexpr int kss_row(int kb) { return kb * 32 + 16; }
 constexpr int kss_bytes(int kb) { return 16 * kss_row(kb) + 16 * kb * 4; }
 
-template <int EPI, int NS, int KB>
-__global__ __launch_bounds__(64 * ks_max_waves(NS, KB), 4) void gemm_q8_kss_kernel(
+// The K-split kernel's fused parts: PRO 1 builds the staged activations
+// from x rows by LayerNorm and rounding, PRO 2 by two LayerNorms with the
+// first stored to x_out; the GLU epilogue's valid rows; a ring copy of the
+// outputs.
+struct KsFuse {
+    const float *x;
+    int lda;
+    const float *lw, *lb, *lw2, *lb2;
+    float *x_out;
+    const int *lens;
+    int T;
+    RingCopy ring;
+};
+constexpr int kKsProPieces = 4;  // a fused prologue's rows: at most 4 float4 pieces a lane (1024 values)
+
+// A fused prologue's LayerNorms (float64 sums and their checks) need more
+// than the 128 registers a lane has at four waves a SIMD: those
+// instantiations run at most kKsProWaves waves a workgroup, two a SIMD.
+constexpr int kKsProWaves = 8;
+template <int EPI, int NS, int KB, int PRO = 0>
+__global__ __launch_bounds__(64 * (PRO != 0 ? kKsProWaves : ks_max_waves(NS, KB)), PRO != 0 ? 2 : 4) void
+gemm_q8_kss_kernel(
     const int8_t *__restrict__ qs, const uint16_t *__restrict__ ds, int rows, int nb, const int8_t *__restrict__ xq,
     const float *__restrict__ xs, int m, const float *__restrict__ bias, float *__restrict__ y, int ldc, float scale,
     int8_t *__restrict__ yq, float *__restrict__ ys, int ncg, int nrf, int bbeg, int bend, const float *init,
-    int ldi) {
+    int ldi, const KsFuse f) {
     static_assert(NS == 1 || NS == 2, "16 or 32 weight rows per tile");
     static_assert(KB % 4 == 0, "blocks per wave in whole groups of four");
+    static_assert(EPI != GRX_GEMM_GLU || NS == 2, "GLU pairs take 32-row tiles");
     __shared__ float cx[2][NS * 4][64];
     extern __shared__ __align__(16) int8_t kss_stage[];
     const int lane = threadIdx.x & 63;
@@ -517,20 +541,22 @@ __global__ __launch_bounds__(64 * ks_max_waves(NS, KB), 4) void gemm_q8_kss_kern
 
     // every load of the wave's blocks in flight at once (block indices past
     // bend are clamped and their results never used; rows past m likewise)
-    constexpr int NA = KB / 2;  // 16-byte loads of the 16 rows x KB blocks
+    constexpr int NA = PRO == 0 ? KB / 2 : 1;  // 16-byte loads of the 16 rows x KB blocks
     int4 ra[NA];
-#pragma unroll
-    for (int j = 0; j < NA; ++j) {
-        const int e = j * 64 + lane, i = e / (2 * KB), pc = e % (2 * KB);
-        const unsigned row = (unsigned)min(16 * rf + i, m - 1), b = (unsigned)min(b0 + pc / 2, bend - 1);
-        ra[j] = *reinterpret_cast<const int4 *>(xq + (row * K + b * GRX_QK + (pc & 1) * 16));
-    }
     constexpr int DQ = KB / 4;  // float4s of scales per row
     float4 rd = make_float4(0.f, 0.f, 0.f, 0.f);
-    if (lane < 16 * DQ) {
-        const int i = lane / DQ, q = lane % DQ;
-        const unsigned row = (unsigned)min(16 * rf + i, m - 1), b = (unsigned)min(b0 + 4 * q, bend - 4);
-        rd = *reinterpret_cast<const float4 *>(xs + (row * (unsigned)nb + b));
+    if constexpr (PRO == 0) {
+#pragma unroll
+        for (int j = 0; j < NA; ++j) {
+            const int e = j * 64 + lane, i = e / (2 * KB), pc = e % (2 * KB);
+            const unsigned row = (unsigned)min(16 * rf + i, m - 1), b = (unsigned)min(b0 + pc / 2, bend - 1);
+            ra[j] = *reinterpret_cast<const int4 *>(xq + (row * K + b * GRX_QK + (pc & 1) * 16));
+        }
+        if (lane < 16 * DQ) {
+            const int i = lane / DQ, q = lane % DQ;
+            const unsigned row = (unsigned)min(16 * rf + i, m - 1), b = (unsigned)min(b0 + 4 * q, bend - 4);
+            rd = *reinterpret_cast<const float4 *>(xs + (row * (unsigned)nb + b));
+        }
     }
     long bv[KB][NS];
 #pragma unroll
@@ -561,17 +587,98 @@ __global__ __launch_bounds__(64 * ks_max_waves(NS, KB), 4) void gemm_q8_kss_kern
                 yr[s][r] = n < rows ? y[(size_t)arow * ldc + n] : 0.0f;
             }
     }
+    // the ring copy's head (the stream's control word), read early
+    const int rhead = f.ring.p != nullptr ? ring_head(f.ring) : 0;
+    if constexpr (PRO == 0) {
 #pragma unroll
-    for (int j = 0; j < NA; ++j) {
-        const int e = j * 64 + lane, i = e / (2 * KB), pc = e % (2 * KB);
-        *reinterpret_cast<int4 *>(sa + i * RS + pc * 16) = ra[j];
-    }
-    if (lane < 16 * DQ) {
-        const int i = lane / DQ, q = lane % DQ;
-        sd[(4 * q + 0) * 16 + i] = rd.x;
-        sd[(4 * q + 1) * 16 + i] = rd.y;
-        sd[(4 * q + 2) * 16 + i] = rd.z;
-        sd[(4 * q + 3) * 16 + i] = rd.w;
+        for (int j = 0; j < NA; ++j) {
+            const int e = j * 64 + lane, i = e / (2 * KB), pc = e % (2 * KB);
+            *reinterpret_cast<int4 *>(sa + i * RS + pc * 16) = ra[j];
+        }
+        if (lane < 16 * DQ) {
+            const int i = lane / DQ, q = lane % DQ;
+            sd[(4 * q + 0) * 16 + i] = rd.x;
+            sd[(4 * q + 1) * 16 + i] = rd.y;
+            sd[(4 * q + 2) * 16 + i] = rd.z;
+            sd[(4 * q + 3) * 16 + i] = rd.w;
+        }
+    } else {
+        // the fused prologue (one run of all nb blocks, K <= 1024): wave w
+        // takes rows w, w + ks, .. of the 16-row group, two at a time with
+        // their loads in flight together (the gains and biases, the same for
+        // every row, loaded once), each held as NP float4 pieces a lane,
+        // LayerNorm'd by wave_ln32 (kern.LayerNorm, internal/kern/mathx.go:
+        // 55-75), and rounds each 32-value block (8 pieces in 8 lanes;
+        // quantU8, q8int.go:88-105) into the stage of the wave that owns the
+        // block.  Rows past m are not staged: their products are never
+        // stored.
+        constexpr int NP = kKsProPieces;
+        const int npc = (int)(K / 4);
+        float4 wv[NP], bw[NP], wv2[PRO == 2 ? NP : 1], bw2[PRO == 2 ? NP : 1];
+#pragma unroll
+        for (int j = 0; j < NP; ++j) {
+            const int P = min(j * 64 + lane, npc - 1);
+            wv[j] = reinterpret_cast<const float4 *>(f.lw)[P];
+            bw[j] = reinterpret_cast<const float4 *>(f.lb)[P];
+            if constexpr (PRO == 2) {
+                wv2[j] = reinterpret_cast<const float4 *>(f.lw2)[P];
+                bw2[j] = reinterpret_cast<const float4 *>(f.lb2)[P];
+            }
+        }
+        auto one_row = [&](float4 (&xv)[NP], int i) {
+            const int row = 16 * rf + i;
+            wave_ln32<NP>(xv, wv, bw, npc, lane);
+            if constexpr (PRO == 2) {
+                // a block's norm_out (conformer/encoder.go:426), kept by the
+                // first column group, then the next block's LayerNorm
+                if (cg == 0) {
+                    float4 *xo = reinterpret_cast<float4 *>(f.x_out + (size_t)row * f.lda);
+#pragma unroll
+                    for (int j = 0; j < NP; ++j)
+                        if (j * 64 + lane < npc) xo[j * 64 + lane] = xv[j];
+                }
+                wave_ln32<NP>(xv, wv2, bw2, npc, lane);
+            }
+#pragma unroll
+            for (int j = 0; j < NP; ++j) {
+                const float4 v = xv[j];
+                float amax = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
+#pragma unroll
+                for (int o = 4; o > 0; o >>= 1) {
+                    const float tt = __shfl_xor(amax, o, 8);
+                    amax = tt > amax ? tt : amax;
+                }
+                const int P = j * 64 + lane;
+                if (P >= npc) continue;
+                const float id = amax != 0.0f ? __fdiv_rn(127.0f, amax) : 0.0f;
+                auto q1 = [&](float x) {
+                    float tq = rintf(__fmul_rn(x, id));
+                    tq = fminf(fmaxf(tq, -128.0f), 127.0f);
+                    return (uint32_t)(uint8_t)(int8_t)(int)tq;
+                };
+                const uint32_t pk = q1(v.x) | q1(v.y) << 8 | q1(v.z) << 16 | q1(v.w) << 24;
+                const int blk = P >> 3, ow = blk / KB, u = blk - ow * KB;
+                int8_t *so = kss_stage + ow * kss_bytes(KB);
+                *reinterpret_cast<uint32_t *>(so + i * RS + u * GRX_QK + 4 * (P & 7)) = pk;
+                if ((P & 7) == 0)
+                    reinterpret_cast<float *>(so + 16 * RS)[u * 16 + i] = __fmul_rn(amax, grx_bits_f32(0x3c010204u));
+            }
+        };
+        for (int i0 = wave; i0 < 16 && 16 * rf + i0 < m; i0 += 2 * ks) {
+            const int i1 = i0 + ks;
+            const bool two = i1 < 16 && 16 * rf + i1 < m;  // uniform across the wave
+            float4 xa[NP], xb[NP];
+            const float4 *x0 = reinterpret_cast<const float4 *>(f.x + (size_t)(16 * rf + i0) * f.lda);
+            const float4 *x1 = reinterpret_cast<const float4 *>(f.x + (size_t)(16 * rf + (two ? i1 : i0)) * f.lda);
+#pragma unroll
+            for (int j = 0; j < NP; ++j) {
+                const int P = min(j * 64 + lane, npc - 1);
+                xa[j] = x0[P];
+                xb[j] = x1[P];
+            }
+            one_row(xa, i0);
+            if (two) one_row(xb, i1);
+        }
     }
     __syncthreads();
 
@@ -691,6 +798,23 @@ __global__ __launch_bounds__(64 * ks_max_waves(NS, KB), 4) void gemm_q8_kss_kern
             }
             if (lk == 0) ys[(size_t)arow * nr + n0 / GRX_QK] = __fmul_rn(amax, grx_bits_f32(0x3c010204u));
         }
+    } else if constexpr (EPI == GRX_GEMM_GLU) {
+        // the tile's rows n0..n0+15 are the a-rows of channels n0/2 ..
+        // n0/2 + 15 and rows n0+16.. their b-rows: lane (li, lk) holds both
+        // for channels n0/2 + 4 lk .. +3 of activation row arow
+        if (arow >= m || n0 >= rows) return;
+        const int sb = arow / f.T;
+        const bool live = arow - sb * f.T < f.lens[sb];
+        const int ch = (n0 >> 1) + 4 * lk;
+        float v[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) v[r] = live ? grx_glu_pair(c[0][r], c[1][r]) : 0.0f;
+        *reinterpret_cast<float4 *>(y + (size_t)arow * ldc + ch) = make_float4(v[0], v[1], v[2], v[3]);
+        if (f.ring.p != nullptr) {
+            float *rr = ring_row(f.ring, rhead, arow);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) ring_put(f.ring, rr, ch + r - f.ring.col0, v[r]);
+        }
     } else {
         if (arow >= m) return;
 #pragma unroll
@@ -704,6 +828,18 @@ __global__ __launch_bounds__(64 * ks_max_waves(NS, KB), 4) void gemm_q8_kss_kern
                 if constexpr (EPI == GRX_GEMM_ADD) yp[r] = __fadd_rn(kResid ? yr[s][r] : yp[r], c[s][r]);
                 if constexpr (EPI == GRX_GEMM_AXPY_HALF) yp[r] = __fmaf_rn(0.5f, c[s][r], kResid ? yr[s][r] : yp[r]);
                 if constexpr (EPI == GRX_GEMM_SCALE) yp[r] = __fmul_rn(c[s][r], scale);
+            }
+        }
+        if constexpr (EPI == GRX_GEMM_STORE) {
+            if (f.ring.p != nullptr) {
+                float *rr = ring_row(f.ring, rhead, arow);
+#pragma unroll
+                for (int s = 0; s < NS; ++s)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        const int n = n0 + 16 * s + 4 * lk + r;
+                        if (n < rows && n >= f.ring.col0) ring_put(f.ring, rr, n - f.ring.col0, c[s][r]);
+                    }
             }
         }
     }
@@ -979,26 +1115,30 @@ int pick_ns(int m, int rows, int epi) {
 // 32-column tiles (whole Q8_0 blocks).  A carried chain runs in 16 waves x
 // 8 blocks (8 x 1280 x 5120: 23.6 us on the GEMV, two runs here).  False
 // when a workgroup of ks_max_waves waves cannot hold the weight's blocks.
-bool pick_ks(int m, int nb, int rows, int epi, bool carry, bool sa, int *ns, int *kb) {
-    const bool few = grx_ceil_div(m, 16) <= 2 && epi != GRX_GEMM_SILU_Q;
+bool pick_ks(int m, int nb, int rows, int epi, bool carry, bool sa, bool pro, int *ns, int *kb) {
+    const bool pair = epi == GRX_GEMM_SILU_Q || epi == GRX_GEMM_GLU;  // whole 32-row tiles
+    const bool few = grx_ceil_div(m, 16) <= 2 && !pair;
     int n, k;
     if (sa) {
-        n = (epi == GRX_GEMM_SILU_Q || (!few && nb <= 2 * 8 * 4 && rows >= 3072)) ? 2 : 1;
+        n = (pair || (!few && nb <= 2 * 8 * 4 && rows >= 3072)) ? 2 : 1;
         k = n == 2 ? 8 : 16;
         if (few) k = nb <= 64 ? 8 : 16;
     } else {
-        n = (epi == GRX_GEMM_SILU_Q || (!few && nb <= 2 * 8 * 4)) ? 2 : 1;
+        n = (pair || (!few && nb <= 2 * 8 * 4)) ? 2 : 1;
         k = n == 2 ? 8 : 16;
         if (few) k = nb <= ks_max_waves(n, 4) * 4 ? 4 : 16;
     }
     if (few && carry && nb > ks_max_waves(n, 16) * 16) k = 8;
+    // a fused prologue: more waves share the rows' LayerNorms (4 blocks a
+    // wave where a workgroup holds them)
+    if (pro) k = nb <= kKsProWaves * 4 ? 4 : 8;
     const int tn = grx_tune(GRX_TUNE_GEMM_NS);
     if (tn == 1 || tn == 2) {
-        n = (epi == GRX_GEMM_SILU_Q) ? 2 : tn;
+        n = pair ? 2 : tn;
         if (n == 2 && k > 8) k = 8;
     }
     const int tk = grx_tune(GRX_TUNE_GEMM_KB);
-    if ((tk == 4 || tk == 8 || tk == 16) && !(n == 2 && tk == 16)) k = tk;
+    if ((tk == 4 || tk == 8 || tk == 16) && !(n == 2 && tk == 16) && !(pro && tk == 16)) k = tk;
     if (n == 2 && k > 8) k = 8;
     if (nb > ks_max_waves(n, k) * k && !(carry && few)) return false;
     *ns = n;
@@ -1008,12 +1148,12 @@ bool pick_ks(int m, int nb, int rows, int epi, bool carry, bool sa, int *ns, int
 
 // Whether the staged-activation instantiation may take its LDS (asked once;
 // more than 64 KB needs the attribute).
-template <int EPI, int NS, int KB>
+template <int EPI, int NS, int KB, int PRO>
 bool ks_stage_ok() {
     static const bool ok = [] {
         const int need = ks_max_waves(NS, KB) * kss_bytes(KB);
         const bool r = need <= 64 * 1024 ||
-                       hipFuncSetAttribute((const void *)gemm_q8_kss_kernel<EPI, NS, KB>,
+                       hipFuncSetAttribute((const void *)gemm_q8_kss_kernel<EPI, NS, KB, PRO>,
                                            hipFuncAttributeMaxDynamicSharedMemorySize, need) == hipSuccess;
         (void)hipGetLastError();
         return r;
@@ -1021,7 +1161,22 @@ bool ks_stage_ok() {
     return ok;
 }
 
-template <int EPI, int NS, int KB, bool SA>
+KsFuse ks_fuse(const GemmOut &o) {
+    KsFuse f{};
+    f.x = o.x;
+    f.lda = o.lda;
+    f.lw = o.ln_w;
+    f.lb = o.ln_b;
+    f.lw2 = o.ln_w2;
+    f.lb2 = o.ln_b2;
+    f.x_out = o.x_out;
+    f.lens = o.lens;
+    f.T = o.T > 0 ? o.T : 1;
+    f.ring = o.ring;
+    return f;
+}
+
+template <int EPI, int NS, int KB, bool SA, int PRO>
 void launch_ks_run(hipStream_t st, const grx_weight *w, const int8_t *xq, const float *xs, int m, const float *bias,
                    float *y, int ldc, const GemmOut &o, int da4, int bbeg, int bend, const float *init) {
     // init (a carried chain) rows are w->rows apart
@@ -1029,9 +1184,9 @@ void launch_ks_run(hipStream_t st, const grx_weight *w, const int8_t *xq, const 
     const int ks = grx_ceil_div(bend - bbeg, KB);
     const int groups = grx_ceil_div(ncg, 8) * 8 * nrf;
     if constexpr (SA)
-        gemm_q8_kss_kernel<EPI, NS, KB><<<groups, 64 * ks, (size_t)ks * kss_bytes(KB), st>>>(
+        gemm_q8_kss_kernel<EPI, NS, KB, PRO><<<groups, 64 * ks, (size_t)ks * kss_bytes(KB), st>>>(
             w->qs, w->ds, w->rows, w->nb, xq, xs, m, bias, y, ldc, o.scale, o.yq, o.ys, ncg, nrf, bbeg, bend, init,
-            w->rows);
+            w->rows, ks_fuse(o));
     else
         gemm_q8_ks_kernel<EPI, NS, KB><<<groups, 64 * ks, 0, st>>>(w->qs, w->ds, w->rows, w->nb, xq, xs, m, bias, y,
                                                                    ldc, o.scale, o.yq, o.ys, ncg, nrf, da4, bbeg, bend,
@@ -1046,17 +1201,18 @@ void launch_ks(hipStream_t st, const grx_weight *w, const int8_t *xq, const floa
                const GemmOut &o, int da4) {
     const int run = ks_max_waves(NS, KB) * KB;
     if (w->nb <= run || o.carry == nullptr) {
-        launch_ks_run<EPI, NS, KB, SA>(st, w, xq, xs, m, bias, o.y, o.ldc, o, da4, 0, w->nb, nullptr);
+        launch_ks_run<EPI, NS, KB, SA, 0>(st, w, xq, xs, m, bias, o.y, o.ldc, o, da4, 0, w->nb, nullptr);
         return;
     }
     const float *init = nullptr;
     for (int b = 0; b < w->nb; b += run) {
         const int e = min(w->nb, b + run);
         if (e < w->nb) {
-            launch_ks_run<GRX_GEMM_STORE, NS, KB, SA>(st, w, xq, xs, m, bias, o.carry, w->rows, o, da4, b, e, init);
+            launch_ks_run<GRX_GEMM_STORE, NS, KB, SA, 0>(st, w, xq, xs, m, bias, o.carry, w->rows, o, da4, b, e,
+                                                         init);
             init = o.carry;
         } else {
-            launch_ks_run<EPI, NS, KB, SA>(st, w, xq, xs, m, bias, o.y, o.ldc, o, da4, b, e, init);
+            launch_ks_run<EPI, NS, KB, SA, 0>(st, w, xq, xs, m, bias, o.y, o.ldc, o, da4, b, e, init);
         }
     }
 }
@@ -1067,7 +1223,7 @@ void launch_ks(hipStream_t st, const grx_weight *w, const int8_t *xq, const floa
 template <int EPI, int NS, int KB>
 void launch_ks_sa(hipStream_t st, const grx_weight *w, const int8_t *xq, const float *xs, int m, const float *bias,
                   const GemmOut &o, int da4, bool sa) {
-    if (sa && ks_stage_ok<EPI, NS, KB>() && ks_stage_ok<GRX_GEMM_STORE, NS, KB>())
+    if (sa && ks_stage_ok<EPI, NS, KB, 0>() && ks_stage_ok<GRX_GEMM_STORE, NS, KB, 0>())
         return launch_ks<EPI, NS, KB, true>(st, w, xq, xs, m, bias, o, da4);
     return launch_ks<EPI, NS, KB, false>(st, w, xq, xs, m, bias, o, da4);
 }
@@ -1086,23 +1242,122 @@ void launch_ks_epi(hipStream_t st, const grx_weight *w, const int8_t *xq, const 
     return launch_ks_sa<EPI, 2, 8>(st, w, xq, xs, m, bias, o, da4, sa);
 }
 
+// The fused forms (a prologue, GLU, a ring copy): the staged kernel in one
+// run of blocks, 4 or 8 blocks a wave.
+template <int EPI, int PRO>
+void launch_ks_fused_pro(hipStream_t st, const grx_weight *w, const int8_t *xq, const float *xs, int m,
+                         const float *bias, const GemmOut &o, int ns, int kb) {
+    // pre-rounded activations come through xq/xs (PRO 0)
+    const int8_t *q = PRO == 0 ? xq : nullptr;
+    const float *sc = PRO == 0 ? xs : nullptr;
+    auto go = [&](auto ns_tag, auto kb_tag) {
+        constexpr int NS = decltype(ns_tag)::value, KB = decltype(kb_tag)::value;
+        (void)ks_stage_ok<EPI, NS, KB, PRO>();
+        launch_ks_run<EPI, NS, KB, true, PRO>(st, w, q, sc, m, bias, o.y, o.ldc, o, 1, 0, w->nb, nullptr);
+    };
+    using I1 = std::integral_constant<int, 1>;
+    using I2 = std::integral_constant<int, 2>;
+    using K4 = std::integral_constant<int, 4>;
+    using K8 = std::integral_constant<int, 8>;
+    using K16 = std::integral_constant<int, 16>;
+    if constexpr (EPI == GRX_GEMM_STORE) {
+        if (ns == 1) {
+            if (kb == 4) return go(I1{}, K4{});
+            if (kb == 8) return go(I1{}, K8{});
+            if constexpr (PRO == 0) return go(I1{}, K16{});
+        }
+    }
+    if (kb == 4) return go(I2{}, K4{});
+    return go(I2{}, K8{});
+}
+
+template <int EPI>
+void launch_ks_fused(hipStream_t st, const grx_weight *w, const int8_t *xq, const float *xs, int m, const float *bias,
+                     const GemmOut &o, int ns, int kb) {
+    if (o.x == nullptr) return launch_ks_fused_pro<EPI, 0>(st, w, xq, xs, m, bias, o, ns, kb);
+    if (o.ln_w2 == nullptr) return launch_ks_fused_pro<EPI, 1>(st, w, xq, xs, m, bias, o, ns, kb);
+    return launch_ks_fused_pro<EPI, 2>(st, w, xq, xs, m, bias, o, ns, kb);
+}
+
+// Which kernel a product takes (GEMM_KERNEL forces one; tests force each
+// with it): the one-row GEMV for one row (a conformer's one-row streaming
+// chunk step, a single latent: the same blocks folded in the same order,
+// its weights streamed once; a forced GEMM_KERNEL keeps the matrix cores,
+// and so does a long K on few rows: 1024 x 4096 10.9 us on the GEMV's 16
+// workgroups against 9.1 K-split); the LDS-staged tiles from 256 rows on;
+// below that the K-split tiles with their activations staged through LDS
+// (at 224 rows: 1024 x 4096 17 us against 26 on the whole-K register walk
+// and 50 on the LDS tiles, 4096 x 1024 12 against 19 and 15); without the
+// staging, the K-split tiles up to 128 rows where the register walk has few
+// tiles or a long K (at 126 rows: 4096 x 1024 10.4 us on the register walk
+// against 11.9 K-split; 2048 x 1024 8.1 against 7.3; 1024 x 4096 25 against
+// 19), the register walk otherwise.  The K-split kernel stages the
+// activations through LDS unless told not to or they are not in 16-byte
+// aligned whole groups of four blocks (a fused prologue builds them there).
+enum Route { kRouteGemv1, kRouteLds, kRouteKs, kRouteMfma };
+struct RoutePick {
+    Route r;
+    int ns, kb, da4;
+    bool sa;
+};
+RoutePick pick_route(const grx_weight *w, const int8_t *xq, const float *xs, int m, const GemmOut &o) {
+    const int kind = grx_tune(GRX_TUNE_GEMM_KERNEL);
+    const bool pro = o.x != nullptr;
+    RoutePick p{kRouteMfma, 1, 4, 0, false};
+    if (m == 1 && kind < 0 && o.carry == nullptr && o.epi != GRX_GEMM_SCALE && w->nb > 0 &&
+        (w->nb <= 64 || w->rows >= 2048 || grx_tune(GRX_TUNE_GEMV1) == 2) && grx_tune(GRX_TUNE_GEMV1) != 0) {
+        p.r = kRouteGemv1;
+        return p;
+    }
+    p.da4 = pro || (w->nb % 4 == 0 && ((uintptr_t)xs & 15) == 0) ? 1 : 0;
+    p.sa = grx_tune(GRX_TUNE_GEMM_STAGE_A) != 0 && p.da4 && (pro || ((uintptr_t)xq & 15) == 0);
+    const bool ks_ok = pick_ks(m, w->nb, w->rows, o.epi, o.carry != nullptr, p.sa, pro, &p.ns, &p.kb) &&
+                       (kind == 2 || (p.sa ? m < 256 : (m <= 128 && (m <= 32 || w->rows <= 2048 || w->nb > 64))));
+    if (kind == 3 || (kind != 1 && kind != 2 && m >= 256)) {
+        p.r = kRouteLds;
+    } else if (kind != 1 && ks_ok) {
+        p.r = kRouteKs;
+    } else {
+        p.r = kRouteMfma;
+    }
+    return p;
+}
+
+bool fused_parts(const GemmOut &o) { return o.x != nullptr || o.epi == GRX_GEMM_GLU || o.ring.p != nullptr; }
+
 }  // namespace
+
+bool grx_gemm_q8_fuses(const grx_weight *w, int m, const GemmOut &o) {
+    if (m <= 0 || w->rows == 0) return false;
+    if (o.epi == GRX_GEMM_GLU && (w->rows % GRX_QK != 0 || o.lens == nullptr)) return false;
+    if (o.ring.p != nullptr && o.epi != GRX_GEMM_STORE && o.epi != GRX_GEMM_GLU) return false;
+    if (o.x != nullptr && (w->cols % GRX_QK != 0 || o.ln_w == nullptr || o.ln_b == nullptr)) return false;
+    if (o.ln_w2 != nullptr && (o.x_out == nullptr || o.x_out == o.x || o.ln_b2 == nullptr)) return false;
+    const RoutePick p = pick_route(w, nullptr, nullptr, m, o);
+    if (p.r == kRouteGemv1)  // the one-row GEMV's prologue holds rows of up to 1280 values
+        return (o.epi == GRX_GEMM_STORE || o.epi == GRX_GEMM_SILU_Q || o.epi == GRX_GEMM_GLU) &&
+               (o.x == nullptr || w->nb * GRX_QK <= 1280);
+    if (p.r != kRouteKs || !p.sa) return false;
+    if (w->nb > ks_max_waves(p.ns, p.kb) * p.kb) return false;  // one run of blocks
+    if (o.x != nullptr && (w->nb * GRX_QK > kKsProPieces * 256 || p.kb == 16 ||
+                           grx_ceil_div(w->nb, p.kb) > kKsProWaves))
+        return false;
+    return true;
+}
 
 grx_status grx_gemm_q8_launch_ex(hipStream_t st, const grx_weight *w, const int8_t *xq, const float *xs, int m,
                                  const float *bias, const GemmOut &o) {
     if (m <= 0 || w->rows == 0) return GRX_OK;
-    if (o.epi < GRX_GEMM_STORE || o.epi > GRX_GEMM_SILU_Q)
+    if (o.epi < GRX_GEMM_STORE || o.epi > GRX_GEMM_GLU)
         return grx_fail(GRX_EINVAL, "unknown product epilogue %d", o.epi);
-    if (o.epi == GRX_GEMM_SILU_Q && w->rows % GRX_QK != 0)
-        return grx_fail(GRX_ESIZE, "rounded product output needs rows %% 32 == 0 (rows %d)", w->rows);
-    const int kind = grx_tune(GRX_TUNE_GEMM_KERNEL);
-    // one row (a conformer's one-row streaming chunk step, a single latent)
-    // on the one-row GEMV: the same blocks folded in the same order, its
-    // weights streamed once; a forced GEMM_KERNEL keeps the matrix cores,
-    // and so does a long K on few rows (1024 x 4096: 10.9 us on the GEMV's
-    // 16 workgroups against 9.1 K-split)
-    if (m == 1 && kind < 0 && o.carry == nullptr && o.epi != GRX_GEMM_SCALE && w->nb > 0 &&
-        (w->nb <= 64 || w->rows >= 2048) && grx_tune(GRX_TUNE_GEMV1) != 0) {
+    if ((o.epi == GRX_GEMM_SILU_Q || o.epi == GRX_GEMM_GLU) && w->rows % GRX_QK != 0)
+        return grx_fail(GRX_ESIZE, "rounded or paired product output needs rows %% 32 == 0 (rows %d)", w->rows);
+    const bool fused = fused_parts(o);
+    if (fused && !grx_gemm_q8_fuses(w, m, o))
+        return grx_fail(GRX_EINVAL, "a fused prologue, GLU or ring copy is not taken for %d rows of %dx%d", m,
+                        w->rows, w->cols);
+    const RoutePick p = pick_route(w, xq, xs, m, o);
+    if (p.r == kRouteGemv1) {
         GemvArgs a = {};
         a.qs = w->qs;
         a.ds = w->ds;
@@ -1110,6 +1365,13 @@ grx_status grx_gemm_q8_launch_ex(hipStream_t st, const grx_weight *w, const int8
         a.nb = w->nb;
         a.xq = xq;
         a.xs = xs;
+        a.x = o.x;
+        a.lda = o.lda;
+        a.ln_w = o.ln_w;
+        a.ln_b = o.ln_b;
+        a.ln_w2 = o.ln_w2;
+        a.ln_b2 = o.ln_b2;
+        a.x_out = o.x_out;
         a.bias = bias;
         a.y = o.y;
         a.ldc = o.ldc;
@@ -1117,30 +1379,19 @@ grx_status grx_gemm_q8_launch_ex(hipStream_t st, const grx_weight *w, const int8
         a.ldr = o.ldc;
         a.yq = o.yq;
         a.ys = o.ys;
+        a.ring = o.ring;
+        a.lens = o.lens;
+        a.T = o.T > 0 ? o.T : 1;
         a.cacheable = 0;  // weights streamed once a step
         const int epi = o.epi == GRX_GEMM_STORE ? GRX_EPI_STORE
                         : o.epi == GRX_GEMM_ADD ? GRX_EPI_RESID
                         : o.epi == GRX_GEMM_AXPY_HALF ? GRX_EPI_AXPY_HALF
+                        : o.epi == GRX_GEMM_GLU ? GRX_EPI_GLU
                                                       : GRX_EPI_SILU_Q;
-        return grx_gemv_launch(st, 1, GRX_PRO_PREQ, epi, a, 0);
+        const int pro = o.x == nullptr ? GRX_PRO_PREQ : o.ln_w2 != nullptr ? GRX_PRO_LN2 : GRX_PRO_LN;
+        return grx_gemv_launch(st, 1, pro, epi, a, 0);
     }
-    // GEMM_KERNEL picks the kernel (tests force each one with it): the
-    // LDS-staged tiles from 256 rows on; below that the K-split tiles with
-    // their activations staged through LDS (at 224 rows: 1024 x 4096 17 us
-    // against 26 on the whole-K register walk and 50 on the LDS tiles,
-    // 4096 x 1024 12 against 19 and 15); without the staging, the K-split
-    // tiles up to 128 rows where the register walk has few tiles or a long K
-    // (at 126 rows: 4096 x 1024 10.4 us on the register walk against 11.9
-    // K-split; 2048 x 1024 8.1 against 7.3; 1024 x 4096 25 against 19), the
-    // register walk otherwise
-    // the K-split kernel stages the activations through LDS unless told not
-    // to or they are not in 16-byte aligned whole groups of four blocks
-    const int da4 = (w->nb % 4 == 0 && ((uintptr_t)xs & 15) == 0) ? 1 : 0;
-    const bool sa = grx_tune(GRX_TUNE_GEMM_STAGE_A) != 0 && da4 && ((uintptr_t)xq & 15) == 0;
-    int ks_ns = 1, ks_kb = 4;
-    const bool ks_ok = pick_ks(m, w->nb, w->rows, o.epi, o.carry != nullptr, sa, &ks_ns, &ks_kb) &&
-                       (kind == 2 || (sa ? m < 256 : (m <= 128 && (m <= 32 || w->rows <= 2048 || w->nb > 64))));
-    if (kind == 3 || (kind != 1 && kind != 2 && m >= 256)) {  // many rows: the LDS-staged 64 x 128 tiles
+    if (p.r == kRouteLds) {  // many rows: the LDS-staged 64 x 128 tiles
         dim3 g2(grx_ceil_div(m, 64), grx_ceil_div(w->tiles, 2));
 #define GRX_GEMM_LDS(E)                                                                                           \
     case E:                                                                                                       \
@@ -1158,20 +1409,30 @@ grx_status grx_gemm_q8_launch_ex(hipStream_t st, const grx_weight *w, const int8
         GRX_LAUNCHED("gemm_q8_lds_kernel");
         return GRX_OK;
     }
-    if (kind != 1 && ks_ok) {  // fewer rows: the K-split tiles
+    if (p.r == kRouteKs) {  // fewer rows: the K-split tiles
+        if (fused) {
+            switch (o.epi) {
+                case GRX_GEMM_STORE: launch_ks_fused<GRX_GEMM_STORE>(st, w, xq, xs, m, bias, o, p.ns, p.kb); break;
+                case GRX_GEMM_SILU_Q: launch_ks_fused<GRX_GEMM_SILU_Q>(st, w, xq, xs, m, bias, o, 2, p.kb); break;
+                case GRX_GEMM_GLU: launch_ks_fused<GRX_GEMM_GLU>(st, w, xq, xs, m, bias, o, 2, p.kb); break;
+                default: return grx_fail(GRX_EINVAL, "product epilogue %d takes no fused prologue", o.epi);
+            }
+            GRX_LAUNCHED("gemm_q8_kss_kernel");
+            return GRX_OK;
+        }
         switch (o.epi) {
             case GRX_GEMM_STORE:
-                launch_ks_epi<GRX_GEMM_STORE>(st, w, xq, xs, m, bias, o, ks_ns, ks_kb, da4, sa);
+                launch_ks_epi<GRX_GEMM_STORE>(st, w, xq, xs, m, bias, o, p.ns, p.kb, p.da4, p.sa);
                 break;
-            case GRX_GEMM_ADD: launch_ks_epi<GRX_GEMM_ADD>(st, w, xq, xs, m, bias, o, ks_ns, ks_kb, da4, sa); break;
+            case GRX_GEMM_ADD: launch_ks_epi<GRX_GEMM_ADD>(st, w, xq, xs, m, bias, o, p.ns, p.kb, p.da4, p.sa); break;
             case GRX_GEMM_AXPY_HALF:
-                launch_ks_epi<GRX_GEMM_AXPY_HALF>(st, w, xq, xs, m, bias, o, ks_ns, ks_kb, da4, sa);
+                launch_ks_epi<GRX_GEMM_AXPY_HALF>(st, w, xq, xs, m, bias, o, p.ns, p.kb, p.da4, p.sa);
                 break;
             case GRX_GEMM_SCALE:
-                launch_ks_epi<GRX_GEMM_SCALE>(st, w, xq, xs, m, bias, o, ks_ns, ks_kb, da4, sa);
+                launch_ks_epi<GRX_GEMM_SCALE>(st, w, xq, xs, m, bias, o, p.ns, p.kb, p.da4, p.sa);
                 break;
             case GRX_GEMM_SILU_Q:
-                launch_ks_epi<GRX_GEMM_SILU_Q>(st, w, xq, xs, m, bias, o, 2, ks_kb, da4, sa);
+                launch_ks_epi<GRX_GEMM_SILU_Q>(st, w, xq, xs, m, bias, o, 2, p.kb, p.da4, p.sa);
                 break;
         }
         GRX_LAUNCHED("gemm_q8_ks_kernel");

@@ -703,7 +703,11 @@ __global__ __launch_bounds__(64 * W) void gemv1_kernel(const GemvArgs a) {
     } else if constexpr (EPI == GRX_EPI_RESID) {
         if (row < a.rows) a.y[row] = __fadd_rn(resid, acc);
     } else if constexpr (EPI == GRX_EPI_STORE) {
-        if (row < a.rows) a.y[row] = acc;
+        if (row < a.rows) {
+            a.y[row] = acc;
+            if (a.ring.p != nullptr && row >= a.ring.col0)
+                ring_put(a.ring, ring_row(a.ring, ring_head(a.ring), 0), row - a.ring.col0, acc);
+        }
     } else {
         const float accm[1] = {acc};
         gemv_epilogue<1, W, false, EPI>(a, accm, row, lane, wave, pos0);
@@ -866,11 +870,7 @@ hipError_t launch1_one(hipStream_t st, const GemvArgs &a, int tiles) {
 // One-row launches: pre-rounded rows on 1..16 waves; rows rounded in the
 // prologue on 1, 4, 8 or 16 waves with 2, 4 or 5 pieces per lane.
 template <int PRO, int EPI>
-hipError_t launch1(hipStream_t st, const GemvArgs &a, int tiles, int W) {
-    if constexpr (EPI != GRX_EPI_ARGMAX && EPI != GRX_EPI_XSCORES) {
-        const int r = grx_gemv1_rows(tiles, PRO, EPI);
-        if (r < 64) return grx_gemv1n_launch(st, a, tiles, r, PRO, EPI);
-    }
+hipError_t launch1_one_w(hipStream_t st, const GemvArgs &a, int tiles, int W) {
     while (W > 1 && W > a.nb) W >>= 1;  // every wave owns a block
     if constexpr (PRO == GRX_PRO_PREQ) {
         switch (W) {
@@ -899,6 +899,17 @@ hipError_t launch1(hipStream_t st, const GemvArgs &a, int tiles, int W) {
         if (np == 4) return go(std::integral_constant<int, 4>{});
         return go(std::integral_constant<int, 5>{});
     }
+}
+
+// The one-row kernel on whole tiles, or on slices (gemv1n_kernel) where
+// those pay and no ring copy is asked for.
+template <int PRO, int EPI>
+hipError_t launch1(hipStream_t st, const GemvArgs &a, int tiles, int W) {
+    if constexpr (EPI != GRX_EPI_ARGMAX && EPI != GRX_EPI_XSCORES) {
+        const int r = grx_gemv1_rows(tiles, PRO, EPI);
+        if (r < 64 && a.ring.p == nullptr) return grx_gemv1n_launch(st, a, tiles, r, PRO, EPI);
+    }
+    return launch1_one_w<PRO, EPI>(st, a, tiles, W);
 }
 
 template <int M, int PRO, int EPI, int NS, int KB>
@@ -966,10 +977,10 @@ int grx_gemv_pick_waves(int tiles, int nb, int m, int pro) {
     while (W < 16 && tiles * W < 2048 && 2 * W <= nb && gemv_smem(m, 2 * W, pro, nb) <= lim) W *= 2;
     // several rows fold in rounds, one wave per row: at least m waves
     if (m > 1 && W > 1 && W < m && gemv_smem(m, m, pro, nb) <= lim) W = m;
-    // the float64 LayerNorm prologue (its bound check included) needs more
-    // than the 128 registers a lane has at 16 waves; 8 waves measured the
-    // same as 16 for these products
-    if (pro == GRX_PRO_LN64 && W > 8) W = 8;
+    // the float64 LayerNorm prologue (its bound check included) and the
+    // two LayerNorms of LN2 need more than the 128 registers a lane has at
+    // 16 waves; 8 waves measured the same as 16 for these products
+    if ((pro == GRX_PRO_LN64 || pro == GRX_PRO_LN2) && W > 8) W = 8;
     return W;
 }
 
@@ -1006,6 +1017,28 @@ grx_status grx_gemv_launch(hipStream_t st, int m, int pro, int epi, const GemvAr
     else if (pro == GRX_PRO_PREQ && epi == GRX_EPI_ARGMAX) e = launch_m<GRX_PRO_PREQ, GRX_EPI_ARGMAX>(st, m, a, tiles, W);
     else if (pro == GRX_PRO_LN64 && epi == GRX_EPI_QKV_ROPE) e = launch_m<GRX_PRO_LN64, GRX_EPI_QKV_ROPE>(st, m, a, tiles, W);
     else if (pro == GRX_PRO_LN64 && epi == GRX_EPI_GELU_Q) e = launch_m<GRX_PRO_LN64, GRX_EPI_GELU_Q>(st, m, a, tiles, W);
+    else if (m == 1 && ((pro == GRX_PRO_PREQ && epi == GRX_EPI_GLU) ||
+                        ((pro == GRX_PRO_LN || pro == GRX_PRO_LN2) && (epi == GRX_EPI_SILU_Q || epi == GRX_EPI_GLU)) ||
+                        (pro == GRX_PRO_LN2 && epi == GRX_EPI_STORE))) {
+        // one row with a fused LayerNorm prologue and the matrix-core
+        // product's epilogues, or a pre-rounded row into the GLU (a streaming
+        // conformer's one-row chunk), on whole 64-row tiles (GLU pairs rows
+        // 16 apart within 32)
+        if (!gemv1_fits(pro, a.nb) || a.rows % GRX_QK != 0)
+            return grx_fail(GRX_EINVAL, "grx: prologue %d epilogue %d needs one row of at most %d values and rows %% 32 == 0",
+                            pro, epi, kRowPieces * 256);
+        if (epi == GRX_EPI_GLU && a.lens == nullptr)
+            return grx_fail(GRX_EINVAL, "grx: the GLU epilogue needs the valid rows");
+        if (pro == GRX_PRO_PREQ)
+            e = launch1_one_w<GRX_PRO_PREQ, GRX_EPI_GLU>(st, a, tiles, W);
+        else if (pro == GRX_PRO_LN)
+            e = epi == GRX_EPI_SILU_Q ? launch1_one_w<GRX_PRO_LN, GRX_EPI_SILU_Q>(st, a, tiles, W)
+                                      : launch1_one_w<GRX_PRO_LN, GRX_EPI_GLU>(st, a, tiles, W);
+        else
+            e = epi == GRX_EPI_SILU_Q ? launch1_one_w<GRX_PRO_LN2, GRX_EPI_SILU_Q>(st, a, tiles, W)
+                : epi == GRX_EPI_GLU  ? launch1_one_w<GRX_PRO_LN2, GRX_EPI_GLU>(st, a, tiles, W)
+                                      : launch1_one_w<GRX_PRO_LN2, GRX_EPI_STORE>(st, a, tiles, W);
+    }
     else if (pro == GRX_PRO_PREQ && (epi == GRX_EPI_AXPY_HALF || epi == GRX_EPI_SILU_Q)) {
         // one pre-rounded row (the matrix-core product's one-row epilogues)
         if (m != 1 || !gemv1_fits(pro, a.nb))

@@ -150,7 +150,8 @@ __device__ __forceinline__ void wave_row_prologue(const GemvArgs &a, int m, int8
     const int nb = a.nb, K = nb * GRX_QK;
     const size_t rq = ldq > 0 ? (size_t)ldq : (size_t)K;  // bytes between the rounded rows in lxq
     const int npc = K / 4;  // float4 pieces
-    float4 xv[NP], wv[NP], bv[NP];
+    constexpr bool L2 = PRO == GRX_PRO_LN2;
+    float4 xv[NP], wv[NP], bv[NP], wv2[L2 ? NP : 1], bv2[L2 ? NP : 1];
     const float4 *x4 = reinterpret_cast<const float4 *>(a.x + (size_t)m * a.lda);
 #pragma unroll
     for (int j = 0; j < NP; ++j) {
@@ -172,11 +173,15 @@ __device__ __forceinline__ void wave_row_prologue(const GemvArgs &a, int m, int8
         } else {
             xv[j] = x4[P];
         }
-        if constexpr (PRO == GRX_PRO_LN || PRO == GRX_PRO_EMBED_LN || PRO == GRX_PRO_LN64) {
+        if constexpr (PRO == GRX_PRO_LN || PRO == GRX_PRO_EMBED_LN || PRO == GRX_PRO_LN64 || L2) {
             if (PRO != GRX_PRO_LN64 || a.ln_w != nullptr) {
                 wv[j] = reinterpret_cast<const float4 *>(a.ln_w)[P];
                 bv[j] = reinterpret_cast<const float4 *>(a.ln_b)[P];
             }
+        }
+        if constexpr (L2) {
+            wv2[j] = reinterpret_cast<const float4 *>(a.ln_w2)[P];
+            bv2[j] = reinterpret_cast<const float4 *>(a.ln_b2)[P];
         }
     }
     // loads issued behind this row's (they complete in order): waiting for
@@ -189,11 +194,21 @@ __device__ __forceinline__ void wave_row_prologue(const GemvArgs &a, int m, int8
                 if (j * 64 + lane < npc) reinterpret_cast<float4 *>(a.x_out + (size_t)m * a.lda)[j * 64 + lane] = xv[j];
         }
     }
-    if constexpr (PRO == GRX_PRO_LN || PRO == GRX_PRO_EMBED_LN) {
+    if constexpr (PRO == GRX_PRO_LN || PRO == GRX_PRO_EMBED_LN || L2) {
         // layerNorm (internal/kern/mathx.go:55-75): float64 sums (in the
         // reference's order where the tree's could round differently),
         // mean and inv rounded to float32, y = (v-mean)*inv*w + b
         wave_ln32<NP>(xv, wv, bv, npc, lane);
+        if constexpr (L2) {
+            // a block's norm_out (conformer/encoder.go:426) kept by tile 0,
+            // then the next block's first LayerNorm
+            if (tile == 0) {
+#pragma unroll
+                for (int j = 0; j < NP; ++j)
+                    if (j * 64 + lane < npc) reinterpret_cast<float4 *>(a.x_out + (size_t)m * a.lda)[j * 64 + lane] = xv[j];
+            }
+            wave_ln32<NP>(xv, wv2, bv2, npc, lane);
+        }
     } else if constexpr (PRO == GRX_PRO_LN64) {
         // layerNorm of pockettts/nn.go:27-49: statistics and the
         // normalized value in float64, gain and bias in float32
@@ -287,6 +302,22 @@ __device__ __forceinline__ void gemv_epilogue(const GemvArgs &a, const float (&a
                     *a.counter = 0u;
                 }
             }
+        }
+        return;
+    }
+    if constexpr (EPI == GRX_EPI_GLU) {
+        // rows paired (grx_glu_row): lane l < 16 of each 32-row half holds
+        // channel 16*(row/32) + l's a-row, lane l + 16 its b-row
+#pragma unroll
+        for (int m = 0; m < M; ++m) {
+            if (!mine(m)) continue;
+            const float b = __shfl_xor(acc[m], 16);
+            if (row >= a.rows || (lane & 16) != 0) continue;
+            const int ch = (row >> 5) * 16 + (lane & 15);
+            const int s = m / a.T;
+            const float v = m - s * a.T < a.lens[s] ? grx_glu_pair(acc[m], b) : 0.0f;
+            a.y[(size_t)m * a.ldc + ch] = v;
+            if (a.ring.p != nullptr) ring_put(a.ring, ring_row(a.ring, ring_head(a.ring), m), ch - a.ring.col0, v);
         }
         return;
     }
