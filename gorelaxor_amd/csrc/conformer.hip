@@ -713,7 +713,13 @@ __device__ __forceinline__ void attn_wg_xcd(int &px, int &h, int &b) {
     b = w / (nx * ny);
 }
 
-template <int RQ>
+// G8: blocks of at most 16 rows (every output on the gemvRows route) whose
+// scores and outputs fit one round of 8-lane groups (one row of up to 128
+// keys and 128 values: a streaming chunk step of one row), each output by
+// a group of 8 lanes (dot8_s: the same sums in the same order; the
+// single-thread chains measured 1.9 us for a row's 71 scores, the groups
+// 0.8); the host picks it.
+template <int RQ, bool G8 = false>
 __global__ __launch_bounds__(kAttnLdsThreads) void conf_attn_lds_kernel(const AttnIO io, const AttnKeys ak,
                                                                         const float *__restrict__ pos_u,
                                                                         const float *__restrict__ pos_v, int D,
@@ -794,7 +800,15 @@ __global__ __launch_bounds__(kAttnLdsThreads) void conf_attn_lds_kernel(const At
         qv[i * sq + j] = __fadd_rn(q, pos_v[h * hd + j]);
     }
     __syncthreads();
-    for (int e = tid; e < ng * nk + (nr - r1) * nk; e += nt) {
+    const int grp = tid >> 3, gq = tid & 7, ngrp = nt >> 3;
+    if constexpr (G8) {
+        for (int e = grp; e < nr * nk; e += ngrp) {
+            const int i = e / nk, kk = e % nk;
+            const float v = dot8_s(qu + i * sq, st + kk * sq, 1, hd, kk < (nk & ~3), gq);
+            if (gq == 0) S[i * sS + kk] = v;
+        }
+    }
+    for (int e = tid; !G8 && e < ng * nk + (nr - r1) * nk; e += nt) {
         if (e < ng * nk) {
             const int i0 = 4 * (e / nk), kk = e % nk;
             float o[4];
@@ -817,7 +831,14 @@ __global__ __launch_bounds__(kAttnLdsThreads) void conf_attn_lds_kernel(const At
     // of their own
     const int nd = nk >= 4 ? nk - 3 : 0, gd = nd > 0 ? ng : 0, rs = nd > 0 ? r1 : 0;
     const int n_diag = gd * nd, n_left = gd * 12, n_rest = (nr - rs) * nk;
-    for (int e = tid; e < n_diag + n_left + n_rest; e += nt) {
+    if constexpr (G8) {
+        for (int e = grp; e < nr * nk; e += ngrp) {
+            const int i = e / nk, kj = e % nk, jj = nq - 1 - (r0 + i) + kj;
+            const float v = dot8_s(qv + i * sq, st + (nr - 1 - i + kj) * sq, 1, hd, jj < (np & ~3), gq);
+            if (gq == 0) BD[i * sS + kj] = v;
+        }
+    }
+    for (int e = tid; !G8 && e < n_diag + n_left + n_rest; e += nt) {
         int i, kj;
         if (e < n_diag) {
             const int i0 = 4 * (e / nd), kd = e % nd;
@@ -841,8 +862,10 @@ __global__ __launch_bounds__(kAttnLdsThreads) void conf_attn_lds_kernel(const At
                              : matmul_f32_one(bq, bpr, 1, hd, r0 + i, nq, jj, np);
     }
     __syncthreads();
-    // values of the head (rows hd apart) while the rows are scored
-    stage_post(st, hd, vv, vp, io.ldkv, nk, hd);
+    // values of the head (rows sv apart: hd, or hd + 1 where 8 lanes read
+    // one column's rows) while the rows are scored
+    const int sv = G8 ? hd + 1 : hd;
+    stage_post(st, sv, vv, vp, io.ldkv, nk, hd);
     const int lane = tid & 63, wave = tid >> 6, nw = nt >> 6;
     for (int i = wave; i < nr; i += nw) {
         int lo, hi;
@@ -902,7 +925,14 @@ __global__ __launch_bounds__(kAttnLdsThreads) void conf_attn_lds_kernel(const At
     }
     __syncthreads();
     float *O = qu;  // [nr][sq]
-    for (int e = tid; e < ng * hd + (nr - r1) * hd; e += nt) {
+    if constexpr (G8) {
+        for (int e = grp; e < nr * hd; e += ngrp) {
+            const int i = e / hd, ee = e % hd;
+            const float v = dot8_s(S + i * sS, st + ee, sv, nk, ee < (hd & ~3), gq);
+            if (gq == 0) O[i * sq + ee] = v;
+        }
+    }
+    for (int e = tid; !G8 && e < ng * hd + (nr - r1) * hd; e += nt) {
         if (e < ng * hd) {
             const int i0 = 4 * (e / hd), ee = e % hd;
             float o[4];
@@ -1730,7 +1760,9 @@ grx_status attn_pick(int B, int heads, int nblk, int bl, int nk, int hd, int *rq
                                 : (const void *)conf_attn_lds_kernel<16>;
     if (*rq != 0 && staged <= 160 * 1024 &&
         (staged <= 64 * 1024 ||
-         hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)staged) == hipSuccess)) {
+         (hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)staged) == hipSuccess &&
+          (*rq != 4 || hipFuncSetAttribute((const void *)conf_attn_lds_kernel<4, true>,
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)staged) == hipSuccess)))) {
         *smem = staged;
         return GRX_OK;
     }
@@ -1861,6 +1893,7 @@ struct CRun {
     int maxfirst;
     const int *ctl;  // streaming: c, ring heads (device); null offline
     int attn_rq;
+    int attn_keys;  // the most keys a block's queries see
     size_t attn_smem;
     bool dw_win;
     // streaming caches per layer (null offline)
@@ -1938,6 +1971,12 @@ grx_status enqueue_run(grx_conformer *m, const CRun &r, hipStream_t st) {
         return grx_gemm_q8_fuses(w, R, o);
     };
     const bool kv_ring = r.kv_ring != nullptr, cv_ring = r.conv_ring != nullptr && padL > 0;
+    // the attention's 8-lane groups: blocks of up to 16 rows whose
+    // workgroups' scores (rows x the most keys a block sees) and outputs
+    // (rows x head width) fit one round of the workgroup's groups
+    const int attn_rows_wg = std::min(r.attn_rq, r.keys.bl), attn_keys_max = r.attn_keys;
+    const bool attn_g8 = grx_tune(GRX_TUNE_CONF_ATTN_G8) != 0 && r.keys.bl <= 16 &&
+                         attn_rows_wg * std::max(attn_keys_max, hd) * 8 <= kAttnLdsThreads;
     const int fz = grx_tune(GRX_TUNE_CONF_FUSE);  // 0 none, 3 LayerNorm prologues on up to 32 rows
     const bool fuse_ln = R <= kFuseLnRows && fz != 0 && (fz == 3 || R == 1) && bf.x2 != nullptr &&
                          probe(B0.qkv, GRX_GEMM_STORE, true, false, kv_ring) &&
@@ -2061,7 +2100,11 @@ grx_status enqueue_run(grx_conformer *m, const CRun &r, hipStream_t st) {
             io.pp = r.pp + (size_t)i * d;
             io.ldp = hp.layers * d;
         }
-        if (r.attn_rq == 4)
+        if (r.attn_rq == 4 && attn_g8)
+            conf_attn_lds_kernel<4, true><<<dim3(nblk * ((r.keys.bl + 3) / 4), hp.heads, B), kAttnLdsThreads,
+                                            r.attn_smem, st>>>(io, r.keys, Bk.pos_u, Bk.pos_v, d, hd, scale, bf.xq,
+                                                               bf.xs);
+        else if (r.attn_rq == 4)
             conf_attn_lds_kernel<4><<<dim3(nblk * ((r.keys.bl + 3) / 4), hp.heads, B), kAttnLdsThreads, r.attn_smem,
                                       st>>>(io, r.keys, Bk.pos_u, Bk.pos_v, d, hd, scale, bf.xq, bf.xs);
         else if (r.attn_rq == 8)
@@ -2214,6 +2257,7 @@ grx_status enqueue_encode(grx_conformer *m, hipStream_t st) {
     r.keys = offline_keys(hp, T);
     r.pp = m->pp;
     r.attn_rq = m->attn_rq;
+    r.attn_keys = T;
     r.attn_smem = m->attn_smem;
     r.dw_win = m->dw_win;
     return enqueue_run(m, r, st);
@@ -2415,6 +2459,7 @@ grx_status stream_run(grx_conformer_stream *s, const float *mel, int nf, const i
     run.maxfirst = s->maxfirst;
     run.ctl = s->ctl;
     run.attn_rq = sh.attn_rq;
+    run.attn_keys = s->g.left + Tp;
     run.attn_smem = sh.attn_smem;
     run.dw_win = s->dw_win;
     run.kv_ring = s->kv_ring;

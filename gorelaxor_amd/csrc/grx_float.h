@@ -449,6 +449,43 @@ __device__ __forceinline__ float dot_x4_s(const float *x, const float *w, size_t
     return o;
 }
 
+// dot_x4_s (x4) or dot_go_s of one output by a group of 8 lanes (lane q
+// of the group; all 8 call it together): lane q runs dot4f32avx's
+// accumulators A[q] and B[q] (elements c+q and c+8+q of each 16, in order)
+// and S[q] = A[q] + B[q], the group's shuffles add the S as hsum8 does
+// ((S0+S4 + S1+S5) + (S2+S6 + S3+S7)); lanes 0..3 run dotF32Go's four sums
+// over the tail (the whole row without x4), the rest into the first.  The
+// result is lane 0's.
+__device__ __forceinline__ float dot8_s(const float *x, const float *w, size_t sb, int k, bool x4, int q) {
+    float o = 0.f;
+    int kk = 0;
+    if (x4) {
+        kk = k & ~15;
+        float A = 0.f, B = 0.f;
+        for (int c = 0; c < kk; c += 16) {
+            A = __fmaf_rn(x[c + q], w[(size_t)(c + q) * sb], A);
+            B = __fmaf_rn(x[c + 8 + q], w[(size_t)(c + 8 + q) * sb], B);
+        }
+        float t = __fadd_rn(A, B);                   // S[q]
+        t = __fadd_rn(t, __shfl_down(t, 4, 8));      // S[q] + S[q+4]
+        t = __fadd_rn(t, __shfl_down(t, 1, 8));      // q = 0: h0 + h1, q = 2: h2 + h3
+        t = __fadd_rn(t, __shfl_down(t, 2, 8));      // q = 0: the sum
+        o = kk > 0 ? t : 0.f;
+        if (kk == k) return o;
+    }
+    const int n = k - kk, n4 = n & ~3;
+    const float *xt = x + kk, *wt = w + (size_t)kk * sb;
+    float s = 0.f;
+    if (q < 4) {
+        for (int i = q; i < n4; i += 4) s = __fadd_rn(s, __fmul_rn(xt[i], wt[(size_t)i * sb]));
+        if (q == 0)
+            for (int i = n4; i < n; ++i) s = __fadd_rn(s, __fmul_rn(xt[i], wt[(size_t)i * sb]));
+    }
+    const float s1 = __shfl_down(s, 1, 8), s2 = __shfl_down(s, 2, 8), s3 = __shfl_down(s, 3, 8);
+    const float go = __fadd_rn(__fadd_rn(__fadd_rn(s, s1), s2), s3);
+    return x4 ? __fadd_rn(o, go) : go;
+}
+
 // One output (row r of m, column j of n) of MatMulF32 (internal/kern/
 // kern.go:205-212 over gemm.go:116-259) with no bias: for m > 16 the rows in
 // whole groups of six take k6x16avx (kernels_amd64.s:5-88: acc = fma(a, b,
