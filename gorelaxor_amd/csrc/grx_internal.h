@@ -117,8 +117,7 @@ enum {
     GRX_TUNE_GEMM_NS,         // 16-column tiles per wave of the register kernels: 1, 2 or 4
     GRX_TUNE_GEMM_KB,         // blocks per wave of the K-split kernel: 4, 8 or 16
     GRX_TUNE_GEMV_WAVES,      // waves per tile of the GEMV: 1, 2, 4, 8 or 16
-    GRX_TUNE_GEMV1,           // 0: one-row products on the general GEMV kernel, 2: every one-row
-                              // matrix-core product on the one-row GEMV
+    GRX_TUNE_GEMV1,           // 0: one-row products on the general GEMV kernel
     GRX_TUNE_CONF_ATTN_RQ,    // conformer attention: 0 unstaged, 8 or 16 query rows per workgroup
     GRX_TUNE_FUSE_LN,         // 0: batched decoder LayerNorm rows in their own launch
     GRX_TUNE_FUSE_XSCORES,    // 0: whisper cross scores without the fused query product

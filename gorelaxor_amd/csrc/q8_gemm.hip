@@ -1282,9 +1282,10 @@ void launch_ks_fused(hipStream_t st, const grx_weight *w, const int8_t *xq, cons
 // Which kernel a product takes (GEMM_KERNEL forces one; tests force each
 // with it): the one-row GEMV for one row (a conformer's one-row streaming
 // chunk step, a single latent: the same blocks folded in the same order,
-// its weights streamed once; a forced GEMM_KERNEL keeps the matrix cores,
-// and so does a long K on few rows: 1024 x 4096 10.9 us on the GEMV's 16
-// workgroups against 9.1 K-split); the LDS-staged tiles from 256 rows on;
+// its weights streamed once, on slices of the weight tiles where those
+// give more workgroups: 1024 x 4096 6.2 us on 128 workgroups of 8 rows
+// against 8.0 K-split; a forced GEMM_KERNEL keeps the matrix cores); the
+// LDS-staged tiles from 256 rows on;
 // below that the K-split tiles with their activations staged through LDS
 // (at 224 rows: 1024 x 4096 17 us against 26 on the whole-K register walk
 // and 50 on the LDS tiles, 4096 x 1024 12 against 19 and 15); without the
@@ -1305,7 +1306,7 @@ RoutePick pick_route(const grx_weight *w, const int8_t *xq, const float *xs, int
     const bool pro = o.x != nullptr;
     RoutePick p{kRouteMfma, 1, 4, 0, false};
     if (m == 1 && kind < 0 && o.carry == nullptr && o.epi != GRX_GEMM_SCALE && w->nb > 0 &&
-        (w->nb <= 64 || w->rows >= 2048 || grx_tune(GRX_TUNE_GEMV1) == 2) && grx_tune(GRX_TUNE_GEMV1) != 0) {
+        grx_tune(GRX_TUNE_GEMV1) != 0) {
         p.r = kRouteGemv1;
         return p;
     }
