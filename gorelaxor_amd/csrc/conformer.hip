@@ -2178,9 +2178,8 @@ grx_status enqueue_run(grx_conformer *m, const CRun &r, hipStream_t st) {
         if (dw == 1 && !r.dw_win) dw = 0;
         // with the LayerNorm: a row per workgroup of float4 pieces where
         // the row has at most 1024 channels and the kernel at most 16 taps
-        // (one row at d 1024: 9.2 -> 4.8 us from the workgroup's start to
-        // its last store, against a channel a thread), else a row per
-        // workgroup whose reductions span it
+        // (one row at d 1024: 5.4 us a launch, against 11.0 for the row per
+        // workgroup with workgroup-wide reductions), else that kernel
         const bool dw_ln4 = d <= 1024 && hp.conv_kernel <= 16 && grx_tune(GRX_TUNE_CONF_DW) != 0;
         const int dw_ln_threads = 64 * grx_ceil_div(d / 4, 64);
         if (hp.conv_ln && dw_ln4 && hp.conv_kernel <= 12)
