@@ -1751,11 +1751,19 @@ grx_status attn_pick(int B, int heads, int nblk, int bl, int nk, int hd, int *rq
     // 4.32 -> 4.20 ms an encode, the streaming chunks 3.28 -> 3.20 ms)
     const long n8 = (long)B * heads * nblk * ((bl + 7) / 8);
     *rq = n8 < 256 ? 4 : n8 < 1024 ? 8 : 16;
-    if (grx_tune(GRX_TUNE_CONF_ATTN_RQ) >= 0) *rq = grx_tune(GRX_TUNE_CONF_ATTN_RQ);  // 0 (unstaged), 4, 8 or 16, for tests
-    if (*rq != 0 && *rq != 4 && *rq != 8 && *rq != 16) *rq = 8;
+    // a row a workgroup on 8-lane groups where a block has at most 16 rows,
+    // a row's scores and outputs fit one round of the groups, and the
+    // workgroups number at most 256 (a streaming chunk step of 14 rows, one
+    // stream: 2.48 -> 2.38 ms against 4 rows a workgroup; of one row 1.75 ->
+    // 1.72, the smaller LDS)
+    if (bl <= 16 && (long)B * heads * nblk * bl <= 256 && std::max(nk, hd) * 8 <= kAttnLdsThreads) *rq = 1;
+    if (grx_tune(GRX_TUNE_CONF_ATTN_RQ) >= 0) *rq = grx_tune(GRX_TUNE_CONF_ATTN_RQ);  // 0 (unstaged), 1, 4, 8 or 16, for tests
+    if (*rq != 0 && *rq != 1 && *rq != 4 && *rq != 8 && *rq != 16) *rq = 8;
+    if (*rq == 1 && !(bl <= 16 && std::max(nk, hd) * 8 <= kAttnLdsThreads)) *rq = 4;
     const size_t staged = attn_lds_smem_floats(nk, hd, *rq) * 4;
     const size_t sq = hd + 1;
-    const void *fn = *rq == 4   ? (const void *)conf_attn_lds_kernel<4>
+    const void *fn = *rq == 1   ? (const void *)conf_attn_lds_kernel<1, true>
+                     : *rq == 4 ? (const void *)conf_attn_lds_kernel<4>
                      : *rq == 8 ? (const void *)conf_attn_lds_kernel<8>
                                 : (const void *)conf_attn_lds_kernel<16>;
     if (*rq != 0 && staged <= 160 * 1024 &&
@@ -2100,7 +2108,10 @@ grx_status enqueue_run(grx_conformer *m, const CRun &r, hipStream_t st) {
             io.pp = r.pp + (size_t)i * d;
             io.ldp = hp.layers * d;
         }
-        if (r.attn_rq == 4 && attn_g8)
+        if (r.attn_rq == 1)
+            conf_attn_lds_kernel<1, true><<<dim3(nblk * r.keys.bl, hp.heads, B), kAttnLdsThreads, r.attn_smem, st>>>(
+                io, r.keys, Bk.pos_u, Bk.pos_v, d, hd, scale, bf.xq, bf.xs);
+        else if (r.attn_rq == 4 && attn_g8)
             conf_attn_lds_kernel<4, true><<<dim3(nblk * ((r.keys.bl + 3) / 4), hp.heads, B), kAttnLdsThreads,
                                             r.attn_smem, st>>>(io, r.keys, Bk.pos_u, Bk.pos_v, d, hd, scale, bf.xq,
                                                                bf.xs);

@@ -105,13 +105,13 @@ def test_stream_long_left_context(kern, orc, right):
     assert _stream_case(kern, orc, STREAM_TINY, t, right, 8.0, 62) >= 99
 
 
-@pytest.mark.parametrize("rq,g8,right", [(0, -1, 6), (4, -1, 6), (8, -1, 6), (16, -1, 6), (4, 0, 1), (4, -1, 1),
-                                         (4, -1, 0)])
+@pytest.mark.parametrize("rq,g8,right", [(0, -1, 6), (1, -1, 6), (4, -1, 6), (8, -1, 6), (16, -1, 6), (4, 0, 1),
+                                         (4, -1, 1), (4, -1, 0), (1, -1, 13)])
 def test_stream_attention_kernels(kern, orc, rq, g8, right):
     """Each attention kernel form on the chunk steps: unstaged, and staged
-    with 4, 8 or 16 query rows per workgroup; at right contexts 1 and 0 with
-    each output of a few-row block by 8 lanes (the default there) or by one
-    thread (CONF_ATTN_G8=0)."""
+    with 1, 4, 8 or 16 query rows per workgroup; at right contexts 1 and 0
+    with each output of a few-row block by 8 lanes or by one thread
+    (CONF_ATTN_G8=0)."""
     t = conformer_model(STREAM_TINY28, seed=39, pointwise_f16=True)
     with kern.tuned(CONF_ATTN_RQ=rq, CONF_ATTN_G8=g8):
         assert _stream_case(kern, orc, STREAM_TINY28, t, right, 3.0, 63, f" rq {rq} g8 {g8}") >= 35
