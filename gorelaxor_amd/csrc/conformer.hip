@@ -555,22 +555,39 @@ __device__ __forceinline__ void put_f4(float *d, bool a16, const float4 &v) {
     }
 }
 
-__device__ __forceinline__ void stage_f4(float *dst, int sdst, const float *src, size_t ssrc, int rows, int cols) {
-    const int c4 = cols >> 2, n = rows * c4, nt = blockDim.x;
-    const bool a16 = (sdst & 3) == 0;
-    for (int e0 = threadIdx.x; e0 < n; e0 += 4 * nt) {
-        float4 v[4];
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {  // clamped: the four loads stay in flight together
-            const int e = min(e0 + u * nt, n - 1);
-            v[u] = *reinterpret_cast<const float4 *>(src + (size_t)(e / c4) * ssrc + 4 * (e % c4));
-        }
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
-            const int e = e0 + u * nt;
-            if (e < n) put_f4(dst + (e / c4) * sdst + 4 * (e % c4), a16, v[u]);
-        }
+// f(row, col) with row(e), col(e) the row and float4 column of element e
+// of rows of cols/4 float4s: a shift and a mask where that is a power of
+// two (the usual head widths), else a division (the choice is uniform, so
+// only one form runs).
+template <class F>
+__device__ __forceinline__ void by_rows(int cols, F f) {
+    const int c4 = cols >> 2;
+    if ((c4 & (c4 - 1)) == 0) {
+        const int sh = __builtin_ctz(c4);
+        f([=](int e) { return e >> sh; }, [=](int e) { return e & (c4 - 1); });
+    } else {
+        f([=](int e) { return e / c4; }, [=](int e) { return e % c4; });
     }
+}
+
+__device__ __forceinline__ void stage_f4(float *dst, int sdst, const float *src, size_t ssrc, int rows, int cols) {
+    const int n = rows * (cols >> 2), nt = blockDim.x;
+    const bool a16 = (sdst & 3) == 0;
+    by_rows(cols, [&](auto row, auto col) {
+        for (int e0 = threadIdx.x; e0 < n; e0 += 4 * nt) {
+            float4 v[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {  // clamped: the four loads stay in flight together
+                const int e = min(e0 + u * nt, n - 1);
+                v[u] = *reinterpret_cast<const float4 *>(src + (size_t)row(e) * ssrc + 4 * col(e));
+            }
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const int e = e0 + u * nt;
+                if (e < n) put_f4(dst + row(e) * sdst + 4 * col(e), a16, v[u]);
+            }
+        }
+    });
 }
 
 // stage_f4 in two halves: the loads of the first U float4s a thread takes
@@ -578,26 +595,30 @@ __device__ __forceinline__ void stage_f4(float *dst, int sdst, const float *src,
 // stores and the rest of the rows.
 template <int U>
 __device__ __forceinline__ void stage_pre(float4 (&v)[U], const float *src, size_t ssrc, int rows, int cols) {
-    const int c4 = cols >> 2, n = rows * c4, nt = blockDim.x;
+    const int n = rows * (cols >> 2), nt = blockDim.x;
+    by_rows(cols, [&](auto row, auto col) {
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-        const int e = min((int)threadIdx.x + u * nt, n - 1);
-        v[u] = *reinterpret_cast<const float4 *>(src + (size_t)(e / c4) * ssrc + 4 * (e % c4));
-    }
+        for (int u = 0; u < U; ++u) {
+            const int e = min((int)threadIdx.x + u * nt, n - 1);
+            v[u] = *reinterpret_cast<const float4 *>(src + (size_t)row(e) * ssrc + 4 * col(e));
+        }
+    });
 }
 template <int U>
 __device__ __forceinline__ void stage_post(float *dst, int sdst, const float4 (&v)[U], const float *src, size_t ssrc,
                                            int rows, int cols) {
-    const int c4 = cols >> 2, n = rows * c4, nt = blockDim.x;
+    const int n = rows * (cols >> 2), nt = blockDim.x;
     const bool a16 = (sdst & 3) == 0;
+    by_rows(cols, [&](auto row, auto col) {
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-        const int e = threadIdx.x + u * nt;
-        if (e < n) put_f4(dst + (e / c4) * sdst + 4 * (e % c4), a16, v[u]);
-    }
-    for (int e = threadIdx.x + U * nt; e < n; e += nt)
-        put_f4(dst + (e / c4) * sdst + 4 * (e % c4), a16,
-               *reinterpret_cast<const float4 *>(src + (size_t)(e / c4) * ssrc + 4 * (e % c4)));
+        for (int u = 0; u < U; ++u) {
+            const int e = threadIdx.x + u * nt;
+            if (e < n) put_f4(dst + row(e) * sdst + 4 * col(e), a16, v[u]);
+        }
+        for (int e = threadIdx.x + U * nt; e < n; e += nt)
+            put_f4(dst + row(e) * sdst + 4 * col(e), a16,
+                   *reinterpret_cast<const float4 *>(src + (size_t)row(e) * ssrc + 4 * col(e)));
+    });
 }
 
 // MatMulF32's 6x16 panel route (kernels_amd64.s:5-88) for R rows a_j
