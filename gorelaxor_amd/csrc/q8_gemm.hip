@@ -863,7 +863,8 @@ __global__ __launch_bounds__(kLdsThreads) void gemm_q8_lds_kernel(const int8_t *
                                                                   const float *__restrict__ xs, int m,
                                                                   const float *__restrict__ bias,
                                                                   float *__restrict__ y, int ldc, float scale,
-                                                                  int8_t *__restrict__ yq, float *__restrict__ ys) {
+                                                                  int8_t *__restrict__ yq, float *__restrict__ ys,
+                                                                  const KsFuse fz) {
     // LDS per buffer: A [64 rows][CB][32] bytes, rows kAr apart (16 bytes of
     // padding: a fragment's 8-byte reads of 16 rows and a row's 16-byte
     // stores fall in distinct banks), B [CB][2 tiles][2 halves][64][16],
@@ -1055,7 +1056,25 @@ __global__ __launch_bounds__(kLdsThreads) void gemm_q8_lds_kernel(const int8_t *
                     if (li == 0) ys[(size_t)drow[r] * nr + n0 / GRX_QK] = __fmul_rn(amax, grx_bits_f32(0x3c010204u));
                 }
             }
+        } else if constexpr (EPI == GRX_GEMM_GLU) {
+            // the wave's 32 columns are one pair group (grx_glu_row): its
+            // 16 a-rows (g = 0) and their b-rows (g = 1) in the same lane,
+            // channel n0/2 + li
+            const int n0 = t0 * 64 + 32 * wn;
+            if (n0 < rows) {
+                const int rh = fz.ring.p != nullptr ? ring_head(fz.ring) : 0;
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    if (!drow_ok[r]) continue;
+                    const int sb = drow[r] / fz.T;
+                    const float v = drow[r] - sb * fz.T < fz.lens[sb] ? grx_glu_pair(c[f][0][r], c[f][1][r]) : 0.0f;
+                    const int ch = (n0 >> 1) + li;
+                    y[(size_t)drow[r] * ldc + ch] = v;
+                    if (fz.ring.p != nullptr) ring_put(fz.ring, ring_row(fz.ring, rh, drow[r]), ch - fz.ring.col0, v);
+                }
+            }
         } else {
+            const int rh = (EPI == GRX_GEMM_STORE && fz.ring.p != nullptr) ? ring_head(fz.ring) : 0;
 #pragma unroll
             for (int g = 0; g < 2; ++g) {
                 const int n = t0 * 64 + 32 * wn + 16 * g + li;
@@ -1064,7 +1083,11 @@ __global__ __launch_bounds__(kLdsThreads) void gemm_q8_lds_kernel(const int8_t *
                 for (int r = 0; r < 4; ++r) {
                     if (!drow_ok[r]) continue;
                     float *yp = y + (size_t)drow[r] * ldc + n;
-                    if constexpr (EPI == GRX_GEMM_STORE) *yp = c[f][g][r];
+                    if constexpr (EPI == GRX_GEMM_STORE) {
+                        *yp = c[f][g][r];
+                        if (fz.ring.p != nullptr && n >= fz.ring.col0)
+                            ring_put(fz.ring, ring_row(fz.ring, rh, drow[r]), n - fz.ring.col0, c[f][g][r]);
+                    }
                     if constexpr (EPI == GRX_GEMM_ADD) *yp = __fadd_rn(*yp, c[f][g][r]);
                     if constexpr (EPI == GRX_GEMM_AXPY_HALF) *yp = __fmaf_rn(0.5f, c[f][g][r], *yp);
                     if constexpr (EPI == GRX_GEMM_SCALE) *yp = __fmul_rn(c[f][g][r], scale);
@@ -1338,6 +1361,8 @@ bool grx_gemm_q8_fuses(const grx_weight *w, int m, const GemmOut &o) {
     if (p.r == kRouteGemv1)  // the one-row GEMV's prologue holds rows of up to 1280 values
         return (o.epi == GRX_GEMM_STORE || o.epi == GRX_GEMM_SILU_Q || o.epi == GRX_GEMM_GLU) &&
                (o.x == nullptr || w->nb * GRX_QK <= 1280);
+    if (p.r == kRouteLds)  // the LDS tiles: GLU and ring copies, no prologue
+        return o.x == nullptr;
     if (p.r != kRouteKs || !p.sa) return false;
     if (w->nb > ks_max_waves(p.ns, p.kb) * p.kb) return false;  // one run of blocks
     if (o.x != nullptr && (w->nb * GRX_QK > kKsProPieces * 256 || p.kb == 16 ||
@@ -1397,7 +1422,7 @@ grx_status grx_gemm_q8_launch_ex(hipStream_t st, const grx_weight *w, const int8
 #define GRX_GEMM_LDS(E)                                                                                           \
     case E:                                                                                                       \
         gemm_q8_lds_kernel<E><<<g2, kLdsThreads, 0, st>>>(w->qs, w->ds, w->rows, w->nb, w->tiles, xq, xs, m, bias, \
-                                                          o.y, o.ldc, o.scale, o.yq, o.ys);                       \
+                                                          o.y, o.ldc, o.scale, o.yq, o.ys, ks_fuse(o));           \
         break;
         switch (o.epi) {
             GRX_GEMM_LDS(GRX_GEMM_STORE)
@@ -1405,6 +1430,7 @@ grx_status grx_gemm_q8_launch_ex(hipStream_t st, const grx_weight *w, const int8
             GRX_GEMM_LDS(GRX_GEMM_AXPY_HALF)
             GRX_GEMM_LDS(GRX_GEMM_SCALE)
             GRX_GEMM_LDS(GRX_GEMM_SILU_Q)
+            GRX_GEMM_LDS(GRX_GEMM_GLU)
         }
 #undef GRX_GEMM_LDS
         GRX_LAUNCHED("gemm_q8_lds_kernel");

@@ -109,17 +109,18 @@ def test_depthwise_variants_bit_exact(kern, orc, dw):
         assert np.array_equal(got[b].view(np.uint32), want.view(np.uint32)), (dw, b)
 
 
-@pytest.mark.parametrize("fuse", [0, 1, 3])
-def test_tiny_fused_layernorms(kern, orc, fuse):
+@pytest.mark.parametrize("fuse,gk", [(0, -1), (1, -1), (3, -1), (1, 3)])
+def test_tiny_fused_layernorms(kern, orc, fuse, gk):
     """One utterance of 0.7 s (9 rows: one 16-row group) and two of 0.5 s:
     with CONF_FUSE=3 the K-split products take the blocks' LayerNorms in
     their prologues (a block's norm_out and the next one's LayerNorm in the
     first); by default pointwise1 takes its GLU; with CONF_FUSE=0 each is a
-    launch of its own - every form bit-identical to the oracle."""
+    launch of its own; on the LDS tiles (GEMM_KERNEL=3) pointwise1 takes
+    the GLU there - every form bit-identical to the oracle."""
     hp = dict(CONFORMER_TINY, layers=3)
     t = conformer_model(hp, seed=27)
     o = orc.ConformerOracle(hp, t)
-    with kern.tuned(CONF_FUSE=fuse):
+    with kern.tuned(CONF_FUSE=fuse, GEMM_KERNEL=gk):
         enc = _enc(kern, hp, t)
         for seconds, n in ((0.7, 1), (0.5, 2)):
             mel, frames, valid = _mels(hp, n, seconds, 41)

@@ -86,17 +86,18 @@ def test_stream_chunks_bit_exact(kern, orc, right):
     assert n >= 60
 
 
-@pytest.mark.parametrize("right,fuse,dw", [(13, 0, -1), (0, 0, -1), (13, 3, -1), (6, 3, -1), (13, -1, 0),
-                                           (0, -1, 0)])
-def test_stream_chunks_fusions(kern, orc, right, fuse, dw):
+@pytest.mark.parametrize("right,fuse,dw,gk", [(13, 0, -1, -1), (0, 0, -1, -1), (13, 3, -1, -1), (6, 3, -1, -1),
+                                              (13, -1, 0, -1), (0, -1, 0, -1), (13, -1, -1, 3), (0, -1, -1, 3)])
+def test_stream_chunks_fusions(kern, orc, right, fuse, dw, gk):
     """The chunk steps with every LayerNorm, GLU and cache copy in a launch
     of its own (CONF_FUSE=0), with the LayerNorms in the prologues of the
-    K-split products too (CONF_FUSE=3), and with the depthwise convolution's
-    LayerNorm by a whole workgroup (CONF_DW=0) instead of one wave: the
-    oracle's bits every way."""
+    K-split products too (CONF_FUSE=3), with the depthwise convolution's
+    LayerNorm by a whole workgroup (CONF_DW=0) instead of one wave, and with
+    every product on the LDS tiles (GEMM_KERNEL=3: their GLU and ring
+    copies): the oracle's bits every way."""
     t = conformer_model(STREAM_TINY28, seed=33, pointwise_f16=True)
-    with kern.tuned(CONF_FUSE=fuse, CONF_DW=dw):
-        assert _stream_case(kern, orc, STREAM_TINY28, t, right, 3.0, 64, f" fuse {fuse} dw {dw}") >= 35
+    with kern.tuned(CONF_FUSE=fuse, CONF_DW=dw, GEMM_KERNEL=gk):
+        assert _stream_case(kern, orc, STREAM_TINY28, t, right, 3.0, 64, f" fuse {fuse} dw {dw} gk {gk}") >= 35
 
 
 @pytest.mark.parametrize("right", [13, 0])
