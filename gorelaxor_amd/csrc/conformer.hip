@@ -151,24 +151,37 @@ __global__ void sub_conv01_kernel(const float *__restrict__ mel, int frames, int
     }
     const float bias0 = b0[ch], bias2 = b2[ch];
     const bool fm = ch < (c & ~7);
+    // the conv0 outputs of column kf = 2 of a position are column kf = 0 of
+    // the next one (conv0 position 2 f2 + 2 - pl): carried, not formed twice
+    float carry[3] = {0.f, 0.f, 0.f};
     for (int f2 = 0; f2 < F2; ++f2) {
         float o = 0.f;
         if (t2 < L2) {
             // the 7x7 mel values of this position: patch columns 4f2 .. 4f2+6,
-            // rows and columns 4t2-3pl.., 4f2-3pl.. of the plane
+            // rows and columns 4t2-3pl.., 4f2-3pl.. of the plane (columns 0
+            // and 1 feed only column kf = 0, carried past the first position)
             float pv[7][7];
 #pragma unroll
             for (int r = 0; r < 7; ++r)
 #pragma unroll
-                for (int q = 0; q < 7; ++q) pv[r][q] = patch[r * W + 4 * f2 + q];
+                for (int q = 2; q < 7; ++q) pv[r][q] = patch[r * W + 4 * f2 + q];
+            if (f2 == 0) {
+#pragma unroll
+                for (int r = 0; r < 7; ++r)
+#pragma unroll
+                    for (int q = 0; q < 2; ++q) pv[r][q] = patch[r * W + q];
+            }
             o = bias2;
+            float next[3];
 #pragma unroll
             for (int j2 = 0; j2 < 9; ++j2) {
                 const int kt = j2 / 3, kf = j2 % 3;
                 const int ti = 2 * t2 + kt - pl, fi = 2 * f2 + kf - pl;  // conv0 output position
-                if (ti < 0 || ti >= T1 || fi < 0 || fi >= F1) continue;
+                const bool in = !(ti < 0 || ti >= T1 || fi < 0 || fi >= F1);
                 float x = 0.f;
-                if (ti < L1) {
+                if (kf == 0 && f2 > 0) {
+                    x = carry[kt];
+                } else if (in && ti < L1) {
                     float a = bias0;
 #pragma unroll
                     for (int j = 0; j < 9; ++j) {
@@ -180,8 +193,12 @@ __global__ void sub_conv01_kernel(const float *__restrict__ mel, int frames, int
                     }
                     x = a < 0.f ? 0.f : a;
                 }
+                if (kf == 2) next[kt] = x;
+                if (!in) continue;
                 o = __fadd_rn(o, __fmul_rn(w2v[j2], x));
             }
+#pragma unroll
+            for (int kt = 0; kt < 3; ++kt) carry[kt] = next[kt];
         }
         const size_t p = ((size_t)b * T2 + t2) * F2 + f2;
         if (xf)
