@@ -467,7 +467,11 @@ __global__ __launch_bounds__(64 * ks_max_waves(NS, KB)) void gemm_q8_ks_kernel(
 // fragment reads of 16 rows fall in different banks), then the scales as
 // [block][row].
 constexpr int kss_row(int kb) { return kb * 32 + 16; }
-constexpr int kss_bytes(int kb) { return 16 * kss_row(kb) + 16 * kb * 4; }
+// The scales as [block][row], blocks kSdStride floats apart: a lane (row i,
+// scale quad q) stores blocks 4q..4q+3, so with a stride of 20 the four
+// lanes of a row write 16 banks apart (with 16 they shared a bank).
+constexpr int kSdStride = 20;
+constexpr int kss_bytes(int kb) { return 16 * kss_row(kb) + kSdStride * kb * 4; }
 
 // The K-split kernel's fused parts: PRO 1 builds the staged activations
 // from x rows by LayerNorm and rounding, PRO 2 by two LayerNorms with the
@@ -597,10 +601,10 @@ gemm_q8_kss_kernel(
         }
         if (lane < 16 * DQ) {
             const int i = lane / DQ, q = lane % DQ;
-            sd[(4 * q + 0) * 16 + i] = rd.x;
-            sd[(4 * q + 1) * 16 + i] = rd.y;
-            sd[(4 * q + 2) * 16 + i] = rd.z;
-            sd[(4 * q + 3) * 16 + i] = rd.w;
+            sd[(4 * q + 0) * kSdStride + i] = rd.x;
+            sd[(4 * q + 1) * kSdStride + i] = rd.y;
+            sd[(4 * q + 2) * kSdStride + i] = rd.z;
+            sd[(4 * q + 3) * kSdStride + i] = rd.w;
         }
     } else {
         // the fused prologue (one run of all nb blocks, K <= 1024): wave w
@@ -661,7 +665,7 @@ gemm_q8_kss_kernel(
                 int8_t *so = kss_stage + ow * kss_bytes(KB);
                 *reinterpret_cast<uint32_t *>(so + i * RS + u * GRX_QK + 4 * (P & 7)) = pk;
                 if ((P & 7) == 0)
-                    reinterpret_cast<float *>(so + 16 * RS)[u * 16 + i] = __fmul_rn(amax, grx_bits_f32(0x3c010204u));
+                    reinterpret_cast<float *>(so + 16 * RS)[u * kSdStride + i] = __fmul_rn(amax, grx_bits_f32(0x3c010204u));
             }
         };
         for (int i0 = wave; i0 < 16 && 16 * rf + i0 < m; i0 += 2 * ks) {
@@ -710,7 +714,7 @@ gemm_q8_kss_kernel(
     float dav[kHoist ? KB : 1];
     if constexpr (kHoist) {
 #pragma unroll
-        for (int u = 0; u < KB; ++u) dav[u] = sd[u * 16 + li];
+        for (int u = 0; u < KB; ++u) dav[u] = sd[u * kSdStride + li];
     }
 
     // the ordered chain, one wave after another
@@ -731,7 +735,7 @@ gemm_q8_kss_kernel(
             if (nbw == KB) {
 #pragma unroll
                 for (int u = 0; u < KB; ++u) {
-                    const float da = kHoist ? dav[kHoist ? u : 0] : sd[u * 16 + li];
+                    const float da = kHoist ? dav[kHoist ? u : 0] : sd[u * kSdStride + li];
 #pragma unroll
                     for (int s = 0; s < NS; ++s)
 #pragma unroll
@@ -741,7 +745,7 @@ gemm_q8_kss_kernel(
 #pragma unroll
                 for (int u = 0; u < KB; ++u) {
                     if (u < nbw) {
-                        const float da = kHoist ? dav[kHoist ? u : 0] : sd[u * 16 + li];
+                        const float da = kHoist ? dav[kHoist ? u : 0] : sd[u * kSdStride + li];
 #pragma unroll
                         for (int s = 0; s < NS; ++s)
 #pragma unroll
