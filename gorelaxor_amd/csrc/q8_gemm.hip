@@ -488,12 +488,15 @@ struct KsFuse {
 };
 constexpr int kKsProPieces = 4;  // a fused prologue's rows: at most 4 float4 pieces a lane (1024 values)
 
-// A fused prologue's LayerNorms (float64 sums and their checks) need more
-// than the 128 registers a lane has at four waves a SIMD: those
-// instantiations run at most kKsProWaves waves a workgroup, two a SIMD.
+// A fused prologue's product runs its chain on at most kKsProWaves waves,
+// and its workgroup has a wave for each row of the 16-row group besides
+// (kKsProLnWaves in all): each row's LayerNorm (float64 sums and their
+// checks, one wave's dependent chain) is one wave's, the waves past the
+// chain's only normalizing their rows.
 constexpr int kKsProWaves = 8;
+constexpr int kKsProLnWaves = 16;
 template <int EPI, int NS, int KB, int PRO = 0>
-__global__ __launch_bounds__(64 * (PRO != 0 ? kKsProWaves : ks_max_waves(NS, KB)), PRO != 0 ? 2 : 4) void
+__global__ __launch_bounds__(64 * (PRO != 0 ? kKsProLnWaves : ks_max_waves(NS, KB)), PRO != 0 ? 1 : 4) void
 gemm_q8_kss_kernel(
     const int8_t *__restrict__ qs, const uint16_t *__restrict__ ds, int rows, int nb, const int8_t *__restrict__ xq,
     const float *__restrict__ xs, int m, const float *__restrict__ bias, float *__restrict__ y, int ldc, float scale,
@@ -506,7 +509,11 @@ gemm_q8_kss_kernel(
     extern __shared__ __align__(16) int8_t kss_stage[];
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int ks = __builtin_amdgcn_readfirstlane(blockDim.x >> 6);
+    // nw waves, the first ks of them the chain's (a fused prologue's
+    // workgroup has more: they only normalize rows, and pass the barriers)
+    const int nw = __builtin_amdgcn_readfirstlane(blockDim.x >> 6);
+    const int ks = PRO != 0 ? (bend - bbeg + KB - 1) / KB : nw;
+    const bool chain = PRO == 0 || wave < ks;  // one of the chain's waves
     const int gi = blockIdx.x, xcd = gi & 7, slot = gi >> 3;
     const int rf = slot % nrf, cg = (slot / nrf) * 8 + xcd;
     if (cg >= ncg) return;  // the whole workgroup: no barrier is skipped
@@ -562,18 +569,41 @@ gemm_q8_kss_kernel(
             rd = *reinterpret_cast<const float4 *>(xs + (row * (unsigned)nb + b));
         }
     }
-    long bv[KB][NS];
+    // a fused prologue's row (row `wave` of the group) and the LayerNorm
+    // gains and biases, issued ahead of the weights so that the LayerNorm
+    // waits on these loads only (a row past m is clamped to row m - 1 and
+    // never staged)
+    constexpr int NPP = PRO == 0 ? 1 : kKsProPieces;
+    const int npc = (int)(K / 4);
+    float4 xv[NPP], wv[NPP], bw[NPP];
+    auto load_gains = [&](const float *lw, const float *lb) {
 #pragma unroll
-    for (int u = 0; u < KB; ++u) {
-        const unsigned b = (unsigned)min(b0 + u, bend - 1);
+        for (int j = 0; j < NPP; ++j) {
+            const int P = min(j * 64 + lane, npc - 1);
+            wv[j] = reinterpret_cast<const float4 *>(lw)[P];
+            bw[j] = reinterpret_cast<const float4 *>(lb)[P];
+        }
+    };
+    if constexpr (PRO != 0) {
+        const float4 *x4 = reinterpret_cast<const float4 *>(f.x + (size_t)min(16 * rf + wave, m - 1) * f.lda);
 #pragma unroll
-        for (int s = 0; s < NS; ++s) bv[u][s] = *reinterpret_cast<const long *>(wq + (qoff + b * 2048 + s * 256));
+        for (int j = 0; j < NPP; ++j) xv[j] = x4[min(j * 64 + lane, npc - 1)];
+        load_gains(f.lw, f.lb);
+        // keep the scheduler from hoisting the weight loads above these
+        __builtin_amdgcn_sched_barrier(0);
     }
-    // the weight scales in one load: lane q (< KB*NS*4) takes the four rows
-    // n0+16s+4j.. of block u, q = (u*NS + s)*4 + j; the lanes that need them
-    // fetch them from lane q with a cross-lane permute
-    uint2 wsq;
-    {
+    long bv[KB][NS];
+    uint2 wsq = make_uint2(0u, 0u);
+    if (chain) {
+#pragma unroll
+        for (int u = 0; u < KB; ++u) {
+            const unsigned b = (unsigned)min(b0 + u, bend - 1);
+#pragma unroll
+            for (int s = 0; s < NS; ++s) bv[u][s] = *reinterpret_cast<const long *>(wq + (qoff + b * 2048 + s * 256));
+        }
+        // the weight scales in one load: lane q (< KB*NS*4) takes the four
+        // rows n0+16s+4j.. of block u, q = (u*NS + s)*4 + j; the lanes that
+        // need them fetch them from lane q with a cross-lane permute
         const int q = min(lane, KB * NS * 4 - 1), u = q / (4 * NS), s = (q >> 2) % NS, j = q & 3;
         const unsigned b = (unsigned)min(b0 + u, bend - 1);
         wsq = *reinterpret_cast<const uint2 *>(reinterpret_cast<const char *>(wd) + 2 * (sub + 16 * s + 4 * j + b * 64));
@@ -608,40 +638,29 @@ gemm_q8_kss_kernel(
         }
     } else {
         // the fused prologue (one run of all nb blocks, K <= 1024): wave w
-        // takes rows w, w + ks, .. of the 16-row group, two at a time with
-        // their loads in flight together (the gains and biases, the same for
-        // every row, loaded once), each held as NP float4 pieces a lane,
+        // takes row w of the 16-row group (the launch gives the workgroup a
+        // wave for each row), held as NP float4 pieces a lane,
         // LayerNorm'd by wave_ln32 (kern.LayerNorm, internal/kern/mathx.go:
         // 55-75), and rounds each 32-value block (8 pieces in 8 lanes;
         // quantU8, q8int.go:88-105) into the stage of the wave that owns the
         // block.  Rows past m are not staged: their products are never
         // stored.
         constexpr int NP = kKsProPieces;
-        const int npc = (int)(K / 4);
-        float4 wv[NP], bw[NP], wv2[PRO == 2 ? NP : 1], bw2[PRO == 2 ? NP : 1];
-#pragma unroll
-        for (int j = 0; j < NP; ++j) {
-            const int P = min(j * 64 + lane, npc - 1);
-            wv[j] = reinterpret_cast<const float4 *>(f.lw)[P];
-            bw[j] = reinterpret_cast<const float4 *>(f.lb)[P];
-            if constexpr (PRO == 2) {
-                wv2[j] = reinterpret_cast<const float4 *>(f.lw2)[P];
-                bw2[j] = reinterpret_cast<const float4 *>(f.lb2)[P];
-            }
-        }
-        auto one_row = [&](float4 (&xv)[NP], int i) {
-            const int row = 16 * rf + i;
+        auto one_row = [&](int i) {
             wave_ln32<NP>(xv, wv, bw, npc, lane);
             if constexpr (PRO == 2) {
                 // a block's norm_out (conformer/encoder.go:426), kept by the
-                // first column group, then the next block's LayerNorm
+                // first column group, then the next block's LayerNorm (its
+                // gains in the first's registers, loaded while its
+                // statistics form)
+                load_gains(f.lw2, f.lb2);
                 if (cg == 0) {
-                    float4 *xo = reinterpret_cast<float4 *>(f.x_out + (size_t)row * f.lda);
+                    float4 *xo = reinterpret_cast<float4 *>(f.x_out + (size_t)(16 * rf + i) * f.lda);
 #pragma unroll
                     for (int j = 0; j < NP; ++j)
                         if (j * 64 + lane < npc) xo[j * 64 + lane] = xv[j];
                 }
-                wave_ln32<NP>(xv, wv2, bw2, npc, lane);
+                wave_ln32<NP>(xv, wv, bw, npc, lane);
             }
 #pragma unroll
             for (int j = 0; j < NP; ++j) {
@@ -668,41 +687,29 @@ gemm_q8_kss_kernel(
                     reinterpret_cast<float *>(so + 16 * RS)[u * kSdStride + i] = __fmul_rn(amax, grx_bits_f32(0x3c010204u));
             }
         };
-        for (int i0 = wave; i0 < 16 && 16 * rf + i0 < m; i0 += 2 * ks) {
-            const int i1 = i0 + ks;
-            const bool two = i1 < 16 && 16 * rf + i1 < m;  // uniform across the wave
-            float4 xa[NP], xb[NP];
-            const float4 *x0 = reinterpret_cast<const float4 *>(f.x + (size_t)(16 * rf + i0) * f.lda);
-            const float4 *x1 = reinterpret_cast<const float4 *>(f.x + (size_t)(16 * rf + (two ? i1 : i0)) * f.lda);
-#pragma unroll
-            for (int j = 0; j < NP; ++j) {
-                const int P = min(j * 64 + lane, npc - 1);
-                xa[j] = x0[P];
-                xb[j] = x1[P];
-            }
-            one_row(xa, i0);
-            if (two) one_row(xb, i1);
-        }
+        if (wave < 16 && 16 * rf + wave < m) one_row(wave);
     }
     __syncthreads();
 
     // the block dots (weight rows 4*lk+r of the 16, activation row li) and
-    // their scaled forms t = f32(s) * dw
+    // their scaled forms t = f32(s) * dw (the chain's waves only)
     float t[KB][NS][4];
+    if (chain) {
 #pragma unroll
-    for (int u = 0; u < KB; ++u) {
-        const long a = *reinterpret_cast<const long *>(sa + li * RS + u * GRX_QK + 8 * lk);
+        for (int u = 0; u < KB; ++u) {
+            const long a = *reinterpret_cast<const long *>(sa + li * RS + u * GRX_QK + 8 * lk);
 #pragma unroll
-        for (int s = 0; s < NS; ++s) {
-            v4i d = {0, 0, 0, 0};
-            d = __builtin_amdgcn_mfma_i32_16x16x32_i8(bv[u][s], a, d, 0, 0, 0);
-            const int src = ((u * NS + s) * 4 + lk) * 4;
-            const uint32_t h[2] = {(uint32_t)__builtin_amdgcn_ds_bpermute(src, (int)wsq.x),
-                                   (uint32_t)__builtin_amdgcn_ds_bpermute(src, (int)wsq.y)};
+            for (int s = 0; s < NS; ++s) {
+                v4i d = {0, 0, 0, 0};
+                d = __builtin_amdgcn_mfma_i32_16x16x32_i8(bv[u][s], a, d, 0, 0, 0);
+                const int src = ((u * NS + s) * 4 + lk) * 4;
+                const uint32_t h[2] = {(uint32_t)__builtin_amdgcn_ds_bpermute(src, (int)wsq.x),
+                                       (uint32_t)__builtin_amdgcn_ds_bpermute(src, (int)wsq.y)};
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const float dw = grx_f16_to_f32((uint16_t)(h[r >> 1] >> (16 * (r & 1))));
-                t[u][s][r] = __fmul_rn((float)d[r], dw);
+                for (int r = 0; r < 4; ++r) {
+                    const float dw = grx_f16_to_f32((uint16_t)(h[r >> 1] >> (16 * (r & 1))));
+                    t[u][s][r] = __fmul_rn((float)d[r], dw);
+                }
             }
         }
     }
@@ -714,7 +721,7 @@ gemm_q8_kss_kernel(
     float dav[kHoist ? KB : 1];
     if constexpr (kHoist) {
 #pragma unroll
-        for (int u = 0; u < KB; ++u) dav[u] = sd[u * kSdStride + li];
+        for (int u = 0; u < KB; ++u) dav[u] = chain ? sd[u * kSdStride + li] : 0.0f;
     }
 
     // the ordered chain, one wave after another
@@ -1156,16 +1163,16 @@ bool pick_ks(int m, int nb, int rows, int epi, bool carry, bool sa, bool pro, in
         if (few) k = nb <= ks_max_waves(n, 4) * 4 ? 4 : 16;
     }
     if (few && carry && nb > ks_max_waves(n, 16) * 16) k = 8;
-    // a fused prologue: more waves share the rows' LayerNorms (4 blocks a
-    // wave where a workgroup holds them)
-    if (pro) k = nb <= kKsProWaves * 4 ? 4 : 8;
+    // a fused prologue: 4 blocks a wave (its rows' LayerNorms take a wave
+    // each besides; K <= 1024 fits kKsProWaves waves of the chain)
+    if (pro) k = 4;
     const int tn = grx_tune(GRX_TUNE_GEMM_NS);
     if (tn == 1 || tn == 2) {
         n = pair ? 2 : tn;
         if (n == 2 && k > 8) k = 8;
     }
     const int tk = grx_tune(GRX_TUNE_GEMM_KB);
-    if ((tk == 4 || tk == 8 || tk == 16) && !(n == 2 && tk == 16) && !(pro && tk == 16)) k = tk;
+    if ((tk == 4 || tk == 8 || tk == 16) && !(n == 2 && tk == 16) && !pro) k = tk;
     if (n == 2 && k > 8) k = 8;
     if (nb > ks_max_waves(n, k) * k && !(carry && few)) return false;
     *ns = n;
@@ -1210,8 +1217,11 @@ void launch_ks_run(hipStream_t st, const grx_weight *w, const int8_t *xq, const 
     const int ncg = grx_ceil_div(w->rows, 16 * NS), nrf = grx_ceil_div(m, 16);
     const int ks = grx_ceil_div(bend - bbeg, KB);
     const int groups = grx_ceil_div(ncg, 8) * 8 * nrf;
+    // a fused prologue's workgroup: a wave for each row of a 16-row group
+    // as well (those past the chain's ks only normalize rows)
+    const int nw = PRO != 0 ? max(ks, min(16, m)) : ks;
     if constexpr (SA)
-        gemm_q8_kss_kernel<EPI, NS, KB, PRO><<<groups, 64 * ks, (size_t)ks * kss_bytes(KB), st>>>(
+        gemm_q8_kss_kernel<EPI, NS, KB, PRO><<<groups, 64 * nw, (size_t)ks * kss_bytes(KB), st>>>(
             w->qs, w->ds, w->rows, w->nb, xq, xs, m, bias, y, ldc, o.scale, o.yq, o.ys, ncg, nrf, bbeg, bend, init,
             w->rows, ks_fuse(o));
     else
@@ -1287,15 +1297,23 @@ void launch_ks_fused_pro(hipStream_t st, const grx_weight *w, const int8_t *xq, 
     using K4 = std::integral_constant<int, 4>;
     using K8 = std::integral_constant<int, 8>;
     using K16 = std::integral_constant<int, 16>;
-    if constexpr (EPI == GRX_GEMM_STORE) {
-        if (ns == 1) {
-            if (kb == 4) return go(I1{}, K4{});
-            if (kb == 8) return go(I1{}, K8{});
-            if constexpr (PRO == 0) return go(I1{}, K16{});
+    if constexpr (PRO != 0) {
+        // a fused prologue: 4 blocks a wave (pick_ks; K <= 1024)
+        (void)kb;
+        if constexpr (EPI == GRX_GEMM_STORE)
+            if (ns == 1) return go(I1{}, K4{});
+        return go(I2{}, K4{});
+    } else {
+        if constexpr (EPI == GRX_GEMM_STORE) {
+            if (ns == 1) {
+                if (kb == 4) return go(I1{}, K4{});
+                if (kb == 8) return go(I1{}, K8{});
+                return go(I1{}, K16{});
+            }
         }
+        if (kb == 4) return go(I2{}, K4{});
+        return go(I2{}, K8{});
     }
-    if (kb == 4) return go(I2{}, K4{});
-    return go(I2{}, K8{});
 }
 
 template <int EPI>

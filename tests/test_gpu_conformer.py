@@ -111,22 +111,25 @@ def test_depthwise_variants_bit_exact(kern, orc, dw):
 
 @pytest.mark.parametrize("fuse,gk", [(0, -1), (1, -1), (3, -1), (1, 3)])
 def test_tiny_fused_layernorms(kern, orc, fuse, gk):
-    """One utterance of 0.7 s (9 rows: one 16-row group) and two of 0.5 s:
-    with CONF_FUSE=3 the K-split products take the blocks' LayerNorms in
-    their prologues (a block's norm_out and the next one's LayerNorm in the
-    first); by default pointwise1 takes its GLU; with CONF_FUSE=0 each is a
-    launch of its own; on the LDS tiles (GEMM_KERNEL=3) pointwise1 takes
-    the GLU there - every form bit-identical to the oracle."""
+    """One utterance of 0.7 s (9 rows: one 16-row group), two of 0.5 s and
+    three of 0.7 s (27 rows: a second, partial group): with CONF_FUSE=3 the
+    K-split products take the blocks' LayerNorms in their prologues (a
+    block's norm_out and the next one's LayerNorm in the first); by default
+    pointwise1 takes its GLU; with CONF_FUSE=0 each is a launch of its own;
+    on the LDS tiles (GEMM_KERNEL=3) pointwise1 takes the GLU there - every
+    form bit-identical to the oracle."""
     hp = dict(CONFORMER_TINY, layers=3)
     t = conformer_model(hp, seed=27)
     o = orc.ConformerOracle(hp, t)
     with kern.tuned(CONF_FUSE=fuse, GEMM_KERNEL=gk):
         enc = _enc(kern, hp, t)
-        for seconds, n in ((0.7, 1), (0.5, 2)):
+        for seconds, n in ((0.7, 1), (0.5, 2), (0.7, 3)):
             mel, frames, valid = _mels(hp, n, seconds, 41)
-            got, lens = enc.encode(mel, [valid, valid - 7][:n])
+            lens_in = [valid, valid - 7, valid - 3][:n]
+            print(f"fused layernorms fuse {fuse} gk {gk}: {n} x {seconds} s", flush=True)
+            got, lens = enc.encode(mel, lens_in)
             for b in range(n):
-                want, L = o.encode(mel[b], [valid, valid - 7][b])
+                want, L = o.encode(mel[b], lens_in[b])
                 assert np.array_equal(got[b].view(np.uint32), want.view(np.uint32)), (fuse, seconds, b)
         enc.close()
 
