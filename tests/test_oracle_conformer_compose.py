@@ -1,0 +1,268 @@
+"""Pins the oracle's conformer block bit for bit, without a GPU.
+
+conformer/encoder.go:411-429 (runBlock) with feedForward (:244-251),
+attention (:259-330, the key ranges of :193-212) and convModule (:343-397)
+is composed here in Python, line by line from the reference, out of the
+oracle's primitives - each pinned on its own (test_oracle_kern.py: the int8
+product, kern's float32 product routes, SiLU, axpy, EXP8/expf and expSub,
+layerNorm; test_oracle_conformer.py: the relative position table and the
+batch norm fold) - and checked against the oracle's own block (one block
+offline, its position projection first: encoder.go:474-486).  Bit-equality
+shows the oracle's wiring (which norm feeds which product, the half-step
+residuals, the position biases u and v, the relative shift, the score
+scale, the key ranges and their blocks, the GLU halves and its masked
+rows, the depthwise taps and padding, the folded batch norm or the
+convolution's LayerNorm) is the reference's.  Planted mistakes in the
+composition must each break the bit-equality, which shows the pin sees
+them."""
+import math
+
+import numpy as np
+import pytest
+
+from gorelaxor_amd.synth import CONFORMER_TINY, conformer_model
+
+F32 = np.float32
+QK, Q8_BYTES = 32, 34
+
+
+def _bits(a):
+    return np.asarray(a, F32).view(np.uint32)
+
+
+def ln_kern(x, w, b, eps=1e-5):
+    """layerNorm (internal/kern/mathx.go:55-75) of each row: float64 sums
+    left to right, mean and inv rounded to float32, then ((v - mean) * inv)
+    * w + b in float32."""
+    x = np.asarray(x, F32)
+    out = np.empty_like(x)
+    for r in range(x.shape[0]):
+        v = x[r]
+        n = v.size
+        mean = F32(np.cumsum(v.astype(np.float64))[-1] / n)
+        d = (v - mean).astype(np.float64)
+        inv = F32(1.0 / math.sqrt(np.cumsum(d * d)[-1] / n + eps))
+        out[r] = ((v - mean) * inv) * np.asarray(w, F32) + np.asarray(b, F32)
+    return out
+
+
+def key_range(hp, T, L, q):
+    """keyRange (encoder.go:193-212) cut at the valid length L, with the
+    offline key form and query block length (offlineKeys, :196-212):
+    chunked limited context for a streaming model with both limits (blocks
+    of one chunk), a window for a regular one whose limits are shorter than
+    the recording (blocks of 16), else every key (blocks of 32)."""
+    al, ar = hp.get("att_left", -1), hp.get("att_right", -1)
+    chunked = hp.get("att_style", "regular") == "chunked_limited"
+    if chunked and al >= 0 and ar >= 0:
+        mode, bl = "chunked", ar + 1
+    elif al >= 0 and ar >= 0 and T - 1 > min(al, ar):
+        mode, bl = "window", 16
+    else:
+        mode, bl = "all", 32
+    if q is None:
+        return bl
+    if q >= L:
+        return 0, 0
+    lo, hi = 0, T
+    if mode == "chunked":
+        c = q // bl
+        lo = max((c - al // bl) * bl, 0)
+        hi = min((c + 1) * bl, T)
+    elif mode == "window":
+        lo, hi = max(q - al, 0), min(q + ar + 1, T)
+    return lo, min(hi, L)
+
+
+class Composed:
+    """runBlock over the oracle's primitives; `plant` names one mistake to
+    put in (None: the reference's block)."""
+
+    def __init__(self, orc, hp, t, plant=None):
+        self.orc, self.hp, self.t, self.plant = orc, hp, t, plant
+
+    def w(self, name, rows, cols):
+        """A product's weight as the encoder binds it: Q8_0 bytes, or a
+        float16 pointwise weight through Weight.ToQ8 (model.go:397-402)."""
+        w = self.t[name]
+        if w.nbytes == rows * cols // QK * Q8_BYTES:
+            return w
+        return self.orc.quant_q8(np.frombuffer(np.ascontiguousarray(w).tobytes(), np.float16).astype(F32))
+
+    def linear(self, x, name, n, k, bias=None):
+        b = self.t.get(bias) if bias else None
+        return self.orc.matmul_q8_int(x, self.w(name, n, k), n, k, bias=b)
+
+    def ln(self, x, name):
+        w, b = self.t[name + ".weight"], self.t[name + ".bias"]
+        if self.plant == "ln_eps":
+            return ln_kern(x, w, b, eps=1e-6)
+        return self.orc.layernorm(x, w, b)
+
+    def feed_forward(self, x, p, f):
+        """feedForward (encoder.go:244-251): x += 0.5 * linear2(SiLU(linear1(LN(x))))."""
+        orc, hp = self.orc, self.hp
+        d, dff = hp["d"], hp["dff"]
+        h = self.linear(self.ln(x, p + "norm_" + f), p + f + ".linear1.weight", dff, d, p + f + ".linear1.bias")
+        h = orc.silu(h.ravel()).reshape(h.shape)
+        y = self.linear(h, p + f + ".linear2.weight", d, dff, p + f + ".linear2.bias")
+        s = 1.0 if self.plant == "ff_full_step" else 0.5
+        return orc.axpy(x.ravel(), y.ravel(), s).reshape(x.shape)
+
+    def attention(self, x, ln, p, L):
+        orc, hp, t = self.orc, self.hp, self.t
+        T, D, H = x.shape[0], hp["d"], hp["heads"]
+        hd = D // H
+        q = self.linear(ln, p + "attn.linear_q.weight", D, D, p + "attn.linear_q.bias")
+        k = self.linear(ln, p + "attn.linear_k.weight", D, D, p + "attn.linear_k.bias")
+        v = self.linear(ln, p + "attn.linear_v.weight", D, D, p + "attn.linear_v.bias")
+        u, w = t[p + "attn.pos_bias_u"].reshape(D), t[p + "attn.pos_bias_v"].reshape(D)
+        if self.plant == "pos_bias_swap":
+            u, w = w, u
+        qu, qv = q + u, q + w
+        # the position rows for relative positions T-1 .. -(T-1) (relPosEmb)
+        pp = self.linear(orc.conf_rel_pos(T, D), p + "attn.linear_pos.weight", D, D)
+        scale = F32(1.0 / math.sqrt(D if self.plant == "scale_d" else hd))
+        bl = key_range(hp, T, L, None)
+        out = np.zeros((T, D), F32)
+        for h in range(H):
+            sl = slice(h * hd, (h + 1) * hd)
+            for q0 in range(0, T, bl):
+                q1 = min(T, q0 + bl)
+                nq = q1 - q0
+                rng = [key_range(hp, T, L, qq) for qq in range(q0, q1)]
+                k0, k1 = min(r[0] for r in rng), max(r[1] for r in rng)
+                nk = k1 - k0
+                if nk <= 0:
+                    continue
+                # the block's scores and position terms by kern's float32
+                # products (MatMulF32), the position rows from jlo on
+                npos = nq + nk - 1
+                jlo = T - 1 - (q1 - 1) + k0
+                sc = orc.matmul_f32(np.ascontiguousarray(qu[q0:q1, sl]), np.ascontiguousarray(k[k0:k1, sl]))
+                bd = orc.matmul_f32(np.ascontiguousarray(qv[q0:q1, sl]),
+                                    np.ascontiguousarray(pp[jlo:jlo + npos, sl]))
+                for i in range(nq):
+                    lo, hi = rng[i]
+                    sh = nq - 1 - i
+                    if self.plant == "rel_shift":
+                        sh = nq - i if nq - i + nk <= npos else nq - 2 - i
+                    row = np.full(nk, -np.inf, F32)
+                    for kk in range(nk):
+                        if lo <= k0 + kk < hi:
+                            row[kk] = F32(sc[i, kk] + bd[i, sh + kk]) * scale
+                    ok = row[np.isfinite(row)]
+                    if ok.size == 0:
+                        sc[i] = 0
+                        continue
+                    e, s = orc.expsub(row, float(ok.max()))
+                    sc[i] = e * (F32(1) / F32(s))
+                vt = np.ascontiguousarray(v[k0:k1, sl].T)
+                out[q0:q1, sl] = orc.matmul_f32(np.ascontiguousarray(sc), vt)
+        att = self.linear(out, p + "attn.linear_out.weight", D, D, p + "attn.linear_out.bias")
+        return x + att
+
+    def conv_module(self, x, ln, p, L):
+        orc, hp, t = self.orc, self.hp, self.t
+        T, D, K = x.shape[0], hp["d"], hp["conv_kernel"]
+        a = self.linear(ln, p + "conv.pointwise1.weight", 2 * D, D, p + "conv.pointwise1.bias")
+        # GLU a * sigmoid(b), rows from the valid length on zero
+        g = np.zeros((T, D), F32)
+        for r in range(T):
+            if r >= L and self.plant != "glu_unmasked":
+                continue
+            lhs, rhs = (a[r, D:], a[r, :D]) if self.plant == "glu_swap" else (a[r, :D], a[r, D:])
+            sg = np.array([F32(1) / (F32(1) + F32(orc.expf(float(-z)))) for z in rhs], F32)
+            g[r] = lhs * sg
+        # depthwise taps from the bias, padL frames of zeros before
+        # (convPadLeft, encoder.go:399-404), unfused w * x sums in tap order
+        cl, cr = hp.get("conv_left", -1), hp.get("conv_right", -1)
+        padL = cl if cl >= 0 and cr >= 0 else (K - 1) // 2
+        dw = np.asarray(t[p + "conv.depthwise.weight"], F32).reshape(D, K)
+        b = t.get(p + "conv.depthwise.bias")
+        y = np.tile(np.asarray(b, F32) if b is not None else np.zeros(D, F32), (T, 1))
+        for r in range(T):
+            for j in range(K):
+                ti = r + j - padL
+                if 0 <= ti < T:
+                    tap = dw[:, K - 1 - j] if self.plant == "dw_reversed" else dw[:, j]
+                    y[r] = y[r] + tap * g[ti]
+        if hp.get("conv_norm", "batch_norm") == "layer_norm":
+            y = orc.layernorm(y, t[p + "conv.bn.weight"], t[p + "conv.bn.bias"])
+        else:
+            s, c = orc.conf_bn_fold(t[p + "conv.bn.weight"], t[p + "conv.bn.bias"], t[p + "conv.bn.running_mean"],
+                                    t[p + "conv.bn.running_var"])
+            y = y * s + c
+        y = orc.silu(y.ravel()).reshape(T, D)
+        return x + self.linear(y, p + "conv.pointwise2.weight", D, D, p + "conv.pointwise2.bias")
+
+    def block(self, i, x, L):
+        """runBlock (encoder.go:411-429)."""
+        p = f"enc.blocks.{i}."
+        x = np.asarray(x, F32).copy()
+        x = self.feed_forward(x, p, "ff1")
+        x = self.attention(x, self.ln(x, p + "norm_attn"), p, L)
+        x = self.conv_module(x, self.ln(x, p + "norm_conv"), p, L)
+        x = self.feed_forward(x, p, "ff2")
+        return self.ln(x, p + "norm_out")
+
+
+# the tiny regular model (every key, blocks of 32, batch norm), and a
+# streaming-shaped one (chunked limited context of 4-row chunks with two
+# chunks of left context, a causal convolution with its LayerNorm)
+CHUNKED = dict(CONFORMER_TINY, conv_norm="layer_norm", att_style="chunked_limited", att_left=8, att_right=3,
+               conv_left=8, conv_right=0)
+
+
+@pytest.fixture(scope="module", params=["regular", "chunked"])
+def model(request):
+    hp = dict(CONFORMER_TINY) if request.param == "regular" else dict(CHUNKED)
+    return hp, conformer_model(hp, seed=9)
+
+
+def test_restated_layernorm_equals_the_oracles(orc):
+    rng = np.random.default_rng(3)
+    for n in (32, 64, 96):
+        x = (rng.standard_normal((5, n)) * 3).astype(F32)
+        w, b = rng.standard_normal(n).astype(F32), rng.standard_normal(n).astype(F32)
+        assert np.array_equal(_bits(ln_kern(x, w, b)), _bits(orc.layernorm(x, w, b))), n
+
+
+def test_key_ranges_equal_the_oracles(orc, model):
+    """The composition's key ranges and block length are the oracle's (its
+    key range loops are pinned to their closed forms on their own)."""
+    hp, t = model
+    m = orc.ConformerOracle(hp, t)
+    for T, L in ((40, 37), (40, 40), (23, 9)):
+        keys, bl = m.offline_keys(T, L)
+        assert bl == key_range(hp, T, L, None), (T, L)
+        assert [tuple(orc.conf_key_range(keys, q)) for q in range(T)] == [key_range(hp, T, L, q) for q in range(T)]
+
+
+@pytest.mark.parametrize("T,L", [(40, 37), (23, 23)])
+def test_oracle_block_is_the_composition(orc, model, T, L):
+    """Each block of the oracle equals the composition bit for bit on an
+    input with valid length L (rows from L on masked)."""
+    hp, t = model
+    m = orc.ConformerOracle(hp, t)
+    comp = Composed(orc, hp, t)
+    rng = np.random.default_rng(T + L)
+    x = rng.standard_normal((T, hp["d"])).astype(F32)
+    for i in range(hp["layers"]):
+        want = m.block(i, x, L)
+        got = comp.block(i, x, L)
+        assert np.array_equal(_bits(got), _bits(want)), (i, T, L)
+        x = want
+
+
+@pytest.mark.parametrize("plant", ["ff_full_step", "pos_bias_swap", "rel_shift", "scale_d", "glu_swap",
+                                   "glu_unmasked", "dw_reversed", "ln_eps"])
+def test_planted_mistakes_break_the_pin(orc, model, plant):
+    """Each planted mistake changes the block's bits."""
+    hp, t = model
+    m = orc.ConformerOracle(hp, t)
+    rng = np.random.default_rng(77)
+    T, L = 40, 37
+    x = rng.standard_normal((T, hp["d"])).astype(F32)
+    got = Composed(orc, hp, t, plant=plant).block(0, x, L)
+    assert not np.array_equal(_bits(got), _bits(m.block(0, x, L))), plant
