@@ -1,8 +1,10 @@
 """Pins the oracle's conformer block bit for bit, without a GPU.
 
 conformer/encoder.go:411-429 (runBlock) with feedForward (:244-251),
-attention (:259-330, the key ranges of :193-212) and convModule (:343-397)
-is composed here in Python, line by line from the reference, out of the
+attention (:259-330, the key ranges of :193-212) and convModule (:343-397),
+and the pre-encoder (subsample, :123-167, with conv0 :41-77 and dwConv2
+:80-110) and the whole encode (:432-489) over them, are composed here in
+Python, line by line from the reference, out of the
 oracle's primitives - each pinned on its own (test_oracle_kern.py: the int8
 product, kern's float32 product routes, SiLU, axpy, EXP8/expf and expSub,
 layerNorm; test_oracle_conformer.py: the relative position table and the
@@ -12,7 +14,8 @@ shows the oracle's wiring (which norm feeds which product, the half-step
 residuals, the position biases u and v, the relative shift, the score
 scale, the key ranges and their blocks, the GLU halves and its masked
 rows, the depthwise taps and padding, the folded batch norm or the
-convolution's LayerNorm) is the reference's.  Planted mistakes in the
+convolution's LayerNorm; the pre-encoder's padding, masks, ReLUs and
+flattening order, the xscale) is the reference's.  Planted mistakes in the
 composition must each break the bit-equality, which shows the pin sees
 them."""
 import math
@@ -196,6 +199,100 @@ class Composed:
         y = orc.silu(y.ravel()).reshape(T, D)
         return x + self.linear(y, p + "conv.pointwise2.weight", D, D, p + "conv.pointwise2.bias")
 
+    def subsample(self, mel, valid):
+        """subsample (encoder.go:123-167): (out [T][d], T, L)."""
+        orc, hp, t = self.orc, self.hp, self.t
+        nm, c, d = hp["n_mels"], hp["sub_channels"], hp["d"]
+        chunked = hp.get("att_style", "regular") == "chunked_limited"
+        causal = bool(hp.get("causal_sub", chunked))
+        pl = 2 if causal else 1  # rows and bins of padding before (subOut, encoder.go:33-38)
+        if self.plant == "sub_pad":
+            pl = 3 - pl
+        out_n = (lambda n: n // 2 + 1) if causal else (lambda n: (n - 1) // 2 + 1)
+        pe = "enc.pre_encode."
+        taps = lambda n: np.ascontiguousarray(np.asarray(t[pe + n], F32).reshape(c, 9).T)  # noqa: E731
+        mel = np.asarray(mel, F32)
+        frames = mel.shape[1]
+        x = np.zeros((frames, nm), F32)
+        x[:min(frames, valid)] = mel[:, :min(frames, valid)].T
+
+        def mask(y, L):
+            if not (self.plant == "sub_unmasked") and L < y.shape[0]:
+                y[max(L, 0):] = 0
+            return y
+
+        def relu(y):
+            return np.where(y < 0, F32(0), y).astype(F32)
+
+        # conv0 (encoder.go:41-77): each output from the bias, AddScaled of
+        # the nine taps in order, taps equal to 0 skipped
+        T, F = frames, nm
+        T1, F1 = out_n(T), out_n(F)
+        w0, b0 = taps("conv.0.weight"), np.asarray(t[pe + "conv.0.bias"], F32)
+        y = np.empty((T1, F1, c), F32)
+        for r in range(T1):
+            for f in range(F1):
+                o = b0.copy()
+                for kt in range(3):
+                    for kf in range(3):
+                        ti, fi = 2 * r + kt - pl, 2 * f + kf - pl
+                        v = x[ti, fi] if (0 <= ti < T and 0 <= fi < F) else F32(0)
+                        if v != 0:
+                            o = orc.axpy(o, w0[kt * 3 + kf], float(v))
+                y[r, f] = o
+        L = out_n(valid)
+        y = relu(mask(y, L))
+
+        def dw(y, name, L):
+            # dwConv2 (encoder.go:80-110): from the bias, w * x unfused over
+            # the taps in range, in order
+            T, F = y.shape[0], y.shape[1]
+            T1, F1 = out_n(T), out_n(F)
+            w, b = taps(name + ".weight"), np.asarray(t[pe + name + ".bias"], F32)
+            o = np.tile(b, (T1, F1, 1))
+            for kt in range(3):
+                for kf in range(3):
+                    for r in range(T1):
+                        ti = 2 * r + kt - pl
+                        if not 0 <= ti < T:
+                            continue
+                        for f in range(F1):
+                            fi = 2 * f + kf - pl
+                            if 0 <= fi < F:
+                                o[r, f] = o[r, f] + w[kt * 3 + kf] * y[ti, fi]
+            L = out_n(L)
+            return mask(o, L), L
+
+        def pointwise(y, name, L):
+            T, F = y.shape[0], y.shape[1]
+            w, b = t[pe + name + ".weight"], t[pe + name + ".bias"]
+            flat = y.reshape(T * F, c)
+            if np.asarray(w).dtype == np.float32:
+                z = orc.matmul_f32(flat, np.asarray(w, F32).reshape(c, c), bias=b)
+            else:
+                z = orc.matmul_q8_int(flat, w, c, c, bias=b)
+            return relu(mask(z.reshape(T, F, c), L))
+
+        y, L = dw(y, "conv.2", L)
+        y = pointwise(y, "conv.3", L)
+        y, L = dw(y, "conv.5", L)
+        y = pointwise(y, "conv.6", L)
+        T, F = y.shape[0], y.shape[1]
+        # flattened [t][c*F+f] (encoder.go:158-166), then the output Linear
+        flat = y.reshape(T, F * c) if self.plant == "sub_flatten" else y.transpose(0, 2, 1).reshape(T, c * F)
+        out = orc.matmul_q8_int(np.ascontiguousarray(flat), t[pe + "out.weight"], d, c * F, bias=t[pe + "out.bias"])
+        return out, T, max(0, min(L, T))
+
+    def encode(self, mel, valid):
+        """Model.encode (encoder.go:432-489): the pre-encoder, x *= f32(sqrt(d))
+        when the model scales, each block; (out [T][d], L)."""
+        x, T, L = self.subsample(mel, valid)
+        if self.hp.get("xscaling", True) and self.plant != "no_xscale":
+            x = x * F32(math.sqrt(self.hp["d"]))
+        for i in range(self.hp["layers"]):
+            x = self.block(i, x, L)
+        return x, L
+
     def block(self, i, x, L):
         """runBlock (encoder.go:411-429)."""
         p = f"enc.blocks.{i}."
@@ -266,3 +363,34 @@ def test_planted_mistakes_break_the_pin(orc, model, plant):
     x = rng.standard_normal((T, hp["d"])).astype(F32)
     got = Composed(orc, hp, t, plant=plant).block(0, x, L)
     assert not np.array_equal(_bits(got), _bits(m.block(0, x, L))), plant
+
+
+def test_oracle_subsample_and_encode_are_the_composition(orc, model):
+    """The oracle's pre-encoder and whole encode (pre-encoder, xscale,
+    every block) equal the composition bit for bit, valid frames short of
+    the recording."""
+    from gorelaxor_amd.synth import noise_mel
+    hp, t = model
+    m = orc.ConformerOracle(hp, t)
+    comp = Composed(orc, hp, t)
+    mel, frames, valid = noise_mel(hp["n_mels"], seconds=0.8, seed=12)
+    for v in (valid, valid - 13):
+        want, T, L = m.subsample(mel, v)
+        got, T2, L2 = comp.subsample(mel, v)
+        assert (T, L) == (T2, L2), v
+        assert np.array_equal(_bits(got), _bits(want)), v
+        want, L = m.encode(mel, v)
+        got, L2 = comp.encode(mel, v)
+        assert L == L2 and np.array_equal(_bits(got), _bits(want)), v
+
+
+@pytest.mark.parametrize("plant", ["sub_pad", "sub_unmasked", "sub_flatten", "no_xscale"])
+def test_planted_pre_encoder_mistakes_break_the_pin(orc, model, plant):
+    """Each planted pre-encoder mistake changes the encode's bits."""
+    from gorelaxor_amd.synth import noise_mel
+    hp, t = model
+    m = orc.ConformerOracle(hp, t)
+    mel, frames, valid = noise_mel(hp["n_mels"], seconds=0.8, seed=12)
+    want, L = m.encode(mel, valid - 13)
+    got, L2 = Composed(orc, hp, t, plant=plant).encode(mel, valid - 13)
+    assert got.shape != want.shape or not np.array_equal(_bits(got), _bits(want)), plant
