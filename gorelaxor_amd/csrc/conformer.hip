@@ -2023,6 +2023,10 @@ grx_status enqueue_run(grx_conformer *m, const CRun &r, hipStream_t st) {
     const int attn_rows_wg = std::min(r.attn_rq, r.keys.bl), attn_keys_max = r.attn_keys;
     const bool attn_g8 = grx_tune(GRX_TUNE_CONF_ATTN_G8) != 0 && r.keys.bl <= 16 &&
                          attn_rows_wg * std::max(attn_keys_max, hd) * 8 <= kAttnLdsThreads;
+    // threads of the row-a-workgroup launch (its loops go by the block's
+    // size, staging what the registers do not hold straight from memory)
+    const int attn_thr = grx_tune(GRX_TUNE_CONF_ATTN_THREADS);
+    const int attn1_threads = attn_thr == 256 || attn_thr == 512 ? attn_thr : kAttnLdsThreads;
     const int fz = grx_tune(GRX_TUNE_CONF_FUSE);  // 0 none, 3 LayerNorm prologues on up to 32 rows
     const bool fuse_ln = R <= kFuseLnRows && fz != 0 && (fz == 3 || R == 1) && bf.x2 != nullptr &&
                          probe(B0.qkv, GRX_GEMM_STORE, true, false, kv_ring) &&
@@ -2147,7 +2151,7 @@ grx_status enqueue_run(grx_conformer *m, const CRun &r, hipStream_t st) {
             io.ldp = hp.layers * d;
         }
         if (r.attn_rq == 1)
-            conf_attn_lds_kernel<1, true><<<dim3(nblk * r.keys.bl, hp.heads, B), kAttnLdsThreads, r.attn_smem, st>>>(
+            conf_attn_lds_kernel<1, true><<<dim3(nblk * r.keys.bl, hp.heads, B), attn1_threads, r.attn_smem, st>>>(
                 io, r.keys, Bk.pos_u, Bk.pos_v, d, hd, scale, bf.xq, bf.xs);
         else if (r.attn_rq == 4 && attn_g8)
             conf_attn_lds_kernel<4, true><<<dim3(nblk * ((r.keys.bl + 3) / 4), hp.heads, B), kAttnLdsThreads,

@@ -50,7 +50,8 @@ extern "C" long long grx_debug_alloc_countdown(void) { return g_alloc_countdown.
 static const char *const kTuneNames[GRX_TUNE_COUNT] = {
     "GEMM_MIN_M", "GEMM_KERNEL", "GEMM_NS",    "GEMM_KB",     "GEMV_WAVES",    "GEMV1",
     "CONF_ATTN_RQ", "FUSE_LN",   "FUSE_XSCORES", "WAVE_VALUES", "ARGMAX_ATOMIC", "NO_GRAPH",
-    "GEMM_STAGE_A", "GEMV_MX", "GEMV1_ROWS", "FUSE_SELF_ATTN", "CONF_DW", "CONF_FUSE", "CONF_ATTN_G8"};
+    "GEMM_STAGE_A", "GEMV_MX", "GEMV1_ROWS", "FUSE_SELF_ATTN", "CONF_DW", "CONF_FUSE", "CONF_ATTN_G8",
+    "CONF_ATTN_THREADS"};
 static std::atomic<int> g_tune[GRX_TUNE_COUNT];
 static std::once_flag g_tune_once;
 

@@ -134,6 +134,7 @@ enum {
                               // 3: LayerNorms in the prologues of products of up to 32 rows too
                               // (default: of one-row products only)
     GRX_TUNE_CONF_ATTN_G8,    // 0: the conformer attention's few-row outputs one a thread, not 8 lanes each
+    GRX_TUNE_CONF_ATTN_THREADS,  // 256 or 512: threads of the conformer attention's row-a-workgroup launch
     GRX_TUNE_COUNT
 };
 int grx_tune(int id);

@@ -249,7 +249,7 @@ def set_tune(name: str, value: int) -> None:
     """Override one of the library's kernel choices (grx_debug_tune: GEMM_MIN_M,
     GEMM_KERNEL, GEMM_NS, GEMM_KB, GEMV_WAVES, GEMV1, CONF_ATTN_RQ, FUSE_LN,
     FUSE_XSCORES, WAVE_VALUES, ARGMAX_ATOMIC, NO_GRAPH, GEMM_STAGE_A, GEMV_MX, GEMV1_ROWS,
-    FUSE_SELF_ATTN, CONF_DW, CONF_FUSE, CONF_ATTN_G8); -1 hands it back.
+    FUSE_SELF_ATTN, CONF_DW, CONF_FUSE, CONF_ATTN_G8, CONF_ATTN_THREADS); -1 hands it back.
     The reference's tests switch kernels the same way (setInt, internal/kern/
     kernels_amd64.go:190-200)."""
     _lib.call("grx_debug_tune", name.encode(), int(value))

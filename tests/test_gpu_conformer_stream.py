@@ -106,16 +106,18 @@ def test_stream_long_left_context(kern, orc, right):
     assert _stream_case(kern, orc, STREAM_TINY, t, right, 8.0, 62) >= 99
 
 
-@pytest.mark.parametrize("rq,g8,right", [(0, -1, 6), (1, -1, 6), (4, -1, 6), (8, -1, 6), (16, -1, 6), (4, 0, 1),
-                                         (4, -1, 1), (4, -1, 0), (1, -1, 13)])
-def test_stream_attention_kernels(kern, orc, rq, g8, right):
+@pytest.mark.parametrize("rq,g8,right,thr", [(0, -1, 6, -1), (1, -1, 6, -1), (4, -1, 6, -1), (8, -1, 6, -1),
+                                             (16, -1, 6, -1), (4, 0, 1, -1), (4, -1, 1, -1), (4, -1, 0, -1),
+                                             (1, -1, 13, -1), (1, -1, 13, 256), (1, -1, 0, 512)])
+def test_stream_attention_kernels(kern, orc, rq, g8, right, thr):
     """Each attention kernel form on the chunk steps: unstaged, and staged
     with 1, 4, 8 or 16 query rows per workgroup; at right contexts 1 and 0
     with each output of a few-row block by 8 lanes or by one thread
-    (CONF_ATTN_G8=0)."""
+    (CONF_ATTN_G8=0); a row a workgroup on 256 or 512 threads
+    (CONF_ATTN_THREADS) as well as 1024."""
     t = conformer_model(STREAM_TINY28, seed=39, pointwise_f16=True)
-    with kern.tuned(CONF_ATTN_RQ=rq, CONF_ATTN_G8=g8):
-        assert _stream_case(kern, orc, STREAM_TINY28, t, right, 3.0, 63, f" rq {rq} g8 {g8}") >= 35
+    with kern.tuned(CONF_ATTN_RQ=rq, CONF_ATTN_G8=g8, CONF_ATTN_THREADS=thr):
+        assert _stream_case(kern, orc, STREAM_TINY28, t, right, 3.0, 63, f" rq {rq} g8 {g8} thr {thr}") >= 35
 
 
 def test_streams_together_equal_alone(kern, orc):
