@@ -120,6 +120,16 @@ def test_stream_attention_kernels(kern, orc, rq, g8, right, thr):
         assert _stream_case(kern, orc, STREAM_TINY28, t, right, 3.0, 63, f" rq {rq} g8 {g8} thr {thr}") >= 35
 
 
+def test_stream_attention_staging_overflow(kern, orc):
+    """A row a workgroup on 256 threads whose staged rows (up to 84 keys of
+    a 64-wide head, 1344 float4s) outnumber the 1024 its registers hold:
+    the rest is staged straight from memory, the same bits."""
+    hp = dict(STREAM_TINY, heads=1)
+    t = conformer_model(hp, seed=40, pointwise_f16=True)
+    with kern.tuned(CONF_ATTN_RQ=1, CONF_ATTN_THREADS=256):
+        assert _stream_case(kern, orc, hp, t, 13, 8.0, 66, " staging overflow") >= 99
+
+
 def test_streams_together_equal_alone(kern, orc):
     """Three streams stepped together: each one's rows are those it gets
     alone (and the oracle's); the last chunks have different real frames."""
