@@ -112,28 +112,32 @@ class Composed:
         s = 1.0 if self.plant == "ff_full_step" else 0.5
         return orc.axpy(x.ravel(), y.ravel(), s).reshape(x.shape)
 
-    def attention(self, x, ln, p, L):
+    def attention(self, x, ln, p, L, kv, keyf, bl, pp):
+        """attention (encoder.go:259-330): queries the T rows ln, keys and
+        values from the Tk rows kv (the queries' own rows last: query i is
+        key Tk - T + i), keyf(key index of a query) its keys [lo, hi),
+        queries in blocks of bl, pp the projected position rows for
+        relative positions Tk - 1 down."""
         orc, hp, t = self.orc, self.hp, self.t
         T, D, H = x.shape[0], hp["d"], hp["heads"]
         hd = D // H
+        Tk = kv.shape[0]
+        qoff = Tk - T
         q = self.linear(ln, p + "attn.linear_q.weight", D, D, p + "attn.linear_q.bias")
-        k = self.linear(ln, p + "attn.linear_k.weight", D, D, p + "attn.linear_k.bias")
-        v = self.linear(ln, p + "attn.linear_v.weight", D, D, p + "attn.linear_v.bias")
+        k = self.linear(kv, p + "attn.linear_k.weight", D, D, p + "attn.linear_k.bias")
+        v = self.linear(kv, p + "attn.linear_v.weight", D, D, p + "attn.linear_v.bias")
         u, w = t[p + "attn.pos_bias_u"].reshape(D), t[p + "attn.pos_bias_v"].reshape(D)
         if self.plant == "pos_bias_swap":
             u, w = w, u
         qu, qv = q + u, q + w
-        # the position rows for relative positions T-1 .. -(T-1) (relPosEmb)
-        pp = self.linear(orc.conf_rel_pos(T, D), p + "attn.linear_pos.weight", D, D)
         scale = F32(1.0 / math.sqrt(D if self.plant == "scale_d" else hd))
-        bl = key_range(hp, T, L, None)
         out = np.zeros((T, D), F32)
         for h in range(H):
             sl = slice(h * hd, (h + 1) * hd)
             for q0 in range(0, T, bl):
                 q1 = min(T, q0 + bl)
                 nq = q1 - q0
-                rng = [key_range(hp, T, L, qq) for qq in range(q0, q1)]
+                rng = [keyf(qoff + qq) for qq in range(q0, q1)]
                 k0, k1 = min(r[0] for r in rng), max(r[1] for r in rng)
                 nk = k1 - k0
                 if nk <= 0:
@@ -141,7 +145,7 @@ class Composed:
                 # the block's scores and position terms by kern's float32
                 # products (MatMulF32), the position rows from jlo on
                 npos = nq + nk - 1
-                jlo = T - 1 - (q1 - 1) + k0
+                jlo = Tk - 1 - (qoff + q1 - 1) + k0
                 sc = orc.matmul_f32(np.ascontiguousarray(qu[q0:q1, sl]), np.ascontiguousarray(k[k0:k1, sl]))
                 bd = orc.matmul_f32(np.ascontiguousarray(qv[q0:q1, sl]),
                                     np.ascontiguousarray(pp[jlo:jlo + npos, sl]))
@@ -165,7 +169,10 @@ class Composed:
         att = self.linear(out, p + "attn.linear_out.weight", D, D, p + "attn.linear_out.bias")
         return x + att
 
-    def conv_module(self, x, ln, p, L):
+    def conv_module(self, x, ln, p, L, prev=None):
+        """convModule (encoder.go:343-397); prev: the padL gated frames
+        before the first (a stream's; none offline).  Returns (x, the gated
+        frames)."""
         orc, hp, t = self.orc, self.hp, self.t
         T, D, K = x.shape[0], hp["d"], hp["conv_kernel"]
         a = self.linear(ln, p + "conv.pointwise1.weight", 2 * D, D, p + "conv.pointwise1.bias")
@@ -187,9 +194,11 @@ class Composed:
         for r in range(T):
             for j in range(K):
                 ti = r + j - padL
+                tap = dw[:, K - 1 - j] if self.plant == "dw_reversed" else dw[:, j]
                 if 0 <= ti < T:
-                    tap = dw[:, K - 1 - j] if self.plant == "dw_reversed" else dw[:, j]
                     y[r] = y[r] + tap * g[ti]
+                elif ti < 0 and prev is not None and padL + ti >= 0:
+                    y[r] = y[r] + tap * prev[padL + ti]
         if hp.get("conv_norm", "batch_norm") == "layer_norm":
             y = orc.layernorm(y, t[p + "conv.bn.weight"], t[p + "conv.bn.bias"])
         else:
@@ -197,7 +206,7 @@ class Composed:
                                     t[p + "conv.bn.running_var"])
             y = y * s + c
         y = orc.silu(y.ravel()).reshape(T, D)
-        return x + self.linear(y, p + "conv.pointwise2.weight", D, D, p + "conv.pointwise2.bias")
+        return x + self.linear(y, p + "conv.pointwise2.weight", D, D, p + "conv.pointwise2.bias"), g
 
     def subsample(self, mel, valid):
         """subsample (encoder.go:123-167): (out [T][d], T, L)."""
@@ -294,14 +303,25 @@ class Composed:
         return x, L
 
     def block(self, i, x, L):
-        """runBlock (encoder.go:411-429)."""
+        """One block offline (encoder.go:474-486): the position projection
+        of relPosEmb(T), offlineKeys' ranges and blocks, runBlock."""
+        T, D = x.shape[0], self.hp["d"]
+        pp = self.linear(self.orc.conf_rel_pos(T, D), f"enc.blocks.{i}.attn.linear_pos.weight", D, D)
+        return self.run_block(i, x, L, None, lambda q: key_range(self.hp, T, L, q), key_range(self.hp, T, L, None),
+                              pp, None)[0]
+
+    def run_block(self, i, x, L, kv_before, keyf, bl, pp, conv_prev):
+        """runBlock (encoder.go:411-429); kv_before: a stream's cached
+        attention inputs.  Returns (x, the key rows, the gated frames)."""
         p = f"enc.blocks.{i}."
         x = np.asarray(x, F32).copy()
         x = self.feed_forward(x, p, "ff1")
-        x = self.attention(x, self.ln(x, p + "norm_attn"), p, L)
-        x = self.conv_module(x, self.ln(x, p + "norm_conv"), p, L)
+        ln = self.ln(x, p + "norm_attn")
+        kv = ln if kv_before is None else np.concatenate([kv_before, ln])
+        x = self.attention(x, ln, p, L, kv, keyf, bl, pp)
+        x, glu = self.conv_module(x, self.ln(x, p + "norm_conv"), p, L, conv_prev)
         x = self.feed_forward(x, p, "ff2")
-        return self.ln(x, p + "norm_out")
+        return self.ln(x, p + "norm_out"), kv, glu
 
 
 # the tiny regular model (every key, blocks of 32, batch norm), and a
@@ -394,3 +414,98 @@ def test_planted_pre_encoder_mistakes_break_the_pin(orc, model, plant):
     want, L = m.encode(mel, valid - 13)
     got, L2 = Composed(orc, hp, t, plant=plant).encode(mel, valid - 13)
     assert got.shape != want.shape or not np.array_equal(_bits(got), _bits(want)), plant
+
+
+class StreamComposed:
+    """A stream's chunk steps (stream.go:241-307) over Composed: each
+    chunk's pre-encoder rows (all but the first chunk's first `drop` cut),
+    xscale, and every block with the stream's cached attention inputs (its
+    last `left` key rows), the chunk keys of stream.go:273-287 (the closed
+    form of its loops), the position rows for relative positions Tk - 1
+    down (relPosRange), and the convolution's last padL gated frames."""
+
+    def __init__(self, comp, right, left, drop, plant=None):
+        hp = comp.hp
+        self.comp, self.left, self.drop, self.plant = comp, left, drop, plant
+        self.chunk = right + 1
+        self.lchunks = left // self.chunk
+        cl, cr = hp.get("conv_left", -1), hp.get("conv_right", -1)
+        self.padL = cl if cl >= 0 and cr >= 0 else (hp["conv_kernel"] - 1) // 2
+        D = hp["d"]
+        self.kv = [np.zeros((0, D), F32) for _ in range(hp["layers"])]
+        self.conv = [np.zeros((self.padL, D), F32) for _ in range(hp["layers"])]
+        self.first = True
+
+    def step(self, mel, length):
+        comp, hp = self.comp, self.comp.hp
+        D = hp["d"]
+        x, T, L = comp.subsample(mel, length)
+        if not self.first and self.plant != "no_drop":
+            x = x[min(self.drop, T):]
+            T, L = max(T - self.drop, 0), max(L - self.drop, 0)
+        self.first = False
+        L = min(L, T)
+        if T <= 0:
+            return np.zeros((0, D), F32)
+        if hp.get("xscaling", True):
+            x = x * F32(math.sqrt(D))
+        c = self.kv[0].shape[0]
+        Tk, slot0 = c + T, self.left - c
+
+        def keyf(q):
+            if q - c >= L:
+                return 0, 0
+            qc = (slot0 + q) // self.chunk
+            return max(0, (qc - self.lchunks) * self.chunk - slot0), min(c + L, (qc + 1) * self.chunk - slot0)
+
+        for i in range(hp["layers"]):
+            pp = comp.linear(comp.orc.conf_rel_pos(Tk, D), f"enc.blocks.{i}.attn.linear_pos.weight", D, D)
+            prev = None if self.plant == "conv_no_carry" else self.conv[i]
+            x, kv, glu = comp.run_block(i, x, L, self.kv[i], keyf, T, pp, prev)
+            self.kv[i] = kv[max(0, Tk - self.left + (1 if self.plant == "kv_keep_fewer" else 0)):]
+            if self.padL > 0:
+                self.conv[i] = np.concatenate([self.conv[i], glu])[T:]
+        return x[:L]
+
+
+@pytest.mark.parametrize("right", [0, 1, 13])
+def test_oracle_stream_is_the_composition(orc, right):
+    """The oracle's chunk steps equal the composition's bit for bit at right
+    contexts 0 (where streaming differs from the offline encode), 1 and 13,
+    past the left context (the key cache full, its oldest rows leaving)."""
+    from gorelaxor_amd.conformer import mel_chunks, stream_geom
+    from gorelaxor_amd.synth import noise_mel
+    hp = dict(CHUNKED, att_left=8, context_choices=[(8, 13), (8, 6), (8, 1), (8, 0)])
+    t = conformer_model(hp, seed=9, pointwise_f16=False)
+    mel, frames, _ = noise_mel(hp["n_mels"], seconds=2.5, seed=5)
+    g = stream_geom(hp, right)
+    ref = orc.ConformerOracle(hp, t).stream(right, g["left"], g["drop"])
+    comp = StreamComposed(Composed(orc, hp, t), right, g["left"], g["drop"])
+    n = 0
+    for j, (ch, length, _) in enumerate(mel_chunks(mel, g)):
+        want = ref.step(ch, length)
+        got = comp.step(ch, length)
+        assert np.array_equal(_bits(got), _bits(want)), (right, j)
+        n += len(want)
+    assert n > 25
+
+
+@pytest.mark.parametrize("plant", ["no_drop", "conv_no_carry", "kv_keep_fewer"])
+def test_planted_stream_mistakes_break_the_pin(orc, plant):
+    """Each planted stream mistake changes the chunks' bits: the first
+    `drop` rows kept, the convolution's gated frames not carried, one key
+    row fewer than the left context kept (one more changes nothing: the
+    chunk keys never reach past the left context)."""
+    from gorelaxor_amd.conformer import mel_chunks, stream_geom
+    from gorelaxor_amd.synth import noise_mel
+    hp = dict(CHUNKED, att_left=8, context_choices=[(8, 13), (8, 6), (8, 1), (8, 0)])
+    t = conformer_model(hp, seed=9, pointwise_f16=False)
+    mel, frames, _ = noise_mel(hp["n_mels"], seconds=2.5, seed=5)
+    g = stream_geom(hp, 1)
+    ref = orc.ConformerOracle(hp, t).stream(1, g["left"], g["drop"])
+    comp = StreamComposed(Composed(orc, hp, t), 1, g["left"], g["drop"], plant=plant)
+    differs = False
+    for ch, length, _ in mel_chunks(mel, g):
+        want, got = ref.step(ch, length), comp.step(ch, length)
+        differs |= got.shape != want.shape or not np.array_equal(_bits(got), _bits(want))
+    assert differs, plant
